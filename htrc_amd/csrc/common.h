@@ -1,0 +1,99 @@
+// Shared device helpers for the flat-HTRC HIP kernels (gfx950 / CDNA4 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace htrc {
+
+constexpr int D = 128;      // head dimension the kernels are specialised for
+constexpr int TILE = 64;    // query rows per tile (one expansion centre)
+constexpr int WAVE = 64;
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// fp32(1/127) = 0x3C010204, the per-row int8 scale factor.
+__device__ constexpr float R127 = 1.0f / 127.0f;
+
+__device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (quiet NaN kept).
+__device__ __forceinline__ uint32_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// where(x >= 0, x + 0.5, x - 0.5) in fp32, then truncation toward zero.
+__device__ __forceinline__ int round_away(float x) {
+    float y = x >= 0.0f ? __fadd_rn(x, 0.5f) : __fsub_rn(x, 0.5f);
+    return (int)truncf(y);
+}
+
+// rint (half to even) clamped to +-127.
+__device__ __forceinline__ int round_even_clamp(float x) {
+    float y = rintf(x);
+    y = y > 127.0f ? 127.0f : y;
+    y = y < -127.0f ? -127.0f : y;
+    return (int)y;
+}
+
+__device__ __forceinline__ float row_scale(float amax, float floor_) {
+    float s = __fmul_rn(amax, R127);
+    return s < floor_ ? floor_ : s;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+// Reductions across the four 16-lane groups that share a column of an MFMA C tile.
+__device__ __forceinline__ float grp_max(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, WAVE));
+    return fmaxf(v, __shfl_xor(v, 32, WAVE));
+}
+__device__ __forceinline__ float grp_sum(float v) {
+    v += __shfl_xor(v, 16, WAVE);
+    return v + __shfl_xor(v, 32, WAVE);
+}
+// Reductions across the 16 lanes of one group (the columns of an MFMA C tile).
+__device__ __forceinline__ float col_max(float v) {
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 u) { return __builtin_bit_cast(bf16x8, u); }
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x2 lo, u32x2 hi) {
+    u32x4 u = {lo.x, lo.y, hi.x, hi.y};
+    return __builtin_bit_cast(bf16x8, u);
+}
+
+__device__ __forceinline__ uint32_t pack2bf(float a, float b) { return f2bf(a) | (f2bf(b) << 16); }
+
+// Eight fp32 -> bf16x8 (round to nearest even).
+__device__ __forceinline__ bf16x8 to_bf16x8(const float* x) {
+    u32x4 u = {pack2bf(x[0], x[1]), pack2bf(x[2], x[3]), pack2bf(x[4], x[5]), pack2bf(x[6], x[7])};
+    return as_bf16x8(u);
+}
+
+__device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Order-preserving uint32 key of a float (larger float -> larger key); -0 maps to +0.
+__device__ __forceinline__ uint32_t order_key(float f) {
+    uint32_t u = __float_as_uint(f == 0.0f ? 0.0f : f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+}  // namespace htrc

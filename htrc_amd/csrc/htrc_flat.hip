@@ -1,0 +1,1061 @@
+// Flat-HTRC attention kernels for MI355X (gfx950, CDNA4), and their C-ABI launchers.
+//
+// Pipeline of one layer call (every kernel takes a head index in grid.z / grid.y, so all
+// heads of a layer go in one launch):
+//   pack_q    q rows -> tile centres mu, q8/sq, dq8/sdq          (HBM-bound)
+//   pack_kv   k, v   -> k8/ks, bf16 K and V in key-quad layout   (HBM-bound)
+//   stats     mu, K, V -> per (tile, leaf) g8/sg, vb, lz          (bf16 MFMA, HBM writes)
+//   select    dq8, g8 -> SEL[t, l]                                (int8 MFMA)
+//   topk      SEL -> idx (ascending), excl                        (LDS radix select)
+//   tile      far (g8, vb) + near (k8, v) online softmax          (int8 + bf16 MFMA)
+//   merge     split partials -> out, logZ
+//
+// MFMA conventions (16x16xK): lane l supplies A[m = l%16][k-set(l/16)] and
+// B[k-set(l/16)][n = l%16]; C[m = 4*(l/16) + i][n = l%16] sits in item i of lane l.
+// Every product below is arranged as C^T = A(keys/dims) * B(query rows or centres), so the
+// query row (or tile centre) of a C element is always lane%16 and the online-softmax
+// statistics of a row never leave its four lanes.
+//
+// Key-quad layout ("q4") of a bf16 matrix X[rows][128]: X4[row / 4][col][row % 4].  It
+// makes the eight k-items of a PV operand (two runs of four consecutive keys at one
+// column) two 8-byte loads.
+#include "common.h"
+
+#include <stdio.h>
+#include <string.h>
+
+using namespace htrc;
+
+// ---------------------------------------------------------------------------------------------
+// pack_q: one workgroup per (tile, head).  Tile centre = sequential fp32 sum over the real
+// rows / row count (h3/htrc_flat.py:142-156); then per padded row the int8 of q and of
+// q - mu with per-row scales (h3/htrc_flat_triton.py:104-117).
+// ---------------------------------------------------------------------------------------------
+template <bool IN_BF16>
+__global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qin, int64_t nq, int nt,
+                                                     float* __restrict__ mu, int8_t* __restrict__ q8,
+                                                     float* __restrict__ sq, int8_t* __restrict__ dq8,
+                                                     float* __restrict__ sdq) {
+    __shared__ float tq[TILE][D + 1];
+    __shared__ float smu[D];
+    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int64_t r0 = (int64_t)t * TILE;
+    const int nr = (int)(nq - r0 < TILE ? nq - r0 : TILE);
+    const int64_t qbase = (int64_t)h * nq * D;
+    for (int e = tid; e < TILE * D; e += 256) {
+        const int r = e >> 7, c = e & (D - 1);
+        const int64_t src = r0 + r < nq ? r0 + r : nq - 1;   // pad rows repeat the last row
+        float x;
+        if (IN_BF16)
+            x = bf2f(((const uint16_t*)qin)[qbase + src * D + c]);
+        else
+            x = ((const float*)qin)[qbase + src * D + c];
+        tq[r][c] = x;
+    }
+    __syncthreads();
+    const int64_t tg = (int64_t)h * nt + t;
+    if (tid < D) {
+        float s = 0.0f;
+        for (int r = 0; r < nr; ++r) s = __fadd_rn(s, tq[r][tid]);
+        const float m = __fdiv_rn(s, (float)nr);
+        smu[tid] = m;
+        mu[tg * D + tid] = m;
+    }
+    __syncthreads();
+    const int w = tid >> 6, lane = tid & 63;
+    const float m0 = smu[2 * lane], m1 = smu[2 * lane + 1];
+    for (int rr = 0; rr < 16; ++rr) {
+        const int r = w * 16 + rr;
+        const float x0 = tq[r][2 * lane], x1 = tq[r][2 * lane + 1];
+        const float d0 = __fsub_rn(x0, m0), d1 = __fsub_rn(x1, m1);
+        const float aq = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+        const float ad = wave_max(fmaxf(fabsf(d0), fabsf(d1)));
+        const float s1 = row_scale(aq, 1e-20f), s2 = row_scale(ad, 1e-20f);
+        const int64_t p = tg * TILE + r;
+        const uint16_t qq = (uint16_t)((round_away(__fdiv_rn(x0, s1)) & 0xff) |
+                                       ((round_away(__fdiv_rn(x1, s1)) & 0xff) << 8));
+        const uint16_t dd = (uint16_t)((round_away(__fdiv_rn(d0, s2)) & 0xff) |
+                                       ((round_away(__fdiv_rn(d1, s2)) & 0xff) << 8));
+        ((uint16_t*)(q8 + p * D))[lane] = qq;
+        ((uint16_t*)(dq8 + p * D))[lane] = dd;
+        if (lane == 0) {
+            sq[p] = s1;
+            sdq[p] = s2;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// pack_kv: one workgroup per 64 key rows of a head.  k8/ks per row (h3/htrc_flat.py:216-218,
+// round half to even), plus bf16 K and V re-laid out in key-quad layout for the PV-type
+// MFMA operands of the stats and tile kernels.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pack_kv_kernel(const uint16_t* __restrict__ k,
+                                                      const uint16_t* __restrict__ v, int64_t nk,
+                                                      int8_t* __restrict__ k8, float* __restrict__ ks,
+                                                      uint16_t* __restrict__ kq, uint16_t* __restrict__ vq) {
+    const int h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int64_t r0 = (int64_t)blockIdx.x * 64;
+    const int64_t base = (int64_t)h * nk;
+    for (int rr = 0; rr < 16; ++rr) {
+        const int64_t r = r0 + w * 16 + rr;
+        if (r >= nk) break;
+        const uint32_t pr = ((const uint32_t*)(k + (base + r) * D))[lane];
+        const float x0 = bf2f(pr & 0xffffu), x1 = bf2f(pr >> 16);
+        const float s = row_scale(wave_max(fmaxf(fabsf(x0), fabsf(x1))), 1e-20f);
+        const uint16_t o = (uint16_t)((round_even_clamp(__fdiv_rn(x0, s)) & 0xff) |
+                                      ((round_even_clamp(__fdiv_rn(x1, s)) & 0xff) << 8));
+        ((uint16_t*)(k8 + (base + r) * D))[lane] = o;
+        if (lane == 0) ks[base + r] = s;
+    }
+    // key-quad relayout: item = (quad within the 64 rows, column pair)
+    for (int it = tid; it < 16 * 64; it += 256) {
+        const int quad = it >> 6, cp = it & 63;
+        const int64_t rq = r0 + quad * 4;
+        if (rq >= nk) continue;
+        uint32_t kk[4], vv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            kk[i] = ((const uint32_t*)(k + (base + rq + i) * D))[cp];
+            vv[i] = ((const uint32_t*)(v + (base + rq + i) * D))[cp];
+        }
+        const int64_t qo = ((base + rq) / 4) * D * 4;   // quad row start (in bf16 units)
+        u32x2 k0 = {(kk[0] & 0xffffu) | (kk[1] << 16), (kk[2] & 0xffffu) | (kk[3] << 16)};
+        u32x2 k1 = {(kk[0] >> 16) | (kk[1] & 0xffff0000u), (kk[2] >> 16) | (kk[3] & 0xffff0000u)};
+        u32x2 v0 = {(vv[0] & 0xffffu) | (vv[1] << 16), (vv[2] & 0xffffu) | (vv[3] << 16)};
+        u32x2 v1 = {(vv[0] >> 16) | (vv[1] & 0xffff0000u), (vv[2] >> 16) | (vv[3] & 0xffff0000u)};
+        *(u32x2*)(kq + qo + (2 * cp) * 4) = k0;
+        *(u32x2*)(kq + qo + (2 * cp + 1) * 4) = k1;
+        *(u32x2*)(vq + qo + (2 * cp) * 4) = v0;
+        *(u32x2*)(vq + qo + (2 * cp + 1) * 4) = v1;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// stats: leaf statistics at the tile centres (h3/htrc_flat_triton.py:41-85, I8 store).
+// Workgroup = 64 tile centres (16 per wave) x a range of leaves of one head.  Per leaf:
+//   a^T = K_l mu^T         bf16 MFMA, mu split into three bf16 terms (~fp32 product)
+//   softmax over the leaf's keys per centre (lane%16 = centre)
+//   g^T = K_l^T w^T, vb^T = V_l^T w^T   bf16 MFMA, w split into 3 (g) / 2 (vb) bf16 terms
+// Leaves are processed four at a time so that vb can be stored in the leaf-quad layout
+// vbq[t][l/4][d][l%4] that the far-field PV operand reads with 8-byte loads.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ void split3(float x, float& a, float& b, float& c) {
+    a = bf2f(f2bf(x));
+    const float r = __fsub_rn(x, a);
+    b = bf2f(f2bf(r));
+    c = __fsub_rn(r, b);
+}
+
+template <int LEAF>
+__global__ __launch_bounds__(256) void stats_kernel(const float* __restrict__ mu, int nt,
+                                                    const uint16_t* __restrict__ k,
+                                                    const uint16_t* __restrict__ kq,
+                                                    const uint16_t* __restrict__ vq, int64_t nk, int nb,
+                                                    int nb_pad, int lpb, float scale,
+                                                    int8_t* __restrict__ g8, float* __restrict__ sg,
+                                                    uint16_t* __restrict__ vbq, float* __restrict__ lz) {
+    constexpr int KB = LEAF / 16;                 // 16-key blocks per leaf
+    constexpr int KK = (LEAF + 31) / 32;          // 32-key MFMA k-steps per leaf
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int h = blockIdx.z;
+    const int t = blockIdx.x * 64 + w * 16 + col;   // tile centre of this lane's C column
+    const bool tval = t < nt;
+    const int64_t th = (int64_t)h * nt + (tval ? t : 0);
+
+    bf16x8 mh[4], mm[4], ml[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        float a[8], b[8], c[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float x = tval ? mu[th * D + 32 * ks + 8 * grp + e] : 0.0f;
+            split3(x, a[e], b[e], c[e]);
+        }
+        mh[ks] = to_bf16x8(a);
+        mm[ks] = to_bf16x8(b);
+        ml[ks] = to_bf16x8(c);
+    }
+
+    const int l0 = blockIdx.y * lpb;
+    const int l1 = min(nb_pad, l0 + lpb);
+    const int64_t kh = (int64_t)h * nk;
+    for (int lq = l0; lq < l1; lq += 4) {
+        f32x4 vacc[4][8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int l = lq + j;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) vacc[j][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (l >= nb) {                     // padded leaf: empty state, excluded everywhere
+                if (tval) {
+                    const int64_t s = th * nb_pad + l;
+#pragma unroll
+                    for (int db = 0; db < 8; ++db)
+                        *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = 0u;
+                    if (grp == 0) {
+                        sg[s] = 0.0f;
+                        lz[s] = -INFINITY;
+                    }
+                }
+                continue;
+            }
+            const uint16_t* K = k + (kh + (int64_t)l * LEAF) * D;
+            f32x4 a[KB];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                a[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const bf16x8 A = as_bf16x8(*(const u32x4*)(K + (16 * kb + col) * D + 32 * ks + 8 * grp));
+                    a[kb] = mfma_bf16(A, mh[ks], a[kb]);
+                    a[kb] = mfma_bf16(A, mm[ks], a[kb]);
+                    a[kb] = mfma_bf16(A, ml[ks], a[kb]);
+                }
+            }
+            // a[kb][i] = mu_t . k_{16kb + 4grp + i}
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    a[kb][i] = __fmul_rn(a[kb][i], scale);
+                    mx = fmaxf(mx, a[kb][i]);
+                }
+            mx = grp_max(mx);
+            float z = 0.0f;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    a[kb][i] = __expf(__fsub_rn(a[kb][i], mx));
+                    z = __fadd_rn(z, a[kb][i]);
+                }
+            z = grp_sum(z);
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[kb][i] = __fdiv_rn(a[kb][i], z);
+
+            f32x4 gacc[8];
+#pragma unroll
+            for (int db = 0; db < 8; ++db) gacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int64_t qrow = (kh + (int64_t)l * LEAF) / 4;   // first key quad of the leaf
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                float w0[8], w1[8], w2[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int kb = 2 * kk + (e >> 2);
+                    const float x = kb < KB ? a[kb < KB ? kb : 0][e & 3] : 0.0f;
+                    split3(x, w0[e], w1[e], w2[e]);
+                }
+                const bf16x8 W0 = to_bf16x8(w0), W1 = to_bf16x8(w1), W2 = to_bf16x8(w2);
+#pragma unroll
+                for (int db = 0; db < 8; ++db) {
+                    const int64_t o0 = ((qrow + 8 * kk + grp) * D + 16 * db + col) * 4;
+                    const int64_t o1 = ((qrow + 8 * kk + 4 + grp) * D + 16 * db + col) * 4;
+                    const u32x2 zero = {0u, 0u};
+                    const u32x2 k0 = *(const u32x2*)(kq + o0);
+                    const u32x2 k1 = (2 * kk + 1 < KB) ? *(const u32x2*)(kq + o1) : zero;
+                    const u32x2 v0 = *(const u32x2*)(vq + o0);
+                    const u32x2 v1 = (2 * kk + 1 < KB) ? *(const u32x2*)(vq + o1) : zero;
+                    const bf16x8 KA = as_bf16x8(k0, k1), VA = as_bf16x8(v0, v1);
+                    gacc[db] = mfma_bf16(KA, W0, gacc[db]);
+                    gacc[db] = mfma_bf16(KA, W1, gacc[db]);
+                    gacc[db] = mfma_bf16(KA, W2, gacc[db]);
+                    vacc[j][db] = mfma_bf16(VA, W0, vacc[j][db]);
+                    vacc[j][db] = mfma_bf16(VA, W1, vacc[j][db]);
+                }
+            }
+            // g^T: lane holds dims 16db + 4grp + i of centre t
+            float am = 0.0f;
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    gacc[db][i] = __fmul_rn(gacc[db][i], scale);
+                    am = fmaxf(am, fabsf(gacc[db][i]));
+                }
+            am = grp_max(am);
+            am = am < 1e-30f ? 1e-30f : am;
+            const float cq = __fdiv_rn(127.0f, am);
+            if (tval) {
+                const int64_t s = th * nb_pad + l;
+#pragma unroll
+                for (int db = 0; db < 8; ++db) {
+                    uint32_t pk = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) pk |= (uint32_t)(round_away(__fmul_rn(gacc[db][i], cq)) & 0xff) << (8 * i);
+                    *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = pk;
+                }
+                if (grp == 0) {
+                    sg[s] = __fmul_rn(am, R127);
+                    lz[s] = __fadd_rn(mx, __logf(z));
+                }
+            }
+        }
+        if (tval) {   // vb of the four leaves -> vbq[t][lq/4][dim][0..3]
+            uint16_t* vo = vbq + ((th * nb_pad + lq) / 4) * D * 4;
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int dim = 16 * db + 4 * grp + i;
+                    u32x2 o = {f2bf(vacc[0][db][i]) | (f2bf(vacc[1][db][i]) << 16),
+                               f2bf(vacc[2][db][i]) | (f2bf(vacc[3][db][i]) << 16)};
+                    *(u32x2*)(vo + dim * 4) = o;
+                }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// select: SEL[t, l] = max_r float(dq8_r . g8_tl) * (sdq_r * sg_tl) + lz_tl
+// (h3/htrc_flat_triton.py:214-254).  Workgroup = one tile x 256 leaves; each wave owns 64
+// leaves and all rows (four 16-row B operands held in registers).  Bit-exact: int32 dot,
+// one fp32 product per row, an exact max, one fp32 add.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ void load_rows_i8(const int8_t* __restrict__ x8, int64_t row0, int stride,
+                                             int ts, int col, int grp, i32x4 (&b)[4][2], bool (&val)[4]) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        const int r = 16 * rb + col;
+        val[rb] = r < ts;
+        const int64_t p = row0 + (int64_t)(val[rb] ? r : 0) * stride;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) b[rb][ks] = *(const i32x4*)(x8 + p * D + 64 * ks + 16 * grp);
+    }
+}
+
+__global__ __launch_bounds__(256) void select_kernel(const int8_t* __restrict__ dq8,
+                                                     const float* __restrict__ sdq, int stride,
+                                                     const int8_t* __restrict__ g8,
+                                                     const float* __restrict__ sg,
+                                                     const float* __restrict__ lz, int nt, int nb,
+                                                     int nb_pad, float* __restrict__ sel) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int t = blockIdx.x, h = blockIdx.z;
+    const int64_t th = (int64_t)h * nt + t;
+    const int ts = TILE / stride;
+    i32x4 b[4][2];
+    bool val[4];
+    load_rows_i8(dq8, th * TILE, stride, ts, col, grp, b, val);
+    float srow[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) srow[rb] = sdq[th * TILE + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
+    const int c0 = blockIdx.y * 256 + w * 64;
+    for (int lb = 0; lb < 4; ++lb) {
+        const int c = c0 + 16 * lb;
+        if (c >= nb) break;
+        const int64_t s0 = th * nb_pad + c;
+        const int8_t* G = g8 + s0 * D;
+        i32x4 acc[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) acc[rb] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const i32x4 A = *(const i32x4*)(G + col * D + 64 * ks + 16 * grp);
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma_i8(A, b[rb][ks], acc[rb]);
+        }
+        const f32x4 sgv = *(const f32x4*)(sg + s0 + 4 * grp);
+        float best[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            best[i] = -INFINITY;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+                if (val[rb]) best[i] = fmaxf(best[i], __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i])));
+            best[i] = col_max(best[i]);
+        }
+        if (col == 0) {
+            const f32x4 lzv = *(const f32x4*)(lz + s0 + 4 * grp);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int l = c + 4 * grp + i;
+                if (l < nb) sel[th * nb_pad + l] = __fadd_rn(best[i], lzv[i]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Top-k of one SEL row by 8-bit MSB-first radix select in LDS, then an ascending-index
+// compaction (ties at the threshold go to the lower leaf index).  Leaves < sink are
+// forced in (h3/htrc_flat.py:262-265).  Used by the topk kernel and the fused route kernel.
+// ---------------------------------------------------------------------------------------------
+struct TopkSmem {
+    uint32_t hist[256];
+    uint32_t cnt_gt[257];
+    uint32_t cnt_eq[257];
+    uint32_t prefix, remaining;
+};
+
+// keys[] holds order_key(sel) for l < nb.  Writes idx[0..kx) ascending and (optionally) excl.
+__device__ void topk_row(const uint32_t* keys, int nb, int kx, TopkSmem& sm, int32_t* idx_out,
+                         int8_t* excl_out, int32_t* idx_lds) {
+    const int tid = threadIdx.x;
+    if (kx >= nb) {               // everything is selected
+        for (int l = tid; l < nb; l += 256) {
+            if (idx_out) idx_out[l] = l;
+            if (idx_lds) idx_lds[l] = l;
+            if (excl_out) excl_out[l] = 1;
+        }
+        __syncthreads();
+        return;
+    }
+    if (tid == 0) {
+        sm.prefix = 0;
+        sm.remaining = (uint32_t)kx;
+    }
+    uint32_t mask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        sm.hist[tid] = 0;
+        __syncthreads();
+        const uint32_t prefix = sm.prefix;
+        for (int l = tid; l < nb; l += 256) {
+            const uint32_t key = keys[l];
+            if ((key & mask) == prefix) atomicAdd(&sm.hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid < 64) {            // one wave: find the digit where the count from the top reaches `remaining`
+            const int lane = tid;
+            uint32_t c[4], s = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {          // lane owns digits 255-4*lane .. 252-4*lane
+                c[j] = sm.hist[255 - (4 * lane + j)];
+                s += c[j];
+            }
+            uint32_t incl = s;                     // inclusive prefix over lanes (descending digits)
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t y = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += y;
+            }
+            const uint32_t excl_before = incl - s;
+            const uint32_t rem = sm.remaining;
+            uint32_t run = excl_before;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (run < rem && run + c[j] >= rem) {
+                    const uint32_t digit = 255u - (uint32_t)(4 * lane + j);
+                    sm.prefix = prefix | (digit << shift);
+                    sm.remaining = rem - run;
+                }
+                run += c[j];
+            }
+        }
+        mask |= 255u << shift;
+        __syncthreads();
+    }
+    const uint32_t thr = sm.prefix, need_eq = sm.remaining;
+    // ascending compaction: thread owns a contiguous chunk of leaves
+    const int chunk = (nb + 255) / 256;
+    const int a = min(nb, tid * chunk), b = min(nb, a + chunk);
+    uint32_t ngt = 0, neq = 0;
+    for (int l = a; l < b; ++l) {
+        const uint32_t key = keys[l];
+        ngt += key > thr;
+        neq += key == thr;
+    }
+    sm.cnt_gt[tid + 1] = ngt;
+    sm.cnt_eq[tid + 1] = neq;
+    if (tid == 0) {
+        sm.cnt_gt[0] = 0;
+        sm.cnt_eq[0] = 0;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int i = 1; i <= 256; ++i) {
+            sm.cnt_gt[i] += sm.cnt_gt[i - 1];
+            sm.cnt_eq[i] += sm.cnt_eq[i - 1];
+        }
+    }
+    __syncthreads();
+    uint32_t eqr = sm.cnt_eq[tid];
+    uint32_t pos = sm.cnt_gt[tid] + (eqr < need_eq ? eqr : need_eq);
+    for (int l = a; l < b; ++l) {
+        const uint32_t key = keys[l];
+        bool take = key > thr;
+        if (key == thr) {
+            take = eqr < need_eq;
+            ++eqr;
+        }
+        take = take && pos < (uint32_t)kx;   // never more than kx, whatever the counts say
+        if (excl_out) excl_out[l] = take ? 1 : 0;
+        if (take) {
+            if (idx_out) idx_out[pos] = l;
+            if (idx_lds) idx_lds[pos] = l;
+            ++pos;
+        }
+    }
+    __syncthreads();
+}
+
+constexpr int MAX_NB_LDS = 8192;   // leaves per head the LDS top-k holds
+
+__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ sel, int nb, int nb_pad,
+                                                   int kx, int sink, int32_t* __restrict__ idx,
+                                                   int8_t* __restrict__ excl) {
+    __shared__ uint32_t keys[MAX_NB_LDS];
+    __shared__ TopkSmem sm;
+    const int64_t row = blockIdx.x;
+    for (int l = threadIdx.x; l < nb; l += 256)
+        keys[l] = l < sink ? 0xffffffffu : order_key(sel[row * nb_pad + l]);
+    for (int l = nb + threadIdx.x; l < nb_pad; l += 256) excl[row * nb_pad + l] = 0;
+    __syncthreads();
+    topk_row(keys, nb, kx, sm, idx + row * kx, excl + row * nb_pad, nullptr);
+}
+
+// ---------------------------------------------------------------------------------------------
+// tile: far field + near field online softmax for one (tile, split)
+// (h3/htrc_flat_triton.py:88-211, DOT=1, I8=1).  Four waves x 16 query rows.  Far leaves in
+// blocks of 32: S^T = g8 dq8^T (int8 MFMA), p = exp(score - m), O^T += vb^T p^T (bf16 MFMA).
+// Near tokens in blocks of 32 (two 16-key runs of selected leaves): S^T = k8 q8^T,
+// O^T += v^T p^T.  O^T keeps the query row on lane%16, so rescaling needs no shuffles.
+// ---------------------------------------------------------------------------------------------
+struct RowState {
+    float m;     // running max (same in the four lanes of a row)
+    float l;     // this lane's share of the running sum
+    f32x4 o[8];  // O^T: dims 16db + 4grp + i of row lane%16
+};
+
+// Online update with the scores of this lane's 8 keys (sc[0..7]) and the PV operand
+// fetch functor for the 8 dim-blocks.
+template <typename VFetch>
+__device__ __forceinline__ void online_block(RowState& st, float (&sc)[8], VFetch&& vfetch) {
+    float bm = sc[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) bm = fmaxf(bm, sc[e]);
+    bm = grp_max(bm);
+    const float m_new = fmaxf(st.m, bm);
+    const float m_s = m_new == -INFINITY ? 0.0f : m_new;
+    float p[8], ps = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        p[e] = __expf(__fsub_rn(sc[e], m_s));
+        ps = __fadd_rn(ps, p[e]);
+    }
+    const float alpha = __expf(__fsub_rn(st.m, m_s));
+    st.l = __fadd_rn(__fmul_rn(st.l, alpha), ps);
+    const bf16x8 P = to_bf16x8(p);
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+        f32x4 o = st.o[db];
+        o[0] = __fmul_rn(o[0], alpha);
+        o[1] = __fmul_rn(o[1], alpha);
+        o[2] = __fmul_rn(o[2], alpha);
+        o[3] = __fmul_rn(o[3], alpha);
+        st.o[db] = mfma_bf16(vfetch(db), P, o);
+    }
+    st.m = m_new;
+}
+
+template <int LEAF>
+__device__ __forceinline__ void tile_far_near(RowState& st, int64_t th, int nt, int nb, int nb_pad,
+                                              int lo, int hi, int e_lo, int e_hi, int kx,
+                                              const i32x4 (&q8r)[2], float sqr, const i32x4 (&dq8r)[2],
+                                              float sdqr, const int8_t* __restrict__ g8,
+                                              const float* __restrict__ sg, const float* __restrict__ lz,
+                                              const uint16_t* __restrict__ vbq,
+                                              const int8_t* __restrict__ excl_row,
+                                              const int32_t* __restrict__ idx_row,
+                                              const int8_t* __restrict__ k8,
+                                              const float* __restrict__ ks,
+                                              const uint16_t* __restrict__ vq, int64_t kh, float scale) {
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    // ---- far field
+    for (int c0 = lo; c0 < hi; c0 += 32) {
+        float sc[8];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const int cb = c0 + 16 * h2;
+            const int64_t s0 = th * nb_pad + cb;
+            i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+            for (int kss = 0; kss < 2; ++kss) {
+                const i32x4 A = *(const i32x4*)(g8 + (s0 + col) * D + 64 * kss + 16 * grp);
+                acc = mfma_i8(A, dq8r[kss], acc);
+            }
+            const f32x4 sgv = *(const f32x4*)(sg + s0 + 4 * grp);
+            const f32x4 lzv = *(const f32x4*)(lz + s0 + 4 * grp);
+            const uint32_t exv = *(const uint32_t*)(excl_row + cb + 4 * grp);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = cb + 4 * grp + i;
+                const bool ok = c < hi && ((exv >> (8 * i)) & 0xffu) == 0u;
+                sc[4 * h2 + i] = ok ? __fadd_rn(__fmul_rn((float)acc[i], __fmul_rn(sdqr, sgv[i])), lzv[i]) : -INFINITY;
+            }
+        }
+        const uint16_t* vb0 = vbq + ((th * nb_pad + c0) / 4) * D * 4;
+        online_block(st, sc, [&](int db) {
+            const int dim = 16 * db + col;
+            const u32x2 v0 = *(const u32x2*)(vb0 + ((int64_t)(grp)*D + dim) * 4);
+            const u32x2 v1 = *(const u32x2*)(vb0 + ((int64_t)(4 + grp) * D + dim) * 4);
+            return as_bf16x8(v0, v1);
+        });
+    }
+    // ---- near field: token j of the tile's selected list -> idx[j / LEAF] * LEAF + j % LEAF
+    for (int e0 = e_lo; e0 < e_hi; e0 += 32) {
+        float sc[8];
+        int64_t tok0[2];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const int j0 = e0 + 16 * h2;
+            const bool ok = j0 < e_hi;
+            const int jj = ok ? j0 : e_lo;
+            tok0[h2] = kh + (int64_t)idx_row[jj / LEAF] * LEAF + (jj % LEAF);
+            i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+            for (int kss = 0; kss < 2; ++kss) {
+                const i32x4 A = *(const i32x4*)(k8 + (tok0[h2] + col) * D + 64 * kss + 16 * grp);
+                acc = mfma_i8(A, q8r[kss], acc);
+            }
+            const f32x4 ksv = *(const f32x4*)(ks + tok0[h2] + 4 * grp);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool oki = ok && (j0 + 4 * grp + i) < e_hi;
+                sc[4 * h2 + i] = oki ? __fmul_rn((float)acc[i], __fmul_rn(__fmul_rn(sqr, ksv[i]), scale)) : -INFINITY;
+            }
+        }
+        online_block(st, sc, [&](int db) {
+            const int dim = 16 * db + col;
+            const u32x2 v0 = *(const u32x2*)(vq + ((tok0[0] / 4 + grp) * D + dim) * 4);
+            const u32x2 v1 = *(const u32x2*)(vq + ((tok0[1] / 4 + grp) * D + dim) * 4);
+            return as_bf16x8(v0, v1);
+        });
+    }
+}
+
+__device__ __forceinline__ void load_row_ops(const int8_t* __restrict__ q8, const int8_t* __restrict__ dq8,
+                                             int64_t p, int grp, i32x4 (&q8r)[2], i32x4 (&dq8r)[2]) {
+#pragma unroll
+    for (int kss = 0; kss < 2; ++kss) {
+        q8r[kss] = *(const i32x4*)(q8 + p * D + 64 * kss + 16 * grp);
+        dq8r[kss] = *(const i32x4*)(dq8 + p * D + 64 * kss + 16 * grp);
+    }
+}
+
+// Final normalisation of a row state (one split): out = O / max(l, 1e-30), logZ = m_s + log l.
+__device__ __forceinline__ void write_final(const RowState& st, float ltot, int64_t orow, bool valid,
+                                            float* __restrict__ out, float* __restrict__ logz) {
+    const int lane = threadIdx.x & 63, grp = lane >> 4;
+    if (!valid) return;
+    const float ms = st.m == -INFINITY ? 0.0f : st.m;
+    const float den = ltot < 1e-30f ? 1e-30f : ltot;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+        f32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = __fdiv_rn(st.o[db][i], den);
+        *(f32x4*)(out + orow * D + 16 * db + 4 * grp) = o;
+    }
+    if (grp == 0) logz[orow] = __fadd_rn(ms, __logf(ltot));
+}
+
+template <int LEAF>
+__global__ __launch_bounds__(256) void tile_kernel(
+    const int8_t* __restrict__ q8, const float* __restrict__ sq, const int8_t* __restrict__ dq8,
+    const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
+    const float* __restrict__ lz, const uint16_t* __restrict__ vbq, const int8_t* __restrict__ excl,
+    const int32_t* __restrict__ idx, const int8_t* __restrict__ k8, const float* __restrict__ ks,
+    const uint16_t* __restrict__ vq, int64_t nq, int nt, int64_t nk, int nb, int nb_pad, int kx, int lps,
+    int eps, float scale, float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc,
+    float* __restrict__ out, float* __restrict__ logz) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int t = blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
+    const int64_t th = (int64_t)h * nt + t;
+    const int r = w * 16 + col;
+    const int64_t p = th * TILE + r;
+    i32x4 q8r[2], dq8r[2];
+    load_row_ops(q8, dq8, p, grp, q8r, dq8r);
+    const float sqr = sq[p], sdqr = sdq[p];
+    RowState st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) st.o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int lo = sp * lps, hi = min(nb, lo + lps);
+    const int e_n = kx * LEAF;
+    const int e_lo = sp * eps, e_hi = min(e_n, e_lo + eps);
+    tile_far_near<LEAF>(st, th, nt, nb, nb_pad, lo, hi, e_lo, e_hi, kx, q8r, sqr, dq8r, sdqr, g8, sg, lz,
+                        vbq, excl + th * nb_pad, idx + th * (kx > 0 ? kx : 1), k8, ks, vq, (int64_t)h * nk, scale);
+    const float ltot = grp_sum(st.l);
+    if (pacc == nullptr) {   // single split: normalise in place
+        const int64_t qi = (int64_t)t * TILE + r;
+        write_final(st, ltot, (int64_t)h * nq + qi, qi < nq, out, logz);
+        return;
+    }
+    const int64_t base = (th * ns + sp) * TILE + r;
+    if (grp == 0) {
+        pm[base] = st.m;
+        pl[base] = ltot;
+    }
+#pragma unroll
+    for (int db = 0; db < 8; ++db) *(f32x4*)(pacc + base * D + 16 * db + 4 * grp) = st.o[db];
+}
+
+// merge: (h3/htrc_flat_triton.py:257-273) + logZ = mm + log(den).  One workgroup per tile.
+__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
+                                                    const float* __restrict__ pacc, int ns, int64_t nq, int nt,
+                                                    float* __restrict__ out, float* __restrict__ logz) {
+    const int t = blockIdx.x, h = blockIdx.y;
+    const int64_t th = (int64_t)h * nt + t;
+    const int r = threadIdx.x >> 2, part = threadIdx.x & 3;   // 4 threads per row, 32 dims each
+    const int64_t qi = (int64_t)t * TILE + r;
+    if (qi >= nq) return;
+    float mm = -INFINITY;
+    for (int s = 0; s < ns; ++s) mm = fmaxf(mm, pm[(th * ns + s) * TILE + r]);
+    if (mm == -INFINITY) mm = 0.0f;
+    float den = 0.0f;
+    float num[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) num[i] = 0.0f;
+    for (int s = 0; s < ns; ++s) {
+        const int64_t b = (th * ns + s) * TILE + r;
+        const float wv = __expf(__fsub_rn(pm[b], mm));
+        den = __fadd_rn(den, __fmul_rn(pl[b], wv));
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            const f32x4 x = *(const f32x4*)(pacc + b * D + part * 32 + i);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) num[i + j] = __fadd_rn(num[i + j], __fmul_rn(x[j], wv));
+        }
+    }
+    const float dd = den < 1e-30f ? 1e-30f : den;
+    const int64_t orow = (int64_t)h * nq + qi;
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+        f32x4 o = {__fdiv_rn(num[i], dd), __fdiv_rn(num[i + 1], dd), __fdiv_rn(num[i + 2], dd),
+                   __fdiv_rn(num[i + 3], dd)};
+        *(f32x4*)(out + orow * D + part * 32 + i) = o;
+    }
+    if (part == 0) logz[orow] = __fadd_rn(mm, __logf(den));
+}
+
+// ---------------------------------------------------------------------------------------------
+// route: the fused per-tile kernel of the production path.  select (SEL of every leaf into
+// LDS) -> LDS top-k (idx ascending, exclusion bitmap) -> far + near online softmax -> out,
+// logZ.  One launch per layer replaces select + topk + tile + merge and never writes the
+// SEL / excl / partial tensors to HBM (it can still emit idx for checking).
+// ---------------------------------------------------------------------------------------------
+template <int LEAF>
+__global__ __launch_bounds__(256) void route_kernel(
+    const int8_t* __restrict__ q8, const float* __restrict__ sq, const int8_t* __restrict__ dq8,
+    const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
+    const float* __restrict__ lz, const uint16_t* __restrict__ vbq, const int8_t* __restrict__ k8,
+    const float* __restrict__ ks, const uint16_t* __restrict__ vq, int64_t nq, int nt, int64_t nk, int nb,
+    int nb_pad, int kx, int sink, int stride, float scale, float* __restrict__ out,
+    float* __restrict__ logz, int32_t* __restrict__ idx_out) {
+    __shared__ uint32_t keys[MAX_NB_LDS];
+    __shared__ __align__(16) int8_t exl[MAX_NB_LDS + 32];
+    __shared__ int32_t sidx[MAX_NB_LDS];
+    __shared__ TopkSmem sm;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int t = blockIdx.x, h = blockIdx.z;
+    const int64_t th = (int64_t)h * nt + t;
+    // ---- select (bit-exact, same arithmetic as select_kernel)
+    {
+        const int ts = TILE / stride;
+        i32x4 b[4][2];
+        bool val[4];
+        load_rows_i8(dq8, th * TILE, stride, ts, col, grp, b, val);
+        float srow[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+            srow[rb] = sdq[th * TILE + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
+        for (int c = 16 * w; c < nb; c += 64) {
+            const int64_t s0 = th * nb_pad + c;
+            i32x4 acc[4];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) acc[rb] = i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int kss = 0; kss < 2; ++kss) {
+                const i32x4 A = *(const i32x4*)(g8 + (s0 + col) * D + 64 * kss + 16 * grp);
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma_i8(A, b[rb][kss], acc[rb]);
+            }
+            const f32x4 sgv = *(const f32x4*)(sg + s0 + 4 * grp);
+            float best[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                best[i] = -INFINITY;
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+                    if (val[rb]) best[i] = fmaxf(best[i], __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i])));
+                best[i] = col_max(best[i]);
+            }
+            if (col == 0) {
+                const f32x4 lzv = *(const f32x4*)(lz + s0 + 4 * grp);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int l = c + 4 * grp + i;
+                    if (l < nb) keys[l] = l < sink ? 0xffffffffu : order_key(__fadd_rn(best[i], lzv[i]));
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const int kxe = kx < nb ? kx : nb;
+    if (kxe > 0) {
+        topk_row(keys, nb, kxe, sm, idx_out ? idx_out + th * kxe : nullptr, exl, sidx);
+    } else {
+        for (int l = threadIdx.x; l < nb; l += 256) exl[l] = 0;
+        __syncthreads();
+    }
+    // ---- far + near, one split
+    const int r = w * 16 + col;
+    const int64_t p = th * TILE + r;
+    i32x4 q8r[2], dq8r[2];
+    load_row_ops(q8, dq8, p, grp, q8r, dq8r);
+    const float sqr = sq[p], sdqr = sdq[p];
+    RowState st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) st.o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    tile_far_near<LEAF>(st, th, nt, nb, nb_pad, 0, nb, 0, kxe * LEAF, kxe, q8r, sqr, dq8r, sdqr, g8, sg, lz,
+                        vbq, exl, sidx, k8, ks, vq, (int64_t)h * nk, scale);
+    const float ltot = grp_sum(st.l);
+    const int64_t qi = (int64_t)t * TILE + r;
+    write_final(st, ltot, (int64_t)h * nq + qi, qi < nq, out, logz);
+}
+
+// ---------------------------------------------------------------------------------------------
+// selftest_mfma: one wave computes C = A B with the operand conventions used above
+// (A row m = lane%16 with k-set lane/16, B column n = lane%16 with the same k-set,
+// C[4*(lane/16) + i][lane%16] in item i).
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void selftest_mfma_kernel(const int8_t* __restrict__ ai, const int8_t* __restrict__ bi,
+                                                           int32_t* __restrict__ ci, const uint16_t* __restrict__ af,
+                                                           const uint16_t* __restrict__ bf, float* __restrict__ cf) {
+    const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
+    i32x4 a = *(const i32x4*)(ai + col * 64 + 16 * grp);
+    int8_t bb[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bb[e] = bi[(16 * grp + e) * 16 + col];
+    i32x4 b = __builtin_bit_cast(i32x4, bb);
+    i32x4 c = mfma_i8(a, b, i32x4{0, 0, 0, 0});
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ci[(4 * grp + i) * 16 + col] = c[i];
+    const bf16x8 fa = as_bf16x8(*(const u32x4*)(af + col * 32 + 8 * grp));
+    uint16_t fb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) fb[e] = bf[(8 * grp + e) * 16 + col];
+    const bf16x8 fbv = __builtin_bit_cast(bf16x8, fb);
+    f32x4 cc = mfma_bf16(fa, fbv, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cf[(4 * grp + i) * 16 + col] = cc[i];
+}
+
+// =============================================================================================
+// C-ABI launchers
+// =============================================================================================
+#include "../../include/htrc_flat.h"
+
+static thread_local char g_err[512] = "";
+
+static int fail(int code, const char* msg) {
+    snprintf(g_err, sizeof(g_err), "%s", msg);
+    return code;
+}
+
+static int launched(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(g_err, sizeof(g_err), "%s: launch failed: %s", what, hipGetErrorString(e));
+        return HTRC_ERR_HIP;
+    }
+    g_err[0] = 0;
+    return HTRC_OK;
+}
+
+static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+#define REQUIRE(cond, msg)                             \
+    do {                                               \
+        if (!(cond)) return fail(HTRC_ERR_ARG, msg);   \
+    } while (0)
+
+extern "C" {
+
+int htrc_abi_version(void) { return HTRC_ABI_VERSION; }
+
+const char* htrc_last_error(void) { return g_err; }
+
+int htrc_nb_pad(int64_t nb) { return (int)((nb + 31) / 32 * 32); }
+
+int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, float* mu, int8_t* q8,
+                float* sq, int8_t* dq8, float* sdq, void* stream) {
+    REQUIRE(q && mu && q8 && sq && dq8 && sdq, "htrc_pack_q: null pointer");
+    REQUIRE(d == D, "htrc_pack_q: head dim must be 128");
+    REQUIRE(heads > 0 && heads <= 65535 && nq > 0, "htrc_pack_q: bad heads / rows");
+    REQUIRE(aligned(q8, 16) && aligned(dq8, 16), "htrc_pack_q: int8 outputs must be 16-byte aligned");
+    const int64_t nt = (nq + TILE - 1) / TILE;
+    REQUIRE(nt <= 0x7fffffff, "htrc_pack_q: too many tiles");
+    dim3 grid((unsigned)nt, (unsigned)heads);
+    if (q_is_bf16)
+        hipLaunchKernelGGL(pack_q_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, q, nq, (int)nt, mu,
+                           q8, sq, dq8, sdq);
+    else
+        hipLaunchKernelGGL(pack_q_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, q, nq, (int)nt, mu,
+                           q8, sq, dq8, sdq);
+    return launched("htrc_pack_q");
+}
+
+int htrc_pack_kv(const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nk, int d, int8_t* k8,
+                 float* ks, uint16_t* kq, uint16_t* vq, void* stream) {
+    REQUIRE(k && v && k8 && ks && kq && vq, "htrc_pack_kv: null pointer");
+    REQUIRE(d == D, "htrc_pack_kv: head dim must be 128");
+    REQUIRE(heads > 0 && heads <= 65535 && nk > 0 && nk % 16 == 0, "htrc_pack_kv: keys must be a positive multiple of 16");
+    REQUIRE(aligned(k, 4) && aligned(v, 4) && aligned(kq, 8) && aligned(vq, 8), "htrc_pack_kv: misaligned buffer");
+    dim3 grid((unsigned)((nk + 63) / 64), (unsigned)heads);
+    hipLaunchKernelGGL(pack_kv_kernel, grid, dim3(256), 0, (hipStream_t)stream, k, v, nk, k8, ks, kq, vq);
+    return launched("htrc_pack_kv");
+}
+
+int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* kq, const uint16_t* vq, int64_t heads,
+                    int64_t nt, int64_t nk, int leaf, int d, float scale, int8_t* g8, float* sg,
+                    uint16_t* vbq, float* lz, void* stream) {
+    REQUIRE(mu && k && kq && vq && g8 && sg && vbq && lz, "htrc_leaf_stats: null pointer");
+    REQUIRE(d == D, "htrc_leaf_stats: head dim must be 128");
+    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_leaf_stats: leaf must be 16/32/64/128");
+    REQUIRE(nk > 0 && nk % leaf == 0, "htrc_leaf_stats: key count must be a multiple of the leaf size");
+    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff, "htrc_leaf_stats: bad heads / tiles");
+    REQUIRE(aligned(k, 16) && aligned(g8, 16) && aligned(sg, 16) && aligned(lz, 16),
+            "htrc_leaf_stats: misaligned buffer");
+    const int64_t nb = nk / leaf;
+    const int nbp = htrc_nb_pad(nb);
+    const int lpb = 16;
+    dim3 grid((unsigned)((nt + 63) / 64), (unsigned)((nbp + lpb - 1) / lpb), (unsigned)heads);
+    hipStream_t s = (hipStream_t)stream;
+#define STATS_CASE(L)                                                                                      \
+    case L:                                                                                                \
+        hipLaunchKernelGGL(stats_kernel<L>, grid, dim3(256), 0, s, mu, (int)nt, k, kq, vq, nk, (int)nb, nbp, \
+                           lpb, scale, g8, sg, vbq, lz);                                                   \
+        break;
+    switch (leaf) {
+        STATS_CASE(16)
+        STATS_CASE(32)
+        STATS_CASE(64)
+        STATS_CASE(128)
+    }
+#undef STATS_CASE
+    return launched("htrc_leaf_stats");
+}
+
+int htrc_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
+                int64_t heads, int64_t nt, int64_t nb, int stride, int d, float* sel, void* stream) {
+    REQUIRE(dq8 && sdq && g8 && sg && lz && sel, "htrc_select: null pointer");
+    REQUIRE(d == D, "htrc_select: head dim must be 128");
+    REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_select: stride must divide 64");
+    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff && nb > 0, "htrc_select: bad sizes");
+    const int nbp = htrc_nb_pad(nb);
+    dim3 grid((unsigned)nt, (unsigned)((nb + 255) / 256), (unsigned)heads);
+    hipLaunchKernelGGL(select_kernel, grid, dim3(256), 0, (hipStream_t)stream, dq8, sdq, stride, g8, sg, lz,
+                       (int)nt, (int)nb, nbp, sel);
+    return launched("htrc_select");
+}
+
+int htrc_topk(const float* sel, int64_t rows, int64_t nb, int kx, int sink, int32_t* idx, int8_t* excl,
+              void* stream) {
+    REQUIRE(sel && idx && excl, "htrc_topk: null pointer");
+    REQUIRE(rows > 0 && rows <= 0x7fffffff && nb > 0 && nb <= MAX_NB_LDS, "htrc_topk: leaves per head must be in [1, 8192]");
+    REQUIRE(kx > 0 && kx <= nb && sink >= 0, "htrc_topk: need 0 < k <= leaves");
+    hipLaunchKernelGGL(topk_kernel, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, sel, (int)nb,
+                       htrc_nb_pad(nb), kx, sink, idx, excl);
+    return launched("htrc_topk");
+}
+
+static int64_t split_len(int64_t n, int64_t ns, int64_t bn) {   // _split, h3/htrc_flat_triton.py:297-299
+    const int64_t per = (n + ns - 1) / ns;
+    const int64_t r = (per + bn - 1) / bn * bn;
+    return r > bn ? r : bn;
+}
+
+int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
+              const float* sg, const float* lz, const uint16_t* vbq, const int8_t* excl, const int32_t* idx,
+              const int8_t* k8, const float* ks, const uint16_t* vq, int64_t heads, int64_t nq, int64_t nk,
+              int leaf, int d, int kx, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
+              float* out, float* logz, void* stream) {
+    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vbq && excl && k8 && ks && vq,
+            "htrc_tile: null input pointer");
+    REQUIRE(d == D, "htrc_tile: head dim must be 128");
+    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_tile: leaf must be 16/32/64/128");
+    REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_tile: bad sizes");
+    const int64_t nb = nk / leaf, nt = (nq + TILE - 1) / TILE;
+    REQUIRE(kx >= 0 && kx <= nb && (kx == 0 || idx), "htrc_tile: need 0 <= kx <= leaves and idx when kx > 0");
+    REQUIRE(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0, "htrc_tile: need 1 <= splits <= 64 and a block that is a multiple of 32");
+    REQUIRE(splits == 1 ? (out && logz) : (pm && pl && pacc), "htrc_tile: missing outputs");
+    const int lps = (int)split_len(nb, splits, bn), eps = (int)split_len((int64_t)kx * leaf, splits, bn);
+    dim3 grid((unsigned)nt, (unsigned)splits, (unsigned)heads);
+    hipStream_t s = (hipStream_t)stream;
+    float* ppm = splits == 1 ? nullptr : pm;
+    float* ppl = splits == 1 ? nullptr : pl;
+    float* ppa = splits == 1 ? nullptr : pacc;
+#define TILE_CASE(L)                                                                                            \
+    case L:                                                                                                     \
+        hipLaunchKernelGGL(tile_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vbq, excl, idx, k8, \
+                           ks, vq, nq, (int)nt, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps, scale, ppm, ppl, ppa,   \
+                           out, logz);                                                                          \
+        break;
+    switch (leaf) {
+        TILE_CASE(16)
+        TILE_CASE(32)
+        TILE_CASE(64)
+        TILE_CASE(128)
+    }
+#undef TILE_CASE
+    return launched("htrc_tile");
+}
+
+int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int splits,
+               int d, float* out, float* logz, void* stream) {
+    REQUIRE(pm && pl && pacc && out && logz, "htrc_merge: null pointer");
+    REQUIRE(d == D && splits >= 1 && heads > 0 && heads <= 65535 && nq > 0, "htrc_merge: bad sizes");
+    const int64_t nt = (nq + TILE - 1) / TILE;
+    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)nt, (unsigned)heads), dim3(256), 0, (hipStream_t)stream, pm,
+                       pl, pacc, splits, nq, (int)nt, out, logz);
+    return launched("htrc_merge");
+}
+
+int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
+               const float* sg, const float* lz, const uint16_t* vbq, const int8_t* k8, const float* ks,
+               const uint16_t* vq, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
+               int stride, float scale, float* out, float* logz, int32_t* idx, void* stream) {
+    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vbq && k8 && ks && vq && out && logz,
+            "htrc_route: null pointer");
+    REQUIRE(d == D, "htrc_route: head dim must be 128");
+    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_route: leaf must be 16/32/64/128");
+    REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_route: bad sizes");
+    const int64_t nb = nk / leaf, nt = (nq + TILE - 1) / TILE;
+    REQUIRE(nb <= MAX_NB_LDS, "htrc_route: at most 8192 leaves per head");
+    REQUIRE(kx >= 0 && sink >= 0, "htrc_route: bad near-leaf count");
+    REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_route: stride must divide 64");
+    dim3 grid((unsigned)nt, 1, (unsigned)heads);
+    hipStream_t s = (hipStream_t)stream;
+#define ROUTE_CASE(L)                                                                                       \
+    case L:                                                                                                 \
+        hipLaunchKernelGGL(route_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vbq, k8, ks, vq, \
+                           nq, (int)nt, nk, (int)nb, htrc_nb_pad(nb), kx, sink, stride, scale, out, logz, idx); \
+        break;
+    switch (leaf) {
+        ROUTE_CASE(16)
+        ROUTE_CASE(32)
+        ROUTE_CASE(64)
+        ROUTE_CASE(128)
+    }
+#undef ROUTE_CASE
+    return launched("htrc_route");
+}
+
+int htrc_selftest_mfma(const int8_t* ai, const int8_t* bi, int32_t* ci, const uint16_t* af, const uint16_t* bf,
+                       float* cf, void* stream) {
+    REQUIRE(ai && bi && ci && af && bf && cf, "htrc_selftest_mfma: null pointer");
+    REQUIRE(aligned(ai, 16) && aligned(af, 16), "htrc_selftest_mfma: A operands must be 16-byte aligned");
+    hipLaunchKernelGGL(selftest_mfma_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, ai, bi, ci, af, bf, cf);
+    return launched("htrc_selftest_mfma");
+}
+
+}  // extern "C"

@@ -1,0 +1,161 @@
+"""Flat (tree-free) HTRC attention operator on MI355X -- the drop-in for h3/htrc_flat.py.
+
+Same call surface as the reference (``flat_attention``, ``PROD``, ``flat_attention_prod``):
+queries are cut into 64-row tiles with centre mu_t; every (tile, leaf) gets the exact
+leaf cumulants at the centre (log-partition lz, tilted key mean g, value mean vb); each
+query sees far leaves through lz + (q - mu).g with value vb, and the ``exact_leaves``
+leaves of largest row-max far logit exactly; both merge in one online softmax.
+
+One backend: hand-written gfx950 HIP kernels (``htrc_flat_hip``), INT8 Q/K dots and bf16
+PV dots with fp32 accumulation (the reference's ``store="int8", dot="bf16"`` path).
+``backend="triton"`` (the reference's GPU backend name) and ``backend="hip"`` select it;
+any other backend, or knobs the HIP path does not implement, raise ``ValueError``.
+
+Extensions over the reference: q/k/v may carry a leading head dimension ([H, N, D]) so a
+whole layer runs in one set of launches, and ``return_logz=True`` also returns the
+per-row log-partition of the approximate attention.
+"""
+from __future__ import annotations
+
+import math
+import time
+
+import torch
+
+from . import htrc_flat_hip as hip
+from ._lib import nb_pad
+
+
+class _Tick:
+    """Per-stage wall time with a device sync per stage (h3/htrc_flat.py:32-44)."""
+
+    def __init__(self, prof):
+        self.prof = prof
+        if prof is not None:
+            torch.cuda.synchronize()
+            self.t = time.perf_counter()
+
+    def __call__(self, name):
+        if self.prof is not None:
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            self.prof[name] = self.prof.get(name, 0.0) + 1e3 * (t - self.t)
+            self.t = t
+
+
+def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot, quant, tail, kern):
+    if backend not in ("hip", "triton"):
+        raise ValueError(f"backend {backend!r} is not part of this build: the flat operator runs only as "
+                         "HIP kernels (backend='hip', alias 'triton')")
+    if curvature != "lin":
+        raise ValueError("the HIP backend needs curvature='lin'")
+    if store != "int8" or dot != "bf16":
+        raise ValueError("the HIP backend implements store='int8', dot='bf16' (int8 Q/K dots, bf16 PV)")
+    if select != "max":
+        raise ValueError("the HIP backend implements select='max'")
+    if order != "seq":
+        raise ValueError("order must be 'seq' on the HIP backend (k-means ordering is not implemented)")
+    if quant:
+        raise ValueError("quant (fake-quant simulation) is not implemented on the HIP backend")
+    if tail is not None:
+        raise ValueError("tail keys are not implemented on the HIP backend: pass keys that are a multiple of the leaf")
+    if int(kern.get("group", 1)) != 1:
+        raise ValueError("kern['group'] > 1 (shared tile centres) is not implemented on the HIP backend")
+    if int(tile) != hip.TILE:
+        raise ValueError("the HIP backend uses tile=64")
+    if leaf not in (16, 32, 64, 128):
+        raise ValueError("leaf must be 16, 32, 64 or 128")
+    if q.dim() not in (2, 3) or k.dim() != q.dim() or v.shape != k.shape:
+        raise ValueError("q [N,D] with k/v [M,D], or q [H,N,D] with k/v [H,M,D]")
+    if q.shape[-1] != hip.D or k.shape[-1] != hip.D:
+        raise ValueError("head dim must be 128")
+    if q.dim() == 3 and q.shape[0] != k.shape[0]:
+        raise ValueError("q and k/v must have the same number of heads")
+    if int(k.shape[-2]) % int(leaf):
+        raise ValueError("HIP backend: key count must be a multiple of the leaf size")
+
+
+@torch.inference_mode()
+def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature="lin", tile_chunk=32,
+                   precision="fp32", leaf=16, scale=None, prof=None, select="max", backend="torch",
+                   store="fp32", splits=8, dot="tf32", sel_stride=1, kern=None, quant=None, sink_leaves=0,
+                   tail=None, ws=None, return_logz=False, state=None):
+    """q [N,D] (or [H,N,D]), k/v [M,D] (or [H,M,D]), any float dtype -> out fp32 of q's shape
+    (h3/htrc_flat.py:99-139).  ``kern['fused']`` (default True) runs select, top-k, far and
+    near field in one fused kernel per layer; False runs the reference's stage structure
+    (select, top-k, split tile kernel, merge) honouring ``splits`` and ``kern['tile_bn']``.
+    ``tile_chunk`` and ``precision`` are accepted for compatibility: all tiles are processed
+    in one launch and accumulation is IEEE fp32.  ``state``, if a dict, receives the packed
+    operands, the leaf state and the routing (for checks)."""
+    kern = dict(kern or {})
+    _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot, quant, tail, kern)
+    squeeze = q.dim() == 2
+    qh = q.unsqueeze(0) if squeeze else q
+    kh = k.unsqueeze(0) if squeeze else k
+    vh = v.unsqueeze(0) if squeeze else v
+    tick = _Tick(prof)
+    h, nq, d = (int(x) for x in qh.shape)
+    nk = int(kh.shape[1])
+    nb = nk // int(leaf)
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    sink = max(0, min(int(sink_leaves), nb))
+    kx = min(int(exact_leaves) + sink, nb)
+    if kx < 0:
+        raise ValueError("exact_leaves must be >= 0")
+    stride = int(sel_stride)
+    if stride < 1 or hip.TILE % stride:
+        raise ValueError("sel_stride must divide 64")
+    if qh.dtype not in (torch.float32, torch.bfloat16):
+        qh = qh.float()
+    mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), ws=ws)
+    kb = kh.to(torch.bfloat16).contiguous()
+    vb = vh.to(torch.bfloat16).contiguous()
+    k8, ks, kq, vq = hip.pack_kv(kb, vb, ws=ws)
+    tick("prep")
+    g8, lz, vbq, sg, _ = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, ws=ws, kq=kq, vq=vq)
+    tick("stats")
+    packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "vq": vq, "mu": mu}
+    lstate = {"g8": g8, "sg": sg, "lz": lz, "vbq": vbq}
+    nt = int(mu.shape[1])
+    idx = None
+    if kern.get("fused", True):
+        if state is not None and kx > 0:
+            idx = hip._buf(ws, "idx", (h, nt, kx), torch.int32, qh.device)
+        out, logz = hip.route(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, sink=sink, stride=stride,
+                              ws=ws, idx=idx)
+        tick("tile")
+    else:
+        excl = None
+        if kx > 0:
+            sel = hip.rowmax_select(g=g8, lz=lz, sg=sg, stride=stride, nb=nb, dq8=dq8, sdq=sdq, ws=ws)
+            idx, excl = hip.topk_excl(sel, nb, kx, sink, ws=ws)
+            if state is not None:
+                state["sel"] = sel
+        else:
+            excl = hip._buf(ws, "excl", (h, nt, nb_pad(nb)), torch.int8, qh.device)
+            excl.zero_()
+        tick("select")
+        out, logz = hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
+                                       bn=int(kern.get("tile_bn", 32)), ws=ws)
+        tick("tile")
+        if state is not None:
+            state["excl"] = excl
+    if state is not None:
+        state.update(packed)
+        state.update(lstate)
+        state["idx"] = idx
+        state["nb"], state["kx"] = nb, kx
+    res = out[0] if squeeze else out
+    lzr = logz[0] if squeeze else logz
+    tick("finish")
+    return (res, lzr) if return_logz else res
+
+
+PROD = dict(tile=64, exact_leaves=256, tile_chunk=128, backend="triton", precision="tf32",
+            store="int8", dot="bf16", splits=4, kern=dict(tile_warps=4, tile_bn=64, tile_stages=2))
+# The reference's production knob set (h3/htrc_flat.py:391-392); "triton" selects the HIP kernels.
+
+
+def flat_attention_prod(q, k, v, **over):
+    """Production configuration of the flat operator (h3/htrc_flat.py:397-399)."""
+    return flat_attention(q, k, v, **{**PROD, **over})

@@ -1,0 +1,225 @@
+"""HIP kernel module of the flat operator -- the drop-in for h3/htrc_flat_triton.py.
+
+Every function launches hand-written gfx950 kernels of libhtrc_flat.so through the C ABI
+(include/htrc_flat.h) on the current HIP stream.  No function allocates when a workspace
+dict ``ws`` is given (buffers are reused, as ``_buf`` does in the reference), none
+synchronises, so a whole operator call can be captured in a HIP graph.
+
+Tensors carry a leading head dimension H (2-D inputs are treated as H = 1).  Layouts are
+those of the C ABI: the leaf-value state ``vb`` is stored leaf-quad interleaved
+(``[H, nt, nbp/4, 128, 4]``, see ``vb_natural``) because that is the operand layout of the
+far-field PV MFMA; ``g`` is int8 ``[H, nt, nbp, 128]`` with row scales ``sg``.
+
+Launch-shape knobs of the reference (bt, bl, warps, stages, prec, sel_bn, rb) are
+accepted for call compatibility and ignored: the HIP kernels have fixed MI355X launch
+shapes.  ``prec`` is always IEEE fp32 accumulate (there is no TF32 on CDNA4).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr, stream_handle, nb_pad
+
+TILE = 64
+D = 128
+
+
+def _split(n: int, ns: int, bn: int) -> int:
+    """Per-split range length (h3/htrc_flat_triton.py:297-299)."""
+    per = -(-int(n) // int(ns))
+    return max(int(bn), -(-per // int(bn)) * int(bn))
+
+
+def _buf(ws, name, shape, dtype, device):
+    """Workspace buffer reused across calls, sliced to the requested leading size
+    (h3/htrc_flat_triton.py:302-312)."""
+    if ws is None:
+        return torch.empty(shape, device=device, dtype=dtype)
+    b = ws.get(name)
+    if b is None or b.dtype != dtype or b.shape[1:] != tuple(shape[1:]) or b.shape[0] < shape[0]:
+        b = torch.empty(shape, device=device, dtype=dtype)
+        ws[name] = b
+    return b[: shape[0]]
+
+
+def _heads(x: torch.Tensor) -> torch.Tensor:
+    return x.unsqueeze(0) if x.dim() == 2 else x
+
+
+def _need(t: torch.Tensor, dtype, name: str):
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a HIP device (got {t.device})")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype} (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def pack_q(q: torch.Tensor, tile: int = TILE, ws=None):
+    """Tile centres and row int8 of q and q - mu -> (mu [H,nt,D], q8, sq, dq8, sdq)."""
+    if tile != TILE:
+        raise ValueError("the HIP kernels use 64-row query tiles")
+    q = _heads(q)
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        q = q.float()
+    q = q.contiguous()
+    _need(q, None, "q")
+    h, nq, d = (int(x) for x in q.shape)
+    nt = -(-nq // TILE)
+    dev = q.device
+    mu = _buf(ws, "mu", (h, nt, d), torch.float32, dev)
+    q8 = _buf(ws, "q8", (h, nt * TILE, d), torch.int8, dev)
+    dq8 = _buf(ws, "dq8", (h, nt * TILE, d), torch.int8, dev)
+    sq = _buf(ws, "sq", (h, nt * TILE), torch.float32, dev)
+    sdq = _buf(ws, "sdq", (h, nt * TILE), torch.float32, dev)
+    call("htrc_pack_q", ptr(q), int(q.dtype == torch.bfloat16), h, nq, d, ptr(mu), ptr(q8), ptr(sq),
+         ptr(dq8), ptr(sdq), stream_handle(dev))
+    return mu, q8, sq, dq8, sdq
+
+
+def pack_kv(k: torch.Tensor, v: torch.Tensor, ws=None):
+    """K int8 (round half to even) and key-quad bf16 K / V -> (k8, ks, kq, vq)."""
+    k, v = _heads(k), _heads(v)
+    k = k.to(torch.bfloat16).contiguous()
+    v = v.to(torch.bfloat16).contiguous()
+    _need(k, torch.bfloat16, "k")
+    _need(v, torch.bfloat16, "v")
+    if k.shape != v.shape:
+        raise ValueError("k and v must have the same shape")
+    h, nk, d = (int(x) for x in k.shape)
+    dev = k.device
+    k8 = _buf(ws, "k8", (h, nk, d), torch.int8, dev)
+    ks = _buf(ws, "ks", (h, nk), torch.float32, dev)
+    kq = _buf(ws, "kq", (h, nk // 4, d, 4), torch.bfloat16, dev)
+    vq = _buf(ws, "vq", (h, nk // 4, d, 4), torch.bfloat16, dev)
+    call("htrc_pack_kv", ptr(k), ptr(v), h, nk, d, ptr(k8), ptr(ks), ptr(kq), ptr(vq), stream_handle(dev))
+    return k8, ks, kq, vq
+
+
+def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4, store=torch.int8, ws=None,
+               kq=None, vq=None):
+    """Leaf statistics at the tile centres (h3/htrc_flat_triton.py:329-345, I8 store).
+    mu [H,nt,D] fp32, kf/vf bf16 [H,nk,D] -> (g8, lz, vbq, sg, None) in the reference's
+    (g, lz, vb, sg, sv) order.  kq/vq: key-quad K/V from pack_kv (computed if absent)."""
+    if store != torch.int8:
+        raise ValueError("the HIP leaf statistics store g as int8 (store='int8')")
+    mu = _heads(mu).contiguous()
+    kf = _heads(kf).contiguous()
+    vf = _heads(vf).contiguous()
+    _need(mu, torch.float32, "mu")
+    _need(kf, torch.bfloat16, "k")
+    _need(vf, torch.bfloat16, "v")
+    h, nt, d = (int(x) for x in mu.shape)
+    nk = int(kf.shape[1])
+    if int(nb) * int(leaf) != nk:
+        raise ValueError("key count must equal nb * leaf")
+    if kq is None or vq is None:
+        _, _, kq, vq = pack_kv(kf, vf)
+    nbp = nb_pad(nb)
+    dev = mu.device
+    g8 = _buf(ws, "g", (h, nt, nbp, d), torch.int8, dev)
+    sg = _buf(ws, "sg", (h, nt, nbp), torch.float32, dev)
+    lz = _buf(ws, "lz", (h, nt, nbp), torch.float32, dev)
+    vbq = _buf(ws, "vb", (h, nt, nbp // 4, d, 4), torch.bfloat16, dev)
+    call("htrc_leaf_stats", ptr(mu), ptr(kf), ptr(kq), ptr(vq), h, nt, nk, int(leaf), d, float(scale), ptr(g8),
+         ptr(sg), ptr(vbq), ptr(lz), stream_handle(dev))
+    return g8, lz, vbq, sg, None
+
+
+def rowmax_select(q_c=None, mu_c=None, g=None, lz=None, prec="ieee", bn=32, warps=4, splits=8, stride=1, dot=1,
+                  ws=None, sg=None, *, nb=None, dq8=None, sdq=None):
+    """SEL [H,nt,nbp] (h3/htrc_flat_triton.py:315-326).  Takes the packed rows dq8/sdq
+    (pack_q); when absent they are packed from q_c (fp32 [H,nq,D] rows)."""
+    if dq8 is None or sdq is None:
+        _, _, _, dq8, sdq = pack_q(q_c)
+    g = _heads(g) if g.dim() == 3 else g
+    h, nt, nbp, d = (int(x) for x in g.shape)
+    nb = nbp if nb is None else int(nb)
+    dev = g.device
+    sel = _buf(ws, "sel", (h, nt, nbp), torch.float32, dev)
+    call("htrc_select", ptr(dq8), ptr(sdq), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), d, ptr(sel),
+         stream_handle(dev))
+    return sel
+
+
+def topk_excl(sel, nb: int, kx: int, sink: int = 0, ws=None):
+    """kx largest SEL per tile (leaves < sink forced), idx ascending -> (idx [H,nt,kx] int32,
+    excl [H,nt,nbp] int8)  (h3/htrc_flat.py:262-265)."""
+    h, nt, nbp = (int(x) for x in sel.shape)
+    dev = sel.device
+    idx = _buf(ws, "idx", (h, nt, kx), torch.int32, dev)
+    excl = _buf(ws, "excl", (h, nt, nbp), torch.int8, dev)
+    call("htrc_topk", ptr(sel), h * nt, int(nb), int(kx), int(sink), ptr(idx), ptr(excl), stream_handle(dev))
+    return idx, excl
+
+
+def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, scale: float, splits: int = 4,
+                   bn: int = 64, ws=None, out=None, logz=None):
+    """Far + near online softmax per (tile, split) and the merge
+    (h3/htrc_flat_triton.py:348-391) -> (out [H,nq,D] fp32, logz [H,nq] fp32)."""
+    q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
+    k8, ks, vq = packed["k8"], packed["ks"], packed["vq"]
+    g8, sg, lz, vbq = state["g8"], state["sg"], state["lz"], state["vbq"]
+    h, nk, d = (int(x) for x in k8.shape)
+    nt = -(-nq // TILE)
+    kx = int(idx.shape[-1]) if idx is not None else 0
+    dev = q8.device
+    ns = max(1, int(splits))
+    if out is None:
+        out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
+    if logz is None:
+        logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
+    pm = pl = pacc = None
+    if ns > 1:
+        pm = _buf(ws, "pm", (h, nt, ns, TILE), torch.float32, dev)
+        pl = _buf(ws, "pl", (h, nt, ns, TILE), torch.float32, dev)
+        pacc = _buf(ws, "pacc", (h, nt, ns, TILE, d), torch.float32, dev)
+    call("htrc_tile", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vbq), ptr(excl),
+         ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(vq), h, nq, nk, int(leaf), d, kx, ns, int(bn),
+         float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
+    if ns > 1:
+        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, ns, d, ptr(out), ptr(logz), stream_handle(dev))
+    return out, logz
+
+
+def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: float, sink: int = 0, stride: int = 1,
+          ws=None, out=None, logz=None, idx=None):
+    """Fused select -> top-k -> far + near -> normalised output (one launch per layer call).
+    -> (out [H,nq,D], logz [H,nq]); idx [H,nt,kx] int32 receives the routing when given."""
+    q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
+    k8, ks, vq = packed["k8"], packed["ks"], packed["vq"]
+    g8, sg, lz, vbq = state["g8"], state["sg"], state["lz"], state["vbq"]
+    h, nk, d = (int(x) for x in k8.shape)
+    dev = q8.device
+    if out is None:
+        out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
+    if logz is None:
+        logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
+    call("htrc_route", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vbq), ptr(k8), ptr(ks),
+         ptr(vq), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), float(scale), ptr(out), ptr(logz),
+         ptr(idx), stream_handle(dev))
+    return out, logz
+
+
+def vb_natural(vbq: torch.Tensor, nb: int | None = None) -> torch.Tensor:
+    """Leaf-quad vb [H,nt,nbp/4,D,4] -> natural [H,nt,nb,D] (a view permutation, for checks)."""
+    h, nt, nq4, d, four = (int(x) for x in vbq.shape)
+    nat = vbq.permute(0, 1, 2, 4, 3).reshape(h, nt, nq4 * 4, d)
+    return nat if nb is None else nat[:, :, :nb]
+
+
+def selftest_mfma(ai, bi, af, bf):
+    """Run the MFMA convention self-test kernel -> (ci int32 [16,16], cf fp32 [16,16])."""
+    dev = ai.device
+    ci = torch.empty((16, 16), dtype=torch.int32, device=dev)
+    cf = torch.empty((16, 16), dtype=torch.float32, device=dev)
+    call("htrc_selftest_mfma", ptr(ai), ptr(bi), ptr(ci), ptr(af), ptr(bf), ptr(cf), stream_handle(dev))
+    return ci, cf
+
+
+def library():
+    """The loaded C-ABI library (raises when it is not built)."""
+    return _lib.lib()

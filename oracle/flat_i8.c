@@ -1,0 +1,412 @@
+/*
+ * CPU restatement of the flat-HTRC INT8 attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker.  The product
+ * path (htrc_amd/) never links or calls it.
+ *
+ * Every function restates one step of the reference operator
+ *   h3/htrc_flat.py            (_tiles :142-156, K int8 pack :213-219, top-k :250-265)
+ *   h3/htrc_flat_triton.py     (_stats_kernel :41-85, _tile_kernel :88-211,
+ *                               _rowmax_kernel :214-254, _merge_kernel :257-273,
+ *                               _split :297-299)
+ * in plain IEEE fp32 (built with -ffp-contract=off, no fast-math).  Where the
+ * reference leaves an order open (sums inside tl.dot / tl.sum / torch.mean), this
+ * file fixes one and the HIP kernels follow the same order wherever a boundary is
+ * required to be bit-exact (pack, select, top-k).
+ *
+ * Layouts (per head; the Python wrapper loops over heads):
+ *   q      fp32 [n, d]                 k, v  bf16 bits [nk, d]
+ *   mu     fp32 [nt, d]                q8/dq8 int8 [nt*tile, d], sq/sdq fp32 [nt*tile]
+ *   k8     int8 [nk, d], ks fp32 [nk]
+ *   g8     int8 [nt, nb, d], sg/lz fp32 [nt, nb], vb bf16 bits [nt, nb, d]
+ *   sel    fp32 [nt, nb]; idx int32 [nt, kx] (ascending); excl int8 [nt, nb]
+ *   pm/pl  fp32 [nt, ns, tile]; pacc fp32 [nt, ns, tile, d]
+ *   out    fp32 [nt*tile, d]; logz fp32 [nt*tile]
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* fp32(1/127) = 0x3C010204: the constant the reference multiplies by
+ * (h3/htrc_flat.py:217, h3/htrc_flat_triton.py:76,112,115,231). */
+static const float R127 = 1.0f / 127.0f;
+
+int oracle_abi_version(void) { return 1; }
+
+float oracle_r127(void) { return R127; }
+
+static inline float bf2f(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* fp32 -> bf16 round-to-nearest-even (torch .to(bfloat16), Triton .to(tl.bfloat16)). */
+static inline uint16_t f2bf(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+uint16_t oracle_f2bf(float f) { return f2bf(f); }
+
+/* In-kernel int8 rounding of the reference: where(x >= 0, x + 0.5, x - 0.5).to(int8),
+ * i.e. an fp32 add followed by truncation toward zero
+ * (h3/htrc_flat_triton.py:78-79, 114, 117, 233). */
+static inline int8_t round_away(float x) {
+    float y = x >= 0.0f ? x + 0.5f : x - 0.5f;
+    return (int8_t)(int)truncf(y);
+}
+
+/* K pack rounding: (k / ks).round_().clamp_(-127, 127) -- round half to even
+ * (h3/htrc_flat.py:218). */
+static inline int8_t round_even_clamp(float x) {
+    float y = rintf(x);
+    if (y > 127.0f) y = 127.0f;
+    if (y < -127.0f) y = -127.0f;
+    return (int8_t)(int)y;
+}
+
+/* Per-row symmetric scale max(amax * fp32(1/127), floor); NaN propagates like
+ * torch.clamp_min / tl.maximum do not matter here (inputs are finite). */
+static inline float row_scale(float amax, float floor_) {
+    float s = amax * R127;
+    return s < floor_ ? floor_ : s;
+}
+
+/* K int8 pack, h3/htrc_flat.py:216-218:
+ *   ks = clamp_min(amax_i |k| * fp32(1/127), 1e-20); k8 = clamp(rne(k / ks), +-127). */
+void oracle_pack_k(const uint16_t *k, int64_t nk, int d, int8_t *k8, float *ks) {
+#pragma omp parallel for schedule(static)
+    for (int64_t j = 0; j < nk; ++j) {
+        const uint16_t *row = k + j * d;
+        float amax = 0.0f;
+        for (int i = 0; i < d; ++i) {
+            float a = fabsf(bf2f(row[i]));
+            if (a > amax) amax = a;
+        }
+        float s = row_scale(amax, 1e-20f);
+        ks[j] = s;
+        for (int i = 0; i < d; ++i) k8[j * d + i] = round_even_clamp(bf2f(row[i]) / s);
+    }
+}
+
+/* Tile centres, h3/htrc_flat.py:142-156: mu[t] = mean of the tile's real rows.
+ * Order fixed here: sequential fp32 sum over rows r = 0..nr-1, then IEEE division
+ * by nr (the HIP pack kernel sums in the same order). */
+void oracle_tile_centres(const float *q, int64_t n, int d, int tile, float *mu) {
+    int64_t nt = (n + tile - 1) / tile;
+#pragma omp parallel for schedule(static)
+    for (int64_t t = 0; t < nt; ++t) {
+        int64_t r0 = t * tile;
+        int nr = (int)((n - r0) < tile ? (n - r0) : tile);
+        for (int i = 0; i < d; ++i) {
+            float s = 0.0f;
+            for (int r = 0; r < nr; ++r) s += q[(r0 + r) * d + i];
+            mu[t * d + i] = s / (float)nr;
+        }
+    }
+}
+
+/* Row quantisation of q and dq = q - mu, h3/htrc_flat_triton.py:104-117 (tile kernel)
+ * and :225-233 (rowmax kernel).  Rows are the padded tile rows: row p of tile t reads
+ * query min(p, n-1) (the reference pads by repeating the last row, h3/htrc_flat.py:150-151). */
+void oracle_pack_q(const float *q, int64_t n, int d, int tile, const float *mu,
+                   int8_t *q8, float *sq, int8_t *dq8, float *sdq) {
+    int64_t nt = (n + tile - 1) / tile;
+#pragma omp parallel for schedule(static)
+    for (int64_t p = 0; p < nt * tile; ++p) {
+        int64_t src = p < n ? p : n - 1;
+        const float *row = q + src * d;
+        const float *m = mu + (p / tile) * d;
+        float aq = 0.0f, adq = 0.0f;
+        for (int i = 0; i < d; ++i) {
+            float a = fabsf(row[i]);
+            float b = fabsf(row[i] - m[i]);
+            if (a > aq) aq = a;
+            if (b > adq) adq = b;
+        }
+        float s1 = row_scale(aq, 1e-20f), s2 = row_scale(adq, 1e-20f);
+        sq[p] = s1;
+        sdq[p] = s2;
+        for (int i = 0; i < d; ++i) {
+            q8[p * d + i] = round_away(row[i] / s1);
+            dq8[p * d + i] = round_away((row[i] - m[i]) / s2);
+        }
+    }
+}
+
+/* Leaf statistics at the tile centres, h3/htrc_flat_triton.py:55-85 (I8 store):
+ *   a_s = (mu_t . k_s) * scale; m = max a; w = exp(a - m); z = sum w; w = w / z
+ *   g = (w . K_l) * scale; vb = w . V_l; lz = m + log z
+ *   am = max(max|g|, 1e-30); sg = am * fp32(1/127); g8 = round_away(g * (127 / am))
+ *   vb stored as bf16 (RNE).
+ * Dots are sequential fp32 sums (dims for a, leaf tokens for g / vb). */
+void oracle_stats(const float *mu, int64_t nt, const uint16_t *k, const uint16_t *v,
+                  int64_t nb, int leaf, int d, float scale,
+                  int8_t *g8, float *sg, uint16_t *vb, float *lz) {
+#pragma omp parallel
+    {
+        float *a = (float *)malloc(sizeof(float) * (size_t)leaf);
+        float *kf = (float *)malloc(sizeof(float) * (size_t)leaf * d);
+        float *gs = (float *)malloc(sizeof(float) * (size_t)d);
+        float *vs = (float *)malloc(sizeof(float) * (size_t)d);
+#pragma omp for schedule(static)
+        for (int64_t tl_ = 0; tl_ < nt * nb; ++tl_) {
+            int64_t t = tl_ / nb, l = tl_ % nb;
+            const float *m_ = mu + t * d;
+            const uint16_t *K = k + l * leaf * d;
+            const uint16_t *V = v + l * leaf * d;
+            for (int s = 0; s < leaf * d; ++s) kf[s] = bf2f(K[s]);
+            for (int s = 0; s < leaf; ++s) a[s] = 0.0f;
+            for (int i = 0; i < d; ++i)          /* a[s] summed over i in order, vectorised over s */
+                for (int s = 0; s < leaf; ++s) a[s] += m_[i] * kf[s * d + i];
+            float mx = -INFINITY;
+            for (int s = 0; s < leaf; ++s) {
+                a[s] = a[s] * scale;
+                if (a[s] > mx) mx = a[s];
+            }
+            float z = 0.0f;
+            for (int s = 0; s < leaf; ++s) {
+                a[s] = expf(a[s] - mx);
+                z += a[s];
+            }
+            for (int s = 0; s < leaf; ++s) a[s] = a[s] / z;
+            for (int i = 0; i < d; ++i) gs[i] = vs[i] = 0.0f;
+            for (int s = 0; s < leaf; ++s)       /* summed over tokens in order, vectorised over dims */
+                for (int i = 0; i < d; ++i) {
+                    gs[i] += a[s] * kf[s * d + i];
+                    vs[i] += a[s] * bf2f(V[s * d + i]);
+                }
+            float am = 0.0f;
+            for (int i = 0; i < d; ++i) {
+                gs[i] = gs[i] * scale;
+                float x = fabsf(gs[i]);
+                if (x > am) am = x;
+            }
+            if (am < 1e-30f) am = 1e-30f;
+            float c = 127.0f / am;
+            int8_t *go = g8 + (t * nb + l) * d;
+            uint16_t *vo = vb + (t * nb + l) * d;
+            for (int i = 0; i < d; ++i) {
+                go[i] = round_away(gs[i] * c);
+                vo[i] = f2bf(vs[i]);
+            }
+            sg[t * nb + l] = am * R127;
+            lz[t * nb + l] = mx + logf(z);
+        }
+        free(a);
+        free(kf);
+        free(gs);
+        free(vs);
+    }
+}
+
+static inline int32_t dot_i8(const int8_t *x, const int8_t *y, int d) {
+    int32_t s = 0;
+    for (int i = 0; i < d; ++i) s += (int32_t)x[i] * (int32_t)y[i];
+    return s;
+}
+
+/* Row-max routing score, h3/htrc_flat_triton.py:214-254 (I8):
+ *   SEL[t,l] = max_{r = 0, stride, ..} ( float(dq8_r . g8_tl) * (sdq_r * sg_tl) ) + lz_tl */
+void oracle_select(const int8_t *dq8, const float *sdq, int tile, int stride,
+                   const int8_t *g8, const float *sg, const float *lz,
+                   int64_t nt, int64_t nb, int d, float *sel) {
+    int ts = tile / stride;
+#pragma omp parallel for schedule(static)
+    for (int64_t tl_ = 0; tl_ < nt * nb; ++tl_) {
+        int64_t t = tl_ / nb;
+        const int8_t *g = g8 + tl_ * d;
+        float best = -INFINITY;
+        for (int rr = 0; rr < ts; ++rr) {
+            int64_t p = t * tile + (int64_t)rr * stride;
+            float x = (float)dot_i8(dq8 + p * d, g, d) * (sdq[p] * sg[tl_]);
+            if (x > best) best = x;
+        }
+        sel[tl_] = best + lz[tl_];
+    }
+}
+
+typedef struct {
+    float v;
+    int32_t i;
+} vi_t;
+
+static int cmp_desc(const void *a, const void *b) {
+    const vi_t *x = (const vi_t *)a, *y = (const vi_t *)b;
+    if (x->v > y->v) return -1;
+    if (x->v < y->v) return 1;
+    return (x->i > y->i) - (x->i < y->i);
+}
+
+static int cmp_i32(const void *a, const void *b) {
+    int32_t x = *(const int32_t *)a, y = *(const int32_t *)b;
+    return (x > y) - (x < y);
+}
+
+/* Near-leaf selection, h3/htrc_flat.py:262-265: sink leaves forced to +inf, then the
+ * kx largest SEL per tile; excl[t, idx] = 1.  torch.topk(sorted=False) fixes neither the
+ * order nor ties: here ties go to the lower leaf index and idx is written ascending. */
+void oracle_topk(const float *sel, int64_t nt, int64_t nb, int kx, int sink,
+                 int32_t *idx, int8_t *excl) {
+#pragma omp parallel
+    {
+        vi_t *buf = (vi_t *)malloc(sizeof(vi_t) * (size_t)nb);
+#pragma omp for schedule(static)
+        for (int64_t t = 0; t < nt; ++t) {
+            for (int64_t l = 0; l < nb; ++l) {
+                buf[l].v = l < sink ? INFINITY : sel[t * nb + l];
+                buf[l].i = (int32_t)l;
+            }
+            qsort(buf, (size_t)nb, sizeof(vi_t), cmp_desc);
+            int32_t *o = idx + t * kx;
+            for (int j = 0; j < kx; ++j) o[j] = buf[j].i;
+            qsort(o, (size_t)kx, sizeof(int32_t), cmp_i32);
+            memset(excl + t * nb, 0, (size_t)nb);
+            for (int j = 0; j < kx; ++j) excl[t * nb + o[j]] = 1;
+        }
+        free(buf);
+    }
+}
+
+/* _split, h3/htrc_flat_triton.py:297-299. */
+int64_t oracle_split(int64_t n, int64_t ns, int64_t bn) {
+    int64_t per = (n + ns - 1) / ns;
+    int64_t r = (per + bn - 1) / bn * bn;
+    return r > bn ? r : bn;
+}
+
+/* One online-softmax block update, h3/htrc_flat_triton.py:143-157 / :177-186:
+ *   m_new = max(m, max sc); m_s = m_new == -inf ? 0 : m_new; p = exp(sc - m_s)
+ *   alpha = exp(m - m_s); l = l * alpha + sum p; acc = acc * alpha + bf16(p) . V. */
+static void block_update(const float *sc, const uint16_t *const *vals, int nc, int d,
+                         float *m, float *l, float *acc, float *dacc) {
+    float bm = -INFINITY;
+    for (int c = 0; c < nc; ++c)
+        if (sc[c] > bm) bm = sc[c];
+    float m_new = *m > bm ? *m : bm;
+    float m_s = (m_new == -INFINITY) ? 0.0f : m_new;
+    float psum = 0.0f;
+    for (int i = 0; i < d; ++i) dacc[i] = 0.0f;
+    for (int c = 0; c < nc; ++c) {
+        float p = expf(sc[c] - m_s);
+        psum += p;
+        if (vals[c] == NULL) continue;
+        float pb = bf2f(f2bf(p));
+        for (int i = 0; i < d; ++i) dacc[i] += pb * bf2f(vals[c][i]);
+    }
+    float alpha = expf(*m - m_s);
+    *l = *l * alpha + psum;
+    for (int i = 0; i < d; ++i) acc[i] = acc[i] * alpha + dacc[i];
+    *m = m_new;
+}
+
+/* Split-K tile kernel, h3/htrc_flat_triton.py:95-211 (DOT=1, I8=1, GR=1, no tail):
+ * program (t, sp) covers far leaves [sp*lps, +lps) not excluded and exact tokens
+ * [sp*eps, +eps) of the tile's kx selected leaves (tok = idx[t, j / leaf] * leaf + j % leaf).
+ *   far  score  float(dq8 . g8) * (sdq * sg) + lz,  value vb (bf16)
+ *   near score  float(q8 . k8)  * ((sq * ks) * scale), value v (bf16)
+ * Writes the partial (m, l, acc) of every (tile, split, row). */
+void oracle_tile(int64_t nt, int tile, int d, int64_t nb, int leaf, int kx,
+                 const int32_t *idx, const int8_t *excl,
+                 const int8_t *q8, const float *sq, const int8_t *dq8, const float *sdq,
+                 const int8_t *g8, const float *sg, const float *lz, const uint16_t *vb,
+                 const int8_t *k8, const float *ks, const uint16_t *v,
+                 float scale, int ns, int bn, float *pm, float *pl, float *pacc) {
+    int64_t lps = oracle_split(nb, ns, bn);
+    int64_t eps = oracle_split((int64_t)kx * leaf, ns, bn);
+#pragma omp parallel
+    {
+        float *sc = (float *)malloc(sizeof(float) * (size_t)bn);
+        const uint16_t **vals = (const uint16_t **)malloc(sizeof(void *) * (size_t)bn);
+        float *acc = (float *)malloc(sizeof(float) * (size_t)d);
+        float *dacc = (float *)malloc(sizeof(float) * (size_t)d);
+#pragma omp for schedule(static)
+        for (int64_t job = 0; job < nt * ns * tile; ++job) {
+            int64_t t = job / ((int64_t)ns * tile);
+            int sp = (int)((job / tile) % ns);
+            int r = (int)(job % tile);
+            int64_t p = t * tile + r;
+            float m = -INFINITY, l = 0.0f;
+            for (int i = 0; i < d; ++i) acc[i] = 0.0f;
+            int64_t lo = sp * lps, hi = lo + lps < nb ? lo + lps : nb;
+            for (int64_t n0 = lo; n0 < hi; n0 += bn) {
+                for (int c = 0; c < bn; ++c) {
+                    int64_t cc = n0 + c;
+                    if (cc < hi && excl[t * nb + cc] == 0) {
+                        int64_t s = t * nb + cc;
+                        sc[c] = (float)dot_i8(dq8 + p * d, g8 + s * d, d) * (sdq[p] * sg[s]) + lz[s];
+                        vals[c] = vb + s * d;
+                    } else {
+                        sc[c] = -INFINITY;
+                        vals[c] = NULL;
+                    }
+                }
+                block_update(sc, vals, bn, d, &m, &l, acc, dacc);
+            }
+            int64_t e_n = (int64_t)kx * leaf;
+            int64_t e_lo = sp * eps, e_hi = e_lo + eps < e_n ? e_lo + eps : e_n;
+            for (int64_t e0 = e_lo; e0 < e_hi; e0 += bn) {
+                for (int c = 0; c < bn; ++c) {
+                    int64_t j = e0 + c;
+                    if (j < e_hi) {
+                        int64_t tok = (int64_t)idx[t * kx + j / leaf] * leaf + j % leaf;
+                        sc[c] = (float)dot_i8(q8 + p * d, k8 + tok * d, d) * ((sq[p] * ks[tok]) * scale);
+                        vals[c] = v + tok * d;
+                    } else {
+                        sc[c] = -INFINITY;
+                        vals[c] = NULL;
+                    }
+                }
+                block_update(sc, vals, bn, d, &m, &l, acc, dacc);
+            }
+            int64_t base = (t * ns + sp) * tile + r;
+            pm[base] = m;
+            pl[base] = l;
+            memcpy(pacc + base * d, acc, sizeof(float) * (size_t)d);
+        }
+        free(sc);
+        free(vals);
+        free(acc);
+        free(dacc);
+    }
+}
+
+/* Split merge, h3/htrc_flat_triton.py:257-273, plus the log-partition of the row
+ * (logz = mm + log den), which the reference computes but discards. */
+void oracle_merge(const float *pm, const float *pl, const float *pacc, int64_t nt, int ns,
+                  int tile, int d, float *out, float *logz) {
+#pragma omp parallel
+    {
+        float *num = (float *)malloc(sizeof(float) * (size_t)d);
+#pragma omp for schedule(static)
+        for (int64_t tr = 0; tr < nt * tile; ++tr) {
+            int64_t t = tr / tile;
+            int r = (int)(tr % tile);
+            float mm = -INFINITY;
+            for (int s = 0; s < ns; ++s) {
+                float x = pm[(t * ns + s) * tile + r];
+                if (x > mm) mm = x;
+            }
+            if (mm == -INFINITY) mm = 0.0f;
+            float den = 0.0f;
+            for (int i = 0; i < d; ++i) num[i] = 0.0f;
+            for (int s = 0; s < ns; ++s) {
+                int64_t b = (t * ns + s) * tile + r;
+                float w = expf(pm[b] - mm);
+                den += pl[b] * w;
+                for (int i = 0; i < d; ++i) num[i] += pacc[b * d + i] * w;
+            }
+            float dd = den < 1e-30f ? 1e-30f : den;
+            for (int i = 0; i < d; ++i) out[tr * d + i] = num[i] / dd;
+            logz[tr] = mm + logf(den);
+        }
+        free(num);
+    }
+}

@@ -1,0 +1,212 @@
+"""ctypes front end of the C oracle ``flat_i8.c`` -- TEST INFRASTRUCTURE ONLY.
+
+Each function wraps one stage of the reference INT8 path and works on one head
+(NumPy arrays, bf16 as uint16 bits).  ``flat_i8`` chains the stages the way
+``_flat_triton`` does (h3/htrc_flat.py:181-276) with the PROD knobs
+(h3/htrc_flat.py:391-392): store="int8", dot="bf16", curvature="lin",
+order="seq", group=1.  Tiles are independent, so ``tile_chunk`` does not enter.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from pathlib import Path
+
+import numpy as np
+
+from . import bf16
+
+_HERE = Path(__file__).resolve().parent
+_LIBNAME = "liboracle_flat.so"
+_lib = None
+
+_F32 = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_I8 = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_U16 = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_I32 = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_flt = ctypes.c_float
+
+
+def build() -> Path:
+    """Compile the oracle with its Makefile (gcc, IEEE fp32, no contraction)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", str(_HERE), "-B", _LIBNAME], check=True)
+    return _HERE / _LIBNAME
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        path = _HERE / _LIBNAME
+        if not path.exists():
+            raise RuntimeError(f"oracle library {path} is not built: run `make -C {_HERE}`")
+        L = ctypes.CDLL(str(path))
+        L.oracle_abi_version.restype = _int
+        L.oracle_r127.restype = _flt
+        L.oracle_f2bf.restype = ctypes.c_uint16
+        L.oracle_f2bf.argtypes = [_flt]
+        L.oracle_split.restype = _i64
+        L.oracle_split.argtypes = [_i64, _i64, _i64]
+        L.oracle_pack_k.argtypes = [_U16, _i64, _int, _I8, _F32]
+        L.oracle_tile_centres.argtypes = [_F32, _i64, _int, _int, _F32]
+        L.oracle_pack_q.argtypes = [_F32, _i64, _int, _int, _F32, _I8, _F32, _I8, _F32]
+        L.oracle_stats.argtypes = [_F32, _i64, _U16, _U16, _i64, _int, _int, _flt,
+                                   _I8, _F32, _U16, _F32]
+        L.oracle_select.argtypes = [_I8, _F32, _int, _int, _I8, _F32, _F32, _i64, _i64, _int, _F32]
+        L.oracle_topk.argtypes = [_F32, _i64, _i64, _int, _int, _I32, _I8]
+        L.oracle_tile.argtypes = [_i64, _int, _int, _i64, _int, _int, _I32, _I8,
+                                  _I8, _F32, _I8, _F32, _I8, _F32, _F32, _U16,
+                                  _I8, _F32, _U16, _flt, _int, _int, _F32, _F32, _F32]
+        L.oracle_merge.argtypes = [_F32, _F32, _F32, _i64, _int, _int, _int, _F32, _F32]
+        _lib = L
+    return _lib
+
+
+def _c(x, dt):
+    return np.ascontiguousarray(x, dtype=dt)
+
+
+def r127() -> float:
+    return float(lib().oracle_r127())
+
+
+def split(n: int, ns: int, bn: int) -> int:
+    """_split (h3/htrc_flat_triton.py:297-299)."""
+    return int(lib().oracle_split(n, ns, bn))
+
+
+def pack_k(k_bits: np.ndarray):
+    """K int8 pack (h3/htrc_flat.py:216-218) -> (k8 int8 [nk,d], ks f32 [nk])."""
+    k_bits = _c(k_bits, np.uint16)
+    nk, d = k_bits.shape
+    k8 = np.empty((nk, d), np.int8)
+    ks = np.empty((nk,), np.float32)
+    lib().oracle_pack_k(k_bits, nk, d, k8, ks)
+    return k8, ks
+
+
+def tile_centres(q: np.ndarray, tile: int) -> np.ndarray:
+    """mu [nt, d] over the real rows of every tile (h3/htrc_flat.py:142-156)."""
+    q = _c(q, np.float32)
+    n, d = q.shape
+    nt = -(-n // tile)
+    mu = np.empty((nt, d), np.float32)
+    lib().oracle_tile_centres(q, n, d, tile, mu)
+    return mu
+
+
+def pack_q(q: np.ndarray, tile: int, mu: np.ndarray):
+    """Row int8 of q and q - mu over the padded tile rows (h3/htrc_flat_triton.py:104-117)."""
+    q = _c(q, np.float32)
+    n, d = q.shape
+    nt = -(-n // tile)
+    rows = nt * tile
+    q8 = np.empty((rows, d), np.int8)
+    dq8 = np.empty((rows, d), np.int8)
+    sq = np.empty((rows,), np.float32)
+    sdq = np.empty((rows,), np.float32)
+    lib().oracle_pack_q(q, n, d, tile, _c(mu, np.float32), q8, sq, dq8, sdq)
+    return q8, sq, dq8, sdq
+
+
+def stats(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int, scale: float):
+    """Leaf statistics (h3/htrc_flat_triton.py:41-85, I8 store)
+    -> g8 int8 [nt,nb,d], sg f32 [nt,nb], vb bf16 bits [nt,nb,d], lz f32 [nt,nb]."""
+    mu = _c(mu, np.float32)
+    k_bits, v_bits = _c(k_bits, np.uint16), _c(v_bits, np.uint16)
+    nt, d = mu.shape
+    nb = k_bits.shape[0] // leaf
+    g8 = np.empty((nt, nb, d), np.int8)
+    vb = np.empty((nt, nb, d), np.uint16)
+    sg = np.empty((nt, nb), np.float32)
+    lz = np.empty((nt, nb), np.float32)
+    lib().oracle_stats(mu, nt, k_bits, v_bits, nb, leaf, d, float(scale), g8, sg, vb, lz)
+    return g8, sg, vb, lz
+
+
+def select(dq8, sdq, tile: int, g8, sg, lz, stride: int = 1) -> np.ndarray:
+    """SEL [nt, nb] (h3/htrc_flat_triton.py:214-254, I8)."""
+    g8 = _c(g8, np.int8)
+    nt, nb, d = g8.shape
+    sel = np.empty((nt, nb), np.float32)
+    lib().oracle_select(_c(dq8, np.int8), _c(sdq, np.float32), tile, stride, g8,
+                        _c(sg, np.float32), _c(lz, np.float32), nt, nb, d, sel)
+    return sel
+
+
+def topk(sel: np.ndarray, kx: int, sink: int = 0):
+    """Near leaves (h3/htrc_flat.py:262-265) -> idx int32 [nt,kx] ascending, excl int8 [nt,nb]."""
+    sel = _c(sel, np.float32)
+    nt, nb = sel.shape
+    idx = np.empty((nt, max(kx, 0)), np.int32)
+    excl = np.zeros((nt, nb), np.int8)
+    if kx > 0:
+        lib().oracle_topk(sel, nt, nb, kx, sink, idx, excl)
+    return idx, excl
+
+
+def tile_partials(st: dict, *, tile: int, leaf: int, scale: float, splits: int, bn: int):
+    """Split partials (pm, pl, pacc) of the tile kernel (h3/htrc_flat_triton.py:88-211)."""
+    g8 = st["g8"]
+    nt, nb, d = g8.shape
+    kx = st["idx"].shape[1]
+    idx = st["idx"] if kx else np.zeros((nt, 1), np.int32)
+    ns = max(1, int(splits))
+    pm = np.empty((nt, ns, tile), np.float32)
+    pl = np.empty((nt, ns, tile), np.float32)
+    pacc = np.empty((nt, ns, tile, d), np.float32)
+    lib().oracle_tile(nt, tile, d, nb, leaf, kx, _c(idx, np.int32), _c(st["excl"], np.int8),
+                      _c(st["q8"], np.int8), _c(st["sq"], np.float32),
+                      _c(st["dq8"], np.int8), _c(st["sdq"], np.float32),
+                      _c(g8, np.int8), _c(st["sg"], np.float32), _c(st["lz"], np.float32),
+                      _c(st["vb"], np.uint16), _c(st["k8"], np.int8), _c(st["ks"], np.float32),
+                      _c(st["v"], np.uint16), float(scale), ns, int(bn), pm, pl, pacc)
+    return pm, pl, pacc
+
+
+def merge(pm, pl, pacc):
+    """Merge of split partials (h3/htrc_flat_triton.py:257-273) -> out [nt*T,d], logz [nt*T]."""
+    pm, pl, pacc = _c(pm, np.float32), _c(pl, np.float32), _c(pacc, np.float32)
+    nt, ns, tile, d = pacc.shape
+    out = np.empty((nt * tile, d), np.float32)
+    logz = np.empty((nt * tile,), np.float32)
+    lib().oracle_merge(pm, pl, pacc, nt, ns, tile, d, out, logz)
+    return out, logz
+
+
+def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: int = 64,
+            splits: int = 4, bn: int = 64, sel_stride: int = 1, sink_leaves: int = 0,
+            scale: float | None = None, keep: bool = True) -> dict:
+    """The INT8 flat operator for one head: q float32 (or bf16 bits) [n,d], k/v bf16 bits
+    [nk,d] with nk % leaf == 0.  Returns every intermediate plus out [n,d] and logz [n]."""
+    q = np.asarray(q)
+    qf = bf16.to_f32(q) if q.dtype == np.uint16 else _c(q, np.float32)
+    n, d = qf.shape
+    nk = k_bits.shape[0]
+    if nk % leaf:
+        raise ValueError("key count must be a multiple of the leaf size")
+    nb = nk // leaf
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    sink = max(0, min(int(sink_leaves), nb))
+    kx = min(int(exact_leaves) + sink, nb)
+    st: dict = {"v": _c(v_bits, np.uint16)}
+    st["k8"], st["ks"] = pack_k(k_bits)
+    st["mu"] = tile_centres(qf, tile)
+    st["q8"], st["sq"], st["dq8"], st["sdq"] = pack_q(qf, tile, st["mu"])
+    st["g8"], st["sg"], st["vb"], st["lz"] = stats(st["mu"], k_bits, v_bits, leaf, scale)
+    if kx > 0:
+        st["sel"] = select(st["dq8"], st["sdq"], tile, st["g8"], st["sg"], st["lz"], sel_stride)
+        st["idx"], st["excl"] = topk(st["sel"], kx, sink)
+    else:
+        nt = st["mu"].shape[0]
+        st["idx"] = np.zeros((nt, 0), np.int32)
+        st["excl"] = np.zeros((nt, nb), np.int8)
+    pm, pl, pacc = tile_partials(st, tile=tile, leaf=leaf, scale=scale, splits=splits, bn=bn)
+    out, logz = merge(pm, pl, pacc)
+    st["out"], st["logz"] = out[:n], logz[:n]
+    if keep:
+        st["pm"], st["pl"], st["pacc"] = pm, pl, pacc
+    return st

@@ -1,0 +1,224 @@
+"""GPU parity of every kernel boundary against the CPU oracle (run on the MI355X box).
+
+Bit-exact: MFMA integer path, pack (mu, q8, sq, dq8, sdq, k8, ks, key-quad copies),
+select (given the oracle's stats), top-k (given SEL).  Tolerance: leaf statistics
+(bf16-split MFMA vs the oracle's sequential fp32), tile/merge/route outputs
+(rel-L2 <= 1e-2 and |dlogZ| <= 1e-3, the operator's stated bar).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits, from_bits, key_quads, rel_l2, vb_to_quads
+from htrc_amd import htrc_flat_hip as hip
+from htrc_amd import workloads
+from htrc_amd._lib import nb_pad
+from oracle import bf16, flat_i8
+
+pytestmark = pytest.mark.gpu
+
+OUT_REL_L2 = 1e-2
+LOGZ_ABS = 1e-3
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def test_mfma_conventions(device):
+    rng = np.random.default_rng(3)
+    ai = rng.integers(-128, 128, (16, 64), dtype=np.int8)
+    bi = rng.integers(-128, 128, (64, 16), dtype=np.int8)
+    af = bf16.from_f32(rng.standard_normal((16, 32)).astype(np.float32))
+    bfm = bf16.from_f32(rng.standard_normal((32, 16)).astype(np.float32))
+    ci, cf = hip.selftest_mfma(torch.from_numpy(ai).to(device), torch.from_numpy(bi).to(device),
+                               torch.from_numpy(af.view(np.int16)).to(device),
+                               torch.from_numpy(bfm.view(np.int16)).to(device))
+    torch.cuda.synchronize()
+    assert np.array_equal(_np(ci), ai.astype(np.int64) @ bi.astype(np.int64))
+    ref = bf16.to_f32(af).astype(np.float64) @ bf16.to_f32(bfm).astype(np.float64)
+    np.testing.assert_allclose(_np(cf), ref, rtol=1e-5, atol=1e-5)
+
+
+def _data(n, nk=None, runs=None, seed=0, heads=1):
+    q, k, v = workloads.clustered_runs(n=max(n, nk or n), runs=runs or max(1, max(n, nk or n) // 64),
+                                       heads=heads, seed=seed)
+    return q[:, :n].contiguous(), k[:, : (nk or n)].contiguous(), v[:, : (nk or n)].contiguous()
+
+
+@pytest.mark.parametrize("nq", [4096, 1000, 64, 1])
+@pytest.mark.parametrize("qdtype", ["bf16", "fp32"])
+def test_pack_bitexact(device, nq, qdtype):
+    q, k, v = _data(max(nq, 256), nk=256, seed=nq)
+    q = q[:, :nq]
+    if qdtype == "fp32":   # non-bf16 fp32 rows exercise the centre division and the q rounding
+        q = q.float() + 1e-3 * torch.randn(q.shape, generator=torch.Generator().manual_seed(7))
+    qd = q.to(device).contiguous()
+    mu, q8, sq, dq8, sdq = hip.pack_q(qd)
+    k8, ks, kq, vq = hip.pack_kv(k.to(device), v.to(device))
+    torch.cuda.synchronize()
+    qf = q[0].float().numpy()
+    omu = flat_i8.tile_centres(qf, 64)
+    oq8, osq, odq8, osdq = flat_i8.pack_q(qf, 64, omu)
+    ok8, oks = flat_i8.pack_k(bits(k[0]))
+    assert np.array_equal(_np(mu[0]).view(np.uint32), omu.view(np.uint32))
+    assert np.array_equal(_np(q8[0]), oq8)
+    assert np.array_equal(_np(dq8[0]), odq8)
+    assert np.array_equal(_np(sq[0]).view(np.uint32), osq.view(np.uint32))
+    assert np.array_equal(_np(sdq[0]).view(np.uint32), osdq.view(np.uint32))
+    assert np.array_equal(_np(k8[0]), ok8)
+    assert np.array_equal(_np(ks[0]).view(np.uint32), oks.view(np.uint32))
+    assert np.array_equal(bits(kq[0]).reshape(-1), key_quads(bits(k[0])).reshape(-1))
+    assert np.array_equal(bits(vq[0]).reshape(-1), key_quads(bits(v[0])).reshape(-1))
+
+
+def test_pack_edge_rows(device):
+    """All-zero rows (scale floor 1e-20), exact .5 ties, and huge/tiny magnitudes."""
+    d = 128
+    rows = np.zeros((64, d), np.float32)
+    rows[1] = np.linspace(-127, 127, d)             # integer grid: x/s lands on ties after scaling
+    rows[2, :] = 0.5
+    rows[2, 0] = 127.0
+    rows[3] = np.float32(1e-30)
+    rows[4, ::2] = 3e38
+    rows[5] = -np.arange(d, dtype=np.float32) / 4
+    kb = bf16.from_f32(rows)
+    qd = torch.from_numpy(bf16.to_f32(kb)).to(device)
+    kd = from_bits(kb, device)
+    mu, q8, sq, dq8, sdq = hip.pack_q(qd)
+    k8, ks, kq, vq = hip.pack_kv(kd, kd)
+    torch.cuda.synchronize()
+    qf = bf16.to_f32(kb)
+    omu = flat_i8.tile_centres(qf, 64)
+    oq8, osq, odq8, osdq = flat_i8.pack_q(qf, 64, omu)
+    ok8, oks = flat_i8.pack_k(kb)
+    assert np.array_equal(_np(q8[0]), oq8) and np.array_equal(_np(dq8[0]), odq8)
+    assert np.array_equal(_np(sq[0]).view(np.uint32), osq.view(np.uint32))
+    assert np.array_equal(_np(k8[0]), ok8) and np.array_equal(_np(ks[0]).view(np.uint32), oks.view(np.uint32))
+
+
+def _oracle_state(q, k, v, leaf, ex, splits=4, bn=64, stride=1, sink=0):
+    return flat_i8.flat_i8(bits(q[0]) if q.dtype == torch.bfloat16 else q[0].numpy(), bits(k[0]), bits(v[0]),
+                           tile=64, leaf=leaf, exact_leaves=ex, splits=splits, bn=bn, sel_stride=stride,
+                           sink_leaves=sink)
+
+
+@pytest.mark.parametrize("leaf", [64, 32, 128, 16])
+def test_stats_close_to_oracle(device, leaf):
+    n = 2048
+    q, k, v = _data(n, seed=leaf)
+    ref = _oracle_state(q, k, v, leaf, 4)
+    nb = n // leaf
+    mu = torch.from_numpy(ref["mu"])[None].to(device)
+    g8, lz, vbq, sg, _ = hip.leaf_stats(mu, k.to(device), v.to(device), nb, 1 / math.sqrt(128), leaf=leaf)
+    torch.cuda.synchronize()
+    nbp = nb_pad(nb)
+    g = _np(g8[0])[:, :nb].astype(np.int32)
+    og = ref["g8"].astype(np.int32)
+    diff = np.abs(g - og)
+    assert diff.max() <= 1
+    assert (diff > 0).mean() < 2e-3, f"g8 mismatch fraction {(diff > 0).mean():.2e}"
+    np.testing.assert_allclose(_np(lz[0])[:, :nb], ref["lz"], rtol=0, atol=2e-5 * (1 + np.abs(ref["lz"]).max()))
+    np.testing.assert_allclose(_np(sg[0])[:, :nb], ref["sg"], rtol=1e-5, atol=0)
+    vb = bf16.to_f32(bits(hip.vb_natural(vbq, nb)[0].contiguous()))
+    ovb = bf16.to_f32(ref["vb"])
+    assert np.abs(vb - ovb).max() <= 2 ** -7 * np.abs(ovb).max()
+    assert (vb != ovb).mean() < 2e-2
+    # padded leaves: empty state
+    if nbp > nb:
+        assert np.all(_np(lz[0])[:, nb:] == -np.inf) and np.all(_np(g8[0])[:, nb:] == 0)
+
+
+def test_select_bitexact_on_oracle_state(device):
+    n, leaf = 4096, 64
+    q, k, v = _data(n, seed=11)
+    ref = _oracle_state(q, k, v, leaf, 8)
+    nt, nb, d = ref["g8"].shape
+    nbp = nb_pad(nb)
+    g8 = np.zeros((1, nt, nbp, d), np.int8)
+    g8[0, :, :nb] = ref["g8"]
+    sg = np.zeros((1, nt, nbp), np.float32)
+    sg[0, :, :nb] = ref["sg"]
+    lz = np.full((1, nt, nbp), -np.inf, np.float32)
+    lz[0, :, :nb] = ref["lz"]
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    for stride in (1, 4):
+        sel = hip.rowmax_select(g=T(g8), lz=T(lz), sg=T(sg), stride=stride, nb=nb, dq8=T(ref["dq8"][None]),
+                                sdq=T(ref["sdq"][None]))
+        torch.cuda.synchronize()
+        osel = flat_i8.select(ref["dq8"], ref["sdq"], 64, ref["g8"], ref["sg"], ref["lz"], stride)
+        assert np.array_equal(_np(sel[0])[:, :nb].view(np.uint32), osel.view(np.uint32)), f"stride {stride}"
+
+
+@pytest.mark.parametrize("nb,kx,sink", [(1008, 32, 0), (256, 16, 3), (37, 37, 0), (100, 1, 0), (8192, 64, 0)])
+def test_topk_bitexact(device, nb, kx, sink):
+    rng = np.random.default_rng(nb + kx)
+    rows = 24
+    sel = rng.standard_normal((rows, nb)).astype(np.float32)
+    sel[:, ::7] = np.float32(0.25)                  # heavy ties across the threshold
+    sel[0, :] = 1.0                                 # a row of all ties
+    sel[1, :5] = -0.0
+    nbp = nb_pad(nb)
+    pad = np.zeros((1, rows, nbp), np.float32)
+    pad[0, :, :nb] = sel
+    idx, excl = hip.topk_excl(torch.from_numpy(pad).to(device), nb, kx, sink)
+    torch.cuda.synchronize()
+    oidx, oexcl = flat_i8.topk(sel, kx, sink)
+    assert np.array_equal(_np(idx[0]), oidx)
+    assert np.array_equal(_np(excl[0])[:, :nb], oexcl)
+    assert np.all(_np(excl[0])[:, nb:] == 0)
+
+
+def _device_state(ref, q, k, v, device):
+    nt, nb, d = ref["g8"].shape
+    nbp = nb_pad(nb)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    g8 = np.zeros((1, nt, nbp, d), np.int8)
+    g8[0, :, :nb] = ref["g8"]
+    sg = np.zeros((1, nt, nbp), np.float32)
+    sg[0, :, :nb] = ref["sg"]
+    lz = np.full((1, nt, nbp), -np.inf, np.float32)
+    lz[0, :, :nb] = ref["lz"]
+    excl = np.zeros((1, nt, nbp), np.int8)
+    excl[0, :, :nb] = ref["excl"]
+    vbq = vb_to_quads(ref["vb"], nbp)[None]
+    packed = {"q8": T(ref["q8"][None]), "sq": T(ref["sq"][None]), "dq8": T(ref["dq8"][None]),
+              "sdq": T(ref["sdq"][None]), "k8": T(ref["k8"][None]), "ks": T(ref["ks"][None]),
+              "vq": from_bits(key_quads(bits(v[0]))[None], device)}
+    state = {"g8": T(g8), "sg": T(sg), "lz": T(lz), "vbq": from_bits(vbq, device)}
+    return packed, state, T(excl), T(ref["idx"][None])
+
+
+@pytest.mark.parametrize("splits,bn", [(1, 64), (4, 64), (3, 32), (8, 128)])
+def test_tile_merge_on_oracle_state(device, splits, bn):
+    n, leaf, ex = 4096, 64, 8
+    q, k, v = _data(n, seed=5)
+    ref = _oracle_state(q, k, v, leaf, ex, splits=splits, bn=bn)
+    packed, state, excl, idx = _device_state(ref, q, k, v, device)
+    out, logz = hip.tile_attention(packed, state, excl, idx, nq=n, leaf=leaf, scale=1 / math.sqrt(128),
+                                   splits=splits, bn=bn)
+    torch.cuda.synchronize()
+    assert rel_l2(_np(out[0]), ref["out"]) <= OUT_REL_L2
+    assert np.abs(_np(logz[0]) - ref["logz"]).max() <= LOGZ_ABS
+
+
+@pytest.mark.parametrize("leaf,ex", [(64, 8), (32, 16), (16, 40), (128, 4), (64, 0), (64, 64)])
+def test_route_on_oracle_state(device, leaf, ex):
+    n = 4096
+    q, k, v = _data(n, seed=leaf + ex)
+    ref = _oracle_state(q, k, v, leaf, ex, splits=1, bn=64)
+    packed, state, _, _ = _device_state(ref, q, k, v, device)
+    kx = ref["idx"].shape[1]
+    nt = ref["g8"].shape[0]
+    idx = torch.full((1, nt, max(kx, 1)), -1, dtype=torch.int32, device=device)
+    out, logz = hip.route(packed, state, nq=n, leaf=leaf, kx=kx, scale=1 / math.sqrt(128),
+                          idx=idx if kx else None)
+    torch.cuda.synchronize()
+    if kx:
+        assert np.array_equal(_np(idx[0]), ref["idx"])
+    assert rel_l2(_np(out[0]), ref["out"]) <= OUT_REL_L2
+    assert np.abs(_np(logz[0]) - ref["logz"]).max() <= LOGZ_ABS
