@@ -1,0 +1,200 @@
+"""Benchmark of the MI355X flat-HTRC layer (BASELINE configuration 3 by default).
+
+One step = one flat-HTRC layer call: B=1, H=24, N=64512, d=128, leaf 64, 32 near leaves,
+int8 Q/K + bf16 PV, on synthetic clustered video-region inputs already resident in HBM.
+Prints ONE JSON line (the driver's contract) with the layer ms/call, the roofline of the
+dominant kernel (HIP events on the launch stream, algorithmic bytes or ops per launch),
+per-kernel figures, and the reference's CPU path (NumPy restatement of the torch backend
+_flat, h3/htrc_flat.py:279-388) timed on a bounded sample of the same workload.
+
+  python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--config cfg3] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "flat-HTRC layer ms/call @B1 H24 N64512 d128; % MFMA peak, HBM GB/s"
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, GB/s
+PEAK_I8_TOPS = 5000.0          # dense int8 MFMA, TOP/s
+PEAK_BF16_TFLOPS = 2500.0      # dense bf16 MFMA, TFLOP/s
+
+
+def algorithmic(h, nq, nk, leaf, kx, d=128, tile=64):
+    """Per-launch algorithmic HBM bytes and MFMA ops of every kernel of one layer call."""
+    nt = -(-nq // tile)
+    nb = nk // leaf
+    rows = nt * tile
+    f = {}
+    f["pack_q"] = {"bytes": h * (2 * nq * d + 2 * rows * d + 8 * rows + 4 * nt * d)}
+    f["pack_kv"] = {"bytes": h * (4 * nk * d + nk * d + 4 * nk + 4 * nk * d)}
+    f["stats"] = {"bytes": h * (4 * nk * d + nt * nb * (3 * d + 8)),
+                  "flops_fp32": h * 6 * nt * nk * d}
+    state = nt * nb * (3 * d + 8)
+    f["route"] = {"bytes": h * (state + 2 * rows * d + 8 * rows + nk * (3 * d + 4) + 4 * nq * (d + 1)),
+                  "i8_ops": h * (2 * rows * nb * d * 2 + 2 * rows * kx * leaf * d),
+                  "bf16_flops": h * (2 * rows * nb * d + 2 * rows * kx * leaf * d)}
+    return f
+
+
+def roofline_entry(name, ms, fig):
+    s = ms * 1e-3
+    e = {"kernel": name, "ms": round(ms, 4)}
+    gbs = fig["bytes"] / s / 1e9
+    e["hbm_GBps"] = round(gbs, 1)
+    e["hbm_frac"] = round(gbs / PEAK_HBM_GBS, 4)
+    t_hbm = fig["bytes"] / (PEAK_HBM_GBS * 1e9)
+    t_mfma = 0.0
+    if "i8_ops" in fig:
+        t_mfma = fig["i8_ops"] / (PEAK_I8_TOPS * 1e12) + fig["bf16_flops"] / (PEAK_BF16_TFLOPS * 1e12)
+        e["mfma_frac"] = round(t_mfma / s, 4)
+    e["bound"] = "mfma" if t_mfma > t_hbm else "hbm"
+    e["ideal_ms"] = round(max(t_hbm, t_mfma) * 1e3, 4)
+    return e
+
+
+def cpu_baseline(name, budget_s=10.0):
+    """Reference CPU path (NumPy restatement of _flat) on whole heads until budget_s has
+    elapsed; extrapolated to the layer's head count."""
+    import numpy as np
+    from htrc_amd import workloads
+    from oracle import flat_fp32
+    gen, kw, leaf, ex, heads = workloads.CONFIGS[name]
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        threads = os.cpu_count() or 1
+    done, elapsed = 0, 0.0
+    seed = 0
+    while done < heads and (elapsed < budget_s or done == 0):
+        q, k, v, _, _ = workloads.make(name, seed=1000 + seed, heads=1)
+        seed += 1
+        qf, kf, vf = (x[0].float().numpy() for x in (q, k, v))
+        if done == 0:       # one warm chunk (BLAS threads, page faults) outside the timing
+            flat_fp32.flat_fp32(qf, kf, vf, tile=64, leaf=leaf, exact_leaves=ex, tile_chunk=32, tiles=slice(0, 32))
+        t0 = time.perf_counter()
+        flat_fp32.flat_fp32(qf, kf, vf, tile=64, leaf=leaf, exact_leaves=ex, tile_chunk=32)
+        elapsed += time.perf_counter() - t0
+        done += 1
+    per_layer_ms = elapsed / done * heads * 1e3
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(per_layer_ms, 1), "unit": "ms/call", "cores": int(threads), "kind": "port",
+            "sample": f"{done} of {heads} heads ({elapsed:.1f} s), extrapolated x{heads / done:.1f}; NumPy fp32 "
+                      f"restatement of the torch backend _flat (h3/htrc_flat.py:279-388), tile_chunk 32",
+            "cpu": cpu_model, "os_cpu_count": os.cpu_count()}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4"])
+    ap.add_argument("--kernel-reps", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {a.gpus}); heads shard across GPUs "
+              "without communication, so multi-GPU figures are not produced", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from htrc_amd import htrc_flat, htrc_flat_hip as hip, workloads
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    dev = torch.device("cuda:0")
+    q, k, v, leaf, ex = workloads.make(a.config, seed=0, device=dev)
+    h, nq, d = (int(x) for x in q.shape)
+    nk = int(k.shape[1])
+    nb = nk // leaf
+    kx = min(ex, nb)
+    ws = {}
+    kw = dict(backend="hip", store="int8", dot="bf16", leaf=leaf, exact_leaves=ex, kern={"fused": True})
+
+    def step():
+        return htrc_flat.flat_attention(q, k, v, ws=ws, **kw)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(a.steps):
+        out = step()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / a.steps
+    assert torch.isfinite(out).all().item(), "non-finite output"
+
+    # per-kernel launch durations, HIP events on the stream the kernels are launched on
+    scale = 1.0 / math.sqrt(d)
+    mu, q8, sq, dq8, sdq = hip.pack_q(q, ws=ws)
+    k8, ks, kq, vq = hip.pack_kv(k, v, ws=ws)
+    g8, lz, vbq, sg, _ = hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws, kq=kq, vq=vq)
+    packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "vq": vq}
+    lstate = {"g8": g8, "sg": sg, "lz": lz, "vbq": vbq}
+    stages = {
+        "pack_q": lambda: hip.pack_q(q, ws=ws),
+        "pack_kv": lambda: hip.pack_kv(k, v, ws=ws),
+        "stats": lambda: hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws, kq=kq, vq=vq),
+        "route": lambda: hip.route(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, ws=ws),
+    }
+    kms = {}
+    stream = torch.cuda.current_stream(dev)
+    for name, fn in stages.items():
+        fn()
+        times = []
+        for _ in range(a.kernel_reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1))
+        kms[name] = statistics.mean(times)
+    figs = algorithmic(h, nq, nk, leaf, kx, d)
+    kernels = {n: roofline_entry(n, kms[n], figs[n]) for n in stages}
+    dom = max(kernels.values(), key=lambda e: e["ms"])
+    fig = figs[dom["kernel"]]
+    if dom["bound"] == "hbm":
+        ach = fig["bytes"] / (dom["ms"] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "kernel": dom["kernel"]}
+    else:
+        # bf16-equivalent rate: an int8 op costs half a bf16 flop at the MI355X dense peaks
+        ach = (fig["bf16_flops"] + fig["i8_ops"] * PEAK_BF16_TFLOPS / PEAK_I8_TOPS) / (dom["ms"] * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "kernel": dom["kernel"], "note": "bf16-equivalent: int8 ops weighted by 2.5/5.0"}
+    res = {"metric": METRIC, "value": round(ms, 4), "unit": "ms/call", "n_gpus": 1, "steps": a.steps,
+           "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+           "vs_baseline": None, "dtype": "i8/bf16 (fp32 accumulate)",
+           "data": "synthetic: clustered spatiotemporal regions, seed 0, generated on device",
+           "config": {"workload": f"{a.config}: B=1 H={h} N={nq} d={d} leaf={leaf} near={kx} tile=64",
+                      "heads": h, "queries": nq, "keys": nk, "leaf": leaf, "near_leaves": kx},
+           "roofline": roof, "kernels": kernels}
+    if not a.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(a.config, a.cpu_budget)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()
