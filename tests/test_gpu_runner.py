@@ -1,0 +1,65 @@
+"""FlatRunner on the GPU (h3/htrc_flat_runner.py:85-203): the captured HIP graph replays
+equal eager launches on every replay (with eager work and syncs in between), head-batched
+replays equal per-head calls, sink mode hands over the static output, and a capture
+failure degrades to eager with ``graph_error`` recorded.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from htrc_amd import htrc_flat, htrc_flat_runner, workloads
+
+pytestmark = pytest.mark.gpu
+
+KW = dict(leaf=64, exact_leaves=8)
+
+
+def _jobs(device, heads=3, n=2048, seed=0):
+    q, k, v = workloads.clustered_runs(n=n, runs=n // 64, heads=heads, seed=seed)
+    return [(h, q[h].float().to(device), k[h].to(device), v[h].to(device)) for h in range(heads)]
+
+
+def test_graph_replays_equal_eager(device):
+    jobs = _jobs(device)
+    r = htrc_flat_runner.FlatRunner(2048, 2048, mode="fast", **KW)
+    assert r.graph is not None, r.graph_error
+    eager = [htrc_flat.flat_attention(j[1], j[2], j[3], **r.cfg) for j in jobs]
+    for rep in range(3):
+        outs = r.run(jobs)
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {rep} differs from eager"
+        _ = torch.randn(1 << 20, device=device).sum().item()      # eager work between replays
+
+
+def test_head_batched_runner_matches_per_head(device):
+    jobs = _jobs(device, heads=5, seed=1)
+    single = htrc_flat_runner.FlatRunner(2048, 2048, mode="fast", use_graph=False, **KW)
+    batched = htrc_flat_runner.FlatRunner(2048, 2048, mode="fast", heads=2, **KW)
+    assert batched.graph is not None, batched.graph_error
+    a = single.run(jobs)
+    b = batched.run(jobs)                      # 2 + 2 + 1 (padded) heads per replay
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    got = {}
+    batched.run(jobs, sink=lambda i, o: got.__setitem__(i, o.clone()))
+    for i, x in enumerate(a):
+        assert torch.equal(got[i], x)
+
+
+def test_capture_failure_falls_back_to_eager(device, monkeypatch):
+    orig = torch.cuda.graph
+
+    def broken(*a, **k):
+        raise RuntimeError("capture refused for the test")
+
+    monkeypatch.setattr(torch.cuda, "graph", broken)
+    r = htrc_flat_runner.FlatRunner(2048, 2048, mode="fast", **KW)
+    monkeypatch.setattr(torch.cuda, "graph", orig)
+    assert r.graph is None and "capture refused" in r.graph_error
+    jobs = _jobs(device, heads=1)
+    out = r.run(jobs)[0]
+    ref = htrc_flat.flat_attention(jobs[0][1], jobs[0][2], jobs[0][3], **r.cfg)
+    assert torch.equal(out, ref)
