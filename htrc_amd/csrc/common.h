@@ -75,12 +75,38 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x2 lo, u32x2 hi) {
     return __builtin_bit_cast(bf16x8, u);
 }
 
-__device__ __forceinline__ uint32_t pack2bf(float a, float b) { return f2bf(a) | (f2bf(b) << 16); }
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16 pair with the hardware conversion (v_cvt_pk_bf16_f32, round to
+// nearest even): a in the low half, b in the high half.
+__device__ __forceinline__ uint32_t pack2bf(float a, float b) {
+    const bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// fp32 rounded to the nearest bf16 value (returned as fp32).
+__device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
 
 // Eight fp32 -> bf16x8 (round to nearest even).
 __device__ __forceinline__ bf16x8 to_bf16x8(const float* x) {
     u32x4 u = {pack2bf(x[0], x[1]), pack2bf(x[2], x[3]), pack2bf(x[4], x[5]), pack2bf(x[6], x[7])};
     return as_bf16x8(u);
+}
+
+// Three-term bf16 split of eight fp32 values: x = hi + mid + lo to ~24 bits.
+__device__ __forceinline__ void split3x8(const float* x, bf16x8& hi, bf16x8& mid, bf16x8& lo) {
+    uint32_t h[4], m[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        h[j] = pack2bf(x[2 * j], x[2 * j + 1]);
+        const float r0 = __fsub_rn(x[2 * j], __uint_as_float(h[j] << 16));
+        const float r1 = __fsub_rn(x[2 * j + 1], __uint_as_float(h[j] & 0xffff0000u));
+        m[j] = pack2bf(r0, r1);
+        l[j] = pack2bf(__fsub_rn(r0, __uint_as_float(m[j] << 16)), __fsub_rn(r1, __uint_as_float(m[j] & 0xffff0000u)));
+    }
+    hi = as_bf16x8(u32x4{h[0], h[1], h[2], h[3]});
+    mid = as_bf16x8(u32x4{m[0], m[1], m[2], m[3]});
+    lo = as_bf16x8(u32x4{l[0], l[1], l[2], l[3]});
 }
 
 __device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {

@@ -137,14 +137,49 @@ __global__ __launch_bounds__(256) void pack_kv_kernel(const uint16_t* __restrict
 //   a^T = K_l mu^T         bf16 MFMA, mu split into three bf16 terms (~fp32 product)
 //   softmax over the leaf's keys per centre (lane%16 = centre)
 //   g^T = K_l^T w^T, vb^T = V_l^T w^T   bf16 MFMA, w split into 3 (g) / 2 (vb) bf16 terms
+// The leaf's K (row layout) and key-quad K, V are staged in LDS by gfx950 direct
+// global->LDS loads, one leaf ahead (double buffer), and shared by the four waves; the LDS
+// chunk order makes every MFMA operand read a contiguous, conflict-free 512 B / 1 KB.
 // Leaves are processed four at a time so that vb can be stored in the leaf-quad layout
 // vbq[t][l/4][d][l%4] that the far-field PV operand reads with 8-byte loads.
 // ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ void split3(float x, float& a, float& b, float& c) {
-    a = bf2f(f2bf(x));
-    const float r = __fsub_rn(x, a);
-    b = bf2f(f2bf(r));
-    c = __fsub_rn(r, b);
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One direct global->LDS load: 16 bytes per lane to lds_base + lane * 16 (lds_base uniform).
+__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_base, 16, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {          // s_waitcnt vmcnt(N), other counters untouched
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Stage leaf l (LEAF keys) of one head into an LDS buffer: chunk c of 16 bytes, c = j*256 + tid.
+//   [0, 16L)      K rows:    c = ((kb*4 + ks)*4 + grp)*16 + col  <- K[16kb + col][dims 32ks + 8grp ..]
+//   [16L, 32L)    key-quad K: c = (((kk*2 + h)*8 + db)*4 + grp)*8 + p <- Kq[8kk + 4h + grp][16db + 2p ..]
+//   [32L, 48L)    key-quad V: same order from Vq
+template <int LEAF>
+__device__ __forceinline__ void stage_leaf(const uint16_t* __restrict__ K, const uint16_t* __restrict__ kq,
+                                           const uint16_t* __restrict__ vq, int64_t key0, char* buf) {
+    constexpr int NC = 48 * LEAF;              // 16-byte chunks per leaf
+    const int tid = threadIdx.x, w = tid >> 6;
+#pragma unroll
+    for (int j = 0; j < NC / 256; ++j) {
+        const int c = j * 256 + tid;
+        const void* src;
+        if (c < 16 * LEAF) {
+            const int col = c & 15, grp = (c >> 4) & 3, ks = (c >> 6) & 3, kb = c >> 8;
+            src = K + (key0 + 16 * kb + col) * D + 32 * ks + 8 * grp;
+        } else {
+            const int cc = c & (16 * LEAF - 1);
+            const int p = cc & 7, grp = (cc >> 3) & 3, db = (cc >> 5) & 7, h = (cc >> 8) & 1, kk = cc >> 9;
+            const int64_t quad = key0 / 4 + 8 * kk + 4 * h + grp;
+            src = (c < 32 * LEAF ? kq : vq) + (quad * D + 16 * db + 2 * p) * 4;
+        }
+        dma16(src, buf + (size_t)(j * 256 + w * 64) * 16);
+    }
 }
 
 template <int LEAF>
@@ -157,6 +192,10 @@ __global__ __launch_bounds__(256) void stats_kernel(const float* __restrict__ mu
                                                     uint16_t* __restrict__ vbq, float* __restrict__ lz) {
     constexpr int KB = LEAF / 16;                 // 16-key blocks per leaf
     constexpr int KK = (LEAF + 31) / 32;          // 32-key MFMA k-steps per leaf
+    constexpr int LEAF_BYTES = 48 * LEAF * 16;
+    constexpr int NBUF = LEAF <= 64 ? 2 : 1;
+    constexpr int NDMA = 48 * LEAF / 256;         // DMA instructions per wave per leaf
+    __shared__ __align__(16) char lds[NBUF * LEAF_BYTES];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int h = blockIdx.z;
     const int t = blockIdx.x * 64 + w * 16 + col;   // tile centre of this lane's C column
@@ -166,20 +205,17 @@ __global__ __launch_bounds__(256) void stats_kernel(const float* __restrict__ mu
     bf16x8 mh[4], mm[4], ml[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-        float a[8], b[8], c[8];
+        float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float x = tval ? mu[th * D + 32 * ks + 8 * grp + e] : 0.0f;
-            split3(x, a[e], b[e], c[e]);
-        }
-        mh[ks] = to_bf16x8(a);
-        mm[ks] = to_bf16x8(b);
-        ml[ks] = to_bf16x8(c);
+        for (int e = 0; e < 8; ++e) x[e] = tval ? mu[th * D + 32 * ks + 8 * grp + e] : 0.0f;
+        split3x8(x, mh[ks], mm[ks], ml[ks]);
     }
 
     const int l0 = blockIdx.y * lpb;
     const int l1 = min(nb_pad, l0 + lpb);
+    const int lr = min(nb, l1);                   // real leaves of this workgroup: [l0, lr)
     const int64_t kh = (int64_t)h * nk;
+    if (NBUF == 2 && l0 < lr) stage_leaf<LEAF>(k, kq, vq, kh + (int64_t)l0 * LEAF, lds);
     for (int lq = l0; lq < l1; lq += 4) {
         f32x4 vacc[4][8];
 #pragma unroll
@@ -200,14 +236,32 @@ __global__ __launch_bounds__(256) void stats_kernel(const float* __restrict__ mu
                 }
                 continue;
             }
-            const uint16_t* K = k + (kh + (int64_t)l * LEAF) * D;
+            // ---- leaf l's operands: staged one leaf ahead (double buffer) or now (single)
+            char* buf;
+            if (NBUF == 2) {
+                buf = lds + ((l - l0) & 1) * LEAF_BYTES;
+                if (l + 1 < lr) {
+                    stage_leaf<LEAF>(k, kq, vq, kh + (int64_t)(l + 1) * LEAF, lds + ((l + 1 - l0) & 1) * LEAF_BYTES);
+                    wait_vmcnt<NDMA>();
+                } else {
+                    wait_vmcnt<0>();
+                }
+            } else {
+                buf = lds;
+                stage_leaf<LEAF>(k, kq, vq, kh + (int64_t)l * LEAF, lds);
+                wait_vmcnt<0>();
+            }
+            __syncthreads();                   // every wave's chunks of leaf l have landed
+            const char* Kr = buf;
+            const char* Kq4 = buf + 16 * LEAF * 16;
+            const char* Vq4 = buf + 32 * LEAF * 16;
             f32x4 a[KB];
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
                 a[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
-                    const bf16x8 A = as_bf16x8(*(const u32x4*)(K + (16 * kb + col) * D + 32 * ks + 8 * grp));
+                    const bf16x8 A = as_bf16x8(*(const u32x4*)(Kr + ((kb * 4 + ks) * 64 + lane) * 16));
                     a[kb] = mfma_bf16(A, mh[ks], a[kb]);
                     a[kb] = mfma_bf16(A, mm[ks], a[kb]);
                     a[kb] = mfma_bf16(A, ml[ks], a[kb]);
@@ -232,34 +286,31 @@ __global__ __launch_bounds__(256) void stats_kernel(const float* __restrict__ mu
                     z = __fadd_rn(z, a[kb][i]);
                 }
             z = grp_sum(z);
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) a[kb][i] = __fdiv_rn(a[kb][i], z);
+            // w = e / z is applied after the dots: g = (e.K) * (scale / z), vb = (e.V) / z
+            const float rz = __fdiv_rn(1.0f, z);
 
             f32x4 gacc[8];
 #pragma unroll
             for (int db = 0; db < 8; ++db) gacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-            const int64_t qrow = (kh + (int64_t)l * LEAF) / 4;   // first key quad of the leaf
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) {
-                float w0[8], w1[8], w2[8];
+                float we[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int kb = 2 * kk + (e >> 2);
-                    const float x = kb < KB ? a[kb < KB ? kb : 0][e & 3] : 0.0f;
-                    split3(x, w0[e], w1[e], w2[e]);
+                    we[e] = kb < KB ? a[kb < KB ? kb : 0][e & 3] : 0.0f;
                 }
-                const bf16x8 W0 = to_bf16x8(w0), W1 = to_bf16x8(w1), W2 = to_bf16x8(w2);
+                bf16x8 W0, W1, W2;
+                split3x8(we, W0, W1, W2);
 #pragma unroll
                 for (int db = 0; db < 8; ++db) {
-                    const int64_t o0 = ((qrow + 8 * kk + grp) * D + 16 * db + col) * 4;
-                    const int64_t o1 = ((qrow + 8 * kk + 4 + grp) * D + 16 * db + col) * 4;
                     const u32x2 zero = {0u, 0u};
-                    const u32x2 k0 = *(const u32x2*)(kq + o0);
-                    const u32x2 k1 = (2 * kk + 1 < KB) ? *(const u32x2*)(kq + o1) : zero;
-                    const u32x2 v0 = *(const u32x2*)(vq + o0);
-                    const u32x2 v1 = (2 * kk + 1 < KB) ? *(const u32x2*)(vq + o1) : zero;
+                    const int u0 = (((kk * 2 + 0) * 8 + db) * 4 + grp) * 16 + col;   // 8-byte units
+                    const int u1 = (((kk * 2 + 1) * 8 + db) * 4 + grp) * 16 + col;
+                    const u32x2 k0 = *(const u32x2*)(Kq4 + u0 * 8);
+                    const u32x2 k1 = (2 * kk + 1 < KB) ? *(const u32x2*)(Kq4 + u1 * 8) : zero;
+                    const u32x2 v0 = *(const u32x2*)(Vq4 + u0 * 8);
+                    const u32x2 v1 = (2 * kk + 1 < KB) ? *(const u32x2*)(Vq4 + u1 * 8) : zero;
                     const bf16x8 KA = as_bf16x8(k0, k1), VA = as_bf16x8(v0, v1);
                     gacc[db] = mfma_bf16(KA, W0, gacc[db]);
                     gacc[db] = mfma_bf16(KA, W1, gacc[db]);
@@ -268,15 +319,19 @@ __global__ __launch_bounds__(256) void stats_kernel(const float* __restrict__ mu
                     vacc[j][db] = mfma_bf16(VA, W1, vacc[j][db]);
                 }
             }
+            __syncthreads();                   // buffer of leaf l free for leaf l + 2
             // g^T: lane holds dims 16db + 4grp + i of centre t
+            const float gs = __fmul_rn(scale, rz);
             float am = 0.0f;
 #pragma unroll
-            for (int db = 0; db < 8; ++db)
+            for (int db = 0; db < 8; ++db) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    gacc[db][i] = __fmul_rn(gacc[db][i], scale);
+                    gacc[db][i] = __fmul_rn(gacc[db][i], gs);
                     am = fmaxf(am, fabsf(gacc[db][i]));
+                    vacc[j][db][i] = __fmul_rn(vacc[j][db][i], rz);
                 }
+            }
             am = grp_max(am);
             am = am < 1e-30f ? 1e-30f : am;
             const float cq = __fdiv_rn(127.0f, am);
@@ -302,8 +357,7 @@ __global__ __launch_bounds__(256) void stats_kernel(const float* __restrict__ mu
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int dim = 16 * db + 4 * grp + i;
-                    u32x2 o = {f2bf(vacc[0][db][i]) | (f2bf(vacc[1][db][i]) << 16),
-                               f2bf(vacc[2][db][i]) | (f2bf(vacc[3][db][i]) << 16)};
+                    u32x2 o = {pack2bf(vacc[0][db][i], vacc[1][db][i]), pack2bf(vacc[2][db][i], vacc[3][db][i])};
                     *(u32x2*)(vo + dim * 4) = o;
                 }
         }
@@ -459,20 +513,32 @@ __device__ void topk_row(const uint32_t* keys, int nb, int kx, TopkSmem& sm, int
         ngt += key > thr;
         neq += key == thr;
     }
-    sm.cnt_gt[tid + 1] = ngt;
-    sm.cnt_eq[tid + 1] = neq;
-    if (tid == 0) {
-        sm.cnt_gt[0] = 0;
-        sm.cnt_eq[0] = 0;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        for (int i = 1; i <= 256; ++i) {
-            sm.cnt_gt[i] += sm.cnt_gt[i - 1];
-            sm.cnt_eq[i] += sm.cnt_eq[i - 1];
+    {   // exclusive prefix over the 256 threads: in-wave inclusive scan, then wave offsets
+        const int lane = tid & 63, wv = tid >> 6;
+        uint32_t ig = ngt, ie = neq;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t yg = __shfl_up(ig, o, 64), ye = __shfl_up(ie, o, 64);
+            if (lane >= o) {
+                ig += yg;
+                ie += ye;
+            }
         }
+        if (lane == 63) {
+            sm.cnt_gt[wv] = ig;
+            sm.cnt_eq[wv] = ie;
+        }
+        __syncthreads();
+        uint32_t og = 0, oe = 0;
+        for (int j = 0; j < wv; ++j) {
+            og += sm.cnt_gt[j];
+            oe += sm.cnt_eq[j];
+        }
+        __syncthreads();
+        sm.cnt_gt[tid] = og + ig - ngt;
+        sm.cnt_eq[tid] = oe + ie - neq;
+        __syncthreads();
     }
-    __syncthreads();
     uint32_t eqr = sm.cnt_eq[tid];
     uint32_t pos = sm.cnt_gt[tid] + (eqr < need_eq ? eqr : need_eq);
     for (int l = a; l < b; ++l) {
@@ -735,11 +801,136 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm
 }
 
 // ---------------------------------------------------------------------------------------------
-// route: the fused per-tile kernel of the production path.  select (SEL of every leaf into
-// LDS) -> LDS top-k (idx ascending, exclusion bitmap) -> far + near online softmax -> out,
-// logZ.  One launch per layer replaces select + topk + tile + merge and never writes the
-// SEL / excl / partial tensors to HBM (it can still emit idx for checking).
+// route: the fused per-tile kernel of the production path (one workgroup of 4 waves per tile).
+//   1. select: SEL of every leaf (bit-exact, same arithmetic as select_kernel) into LDS;
+//   2. top-k in LDS (idx ascending, exclusion bytes);
+//   3. split-K far + near: wave w owns ALL 64 query rows (four 16-row MFMA column blocks, so
+//      every A operand it loads feeds four MFMAs) for a quarter of the far leaves and a
+//      quarter of the near tokens; the A operands of the next 32-key block are loaded while
+//      the current block is computed;
+//   4. the four partial (m, l, O) states merge through LDS into out / logZ.
+// SEL, excl and the partials never reach HBM (idx can be emitted for checking).
 // ---------------------------------------------------------------------------------------------
+struct FarQK {          // prefetched one block ahead
+    i32x4 g[2][2];     // g8 A operands: [16-leaf half][64-dim k-step]
+    f32x4 sg[2], lz[2];
+    uint32_t ex[2];
+};
+
+struct NearQK {
+    i32x4 k[2][2];     // k8 A operands: [16-token run][64-dim k-step]
+    f32x4 ks[2];
+    int64_t tok0[2];
+    bool ok[2];
+};
+
+struct Rows4 {         // online-softmax state of 64 rows held by one wave
+    float m[4];
+    float l[4];        // this lane's share of the row sums
+    f32x4 o[4][8];     // O^T per row block: dims 16db + 4grp + i of row 16rb + lane%16
+};
+
+__device__ __forceinline__ void load_far_qk(FarQK& f, int64_t srow, const int8_t* __restrict__ g8,
+                                            const float* __restrict__ sg, const float* __restrict__ lz,
+                                            const int8_t* __restrict__ excl_row, int c0, int col, int grp) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int64_t s0 = srow + c0 + 16 * h;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) f.g[h][ks] = *(const i32x4*)(g8 + (s0 + col) * D + 64 * ks + 16 * grp);
+        f.sg[h] = *(const f32x4*)(sg + s0 + 4 * grp);
+        f.lz[h] = *(const f32x4*)(lz + s0 + 4 * grp);
+        f.ex[h] = *(const uint32_t*)(excl_row + c0 + 16 * h + 4 * grp);
+    }
+}
+
+// PV operands of a 32-key block in key-quad layout: quads q0 + grp and q1 + grp.
+__device__ __forceinline__ void load_pv(u32x2 (&v)[8][2], const uint16_t* __restrict__ x4, int64_t q0, int64_t q1,
+                                        int col, int grp) {
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+        const int dim = 16 * db + col;
+        v[db][0] = *(const u32x2*)(x4 + ((q0 + grp) * D + dim) * 4);
+        v[db][1] = *(const u32x2*)(x4 + ((q1 + grp) * D + dim) * 4);
+    }
+}
+
+template <int LEAF>
+__device__ __forceinline__ void load_near_qk(NearQK& n, int e0, int e_hi, int e_lo, const int32_t* idx_row, int64_t kh,
+                                             const int8_t* __restrict__ k8, const float* __restrict__ ks, int col,
+                                             int grp) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int j0 = e0 + 16 * h;
+        n.ok[h] = j0 < e_hi;
+        const int jj = n.ok[h] ? j0 : e_lo;
+        n.tok0[h] = kh + (int64_t)idx_row[jj / LEAF] * LEAF + (jj % LEAF);
+#pragma unroll
+        for (int kss = 0; kss < 2; ++kss)
+            n.k[h][kss] = *(const i32x4*)(k8 + (n.tok0[h] + col) * D + 64 * kss + 16 * grp);
+        n.ks[h] = *(const f32x4*)(ks + n.tok0[h] + 4 * grp);
+    }
+}
+
+// Online update of the four row blocks with scores sc[rb][0..7] (keys 16(e/4) + 4grp + e%4 of
+// the block) and PV operands v[db][half].  Lazy rescaling: a row keeps its reference max
+// m until a block exceeds it by more than RESCALE_MARGIN, so p <= e^8 and O is rescaled
+// (rarely) only then; the result is the same softmax, and O never leaves the accumulators.
+constexpr float RESCALE_MARGIN = 8.0f;
+
+__device__ __forceinline__ void rows4_update(Rows4& st, float (&sc)[4][8], const u32x2 (&v)[8][2]) {
+    float bm[4];
+    bool need = false;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        float x = sc[rb][0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) x = fmaxf(x, sc[rb][e]);
+        bm[rb] = grp_max(x);
+        need |= bm[rb] > st.m[rb] + RESCALE_MARGIN;
+    }
+    if (__any(need)) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            if (bm[rb] > st.m[rb] + RESCALE_MARGIN) {
+                const float alpha = __expf(__fsub_rn(st.m[rb], bm[rb]));   // 0 when m = -inf
+                st.l[rb] = __fmul_rn(st.l[rb], alpha);
+#pragma unroll
+                for (int db = 0; db < 8; ++db) {
+                    f32x4 o = st.o[rb][db];
+                    o[0] = __fmul_rn(o[0], alpha);
+                    o[1] = __fmul_rn(o[1], alpha);
+                    o[2] = __fmul_rn(o[2], alpha);
+                    o[3] = __fmul_rn(o[3], alpha);
+                    st.o[rb][db] = o;
+                }
+                st.m[rb] = bm[rb];
+            }
+        }
+    }
+    bf16x8 P[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        const float m_s = st.m[rb] == -INFINITY ? 0.0f : st.m[rb];
+        float p[8], ps = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            p[e] = __expf(__fsub_rn(sc[rb][e], m_s));
+            ps = __fadd_rn(ps, p[e]);
+        }
+        st.l[rb] = __fadd_rn(st.l[rb], ps);
+        P[rb] = to_bf16x8(p);
+    }
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+        const bf16x8 A = as_bf16x8(v[db][0], v[db][1]);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) st.o[rb][db] = mfma_bf16(A, P[rb], st.o[rb][db]);
+    }
+}
+
+constexpr int ROUTE_LDS_WORDS = 2 * MAX_NB_LDS + MAX_NB_LDS / 4 + 8;   // keys + sidx + excl bytes
+
 template <int LEAF>
 __global__ __launch_bounds__(256) void route_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ sq, const int8_t* __restrict__ dq8,
@@ -748,14 +939,17 @@ __global__ __launch_bounds__(256) void route_kernel(
     const float* __restrict__ ks, const uint16_t* __restrict__ vq, int64_t nq, int nt, int64_t nk, int nb,
     int nb_pad, int kx, int sink, int stride, float scale, float* __restrict__ out,
     float* __restrict__ logz, int32_t* __restrict__ idx_out) {
-    __shared__ uint32_t keys[MAX_NB_LDS];
-    __shared__ __align__(16) int8_t exl[MAX_NB_LDS + 32];
-    __shared__ int32_t sidx[MAX_NB_LDS];
+    __shared__ __align__(16) uint32_t smem[ROUTE_LDS_WORDS];
     __shared__ TopkSmem sm;
+    __shared__ float red_m[4][64], red_l[4][64];
+    uint32_t* keys = smem;                                   // [MAX_NB_LDS] during select / top-k
+    int32_t* sidx = (int32_t*)(smem + MAX_NB_LDS);           // [MAX_NB_LDS] selected leaves
+    int8_t* exl = (int8_t*)(smem + 2 * MAX_NB_LDS);          // [MAX_NB_LDS + 32] exclusion bytes
+    float* mrg = (float*)smem;                               // merge staging (after top-k): 4 x 64 x 32 floats
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int t = blockIdx.x, h = blockIdx.z;
     const int64_t th = (int64_t)h * nt + t;
-    // ---- select (bit-exact, same arithmetic as select_kernel)
+    // ---- 1. select (bit-exact)
     {
         const int ts = TILE / stride;
         i32x4 b[4][2];
@@ -765,38 +959,54 @@ __global__ __launch_bounds__(256) void route_kernel(
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
             srow[rb] = sdq[th * TILE + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
-        for (int c = 16 * w; c < nb; c += 64) {
+        struct SelOps {
+            i32x4 a[2];
+            f32x4 sg, lz;
+        };
+        auto sel_load = [&](SelOps& o, int c) {
             const int64_t s0 = th * nb_pad + c;
+#pragma unroll
+            for (int kss = 0; kss < 2; ++kss) o.a[kss] = *(const i32x4*)(g8 + (s0 + col) * D + 64 * kss + 16 * grp);
+            o.sg = *(const f32x4*)(sg + s0 + 4 * grp);
+            o.lz = *(const f32x4*)(lz + s0 + 4 * grp);
+        };
+        auto sel_block = [&](const SelOps& o, int c) {
             i32x4 acc[4];
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) acc[rb] = i32x4{0, 0, 0, 0};
-#pragma unroll
-            for (int kss = 0; kss < 2; ++kss) {
-                const i32x4 A = *(const i32x4*)(g8 + (s0 + col) * D + 64 * kss + 16 * grp);
-#pragma unroll
-                for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma_i8(A, b[rb][kss], acc[rb]);
+            for (int rb = 0; rb < 4; ++rb) {
+                acc[rb] = mfma_i8(o.a[0], b[rb][0], i32x4{0, 0, 0, 0});
+                acc[rb] = mfma_i8(o.a[1], b[rb][1], acc[rb]);
             }
-            const f32x4 sgv = *(const f32x4*)(sg + s0 + 4 * grp);
             float best[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 best[i] = -INFINITY;
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb)
-                    if (val[rb]) best[i] = fmaxf(best[i], __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i])));
+                    if (val[rb]) best[i] = fmaxf(best[i], __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], o.sg[i])));
                 best[i] = col_max(best[i]);
             }
             if (col == 0) {
-                const f32x4 lzv = *(const f32x4*)(lz + s0 + 4 * grp);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int l = c + 4 * grp + i;
-                    if (l < nb) keys[l] = l < sink ? 0xffffffffu : order_key(__fadd_rn(best[i], lzv[i]));
+                    if (l < nb) keys[l] = l < sink ? 0xffffffffu : order_key(__fadd_rn(best[i], o.lz[i]));
                 }
             }
+        };
+        SelOps sa, sb2;
+        if (16 * w < nb) sel_load(sa, 16 * w);
+        for (int c = 16 * w; c < nb; c += 128) {
+            const int c1 = c + 64;
+            if (c1 < nb) sel_load(sb2, c1);
+            sel_block(sa, c);
+            if (c1 >= nb) break;
+            if (c1 + 64 < nb) sel_load(sa, c1 + 64);
+            sel_block(sb2, c1);
         }
     }
     __syncthreads();
+    // ---- 2. top-k
     const int kxe = kx < nb ? kx : nb;
     if (kxe > 0) {
         topk_row(keys, nb, kxe, sm, idx_out ? idx_out + th * kxe : nullptr, exl, sidx);
@@ -804,22 +1014,175 @@ __global__ __launch_bounds__(256) void route_kernel(
         for (int l = threadIdx.x; l < nb; l += 256) exl[l] = 0;
         __syncthreads();
     }
-    // ---- far + near, one split
-    const int r = w * 16 + col;
-    const int64_t p = th * TILE + r;
-    i32x4 q8r[2], dq8r[2];
-    load_row_ops(q8, dq8, p, grp, q8r, dq8r);
-    const float sqr = sq[p], sdqr = sdq[p];
-    RowState st;
-    st.m = -INFINITY;
-    st.l = 0.0f;
+    // ---- 3. split-K far + near: wave w, all rows
+    Rows4 st;
 #pragma unroll
-    for (int db = 0; db < 8; ++db) st.o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-    tile_far_near<LEAF>(st, th, nt, nb, nb_pad, 0, nb, 0, kxe * LEAF, kxe, q8r, sqr, dq8r, sdqr, g8, sg, lz,
-                        vbq, exl, sidx, k8, ks, vq, (int64_t)h * nk, scale);
-    const float ltot = grp_sum(st.l);
-    const int64_t qi = (int64_t)t * TILE + r;
-    write_final(st, ltot, (int64_t)h * nq + qi, qi < nq, out, logz);
+    for (int rb = 0; rb < 4; ++rb) {
+        st.m[rb] = -INFINITY;
+        st.l[rb] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int64_t kh = (int64_t)h * nk;
+    {   // far field: leaves [lo, hi)
+        const int lpw = ((nb + 3) / 4 + 31) / 32 * 32;
+        const int lo = w * lpw, hi = min(nb, lo + lpw);
+        i32x4 bq[4][2];
+        float srow[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int64_t p = th * TILE + 16 * rb + col;
+#pragma unroll
+            for (int kss = 0; kss < 2; ++kss) bq[rb][kss] = *(const i32x4*)(dq8 + p * D + 64 * kss + 16 * grp);
+            srow[rb] = sdq[p];
+        }
+        const int64_t srow0 = th * nb_pad;
+        const uint16_t* vb0 = vbq + (th * nb_pad / 4) * D * 4;
+        FarQK qa, qb;
+        auto far_block = [&](const FarQK& f, int c0) {
+            u32x2 v[8][2];
+            load_pv(v, vb0, c0 / 4, c0 / 4 + 4, col, grp);
+            float sc[4][8];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                i32x4 acc[4];
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    acc[rb] = mfma_i8(f.g[hh][0], bq[rb][0], i32x4{0, 0, 0, 0});
+                    acc[rb] = mfma_i8(f.g[hh][1], bq[rb][1], acc[rb]);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int c = c0 + 16 * hh + 4 * grp + i;
+                    const bool ok = c < hi && ((f.ex[hh] >> (8 * i)) & 0xffu) == 0u;
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb)
+                        sc[rb][4 * hh + i] =
+                            ok ? __fadd_rn(__fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], f.sg[hh][i])), f.lz[hh][i])
+                               : -INFINITY;
+                }
+            }
+            rows4_update(st, sc, v);
+        };
+        if (lo < hi) load_far_qk(qa, srow0, g8, sg, lz, exl, lo, col, grp);
+        for (int c0 = lo; c0 < hi; c0 += 64) {
+            const int c1 = c0 + 32;
+            if (c1 < hi) load_far_qk(qb, srow0, g8, sg, lz, exl, c1, col, grp);
+            far_block(qa, c0);
+            if (c1 >= hi) break;
+            if (c1 + 32 < hi) load_far_qk(qa, srow0, g8, sg, lz, exl, c1 + 32, col, grp);
+            far_block(qb, c1);
+        }
+    }
+    {   // near field: tokens [e_lo, e_hi) of the selected list
+        const int e_n = kxe * LEAF;
+        const int epw = ((e_n + 3) / 4 + 31) / 32 * 32;
+        const int e_lo = w * epw, e_hi = min(e_n, e_lo + epw);
+        i32x4 bq[4][2];
+        float srow[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int64_t p = th * TILE + 16 * rb + col;
+#pragma unroll
+            for (int kss = 0; kss < 2; ++kss) bq[rb][kss] = *(const i32x4*)(q8 + p * D + 64 * kss + 16 * grp);
+            srow[rb] = sq[p];
+        }
+        NearQK qa, qb;
+        auto near_block = [&](const NearQK& n, int e0) {
+            u32x2 v[8][2];
+            load_pv(v, vq, n.tok0[0] / 4, n.tok0[1] / 4, col, grp);
+            float sc[4][8];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                i32x4 acc[4];
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    acc[rb] = mfma_i8(n.k[hh][0], bq[rb][0], i32x4{0, 0, 0, 0});
+                    acc[rb] = mfma_i8(n.k[hh][1], bq[rb][1], acc[rb]);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bool ok = n.ok[hh] && (e0 + 16 * hh + 4 * grp + i) < e_hi;
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb)
+                        sc[rb][4 * hh + i] =
+                            ok ? __fmul_rn((float)acc[rb][i], __fmul_rn(__fmul_rn(srow[rb], n.ks[hh][i]), scale))
+                               : -INFINITY;
+                }
+            }
+            rows4_update(st, sc, v);
+        };
+        if (e_lo < e_hi) load_near_qk<LEAF>(qa, e_lo, e_hi, e_lo, sidx, kh, k8, ks, col, grp);
+        for (int e0 = e_lo; e0 < e_hi; e0 += 64) {
+            const int e1 = e0 + 32;
+            if (e1 < e_hi) load_near_qk<LEAF>(qb, e1, e_hi, e_lo, sidx, kh, k8, ks, col, grp);
+            near_block(qa, e0);
+            if (e1 >= e_hi) break;
+            if (e1 + 32 < e_hi) load_near_qk<LEAF>(qa, e1 + 32, e_hi, e_lo, sidx, kh, k8, ks, col, grp);
+            near_block(qb, e1);
+        }
+    }
+    // ---- 4. merge the four partial states (h3/htrc_flat_triton.py:263-273 algebra)
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        const float lt = grp_sum(st.l[rb]);
+        if (grp == 0) {
+            red_m[w][16 * rb + col] = st.m[rb];
+            red_l[w][16 * rb + col] = lt;
+        }
+    }
+    __syncthreads();                      // also: every wave is done with keys / sidx / exl
+    float wsc[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        const int r = 16 * rb + col;
+        float mm = fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r]));
+        mm = mm == -INFINITY ? 0.0f : mm;
+        wsc[rb] = __expf(__fsub_rn(st.m[rb], mm));
+    }
+    // row r handled by thread (r, quarter): merged den and logZ
+    const int r_out = threadIdx.x >> 2, qd = threadIdx.x & 3;
+    float den = 0.0f, mmr;
+    {
+        mmr = fmaxf(fmaxf(red_m[0][r_out], red_m[1][r_out]), fmaxf(red_m[2][r_out], red_m[3][r_out]));
+        mmr = mmr == -INFINITY ? 0.0f : mmr;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) den = __fadd_rn(den, __fmul_rn(red_l[s][r_out], __expf(__fsub_rn(red_m[s][r_out], mmr))));
+    }
+    const float dd = den < 1e-30f ? 1e-30f : den;
+    const int64_t qi = (int64_t)t * TILE + r_out;
+    const bool rvalid = qi < nq;
+    const int64_t orow = (int64_t)h * nq + qi;
+    for (int pass = 0; pass < 4; ++pass) {           // 32 dims (two dim blocks) per pass
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int db = 2 * pass + j;
+                const f32x4 o = st.o[rb][db];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 16 * rb + col, dl = 16 * j + 4 * grp + i;   // dim within the pass
+                    mrg[(w * 64 + r) * 33 + dl] = __fmul_rn(o[i], wsc[rb]);
+                }
+            }
+        __syncthreads();
+        if (rvalid) {
+            f32x4 res[2];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int dl = 8 * qd + u;
+                float acc = 0.0f;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) acc = __fadd_rn(acc, mrg[(s * 64 + r_out) * 33 + dl]);
+                res[u >> 2][u & 3] = __fdiv_rn(acc, dd);
+            }
+            *(f32x4*)(out + orow * D + 32 * pass + 8 * qd) = res[0];
+            *(f32x4*)(out + orow * D + 32 * pass + 8 * qd + 4) = res[1];
+        }
+        __syncthreads();
+    }
+    if (rvalid && qd == 0) logz[orow] = __fadd_rn(mmr, __logf(den));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -852,7 +1215,7 @@ __global__ __launch_bounds__(64) void selftest_mfma_kernel(const int8_t* __restr
 // =============================================================================================
 // C-ABI launchers
 // =============================================================================================
-#include "../../include/htrc_flat.h"
+#include "htrc_flat.h"
 
 static thread_local char g_err[512] = "";
 
