@@ -17,6 +17,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // fp32(1/127) = 0x3C010204, the per-row int8 scale factor.
 __device__ constexpr float R127 = 1.0f / 127.0f;
+__device__ constexpr float LOG2E = 1.4426950408889634f;
+__device__ constexpr float LN2 = 0.6931471805599453f;
 
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 
@@ -53,20 +55,35 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// Reductions across the four 16-lane groups that share a column of an MFMA C tile.
-__device__ __forceinline__ float grp_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, WAVE));
-    return fmaxf(v, __shfl_xor(v, 32, WAVE));
+// Reductions across the four 16-lane groups that share a column of an MFMA C tile, with the
+// gfx950 lane swaps: with both operands equal, the two results of v_permlane{16,32}_swap hold
+// {v[i], v[i ^ 16]} (resp. {v[i], v[i ^ 32]}) in each lane, so one max / add reduces a pair.
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float grp_max(float v) { return xor32_max(xor16_max(v)); }
 __device__ __forceinline__ float grp_sum(float v) {
-    v += __shfl_xor(v, 16, WAVE);
-    return v + __shfl_xor(v, 32, WAVE);
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __fadd_rn(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __fadd_rn(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
-// Reductions across the 16 lanes of one group (the columns of an MFMA C tile).
+// Max across the 16 lanes of one group (the columns of an MFMA C tile) with DPP: xor 1,
+// xor 2 (quad permutes), then half-row and row mirrors; every lane ends with the maximum.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xf, 0xf, false)));
+}
 __device__ __forceinline__ float col_max(float v) {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
+    v = dpp_max<0xB1>(v);     // quad_perm [1,0,3,2]
+    v = dpp_max<0x4E>(v);     // quad_perm [2,3,0,1]
+    v = dpp_max<0x141>(v);    // row_half_mirror
+    return dpp_max<0x140>(v);   // row_mirror
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 u) { return __builtin_bit_cast(bf16x8, u); }

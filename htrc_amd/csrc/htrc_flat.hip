@@ -872,53 +872,25 @@ __device__ __forceinline__ void load_near_qk(NearQK& n, int e0, int e_hi, int e_
     }
 }
 
-// Online update of the four row blocks with scores sc[rb][0..7] (keys 16(e/4) + 4grp + e%4 of
-// the block) and PV operands v[db][half].  Lazy rescaling: a row keeps its reference max
-// m until a block exceeds it by more than RESCALE_MARGIN, so p <= e^8 and O is rescaled
-// (rarely) only then; the result is the same softmax, and O never leaves the accumulators.
-constexpr float RESCALE_MARGIN = 8.0f;
+// Softmax accumulation of the four row blocks with log2-domain scores u[rb][0..7] =
+// score * log2(e) (keys 16(e/4) + 4grp + e%4 of the block; masked keys -inf) and PV operands
+// v[db][half].  The reference max m of each row is fixed before the loops (the row's largest
+// far-field score, found by the select phase), so p = 2^(u - m) needs no running rescale and
+// O never leaves the MFMA accumulators; umax tracks the true maximum so the caller can redo
+// the (never observed) rows whose scores exceed m by more than 2^64 or underflow.
+constexpr float REF_SLACK = 64.0f;
 
-__device__ __forceinline__ void rows4_update(Rows4& st, float (&sc)[4][8], const u32x2 (&v)[8][2]) {
-    float bm[4];
-    bool need = false;
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-        float x = sc[rb][0];
-#pragma unroll
-        for (int e = 1; e < 8; ++e) x = fmaxf(x, sc[rb][e]);
-        bm[rb] = grp_max(x);
-        need |= bm[rb] > st.m[rb] + RESCALE_MARGIN;
-    }
-    if (__any(need)) {
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            if (bm[rb] > st.m[rb] + RESCALE_MARGIN) {
-                const float alpha = __expf(__fsub_rn(st.m[rb], bm[rb]));   // 0 when m = -inf
-                st.l[rb] = __fmul_rn(st.l[rb], alpha);
-#pragma unroll
-                for (int db = 0; db < 8; ++db) {
-                    f32x4 o = st.o[rb][db];
-                    o[0] = __fmul_rn(o[0], alpha);
-                    o[1] = __fmul_rn(o[1], alpha);
-                    o[2] = __fmul_rn(o[2], alpha);
-                    o[3] = __fmul_rn(o[3], alpha);
-                    st.o[rb][db] = o;
-                }
-                st.m[rb] = bm[rb];
-            }
-        }
-    }
+__device__ __forceinline__ void rows4_update(Rows4& st, float (&umax)[4], float (&sc)[4][8], const u32x2 (&v)[8][2]) {
     bf16x8 P[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
-        const float m_s = st.m[rb] == -INFINITY ? 0.0f : st.m[rb];
-        float p[8], ps = 0.0f;
+        umax[rb] = fmaxf(umax[rb], fmaxf(fmaxf(fmaxf(sc[rb][0], sc[rb][1]), fmaxf(sc[rb][2], sc[rb][3])),
+                                         fmaxf(fmaxf(sc[rb][4], sc[rb][5]), fmaxf(sc[rb][6], sc[rb][7]))));
+        float p[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            p[e] = __expf(__fsub_rn(sc[rb][e], m_s));
-            ps = __fadd_rn(ps, p[e]);
-        }
-        st.l[rb] = __fadd_rn(st.l[rb], ps);
+        for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(__fsub_rn(sc[rb][e], st.m[rb]));
+        st.l[rb] = __fadd_rn(st.l[rb], __fadd_rn(__fadd_rn(__fadd_rn(p[0], p[1]), __fadd_rn(p[2], p[3])),
+                                                 __fadd_rn(__fadd_rn(p[4], p[5]), __fadd_rn(p[6], p[7]))));
         P[rb] = to_bf16x8(p);
     }
 #pragma unroll
@@ -929,7 +901,36 @@ __device__ __forceinline__ void rows4_update(Rows4& st, float (&sc)[4][8], const
     }
 }
 
-constexpr int ROUTE_LDS_WORDS = 2 * MAX_NB_LDS + MAX_NB_LDS / 4 + 8;   // keys + sidx + excl bytes
+// Per-wave LDS ring of 32-key blocks: [QK A operands 4 KB | PV A operands 8 KB | scales 256 B].
+constexpr int RING_SLOTS = 3;
+constexpr int SLOT_BYTES = 4096 + 8192 + 256;
+constexpr int BLOCK_DMA = 13;                       // direct-to-LDS loads per wave per block
+constexpr int MAX_KX_LDS = 1024;                    // near leaves per tile the route kernel holds
+
+// QK operand chunk j (0..3) of lane: [hh = j>>1][ks = j&1][grp][col] <- row (row0[hh] + col),
+// bytes (4ks + grp)*16 of an int8 [*, 128] matrix.
+__device__ __forceinline__ void dma_qk(const int8_t* __restrict__ x8, int64_t row0a, int64_t row0b, char* slot,
+                                       int lane) {
+    const int col = lane & 15, grp = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t row = ((j >> 1) ? row0b : row0a) + col;
+        dma16(x8 + row * D + (4 * (j & 1) + grp) * 16, slot + j * 1024);
+    }
+}
+
+// PV operand chunk j (0..7) of lane: 8-byte units [h][db][grp][col], 16-byte chunk = col pair p,
+// from quad (q0[h] + grp), dims 16db + 2p .. +1 of a key-quad bf16 matrix.
+__device__ __forceinline__ void dma_pv(const uint16_t* __restrict__ x4, int64_t q0a, int64_t q0b, char* slot,
+                                       int lane) {
+    const int p = lane & 7, grp = (lane >> 3) & 3, dbl = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int db = (2 * j + dbl) & 7;
+        const int64_t quad = ((j >> 2) ? q0b : q0a) + grp;
+        dma16(x4 + (quad * D + 16 * db + 2 * p) * 4, slot + 4096 + j * 1024);
+    }
+}
 
 template <int LEAF>
 __global__ __launch_bounds__(256) void route_kernel(
@@ -939,17 +940,17 @@ __global__ __launch_bounds__(256) void route_kernel(
     const float* __restrict__ ks, const uint16_t* __restrict__ vq, int64_t nq, int nt, int64_t nk, int nb,
     int nb_pad, int kx, int sink, int stride, float scale, float* __restrict__ out,
     float* __restrict__ logz, int32_t* __restrict__ idx_out) {
-    __shared__ __align__(16) uint32_t smem[ROUTE_LDS_WORDS];
+    __shared__ __align__(16) char ring[4][RING_SLOTS][SLOT_BYTES];   // also: SEL keys, merge staging
+    __shared__ int32_t sidx[MAX_KX_LDS];
+    __shared__ uint32_t exbits[MAX_NB_LDS / 32 + 1];
     __shared__ TopkSmem sm;
     __shared__ float red_m[4][64], red_l[4][64];
-    uint32_t* keys = smem;                                   // [MAX_NB_LDS] during select / top-k
-    int32_t* sidx = (int32_t*)(smem + MAX_NB_LDS);           // [MAX_NB_LDS] selected leaves
-    int8_t* exl = (int8_t*)(smem + 2 * MAX_NB_LDS);          // [MAX_NB_LDS + 32] exclusion bytes
-    float* mrg = (float*)smem;                               // merge staging (after top-k): 4 x 64 x 32 floats
+    uint32_t* keys = (uint32_t*)&ring[0][0][0];               // [nb] during select / top-k
+    float* mrg = (float*)&ring[0][0][0];                       // merge staging: 4 x 64 x 33 floats
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int t = blockIdx.x, h = blockIdx.z;
     const int64_t th = (int64_t)h * nt + t;
-    // ---- 1. select (bit-exact)
+    // ---- 1. select (bit-exact, same arithmetic as select_kernel)
     {
         const int ts = TILE / stride;
         i32x4 b[4][2];
@@ -963,6 +964,7 @@ __global__ __launch_bounds__(256) void route_kernel(
             i32x4 a[2];
             f32x4 sg, lz;
         };
+        float rmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // row max of the far scores
         auto sel_load = [&](SelOps& o, int c) {
             const int64_t s0 = th * nb_pad + c;
 #pragma unroll
@@ -980,10 +982,14 @@ __global__ __launch_bounds__(256) void route_kernel(
             float best[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                const bool lv = c + 4 * grp + i < nb;
                 best[i] = -INFINITY;
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb)
-                    if (val[rb]) best[i] = fmaxf(best[i], __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], o.sg[i])));
+                for (int rb = 0; rb < 4; ++rb) {
+                    const float x = __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], o.sg[i]));
+                    best[i] = fmaxf(best[i], val[rb] ? x : -INFINITY);
+                    rmax[rb] = fmaxf(rmax[rb], lv ? __fadd_rn(x, o.lz[i]) : -INFINITY);
+                }
                 best[i] = col_max(best[i]);
             }
             if (col == 0) {
@@ -1004,29 +1010,54 @@ __global__ __launch_bounds__(256) void route_kernel(
             if (c1 + 64 < nb) sel_load(sa, c1 + 64);
             sel_block(sb2, c1);
         }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {       // row r = stride * (16 rb + col) of the sampled rows
+            const float mx = grp_max(rmax[rb]);
+            if (grp == 0) red_m[w][16 * rb + col] = mx;
+        }
     }
+    for (int i = threadIdx.x; i < MAX_NB_LDS / 32 + 1; i += 256) exbits[i] = 0u;
     __syncthreads();
-    // ---- 2. top-k
-    const int kxe = kx < nb ? kx : nb;
+    // ---- 2. top-k -> sidx (ascending), exclusion bits
+    const int kxe = min(min(kx, nb), MAX_KX_LDS);
     if (kxe > 0) {
-        topk_row(keys, nb, kxe, sm, idx_out ? idx_out + th * kxe : nullptr, exl, sidx);
-    } else {
-        for (int l = threadIdx.x; l < nb; l += 256) exl[l] = 0;
-        __syncthreads();
+        topk_row(keys, nb, kxe, sm, idx_out ? idx_out + th * kxe : nullptr, nullptr, sidx);
+        for (int j = threadIdx.x; j < kxe; j += 256) atomicOr(&exbits[sidx[j] >> 5], 1u << (sidx[j] & 31));
     }
-    // ---- 3. split-K far + near: wave w, all rows
+    __syncthreads();                       // keys dead from here: the ring may be overwritten
+    // ---- 3. split-K far + near: wave w, all rows, fixed reference max per row
+    float mref[4];
+    {
+        const int ts = TILE / stride;
+        float tile_max = -INFINITY;              // fallback reference for rows the select skipped
+        for (int r = 0; r < ts; ++r)
+            tile_max = fmaxf(tile_max, fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r])));
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int r = 16 * rb + col;
+            float m = tile_max;
+            if (stride == 1) m = fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r]));
+            mref[rb] = m == -INFINITY ? 0.0f : __fmul_rn(m, LOG2E);
+        }
+    }
+    __syncthreads();                       // red_m is reused by the merge
     Rows4 st;
+    float umax[4];
+    char* myring = &ring[w][0][0];
+    const int64_t kh = (int64_t)h * nk;
+    for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
-        st.m[rb] = -INFINITY;
+        st.m[rb] = mref[rb];
         st.l[rb] = 0.0f;
+        umax[rb] = -INFINITY;
 #pragma unroll
         for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    const int64_t kh = (int64_t)h * nk;
-    {   // far field: leaves [lo, hi)
+    {   // far field: leaves [lo, hi), 32-leaf blocks through the LDS ring
         const int lpw = ((nb + 3) / 4 + 31) / 32 * 32;
         const int lo = w * lpw, hi = min(nb, lo + lpw);
+        const int nblk = hi > lo ? (hi - lo + 31) / 32 : 0;
         i32x4 bq[4][2];
         float srow[4];
 #pragma unroll
@@ -1034,50 +1065,68 @@ __global__ __launch_bounds__(256) void route_kernel(
             const int64_t p = th * TILE + 16 * rb + col;
 #pragma unroll
             for (int kss = 0; kss < 2; ++kss) bq[rb][kss] = *(const i32x4*)(dq8 + p * D + 64 * kss + 16 * grp);
-            srow[rb] = sdq[p];
+            srow[rb] = __fmul_rn(sdq[p], LOG2E);
         }
         const int64_t srow0 = th * nb_pad;
-        const uint16_t* vb0 = vbq + (th * nb_pad / 4) * D * 4;
-        FarQK qa, qb;
-        auto far_block = [&](const FarQK& f, int c0) {
-            u32x2 v[8][2];
-            load_pv(v, vb0, c0 / 4, c0 / 4 + 4, col, grp);
+        const int64_t qbase = th * nb_pad / 4;
+        auto issue = [&](int bi) {
+            const int c0 = lo + 32 * bi;
+            char* slot = myring + (bi % RING_SLOTS) * SLOT_BYTES;
+            dma_qk(g8, srow0 + c0, srow0 + c0 + 16, slot, lane);
+            dma_pv(vbq, qbase + c0 / 4, qbase + c0 / 4 + 4, slot, lane);
+            if (lane < 16) {
+                const float* src = (lane < 8 ? sg + srow0 + c0 + 4 * lane : lz + srow0 + c0 + 4 * (lane - 8));
+                dma16(src, slot + 12288);
+            }
+        };
+        if (nblk > 0) issue(0);
+        if (nblk > 1) issue(1);
+        for (int bi = 0; bi < nblk; ++bi) {
+            if (bi + 2 < nblk) issue(bi + 2);
+            const int ahead = min(2, nblk - 1 - bi);
+            if (ahead == 2) wait_vmcnt<2 * BLOCK_DMA>();
+            else if (ahead == 1) wait_vmcnt<BLOCK_DMA>();
+            else wait_vmcnt<0>();
+            const char* slot = myring + (bi % RING_SLOTS) * SLOT_BYTES;
+            const int c0 = lo + 32 * bi;
+            const uint32_t exw = exbits[c0 >> 5];
             float sc[4][8];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
+                const i32x4 A0 = *(const i32x4*)(slot + ((hh * 2 + 0) * 64 + lane) * 16);
+                const i32x4 A1 = *(const i32x4*)(slot + ((hh * 2 + 1) * 64 + lane) * 16);
                 i32x4 acc[4];
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb) {
-                    acc[rb] = mfma_i8(f.g[hh][0], bq[rb][0], i32x4{0, 0, 0, 0});
-                    acc[rb] = mfma_i8(f.g[hh][1], bq[rb][1], acc[rb]);
+                    acc[rb] = mfma_i8(A0, bq[rb][0], i32x4{0, 0, 0, 0});
+                    acc[rb] = mfma_i8(A1, bq[rb][1], acc[rb]);
                 }
+                const f32x4 sgv = *(const f32x4*)(slot + 12288 + (16 * hh + 4 * grp) * 4);
+                const f32x4 lzv = *(const f32x4*)(slot + 12288 + 128 + (16 * hh + 4 * grp) * 4);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int c = c0 + 16 * hh + 4 * grp + i;
-                    const bool ok = c < hi && ((f.ex[hh] >> (8 * i)) & 0xffu) == 0u;
+                    const int cl = 16 * hh + 4 * grp + i;          // leaf within the block
+                    const bool ok = c0 + cl < hi && ((exw >> cl) & 1u) == 0u;
+                    const float bias = ok ? __fmul_rn(lzv[i], LOG2E) : -INFINITY;
 #pragma unroll
                     for (int rb = 0; rb < 4; ++rb)
-                        sc[rb][4 * hh + i] =
-                            ok ? __fadd_rn(__fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], f.sg[hh][i])), f.lz[hh][i])
-                               : -INFINITY;
+                        sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i]), bias);
                 }
             }
-            rows4_update(st, sc, v);
-        };
-        if (lo < hi) load_far_qk(qa, srow0, g8, sg, lz, exl, lo, col, grp);
-        for (int c0 = lo; c0 < hi; c0 += 64) {
-            const int c1 = c0 + 32;
-            if (c1 < hi) load_far_qk(qb, srow0, g8, sg, lz, exl, c1, col, grp);
-            far_block(qa, c0);
-            if (c1 >= hi) break;
-            if (c1 + 32 < hi) load_far_qk(qa, srow0, g8, sg, lz, exl, c1 + 32, col, grp);
-            far_block(qb, c1);
+            u32x2 v[8][2];
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+                    v[db][hf] = *(const u32x2*)(slot + 4096 + ((((hf * 8 + db) * 4 + grp) * 16 + col) * 8));
+            rows4_update(st, umax, sc, v);
         }
     }
-    {   // near field: tokens [e_lo, e_hi) of the selected list
+    {   // near field: tokens [e_lo, e_hi) of the selected list, same ring
         const int e_n = kxe * LEAF;
         const int epw = ((e_n + 3) / 4 + 31) / 32 * 32;
         const int e_lo = w * epw, e_hi = min(e_n, e_lo + epw);
+        const int nblk = e_hi > e_lo ? (e_hi - e_lo + 31) / 32 : 0;
         i32x4 bq[4][2];
         float srow[4];
 #pragma unroll
@@ -1085,44 +1134,73 @@ __global__ __launch_bounds__(256) void route_kernel(
             const int64_t p = th * TILE + 16 * rb + col;
 #pragma unroll
             for (int kss = 0; kss < 2; ++kss) bq[rb][kss] = *(const i32x4*)(q8 + p * D + 64 * kss + 16 * grp);
-            srow[rb] = sq[p];
+            srow[rb] = __fmul_rn(__fmul_rn(sq[p], scale), LOG2E);
         }
-        NearQK qa, qb;
-        auto near_block = [&](const NearQK& n, int e0) {
-            u32x2 v[8][2];
-            load_pv(v, vq, n.tok0[0] / 4, n.tok0[1] / 4, col, grp);
+        auto tok_of = [&](int j) {         // first token of the 16-token run at list position j
+            const int jj = j < e_hi ? j : e_lo;
+            return kh + (int64_t)sidx[jj / LEAF] * LEAF + (jj % LEAF);
+        };
+        auto issue = [&](int bi) {
+            const int e0 = e_lo + 32 * bi;
+            const int64_t t0 = tok_of(e0), t1 = tok_of(e0 + 16);
+            char* slot = myring + (bi % RING_SLOTS) * SLOT_BYTES;
+            dma_qk(k8, t0, t1, slot, lane);
+            dma_pv(vq, t0 / 4, t1 / 4, slot, lane);
+            if (lane < 8) dma16(ks + (lane < 4 ? t0 + 4 * lane : t1 + 4 * (lane - 4)), slot + 12288);
+        };
+        // the ring slots of the far loop are all consumed: the near loop restarts at slot 0
+        if (nblk > 0) issue(0);
+        if (nblk > 1) issue(1);
+        for (int bi = 0; bi < nblk; ++bi) {
+            if (bi + 2 < nblk) issue(bi + 2);
+            const int ahead = min(2, nblk - 1 - bi);
+            if (ahead == 2) wait_vmcnt<2 * BLOCK_DMA>();
+            else if (ahead == 1) wait_vmcnt<BLOCK_DMA>();
+            else wait_vmcnt<0>();
+            const char* slot = myring + (bi % RING_SLOTS) * SLOT_BYTES;
+            const int e0 = e_lo + 32 * bi;
             float sc[4][8];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
+                const i32x4 A0 = *(const i32x4*)(slot + ((hh * 2 + 0) * 64 + lane) * 16);
+                const i32x4 A1 = *(const i32x4*)(slot + ((hh * 2 + 1) * 64 + lane) * 16);
                 i32x4 acc[4];
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb) {
-                    acc[rb] = mfma_i8(n.k[hh][0], bq[rb][0], i32x4{0, 0, 0, 0});
-                    acc[rb] = mfma_i8(n.k[hh][1], bq[rb][1], acc[rb]);
+                    acc[rb] = mfma_i8(A0, bq[rb][0], i32x4{0, 0, 0, 0});
+                    acc[rb] = mfma_i8(A1, bq[rb][1], acc[rb]);
                 }
+                const f32x4 ksv = *(const f32x4*)(slot + 12288 + (16 * hh + 4 * grp) * 4);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const bool ok = n.ok[hh] && (e0 + 16 * hh + 4 * grp + i) < e_hi;
+                    const bool ok = (e0 + 16 * hh + 4 * grp + i) < e_hi;
+                    const float bias = ok ? 0.0f : -INFINITY;
 #pragma unroll
                     for (int rb = 0; rb < 4; ++rb)
-                        sc[rb][4 * hh + i] =
-                            ok ? __fmul_rn((float)acc[rb][i], __fmul_rn(__fmul_rn(srow[rb], n.ks[hh][i]), scale))
-                               : -INFINITY;
+                        sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]), bias);
                 }
             }
-            rows4_update(st, sc, v);
-        };
-        if (e_lo < e_hi) load_near_qk<LEAF>(qa, e_lo, e_hi, e_lo, sidx, kh, k8, ks, col, grp);
-        for (int e0 = e_lo; e0 < e_hi; e0 += 64) {
-            const int e1 = e0 + 32;
-            if (e1 < e_hi) load_near_qk<LEAF>(qb, e1, e_hi, e_lo, sidx, kh, k8, ks, col, grp);
-            near_block(qa, e0);
-            if (e1 >= e_hi) break;
-            if (e1 + 32 < e_hi) load_near_qk<LEAF>(qa, e1 + 32, e_hi, e_lo, sidx, kh, k8, ks, col, grp);
-            near_block(qb, e1);
+            u32x2 v[8][2];
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+                    v[db][hf] = *(const u32x2*)(slot + 4096 + ((((hf * 8 + db) * 4 + grp) * 16 + col) * 8));
+            rows4_update(st, umax, sc, v);
         }
     }
-    // ---- 4. merge the four partial states (h3/htrc_flat_triton.py:263-273 algebra)
+        // rows whose scores outran the reference by 2^64, or underflowed: redo with the true max
+        bool bad = false;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const float lt = grp_sum(st.l[rb]);
+            const bool r_bad = umax[rb] > mref[rb] + REF_SLACK || (umax[rb] > -INFINITY && lt < 0x1p-60f);
+            if (r_bad) mref[rb] = umax[rb];
+            bad |= r_bad;
+        }
+        if (!__any(bad)) break;
+    }
+    // ---- 4. merge the four partial states (h3/htrc_flat_triton.py:263-273 algebra, log2 units)
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
         const float lt = grp_sum(st.l[rb]);
@@ -1131,23 +1209,22 @@ __global__ __launch_bounds__(256) void route_kernel(
             red_l[w][16 * rb + col] = lt;
         }
     }
-    __syncthreads();                      // also: every wave is done with keys / sidx / exl
+    __syncthreads();                      // every wave is done with its ring
     float wsc[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
         const int r = 16 * rb + col;
         float mm = fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r]));
         mm = mm == -INFINITY ? 0.0f : mm;
-        wsc[rb] = __expf(__fsub_rn(st.m[rb], mm));
+        wsc[rb] = exp2f(__fsub_rn(st.m[rb], mm));
     }
-    // row r handled by thread (r, quarter): merged den and logZ
     const int r_out = threadIdx.x >> 2, qd = threadIdx.x & 3;
     float den = 0.0f, mmr;
     {
         mmr = fmaxf(fmaxf(red_m[0][r_out], red_m[1][r_out]), fmaxf(red_m[2][r_out], red_m[3][r_out]));
         mmr = mmr == -INFINITY ? 0.0f : mmr;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) den = __fadd_rn(den, __fmul_rn(red_l[s][r_out], __expf(__fsub_rn(red_m[s][r_out], mmr))));
+        for (int s = 0; s < 4; ++s) den = __fadd_rn(den, __fmul_rn(red_l[s][r_out], exp2f(__fsub_rn(red_m[s][r_out], mmr))));
     }
     const float dd = den < 1e-30f ? 1e-30f : den;
     const int64_t qi = (int64_t)t * TILE + r_out;
@@ -1182,7 +1259,7 @@ __global__ __launch_bounds__(256) void route_kernel(
         }
         __syncthreads();
     }
-    if (rvalid && qd == 0) logz[orow] = __fadd_rn(mmr, __logf(den));
+    if (rvalid && qd == 0) logz[orow] = __fadd_rn(__fmul_rn(mmr, LN2), __logf(den));   // m in log2 units
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1394,7 +1471,7 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
     REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_route: bad sizes");
     const int64_t nb = nk / leaf, nt = (nq + TILE - 1) / TILE;
     REQUIRE(nb <= MAX_NB_LDS, "htrc_route: at most 8192 leaves per head");
-    REQUIRE(kx >= 0 && sink >= 0, "htrc_route: bad near-leaf count");
+    REQUIRE(kx >= 0 && sink >= 0 && (kx < nb ? kx : nb) <= MAX_KX_LDS, "htrc_route: at most 1024 near leaves per tile");
     REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_route: stride must divide 64");
     dim3 grid((unsigned)nt, 1, (unsigned)heads);
     hipStream_t s = (hipStream_t)stream;
