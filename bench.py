@@ -36,7 +36,7 @@ def algorithmic(h, nq, nk, leaf, kx, d=128, tile=64):
     rows = nt * tile
     f = {}
     f["pack_q"] = {"bytes": h * (2 * nq * d + 2 * rows * d + 8 * rows + 4 * nt * d)}
-    f["pack_kv"] = {"bytes": h * (4 * nk * d + nk * d + 4 * nk + 4 * nk * d)}
+    f["pack_k"] = {"bytes": h * (2 * nk * d + nk * d + 4 * nk)}
     f["stats"] = {"bytes": h * (4 * nk * d + nt * nb * (3 * d + 8)),
                   "flops_fp32": h * 6 * nt * nk * d}
     state = nt * nb * (3 * d + 8)
@@ -147,14 +147,14 @@ def main():
     # per-kernel launch durations, HIP events on the stream the kernels are launched on
     scale = 1.0 / math.sqrt(d)
     mu, q8, sq, dq8, sdq = hip.pack_q(q, ws=ws)
-    k8, ks, kq, vq = hip.pack_kv(k, v, ws=ws)
-    g8, lz, vbq, sg, _ = hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws, kq=kq, vq=vq)
-    packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "vq": vq}
-    lstate = {"g8": g8, "sg": sg, "lz": lz, "vbq": vbq}
+    k8, ks = hip.pack_k(k, ws=ws)
+    g8, lz, vbs, sg, _ = hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws)
+    packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "v": v}
+    lstate = {"g8": g8, "sg": sg, "lz": lz, "vb": vbs}
     stages = {
         "pack_q": lambda: hip.pack_q(q, ws=ws),
-        "pack_kv": lambda: hip.pack_kv(k, v, ws=ws),
-        "stats": lambda: hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws, kq=kq, vq=vq),
+        "pack_k": lambda: hip.pack_k(k, ws=ws),
+        "stats": lambda: hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws),
         "route": lambda: hip.route(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, ws=ws),
     }
     kms = {}

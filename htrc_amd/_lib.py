@@ -13,7 +13,7 @@ import torch
 
 HERE = Path(__file__).resolve().parent
 LIBPATH = HERE / "libhtrc_flat.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -26,8 +26,8 @@ SIGNATURES = {
     "htrc_last_error": [],
     "htrc_nb_pad": [_i64],
     "htrc_pack_q": [_vp, _int, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp],
-    "htrc_pack_kv": [_vp, _vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp],
-    "htrc_leaf_stats": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _flt, _vp, _vp, _vp, _vp, _vp],
+    "htrc_pack_k": [_vp, _i64, _i64, _int, _vp, _vp, _vp],
+    "htrc_leaf_stats": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _flt, _vp, _vp, _vp, _vp, _vp],
     "htrc_select": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp, _vp],
     "htrc_topk": [_vp, _i64, _i64, _int, _int, _vp, _vp, _vp],
     "htrc_tile": [_vp] * 13 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _flt] + [_vp] * 6,

@@ -30,10 +30,13 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
     return u >> 16;
 }
 
-// where(x >= 0, x + 0.5, x - 0.5) in fp32, then truncation toward zero.
-__device__ __forceinline__ int round_away(float x) {
-    float y = x >= 0.0f ? __fadd_rn(x, 0.5f) : __fsub_rn(x, 0.5f);
-    return (int)truncf(y);
+// where(x >= 0, x + 0.5, x - 0.5) in fp32, then truncation toward zero: the same fp32 sum
+// as x + copysign(0.5, x) (for x = -0 both truncate to 0), and v_cvt_i32_f32 truncates.
+__device__ __forceinline__ int round_away(float x) { return (int)__fadd_rn(x, copysignf(0.5f, x)); }
+
+// Four int8 values (given as int32 in [-128, 127]) packed little-endian into a dword.
+__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)d << 24);
 }
 
 // rint (half to even) clamped to +-127.
@@ -132,6 +135,24 @@ __device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Transposing 64-bit LDS read (ds_read_b64_tr_b16).  Within each 16-lane group, lane i
+// receives element i % 4 of the 8-byte reads of lanes 4j + i / 4, j = 0..3.  When lane L of
+// a group points at 4 consecutive bf16 of row (R0 + L / 4) at column C0 + 4 (L % 4), lane i
+// gets X[R0 + j][C0 + i] for j = 0..3: four consecutive keys at one column, the k-items of
+// a PV-type MFMA operand, read straight from row-major data.
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+    return __builtin_bit_cast(u32x2, v);
+}
+
+// XOR swizzle of the 16-byte chunks of a 256-byte LDS row: row r keeps chunk c at c ^ swz(r).
+// 16 consecutive rows read at one chunk hit 16 different chunks (QK operand reads), and
+// 8 consecutive rows read at a chunk pair hit 16 different chunks (transposing reads).
+__device__ __forceinline__ int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
 // Order-preserving uint32 key of a float (larger float -> larger key); -0 maps to +0.
 __device__ __forceinline__ uint32_t order_key(float f) {

@@ -3,7 +3,7 @@
 // Pipeline of one layer call (every kernel takes a head index in grid.z / grid.y, so all
 // heads of a layer go in one launch):
 //   pack_q    q rows -> tile centres mu, q8/sq, dq8/sdq          (HBM-bound)
-//   pack_kv   k, v   -> k8/ks, bf16 K and V in key-quad layout   (HBM-bound)
+//   pack_k    k      -> k8/ks                                     (HBM-bound)
 //   stats     mu, K, V -> per (tile, leaf) g8/sg, vb, lz          (bf16 MFMA, HBM writes)
 //   select    dq8, g8 -> SEL[t, l]                                (int8 MFMA)
 //   topk      SEL -> idx (ascending), excl                        (LDS radix select)
@@ -16,9 +16,8 @@
 // query row (or tile centre) of a C element is always lane%16 and the online-softmax
 // statistics of a row never leave its four lanes.
 //
-// Key-quad layout ("q4") of a bf16 matrix X[rows][128]: X4[row / 4][col][row % 4].  It
-// makes the eight k-items of a PV operand (two runs of four consecutive keys at one
-// column) two 8-byte loads.
+// PV-type operands (eight k-items = two runs of four consecutive keys at one column) are
+// read from row-major data staged in LDS with the gfx950 transposing read (lds_read_tr16).
 #include "common.h"
 
 #include <stdio.h>
@@ -86,14 +85,11 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
 }
 
 // ---------------------------------------------------------------------------------------------
-// pack_kv: one workgroup per 64 key rows of a head.  k8/ks per row (h3/htrc_flat.py:216-218,
-// round half to even), plus bf16 K and V re-laid out in key-quad layout for the PV-type
-// MFMA operands of the stats and tile kernels.
+// pack_k: one workgroup per 64 key rows of a head.  k8/ks per row (h3/htrc_flat.py:216-218,
+// round half to even).
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void pack_kv_kernel(const uint16_t* __restrict__ k,
-                                                      const uint16_t* __restrict__ v, int64_t nk,
-                                                      int8_t* __restrict__ k8, float* __restrict__ ks,
-                                                      uint16_t* __restrict__ kq, uint16_t* __restrict__ vq) {
+__global__ __launch_bounds__(256) void pack_k_kernel(const uint16_t* __restrict__ k, int64_t nk,
+                                                     int8_t* __restrict__ k8, float* __restrict__ ks) {
     const int h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int64_t r0 = (int64_t)blockIdx.x * 64;
     const int64_t base = (int64_t)h * nk;
@@ -102,46 +98,26 @@ __global__ __launch_bounds__(256) void pack_kv_kernel(const uint16_t* __restrict
         if (r >= nk) break;
         const uint32_t pr = ((const uint32_t*)(k + (base + r) * D))[lane];
         const float x0 = bf2f(pr & 0xffffu), x1 = bf2f(pr >> 16);
-        const float s = row_scale(wave_max(fmaxf(fabsf(x0), fabsf(x1))), 1e-20f);
-        const uint16_t o = (uint16_t)((round_even_clamp(__fdiv_rn(x0, s)) & 0xff) |
-                                      ((round_even_clamp(__fdiv_rn(x1, s)) & 0xff) << 8));
+        const float sc = row_scale(wave_max(fmaxf(fabsf(x0), fabsf(x1))), 1e-20f);
+        const uint16_t o = (uint16_t)((round_even_clamp(__fdiv_rn(x0, sc)) & 0xff) |
+                                      ((round_even_clamp(__fdiv_rn(x1, sc)) & 0xff) << 8));
         ((uint16_t*)(k8 + (base + r) * D))[lane] = o;
-        if (lane == 0) ks[base + r] = s;
-    }
-    // key-quad relayout: item = (quad within the 64 rows, column pair)
-    for (int it = tid; it < 16 * 64; it += 256) {
-        const int quad = it >> 6, cp = it & 63;
-        const int64_t rq = r0 + quad * 4;
-        if (rq >= nk) continue;
-        uint32_t kk[4], vv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            kk[i] = ((const uint32_t*)(k + (base + rq + i) * D))[cp];
-            vv[i] = ((const uint32_t*)(v + (base + rq + i) * D))[cp];
-        }
-        const int64_t qo = ((base + rq) / 4) * D * 4;   // quad row start (in bf16 units)
-        u32x2 k0 = {(kk[0] & 0xffffu) | (kk[1] << 16), (kk[2] & 0xffffu) | (kk[3] << 16)};
-        u32x2 k1 = {(kk[0] >> 16) | (kk[1] & 0xffff0000u), (kk[2] >> 16) | (kk[3] & 0xffff0000u)};
-        u32x2 v0 = {(vv[0] & 0xffffu) | (vv[1] << 16), (vv[2] & 0xffffu) | (vv[3] << 16)};
-        u32x2 v1 = {(vv[0] >> 16) | (vv[1] & 0xffff0000u), (vv[2] >> 16) | (vv[3] & 0xffff0000u)};
-        *(u32x2*)(kq + qo + (2 * cp) * 4) = k0;
-        *(u32x2*)(kq + qo + (2 * cp + 1) * 4) = k1;
-        *(u32x2*)(vq + qo + (2 * cp) * 4) = v0;
-        *(u32x2*)(vq + qo + (2 * cp + 1) * 4) = v1;
+        if (lane == 0) ks[base + r] = sc;
     }
 }
 
 // ---------------------------------------------------------------------------------------------
 // stats: leaf statistics at the tile centres (h3/htrc_flat_triton.py:41-85, I8 store).
 // Workgroup = 64 tile centres (16 per wave) x a range of leaves of one head.  Per leaf:
-//   a^T = K_l mu^T         bf16 MFMA, mu split into three bf16 terms (~fp32 product)
-//   softmax over the leaf's keys per centre (lane%16 = centre)
-//   g^T = K_l^T w^T, vb^T = V_l^T w^T   bf16 MFMA, w split into 3 (g) / 2 (vb) bf16 terms
-// The leaf's K (row layout) and key-quad K, V are staged in LDS by gfx950 direct
-// global->LDS loads, one leaf ahead (double buffer), and shared by the four waves; the LDS
-// chunk order makes every MFMA operand read a contiguous, conflict-free 512 B / 1 KB.
-// Leaves are processed four at a time so that vb can be stored in the leaf-quad layout
-// vbq[t][l/4][d][l%4] that the far-field PV operand reads with 8-byte loads.
+//   a^T = K_l mu^T                      bf16 MFMA, mu split into three bf16 terms (~fp32)
+//   e = exp(a - max) per centre (lane%16 = centre), z = sum e
+//   g^T = K_l^T w_g^T, vb^T = V_l^T w_v^T   w_g = e * scale / z in three bf16 terms,
+//                                            w_v = e / z in two
+// The leaf's K and V rows are staged in LDS (XOR-swizzled 16-byte chunks) by gfx950 direct
+// global->LDS loads one leaf ahead; the QK operand is a plain 16-byte read, the PV-type
+// operands come from the same rows through transposing reads.  Each leaf's outputs are
+// stored during the next leaf, so the one vmcnt wait per leaf only covers loads and stores
+// issued a full leaf earlier.
 // ---------------------------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -156,46 +132,42 @@ __device__ __forceinline__ void wait_vmcnt() {          // s_waitcnt vmcnt(N), o
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-// Stage leaf l (LEAF keys) of one head into an LDS buffer: chunk c of 16 bytes, c = j*256 + tid.
-//   [0, 16L)      K rows:    c = ((kb*4 + ks)*4 + grp)*16 + col  <- K[16kb + col][dims 32ks + 8grp ..]
-//   [16L, 32L)    key-quad K: c = (((kk*2 + h)*8 + db)*4 + grp)*8 + p <- Kq[8kk + 4h + grp][16db + 2p ..]
-//   [32L, 48L)    key-quad V: same order from Vq
+// Stage leaf rows [key0, key0 + LEAF) of K and V: LDS chunk s = j*256 + tid holds the
+// 16-byte chunk (s % 16) ^ swz(row) of row (s / 16) % LEAF of K (first half) or V.
 template <int LEAF>
-__device__ __forceinline__ void stage_leaf(const uint16_t* __restrict__ K, const uint16_t* __restrict__ kq,
-                                           const uint16_t* __restrict__ vq, int64_t key0, char* buf) {
-    constexpr int NC = 48 * LEAF;              // 16-byte chunks per leaf
+__device__ __forceinline__ void stage_leaf(const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+                                           int64_t key0, char* buf) {
+    constexpr int NC = 32 * LEAF;              // 16-byte chunks per leaf (K and V)
     const int tid = threadIdx.x, w = tid >> 6;
 #pragma unroll
     for (int j = 0; j < NC / 256; ++j) {
         const int c = j * 256 + tid;
-        const void* src;
-        if (c < 16 * LEAF) {
-            const int col = c & 15, grp = (c >> 4) & 3, ks = (c >> 6) & 3, kb = c >> 8;
-            src = K + (key0 + 16 * kb + col) * D + 32 * ks + 8 * grp;
-        } else {
-            const int cc = c & (16 * LEAF - 1);
-            const int p = cc & 7, grp = (cc >> 3) & 3, db = (cc >> 5) & 7, h = (cc >> 8) & 1, kk = cc >> 9;
-            const int64_t quad = key0 / 4 + 8 * kk + 4 * h + grp;
-            src = (c < 32 * LEAF ? kq : vq) + (quad * D + 16 * db + 2 * p) * 4;
-        }
-        dma16(src, buf + (size_t)(j * 256 + w * 64) * 16);
+        const int row = (c >> 4) & (LEAF - 1), pc = c & 15;
+        const uint16_t* X = c < 16 * LEAF ? K : V;
+        dma16(X + (key0 + row) * D + 8 * (pc ^ swz(row)), buf + (size_t)(j * 256 + w * 64) * 16);
     }
 }
 
+// PV-type operand half from swizzled LDS rows: keys rbase + 4grp + j (j = 0..3) at column
+// 16db + lane%16.
+__device__ __forceinline__ u32x2 tr_operand(const char* rows, int rbase, int db, int lane) {
+    const int L = lane & 15, grp = lane >> 4;
+    const int row = rbase + 4 * grp + (L >> 2);
+    const int c = 2 * db + ((L & 3) >> 1);
+    return lds_read_tr16(rows + (row * 16 + (c ^ swz(row))) * 16 + 8 * (L & 1));
+}
+
 template <int LEAF>
-__global__ __launch_bounds__(256) void stats_kernel(const float* __restrict__ mu, int nt,
-                                                    const uint16_t* __restrict__ k,
-                                                    const uint16_t* __restrict__ kq,
-                                                    const uint16_t* __restrict__ vq, int64_t nk, int nb,
-                                                    int nb_pad, int lpb, float scale,
-                                                    int8_t* __restrict__ g8, float* __restrict__ sg,
-                                                    uint16_t* __restrict__ vbq, float* __restrict__ lz) {
+__global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__ mu, int nt,
+                                                       const uint16_t* __restrict__ k,
+                                                       const uint16_t* __restrict__ v, int64_t nk, int nb,
+                                                       int nb_pad, int lpb, float scale,
+                                                       int8_t* __restrict__ g8, float* __restrict__ sg,
+                                                       uint16_t* __restrict__ vb, float* __restrict__ lz) {
     constexpr int KB = LEAF / 16;                 // 16-key blocks per leaf
     constexpr int KK = (LEAF + 31) / 32;          // 32-key MFMA k-steps per leaf
-    constexpr int LEAF_BYTES = 48 * LEAF * 16;
-    constexpr int NBUF = LEAF <= 64 ? 2 : 1;
-    constexpr int NDMA = 48 * LEAF / 256;         // DMA instructions per wave per leaf
-    __shared__ __align__(16) char lds[NBUF * LEAF_BYTES];
+    constexpr int LEAF_BYTES = 32 * LEAF * 16;
+    __shared__ __align__(16) char lds[2 * LEAF_BYTES];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int h = blockIdx.z;
     const int t = blockIdx.x * 64 + w * 16 + col;   // tile centre of this lane's C column
@@ -215,151 +187,132 @@ __global__ __launch_bounds__(256) void stats_kernel(const float* __restrict__ mu
     const int l1 = min(nb_pad, l0 + lpb);
     const int lr = min(nb, l1);                   // real leaves of this workgroup: [l0, lr)
     const int64_t kh = (int64_t)h * nk;
-    if (NBUF == 2 && l0 < lr) stage_leaf<LEAF>(k, kq, vq, kh + (int64_t)l0 * LEAF, lds);
-    for (int lq = l0; lq < l1; lq += 4) {
-        f32x4 vacc[4][8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int l = lq + j;
-#pragma unroll
-            for (int db = 0; db < 8; ++db) vacc[j][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (l >= nb) {                     // padded leaf: empty state, excluded everywhere
-                if (tval) {
-                    const int64_t s = th * nb_pad + l;
-#pragma unroll
-                    for (int db = 0; db < 8; ++db)
-                        *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = 0u;
-                    if (grp == 0) {
-                        sg[s] = 0.0f;
-                        lz[s] = -INFINITY;
-                    }
-                }
-                continue;
-            }
-            // ---- leaf l's operands: staged one leaf ahead (double buffer) or now (single)
-            char* buf;
-            if (NBUF == 2) {
-                buf = lds + ((l - l0) & 1) * LEAF_BYTES;
-                if (l + 1 < lr) {
-                    stage_leaf<LEAF>(k, kq, vq, kh + (int64_t)(l + 1) * LEAF, lds + ((l + 1 - l0) & 1) * LEAF_BYTES);
-                    wait_vmcnt<NDMA>();
-                } else {
-                    wait_vmcnt<0>();
-                }
-            } else {
-                buf = lds;
-                stage_leaf<LEAF>(k, kq, vq, kh + (int64_t)l * LEAF, lds);
-                wait_vmcnt<0>();
-            }
-            __syncthreads();                   // every wave's chunks of leaf l have landed
-            const char* Kr = buf;
-            const char* Kq4 = buf + 16 * LEAF * 16;
-            const char* Vq4 = buf + 32 * LEAF * 16;
-            f32x4 a[KB];
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                a[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const bf16x8 A = as_bf16x8(*(const u32x4*)(Kr + ((kb * 4 + ks) * 64 + lane) * 16));
-                    a[kb] = mfma_bf16(A, mh[ks], a[kb]);
-                    a[kb] = mfma_bf16(A, mm[ks], a[kb]);
-                    a[kb] = mfma_bf16(A, ml[ks], a[kb]);
-                }
-            }
-            // a[kb][i] = mu_t . k_{16kb + 4grp + i}
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    a[kb][i] = __fmul_rn(a[kb][i], scale);
-                    mx = fmaxf(mx, a[kb][i]);
-                }
-            mx = grp_max(mx);
-            float z = 0.0f;
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    a[kb][i] = __expf(__fsub_rn(a[kb][i], mx));
-                    z = __fadd_rn(z, a[kb][i]);
-                }
-            z = grp_sum(z);
-            // w = e / z is applied after the dots: g = (e.K) * (scale / z), vb = (e.V) / z
-            const float rz = __fdiv_rn(1.0f, z);
-
-            f32x4 gacc[8];
-#pragma unroll
-            for (int db = 0; db < 8; ++db) gacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                float we[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int kb = 2 * kk + (e >> 2);
-                    we[e] = kb < KB ? a[kb < KB ? kb : 0][e & 3] : 0.0f;
-                }
-                bf16x8 W0, W1, W2;
-                split3x8(we, W0, W1, W2);
-#pragma unroll
-                for (int db = 0; db < 8; ++db) {
-                    const u32x2 zero = {0u, 0u};
-                    const int u0 = (((kk * 2 + 0) * 8 + db) * 4 + grp) * 16 + col;   // 8-byte units
-                    const int u1 = (((kk * 2 + 1) * 8 + db) * 4 + grp) * 16 + col;
-                    const u32x2 k0 = *(const u32x2*)(Kq4 + u0 * 8);
-                    const u32x2 k1 = (2 * kk + 1 < KB) ? *(const u32x2*)(Kq4 + u1 * 8) : zero;
-                    const u32x2 v0 = *(const u32x2*)(Vq4 + u0 * 8);
-                    const u32x2 v1 = (2 * kk + 1 < KB) ? *(const u32x2*)(Vq4 + u1 * 8) : zero;
-                    const bf16x8 KA = as_bf16x8(k0, k1), VA = as_bf16x8(v0, v1);
-                    gacc[db] = mfma_bf16(KA, W0, gacc[db]);
-                    gacc[db] = mfma_bf16(KA, W1, gacc[db]);
-                    gacc[db] = mfma_bf16(KA, W2, gacc[db]);
-                    vacc[j][db] = mfma_bf16(VA, W0, vacc[j][db]);
-                    vacc[j][db] = mfma_bf16(VA, W1, vacc[j][db]);
-                }
-            }
-            __syncthreads();                   // buffer of leaf l free for leaf l + 2
-            // g^T: lane holds dims 16db + 4grp + i of centre t
-            const float gs = __fmul_rn(scale, rz);
-            float am = 0.0f;
+    // outputs of the previous leaf, stored during the next one
+    uint32_t pg[8];
+    u32x2 pv[8];
+    float psg = 0.0f, plz = 0.0f;
+    int pl = -1;
+    auto flush = [&]() {
+        if (pl >= 0 && tval) {
+            const int64_t s = th * nb_pad + pl;
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    gacc[db][i] = __fmul_rn(gacc[db][i], gs);
-                    am = fmaxf(am, fabsf(gacc[db][i]));
-                    vacc[j][db][i] = __fmul_rn(vacc[j][db][i], rz);
-                }
+                *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = pg[db];
+                *(u32x2*)(vb + s * D + 16 * db + 4 * grp) = pv[db];
             }
-            am = grp_max(am);
-            am = am < 1e-30f ? 1e-30f : am;
-            const float cq = __fdiv_rn(127.0f, am);
-            if (tval) {
-                const int64_t s = th * nb_pad + l;
-#pragma unroll
-                for (int db = 0; db < 8; ++db) {
-                    uint32_t pk = 0;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) pk |= (uint32_t)(round_away(__fmul_rn(gacc[db][i], cq)) & 0xff) << (8 * i);
-                    *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = pk;
-                }
-                if (grp == 0) {
-                    sg[s] = __fmul_rn(am, R127);
-                    lz[s] = __fadd_rn(mx, __logf(z));
-                }
+            if (grp == 0) {
+                sg[s] = psg;
+                lz[s] = plz;
             }
         }
-        if (tval) {   // vb of the four leaves -> vbq[t][lq/4][dim][0..3]
-            uint16_t* vo = vbq + ((th * nb_pad + lq) / 4) * D * 4;
+        pl = -1;
+    };
+    if (l0 < lr) stage_leaf<LEAF>(k, v, kh + (int64_t)l0 * LEAF, lds);
+    for (int l = l0; l < lr; ++l) {
+        wait_vmcnt<0>();                       // leaf l landed; stores of leaf l - 2 done
+        __syncthreads();                       // ... for every wave; buffer of leaf l - 1 free
+        flush();                               // stores of leaf l - 1
+        if (l + 1 < lr) stage_leaf<LEAF>(k, v, kh + (int64_t)(l + 1) * LEAF, lds + ((l + 1 - l0) & 1) * LEAF_BYTES);
+        const char* Kr = lds + ((l - l0) & 1) * LEAF_BYTES;
+        const char* Vr = Kr + 16 * LEAF * 16;
+        f32x4 a[KB];
 #pragma unroll
-            for (int db = 0; db < 8; ++db)
+        for (int kb = 0; kb < KB; ++kb) {
+            a[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int row = 16 * kb + col;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int dim = 16 * db + 4 * grp + i;
-                    u32x2 o = {pack2bf(vacc[0][db][i], vacc[1][db][i]), pack2bf(vacc[2][db][i], vacc[3][db][i])};
-                    *(u32x2*)(vo + dim * 4) = o;
-                }
+            for (int ks = 0; ks < 4; ++ks) {
+                const bf16x8 A = as_bf16x8(*(const u32x4*)(Kr + (row * 16 + ((4 * ks + grp) ^ swz(row))) * 16));
+                a[kb] = mfma_bf16(A, mh[ks], a[kb]);
+                a[kb] = mfma_bf16(A, mm[ks], a[kb]);
+                a[kb] = mfma_bf16(A, ml[ks], a[kb]);
+            }
+        }
+        // a[kb][i] = mu_t . k_{16kb + 4grp + i}
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[kb][i] = __fmul_rn(a[kb][i], scale);
+                mx = fmaxf(mx, a[kb][i]);
+            }
+        mx = grp_max(mx);
+        float z = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[kb][i] = __expf(__fsub_rn(a[kb][i], mx));
+                z = __fadd_rn(z, a[kb][i]);
+            }
+        z = grp_sum(z);
+        const float rz = __fdiv_rn(1.0f, z);
+        const float cg = __fmul_rn(scale, rz);
+        f32x4 gacc[8], vacc[8];
+#pragma unroll
+        for (int db = 0; db < 8; ++db) gacc[db] = vacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            float wg[8], wv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int kb = 2 * kk + (e >> 2);
+                const float x = kb < KB ? a[kb < KB ? kb : 0][e & 3] : 0.0f;
+                wg[e] = __fmul_rn(x, cg);
+                wv[e] = __fmul_rn(x, rz);
+            }
+            bf16x8 G0, G1, G2, V0, V1, V2;
+            split3x8(wg, G0, G1, G2);
+            split3x8(wv, V0, V1, V2);
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                const u32x2 zero = {0u, 0u};
+                const u32x2 k0 = tr_operand(Kr, 32 * kk, db, lane);
+                const u32x2 k1 = (2 * kk + 1 < KB) ? tr_operand(Kr, 32 * kk + 16, db, lane) : zero;
+                const u32x2 v0 = tr_operand(Vr, 32 * kk, db, lane);
+                const u32x2 v1 = (2 * kk + 1 < KB) ? tr_operand(Vr, 32 * kk + 16, db, lane) : zero;
+                const bf16x8 KA = as_bf16x8(k0, k1), VA = as_bf16x8(v0, v1);
+                gacc[db] = mfma_bf16(KA, G0, gacc[db]);
+                gacc[db] = mfma_bf16(KA, G1, gacc[db]);
+                gacc[db] = mfma_bf16(KA, G2, gacc[db]);
+                vacc[db] = mfma_bf16(VA, V0, vacc[db]);
+                vacc[db] = mfma_bf16(VA, V1, vacc[db]);
+            }
+        }
+        // g^T, vb^T: lane holds dims 16db + 4grp + i of centre t
+        float am = 0.0f;
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) am = fmaxf(am, fabsf(gacc[db][i]));
+        am = grp_max(am);
+        am = am < 1e-30f ? 1e-30f : am;
+        const float cq = __fdiv_rn(127.0f, am);
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            pg[db] = pack4_i8(round_away(__fmul_rn(gacc[db][0], cq)), round_away(__fmul_rn(gacc[db][1], cq)),
+                              round_away(__fmul_rn(gacc[db][2], cq)), round_away(__fmul_rn(gacc[db][3], cq)));
+            pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
+        }
+        psg = __fmul_rn(am, R127);
+        plz = __fadd_rn(mx, __logf(z));
+        pl = l;
+    }
+    flush();
+    // padded leaves [max(l0, nb), l1): empty state, excluded everywhere
+    if (tval) {
+        for (int l = max(l0, nb); l < l1; ++l) {
+            const int64_t s = th * nb_pad + l;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = 0u;
+                *(u32x2*)(vb + s * D + 16 * db + 4 * grp) = u32x2{0u, 0u};
+            }
+            if (grp == 0) {
+                sg[s] = 0.0f;
+                lz[s] = -INFINITY;
+            }
         }
     }
 }
@@ -618,18 +571,31 @@ __device__ __forceinline__ void online_block(RowState& st, float (&sc)[8], VFetc
     st.m = m_new;
 }
 
+// PV operand from a natural-layout bf16 matrix X[row][128]: rows r0 + 4grp + i and
+// r1 + 4grp + i (i = 0..3) at column dim.
+__device__ __forceinline__ bf16x8 gather_pv(const uint16_t* __restrict__ X, int64_t r0, int64_t r1, int dim, int grp) {
+    uint32_t u[4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint16_t* b = X + ((j ? r1 : r0) + 4 * grp) * D + dim;
+        u[2 * j] = (uint32_t)b[0] | ((uint32_t)b[D] << 16);
+        u[2 * j + 1] = (uint32_t)b[2 * D] | ((uint32_t)b[3 * D] << 16);
+    }
+    return as_bf16x8(u32x4{u[0], u[1], u[2], u[3]});
+}
+
 template <int LEAF>
 __device__ __forceinline__ void tile_far_near(RowState& st, int64_t th, int nt, int nb, int nb_pad,
                                               int lo, int hi, int e_lo, int e_hi, int kx,
                                               const i32x4 (&q8r)[2], float sqr, const i32x4 (&dq8r)[2],
                                               float sdqr, const int8_t* __restrict__ g8,
                                               const float* __restrict__ sg, const float* __restrict__ lz,
-                                              const uint16_t* __restrict__ vbq,
+                                              const uint16_t* __restrict__ vb,
                                               const int8_t* __restrict__ excl_row,
                                               const int32_t* __restrict__ idx_row,
                                               const int8_t* __restrict__ k8,
                                               const float* __restrict__ ks,
-                                              const uint16_t* __restrict__ vq, int64_t kh, float scale) {
+                                              const uint16_t* __restrict__ v, int64_t kh, float scale) {
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     // ---- far field
     for (int c0 = lo; c0 < hi; c0 += 32) {
@@ -654,13 +620,8 @@ __device__ __forceinline__ void tile_far_near(RowState& st, int64_t th, int nt, 
                 sc[4 * h2 + i] = ok ? __fadd_rn(__fmul_rn((float)acc[i], __fmul_rn(sdqr, sgv[i])), lzv[i]) : -INFINITY;
             }
         }
-        const uint16_t* vb0 = vbq + ((th * nb_pad + c0) / 4) * D * 4;
-        online_block(st, sc, [&](int db) {
-            const int dim = 16 * db + col;
-            const u32x2 v0 = *(const u32x2*)(vb0 + ((int64_t)(grp)*D + dim) * 4);
-            const u32x2 v1 = *(const u32x2*)(vb0 + ((int64_t)(4 + grp) * D + dim) * 4);
-            return as_bf16x8(v0, v1);
-        });
+        const uint16_t* vb0 = vb + (th * nb_pad + c0) * D;
+        online_block(st, sc, [&](int db) { return gather_pv(vb0, 0, 16, 16 * db + col, grp); });
     }
     // ---- near field: token j of the tile's selected list -> idx[j / LEAF] * LEAF + j % LEAF
     for (int e0 = e_lo; e0 < e_hi; e0 += 32) {
@@ -685,12 +646,7 @@ __device__ __forceinline__ void tile_far_near(RowState& st, int64_t th, int nt, 
                 sc[4 * h2 + i] = oki ? __fmul_rn((float)acc[i], __fmul_rn(__fmul_rn(sqr, ksv[i]), scale)) : -INFINITY;
             }
         }
-        online_block(st, sc, [&](int db) {
-            const int dim = 16 * db + col;
-            const u32x2 v0 = *(const u32x2*)(vq + ((tok0[0] / 4 + grp) * D + dim) * 4);
-            const u32x2 v1 = *(const u32x2*)(vq + ((tok0[1] / 4 + grp) * D + dim) * 4);
-            return as_bf16x8(v0, v1);
-        });
+        online_block(st, sc, [&](int db) { return gather_pv(v, tok0[0], tok0[1], 16 * db + col, grp); });
     }
 }
 
@@ -724,9 +680,9 @@ template <int LEAF>
 __global__ __launch_bounds__(256) void tile_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ sq, const int8_t* __restrict__ dq8,
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
-    const float* __restrict__ lz, const uint16_t* __restrict__ vbq, const int8_t* __restrict__ excl,
+    const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ excl,
     const int32_t* __restrict__ idx, const int8_t* __restrict__ k8, const float* __restrict__ ks,
-    const uint16_t* __restrict__ vq, int64_t nq, int nt, int64_t nk, int nb, int nb_pad, int kx, int lps,
+    const uint16_t* __restrict__ v, int64_t nq, int nt, int64_t nk, int nb, int nb_pad, int kx, int lps,
     int eps, float scale, float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc,
     float* __restrict__ out, float* __restrict__ logz) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
@@ -746,7 +702,7 @@ __global__ __launch_bounds__(256) void tile_kernel(
     const int e_n = kx * LEAF;
     const int e_lo = sp * eps, e_hi = min(e_n, e_lo + eps);
     tile_far_near<LEAF>(st, th, nt, nb, nb_pad, lo, hi, e_lo, e_hi, kx, q8r, sqr, dq8r, sdqr, g8, sg, lz,
-                        vbq, excl + th * nb_pad, idx + th * (kx > 0 ? kx : 1), k8, ks, vq, (int64_t)h * nk, scale);
+                        vb, excl + th * nb_pad, idx + th * (kx > 0 ? kx : 1), k8, ks, v, (int64_t)h * nk, scale);
     const float ltot = grp_sum(st.l);
     if (pacc == nullptr) {   // single split: normalise in place
         const int64_t qi = (int64_t)t * TILE + r;
@@ -919,16 +875,16 @@ __device__ __forceinline__ void dma_qk(const int8_t* __restrict__ x8, int64_t ro
     }
 }
 
-// PV operand chunk j (0..7) of lane: 8-byte units [h][db][grp][col], 16-byte chunk = col pair p,
-// from quad (q0[h] + grp), dims 16db + 2p .. +1 of a key-quad bf16 matrix.
-__device__ __forceinline__ void dma_pv(const uint16_t* __restrict__ x4, int64_t q0a, int64_t q0b, char* slot,
-                                       int lane) {
-    const int p = lane & 7, grp = (lane >> 3) & 3, dbl = lane >> 5;
+// PV rows of a 32-key block: ring chunk s = 64j + lane holds the 16-byte chunk (s % 16) ^
+// swz(row) of row s / 16 (rows 0..15 from row0a, 16..31 from row0b) of a bf16 [*, 128] matrix.
+__device__ __forceinline__ void dma_rows(const uint16_t* __restrict__ X, int64_t row0a, int64_t row0b, char* slot,
+                                         int lane) {
+    const int pc = lane & 15;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int db = (2 * j + dbl) & 7;
-        const int64_t quad = ((j >> 2) ? q0b : q0a) + grp;
-        dma16(x4 + (quad * D + 16 * db + 2 * p) * 4, slot + 4096 + j * 1024);
+        const int row = 4 * j + (lane >> 4);
+        const int64_t r = (row < 16 ? row0a : row0b) + (row & 15);
+        dma16(X + r * D + 8 * (pc ^ swz(row)), slot + 4096 + j * 1024);
     }
 }
 
@@ -936,8 +892,8 @@ template <int LEAF>
 __global__ __launch_bounds__(256) void route_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ sq, const int8_t* __restrict__ dq8,
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
-    const float* __restrict__ lz, const uint16_t* __restrict__ vbq, const int8_t* __restrict__ k8,
-    const float* __restrict__ ks, const uint16_t* __restrict__ vq, int64_t nq, int nt, int64_t nk, int nb,
+    const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ k8,
+    const float* __restrict__ ks, const uint16_t* __restrict__ v, int64_t nq, int nt, int64_t nk, int nb,
     int nb_pad, int kx, int sink, int stride, float scale, float* __restrict__ out,
     float* __restrict__ logz, int32_t* __restrict__ idx_out) {
     __shared__ __align__(16) char ring[4][RING_SLOTS][SLOT_BYTES];   // also: SEL keys, merge staging
@@ -1068,12 +1024,11 @@ __global__ __launch_bounds__(256) void route_kernel(
             srow[rb] = __fmul_rn(sdq[p], LOG2E);
         }
         const int64_t srow0 = th * nb_pad;
-        const int64_t qbase = th * nb_pad / 4;
         auto issue = [&](int bi) {
             const int c0 = lo + 32 * bi;
             char* slot = myring + (bi % RING_SLOTS) * SLOT_BYTES;
             dma_qk(g8, srow0 + c0, srow0 + c0 + 16, slot, lane);
-            dma_pv(vbq, qbase + c0 / 4, qbase + c0 / 4 + 4, slot, lane);
+            dma_rows(vb, srow0 + c0, srow0 + c0 + 16, slot, lane);
             if (lane < 16) {
                 const float* src = (lane < 8 ? sg + srow0 + c0 + 4 * lane : lz + srow0 + c0 + 4 * (lane - 8));
                 dma16(src, slot + 12288);
@@ -1113,13 +1068,12 @@ __global__ __launch_bounds__(256) void route_kernel(
                         sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i]), bias);
                 }
             }
-            u32x2 v[8][2];
+            u32x2 pvop[8][2];
 #pragma unroll
             for (int db = 0; db < 8; ++db)
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf)
-                    v[db][hf] = *(const u32x2*)(slot + 4096 + ((((hf * 8 + db) * 4 + grp) * 16 + col) * 8));
-            rows4_update(st, umax, sc, v);
+                for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
+            rows4_update(st, umax, sc, pvop);
         }
     }
     {   // near field: tokens [e_lo, e_hi) of the selected list, same ring
@@ -1145,7 +1099,7 @@ __global__ __launch_bounds__(256) void route_kernel(
             const int64_t t0 = tok_of(e0), t1 = tok_of(e0 + 16);
             char* slot = myring + (bi % RING_SLOTS) * SLOT_BYTES;
             dma_qk(k8, t0, t1, slot, lane);
-            dma_pv(vq, t0 / 4, t1 / 4, slot, lane);
+            dma_rows(v, t0, t1, slot, lane);
             if (lane < 8) dma16(ks + (lane < 4 ? t0 + 4 * lane : t1 + 4 * (lane - 4)), slot + 12288);
         };
         // the ring slots of the far loop are all consumed: the near loop restarts at slot 0
@@ -1180,13 +1134,12 @@ __global__ __launch_bounds__(256) void route_kernel(
                         sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]), bias);
                 }
             }
-            u32x2 v[8][2];
+            u32x2 pvop[8][2];
 #pragma unroll
             for (int db = 0; db < 8; ++db)
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf)
-                    v[db][hf] = *(const u32x2*)(slot + 4096 + ((((hf * 8 + db) * 4 + grp) * 16 + col) * 8));
-            rows4_update(st, umax, sc, v);
+                for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
+            rows4_update(st, umax, sc, pvop);
         }
     }
         // rows whose scores outran the reference by 2^64, or underflowed: redo with the true max
@@ -1344,36 +1297,34 @@ int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, 
     return launched("htrc_pack_q");
 }
 
-int htrc_pack_kv(const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nk, int d, int8_t* k8,
-                 float* ks, uint16_t* kq, uint16_t* vq, void* stream) {
-    REQUIRE(k && v && k8 && ks && kq && vq, "htrc_pack_kv: null pointer");
-    REQUIRE(d == D, "htrc_pack_kv: head dim must be 128");
-    REQUIRE(heads > 0 && heads <= 65535 && nk > 0 && nk % 16 == 0, "htrc_pack_kv: keys must be a positive multiple of 16");
-    REQUIRE(aligned(k, 4) && aligned(v, 4) && aligned(kq, 8) && aligned(vq, 8), "htrc_pack_kv: misaligned buffer");
+int htrc_pack_k(const uint16_t* k, int64_t heads, int64_t nk, int d, int8_t* k8, float* ks, void* stream) {
+    REQUIRE(k && k8 && ks, "htrc_pack_k: null pointer");
+    REQUIRE(d == D, "htrc_pack_k: head dim must be 128");
+    REQUIRE(heads > 0 && heads <= 65535 && nk > 0 && nk % 16 == 0, "htrc_pack_k: keys must be a positive multiple of 16");
+    REQUIRE(aligned(k, 4) && aligned(k8, 4), "htrc_pack_k: misaligned buffer");
     dim3 grid((unsigned)((nk + 63) / 64), (unsigned)heads);
-    hipLaunchKernelGGL(pack_kv_kernel, grid, dim3(256), 0, (hipStream_t)stream, k, v, nk, k8, ks, kq, vq);
-    return launched("htrc_pack_kv");
+    hipLaunchKernelGGL(pack_k_kernel, grid, dim3(256), 0, (hipStream_t)stream, k, nk, k8, ks);
+    return launched("htrc_pack_k");
 }
 
-int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* kq, const uint16_t* vq, int64_t heads,
-                    int64_t nt, int64_t nk, int leaf, int d, float scale, int8_t* g8, float* sg,
-                    uint16_t* vbq, float* lz, void* stream) {
-    REQUIRE(mu && k && kq && vq && g8 && sg && vbq && lz, "htrc_leaf_stats: null pointer");
+int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
+                    int leaf, int d, float scale, int8_t* g8, float* sg, uint16_t* vb, float* lz, void* stream) {
+    REQUIRE(mu && k && v && g8 && sg && vb && lz, "htrc_leaf_stats: null pointer");
     REQUIRE(d == D, "htrc_leaf_stats: head dim must be 128");
     REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_leaf_stats: leaf must be 16/32/64/128");
     REQUIRE(nk > 0 && nk % leaf == 0, "htrc_leaf_stats: key count must be a multiple of the leaf size");
     REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff, "htrc_leaf_stats: bad heads / tiles");
-    REQUIRE(aligned(k, 16) && aligned(g8, 16) && aligned(sg, 16) && aligned(lz, 16),
+    REQUIRE(aligned(k, 16) && aligned(v, 16) && aligned(g8, 16) && aligned(vb, 16) && aligned(sg, 16) && aligned(lz, 16),
             "htrc_leaf_stats: misaligned buffer");
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
     const int lpb = 16;
     dim3 grid((unsigned)((nt + 63) / 64), (unsigned)((nbp + lpb - 1) / lpb), (unsigned)heads);
     hipStream_t s = (hipStream_t)stream;
-#define STATS_CASE(L)                                                                                      \
-    case L:                                                                                                \
-        hipLaunchKernelGGL(stats_kernel<L>, grid, dim3(256), 0, s, mu, (int)nt, k, kq, vq, nk, (int)nb, nbp, \
-                           lpb, scale, g8, sg, vbq, lz);                                                   \
+#define STATS_CASE(L)                                                                                         \
+    case L:                                                                                                   \
+        hipLaunchKernelGGL(stats_kernel<L>, grid, dim3(256), 0, s, mu, (int)nt, k, v, nk, (int)nb, nbp, lpb, scale, \
+                           g8, sg, vb, lz);                                                                   \
         break;
     switch (leaf) {
         STATS_CASE(16)
@@ -1415,11 +1366,11 @@ static int64_t split_len(int64_t n, int64_t ns, int64_t bn) {   // _split, h3/ht
 }
 
 int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
-              const float* sg, const float* lz, const uint16_t* vbq, const int8_t* excl, const int32_t* idx,
-              const int8_t* k8, const float* ks, const uint16_t* vq, int64_t heads, int64_t nq, int64_t nk,
+              const float* sg, const float* lz, const uint16_t* vb, const int8_t* excl, const int32_t* idx,
+              const int8_t* k8, const float* ks, const uint16_t* v, int64_t heads, int64_t nq, int64_t nk,
               int leaf, int d, int kx, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
               float* out, float* logz, void* stream) {
-    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vbq && excl && k8 && ks && vq,
+    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && excl && k8 && ks && v,
             "htrc_tile: null input pointer");
     REQUIRE(d == D, "htrc_tile: head dim must be 128");
     REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_tile: leaf must be 16/32/64/128");
@@ -1436,8 +1387,8 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
     float* ppa = splits == 1 ? nullptr : pacc;
 #define TILE_CASE(L)                                                                                            \
     case L:                                                                                                     \
-        hipLaunchKernelGGL(tile_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vbq, excl, idx, k8, \
-                           ks, vq, nq, (int)nt, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps, scale, ppm, ppl, ppa,   \
+        hipLaunchKernelGGL(tile_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, excl, idx, k8, \
+                           ks, v, nq, (int)nt, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps, scale, ppm, ppl, ppa,   \
                            out, logz);                                                                          \
         break;
     switch (leaf) {
@@ -1461,11 +1412,13 @@ int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t head
 }
 
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
-               const float* sg, const float* lz, const uint16_t* vbq, const int8_t* k8, const float* ks,
-               const uint16_t* vq, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
+               const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
+               const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
                int stride, float scale, float* out, float* logz, int32_t* idx, void* stream) {
-    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vbq && k8 && ks && vq && out && logz,
+    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && k8 && ks && v && out && logz,
             "htrc_route: null pointer");
+    REQUIRE(aligned(vb, 16) && aligned(v, 16) && aligned(g8, 16) && aligned(k8, 16) && aligned(sg, 16) && aligned(ks, 16),
+            "htrc_route: misaligned buffer");
     REQUIRE(d == D, "htrc_route: head dim must be 128");
     REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_route: leaf must be 16/32/64/128");
     REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_route: bad sizes");
@@ -1477,7 +1430,7 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
     hipStream_t s = (hipStream_t)stream;
 #define ROUTE_CASE(L)                                                                                       \
     case L:                                                                                                 \
-        hipLaunchKernelGGL(route_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vbq, k8, ks, vq, \
+        hipLaunchKernelGGL(route_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, \
                            nq, (int)nt, nk, (int)nb, htrc_nb_pad(nb), kx, sink, stride, scale, out, logz, idx); \
         break;
     switch (leaf) {

@@ -110,12 +110,12 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), ws=ws)
     kb = kh.to(torch.bfloat16).contiguous()
     vb = vh.to(torch.bfloat16).contiguous()
-    k8, ks, kq, vq = hip.pack_kv(kb, vb, ws=ws)
+    k8, ks = hip.pack_k(kb, ws=ws)
     tick("prep")
-    g8, lz, vbq, sg, _ = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, ws=ws, kq=kq, vq=vq)
+    g8, lz, vbs, sg, _ = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, ws=ws)
     tick("stats")
-    packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "vq": vq, "mu": mu}
-    lstate = {"g8": g8, "sg": sg, "lz": lz, "vbq": vbq}
+    packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "v": vb, "mu": mu}
+    lstate = {"g8": g8, "sg": sg, "lz": lz, "vb": vbs}
     nt = int(mu.shape[1])
     idx = None
     if kern.get("fused", True):

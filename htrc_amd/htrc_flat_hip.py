@@ -6,9 +6,9 @@ dict ``ws`` is given (buffers are reused, as ``_buf`` does in the reference), no
 synchronises, so a whole operator call can be captured in a HIP graph.
 
 Tensors carry a leading head dimension H (2-D inputs are treated as H = 1).  Layouts are
-those of the C ABI: the leaf-value state ``vb`` is stored leaf-quad interleaved
-(``[H, nt, nbp/4, 128, 4]``, see ``vb_natural``) because that is the operand layout of the
-far-field PV MFMA; ``g`` is int8 ``[H, nt, nbp, 128]`` with row scales ``sg``.
+those of the C ABI: the per-(tile, leaf) state is ``g`` int8 ``[H, nt, nbp, 128]`` with row
+scales ``sg``, ``lz`` fp32 and ``vb`` bf16 ``[H, nt, nbp, 128]`` (nbp = leaves rounded up to
+32; padded leaves have lz = -inf).
 
 Launch-shape knobs of the reference (bt, bl, warps, stages, prec, sel_bn, rb) are
 accepted for call compatibility and ignored: the HIP kernels have fixed MI355X launch
@@ -80,30 +80,22 @@ def pack_q(q: torch.Tensor, tile: int = TILE, ws=None):
     return mu, q8, sq, dq8, sdq
 
 
-def pack_kv(k: torch.Tensor, v: torch.Tensor, ws=None):
-    """K int8 (round half to even) and key-quad bf16 K / V -> (k8, ks, kq, vq)."""
-    k, v = _heads(k), _heads(v)
-    k = k.to(torch.bfloat16).contiguous()
-    v = v.to(torch.bfloat16).contiguous()
+def pack_k(k: torch.Tensor, ws=None):
+    """K int8 per row (round half to even) -> (k8 [H,nk,D] int8, ks [H,nk] fp32)."""
+    k = _heads(k).to(torch.bfloat16).contiguous()
     _need(k, torch.bfloat16, "k")
-    _need(v, torch.bfloat16, "v")
-    if k.shape != v.shape:
-        raise ValueError("k and v must have the same shape")
     h, nk, d = (int(x) for x in k.shape)
     dev = k.device
     k8 = _buf(ws, "k8", (h, nk, d), torch.int8, dev)
     ks = _buf(ws, "ks", (h, nk), torch.float32, dev)
-    kq = _buf(ws, "kq", (h, nk // 4, d, 4), torch.bfloat16, dev)
-    vq = _buf(ws, "vq", (h, nk // 4, d, 4), torch.bfloat16, dev)
-    call("htrc_pack_kv", ptr(k), ptr(v), h, nk, d, ptr(k8), ptr(ks), ptr(kq), ptr(vq), stream_handle(dev))
-    return k8, ks, kq, vq
+    call("htrc_pack_k", ptr(k), h, nk, d, ptr(k8), ptr(ks), stream_handle(dev))
+    return k8, ks
 
 
-def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4, store=torch.int8, ws=None,
-               kq=None, vq=None):
+def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4, store=torch.int8, ws=None):
     """Leaf statistics at the tile centres (h3/htrc_flat_triton.py:329-345, I8 store).
-    mu [H,nt,D] fp32, kf/vf bf16 [H,nk,D] -> (g8, lz, vbq, sg, None) in the reference's
-    (g, lz, vb, sg, sv) order.  kq/vq: key-quad K/V from pack_kv (computed if absent)."""
+    mu [H,nt,D] fp32, kf/vf bf16 [H,nk,D] -> (g8 [H,nt,nbp,D] int8, lz [H,nt,nbp], vb [H,nt,nbp,D]
+    bf16, sg [H,nt,nbp], None) in the reference's (g, lz, vb, sg, sv) order."""
     if store != torch.int8:
         raise ValueError("the HIP leaf statistics store g as int8 (store='int8')")
     mu = _heads(mu).contiguous()
@@ -114,19 +106,17 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
     _need(vf, torch.bfloat16, "v")
     h, nt, d = (int(x) for x in mu.shape)
     nk = int(kf.shape[1])
-    if int(nb) * int(leaf) != nk:
-        raise ValueError("key count must equal nb * leaf")
-    if kq is None or vq is None:
-        _, _, kq, vq = pack_kv(kf, vf)
+    if int(nb) * int(leaf) != nk or tuple(vf.shape) != tuple(kf.shape):
+        raise ValueError("keys and values must be [H, nb * leaf, D]")
     nbp = nb_pad(nb)
     dev = mu.device
     g8 = _buf(ws, "g", (h, nt, nbp, d), torch.int8, dev)
     sg = _buf(ws, "sg", (h, nt, nbp), torch.float32, dev)
     lz = _buf(ws, "lz", (h, nt, nbp), torch.float32, dev)
-    vbq = _buf(ws, "vb", (h, nt, nbp // 4, d, 4), torch.bfloat16, dev)
-    call("htrc_leaf_stats", ptr(mu), ptr(kf), ptr(kq), ptr(vq), h, nt, nk, int(leaf), d, float(scale), ptr(g8),
-         ptr(sg), ptr(vbq), ptr(lz), stream_handle(dev))
-    return g8, lz, vbq, sg, None
+    vb = _buf(ws, "vb", (h, nt, nbp, d), torch.bfloat16, dev)
+    call("htrc_leaf_stats", ptr(mu), ptr(kf), ptr(vf), h, nt, nk, int(leaf), d, float(scale), ptr(g8), ptr(sg),
+         ptr(vb), ptr(lz), stream_handle(dev))
+    return g8, lz, vb, sg, None
 
 
 def rowmax_select(q_c=None, mu_c=None, g=None, lz=None, prec="ieee", bn=32, warps=4, splits=8, stride=1, dot=1,
@@ -161,8 +151,8 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
     """Far + near online softmax per (tile, split) and the merge
     (h3/htrc_flat_triton.py:348-391) -> (out [H,nq,D] fp32, logz [H,nq] fp32)."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
-    k8, ks, vq = packed["k8"], packed["ks"], packed["vq"]
-    g8, sg, lz, vbq = state["g8"], state["sg"], state["lz"], state["vbq"]
+    k8, ks, v = packed["k8"], packed["ks"], packed["v"]
+    g8, sg, lz, vb = state["g8"], state["sg"], state["lz"], state["vb"]
     h, nk, d = (int(x) for x in k8.shape)
     nt = -(-nq // TILE)
     kx = int(idx.shape[-1]) if idx is not None else 0
@@ -177,8 +167,8 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
         pm = _buf(ws, "pm", (h, nt, ns, TILE), torch.float32, dev)
         pl = _buf(ws, "pl", (h, nt, ns, TILE), torch.float32, dev)
         pacc = _buf(ws, "pacc", (h, nt, ns, TILE, d), torch.float32, dev)
-    call("htrc_tile", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vbq), ptr(excl),
-         ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(vq), h, nq, nk, int(leaf), d, kx, ns, int(bn),
+    call("htrc_tile", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(excl),
+         ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(v), h, nq, nk, int(leaf), d, kx, ns, int(bn),
          float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
     if ns > 1:
         call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, ns, d, ptr(out), ptr(logz), stream_handle(dev))
@@ -190,25 +180,18 @@ def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: floa
     """Fused select -> top-k -> far + near -> normalised output (one launch per layer call).
     -> (out [H,nq,D], logz [H,nq]); idx [H,nt,kx] int32 receives the routing when given."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
-    k8, ks, vq = packed["k8"], packed["ks"], packed["vq"]
-    g8, sg, lz, vbq = state["g8"], state["sg"], state["lz"], state["vbq"]
+    k8, ks, v = packed["k8"], packed["ks"], packed["v"]
+    g8, sg, lz, vb = state["g8"], state["sg"], state["lz"], state["vb"]
     h, nk, d = (int(x) for x in k8.shape)
     dev = q8.device
     if out is None:
         out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
     if logz is None:
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
-    call("htrc_route", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vbq), ptr(k8), ptr(ks),
-         ptr(vq), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), float(scale), ptr(out), ptr(logz),
+    call("htrc_route", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8), ptr(ks),
+         ptr(v), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), float(scale), ptr(out), ptr(logz),
          ptr(idx), stream_handle(dev))
     return out, logz
-
-
-def vb_natural(vbq: torch.Tensor, nb: int | None = None) -> torch.Tensor:
-    """Leaf-quad vb [H,nt,nbp/4,D,4] -> natural [H,nt,nb,D] (a view permutation, for checks)."""
-    h, nt, nq4, d, four = (int(x) for x in vbq.shape)
-    nat = vbq.permute(0, 1, 2, 4, 3).reshape(h, nt, nq4 * 4, d)
-    return nat if nb is None else nat[:, :, :nb]
 
 
 def selftest_mfma(ai, bi, af, bf):

@@ -48,7 +48,6 @@ def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, hea
         4 * nt * dim                       # mu
         + 2 * rows * dim + 8 * rows        # q8, dq8, sq, sdq
         + keys * dim + 4 * keys            # k8, ks
-        + 4 * keys * dim                   # key-quad K and V (bf16)
         + 2 * keys * dim * 2               # bf16 copies of k and v when the inputs are not bf16
         + nt * nbp * (3 * dim + 8)         # g8, vb, sg, lz
         + 4 * queries * (dim + 1)          # out, logz

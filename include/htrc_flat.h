@@ -11,10 +11,9 @@
  *   mu       fp32 [H, nt, 128]                  nt = ceil(nq / 64)  (tiles of 64 query rows)
  *   q8, dq8  int8 [H, nt*64, 128]               sq, sdq fp32 [H, nt*64]   (padded rows)
  *   k8       int8 [H, nk, 128], ks fp32 [H, nk]
- *   kq, vq   bf16 [H, nk/4, 128, 4]             key-quad layout of K and V
  *   g8       int8 [H, nt, nbp, 128]             nb = nk / leaf, nbp = htrc_nb_pad(nb)
  *   sg, lz   fp32 [H, nt, nbp]                  padded leaves: sg = 0, lz = -inf
- *   vbq      bf16 [H, nt, nbp/4, 128, 4]        leaf-quad layout of the leaf value means
+ *   vb       bf16 [H, nt, nbp, 128]             leaf value means
  *   sel      fp32 [H, nt, nbp]                  excl int8 [H, nt, nbp]; idx int32 [H, nt, kx]
  *   pm, pl   fp32 [H, nt, splits, 64]           pacc fp32 [H, nt, splits, 64, 128]
  *   out      fp32 [H, nq, 128]                  logz fp32 [H, nq]
@@ -31,7 +30,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 1
+#define HTRC_ABI_VERSION 2
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -49,16 +48,14 @@ int htrc_nb_pad(int64_t nb);
 int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, float* mu, int8_t* q8,
                 float* sq, int8_t* dq8, float* sdq, void* stream);
 
-/* K int8 pack (round half to even, per-row scale) plus key-quad copies of K and V.
+/* K int8 pack (round half to even, per-row scale).
  * Replaces the host-side K pack of _flat_triton (h3/htrc_flat.py:213-219). */
-int htrc_pack_kv(const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nk, int d, int8_t* k8,
-                 float* ks, uint16_t* kq, uint16_t* vq, void* stream);
+int htrc_pack_k(const uint16_t* k, int64_t heads, int64_t nk, int d, int8_t* k8, float* ks, void* stream);
 
 /* Leaf statistics at the tile centres with the int8 store of g.
  * Replaces leaf_stats / _stats_kernel (h3/htrc_flat_triton.py:329-345, 41-85). */
-int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* kq, const uint16_t* vq,
-                    int64_t heads, int64_t nt, int64_t nk, int leaf, int d, float scale, int8_t* g8,
-                    float* sg, uint16_t* vbq, float* lz, void* stream);
+int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
+                    int leaf, int d, float scale, int8_t* g8, float* sg, uint16_t* vb, float* lz, void* stream);
 
 /* Row-max routing score SEL[t, l] over every `stride`-th tile row.
  * Replaces rowmax_select / _rowmax_kernel (h3/htrc_flat_triton.py:315-326, 214-254). */
@@ -74,8 +71,8 @@ int htrc_topk(const float* sel, int64_t rows, int64_t nb, int kx, int sink, int3
  * splits > 1 writes the partials pm/pl/pacc for htrc_merge.
  * Replaces tile_attention / _tile_kernel (h3/htrc_flat_triton.py:348-391, 88-211). */
 int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
-              const float* sg, const float* lz, const uint16_t* vbq, const int8_t* excl, const int32_t* idx,
-              const int8_t* k8, const float* ks, const uint16_t* vq, int64_t heads, int64_t nq, int64_t nk,
+              const float* sg, const float* lz, const uint16_t* vb, const int8_t* excl, const int32_t* idx,
+              const int8_t* k8, const float* ks, const uint16_t* v, int64_t heads, int64_t nq, int64_t nk,
               int leaf, int d, int kx, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
               float* out, float* logz, void* stream);
 
@@ -88,8 +85,8 @@ int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t head
  * SEL and the exclusion mask kept in LDS; idx (optional, may be NULL) receives the routing.
  * Replaces the chunk loop body of _flat_triton after leaf_stats (h3/htrc_flat.py:250-271). */
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
-               const float* sg, const float* lz, const uint16_t* vbq, const int8_t* k8, const float* ks,
-               const uint16_t* vq, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
+               const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
+               const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
                int stride, float scale, float* out, float* logz, int32_t* idx, void* stream);
 
 /* Self-test of the MFMA operand conventions the kernels rely on (no reference counterpart):

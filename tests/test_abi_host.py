@@ -53,10 +53,10 @@ def test_launchers_reject_bad_arguments_on_host(case):
         rc = lib.htrc_pack_q(None, 1, 1, 64, 128, f, f, f, f, f, None)
         msg = "null"
     elif case == "dim":
-        rc = lib.htrc_pack_kv(f, f, 1, 64, 64, f, f, f, f, None)
+        rc = lib.htrc_pack_k(f, 1, 64, 64, f, f, None)
         msg = "128"
     elif case == "leaf":
-        rc = lib.htrc_leaf_stats(f, f, f, f, 1, 1, 96, 48, 128, 0.1, f, f, f, f, None)
+        rc = lib.htrc_leaf_stats(f, f, f, 1, 1, 96, 48, 128, 0.1, f, f, f, f, None)
         msg = "leaf"
     elif case == "block":
         rc = lib.htrc_tile(*([f] * 13), 1, 64, 128, 64, 128, 1, 4, 48, 0.1, f, f, f, f, f, None)

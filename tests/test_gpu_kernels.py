@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bits, from_bits, key_quads, rel_l2, vb_to_quads
+from helpers import bits, from_bits, rel_l2
 from htrc_amd import htrc_flat_hip as hip
 from htrc_amd import workloads
 from htrc_amd._lib import nb_pad
@@ -59,7 +59,7 @@ def test_pack_bitexact(device, nq, qdtype):
         q = q.float() + 1e-3 * torch.randn(q.shape, generator=torch.Generator().manual_seed(7))
     qd = q.to(device).contiguous()
     mu, q8, sq, dq8, sdq = hip.pack_q(qd)
-    k8, ks, kq, vq = hip.pack_kv(k.to(device), v.to(device))
+    k8, ks = hip.pack_k(k.to(device))
     torch.cuda.synchronize()
     qf = q[0].float().numpy()
     omu = flat_i8.tile_centres(qf, 64)
@@ -72,8 +72,6 @@ def test_pack_bitexact(device, nq, qdtype):
     assert np.array_equal(_np(sdq[0]).view(np.uint32), osdq.view(np.uint32))
     assert np.array_equal(_np(k8[0]), ok8)
     assert np.array_equal(_np(ks[0]).view(np.uint32), oks.view(np.uint32))
-    assert np.array_equal(bits(kq[0]).reshape(-1), key_quads(bits(k[0])).reshape(-1))
-    assert np.array_equal(bits(vq[0]).reshape(-1), key_quads(bits(v[0])).reshape(-1))
 
 
 def test_pack_edge_rows(device):
@@ -90,7 +88,7 @@ def test_pack_edge_rows(device):
     qd = torch.from_numpy(bf16.to_f32(kb)).to(device)
     kd = from_bits(kb, device)
     mu, q8, sq, dq8, sdq = hip.pack_q(qd)
-    k8, ks, kq, vq = hip.pack_kv(kd, kd)
+    k8, ks = hip.pack_k(kd)
     torch.cuda.synchronize()
     qf = bf16.to_f32(kb)
     omu = flat_i8.tile_centres(qf, 64)
@@ -114,7 +112,7 @@ def test_stats_close_to_oracle(device, leaf):
     ref = _oracle_state(q, k, v, leaf, 4)
     nb = n // leaf
     mu = torch.from_numpy(ref["mu"])[None].to(device)
-    g8, lz, vbq, sg, _ = hip.leaf_stats(mu, k.to(device), v.to(device), nb, 1 / math.sqrt(128), leaf=leaf)
+    g8, lz, vbs, sg, _ = hip.leaf_stats(mu, k.to(device), v.to(device), nb, 1 / math.sqrt(128), leaf=leaf)
     torch.cuda.synchronize()
     nbp = nb_pad(nb)
     g = _np(g8[0])[:, :nb].astype(np.int32)
@@ -124,7 +122,7 @@ def test_stats_close_to_oracle(device, leaf):
     assert (diff > 0).mean() < 2e-3, f"g8 mismatch fraction {(diff > 0).mean():.2e}"
     np.testing.assert_allclose(_np(lz[0])[:, :nb], ref["lz"], rtol=0, atol=2e-5 * (1 + np.abs(ref["lz"]).max()))
     np.testing.assert_allclose(_np(sg[0])[:, :nb], ref["sg"], rtol=1e-5, atol=0)
-    vb = bf16.to_f32(bits(hip.vb_natural(vbq, nb)[0].contiguous()))
+    vb = bf16.to_f32(bits(vbs[0, :, :nb].contiguous()))
     ovb = bf16.to_f32(ref["vb"])
     assert np.abs(vb - ovb).max() <= 2 ** -7 * np.abs(ovb).max()
     assert (vb != ovb).mean() < 2e-2
@@ -185,11 +183,12 @@ def _device_state(ref, q, k, v, device):
     lz[0, :, :nb] = ref["lz"]
     excl = np.zeros((1, nt, nbp), np.int8)
     excl[0, :, :nb] = ref["excl"]
-    vbq = vb_to_quads(ref["vb"], nbp)[None]
+    vbp = np.zeros((1, nt, nbp, d), np.uint16)
+    vbp[0, :, :nb] = ref["vb"]
     packed = {"q8": T(ref["q8"][None]), "sq": T(ref["sq"][None]), "dq8": T(ref["dq8"][None]),
               "sdq": T(ref["sdq"][None]), "k8": T(ref["k8"][None]), "ks": T(ref["ks"][None]),
-              "vq": from_bits(key_quads(bits(v[0]))[None], device)}
-    state = {"g8": T(g8), "sg": T(sg), "lz": T(lz), "vbq": from_bits(vbq, device)}
+              "v": v.to(device)}
+    state = {"g8": T(g8), "sg": T(sg), "lz": T(lz), "vb": from_bits(vbp, device)}
     return packed, state, T(excl), T(ref["idx"][None])
 
 
