@@ -110,6 +110,8 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also launch one copy-shaped 1 GiB kernel (the scale of the FETCH_SIZE/WRITE_SIZE counters)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {a.gpus}); heads shard across GPUs "
@@ -170,6 +172,14 @@ def main():
             e1.synchronize()
             times.append(e0.elapsed_time(e1))
         kms[name] = statistics.mean(times)
+    if a.calib_copy:
+        # copy-shaped elementwise kernel: reads 1 GiB once, writes 1 GiB once
+        src = torch.empty(1 << 28, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.bitwise_not(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     figs = algorithmic(h, nq, nk, leaf, kx, d)
     kernels = {n: roofline_entry(n, kms[n], figs[n]) for n in stages}
     dom = max(kernels.values(), key=lambda e: e["ms"])

@@ -20,6 +20,17 @@ __device__ constexpr float R127 = 1.0f / 127.0f;
 __device__ constexpr float LOG2E = 1.4426950408889634f;
 __device__ constexpr float LN2 = 0.6931471805599453f;
 
+constexpr uint32_t NXCD = 8;   // MI355X: 8 accelerator dies, each with its own L2
+
+// Workgroups of a 1-D grid of n are dispatched round-robin over the XCDs (workgroup i runs on
+// XCD i % 8).  This maps i to the logical block x * q + min(x, r) + i / 8 (q = n / 8,
+// r = n % 8): a bijection of [0, n) under which every XCD walks one contiguous range of
+// logical blocks, so neighbouring blocks (the same head, adjacent tiles) share one L2.
+__device__ __forceinline__ uint32_t xcd_block(uint32_t i, uint32_t n) {
+    const uint32_t x = i % NXCD, q = n / NXCD, r = n % NXCD;
+    return x * q + (x < r ? x : r) + i / NXCD;
+}
+
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 
 // fp32 -> bf16 bits, round to nearest even (quiet NaN kept).

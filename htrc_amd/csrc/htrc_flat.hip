@@ -121,15 +121,31 @@ __global__ __launch_bounds__(256) void pack_k_kernel(const uint16_t* __restrict_
 // ---------------------------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
 
-// One direct global->LDS load: 16 bytes per lane to lds_base + lane * 16 (lds_base uniform).
+// One direct global->LDS load: 16 bytes per lane to lds_base + lane * 16 (lds_base uniform,
+// M0 = its LDS byte address).  Issued as inline asm on purpose: the compiler's wait-count pass
+// treats every LDS DMA in flight as aliasing every later LDS read and puts a vmcnt(0) before
+// it, which would serialise each ring slot with the loads issued for the slots after it.  The
+// kernels order their LDS reads after the DMA themselves, with wait_vmcnt<N>.
 __device__ __forceinline__ void dma16(const void* src, void* lds_base) {
-    __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_base, 16, 0, 0);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_base);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0) : "memory", "m0");
 }
 
+// s_waitcnt vmcnt(N): at most N vector-memory operations of this wave still in flight (they
+// complete in issue order).  The memory clobber keeps the compiler from moving LDS reads of a
+// DMA'd slot above the wait.
 template <int N>
-__device__ __forceinline__ void wait_vmcnt() {          // s_waitcnt vmcnt(N), other counters untouched
+__device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// Operands loaded from global memory before a DMA loop: consuming them here makes the compiler
+// wait for those loads before the loop's first DMA is issued (its own wait inside the loop would
+// otherwise also drain the DMAs, which it cannot see).
+__device__ __forceinline__ void settle(const i32x4 (&b)[4][2], const float (&s)[4]) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) asm volatile("" : : "v"(b[rb][0]), "v"(b[rb][1]), "v"(s[rb]));
 }
 
 // Stage leaf rows [key0, key0 + LEAF) of K and V: LDS chunk s = j*256 + tid holds the
@@ -169,8 +185,13 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
     constexpr int LEAF_BYTES = 32 * LEAF * 16;
     __shared__ __align__(16) char lds[2 * LEAF_BYTES];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    const int h = blockIdx.z;
-    const int t = blockIdx.x * 64 + w * 16 + col;   // tile centre of this lane's C column
+    // 1-D grid over (tile group, leaf group, head), tile group fastest: the tile groups that
+    // read the same leaves run together on one XCD and share its L2.
+    const int ntg = (nt + 63) / 64, nlg = (nb_pad + lpb - 1) / lpb;
+    const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
+    const int tg = (int)(blk % (uint32_t)ntg), lg = (int)((blk / (uint32_t)ntg) % (uint32_t)nlg);
+    const int h = (int)(blk / ((uint32_t)ntg * (uint32_t)nlg));
+    const int t = tg * 64 + w * 16 + col;           // tile centre of this lane's C column
     const bool tval = t < nt;
     const int64_t th = (int64_t)h * nt + (tval ? t : 0);
 
@@ -183,7 +204,7 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
         split3x8(x, mh[ks], mm[ks], ml[ks]);
     }
 
-    const int l0 = blockIdx.y * lpb;
+    const int l0 = lg * lpb;
     const int l1 = min(nb_pad, l0 + lpb);
     const int lr = min(nb, l1);                   // real leaves of this workgroup: [l0, lr)
     const int64_t kh = (int64_t)h * nk;
@@ -862,6 +883,9 @@ constexpr int RING_SLOTS = 3;
 constexpr int SLOT_BYTES = 4096 + 8192 + 256;
 constexpr int BLOCK_DMA = 13;                       // direct-to-LDS loads per wave per block
 constexpr int MAX_KX_LDS = 1024;                    // near leaves per tile the route kernel holds
+// Merge: the four waves' scaled partial O, 64 rows x 128 dims each, rows padded to 132 floats.
+constexpr int MRG_STRIDE = 132;
+static_assert(4 * 64 * MRG_STRIDE * 4 <= 4 * RING_SLOTS * SLOT_BYTES, "merge staging");
 
 // QK operand chunk j (0..3) of lane: [hh = j>>1][ks = j&1][grp][col] <- row (row0[hh] + col),
 // bytes (4ks + grp)*16 of an int8 [*, 128] matrix.
@@ -888,115 +912,129 @@ __device__ __forceinline__ void dma_rows(const uint16_t* __restrict__ X, int64_t
     }
 }
 
+// route_select: first launch of the fused production path, one workgroup (4 waves) per tile.
+//   SEL of every leaf (bit-exact, the select_kernel arithmetic) into LDS, its kx largest
+//   (idx ascending, leaves < sink forced in), and per row the largest far-field score, the
+//   fixed softmax reference of route_kernel (the tile maximum when rows are sampled).
+// Small register and LDS footprint: several tiles share a CU, so their load latency and their
+// top-k overlap.  SEL never reaches HBM.
+__global__ __launch_bounds__(256, 4) void route_select_kernel(
+    const int8_t* __restrict__ dq8, const float* __restrict__ sdq, const int8_t* __restrict__ g8,
+    const float* __restrict__ sg, const float* __restrict__ lz, int nt, int nb, int nb_pad, int kx, int sink,
+    int stride, int32_t* __restrict__ idx, float* __restrict__ rowmax) {
+    extern __shared__ uint32_t keys[];        // [nb]
+    __shared__ TopkSmem sm;
+    __shared__ float red_m[4][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
+    const int t = (int)(blk % (uint32_t)nt), h = (int)(blk / (uint32_t)nt);
+    const int64_t th = (int64_t)h * nt + t;
+    const int ts = TILE / stride;
+    i32x4 b[4][2];
+    bool val[4];
+    load_rows_i8(dq8, th * TILE, stride, ts, col, grp, b, val);
+    float srow[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) srow[rb] = sdq[th * TILE + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
+    struct SelOps {
+        i32x4 a[2];
+        f32x4 sg, lz;
+    };
+    float rmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // row max of the far scores
+    auto sel_load = [&](SelOps& o, int c) {
+        const int64_t s0 = th * nb_pad + c;
+#pragma unroll
+        for (int kss = 0; kss < 2; ++kss) o.a[kss] = *(const i32x4*)(g8 + (s0 + col) * D + 64 * kss + 16 * grp);
+        o.sg = *(const f32x4*)(sg + s0 + 4 * grp);
+        o.lz = *(const f32x4*)(lz + s0 + 4 * grp);
+    };
+    auto sel_block = [&](const SelOps& o, int c) {
+        i32x4 acc[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            acc[rb] = mfma_i8(o.a[0], b[rb][0], i32x4{0, 0, 0, 0});
+            acc[rb] = mfma_i8(o.a[1], b[rb][1], acc[rb]);
+        }
+        float best[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool lv = c + 4 * grp + i < nb;
+            best[i] = -INFINITY;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const float x = __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], o.sg[i]));
+                best[i] = fmaxf(best[i], val[rb] ? x : -INFINITY);
+                rmax[rb] = fmaxf(rmax[rb], lv ? __fadd_rn(x, o.lz[i]) : -INFINITY);
+            }
+            best[i] = col_max(best[i]);
+        }
+        if (col == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int l = c + 4 * grp + i;
+                if (l < nb) keys[l] = l < sink ? 0xffffffffu : order_key(__fadd_rn(best[i], o.lz[i]));
+            }
+        }
+    };
+    // wave w: 16-leaf groups c = 16 w + 64 j, each loaded one group ahead
+    SelOps sa, sb;
+    if (16 * w < nb) sel_load(sa, 16 * w);
+    for (int c = 16 * w; c < nb; c += 128) {
+        const int c1 = c + 64;
+        if (c1 < nb) sel_load(sb, c1);
+        sel_block(sa, c);
+        if (c1 >= nb) break;
+        if (c1 + 64 < nb) sel_load(sa, c1 + 64);
+        sel_block(sb, c1);
+    }
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {          // row r = stride * (16 rb + col) of the sampled rows
+        const float mx = grp_max(rmax[rb]);
+        if (grp == 0) red_m[w][16 * rb + col] = mx;
+    }
+    __syncthreads();
+    if (w == 0) {
+        const int r = lane;
+        float m = r < ts ? fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r])) : -INFINITY;
+        if (stride != 1) m = wave_max(m);     // sampled rows: one reference for the whole tile
+        rowmax[th * TILE + r] = m;
+    }
+    const int kxe = min(kx, nb);
+    if (kxe > 0) topk_row(keys, nb, kxe, sm, idx + th * kxe, nullptr, nullptr);
+}
+
 template <int LEAF>
 __global__ __launch_bounds__(256) void route_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ sq, const int8_t* __restrict__ dq8,
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ k8,
-    const float* __restrict__ ks, const uint16_t* __restrict__ v, int64_t nq, int nt, int64_t nk, int nb,
-    int nb_pad, int kx, int sink, int stride, float scale, float* __restrict__ out,
-    float* __restrict__ logz, int32_t* __restrict__ idx_out) {
-    __shared__ __align__(16) char ring[4][RING_SLOTS][SLOT_BYTES];   // also: SEL keys, merge staging
+    const float* __restrict__ ks, const uint16_t* __restrict__ v, const int32_t* __restrict__ idx,
+    const float* __restrict__ rowmax, int64_t nq, int nt, int64_t nk, int nb, int nb_pad, int kxe, float scale,
+    float* __restrict__ out, float* __restrict__ logz) {
+    __shared__ __align__(16) char ring[4][RING_SLOTS][SLOT_BYTES];   // also: merge staging
     __shared__ int32_t sidx[MAX_KX_LDS];
     __shared__ uint32_t exbits[MAX_NB_LDS / 32 + 1];
-    __shared__ TopkSmem sm;
     __shared__ float red_m[4][64], red_l[4][64];
-    uint32_t* keys = (uint32_t*)&ring[0][0][0];               // [nb] during select / top-k
-    float* mrg = (float*)&ring[0][0][0];                       // merge staging: 4 x 64 x 33 floats
+    float* mrg = (float*)&ring[0][0][0];                       // merge staging: 4 x 64 x MRG_STRIDE floats
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    const int t = blockIdx.x, h = blockIdx.z;
+    // 1-D grid over (tile, head), tile fastest: each XCD runs a contiguous run of tiles of one
+    // head at a time, so the near-field leaves adjacent tiles share are fetched into one L2.
+    const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
+    const int t = (int)(blk % (uint32_t)nt), h = (int)(blk / (uint32_t)nt);
     const int64_t th = (int64_t)h * nt + t;
-    // ---- 1. select (bit-exact, same arithmetic as select_kernel)
-    {
-        const int ts = TILE / stride;
-        i32x4 b[4][2];
-        bool val[4];
-        load_rows_i8(dq8, th * TILE, stride, ts, col, grp, b, val);
-        float srow[4];
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-            srow[rb] = sdq[th * TILE + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
-        struct SelOps {
-            i32x4 a[2];
-            f32x4 sg, lz;
-        };
-        float rmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // row max of the far scores
-        auto sel_load = [&](SelOps& o, int c) {
-            const int64_t s0 = th * nb_pad + c;
-#pragma unroll
-            for (int kss = 0; kss < 2; ++kss) o.a[kss] = *(const i32x4*)(g8 + (s0 + col) * D + 64 * kss + 16 * grp);
-            o.sg = *(const f32x4*)(sg + s0 + 4 * grp);
-            o.lz = *(const f32x4*)(lz + s0 + 4 * grp);
-        };
-        auto sel_block = [&](const SelOps& o, int c) {
-            i32x4 acc[4];
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
-                acc[rb] = mfma_i8(o.a[0], b[rb][0], i32x4{0, 0, 0, 0});
-                acc[rb] = mfma_i8(o.a[1], b[rb][1], acc[rb]);
-            }
-            float best[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const bool lv = c + 4 * grp + i < nb;
-                best[i] = -INFINITY;
-#pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    const float x = __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], o.sg[i]));
-                    best[i] = fmaxf(best[i], val[rb] ? x : -INFINITY);
-                    rmax[rb] = fmaxf(rmax[rb], lv ? __fadd_rn(x, o.lz[i]) : -INFINITY);
-                }
-                best[i] = col_max(best[i]);
-            }
-            if (col == 0) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int l = c + 4 * grp + i;
-                    if (l < nb) keys[l] = l < sink ? 0xffffffffu : order_key(__fadd_rn(best[i], o.lz[i]));
-                }
-            }
-        };
-        SelOps sa, sb2;
-        if (16 * w < nb) sel_load(sa, 16 * w);
-        for (int c = 16 * w; c < nb; c += 128) {
-            const int c1 = c + 64;
-            if (c1 < nb) sel_load(sb2, c1);
-            sel_block(sa, c);
-            if (c1 >= nb) break;
-            if (c1 + 64 < nb) sel_load(sa, c1 + 64);
-            sel_block(sb2, c1);
-        }
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {       // row r = stride * (16 rb + col) of the sampled rows
-            const float mx = grp_max(rmax[rb]);
-            if (grp == 0) red_m[w][16 * rb + col] = mx;
-        }
-    }
-    for (int i = threadIdx.x; i < MAX_NB_LDS / 32 + 1; i += 256) exbits[i] = 0u;
-    __syncthreads();
-    // ---- 2. top-k -> sidx (ascending), exclusion bits
-    const int kxe = min(min(kx, nb), MAX_KX_LDS);
-    if (kxe > 0) {
-        topk_row(keys, nb, kxe, sm, idx_out ? idx_out + th * kxe : nullptr, nullptr, sidx);
-        for (int j = threadIdx.x; j < kxe; j += 256) atomicOr(&exbits[sidx[j] >> 5], 1u << (sidx[j] & 31));
-    }
-    __syncthreads();                       // keys dead from here: the ring may be overwritten
-    // ---- 3. split-K far + near: wave w, all rows, fixed reference max per row
+    // ---- routing of this tile (route_select_kernel): near leaves and row reference maxima
+    for (int i = threadIdx.x; i <= nb / 32; i += 256) exbits[i] = 0u;
+    for (int j = threadIdx.x; j < kxe; j += 256) sidx[j] = idx[th * kxe + j];
     float mref[4];
-    {
-        const int ts = TILE / stride;
-        float tile_max = -INFINITY;              // fallback reference for rows the select skipped
-        for (int r = 0; r < ts; ++r)
-            tile_max = fmaxf(tile_max, fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r])));
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            const int r = 16 * rb + col;
-            float m = tile_max;
-            if (stride == 1) m = fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r]));
-            mref[rb] = m == -INFINITY ? 0.0f : __fmul_rn(m, LOG2E);
-        }
+    for (int rb = 0; rb < 4; ++rb) {
+        const float m = rowmax[th * TILE + 16 * rb + col];
+        mref[rb] = m == -INFINITY ? 0.0f : __fmul_rn(m, LOG2E);
+        asm volatile("" : : "v"(mref[rb]));        // loaded before the first DMA (see settle)
     }
-    __syncthreads();                       // red_m is reused by the merge
+    __syncthreads();
+    for (int j = threadIdx.x; j < kxe; j += 256) atomicOr(&exbits[sidx[j] >> 5], 1u << (sidx[j] & 31));
+    __syncthreads();
     Rows4 st;
     float umax[4];
     char* myring = &ring[w][0][0];
@@ -1023,6 +1061,7 @@ __global__ __launch_bounds__(256) void route_kernel(
             for (int kss = 0; kss < 2; ++kss) bq[rb][kss] = *(const i32x4*)(dq8 + p * D + 64 * kss + 16 * grp);
             srow[rb] = __fmul_rn(sdq[p], LOG2E);
         }
+        settle(bq, srow);
         const int64_t srow0 = th * nb_pad;
         auto issue = [&](int bi) {
             const int c0 = lo + 32 * bi;
@@ -1090,6 +1129,7 @@ __global__ __launch_bounds__(256) void route_kernel(
             for (int kss = 0; kss < 2; ++kss) bq[rb][kss] = *(const i32x4*)(q8 + p * D + 64 * kss + 16 * grp);
             srow[rb] = __fmul_rn(__fmul_rn(sq[p], scale), LOG2E);
         }
+        settle(bq, srow);
         auto tok_of = [&](int j) {         // first token of the 16-token run at list position j
             const int jj = j < e_hi ? j : e_lo;
             return kh + (int64_t)sidx[jj / LEAF] * LEAF + (jj % LEAF);
@@ -1163,56 +1203,46 @@ __global__ __launch_bounds__(256) void route_kernel(
         }
     }
     __syncthreads();                      // every wave is done with its ring
-    float wsc[4];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
+    for (int rb = 0; rb < 4; ++rb) {      // O of wave w scaled to the merged maximum, into LDS
         const int r = 16 * rb + col;
         float mm = fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r]));
         mm = mm == -INFINITY ? 0.0f : mm;
-        wsc[rb] = exp2f(__fsub_rn(st.m[rb], mm));
-    }
-    const int r_out = threadIdx.x >> 2, qd = threadIdx.x & 3;
-    float den = 0.0f, mmr;
-    {
-        mmr = fmaxf(fmaxf(red_m[0][r_out], red_m[1][r_out]), fmaxf(red_m[2][r_out], red_m[3][r_out]));
-        mmr = mmr == -INFINITY ? 0.0f : mmr;
+        const float wsc = exp2f(__fsub_rn(st.m[rb], mm));
+        float* dst = mrg + (w * 64 + r) * MRG_STRIDE + 4 * grp;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) den = __fadd_rn(den, __fmul_rn(red_l[s][r_out], exp2f(__fsub_rn(red_m[s][r_out], mmr))));
-    }
-    const float dd = den < 1e-30f ? 1e-30f : den;
-    const int64_t qi = (int64_t)t * TILE + r_out;
-    const bool rvalid = qi < nq;
-    const int64_t orow = (int64_t)h * nq + qi;
-    for (int pass = 0; pass < 4; ++pass) {           // 32 dims (two dim blocks) per pass
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int db = 2 * pass + j;
-                const f32x4 o = st.o[rb][db];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = 16 * rb + col, dl = 16 * j + 4 * grp + i;   // dim within the pass
-                    mrg[(w * 64 + r) * 33 + dl] = __fmul_rn(o[i], wsc[rb]);
-                }
-            }
-        __syncthreads();
-        if (rvalid) {
-            f32x4 res[2];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int dl = 8 * qd + u;
-                float acc = 0.0f;
-#pragma unroll
-                for (int s = 0; s < 4; ++s) acc = __fadd_rn(acc, mrg[(s * 64 + r_out) * 33 + dl]);
-                res[u >> 2][u & 3] = __fdiv_rn(acc, dd);
-            }
-            *(f32x4*)(out + orow * D + 32 * pass + 8 * qd) = res[0];
-            *(f32x4*)(out + orow * D + 32 * pass + 8 * qd + 4) = res[1];
+        for (int db = 0; db < 8; ++db) {
+            const f32x4 o = st.o[rb][db];
+            *(f32x4*)(dst + 16 * db) = f32x4{__fmul_rn(o[0], wsc), __fmul_rn(o[1], wsc), __fmul_rn(o[2], wsc),
+                                             __fmul_rn(o[3], wsc)};
         }
-        __syncthreads();
     }
-    if (rvalid && qd == 0) logz[orow] = __fadd_rn(__fmul_rn(mmr, LN2), __logf(den));   // m in log2 units
+    const int r_out = threadIdx.x >> 2, qd = threadIdx.x & 3;      // row, 32-dim quarter
+    float mmr = fmaxf(fmaxf(red_m[0][r_out], red_m[1][r_out]), fmaxf(red_m[2][r_out], red_m[3][r_out]));
+    mmr = mmr == -INFINITY ? 0.0f : mmr;
+    float den = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) den = __fadd_rn(den, __fmul_rn(red_l[s][r_out], exp2f(__fsub_rn(red_m[s][r_out], mmr))));
+    const float inv = 1.0f / (den < 1e-30f ? 1e-30f : den);
+    const int64_t qi = (int64_t)t * TILE + r_out;
+    const int64_t orow = (int64_t)h * nq + qi;
+    __syncthreads();
+    if (qi < nq) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int dl = 32 * qd + 4 * u;
+            f32x4 acc = *(const f32x4*)(mrg + r_out * MRG_STRIDE + dl);
+#pragma unroll
+            for (int s = 1; s < 4; ++s) {
+                const f32x4 y = *(const f32x4*)(mrg + (s * 64 + r_out) * MRG_STRIDE + dl);
+                acc = f32x4{__fadd_rn(acc[0], y[0]), __fadd_rn(acc[1], y[1]), __fadd_rn(acc[2], y[2]),
+                            __fadd_rn(acc[3], y[3])};
+            }
+            *(f32x4*)(out + orow * D + dl) = f32x4{__fmul_rn(acc[0], inv), __fmul_rn(acc[1], inv),
+                                                   __fmul_rn(acc[2], inv), __fmul_rn(acc[3], inv)};
+        }
+        if (qd == 0) logz[orow] = __fadd_rn(__fmul_rn(mmr, LN2), __logf(den));   // m in log2 units
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1319,7 +1349,9 @@ int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
     const int lpb = 16;
-    dim3 grid((unsigned)((nt + 63) / 64), (unsigned)((nbp + lpb - 1) / lpb), (unsigned)heads);
+    const int64_t nblocks = (nt + 63) / 64 * ((nbp + lpb - 1) / lpb) * heads;
+    REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats: too many tiles x leaves x heads for one launch");
+    dim3 grid((unsigned)nblocks);
     hipStream_t s = (hipStream_t)stream;
 #define STATS_CASE(L)                                                                                         \
     case L:                                                                                                   \
@@ -1414,24 +1446,34 @@ int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t head
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
-               int stride, float scale, float* out, float* logz, int32_t* idx, void* stream) {
-    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && k8 && ks && v && out && logz,
+               int stride, float scale, float* out, float* logz, int32_t* idx, float* rowmax, void* stream) {
+    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && k8 && ks && v && out && logz && rowmax,
             "htrc_route: null pointer");
-    REQUIRE(aligned(vb, 16) && aligned(v, 16) && aligned(g8, 16) && aligned(k8, 16) && aligned(sg, 16) && aligned(ks, 16),
+    REQUIRE(aligned(vb, 16) && aligned(v, 16) && aligned(g8, 16) && aligned(k8, 16) && aligned(sg, 16) &&
+                aligned(ks, 16) && aligned(lz, 16),
             "htrc_route: misaligned buffer");
     REQUIRE(d == D, "htrc_route: head dim must be 128");
     REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_route: leaf must be 16/32/64/128");
     REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_route: bad sizes");
     const int64_t nb = nk / leaf, nt = (nq + TILE - 1) / TILE;
     REQUIRE(nb <= MAX_NB_LDS, "htrc_route: at most 8192 leaves per head");
-    REQUIRE(kx >= 0 && sink >= 0 && (kx < nb ? kx : nb) <= MAX_KX_LDS, "htrc_route: at most 1024 near leaves per tile");
+    REQUIRE(kx >= 0 && sink >= 0, "htrc_route: need kx >= 0 and sink >= 0");
+    const int kxe = (int)(kx < nb ? kx : nb);
+    REQUIRE(kxe <= MAX_KX_LDS, "htrc_route: at most 1024 near leaves per tile");
+    REQUIRE(kxe == 0 || idx, "htrc_route: idx is required when kx > 0");
     REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_route: stride must divide 64");
-    dim3 grid((unsigned)nt, 1, (unsigned)heads);
+    REQUIRE(nt * heads <= 0x7fffffff, "htrc_route: too many tiles x heads for one launch");
+    const int nbp = htrc_nb_pad(nb);
+    dim3 grid((unsigned)(nt * heads));
     hipStream_t s = (hipStream_t)stream;
-#define ROUTE_CASE(L)                                                                                       \
-    case L:                                                                                                 \
-        hipLaunchKernelGGL(route_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, \
-                           nq, (int)nt, nk, (int)nb, htrc_nb_pad(nb), kx, sink, stride, scale, out, logz, idx); \
+    hipLaunchKernelGGL(route_select_kernel, grid, dim3(256), (size_t)4 * nbp, s, dq8, sdq, g8, sg, lz, (int)nt,
+                       (int)nb, nbp, kxe, sink, stride, idx, rowmax);
+    int rc = launched("htrc_route");
+    if (rc != HTRC_OK) return rc;
+#define ROUTE_CASE(L)                                                                                          \
+    case L:                                                                                                    \
+        hipLaunchKernelGGL(route_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, \
+                           rowmax, nq, (int)nt, nk, (int)nb, nbp, kxe, scale, out, logz);                    \
         break;
     switch (leaf) {
         ROUTE_CASE(16)

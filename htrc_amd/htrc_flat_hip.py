@@ -177,20 +177,26 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
 
 def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: float, sink: int = 0, stride: int = 1,
           ws=None, out=None, logz=None, idx=None):
-    """Fused select -> top-k -> far + near -> normalised output (one launch per layer call).
-    -> (out [H,nq,D], logz [H,nq]); idx [H,nt,kx] int32 receives the routing when given."""
+    """Fused select -> top-k, then far + near -> normalised output (two launches per layer call).
+    -> (out [H,nq,D], logz [H,nq]); idx [H,nt,min(kx,nb)] int32 receives the routing (a
+    workspace buffer when not given)."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
     g8, sg, lz, vb = state["g8"], state["sg"], state["lz"], state["vb"]
     h, nk, d = (int(x) for x in k8.shape)
     dev = q8.device
+    nt = -(-int(nq) // TILE)
+    kxe = min(int(kx), nk // int(leaf))
     if out is None:
         out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
     if logz is None:
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
+    if idx is None and kxe > 0:
+        idx = _buf(ws, "idx", (h, nt, kxe), torch.int32, dev)
+    rowmax = _buf(ws, "rowmax", (h, nt * TILE), torch.float32, dev)
     call("htrc_route", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8), ptr(ks),
          ptr(v), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), float(scale), ptr(out), ptr(logz),
-         ptr(idx), stream_handle(dev))
+         ptr(idx), ptr(rowmax), stream_handle(dev))
     return out, logz
 
 

@@ -17,6 +17,7 @@
  *   sel      fp32 [H, nt, nbp]                  excl int8 [H, nt, nbp]; idx int32 [H, nt, kx]
  *   pm, pl   fp32 [H, nt, splits, 64]           pacc fp32 [H, nt, splits, 64, 128]
  *   out      fp32 [H, nq, 128]                  logz fp32 [H, nq]
+ *   rowmax   fp32 [H, nt*64]                    per-row far-field maximum (route)
  *
  * The reference implements the same path as Triton kernels driven from Python;
  * each entry point below names the reference interface it replaces.
@@ -30,7 +31,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 2
+#define HTRC_ABI_VERSION 3
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -81,13 +82,15 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
 int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int splits,
                int d, float* out, float* logz, void* stream);
 
-/* Fused production kernel: select -> top-k -> far + near -> normalised out/logz, one split,
- * SEL and the exclusion mask kept in LDS; idx (optional, may be NULL) receives the routing.
+/* Fused production path, two launches: (1) select -> top-k per tile, SEL kept in LDS, writing
+ * the routing idx [H, nt, min(kx, nb)] (ascending; required when kx > 0) and rowmax fp32
+ * [H, nt*64], each row's largest far-field score; (2) far + near field of every tile in one
+ * online softmax with that fixed reference, merged into normalised out / logz.
  * Replaces the chunk loop body of _flat_triton after leaf_stats (h3/htrc_flat.py:250-271). */
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
-               int stride, float scale, float* out, float* logz, int32_t* idx, void* stream);
+               int stride, float scale, float* out, float* logz, int32_t* idx, float* rowmax, void* stream);
 
 /* Self-test of the MFMA operand conventions the kernels rely on (no reference counterpart):
  * one 64-lane wave computes C = A B for A int8 [16, 64] / B int8 [64, 16] (i8 path) and

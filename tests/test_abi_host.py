@@ -62,7 +62,7 @@ def test_launchers_reject_bad_arguments_on_host(case):
         rc = lib.htrc_tile(*([f] * 13), 1, 64, 128, 64, 128, 1, 4, 48, 0.1, f, f, f, f, f, None)
         msg = "multiple of 32"
     else:
-        rc = lib.htrc_route(*([f] * 11), 1, 64, 64 * 9000, 64, 128, 4, 0, 1, 0.1, f, f, None, None)
+        rc = lib.htrc_route(*([f] * 11), 1, 64, 64 * 9000, 64, 128, 4, 0, 1, 0.1, f, f, None, f, None)
         msg = "8192"
     assert rc == 1
     assert msg in lib.htrc_last_error().decode()
