@@ -121,14 +121,29 @@ __global__ __launch_bounds__(256) void pack_k_kernel(const uint16_t* __restrict_
 // ---------------------------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
 
-// One direct global->LDS load: 16 bytes per lane to lds_base + lane * 16 (lds_base uniform,
-// M0 = its LDS byte address).  Issued as inline asm on purpose: the compiler's wait-count pass
-// treats every LDS DMA in flight as aliasing every later LDS read and puts a vmcnt(0) before
-// it, which would serialise each ring slot with the loads issued for the slots after it.  The
-// kernels order their LDS reads after the DMA themselves, with wait_vmcnt<N>.
-__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_base);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0) : "memory", "m0");
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
+
+// One direct global->LDS load: 16 bytes per lane from src to LDS address lds + lane * 16 (lds
+// wave-uniform; it goes to M0).  Issued as inline asm on purpose: the compiler's wait-count
+// pass treats every LDS DMA in flight as aliasing every later LDS read and puts a vmcnt(0)
+// before it, which would serialise each ring slot with the loads issued for the slots after
+// it.  The kernels order their LDS reads after the DMA themselves, with wait_vmcnt<N>.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 : : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+
+// The same load from a wave-uniform base (kept in SGPRs) plus a 32-bit per-lane byte offset
+// voff.  (No instruction offset: on these loads it moves the LDS destination as well.)
+__device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
+    // readfirstlane returns int: widen each half through uint32_t so the low half is not
+    // sign-extended into the high one
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 : : "v"(voff), "s"(bs), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 
 // s_waitcnt vmcnt(N): at most N vector-memory operations of this wave still in flight (they
@@ -160,7 +175,7 @@ __device__ __forceinline__ void stage_leaf(const uint16_t* __restrict__ K, const
         const int c = j * 256 + tid;
         const int row = (c >> 4) & (LEAF - 1), pc = c & 15;
         const uint16_t* X = c < 16 * LEAF ? K : V;
-        dma16(X + (key0 + row) * D + 8 * (pc ^ swz(row)), buf + (size_t)(j * 256 + w * 64) * 16);
+        dma16(X + (key0 + row) * D + 8 * (pc ^ swz(row)), lds_addr(buf + (size_t)(j * 256 + w * 64) * 16));
     }
 }
 
@@ -778,91 +793,29 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm
 }
 
 // ---------------------------------------------------------------------------------------------
-// route: the fused per-tile kernel of the production path (one workgroup of 4 waves per tile).
-//   1. select: SEL of every leaf (bit-exact, same arithmetic as select_kernel) into LDS;
-//   2. top-k in LDS (idx ascending, exclusion bytes);
-//   3. split-K far + near: wave w owns ALL 64 query rows (four 16-row MFMA column blocks, so
-//      every A operand it loads feeds four MFMAs) for a quarter of the far leaves and a
-//      quarter of the near tokens; the A operands of the next 32-key block are loaded while
-//      the current block is computed;
-//   4. the four partial (m, l, O) states merge through LDS into out / logZ.
-// SEL, excl and the partials never reach HBM (idx can be emitted for checking).
+// route: the production path, two launches per layer call.
+//   route_select_kernel, one 4-wave workgroup per tile: SEL of every leaf into LDS (bit-exact,
+//     the select_kernel arithmetic), top-k -> idx, and each row's largest far-field score;
+//   route_kernel, one 8-wave workgroup per tile: far + near field in one online softmax whose
+//     reference max is that score.  Wave pair pr = wave % 4 takes a quarter of the keys (its
+//     far leaves, then its near tokens, in 32-key blocks) and wave wave / 4 of the pair takes 32
+//     of the 64 rows: two waves share each SIMD, and each block in LDS feeds both.  A pair's
+//     blocks stream through a 3-slot LDS ring, loaded two blocks ahead by direct global->LDS
+//     loads split between the two waves; the four partial states merge through LDS.
+// SEL and the partial states never reach HBM.
 // ---------------------------------------------------------------------------------------------
-struct FarQK {          // prefetched one block ahead
-    i32x4 g[2][2];     // g8 A operands: [16-leaf half][64-dim k-step]
-    f32x4 sg[2], lz[2];
-    uint32_t ex[2];
+struct Rows2 {         // softmax state of the 32 rows of one wave
+    float m[2];        // reference max (log2 units), fixed during a pass
+    float l[2];        // this lane's share of the row sums
+    f32x4 o[2][8];     // O^T per row block: dims 16db + 4grp + i of row 16rb + lane%16
 };
 
-struct NearQK {
-    i32x4 k[2][2];     // k8 A operands: [16-token run][64-dim k-step]
-    f32x4 ks[2];
-    int64_t tok0[2];
-    bool ok[2];
-};
-
-struct Rows4 {         // online-softmax state of 64 rows held by one wave
-    float m[4];
-    float l[4];        // this lane's share of the row sums
-    f32x4 o[4][8];     // O^T per row block: dims 16db + 4grp + i of row 16rb + lane%16
-};
-
-__device__ __forceinline__ void load_far_qk(FarQK& f, int64_t srow, const int8_t* __restrict__ g8,
-                                            const float* __restrict__ sg, const float* __restrict__ lz,
-                                            const int8_t* __restrict__ excl_row, int c0, int col, int grp) {
+// p = 2^(u - m) for the log2-domain scores u[rb][0..7] of the two row blocks (keys
+// 16(e/4) + 4grp + e%4 of the block; masked keys -inf), l += p, O^T += V^T P^T.
+__device__ __forceinline__ void rows2_update(Rows2& st, const float (&sc)[2][8], const u32x2 (&v)[8][2]) {
+    bf16x8 P[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int64_t s0 = srow + c0 + 16 * h;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) f.g[h][ks] = *(const i32x4*)(g8 + (s0 + col) * D + 64 * ks + 16 * grp);
-        f.sg[h] = *(const f32x4*)(sg + s0 + 4 * grp);
-        f.lz[h] = *(const f32x4*)(lz + s0 + 4 * grp);
-        f.ex[h] = *(const uint32_t*)(excl_row + c0 + 16 * h + 4 * grp);
-    }
-}
-
-// PV operands of a 32-key block in key-quad layout: quads q0 + grp and q1 + grp.
-__device__ __forceinline__ void load_pv(u32x2 (&v)[8][2], const uint16_t* __restrict__ x4, int64_t q0, int64_t q1,
-                                        int col, int grp) {
-#pragma unroll
-    for (int db = 0; db < 8; ++db) {
-        const int dim = 16 * db + col;
-        v[db][0] = *(const u32x2*)(x4 + ((q0 + grp) * D + dim) * 4);
-        v[db][1] = *(const u32x2*)(x4 + ((q1 + grp) * D + dim) * 4);
-    }
-}
-
-template <int LEAF>
-__device__ __forceinline__ void load_near_qk(NearQK& n, int e0, int e_hi, int e_lo, const int32_t* idx_row, int64_t kh,
-                                             const int8_t* __restrict__ k8, const float* __restrict__ ks, int col,
-                                             int grp) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int j0 = e0 + 16 * h;
-        n.ok[h] = j0 < e_hi;
-        const int jj = n.ok[h] ? j0 : e_lo;
-        n.tok0[h] = kh + (int64_t)idx_row[jj / LEAF] * LEAF + (jj % LEAF);
-#pragma unroll
-        for (int kss = 0; kss < 2; ++kss)
-            n.k[h][kss] = *(const i32x4*)(k8 + (n.tok0[h] + col) * D + 64 * kss + 16 * grp);
-        n.ks[h] = *(const f32x4*)(ks + n.tok0[h] + 4 * grp);
-    }
-}
-
-// Softmax accumulation of the four row blocks with log2-domain scores u[rb][0..7] =
-// score * log2(e) (keys 16(e/4) + 4grp + e%4 of the block; masked keys -inf) and PV operands
-// v[db][half].  The reference max m of each row is fixed before the loops (the row's largest
-// far-field score, found by the select phase), so p = 2^(u - m) needs no running rescale and
-// O never leaves the MFMA accumulators; umax tracks the true maximum so the caller can redo
-// the (never observed) rows whose scores exceed m by more than 2^64 or underflow.
-constexpr float REF_SLACK = 64.0f;
-
-__device__ __forceinline__ void rows4_update(Rows4& st, float (&umax)[4], float (&sc)[4][8], const u32x2 (&v)[8][2]) {
-    bf16x8 P[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-        umax[rb] = fmaxf(umax[rb], fmaxf(fmaxf(fmaxf(sc[rb][0], sc[rb][1]), fmaxf(sc[rb][2], sc[rb][3])),
-                                         fmaxf(fmaxf(sc[rb][4], sc[rb][5]), fmaxf(sc[rb][6], sc[rb][7]))));
+    for (int rb = 0; rb < 2; ++rb) {
         float p[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(__fsub_rn(sc[rb][e], st.m[rb]));
@@ -874,42 +827,57 @@ __device__ __forceinline__ void rows4_update(Rows4& st, float (&umax)[4], float 
     for (int db = 0; db < 8; ++db) {
         const bf16x8 A = as_bf16x8(v[db][0], v[db][1]);
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) st.o[rb][db] = mfma_bf16(A, P[rb], st.o[rb][db]);
+        for (int rb = 0; rb < 2; ++rb) st.o[rb][db] = mfma_bf16(A, P[rb], st.o[rb][db]);
     }
 }
 
-// Per-wave LDS ring of 32-key blocks: [QK A operands 4 KB | PV A operands 8 KB | scales 256 B].
+// Ring slot of one 32-key block: [QK A operands 4 KB | PV rows 8 KB | scales 256 B].
 constexpr int RING_SLOTS = 3;
 constexpr int SLOT_BYTES = 4096 + 8192 + 256;
-constexpr int BLOCK_DMA = 13;                       // direct-to-LDS loads per wave per block
+constexpr int DMA_W0 = 7;                           // loads per block, first wave of a pair
+constexpr int DMA_W1 = 6;                           // ... second wave
 constexpr int MAX_KX_LDS = 1024;                    // near leaves per tile the route kernel holds
-// Merge: the four waves' scaled partial O, 64 rows x 128 dims each, rows padded to 132 floats.
+constexpr int MAX_PASSES = 3;                       // reference-max retries of a tile
+// Merge: the four wave pairs' partial O, 64 rows x 128 dims each, rows padded to 132 floats.
 constexpr int MRG_STRIDE = 132;
 static_assert(4 * 64 * MRG_STRIDE * 4 <= 4 * RING_SLOTS * SLOT_BYTES, "merge staging");
 
-// QK operand chunk j (0..3) of lane: [hh = j>>1][ks = j&1][grp][col] <- row (row0[hh] + col),
-// bytes (4ks + grp)*16 of an int8 [*, 128] matrix.
-__device__ __forceinline__ void dma_qk(const int8_t* __restrict__ x8, int64_t row0a, int64_t row0b, char* slot,
-                                       int lane) {
-    const int col = lane & 15, grp = lane >> 4;
+// Per-lane byte offsets of the 32-key block loads (loop invariant): the QK operand chunk of
+// lane (col, grp) and the swizzled PV row chunks (see dma_rows).
+struct BlockOffsets {
+    uint32_t qk[2];                                    // k-steps 0 and 1 (dims 0..63, 64..127)
+    uint32_t rows[4];
+};
+
+__device__ __forceinline__ BlockOffsets block_offsets(int lane) {
+    const int col = lane & 15, grp = lane >> 4, pc = lane & 15;
+    BlockOffsets o;
+    o.qk[0] = (uint32_t)(col * D + 16 * grp);
+    o.qk[1] = o.qk[0] + 64;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int64_t row = ((j >> 1) ? row0b : row0a) + col;
-        dma16(x8 + row * D + (4 * (j & 1) + grp) * 16, slot + j * 1024);
+        const int row = 4 * j + grp;                   // rows j*4 + grp, and the same + 16
+        o.rows[j] = (uint32_t)(row * 2 * D + 16 * (pc ^ swz(row)));
     }
+    return o;
 }
 
-// PV rows of a 32-key block: ring chunk s = 64j + lane holds the 16-byte chunk (s % 16) ^
-// swz(row) of row s / 16 (rows 0..15 from row0a, 16..31 from row0b) of a bf16 [*, 128] matrix.
-__device__ __forceinline__ void dma_rows(const uint16_t* __restrict__ X, int64_t row0a, int64_t row0b, char* slot,
-                                         int lane) {
-    const int pc = lane & 15;
+// QK operand chunk j (0..3) of lane: [hh = j>>1][ks = j&1][grp][col] <- row (row0[hh] + col),
+// bytes (4ks + grp)*16 of an int8 [*, 128] matrix; x0/x1 point at rows row0a/row0b.
+__device__ __forceinline__ void dma_qk(const int8_t* x0, const int8_t* x1, const BlockOffsets& bo, uint32_t slot) {
+    dma16s(x0, bo.qk[0], slot);
+    dma16s(x0, bo.qk[1], slot + 1024);
+    dma16s(x1, bo.qk[0], slot + 2048);
+    dma16s(x1, bo.qk[1], slot + 3072);
+}
+
+// PV rows of a 32-key block, chunks j in [J0, J1): ring chunk s = 64j + lane holds the 16-byte
+// chunk (s % 16) ^ swz(row) of row s / 16 (rows 0..15 from x0, 16..31 from x1) of a bf16
+// [*, 128] matrix.  swz(row) = swz(row - 16), so both halves share the lane offsets.
+template <int J0, int J1>
+__device__ __forceinline__ void dma_rows(const uint16_t* x0, const uint16_t* x1, const BlockOffsets& bo, uint32_t slot) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int row = 4 * j + (lane >> 4);
-        const int64_t r = (row < 16 ? row0a : row0b) + (row & 15);
-        dma16(X + r * D + 8 * (pc ^ swz(row)), slot + 4096 + j * 1024);
-    }
+    for (int j = J0; j < J1; ++j) dma16s(j < 4 ? x0 : x1, bo.rows[j & 3], slot + 4096 + j * 1024);
 }
 
 // route_select: first launch of the fused production path, one workgroup (4 waves) per tile.
@@ -1004,233 +972,256 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
 }
 
 template <int LEAF>
-__global__ __launch_bounds__(256) void route_kernel(
+__global__ __launch_bounds__(512) void route_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ sq, const int8_t* __restrict__ dq8,
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ k8,
     const float* __restrict__ ks, const uint16_t* __restrict__ v, const int32_t* __restrict__ idx,
     const float* __restrict__ rowmax, int64_t nq, int nt, int64_t nk, int nb, int nb_pad, int kxe, float scale,
     float* __restrict__ out, float* __restrict__ logz) {
-    __shared__ __align__(16) char ring[4][RING_SLOTS][SLOT_BYTES];   // also: merge staging
+    __shared__ __align__(16) char ring[4][RING_SLOTS][SLOT_BYTES];   // one per wave pair; also merge staging
     __shared__ int32_t sidx[MAX_KX_LDS];
     __shared__ uint32_t exbits[MAX_NB_LDS / 32 + 1];
-    __shared__ float red_m[4][64], red_l[4][64];
+    __shared__ float red_m[64], red_l[4][64];
+    __shared__ int redo;
     float* mrg = (float*)&ring[0][0][0];                       // merge staging: 4 x 64 x MRG_STRIDE floats
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar bookkeeping
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int pr = wv & 3, hr = wv >> 2;                       // key quarter (wave pair), row half
     // 1-D grid over (tile, head), tile fastest: each XCD runs a contiguous run of tiles of one
     // head at a time, so the near-field leaves adjacent tiles share are fetched into one L2.
     const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
     const int t = (int)(blk % (uint32_t)nt), h = (int)(blk / (uint32_t)nt);
     const int64_t th = (int64_t)h * nt + t;
-    // ---- routing of this tile (route_select_kernel): near leaves and row reference maxima
-    for (int i = threadIdx.x; i <= nb / 32; i += 256) exbits[i] = 0u;
-    for (int j = threadIdx.x; j < kxe; j += 256) sidx[j] = idx[th * kxe + j];
-    float mref[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-        const float m = rowmax[th * TILE + 16 * rb + col];
-        mref[rb] = m == -INFINITY ? 0.0f : __fmul_rn(m, LOG2E);
-        asm volatile("" : : "v"(mref[rb]));        // loaded before the first DMA (see settle)
-    }
-    __syncthreads();
-    for (int j = threadIdx.x; j < kxe; j += 256) atomicOr(&exbits[sidx[j] >> 5], 1u << (sidx[j] & 31));
-    __syncthreads();
-    Rows4 st;
-    float umax[4];
-    char* myring = &ring[w][0][0];
     const int64_t kh = (int64_t)h * nk;
-    for (int pass = 0; pass < 2; ++pass) {
+    const int64_t row0 = th * TILE + 32 * hr + col;            // this lane's rows: row0, row0 + 16
+    // ---- routing of this tile (route_select_kernel)
+    for (int i = threadIdx.x; i <= nb / 32; i += 512) exbits[i] = 0u;
+    for (int j = threadIdx.x; j < kxe; j += 512) sidx[j] = idx[th * kxe + j];
+    float mref[2];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-        st.m[rb] = mref[rb];
-        st.l[rb] = 0.0f;
-        umax[rb] = -INFINITY;
-#pragma unroll
-        for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rb = 0; rb < 2; ++rb) {
+        const float m = rowmax[row0 + 16 * rb];
+        mref[rb] = m == -INFINITY ? 0.0f : __fmul_rn(m, LOG2E);
     }
-    {   // far field: leaves [lo, hi), 32-leaf blocks through the LDS ring
-        const int lpw = ((nb + 3) / 4 + 31) / 32 * 32;
-        const int lo = w * lpw, hi = min(nb, lo + lpw);
-        const int nblk = hi > lo ? (hi - lo + 31) / 32 : 0;
-        i32x4 bq[4][2];
-        float srow[4];
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            const int64_t p = th * TILE + 16 * rb + col;
-#pragma unroll
-            for (int kss = 0; kss < 2; ++kss) bq[rb][kss] = *(const i32x4*)(dq8 + p * D + 64 * kss + 16 * grp);
-            srow[rb] = __fmul_rn(sdq[p], LOG2E);
+    __syncthreads();
+    for (int j = threadIdx.x; j < kxe; j += 512) atomicOr(&exbits[sidx[j] >> 5], 1u << (sidx[j] & 31));
+    // ---- key ranges: pair q owns far leaves [q lpw, q lpw + lpw) and near list positions
+    // [q epw, q epw + epw), in 32-key blocks; every wave runs the longest pair's step count
+    const int lpw = ((nb + 3) / 4 + 31) / 32 * 32;
+    const int e_n = kxe * LEAF;
+    const int epw = ((e_n + 3) / 4 + 31) / 32 * 32;
+    const int lo = pr * lpw, hi = min(nb, lo + lpw);
+    const int e_lo = pr * epw, e_hi = min(e_n, e_lo + epw);
+    const int nf = hi > lo ? (hi - lo + 31) / 32 : 0;
+    const int nn = e_hi > e_lo ? (e_hi - e_lo + 31) / 32 : 0;
+    const int sf_steps = min(nb, lpw) > 0 ? (min(nb, lpw) + 31) / 32 : 0;        // pair 0 is the longest
+    const int sn_steps = min(e_n, epw) > 0 ? (min(e_n, epw) + 31) / 32 : 0;
+    const int64_t srow0 = th * nb_pad;
+    char* pring = &ring[pr][0][0];
+    const uint32_t pring_lds = lds_addr(pring);
+    auto wait_block = [&](int bi, int nblk) {    // this wave's loads of block bi have landed
+        if (bi + 1 < nblk) {
+            if (hr == 0) wait_vmcnt<DMA_W0>();
+            else wait_vmcnt<DMA_W1>();
+        } else {
+            wait_vmcnt<0>();
         }
-        settle(bq, srow);
-        const int64_t srow0 = th * nb_pad;
-        auto issue = [&](int bi) {
-            const int c0 = lo + 32 * bi;
-            char* slot = myring + (bi % RING_SLOTS) * SLOT_BYTES;
-            dma_qk(g8, srow0 + c0, srow0 + c0 + 16, slot, lane);
-            dma_rows(vb, srow0 + c0, srow0 + c0 + 16, slot, lane);
-            if (lane < 16) {
-                const float* src = (lane < 8 ? sg + srow0 + c0 + 4 * lane : lz + srow0 + c0 + 4 * (lane - 8));
-                dma16(src, slot + 12288);
+    };
+    const BlockOffsets bo = block_offsets(lane);
+    // This wave's share of the loads of a 32-key block with rows r0.. and r1.. (16 each).  The
+    // scale area gets 32 floats from s_lo (lanes 0..7) and 32 from s_hi (lanes 8..15); a near
+    // block's runs hold only 16 tokens each, so there (nlim = 3) lanes 4..7 and 12..15 repeat
+    // the run's first 16 scales instead of reading past it.
+    auto load_block = [&](uint32_t slot, const int8_t* X8, const uint16_t* XV, int64_t r0, int64_t r1,
+                          const float* s_lo, const float* s_hi, int nlim) {
+        if (hr == 0) {
+            dma_qk(X8 + r0 * D, X8 + r1 * D, bo, slot);
+            dma_rows<0, 2>(XV + r0 * D, XV + r1 * D, bo, slot);
+            if (lane < 16) dma16((lane < 8 ? s_lo : s_hi) + 4 * (lane & nlim), slot + 12288);
+        } else {
+            dma_rows<2, 8>(XV + r0 * D, XV + r1 * D, bo, slot);
+        }
+    };
+    Rows2 st;
+#pragma unroll 1
+    for (int pass = 0; pass < MAX_PASSES; ++pass) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            st.m[rb] = mref[rb];
+            st.l[rb] = 0.0f;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        {   // ---- far field: S^T = g8 dq8^T, score = dot * sdq * sg + lz, excluded leaves masked
+            i32x4 bq[2][2];
+            float srow[2];
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                const int64_t p = row0 + 16 * rb;
+                bq[rb][0] = *(const i32x4*)(dq8 + p * D + 16 * grp);
+                bq[rb][1] = *(const i32x4*)(dq8 + p * D + 64 + 16 * grp);
+                srow[rb] = __fmul_rn(sdq[p], LOG2E);
+                // loaded before the first DMA: the compiler's own wait for them would drain the ring
+                asm volatile("" : : "v"(bq[rb][0]), "v"(bq[rb][1]), "v"(srow[rb]), "v"(mref[rb]));
             }
-        };
-        if (nblk > 0) issue(0);
-        if (nblk > 1) issue(1);
-        for (int bi = 0; bi < nblk; ++bi) {
-            if (bi + 2 < nblk) issue(bi + 2);
-            const int ahead = min(2, nblk - 1 - bi);
-            if (ahead == 2) wait_vmcnt<2 * BLOCK_DMA>();
-            else if (ahead == 1) wait_vmcnt<BLOCK_DMA>();
-            else wait_vmcnt<0>();
-            const char* slot = myring + (bi % RING_SLOTS) * SLOT_BYTES;
-            const int c0 = lo + 32 * bi;
-            const uint32_t exw = exbits[c0 >> 5];
-            float sc[4][8];
+            __syncthreads();            // exbits complete; the ring is free (merge / earlier pass)
+            auto issue = [&](int bi) {
+                if (bi >= nf) return;
+                const int64_t r0 = srow0 + lo + 32 * bi;
+                load_block(pring_lds + (bi % RING_SLOTS) * SLOT_BYTES, g8, vb, r0, r0 + 16, sg + r0, lz + r0, 7);
+            };
+            issue(0);
+            issue(1);
+#pragma unroll 1
+            for (int bi = 0; bi < sf_steps; ++bi) {
+                if (bi < nf) wait_block(bi, nf);
+                __syncthreads();        // the partner's loads have landed too; slot (bi + 2) % 3 is free
+                issue(bi + 2);
+                if (bi >= nf) continue;
+                const char* slot = pring + (bi % RING_SLOTS) * SLOT_BYTES;
+                const int c0 = lo + 32 * bi;
+                const uint32_t exw = exbits[c0 >> 5];
+                float sc[2][8];
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const i32x4 A0 = *(const i32x4*)(slot + ((hh * 2 + 0) * 64 + lane) * 16);
-                const i32x4 A1 = *(const i32x4*)(slot + ((hh * 2 + 1) * 64 + lane) * 16);
-                i32x4 acc[4];
+                for (int hh = 0; hh < 2; ++hh) {
+                    const i32x4 A0 = *(const i32x4*)(slot + ((hh * 2 + 0) * 64 + lane) * 16);
+                    const i32x4 A1 = *(const i32x4*)(slot + ((hh * 2 + 1) * 64 + lane) * 16);
+                    i32x4 acc[2];
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    acc[rb] = mfma_i8(A0, bq[rb][0], i32x4{0, 0, 0, 0});
-                    acc[rb] = mfma_i8(A1, bq[rb][1], acc[rb]);
+                    for (int rb = 0; rb < 2; ++rb) {
+                        acc[rb] = mfma_i8(A0, bq[rb][0], i32x4{0, 0, 0, 0});
+                        acc[rb] = mfma_i8(A1, bq[rb][1], acc[rb]);
+                    }
+                    const f32x4 sgv = *(const f32x4*)(slot + 12288 + (16 * hh + 4 * grp) * 4);
+                    const f32x4 lzv = *(const f32x4*)(slot + 12288 + 128 + (16 * hh + 4 * grp) * 4);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int cl = 16 * hh + 4 * grp + i;          // leaf within the block
+                        const bool ok = c0 + cl < hi && ((exw >> cl) & 1u) == 0u;
+                        const float bias = ok ? __fmul_rn(lzv[i], LOG2E) : -INFINITY;
+#pragma unroll
+                        for (int rb = 0; rb < 2; ++rb)
+                            sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i]), bias);
+                    }
                 }
-                const f32x4 sgv = *(const f32x4*)(slot + 12288 + (16 * hh + 4 * grp) * 4);
-                const f32x4 lzv = *(const f32x4*)(slot + 12288 + 128 + (16 * hh + 4 * grp) * 4);
+                u32x2 pvop[8][2];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int cl = 16 * hh + 4 * grp + i;          // leaf within the block
-                    const bool ok = c0 + cl < hi && ((exw >> cl) & 1u) == 0u;
-                    const float bias = ok ? __fmul_rn(lzv[i], LOG2E) : -INFINITY;
+                for (int db = 0; db < 8; ++db)
 #pragma unroll
-                    for (int rb = 0; rb < 4; ++rb)
-                        sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i]), bias);
-                }
+                    for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
+                rows2_update(st, sc, pvop);
             }
-            u32x2 pvop[8][2];
-#pragma unroll
-            for (int db = 0; db < 8; ++db)
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
-            rows4_update(st, umax, sc, pvop);
         }
-    }
-    {   // near field: tokens [e_lo, e_hi) of the selected list, same ring
-        const int e_n = kxe * LEAF;
-        const int epw = ((e_n + 3) / 4 + 31) / 32 * 32;
-        const int e_lo = w * epw, e_hi = min(e_n, e_lo + epw);
-        const int nblk = e_hi > e_lo ? (e_hi - e_lo + 31) / 32 : 0;
-        i32x4 bq[4][2];
-        float srow[4];
+        {   // ---- near field: S^T = k8 q8^T, score = dot * sq * ks * scale
+            i32x4 bq[2][2];
+            float srow[2];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            const int64_t p = th * TILE + 16 * rb + col;
-#pragma unroll
-            for (int kss = 0; kss < 2; ++kss) bq[rb][kss] = *(const i32x4*)(q8 + p * D + 64 * kss + 16 * grp);
-            srow[rb] = __fmul_rn(__fmul_rn(sq[p], scale), LOG2E);
-        }
-        settle(bq, srow);
-        auto tok_of = [&](int j) {         // first token of the 16-token run at list position j
-            const int jj = j < e_hi ? j : e_lo;
-            return kh + (int64_t)sidx[jj / LEAF] * LEAF + (jj % LEAF);
-        };
-        auto issue = [&](int bi) {
-            const int e0 = e_lo + 32 * bi;
-            const int64_t t0 = tok_of(e0), t1 = tok_of(e0 + 16);
-            char* slot = myring + (bi % RING_SLOTS) * SLOT_BYTES;
-            dma_qk(k8, t0, t1, slot, lane);
-            dma_rows(v, t0, t1, slot, lane);
-            if (lane < 8) dma16(ks + (lane < 4 ? t0 + 4 * lane : t1 + 4 * (lane - 4)), slot + 12288);
-        };
-        // the ring slots of the far loop are all consumed: the near loop restarts at slot 0
-        if (nblk > 0) issue(0);
-        if (nblk > 1) issue(1);
-        for (int bi = 0; bi < nblk; ++bi) {
-            if (bi + 2 < nblk) issue(bi + 2);
-            const int ahead = min(2, nblk - 1 - bi);
-            if (ahead == 2) wait_vmcnt<2 * BLOCK_DMA>();
-            else if (ahead == 1) wait_vmcnt<BLOCK_DMA>();
-            else wait_vmcnt<0>();
-            const char* slot = myring + (bi % RING_SLOTS) * SLOT_BYTES;
-            const int e0 = e_lo + 32 * bi;
-            float sc[4][8];
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const i32x4 A0 = *(const i32x4*)(slot + ((hh * 2 + 0) * 64 + lane) * 16);
-                const i32x4 A1 = *(const i32x4*)(slot + ((hh * 2 + 1) * 64 + lane) * 16);
-                i32x4 acc[4];
-#pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    acc[rb] = mfma_i8(A0, bq[rb][0], i32x4{0, 0, 0, 0});
-                    acc[rb] = mfma_i8(A1, bq[rb][1], acc[rb]);
-                }
-                const f32x4 ksv = *(const f32x4*)(slot + 12288 + (16 * hh + 4 * grp) * 4);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bool ok = (e0 + 16 * hh + 4 * grp + i) < e_hi;
-                    const float bias = ok ? 0.0f : -INFINITY;
-#pragma unroll
-                    for (int rb = 0; rb < 4; ++rb)
-                        sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]), bias);
-                }
+            for (int rb = 0; rb < 2; ++rb) {
+                const int64_t p = row0 + 16 * rb;
+                bq[rb][0] = *(const i32x4*)(q8 + p * D + 16 * grp);
+                bq[rb][1] = *(const i32x4*)(q8 + p * D + 64 + 16 * grp);
+                srow[rb] = __fmul_rn(__fmul_rn(sq[p], scale), LOG2E);
+                asm volatile("" : : "v"(bq[rb][0]), "v"(bq[rb][1]), "v"(srow[rb]));
             }
-            u32x2 pvop[8][2];
+            __syncthreads();            // every wave is done with the far blocks in the ring
+            auto tok_of = [&](int j) {  // first token of the 16-token run at list position j
+                const int jj = j < e_hi ? j : e_lo;
+                return kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[jj / LEAF]) * LEAF + (jj % LEAF);
+            };
+            auto issue = [&](int bi) {
+                if (bi >= nn) return;
+                const int e0 = e_lo + 32 * bi;
+                const int64_t r0 = tok_of(e0), r1 = tok_of(e0 + 16);
+                load_block(pring_lds + (bi % RING_SLOTS) * SLOT_BYTES, k8, v, r0, r1, ks + r0, ks + r1, 3);
+            };
+            issue(0);
+            issue(1);
+#pragma unroll 1
+            for (int bi = 0; bi < sn_steps; ++bi) {
+                if (bi < nn) wait_block(bi, nn);
+                __syncthreads();
+                issue(bi + 2);
+                if (bi >= nn) continue;
+                const char* slot = pring + (bi % RING_SLOTS) * SLOT_BYTES;
+                const int e0 = e_lo + 32 * bi;
+                float sc[2][8];
 #pragma unroll
-            for (int db = 0; db < 8; ++db)
+                for (int hh = 0; hh < 2; ++hh) {
+                    const i32x4 A0 = *(const i32x4*)(slot + ((hh * 2 + 0) * 64 + lane) * 16);
+                    const i32x4 A1 = *(const i32x4*)(slot + ((hh * 2 + 1) * 64 + lane) * 16);
+                    i32x4 acc[2];
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
-            rows4_update(st, umax, sc, pvop);
+                    for (int rb = 0; rb < 2; ++rb) {
+                        acc[rb] = mfma_i8(A0, bq[rb][0], i32x4{0, 0, 0, 0});
+                        acc[rb] = mfma_i8(A1, bq[rb][1], acc[rb]);
+                    }
+                    // ks of the 32 tokens: run 0 at bytes 0..63, run 1 at 128..191
+                    const f32x4 ksv = *(const f32x4*)(slot + 12288 + 128 * hh + 16 * grp);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const bool ok = (e0 + 16 * hh + 4 * grp + i) < e_hi;
+                        const float bias = ok ? 0.0f : -INFINITY;
+#pragma unroll
+                        for (int rb = 0; rb < 2; ++rb)
+                            sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]), bias);
+                    }
+                }
+                u32x2 pvop[8][2];
+#pragma unroll
+                for (int db = 0; db < 8; ++db)
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
+                rows2_update(st, sc, pvop);
+            }
         }
-    }
-        // rows whose scores outran the reference by 2^64, or underflowed: redo with the true max
+        // Row totals over the four key quarters (all at the same reference).  A total outside
+        // [2^-60, 2^64] means the reference missed the row's maximum by more than 60 octaves
+        // (never observed on real scores): every p <= total, so the pass is redone with the
+        // reference moved to m + log2(total).
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            const float lt = grp_sum(st.l[rb]);
+            if (grp == 0) red_l[pr][32 * hr + 16 * rb + col] = lt;
+        }
+        if (threadIdx.x == 0) redo = 0;
+        __syncthreads();
         bool bad = false;
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            const float lt = grp_sum(st.l[rb]);
-            const bool r_bad = umax[rb] > mref[rb] + REF_SLACK || (umax[rb] > -INFINITY && lt < 0x1p-60f);
-            if (r_bad) mref[rb] = umax[rb];
-            bad |= r_bad;
+        for (int rb = 0; rb < 2; ++rb) {
+            const int r = 32 * hr + 16 * rb + col;
+            const float tot = __fadd_rn(__fadd_rn(red_l[0][r], red_l[1][r]), __fadd_rn(red_l[2][r], red_l[3][r]));
+            if (!(tot >= 0x1p-60f && tot <= 0x1p64f)) {
+                bad = true;
+                mref[rb] = tot > 0.0f && tot <= 3.0e38f ? __fadd_rn(mref[rb], __log2f(tot))
+                                                        : __fadd_rn(mref[rb], tot == 0.0f ? -120.0f : 120.0f);
+            }
         }
-        if (!__any(bad)) break;
+        if (bad) redo = 1;
+        __syncthreads();
+        if (redo == 0 || pass + 1 == MAX_PASSES) break;
     }
-    // ---- 4. merge the four partial states (h3/htrc_flat_triton.py:263-273 algebra, log2 units)
+    // ---- merge: every pair used the same reference per row, so the partial sums simply add
+    // (h3/htrc_flat_triton.py:263-273 with equal maxima)
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-        const float lt = grp_sum(st.l[rb]);
-        if (grp == 0) {
-            red_m[w][16 * rb + col] = st.m[rb];
-            red_l[w][16 * rb + col] = lt;
-        }
+    for (int rb = 0; rb < 2; ++rb) {
+        const int r = 32 * hr + 16 * rb + col;
+        if (pr == 0 && grp == 0) red_m[r] = st.m[rb];
+        float* dst = mrg + (pr * 64 + r) * MRG_STRIDE + 4 * grp;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) *(f32x4*)(dst + 16 * db) = st.o[rb][db];
     }
-    __syncthreads();                      // every wave is done with its ring
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {      // O of wave w scaled to the merged maximum, into LDS
-        const int r = 16 * rb + col;
-        float mm = fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r]));
-        mm = mm == -INFINITY ? 0.0f : mm;
-        const float wsc = exp2f(__fsub_rn(st.m[rb], mm));
-        float* dst = mrg + (w * 64 + r) * MRG_STRIDE + 4 * grp;
-#pragma unroll
-        for (int db = 0; db < 8; ++db) {
-            const f32x4 o = st.o[rb][db];
-            *(f32x4*)(dst + 16 * db) = f32x4{__fmul_rn(o[0], wsc), __fmul_rn(o[1], wsc), __fmul_rn(o[2], wsc),
-                                             __fmul_rn(o[3], wsc)};
-        }
-    }
-    const int r_out = threadIdx.x >> 2, qd = threadIdx.x & 3;      // row, 32-dim quarter
-    float mmr = fmaxf(fmaxf(red_m[0][r_out], red_m[1][r_out]), fmaxf(red_m[2][r_out], red_m[3][r_out]));
-    mmr = mmr == -INFINITY ? 0.0f : mmr;
-    float den = 0.0f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) den = __fadd_rn(den, __fmul_rn(red_l[s][r_out], exp2f(__fsub_rn(red_m[s][r_out], mmr))));
+    __syncthreads();
+    const int r_out = threadIdx.x >> 3, part = threadIdx.x & 7;    // row, 16-dim eighth
+    const float den =
+        __fadd_rn(__fadd_rn(red_l[0][r_out], red_l[1][r_out]), __fadd_rn(red_l[2][r_out], red_l[3][r_out]));
     const float inv = 1.0f / (den < 1e-30f ? 1e-30f : den);
     const int64_t qi = (int64_t)t * TILE + r_out;
-    const int64_t orow = (int64_t)h * nq + qi;
-    __syncthreads();
     if (qi < nq) {
+        const int64_t orow = (int64_t)h * nq + qi;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int dl = 32 * qd + 4 * u;
+        for (int u = 0; u < 4; ++u) {
+            const int dl = 16 * part + 4 * u;
             f32x4 acc = *(const f32x4*)(mrg + r_out * MRG_STRIDE + dl);
 #pragma unroll
             for (int s = 1; s < 4; ++s) {
@@ -1241,7 +1232,7 @@ __global__ __launch_bounds__(256) void route_kernel(
             *(f32x4*)(out + orow * D + dl) = f32x4{__fmul_rn(acc[0], inv), __fmul_rn(acc[1], inv),
                                                    __fmul_rn(acc[2], inv), __fmul_rn(acc[3], inv)};
         }
-        if (qd == 0) logz[orow] = __fadd_rn(__fmul_rn(mmr, LN2), __logf(den));   // m in log2 units
+        if (part == 0) logz[orow] = __fadd_rn(__fmul_rn(red_m[r_out], LN2), __logf(den));   // m in log2 units
     }
 }
 
@@ -1472,7 +1463,7 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
     if (rc != HTRC_OK) return rc;
 #define ROUTE_CASE(L)                                                                                          \
     case L:                                                                                                    \
-        hipLaunchKernelGGL(route_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, \
+        hipLaunchKernelGGL(route_kernel<L>, grid, dim3(512), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, \
                            rowmax, nq, (int)nt, nk, (int)nb, nbp, kxe, scale, out, logz);                    \
         break;
     switch (leaf) {
