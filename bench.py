@@ -30,20 +30,38 @@ PEAK_BF16_TFLOPS = 2500.0      # dense bf16 MFMA, TFLOP/s
 
 
 def algorithmic(h, nq, nk, leaf, kx, d=128, tile=64):
-    """Per-launch algorithmic HBM bytes and MFMA ops of every kernel of one layer call."""
+    """Per-launch algorithmic HBM bytes and MFMA ops of every kernel of one layer call.
+    Each operand is counted once per launch (near-field K/V once per head: adjacent tiles
+    share leaves in L2); the per-(tile, leaf) state is g8 d + vb 2d + sg 4 + lz 4 bytes."""
     nt = -(-nq // tile)
     nb = nk // leaf
     rows = nt * tile
+    kx = min(kx, nb)
+    state = nt * nb * (3 * d + 8)
     f = {}
     f["pack_q"] = {"bytes": h * (2 * nq * d + 2 * rows * d + 8 * rows + 4 * nt * d)}
     f["pack_k"] = {"bytes": h * (2 * nk * d + nk * d + 4 * nk)}
-    f["stats"] = {"bytes": h * (4 * nk * d + nt * nb * (3 * d + 8)),
-                  "flops_fp32": h * 6 * nt * nk * d}
-    state = nt * nb * (3 * d + 8)
-    f["route"] = {"bytes": h * (state + 2 * rows * d + 8 * rows + nk * (3 * d + 4) + 4 * nq * (d + 1)),
-                  "i8_ops": h * (2 * rows * nb * d * 2 + 2 * rows * kx * leaf * d),
-                  "bf16_flops": h * (2 * rows * nb * d + 2 * rows * kx * leaf * d)}
+    f["stats"] = {"bytes": h * (4 * nk * d + state + 4 * nt * d)}
+    f["route_select"] = {"bytes": h * (nt * nb * (d + 8) + rows * (d + 4) + nt * kx * 4 + rows * 4),
+                         "i8_ops": h * 2 * rows * nb * d, "bf16_flops": 0}
+    f["route_attend"] = {"bytes": h * (state + 2 * rows * (d + 4) + nk * (3 * d + 4) + nt * kx * 4 + rows * 4
+                                       + 4 * nq * (d + 1)),
+                         "i8_ops": h * (2 * rows * nb * d + 2 * rows * kx * leaf * d),
+                         "bf16_flops": h * (2 * rows * nb * d + 2 * rows * kx * leaf * d)}
     return f
+
+
+def measured_traffic(config):
+    """HBM bytes per launch of each kernel, measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    (scaled by a copy kernel of known size) and committed in profiles/flat_kernels_<config>.md
+    as a JSON block; {} when there is no such summary."""
+    path = ROOT / "profiles" / f"flat_kernels_{config}.md"
+    try:
+        text = path.read_text()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(block).get("traffic_bytes", {})
+    except (OSError, IndexError, ValueError):
+        return {}
 
 
 def roofline_entry(name, ms, fig):
@@ -153,11 +171,14 @@ def main():
     g8, lz, vbs, sg, _ = hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws)
     packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "v": v}
     lstate = {"g8": g8, "sg": sg, "lz": lz, "vb": vbs}
+    idx, rowmax = hip.route_select(packed, lstate, nq=nq, leaf=leaf, kx=kx, ws=ws)
     stages = {
         "pack_q": lambda: hip.pack_q(q, ws=ws),
         "pack_k": lambda: hip.pack_k(k, ws=ws),
         "stats": lambda: hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws),
-        "route": lambda: hip.route(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, ws=ws),
+        "route_select": lambda: hip.route_select(packed, lstate, nq=nq, leaf=leaf, kx=kx, ws=ws),
+        "route_attend": lambda: hip.route_attend(packed, lstate, idx, rowmax, nq=nq, leaf=leaf, kx=kx, scale=scale,
+                                                 ws=ws),
     }
     kms = {}
     stream = torch.cuda.current_stream(dev)
@@ -182,17 +203,21 @@ def main():
         del src, dst
     figs = algorithmic(h, nq, nk, leaf, kx, d)
     kernels = {n: roofline_entry(n, kms[n], figs[n]) for n in stages}
+    traffic = measured_traffic(a.config)
+    for n, e in kernels.items():
+        e["traffic"] = traffic.get(n)
     dom = max(kernels.values(), key=lambda e: e["ms"])
     fig = figs[dom["kernel"]]
     if dom["bound"] == "hbm":
         ach = fig["bytes"] / (dom["ms"] * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "kernel": dom["kernel"]}
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic.get(dom["kernel"]), "kernel": dom["kernel"],
+                "algorithmic_bytes": fig["bytes"]}
     else:
         # bf16-equivalent rate: an int8 op costs half a bf16 flop at the MI355X dense peaks
         ach = (fig["bf16_flops"] + fig["i8_ops"] * PEAK_BF16_TFLOPS / PEAK_I8_TOPS) / (dom["ms"] * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic.get(dom["kernel"]),
                 "kernel": dom["kernel"], "note": "bf16-equivalent: int8 ops weighted by 2.5/5.0"}
     res = {"metric": METRIC, "value": round(ms, 4), "unit": "ms/call", "n_gpus": 1, "steps": a.steps,
            "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",

@@ -13,7 +13,7 @@ import torch
 
 HERE = Path(__file__).resolve().parent
 LIBPATH = HERE / "libhtrc_flat.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -32,6 +32,8 @@ SIGNATURES = {
     "htrc_topk": [_vp, _i64, _i64, _int, _int, _vp, _vp, _vp],
     "htrc_tile": [_vp] * 13 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _flt] + [_vp] * 6,
     "htrc_merge": [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp, _vp],
+    "htrc_route_select": [_vp] * 5 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _vp, _vp, _vp],
+    "htrc_route_attend": [_vp] * 13 + [_i64, _i64, _i64, _int, _int, _int, _flt, _vp, _vp, _vp],
     "htrc_route": [_vp] * 11 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _flt, _vp, _vp, _vp, _vp, _vp],
     "htrc_selftest_mfma": [_vp] * 7,
 }

@@ -1434,33 +1434,62 @@ int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t head
     return launched("htrc_merge");
 }
 
-int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
-               const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
-               const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
-               int stride, float scale, float* out, float* logz, int32_t* idx, float* rowmax, void* stream) {
-    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && k8 && ks && v && out && logz && rowmax,
-            "htrc_route: null pointer");
-    REQUIRE(aligned(vb, 16) && aligned(v, 16) && aligned(g8, 16) && aligned(k8, 16) && aligned(sg, 16) &&
-                aligned(ks, 16) && aligned(lz, 16),
-            "htrc_route: misaligned buffer");
-    REQUIRE(d == D, "htrc_route: head dim must be 128");
-    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_route: leaf must be 16/32/64/128");
-    REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_route: bad sizes");
-    const int64_t nb = nk / leaf, nt = (nq + TILE - 1) / TILE;
-    REQUIRE(nb <= MAX_NB_LDS, "htrc_route: at most 8192 leaves per head");
-    REQUIRE(kx >= 0 && sink >= 0, "htrc_route: need kx >= 0 and sink >= 0");
-    const int kxe = (int)(kx < nb ? kx : nb);
-    REQUIRE(kxe <= MAX_KX_LDS, "htrc_route: at most 1024 near leaves per tile");
-    REQUIRE(kxe == 0 || idx, "htrc_route: idx is required when kx > 0");
-    REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_route: stride must divide 64");
-    REQUIRE(nt * heads <= 0x7fffffff, "htrc_route: too many tiles x heads for one launch");
-    const int nbp = htrc_nb_pad(nb);
-    dim3 grid((unsigned)(nt * heads));
-    hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(route_select_kernel, grid, dim3(256), (size_t)4 * nbp, s, dq8, sdq, g8, sg, lz, (int)nt,
-                       (int)nb, nbp, kxe, sink, stride, idx, rowmax);
-    int rc = launched("htrc_route");
+// Shape checks shared by the route entry points; sets nb, nt, kxe.
+static int route_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx,
+                        int64_t& nb, int64_t& nt, int& kxe) {
+    static thread_local char msg[160];
+    auto bad = [&](const char* what) {
+        snprintf(msg, sizeof msg, "%s: %s", who, what);
+        return fail(HTRC_ERR_ARG, msg);
+    };
+    if (d != D) return bad("head dim must be 128");
+    if (!(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128)) return bad("leaf must be 16/32/64/128");
+    if (!(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535)) return bad("bad sizes");
+    nb = nk / leaf;
+    nt = (nq + TILE - 1) / TILE;
+    if (nb > MAX_NB_LDS) return bad("at most 8192 leaves per head");
+    if (kx < 0) return bad("need kx >= 0");
+    kxe = (int)(kx < nb ? kx : nb);
+    if (kxe > MAX_KX_LDS) return bad("at most 1024 near leaves per tile");
+    if (nt * heads > 0x7fffffff) return bad("too many tiles x heads for one launch");
+    return HTRC_OK;
+}
+
+int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
+                      int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink, int stride,
+                      int32_t* idx, float* rowmax, void* stream) {
+    REQUIRE(dq8 && sdq && g8 && sg && lz && rowmax, "htrc_route_select: null pointer");
+    REQUIRE(aligned(g8, 16) && aligned(sg, 16) && aligned(lz, 16), "htrc_route_select: misaligned buffer");
+    int64_t nb, nt;
+    int kxe;
+    const int rc = route_shapes("htrc_route_select", heads, nq, nk, leaf, d, kx, nb, nt, kxe);
     if (rc != HTRC_OK) return rc;
+    REQUIRE(sink >= 0, "htrc_route_select: need sink >= 0");
+    REQUIRE(kxe == 0 || idx, "htrc_route_select: idx is required when kx > 0");
+    REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_route_select: stride must divide 64");
+    const int nbp = htrc_nb_pad(nb);
+    hipLaunchKernelGGL(route_select_kernel, dim3((unsigned)(nt * heads)), dim3(256), (size_t)4 * nbp,
+                       (hipStream_t)stream, dq8, sdq, g8, sg, lz, (int)nt, (int)nb, nbp, kxe, sink, stride, idx, rowmax);
+    return launched("htrc_route_select");
+}
+
+int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
+                      const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
+                      const uint16_t* v, const int32_t* idx, const float* rowmax, int64_t heads, int64_t nq,
+                      int64_t nk, int leaf, int d, int kx, float scale, float* out, float* logz, void* stream) {
+    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && k8 && ks && v && rowmax && out && logz,
+            "htrc_route_attend: null pointer");
+    REQUIRE(aligned(vb, 16) && aligned(v, 16) && aligned(g8, 16) && aligned(k8, 16) && aligned(sg, 16) &&
+                aligned(ks, 16) && aligned(lz, 16) && aligned(q8, 16) && aligned(dq8, 16),
+            "htrc_route_attend: misaligned buffer");
+    int64_t nb, nt;
+    int kxe;
+    const int rc = route_shapes("htrc_route_attend", heads, nq, nk, leaf, d, kx, nb, nt, kxe);
+    if (rc != HTRC_OK) return rc;
+    REQUIRE(kxe == 0 || idx, "htrc_route_attend: idx is required when kx > 0");
+    const int nbp = htrc_nb_pad(nb);
+    const dim3 grid((unsigned)(nt * heads));
+    hipStream_t s = (hipStream_t)stream;
 #define ROUTE_CASE(L)                                                                                          \
     case L:                                                                                                    \
         hipLaunchKernelGGL(route_kernel<L>, grid, dim3(512), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, \
@@ -1473,7 +1502,18 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
         ROUTE_CASE(128)
     }
 #undef ROUTE_CASE
-    return launched("htrc_route");
+    return launched("htrc_route_attend");
+}
+
+int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
+               const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
+               const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
+               int stride, float scale, float* out, float* logz, int32_t* idx, float* rowmax, void* stream) {
+    REQUIRE(q8 && sq && vb && k8 && ks && v && out && logz, "htrc_route: null pointer");
+    int rc = htrc_route_select(dq8, sdq, g8, sg, lz, heads, nq, nk, leaf, d, kx, sink, stride, idx, rowmax, stream);
+    if (rc != HTRC_OK) return rc;
+    return htrc_route_attend(q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, rowmax, heads, nq, nk, leaf, d, kx,
+                             scale, out, logz, stream);
 }
 
 int htrc_selftest_mfma(const int8_t* ai, const int8_t* bi, int32_t* ci, const uint16_t* af, const uint16_t* bf,

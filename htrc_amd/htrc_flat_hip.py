@@ -200,6 +200,42 @@ def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: floa
     return out, logz
 
 
+def route_select(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, sink: int = 0, stride: int = 1,
+                 ws=None, idx=None):
+    """First launch of route: select -> top-k per tile -> (idx [H,nt,min(kx,nb)] int32 or None,
+    rowmax [H,nt*64] fp32, each row's largest far-field score)."""
+    dq8, sdq = packed["dq8"], packed["sdq"]
+    g8, sg, lz = state["g8"], state["sg"], state["lz"]
+    h, nk = int(packed["k8"].shape[0]), int(packed["k8"].shape[1])
+    dev = dq8.device
+    nt = -(-int(nq) // TILE)
+    kxe = min(int(kx), nk // int(leaf))
+    if idx is None and kxe > 0:
+        idx = _buf(ws, "idx", (h, nt, kxe), torch.int32, dev)
+    rowmax = _buf(ws, "rowmax", (h, nt * TILE), torch.float32, dev)
+    call("htrc_route_select", ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), h, nq, nk, int(leaf), D, int(kx),
+         int(sink), int(stride), ptr(idx), ptr(rowmax), stream_handle(dev))
+    return idx, rowmax
+
+
+def route_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, kx: int, scale: float, ws=None,
+                 out=None, logz=None):
+    """Second launch of route: far + near field with the row reference rowmax -> (out, logz)."""
+    q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
+    k8, ks, v = packed["k8"], packed["ks"], packed["v"]
+    g8, sg, lz, vb = state["g8"], state["sg"], state["lz"], state["vb"]
+    h, nk, d = (int(x) for x in k8.shape)
+    dev = q8.device
+    if out is None:
+        out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
+    if logz is None:
+        logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
+    call("htrc_route_attend", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8),
+         ptr(ks), ptr(v), ptr(idx), ptr(rowmax), h, nq, nk, int(leaf), d, int(kx), float(scale), ptr(out), ptr(logz),
+         stream_handle(dev))
+    return out, logz
+
+
 def selftest_mfma(ai, bi, af, bf):
     """Run the MFMA convention self-test kernel -> (ci int32 [16,16], cf fp32 [16,16])."""
     dev = ai.device

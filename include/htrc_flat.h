@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 3
+#define HTRC_ABI_VERSION 4
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -82,10 +82,23 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
 int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int splits,
                int d, float* out, float* logz, void* stream);
 
-/* Fused production path, two launches: (1) select -> top-k per tile, SEL kept in LDS, writing
- * the routing idx [H, nt, min(kx, nb)] (ascending; required when kx > 0) and rowmax fp32
- * [H, nt*64], each row's largest far-field score; (2) far + near field of every tile in one
- * online softmax with that fixed reference, merged into normalised out / logz.
+/* Production path, first launch: select -> top-k per tile with SEL kept in LDS, writing the
+ * routing idx [H, nt, min(kx, nb)] (ascending; required when kx > 0) and rowmax fp32
+ * [H, nt*64], each row's largest far-field score (the tile's largest when stride > 1).
+ * Replaces rowmax_select + torch.topk of the chunk loop (h3/htrc_flat.py:258-265). */
+int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
+                      int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink, int stride,
+                      int32_t* idx, float* rowmax, void* stream);
+
+/* Production path, second launch: far + near field of every tile in one softmax whose
+ * reference is rowmax, merged into normalised out / logz (one split per tile).
+ * Replaces tile_attention + _merge_kernel of the chunk loop (h3/htrc_flat.py:266-271). */
+int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
+                      const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
+                      const uint16_t* v, const int32_t* idx, const float* rowmax, int64_t heads, int64_t nq,
+                      int64_t nk, int leaf, int d, int kx, float scale, float* out, float* logz, void* stream);
+
+/* Both launches of the production path: htrc_route_select then htrc_route_attend.
  * Replaces the chunk loop body of _flat_triton after leaf_stats (h3/htrc_flat.py:250-271). */
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,

@@ -205,6 +205,30 @@ def test_tile_merge_on_oracle_state(device, splits, bn):
     assert np.abs(_np(logz[0]) - ref["logz"]).max() <= LOGZ_ABS
 
 
+def test_route_two_launches_equal_fused(device):
+    """htrc_route_select + htrc_route_attend give exactly htrc_route; idx is the oracle's top-k
+    and rowmax each row's largest far-field score, the same fp32 products as SEL."""
+    n, leaf, ex = 4096, 64, 8
+    q, k, v = _data(n, seed=5)
+    ref = _oracle_state(q, k, v, leaf, ex, splits=1, bn=64)
+    packed, state, _, _ = _device_state(ref, q, k, v, device)
+    kx = ref["idx"].shape[1]
+    scale = 1 / math.sqrt(128)
+    out1, lz1 = hip.route(packed, state, nq=n, leaf=leaf, kx=kx, scale=scale)
+    out1, lz1 = out1.clone(), lz1.clone()
+    idx, rowmax = hip.route_select(packed, state, nq=n, leaf=leaf, kx=kx)
+    out2, lz2 = hip.route_attend(packed, state, idx, rowmax, nq=n, leaf=leaf, kx=kx, scale=scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2) and torch.equal(lz1, lz2)
+    assert np.array_equal(_np(idx[0]), ref["idx"])
+    nt, nb, d = ref["g8"].shape
+    dq = ref["dq8"].astype(np.int64).reshape(nt, 64, d)
+    acc = np.einsum("trd,tld->trl", dq, ref["g8"].astype(np.int64)).astype(np.float32)   # exact: |acc| < 2^24
+    c = (ref["sdq"].reshape(nt, 64)[:, :, None] * ref["sg"][:, None, :]).astype(np.float32)
+    want = ((acc * c).astype(np.float32) + ref["lz"][:, None, :]).astype(np.float32).max(axis=2)
+    assert np.array_equal(_np(rowmax[0]).reshape(nt, 64), want)
+
+
 @pytest.mark.parametrize("leaf,ex", [(64, 8), (32, 16), (16, 40), (128, 4), (64, 0), (64, 64)])
 def test_route_on_oracle_state(device, leaf, ex):
     n = 4096
