@@ -140,6 +140,19 @@ __device__ __forceinline__ void split3x8(const float* x, bf16x8& hi, bf16x8& mid
     lo = as_bf16x8(u32x4{l[0], l[1], l[2], l[3]});
 }
 
+// Two-term bf16 split of eight fp32 values: x = hi + lo to ~16 bits (|x - hi - lo| <= 2^-17 |x|).
+__device__ __forceinline__ void split2x8(const float* x, bf16x8& hi, bf16x8& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        h[j] = pack2bf(x[2 * j], x[2 * j + 1]);
+        l[j] = pack2bf(__fsub_rn(x[2 * j], __uint_as_float(h[j] << 16)),
+                       __fsub_rn(x[2 * j + 1], __uint_as_float(h[j] & 0xffff0000u)));
+    }
+    hi = as_bf16x8(u32x4{h[0], h[1], h[2], h[3]});
+    lo = as_bf16x8(u32x4{l[0], l[1], l[2], l[3]});
+}
+
 __device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }

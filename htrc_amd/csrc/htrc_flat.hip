@@ -164,18 +164,19 @@ __device__ __forceinline__ void settle(const i32x4 (&b)[4][2], const float (&s)[
 }
 
 // Stage leaf rows [key0, key0 + LEAF) of K and V: LDS chunk s = j*256 + tid holds the
-// 16-byte chunk (s % 16) ^ swz(row) of row (s / 16) % LEAF of K (first half) or V.
+// 16-byte chunk (s % 16) ^ swz(row) of row (s / 16) % LEAF of K (first half) or V.  Row
+// 16 jj + tid / 16 of chunk j keeps the swizzle of row tid / 16, so every chunk of a thread
+// uses one per-lane offset from a wave-uniform base (rows 16 jj).  lds0 = LDS address of buf.
 template <int LEAF>
 __device__ __forceinline__ void stage_leaf(const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-                                           int64_t key0, char* buf) {
-    constexpr int NC = 32 * LEAF;              // 16-byte chunks per leaf (K and V)
-    const int tid = threadIdx.x, w = tid >> 6;
+                                           int64_t key0, uint32_t lds0, uint32_t voff) {
+    constexpr int NJ = 32 * LEAF / 256;         // 16-byte chunks per thread (K and V)
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
-    for (int j = 0; j < NC / 256; ++j) {
-        const int c = j * 256 + tid;
-        const int row = (c >> 4) & (LEAF - 1), pc = c & 15;
-        const uint16_t* X = c < 16 * LEAF ? K : V;
-        dma16(X + (key0 + row) * D + 8 * (pc ^ swz(row)), lds_addr(buf + (size_t)(j * 256 + w * 64) * 16));
+    for (int j = 0; j < NJ; ++j) {
+        const int jj = j % (NJ / 2);
+        const uint16_t* X = j < NJ / 2 ? K : V;
+        dma16s(X + (key0 + 16 * jj) * D, voff, lds0 + (uint32_t)(j * 256 + w * 64) * 16);
     }
 }
 
@@ -198,7 +199,9 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
     constexpr int KB = LEAF / 16;                 // 16-key blocks per leaf
     constexpr int KK = (LEAF + 31) / 32;          // 32-key MFMA k-steps per leaf
     constexpr int LEAF_BYTES = 32 * LEAF * 16;
+    constexpr int LPB = 16;                       // leaves per workgroup (the launcher's lpb)
     __shared__ __align__(16) char lds[2 * LEAF_BYTES];
+    __shared__ __align__(16) float s_sg[64][LPB], s_lz[64][LPB];   // per tile, the workgroup's leaves
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     // 1-D grid over (tile group, leaf group, head), tile group fastest: the tile groups that
     // read the same leaves run together on one XCD and share its L2.
@@ -209,24 +212,26 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
     const int t = tg * 64 + w * 16 + col;           // tile centre of this lane's C column
     const bool tval = t < nt;
     const int64_t th = (int64_t)h * nt + (tval ? t : 0);
+    const uint32_t lds0 = lds_addr(lds);
+    const uint32_t voff = (uint32_t)((threadIdx.x >> 4) * 2 * D + 16 * ((threadIdx.x & 15) ^ swz(threadIdx.x >> 4)));
 
-    bf16x8 mh[4], mm[4], ml[4];
+    // mu in two bf16 terms (~16 bits; the reference's production path computes these dots in TF32)
+    bf16x8 mh[4], ml[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
         float x[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = tval ? mu[th * D + 32 * ks + 8 * grp + e] : 0.0f;
-        split3x8(x, mh[ks], mm[ks], ml[ks]);
+        split2x8(x, mh[ks], ml[ks]);
     }
 
     const int l0 = lg * lpb;
     const int l1 = min(nb_pad, l0 + lpb);
     const int lr = min(nb, l1);                   // real leaves of this workgroup: [l0, lr)
     const int64_t kh = (int64_t)h * nk;
-    // outputs of the previous leaf, stored during the next one
+    // g8 / vb of the previous leaf, stored during the next one
     uint32_t pg[8];
     u32x2 pv[8];
-    float psg = 0.0f, plz = 0.0f;
     int pl = -1;
     auto flush = [&]() {
         if (pl >= 0 && tval) {
@@ -236,19 +241,18 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
                 *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = pg[db];
                 *(u32x2*)(vb + s * D + 16 * db + 4 * grp) = pv[db];
             }
-            if (grp == 0) {
-                sg[s] = psg;
-                lz[s] = plz;
-            }
         }
         pl = -1;
     };
-    if (l0 < lr) stage_leaf<LEAF>(k, v, kh + (int64_t)l0 * LEAF, lds);
+    if (l0 < lr) stage_leaf<LEAF>(k, v, kh + (int64_t)l0 * LEAF, lds0, voff);
     for (int l = l0; l < lr; ++l) {
-        wait_vmcnt<0>();                       // leaf l landed; stores of leaf l - 2 done
+        // Leaf l landed and the stores of leaf l - 2 are done (measured: letting those stores
+        // stay in flight past this wait, behind the next loads, is slower).
+        wait_vmcnt<0>();
         __syncthreads();                       // ... for every wave; buffer of leaf l - 1 free
         flush();                               // stores of leaf l - 1
-        if (l + 1 < lr) stage_leaf<LEAF>(k, v, kh + (int64_t)(l + 1) * LEAF, lds + ((l + 1 - l0) & 1) * LEAF_BYTES);
+        if (l + 1 < lr)
+            stage_leaf<LEAF>(k, v, kh + (int64_t)(l + 1) * LEAF, lds0 + ((l + 1 - l0) & 1) * LEAF_BYTES, voff);
         const char* Kr = lds + ((l - l0) & 1) * LEAF_BYTES;
         const char* Vr = Kr + 16 * LEAF * 16;
         f32x4 a[KB];
@@ -260,7 +264,6 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
             for (int ks = 0; ks < 4; ++ks) {
                 const bf16x8 A = as_bf16x8(*(const u32x4*)(Kr + (row * 16 + ((4 * ks + grp) ^ swz(row))) * 16));
                 a[kb] = mfma_bf16(A, mh[ks], a[kb]);
-                a[kb] = mfma_bf16(A, mm[ks], a[kb]);
                 a[kb] = mfma_bf16(A, ml[ks], a[kb]);
             }
         }
@@ -284,23 +287,20 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
             }
         z = grp_sum(z);
         const float rz = __fdiv_rn(1.0f, z);
-        const float cg = __fmul_rn(scale, rz);
+        // w = e / z in two bf16 terms, shared by both products: gacc = w K (g = scale gacc), vb = w V
         f32x4 gacc[8], vacc[8];
 #pragma unroll
         for (int db = 0; db < 8; ++db) gacc[db] = vacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-            float wg[8], wv[8];
+            float wv[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int kb = 2 * kk + (e >> 2);
-                const float x = kb < KB ? a[kb < KB ? kb : 0][e & 3] : 0.0f;
-                wg[e] = __fmul_rn(x, cg);
-                wv[e] = __fmul_rn(x, rz);
+                wv[e] = kb < KB ? __fmul_rn(a[kb < KB ? kb : 0][e & 3], rz) : 0.0f;
             }
-            bf16x8 G0, G1, G2, V0, V1, V2;
-            split3x8(wg, G0, G1, G2);
-            split3x8(wv, V0, V1, V2);
+            bf16x8 W0, W1;
+            split2x8(wv, W0, W1);
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
                 const u32x2 zero = {0u, 0u};
@@ -309,30 +309,32 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
                 const u32x2 v0 = tr_operand(Vr, 32 * kk, db, lane);
                 const u32x2 v1 = (2 * kk + 1 < KB) ? tr_operand(Vr, 32 * kk + 16, db, lane) : zero;
                 const bf16x8 KA = as_bf16x8(k0, k1), VA = as_bf16x8(v0, v1);
-                gacc[db] = mfma_bf16(KA, G0, gacc[db]);
-                gacc[db] = mfma_bf16(KA, G1, gacc[db]);
-                gacc[db] = mfma_bf16(KA, G2, gacc[db]);
-                vacc[db] = mfma_bf16(VA, V0, vacc[db]);
-                vacc[db] = mfma_bf16(VA, V1, vacc[db]);
+                gacc[db] = mfma_bf16(KA, W0, gacc[db]);
+                gacc[db] = mfma_bf16(KA, W1, gacc[db]);
+                vacc[db] = mfma_bf16(VA, W0, vacc[db]);
+                vacc[db] = mfma_bf16(VA, W1, vacc[db]);
             }
         }
-        // g^T, vb^T: lane holds dims 16db + 4grp + i of centre t
+        // g^T = scale gacc^T, vb^T: lane holds dims 16db + 4grp + i of centre t.  The int8 code
+        // of g is round(127 g / max|g|) = round(gacc * 127 scale / max|g|).
         float am = 0.0f;
 #pragma unroll
         for (int db = 0; db < 8; ++db)
 #pragma unroll
             for (int i = 0; i < 4; ++i) am = fmaxf(am, fabsf(gacc[db][i]));
-        am = grp_max(am);
+        am = __fmul_rn(grp_max(am), scale);             // max |g|
         am = am < 1e-30f ? 1e-30f : am;
-        const float cq = __fdiv_rn(127.0f, am);
+        const float cq = __fdiv_rn(__fmul_rn(127.0f, scale), am);
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
             pg[db] = pack4_i8(round_away(__fmul_rn(gacc[db][0], cq)), round_away(__fmul_rn(gacc[db][1], cq)),
                               round_away(__fmul_rn(gacc[db][2], cq)), round_away(__fmul_rn(gacc[db][3], cq)));
             pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
         }
-        psg = __fmul_rn(am, R127);
-        plz = __fadd_rn(mx, __logf(z));
+        if (grp == 0) {
+            s_sg[w * 16 + col][l - l0] = __fmul_rn(am, R127);
+            s_lz[w * 16 + col][l - l0] = __fadd_rn(mx, __logf(z));
+        }
         pl = l;
     }
     flush();
@@ -346,9 +348,19 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
                 *(u32x2*)(vb + s * D + 16 * db + 4 * grp) = u32x2{0u, 0u};
             }
             if (grp == 0) {
-                sg[s] = 0.0f;
-                lz[s] = -INFINITY;
+                s_sg[w * 16 + col][l - l0] = 0.0f;
+                s_lz[w * 16 + col][l - l0] = -INFINITY;
             }
+        }
+    }
+    __syncthreads();
+    {   // sg, lz of the workgroup's leaves: 64 contiguous bytes per tile
+        const int tt = threadIdx.x >> 2, qq = threadIdx.x & 3;
+        const int tq = tg * 64 + tt;
+        if (tq < nt && 4 * qq < l1 - l0) {
+            const int64_t s = ((int64_t)h * nt + tq) * nb_pad + l0 + 4 * qq;
+            *(f32x4*)(sg + s) = *(const f32x4*)&s_sg[tt][4 * qq];
+            *(f32x4*)(lz + s) = *(const f32x4*)&s_lz[tt][4 * qq];
         }
     }
 }
@@ -1339,7 +1351,7 @@ int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64
             "htrc_leaf_stats: misaligned buffer");
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
-    const int lpb = 16;
+    const int lpb = 16;                    // stats_kernel's LPB
     const int64_t nblocks = (nt + 63) / 64 * ((nbp + lpb - 1) / lpb) * heads;
     REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats: too many tiles x leaves x heads for one launch");
     dim3 grid((unsigned)nblocks);
