@@ -87,6 +87,34 @@ __device__ __forceinline__ float grp_sum(float v) {
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __fadd_rn(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
+// a in lanes 32..63 <-> b in lanes 0..31 (v_permlane32_swap), and a in the odd 16-lane rows
+// <-> b in the even rows (v_permlane16_swap).
+__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
+__device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
+
+// 4 x 4 block transpose across the four 16-lane rows: row g holds blocks B_g[c] = (x[2c],
+// x[2c+1]) (c = 0..3); afterwards row g holds B_c[g] in (x[2c], x[2c+1]).  When x[j] of row g
+// is the dword of dims 16j + 4g.. of an MFMA C column, row g ends with dims 32g + 4c in x[2c]
+// and 32g + 16 + 4c in x[2c + 1].
+__device__ __forceinline__ void rows_transpose(uint32_t (&x)[8]) {
+    swap32(x[0], x[4]);
+    swap32(x[1], x[5]);
+    swap32(x[2], x[6]);
+    swap32(x[3], x[7]);
+    swap16(x[0], x[2]);
+    swap16(x[1], x[3]);
+    swap16(x[4], x[6]);
+    swap16(x[5], x[7]);
+}
+
 // Max across the 16 lanes of one group (the columns of an MFMA C tile) with DPP: xor 1,
 // xor 2 (quad permutes), then half-row and row mirrors; every lane ends with the maximum.
 template <int CTRL>

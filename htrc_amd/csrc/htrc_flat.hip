@@ -28,28 +28,40 @@ using namespace htrc;
 // ---------------------------------------------------------------------------------------------
 // pack_q: one workgroup per (tile, head).  Tile centre = sequential fp32 sum over the real
 // rows / row count (h3/htrc_flat.py:142-156); then per padded row the int8 of q and of
-// q - mu with per-row scales (h3/htrc_flat_triton.py:104-117).
+// q - mu with per-row scales (h3/htrc_flat_triton.py:104-117).  Each 16-lane group of a wave
+// quantises one row (8 values per lane, row max by DPP), 16-byte loads and 8-byte stores.
 // ---------------------------------------------------------------------------------------------
+// Eight int8 codes, as int32 in [-128, 127], packed little-endian.
+__device__ __forceinline__ u32x2 pack8_i8(const int (&c)[8]) {
+    return u32x2{pack4_i8(c[0], c[1], c[2], c[3]), pack4_i8(c[4], c[5], c[6], c[7])};
+}
+
 template <bool IN_BF16>
 __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qin, int64_t nq, int nt,
                                                      float* __restrict__ mu, int8_t* __restrict__ q8,
                                                      float* __restrict__ sq, int8_t* __restrict__ dq8,
                                                      float* __restrict__ sdq) {
-    __shared__ float tq[TILE][D + 1];
-    __shared__ float smu[D];
+    __shared__ __align__(16) float tq[TILE][D + 4];
+    __shared__ __align__(16) float smu[D];
     const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const int64_t r0 = (int64_t)t * TILE;
     const int nr = (int)(nq - r0 < TILE ? nq - r0 : TILE);
     const int64_t qbase = (int64_t)h * nq * D;
-    for (int e = tid; e < TILE * D; e += 256) {
-        const int r = e >> 7, c = e & (D - 1);
-        const int64_t src = r0 + r < nq ? r0 + r : nq - 1;   // pad rows repeat the last row
-        float x;
-        if (IN_BF16)
-            x = bf2f(((const uint16_t*)qin)[qbase + src * D + c]);
-        else
-            x = ((const float*)qin)[qbase + src * D + c];
-        tq[r][c] = x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {               // 8 consecutive values per thread and chunk
+        const int c = tid + 256 * j, r = c >> 4, c8 = (c & 15) * 8;
+        const int64_t src = qbase + (r0 + r < nq ? r0 + r : nq - 1) * D + c8;   // pad rows repeat the last row
+        f32x4 lo, hi;
+        if (IN_BF16) {
+            const u32x4 u = *(const u32x4*)((const uint16_t*)qin + src);
+            lo = f32x4{bf2f(u.x & 0xffffu), bf2f(u.x >> 16), bf2f(u.y & 0xffffu), bf2f(u.y >> 16)};
+            hi = f32x4{bf2f(u.z & 0xffffu), bf2f(u.z >> 16), bf2f(u.w & 0xffffu), bf2f(u.w >> 16)};
+        } else {
+            lo = *(const f32x4*)((const float*)qin + src);
+            hi = *(const f32x4*)((const float*)qin + src + 4);
+        }
+        *(f32x4*)&tq[r][c8] = lo;
+        *(f32x4*)&tq[r][c8 + 4] = hi;
     }
     __syncthreads();
     const int64_t tg = (int64_t)h * nt + t;
@@ -61,23 +73,32 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
         mu[tg * D + tid] = m;
     }
     __syncthreads();
-    const int w = tid >> 6, lane = tid & 63;
-    const float m0 = smu[2 * lane], m1 = smu[2 * lane + 1];
-    for (int rr = 0; rr < 16; ++rr) {
-        const int r = w * 16 + rr;
-        const float x0 = tq[r][2 * lane], x1 = tq[r][2 * lane + 1];
-        const float d0 = __fsub_rn(x0, m0), d1 = __fsub_rn(x1, m1);
-        const float aq = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-        const float ad = wave_max(fmaxf(fabsf(d0), fabsf(d1)));
-        const float s1 = row_scale(aq, 1e-20f), s2 = row_scale(ad, 1e-20f);
+    const int w = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
+    float m[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m[e] = smu[8 * i + e];
+#pragma unroll 1
+    for (int it = 0; it < 4; ++it) {
+        const int r = 16 * w + 4 * it + g;         // row of this 16-lane group
+        float x[8], d[8], aq = 0.0f, ad = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            x[e] = tq[r][8 * i + e];
+            d[e] = __fsub_rn(x[e], m[e]);
+            aq = fmaxf(aq, fabsf(x[e]));
+            ad = fmaxf(ad, fabsf(d[e]));
+        }
+        const float s1 = row_scale(col_max(aq), 1e-20f), s2 = row_scale(col_max(ad), 1e-20f);
+        int cq[8], cd[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            cq[e] = round_away(__fdiv_rn(x[e], s1));
+            cd[e] = round_away(__fdiv_rn(d[e], s2));
+        }
         const int64_t p = tg * TILE + r;
-        const uint16_t qq = (uint16_t)((round_away(__fdiv_rn(x0, s1)) & 0xff) |
-                                       ((round_away(__fdiv_rn(x1, s1)) & 0xff) << 8));
-        const uint16_t dd = (uint16_t)((round_away(__fdiv_rn(d0, s2)) & 0xff) |
-                                       ((round_away(__fdiv_rn(d1, s2)) & 0xff) << 8));
-        ((uint16_t*)(q8 + p * D))[lane] = qq;
-        ((uint16_t*)(dq8 + p * D))[lane] = dd;
-        if (lane == 0) {
+        *(u32x2*)(q8 + p * D + 8 * i) = pack8_i8(cq);
+        *(u32x2*)(dq8 + p * D + 8 * i) = pack8_i8(cd);
+        if (i == 0) {
             sq[p] = s1;
             sdq[p] = s2;
         }
@@ -85,24 +106,30 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
 }
 
 // ---------------------------------------------------------------------------------------------
-// pack_k: one workgroup per 64 key rows of a head.  k8/ks per row (h3/htrc_flat.py:216-218,
-// round half to even).
+// pack_k: one workgroup per 64 key rows of a head; each 16-lane group quantises one row
+// (8 values per lane, row max by DPP).  k8/ks per row (h3/htrc_flat.py:216-218, round half
+// to even).
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void pack_k_kernel(const uint16_t* __restrict__ k, int64_t nk,
                                                      int8_t* __restrict__ k8, float* __restrict__ ks) {
-    const int h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int64_t r0 = (int64_t)blockIdx.x * 64;
+    const int h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
     const int64_t base = (int64_t)h * nk;
-    for (int rr = 0; rr < 16; ++rr) {
-        const int64_t r = r0 + w * 16 + rr;
-        if (r >= nk) break;
-        const uint32_t pr = ((const uint32_t*)(k + (base + r) * D))[lane];
-        const float x0 = bf2f(pr & 0xffffu), x1 = bf2f(pr >> 16);
-        const float sc = row_scale(wave_max(fmaxf(fabsf(x0), fabsf(x1))), 1e-20f);
-        const uint16_t o = (uint16_t)((round_even_clamp(__fdiv_rn(x0, sc)) & 0xff) |
-                                      ((round_even_clamp(__fdiv_rn(x1, sc)) & 0xff) << 8));
-        ((uint16_t*)(k8 + (base + r) * D))[lane] = o;
-        if (lane == 0) ks[base + r] = sc;
+#pragma unroll 1
+    for (int it = 0; it < 4; ++it) {
+        const int64_t r = (int64_t)blockIdx.x * 64 + 16 * w + 4 * it + g;
+        if (r >= nk) break;                       // nk % 16 == 0: whole 16-lane groups leave together
+        const u32x4 u = *(const u32x4*)(k + (base + r) * D + 8 * i);
+        const float x[8] = {bf2f(u.x & 0xffffu), bf2f(u.x >> 16), bf2f(u.y & 0xffffu), bf2f(u.y >> 16),
+                            bf2f(u.z & 0xffffu), bf2f(u.z >> 16), bf2f(u.w & 0xffffu), bf2f(u.w >> 16)};
+        float a = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(x[e]));
+        const float sc = row_scale(col_max(a), 1e-20f);
+        int c[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) c[e] = round_even_clamp(__fdiv_rn(x[e], sc));
+        *(u32x2*)(k8 + (base + r) * D + 8 * i) = pack8_i8(c);
+        if (i == 0) ks[base + r] = sc;
     }
 }
 
@@ -233,13 +260,29 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
     uint32_t pg[8];
     u32x2 pv[8];
     int pl = -1;
+    // The MFMA C layout leaves lane (col, grp) with dims 16db + 4grp.. of centre col; a block
+    // transpose across the four lanes of the column gives each lane the 32 contiguous dims
+    // 32grp.., so each row goes out in 16-byte stores (g8: 2, vb: 4).
     auto flush = [&]() {
-        if (pl >= 0 && tval) {
-            const int64_t s = th * nb_pad + pl;
+        if (pl >= 0) {
+            uint32_t vlo[8], vhi[8];
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
-                *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = pg[db];
-                *(u32x2*)(vb + s * D + 16 * db + 4 * grp) = pv[db];
+                vlo[db] = pv[db].x;
+                vhi[db] = pv[db].y;
+            }
+            rows_transpose(pg);
+            rows_transpose(vlo);
+            rows_transpose(vhi);
+            if (tval) {
+                const int64_t s = th * nb_pad + pl;
+                *(u32x4*)(g8 + s * D + 32 * grp) = u32x4{pg[0], pg[2], pg[4], pg[6]};
+                *(u32x4*)(g8 + s * D + 32 * grp + 16) = u32x4{pg[1], pg[3], pg[5], pg[7]};
+                uint16_t* vr = vb + s * D + 32 * grp;        // dims 32grp + 4c: (vlo, vhi)[2c]
+                *(u32x4*)(vr) = u32x4{vlo[0], vhi[0], vlo[2], vhi[2]};
+                *(u32x4*)(vr + 8) = u32x4{vlo[4], vhi[4], vlo[6], vhi[6]};
+                *(u32x4*)(vr + 16) = u32x4{vlo[1], vhi[1], vlo[3], vhi[3]};
+                *(u32x4*)(vr + 24) = u32x4{vlo[5], vhi[5], vlo[7], vhi[7]};
             }
         }
         pl = -1;
@@ -1317,7 +1360,7 @@ int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, 
     REQUIRE(q && mu && q8 && sq && dq8 && sdq, "htrc_pack_q: null pointer");
     REQUIRE(d == D, "htrc_pack_q: head dim must be 128");
     REQUIRE(heads > 0 && heads <= 65535 && nq > 0, "htrc_pack_q: bad heads / rows");
-    REQUIRE(aligned(q8, 16) && aligned(dq8, 16), "htrc_pack_q: int8 outputs must be 16-byte aligned");
+    REQUIRE(aligned(q, 16) && aligned(q8, 16) && aligned(dq8, 16), "htrc_pack_q: q and the int8 outputs must be 16-byte aligned");
     const int64_t nt = (nq + TILE - 1) / TILE;
     REQUIRE(nt <= 0x7fffffff, "htrc_pack_q: too many tiles");
     dim3 grid((unsigned)nt, (unsigned)heads);
@@ -1334,7 +1377,7 @@ int htrc_pack_k(const uint16_t* k, int64_t heads, int64_t nk, int d, int8_t* k8,
     REQUIRE(k && k8 && ks, "htrc_pack_k: null pointer");
     REQUIRE(d == D, "htrc_pack_k: head dim must be 128");
     REQUIRE(heads > 0 && heads <= 65535 && nk > 0 && nk % 16 == 0, "htrc_pack_k: keys must be a positive multiple of 16");
-    REQUIRE(aligned(k, 4) && aligned(k8, 4), "htrc_pack_k: misaligned buffer");
+    REQUIRE(aligned(k, 16) && aligned(k8, 16), "htrc_pack_k: k and k8 must be 16-byte aligned");
     dim3 grid((unsigned)((nk + 63) / 64), (unsigned)heads);
     hipLaunchKernelGGL(pack_k_kernel, grid, dim3(256), 0, (hipStream_t)stream, k, nk, k8, ks);
     return launched("htrc_pack_k");
