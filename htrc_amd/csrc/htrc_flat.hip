@@ -173,6 +173,33 @@ __device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t
                  : : "v"(voff), "s"(bs), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 
+// Wave-uniform 64-bit address p - shift in an SGPR pair.
+__device__ __forceinline__ uint64_t sbase(const void* p, uint32_t shift = 0) {
+    const uint64_t b = (uint64_t)(uintptr_t)p - shift;
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+           (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+}
+
+// Direct global->LDS loads sharing one M0 (= LDS address lds): load i writes LDS lds + 1024 i
+// (+ lane * 16) from b_i + v_i + 1024 i.  The instruction offset moves the global and the LDS
+// address alike (checked on gfx950), so callers pass base i already lowered by 1024 i.
+__device__ __forceinline__ void dma_x2(uint64_t b0, uint32_t v0, uint64_t b1, uint32_t v1, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %4\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %0, %2\n\t"
+                 "global_load_lds_dwordx4 %1, %3 offset:1024"
+                 : : "v"(v0), "v"(v1), "s"(b0), "s"(b1), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_x4(uint64_t b0, uint32_t v0, uint64_t b1, uint32_t v1, uint64_t b2, uint32_t v2,
+                                       uint64_t b3, uint32_t v3, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %8\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %0, %4\n\t"
+                 "global_load_lds_dwordx4 %1, %5 offset:1024\n\t"
+                 "global_load_lds_dwordx4 %2, %6 offset:2048\n\t"
+                 "global_load_lds_dwordx4 %3, %7 offset:3072"
+                 : : "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(b0), "s"(b1), "s"(b2), "s"(b3),
+                   "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+
 // s_waitcnt vmcnt(N): at most N vector-memory operations of this wave still in flight (they
 // complete in issue order).  The memory clobber keeps the compiler from moving LDS reads of a
 // DMA'd slot above the wait.
@@ -917,22 +944,24 @@ __device__ __forceinline__ BlockOffsets block_offsets(int lane) {
     return o;
 }
 
-// QK operand chunk j (0..3) of lane: [hh = j>>1][ks = j&1][grp][col] <- row (row0[hh] + col),
-// bytes (4ks + grp)*16 of an int8 [*, 128] matrix; x0/x1 point at rows row0a/row0b.
+// QK operand chunks j (0..3) of lane: [hh = j>>1][ks = j&1][grp][col] <- row (row0[hh] + col),
+// bytes (4ks + grp)*16 of an int8 [*, 128] matrix; x0/x1 point at rows row0a/row0b.  One M0.
 __device__ __forceinline__ void dma_qk(const int8_t* x0, const int8_t* x1, const BlockOffsets& bo, uint32_t slot) {
-    dma16s(x0, bo.qk[0], slot);
-    dma16s(x0, bo.qk[1], slot + 1024);
-    dma16s(x1, bo.qk[0], slot + 2048);
-    dma16s(x1, bo.qk[1], slot + 3072);
+    dma_x4(sbase(x0), bo.qk[0], sbase(x0, 1024), bo.qk[1], sbase(x1, 2048), bo.qk[0], sbase(x1, 3072), bo.qk[1], slot);
 }
 
-// PV rows of a 32-key block, chunks j in [J0, J1): ring chunk s = 64j + lane holds the 16-byte
-// chunk (s % 16) ^ swz(row) of row s / 16 (rows 0..15 from x0, 16..31 from x1) of a bf16
-// [*, 128] matrix.  swz(row) = swz(row - 16), so both halves share the lane offsets.
-template <int J0, int J1>
-__device__ __forceinline__ void dma_rows(const uint16_t* x0, const uint16_t* x1, const BlockOffsets& bo, uint32_t slot) {
-#pragma unroll
-    for (int j = J0; j < J1; ++j) dma16s(j < 4 ? x0 : x1, bo.rows[j & 3], slot + 4096 + j * 1024);
+// PV rows of a 32-key block: ring chunk s = 64j + lane (j = 0..7) holds the 16-byte chunk
+// (s % 16) ^ swz(row) of row s / 16 (rows 0..15 from x0, 16..31 from x1) of a bf16 [*, 128]
+// matrix; swz(row) = swz(row - 16), so both halves share the lane offsets.  Chunks 0, 1:
+__device__ __forceinline__ void dma_rows01(const uint16_t* x0, const BlockOffsets& bo, uint32_t slot) {
+    dma_x2(sbase(x0), bo.rows[0], sbase(x0, 1024), bo.rows[1], slot + 4096);
+}
+// chunks 2..7:
+__device__ __forceinline__ void dma_rows27(const uint16_t* x0, const uint16_t* x1, const BlockOffsets& bo,
+                                           uint32_t slot) {
+    dma_x2(sbase(x0), bo.rows[2], sbase(x0, 1024), bo.rows[3], slot + 4096 + 2048);
+    dma_x4(sbase(x1), bo.rows[0], sbase(x1, 1024), bo.rows[1], sbase(x1, 2048), bo.rows[2], sbase(x1, 3072),
+           bo.rows[3], slot + 8192);
 }
 
 // route_select: first launch of the fused production path, one workgroup (4 waves) per tile.
@@ -1092,10 +1121,10 @@ __global__ __launch_bounds__(512) void route_kernel(
                           const float* s_lo, const float* s_hi, int nlim) {
         if (hr == 0) {
             dma_qk(X8 + r0 * D, X8 + r1 * D, bo, slot);
-            dma_rows<0, 2>(XV + r0 * D, XV + r1 * D, bo, slot);
+            dma_rows01(XV + r0 * D, bo, slot);
             if (lane < 16) dma16((lane < 8 ? s_lo : s_hi) + 4 * (lane & nlim), slot + 12288);
         } else {
-            dma_rows<2, 8>(XV + r0 * D, XV + r1 * D, bo, slot);
+            dma_rows27(XV + r0 * D, XV + r1 * D, bo, slot);
         }
     };
     Rows2 st;
@@ -1121,20 +1150,20 @@ __global__ __launch_bounds__(512) void route_kernel(
                 asm volatile("" : : "v"(bq[rb][0]), "v"(bq[rb][1]), "v"(srow[rb]), "v"(mref[rb]));
             }
             __syncthreads();            // exbits complete; the ring is free (merge / earlier pass)
-            auto issue = [&](int bi) {
+            auto issue = [&](int bi, int slot) {
                 if (bi >= nf) return;
                 const int64_t r0 = srow0 + lo + 32 * bi;
-                load_block(pring_lds + (bi % RING_SLOTS) * SLOT_BYTES, g8, vb, r0, r0 + 16, sg + r0, lz + r0, 7);
+                load_block(pring_lds + slot * SLOT_BYTES, g8, vb, r0, r0 + 16, sg + r0, lz + r0, 7);
             };
-            issue(0);
-            issue(1);
-#pragma unroll 1
-            for (int bi = 0; bi < sf_steps; ++bi) {
+            // one step per 32-leaf block; the ring slot of block bi is bi % 3, a constant in each
+            // of the three unrolled steps, so every LDS read uses an immediate offset
+            auto step = [&](auto S_, int bi) {
+                constexpr int S = decltype(S_)::value;
                 if (bi < nf) wait_block(bi, nf);
                 __syncthreads();        // the partner's loads have landed too; slot (bi + 2) % 3 is free
-                issue(bi + 2);
-                if (bi >= nf) continue;
-                const char* slot = pring + (bi % RING_SLOTS) * SLOT_BYTES;
+                issue(bi + 2, (S + 2) % RING_SLOTS);
+                if (bi >= nf) return;
+                const char* slot = pring + S * SLOT_BYTES;
                 const int c0 = lo + 32 * bi;
                 const uint32_t exw = exbits[c0 >> 5];
                 float sc[2][8];
@@ -1166,6 +1195,14 @@ __global__ __launch_bounds__(512) void route_kernel(
 #pragma unroll
                     for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
                 rows2_update(st, sc, pvop);
+            };
+            issue(0, 0);
+            issue(1, 1);
+#pragma unroll 1
+            for (int bi = 0; bi < sf_steps; bi += RING_SLOTS) {
+                step(std::integral_constant<int, 0>{}, bi);
+                if (bi + 1 < sf_steps) step(std::integral_constant<int, 1>{}, bi + 1);
+                if (bi + 2 < sf_steps) step(std::integral_constant<int, 2>{}, bi + 2);
             }
         }
         {   // ---- near field: S^T = k8 q8^T, score = dot * sq * ks * scale
@@ -1184,21 +1221,19 @@ __global__ __launch_bounds__(512) void route_kernel(
                 const int jj = j < e_hi ? j : e_lo;
                 return kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[jj / LEAF]) * LEAF + (jj % LEAF);
             };
-            auto issue = [&](int bi) {
+            auto issue = [&](int bi, int slot) {
                 if (bi >= nn) return;
                 const int e0 = e_lo + 32 * bi;
                 const int64_t r0 = tok_of(e0), r1 = tok_of(e0 + 16);
-                load_block(pring_lds + (bi % RING_SLOTS) * SLOT_BYTES, k8, v, r0, r1, ks + r0, ks + r1, 3);
+                load_block(pring_lds + slot * SLOT_BYTES, k8, v, r0, r1, ks + r0, ks + r1, 3);
             };
-            issue(0);
-            issue(1);
-#pragma unroll 1
-            for (int bi = 0; bi < sn_steps; ++bi) {
+            auto step = [&](auto S_, int bi) {
+                constexpr int S = decltype(S_)::value;
                 if (bi < nn) wait_block(bi, nn);
                 __syncthreads();
-                issue(bi + 2);
-                if (bi >= nn) continue;
-                const char* slot = pring + (bi % RING_SLOTS) * SLOT_BYTES;
+                issue(bi + 2, (S + 2) % RING_SLOTS);
+                if (bi >= nn) return;
+                const char* slot = pring + S * SLOT_BYTES;
                 const int e0 = e_lo + 32 * bi;
                 float sc[2][8];
 #pragma unroll
@@ -1228,6 +1263,14 @@ __global__ __launch_bounds__(512) void route_kernel(
 #pragma unroll
                     for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
                 rows2_update(st, sc, pvop);
+            };
+            issue(0, 0);
+            issue(1, 1);
+#pragma unroll 1
+            for (int bi = 0; bi < sn_steps; bi += RING_SLOTS) {
+                step(std::integral_constant<int, 0>{}, bi);
+                if (bi + 1 < sn_steps) step(std::integral_constant<int, 1>{}, bi + 1);
+                if (bi + 2 < sn_steps) step(std::integral_constant<int, 2>{}, bi + 2);
             }
         }
         // Row totals over the four key quarters (all at the same reference).  A total outside
