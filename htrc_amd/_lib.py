@@ -13,7 +13,7 @@ import torch
 
 HERE = Path(__file__).resolve().parent
 LIBPATH = HERE / "libhtrc_flat.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -35,6 +35,7 @@ SIGNATURES = {
     "htrc_route_select": [_vp] * 5 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _vp, _vp, _vp],
     "htrc_route_attend": [_vp] * 13 + [_i64, _i64, _i64, _int, _int, _int, _flt, _vp, _vp, _vp],
     "htrc_route": [_vp] * 11 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _flt, _vp, _vp, _vp, _vp, _vp],
+    "htrc_tail": [_vp, _int, _vp, _vp, _i64, _i64, _i64, _int, _flt, _vp, _vp, _vp],
     "htrc_selftest_mfma": [_vp] * 7,
 }
 _RESTYPES = {"htrc_last_error": ctypes.c_char_p}

@@ -1335,6 +1335,66 @@ __global__ __launch_bounds__(512) void route_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------
+// tail: keys past the last full leaf, attended exactly by every query, merged into a finished
+// (out, logz).  The reference folds up to 16 such keys into the last split of its tile kernel
+// with q, k, v and p rounded to bf16 (h3/htrc_flat_triton.py:187-207) and takes a host-side fp32
+// partial for more (:381-388); both end as one softmax over far, near and tail, which is what
+// the log-sum-exp merge here computes.  Four lanes per query row (32 dims each).
+// ---------------------------------------------------------------------------------------------
+template <bool IN_BF16>
+__global__ __launch_bounds__(256) void tail_kernel(const void* __restrict__ q, const float* __restrict__ tk,
+                                                   const float* __restrict__ tv, int64_t nq, int ntail,
+                                                   float scale, float* __restrict__ out, float* __restrict__ logz) {
+    const int t = blockIdx.x, h = blockIdx.y, r = threadIdx.x >> 2, qd = threadIdx.x & 3;
+    const int64_t qi = (int64_t)t * TILE + r;
+    if (qi >= nq) return;                         // whole 4-lane groups leave together
+    const bool bfr = ntail <= 16;                 // the in-kernel path of the reference works in bf16
+    const int64_t row = (int64_t)h * nq + qi;
+    float qv[32];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+        const float x = IN_BF16 ? bf2f(((const uint16_t*)q)[row * D + 32 * qd + e]) : ((const float*)q)[row * D + 32 * qd + e];
+        qv[e] = bfr ? bf16_round(x) : x;
+    }
+    auto score = [&](int j) {                     // (q . k_j) * scale, the row's four lanes together
+        const float* kj = tk + ((int64_t)h * ntail + j) * D + 32 * qd;
+        float sdot = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) sdot = fmaf(qv[e], bfr ? bf16_round(kj[e]) : kj[e], sdot);
+        sdot = __fadd_rn(sdot, __shfl_xor(sdot, 1, 4));
+        sdot = __fadd_rn(sdot, __shfl_xor(sdot, 2, 4));
+        return __fmul_rn(sdot, scale);
+    };
+    // two passes: p = exp(s - max over the tail), so its bf16 rounding does not depend on key order
+    float m = -INFINITY;
+    for (int j = 0; j < ntail; ++j) m = fmaxf(m, score(j));
+    float l = 0.0f, acc[32];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) acc[e] = 0.0f;
+    for (int j = 0; j < ntail; ++j) {
+        const float* vj = tv + ((int64_t)h * ntail + j) * D + 32 * qd;
+        const float p = expf(__fsub_rn(score(j), m));
+        l = __fadd_rn(l, p);
+        const float pv = bfr ? bf16_round(p) : p;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) acc[e] = fmaf(pv, bfr ? bf16_round(vj[e]) : vj[e], acc[e]);
+    }
+    const float lse = __fadd_rn(m, logf(l));
+    const float lz0 = logz[row];
+    const float mx = fmaxf(lz0, lse);
+    const float nz = __fadd_rn(mx, logf(__fadd_rn(expf(__fsub_rn(lz0, mx)), expf(__fsub_rn(lse, mx)))));
+    const float w0 = expf(__fsub_rn(lz0, nz)), w1 = __fdiv_rn(expf(__fsub_rn(lse, nz)), l);
+    float* o = out + row * D + 32 * qd;
+#pragma unroll
+    for (int e = 0; e < 32; e += 4) {
+        const f32x4 x = *(const f32x4*)(o + e);
+        *(f32x4*)(o + e) = f32x4{fmaf(acc[e], w1, __fmul_rn(x[0], w0)), fmaf(acc[e + 1], w1, __fmul_rn(x[1], w0)),
+                                 fmaf(acc[e + 2], w1, __fmul_rn(x[2], w0)), fmaf(acc[e + 3], w1, __fmul_rn(x[3], w0))};
+    }
+    if (qd == 0) logz[row] = nz;
+}
+
+// ---------------------------------------------------------------------------------------------
 // selftest_mfma: one wave computes C = A B with the operand conventions used above
 // (A row m = lane%16 with k-set lane/16, B column n = lane%16 with the same k-set,
 // C[4*(lane/16) + i][lane%16] in item i).
@@ -1612,6 +1672,24 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
     if (rc != HTRC_OK) return rc;
     return htrc_route_attend(q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, rowmax, heads, nq, nk, leaf, d, kx,
                              scale, out, logz, stream);
+}
+
+int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
+              int64_t ntail, int d, float scale, float* out, float* logz, void* stream) {
+    REQUIRE(q && tk && tv && out && logz, "htrc_tail: null pointer");
+    REQUIRE(d == D, "htrc_tail: head dim must be 128");
+    REQUIRE(heads > 0 && heads <= 65535 && nq > 0 && ntail > 0 && ntail <= (1 << 24), "htrc_tail: bad sizes");
+    REQUIRE(aligned(out, 16), "htrc_tail: out must be 16-byte aligned");
+    const int64_t nt = (nq + TILE - 1) / TILE;
+    REQUIRE(nt <= 0x7fffffff, "htrc_tail: too many tiles");
+    const dim3 grid((unsigned)nt, (unsigned)heads);
+    if (q_is_bf16)
+        hipLaunchKernelGGL(tail_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, q, tk, tv, nq, (int)ntail, scale,
+                           out, logz);
+    else
+        hipLaunchKernelGGL(tail_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, q, tk, tv, nq, (int)ntail,
+                           scale, out, logz);
+    return launched("htrc_tail");
 }
 
 int htrc_selftest_mfma(const int8_t* ai, const int8_t* bi, int32_t* ci, const uint16_t* af, const uint16_t* bf,

@@ -13,7 +13,9 @@ any other backend, or knobs the HIP path does not implement, raise ``ValueError`
 
 Extensions over the reference: q/k/v may carry a leading head dimension ([H, N, D]) so a
 whole layer runs in one set of launches, and ``return_logz=True`` also returns the
-per-row log-partition of the approximate attention.
+per-row log-partition of the approximate attention.  ``tail=(tk, tv)`` ([n, D], or [H, n, D])
+are keys past the last full leaf, attended exactly by every query (as the reference's GPU
+backend does).
 """
 from __future__ import annotations
 
@@ -58,7 +60,12 @@ def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot
     if quant:
         raise ValueError("quant (fake-quant simulation) is not implemented on the HIP backend")
     if tail is not None:
-        raise ValueError("tail keys are not implemented on the HIP backend: pass keys that are a multiple of the leaf")
+        if not isinstance(tail, (tuple, list)) or len(tail) != 2:
+            raise ValueError("tail must be (tail_keys, tail_values)")
+        tk, tv = tail
+        want = (q.dim() == 2 and tk.dim() == 2) or (q.dim() == 3 and tk.dim() == 3 and tk.shape[0] == q.shape[0])
+        if not want or tuple(tk.shape) != tuple(tv.shape) or tk.shape[-1] != q.shape[-1]:
+            raise ValueError("tail keys / values must be [n, D] (or [H, n, D] with q [H, N, D])")
     if int(kern.get("group", 1)) != 1:
         raise ValueError("kern['group'] > 1 (shared tile centres) is not implemented on the HIP backend")
     if int(tile) != hip.TILE:
@@ -145,6 +152,11 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         state.update(lstate)
         state["idx"] = idx
         state["nb"], state["kx"] = nb, kx
+    if tail is not None and int(tail[0].shape[-2]) > 0:
+        # keys past the last full leaf, exact for every query (h3/htrc_flat_triton.py:187-207, 381-388)
+        tk, tv = (x.unsqueeze(0) if squeeze else x for x in tail)
+        hip.tail_merge(qh, tk.to(qh.device), tv.to(qh.device), scale=scale, out=out, logz=logz)
+        tick("tail")
     res = out[0] if squeeze else out
     lzr = logz[0] if squeeze else logz
     tick("finish")

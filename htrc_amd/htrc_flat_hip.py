@@ -236,6 +236,28 @@ def route_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, 
     return out, logz
 
 
+def tail_merge(q, tk, tv, *, scale: float, out, logz):
+    """Tail keys tk, tv [H, n, D] (past the last full leaf) attended exactly by every query and
+    merged in place into out [H, nq, D] / logz [H, nq] (h3/htrc_flat_triton.py:187-207, 381-388)."""
+    q = _heads(q)
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        q = q.float()
+    q = q.contiguous()
+    tk = _heads(tk).float().contiguous()
+    tv = _heads(tv).float().contiguous()
+    _need(q, None, "q")
+    _need(tk, torch.float32, "tail keys")
+    _need(tv, torch.float32, "tail values")
+    h, nq, d = (int(x) for x in q.shape)
+    if tk.shape != tv.shape or tk.shape[0] != h or tk.shape[2] != d:
+        raise ValueError("tail keys / values must be [H, n, D] matching q")
+    _need(out, torch.float32, "out")
+    _need(logz, torch.float32, "logz")
+    call("htrc_tail", ptr(q), int(q.dtype == torch.bfloat16), ptr(tk), ptr(tv), h, nq, int(tk.shape[1]), d,
+         float(scale), ptr(out), ptr(logz), stream_handle(q.device))
+    return out, logz
+
+
 def selftest_mfma(ai, bi, af, bf):
     """Run the MFMA convention self-test kernel -> (ci int32 [16,16], cf fp32 [16,16])."""
     dev = ai.device

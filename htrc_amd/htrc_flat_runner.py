@@ -92,8 +92,6 @@ class FlatRunner:
             raise ValueError(f"mode must be one of {list(MODES)}")
         if mode not in SUPPORTED_MODES:
             raise ValueError(f"mode {mode!r} needs k-means query ordering, which the HIP backend does not implement")
-        if tail_rows:
-            raise ValueError("tail rows are not implemented on the HIP backend")
         from . import htrc_flat
         self.flat = htrc_flat
         self.mode = mode
@@ -119,7 +117,8 @@ class FlatRunner:
                                                 leaf=leaf, order=base["order"], graph=use_graph,
                                                 queries=int(queries), heads=self.heads)
         self.queries, self.keys, self.dim = int(queries), int(keys), int(dim)
-        self.tail_rows = 0
+        self.tail_rows = int(tail_rows)                  # keys past the last full leaf, exact
+        self._tk = self._tv = None
         self.ws = {}                                     # reusable workspace (eager path)
         self.graph = None
         self._capturing = False
@@ -132,6 +131,8 @@ class FlatRunner:
         return (self.heads, n, self.dim) if self.heads > 1 else (n, self.dim)
 
     def _call(self, q, k, v, tail=None):
+        if tail is None and self._tk is not None:
+            tail = (self._tk, self._tv)
         ws = self.ws if self.graph is None and not self._capturing else None
         return self.flat.flat_attention(q, k, v, tail=tail, ws=ws, **self.cfg)
 
@@ -144,6 +145,9 @@ class FlatRunner:
             self._sq.normal_()
             self._sk.normal_()
             self._sv.normal_()
+            if self.tail_rows:
+                self._tk = torch.randn(self._shape(self.tail_rows), device=dev, dtype=torch.float32)
+                self._tv = torch.randn_like(self._tk)
             self._capturing = True
             try:
                 side = torch.cuda.Stream()
@@ -164,15 +168,24 @@ class FlatRunner:
                 self._capturing = False
                 self.graph_error = f"{type(exc).__name__}: {exc}"[:300]
                 self._sq = self._sk = self._sv = self._so = None
+                self._tk = self._tv = None
                 torch.cuda.empty_cache()
 
+    def _set_tail(self, tail):
+        """Copy this call's tail into the captured static buffers (h3/htrc_flat_runner.py:162-165)."""
+        if self.tail_rows and self.graph is not None:
+            if tail is None:
+                raise ValueError(f"this runner was captured with tail_rows={self.tail_rows}: pass tail=(tk, tv)")
+            self._tk.copy_(tail[0])
+            self._tv.copy_(tail[1])
+
     def head(self, q, k, v, tail=None):
-        """One call (one head, or ``heads`` stacked heads); returns a fresh fp32 tensor."""
-        if tail is not None:
-            raise ValueError("tail keys are not implemented on the HIP backend")
+        """One call (one head, or ``heads`` stacked heads); returns a fresh fp32 tensor.
+        tail=(tk, tv) [tail_rows, D] (or [heads, tail_rows, D])."""
         if self.graph is None:      # the eager result is a view of the reused workspace: copy it
             with torch.inference_mode():
-                return self._call(q, k, v).clone()
+                return self._call(q, k, v, tail=tail).clone()
+        self._set_tail(tail)
         self._sq.copy_(q)
         self._sk.copy_(k)
         self._sv.copy_(v)
@@ -193,9 +206,13 @@ class FlatRunner:
             q = torch.stack([jobs[i][1] for i in grp_src])
             k = torch.stack([jobs[i][2] for i in grp_src])
             v = torch.stack([jobs[i][3] for i in grp_src])
-            if any(len(jobs[i]) > 4 and jobs[i][4] is not None for i in grp):
-                raise ValueError("tail keys are not implemented on the HIP backend")
-            yield grp, q, k, v, None
+            tails = [jobs[i][4] if len(jobs[i]) > 4 else None for i in grp_src]
+            if all(t is None for t in tails):
+                yield grp, q, k, v, None
+            elif any(t is None for t in tails):
+                raise ValueError("a batch of heads needs a tail for every head or for none")
+            else:
+                yield grp, q, k, v, (torch.stack([t[0] for t in tails]), torch.stack([t[1] for t in tails]))
 
     def run(self, jobs, sink=None):
         """jobs: list of (head_index, q, k, v[, (tail_k, tail_v)]).  Outputs in job order, or
@@ -206,6 +223,7 @@ class FlatRunner:
                 out = self.head(q, k, v, tail=tail)
                 outs = [out] if self.heads == 1 else [out[j] for j in range(len(grp))]
             else:
+                self._set_tail(tail)
                 self._sq.copy_(q)
                 self._sk.copy_(k)
                 self._sv.copy_(v)

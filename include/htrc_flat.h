@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 4
+#define HTRC_ABI_VERSION 5
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -104,6 +104,13 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
                int stride, float scale, float* out, float* logz, int32_t* idx, float* rowmax, void* stream);
+
+/* Tail keys: tk, tv fp32 [H, ntail, 128] (keys past the last full leaf) attended exactly by
+ * every query and merged in place into a finished out / logz (log-sum-exp merge).  Up to 16
+ * tail keys are taken with q, k, v and p rounded to bf16, more in fp32, as the reference does.
+ * Replaces the tail handling of tile_attention (h3/htrc_flat_triton.py:187-207, 366-388). */
+int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
+              int64_t ntail, int d, float scale, float* out, float* logz, void* stream);
 
 /* Self-test of the MFMA operand conventions the kernels rely on (no reference counterpart):
  * one 64-lane wave computes C = A B for A int8 [16, 64] / B int8 [64, 16] (i8 path) and

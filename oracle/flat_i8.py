@@ -177,6 +177,31 @@ def merge(pm, pl, pacc):
     return out, logz
 
 
+def tail_merge(out, logz, q, tk, tv, scale: float):
+    """Keys past the last full leaf, attended exactly by every query, merged into a finished
+    (out [n,d], logz [n]).  Up to 16 tail keys: q, k, v and p rounded to bf16, fp32
+    accumulation, as the tile kernel's tail block (h3/htrc_flat_triton.py:187-207); more:
+    fp32 throughout, as the host-side partial (h3/htrc_flat_triton.py:381-388).  Either way the
+    result is one softmax over all keys: the split-merge algebra (:257-273) on the partials
+    (logz, out) and (lse_tail, mean_tail).  q float32 [n,d]; tk, tv float32 [m,d]."""
+    out = _c(out, np.float32)
+    logz = _c(logz, np.float32)
+    qf, kf, vf = (_c(x, np.float32) for x in (q, tk, tv))
+    bfr = kf.shape[0] <= 16
+    if bfr:
+        qf, kf, vf = bf16.round_f32(qf), bf16.round_f32(kf), bf16.round_f32(vf)
+    s = ((qf.astype(np.float64) @ kf.T.astype(np.float64)).astype(np.float32) * np.float32(scale)).astype(np.float32)
+    m = s.max(axis=1)
+    p = np.exp(s - m[:, None]).astype(np.float32)
+    l = p.sum(axis=1, dtype=np.float64).astype(np.float32)
+    pv = bf16.round_f32(p) if bfr else p
+    mean = ((pv.astype(np.float64) @ vf.astype(np.float64)) / l[:, None].astype(np.float64))
+    lse = m.astype(np.float64) + np.log(l.astype(np.float64))
+    z = np.logaddexp(logz.astype(np.float64), lse)
+    res = out.astype(np.float64) * np.exp(logz - z)[:, None] + mean * np.exp(lse - z)[:, None]
+    return res.astype(np.float32), z.astype(np.float32)
+
+
 def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: int = 64,
             splits: int = 4, bn: int = 64, sel_stride: int = 1, sink_leaves: int = 0,
             scale: float | None = None, keep: bool = True) -> dict:

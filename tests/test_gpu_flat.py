@@ -12,8 +12,8 @@ import pytest
 import torch
 
 from helpers import bits, rel_l2
-from htrc_amd import htrc_flat, workloads
-from oracle import flat_i8
+from htrc_amd import htrc_flat, htrc_flat_hip as hip, workloads
+from oracle import bf16, flat_i8
 
 pytestmark = pytest.mark.gpu
 
@@ -74,3 +74,49 @@ def test_deterministic(device):
     a = htrc_flat.flat_attention(q.to(device), k.to(device), v.to(device), **kw).clone()
     b = htrc_flat.flat_attention(q.to(device), k.to(device), v.to(device), **kw)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("ntail", [7, 16, 33])
+def test_tail_keys_vs_oracle(device, fused, ntail):
+    """Keys past the last full leaf (h3/htrc_flat_triton.py:187-207, 381-388): the oracle's
+    operator output merged with its tail restatement."""
+    n, leaf, ex = 4096, 64, 8
+    q, k, v = workloads.clustered_runs(n=n, runs=n // 64, heads=1, seed=100 + ntail)
+    g = torch.Generator().manual_seed(ntail)
+    tk = torch.randn((ntail, 128), generator=g) * 1.5
+    tv = torch.randn((ntail, 128), generator=g)
+    out, logz = htrc_flat.flat_attention(q[0].to(device), k[0].to(device), v[0].to(device), backend="hip",
+                                         store="int8", dot="bf16", leaf=leaf, exact_leaves=ex, splits=4,
+                                         kern={"fused": fused, "tile_bn": 64}, tail=(tk.to(device), tv.to(device)),
+                                         return_logz=True)
+    torch.cuda.synchronize()
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=ex,
+                          splits=1 if fused else 4, bn=64)
+    want, wz = flat_i8.tail_merge(ref["out"], ref["logz"], bf16.to_f32(bits(q[0])), tk.numpy(), tv.numpy(),
+                                  1 / np.sqrt(128))
+    assert rel_l2(out.cpu().numpy(), want) <= OUT_REL_L2
+    assert np.abs(logz.cpu().numpy() - wz).max() <= LOGZ_ABS
+
+
+@pytest.mark.parametrize("ntail", [1, 5, 16, 20])
+def test_tail_merge_kernel_matches_oracle(device, ntail):
+    """The tail kernel alone on arbitrary (out, logz): the oracle's merge to fp32 rounding (a p
+    next to a bf16 rounding boundary may round the other way: 2e-3 relative at most)."""
+    g = torch.Generator().manual_seed(7 + ntail)
+    h, nq = 2, 300
+    q = (torch.randn((h, nq, 128), generator=g)).to(torch.bfloat16)
+    out0 = torch.randn((h, nq, 128), generator=g)
+    lz0 = torch.randn((h, nq), generator=g) * 3
+    tk = torch.randn((h, ntail, 128), generator=g)
+    tv = torch.randn((h, ntail, 128), generator=g)
+    out, lz = out0.clone().to(device), lz0.clone().to(device)
+    hip.tail_merge(q.to(device), tk.to(device), tv.to(device), scale=0.0884, out=out, logz=lz)
+    torch.cuda.synchronize()
+    for i in range(h):
+        want, wz = flat_i8.tail_merge(out0[i].numpy(), lz0[i].numpy(), bf16.to_f32(bits(q[i])), tk[i].numpy(),
+                                      tv[i].numpy(), 0.0884)
+        got = out[i].cpu().numpy()
+        assert np.abs(got - want).max() <= 2e-3 * np.abs(want).max()
+        assert rel_l2(got, want) <= 1e-5 if ntail > 16 else rel_l2(got, want) <= 2e-4
+        assert np.abs(lz[i].cpu().numpy() - wz).max() <= 2e-5 * (1 + np.abs(wz).max())

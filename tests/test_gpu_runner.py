@@ -63,3 +63,27 @@ def test_capture_failure_falls_back_to_eager(device, monkeypatch):
     out = r.run(jobs)[0]
     ref = htrc_flat.flat_attention(jobs[0][1], jobs[0][2], jobs[0][3], **r.cfg)
     assert torch.equal(out, ref)
+
+
+def test_tail_rows_graph_equals_eager(device):
+    """tail_rows: the captured graph reads the tail from static buffers, refreshed per call
+    (h3/htrc_flat_runner.py:136-139, 162-165)."""
+    jobs = _jobs(device, heads=3, seed=4)
+    g = torch.Generator().manual_seed(4)
+    tails = [(torch.randn((7, 128), generator=g).to(device), torch.randn((7, 128), generator=g).to(device))
+             for _ in jobs]
+    r = htrc_flat_runner.FlatRunner(2048, 2048, mode="fast", tail_rows=7, **KW)
+    assert r.graph is not None, r.graph_error
+    eager = [htrc_flat.flat_attention(j[1], j[2], j[3], tail=t, **r.cfg) for j, t in zip(jobs, tails)]
+    outs = r.run([(*j, t) for j, t in zip(jobs, tails)])
+    torch.cuda.synchronize()
+    for o, e in zip(outs, eager):
+        assert torch.equal(o, e)
+    with pytest.raises(ValueError, match="tail"):
+        r.head(jobs[0][1], jobs[0][2], jobs[0][3])
+    batched = htrc_flat_runner.FlatRunner(2048, 2048, mode="fast", tail_rows=7, heads=2, **KW)
+    assert batched.graph is not None, batched.graph_error
+    got = batched.run([(*j, t) for j, t in zip(jobs, tails)])
+    torch.cuda.synchronize()
+    for o, e in zip(got, eager):
+        assert torch.equal(o, e)
