@@ -243,6 +243,23 @@ __device__ __forceinline__ u32x2 tr_operand(const char* rows, int rbase, int db,
     return lds_read_tr16(rows + (row * 16 + (c ^ swz(row))) * 16 + 8 * (L & 1));
 }
 
+// int8 codes of x_i * c rounded to nearest (ties to even), packed little-endian.  Adding
+// 1.5 * 2^23 to a value of magnitude below 2^22 rounds it to an integer held in the low mantissa
+// bits, so the low byte of the sum is the two's-complement code; SDWA adds write the codes of
+// x_1..x_3 into bytes 1..3 of the first sum in place.
+__device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
+    const float m = 12582912.0f;
+    uint32_t u = __float_as_uint(__fadd_rn(__fmul_rn(x[0], c), m));
+    const float y1 = __fmul_rn(x[1], c), y2 = __fmul_rn(x[2], c), y3 = __fmul_rn(x[3], c);
+    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+        : "+v"(u) : "v"(y1), "v"(m));
+    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+        : "+v"(u) : "v"(y2), "v"(m));
+    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+        : "+v"(u) : "v"(y3), "v"(m));
+    return u;
+}
+
 template <int LEAF>
 __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__ mu, int nt,
                                                        const uint16_t* __restrict__ k,
@@ -268,6 +285,7 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
     const int64_t th = (int64_t)h * nt + (tval ? t : 0);
     const uint32_t lds0 = lds_addr(lds);
     const uint32_t voff = (uint32_t)((threadIdx.x >> 4) * 2 * D + 16 * ((threadIdx.x & 15) ^ swz(threadIdx.x >> 4)));
+    const float sl2 = __fmul_rn(scale, LOG2E);
 
     // mu in two bf16 terms (~16 bits; the reference's production path computes these dots in TF32)
     bf16x8 mh[4], ml[4];
@@ -291,42 +309,49 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
     // exchange dwords within the column so that every store instruction writes 64 contiguous
     // bytes of each row (the four lanes of a column side by side): measured on the state rows,
     // 64-byte segments store at 5.2 TB/s where 16-byte pieces 32 bytes apart reach 4.2 TB/s.
-    auto flush = [&]() {
-        if (pl >= 0) {
-            // g8: 4 x 4 block transpose of (pg[g], pg[4 + g]); row g then holds dims 16g + 4c in
-            // x[2c] and 64 + 16g + 4c in x[2c + 1]
+    // The six stores of leaf l - 1 are spread through leaf l's products, so the write queue
+    // sees a steady stream rather than one burst per leaf.
+    auto store_g = [&]() {       // g8: 4 x 4 block transpose of (pg[g], pg[4 + g]); row g then
+        if (pl >= 0) {           // holds dims 16g + 4c in x[2c] and 64 + 16g + 4c in x[2c + 1]
             uint32_t x[8] = {pg[0], pg[4], pg[1], pg[5], pg[2], pg[6], pg[3], pg[7]};
             rows_transpose(x);
-            // vb: rows 2j and 2j + 1 swap halves; row g then holds, for db = 2m + (g & 1), the
-            // dims 16db + 8(g >> 1) .. + 3 in va[m] and .. + 4 .. + 7 in vc[m]
-            u32x2 va[4], vc[4];
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                uint32_t a0 = pv[2 * m].x, a1 = pv[2 * m].y, c0 = pv[2 * m + 1].x, c1 = pv[2 * m + 1].y;
-                swap16(a0, c0);
-                swap16(a1, c1);
-                va[m] = u32x2{a0, a1};
-                vc[m] = u32x2{c0, c1};
-            }
             if (tval) {
                 const int64_t s = th * nb_pad + pl;
                 *(u32x4*)(g8 + s * D + 16 * grp) = u32x4{x[0], x[2], x[4], x[6]};
                 *(u32x4*)(g8 + s * D + 64 + 16 * grp) = u32x4{x[1], x[3], x[5], x[7]};
-                uint16_t* vr = vb + s * D + 16 * (grp & 1) + 8 * (grp >> 1);
-#pragma unroll
-                for (int m = 0; m < 4; ++m)
-                    *(u32x4*)(vr + 32 * m) = u32x4{va[m].x, va[m].y, vc[m].x, vc[m].y};
             }
         }
-        pl = -1;
+    };
+    // vb half hf (dims 64hf..): rows 2j and 2j + 1 swap halves; row g then holds, for
+    // db = 2m + (g & 1), the dims 16db + 8(g >> 1) .. + 3 in va and .. + 4 .. + 7 in vc
+    auto store_v = [&](int hf) {
+        if (pl >= 0) {
+            u32x2 va[2], vc[2];
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm) {
+                const int m = 2 * hf + mm;
+                uint32_t a0 = pv[2 * m].x, a1 = pv[2 * m].y, c0 = pv[2 * m + 1].x, c1 = pv[2 * m + 1].y;
+                swap16(a0, c0);
+                swap16(a1, c1);
+                va[mm] = u32x2{a0, a1};
+                vc[mm] = u32x2{c0, c1};
+            }
+            if (tval) {
+                const int64_t s = th * nb_pad + pl;
+                uint16_t* vr = vb + s * D + 16 * (grp & 1) + 8 * (grp >> 1);
+#pragma unroll
+                for (int mm = 0; mm < 2; ++mm)
+                    *(u32x4*)(vr + 32 * (2 * hf + mm)) = u32x4{va[mm].x, va[mm].y, vc[mm].x, vc[mm].y};
+            }
+        }
     };
     if (l0 < lr) stage_leaf<LEAF>(k, v, kh + (int64_t)l0 * LEAF, lds0, voff);
     for (int l = l0; l < lr; ++l) {
-        // Leaf l landed and the stores of leaf l - 2 are done (measured: letting those stores
-        // stay in flight past this wait, behind the next loads, is slower).
+        // Leaf l landed and the stores of leaf l - 2 are done (measured: issuing the next
+        // loads ahead of the stores, or letting the stores stay in flight past this wait, is
+        // slower).
         wait_vmcnt<0>();
         __syncthreads();                       // ... for every wave; buffer of leaf l - 1 free
-        flush();                               // stores of leaf l - 1
         if (l + 1 < lr)
             stage_leaf<LEAF>(k, v, kh + (int64_t)(l + 1) * LEAF, lds0 + ((l + 1 - l0) & 1) * LEAF_BYTES, voff);
         const char* Kr = lds + ((l - l0) & 1) * LEAF_BYTES;
@@ -343,22 +368,22 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
                 a[kb] = mfma_bf16(A, ml[ks], a[kb]);
             }
         }
-        // a[kb][i] = mu_t . k_{16kb + 4grp + i}
-        float mx = -INFINITY;
+        store_g();                             // stores of leaf l - 1, first part
+        // a[kb][i] = mu_t . k_{16kb + 4grp + i}; the logits are a * scale, their maximum
+        // mx = amx * scale (rounding is monotone), e = 2^(a * scale * log2e - amx * scale * log2e)
+        float amx = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                a[kb][i] = __fmul_rn(a[kb][i], scale);
-                mx = fmaxf(mx, a[kb][i]);
-            }
-        mx = grp_max(mx);
+            for (int i = 0; i < 4; ++i) amx = fmaxf(amx, a[kb][i]);
+        amx = grp_max(amx);
+        const float mx = __fmul_rn(amx, scale), ml = __fmul_rn(amx, sl2);
         float z = 0.0f;
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                a[kb][i] = __expf(__fsub_rn(a[kb][i], mx));
+                a[kb][i] = __builtin_amdgcn_exp2f(__fmaf_rn(a[kb][i], sl2, -ml));
                 z = __fadd_rn(z, a[kb][i]);
             }
         z = grp_sum(z);
@@ -390,7 +415,10 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
                 vacc[db] = mfma_bf16(VA, W0, vacc[db]);
                 vacc[db] = mfma_bf16(VA, W1, vacc[db]);
             }
+            if (kk == 0 && KK > 1) store_v(0);
         }
+        if (KK == 1) store_v(0);
+        store_v(1);
         // g^T = scale gacc^T, vb^T: lane holds dims 16db + 4grp + i of centre t.  The int8 code
         // of g is round(127 g / max|g|) = round(gacc * 127 scale / max|g|).
         float am = 0.0f;
@@ -403,8 +431,7 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
         const float cq = __fdiv_rn(__fmul_rn(127.0f, scale), am);
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
-            pg[db] = pack4_i8(round_away(__fmul_rn(gacc[db][0], cq)), round_away(__fmul_rn(gacc[db][1], cq)),
-                              round_away(__fmul_rn(gacc[db][2], cq)), round_away(__fmul_rn(gacc[db][3], cq)));
+            pg[db] = quant4(gacc[db], cq);
             pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
         }
         if (grp == 0) {
@@ -413,7 +440,9 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
         }
         pl = l;
     }
-    flush();
+    store_g();
+    store_v(0);
+    store_v(1);
     // padded leaves [max(l0, nb), l1): empty state, excluded everywhere
     if (tval) {
         for (int l = max(l0, nb); l < l1; ++l) {
