@@ -36,9 +36,38 @@ __device__ __forceinline__ u32x2 pack8_i8(const int (&c)[8]) {
     return u32x2{pack4_i8(c[0], c[1], c[2], c[3]), pack4_i8(c[4], c[5], c[6], c[7])};
 }
 
+// Shared centres of tile groups (h3/htrc_flat.py:223-229): mu_g is the mean of the G * 64 rows
+// of tiles gG .. gG + G - 1, where tiles past the last repeat the last tile and rows past the
+// last query repeat the last query (the reference pads the tiles, then averages every padded
+// row).  One thread per dim: sequential fp32 sum over the group's rows in order, then one IEEE
+// division.
 template <bool IN_BF16>
-__global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qin, int64_t nq, int nt,
-                                                     float* __restrict__ mu, int8_t* __restrict__ q8,
+__global__ __launch_bounds__(128) void group_centres_kernel(const void* __restrict__ qin, int64_t nq, int nt,
+                                                            int group, int ng, float* __restrict__ mu) {
+    const int g = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
+    const int64_t qbase = (int64_t)h * nq * D;
+    const int rows = group * TILE;
+    float s = 0.0f;
+    for (int j0 = 0; j0 < rows; j0 += 8) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = j0 + u;
+            const int t = min(g * group + j / TILE, nt - 1);
+            const int64_t p = min((int64_t)t * TILE + j % TILE, nq - 1);
+            x[u] = IN_BF16 ? bf2f(((const uint16_t*)qin)[qbase + p * D + i]) : ((const float*)qin)[qbase + p * D + i];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s = __fadd_rn(s, x[u]);
+    }
+    mu[((int64_t)h * ng + g) * D + i] = __fdiv_rn(s, (float)rows);
+}
+
+// group == 1: the tile's centre over its real rows is computed here and written to mu; group > 1:
+// the group's centre is read from mu (group_centres_kernel).
+template <bool IN_BF16>
+__global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qin, int64_t nq, int nt, int group,
+                                                     int ng, float* __restrict__ mu, int8_t* __restrict__ q8,
                                                      float* __restrict__ sq, int8_t* __restrict__ dq8,
                                                      float* __restrict__ sdq) {
     __shared__ __align__(16) float tq[TILE][D + 4];
@@ -66,11 +95,15 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
     __syncthreads();
     const int64_t tg = (int64_t)h * nt + t;
     if (tid < D) {
-        float s = 0.0f;
-        for (int r = 0; r < nr; ++r) s = __fadd_rn(s, tq[r][tid]);
-        const float m = __fdiv_rn(s, (float)nr);
-        smu[tid] = m;
-        mu[tg * D + tid] = m;
+        if (group == 1) {
+            float s = 0.0f;
+            for (int r = 0; r < nr; ++r) s = __fadd_rn(s, tq[r][tid]);
+            const float m = __fdiv_rn(s, (float)nr);
+            smu[tid] = m;
+            mu[tg * D + tid] = m;
+        } else {
+            smu[tid] = mu[((int64_t)h * ng + t / group) * D + tid];
+        }
     }
     __syncthreads();
     const int w = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
@@ -488,53 +521,71 @@ __device__ __forceinline__ void load_rows_i8(const int8_t* __restrict__ x8, int6
     }
 }
 
+// SEL of one tile group (G tiles sharing a centre; G = 1: one tile): the max runs over the
+// rows of every tile of the group (h3/htrc_flat.py:244-252 hands the kernel the G * 64 rows).
 __global__ __launch_bounds__(256) void select_kernel(const int8_t* __restrict__ dq8,
                                                      const float* __restrict__ sdq, int stride,
                                                      const int8_t* __restrict__ g8,
                                                      const float* __restrict__ sg,
-                                                     const float* __restrict__ lz, int nt, int nb,
-                                                     int nb_pad, float* __restrict__ sel) {
+                                                     const float* __restrict__ lz, int nt, int group, int ng,
+                                                     int nb, int nb_pad, float* __restrict__ sel) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    const int t = blockIdx.x, h = blockIdx.z;
-    const int64_t th = (int64_t)h * nt + t;
+    const int gi = blockIdx.x, h = blockIdx.z;
+    const int64_t gs = (int64_t)h * ng + gi;          // state / SEL row of the group
     const int ts = TILE / stride;
-    i32x4 b[4][2];
-    bool val[4];
-    load_rows_i8(dq8, th * TILE, stride, ts, col, grp, b, val);
-    float srow[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) srow[rb] = sdq[th * TILE + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
     const int c0 = blockIdx.y * 256 + w * 64;
-    for (int lb = 0; lb < 4; ++lb) {
-        const int c = c0 + 16 * lb;
-        if (c >= nb) break;
-        const int64_t s0 = th * nb_pad + c;
-        const int8_t* G = g8 + s0 * D;
-        i32x4 acc[4];
+    float bsel[4][4];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) acc[rb] = i32x4{0, 0, 0, 0};
+    for (int lb = 0; lb < 4; ++lb)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const i32x4 A = *(const i32x4*)(G + col * D + 64 * ks + 16 * grp);
+        for (int i = 0; i < 4; ++i) bsel[lb][i] = -INFINITY;
+    for (int j = 0; j < group; ++j) {
+        const int t = gi * group + j;
+        if (t >= nt) break;                           // padded tiles repeat the last one
+        const int64_t th = (int64_t)h * nt + t;
+        i32x4 b[4][2];
+        bool val[4];
+        load_rows_i8(dq8, th * TILE, stride, ts, col, grp, b, val);
+        float srow[4];
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma_i8(A, b[rb][ks], acc[rb]);
+        for (int rb = 0; rb < 4; ++rb) srow[rb] = sdq[th * TILE + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
+#pragma unroll
+        for (int lb = 0; lb < 4; ++lb) {
+            const int c = c0 + 16 * lb;
+            if (c < nb) {
+                const int64_t s0 = gs * nb_pad + c;
+                const int8_t* G = g8 + s0 * D;
+                i32x4 acc[4];
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) acc[rb] = i32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const i32x4 A = *(const i32x4*)(G + col * D + 64 * ks + 16 * grp);
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma_i8(A, b[rb][ks], acc[rb]);
+                }
+                const f32x4 sgv = *(const f32x4*)(sg + s0 + 4 * grp);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float best = -INFINITY;
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb)
+                        if (val[rb]) best = fmaxf(best, __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i])));
+                    bsel[lb][i] = fmaxf(bsel[lb][i], col_max(best));
+                }
+            }
         }
-        const f32x4 sgv = *(const f32x4*)(sg + s0 + 4 * grp);
-        float best[4];
+    }
+    if (col == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            best[i] = -INFINITY;
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-                if (val[rb]) best[i] = fmaxf(best[i], __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i])));
-            best[i] = col_max(best[i]);
-        }
-        if (col == 0) {
-            const f32x4 lzv = *(const f32x4*)(lz + s0 + 4 * grp);
+        for (int lb = 0; lb < 4; ++lb) {
+            const int c = c0 + 16 * lb;
+            if (c >= nb) break;
+            const f32x4 lzv = *(const f32x4*)(lz + gs * nb_pad + c + 4 * grp);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int l = c + 4 * grp + i;
-                if (l < nb) sel[th * nb_pad + l] = __fadd_rn(best[i], lzv[i]);
+                if (l < nb) sel[gs * nb_pad + l] = __fadd_rn(bsel[lb][i], lzv[i]);
             }
         }
     }
@@ -738,7 +789,7 @@ __device__ __forceinline__ bf16x8 gather_pv(const uint16_t* __restrict__ X, int6
 }
 
 template <int LEAF>
-__device__ __forceinline__ void tile_far_near(RowState& st, int64_t th, int nt, int nb, int nb_pad,
+__device__ __forceinline__ void tile_far_near(RowState& st, int64_t srow, int nb, int nb_pad,
                                               int lo, int hi, int e_lo, int e_hi, int kx,
                                               const i32x4 (&q8r)[2], float sqr, const i32x4 (&dq8r)[2],
                                               float sdqr, const int8_t* __restrict__ g8,
@@ -756,7 +807,7 @@ __device__ __forceinline__ void tile_far_near(RowState& st, int64_t th, int nt, 
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
             const int cb = c0 + 16 * h2;
-            const int64_t s0 = th * nb_pad + cb;
+            const int64_t s0 = srow * nb_pad + cb;
             i32x4 acc = {0, 0, 0, 0};
 #pragma unroll
             for (int kss = 0; kss < 2; ++kss) {
@@ -773,7 +824,7 @@ __device__ __forceinline__ void tile_far_near(RowState& st, int64_t th, int nt, 
                 sc[4 * h2 + i] = ok ? __fadd_rn(__fmul_rn((float)acc[i], __fmul_rn(sdqr, sgv[i])), lzv[i]) : -INFINITY;
             }
         }
-        const uint16_t* vb0 = vb + (th * nb_pad + c0) * D;
+        const uint16_t* vb0 = vb + (srow * nb_pad + c0) * D;
         online_block(st, sc, [&](int db) { return gather_pv(vb0, 0, 16, 16 * db + col, grp); });
     }
     // ---- near field: token j of the tile's selected list -> idx[j / LEAF] * LEAF + j % LEAF
@@ -835,12 +886,13 @@ __global__ __launch_bounds__(256) void tile_kernel(
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ excl,
     const int32_t* __restrict__ idx, const int8_t* __restrict__ k8, const float* __restrict__ ks,
-    const uint16_t* __restrict__ v, int64_t nq, int nt, int64_t nk, int nb, int nb_pad, int kx, int lps,
-    int eps, float scale, float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc,
+    const uint16_t* __restrict__ v, int64_t nq, int nt, int group, int ng, int64_t nk, int nb, int nb_pad, int kx,
+    int lps, int eps, float scale, float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc,
     float* __restrict__ out, float* __restrict__ logz) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int t = blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
     const int64_t th = (int64_t)h * nt + t;
+    const int64_t gs = (int64_t)h * ng + t / group;       // state / routing row: the tile's group
     const int r = w * 16 + col;
     const int64_t p = th * TILE + r;
     i32x4 q8r[2], dq8r[2];
@@ -854,8 +906,8 @@ __global__ __launch_bounds__(256) void tile_kernel(
     const int lo = sp * lps, hi = min(nb, lo + lps);
     const int e_n = kx * LEAF;
     const int e_lo = sp * eps, e_hi = min(e_n, e_lo + eps);
-    tile_far_near<LEAF>(st, th, nt, nb, nb_pad, lo, hi, e_lo, e_hi, kx, q8r, sqr, dq8r, sdqr, g8, sg, lz,
-                        vb, excl + th * nb_pad, idx + th * (kx > 0 ? kx : 1), k8, ks, v, (int64_t)h * nk, scale);
+    tile_far_near<LEAF>(st, gs, nb, nb_pad, lo, hi, e_lo, e_hi, kx, q8r, sqr, dq8r, sdqr, g8, sg, lz,
+                        vb, excl + gs * nb_pad, idx + gs * (kx > 0 ? kx : 1), k8, ks, v, (int64_t)h * nk, scale);
     const float ltot = grp_sum(st.l);
     if (pacc == nullptr) {   // single split: normalise in place
         const int64_t qi = (int64_t)t * TILE + r;
@@ -1007,34 +1059,33 @@ __device__ __forceinline__ void dma_rows27(const uint16_t* x0, const uint16_t* x
 // top-k overlap.  SEL never reaches HBM.
 __global__ __launch_bounds__(256, 4) void route_select_kernel(
     const int8_t* __restrict__ dq8, const float* __restrict__ sdq, const int8_t* __restrict__ g8,
-    const float* __restrict__ sg, const float* __restrict__ lz, int nt, int nb, int nb_pad, int kx, int sink,
-    int stride, int32_t* __restrict__ idx, float* __restrict__ rowmax) {
+    const float* __restrict__ sg, const float* __restrict__ lz, int nt, int group, int ng, int nb, int nb_pad,
+    int kx, int sink, int stride, int32_t* __restrict__ idx, float* __restrict__ rowmax) {
     extern __shared__ uint32_t keys[];        // [nb]
     __shared__ TopkSmem sm;
     __shared__ float red_m[4][64];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    // one workgroup per tile group (G tiles sharing a centre, state and near leaves; G = 1: a tile)
     const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
-    const int t = (int)(blk % (uint32_t)nt), h = (int)(blk / (uint32_t)nt);
-    const int64_t th = (int64_t)h * nt + t;
+    const int gi = (int)(blk % (uint32_t)ng), h = (int)(blk / (uint32_t)ng);
+    const int64_t gs = (int64_t)h * ng + gi;
     const int ts = TILE / stride;
-    i32x4 b[4][2];
-    bool val[4];
-    load_rows_i8(dq8, th * TILE, stride, ts, col, grp, b, val);
-    float srow[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) srow[rb] = sdq[th * TILE + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
     struct SelOps {
         i32x4 a[2];
         f32x4 sg, lz;
     };
-    float rmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // row max of the far scores
     auto sel_load = [&](SelOps& o, int c) {
-        const int64_t s0 = th * nb_pad + c;
+        const int64_t s0 = gs * nb_pad + c;
 #pragma unroll
         for (int kss = 0; kss < 2; ++kss) o.a[kss] = *(const i32x4*)(g8 + (s0 + col) * D + 64 * kss + 16 * grp);
         o.sg = *(const f32x4*)(sg + s0 + 4 * grp);
         o.lz = *(const f32x4*)(lz + s0 + 4 * grp);
     };
+    i32x4 b[4][2];
+    bool val[4];
+    float srow[4];
+    float rmax[4];                            // row max of the far scores
+    bool first = true;                        // first tile of the group: set the keys, later: max
     auto sel_block = [&](const SelOps& o, int c) {
         i32x4 acc[4];
 #pragma unroll
@@ -1055,39 +1106,55 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
             }
             best[i] = col_max(best[i]);
         }
-        if (col == 0) {
+        if (col == 0) {               // leaf l is always this lane's: no race across tiles
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int l = c + 4 * grp + i;
-                if (l < nb) keys[l] = l < sink ? 0xffffffffu : order_key(__fadd_rn(best[i], o.lz[i]));
+                if (l < nb) {
+                    const uint32_t key = l < sink ? 0xffffffffu : order_key(__fadd_rn(best[i], o.lz[i]));
+                    keys[l] = first ? key : max(keys[l], key);
+                }
             }
         }
     };
-    // wave w: 16-leaf groups c = 16 w + 64 j, each loaded one group ahead
-    SelOps sa, sb;
-    if (16 * w < nb) sel_load(sa, 16 * w);
-    for (int c = 16 * w; c < nb; c += 128) {
-        const int c1 = c + 64;
-        if (c1 < nb) sel_load(sb, c1);
-        sel_block(sa, c);
-        if (c1 >= nb) break;
-        if (c1 + 64 < nb) sel_load(sa, c1 + 64);
-        sel_block(sb, c1);
-    }
+    for (int j = 0; j < group; ++j) {
+        const int t = gi * group + j;
+        if (t >= nt) break;                   // padded tiles repeat the last one
+        const int64_t th = (int64_t)h * nt + t;
+        load_rows_i8(dq8, th * TILE, stride, ts, col, grp, b, val);
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {          // row r = stride * (16 rb + col) of the sampled rows
-        const float mx = grp_max(rmax[rb]);
-        if (grp == 0) red_m[w][16 * rb + col] = mx;
-    }
-    __syncthreads();
-    if (w == 0) {
-        const int r = lane;
-        float m = r < ts ? fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r])) : -INFINITY;
-        if (stride != 1) m = wave_max(m);     // sampled rows: one reference for the whole tile
-        rowmax[th * TILE + r] = m;
+        for (int rb = 0; rb < 4; ++rb) {
+            srow[rb] = sdq[th * TILE + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
+            rmax[rb] = -INFINITY;
+        }
+        // wave w: 16-leaf groups c = 16 w + 64 j, each loaded one group ahead
+        SelOps sa, sb;
+        if (16 * w < nb) sel_load(sa, 16 * w);
+        for (int c = 16 * w; c < nb; c += 128) {
+            const int c1 = c + 64;
+            if (c1 < nb) sel_load(sb, c1);
+            sel_block(sa, c);
+            if (c1 >= nb) break;
+            if (c1 + 64 < nb) sel_load(sa, c1 + 64);
+            sel_block(sb, c1);
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {      // row r = stride * (16 rb + col) of the sampled rows
+            const float mx = grp_max(rmax[rb]);
+            if (grp == 0) red_m[w][16 * rb + col] = mx;
+        }
+        __syncthreads();
+        if (w == 0) {
+            const int r = lane;
+            float m = r < ts ? fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r])) : -INFINITY;
+            if (stride != 1) m = wave_max(m); // sampled rows: one reference for the whole tile
+            rowmax[th * TILE + r] = m;
+        }
+        __syncthreads();                      // red_m is free for the next tile; keys complete
+        first = false;
     }
     const int kxe = min(kx, nb);
-    if (kxe > 0) topk_row(keys, nb, kxe, sm, idx + th * kxe, nullptr, nullptr);
+    if (kxe > 0) topk_row(keys, nb, kxe, sm, idx + gs * kxe, nullptr, nullptr);
 }
 
 template <int LEAF>
@@ -1096,8 +1163,8 @@ __global__ __launch_bounds__(512) void route_kernel(
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ k8,
     const float* __restrict__ ks, const uint16_t* __restrict__ v, const int32_t* __restrict__ idx,
-    const float* __restrict__ rowmax, int64_t nq, int nt, int64_t nk, int nb, int nb_pad, int kxe, float scale,
-    float* __restrict__ out, float* __restrict__ logz) {
+    const float* __restrict__ rowmax, int64_t nq, int nt, int group, int ng, int64_t nk, int nb, int nb_pad, int kxe,
+    float scale, float* __restrict__ out, float* __restrict__ logz) {
     __shared__ __align__(16) char ring[4][RING_SLOTS][SLOT_BYTES];   // one per wave pair; also merge staging
     __shared__ int32_t sidx[MAX_KX_LDS];
     __shared__ uint32_t exbits[MAX_NB_LDS / 32 + 1];
@@ -1112,11 +1179,12 @@ __global__ __launch_bounds__(512) void route_kernel(
     const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
     const int t = (int)(blk % (uint32_t)nt), h = (int)(blk / (uint32_t)nt);
     const int64_t th = (int64_t)h * nt + t;
+    const int64_t gs = (int64_t)h * ng + t / group;            // state / routing row: the tile's group
     const int64_t kh = (int64_t)h * nk;
     const int64_t row0 = th * TILE + 32 * hr + col;            // this lane's rows: row0, row0 + 16
     // ---- routing of this tile (route_select_kernel)
     for (int i = threadIdx.x; i <= nb / 32; i += 512) exbits[i] = 0u;
-    for (int j = threadIdx.x; j < kxe; j += 512) sidx[j] = idx[th * kxe + j];
+    for (int j = threadIdx.x; j < kxe; j += 512) sidx[j] = idx[gs * kxe + j];
     float mref[2];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
@@ -1136,7 +1204,7 @@ __global__ __launch_bounds__(512) void route_kernel(
     const int nn = e_hi > e_lo ? (e_hi - e_lo + 31) / 32 : 0;
     const int sf_steps = min(nb, lpw) > 0 ? (min(nb, lpw) + 31) / 32 : 0;        // pair 0 is the longest
     const int sn_steps = min(e_n, epw) > 0 ? (min(e_n, epw) + 31) / 32 : 0;
-    const int64_t srow0 = th * nb_pad;
+    const int64_t srow0 = gs * nb_pad;
     char* pring = &ring[pr][0][0];
     const uint32_t pring_lds = lds_addr(pring);
     auto wait_block = [&](int bi, int nblk) {    // this wave's loads of block bi have landed
@@ -1493,21 +1561,31 @@ const char* htrc_last_error(void) { return g_err; }
 
 int htrc_nb_pad(int64_t nb) { return (int)((nb + 31) / 32 * 32); }
 
-int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, float* mu, int8_t* q8,
+int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, float* mu, int8_t* q8,
                 float* sq, int8_t* dq8, float* sdq, void* stream) {
     REQUIRE(q && mu && q8 && sq && dq8 && sdq, "htrc_pack_q: null pointer");
     REQUIRE(d == D, "htrc_pack_q: head dim must be 128");
     REQUIRE(heads > 0 && heads <= 65535 && nq > 0, "htrc_pack_q: bad heads / rows");
+    REQUIRE(group >= 1 && group <= 1024, "htrc_pack_q: group must be in [1, 1024]");
     REQUIRE(aligned(q, 16) && aligned(q8, 16) && aligned(dq8, 16), "htrc_pack_q: q and the int8 outputs must be 16-byte aligned");
     const int64_t nt = (nq + TILE - 1) / TILE;
     REQUIRE(nt <= 0x7fffffff, "htrc_pack_q: too many tiles");
+    const int64_t ng = (nt + group - 1) / group;
+    hipStream_t s = (hipStream_t)stream;
+    if (group > 1) {
+        const dim3 gg((unsigned)ng, (unsigned)heads);
+        if (q_is_bf16)
+            hipLaunchKernelGGL(group_centres_kernel<true>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, mu);
+        else
+            hipLaunchKernelGGL(group_centres_kernel<false>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, mu);
+    }
     dim3 grid((unsigned)nt, (unsigned)heads);
     if (q_is_bf16)
-        hipLaunchKernelGGL(pack_q_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, q, nq, (int)nt, mu,
-                           q8, sq, dq8, sdq);
+        hipLaunchKernelGGL(pack_q_kernel<true>, grid, dim3(256), 0, s, q, nq, (int)nt, group, (int)ng, mu, q8, sq,
+                           dq8, sdq);
     else
-        hipLaunchKernelGGL(pack_q_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, q, nq, (int)nt, mu,
-                           q8, sq, dq8, sdq);
+        hipLaunchKernelGGL(pack_q_kernel<false>, grid, dim3(256), 0, s, q, nq, (int)nt, group, (int)ng, mu, q8, sq,
+                           dq8, sdq);
     return launched("htrc_pack_q");
 }
 
@@ -1553,15 +1631,17 @@ int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64
 }
 
 int htrc_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
-                int64_t heads, int64_t nt, int64_t nb, int stride, int d, float* sel, void* stream) {
+                int64_t heads, int64_t nt, int64_t nb, int stride, int group, int d, float* sel, void* stream) {
     REQUIRE(dq8 && sdq && g8 && sg && lz && sel, "htrc_select: null pointer");
     REQUIRE(d == D, "htrc_select: head dim must be 128");
     REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_select: stride must divide 64");
+    REQUIRE(group >= 1 && group <= 1024, "htrc_select: group must be in [1, 1024]");
     REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff && nb > 0, "htrc_select: bad sizes");
     const int nbp = htrc_nb_pad(nb);
-    dim3 grid((unsigned)nt, (unsigned)((nb + 255) / 256), (unsigned)heads);
+    const int64_t ng = (nt + group - 1) / group;
+    dim3 grid((unsigned)ng, (unsigned)((nb + 255) / 256), (unsigned)heads);
     hipLaunchKernelGGL(select_kernel, grid, dim3(256), 0, (hipStream_t)stream, dq8, sdq, stride, g8, sg, lz,
-                       (int)nt, (int)nb, nbp, sel);
+                       (int)nt, group, (int)ng, (int)nb, nbp, sel);
     return launched("htrc_select");
 }
 
@@ -1584,7 +1664,7 @@ static int64_t split_len(int64_t n, int64_t ns, int64_t bn) {   // _split, h3/ht
 int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
               const float* sg, const float* lz, const uint16_t* vb, const int8_t* excl, const int32_t* idx,
               const int8_t* k8, const float* ks, const uint16_t* v, int64_t heads, int64_t nq, int64_t nk,
-              int leaf, int d, int kx, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
+              int leaf, int d, int kx, int group, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
               float* out, float* logz, void* stream) {
     REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && excl && k8 && ks && v,
             "htrc_tile: null input pointer");
@@ -1595,6 +1675,8 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
     REQUIRE(kx >= 0 && kx <= nb && (kx == 0 || idx), "htrc_tile: need 0 <= kx <= leaves and idx when kx > 0");
     REQUIRE(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0, "htrc_tile: need 1 <= splits <= 64 and a block that is a multiple of 32");
     REQUIRE(splits == 1 ? (out && logz) : (pm && pl && pacc), "htrc_tile: missing outputs");
+    REQUIRE(group >= 1 && group <= 1024, "htrc_tile: group must be in [1, 1024]");
+    const int64_t ng = (nt + group - 1) / group;
     const int lps = (int)split_len(nb, splits, bn), eps = (int)split_len((int64_t)kx * leaf, splits, bn);
     dim3 grid((unsigned)nt, (unsigned)splits, (unsigned)heads);
     hipStream_t s = (hipStream_t)stream;
@@ -1604,8 +1686,8 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
 #define TILE_CASE(L)                                                                                            \
     case L:                                                                                                     \
         hipLaunchKernelGGL(tile_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, excl, idx, k8, \
-                           ks, v, nq, (int)nt, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps, scale, ppm, ppl, ppa,   \
-                           out, logz);                                                                          \
+                           ks, v, nq, (int)nt, group, (int)ng, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps, scale,  \
+                           ppm, ppl, ppa, out, logz);                                                           \
         break;
     switch (leaf) {
         TILE_CASE(16)
@@ -1627,9 +1709,9 @@ int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t head
     return launched("htrc_merge");
 }
 
-// Shape checks shared by the route entry points; sets nb, nt, kxe.
-static int route_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx,
-                        int64_t& nb, int64_t& nt, int& kxe) {
+// Shape checks shared by the route entry points; sets nb, nt, ng (tile groups), kxe.
+static int route_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int group,
+                        int64_t& nb, int64_t& nt, int64_t& ng, int& kxe) {
     static thread_local char msg[160];
     auto bad = [&](const char* what) {
         snprintf(msg, sizeof msg, "%s: %s", who, what);
@@ -1642,6 +1724,8 @@ static int route_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, 
     nt = (nq + TILE - 1) / TILE;
     if (nb > MAX_NB_LDS) return bad("at most 8192 leaves per head");
     if (kx < 0) return bad("need kx >= 0");
+    if (group < 1 || group > 1024) return bad("group must be in [1, 1024]");
+    ng = (nt + group - 1) / group;
     kxe = (int)(kx < nb ? kx : nb);
     if (kxe > MAX_KX_LDS) return bad("at most 1024 near leaves per tile");
     if (nt * heads > 0x7fffffff) return bad("too many tiles x heads for one launch");
@@ -1650,34 +1734,36 @@ static int route_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, 
 
 int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
                       int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink, int stride,
-                      int32_t* idx, float* rowmax, void* stream) {
+                      int group, int32_t* idx, float* rowmax, void* stream) {
     REQUIRE(dq8 && sdq && g8 && sg && lz && rowmax, "htrc_route_select: null pointer");
     REQUIRE(aligned(g8, 16) && aligned(sg, 16) && aligned(lz, 16), "htrc_route_select: misaligned buffer");
-    int64_t nb, nt;
+    int64_t nb, nt, ng;
     int kxe;
-    const int rc = route_shapes("htrc_route_select", heads, nq, nk, leaf, d, kx, nb, nt, kxe);
+    const int rc = route_shapes("htrc_route_select", heads, nq, nk, leaf, d, kx, group, nb, nt, ng, kxe);
     if (rc != HTRC_OK) return rc;
     REQUIRE(sink >= 0, "htrc_route_select: need sink >= 0");
     REQUIRE(kxe == 0 || idx, "htrc_route_select: idx is required when kx > 0");
     REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_route_select: stride must divide 64");
     const int nbp = htrc_nb_pad(nb);
-    hipLaunchKernelGGL(route_select_kernel, dim3((unsigned)(nt * heads)), dim3(256), (size_t)4 * nbp,
-                       (hipStream_t)stream, dq8, sdq, g8, sg, lz, (int)nt, (int)nb, nbp, kxe, sink, stride, idx, rowmax);
+    hipLaunchKernelGGL(route_select_kernel, dim3((unsigned)(ng * heads)), dim3(256), (size_t)4 * nbp,
+                       (hipStream_t)stream, dq8, sdq, g8, sg, lz, (int)nt, group, (int)ng, (int)nb, nbp, kxe, sink,
+                       stride, idx, rowmax);
     return launched("htrc_route_select");
 }
 
 int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                       const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                       const uint16_t* v, const int32_t* idx, const float* rowmax, int64_t heads, int64_t nq,
-                      int64_t nk, int leaf, int d, int kx, float scale, float* out, float* logz, void* stream) {
+                      int64_t nk, int leaf, int d, int kx, int group, float scale, float* out, float* logz,
+                      void* stream) {
     REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && k8 && ks && v && rowmax && out && logz,
             "htrc_route_attend: null pointer");
     REQUIRE(aligned(vb, 16) && aligned(v, 16) && aligned(g8, 16) && aligned(k8, 16) && aligned(sg, 16) &&
                 aligned(ks, 16) && aligned(lz, 16) && aligned(q8, 16) && aligned(dq8, 16),
             "htrc_route_attend: misaligned buffer");
-    int64_t nb, nt;
+    int64_t nb, nt, ng;
     int kxe;
-    const int rc = route_shapes("htrc_route_attend", heads, nq, nk, leaf, d, kx, nb, nt, kxe);
+    const int rc = route_shapes("htrc_route_attend", heads, nq, nk, leaf, d, kx, group, nb, nt, ng, kxe);
     if (rc != HTRC_OK) return rc;
     REQUIRE(kxe == 0 || idx, "htrc_route_attend: idx is required when kx > 0");
     const int nbp = htrc_nb_pad(nb);
@@ -1686,7 +1772,7 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
 #define ROUTE_CASE(L)                                                                                          \
     case L:                                                                                                    \
         hipLaunchKernelGGL(route_kernel<L>, grid, dim3(512), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, \
-                           rowmax, nq, (int)nt, nk, (int)nb, nbp, kxe, scale, out, logz);                    \
+                           rowmax, nq, (int)nt, group, (int)ng, nk, (int)nb, nbp, kxe, scale, out, logz);     \
         break;
     switch (leaf) {
         ROUTE_CASE(16)
@@ -1701,12 +1787,13 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
-               int stride, float scale, float* out, float* logz, int32_t* idx, float* rowmax, void* stream) {
+               int stride, int group, float scale, float* out, float* logz, int32_t* idx, float* rowmax, void* stream) {
     REQUIRE(q8 && sq && vb && k8 && ks && v && out && logz, "htrc_route: null pointer");
-    int rc = htrc_route_select(dq8, sdq, g8, sg, lz, heads, nq, nk, leaf, d, kx, sink, stride, idx, rowmax, stream);
+    int rc = htrc_route_select(dq8, sdq, g8, sg, lz, heads, nq, nk, leaf, d, kx, sink, stride, group, idx, rowmax,
+                               stream);
     if (rc != HTRC_OK) return rc;
     return htrc_route_attend(q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, rowmax, heads, nq, nk, leaf, d, kx,
-                             scale, out, logz, stream);
+                             group, scale, out, logz, stream);
 }
 
 int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,

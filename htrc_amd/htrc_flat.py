@@ -66,8 +66,8 @@ def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot
         want = (q.dim() == 2 and tk.dim() == 2) or (q.dim() == 3 and tk.dim() == 3 and tk.shape[0] == q.shape[0])
         if not want or tuple(tk.shape) != tuple(tv.shape) or tk.shape[-1] != q.shape[-1]:
             raise ValueError("tail keys / values must be [n, D] (or [H, n, D] with q [H, N, D])")
-    if int(kern.get("group", 1)) != 1:
-        raise ValueError("kern['group'] > 1 (shared tile centres) is not implemented on the HIP backend")
+    if int(kern.get("group", 1)) > 1024:
+        raise ValueError("kern['group'] must be at most 1024 tiles")
     if int(tile) != hip.TILE:
         raise ValueError("the HIP backend uses tile=64")
     if leaf not in (16, 32, 64, 128):
@@ -91,6 +91,8 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     (h3/htrc_flat.py:99-139).  ``kern['fused']`` (default True) runs select, top-k, far and
     near field in one fused kernel per layer; False runs the reference's stage structure
     (select, top-k, split tile kernel, merge) honouring ``splits`` and ``kern['tile_bn']``.
+    ``kern['group']`` = G > 1 makes G consecutive tiles share one expansion centre (the mean
+    of their rows), one leaf state and one near set (h3/htrc_flat.py:223-231).
     ``tile_chunk`` and ``precision`` are accepted for compatibility: all tiles are processed
     in one launch and accumulation is IEEE fp32.  ``state``, if a dict, receives the packed
     operands, the leaf state and the routing (for checks)."""
@@ -112,9 +114,10 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     stride = int(sel_stride)
     if stride < 1 or hip.TILE % stride:
         raise ValueError("sel_stride must divide 64")
+    group = max(1, int(kern.get("group", 1)))           # G consecutive tiles share one centre
     if qh.dtype not in (torch.float32, torch.bfloat16):
         qh = qh.float()
-    mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), ws=ws)
+    mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), ws=ws, group=group)
     kb = kh.to(torch.bfloat16).contiguous()
     vb = vh.to(torch.bfloat16).contiguous()
     k8, ks = hip.pack_k(kb, ws=ws)
@@ -123,27 +126,27 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     tick("stats")
     packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "v": vb, "mu": mu}
     lstate = {"g8": g8, "sg": sg, "lz": lz, "vb": vbs}
-    nt = int(mu.shape[1])
+    ng = int(mu.shape[1])                               # centres: tiles, or tile groups
     idx = None
     if kern.get("fused", True):
         if state is not None and kx > 0:
-            idx = hip._buf(ws, "idx", (h, nt, kx), torch.int32, qh.device)
+            idx = hip._buf(ws, "idx", (h, ng, kx), torch.int32, qh.device)
         out, logz = hip.route(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, sink=sink, stride=stride,
-                              ws=ws, idx=idx)
+                              ws=ws, idx=idx, group=group)
         tick("tile")
     else:
         excl = None
         if kx > 0:
-            sel = hip.rowmax_select(g=g8, lz=lz, sg=sg, stride=stride, nb=nb, dq8=dq8, sdq=sdq, ws=ws)
+            sel = hip.rowmax_select(g=g8, lz=lz, sg=sg, stride=stride, nb=nb, dq8=dq8, sdq=sdq, ws=ws, group=group)
             idx, excl = hip.topk_excl(sel, nb, kx, sink, ws=ws)
             if state is not None:
                 state["sel"] = sel
         else:
-            excl = hip._buf(ws, "excl", (h, nt, nb_pad(nb)), torch.int8, qh.device)
+            excl = hip._buf(ws, "excl", (h, ng, nb_pad(nb)), torch.int8, qh.device)
             excl.zero_()
         tick("select")
         out, logz = hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
-                                       bn=int(kern.get("tile_bn", 32)), ws=ws)
+                                       bn=int(kern.get("tile_bn", 32)), ws=ws, group=group)
         tick("tile")
         if state is not None:
             state["excl"] = excl
@@ -151,7 +154,7 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         state.update(packed)
         state.update(lstate)
         state["idx"] = idx
-        state["nb"], state["kx"] = nb, kx
+        state["nb"], state["kx"], state["group"] = nb, kx, group
     if tail is not None and int(tail[0].shape[-2]) > 0:
         # keys past the last full leaf, exact for every query (h3/htrc_flat_triton.py:187-207, 381-388)
         tk, tv = (x.unsqueeze(0) if squeeze else x for x in tail)

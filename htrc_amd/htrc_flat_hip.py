@@ -6,9 +6,10 @@ dict ``ws`` is given (buffers are reused, as ``_buf`` does in the reference), no
 synchronises, so a whole operator call can be captured in a HIP graph.
 
 Tensors carry a leading head dimension H (2-D inputs are treated as H = 1).  Layouts are
-those of the C ABI: the per-(tile, leaf) state is ``g`` int8 ``[H, nt, nbp, 128]`` with row
-scales ``sg``, ``lz`` fp32 and ``vb`` bf16 ``[H, nt, nbp, 128]`` (nbp = leaves rounded up to
-32; padded leaves have lz = -inf).
+those of the C ABI: the per-(centre, leaf) state is ``g`` int8 ``[H, ng, nbp, 128]`` with row
+scales ``sg``, ``lz`` fp32 and ``vb`` bf16 ``[H, ng, nbp, 128]`` (nbp = leaves rounded up to
+32; padded leaves have lz = -inf).  ng = nt tiles, or ceil(nt / G) when ``group`` = G tiles
+share one centre, one state and one near set (the reference's ``kern["group"]``).
 
 Launch-shape knobs of the reference (bt, bl, warps, stages, prec, sel_bn, rb) are
 accepted for call compatibility and ignored: the HIP kernels have fixed MI355X launch
@@ -58,10 +59,15 @@ def _need(t: torch.Tensor, dtype, name: str):
         raise ValueError(f"{name} must be contiguous")
 
 
-def pack_q(q: torch.Tensor, tile: int = TILE, ws=None):
-    """Tile centres and row int8 of q and q - mu -> (mu [H,nt,D], q8, sq, dq8, sdq)."""
+def pack_q(q: torch.Tensor, tile: int = TILE, ws=None, group: int = 1):
+    """Centres and row int8 of q and q - mu -> (mu [H,ng,D], q8, sq, dq8, sdq).  group 1: the
+    centre of each tile over its real rows (h3/htrc_flat.py:142-156); group G: the centre of
+    each G tiles over their padded rows (:223-229)."""
     if tile != TILE:
         raise ValueError("the HIP kernels use 64-row query tiles")
+    group = int(group)
+    if group < 1:
+        raise ValueError("group must be >= 1")
     q = _heads(q)
     if q.dtype not in (torch.float32, torch.bfloat16):
         q = q.float()
@@ -69,13 +75,14 @@ def pack_q(q: torch.Tensor, tile: int = TILE, ws=None):
     _need(q, None, "q")
     h, nq, d = (int(x) for x in q.shape)
     nt = -(-nq // TILE)
+    ng = -(-nt // group)
     dev = q.device
-    mu = _buf(ws, "mu", (h, nt, d), torch.float32, dev)
+    mu = _buf(ws, "mu", (h, ng, d), torch.float32, dev)
     q8 = _buf(ws, "q8", (h, nt * TILE, d), torch.int8, dev)
     dq8 = _buf(ws, "dq8", (h, nt * TILE, d), torch.int8, dev)
     sq = _buf(ws, "sq", (h, nt * TILE), torch.float32, dev)
     sdq = _buf(ws, "sdq", (h, nt * TILE), torch.float32, dev)
-    call("htrc_pack_q", ptr(q), int(q.dtype == torch.bfloat16), h, nq, d, ptr(mu), ptr(q8), ptr(sq),
+    call("htrc_pack_q", ptr(q), int(q.dtype == torch.bfloat16), h, nq, d, group, ptr(mu), ptr(q8), ptr(sq),
          ptr(dq8), ptr(sdq), stream_handle(dev))
     return mu, q8, sq, dq8, sdq
 
@@ -120,24 +127,28 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
 
 
 def rowmax_select(q_c=None, mu_c=None, g=None, lz=None, prec="ieee", bn=32, warps=4, splits=8, stride=1, dot=1,
-                  ws=None, sg=None, *, nb=None, dq8=None, sdq=None):
-    """SEL [H,nt,nbp] (h3/htrc_flat_triton.py:315-326).  Takes the packed rows dq8/sdq
-    (pack_q); when absent they are packed from q_c (fp32 [H,nq,D] rows)."""
+                  ws=None, sg=None, *, nb=None, dq8=None, sdq=None, group=1):
+    """SEL [H,ng,nbp] (h3/htrc_flat_triton.py:315-326), the max over the rows of each group of
+    ``group`` tiles.  Takes the packed rows dq8/sdq (pack_q); when absent they are packed from
+    q_c (fp32 [H,nq,D] rows)."""
     if dq8 is None or sdq is None:
-        _, _, _, dq8, sdq = pack_q(q_c)
+        _, _, _, dq8, sdq = pack_q(q_c, group=group)
     g = _heads(g) if g.dim() == 3 else g
-    h, nt, nbp, d = (int(x) for x in g.shape)
+    h, ng, nbp, d = (int(x) for x in g.shape)
+    nt = int(_heads(dq8).shape[1]) // TILE
+    if -(-nt // int(group)) != ng:
+        raise ValueError("state rows do not match the tile groups of the packed rows")
     nb = nbp if nb is None else int(nb)
     dev = g.device
-    sel = _buf(ws, "sel", (h, nt, nbp), torch.float32, dev)
-    call("htrc_select", ptr(dq8), ptr(sdq), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), d, ptr(sel),
-         stream_handle(dev))
+    sel = _buf(ws, "sel", (h, ng, nbp), torch.float32, dev)
+    call("htrc_select", ptr(dq8), ptr(sdq), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), int(group), d,
+         ptr(sel), stream_handle(dev))
     return sel
 
 
 def topk_excl(sel, nb: int, kx: int, sink: int = 0, ws=None):
-    """kx largest SEL per tile (leaves < sink forced), idx ascending -> (idx [H,nt,kx] int32,
-    excl [H,nt,nbp] int8)  (h3/htrc_flat.py:262-265)."""
+    """kx largest SEL per row (leaves < sink forced), idx ascending -> (idx [H,ng,kx] int32,
+    excl [H,ng,nbp] int8)  (h3/htrc_flat.py:262-265)."""
     h, nt, nbp = (int(x) for x in sel.shape)
     dev = sel.device
     idx = _buf(ws, "idx", (h, nt, kx), torch.int32, dev)
@@ -147,7 +158,7 @@ def topk_excl(sel, nb: int, kx: int, sink: int = 0, ws=None):
 
 
 def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, scale: float, splits: int = 4,
-                   bn: int = 64, ws=None, out=None, logz=None):
+                   bn: int = 64, ws=None, out=None, logz=None, group: int = 1):
     """Far + near online softmax per (tile, split) and the merge
     (h3/htrc_flat_triton.py:348-391) -> (out [H,nq,D] fp32, logz [H,nq] fp32)."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
@@ -168,7 +179,7 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
         pl = _buf(ws, "pl", (h, nt, ns, TILE), torch.float32, dev)
         pacc = _buf(ws, "pacc", (h, nt, ns, TILE, d), torch.float32, dev)
     call("htrc_tile", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(excl),
-         ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(v), h, nq, nk, int(leaf), d, kx, ns, int(bn),
+         ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(v), h, nq, nk, int(leaf), d, kx, int(group), ns, int(bn),
          float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
     if ns > 1:
         call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, ns, d, ptr(out), ptr(logz), stream_handle(dev))
@@ -176,9 +187,9 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
 
 
 def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: float, sink: int = 0, stride: int = 1,
-          ws=None, out=None, logz=None, idx=None):
+          ws=None, out=None, logz=None, idx=None, group: int = 1):
     """Fused select -> top-k, then far + near -> normalised output (two launches per layer call).
-    -> (out [H,nq,D], logz [H,nq]); idx [H,nt,min(kx,nb)] int32 receives the routing (a
+    -> (out [H,nq,D], logz [H,nq]); idx [H,ng,min(kx,nb)] int32 receives the routing (a
     workspace buffer when not given)."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
@@ -186,40 +197,42 @@ def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: floa
     h, nk, d = (int(x) for x in k8.shape)
     dev = q8.device
     nt = -(-int(nq) // TILE)
+    ng = -(-nt // int(group))
     kxe = min(int(kx), nk // int(leaf))
     if out is None:
         out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
     if logz is None:
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     if idx is None and kxe > 0:
-        idx = _buf(ws, "idx", (h, nt, kxe), torch.int32, dev)
+        idx = _buf(ws, "idx", (h, ng, kxe), torch.int32, dev)
     rowmax = _buf(ws, "rowmax", (h, nt * TILE), torch.float32, dev)
     call("htrc_route", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8), ptr(ks),
-         ptr(v), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), float(scale), ptr(out), ptr(logz),
-         ptr(idx), ptr(rowmax), stream_handle(dev))
+         ptr(v), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), int(group), float(scale), ptr(out),
+         ptr(logz), ptr(idx), ptr(rowmax), stream_handle(dev))
     return out, logz
 
 
 def route_select(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, sink: int = 0, stride: int = 1,
-                 ws=None, idx=None):
-    """First launch of route: select -> top-k per tile -> (idx [H,nt,min(kx,nb)] int32 or None,
-    rowmax [H,nt*64] fp32, each row's largest far-field score)."""
+                 ws=None, idx=None, group: int = 1):
+    """First launch of route: select -> top-k per tile group -> (idx [H,ng,min(kx,nb)] int32 or
+    None, rowmax [H,nt*64] fp32, each row's largest far-field score)."""
     dq8, sdq = packed["dq8"], packed["sdq"]
     g8, sg, lz = state["g8"], state["sg"], state["lz"]
     h, nk = int(packed["k8"].shape[0]), int(packed["k8"].shape[1])
     dev = dq8.device
     nt = -(-int(nq) // TILE)
+    ng = -(-nt // int(group))
     kxe = min(int(kx), nk // int(leaf))
     if idx is None and kxe > 0:
-        idx = _buf(ws, "idx", (h, nt, kxe), torch.int32, dev)
+        idx = _buf(ws, "idx", (h, ng, kxe), torch.int32, dev)
     rowmax = _buf(ws, "rowmax", (h, nt * TILE), torch.float32, dev)
     call("htrc_route_select", ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), h, nq, nk, int(leaf), D, int(kx),
-         int(sink), int(stride), ptr(idx), ptr(rowmax), stream_handle(dev))
+         int(sink), int(stride), int(group), ptr(idx), ptr(rowmax), stream_handle(dev))
     return idx, rowmax
 
 
 def route_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, kx: int, scale: float, ws=None,
-                 out=None, logz=None):
+                 out=None, logz=None, group: int = 1):
     """Second launch of route: far + near field with the row reference rowmax -> (out, logz)."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
@@ -231,8 +244,8 @@ def route_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, 
     if logz is None:
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     call("htrc_route_attend", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8),
-         ptr(ks), ptr(v), ptr(idx), ptr(rowmax), h, nq, nk, int(leaf), d, int(kx), float(scale), ptr(out), ptr(logz),
-         stream_handle(dev))
+         ptr(ks), ptr(v), ptr(idx), ptr(rowmax), h, nq, nk, int(leaf), d, int(kx), int(group), float(scale), ptr(out),
+         ptr(logz), stream_handle(dev))
     return out, logz
 
 

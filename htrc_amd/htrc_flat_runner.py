@@ -38,46 +38,49 @@ TILE = 64
 
 
 def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, heads: int = 1,
-                    splits: int = 1, kx: int = 0) -> int:
-    """Device bytes the operator's workspace holds for one call (all tiles at once)."""
+                    splits: int = 1, kx: int = 0, group: int = 1) -> int:
+    """Device bytes the operator's workspace holds for one call (all tiles at once); the leaf
+    state and the routing hold one row per centre (ng = ceil(nt / group))."""
     nt = -(-int(queries) // TILE)
+    ng = -(-nt // max(1, int(group)))
     rows = nt * TILE
     nb = int(keys) // int(leaf)
     nbp = (nb + 31) // 32 * 32
     per_head = (
-        4 * nt * dim                       # mu
+        4 * ng * dim                       # mu
         + 2 * rows * dim + 8 * rows        # q8, dq8, sq, sdq
         + keys * dim + 4 * keys            # k8, ks
         + 2 * keys * dim * 2               # bf16 copies of k and v when the inputs are not bf16
-        + nt * nbp * (3 * dim + 8)         # g8, vb, sg, lz
+        + ng * nbp * (3 * dim + 8)         # g8, vb, sg, lz
         + 4 * queries * (dim + 1)          # out, logz
-        + 4 * nt * kx                      # idx (when recorded)
+        + 4 * rows                         # rowmax
+        + 4 * ng * kx                      # idx (when recorded)
     )
     if splits > 1:
-        per_head += nt * splits * TILE * (2 + dim) * 4 + nt * nbp * 5 + 4 * nt * kx   # partials, excl, sel
+        per_head += nt * splits * TILE * (2 + dim) * 4 + ng * nbp * 5 + 4 * ng * kx   # partials, excl, sel
     return int(heads) * per_head
 
 
 def predicted_peak_mib(keys: int, tile: int, tile_chunk: int, splits: int = 8, leaf: int = 16,
                        dim: int = 128, order: str = "seq", graph: bool = True, queries: int = 0,
-                       heads: int = 1) -> float:
+                       heads: int = 1, group: int = 1) -> float:
     """Peak device MiB above the caller's q/k/v (signature of h3/htrc_flat_runner.py:61-68).
     This implementation processes every tile in one launch, so ``tile_chunk`` does not
     bound the workspace; ``queries`` (default: as many as keys) sizes it.  Graph mode adds
     the static fp32 q and bf16 k/v copies."""
     q = int(queries) if queries else int(keys)
-    b = workspace_bytes(q, keys, leaf, dim, heads, splits=1)
+    b = workspace_bytes(q, keys, leaf, dim, heads, splits=1, group=group)
     if graph:
         b += int(heads) * (4 * q * dim + 2 * 2 * int(keys) * dim)
     return b / 2 ** 20
 
 
 def plan_chunk(free_bytes: int, keys: int, tile: int, splits: int = 8, order: str = "seq",
-               graph: bool = True, queries: int = 0, leaf: int = 16, heads: int = 1) -> int:
+               graph: bool = True, queries: int = 0, leaf: int = 16, heads: int = 1, group: int = 1) -> int:
     """Tile chunk for the call (h3/htrc_flat_runner.py:71-82): the largest of CHUNKS when the
     whole workspace fits in ``free_bytes``; MemoryError otherwise."""
     need = predicted_peak_mib(keys, tile, CHUNKS[0], splits, leaf=leaf, order=order, graph=graph,
-                              queries=queries, heads=heads)
+                              queries=queries, heads=heads, group=group)
     if need * 2 ** 20 <= free_bytes:
         return CHUNKS[0]
     raise MemoryError(f"flat HTRC needs ~{need:.0f} MiB, {int(free_bytes) >> 20} MiB free")
@@ -105,17 +108,18 @@ class FlatRunner:
         base["sink_leaves"] = int(sink_leaves)
         self.heads = max(1, int(heads))
         leaf = int(base.get("leaf", 16))
+        group = max(1, int(base.get("kern", {}).get("group", 1)))
         if tile_chunk is None:
             if free_bytes is not None:
                 tile_chunk = plan_chunk(free_bytes, keys, base["tile"], base.get("splits", 8), base["order"],
-                                        use_graph, queries=int(queries), leaf=leaf, heads=self.heads)
+                                        use_graph, queries=int(queries), leaf=leaf, heads=self.heads, group=group)
             else:
                 tile_chunk = base["tile_chunk"]
         base["tile_chunk"] = int(tile_chunk)
         self.cfg = base
         self.predicted_mib = predicted_peak_mib(keys, base["tile"], base["tile_chunk"], base.get("splits", 8),
                                                 leaf=leaf, order=base["order"], graph=use_graph,
-                                                queries=int(queries), heads=self.heads)
+                                                queries=int(queries), heads=self.heads, group=group)
         self.queries, self.keys, self.dim = int(queries), int(keys), int(dim)
         self.tail_rows = int(tail_rows)                  # keys past the last full leaf, exact
         self._tk = self._tv = None

@@ -8,17 +8,20 @@
  *
  * All tensors carry a leading head dimension H and are contiguous:
  *   q        fp32 or bf16 [H, nq, 128]          k, v  bf16 [H, nk, 128]
- *   mu       fp32 [H, nt, 128]                  nt = ceil(nq / 64)  (tiles of 64 query rows)
+ *   mu       fp32 [H, ng, 128]                  nt = ceil(nq / 64)  (tiles of 64 query rows)
  *   q8, dq8  int8 [H, nt*64, 128]               sq, sdq fp32 [H, nt*64]   (padded rows)
  *   k8       int8 [H, nk, 128], ks fp32 [H, nk]
- *   g8       int8 [H, nt, nbp, 128]             nb = nk / leaf, nbp = htrc_nb_pad(nb)
- *   sg, lz   fp32 [H, nt, nbp]                  padded leaves: sg = 0, lz = -inf
- *   vb       bf16 [H, nt, nbp, 128]             leaf value means
- *   sel      fp32 [H, nt, nbp]                  excl int8 [H, nt, nbp]; idx int32 [H, nt, kx]
+ *   g8       int8 [H, ng, nbp, 128]             nb = nk / leaf, nbp = htrc_nb_pad(nb)
+ *   sg, lz   fp32 [H, ng, nbp]                  padded leaves: sg = 0, lz = -inf
+ *   vb       bf16 [H, ng, nbp, 128]             leaf value means
+ *   sel      fp32 [H, ng, nbp]                  excl int8 [H, ng, nbp]; idx int32 [H, ng, kx]
  *   pm, pl   fp32 [H, nt, splits, 64]           pacc fp32 [H, nt, splits, 64, 128]
  *   out      fp32 [H, nq, 128]                  logz fp32 [H, nq]
  *   rowmax   fp32 [H, nt*64]                    per-row far-field maximum (route)
  *
+ * group = G >= 1 consecutive tiles share one expansion centre, one leaf state and one near
+ * set (the reference's kern["group"], h3/htrc_flat.py:223-231): ng = ceil(nt / G) centres,
+ * the last group padded with repeats of the last tile.  G = 1 is the plain per-tile path.
  * The reference implements the same path as Triton kernels driven from Python;
  * each entry point below names the reference interface it replaces.
  */
@@ -31,7 +34,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 5
+#define HTRC_ABI_VERSION 6
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -43,28 +46,32 @@ const char* htrc_last_error(void);
 /* Padded leaf count of the per-(tile, leaf) state: nb rounded up to a multiple of 32. */
 int htrc_nb_pad(int64_t nb);
 
-/* Tile centres and the row int8 of q and q - mu.
- * Replaces _tiles (h3/htrc_flat.py:142-156) and the in-kernel Q / dQ quantisation of
- * _tile_kernel and _rowmax_kernel (h3/htrc_flat_triton.py:104-117, 225-233). */
-int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, float* mu, int8_t* q8,
+/* Centres and the row int8 of q and q - mu.  group 1: mu[t] is the mean of tile t's real rows;
+ * group G > 1: mu[g] is the mean of the G * 64 padded rows of tiles gG.., and q - mu uses the
+ * centre of the row's group.
+ * Replaces _tiles (h3/htrc_flat.py:142-156), the group centres (:223-229) and the in-kernel
+ * Q / dQ quantisation of _tile_kernel and _rowmax_kernel (h3/htrc_flat_triton.py:104-117,
+ * 225-233). */
+int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, float* mu, int8_t* q8,
                 float* sq, int8_t* dq8, float* sdq, void* stream);
 
 /* K int8 pack (round half to even, per-row scale).
  * Replaces the host-side K pack of _flat_triton (h3/htrc_flat.py:213-219). */
 int htrc_pack_k(const uint16_t* k, int64_t heads, int64_t nk, int d, int8_t* k8, float* ks, void* stream);
 
-/* Leaf statistics at the tile centres with the int8 store of g.
+/* Leaf statistics at the centres with the int8 store of g; nt = the number of centres
+ * (ng when tiles are grouped).
  * Replaces leaf_stats / _stats_kernel (h3/htrc_flat_triton.py:329-345, 41-85). */
 int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
                     int leaf, int d, float scale, int8_t* g8, float* sg, uint16_t* vb, float* lz, void* stream);
 
-/* Row-max routing score SEL[t, l] over every `stride`-th tile row.
+/* Row-max routing score SEL[g, l] over every `stride`-th row of the group's tiles; nt = tiles.
  * Replaces rowmax_select / _rowmax_kernel (h3/htrc_flat_triton.py:315-326, 214-254). */
 int htrc_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
-                int64_t heads, int64_t nt, int64_t nb, int stride, int d, float* sel, void* stream);
+                int64_t heads, int64_t nt, int64_t nb, int stride, int group, int d, float* sel, void* stream);
 
 /* kx largest SEL per row (leaves < sink forced in), idx ascending, exclusion mask.
- * Replaces torch.topk + excl.scatter_ (h3/htrc_flat.py:262-265). `rows` = H * nt. */
+ * Replaces torch.topk + excl.scatter_ (h3/htrc_flat.py:262-265). `rows` = H * ng. */
 int htrc_topk(const float* sel, int64_t rows, int64_t nb, int kx, int sink, int32_t* idx, int8_t* excl,
               void* stream);
 
@@ -74,7 +81,7 @@ int htrc_topk(const float* sel, int64_t rows, int64_t nb, int kx, int sink, int3
 int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
               const float* sg, const float* lz, const uint16_t* vb, const int8_t* excl, const int32_t* idx,
               const int8_t* k8, const float* ks, const uint16_t* v, int64_t heads, int64_t nq, int64_t nk,
-              int leaf, int d, int kx, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
+              int leaf, int d, int kx, int group, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
               float* out, float* logz, void* stream);
 
 /* Merge of split partials into normalised rows, plus logz = max + log(sum).
@@ -82,13 +89,13 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
 int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int splits,
                int d, float* out, float* logz, void* stream);
 
-/* Production path, first launch: select -> top-k per tile with SEL kept in LDS, writing the
- * routing idx [H, nt, min(kx, nb)] (ascending; required when kx > 0) and rowmax fp32
+/* Production path, first launch: select -> top-k per tile group with SEL kept in LDS, writing
+ * the routing idx [H, ng, min(kx, nb)] (ascending; required when kx > 0) and rowmax fp32
  * [H, nt*64], each row's largest far-field score (the tile's largest when stride > 1).
  * Replaces rowmax_select + torch.topk of the chunk loop (h3/htrc_flat.py:258-265). */
 int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
                       int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink, int stride,
-                      int32_t* idx, float* rowmax, void* stream);
+                      int group, int32_t* idx, float* rowmax, void* stream);
 
 /* Production path, second launch: far + near field of every tile in one softmax whose
  * reference is rowmax, merged into normalised out / logz (one split per tile).
@@ -96,14 +103,16 @@ int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, con
 int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                       const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                       const uint16_t* v, const int32_t* idx, const float* rowmax, int64_t heads, int64_t nq,
-                      int64_t nk, int leaf, int d, int kx, float scale, float* out, float* logz, void* stream);
+                      int64_t nk, int leaf, int d, int kx, int group, float scale, float* out, float* logz,
+                      void* stream);
 
 /* Both launches of the production path: htrc_route_select then htrc_route_attend.
  * Replaces the chunk loop body of _flat_triton after leaf_stats (h3/htrc_flat.py:250-271). */
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
-               int stride, float scale, float* out, float* logz, int32_t* idx, float* rowmax, void* stream);
+               int stride, int group, float scale, float* out, float* logz, int32_t* idx, float* rowmax,
+               void* stream);
 
 /* Tail keys: tk, tv fp32 [H, ntail, 128] (keys past the last full leaf) attended exactly by
  * every query and merged in place into a finished out / logz (log-sum-exp merge).  Up to 16

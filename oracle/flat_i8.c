@@ -17,12 +17,14 @@
  *
  * Layouts (per head; the Python wrapper loops over heads):
  *   q      fp32 [n, d]                 k, v  bf16 bits [nk, d]
- *   mu     fp32 [nt, d]                q8/dq8 int8 [nt*tile, d], sq/sdq fp32 [nt*tile]
+ *   mu     fp32 [ng, d]                q8/dq8 int8 [nt*tile, d], sq/sdq fp32 [nt*tile]
  *   k8     int8 [nk, d], ks fp32 [nk]
- *   g8     int8 [nt, nb, d], sg/lz fp32 [nt, nb], vb bf16 bits [nt, nb, d]
- *   sel    fp32 [nt, nb]; idx int32 [nt, kx] (ascending); excl int8 [nt, nb]
+ *   g8     int8 [ng, nb, d], sg/lz fp32 [ng, nb], vb bf16 bits [ng, nb, d]
+ *   sel    fp32 [ng, nb]; idx int32 [ng, kx] (ascending); excl int8 [ng, nb]
  *   pm/pl  fp32 [nt, ns, tile]; pacc fp32 [nt, ns, tile, d]
  *   out    fp32 [nt*tile, d]; logz fp32 [nt*tile]
+ * ng = nt, or ceil(nt / G) when G consecutive tiles share one centre, one state and one near
+ * set (kern["group"], h3/htrc_flat.py:223-231; the tile kernel's gt = t // GR).
  */
 #include <math.h>
 #include <stdint.h>
@@ -33,7 +35,7 @@
  * (h3/htrc_flat.py:217, h3/htrc_flat_triton.py:76,112,115,231). */
 static const float R127 = 1.0f / 127.0f;
 
-int oracle_abi_version(void) { return 1; }
+int oracle_abi_version(void) { return 2; }
 
 float oracle_r127(void) { return R127; }
 
@@ -113,17 +115,43 @@ void oracle_tile_centres(const float *q, int64_t n, int d, int tile, float *mu) 
     }
 }
 
+/* Shared centres of groups of G tiles, h3/htrc_flat.py:223-229: the tiles are padded to a
+ * multiple of G with repeats of the last tile (itself padded with repeats of the last row),
+ * and mu[g] is the mean of the G * tile rows of tiles gG .. gG + G - 1.
+ * Order fixed here: sequential fp32 sum over the group's rows j = 0 .. G*tile - 1, then IEEE
+ * division by G*tile (the HIP group_centres kernel sums in the same order). */
+void oracle_group_centres(const float *q, int64_t n, int d, int tile, int group, float *mu) {
+    int64_t nt = (n + tile - 1) / tile;
+    int64_t ng = (nt + group - 1) / group;
+    int rows = group * tile;
+#pragma omp parallel for schedule(static)
+    for (int64_t g = 0; g < ng; ++g) {
+        for (int i = 0; i < d; ++i) {
+            float s = 0.0f;
+            for (int j = 0; j < rows; ++j) {
+                int64_t t = g * group + j / tile;
+                if (t > nt - 1) t = nt - 1;
+                int64_t p = t * tile + j % tile;
+                if (p > n - 1) p = n - 1;
+                s += q[p * d + i];
+            }
+            mu[g * d + i] = s / (float)rows;
+        }
+    }
+}
+
 /* Row quantisation of q and dq = q - mu, h3/htrc_flat_triton.py:104-117 (tile kernel)
  * and :225-233 (rowmax kernel).  Rows are the padded tile rows: row p of tile t reads
- * query min(p, n-1) (the reference pads by repeating the last row, h3/htrc_flat.py:150-151). */
-void oracle_pack_q(const float *q, int64_t n, int d, int tile, const float *mu,
+ * query min(p, n-1) (the reference pads by repeating the last row, h3/htrc_flat.py:150-151).
+ * The centre of tile t is mu[t / group] (the tile kernel's gt = t // GR, :96). */
+void oracle_pack_q(const float *q, int64_t n, int d, int tile, int group, const float *mu,
                    int8_t *q8, float *sq, int8_t *dq8, float *sdq) {
     int64_t nt = (n + tile - 1) / tile;
 #pragma omp parallel for schedule(static)
     for (int64_t p = 0; p < nt * tile; ++p) {
         int64_t src = p < n ? p : n - 1;
         const float *row = q + src * d;
-        const float *m = mu + (p / tile) * d;
+        const float *m = mu + (p / tile / group) * d;
         float aq = 0.0f, adq = 0.0f;
         for (int i = 0; i < d; ++i) {
             float a = fabsf(row[i]);
@@ -213,19 +241,24 @@ static inline int32_t dot_i8(const int8_t *x, const int8_t *y, int d) {
     return s;
 }
 
-/* Row-max routing score, h3/htrc_flat_triton.py:214-254 (I8):
- *   SEL[t,l] = max_{r = 0, stride, ..} ( float(dq8_r . g8_tl) * (sdq_r * sg_tl) ) + lz_tl */
-void oracle_select(const int8_t *dq8, const float *sdq, int tile, int stride,
+/* Row-max routing score, h3/htrc_flat_triton.py:214-254 (I8), per group of G tiles over the
+ * group's G * tile rows (h3/htrc_flat.py:244-252 passes them as one row block):
+ *   SEL[g,l] = max_{r = 0, stride, ..} ( float(dq8_r . g8_gl) * (sdq_r * sg_gl) ) + lz_gl
+ * Rows of padded tiles (past the nt real ones) are those of the last tile. */
+void oracle_select(const int8_t *dq8, const float *sdq, int tile, int stride, int group, int64_t nt,
                    const int8_t *g8, const float *sg, const float *lz,
-                   int64_t nt, int64_t nb, int d, float *sel) {
-    int ts = tile / stride;
+                   int64_t ng, int64_t nb, int d, float *sel) {
+    int ts = group * tile / stride;
 #pragma omp parallel for schedule(static)
-    for (int64_t tl_ = 0; tl_ < nt * nb; ++tl_) {
-        int64_t t = tl_ / nb;
+    for (int64_t tl_ = 0; tl_ < ng * nb; ++tl_) {
+        int64_t gi = tl_ / nb;
         const int8_t *g = g8 + tl_ * d;
         float best = -INFINITY;
         for (int rr = 0; rr < ts; ++rr) {
-            int64_t p = t * tile + (int64_t)rr * stride;
+            int64_t j = (int64_t)rr * stride;
+            int64_t t = gi * group + j / tile;
+            if (t > nt - 1) t = nt - 1;
+            int64_t p = t * tile + j % tile;
             float x = (float)dot_i8(dq8 + p * d, g, d) * (sdq[p] * sg[tl_]);
             if (x > best) best = x;
         }
@@ -313,7 +346,7 @@ static void block_update(const float *sc, const uint16_t *const *vals, int nc, i
  *   far  score  float(dq8 . g8) * (sdq * sg) + lz,  value vb (bf16)
  *   near score  float(q8 . k8)  * ((sq * ks) * scale), value v (bf16)
  * Writes the partial (m, l, acc) of every (tile, split, row). */
-void oracle_tile(int64_t nt, int tile, int d, int64_t nb, int leaf, int kx,
+void oracle_tile(int64_t nt, int tile, int d, int64_t nb, int leaf, int kx, int group,
                  const int32_t *idx, const int8_t *excl,
                  const int8_t *q8, const float *sq, const int8_t *dq8, const float *sdq,
                  const int8_t *g8, const float *sg, const float *lz, const uint16_t *vb,
@@ -333,14 +366,15 @@ void oracle_tile(int64_t nt, int tile, int d, int64_t nb, int leaf, int kx,
             int sp = (int)((job / tile) % ns);
             int r = (int)(job % tile);
             int64_t p = t * tile + r;
+            int64_t gs = t / group;          /* the group's state and near set (gt = t // GR) */
             float m = -INFINITY, l = 0.0f;
             for (int i = 0; i < d; ++i) acc[i] = 0.0f;
             int64_t lo = sp * lps, hi = lo + lps < nb ? lo + lps : nb;
             for (int64_t n0 = lo; n0 < hi; n0 += bn) {
                 for (int c = 0; c < bn; ++c) {
                     int64_t cc = n0 + c;
-                    if (cc < hi && excl[t * nb + cc] == 0) {
-                        int64_t s = t * nb + cc;
+                    if (cc < hi && excl[gs * nb + cc] == 0) {
+                        int64_t s = gs * nb + cc;
                         sc[c] = (float)dot_i8(dq8 + p * d, g8 + s * d, d) * (sdq[p] * sg[s]) + lz[s];
                         vals[c] = vb + s * d;
                     } else {
@@ -356,7 +390,7 @@ void oracle_tile(int64_t nt, int tile, int d, int64_t nb, int leaf, int kx,
                 for (int c = 0; c < bn; ++c) {
                     int64_t j = e0 + c;
                     if (j < e_hi) {
-                        int64_t tok = (int64_t)idx[t * kx + j / leaf] * leaf + j % leaf;
+                        int64_t tok = (int64_t)idx[gs * kx + j / leaf] * leaf + j % leaf;
                         sc[c] = (float)dot_i8(q8 + p * d, k8 + tok * d, d) * ((sq[p] * ks[tok]) * scale);
                         vals[c] = v + tok * d;
                     } else {

@@ -4,7 +4,8 @@ Each function wraps one stage of the reference INT8 path and works on one head
 (NumPy arrays, bf16 as uint16 bits).  ``flat_i8`` chains the stages the way
 ``_flat_triton`` does (h3/htrc_flat.py:181-276) with the PROD knobs
 (h3/htrc_flat.py:391-392): store="int8", dot="bf16", curvature="lin",
-order="seq", group=1.  Tiles are independent, so ``tile_chunk`` does not enter.
+order="seq", and ``group`` tiles per shared centre (kern["group"], :223-231; 1 by default).
+Tiles are independent, so ``tile_chunk`` does not enter.
 """
 from __future__ import annotations
 
@@ -52,15 +53,18 @@ def lib():
         L.oracle_split.argtypes = [_i64, _i64, _i64]
         L.oracle_pack_k.argtypes = [_U16, _i64, _int, _I8, _F32]
         L.oracle_tile_centres.argtypes = [_F32, _i64, _int, _int, _F32]
-        L.oracle_pack_q.argtypes = [_F32, _i64, _int, _int, _F32, _I8, _F32, _I8, _F32]
+        L.oracle_group_centres.argtypes = [_F32, _i64, _int, _int, _int, _F32]
+        L.oracle_pack_q.argtypes = [_F32, _i64, _int, _int, _int, _F32, _I8, _F32, _I8, _F32]
         L.oracle_stats.argtypes = [_F32, _i64, _U16, _U16, _i64, _int, _int, _flt,
                                    _I8, _F32, _U16, _F32]
-        L.oracle_select.argtypes = [_I8, _F32, _int, _int, _I8, _F32, _F32, _i64, _i64, _int, _F32]
+        L.oracle_select.argtypes = [_I8, _F32, _int, _int, _int, _i64, _I8, _F32, _F32, _i64, _i64, _int, _F32]
         L.oracle_topk.argtypes = [_F32, _i64, _i64, _int, _int, _I32, _I8]
-        L.oracle_tile.argtypes = [_i64, _int, _int, _i64, _int, _int, _I32, _I8,
+        L.oracle_tile.argtypes = [_i64, _int, _int, _i64, _int, _int, _int, _I32, _I8,
                                   _I8, _F32, _I8, _F32, _I8, _F32, _F32, _U16,
                                   _I8, _F32, _U16, _flt, _int, _int, _F32, _F32, _F32]
         L.oracle_merge.argtypes = [_F32, _F32, _F32, _i64, _int, _int, _int, _F32, _F32]
+        if L.oracle_abi_version() != 2:
+            raise RuntimeError(f"{path} is stale (oracle ABI {L.oracle_abi_version()}): rebuild it")
         _lib = L
     return _lib
 
@@ -98,8 +102,21 @@ def tile_centres(q: np.ndarray, tile: int) -> np.ndarray:
     return mu
 
 
-def pack_q(q: np.ndarray, tile: int, mu: np.ndarray):
-    """Row int8 of q and q - mu over the padded tile rows (h3/htrc_flat_triton.py:104-117)."""
+def group_centres(q: np.ndarray, tile: int, group: int) -> np.ndarray:
+    """mu [ng, d], the mean of the padded rows of every group of ``group`` tiles
+    (h3/htrc_flat.py:223-229)."""
+    q = _c(q, np.float32)
+    n, d = q.shape
+    nt = -(-n // tile)
+    ng = -(-nt // group)
+    mu = np.empty((ng, d), np.float32)
+    lib().oracle_group_centres(q, n, d, tile, int(group), mu)
+    return mu
+
+
+def pack_q(q: np.ndarray, tile: int, mu: np.ndarray, group: int = 1):
+    """Row int8 of q and q - mu over the padded tile rows (h3/htrc_flat_triton.py:104-117);
+    tile t uses centre mu[t // group]."""
     q = _c(q, np.float32)
     n, d = q.shape
     nt = -(-n // tile)
@@ -108,7 +125,7 @@ def pack_q(q: np.ndarray, tile: int, mu: np.ndarray):
     dq8 = np.empty((rows, d), np.int8)
     sq = np.empty((rows,), np.float32)
     sdq = np.empty((rows,), np.float32)
-    lib().oracle_pack_q(q, n, d, tile, _c(mu, np.float32), q8, sq, dq8, sdq)
+    lib().oracle_pack_q(q, n, d, tile, int(group), _c(mu, np.float32), q8, sq, dq8, sdq)
     return q8, sq, dq8, sdq
 
 
@@ -127,13 +144,14 @@ def stats(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int, sca
     return g8, sg, vb, lz
 
 
-def select(dq8, sdq, tile: int, g8, sg, lz, stride: int = 1) -> np.ndarray:
-    """SEL [nt, nb] (h3/htrc_flat_triton.py:214-254, I8)."""
+def select(dq8, sdq, tile: int, g8, sg, lz, stride: int = 1, group: int = 1) -> np.ndarray:
+    """SEL [ng, nb] (h3/htrc_flat_triton.py:214-254, I8), the max over the rows of each group."""
     g8 = _c(g8, np.int8)
-    nt, nb, d = g8.shape
-    sel = np.empty((nt, nb), np.float32)
-    lib().oracle_select(_c(dq8, np.int8), _c(sdq, np.float32), tile, stride, g8,
-                        _c(sg, np.float32), _c(lz, np.float32), nt, nb, d, sel)
+    ng, nb, d = g8.shape
+    nt = dq8.shape[0] // tile
+    sel = np.empty((ng, nb), np.float32)
+    lib().oracle_select(_c(dq8, np.int8), _c(sdq, np.float32), tile, stride, int(group), nt, g8,
+                        _c(sg, np.float32), _c(lz, np.float32), ng, nb, d, sel)
     return sel
 
 
@@ -148,17 +166,19 @@ def topk(sel: np.ndarray, kx: int, sink: int = 0):
     return idx, excl
 
 
-def tile_partials(st: dict, *, tile: int, leaf: int, scale: float, splits: int, bn: int):
-    """Split partials (pm, pl, pacc) of the tile kernel (h3/htrc_flat_triton.py:88-211)."""
+def tile_partials(st: dict, *, tile: int, leaf: int, scale: float, splits: int, bn: int, group: int = 1):
+    """Split partials (pm, pl, pacc) of the tile kernel (h3/htrc_flat_triton.py:88-211); tile t
+    uses the state and near set of its group t // group."""
     g8 = st["g8"]
-    nt, nb, d = g8.shape
+    ng, nb, d = g8.shape
+    nt = st["dq8"].shape[0] // tile
     kx = st["idx"].shape[1]
-    idx = st["idx"] if kx else np.zeros((nt, 1), np.int32)
+    idx = st["idx"] if kx else np.zeros((ng, 1), np.int32)
     ns = max(1, int(splits))
     pm = np.empty((nt, ns, tile), np.float32)
     pl = np.empty((nt, ns, tile), np.float32)
     pacc = np.empty((nt, ns, tile, d), np.float32)
-    lib().oracle_tile(nt, tile, d, nb, leaf, kx, _c(idx, np.int32), _c(st["excl"], np.int8),
+    lib().oracle_tile(nt, tile, d, nb, leaf, kx, int(group), _c(idx, np.int32), _c(st["excl"], np.int8),
                       _c(st["q8"], np.int8), _c(st["sq"], np.float32),
                       _c(st["dq8"], np.int8), _c(st["sdq"], np.float32),
                       _c(g8, np.int8), _c(st["sg"], np.float32), _c(st["lz"], np.float32),
@@ -204,7 +224,7 @@ def tail_merge(out, logz, q, tk, tv, scale: float):
 
 def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: int = 64,
             splits: int = 4, bn: int = 64, sel_stride: int = 1, sink_leaves: int = 0,
-            scale: float | None = None, keep: bool = True) -> dict:
+            scale: float | None = None, keep: bool = True, group: int = 1) -> dict:
     """The INT8 flat operator for one head: q float32 (or bf16 bits) [n,d], k/v bf16 bits
     [nk,d] with nk % leaf == 0.  Returns every intermediate plus out [n,d] and logz [n]."""
     q = np.asarray(q)
@@ -219,17 +239,17 @@ def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: 
     kx = min(int(exact_leaves) + sink, nb)
     st: dict = {"v": _c(v_bits, np.uint16)}
     st["k8"], st["ks"] = pack_k(k_bits)
-    st["mu"] = tile_centres(qf, tile)
-    st["q8"], st["sq"], st["dq8"], st["sdq"] = pack_q(qf, tile, st["mu"])
+    st["mu"] = tile_centres(qf, tile) if group == 1 else group_centres(qf, tile, group)
+    st["q8"], st["sq"], st["dq8"], st["sdq"] = pack_q(qf, tile, st["mu"], group)
     st["g8"], st["sg"], st["vb"], st["lz"] = stats(st["mu"], k_bits, v_bits, leaf, scale)
     if kx > 0:
-        st["sel"] = select(st["dq8"], st["sdq"], tile, st["g8"], st["sg"], st["lz"], sel_stride)
+        st["sel"] = select(st["dq8"], st["sdq"], tile, st["g8"], st["sg"], st["lz"], sel_stride, group)
         st["idx"], st["excl"] = topk(st["sel"], kx, sink)
     else:
         nt = st["mu"].shape[0]
         st["idx"] = np.zeros((nt, 0), np.int32)
         st["excl"] = np.zeros((nt, nb), np.int8)
-    pm, pl, pacc = tile_partials(st, tile=tile, leaf=leaf, scale=scale, splits=splits, bn=bn)
+    pm, pl, pacc = tile_partials(st, tile=tile, leaf=leaf, scale=scale, splits=splits, bn=bn, group=group)
     out, logz = merge(pm, pl, pacc)
     st["out"], st["logz"] = out[:n], logz[:n]
     if keep:

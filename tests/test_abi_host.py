@@ -45,12 +45,12 @@ def test_nb_pad():
 _FAKE = ctypes.c_void_p(256)   # never dereferenced: validation fails before any launch
 
 
-@pytest.mark.parametrize("case", ["null", "dim", "leaf", "block", "leaves"])
+@pytest.mark.parametrize("case", ["null", "dim", "leaf", "block", "leaves", "group"])
 def test_launchers_reject_bad_arguments_on_host(case):
     lib = _lib.lib()
     f = _FAKE
     if case == "null":
-        rc = lib.htrc_pack_q(None, 1, 1, 64, 128, f, f, f, f, f, None)
+        rc = lib.htrc_pack_q(None, 1, 1, 64, 128, 1, f, f, f, f, f, None)
         msg = "null"
     elif case == "dim":
         rc = lib.htrc_pack_k(f, 1, 64, 64, f, f, None)
@@ -59,18 +59,21 @@ def test_launchers_reject_bad_arguments_on_host(case):
         rc = lib.htrc_leaf_stats(f, f, f, 1, 1, 96, 48, 128, 0.1, f, f, f, f, None)
         msg = "leaf"
     elif case == "block":
-        rc = lib.htrc_tile(*([f] * 13), 1, 64, 128, 64, 128, 1, 4, 48, 0.1, f, f, f, f, f, None)
+        rc = lib.htrc_tile(*([f] * 13), 1, 64, 128, 64, 128, 1, 1, 4, 48, 0.1, f, f, f, f, f, None)
         msg = "multiple of 32"
-    else:
-        rc = lib.htrc_route(*([f] * 11), 1, 64, 64 * 9000, 64, 128, 4, 0, 1, 0.1, f, f, None, f, None)
+    elif case == "leaves":
+        rc = lib.htrc_route(*([f] * 11), 1, 64, 64 * 9000, 64, 128, 4, 0, 1, 1, 0.1, f, f, None, f, None)
         msg = "8192"
+    else:
+        rc = lib.htrc_route_select(*([f] * 5), 1, 640, 640, 64, 128, 4, 0, 1, 0, f, f, None)
+        msg = "group"
     assert rc == 1
     assert msg in lib.htrc_last_error().decode()
 
 
 def test_call_maps_errors_to_value_error():
     with pytest.raises(ValueError, match="null"):
-        _lib.call("htrc_pack_q", None, 1, 1, 64, 128, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, None)
+        _lib.call("htrc_pack_q", None, 1, 1, 64, 128, 1, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, None)
 
 
 def test_split_and_buf_match_reference_semantics():
@@ -100,7 +103,7 @@ def _qkv(n=128, m=128, d=128):
     ({"tile": 32}, "tile=64"),
     ({"leaf": 48}, "leaf"),
     ({"quant": {"q": "int8"}}, "quant"),
-    ({"kern": {"group": 2}}, "group"),
+    ({"kern": {"group": 2000}}, "group"),
 ])
 def test_flat_attention_rejects_unimplemented_knobs(over, match):
     q, k, v = _qkv()

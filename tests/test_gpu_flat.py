@@ -120,3 +120,37 @@ def test_tail_merge_kernel_matches_oracle(device, ntail):
         assert np.abs(got - want).max() <= 2e-3 * np.abs(want).max()
         assert rel_l2(got, want) <= 1e-5 if ntail > 16 else rel_l2(got, want) <= 2e-4
         assert np.abs(lz[i].cpu().numpy() - wz).max() <= 2e-5 * (1 + np.abs(wz).max())
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("n,group,stride", [(8192, 2, 1), (5000, 4, 1), (4096, 3, 4)])
+def test_group_centres_vs_oracle(device, fused, n, group, stride):
+    """kern["group"] (h3/htrc_flat.py:223-231): G tiles share one centre, state and near set.
+    The group centres, packed rows and SEL are bit-exact; routing per group as above."""
+    leaf, ex = 64, 12
+    nk = (n // leaf) * leaf
+    q, k, v = workloads.clustered_runs(n=n, runs=max(1, n // 64), heads=1, seed=n + group)
+    k, v = k[:, :nk].contiguous(), v[:, :nk].contiguous()
+    st = {}
+    out, logz = htrc_flat.flat_attention(q[0].to(device), k[0].to(device), v[0].to(device), backend="hip",
+                                         store="int8", dot="bf16", leaf=leaf, exact_leaves=ex, splits=4,
+                                         sel_stride=stride, kern={"fused": fused, "tile_bn": 64, "group": group},
+                                         return_logz=True, state=st)
+    torch.cuda.synchronize()
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=ex,
+                          splits=1 if fused else 4, bn=64, sel_stride=stride, group=group)
+    assert np.array_equal(st["mu"][0].cpu().numpy(), ref["mu"])
+    assert np.array_equal(st["dq8"][0].cpu().numpy(), ref["dq8"])
+    assert np.array_equal(st["sdq"][0].cpu().numpy(), ref["sdq"])
+    if not fused:
+        # SEL from the GPU state vs the oracle's select on that same state: bit-exact
+        nb = ref["g8"].shape[1]
+        g8 = st["g8"][0, :, :nb].cpu().numpy()
+        sg = st["sg"][0, :, :nb].cpu().numpy()
+        lz = st["lz"][0, :, :nb].cpu().numpy()
+        want = flat_i8.select(ref["dq8"], ref["sdq"], 64, g8, sg, lz, stride, group)
+        assert np.array_equal(st["sel"][0, :, :nb].cpu().numpy().view(np.uint32), want.view(np.uint32))
+    mism = _routing_check(st["idx"][0].cpu().numpy(), ref)
+    assert mism <= max(1, ref["idx"].shape[0] // 50)
+    assert rel_l2(out.cpu().numpy(), ref["out"]) <= OUT_REL_L2
+    assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS

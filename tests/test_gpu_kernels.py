@@ -99,10 +99,10 @@ def test_pack_edge_rows(device):
     assert np.array_equal(_np(k8[0]), ok8) and np.array_equal(_np(ks[0]).view(np.uint32), oks.view(np.uint32))
 
 
-def _oracle_state(q, k, v, leaf, ex, splits=4, bn=64, stride=1, sink=0):
+def _oracle_state(q, k, v, leaf, ex, splits=4, bn=64, stride=1, sink=0, group=1):
     return flat_i8.flat_i8(bits(q[0]) if q.dtype == torch.bfloat16 else q[0].numpy(), bits(k[0]), bits(v[0]),
                            tile=64, leaf=leaf, exact_leaves=ex, splits=splits, bn=bn, sel_stride=stride,
-                           sink_leaves=sink)
+                           sink_leaves=sink, group=group)
 
 
 @pytest.mark.parametrize("leaf", [64, 32, 128, 16])
@@ -245,3 +245,47 @@ def test_route_on_oracle_state(device, leaf, ex):
         assert np.array_equal(_np(idx[0]), ref["idx"])
     assert rel_l2(_np(out[0]), ref["out"]) <= OUT_REL_L2
     assert np.abs(_np(logz[0]) - ref["logz"]).max() <= LOGZ_ABS
+
+
+@pytest.mark.parametrize("nq,group", [(4096, 2), (1000, 4), (64 * 9 + 3, 8), (64, 3)])
+@pytest.mark.parametrize("qdtype", ["bf16", "fp32"])
+def test_pack_group_centres_bitexact(device, nq, group, qdtype):
+    """Shared centres of G tiles (h3/htrc_flat.py:223-229): mean of the G * 64 padded rows in
+    the oracle's order, and the rows' q - mu against their group's centre."""
+    q, _, _ = _data(max(nq, 256), nk=256, seed=nq + group)
+    q = q[:, :nq]
+    if qdtype == "fp32":
+        q = q.float() + 1e-3 * torch.randn(q.shape, generator=torch.Generator().manual_seed(3))
+    mu, q8, sq, dq8, sdq = hip.pack_q(q.to(device).contiguous(), group=group)
+    torch.cuda.synchronize()
+    qf = q[0].float().numpy()
+    omu = flat_i8.group_centres(qf, 64, group)
+    oq8, osq, odq8, osdq = flat_i8.pack_q(qf, 64, omu, group)
+    assert np.array_equal(_np(mu[0]).view(np.uint32), omu.view(np.uint32))
+    for a, b in ((q8, oq8), (sq, osq), (dq8, odq8), (sdq, osdq)):
+        assert np.array_equal(_np(a[0]), b)
+
+
+@pytest.mark.parametrize("group,ex,stride", [(2, 8, 1), (4, 16, 1), (3, 5, 2), (16, 8, 1)])
+def test_route_on_oracle_group_state(device, group, ex, stride):
+    """Route kernels with G tiles per state row, on the oracle's state: idx is the oracle's
+    per-group top-k exactly (select over every row of the group's tiles), the output within
+    the stated bar, and the split tile kernel agrees."""
+    n, leaf = 64 * 37 + 11, 64
+    q, k, v = _data(n, nk=64 * 40, seed=group * 10 + ex)
+    ref = _oracle_state(q, k, v, leaf, ex, splits=1, bn=64, stride=stride, group=group)
+    packed, state, excl, _ = _device_state(ref, q, k, v, device)
+    kx = ref["idx"].shape[1]
+    ng = ref["g8"].shape[0]
+    idx = torch.full((1, ng, kx), -1, dtype=torch.int32, device=device)
+    out, logz = hip.route(packed, state, nq=n, leaf=leaf, kx=kx, scale=1 / math.sqrt(128), stride=stride,
+                          idx=idx, group=group)
+    torch.cuda.synchronize()
+    assert np.array_equal(_np(idx[0]), ref["idx"])
+    assert rel_l2(_np(out[0]), ref["out"]) <= OUT_REL_L2
+    assert np.abs(_np(logz[0]) - ref["logz"]).max() <= LOGZ_ABS
+    out2, logz2 = hip.tile_attention(packed, state, excl, idx, nq=n, leaf=leaf, scale=1 / math.sqrt(128),
+                                     splits=1, bn=64, group=group)
+    torch.cuda.synchronize()
+    assert rel_l2(_np(out2[0]), ref["out"]) <= OUT_REL_L2
+    assert np.abs(_np(logz2[0]) - ref["logz"]).max() <= LOGZ_ABS
