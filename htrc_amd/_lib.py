@@ -13,7 +13,7 @@ import torch
 
 HERE = Path(__file__).resolve().parent
 LIBPATH = HERE / "libhtrc_flat.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -36,6 +36,7 @@ SIGNATURES = {
     "htrc_route_attend": [_vp] * 13 + [_i64, _i64, _i64, _int, _int, _int, _int, _flt, _vp, _vp, _vp],
     "htrc_route": [_vp] * 11 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _flt, _vp, _vp, _vp, _vp, _vp],
     "htrc_tail": [_vp, _int, _vp, _vp, _i64, _i64, _i64, _int, _flt, _vp, _vp, _vp],
+    "htrc_dequant_rows": [_vp, _i64, _vp, _i64, _i64, _int, _vp, _int, _vp],
     "htrc_selftest_mfma": [_vp] * 7,
 }
 _RESTYPES = {"htrc_last_error": ctypes.c_char_p}

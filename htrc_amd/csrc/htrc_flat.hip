@@ -1502,6 +1502,34 @@ __global__ __launch_bounds__(256) void tail_kernel(const void* __restrict__ q, c
 // (A row m = lane%16 with k-set lane/16, B column n = lane%16 with the same k-set,
 // C[4*(lane/16) + i][lane%16] in item i).
 // ---------------------------------------------------------------------------------------------
+// ---------------------------------------------------------------------------------------------
+// dequant_rows: out[r, :] = e4m3(x8[r, :]) * scale[r] (h3/htrc_flat_triton.py:276-294), the
+// per-token fp8 cache to bf16 (or fp32) in one pass.  Rows of x8 and scale may be strided
+// views; out is contiguous [rows, d].  One thread per element, consecutive threads on
+// consecutive elements of a row.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {   // OCP e4m3fn: bias 7, no infinities
+    const uint32_t sgn = (b & 0x80u) << 24, e = (b >> 3) & 15u, m = b & 7u;
+    if (e == 15u && m == 7u) return __uint_as_float(sgn | 0x7fc00000u);                    // NaN
+    if (e == 0u) return __uint_as_float(sgn | __float_as_uint((float)m * 0.001953125f));   // m * 2^-9
+    return __uint_as_float(sgn | ((e + 120u) << 23) | (m << 20));
+}
+
+template <bool OUT_BF16>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ x8, int64_t stride_x,
+                                                      const float* __restrict__ scale, int64_t stride_s,
+                                                      int64_t rows, int d, void* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * d) return;
+    const int64_t r = i / d;
+    const int c = (int)(i - r * d);
+    const float y = __fmul_rn(e4m3_to_f32(x8[r * stride_x + c]), scale[r * stride_s]);
+    if (OUT_BF16)
+        ((uint16_t*)out)[i] = (uint16_t)f2bf(y);
+    else
+        ((float*)out)[i] = y;
+}
+
 __global__ __launch_bounds__(64) void selftest_mfma_kernel(const int8_t* __restrict__ ai, const int8_t* __restrict__ bi,
                                                            int32_t* __restrict__ ci, const uint16_t* __restrict__ af,
                                                            const uint16_t* __restrict__ bf, float* __restrict__ cf) {
@@ -1812,6 +1840,23 @@ int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, in
         hipLaunchKernelGGL(tail_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, q, tk, tv, nq, (int)ntail,
                            scale, out, logz);
     return launched("htrc_tail");
+}
+
+int htrc_dequant_rows(const uint8_t* x8, int64_t stride_x, const float* scale, int64_t stride_s, int64_t rows,
+                      int d, void* out, int out_is_bf16, void* stream) {
+    REQUIRE(x8 && scale && out, "htrc_dequant_rows: null pointer");
+    REQUIRE(rows >= 0 && d > 0 && stride_x >= d && stride_s >= 0, "htrc_dequant_rows: bad sizes or strides");
+    REQUIRE(rows * (int64_t)d <= ((int64_t)1 << 40), "htrc_dequant_rows: too many elements");
+    if (rows == 0) return HTRC_OK;
+    const int64_t nblk = (rows * d + 255) / 256;
+    REQUIRE(nblk <= 0x7fffffff, "htrc_dequant_rows: too many elements for one launch");
+    if (out_is_bf16)
+        hipLaunchKernelGGL(dequant_kernel<true>, dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, x8, stride_x,
+                           scale, stride_s, rows, d, out);
+    else
+        hipLaunchKernelGGL(dequant_kernel<false>, dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, x8,
+                           stride_x, scale, stride_s, rows, d, out);
+    return launched("htrc_dequant_rows");
 }
 
 int htrc_selftest_mfma(const int8_t* ai, const int8_t* bi, int32_t* ci, const uint16_t* af, const uint16_t* bf,

@@ -271,6 +271,30 @@ def tail_merge(q, tk, tv, *, scale: float, out, logz):
     return out, logz
 
 
+def dequant_rows(x8, scale, out, br=64):
+    """out[r, :] = x8[r, :] * scale[r] in one pass, fp8 (e4m3fn) -> out's dtype (bf16 or fp32)
+    (h3/htrc_flat_triton.py:287-294).  x8 [rows, D] and scale [rows] may be strided head
+    views of the per-token cache; out [rows, D] contiguous.  ``br`` is accepted for call
+    compatibility."""
+    if x8.dtype != torch.float8_e4m3fn:
+        raise ValueError("x8 must be float8_e4m3fn")
+    if x8.dim() != 2 or x8.stride(1) != 1:
+        raise ValueError("x8 must be [rows, D] with unit stride along D")
+    rows, d = int(x8.shape[0]), int(x8.shape[1])
+    if scale.dim() != 1 or int(scale.shape[0]) != rows:
+        raise ValueError("scale must be [rows]")
+    if scale.dtype != torch.float32:
+        scale = scale.float()
+    if out.dtype not in (torch.bfloat16, torch.float32) or tuple(out.shape) != (rows, d) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [rows, D] bf16 or fp32 tensor")
+    for t, n in ((x8, "x8"), (scale, "scale"), (out, "out")):
+        if t.device.type != "cuda":
+            raise ValueError(f"{n} must be on a HIP device (got {t.device})")
+    call("htrc_dequant_rows", ptr(x8), int(x8.stride(0)) if rows > 1 else d, ptr(scale), int(scale.stride(0)), rows, d,
+         ptr(out), int(out.dtype == torch.bfloat16), stream_handle(out.device))
+    return out
+
+
 def selftest_mfma(ai, bi, af, bf):
     """Run the MFMA convention self-test kernel -> (ci int32 [16,16], cf fp32 [16,16])."""
     dev = ai.device

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 6
+#define HTRC_ABI_VERSION 7
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -120,6 +120,13 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
  * Replaces the tail handling of tile_attention (h3/htrc_flat_triton.py:187-207, 366-388). */
 int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
               int64_t ntail, int d, float scale, float* out, float* logz, void* stream);
+
+/* fp8 rows to bf16 (out_is_bf16 = 1) or fp32: out[r, :] = e4m3fn(x8[r, :]) * scale[r], rounded
+ * to nearest even.  x8 rows are stride_x bytes apart and scale entries stride_s floats apart
+ * (strided head views of a per-token cache); out is contiguous [rows, d].
+ * Replaces dequant_rows / _dequant_kernel (h3/htrc_flat_triton.py:276-294). */
+int htrc_dequant_rows(const uint8_t* x8, int64_t stride_x, const float* scale, int64_t stride_s, int64_t rows,
+                      int d, void* out, int out_is_bf16, void* stream);
 
 /* Self-test of the MFMA operand conventions the kernels rely on (no reference counterpart):
  * one 64-lane wave computes C = A B for A int8 [16, 64] / B int8 [64, 16] (i8 path) and

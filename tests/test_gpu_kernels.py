@@ -289,3 +289,24 @@ def test_route_on_oracle_group_state(device, group, ex, stride):
     torch.cuda.synchronize()
     assert rel_l2(_np(out2[0]), ref["out"]) <= OUT_REL_L2
     assert np.abs(_np(logz2[0]) - ref["logz"]).max() <= LOGZ_ABS
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_dequant_rows_all_patterns(device, out_dtype):
+    """dequant_rows (h3/htrc_flat_triton.py:276-294) from strided head views of a per-token
+    cache: every e4m3fn bit pattern (NaN included) times its row scale equals torch's own
+    float8_e4m3fn decode times the scale, rounded to out's dtype."""
+    rows, heads, d = 96, 3, 256
+    g = torch.Generator().manual_seed(1)
+    cache = torch.randint(0, 256, (rows, heads, d), dtype=torch.uint8, generator=g)
+    cache[0, 1, :] = torch.arange(256, dtype=torch.uint8)
+    scales = torch.rand((rows, heads), generator=g) * 4 + 0.01
+    x8 = cache.view(torch.float8_e4m3fn)[:, 1, :]
+    want = (x8.float() * scales[:, 1, None]).to(out_dtype)
+    dx8 = cache.to(device).view(torch.float8_e4m3fn)[:, 1, :]
+    dsc = scales.to(device)[:, 1]
+    assert dx8.stride(0) == heads * d and dsc.stride(0) == heads
+    out = torch.empty((rows, d), dtype=out_dtype, device=device)
+    hip.dequant_rows(dx8, dsc, out)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu(), want, rtol=0, atol=0, equal_nan=True)
