@@ -36,6 +36,14 @@ __device__ __forceinline__ u32x2 pack8_i8(const int (&c)[8]) {
     return u32x2{pack4_i8(c[0], c[1], c[2], c[3]), pack4_i8(c[4], c[5], c[6], c[7])};
 }
 
+// Query row of operator row p of head h under an optional permutation (order="kmeans"); entries
+// are clamped to the head, so a malformed permutation cannot address outside it.
+__device__ __forceinline__ int64_t perm_row(const int32_t* perm, int64_t h, int64_t nq, int64_t p) {
+    if (!perm) return p;
+    const int64_t r = perm[h * nq + p];
+    return r < 0 ? 0 : (r >= nq ? nq - 1 : r);
+}
+
 // Shared centres of tile groups (h3/htrc_flat.py:223-229): mu_g is the mean of the G * 64 rows
 // of tiles gG .. gG + G - 1, where tiles past the last repeat the last tile and rows past the
 // last query repeat the last query (the reference pads the tiles, then averages every padded
@@ -43,7 +51,8 @@ __device__ __forceinline__ u32x2 pack8_i8(const int (&c)[8]) {
 // division.
 template <bool IN_BF16>
 __global__ __launch_bounds__(128) void group_centres_kernel(const void* __restrict__ qin, int64_t nq, int nt,
-                                                            int group, int ng, float* __restrict__ mu) {
+                                                            int group, int ng, const int32_t* __restrict__ perm,
+                                                            float* __restrict__ mu) {
     const int g = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
     const int64_t qbase = (int64_t)h * nq * D;
     const int rows = group * TILE;
@@ -54,7 +63,8 @@ __global__ __launch_bounds__(128) void group_centres_kernel(const void* __restri
         for (int u = 0; u < 8; ++u) {
             const int j = j0 + u;
             const int t = min(g * group + j / TILE, nt - 1);
-            const int64_t p = min((int64_t)t * TILE + j % TILE, nq - 1);
+            const int64_t pp = min((int64_t)t * TILE + j % TILE, nq - 1);
+            const int64_t p = perm_row(perm, h, nq, pp);
             x[u] = IN_BF16 ? bf2f(((const uint16_t*)qin)[qbase + p * D + i]) : ((const float*)qin)[qbase + p * D + i];
         }
 #pragma unroll
@@ -64,10 +74,12 @@ __global__ __launch_bounds__(128) void group_centres_kernel(const void* __restri
 }
 
 // group == 1: the tile's centre over its real rows is computed here and written to mu; group > 1:
-// the group's centre is read from mu (group_centres_kernel).
+// the group's centre is read from mu (group_centres_kernel).  perm (optional): row p of the
+// operator is query perm[p] (order="kmeans").
 template <bool IN_BF16>
 __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qin, int64_t nq, int nt, int group,
-                                                     int ng, float* __restrict__ mu, int8_t* __restrict__ q8,
+                                                     int ng, const int32_t* __restrict__ perm,
+                                                     float* __restrict__ mu, int8_t* __restrict__ q8,
                                                      float* __restrict__ sq, int8_t* __restrict__ dq8,
                                                      float* __restrict__ sdq) {
     __shared__ __align__(16) float tq[TILE][D + 4];
@@ -79,7 +91,8 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
 #pragma unroll
     for (int j = 0; j < 4; ++j) {               // 8 consecutive values per thread and chunk
         const int c = tid + 256 * j, r = c >> 4, c8 = (c & 15) * 8;
-        const int64_t src = qbase + (r0 + r < nq ? r0 + r : nq - 1) * D + c8;   // pad rows repeat the last row
+        const int64_t pr = r0 + r < nq ? r0 + r : nq - 1;                      // pad rows repeat the last row
+        const int64_t src = qbase + perm_row(perm, h, nq, pr) * D + c8;
         f32x4 lo, hi;
         if (IN_BF16) {
             const u32x4 u = *(const u32x4*)((const uint16_t*)qin + src);
@@ -886,8 +899,9 @@ __global__ __launch_bounds__(256) void tile_kernel(
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ excl,
     const int32_t* __restrict__ idx, const int8_t* __restrict__ k8, const float* __restrict__ ks,
-    const uint16_t* __restrict__ v, int64_t nq, int nt, int group, int ng, int64_t nk, int nb, int nb_pad, int kx,
-    int lps, int eps, float scale, float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc,
+    const uint16_t* __restrict__ v, int64_t nq, int nt, int group, int ng, const int32_t* __restrict__ perm,
+    int64_t nk, int nb, int nb_pad, int kx, int lps, int eps, float scale, float* __restrict__ pm,
+    float* __restrict__ pl, float* __restrict__ pacc,
     float* __restrict__ out, float* __restrict__ logz) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int t = blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
@@ -911,7 +925,8 @@ __global__ __launch_bounds__(256) void tile_kernel(
     const float ltot = grp_sum(st.l);
     if (pacc == nullptr) {   // single split: normalise in place
         const int64_t qi = (int64_t)t * TILE + r;
-        write_final(st, ltot, (int64_t)h * nq + qi, qi < nq, out, logz);
+        const int64_t oq = qi < nq ? perm_row(perm, h, nq, qi) : qi;
+        write_final(st, ltot, (int64_t)h * nq + oq, qi < nq, out, logz);
         return;
     }
     const int64_t base = (th * ns + sp) * TILE + r;
@@ -926,7 +941,8 @@ __global__ __launch_bounds__(256) void tile_kernel(
 // merge: (h3/htrc_flat_triton.py:257-273) + logZ = mm + log(den).  One workgroup per tile.
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
                                                     const float* __restrict__ pacc, int ns, int64_t nq, int nt,
-                                                    float* __restrict__ out, float* __restrict__ logz) {
+                                                    const int32_t* __restrict__ perm, float* __restrict__ out,
+                                                    float* __restrict__ logz) {
     const int t = blockIdx.x, h = blockIdx.y;
     const int64_t th = (int64_t)h * nt + t;
     const int r = threadIdx.x >> 2, part = threadIdx.x & 3;   // 4 threads per row, 32 dims each
@@ -951,7 +967,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm
         }
     }
     const float dd = den < 1e-30f ? 1e-30f : den;
-    const int64_t orow = (int64_t)h * nq + qi;
+    const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
 #pragma unroll
     for (int i = 0; i < 32; i += 4) {
         f32x4 o = {__fdiv_rn(num[i], dd), __fdiv_rn(num[i + 1], dd), __fdiv_rn(num[i + 2], dd),
@@ -1163,8 +1179,8 @@ __global__ __launch_bounds__(512) void route_kernel(
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ k8,
     const float* __restrict__ ks, const uint16_t* __restrict__ v, const int32_t* __restrict__ idx,
-    const float* __restrict__ rowmax, int64_t nq, int nt, int group, int ng, int64_t nk, int nb, int nb_pad, int kxe,
-    float scale, float* __restrict__ out, float* __restrict__ logz) {
+    const float* __restrict__ rowmax, int64_t nq, int nt, int group, int ng, const int32_t* __restrict__ perm, int64_t nk,
+    int nb, int nb_pad, int kxe, float scale, float* __restrict__ out, float* __restrict__ logz) {
     __shared__ __align__(16) char ring[4][RING_SLOTS][SLOT_BYTES];   // one per wave pair; also merge staging
     __shared__ int32_t sidx[MAX_KX_LDS];
     __shared__ uint32_t exbits[MAX_NB_LDS / 32 + 1];
@@ -1419,7 +1435,7 @@ __global__ __launch_bounds__(512) void route_kernel(
     const float inv = 1.0f / (den < 1e-30f ? 1e-30f : den);
     const int64_t qi = (int64_t)t * TILE + r_out;
     if (qi < nq) {
-        const int64_t orow = (int64_t)h * nq + qi;
+        const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int dl = 16 * part + 4 * u;
@@ -1502,6 +1518,183 @@ __global__ __launch_bounds__(256) void tail_kernel(const void* __restrict__ q, c
 // (A row m = lane%16 with k-set lane/16, B column n = lane%16 with the same k-set,
 // C[4*(lane/16) + i][lane%16] in item i).
 // ---------------------------------------------------------------------------------------------
+// ---------------------------------------------------------------------------------------------
+// k-means query order (h3/htrc_flat.py:47-61): Lloyd's k-means on an even sample of the
+// queries, every query assigned to its nearest centre, and the rows ordered by centre (stable).
+//   sample i: row round(linspace(0, n - 1, m)[i]), m = min(sample, n), in torch's float32
+//   device linspace (step = (n - 1) / (m - 1); i < m / 2: i step, else the fused
+//   (n - 1) - (m - 1 - i) step), rounded to nearest even; initial centre j: sample
+//   round(linspace(0, m - 1, C)[j]).
+//   distance: sequential fp32 sum over the dims of (x - c)^2, ties to the lower centre (the
+//   reference ranks sqrt of the matrix-product form; both give the same order except where
+//   two centres tie to rounding).
+//   update: per centre, the sequential fp32 sum of its samples in sample order divided by their
+//   count; a centre without samples keeps its position.
+// ---------------------------------------------------------------------------------------------
+constexpr int KM_MAX_C = 64;           // clusters
+constexpr int KM_MAX_SAMPLE = 16384;   // sample rows
+
+__device__ __forceinline__ int64_t linspace_round(int64_t hi, int64_t steps, int64_t i) {
+    if (steps <= 1) return 0;
+    const float step = __fdiv_rn((float)hi, (float)(steps - 1));
+    // lower half step * i; upper half hi - step * (steps - 1 - i) in one fused multiply-add, as
+    // torch's device kernel computes it (checked against torch.linspace on this GPU)
+    const float v = i < steps / 2 ? __fmul_rn(step, (float)i) : __fmaf_rn(-step, (float)(steps - 1 - i), (float)hi);
+    const int64_t r = (int64_t)rintf(v);
+    return r < 0 ? 0 : (r > hi ? hi : r);      // (float)hi may round above hi for hi >= 2^24
+}
+
+template <bool IN_BF16>
+__device__ __forceinline__ float qval(const void* q, int64_t idx) {
+    return IN_BF16 ? bf2f(((const uint16_t*)q)[idx]) : ((const float*)q)[idx];
+}
+
+template <bool IN_BF16>
+__global__ __launch_bounds__(128) void km_init_kernel(const void* __restrict__ q, int64_t nq, int m, int C,
+                                                      float* __restrict__ cen) {
+    const int j = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
+    const int64_t row = linspace_round(nq - 1, m, linspace_round(m - 1, C, j));
+    cen[((int64_t)h * C + j) * D + i] = qval<IN_BF16>(q, ((int64_t)h * nq + row) * D + i);
+}
+
+// Nearest centre of 64 rows (of the sample when sm > 0, else of the queries): four lanes per
+// row, lane `part` taking centres part, part + 4, ..; rows and centres staged in LDS.
+template <bool IN_BF16>
+__global__ __launch_bounds__(256) void km_assign_kernel(const void* __restrict__ q, int64_t nq, int64_t nrows, int sm,
+                                                        int C, const float* __restrict__ cen,
+                                                        int32_t* __restrict__ assign) {
+    __shared__ __align__(16) float xs[64][D + 4];
+    __shared__ __align__(16) float cs[KM_MAX_C][D + 4];
+    const int h = blockIdx.y, tid = threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.x * 64;
+    for (int e = tid; e < C * D; e += 256) cs[e / D][e % D] = cen[(int64_t)h * C * D + e];
+    for (int e = tid; e < 64 * (D / 4); e += 256) {
+        const int r = e / (D / 4), c4 = (e % (D / 4)) * 4;
+        const int64_t ri = r0 + r < nrows ? r0 + r : nrows - 1;
+        const int64_t row = sm > 0 ? linspace_round(nq - 1, sm, ri) : ri;
+        const int64_t base = ((int64_t)h * nq + row) * D + c4;
+        f32x4 x;
+        if (IN_BF16) {
+            const u32x2 u = *(const u32x2*)((const uint16_t*)q + base);
+            x = f32x4{bf2f(u.x & 0xffffu), bf2f(u.x >> 16), bf2f(u.y & 0xffffu), bf2f(u.y >> 16)};
+        } else {
+            x = *(const f32x4*)((const float*)q + base);
+        }
+        *(f32x4*)&xs[r][c4] = x;
+    }
+    __syncthreads();
+    const int r = tid >> 2, part = tid & 3;
+    float best = INFINITY;
+    int bj = C;
+    for (int j = part; j < C; j += 4) {
+        float acc = 0.0f;
+        for (int d0 = 0; d0 < D; d0 += 4) {
+            const f32x4 x = *(const f32x4*)&xs[r][d0], c = *(const f32x4*)&cs[j][d0];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float df = __fsub_rn(x[u], c[u]);
+                acc = __fadd_rn(acc, __fmul_rn(df, df));
+            }
+        }
+        if (acc < best) {            // centres visited in increasing order: ties keep the lower
+            best = acc;
+            bj = j;
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 4; o <<= 1) {   // the row's four lanes: lowest distance, then lowest centre
+        const float ob = __shfl_xor(best, o);
+        const int oj = __shfl_xor(bj, o);
+        if (ob < best || (ob == best && oj < bj)) {
+            best = ob;
+            bj = oj;
+        }
+    }
+    if (bj < 0 || bj >= C) bj = 0;      // no finite distance (non-finite rows): centre 0
+    if (part == 0 && r0 + r < nrows) assign[(int64_t)h * nq + r0 + r] = bj;
+}
+
+// New centre j: the samples assigned to j (listed in sample order by a ballot compaction) summed
+// in that order and divided by their count.
+template <bool IN_BF16>
+__global__ __launch_bounds__(128) void km_update_kernel(const void* __restrict__ q, int64_t nq, int m, int C,
+                                                        const int32_t* __restrict__ assign,
+                                                        float* __restrict__ cen) {
+    __shared__ int32_t list[KM_MAX_SAMPLE];
+    __shared__ int wcnt[2];
+    const int j = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    int cnt = 0;
+    for (int i0 = 0; i0 < m; i0 += 128) {
+        const int i = i0 + tid;
+        const bool hit = i < m && assign[(int64_t)h * nq + i] == j;
+        const uint64_t bal = __ballot(hit);
+        if (lane == 0) wcnt[w] = __popcll(bal);
+        __syncthreads();
+        if (hit) list[cnt + (w ? wcnt[0] : 0) + __popcll(bal & ((1ull << lane) - 1ull))] = i;
+        cnt += wcnt[0] + wcnt[1];
+        __syncthreads();
+    }
+    float acc = 0.0f;
+    for (int k0 = 0; k0 < cnt; k0 += 8) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            x[u] = k0 + u < cnt ? qval<IN_BF16>(q, ((int64_t)h * nq + linspace_round(nq - 1, m, list[k0 + u])) * D + tid)
+                                : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (k0 + u < cnt) acc = __fadd_rn(acc, x[u]);
+    }
+    if (cnt > 0) cen[((int64_t)h * C + j) * D + tid] = __fdiv_rn(acc, (float)cnt);
+}
+
+// perm = the rows ordered by centre, the rows of one centre in row order (stable counting sort
+// of one head per workgroup: histogram, prefix, then 1024-row chunks placed with ballot ranks).
+__global__ __launch_bounds__(1024) void km_sort_kernel(const int32_t* __restrict__ assign, int64_t nq, int C,
+                                                       int32_t* __restrict__ perm) {
+    __shared__ uint32_t cnt[KM_MAX_C], base[KM_MAX_C];
+    __shared__ uint32_t wc[16][KM_MAX_C];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int32_t* a = assign + (int64_t)h * nq;
+    int32_t* out = perm + (int64_t)h * nq;
+    auto centre = [&](int64_t p) { const int c = a[p]; return c >= 0 && c < C ? c : 0; };
+    if (tid < C) cnt[tid] = 0u;
+    __syncthreads();
+    for (int64_t p = tid; p < nq; p += 1024) atomicAdd(&cnt[centre(p)], 1u);
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t acc = 0u;
+        for (int c = 0; c < C; ++c) {
+            base[c] = acc;
+            acc += cnt[c];
+        }
+    }
+    __syncthreads();
+    for (int64_t p0 = 0; p0 < nq; p0 += 1024) {
+        const int64_t p = p0 + tid;
+        const int c = p < nq ? centre(p) : -1;
+        uint32_t rank = 0u;
+        for (int cc = 0; cc < C; ++cc) {
+            const uint64_t bal = __ballot(c == cc);
+            if (lane == 0) wc[w][cc] = (uint32_t)__popcll(bal);
+            if (c == cc) rank = (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
+        }
+        __syncthreads();
+        if (c >= 0) {
+            uint32_t pos = base[c] + rank;
+            for (int ww = 0; ww < w; ++ww) pos += wc[ww][c];
+            out[pos] = (int32_t)p;
+        }
+        __syncthreads();
+        if (tid < C) {
+            uint32_t acc = 0u;
+            for (int ww = 0; ww < 16; ++ww) acc += wc[ww][tid];
+            base[tid] += acc;
+        }
+        __syncthreads();
+    }
+}
+
 // ---------------------------------------------------------------------------------------------
 // dequant_rows: out[r, :] = e4m3(x8[r, :]) * scale[r] (h3/htrc_flat_triton.py:276-294), the
 // per-token fp8 cache to bf16 (or fp32) in one pass.  Rows of x8 and scale may be strided
@@ -1589,8 +1782,8 @@ const char* htrc_last_error(void) { return g_err; }
 
 int htrc_nb_pad(int64_t nb) { return (int)((nb + 31) / 32 * 32); }
 
-int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, float* mu, int8_t* q8,
-                float* sq, int8_t* dq8, float* sdq, void* stream) {
+int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, const int32_t* perm,
+                float* mu, int8_t* q8, float* sq, int8_t* dq8, float* sdq, void* stream) {
     REQUIRE(q && mu && q8 && sq && dq8 && sdq, "htrc_pack_q: null pointer");
     REQUIRE(d == D, "htrc_pack_q: head dim must be 128");
     REQUIRE(heads > 0 && heads <= 65535 && nq > 0, "htrc_pack_q: bad heads / rows");
@@ -1603,17 +1796,18 @@ int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, 
     if (group > 1) {
         const dim3 gg((unsigned)ng, (unsigned)heads);
         if (q_is_bf16)
-            hipLaunchKernelGGL(group_centres_kernel<true>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, mu);
+            hipLaunchKernelGGL(group_centres_kernel<true>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, perm, mu);
         else
-            hipLaunchKernelGGL(group_centres_kernel<false>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, mu);
+            hipLaunchKernelGGL(group_centres_kernel<false>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, perm,
+                               mu);
     }
     dim3 grid((unsigned)nt, (unsigned)heads);
     if (q_is_bf16)
-        hipLaunchKernelGGL(pack_q_kernel<true>, grid, dim3(256), 0, s, q, nq, (int)nt, group, (int)ng, mu, q8, sq,
-                           dq8, sdq);
+        hipLaunchKernelGGL(pack_q_kernel<true>, grid, dim3(256), 0, s, q, nq, (int)nt, group, (int)ng, perm, mu, q8,
+                           sq, dq8, sdq);
     else
-        hipLaunchKernelGGL(pack_q_kernel<false>, grid, dim3(256), 0, s, q, nq, (int)nt, group, (int)ng, mu, q8, sq,
-                           dq8, sdq);
+        hipLaunchKernelGGL(pack_q_kernel<false>, grid, dim3(256), 0, s, q, nq, (int)nt, group, (int)ng, perm, mu, q8,
+                           sq, dq8, sdq);
     return launched("htrc_pack_q");
 }
 
@@ -1692,8 +1886,8 @@ static int64_t split_len(int64_t n, int64_t ns, int64_t bn) {   // _split, h3/ht
 int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
               const float* sg, const float* lz, const uint16_t* vb, const int8_t* excl, const int32_t* idx,
               const int8_t* k8, const float* ks, const uint16_t* v, int64_t heads, int64_t nq, int64_t nk,
-              int leaf, int d, int kx, int group, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
-              float* out, float* logz, void* stream) {
+              int leaf, int d, int kx, int group, const int32_t* perm, int splits, int bn, float scale, float* pm,
+              float* pl, float* pacc, float* out, float* logz, void* stream) {
     REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && excl && k8 && ks && v,
             "htrc_tile: null input pointer");
     REQUIRE(d == D, "htrc_tile: head dim must be 128");
@@ -1714,8 +1908,8 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
 #define TILE_CASE(L)                                                                                            \
     case L:                                                                                                     \
         hipLaunchKernelGGL(tile_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, excl, idx, k8, \
-                           ks, v, nq, (int)nt, group, (int)ng, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps, scale,  \
-                           ppm, ppl, ppa, out, logz);                                                           \
+                           ks, v, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps,   \
+                           scale, ppm, ppl, ppa, out, logz);                                                    \
         break;
     switch (leaf) {
         TILE_CASE(16)
@@ -1728,12 +1922,12 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
 }
 
 int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int splits,
-               int d, float* out, float* logz, void* stream) {
+               int d, const int32_t* perm, float* out, float* logz, void* stream) {
     REQUIRE(pm && pl && pacc && out && logz, "htrc_merge: null pointer");
     REQUIRE(d == D && splits >= 1 && heads > 0 && heads <= 65535 && nq > 0, "htrc_merge: bad sizes");
     const int64_t nt = (nq + TILE - 1) / TILE;
     hipLaunchKernelGGL(merge_kernel, dim3((unsigned)nt, (unsigned)heads), dim3(256), 0, (hipStream_t)stream, pm,
-                       pl, pacc, splits, nq, (int)nt, out, logz);
+                       pl, pacc, splits, nq, (int)nt, perm, out, logz);
     return launched("htrc_merge");
 }
 
@@ -1782,8 +1976,8 @@ int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, con
 int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                       const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                       const uint16_t* v, const int32_t* idx, const float* rowmax, int64_t heads, int64_t nq,
-                      int64_t nk, int leaf, int d, int kx, int group, float scale, float* out, float* logz,
-                      void* stream) {
+                      int64_t nk, int leaf, int d, int kx, int group, const int32_t* perm, float scale, float* out,
+                      float* logz, void* stream) {
     REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && k8 && ks && v && rowmax && out && logz,
             "htrc_route_attend: null pointer");
     REQUIRE(aligned(vb, 16) && aligned(v, 16) && aligned(g8, 16) && aligned(k8, 16) && aligned(sg, 16) &&
@@ -1800,7 +1994,7 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
 #define ROUTE_CASE(L)                                                                                          \
     case L:                                                                                                    \
         hipLaunchKernelGGL(route_kernel<L>, grid, dim3(512), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, \
-                           rowmax, nq, (int)nt, group, (int)ng, nk, (int)nb, nbp, kxe, scale, out, logz);     \
+                           rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp, kxe, scale, out, logz); \
         break;
     switch (leaf) {
         ROUTE_CASE(16)
@@ -1815,13 +2009,14 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
-               int stride, int group, float scale, float* out, float* logz, int32_t* idx, float* rowmax, void* stream) {
+               int stride, int group, const int32_t* perm, float scale, float* out, float* logz, int32_t* idx,
+               float* rowmax, void* stream) {
     REQUIRE(q8 && sq && vb && k8 && ks && v && out && logz, "htrc_route: null pointer");
     int rc = htrc_route_select(dq8, sdq, g8, sg, lz, heads, nq, nk, leaf, d, kx, sink, stride, group, idx, rowmax,
                                stream);
     if (rc != HTRC_OK) return rc;
     return htrc_route_attend(q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, rowmax, heads, nq, nk, leaf, d, kx,
-                             group, scale, out, logz, stream);
+                             group, perm, scale, out, logz, stream);
 }
 
 int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
@@ -1840,6 +2035,36 @@ int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, in
         hipLaunchKernelGGL(tail_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, q, tk, tv, nq, (int)ntail,
                            scale, out, logz);
     return launched("htrc_tail");
+}
+
+int htrc_kmeans_order(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int clusters, int sample,
+                      int iters, float* centres, int32_t* assign, int32_t* perm, void* stream) {
+    REQUIRE(q && centres && assign && perm, "htrc_kmeans_order: null pointer");
+    REQUIRE(d == D, "htrc_kmeans_order: head dim must be 128");
+    REQUIRE(heads > 0 && heads <= 65535 && nq > 0 && nq <= 0x7fffffff, "htrc_kmeans_order: bad heads / rows");
+    REQUIRE(clusters >= 1 && clusters <= KM_MAX_C, "htrc_kmeans_order: clusters must be in [1, 64]");
+    REQUIRE(sample >= 1 && iters >= 0 && iters <= 1000, "htrc_kmeans_order: need sample >= 1 and 0 <= iters <= 1000");
+    REQUIRE(aligned(q, 16) && aligned(centres, 16), "htrc_kmeans_order: q and centres must be 16-byte aligned");
+    const int64_t m = sample < nq ? sample : nq;
+    REQUIRE(m <= KM_MAX_SAMPLE, "htrc_kmeans_order: at most 16384 sample rows");
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 gc((unsigned)clusters, (unsigned)heads);
+    const dim3 gs((unsigned)((m + 63) / 64), (unsigned)heads), ga((unsigned)((nq + 63) / 64), (unsigned)heads);
+#define KM_LAUNCH(BF)                                                                                              \
+    hipLaunchKernelGGL(km_init_kernel<BF>, gc, dim3(D), 0, s, q, nq, (int)m, clusters, centres);                 \
+    for (int it = 0; it < iters; ++it) {                                                                           \
+        hipLaunchKernelGGL(km_assign_kernel<BF>, gs, dim3(256), 0, s, q, nq, m, (int)m, clusters, centres, assign); \
+        hipLaunchKernelGGL(km_update_kernel<BF>, gc, dim3(D), 0, s, q, nq, (int)m, clusters, assign, centres);    \
+    }                                                                                                              \
+    hipLaunchKernelGGL(km_assign_kernel<BF>, ga, dim3(256), 0, s, q, nq, nq, 0, clusters, centres, assign);
+    if (q_is_bf16) {
+        KM_LAUNCH(true)
+    } else {
+        KM_LAUNCH(false)
+    }
+#undef KM_LAUNCH
+    hipLaunchKernelGGL(km_sort_kernel, dim3((unsigned)heads), dim3(1024), 0, s, assign, nq, clusters, perm);
+    return launched("htrc_kmeans_order");
 }
 
 int htrc_dequant_rows(const uint8_t* x8, int64_t stride_x, const float* scale, int64_t stride_s, int64_t rows,

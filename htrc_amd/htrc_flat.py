@@ -28,6 +28,14 @@ from . import htrc_flat_hip as hip
 from ._lib import nb_pad
 
 
+def kmeans_order(q, clusters=32, sample=4096, iters=8):
+    """Permutation grouping queries by a small k-means (h3/htrc_flat.py:47-61): Lloyd's k-means
+    on an even sample, every query to its nearest centre, stable order by centre.  q [N, D]
+    (or [H, N, D]) on the device -> int64 [N] (or [H, N]), as ``torch.argsort`` returns."""
+    perm = hip.kmeans_order(q, clusters=clusters, sample=sample, iters=iters)
+    return perm[0].long() if q.dim() == 2 else perm.long()
+
+
 class _Tick:
     """Per-stage wall time with a device sync per stage (h3/htrc_flat.py:32-44)."""
 
@@ -55,8 +63,8 @@ def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot
         raise ValueError("the HIP backend implements store='int8', dot='bf16' (int8 Q/K dots, bf16 PV)")
     if select != "max":
         raise ValueError("the HIP backend implements select='max'")
-    if order != "seq":
-        raise ValueError("order must be 'seq' on the HIP backend (k-means ordering is not implemented)")
+    if order not in ("seq", "kmeans"):
+        raise ValueError("order must be seq or kmeans")
     if quant:
         raise ValueError("quant (fake-quant simulation) is not implemented on the HIP backend")
     if tail is not None:
@@ -93,6 +101,8 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     (select, top-k, split tile kernel, merge) honouring ``splits`` and ``kern['tile_bn']``.
     ``kern['group']`` = G > 1 makes G consecutive tiles share one expansion centre (the mean
     of their rows), one leaf state and one near set (h3/htrc_flat.py:223-231).
+    ``order='kmeans'`` cuts the tiles from the queries regrouped by ``kmeans_order``; the
+    output rows come back in query order (:148-149, 159-165).
     ``tile_chunk`` and ``precision`` are accepted for compatibility: all tiles are processed
     in one launch and accumulation is IEEE fp32.  ``state``, if a dict, receives the packed
     operands, the leaf state and the routing (for checks)."""
@@ -117,7 +127,8 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     group = max(1, int(kern.get("group", 1)))           # G consecutive tiles share one centre
     if qh.dtype not in (torch.float32, torch.bfloat16):
         qh = qh.float()
-    mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), ws=ws, group=group)
+    perm = hip.kmeans_order(qh, ws=ws) if order == "kmeans" else None   # query rows regrouped by k-means
+    mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), ws=ws, group=group, perm=perm)
     kb = kh.to(torch.bfloat16).contiguous()
     vb = vh.to(torch.bfloat16).contiguous()
     k8, ks = hip.pack_k(kb, ws=ws)
@@ -132,7 +143,7 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         if state is not None and kx > 0:
             idx = hip._buf(ws, "idx", (h, ng, kx), torch.int32, qh.device)
         out, logz = hip.route(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, sink=sink, stride=stride,
-                              ws=ws, idx=idx, group=group)
+                              ws=ws, idx=idx, group=group, perm=perm)
         tick("tile")
     else:
         excl = None
@@ -146,7 +157,7 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
             excl.zero_()
         tick("select")
         out, logz = hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
-                                       bn=int(kern.get("tile_bn", 32)), ws=ws, group=group)
+                                       bn=int(kern.get("tile_bn", 32)), ws=ws, group=group, perm=perm)
         tick("tile")
         if state is not None:
             state["excl"] = excl
@@ -154,7 +165,7 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         state.update(packed)
         state.update(lstate)
         state["idx"] = idx
-        state["nb"], state["kx"], state["group"] = nb, kx, group
+        state["nb"], state["kx"], state["group"], state["perm"] = nb, kx, group, perm
     if tail is not None and int(tail[0].shape[-2]) > 0:
         # keys past the last full leaf, exact for every query (h3/htrc_flat_triton.py:187-207, 381-388)
         tk, tv = (x.unsqueeze(0) if squeeze else x for x in tail)

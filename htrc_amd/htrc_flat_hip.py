@@ -59,10 +59,11 @@ def _need(t: torch.Tensor, dtype, name: str):
         raise ValueError(f"{name} must be contiguous")
 
 
-def pack_q(q: torch.Tensor, tile: int = TILE, ws=None, group: int = 1):
+def pack_q(q: torch.Tensor, tile: int = TILE, ws=None, group: int = 1, perm=None):
     """Centres and row int8 of q and q - mu -> (mu [H,ng,D], q8, sq, dq8, sdq).  group 1: the
     centre of each tile over its real rows (h3/htrc_flat.py:142-156); group G: the centre of
-    each G tiles over their padded rows (:223-229)."""
+    each G tiles over their padded rows (:223-229).  perm (int32 [H, nq], optional): row p of
+    the packed operands is query perm[p] (order="kmeans", :148-149)."""
     if tile != TILE:
         raise ValueError("the HIP kernels use 64-row query tiles")
     group = int(group)
@@ -82,7 +83,11 @@ def pack_q(q: torch.Tensor, tile: int = TILE, ws=None, group: int = 1):
     dq8 = _buf(ws, "dq8", (h, nt * TILE, d), torch.int8, dev)
     sq = _buf(ws, "sq", (h, nt * TILE), torch.float32, dev)
     sdq = _buf(ws, "sdq", (h, nt * TILE), torch.float32, dev)
-    call("htrc_pack_q", ptr(q), int(q.dtype == torch.bfloat16), h, nq, d, group, ptr(mu), ptr(q8), ptr(sq),
+    if perm is not None:
+        _need(perm, torch.int32, "perm")
+        if tuple(perm.shape) != (h, nq):
+            raise ValueError("perm must be int32 [H, nq]")
+    call("htrc_pack_q", ptr(q), int(q.dtype == torch.bfloat16), h, nq, d, group, ptr(perm), ptr(mu), ptr(q8), ptr(sq),
          ptr(dq8), ptr(sdq), stream_handle(dev))
     return mu, q8, sq, dq8, sdq
 
@@ -158,7 +163,7 @@ def topk_excl(sel, nb: int, kx: int, sink: int = 0, ws=None):
 
 
 def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, scale: float, splits: int = 4,
-                   bn: int = 64, ws=None, out=None, logz=None, group: int = 1):
+                   bn: int = 64, ws=None, out=None, logz=None, group: int = 1, perm=None):
     """Far + near online softmax per (tile, split) and the merge
     (h3/htrc_flat_triton.py:348-391) -> (out [H,nq,D] fp32, logz [H,nq] fp32)."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
@@ -179,15 +184,15 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
         pl = _buf(ws, "pl", (h, nt, ns, TILE), torch.float32, dev)
         pacc = _buf(ws, "pacc", (h, nt, ns, TILE, d), torch.float32, dev)
     call("htrc_tile", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(excl),
-         ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(v), h, nq, nk, int(leaf), d, kx, int(group), ns, int(bn),
+         ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(v), h, nq, nk, int(leaf), d, kx, int(group), ptr(perm), ns, int(bn),
          float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
     if ns > 1:
-        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, ns, d, ptr(out), ptr(logz), stream_handle(dev))
+        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, ns, d, ptr(perm), ptr(out), ptr(logz), stream_handle(dev))
     return out, logz
 
 
 def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: float, sink: int = 0, stride: int = 1,
-          ws=None, out=None, logz=None, idx=None, group: int = 1):
+          ws=None, out=None, logz=None, idx=None, group: int = 1, perm=None):
     """Fused select -> top-k, then far + near -> normalised output (two launches per layer call).
     -> (out [H,nq,D], logz [H,nq]); idx [H,ng,min(kx,nb)] int32 receives the routing (a
     workspace buffer when not given)."""
@@ -207,8 +212,8 @@ def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: floa
         idx = _buf(ws, "idx", (h, ng, kxe), torch.int32, dev)
     rowmax = _buf(ws, "rowmax", (h, nt * TILE), torch.float32, dev)
     call("htrc_route", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8), ptr(ks),
-         ptr(v), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), int(group), float(scale), ptr(out),
-         ptr(logz), ptr(idx), ptr(rowmax), stream_handle(dev))
+         ptr(v), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), int(group), ptr(perm), float(scale),
+         ptr(out), ptr(logz), ptr(idx), ptr(rowmax), stream_handle(dev))
     return out, logz
 
 
@@ -232,7 +237,7 @@ def route_select(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, sink
 
 
 def route_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, kx: int, scale: float, ws=None,
-                 out=None, logz=None, group: int = 1):
+                 out=None, logz=None, group: int = 1, perm=None):
     """Second launch of route: far + near field with the row reference rowmax -> (out, logz)."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
@@ -244,8 +249,8 @@ def route_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, 
     if logz is None:
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     call("htrc_route_attend", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8),
-         ptr(ks), ptr(v), ptr(idx), ptr(rowmax), h, nq, nk, int(leaf), d, int(kx), int(group), float(scale), ptr(out),
-         ptr(logz), stream_handle(dev))
+         ptr(ks), ptr(v), ptr(idx), ptr(rowmax), h, nq, nk, int(leaf), d, int(kx), int(group), ptr(perm),
+         float(scale), ptr(out), ptr(logz), stream_handle(dev))
     return out, logz
 
 
@@ -269,6 +274,25 @@ def tail_merge(q, tk, tv, *, scale: float, out, logz):
     call("htrc_tail", ptr(q), int(q.dtype == torch.bfloat16), ptr(tk), ptr(tv), h, nq, int(tk.shape[1]), d,
          float(scale), ptr(out), ptr(logz), stream_handle(q.device))
     return out, logz
+
+
+def kmeans_order(q: torch.Tensor, clusters: int = 32, sample: int = 4096, iters: int = 8, ws=None):
+    """k-means query order (h3/htrc_flat.py:47-61) -> perm int32 [H, nq]: the queries ordered by
+    their nearest centre (stable), the centres from ``iters`` Lloyd steps on ``sample`` evenly
+    spaced queries."""
+    q = _heads(q)
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        q = q.float()
+    q = q.contiguous()
+    _need(q, None, "q")
+    h, nq, d = (int(x) for x in q.shape)
+    dev = q.device
+    cen = _buf(ws, "km_centres", (h, int(clusters), d), torch.float32, dev)
+    assign = _buf(ws, "km_assign", (h, nq), torch.int32, dev)
+    perm = _buf(ws, "perm", (h, nq), torch.int32, dev)
+    call("htrc_kmeans_order", ptr(q), int(q.dtype == torch.bfloat16), h, nq, d, int(clusters), int(sample), int(iters),
+         ptr(cen), ptr(assign), ptr(perm), stream_handle(dev))
+    return perm
 
 
 def dequant_rows(x8, scale, out, br=64):

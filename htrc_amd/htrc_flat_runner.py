@@ -30,17 +30,18 @@ MODES = {
     "accurate": dict(exact_leaves=1024, order="kmeans", tile=64),
     "max": dict(exact_leaves=1024, order="kmeans", tile=32),
 }
-# The reference's quality modes (h3/htrc_flat_runner.py:48-53).  "accurate" and "max" need
-# k-means query ordering (and "max" 32-row tiles), which the HIP backend does not implement.
-SUPPORTED_MODES = ("fast", "balanced")
+# The reference's quality modes (h3/htrc_flat_runner.py:48-53).  "max" needs 32-row tiles,
+# which the HIP kernels (64-row tiles) do not implement.
+SUPPORTED_MODES = ("fast", "balanced", "accurate")
 CHUNKS = (1024, 512, 256, 128, 64, 32, 16)
 TILE = 64
 
 
 def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, heads: int = 1,
-                    splits: int = 1, kx: int = 0, group: int = 1) -> int:
+                    splits: int = 1, kx: int = 0, group: int = 1, order: str = "seq") -> int:
     """Device bytes the operator's workspace holds for one call (all tiles at once); the leaf
-    state and the routing hold one row per centre (ng = ceil(nt / group))."""
+    state and the routing hold one row per centre (ng = ceil(nt / group)); order="kmeans"
+    adds the permutation, the assignments and 32 centres."""
     nt = -(-int(queries) // TILE)
     ng = -(-nt // max(1, int(group)))
     rows = nt * TILE
@@ -58,6 +59,8 @@ def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, hea
     )
     if splits > 1:
         per_head += nt * splits * TILE * (2 + dim) * 4 + ng * nbp * 5 + 4 * ng * kx   # partials, excl, sel
+    if order == "kmeans":
+        per_head += 8 * int(queries) + 4 * 32 * dim                                   # perm, assign, centres
     return int(heads) * per_head
 
 
@@ -69,7 +72,7 @@ def predicted_peak_mib(keys: int, tile: int, tile_chunk: int, splits: int = 8, l
     bound the workspace; ``queries`` (default: as many as keys) sizes it.  Graph mode adds
     the static fp32 q and bf16 k/v copies."""
     q = int(queries) if queries else int(keys)
-    b = workspace_bytes(q, keys, leaf, dim, heads, splits=1, group=group)
+    b = workspace_bytes(q, keys, leaf, dim, heads, splits=1, group=group, order=order)
     if graph:
         b += int(heads) * (4 * q * dim + 2 * 2 * int(keys) * dim)
     return b / 2 ** 20
@@ -94,7 +97,7 @@ class FlatRunner:
         if mode not in MODES:
             raise ValueError(f"mode must be one of {list(MODES)}")
         if mode not in SUPPORTED_MODES:
-            raise ValueError(f"mode {mode!r} needs k-means query ordering, which the HIP backend does not implement")
+            raise ValueError(f"mode {mode!r} needs 32-row tiles, which the HIP kernels do not implement")
         from . import htrc_flat
         self.flat = htrc_flat
         self.mode = mode

@@ -22,6 +22,10 @@
  * group = G >= 1 consecutive tiles share one expansion centre, one leaf state and one near
  * set (the reference's kern["group"], h3/htrc_flat.py:223-231): ng = ceil(nt / G) centres,
  * the last group padded with repeats of the last tile.  G = 1 is the plain per-tile path.
+ *
+ * perm (optional, int32 [H, nq]; NULL = identity): the operator works on the queries in the
+ * order perm (row p is query perm[p], order="kmeans"); pack_q gathers through it and the
+ * entry points that write out / logz scatter back, so out / logz stay in query order.
  * The reference implements the same path as Triton kernels driven from Python;
  * each entry point below names the reference interface it replaces.
  */
@@ -34,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 7
+#define HTRC_ABI_VERSION 8
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -52,8 +56,8 @@ int htrc_nb_pad(int64_t nb);
  * Replaces _tiles (h3/htrc_flat.py:142-156), the group centres (:223-229) and the in-kernel
  * Q / dQ quantisation of _tile_kernel and _rowmax_kernel (h3/htrc_flat_triton.py:104-117,
  * 225-233). */
-int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, float* mu, int8_t* q8,
-                float* sq, int8_t* dq8, float* sdq, void* stream);
+int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, const int32_t* perm,
+                float* mu, int8_t* q8, float* sq, int8_t* dq8, float* sdq, void* stream);
 
 /* K int8 pack (round half to even, per-row scale).
  * Replaces the host-side K pack of _flat_triton (h3/htrc_flat.py:213-219). */
@@ -81,13 +85,13 @@ int htrc_topk(const float* sel, int64_t rows, int64_t nb, int kx, int sink, int3
 int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
               const float* sg, const float* lz, const uint16_t* vb, const int8_t* excl, const int32_t* idx,
               const int8_t* k8, const float* ks, const uint16_t* v, int64_t heads, int64_t nq, int64_t nk,
-              int leaf, int d, int kx, int group, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
-              float* out, float* logz, void* stream);
+              int leaf, int d, int kx, int group, const int32_t* perm, int splits, int bn, float scale, float* pm,
+              float* pl, float* pacc, float* out, float* logz, void* stream);
 
 /* Merge of split partials into normalised rows, plus logz = max + log(sum).
  * Replaces _merge_kernel (h3/htrc_flat_triton.py:257-273, launched at :389-390). */
 int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int splits,
-               int d, float* out, float* logz, void* stream);
+               int d, const int32_t* perm, float* out, float* logz, void* stream);
 
 /* Production path, first launch: select -> top-k per tile group with SEL kept in LDS, writing
  * the routing idx [H, ng, min(kx, nb)] (ascending; required when kx > 0) and rowmax fp32
@@ -103,16 +107,16 @@ int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, con
 int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                       const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                       const uint16_t* v, const int32_t* idx, const float* rowmax, int64_t heads, int64_t nq,
-                      int64_t nk, int leaf, int d, int kx, int group, float scale, float* out, float* logz,
-                      void* stream);
+                      int64_t nk, int leaf, int d, int kx, int group, const int32_t* perm, float scale, float* out,
+                      float* logz, void* stream);
 
 /* Both launches of the production path: htrc_route_select then htrc_route_attend.
  * Replaces the chunk loop body of _flat_triton after leaf_stats (h3/htrc_flat.py:250-271). */
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
-               int stride, int group, float scale, float* out, float* logz, int32_t* idx, float* rowmax,
-               void* stream);
+               int stride, int group, const int32_t* perm, float scale, float* out, float* logz, int32_t* idx,
+               float* rowmax, void* stream);
 
 /* Tail keys: tk, tv fp32 [H, ntail, 128] (keys past the last full leaf) attended exactly by
  * every query and merged in place into a finished out / logz (log-sum-exp merge).  Up to 16
@@ -120,6 +124,14 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
  * Replaces the tail handling of tile_attention (h3/htrc_flat_triton.py:187-207, 366-388). */
 int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
               int64_t ntail, int d, float scale, float* out, float* logz, void* stream);
+
+/* k-means query order: perm int32 [H, nq], the queries ordered by their nearest of `clusters`
+ * centres (stable), the centres from `iters` Lloyd steps on `sample` evenly spaced queries.
+ * Workspace: centres fp32 [H, clusters, 128], assign int32 [H, nq].  1 <= clusters <= 64,
+ * min(sample, nq) <= 16384.
+ * Replaces kmeans_order (h3/htrc_flat.py:47-61). */
+int htrc_kmeans_order(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int clusters, int sample,
+                      int iters, float* centres, int32_t* assign, int32_t* perm, void* stream);
 
 /* fp8 rows to bf16 (out_is_bf16 = 1) or fp32: out[r, :] = e4m3fn(x8[r, :]) * scale[r], rounded
  * to nearest even.  x8 rows are stride_x bytes apart and scale entries stride_s floats apart

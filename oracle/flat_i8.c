@@ -35,7 +35,7 @@
  * (h3/htrc_flat.py:217, h3/htrc_flat_triton.py:76,112,115,231). */
 static const float R127 = 1.0f / 127.0f;
 
-int oracle_abi_version(void) { return 2; }
+int oracle_abi_version(void) { return 3; }
 
 float oracle_r127(void) { return R127; }
 
@@ -443,4 +443,77 @@ void oracle_merge(const float *pm, const float *pl, const float *pacc, int64_t n
         }
         free(num);
     }
+}
+
+/* k-means query order, h3/htrc_flat.py:47-61, in the arithmetic the HIP kernels fix:
+ *   sample i: query round(linspace(0, n-1, m)[i]), m = min(sample, n), with torch's float32
+ *   device linspace (step = (n-1)/(m-1); i < m/2: step*i, else fma(-step, m-1-i, n-1), one
+ *   rounding) rounded to nearest even; initial centre j: sample round(linspace(0, m-1, C)[j]);
+ *   nearest centre: squared distance as a sequential fp32 sum over the dims, the lowest centre
+ *   on ties (none finite: centre 0);
+ *   Lloyd update: per centre the sequential fp32 sum of its samples in sample order / count,
+ *   a centre without samples keeps its position;
+ *   perm: the queries ordered by centre, stable (torch.argsort(stable=True)). */
+int64_t oracle_linspace_round(int64_t hi, int64_t steps, int64_t i) {
+    if (steps <= 1) return 0;
+    float step = (float)hi / (float)(steps - 1);
+    /* upper half in one fused multiply-add, as torch's device linspace computes it */
+    float v = i < steps / 2 ? step * (float)i : fmaf(-step, (float)(steps - 1 - i), (float)hi);
+    int64_t r = (int64_t)nearbyintf(v);
+    return r < 0 ? 0 : (r > hi ? hi : r);      /* (float)hi may round above hi for hi >= 2^24 */
+}
+
+static int nearest_centre(const float *x, const float *c, int clusters, int d) {
+    float best = INFINITY;
+    int bj = clusters;
+    for (int j = 0; j < clusters; ++j) {
+        float acc = 0.0f;
+        for (int i = 0; i < d; ++i) {
+            float df = x[i] - c[(int64_t)j * d + i];
+            acc += df * df;
+        }
+        if (acc < best) {
+            best = acc;
+            bj = j;
+        }
+    }
+    return bj < clusters ? bj : 0;
+}
+
+void oracle_kmeans_order(const float *q, int64_t n, int d, int clusters, int sample, int iters, int32_t *perm) {
+    int64_t m = sample < n ? sample : n;
+    float *c = (float *)malloc(sizeof(float) * (size_t)clusters * (size_t)d);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)d);
+    int32_t *a = (int32_t *)malloc(sizeof(int32_t) * (size_t)n);
+    int64_t *cnt = (int64_t *)calloc((size_t)clusters + 1, sizeof(int64_t));
+    for (int j = 0; j < clusters; ++j) {
+        int64_t row = oracle_linspace_round(n - 1, m, oracle_linspace_round(m - 1, clusters, j));
+        memcpy(c + (int64_t)j * d, q + row * d, sizeof(float) * (size_t)d);
+    }
+    for (int it = 0; it < iters; ++it) {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < m; ++i)
+            a[i] = nearest_centre(q + oracle_linspace_round(n - 1, m, i) * d, c, clusters, d);
+        for (int j = 0; j < clusters; ++j) {
+            int64_t k = 0;
+            for (int e = 0; e < d; ++e) acc[e] = 0.0f;
+            for (int64_t i = 0; i < m; ++i) {
+                if (a[i] != j) continue;
+                const float *x = q + oracle_linspace_round(n - 1, m, i) * d;
+                for (int e = 0; e < d; ++e) acc[e] += x[e];
+                ++k;
+            }
+            if (k > 0)
+                for (int e = 0; e < d; ++e) c[(int64_t)j * d + e] = acc[e] / (float)k;
+        }
+    }
+#pragma omp parallel for schedule(static)
+    for (int64_t p = 0; p < n; ++p) a[p] = nearest_centre(q + p * d, c, clusters, d);
+    for (int64_t p = 0; p < n; ++p) cnt[a[p] + 1]++;
+    for (int j = 0; j < clusters; ++j) cnt[j + 1] += cnt[j];
+    for (int64_t p = 0; p < n; ++p) perm[cnt[a[p]]++] = (int32_t)p;
+    free(c);
+    free(acc);
+    free(a);
+    free(cnt);
 }

@@ -63,7 +63,10 @@ def lib():
                                   _I8, _F32, _I8, _F32, _I8, _F32, _F32, _U16,
                                   _I8, _F32, _U16, _flt, _int, _int, _F32, _F32, _F32]
         L.oracle_merge.argtypes = [_F32, _F32, _F32, _i64, _int, _int, _int, _F32, _F32]
-        if L.oracle_abi_version() != 2:
+        L.oracle_linspace_round.restype = _i64
+        L.oracle_linspace_round.argtypes = [_i64, _i64, _i64]
+        L.oracle_kmeans_order.argtypes = [_F32, _i64, _int, _int, _int, _int, _I32]
+        if L.oracle_abi_version() != 3:
             raise RuntimeError(f"{path} is stale (oracle ABI {L.oracle_abi_version()}): rebuild it")
         _lib = L
     return _lib
@@ -100,6 +103,20 @@ def tile_centres(q: np.ndarray, tile: int) -> np.ndarray:
     mu = np.empty((nt, d), np.float32)
     lib().oracle_tile_centres(q, n, d, tile, mu)
     return mu
+
+
+def linspace_round(hi: int, steps: int, i: int) -> int:
+    """round(torch.linspace(0, hi, steps, dtype=float32)[i]) (round half to even)."""
+    return int(lib().oracle_linspace_round(int(hi), int(steps), int(i)))
+
+
+def kmeans_order(q: np.ndarray, clusters: int = 32, sample: int = 4096, iters: int = 8) -> np.ndarray:
+    """k-means query order (h3/htrc_flat.py:47-61) -> perm int32 [n]."""
+    q = _c(q, np.float32)
+    n, d = q.shape
+    perm = np.empty((n,), np.int32)
+    lib().oracle_kmeans_order(q, n, d, int(clusters), int(sample), int(iters), perm)
+    return perm
 
 
 def group_centres(q: np.ndarray, tile: int, group: int) -> np.ndarray:
@@ -224,9 +241,11 @@ def tail_merge(out, logz, q, tk, tv, scale: float):
 
 def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: int = 64,
             splits: int = 4, bn: int = 64, sel_stride: int = 1, sink_leaves: int = 0,
-            scale: float | None = None, keep: bool = True, group: int = 1) -> dict:
+            scale: float | None = None, keep: bool = True, group: int = 1, order: str = "seq") -> dict:
     """The INT8 flat operator for one head: q float32 (or bf16 bits) [n,d], k/v bf16 bits
-    [nk,d] with nk % leaf == 0.  Returns every intermediate plus out [n,d] and logz [n]."""
+    [nk,d] with nk % leaf == 0.  Returns every intermediate plus out [n,d] and logz [n].
+    order="kmeans": the tiles are cut from q[perm] (perm = kmeans_order(q)) and out / logz
+    are returned in query order (h3/htrc_flat.py:146-149, 159-165)."""
     q = np.asarray(q)
     qf = bf16.to_f32(q) if q.dtype == np.uint16 else _c(q, np.float32)
     n, d = qf.shape
@@ -238,6 +257,11 @@ def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: 
     sink = max(0, min(int(sink_leaves), nb))
     kx = min(int(exact_leaves) + sink, nb)
     st: dict = {"v": _c(v_bits, np.uint16)}
+    if order == "kmeans":
+        st["perm"] = kmeans_order(qf)
+        qf = qf[st["perm"]]
+    elif order != "seq":
+        raise ValueError("order must be seq or kmeans")
     st["k8"], st["ks"] = pack_k(k_bits)
     st["mu"] = tile_centres(qf, tile) if group == 1 else group_centres(qf, tile, group)
     st["q8"], st["sq"], st["dq8"], st["sdq"] = pack_q(qf, tile, st["mu"], group)
@@ -252,6 +276,11 @@ def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: 
     pm, pl, pacc = tile_partials(st, tile=tile, leaf=leaf, scale=scale, splits=splits, bn=bn, group=group)
     out, logz = merge(pm, pl, pacc)
     st["out"], st["logz"] = out[:n], logz[:n]
+    if order == "kmeans":
+        st["out_perm"], st["logz_perm"] = st["out"], st["logz"]
+        st["out"], st["logz"] = np.empty_like(out[:n]), np.empty_like(logz[:n])
+        st["out"][st["perm"]] = st["out_perm"]
+        st["logz"][st["perm"]] = st["logz_perm"]
     if keep:
         st["pm"], st["pl"], st["pacc"] = pm, pl, pacc
     return st

@@ -154,3 +154,30 @@ def test_group_centres_vs_oracle(device, fused, n, group, stride):
     assert mism <= max(1, ref["idx"].shape[0] // 50)
     assert rel_l2(out.cpu().numpy(), ref["out"]) <= OUT_REL_L2
     assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("n,group", [(8192, 1), (5000, 2)])
+def test_kmeans_order_vs_oracle(device, fused, n, group):
+    """order="kmeans" (h3/htrc_flat.py:146-149, 159-165): tiles cut from the queries regrouped
+    by the k-means order, the output back in query order.  The permutation and the packed
+    rows are bit-exact; routing and output as above."""
+    leaf, ex = 64, 12
+    nk = (n // leaf) * leaf
+    q, k, v = workloads.clustered_runs(n=n, runs=max(1, n // 64), heads=1, seed=n + 7)
+    k, v = k[:, :nk].contiguous(), v[:, :nk].contiguous()
+    perm = q[0][torch.randperm(n, generator=torch.Generator().manual_seed(n))]   # spatially mixed queries
+    st = {}
+    out, logz = htrc_flat.flat_attention(perm.to(device), k[0].to(device), v[0].to(device), backend="hip",
+                                         store="int8", dot="bf16", leaf=leaf, exact_leaves=ex, splits=4,
+                                         order="kmeans", kern={"fused": fused, "tile_bn": 64, "group": group},
+                                         return_logz=True, state=st)
+    torch.cuda.synchronize()
+    ref = flat_i8.flat_i8(bits(perm), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=ex,
+                          splits=1 if fused else 4, bn=64, group=group, order="kmeans")
+    assert np.array_equal(st["perm"][0].cpu().numpy(), ref["perm"])
+    assert np.array_equal(st["dq8"][0].cpu().numpy(), ref["dq8"])
+    mism = _routing_check(st["idx"][0].cpu().numpy(), ref)
+    assert mism <= max(1, ref["idx"].shape[0] // 50)
+    assert rel_l2(out.cpu().numpy(), ref["out"]) <= OUT_REL_L2
+    assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS

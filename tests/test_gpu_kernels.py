@@ -310,3 +310,29 @@ def test_dequant_rows_all_patterns(device, out_dtype):
     hip.dequant_rows(dx8, dsc, out)
     torch.cuda.synchronize()
     torch.testing.assert_close(out.cpu(), want, rtol=0, atol=0, equal_nan=True)
+
+
+@pytest.mark.parametrize("n,m", [(64512, 4096), (124992, 4096), (5000, 4096), (4096, 4096), (1000, 33),
+                                 (64512, 32), (4096, 32), (77, 1)])
+def test_linspace_positions_equal_device_torch(device, n, m):
+    """The sample / initial-centre positions of the k-means order are torch's device
+    linspace rounded (h3/htrc_flat.py:50-52 run on the query's device)."""
+    want = torch.linspace(0, n - 1, m, device=device).round().long().cpu().numpy()
+    got = np.array([flat_i8.linspace_round(n - 1, m, i) for i in range(m)])
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("n,clusters,sample,iters", [(64512, 32, 4096, 8), (5000, 32, 4096, 8), (3001, 17, 700, 4),
+                                                     (64, 32, 4096, 8), (9000, 64, 9000, 2), (10, 3, 5, 0)])
+@pytest.mark.parametrize("qdtype", ["bf16", "fp32"])
+def test_kmeans_order_bitexact(device, n, clusters, sample, iters, qdtype):
+    """k-means order (h3/htrc_flat.py:47-61): the GPU permutation is the oracle's, bit for bit
+    (same sample, distances, update order and stable sort), for every head."""
+    q, _, _ = _data(n, nk=64, seed=n + clusters, heads=2)
+    if qdtype == "fp32":
+        q = q.float() + 1e-3 * torch.randn(q.shape, generator=torch.Generator().manual_seed(5))
+    perm = hip.kmeans_order(q.to(device).contiguous(), clusters=clusters, sample=sample, iters=iters)
+    torch.cuda.synchronize()
+    for h in range(2):
+        want = flat_i8.kmeans_order(q[h].float().numpy(), clusters, sample, iters)
+        assert np.array_equal(_np(perm[h]), want), f"head {h}"

@@ -87,3 +87,19 @@ def test_tail_rows_graph_equals_eager(device):
     torch.cuda.synchronize()
     for o, e in zip(got, eager):
         assert torch.equal(o, e)
+
+
+def test_accurate_mode_graph_replays_equal_eager(device):
+    """mode="accurate" (k-means query order, h3/htrc_flat_runner.py:51): the k-means launches
+    are captured with the rest; every replay equals the eager operator call."""
+    jobs = _jobs(device, heads=2, seed=4)
+    r = htrc_flat_runner.FlatRunner(2048, 2048, mode="accurate", **KW)
+    assert r.cfg["order"] == "kmeans"
+    assert r.graph is not None, r.graph_error
+    eager = [htrc_flat.flat_attention(j[1], j[2], j[3], **r.cfg) for j in jobs]
+    for rep in range(3):
+        outs = r.run(jobs)
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {rep} differs from eager"
+        _ = torch.randn(1 << 20, device=device).sum().item()
