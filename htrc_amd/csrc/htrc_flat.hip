@@ -1073,6 +1073,7 @@ __device__ __forceinline__ void dma_rows27(const uint16_t* x0, const uint16_t* x
 //   fixed softmax reference of route_kernel (the tile maximum when rows are sampled).
 // Small register and LDS footprint: several tiles share a CU, so their load latency and their
 // top-k overlap.  SEL never reaches HBM.
+template <bool MULTI>      // MULTI: tile groups of G > 1 tiles (keys merged by max over the tiles)
 __global__ __launch_bounds__(256, 4) void route_select_kernel(
     const int8_t* __restrict__ dq8, const float* __restrict__ sdq, const int8_t* __restrict__ g8,
     const float* __restrict__ sg, const float* __restrict__ lz, int nt, int group, int ng, int nb, int nb_pad,
@@ -1128,12 +1129,12 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
                 const int l = c + 4 * grp + i;
                 if (l < nb) {
                     const uint32_t key = l < sink ? 0xffffffffu : order_key(__fadd_rn(best[i], o.lz[i]));
-                    keys[l] = first ? key : max(keys[l], key);
+                    keys[l] = (!MULTI || first) ? key : max(keys[l], key);
                 }
             }
         }
     };
-    for (int j = 0; j < group; ++j) {
+    for (int j = 0; j < (MULTI ? group : 1); ++j) {
         const int t = gi * group + j;
         if (t >= nt) break;                   // padded tiles repeat the last one
         const int64_t th = (int64_t)h * nt + t;
@@ -1166,7 +1167,7 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
             if (stride != 1) m = wave_max(m); // sampled rows: one reference for the whole tile
             rowmax[th * TILE + r] = m;
         }
-        __syncthreads();                      // red_m is free for the next tile; keys complete
+        if (MULTI) __syncthreads();           // red_m is free for the next tile
         first = false;
     }
     const int kxe = min(kx, nb);
@@ -1199,7 +1200,13 @@ __global__ __launch_bounds__(512) void route_kernel(
     const int64_t kh = (int64_t)h * nk;
     const int64_t row0 = th * TILE + 32 * hr + col;            // this lane's rows: row0, row0 + 16
     // ---- routing of this tile (route_select_kernel)
-    for (int i = threadIdx.x; i <= nb / 32; i += 512) exbits[i] = 0u;
+    // exclusion bits: the selected (near) leaves, and every leaf >= nb, so the far loop needs no
+    // range test (far blocks are 32-leaf aligned and a pair's range ends on a 32-leaf boundary
+    // or at nb)
+    for (int i = threadIdx.x; i <= nb / 32; i += 512) {
+        const int past = nb - 32 * i;          // leaves of word i below nb
+        exbits[i] = past >= 32 ? 0u : (past <= 0 ? ~0u : ~0u << past);
+    }
     for (int j = threadIdx.x; j < kxe; j += 512) sidx[j] = idx[gs * kxe + j];
     float mref[2];
 #pragma unroll
@@ -1284,7 +1291,7 @@ __global__ __launch_bounds__(512) void route_kernel(
                 if (bi >= nf) return;
                 const char* slot = pring + S * SLOT_BYTES;
                 const int c0 = lo + 32 * bi;
-                const uint32_t exw = exbits[c0 >> 5];
+                const uint32_t exw = exbits[c0 >> 5] >> (4 * grp);       // bit 16 hh + i: this lane's key
                 float sc[2][8];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
@@ -1300,8 +1307,7 @@ __global__ __launch_bounds__(512) void route_kernel(
                     const f32x4 lzv = *(const f32x4*)(slot + 12288 + 128 + (16 * hh + 4 * grp) * 4);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const int cl = 16 * hh + 4 * grp + i;          // leaf within the block
-                        const bool ok = c0 + cl < hi && ((exw >> cl) & 1u) == 0u;
+                        const bool ok = ((exw >> (16 * hh + i)) & 1u) == 0u;
                         const float bias = ok ? __fmul_rn(lzv[i], LOG2E) : -INFINITY;
 #pragma unroll
                         for (int rb = 0; rb < 2; ++rb)
@@ -1369,11 +1375,17 @@ __global__ __launch_bounds__(512) void route_kernel(
                     const f32x4 ksv = *(const f32x4*)(slot + 12288 + 128 * hh + 16 * grp);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const bool ok = (e0 + 16 * hh + 4 * grp + i) < e_hi;
-                        const float bias = ok ? 0.0f : -INFINITY;
+                        if constexpr (LEAF % 32 == 0) {   // the near list is whole 32-token blocks
 #pragma unroll
-                        for (int rb = 0; rb < 2; ++rb)
-                            sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]), bias);
+                            for (int rb = 0; rb < 2; ++rb)
+                                sc[rb][4 * hh + i] = __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]));
+                        } else {                          // leaf 16: the last block may be half empty
+                            const bool ok = (e0 + 16 * hh + 4 * grp + i) < e_hi;
+                            const float bias = ok ? 0.0f : -INFINITY;
+#pragma unroll
+                            for (int rb = 0; rb < 2; ++rb)
+                                sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]), bias);
+                        }
                     }
                 }
                 u32x2 pvop[8][2];
@@ -1967,9 +1979,14 @@ int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, con
     REQUIRE(kxe == 0 || idx, "htrc_route_select: idx is required when kx > 0");
     REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_route_select: stride must divide 64");
     const int nbp = htrc_nb_pad(nb);
-    hipLaunchKernelGGL(route_select_kernel, dim3((unsigned)(ng * heads)), dim3(256), (size_t)4 * nbp,
-                       (hipStream_t)stream, dq8, sdq, g8, sg, lz, (int)nt, group, (int)ng, (int)nb, nbp, kxe, sink,
-                       stride, idx, rowmax);
+    if (group == 1)
+        hipLaunchKernelGGL(route_select_kernel<false>, dim3((unsigned)(ng * heads)), dim3(256), (size_t)4 * nbp,
+                           (hipStream_t)stream, dq8, sdq, g8, sg, lz, (int)nt, group, (int)ng, (int)nb, nbp, kxe, sink,
+                           stride, idx, rowmax);
+    else
+        hipLaunchKernelGGL(route_select_kernel<true>, dim3((unsigned)(ng * heads)), dim3(256), (size_t)4 * nbp,
+                           (hipStream_t)stream, dq8, sdq, g8, sg, lz, (int)nt, group, (int)ng, (int)nb, nbp, kxe, sink,
+                           stride, idx, rowmax);
     return launched("htrc_route_select");
 }
 
