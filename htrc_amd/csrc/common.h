@@ -17,6 +17,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // fp32(1/127) = 0x3C010204, the per-row int8 scale factor.
 __device__ constexpr float R127 = 1.0f / 127.0f;
+__device__ constexpr float R448 = 1.0f / 448.0f;   // e4m3 state scales (h3/htrc_flat_triton.py:67-68)
 __device__ constexpr float LOG2E = 1.4426950408889634f;
 __device__ constexpr float LN2 = 0.6931471805599453f;
 
@@ -143,6 +144,12 @@ __device__ __forceinline__ uint32_t pack2bf(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// Two fp32 -> packed fp16 pair, round to nearest even (v_cvt_f16_f32 in the default mode).
+__device__ __forceinline__ uint32_t pack2h(float a, float b) {
+    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+
 // fp32 rounded to the nearest bf16 value (returned as fp32).
 __device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
 
@@ -183,6 +190,21 @@ __device__ __forceinline__ void split2x8(const float* x, bf16x8& hi, bf16x8& lo)
 
 __device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+// Two e4m3 codes (bits 0..7, 8..15) -> an fp16 pair holding value * 2^-8, exactly: the code's
+// exponent and mantissa fields shifted into fp16 position (biases 7 and 15 differ by 8), which
+// also maps e4m3 subnormals onto fp16 subnormals.
+__device__ __forceinline__ uint32_t e4m3x2_to_h2(uint32_t b2) {
+    const uint32_t t = (b2 & 0xffu) | ((b2 & 0xff00u) << 8);
+    return ((t & 0x007f007fu) << 7) | ((t & 0x00800080u) << 8);
+}
+// Eight e4m3 codes -> eight fp16 (value * 2^-8).
+__device__ __forceinline__ u32x4 e4m3x8_to_h8(u32x2 b) {
+    return u32x4{e4m3x2_to_h2(b.x & 0xffffu), e4m3x2_to_h2(b.x >> 16), e4m3x2_to_h2(b.y & 0xffffu), e4m3x2_to_h2(b.y >> 16)};
 }
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

@@ -76,7 +76,10 @@ __global__ __launch_bounds__(128) void group_centres_kernel(const void* __restri
 // group == 1: the tile's centre over its real rows is computed here and written to mu; group > 1:
 // the group's centre is read from mu (group_centres_kernel).  perm (optional): row p of the
 // operator is query perm[p] (order="kmeans").
-template <bool IN_BF16>
+// QM = 0: row int8 of q and q - mu (q8 / sq, dq8 / sdq).  QM = 1, 2: the 16-bit operands of the
+// reference's bf16 and fp8 state stores: q in bf16 (q8 holds uint16 rows, sq unused) and q - mu in
+// bf16 (QM = 1) or fp16 (QM = 2) (h3/htrc_flat_triton.py:104-108, dqb / dqh; dq8 holds them).
+template <bool IN_BF16, int QM = 0>
 __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qin, int64_t nq, int nt, int group,
                                                      int ng, const int32_t* __restrict__ perm,
                                                      float* __restrict__ mu, int8_t* __restrict__ q8,
@@ -134,6 +137,18 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
             aq = fmaxf(aq, fabsf(x[e]));
             ad = fmaxf(ad, fabsf(d[e]));
         }
+        const int64_t p = tg * TILE + r;
+        if constexpr (QM != 0) {
+            uint32_t uq[4], ud[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uq[e] = pack2bf(x[2 * e], x[2 * e + 1]);
+                ud[e] = QM == 1 ? pack2bf(d[2 * e], d[2 * e + 1]) : pack2h(d[2 * e], d[2 * e + 1]);
+            }
+            *(u32x4*)((uint16_t*)q8 + p * D + 8 * i) = u32x4{uq[0], uq[1], uq[2], uq[3]};
+            *(u32x4*)((uint16_t*)dq8 + p * D + 8 * i) = u32x4{ud[0], ud[1], ud[2], ud[3]};
+            continue;
+        }
         const float s1 = row_scale(col_max(aq), 1e-20f), s2 = row_scale(col_max(ad), 1e-20f);
         int cq[8], cd[8];
 #pragma unroll
@@ -141,7 +156,6 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
             cq[e] = round_away(__fdiv_rn(x[e], s1));
             cd[e] = round_away(__fdiv_rn(d[e], s2));
         }
-        const int64_t p = tg * TILE + r;
         *(u32x2*)(q8 + p * D + 8 * i) = pack8_i8(cq);
         *(u32x2*)(dq8 + p * D + 8 * i) = pack8_i8(cd);
         if (i == 0) {
@@ -289,6 +303,29 @@ __device__ __forceinline__ u32x2 tr_operand(const char* rows, int rbase, int db,
     return lds_read_tr16(rows + (row * 16 + (c ^ swz(row))) * 16 + 8 * (L & 1));
 }
 
+// OCP e4m3 (e4m3fn) code of x rounded to nearest even, |x| saturated at 448 (the largest
+// finite value; the state scales keep |x| <= 448): below 2^-6 the subnormal grid m * 2^-9,
+// above it the mantissa rounded to 3 bits in the float's bit pattern.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+    const uint32_t sgn = (__float_as_uint(x) >> 24) & 0x80u;
+    const float a = fminf(fabsf(x), 448.0f);
+    uint32_t c;
+    if (a < 0.015625f) {
+        c = (uint32_t)rintf(__fmul_rn(a, 512.0f));                 // 0 .. 8 (8: the smallest normal)
+    } else {
+        const uint32_t b = __float_as_uint(a);
+        const uint32_t r = (b + 0x7ffffu + ((b >> 20) & 1u)) & 0xfff00000u;
+        c = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
+    }
+    return sgn | c;
+}
+
+// e4m3 codes of x_i * c packed little-endian.
+__device__ __forceinline__ uint32_t quant4_e4m3(f32x4 x, float c) {
+    return f32_to_e4m3(__fmul_rn(x[0], c)) | (f32_to_e4m3(__fmul_rn(x[1], c)) << 8) |
+           (f32_to_e4m3(__fmul_rn(x[2], c)) << 16) | (f32_to_e4m3(__fmul_rn(x[3], c)) << 24);
+}
+
 // int8 codes of x_i * c rounded to nearest (ties to even), packed little-endian.  Adding
 // 1.5 * 2^23 to a value of magnitude below 2^22 rounds it to an integer held in the low mantissa
 // bits, so the low byte of the sum is the two's-complement code; SDWA adds write the codes of
@@ -306,19 +343,23 @@ __device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
     return u;
 }
 
-template <int LEAF>
+// FP8: the reference's fp8 state store (h3/htrc_flat_triton.py:65-72): g and vb as e4m3 codes of
+// x / s with row scales s = max(max|x| * fp32(1/448), 1e-30) (sg, sv); vb then holds bytes.
+template <int LEAF, bool FP8 = false>
 __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__ mu, int nt,
                                                        const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v, int64_t nk, int nb,
                                                        int nb_pad, int lpb, float scale,
                                                        int8_t* __restrict__ g8, float* __restrict__ sg,
-                                                       uint16_t* __restrict__ vb, float* __restrict__ lz) {
+                                                       uint16_t* __restrict__ vb, float* __restrict__ sv,
+                                                       float* __restrict__ lz) {
     constexpr int KB = LEAF / 16;                 // 16-key blocks per leaf
     constexpr int KK = (LEAF + 31) / 32;          // 32-key MFMA k-steps per leaf
     constexpr int LEAF_BYTES = 32 * LEAF * 16;
     constexpr int LPB = 16;                       // leaves per workgroup (the launcher's lpb)
     __shared__ __align__(16) char lds[2 * LEAF_BYTES];
     __shared__ __align__(16) float s_sg[64][LPB], s_lz[64][LPB];   // per tile, the workgroup's leaves
+    __shared__ __align__(16) float s_sv[FP8 ? 64 : 1][LPB];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     // 1-D grid over (tile group, leaf group, head), tile group fastest: the tile groups that
     // read the same leaves run together on one XCD and share its L2.
@@ -349,7 +390,7 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
     const int64_t kh = (int64_t)h * nk;
     // g8 / vb of the previous leaf, stored during the next one
     uint32_t pg[8];
-    u32x2 pv[8];
+    u32x2 pv[8];                 // vb bf16 pairs (FP8: pv[db].x holds the four e4m3 codes)
     int pl = -1;
     // The MFMA C layout leaves lane (col, grp) with dims 16db + 4grp.. of centre col.  Lanes
     // exchange dwords within the column so that every store instruction writes 64 contiguous
@@ -357,21 +398,31 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
     // 64-byte segments store at 5.2 TB/s where 16-byte pieces 32 bytes apart reach 4.2 TB/s.
     // The six stores of leaf l - 1 are spread through leaf l's products, so the write queue
     // sees a steady stream rather than one burst per leaf.
-    auto store_g = [&]() {       // g8: 4 x 4 block transpose of (pg[g], pg[4 + g]); row g then
-        if (pl >= 0) {           // holds dims 16g + 4c in x[2c] and 64 + 16g + 4c in x[2c + 1]
-            uint32_t x[8] = {pg[0], pg[4], pg[1], pg[5], pg[2], pg[6], pg[3], pg[7]};
-            rows_transpose(x);
-            if (tval) {
-                const int64_t s = th * nb_pad + pl;
-                *(u32x4*)(g8 + s * D + 16 * grp) = u32x4{x[0], x[2], x[4], x[6]};
-                *(u32x4*)(g8 + s * D + 64 + 16 * grp) = u32x4{x[1], x[3], x[5], x[7]};
-            }
+    // one-byte rows (g8, FP8 vb): 4 x 4 block transpose of (c[g], c[4 + g]); row g then holds
+    // dims 16g + 4c in x[2c] and 64 + 16g + 4c in x[2c + 1]
+    auto store_bytes = [&](const uint32_t (&c)[8], uint8_t* dst) {
+        uint32_t x[8] = {c[0], c[4], c[1], c[5], c[2], c[6], c[3], c[7]};
+        rows_transpose(x);
+        if (tval) {
+            const int64_t s = th * nb_pad + pl;
+            *(u32x4*)(dst + s * D + 16 * grp) = u32x4{x[0], x[2], x[4], x[6]};
+            *(u32x4*)(dst + s * D + 64 + 16 * grp) = u32x4{x[1], x[3], x[5], x[7]};
         }
+    };
+    auto store_g = [&]() {
+        if (pl >= 0) store_bytes(pg, (uint8_t*)g8);
     };
     // vb half hf (dims 64hf..): rows 2j and 2j + 1 swap halves; row g then holds, for
     // db = 2m + (g & 1), the dims 16db + 8(g >> 1) .. + 3 in va and .. + 4 .. + 7 in vc
     auto store_v = [&](int hf) {
-        if (pl >= 0) {
+        if constexpr (FP8) {
+            if (pl >= 0 && hf == 0) {
+                uint32_t c[8];
+#pragma unroll
+                for (int db = 0; db < 8; ++db) c[db] = pv[db].x;
+                store_bytes(c, (uint8_t*)vb);
+            }
+        } else if (pl >= 0) {
             u32x2 va[2], vc[2];
 #pragma unroll
             for (int mm = 0; mm < 2; ++mm) {
@@ -473,16 +524,39 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
 #pragma unroll
             for (int i = 0; i < 4; ++i) am = fmaxf(am, fabsf(gacc[db][i]));
         am = __fmul_rn(grp_max(am), scale);             // max |g|
-        am = am < 1e-30f ? 1e-30f : am;
-        const float cq = __fdiv_rn(__fmul_rn(127.0f, scale), am);
+        if constexpr (FP8) {
+            // sg = max(max|g| / 448, 1e-30), code = e4m3(g / sg) with g / sg taken as
+            // gacc * (scale / sg); vb the same with sv
+            const float sgv = fmaxf(__fmul_rn(am, R448), 1e-30f);
+            float av = 0.0f;
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-            pg[db] = quant4(gacc[db], cq);
-            pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
-        }
-        if (grp == 0) {
-            s_sg[w * 16 + col][l - l0] = __fmul_rn(am, R127);
-            s_lz[w * 16 + col][l - l0] = __fadd_rn(mx, __logf(z));
+            for (int db = 0; db < 8; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) av = fmaxf(av, fabsf(vacc[db][i]));
+            const float svv = fmaxf(__fmul_rn(grp_max(av), R448), 1e-30f);
+            const float cg = __fdiv_rn(scale, sgv), cv = __fdiv_rn(1.0f, svv);
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                pg[db] = quant4_e4m3(gacc[db], cg);
+                pv[db] = u32x2{quant4_e4m3(vacc[db], cv), 0u};
+            }
+            if (grp == 0) {
+                s_sg[w * 16 + col][l - l0] = sgv;
+                s_sv[w * 16 + col][l - l0] = svv;
+                s_lz[w * 16 + col][l - l0] = __fadd_rn(mx, __logf(z));
+            }
+        } else {
+            am = am < 1e-30f ? 1e-30f : am;
+            const float cq = __fdiv_rn(__fmul_rn(127.0f, scale), am);
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                pg[db] = quant4(gacc[db], cq);
+                pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
+            }
+            if (grp == 0) {
+                s_sg[w * 16 + col][l - l0] = __fmul_rn(am, R127);
+                s_lz[w * 16 + col][l - l0] = __fadd_rn(mx, __logf(z));
+            }
         }
         pl = l;
     }
@@ -496,10 +570,14 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
                 *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = 0u;
-                *(u32x2*)(vb + s * D + 16 * db + 4 * grp) = u32x2{0u, 0u};
+                if (FP8)
+                    *(uint32_t*)((uint8_t*)vb + s * D + 16 * db + 4 * grp) = 0u;
+                else
+                    *(u32x2*)(vb + s * D + 16 * db + 4 * grp) = u32x2{0u, 0u};
             }
             if (grp == 0) {
                 s_sg[w * 16 + col][l - l0] = 0.0f;
+                if (FP8) s_sv[w * 16 + col][l - l0] = 0.0f;
                 s_lz[w * 16 + col][l - l0] = -INFINITY;
             }
         }
@@ -512,6 +590,7 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
             const int64_t s = ((int64_t)h * nt + tq) * nb_pad + l0 + 4 * qq;
             *(f32x4*)(sg + s) = *(const f32x4*)&s_sg[tt][4 * qq];
             *(f32x4*)(lz + s) = *(const f32x4*)&s_lz[tt][4 * qq];
+            if (FP8) *(f32x4*)(sv + s) = *(const f32x4*)&s_sv[tt][4 * qq];
         }
     }
 }
@@ -922,6 +1001,225 @@ __global__ __launch_bounds__(256) void tile_kernel(
     const int e_lo = sp * eps, e_hi = min(e_n, e_lo + eps);
     tile_far_near<LEAF>(st, gs, nb, nb_pad, lo, hi, e_lo, e_hi, kx, q8r, sqr, dq8r, sdqr, g8, sg, lz,
                         vb, excl + gs * nb_pad, idx + gs * (kx > 0 ? kx : 1), k8, ks, v, (int64_t)h * nk, scale);
+    const float ltot = grp_sum(st.l);
+    if (pacc == nullptr) {   // single split: normalise in place
+        const int64_t qi = (int64_t)t * TILE + r;
+        const int64_t oq = qi < nq ? perm_row(perm, h, nq, qi) : qi;
+        write_final(st, ltot, (int64_t)h * nq + oq, qi < nq, out, logz);
+        return;
+    }
+    const int64_t base = (th * ns + sp) * TILE + r;
+    if (grp == 0) {
+        pm[base] = st.m;
+        pl[base] = ltot;
+    }
+#pragma unroll
+    for (int db = 0; db < 8; ++db) *(f32x4*)(pacc + base * D + 16 * db + 4 * grp) = st.o[db];
+}
+
+// ---------------------------------------------------------------------------------------------
+// fp8 state store (store="fp8", h3/htrc_flat_triton.py:65-72, 132-153, 214-254 with FP8 = 1).
+//   select: SEL[g, l] = max_r (dq_r(fp16) . g_l(e4m3 -> fp16)) * sg_l + lz_l;
+//   tile, far: score = (dq(fp16) . g) * sg + lz, O += (p * sv)(fp16) . vb(e4m3 -> fp16);
+//   tile, near: score = (q(bf16) . k(bf16)) * scale, O += p(bf16) . v(bf16).
+// The e4m3 codes are widened to fp16 holding value * 2^-8 (e4m3x8_to_h8), exactly; sg and sv
+// are taken times 256 (exact), so every product is the reference's.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void select_fp8_kernel(const uint16_t* __restrict__ dq16, int stride,
+                                                         const uint8_t* __restrict__ g, const float* __restrict__ sg,
+                                                         const float* __restrict__ lz, int nt, int group, int ng,
+                                                         int nb, int nb_pad, float* __restrict__ sel) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int gi = blockIdx.x, h = blockIdx.z;
+    const int64_t gs = (int64_t)h * ng + gi;
+    const int ts = TILE / stride;
+    const int c0 = blockIdx.y * 256 + w * 64;
+    float bsel[4][4];
+#pragma unroll
+    for (int lb = 0; lb < 4; ++lb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bsel[lb][i] = -INFINITY;
+    for (int j = 0; j < group; ++j) {
+        const int t = gi * group + j;
+        if (t >= nt) break;                           // padded tiles repeat the last one
+        const int64_t th = (int64_t)h * nt + t;
+        u32x4 b[4][4];
+        bool val[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int r = 16 * rb + col;
+            val[rb] = r < ts;
+            const int64_t p = th * TILE + (int64_t)(val[rb] ? r : 0) * stride;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) b[rb][ks] = *(const u32x4*)(dq16 + p * D + 32 * ks + 8 * grp);
+        }
+#pragma unroll
+        for (int lb = 0; lb < 4; ++lb) {
+            const int c = c0 + 16 * lb;
+            if (c < nb) {
+                const int64_t s0 = gs * nb_pad + c;
+                f32x4 acc[4];
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const u32x4 A = e4m3x8_to_h8(*(const u32x2*)(g + (s0 + col) * D + 32 * ks + 8 * grp));
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma_f16(A, b[rb][ks], acc[rb]);
+                }
+                const f32x4 sgv = *(const f32x4*)(sg + s0 + 4 * grp);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float best = -INFINITY;
+                    const float sc = __fmul_rn(sgv[i], 256.0f);
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb)
+                        if (val[rb]) best = fmaxf(best, __fmul_rn(acc[rb][i], sc));
+                    bsel[lb][i] = fmaxf(bsel[lb][i], col_max(best));
+                }
+            }
+        }
+    }
+    if (col == 0) {
+#pragma unroll
+        for (int lb = 0; lb < 4; ++lb) {
+            const int c = c0 + 16 * lb;
+            if (c >= nb) break;
+            const f32x4 lzv = *(const f32x4*)(lz + gs * nb_pad + c + 4 * grp);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int l = c + 4 * grp + i;
+                if (l < nb) sel[gs * nb_pad + l] = __fadd_rn(bsel[lb][i], lzv[i]);
+            }
+        }
+    }
+}
+
+// Online update (as online_block) whose PV operand is fp16: P = fp16(p * pscale) per key.
+template <typename VFetch>
+__device__ __forceinline__ void online_block_f16(RowState& st, float (&sc)[8], const float (&pscale)[8],
+                                                 VFetch&& vfetch) {
+    float bm = sc[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) bm = fmaxf(bm, sc[e]);
+    bm = grp_max(bm);
+    const float m_new = fmaxf(st.m, bm);
+    const float m_s = m_new == -INFINITY ? 0.0f : m_new;
+    float p[8], ps = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        p[e] = __expf(__fsub_rn(sc[e], m_s));
+        ps = __fadd_rn(ps, p[e]);
+    }
+    const float alpha = __expf(__fsub_rn(st.m, m_s));
+    st.l = __fadd_rn(__fmul_rn(st.l, alpha), ps);
+    uint32_t ph[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        ph[j] = pack2h(__fmul_rn(p[2 * j], pscale[2 * j]), __fmul_rn(p[2 * j + 1], pscale[2 * j + 1]));
+    const u32x4 P = u32x4{ph[0], ph[1], ph[2], ph[3]};
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+        f32x4 o = st.o[db];
+        o[0] = __fmul_rn(o[0], alpha);
+        o[1] = __fmul_rn(o[1], alpha);
+        o[2] = __fmul_rn(o[2], alpha);
+        o[3] = __fmul_rn(o[3], alpha);
+        st.o[db] = mfma_f16(vfetch(db), P, o);
+    }
+    st.m = m_new;
+}
+
+template <int LEAF>
+__global__ __launch_bounds__(256) void tile_fp8_kernel(
+    const uint16_t* __restrict__ q16, const uint16_t* __restrict__ dq16, const uint8_t* __restrict__ g,
+    const float* __restrict__ sg, const float* __restrict__ lz, const uint8_t* __restrict__ vb,
+    const float* __restrict__ sv, const int8_t* __restrict__ excl, const int32_t* __restrict__ idx,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t nq, int nt, int group, int ng,
+    const int32_t* __restrict__ perm, int64_t nk, int nb, int nb_pad, int kx, int lps, int eps, float scale,
+    float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc, float* __restrict__ out,
+    float* __restrict__ logz) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int t = blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
+    const int64_t th = (int64_t)h * nt + t;
+    const int64_t gs = (int64_t)h * ng + t / group;       // state / routing row: the tile's group
+    const int r = w * 16 + col;
+    const int64_t p = th * TILE + r;
+    u32x4 qb[4], dqh[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        qb[ks] = *(const u32x4*)(q16 + p * D + 32 * ks + 8 * grp);
+        dqh[ks] = *(const u32x4*)(dq16 + p * D + 32 * ks + 8 * grp);
+    }
+    RowState st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) st.o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int lo = sp * lps, hi = min(nb, lo + lps);
+    const int e_n = kx * LEAF;
+    const int e_lo = sp * eps, e_hi = min(e_n, e_lo + eps);
+    const int8_t* excl_row = excl + gs * nb_pad;
+    // ---- far field
+    for (int c0 = lo; c0 < hi; c0 += 32) {
+        float sc[8], pscale[8];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const int cb = c0 + 16 * h2;
+            const int64_t s0 = gs * nb_pad + cb;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                acc = mfma_f16(e4m3x8_to_h8(*(const u32x2*)(g + (s0 + col) * D + 32 * ks + 8 * grp)), dqh[ks], acc);
+            const f32x4 sgv = *(const f32x4*)(sg + s0 + 4 * grp);
+            const f32x4 svv = *(const f32x4*)(sv + s0 + 4 * grp);
+            const f32x4 lzv = *(const f32x4*)(lz + s0 + 4 * grp);
+            const uint32_t exv = *(const uint32_t*)(excl_row + cb + 4 * grp);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = cb + 4 * grp + i;
+                const bool ok = c < hi && ((exv >> (8 * i)) & 0xffu) == 0u;
+                sc[4 * h2 + i] = ok ? __fadd_rn(__fmul_rn(acc[i], __fmul_rn(sgv[i], 256.0f)), lzv[i]) : -INFINITY;
+                pscale[4 * h2 + i] = __fmul_rn(svv[i], 256.0f);
+            }
+        }
+        const uint8_t* vb0 = vb + (gs * nb_pad + c0) * D;
+        online_block_f16(st, sc, pscale, [&](int db) {   // vb^T: keys 4grp + j and 16 + 4grp + j at one dim
+            const int dim = 16 * db + col;
+            uint32_t u[2];
+#pragma unroll
+            for (int jh = 0; jh < 2; ++jh) {
+                const uint8_t* b = vb0 + (16 * jh + 4 * grp) * D + dim;
+                u[jh] = (uint32_t)b[0] | ((uint32_t)b[D] << 8) | ((uint32_t)b[2 * D] << 16) | ((uint32_t)b[3 * D] << 24);
+            }
+            return e4m3x8_to_h8(u32x2{u[0], u[1]});
+        });
+    }
+    // ---- near field: token j of the tile's selected list -> idx[j / LEAF] * LEAF + j % LEAF
+    const int32_t* idx_row = idx + gs * (kx > 0 ? kx : 1);
+    const int64_t kh = (int64_t)h * nk;
+    for (int e0 = e_lo; e0 < e_hi; e0 += 32) {
+        float sc[8];
+        int64_t tok0[2];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const int j0 = e0 + 16 * h2;
+            const bool ok = j0 < e_hi;
+            const int jj = ok ? j0 : e_lo;
+            tok0[h2] = kh + (int64_t)idx_row[jj / LEAF] * LEAF + (jj % LEAF);
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                acc = mfma_bf16(as_bf16x8(*(const u32x4*)(k + (tok0[h2] + col) * D + 32 * ks + 8 * grp)),
+                                as_bf16x8(qb[ks]), acc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool oki = ok && (j0 + 4 * grp + i) < e_hi;
+                sc[4 * h2 + i] = oki ? __fmul_rn(acc[i], scale) : -INFINITY;
+            }
+        }
+        online_block(st, sc, [&](int db) { return gather_pv(v, tok0[0], tok0[1], 16 * db + col, grp); });
+    }
     const float ltot = grp_sum(st.l);
     if (pacc == nullptr) {   // single split: normalise in place
         const int64_t qi = (int64_t)t * TILE + r;
@@ -1852,7 +2150,7 @@ int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64
 #define STATS_CASE(L)                                                                                         \
     case L:                                                                                                   \
         hipLaunchKernelGGL(stats_kernel<L>, grid, dim3(256), 0, s, mu, (int)nt, k, v, nk, (int)nb, nbp, lpb, scale, \
-                           g8, sg, vb, lz);                                                                   \
+                           g8, sg, vb, nullptr, lz);                                                          \
         break;
     switch (leaf) {
         STATS_CASE(16)
@@ -1862,6 +2160,39 @@ int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64
     }
 #undef STATS_CASE
     return launched("htrc_leaf_stats");
+}
+
+int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
+                        int leaf, int d, float scale, uint8_t* g, float* sg, uint8_t* vb, float* sv, float* lz,
+                        void* stream) {
+    REQUIRE(mu && k && v && g && sg && vb && sv && lz, "htrc_leaf_stats_fp8: null pointer");
+    REQUIRE(d == D, "htrc_leaf_stats_fp8: head dim must be 128");
+    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_leaf_stats_fp8: leaf must be 16/32/64/128");
+    REQUIRE(nk > 0 && nk % leaf == 0, "htrc_leaf_stats_fp8: key count must be a multiple of the leaf size");
+    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff, "htrc_leaf_stats_fp8: bad heads / tiles");
+    REQUIRE(aligned(k, 16) && aligned(v, 16) && aligned(g, 16) && aligned(vb, 16) && aligned(sg, 16) && aligned(sv, 16) &&
+                aligned(lz, 16),
+            "htrc_leaf_stats_fp8: misaligned buffer");
+    const int64_t nb = nk / leaf;
+    const int nbp = htrc_nb_pad(nb);
+    const int lpb = 16;
+    const int64_t nblocks = (nt + 63) / 64 * ((nbp + lpb - 1) / lpb) * heads;
+    REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats_fp8: too many tiles x leaves x heads for one launch");
+    dim3 grid((unsigned)nblocks);
+    hipStream_t s = (hipStream_t)stream;
+#define STATS8_CASE(L)                                                                                         \
+    case L:                                                                                                    \
+        hipLaunchKernelGGL((stats_kernel<L, true>), grid, dim3(256), 0, s, mu, (int)nt, k, v, nk, (int)nb, nbp, lpb, \
+                           scale, (int8_t*)g, sg, (uint16_t*)vb, sv, lz);                                      \
+        break;
+    switch (leaf) {
+        STATS8_CASE(16)
+        STATS8_CASE(32)
+        STATS8_CASE(64)
+        STATS8_CASE(128)
+    }
+#undef STATS8_CASE
+    return launched("htrc_leaf_stats_fp8");
 }
 
 int htrc_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
@@ -1931,6 +2262,96 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
     }
 #undef TILE_CASE
     return launched("htrc_tile");
+}
+
+int htrc_pack_q16(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, const int32_t* perm,
+                  int dq_fp16, float* mu, uint16_t* q16, uint16_t* dq16, void* stream) {
+    REQUIRE(q && mu && q16 && dq16, "htrc_pack_q16: null pointer");
+    REQUIRE(d == D, "htrc_pack_q16: head dim must be 128");
+    REQUIRE(heads > 0 && heads <= 65535 && nq > 0, "htrc_pack_q16: bad heads / rows");
+    REQUIRE(group >= 1 && group <= 1024, "htrc_pack_q16: group must be in [1, 1024]");
+    REQUIRE(aligned(q, 16) && aligned(q16, 16) && aligned(dq16, 16), "htrc_pack_q16: misaligned buffer");
+    const int64_t nt = (nq + TILE - 1) / TILE;
+    REQUIRE(nt <= 0x7fffffff, "htrc_pack_q16: too many tiles");
+    const int64_t ng = (nt + group - 1) / group;
+    hipStream_t s = (hipStream_t)stream;
+    if (group > 1) {
+        const dim3 gg((unsigned)ng, (unsigned)heads);
+        if (q_is_bf16)
+            hipLaunchKernelGGL(group_centres_kernel<true>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, perm, mu);
+        else
+            hipLaunchKernelGGL(group_centres_kernel<false>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, perm,
+                               mu);
+    }
+    dim3 grid((unsigned)nt, (unsigned)heads);
+    int8_t* a = (int8_t*)q16;
+    int8_t* b = (int8_t*)dq16;
+#define PACK16(BF, QM)                                                                                          \
+    hipLaunchKernelGGL((pack_q_kernel<BF, QM>), grid, dim3(256), 0, s, q, nq, (int)nt, group, (int)ng, perm, mu, a, \
+                       nullptr, b, nullptr)
+    if (q_is_bf16) {
+        if (dq_fp16) PACK16(true, 2); else PACK16(true, 1);
+    } else {
+        if (dq_fp16) PACK16(false, 2); else PACK16(false, 1);
+    }
+#undef PACK16
+    return launched("htrc_pack_q16");
+}
+
+int htrc_select_fp8(const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz, int64_t heads, int64_t nt,
+                    int64_t nb, int stride, int group, int d, float* sel, void* stream) {
+    REQUIRE(dq16 && g && sg && lz && sel, "htrc_select_fp8: null pointer");
+    REQUIRE(d == D, "htrc_select_fp8: head dim must be 128");
+    REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_select_fp8: stride must divide 64");
+    REQUIRE(group >= 1 && group <= 1024, "htrc_select_fp8: group must be in [1, 1024]");
+    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff && nb > 0, "htrc_select_fp8: bad sizes");
+    REQUIRE(aligned(dq16, 16) && aligned(g, 16) && aligned(sg, 16) && aligned(lz, 16), "htrc_select_fp8: misaligned buffer");
+    const int nbp = htrc_nb_pad(nb);
+    const int64_t ng = (nt + group - 1) / group;
+    dim3 grid((unsigned)ng, (unsigned)((nb + 255) / 256), (unsigned)heads);
+    hipLaunchKernelGGL(select_fp8_kernel, grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, sg, lz, (int)nt,
+                       group, (int)ng, (int)nb, nbp, sel);
+    return launched("htrc_select_fp8");
+}
+
+int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz,
+                  const uint8_t* vb, const float* sv, const int8_t* excl, const int32_t* idx, const uint16_t* k,
+                  const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int group,
+                  const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out,
+                  float* logz, void* stream) {
+    REQUIRE(q16 && dq16 && g && sg && lz && vb && sv && excl && k && v, "htrc_tile_fp8: null input pointer");
+    REQUIRE(d == D, "htrc_tile_fp8: head dim must be 128");
+    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_tile_fp8: leaf must be 16/32/64/128");
+    REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_tile_fp8: bad sizes");
+    const int64_t nb = nk / leaf, nt = (nq + TILE - 1) / TILE;
+    REQUIRE(kx >= 0 && kx <= nb && (kx == 0 || idx), "htrc_tile_fp8: need 0 <= kx <= leaves and idx when kx > 0");
+    REQUIRE(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0, "htrc_tile_fp8: need 1 <= splits <= 64 and a block that is a multiple of 32");
+    REQUIRE(splits == 1 ? (out && logz) : (pm && pl && pacc), "htrc_tile_fp8: missing outputs");
+    REQUIRE(group >= 1 && group <= 1024, "htrc_tile_fp8: group must be in [1, 1024]");
+    REQUIRE(aligned(q16, 16) && aligned(dq16, 16) && aligned(g, 16) && aligned(k, 16) && aligned(sg, 16) &&
+                aligned(sv, 16) && aligned(lz, 16),
+            "htrc_tile_fp8: misaligned buffer");
+    const int64_t ng = (nt + group - 1) / group;
+    const int lps = (int)split_len(nb, splits, bn), eps = (int)split_len((int64_t)kx * leaf, splits, bn);
+    dim3 grid((unsigned)nt, (unsigned)splits, (unsigned)heads);
+    hipStream_t s = (hipStream_t)stream;
+    float* ppm = splits == 1 ? nullptr : pm;
+    float* ppl = splits == 1 ? nullptr : pl;
+    float* ppa = splits == 1 ? nullptr : pacc;
+#define TILE8_CASE(L)                                                                                              \
+    case L:                                                                                                        \
+        hipLaunchKernelGGL(tile_fp8_kernel<L>, grid, dim3(256), 0, s, q16, dq16, g, sg, lz, vb, sv, excl, idx, k, v, nq, \
+                           (int)nt, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps, scale, ppm, ppl,   \
+                           ppa, out, logz);                                                                        \
+        break;
+    switch (leaf) {
+        TILE8_CASE(16)
+        TILE8_CASE(32)
+        TILE8_CASE(64)
+        TILE8_CASE(128)
+    }
+#undef TILE8_CASE
+    return launched("htrc_tile_fp8");
 }
 
 int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int splits,

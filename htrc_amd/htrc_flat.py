@@ -59,8 +59,9 @@ def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot
                          "HIP kernels (backend='hip', alias 'triton')")
     if curvature != "lin":
         raise ValueError("the HIP backend needs curvature='lin'")
-    if store != "int8" or dot != "bf16":
-        raise ValueError("the HIP backend implements store='int8', dot='bf16' (int8 Q/K dots, bf16 PV)")
+    if store not in ("int8", "fp8") or dot != "bf16":
+        raise ValueError("the HIP backend implements dot='bf16' with store='int8' (int8 Q/K dots, bf16 PV) "
+                         "or store='fp8' (e4m3 leaf state)")
     if select != "max":
         raise ValueError("the HIP backend implements select='max'")
     if order not in ("seq", "kmeans"):
@@ -128,6 +129,9 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     if qh.dtype not in (torch.float32, torch.bfloat16):
         qh = qh.float()
     perm = hip.kmeans_order(qh, ws=ws) if order == "kmeans" else None   # query rows regrouped by k-means
+    if store == "fp8":
+        return _flat_fp8(qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, stride, group, perm, splits, kern,
+                         tail, ws, return_logz, state)
     mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), ws=ws, group=group, perm=perm)
     kb = kh.to(torch.bfloat16).contiguous()
     vb = vh.to(torch.bfloat16).contiguous()
@@ -168,6 +172,49 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         state["nb"], state["kx"], state["group"], state["perm"] = nb, kx, group, perm
     if tail is not None and int(tail[0].shape[-2]) > 0:
         # keys past the last full leaf, exact for every query (h3/htrc_flat_triton.py:187-207, 381-388)
+        tk, tv = (x.unsqueeze(0) if squeeze else x for x in tail)
+        hip.tail_merge(qh, tk.to(qh.device), tv.to(qh.device), scale=scale, out=out, logz=logz)
+        tick("tail")
+    res = out[0] if squeeze else out
+    lzr = logz[0] if squeeze else logz
+    tick("finish")
+    return (res, lzr) if return_logz else res
+
+
+def _flat_fp8(qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, stride, group, perm, splits, kern, tail, ws,
+              return_logz, state):
+    """store="fp8": e4m3 leaf state with row scales, fp16 far dots, bf16 near dots, run as the
+    reference's stage structure (select, top-k, split tile kernel, merge;
+    h3/htrc_flat_triton.py:65-72, 104-108, 132-153, 165-184, 214-254 with FP8 = 1)."""
+    h = int(qh.shape[0])
+    mu, q16, dq16 = hip.pack_q16(qh.contiguous(), ws=ws, group=group, perm=perm, dq_fp16=True)
+    kb = kh.to(torch.bfloat16).contiguous()
+    vb = vh.to(torch.bfloat16).contiguous()
+    tick("prep")
+    g, lz, vbs, sg, sv = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=torch.float8_e4m3fn, ws=ws)
+    tick("stats")
+    ng = int(mu.shape[1])
+    idx = None
+    if kx > 0:
+        sel = hip.rowmax_select(g=g, lz=lz, sg=sg, stride=stride, nb=nb, dq8=dq16, ws=ws, group=group)
+        idx, excl = hip.topk_excl(sel, nb, kx, sink, ws=ws)
+        if state is not None:
+            state["sel"] = sel
+    else:
+        excl = hip._buf(ws, "excl", (h, ng, nb_pad(nb)), torch.int8, qh.device)
+        excl.zero_()
+    tick("select")
+    packed = {"q16": q16, "dq16": dq16, "k": kb, "v": vb, "mu": mu}
+    lstate = {"g8": g, "sg": sg, "lz": lz, "vb": vbs, "sv": sv}
+    out, logz = hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
+                                   bn=int(kern.get("tile_bn", 32)), ws=ws, group=group, perm=perm)
+    tick("tile")
+    if state is not None:
+        state.update(packed)
+        state.update(lstate)
+        state["idx"], state["excl"] = idx, excl
+        state["nb"], state["kx"], state["group"], state["perm"] = nb, kx, group, perm
+    if tail is not None and int(tail[0].shape[-2]) > 0:
         tk, tv = (x.unsqueeze(0) if squeeze else x for x in tail)
         hip.tail_merge(qh, tk.to(qh.device), tv.to(qh.device), scale=scale, out=out, logz=logz)
         tick("tail")

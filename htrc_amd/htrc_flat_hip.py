@@ -92,6 +92,31 @@ def pack_q(q: torch.Tensor, tile: int = TILE, ws=None, group: int = 1, perm=None
     return mu, q8, sq, dq8, sdq
 
 
+def pack_q16(q: torch.Tensor, tile: int = TILE, ws=None, group: int = 1, perm=None, dq_fp16: bool = True):
+    """Centres and the 16-bit operands of the fp8 (and bf16) state stores -> (mu [H,ng,D],
+    q16 bf16 [H,nt*64,D] = bf16(q), dq16 [H,nt*64,D] = fp16(q - mu) (bf16 when dq_fp16 is
+    False)) over the padded tile rows (h3/htrc_flat_triton.py:104-108)."""
+    if tile != TILE:
+        raise ValueError("the HIP kernels use 64-row query tiles")
+    q = _heads(q)
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        q = q.float()
+    q = q.contiguous()
+    _need(q, None, "q")
+    h, nq, d = (int(x) for x in q.shape)
+    nt = -(-nq // TILE)
+    ng = -(-nt // int(group))
+    dev = q.device
+    if perm is not None:
+        _need(perm, torch.int32, "perm")
+    mu = _buf(ws, "mu", (h, ng, d), torch.float32, dev)
+    q16 = _buf(ws, "q16", (h, nt * TILE, d), torch.bfloat16, dev)
+    dq16 = _buf(ws, "dq16" if dq_fp16 else "dqb16", (h, nt * TILE, d), torch.float16 if dq_fp16 else torch.bfloat16, dev)
+    call("htrc_pack_q16", ptr(q), int(q.dtype == torch.bfloat16), h, nq, d, int(group), ptr(perm), int(bool(dq_fp16)),
+         ptr(mu), ptr(q16), ptr(dq16), stream_handle(dev))
+    return mu, q16, dq16
+
+
 def pack_k(k: torch.Tensor, ws=None):
     """K int8 per row (round half to even) -> (k8 [H,nk,D] int8, ks [H,nk] fp32)."""
     k = _heads(k).to(torch.bfloat16).contiguous()
@@ -105,11 +130,12 @@ def pack_k(k: torch.Tensor, ws=None):
 
 
 def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4, store=torch.int8, ws=None):
-    """Leaf statistics at the tile centres (h3/htrc_flat_triton.py:329-345, I8 store).
-    mu [H,nt,D] fp32, kf/vf bf16 [H,nk,D] -> (g8 [H,nt,nbp,D] int8, lz [H,nt,nbp], vb [H,nt,nbp,D]
-    bf16, sg [H,nt,nbp], None) in the reference's (g, lz, vb, sg, sv) order."""
-    if store != torch.int8:
-        raise ValueError("the HIP leaf statistics store g as int8 (store='int8')")
+    """Leaf statistics at the tile centres (h3/htrc_flat_triton.py:329-345).
+    mu [H,nt,D] fp32, kf/vf bf16 [H,nk,D] -> (g, lz, vb, sg, sv) in the reference's order:
+    store=int8: g int8 [H,nt,nbp,D], vb bf16, sv None; store=float8_e4m3fn: g and vb e4m3
+    with the row scales sg, sv (h3/htrc_flat_triton.py:65-72)."""
+    if store not in (torch.int8, torch.float8_e4m3fn):
+        raise ValueError("the HIP leaf statistics store g as int8 or float8_e4m3fn")
     mu = _heads(mu).contiguous()
     kf = _heads(kf).contiguous()
     vf = _heads(vf).contiguous()
@@ -122,6 +148,15 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
         raise ValueError("keys and values must be [H, nb * leaf, D]")
     nbp = nb_pad(nb)
     dev = mu.device
+    if store == torch.float8_e4m3fn:
+        g = _buf(ws, "g_fp8", (h, nt, nbp, d), torch.float8_e4m3fn, dev)
+        vb = _buf(ws, "vb_fp8", (h, nt, nbp, d), torch.float8_e4m3fn, dev)
+        sg = _buf(ws, "sg", (h, nt, nbp), torch.float32, dev)
+        sv = _buf(ws, "sv", (h, nt, nbp), torch.float32, dev)
+        lz = _buf(ws, "lz", (h, nt, nbp), torch.float32, dev)
+        call("htrc_leaf_stats_fp8", ptr(mu), ptr(kf), ptr(vf), h, nt, nk, int(leaf), d, float(scale), ptr(g), ptr(sg),
+             ptr(vb), ptr(sv), ptr(lz), stream_handle(dev))
+        return g, lz, vb, sg, sv
     g8 = _buf(ws, "g", (h, nt, nbp, d), torch.int8, dev)
     sg = _buf(ws, "sg", (h, nt, nbp), torch.float32, dev)
     lz = _buf(ws, "lz", (h, nt, nbp), torch.float32, dev)
@@ -136,6 +171,8 @@ def rowmax_select(q_c=None, mu_c=None, g=None, lz=None, prec="ieee", bn=32, warp
     """SEL [H,ng,nbp] (h3/htrc_flat_triton.py:315-326), the max over the rows of each group of
     ``group`` tiles.  Takes the packed rows dq8/sdq (pack_q); when absent they are packed from
     q_c (fp32 [H,nq,D] rows)."""
+    if g.dtype == torch.float8_e4m3fn:
+        return _select_fp8(g, lz, sg, stride, nb, dq8, group, ws, q_c)
     if dq8 is None or sdq is None:
         _, _, _, dq8, sdq = pack_q(q_c, group=group)
     g = _heads(g) if g.dim() == 3 else g
@@ -148,6 +185,20 @@ def rowmax_select(q_c=None, mu_c=None, g=None, lz=None, prec="ieee", bn=32, warp
     sel = _buf(ws, "sel", (h, ng, nbp), torch.float32, dev)
     call("htrc_select", ptr(dq8), ptr(sdq), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), int(group), d,
          ptr(sel), stream_handle(dev))
+    return sel
+
+
+def _select_fp8(g, lz, sg, stride, nb, dq16, group, ws, q_c):
+    """SEL over the fp8 state: dq16 are the fp16 rows of pack_q16 (passed as ``dq8``)."""
+    if dq16 is None:
+        _, _, dq16 = pack_q16(q_c, group=group)
+    _need(dq16, torch.float16, "dq16")
+    h, ng, nbp, d = (int(x) for x in g.shape)
+    nt = int(_heads(dq16).shape[1]) // TILE
+    nb = nbp if nb is None else int(nb)
+    sel = _buf(ws, "sel", (h, ng, nbp), torch.float32, g.device)
+    call("htrc_select_fp8", ptr(dq16), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), int(group), d, ptr(sel),
+         stream_handle(g.device))
     return sel
 
 
@@ -166,6 +217,9 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
                    bn: int = 64, ws=None, out=None, logz=None, group: int = 1, perm=None):
     """Far + near online softmax per (tile, split) and the merge
     (h3/htrc_flat_triton.py:348-391) -> (out [H,nq,D] fp32, logz [H,nq] fp32)."""
+    if state["g8"].dtype == torch.float8_e4m3fn:
+        return _tile_fp8(packed, state, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits, bn=bn, ws=ws,
+                         out=out, logz=logz, group=group, perm=perm)
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
     g8, sg, lz, vb = state["g8"], state["sg"], state["lz"], state["vb"]
@@ -185,6 +239,33 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
         pacc = _buf(ws, "pacc", (h, nt, ns, TILE, d), torch.float32, dev)
     call("htrc_tile", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(excl),
          ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(v), h, nq, nk, int(leaf), d, kx, int(group), ptr(perm), ns, int(bn),
+         float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
+    if ns > 1:
+        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, ns, d, ptr(perm), ptr(out), ptr(logz), stream_handle(dev))
+    return out, logz
+
+
+def _tile_fp8(packed, state, excl, idx, *, nq, leaf, scale, splits, bn, ws, out, logz, group, perm):
+    """Far + near softmax per (tile, split) over the fp8 state, and the merge: packed holds
+    q16, dq16 (pack_q16) and the bf16 k, v; state g8 / vb (e4m3), sg, sv, lz."""
+    q16, dq16, k, v = packed["q16"], packed["dq16"], packed["k"], packed["v"]
+    g, sg, lz, vb, sv = state["g8"], state["sg"], state["lz"], state["vb"], state["sv"]
+    h, nk, d = (int(x) for x in k.shape)
+    nt = -(-nq // TILE)
+    kx = int(idx.shape[-1]) if idx is not None else 0
+    dev = q16.device
+    ns = max(1, int(splits))
+    if out is None:
+        out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
+    if logz is None:
+        logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
+    pm = pl = pacc = None
+    if ns > 1:
+        pm = _buf(ws, "pm", (h, nt, ns, TILE), torch.float32, dev)
+        pl = _buf(ws, "pl", (h, nt, ns, TILE), torch.float32, dev)
+        pacc = _buf(ws, "pacc", (h, nt, ns, TILE, d), torch.float32, dev)
+    call("htrc_tile_fp8", ptr(q16), ptr(dq16), ptr(g), ptr(sg), ptr(lz), ptr(vb), ptr(sv), ptr(excl),
+         ptr(idx) if kx else None, ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, int(group), ptr(perm), ns, int(bn),
          float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
     if ns > 1:
         call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, ns, d, ptr(perm), ptr(out), ptr(logz), stream_handle(dev))

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 8
+#define HTRC_ABI_VERSION 9
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -124,6 +124,27 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
  * Replaces the tail handling of tile_attention (h3/htrc_flat_triton.py:187-207, 366-388). */
 int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
               int64_t ntail, int d, float scale, float* out, float* logz, void* stream);
+
+/* fp8 state store (store="fp8"; h3/htrc_flat_triton.py:65-72, 104-108, 132-153, 165-184,
+ * 214-254 with FP8 = 1), run in the reference's stage structure (select, top-k, tile, merge):
+ *   q16 bf16 [H, nt*64, 128] = bf16(q), dq16 [H, nt*64, 128] = fp16(q - mu) (dq_fp16 = 1) or
+ *   bf16(q - mu) (dq_fp16 = 0); g, vb uint8 e4m3fn [H, ng, nbp, 128] = code(x / s) with row
+ *   scales sg, sv fp32 [H, ng, nbp] = max(max|x| * fp32(1/448), 1e-30); lz as the int8 path.
+ *   select: SEL = max_r (fp16 dq . g) * sg + lz; tile far: (fp16 dq . g) * sg + lz with
+ *   PV (p sv)(fp16) . vb; near: (bf16 q . bf16 k) * scale with PV bf16(p) . v.
+ * Replace leaf_stats(store=float8_e4m3fn), rowmax_select and tile_attention on that state. */
+int htrc_pack_q16(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, const int32_t* perm,
+                  int dq_fp16, float* mu, uint16_t* q16, uint16_t* dq16, void* stream);
+int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
+                        int leaf, int d, float scale, uint8_t* g, float* sg, uint8_t* vb, float* sv, float* lz,
+                        void* stream);
+int htrc_select_fp8(const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz, int64_t heads, int64_t nt,
+                    int64_t nb, int stride, int group, int d, float* sel, void* stream);
+int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz,
+                  const uint8_t* vb, const float* sv, const int8_t* excl, const int32_t* idx, const uint16_t* k,
+                  const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int group,
+                  const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out,
+                  float* logz, void* stream);
 
 /* k-means query order: perm int32 [H, nq], the queries ordered by their nearest of `clusters`
  * centres (stable), the centres from `iters` Lloyd steps on `sample` evenly spaced queries.

@@ -35,7 +35,7 @@
  * (h3/htrc_flat.py:217, h3/htrc_flat_triton.py:76,112,115,231). */
 static const float R127 = 1.0f / 127.0f;
 
-int oracle_abi_version(void) { return 3; }
+int oracle_abi_version(void) { return 4; }
 
 float oracle_r127(void) { return R127; }
 
@@ -175,6 +175,36 @@ void oracle_pack_q(const float *q, int64_t n, int d, int tile, int group, const 
  *   am = max(max|g|, 1e-30); sg = am * fp32(1/127); g8 = round_away(g * (127 / am))
  *   vb stored as bf16 (RNE).
  * Dots are sequential fp32 sums (dims for a, leaf tokens for g / vb). */
+/* The fp32 leaf state of centre m_ and leaf rows K, V (bf16): g (scaled) in gs, vb in vs,
+ * returning max a and z through mx, z.  a, kf are work arrays of leaf and leaf * d floats. */
+static void leaf_state(const float *m_, const uint16_t *K, const uint16_t *V, int leaf, int d, float scale,
+                       float *a, float *kf, float *gs, float *vs, float *mx_out, float *z_out) {
+    for (int s = 0; s < leaf * d; ++s) kf[s] = bf2f(K[s]);
+    for (int s = 0; s < leaf; ++s) a[s] = 0.0f;
+    for (int i = 0; i < d; ++i)          /* a[s] summed over i in order, vectorised over s */
+        for (int s = 0; s < leaf; ++s) a[s] += m_[i] * kf[s * d + i];
+    float mx = -INFINITY;
+    for (int s = 0; s < leaf; ++s) {
+        a[s] = a[s] * scale;
+        if (a[s] > mx) mx = a[s];
+    }
+    float z = 0.0f;
+    for (int s = 0; s < leaf; ++s) {
+        a[s] = expf(a[s] - mx);
+        z += a[s];
+    }
+    for (int s = 0; s < leaf; ++s) a[s] = a[s] / z;
+    for (int i = 0; i < d; ++i) gs[i] = vs[i] = 0.0f;
+    for (int s = 0; s < leaf; ++s)       /* summed over tokens in order, vectorised over dims */
+        for (int i = 0; i < d; ++i) {
+            gs[i] += a[s] * kf[s * d + i];
+            vs[i] += a[s] * bf2f(V[s * d + i]);
+        }
+    for (int i = 0; i < d; ++i) gs[i] = gs[i] * scale;
+    *mx_out = mx;
+    *z_out = z;
+}
+
 void oracle_stats(const float *mu, int64_t nt, const uint16_t *k, const uint16_t *v,
                   int64_t nb, int leaf, int d, float scale,
                   int8_t *g8, float *sg, uint16_t *vb, float *lz) {
@@ -187,33 +217,10 @@ void oracle_stats(const float *mu, int64_t nt, const uint16_t *k, const uint16_t
 #pragma omp for schedule(static)
         for (int64_t tl_ = 0; tl_ < nt * nb; ++tl_) {
             int64_t t = tl_ / nb, l = tl_ % nb;
-            const float *m_ = mu + t * d;
-            const uint16_t *K = k + l * leaf * d;
-            const uint16_t *V = v + l * leaf * d;
-            for (int s = 0; s < leaf * d; ++s) kf[s] = bf2f(K[s]);
-            for (int s = 0; s < leaf; ++s) a[s] = 0.0f;
-            for (int i = 0; i < d; ++i)          /* a[s] summed over i in order, vectorised over s */
-                for (int s = 0; s < leaf; ++s) a[s] += m_[i] * kf[s * d + i];
-            float mx = -INFINITY;
-            for (int s = 0; s < leaf; ++s) {
-                a[s] = a[s] * scale;
-                if (a[s] > mx) mx = a[s];
-            }
-            float z = 0.0f;
-            for (int s = 0; s < leaf; ++s) {
-                a[s] = expf(a[s] - mx);
-                z += a[s];
-            }
-            for (int s = 0; s < leaf; ++s) a[s] = a[s] / z;
-            for (int i = 0; i < d; ++i) gs[i] = vs[i] = 0.0f;
-            for (int s = 0; s < leaf; ++s)       /* summed over tokens in order, vectorised over dims */
-                for (int i = 0; i < d; ++i) {
-                    gs[i] += a[s] * kf[s * d + i];
-                    vs[i] += a[s] * bf2f(V[s * d + i]);
-                }
+            float mx, z;
+            leaf_state(mu + t * d, k + l * leaf * d, v + l * leaf * d, leaf, d, scale, a, kf, gs, vs, &mx, &z);
             float am = 0.0f;
             for (int i = 0; i < d; ++i) {
-                gs[i] = gs[i] * scale;
                 float x = fabsf(gs[i]);
                 if (x > am) am = x;
             }
@@ -227,6 +234,72 @@ void oracle_stats(const float *mu, int64_t nt, const uint16_t *k, const uint16_t
             }
             sg[t * nb + l] = am * R127;
             lz[t * nb + l] = mx + logf(z);
+        }
+        free(a);
+        free(kf);
+        free(gs);
+        free(vs);
+    }
+}
+
+/* e4m3fn (OCP fp8, bias 7, no infinities) code of x, round to nearest even; |x| above 448 (the
+ * largest finite value) saturates to 448 (Triton's satfinite conversion; the state scales keep
+ * |x| <= 448). */
+uint8_t oracle_f32_to_e4m3(float x) {
+    uint8_t sgn = (uint8_t)(signbit(x) ? 0x80 : 0);
+    float a = fabsf(x);
+    if (!(a <= 448.0f)) a = 448.0f;
+    if (a < 0.015625f) return sgn | (uint8_t)nearbyintf(a * 512.0f);   /* subnormal grid m * 2^-9 */
+    int e;
+    float f = frexpf(a, &e);                    /* a = f * 2^e, f in [0.5, 1) */
+    float m = nearbyintf(f * 16.0f);            /* 4 significant bits: 8 .. 16 */
+    if (m == 16.0f) {
+        m = 8.0f;
+        e += 1;
+    }
+    int ex = e - 1 + 7;                         /* biased exponent of 1.mmm * 2^(e-1) */
+    return sgn | (uint8_t)((ex << 3) | ((int)m - 8));
+}
+
+float oracle_e4m3_to_f32(uint8_t b) {
+    int e = (b >> 3) & 15, m = b & 7;
+    float v = e == 0 ? ldexpf((float)m, -9) : ldexpf((float)(8 + m), e - 10);
+    if (e == 15 && m == 7) v = NAN;
+    return (b & 0x80) ? -v : v;
+}
+
+/* Leaf statistics with the fp8 state store, h3/htrc_flat_triton.py:65-72:
+ *   sg = max(max|g| * fp32(1/448), 1e-30), g code = e4m3(g / sg); sv, vb code likewise. */
+void oracle_stats_fp8(const float *mu, int64_t nt, const uint16_t *k, const uint16_t *v,
+                      int64_t nb, int leaf, int d, float scale,
+                      uint8_t *g8, float *sg, uint8_t *vb8, float *sv, float *lz) {
+    const float r448 = 1.0f / 448.0f;
+#pragma omp parallel
+    {
+        float *a = (float *)malloc(sizeof(float) * (size_t)leaf);
+        float *kf = (float *)malloc(sizeof(float) * (size_t)leaf * d);
+        float *gs = (float *)malloc(sizeof(float) * (size_t)d);
+        float *vs = (float *)malloc(sizeof(float) * (size_t)d);
+#pragma omp for schedule(static)
+        for (int64_t tl_ = 0; tl_ < nt * nb; ++tl_) {
+            int64_t t = tl_ / nb, l = tl_ % nb;
+            float mx, z;
+            leaf_state(mu + t * d, k + l * leaf * d, v + l * leaf * d, leaf, d, scale, a, kf, gs, vs, &mx, &z);
+            float ag = 0.0f, av = 0.0f;
+            for (int i = 0; i < d; ++i) {
+                if (fabsf(gs[i]) > ag) ag = fabsf(gs[i]);
+                if (fabsf(vs[i]) > av) av = fabsf(vs[i]);
+            }
+            float sgv = ag * r448, svv = av * r448;
+            if (sgv < 1e-30f) sgv = 1e-30f;
+            if (svv < 1e-30f) svv = 1e-30f;
+            for (int i = 0; i < d; ++i) {
+                g8[(t * nb + l) * d + i] = oracle_f32_to_e4m3(gs[i] / sgv);
+                vb8[(t * nb + l) * d + i] = oracle_f32_to_e4m3(vs[i] / svv);
+            }
+            sg[tl_] = sgv;
+            sv[tl_] = svv;
+            lz[tl_] = mx + logf(z);
         }
         free(a);
         free(kf);
@@ -409,6 +482,168 @@ void oracle_tile(int64_t nt, int tile, int d, int64_t nb, int leaf, int kx, int 
         free(vals);
         free(acc);
         free(dacc);
+    }
+}
+
+/* fp16 <-> fp32 (IEEE binary16, round to nearest even). */
+static float f16_to_f32(uint16_t h) {
+    int e = (h >> 10) & 31, m = h & 1023;
+    float v;
+    if (e == 0) v = ldexpf((float)m, -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = ldexpf((float)(1024 + m), e - 25);
+    return (h & 0x8000) ? -v : v;
+}
+
+uint16_t oracle_f32_to_f16(float x) {
+    uint16_t sgn = (uint16_t)(signbit(x) ? 0x8000 : 0);
+    float a = fabsf(x);
+    if (isnan(a)) return sgn | 0x7e00;
+    if (a >= 65520.0f) return sgn | 0x7c00;                     /* rounds to infinity */
+    if (a < 6.103515625e-05f) return sgn | (uint16_t)nearbyintf(a * 16777216.0f);   /* subnormal: m * 2^-24 */
+    int e;
+    float f = frexpf(a, &e);
+    float m = nearbyintf(f * 2048.0f);                          /* 11 significant bits */
+    if (m == 2048.0f) {
+        m = 1024.0f;
+        e += 1;
+    }
+    return sgn | (uint16_t)(((e - 1 + 15) << 10) | ((int)m - 1024));
+}
+
+/* fp8 state store select, h3/htrc_flat_triton.py:214-254 with FP8 = 1:
+ *   SEL[g,l] = max_r (sum_i dq_ri * g_li) * sg_gl + lz_gl, dq in fp16, g the e4m3 value
+ *   (every product exact in fp32; summed over the dims in order). */
+void oracle_select_fp8(const uint16_t *dq16, int tile, int stride, int group, int64_t nt,
+                       const uint8_t *g8, const float *sg, const float *lz, int64_t ng, int64_t nb, int d,
+                       float *sel) {
+    int ts = group * tile / stride;
+#pragma omp parallel for schedule(static)
+    for (int64_t tl_ = 0; tl_ < ng * nb; ++tl_) {
+        int64_t gi = tl_ / nb;
+        const uint8_t *g = g8 + tl_ * d;
+        float best = -INFINITY;
+        for (int rr = 0; rr < ts; ++rr) {
+            int64_t j = (int64_t)rr * stride;
+            int64_t t = gi * group + j / tile;
+            if (t > nt - 1) t = nt - 1;
+            int64_t p = t * tile + j % tile;
+            float acc = 0.0f;
+            for (int i = 0; i < d; ++i) acc += f16_to_f32(dq16[p * d + i]) * oracle_e4m3_to_f32(g[i]);
+            float x = acc * sg[tl_];
+            if (x > best) best = x;
+        }
+        sel[tl_] = best + lz[tl_];
+    }
+}
+
+/* Online update whose PV operand is fp16: P = fp16(p * pscale[c]), values e4m3 rows. */
+static void block_update_f16(const float *sc, const uint8_t *const *vals, const float *pscale, int nc, int d,
+                             float *m, float *l, float *acc, float *dacc) {
+    float bm = -INFINITY;
+    for (int c = 0; c < nc; ++c)
+        if (sc[c] > bm) bm = sc[c];
+    float m_new = *m > bm ? *m : bm;
+    float m_s = (m_new == -INFINITY) ? 0.0f : m_new;
+    float psum = 0.0f;
+    for (int i = 0; i < d; ++i) dacc[i] = 0.0f;
+    for (int c = 0; c < nc; ++c) {
+        float p = expf(sc[c] - m_s);
+        psum += p;
+        if (vals[c] == NULL) continue;
+        float ph = f16_to_f32(oracle_f32_to_f16(p * pscale[c]));
+        for (int i = 0; i < d; ++i) dacc[i] += ph * oracle_e4m3_to_f32(vals[c][i]);
+    }
+    float alpha = expf(*m - m_s);
+    *l = *l * alpha + psum;
+    for (int i = 0; i < d; ++i) acc[i] = acc[i] * alpha + dacc[i];
+    *m = m_new;
+}
+
+/* Split-K tile kernel with the fp8 state store, h3/htrc_flat_triton.py:95-211 (DOT=1, FP8=1):
+ *   far  score (sum dq16 . g) * sg + lz,  PV fp16(p * sv) . vb (e4m3)
+ *   near score (sum q(bf16) . k(bf16)) * scale, PV bf16(p) . v (bf16)
+ * Tile t uses the state and near set of its group t / group. */
+void oracle_tile_fp8(int64_t nt, int tile, int d, int64_t nb, int leaf, int kx, int group,
+                     const int32_t *idx, const int8_t *excl, const uint16_t *q16, const uint16_t *dq16,
+                     const uint8_t *g8, const float *sg, const float *lz, const uint8_t *vb8, const float *sv,
+                     const uint16_t *k, const uint16_t *v, float scale, int ns, int bn,
+                     float *pm, float *pl, float *pacc) {
+    int64_t lps = oracle_split(nb, ns, bn);
+    int64_t eps = oracle_split((int64_t)kx * leaf, ns, bn);
+#pragma omp parallel
+    {
+        float *sc = (float *)malloc(sizeof(float) * (size_t)bn);
+        float *ps = (float *)malloc(sizeof(float) * (size_t)bn);
+        const uint8_t **v8 = (const uint8_t **)malloc(sizeof(void *) * (size_t)bn);
+        const uint16_t **vals = (const uint16_t **)malloc(sizeof(void *) * (size_t)bn);
+        float *acc = (float *)malloc(sizeof(float) * (size_t)d);
+        float *dacc = (float *)malloc(sizeof(float) * (size_t)d);
+        float *qf = (float *)malloc(sizeof(float) * (size_t)d);
+        float *dqf = (float *)malloc(sizeof(float) * (size_t)d);
+#pragma omp for schedule(static)
+        for (int64_t job = 0; job < nt * ns * tile; ++job) {
+            int64_t t = job / ((int64_t)ns * tile);
+            int sp = (int)((job / tile) % ns);
+            int r = (int)(job % tile);
+            int64_t p = t * tile + r;
+            int64_t gs = t / group;
+            for (int i = 0; i < d; ++i) {
+                qf[i] = bf2f(q16[p * d + i]);
+                dqf[i] = f16_to_f32(dq16[p * d + i]);
+            }
+            float m = -INFINITY, l = 0.0f;
+            for (int i = 0; i < d; ++i) acc[i] = 0.0f;
+            int64_t lo = sp * lps, hi = lo + lps < nb ? lo + lps : nb;
+            for (int64_t n0 = lo; n0 < hi; n0 += bn) {
+                for (int c = 0; c < bn; ++c) {
+                    int64_t cc = n0 + c;
+                    if (cc < hi && excl[gs * nb + cc] == 0) {
+                        int64_t s_ = gs * nb + cc;
+                        float a = 0.0f;
+                        for (int i = 0; i < d; ++i) a += dqf[i] * oracle_e4m3_to_f32(g8[s_ * d + i]);
+                        sc[c] = a * sg[s_] + lz[s_];
+                        v8[c] = vb8 + s_ * d;
+                        ps[c] = sv[s_];
+                    } else {
+                        sc[c] = -INFINITY;
+                        v8[c] = NULL;
+                        ps[c] = 0.0f;
+                    }
+                }
+                block_update_f16(sc, v8, ps, bn, d, &m, &l, acc, dacc);
+            }
+            int64_t e_n = (int64_t)kx * leaf;
+            int64_t e_lo = sp * eps, e_hi = e_lo + eps < e_n ? e_lo + eps : e_n;
+            for (int64_t e0 = e_lo; e0 < e_hi; e0 += bn) {
+                for (int c = 0; c < bn; ++c) {
+                    int64_t j = e0 + c;
+                    if (j < e_hi) {
+                        int64_t tok = (int64_t)idx[gs * kx + j / leaf] * leaf + j % leaf;
+                        float a = 0.0f;
+                        for (int i = 0; i < d; ++i) a += qf[i] * bf2f(k[tok * d + i]);
+                        sc[c] = a * scale;
+                        vals[c] = v + tok * d;
+                    } else {
+                        sc[c] = -INFINITY;
+                        vals[c] = NULL;
+                    }
+                }
+                block_update(sc, vals, bn, d, &m, &l, acc, dacc);
+            }
+            int64_t base = (t * ns + sp) * tile + r;
+            pm[base] = m;
+            pl[base] = l;
+            memcpy(pacc + base * d, acc, sizeof(float) * (size_t)d);
+        }
+        free(sc);
+        free(ps);
+        free(v8);
+        free(vals);
+        free(acc);
+        free(dacc);
+        free(qf);
+        free(dqf);
     }
 }
 

@@ -66,7 +66,18 @@ def lib():
         L.oracle_linspace_round.restype = _i64
         L.oracle_linspace_round.argtypes = [_i64, _i64, _i64]
         L.oracle_kmeans_order.argtypes = [_F32, _i64, _int, _int, _int, _int, _I32]
-        if L.oracle_abi_version() != 3:
+        L.oracle_f32_to_e4m3.restype = ctypes.c_uint8
+        L.oracle_f32_to_e4m3.argtypes = [_flt]
+        L.oracle_e4m3_to_f32.restype = _flt
+        L.oracle_e4m3_to_f32.argtypes = [ctypes.c_uint8]
+        L.oracle_f32_to_f16.restype = ctypes.c_uint16
+        L.oracle_f32_to_f16.argtypes = [_flt]
+        _U8 = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+        L.oracle_stats_fp8.argtypes = [_F32, _i64, _U16, _U16, _i64, _int, _int, _flt, _U8, _F32, _U8, _F32, _F32]
+        L.oracle_select_fp8.argtypes = [_U16, _int, _int, _int, _i64, _U8, _F32, _F32, _i64, _i64, _int, _F32]
+        L.oracle_tile_fp8.argtypes = [_i64, _int, _int, _i64, _int, _int, _int, _I32, _I8, _U16, _U16,
+                                      _U8, _F32, _F32, _U8, _F32, _U16, _U16, _flt, _int, _int, _F32, _F32, _F32]
+        if L.oracle_abi_version() != 4:
             raise RuntimeError(f"{path} is stale (oracle ABI {L.oracle_abi_version()}): rebuild it")
         _lib = L
     return _lib
@@ -214,6 +225,83 @@ def merge(pm, pl, pacc):
     return out, logz
 
 
+def f32_to_e4m3(x) -> np.ndarray:
+    """e4m3fn codes of float32 values (round to nearest even, |x| saturated at 448)."""
+    f = lib().oracle_f32_to_e4m3
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], np.uint8).reshape(np.shape(x))
+
+
+def e4m3_to_f32(b) -> np.ndarray:
+    f = lib().oracle_e4m3_to_f32
+    return np.array([f(int(v)) for v in np.asarray(b, np.uint8).ravel()], np.float32).reshape(np.shape(b))
+
+
+def f32_to_f16(x) -> np.ndarray:
+    """fp16 bits of float32 values (round to nearest even)."""
+    f = lib().oracle_f32_to_f16
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], np.uint16).reshape(np.shape(x))
+
+
+def pack_q16(q: np.ndarray, tile: int, mu: np.ndarray, group: int = 1, dq_fp16: bool = True):
+    """16-bit operands of the bf16 / fp8 state stores (h3/htrc_flat_triton.py:104-108) over the
+    padded tile rows: q16 = bf16(q) bits, dq16 = fp16(q - mu) (or bf16) bits."""
+    q = _c(q, np.float32)
+    n, d = q.shape
+    nt = -(-n // tile)
+    p = np.arange(nt * tile)
+    rows = q[np.minimum(p, n - 1)]
+    dq = (rows - _c(mu, np.float32)[p // tile // group]).astype(np.float32)
+    q16 = bf16.from_f32(rows)
+    dq16 = dq.astype(np.float16).view(np.uint16) if dq_fp16 else bf16.from_f32(dq)
+    return q16, dq16
+
+
+def stats_fp8(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int, scale: float):
+    """Leaf statistics with the fp8 state store (h3/htrc_flat_triton.py:65-72)
+    -> g8 e4m3 [nt,nb,d], sg [nt,nb], vb8 e4m3 [nt,nb,d], sv [nt,nb], lz [nt,nb]."""
+    mu = _c(mu, np.float32)
+    k_bits, v_bits = _c(k_bits, np.uint16), _c(v_bits, np.uint16)
+    nt, d = mu.shape
+    nb = k_bits.shape[0] // leaf
+    g8 = np.empty((nt, nb, d), np.uint8)
+    vb8 = np.empty((nt, nb, d), np.uint8)
+    sg = np.empty((nt, nb), np.float32)
+    sv = np.empty((nt, nb), np.float32)
+    lz = np.empty((nt, nb), np.float32)
+    lib().oracle_stats_fp8(mu, nt, k_bits, v_bits, nb, leaf, d, float(scale), g8, sg, vb8, sv, lz)
+    return g8, sg, vb8, sv, lz
+
+
+def select_fp8(dq16, tile: int, g8, sg, lz, stride: int = 1, group: int = 1) -> np.ndarray:
+    """SEL [ng, nb] with the fp8 state store (h3/htrc_flat_triton.py:214-254, FP8 = 1)."""
+    g8 = _c(g8, np.uint8)
+    ng, nb, d = g8.shape
+    nt = dq16.shape[0] // tile
+    sel = np.empty((ng, nb), np.float32)
+    lib().oracle_select_fp8(_c(dq16, np.uint16), tile, stride, int(group), nt, g8, _c(sg, np.float32),
+                            _c(lz, np.float32), ng, nb, d, sel)
+    return sel
+
+
+def tile_partials_fp8(st: dict, *, tile: int, leaf: int, scale: float, splits: int, bn: int, group: int = 1):
+    """Split partials of the tile kernel with the fp8 state store (h3/htrc_flat_triton.py:88-211)."""
+    g8 = st["g8"]
+    ng, nb, d = g8.shape
+    nt = st["dq16"].shape[0] // tile
+    kx = st["idx"].shape[1]
+    idx = st["idx"] if kx else np.zeros((ng, 1), np.int32)
+    ns = max(1, int(splits))
+    pm = np.empty((nt, ns, tile), np.float32)
+    pl = np.empty((nt, ns, tile), np.float32)
+    pacc = np.empty((nt, ns, tile, d), np.float32)
+    lib().oracle_tile_fp8(nt, tile, d, nb, leaf, kx, int(group), _c(idx, np.int32), _c(st["excl"], np.int8),
+                          _c(st["q16"], np.uint16), _c(st["dq16"], np.uint16), _c(g8, np.uint8),
+                          _c(st["sg"], np.float32), _c(st["lz"], np.float32), _c(st["vb8"], np.uint8),
+                          _c(st["sv"], np.float32), _c(st["k"], np.uint16), _c(st["v"], np.uint16), float(scale),
+                          ns, int(bn), pm, pl, pacc)
+    return pm, pl, pacc
+
+
 def tail_merge(out, logz, q, tk, tv, scale: float):
     """Keys past the last full leaf, attended exactly by every query, merged into a finished
     (out [n,d], logz [n]).  Up to 16 tail keys: q, k, v and p rounded to bf16, fp32
@@ -241,11 +329,13 @@ def tail_merge(out, logz, q, tk, tv, scale: float):
 
 def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: int = 64,
             splits: int = 4, bn: int = 64, sel_stride: int = 1, sink_leaves: int = 0,
-            scale: float | None = None, keep: bool = True, group: int = 1, order: str = "seq") -> dict:
+            scale: float | None = None, keep: bool = True, group: int = 1, order: str = "seq",
+            store: str = "int8") -> dict:
     """The INT8 flat operator for one head: q float32 (or bf16 bits) [n,d], k/v bf16 bits
     [nk,d] with nk % leaf == 0.  Returns every intermediate plus out [n,d] and logz [n].
     order="kmeans": the tiles are cut from q[perm] (perm = kmeans_order(q)) and out / logz
-    are returned in query order (h3/htrc_flat.py:146-149, 159-165)."""
+    are returned in query order (h3/htrc_flat.py:146-149, 159-165).  store="fp8": the fp8
+    state store (e4m3 g / vb with row scales, fp16 far dots, bf16 near dots)."""
     q = np.asarray(q)
     qf = bf16.to_f32(q) if q.dtype == np.uint16 else _c(q, np.float32)
     n, d = qf.shape
@@ -264,16 +354,27 @@ def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: 
         raise ValueError("order must be seq or kmeans")
     st["k8"], st["ks"] = pack_k(k_bits)
     st["mu"] = tile_centres(qf, tile) if group == 1 else group_centres(qf, tile, group)
-    st["q8"], st["sq"], st["dq8"], st["sdq"] = pack_q(qf, tile, st["mu"], group)
-    st["g8"], st["sg"], st["vb"], st["lz"] = stats(st["mu"], k_bits, v_bits, leaf, scale)
+    if store == "fp8":
+        st["k"] = _c(k_bits, np.uint16)
+        st["q16"], st["dq16"] = pack_q16(qf, tile, st["mu"], group, dq_fp16=True)
+        st["g8"], st["sg"], st["vb8"], st["sv"], st["lz"] = stats_fp8(st["mu"], k_bits, v_bits, leaf, scale)
+    elif store == "int8":
+        st["q8"], st["sq"], st["dq8"], st["sdq"] = pack_q(qf, tile, st["mu"], group)
+        st["g8"], st["sg"], st["vb"], st["lz"] = stats(st["mu"], k_bits, v_bits, leaf, scale)
+    else:
+        raise ValueError("store must be int8 or fp8")
     if kx > 0:
-        st["sel"] = select(st["dq8"], st["sdq"], tile, st["g8"], st["sg"], st["lz"], sel_stride, group)
+        if store == "fp8":
+            st["sel"] = select_fp8(st["dq16"], tile, st["g8"], st["sg"], st["lz"], sel_stride, group)
+        else:
+            st["sel"] = select(st["dq8"], st["sdq"], tile, st["g8"], st["sg"], st["lz"], sel_stride, group)
         st["idx"], st["excl"] = topk(st["sel"], kx, sink)
     else:
         nt = st["mu"].shape[0]
         st["idx"] = np.zeros((nt, 0), np.int32)
         st["excl"] = np.zeros((nt, nb), np.int8)
-    pm, pl, pacc = tile_partials(st, tile=tile, leaf=leaf, scale=scale, splits=splits, bn=bn, group=group)
+    tp = tile_partials_fp8 if store == "fp8" else tile_partials
+    pm, pl, pacc = tp(st, tile=tile, leaf=leaf, scale=scale, splits=splits, bn=bn, group=group)
     out, logz = merge(pm, pl, pacc)
     st["out"], st["logz"] = out[:n], logz[:n]
     if order == "kmeans":

@@ -336,3 +336,88 @@ def test_kmeans_order_bitexact(device, n, clusters, sample, iters, qdtype):
     for h in range(2):
         want = flat_i8.kmeans_order(q[h].float().numpy(), clusters, sample, iters)
         assert np.array_equal(_np(perm[h]), want), f"head {h}"
+
+
+# ---- fp8 state store (store="fp8", h3/htrc_flat_triton.py:65-72, 104-108, 132-153, 214-254)
+
+@pytest.mark.parametrize("nq,group", [(4096, 1), (1000, 2)])
+@pytest.mark.parametrize("qdtype", ["bf16", "fp32"])
+def test_pack_q16_bitexact(device, nq, group, qdtype):
+    q, _, _ = _data(max(nq, 256), nk=256, seed=nq + 3)
+    q = q[:, :nq]
+    if qdtype == "fp32":
+        q = q.float() + 1e-3 * torch.randn(q.shape, generator=torch.Generator().manual_seed(8))
+    mu, q16, dq16 = hip.pack_q16(q.to(device).contiguous(), group=group)
+    torch.cuda.synchronize()
+    qf = q[0].float().numpy()
+    omu = flat_i8.tile_centres(qf, 64) if group == 1 else flat_i8.group_centres(qf, 64, group)
+    oq16, odq16 = flat_i8.pack_q16(qf, 64, omu, group, dq_fp16=True)
+    assert np.array_equal(_np(mu[0]).view(np.uint32), omu.view(np.uint32))
+    assert np.array_equal(_np(q16[0].view(torch.int16)).view(np.uint16), oq16)
+    assert np.array_equal(_np(dq16[0].view(torch.int16)).view(np.uint16), odq16)
+
+
+def _fp8_state(ref, k, v, device):
+    """The oracle's fp8 state (padded to the HIP layout) and packed operands on the device."""
+    ng, nb, d = ref["g8"].shape
+    nbp = nb_pad(nb)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    g = np.zeros((1, ng, nbp, d), np.uint8)
+    g[0, :, :nb] = ref["g8"]
+    vb = np.zeros((1, ng, nbp, d), np.uint8)
+    vb[0, :, :nb] = ref["vb8"]
+    sg = np.zeros((1, ng, nbp), np.float32)
+    sg[0, :, :nb] = ref["sg"]
+    sv = np.zeros((1, ng, nbp), np.float32)
+    sv[0, :, :nb] = ref["sv"]
+    lz = np.full((1, ng, nbp), -np.inf, np.float32)
+    lz[0, :, :nb] = ref["lz"]
+    excl = np.zeros((1, ng, nbp), np.int8)
+    excl[0, :, :nb] = ref["excl"]
+    packed = {"q16": T(ref["q16"][None]).view(torch.bfloat16), "dq16": T(ref["dq16"][None]).view(torch.float16),
+              "k": k.to(device), "v": v.to(device)}
+    state = {"g8": T(g).view(torch.float8_e4m3fn), "vb": T(vb).view(torch.float8_e4m3fn), "sg": T(sg), "sv": T(sv),
+             "lz": T(lz)}
+    return packed, state, T(excl), T(ref["idx"][None])
+
+
+@pytest.mark.parametrize("leaf", [64, 32])
+def test_stats_fp8_close_to_oracle(device, leaf):
+    n = 2048
+    q, k, v = _data(n, seed=leaf + 1)
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=4, store="fp8")
+    nb = n // leaf
+    mu = torch.from_numpy(ref["mu"])[None].to(device)
+    g, lz, vbs, sg, sv = hip.leaf_stats(mu, k.to(device), v.to(device), nb, 1 / math.sqrt(128), leaf=leaf,
+                                        store=torch.float8_e4m3fn)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(_np(sg[0])[:, :nb], ref["sg"], rtol=1e-5)
+    np.testing.assert_allclose(_np(sv[0])[:, :nb], ref["sv"], rtol=1e-5)
+    np.testing.assert_allclose(_np(lz[0])[:, :nb], ref["lz"], rtol=0, atol=2e-5 * (1 + np.abs(ref["lz"]).max()))
+    for got, want in ((g, ref["g8"]), (vbs, ref["vb8"])):
+        gv = _np(got[0].view(torch.uint8))[:, :nb]
+        a = flat_i8.e4m3_to_f32(gv).astype(np.float64)
+        b = flat_i8.e4m3_to_f32(want).astype(np.float64)
+        step = np.maximum(np.abs(b) * 2 ** -3, 2.0 ** -9)      # one e4m3 step
+        assert np.all(np.abs(a - b) <= step * 1.001)
+        assert (gv != want).mean() < 2e-2
+
+
+@pytest.mark.parametrize("group,stride", [(1, 1), (2, 4)])
+def test_select_and_tile_fp8_on_oracle_state(device, group, stride):
+    n, leaf, ex = 64 * 21 + 5, 64, 6
+    q, k, v = _data(n, nk=64 * 24, seed=group + 40)
+    scale = 1 / math.sqrt(128)
+    for splits in (1, 4):
+        ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=ex, splits=splits,
+                              bn=64, sel_stride=stride, group=group, store="fp8")
+        packed, state, excl, idx = _fp8_state(ref, k, v, device)
+        nb = ref["g8"].shape[1]
+        sel = hip.rowmax_select(g=state["g8"], lz=state["lz"], sg=state["sg"], stride=stride, nb=nb,
+                                dq8=packed["dq16"], group=group)
+        out, logz = hip.tile_attention(packed, state, excl, idx, nq=n, leaf=leaf, scale=scale, splits=splits, bn=64,
+                                       group=group)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(_np(sel[0])[:, :nb], ref["sel"], rtol=2e-5, atol=2e-5)
+        assert rel_l2(_np(out[0]), ref["out"]) <= OUT_REL_L2
+        assert np.abs(_np(logz[0]) - ref["logz"]).max() <= LOGZ_ABS
