@@ -343,9 +343,11 @@ __device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
     return u;
 }
 
-// FP8: the reference's fp8 state store (h3/htrc_flat_triton.py:65-72): g and vb as e4m3 codes of
-// x / s with row scales s = max(max|x| * fp32(1/448), 1e-30) (sg, sv); vb then holds bytes.
-template <int LEAF, bool FP8 = false>
+// STORE 0: g int8 with row scale sg, vb bf16 (the production I8 store, :73-80);
+// STORE 1: g and vb bf16, no scales (store="bf16", :82-83);
+// STORE 2: g and vb as e4m3 codes of x / s with row scales s = max(max|x| * fp32(1/448), 1e-30)
+// (sg, sv; store="fp8", :65-72); vb then holds bytes.
+template <int LEAF, int STORE = 0>
 __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__ mu, int nt,
                                                        const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v, int64_t nk, int nb,
@@ -357,6 +359,7 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
     constexpr int KK = (LEAF + 31) / 32;          // 32-key MFMA k-steps per leaf
     constexpr int LEAF_BYTES = 32 * LEAF * 16;
     constexpr int LPB = 16;                       // leaves per workgroup (the launcher's lpb)
+    constexpr bool FP8 = STORE == 2, BF16 = STORE == 1;
     __shared__ __align__(16) char lds[2 * LEAF_BYTES];
     __shared__ __align__(16) float s_sg[64][LPB], s_lz[64][LPB];   // per tile, the workgroup's leaves
     __shared__ __align__(16) float s_sv[FP8 ? 64 : 1][LPB];
@@ -389,7 +392,8 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
     const int lr = min(nb, l1);                   // real leaves of this workgroup: [l0, lr)
     const int64_t kh = (int64_t)h * nk;
     // g8 / vb of the previous leaf, stored during the next one
-    uint32_t pg[8];
+    uint32_t pg[8];              // g codes (int8 / e4m3)
+    u32x2 pgb[BF16 ? 8 : 1];     // g bf16 pairs (STORE 1)
     u32x2 pv[8];                 // vb bf16 pairs (FP8: pv[db].x holds the four e4m3 codes)
     int pl = -1;
     // The MFMA C layout leaves lane (col, grp) with dims 16db + 4grp.. of centre col.  Lanes
@@ -409,11 +413,36 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
             *(u32x4*)(dst + s * D + 64 + 16 * grp) = u32x4{x[1], x[3], x[5], x[7]};
         }
     };
-    auto store_g = [&]() {
-        if (pl >= 0) store_bytes(pg, (uint8_t*)g8);
-    };
-    // vb half hf (dims 64hf..): rows 2j and 2j + 1 swap halves; row g then holds, for
+    // bf16 rows, half hf (dims 64hf..): rows 2j and 2j + 1 swap halves; row g then holds, for
     // db = 2m + (g & 1), the dims 16db + 8(g >> 1) .. + 3 in va and .. + 4 .. + 7 in vc
+    auto store_rows16 = [&](const u32x2 (&c)[8], uint16_t* dst, int hf) {
+        u32x2 va[2], vc[2];
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+            const int m = 2 * hf + mm;
+            uint32_t a0 = c[2 * m].x, a1 = c[2 * m].y, c0 = c[2 * m + 1].x, c1 = c[2 * m + 1].y;
+            swap16(a0, c0);
+            swap16(a1, c1);
+            va[mm] = u32x2{a0, a1};
+            vc[mm] = u32x2{c0, c1};
+        }
+        if (tval) {
+            const int64_t s = th * nb_pad + pl;
+            uint16_t* vr = dst + s * D + 16 * (grp & 1) + 8 * (grp >> 1);
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm)
+                *(u32x4*)(vr + 32 * (2 * hf + mm)) = u32x4{va[mm].x, va[mm].y, vc[mm].x, vc[mm].y};
+        }
+    };
+    auto store_g = [&]() {
+        if (pl < 0) return;
+        if constexpr (BF16) {
+            store_rows16(pgb, (uint16_t*)g8, 0);
+            store_rows16(pgb, (uint16_t*)g8, 1);
+        } else {
+            store_bytes(pg, (uint8_t*)g8);
+        }
+    };
     auto store_v = [&](int hf) {
         if constexpr (FP8) {
             if (pl >= 0 && hf == 0) {
@@ -423,23 +452,7 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
                 store_bytes(c, (uint8_t*)vb);
             }
         } else if (pl >= 0) {
-            u32x2 va[2], vc[2];
-#pragma unroll
-            for (int mm = 0; mm < 2; ++mm) {
-                const int m = 2 * hf + mm;
-                uint32_t a0 = pv[2 * m].x, a1 = pv[2 * m].y, c0 = pv[2 * m + 1].x, c1 = pv[2 * m + 1].y;
-                swap16(a0, c0);
-                swap16(a1, c1);
-                va[mm] = u32x2{a0, a1};
-                vc[mm] = u32x2{c0, c1};
-            }
-            if (tval) {
-                const int64_t s = th * nb_pad + pl;
-                uint16_t* vr = vb + s * D + 16 * (grp & 1) + 8 * (grp >> 1);
-#pragma unroll
-                for (int mm = 0; mm < 2; ++mm)
-                    *(u32x4*)(vr + 32 * (2 * hf + mm)) = u32x4{va[mm].x, va[mm].y, vc[mm].x, vc[mm].y};
-            }
+            store_rows16(pv, vb, hf);
         }
     };
     if (l0 < lr) stage_leaf<LEAF>(k, v, kh + (int64_t)l0 * LEAF, lds0, voff);
@@ -524,7 +537,16 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
 #pragma unroll
             for (int i = 0; i < 4; ++i) am = fmaxf(am, fabsf(gacc[db][i]));
         am = __fmul_rn(grp_max(am), scale);             // max |g|
-        if constexpr (FP8) {
+        if constexpr (BF16) {
+            // g = gacc * scale and vb rounded to bf16, no scales
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                pgb[db] = u32x2{pack2bf(__fmul_rn(gacc[db][0], scale), __fmul_rn(gacc[db][1], scale)),
+                                pack2bf(__fmul_rn(gacc[db][2], scale), __fmul_rn(gacc[db][3], scale))};
+                pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
+            }
+            if (grp == 0) s_lz[w * 16 + col][l - l0] = __fadd_rn(mx, __logf(z));
+        } else if constexpr (FP8) {
             // sg = max(max|g| / 448, 1e-30), code = e4m3(g / sg) with g / sg taken as
             // gacc * (scale / sg); vb the same with sv
             const float sgv = fmaxf(__fmul_rn(am, R448), 1e-30f);
@@ -569,7 +591,10 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
             const int64_t s = th * nb_pad + l;
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
-                *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = 0u;
+                if (BF16)
+                    *(u32x2*)((uint16_t*)g8 + s * D + 16 * db + 4 * grp) = u32x2{0u, 0u};
+                else
+                    *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = 0u;
                 if (FP8)
                     *(uint32_t*)((uint8_t*)vb + s * D + 16 * db + 4 * grp) = 0u;
                 else
@@ -588,7 +613,7 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
         const int tq = tg * 64 + tt;
         if (tq < nt && 4 * qq < l1 - l0) {
             const int64_t s = ((int64_t)h * nt + tq) * nb_pad + l0 + 4 * qq;
-            *(f32x4*)(sg + s) = *(const f32x4*)&s_sg[tt][4 * qq];
+            if (!BF16) *(f32x4*)(sg + s) = *(const f32x4*)&s_sg[tt][4 * qq];
             *(f32x4*)(lz + s) = *(const f32x4*)&s_lz[tt][4 * qq];
             if (FP8) *(f32x4*)(sv + s) = *(const f32x4*)&s_sv[tt][4 * qq];
         }
@@ -1018,17 +1043,30 @@ __global__ __launch_bounds__(256) void tile_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------
-// fp8 state store (store="fp8", h3/htrc_flat_triton.py:65-72, 132-153, 214-254 with FP8 = 1).
-//   select: SEL[g, l] = max_r (dq_r(fp16) . g_l(e4m3 -> fp16)) * sg_l + lz_l;
-//   tile, far: score = (dq(fp16) . g) * sg + lz, O += (p * sv)(fp16) . vb(e4m3 -> fp16);
-//   tile, near: score = (q(bf16) . k(bf16)) * scale, O += p(bf16) . v(bf16).
+// 16-bit state stores, in the reference's stage structure:
+//   fp8 (store="fp8", h3/htrc_flat_triton.py:65-72, 132-153, 214-254 with FP8 = 1):
+//     select: SEL[g, l] = max_r (dq_r(fp16) . g_l(e4m3 -> fp16)) * sg_l + lz_l;
+//     tile, far: score = (dq(fp16) . g) * sg + lz, O += (p * sv)(fp16) . vb(e4m3 -> fp16);
+//   bf16 (store="bf16", DOT = 1 without FP8 / I8):
+//     select: SEL = max_r dq_r(bf16) . g_l(bf16) + lz_l; far: score = dq . g + lz, O += p(bf16) . vb;
+//   both, near: score = (q(bf16) . k(bf16)) * scale, O += p(bf16) . v(bf16).
 // The e4m3 codes are widened to fp16 holding value * 2^-8 (e4m3x8_to_h8), exactly; sg and sv
 // are taken times 256 (exact), so every product is the reference's.
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void select_fp8_kernel(const uint16_t* __restrict__ dq16, int stride,
-                                                         const uint8_t* __restrict__ g, const float* __restrict__ sg,
-                                                         const float* __restrict__ lz, int nt, int group, int ng,
-                                                         int nb, int nb_pad, float* __restrict__ sel) {
+// QK A operand of state rows: 16 leaves x dims 32 ks + 8 grp .. + 7 of row `row`.
+template <bool FP8>
+__device__ __forceinline__ f32x4 state_qk(const void* g, int64_t row, int ks, int grp, const u32x4& b, f32x4 acc) {
+    if constexpr (FP8)
+        return mfma_f16(e4m3x8_to_h8(*(const u32x2*)((const uint8_t*)g + row * D + 32 * ks + 8 * grp)), b, acc);
+    else
+        return mfma_bf16(as_bf16x8(*(const u32x4*)((const uint16_t*)g + row * D + 32 * ks + 8 * grp)), as_bf16x8(b), acc);
+}
+
+template <bool FP8>
+__global__ __launch_bounds__(256) void select16_kernel(const uint16_t* __restrict__ dq16, int stride,
+                                                       const void* __restrict__ g, const float* __restrict__ sg,
+                                                       const float* __restrict__ lz, int nt, int group, int ng,
+                                                       int nb, int nb_pad, float* __restrict__ sel) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int gi = blockIdx.x, h = blockIdx.z;
     const int64_t gs = (int64_t)h * ng + gi;
@@ -1062,19 +1100,17 @@ __global__ __launch_bounds__(256) void select_fp8_kernel(const uint16_t* __restr
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const u32x4 A = e4m3x8_to_h8(*(const u32x2*)(g + (s0 + col) * D + 32 * ks + 8 * grp));
+                for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-                    for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma_f16(A, b[rb][ks], acc[rb]);
-                }
-                const f32x4 sgv = *(const f32x4*)(sg + s0 + 4 * grp);
+                    for (int rb = 0; rb < 4; ++rb) acc[rb] = state_qk<FP8>(g, s0 + col, ks, grp, b[rb][ks], acc[rb]);
+                const f32x4 sgv = FP8 ? *(const f32x4*)(sg + s0 + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     float best = -INFINITY;
                     const float sc = __fmul_rn(sgv[i], 256.0f);
 #pragma unroll
                     for (int rb = 0; rb < 4; ++rb)
-                        if (val[rb]) best = fmaxf(best, __fmul_rn(acc[rb][i], sc));
+                        if (val[rb]) best = fmaxf(best, FP8 ? __fmul_rn(acc[rb][i], sc) : acc[rb][i]);
                     bsel[lb][i] = fmaxf(bsel[lb][i], col_max(best));
                 }
             }
@@ -1130,10 +1166,10 @@ __device__ __forceinline__ void online_block_f16(RowState& st, float (&sc)[8], c
     st.m = m_new;
 }
 
-template <int LEAF>
-__global__ __launch_bounds__(256) void tile_fp8_kernel(
-    const uint16_t* __restrict__ q16, const uint16_t* __restrict__ dq16, const uint8_t* __restrict__ g,
-    const float* __restrict__ sg, const float* __restrict__ lz, const uint8_t* __restrict__ vb,
+template <int LEAF, bool FP8>
+__global__ __launch_bounds__(256) void tile16_kernel(
+    const uint16_t* __restrict__ q16, const uint16_t* __restrict__ dq16, const void* __restrict__ g,
+    const float* __restrict__ sg, const float* __restrict__ lz, const void* __restrict__ vb,
     const float* __restrict__ sv, const int8_t* __restrict__ excl, const int32_t* __restrict__ idx,
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t nq, int nt, int group, int ng,
     const int32_t* __restrict__ perm, int64_t nk, int nb, int nb_pad, int kx, int lps, int eps, float scale,
@@ -1169,31 +1205,37 @@ __global__ __launch_bounds__(256) void tile_fp8_kernel(
             const int64_t s0 = gs * nb_pad + cb;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                acc = mfma_f16(e4m3x8_to_h8(*(const u32x2*)(g + (s0 + col) * D + 32 * ks + 8 * grp)), dqh[ks], acc);
-            const f32x4 sgv = *(const f32x4*)(sg + s0 + 4 * grp);
-            const f32x4 svv = *(const f32x4*)(sv + s0 + 4 * grp);
+            for (int ks = 0; ks < 4; ++ks) acc = state_qk<FP8>(g, s0 + col, ks, grp, dqh[ks], acc);
+            const f32x4 sgv = FP8 ? *(const f32x4*)(sg + s0 + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
+            const f32x4 svv = FP8 ? *(const f32x4*)(sv + s0 + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
             const f32x4 lzv = *(const f32x4*)(lz + s0 + 4 * grp);
             const uint32_t exv = *(const uint32_t*)(excl_row + cb + 4 * grp);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int c = cb + 4 * grp + i;
                 const bool ok = c < hi && ((exv >> (8 * i)) & 0xffu) == 0u;
-                sc[4 * h2 + i] = ok ? __fadd_rn(__fmul_rn(acc[i], __fmul_rn(sgv[i], 256.0f)), lzv[i]) : -INFINITY;
+                const float dot = FP8 ? __fmul_rn(acc[i], __fmul_rn(sgv[i], 256.0f)) : acc[i];
+                sc[4 * h2 + i] = ok ? __fadd_rn(dot, lzv[i]) : -INFINITY;
                 pscale[4 * h2 + i] = __fmul_rn(svv[i], 256.0f);
             }
         }
-        const uint8_t* vb0 = vb + (gs * nb_pad + c0) * D;
-        online_block_f16(st, sc, pscale, [&](int db) {   // vb^T: keys 4grp + j and 16 + 4grp + j at one dim
-            const int dim = 16 * db + col;
-            uint32_t u[2];
+        if constexpr (FP8) {
+            const uint8_t* vb0 = (const uint8_t*)vb + (gs * nb_pad + c0) * D;
+            online_block_f16(st, sc, pscale, [&](int db) {   // vb^T: keys 4grp + j and 16 + 4grp + j at one dim
+                const int dim = 16 * db + col;
+                uint32_t u[2];
 #pragma unroll
-            for (int jh = 0; jh < 2; ++jh) {
-                const uint8_t* b = vb0 + (16 * jh + 4 * grp) * D + dim;
-                u[jh] = (uint32_t)b[0] | ((uint32_t)b[D] << 8) | ((uint32_t)b[2 * D] << 16) | ((uint32_t)b[3 * D] << 24);
-            }
-            return e4m3x8_to_h8(u32x2{u[0], u[1]});
-        });
+                for (int jh = 0; jh < 2; ++jh) {
+                    const uint8_t* b = vb0 + (16 * jh + 4 * grp) * D + dim;
+                    u[jh] = (uint32_t)b[0] | ((uint32_t)b[D] << 8) | ((uint32_t)b[2 * D] << 16) |
+                            ((uint32_t)b[3 * D] << 24);
+                }
+                return e4m3x8_to_h8(u32x2{u[0], u[1]});
+            });
+        } else {
+            const uint16_t* vb0 = (const uint16_t*)vb + (gs * nb_pad + c0) * D;
+            online_block(st, sc, [&](int db) { return gather_pv(vb0, 0, 16, 16 * db + col, grp); });
+        }
     }
     // ---- near field: token j of the tile's selected list -> idx[j / LEAF] * LEAF + j % LEAF
     const int32_t* idx_row = idx + gs * (kx > 0 ? kx : 1);
@@ -2182,7 +2224,7 @@ int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, i
     hipStream_t s = (hipStream_t)stream;
 #define STATS8_CASE(L)                                                                                         \
     case L:                                                                                                    \
-        hipLaunchKernelGGL((stats_kernel<L, true>), grid, dim3(256), 0, s, mu, (int)nt, k, v, nk, (int)nb, nbp, lpb, \
+        hipLaunchKernelGGL((stats_kernel<L, 2>), grid, dim3(256), 0, s, mu, (int)nt, k, v, nk, (int)nb, nbp, lpb,    \
                            scale, (int8_t*)g, sg, (uint16_t*)vb, sv, lz);                                      \
         break;
     switch (leaf) {
@@ -2193,6 +2235,37 @@ int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, i
     }
 #undef STATS8_CASE
     return launched("htrc_leaf_stats_fp8");
+}
+
+int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
+                         int leaf, int d, float scale, uint16_t* g, uint16_t* vb, float* lz, void* stream) {
+    REQUIRE(mu && k && v && g && vb && lz, "htrc_leaf_stats_bf16: null pointer");
+    REQUIRE(d == D, "htrc_leaf_stats_bf16: head dim must be 128");
+    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_leaf_stats_bf16: leaf must be 16/32/64/128");
+    REQUIRE(nk > 0 && nk % leaf == 0, "htrc_leaf_stats_bf16: key count must be a multiple of the leaf size");
+    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff, "htrc_leaf_stats_bf16: bad heads / tiles");
+    REQUIRE(aligned(k, 16) && aligned(v, 16) && aligned(g, 16) && aligned(vb, 16) && aligned(lz, 16),
+            "htrc_leaf_stats_bf16: misaligned buffer");
+    const int64_t nb = nk / leaf;
+    const int nbp = htrc_nb_pad(nb);
+    const int lpb = 16;
+    const int64_t nblocks = (nt + 63) / 64 * ((nbp + lpb - 1) / lpb) * heads;
+    REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats_bf16: too many tiles x leaves x heads for one launch");
+    dim3 grid((unsigned)nblocks);
+    hipStream_t s = (hipStream_t)stream;
+#define STATSB_CASE(L)                                                                                         \
+    case L:                                                                                                    \
+        hipLaunchKernelGGL((stats_kernel<L, 1>), grid, dim3(256), 0, s, mu, (int)nt, k, v, nk, (int)nb, nbp, lpb,    \
+                           scale, (int8_t*)g, nullptr, vb, nullptr, lz);                                       \
+        break;
+    switch (leaf) {
+        STATSB_CASE(16)
+        STATSB_CASE(32)
+        STATSB_CASE(64)
+        STATSB_CASE(128)
+    }
+#undef STATSB_CASE
+    return launched("htrc_leaf_stats_bf16");
 }
 
 int htrc_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
@@ -2309,9 +2382,25 @@ int htrc_select_fp8(const uint16_t* dq16, const uint8_t* g, const float* sg, con
     const int nbp = htrc_nb_pad(nb);
     const int64_t ng = (nt + group - 1) / group;
     dim3 grid((unsigned)ng, (unsigned)((nb + 255) / 256), (unsigned)heads);
-    hipLaunchKernelGGL(select_fp8_kernel, grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, sg, lz, (int)nt,
+    hipLaunchKernelGGL(select16_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, sg, lz, (int)nt,
                        group, (int)ng, (int)nb, nbp, sel);
     return launched("htrc_select_fp8");
+}
+
+int htrc_select_bf16(const uint16_t* dq16, const uint16_t* g, const float* lz, int64_t heads, int64_t nt, int64_t nb,
+                     int stride, int group, int d, float* sel, void* stream) {
+    REQUIRE(dq16 && g && lz && sel, "htrc_select_bf16: null pointer");
+    REQUIRE(d == D, "htrc_select_bf16: head dim must be 128");
+    REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_select_bf16: stride must divide 64");
+    REQUIRE(group >= 1 && group <= 1024, "htrc_select_bf16: group must be in [1, 1024]");
+    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff && nb > 0, "htrc_select_bf16: bad sizes");
+    REQUIRE(aligned(dq16, 16) && aligned(g, 16) && aligned(lz, 16), "htrc_select_bf16: misaligned buffer");
+    const int nbp = htrc_nb_pad(nb);
+    const int64_t ng = (nt + group - 1) / group;
+    dim3 grid((unsigned)ng, (unsigned)((nb + 255) / 256), (unsigned)heads);
+    hipLaunchKernelGGL(select16_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, nullptr, lz,
+                       (int)nt, group, (int)ng, (int)nb, nbp, sel);
+    return launched("htrc_select_bf16");
 }
 
 int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz,
@@ -2340,7 +2429,7 @@ int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, c
     float* ppa = splits == 1 ? nullptr : pacc;
 #define TILE8_CASE(L)                                                                                              \
     case L:                                                                                                        \
-        hipLaunchKernelGGL(tile_fp8_kernel<L>, grid, dim3(256), 0, s, q16, dq16, g, sg, lz, vb, sv, excl, idx, k, v, nq, \
+        hipLaunchKernelGGL((tile16_kernel<L, true>), grid, dim3(256), 0, s, q16, dq16, g, sg, lz, vb, sv, excl, idx, k, v, nq, \
                            (int)nt, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps, scale, ppm, ppl,   \
                            ppa, out, logz);                                                                        \
         break;
@@ -2352,6 +2441,44 @@ int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, c
     }
 #undef TILE8_CASE
     return launched("htrc_tile_fp8");
+}
+
+int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g, const float* lz, const uint16_t* vb,
+                   const int8_t* excl, const int32_t* idx, const uint16_t* k, const uint16_t* v, int64_t heads,
+                   int64_t nq, int64_t nk, int leaf, int d, int kx, int group, const int32_t* perm, int splits, int bn,
+                   float scale, float* pm, float* pl, float* pacc, float* out, float* logz, void* stream) {
+    REQUIRE(q16 && dq16 && g && lz && vb && excl && k && v, "htrc_tile_bf16: null input pointer");
+    REQUIRE(d == D, "htrc_tile_bf16: head dim must be 128");
+    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_tile_bf16: leaf must be 16/32/64/128");
+    REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_tile_bf16: bad sizes");
+    const int64_t nb = nk / leaf, nt = (nq + TILE - 1) / TILE;
+    REQUIRE(kx >= 0 && kx <= nb && (kx == 0 || idx), "htrc_tile_bf16: need 0 <= kx <= leaves and idx when kx > 0");
+    REQUIRE(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0, "htrc_tile_bf16: need 1 <= splits <= 64 and a block that is a multiple of 32");
+    REQUIRE(splits == 1 ? (out && logz) : (pm && pl && pacc), "htrc_tile_bf16: missing outputs");
+    REQUIRE(group >= 1 && group <= 1024, "htrc_tile_bf16: group must be in [1, 1024]");
+    REQUIRE(aligned(q16, 16) && aligned(dq16, 16) && aligned(g, 16) && aligned(k, 16) && aligned(lz, 16),
+            "htrc_tile_bf16: misaligned buffer");
+    const int64_t ng = (nt + group - 1) / group;
+    const int lps = (int)split_len(nb, splits, bn), eps = (int)split_len((int64_t)kx * leaf, splits, bn);
+    dim3 grid((unsigned)nt, (unsigned)splits, (unsigned)heads);
+    hipStream_t s = (hipStream_t)stream;
+    float* ppm = splits == 1 ? nullptr : pm;
+    float* ppl = splits == 1 ? nullptr : pl;
+    float* ppa = splits == 1 ? nullptr : pacc;
+#define TILEB_CASE(L)                                                                                              \
+    case L:                                                                                                        \
+        hipLaunchKernelGGL((tile16_kernel<L, false>), grid, dim3(256), 0, s, q16, dq16, g, nullptr, lz, vb, nullptr, excl, \
+                           idx, k, v, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps,  \
+                           scale, ppm, ppl, ppa, out, logz);                                                       \
+        break;
+    switch (leaf) {
+        TILEB_CASE(16)
+        TILEB_CASE(32)
+        TILEB_CASE(64)
+        TILEB_CASE(128)
+    }
+#undef TILEB_CASE
+    return launched("htrc_tile_bf16");
 }
 
 int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int splits,

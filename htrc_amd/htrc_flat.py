@@ -59,9 +59,9 @@ def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot
                          "HIP kernels (backend='hip', alias 'triton')")
     if curvature != "lin":
         raise ValueError("the HIP backend needs curvature='lin'")
-    if store not in ("int8", "fp8") or dot != "bf16":
-        raise ValueError("the HIP backend implements dot='bf16' with store='int8' (int8 Q/K dots, bf16 PV) "
-                         "or store='fp8' (e4m3 leaf state)")
+    if store not in ("int8", "fp8", "bf16") or dot != "bf16":
+        raise ValueError("the HIP backend implements dot='bf16' with store='int8' (int8 Q/K dots, bf16 PV), "
+                         "store='fp8' (e4m3 leaf state) or store='bf16'")
     if select != "max":
         raise ValueError("the HIP backend implements select='max'")
     if order not in ("seq", "kmeans"):
@@ -129,9 +129,9 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     if qh.dtype not in (torch.float32, torch.bfloat16):
         qh = qh.float()
     perm = hip.kmeans_order(qh, ws=ws) if order == "kmeans" else None   # query rows regrouped by k-means
-    if store == "fp8":
-        return _flat_fp8(qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, stride, group, perm, splits, kern,
-                         tail, ws, return_logz, state)
+    if store in ("fp8", "bf16"):
+        return _flat16(store, qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, stride, group, perm, splits,
+                       kern, tail, ws, return_logz, state)
     mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), ws=ws, group=group, perm=perm)
     kb = kh.to(torch.bfloat16).contiguous()
     vb = vh.to(torch.bfloat16).contiguous()
@@ -181,17 +181,20 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     return (res, lzr) if return_logz else res
 
 
-def _flat_fp8(qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, stride, group, perm, splits, kern, tail, ws,
-              return_logz, state):
-    """store="fp8": e4m3 leaf state with row scales, fp16 far dots, bf16 near dots, run as the
-    reference's stage structure (select, top-k, split tile kernel, merge;
-    h3/htrc_flat_triton.py:65-72, 104-108, 132-153, 165-184, 214-254 with FP8 = 1)."""
+def _flat16(store, qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, stride, group, perm, splits, kern, tail,
+            ws, return_logz, state):
+    """store="fp8": e4m3 leaf state with row scales, fp16 far dots; store="bf16": bf16 leaf
+    state and far dots; both with bf16 near dots, run as the reference's stage structure
+    (select, top-k, split tile kernel, merge; h3/htrc_flat_triton.py:65-72, 82-83, 104-108,
+    132-153, 165-184, 214-254)."""
     h = int(qh.shape[0])
-    mu, q16, dq16 = hip.pack_q16(qh.contiguous(), ws=ws, group=group, perm=perm, dq_fp16=True)
+    fp8 = store == "fp8"
+    mu, q16, dq16 = hip.pack_q16(qh.contiguous(), ws=ws, group=group, perm=perm, dq_fp16=fp8)
     kb = kh.to(torch.bfloat16).contiguous()
     vb = vh.to(torch.bfloat16).contiguous()
     tick("prep")
-    g, lz, vbs, sg, sv = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=torch.float8_e4m3fn, ws=ws)
+    g, lz, vbs, sg, sv = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf,
+                                        store=torch.float8_e4m3fn if fp8 else torch.bfloat16, ws=ws)
     tick("stats")
     ng = int(mu.shape[1])
     idx = None

@@ -133,9 +133,10 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
     """Leaf statistics at the tile centres (h3/htrc_flat_triton.py:329-345).
     mu [H,nt,D] fp32, kf/vf bf16 [H,nk,D] -> (g, lz, vb, sg, sv) in the reference's order:
     store=int8: g int8 [H,nt,nbp,D], vb bf16, sv None; store=float8_e4m3fn: g and vb e4m3
-    with the row scales sg, sv (h3/htrc_flat_triton.py:65-72)."""
-    if store not in (torch.int8, torch.float8_e4m3fn):
-        raise ValueError("the HIP leaf statistics store g as int8 or float8_e4m3fn")
+    with the row scales sg, sv (h3/htrc_flat_triton.py:65-72); store=bfloat16: g and vb bf16,
+    sg and sv None."""
+    if store not in (torch.int8, torch.float8_e4m3fn, torch.bfloat16):
+        raise ValueError("the HIP leaf statistics store g as int8, float8_e4m3fn or bfloat16")
     mu = _heads(mu).contiguous()
     kf = _heads(kf).contiguous()
     vf = _heads(vf).contiguous()
@@ -148,6 +149,13 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
         raise ValueError("keys and values must be [H, nb * leaf, D]")
     nbp = nb_pad(nb)
     dev = mu.device
+    if store == torch.bfloat16:
+        g = _buf(ws, "g_bf16", (h, nt, nbp, d), torch.bfloat16, dev)
+        vb = _buf(ws, "vb", (h, nt, nbp, d), torch.bfloat16, dev)
+        lz = _buf(ws, "lz", (h, nt, nbp), torch.float32, dev)
+        call("htrc_leaf_stats_bf16", ptr(mu), ptr(kf), ptr(vf), h, nt, nk, int(leaf), d, float(scale), ptr(g), ptr(vb),
+             ptr(lz), stream_handle(dev))
+        return g, lz, vb, None, None
     if store == torch.float8_e4m3fn:
         g = _buf(ws, "g_fp8", (h, nt, nbp, d), torch.float8_e4m3fn, dev)
         vb = _buf(ws, "vb_fp8", (h, nt, nbp, d), torch.float8_e4m3fn, dev)
@@ -171,8 +179,8 @@ def rowmax_select(q_c=None, mu_c=None, g=None, lz=None, prec="ieee", bn=32, warp
     """SEL [H,ng,nbp] (h3/htrc_flat_triton.py:315-326), the max over the rows of each group of
     ``group`` tiles.  Takes the packed rows dq8/sdq (pack_q); when absent they are packed from
     q_c (fp32 [H,nq,D] rows)."""
-    if g.dtype == torch.float8_e4m3fn:
-        return _select_fp8(g, lz, sg, stride, nb, dq8, group, ws, q_c)
+    if g.dtype in (torch.float8_e4m3fn, torch.bfloat16):
+        return _select16(g, lz, sg, stride, nb, dq8, group, ws, q_c)
     if dq8 is None or sdq is None:
         _, _, _, dq8, sdq = pack_q(q_c, group=group)
     g = _heads(g) if g.dim() == 3 else g
@@ -188,17 +196,23 @@ def rowmax_select(q_c=None, mu_c=None, g=None, lz=None, prec="ieee", bn=32, warp
     return sel
 
 
-def _select_fp8(g, lz, sg, stride, nb, dq16, group, ws, q_c):
-    """SEL over the fp8 state: dq16 are the fp16 rows of pack_q16 (passed as ``dq8``)."""
+def _select16(g, lz, sg, stride, nb, dq16, group, ws, q_c):
+    """SEL over a 16-bit state: dq16 are the rows of pack_q16 (passed as ``dq8``): fp16 for the
+    fp8 state, bf16 for the bf16 state."""
+    fp8 = g.dtype == torch.float8_e4m3fn
     if dq16 is None:
-        _, _, dq16 = pack_q16(q_c, group=group)
-    _need(dq16, torch.float16, "dq16")
+        _, _, dq16 = pack_q16(q_c, group=group, dq_fp16=fp8)
+    _need(dq16, torch.float16 if fp8 else torch.bfloat16, "dq16")
     h, ng, nbp, d = (int(x) for x in g.shape)
     nt = int(_heads(dq16).shape[1]) // TILE
     nb = nbp if nb is None else int(nb)
     sel = _buf(ws, "sel", (h, ng, nbp), torch.float32, g.device)
-    call("htrc_select_fp8", ptr(dq16), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), int(group), d, ptr(sel),
-         stream_handle(g.device))
+    if fp8:
+        call("htrc_select_fp8", ptr(dq16), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), int(group), d, ptr(sel),
+             stream_handle(g.device))
+    else:
+        call("htrc_select_bf16", ptr(dq16), ptr(g), ptr(lz), h, nt, nb, int(stride), int(group), d, ptr(sel),
+             stream_handle(g.device))
     return sel
 
 
@@ -217,8 +231,8 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
                    bn: int = 64, ws=None, out=None, logz=None, group: int = 1, perm=None):
     """Far + near online softmax per (tile, split) and the merge
     (h3/htrc_flat_triton.py:348-391) -> (out [H,nq,D] fp32, logz [H,nq] fp32)."""
-    if state["g8"].dtype == torch.float8_e4m3fn:
-        return _tile_fp8(packed, state, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits, bn=bn, ws=ws,
+    if state["g8"].dtype in (torch.float8_e4m3fn, torch.bfloat16):
+        return _tile16(packed, state, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits, bn=bn, ws=ws,
                          out=out, logz=logz, group=group, perm=perm)
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
@@ -245,11 +259,12 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
     return out, logz
 
 
-def _tile_fp8(packed, state, excl, idx, *, nq, leaf, scale, splits, bn, ws, out, logz, group, perm):
-    """Far + near softmax per (tile, split) over the fp8 state, and the merge: packed holds
-    q16, dq16 (pack_q16) and the bf16 k, v; state g8 / vb (e4m3), sg, sv, lz."""
+def _tile16(packed, state, excl, idx, *, nq, leaf, scale, splits, bn, ws, out, logz, group, perm):
+    """Far + near softmax per (tile, split) over a 16-bit state, and the merge: packed holds q16,
+    dq16 (pack_q16) and the bf16 k, v; state g8 / vb (e4m3 with sg, sv; or bf16) and lz."""
     q16, dq16, k, v = packed["q16"], packed["dq16"], packed["k"], packed["v"]
-    g, sg, lz, vb, sv = state["g8"], state["sg"], state["lz"], state["vb"], state["sv"]
+    g, sg, lz, vb, sv = state["g8"], state.get("sg"), state["lz"], state["vb"], state.get("sv")
+    fp8 = g.dtype == torch.float8_e4m3fn
     h, nk, d = (int(x) for x in k.shape)
     nt = -(-nq // TILE)
     kx = int(idx.shape[-1]) if idx is not None else 0
@@ -264,9 +279,14 @@ def _tile_fp8(packed, state, excl, idx, *, nq, leaf, scale, splits, bn, ws, out,
         pm = _buf(ws, "pm", (h, nt, ns, TILE), torch.float32, dev)
         pl = _buf(ws, "pl", (h, nt, ns, TILE), torch.float32, dev)
         pacc = _buf(ws, "pacc", (h, nt, ns, TILE, d), torch.float32, dev)
-    call("htrc_tile_fp8", ptr(q16), ptr(dq16), ptr(g), ptr(sg), ptr(lz), ptr(vb), ptr(sv), ptr(excl),
-         ptr(idx) if kx else None, ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, int(group), ptr(perm), ns, int(bn),
-         float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
+    if fp8:
+        call("htrc_tile_fp8", ptr(q16), ptr(dq16), ptr(g), ptr(sg), ptr(lz), ptr(vb), ptr(sv), ptr(excl),
+             ptr(idx) if kx else None, ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, int(group), ptr(perm), ns, int(bn),
+             float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
+    else:
+        call("htrc_tile_bf16", ptr(q16), ptr(dq16), ptr(g), ptr(lz), ptr(vb), ptr(excl), ptr(idx) if kx else None,
+             ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, int(group), ptr(perm), ns, int(bn), float(scale), ptr(pm),
+             ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
     if ns > 1:
         call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, ns, d, ptr(perm), ptr(out), ptr(logz), stream_handle(dev))
     return out, logz

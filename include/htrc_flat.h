@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 9
+#define HTRC_ABI_VERSION 10
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -145,6 +145,20 @@ int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, c
                   const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int group,
                   const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out,
                   float* logz, void* stream);
+
+/* bf16 state store (store="bf16"; DOT = 1 without FP8 / I8 in h3/htrc_flat_triton.py:82-83,
+ * 132-153, 165-184, 214-254): g, vb bf16 [H, ng, nbp, 128], no row scales; q16 / dq16 from
+ * htrc_pack_q16 with dq_fp16 = 0 (bf16 q - mu).  select: SEL = max_r bf16 dq . g + lz;
+ * tile far: bf16 dq . g + lz with PV bf16(p) . vb; near as the fp8 store.
+ * Replace leaf_stats(store=bfloat16), rowmax_select and tile_attention on that state. */
+int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
+                         int leaf, int d, float scale, uint16_t* g, uint16_t* vb, float* lz, void* stream);
+int htrc_select_bf16(const uint16_t* dq16, const uint16_t* g, const float* lz, int64_t heads, int64_t nt, int64_t nb,
+                     int stride, int group, int d, float* sel, void* stream);
+int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g, const float* lz, const uint16_t* vb,
+                   const int8_t* excl, const int32_t* idx, const uint16_t* k, const uint16_t* v, int64_t heads,
+                   int64_t nq, int64_t nk, int leaf, int d, int kx, int group, const int32_t* perm, int splits, int bn,
+                   float scale, float* pm, float* pl, float* pacc, float* out, float* logz, void* stream);
 
 /* k-means query order: perm int32 [H, nq], the queries ordered by their nearest of `clusters`
  * centres (stable), the centres from `iters` Lloyd steps on `sample` evenly spaced queries.

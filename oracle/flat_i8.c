@@ -35,7 +35,7 @@
  * (h3/htrc_flat.py:217, h3/htrc_flat_triton.py:76,112,115,231). */
 static const float R127 = 1.0f / 127.0f;
 
-int oracle_abi_version(void) { return 4; }
+int oracle_abi_version(void) { return 5; }
 
 float oracle_r127(void) { return R127; }
 
@@ -639,6 +639,133 @@ void oracle_tile_fp8(int64_t nt, int tile, int d, int64_t nb, int leaf, int kx, 
         free(sc);
         free(ps);
         free(v8);
+        free(vals);
+        free(acc);
+        free(dacc);
+        free(qf);
+        free(dqf);
+    }
+}
+
+/* Leaf statistics with the bf16 state store (store="bf16"): g (scaled) and vb rounded to bf16. */
+void oracle_stats_bf16(const float *mu, int64_t nt, const uint16_t *k, const uint16_t *v,
+                       int64_t nb, int leaf, int d, float scale, uint16_t *g16, uint16_t *vb16, float *lz) {
+#pragma omp parallel
+    {
+        float *a = (float *)malloc(sizeof(float) * (size_t)leaf);
+        float *kf = (float *)malloc(sizeof(float) * (size_t)leaf * d);
+        float *gs = (float *)malloc(sizeof(float) * (size_t)d);
+        float *vs = (float *)malloc(sizeof(float) * (size_t)d);
+#pragma omp for schedule(static)
+        for (int64_t tl_ = 0; tl_ < nt * nb; ++tl_) {
+            int64_t t = tl_ / nb, l = tl_ % nb;
+            float mx, z;
+            leaf_state(mu + t * d, k + l * leaf * d, v + l * leaf * d, leaf, d, scale, a, kf, gs, vs, &mx, &z);
+            for (int i = 0; i < d; ++i) {
+                g16[tl_ * d + i] = f2bf(gs[i]);
+                vb16[tl_ * d + i] = f2bf(vs[i]);
+            }
+            lz[tl_] = mx + logf(z);
+        }
+        free(a);
+        free(kf);
+        free(gs);
+        free(vs);
+    }
+}
+
+/* bf16 state store select: SEL[g,l] = max_r (sum_i bf16(dq)_ri * g_li) + lz_gl (products exact). */
+void oracle_select_bf16(const uint16_t *dq16, int tile, int stride, int group, int64_t nt,
+                        const uint16_t *g16, const float *lz, int64_t ng, int64_t nb, int d, float *sel) {
+    int ts = group * tile / stride;
+#pragma omp parallel for schedule(static)
+    for (int64_t tl_ = 0; tl_ < ng * nb; ++tl_) {
+        int64_t gi = tl_ / nb;
+        const uint16_t *g = g16 + tl_ * d;
+        float best = -INFINITY;
+        for (int rr = 0; rr < ts; ++rr) {
+            int64_t j = (int64_t)rr * stride;
+            int64_t t = gi * group + j / tile;
+            if (t > nt - 1) t = nt - 1;
+            int64_t p = t * tile + j % tile;
+            float acc = 0.0f;
+            for (int i = 0; i < d; ++i) acc += bf2f(dq16[p * d + i]) * bf2f(g[i]);
+            if (acc > best) best = acc;
+        }
+        sel[tl_] = best + lz[tl_];
+    }
+}
+
+/* Split-K tile kernel with the bf16 state store: far score (sum bf16 dq . g) + lz, PV bf16(p) . vb;
+ * near as oracle_tile_fp8. */
+void oracle_tile_bf16(int64_t nt, int tile, int d, int64_t nb, int leaf, int kx, int group,
+                      const int32_t *idx, const int8_t *excl, const uint16_t *q16, const uint16_t *dq16,
+                      const uint16_t *g16, const float *lz, const uint16_t *vb16, const uint16_t *k, const uint16_t *v,
+                      float scale, int ns, int bn, float *pm, float *pl, float *pacc) {
+    int64_t lps = oracle_split(nb, ns, bn);
+    int64_t eps = oracle_split((int64_t)kx * leaf, ns, bn);
+#pragma omp parallel
+    {
+        float *sc = (float *)malloc(sizeof(float) * (size_t)bn);
+        const uint16_t **vals = (const uint16_t **)malloc(sizeof(void *) * (size_t)bn);
+        float *acc = (float *)malloc(sizeof(float) * (size_t)d);
+        float *dacc = (float *)malloc(sizeof(float) * (size_t)d);
+        float *qf = (float *)malloc(sizeof(float) * (size_t)d);
+        float *dqf = (float *)malloc(sizeof(float) * (size_t)d);
+#pragma omp for schedule(static)
+        for (int64_t job = 0; job < nt * ns * tile; ++job) {
+            int64_t t = job / ((int64_t)ns * tile);
+            int sp = (int)((job / tile) % ns);
+            int r = (int)(job % tile);
+            int64_t p = t * tile + r;
+            int64_t gs = t / group;
+            for (int i = 0; i < d; ++i) {
+                qf[i] = bf2f(q16[p * d + i]);
+                dqf[i] = bf2f(dq16[p * d + i]);
+            }
+            float m = -INFINITY, l = 0.0f;
+            for (int i = 0; i < d; ++i) acc[i] = 0.0f;
+            int64_t lo = sp * lps, hi = lo + lps < nb ? lo + lps : nb;
+            for (int64_t n0 = lo; n0 < hi; n0 += bn) {
+                for (int c = 0; c < bn; ++c) {
+                    int64_t cc = n0 + c;
+                    if (cc < hi && excl[gs * nb + cc] == 0) {
+                        int64_t s_ = gs * nb + cc;
+                        float a = 0.0f;
+                        for (int i = 0; i < d; ++i) a += dqf[i] * bf2f(g16[s_ * d + i]);
+                        sc[c] = a + lz[s_];
+                        vals[c] = vb16 + s_ * d;
+                    } else {
+                        sc[c] = -INFINITY;
+                        vals[c] = NULL;
+                    }
+                }
+                block_update(sc, vals, bn, d, &m, &l, acc, dacc);
+            }
+            int64_t e_n = (int64_t)kx * leaf;
+            int64_t e_lo = sp * eps, e_hi = e_lo + eps < e_n ? e_lo + eps : e_n;
+            for (int64_t e0 = e_lo; e0 < e_hi; e0 += bn) {
+                for (int c = 0; c < bn; ++c) {
+                    int64_t j = e0 + c;
+                    if (j < e_hi) {
+                        int64_t tok = (int64_t)idx[gs * kx + j / leaf] * leaf + j % leaf;
+                        float a = 0.0f;
+                        for (int i = 0; i < d; ++i) a += qf[i] * bf2f(k[tok * d + i]);
+                        sc[c] = a * scale;
+                        vals[c] = v + tok * d;
+                    } else {
+                        sc[c] = -INFINITY;
+                        vals[c] = NULL;
+                    }
+                }
+                block_update(sc, vals, bn, d, &m, &l, acc, dacc);
+            }
+            int64_t base = (t * ns + sp) * tile + r;
+            pm[base] = m;
+            pl[base] = l;
+            memcpy(pacc + base * d, acc, sizeof(float) * (size_t)d);
+        }
+        free(sc);
         free(vals);
         free(acc);
         free(dacc);

@@ -77,7 +77,11 @@ def lib():
         L.oracle_select_fp8.argtypes = [_U16, _int, _int, _int, _i64, _U8, _F32, _F32, _i64, _i64, _int, _F32]
         L.oracle_tile_fp8.argtypes = [_i64, _int, _int, _i64, _int, _int, _int, _I32, _I8, _U16, _U16,
                                       _U8, _F32, _F32, _U8, _F32, _U16, _U16, _flt, _int, _int, _F32, _F32, _F32]
-        if L.oracle_abi_version() != 4:
+        L.oracle_stats_bf16.argtypes = [_F32, _i64, _U16, _U16, _i64, _int, _int, _flt, _U16, _U16, _F32]
+        L.oracle_select_bf16.argtypes = [_U16, _int, _int, _int, _i64, _U16, _F32, _i64, _i64, _int, _F32]
+        L.oracle_tile_bf16.argtypes = [_i64, _int, _int, _i64, _int, _int, _int, _I32, _I8, _U16, _U16,
+                                       _U16, _F32, _U16, _U16, _U16, _flt, _int, _int, _F32, _F32, _F32]
+        if L.oracle_abi_version() != 5:
             raise RuntimeError(f"{path} is stale (oracle ABI {L.oracle_abi_version()}): rebuild it")
         _lib = L
     return _lib
@@ -272,6 +276,47 @@ def stats_fp8(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int,
     return g8, sg, vb8, sv, lz
 
 
+def stats_bf16(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int, scale: float):
+    """Leaf statistics with the bf16 state store -> g bf16 bits [nt,nb,d], vb bf16 bits, lz [nt,nb]."""
+    mu = _c(mu, np.float32)
+    k_bits, v_bits = _c(k_bits, np.uint16), _c(v_bits, np.uint16)
+    nt, d = mu.shape
+    nb = k_bits.shape[0] // leaf
+    g16 = np.empty((nt, nb, d), np.uint16)
+    vb16 = np.empty((nt, nb, d), np.uint16)
+    lz = np.empty((nt, nb), np.float32)
+    lib().oracle_stats_bf16(mu, nt, k_bits, v_bits, nb, leaf, d, float(scale), g16, vb16, lz)
+    return g16, vb16, lz
+
+
+def select_bf16(dq16, tile: int, g16, lz, stride: int = 1, group: int = 1) -> np.ndarray:
+    """SEL [ng, nb] with the bf16 state store (bf16 dq . g + lz)."""
+    g16 = _c(g16, np.uint16)
+    ng, nb, d = g16.shape
+    nt = dq16.shape[0] // tile
+    sel = np.empty((ng, nb), np.float32)
+    lib().oracle_select_bf16(_c(dq16, np.uint16), tile, stride, int(group), nt, g16, _c(lz, np.float32), ng, nb, d, sel)
+    return sel
+
+
+def tile_partials_bf16(st: dict, *, tile: int, leaf: int, scale: float, splits: int, bn: int, group: int = 1):
+    """Split partials of the tile kernel with the bf16 state store."""
+    g16 = st["g16"]
+    ng, nb, d = g16.shape
+    nt = st["dq16"].shape[0] // tile
+    kx = st["idx"].shape[1]
+    idx = st["idx"] if kx else np.zeros((ng, 1), np.int32)
+    ns = max(1, int(splits))
+    pm = np.empty((nt, ns, tile), np.float32)
+    pl = np.empty((nt, ns, tile), np.float32)
+    pacc = np.empty((nt, ns, tile, d), np.float32)
+    lib().oracle_tile_bf16(nt, tile, d, nb, leaf, kx, int(group), _c(idx, np.int32), _c(st["excl"], np.int8),
+                           _c(st["q16"], np.uint16), _c(st["dq16"], np.uint16), g16, _c(st["lz"], np.float32),
+                           _c(st["vb16"], np.uint16), _c(st["k"], np.uint16), _c(st["v"], np.uint16), float(scale),
+                           ns, int(bn), pm, pl, pacc)
+    return pm, pl, pacc
+
+
 def select_fp8(dq16, tile: int, g8, sg, lz, stride: int = 1, group: int = 1) -> np.ndarray:
     """SEL [ng, nb] with the fp8 state store (h3/htrc_flat_triton.py:214-254, FP8 = 1)."""
     g8 = _c(g8, np.uint8)
@@ -358,14 +403,20 @@ def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: 
         st["k"] = _c(k_bits, np.uint16)
         st["q16"], st["dq16"] = pack_q16(qf, tile, st["mu"], group, dq_fp16=True)
         st["g8"], st["sg"], st["vb8"], st["sv"], st["lz"] = stats_fp8(st["mu"], k_bits, v_bits, leaf, scale)
+    elif store == "bf16":
+        st["k"] = _c(k_bits, np.uint16)
+        st["q16"], st["dq16"] = pack_q16(qf, tile, st["mu"], group, dq_fp16=False)
+        st["g16"], st["vb16"], st["lz"] = stats_bf16(st["mu"], k_bits, v_bits, leaf, scale)
     elif store == "int8":
         st["q8"], st["sq"], st["dq8"], st["sdq"] = pack_q(qf, tile, st["mu"], group)
         st["g8"], st["sg"], st["vb"], st["lz"] = stats(st["mu"], k_bits, v_bits, leaf, scale)
     else:
-        raise ValueError("store must be int8 or fp8")
+        raise ValueError("store must be int8, fp8 or bf16")
     if kx > 0:
         if store == "fp8":
             st["sel"] = select_fp8(st["dq16"], tile, st["g8"], st["sg"], st["lz"], sel_stride, group)
+        elif store == "bf16":
+            st["sel"] = select_bf16(st["dq16"], tile, st["g16"], st["lz"], sel_stride, group)
         else:
             st["sel"] = select(st["dq8"], st["sdq"], tile, st["g8"], st["sg"], st["lz"], sel_stride, group)
         st["idx"], st["excl"] = topk(st["sel"], kx, sink)
@@ -373,7 +424,7 @@ def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: 
         nt = st["mu"].shape[0]
         st["idx"] = np.zeros((nt, 0), np.int32)
         st["excl"] = np.zeros((nt, nb), np.int8)
-    tp = tile_partials_fp8 if store == "fp8" else tile_partials
+    tp = {"fp8": tile_partials_fp8, "bf16": tile_partials_bf16}.get(store, tile_partials)
     pm, pl, pacc = tp(st, tile=tile, leaf=leaf, scale=scale, splits=splits, bn=bn, group=group)
     out, logz = merge(pm, pl, pacc)
     st["out"], st["logz"] = out[:n], logz[:n]

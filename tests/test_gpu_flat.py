@@ -202,3 +202,24 @@ def test_fp8_store_vs_oracle(device, n, leaf, ex, group):
     assert mism <= max(1, ref["idx"].shape[0] // 50)
     assert rel_l2(out.cpu().numpy(), ref["out"]) <= OUT_REL_L2
     assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
+
+
+@pytest.mark.parametrize("n,leaf,ex,group", [(8192, 64, 16, 1), (3000, 32, 8, 2)])
+def test_bf16_store_vs_oracle(device, n, leaf, ex, group):
+    """store="bf16" (the 16-bit state of h3/htrc_flat_triton.py:132-153, 214-254 with FP8 = 0):
+    bf16 leaf state, bf16 far and near dots, in the reference's stage structure."""
+    nk = (n // leaf) * leaf
+    q, k, v = workloads.clustered_runs(n=n, runs=max(1, n // 64), heads=1, seed=n + leaf + 7)
+    k, v = k[:, :nk].contiguous(), v[:, :nk].contiguous()
+    st = {}
+    out, logz = htrc_flat.flat_attention(q[0].to(device), k[0].to(device), v[0].to(device), backend="hip",
+                                         store="bf16", dot="bf16", leaf=leaf, exact_leaves=ex, splits=4,
+                                         kern={"tile_bn": 64, "group": group}, return_logz=True, state=st)
+    torch.cuda.synchronize()
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=ex, splits=4, bn=64,
+                          group=group, store="bf16")
+    assert np.array_equal(st["dq16"][0].view(torch.int16).cpu().numpy().view(np.uint16), ref["dq16"])
+    mism = _routing_check(st["idx"][0].cpu().numpy(), ref)
+    assert mism <= max(1, ref["idx"].shape[0] // 50)
+    assert rel_l2(out.cpu().numpy(), ref["out"]) <= OUT_REL_L2
+    assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS

@@ -421,3 +421,79 @@ def test_select_and_tile_fp8_on_oracle_state(device, group, stride):
         np.testing.assert_allclose(_np(sel[0])[:, :nb], ref["sel"], rtol=2e-5, atol=2e-5)
         assert rel_l2(_np(out[0]), ref["out"]) <= OUT_REL_L2
         assert np.abs(_np(logz[0]) - ref["logz"]).max() <= LOGZ_ABS
+
+
+# ---- bf16 state store (store="bf16", the 16-bit state of h3/htrc_flat_triton.py:132-153, 214-254)
+
+@pytest.mark.parametrize("nq,group", [(4096, 1), (1000, 2)])
+def test_pack_q16_bf16_dq_bitexact(device, nq, group):
+    q, _, _ = _data(max(nq, 256), nk=256, seed=nq + 9)
+    q = q[:, :nq].float() + 1e-3 * torch.randn((1, nq, 128), generator=torch.Generator().manual_seed(3))
+    mu, q16, dq16 = hip.pack_q16(q.to(device).contiguous(), group=group, dq_fp16=False)
+    torch.cuda.synchronize()
+    assert dq16.dtype == torch.bfloat16
+    qf = q[0].float().numpy()
+    omu = flat_i8.tile_centres(qf, 64) if group == 1 else flat_i8.group_centres(qf, 64, group)
+    oq16, odq16 = flat_i8.pack_q16(qf, 64, omu, group, dq_fp16=False)
+    assert np.array_equal(_np(q16[0].view(torch.int16)).view(np.uint16), oq16)
+    assert np.array_equal(_np(dq16[0].view(torch.int16)).view(np.uint16), odq16)
+
+
+def _bf16_state(ref, k, v, device):
+    """The oracle's bf16 state (padded to the HIP layout) and packed operands on the device."""
+    ng, nb, d = ref["g16"].shape
+    nbp = nb_pad(nb)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    g = np.zeros((1, ng, nbp, d), np.uint16)
+    g[0, :, :nb] = ref["g16"]
+    vb = np.zeros((1, ng, nbp, d), np.uint16)
+    vb[0, :, :nb] = ref["vb16"]
+    lz = np.full((1, ng, nbp), -np.inf, np.float32)
+    lz[0, :, :nb] = ref["lz"]
+    excl = np.zeros((1, ng, nbp), np.int8)
+    excl[0, :, :nb] = ref["excl"]
+    bfv = lambda a: T(a.view(np.int16)).view(torch.bfloat16)  # noqa: E731
+    packed = {"q16": bfv(ref["q16"][None]), "dq16": bfv(ref["dq16"][None]), "k": k.to(device), "v": v.to(device)}
+    state = {"g8": bfv(g), "vb": bfv(vb), "sg": None, "sv": None, "lz": T(lz)}
+    return packed, state, T(excl), T(ref["idx"][None])
+
+
+@pytest.mark.parametrize("leaf", [64, 32])
+def test_stats_bf16_close_to_oracle(device, leaf):
+    n = 2048
+    q, k, v = _data(n, seed=leaf + 11)
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=4, store="bf16")
+    nb = n // leaf
+    mu = torch.from_numpy(ref["mu"])[None].to(device)
+    g, lz, vbs, sg, sv = hip.leaf_stats(mu, k.to(device), v.to(device), nb, 1 / math.sqrt(128), leaf=leaf,
+                                        store=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert sg is None and sv is None
+    np.testing.assert_allclose(_np(lz[0])[:, :nb], ref["lz"], rtol=0, atol=2e-5 * (1 + np.abs(ref["lz"]).max()))
+    for got, want in ((g, ref["g16"]), (vbs, ref["vb16"])):
+        a = _np(got[0].float())[:, :nb].astype(np.float64)
+        b = bf16.to_f32(want).astype(np.float64)
+        # one bf16 step, over a floor at 2^-8 of the row's largest entry (fp32 moment sums)
+        floor = np.abs(b).max(-1, keepdims=True) * 2 ** -8
+        assert np.all(np.abs(a - b) <= np.maximum(np.abs(b) * 2 ** -7, floor) * 1.001)
+        assert (_np(got[0].view(torch.int16))[:, :nb].view(np.uint16) != want).mean() < 5e-2
+
+
+@pytest.mark.parametrize("group,stride", [(1, 1), (2, 4)])
+def test_select_and_tile_bf16_on_oracle_state(device, group, stride):
+    n, leaf, ex = 64 * 21 + 5, 64, 6
+    q, k, v = _data(n, nk=64 * 24, seed=group + 60)
+    scale = 1 / math.sqrt(128)
+    for splits in (1, 4):
+        ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=ex, splits=splits,
+                              bn=64, sel_stride=stride, group=group, store="bf16")
+        packed, state, excl, idx = _bf16_state(ref, k, v, device)
+        nb = ref["g16"].shape[1]
+        sel = hip.rowmax_select(g=state["g8"], lz=state["lz"], sg=None, stride=stride, nb=nb,
+                                dq8=packed["dq16"], group=group)
+        out, logz = hip.tile_attention(packed, state, excl, idx, nq=n, leaf=leaf, scale=scale, splits=splits, bn=64,
+                                       group=group)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(_np(sel[0])[:, :nb], ref["sel"], rtol=2e-5, atol=2e-5)
+        assert rel_l2(_np(out[0]), ref["out"]) <= OUT_REL_L2
+        assert np.abs(_np(logz[0]) - ref["logz"]).max() <= LOGZ_ABS
