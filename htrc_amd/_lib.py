@@ -13,7 +13,7 @@ import torch
 
 HERE = Path(__file__).resolve().parent
 LIBPATH = HERE / "libhtrc_flat.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -25,25 +25,25 @@ SIGNATURES = {
     "htrc_abi_version": [],
     "htrc_last_error": [],
     "htrc_nb_pad": [_i64],
-    "htrc_pack_q": [_vp, _int, _i64, _i64, _int, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    "htrc_pack_q": [_vp, _int, _i64, _i64, _int, _int, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "htrc_pack_k": [_vp, _i64, _i64, _int, _vp, _vp, _vp],
     "htrc_leaf_stats": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _flt, _vp, _vp, _vp, _vp, _vp],
-    "htrc_select": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _vp, _vp],
+    "htrc_select": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _vp],
     "htrc_topk": [_vp, _i64, _i64, _int, _int, _vp, _vp, _vp],
-    "htrc_tile": [_vp] * 13 + [_i64, _i64, _i64, _int, _int, _int, _int, _vp, _int, _int, _flt] + [_vp] * 6,
-    "htrc_merge": [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp, _vp, _vp],
-    "htrc_route_select": [_vp] * 5 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _vp, _vp, _vp],
-    "htrc_route_attend": [_vp] * 13 + [_i64, _i64, _i64, _int, _int, _int, _int, _vp, _flt, _vp, _vp, _vp],
-    "htrc_route": [_vp] * 11 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _vp, _flt, _vp, _vp, _vp, _vp,
+    "htrc_tile": [_vp] * 13 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _vp, _int, _int, _flt] + [_vp] * 6,
+    "htrc_merge": [_vp, _vp, _vp, _i64, _i64, _int, _int, _int, _vp, _vp, _vp, _vp],
+    "htrc_route_select": [_vp] * 5 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _int, _vp, _vp, _vp],
+    "htrc_route_attend": [_vp] * 13 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _vp, _flt, _vp, _vp, _vp],
+    "htrc_route": [_vp] * 11 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _int, _vp, _flt, _vp, _vp, _vp, _vp,
                                  _vp],
     "htrc_tail": [_vp, _int, _vp, _vp, _i64, _i64, _i64, _int, _flt, _vp, _vp, _vp],
-    "htrc_pack_q16": [_vp, _int, _i64, _i64, _int, _int, _vp, _int, _vp, _vp, _vp, _vp],
+    "htrc_pack_q16": [_vp, _int, _i64, _i64, _int, _int, _int, _vp, _int, _vp, _vp, _vp, _vp],
     "htrc_leaf_stats_fp8": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _flt, _vp, _vp, _vp, _vp, _vp, _vp],
-    "htrc_select_fp8": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _vp, _vp],
-    "htrc_tile_fp8": [_vp] * 11 + [_i64, _i64, _i64, _int, _int, _int, _int, _vp, _int, _int, _flt] + [_vp] * 6,
+    "htrc_select_fp8": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _vp],
+    "htrc_tile_fp8": [_vp] * 11 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _vp, _int, _int, _flt] + [_vp] * 6,
     "htrc_leaf_stats_bf16": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _flt, _vp, _vp, _vp, _vp],
-    "htrc_select_bf16": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _vp, _vp],
-    "htrc_tile_bf16": [_vp] * 9 + [_i64, _i64, _i64, _int, _int, _int, _int, _vp, _int, _int, _flt] + [_vp] * 6,
+    "htrc_select_bf16": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _vp],
+    "htrc_tile_bf16": [_vp] * 9 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _vp, _int, _int, _flt] + [_vp] * 6,
     "htrc_kmeans_order": [_vp, _int, _i64, _i64, _int, _int, _int, _int, _vp, _vp, _vp, _vp],
     "htrc_dequant_rows": [_vp, _i64, _vp, _i64, _i64, _int, _vp, _int, _vp],
     "htrc_selftest_mfma": [_vp] * 7,

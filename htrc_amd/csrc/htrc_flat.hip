@@ -44,26 +44,26 @@ __device__ __forceinline__ int64_t perm_row(const int32_t* perm, int64_t h, int6
     return r < 0 ? 0 : (r >= nq ? nq - 1 : r);
 }
 
-// Shared centres of tile groups (h3/htrc_flat.py:223-229): mu_g is the mean of the G * 64 rows
-// of tiles gG .. gG + G - 1, where tiles past the last repeat the last tile and rows past the
-// last query repeat the last query (the reference pads the tiles, then averages every padded
-// row).  One thread per dim: sequential fp32 sum over the group's rows in order, then one IEEE
-// division.
+// Shared centres of tile groups (h3/htrc_flat.py:223-229): mu_g is the mean of the G * tile
+// rows of tiles gG .. gG + G - 1, where tiles past the last repeat the last tile and rows past
+// the last query repeat the last query (the reference pads the tiles, then averages every
+// padded row).  One thread per dim: sequential fp32 sum over the group's rows in order, then
+// one IEEE division.
 template <bool IN_BF16>
 __global__ __launch_bounds__(128) void group_centres_kernel(const void* __restrict__ qin, int64_t nq, int nt,
-                                                            int group, int ng, const int32_t* __restrict__ perm,
-                                                            float* __restrict__ mu) {
+                                                            int tile, int group, int ng,
+                                                            const int32_t* __restrict__ perm, float* __restrict__ mu) {
     const int g = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
     const int64_t qbase = (int64_t)h * nq * D;
-    const int rows = group * TILE;
+    const int rows = group * tile;
     float s = 0.0f;
     for (int j0 = 0; j0 < rows; j0 += 8) {
         float x[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int j = j0 + u;
-            const int t = min(g * group + j / TILE, nt - 1);
-            const int64_t pp = min((int64_t)t * TILE + j % TILE, nq - 1);
+            const int t = min(g * group + j / tile, nt - 1);
+            const int64_t pp = min((int64_t)t * tile + j % tile, nq - 1);
             const int64_t p = perm_row(perm, h, nq, pp);
             x[u] = IN_BF16 ? bf2f(((const uint16_t*)qin)[qbase + p * D + i]) : ((const float*)qin)[qbase + p * D + i];
         }
@@ -73,26 +73,28 @@ __global__ __launch_bounds__(128) void group_centres_kernel(const void* __restri
     mu[((int64_t)h * ng + g) * D + i] = __fdiv_rn(s, (float)rows);
 }
 
-// group == 1: the tile's centre over its real rows is computed here and written to mu; group > 1:
-// the group's centre is read from mu (group_centres_kernel).  perm (optional): row p of the
-// operator is query perm[p] (order="kmeans").
+// One workgroup per tile of `tile` (32 or 64) rows.  group == 1: the tile's centre over its
+// real rows is computed here and written to mu; group > 1: the group's centre is read from mu
+// (group_centres_kernel).  perm (optional): row p of the operator is query perm[p]
+// (order="kmeans").
 // QM = 0: row int8 of q and q - mu (q8 / sq, dq8 / sdq).  QM = 1, 2: the 16-bit operands of the
 // reference's bf16 and fp8 state stores: q in bf16 (q8 holds uint16 rows, sq unused) and q - mu in
 // bf16 (QM = 1) or fp16 (QM = 2) (h3/htrc_flat_triton.py:104-108, dqb / dqh; dq8 holds them).
 template <bool IN_BF16, int QM = 0>
-__global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qin, int64_t nq, int nt, int group,
-                                                     int ng, const int32_t* __restrict__ perm,
+__global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qin, int64_t nq, int nt, int tile,
+                                                     int group, int ng, const int32_t* __restrict__ perm,
                                                      float* __restrict__ mu, int8_t* __restrict__ q8,
                                                      float* __restrict__ sq, int8_t* __restrict__ dq8,
                                                      float* __restrict__ sdq) {
     __shared__ __align__(16) float tq[TILE][D + 4];
     __shared__ __align__(16) float smu[D];
     const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    const int64_t r0 = (int64_t)t * TILE;
-    const int nr = (int)(nq - r0 < TILE ? nq - r0 : TILE);
+    const int64_t r0 = (int64_t)t * tile;
+    const int nr = (int)(nq - r0 < tile ? nq - r0 : tile);
     const int64_t qbase = (int64_t)h * nq * D;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {               // 8 consecutive values per thread and chunk
+        if (16 * j >= tile) break;              // chunk j holds rows 16j .. 16j + 15
         const int c = tid + 256 * j, r = c >> 4, c8 = (c & 15) * 8;
         const int64_t pr = r0 + r < nq ? r0 + r : nq - 1;                      // pad rows repeat the last row
         const int64_t src = qbase + perm_row(perm, h, nq, pr) * D + c8;
@@ -123,6 +125,7 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
     }
     __syncthreads();
     const int w = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
+    if (16 * w >= tile) return;                    // wave w packs rows 16w .. 16w + 15
     float m[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) m[e] = smu[8 * i + e];
@@ -137,7 +140,7 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
             aq = fmaxf(aq, fabsf(x[e]));
             ad = fmaxf(ad, fabsf(d[e]));
         }
-        const int64_t p = tg * TILE + r;
+        const int64_t p = tg * tile + r;
         if constexpr (QM != 0) {
             uint32_t uq[4], ud[4];
 #pragma unroll
@@ -623,13 +626,14 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
 // ---------------------------------------------------------------------------------------------
 // select: SEL[t, l] = max_r float(dq8_r . g8_tl) * (sdq_r * sg_tl) + lz_tl
 // (h3/htrc_flat_triton.py:214-254).  Workgroup = one tile x 256 leaves; each wave owns 64
-// leaves and all rows (four 16-row B operands held in registers).  Bit-exact: int32 dot,
+// leaves and all rows (tile / 16 B operands of 16 rows held in registers).  Bit-exact: int32 dot,
 // one fp32 product per row, an exact max, one fp32 add.
 // ---------------------------------------------------------------------------------------------
+template <int NRB>
 __device__ __forceinline__ void load_rows_i8(const int8_t* __restrict__ x8, int64_t row0, int stride,
-                                             int ts, int col, int grp, i32x4 (&b)[4][2], bool (&val)[4]) {
+                                             int ts, int col, int grp, i32x4 (&b)[NRB][2], bool (&val)[NRB]) {
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
+    for (int rb = 0; rb < NRB; ++rb) {
         const int r = 16 * rb + col;
         val[rb] = r < ts;
         const int64_t p = row0 + (int64_t)(val[rb] ? r : 0) * stride;
@@ -639,17 +643,20 @@ __device__ __forceinline__ void load_rows_i8(const int8_t* __restrict__ x8, int6
 }
 
 // SEL of one tile group (G tiles sharing a centre; G = 1: one tile): the max runs over the
-// rows of every tile of the group (h3/htrc_flat.py:244-252 hands the kernel the G * 64 rows).
+// rows of every tile of the group (h3/htrc_flat.py:244-252 hands the kernel the G * tile rows).
+// NRB = tile / 16 row blocks of 16 rows held as B operands.
+template <int NRB>
 __global__ __launch_bounds__(256) void select_kernel(const int8_t* __restrict__ dq8,
                                                      const float* __restrict__ sdq, int stride,
                                                      const int8_t* __restrict__ g8,
                                                      const float* __restrict__ sg,
                                                      const float* __restrict__ lz, int nt, int group, int ng,
                                                      int nb, int nb_pad, float* __restrict__ sel) {
+    constexpr int TR = 16 * NRB;                      // rows per tile
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int gi = blockIdx.x, h = blockIdx.z;
     const int64_t gs = (int64_t)h * ng + gi;          // state / SEL row of the group
-    const int ts = TILE / stride;
+    const int ts = TR / stride;
     const int c0 = blockIdx.y * 256 + w * 64;
     float bsel[4][4];
 #pragma unroll
@@ -660,33 +667,33 @@ __global__ __launch_bounds__(256) void select_kernel(const int8_t* __restrict__ 
         const int t = gi * group + j;
         if (t >= nt) break;                           // padded tiles repeat the last one
         const int64_t th = (int64_t)h * nt + t;
-        i32x4 b[4][2];
-        bool val[4];
-        load_rows_i8(dq8, th * TILE, stride, ts, col, grp, b, val);
-        float srow[4];
+        i32x4 b[NRB][2];
+        bool val[NRB];
+        load_rows_i8(dq8, th * TR, stride, ts, col, grp, b, val);
+        float srow[NRB];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) srow[rb] = sdq[th * TILE + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
+        for (int rb = 0; rb < NRB; ++rb) srow[rb] = sdq[th * TR + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
 #pragma unroll
         for (int lb = 0; lb < 4; ++lb) {
             const int c = c0 + 16 * lb;
             if (c < nb) {
                 const int64_t s0 = gs * nb_pad + c;
                 const int8_t* G = g8 + s0 * D;
-                i32x4 acc[4];
+                i32x4 acc[NRB];
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb) acc[rb] = i32x4{0, 0, 0, 0};
+                for (int rb = 0; rb < NRB; ++rb) acc[rb] = i32x4{0, 0, 0, 0};
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
                     const i32x4 A = *(const i32x4*)(G + col * D + 64 * ks + 16 * grp);
 #pragma unroll
-                    for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma_i8(A, b[rb][ks], acc[rb]);
+                    for (int rb = 0; rb < NRB; ++rb) acc[rb] = mfma_i8(A, b[rb][ks], acc[rb]);
                 }
                 const f32x4 sgv = *(const f32x4*)(sg + s0 + 4 * grp);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     float best = -INFINITY;
 #pragma unroll
-                    for (int rb = 0; rb < 4; ++rb)
+                    for (int rb = 0; rb < NRB; ++rb)
                         if (val[rb]) best = fmaxf(best, __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i])));
                     bsel[lb][i] = fmaxf(bsel[lb][i], col_max(best));
                 }
@@ -1003,16 +1010,16 @@ __global__ __launch_bounds__(256) void tile_kernel(
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ excl,
     const int32_t* __restrict__ idx, const int8_t* __restrict__ k8, const float* __restrict__ ks,
-    const uint16_t* __restrict__ v, int64_t nq, int nt, int group, int ng, const int32_t* __restrict__ perm,
-    int64_t nk, int nb, int nb_pad, int kx, int lps, int eps, float scale, float* __restrict__ pm,
-    float* __restrict__ pl, float* __restrict__ pacc,
+    const uint16_t* __restrict__ v, int64_t nq, int nt, int tile, int group, int ng,
+    const int32_t* __restrict__ perm, int64_t nk, int nb, int nb_pad, int kx, int lps, int eps, float scale,
+    float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc,
     float* __restrict__ out, float* __restrict__ logz) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int t = blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
     const int64_t th = (int64_t)h * nt + t;
     const int64_t gs = (int64_t)h * ng + t / group;       // state / routing row: the tile's group
-    const int r = w * 16 + col;
-    const int64_t p = th * TILE + r;
+    const int r = w * 16 + col;                           // blockDim = 4 * tile: one wave per 16 rows
+    const int64_t p = th * tile + r;
     i32x4 q8r[2], dq8r[2];
     load_row_ops(q8, dq8, p, grp, q8r, dq8r);
     const float sqr = sq[p], sdqr = sdq[p];
@@ -1028,12 +1035,12 @@ __global__ __launch_bounds__(256) void tile_kernel(
                         vb, excl + gs * nb_pad, idx + gs * (kx > 0 ? kx : 1), k8, ks, v, (int64_t)h * nk, scale);
     const float ltot = grp_sum(st.l);
     if (pacc == nullptr) {   // single split: normalise in place
-        const int64_t qi = (int64_t)t * TILE + r;
+        const int64_t qi = (int64_t)t * tile + r;
         const int64_t oq = qi < nq ? perm_row(perm, h, nq, qi) : qi;
         write_final(st, ltot, (int64_t)h * nq + oq, qi < nq, out, logz);
         return;
     }
-    const int64_t base = (th * ns + sp) * TILE + r;
+    const int64_t base = (th * ns + sp) * tile + r;
     if (grp == 0) {
         pm[base] = st.m;
         pl[base] = ltot;
@@ -1062,15 +1069,16 @@ __device__ __forceinline__ f32x4 state_qk(const void* g, int64_t row, int ks, in
         return mfma_bf16(as_bf16x8(*(const u32x4*)((const uint16_t*)g + row * D + 32 * ks + 8 * grp)), as_bf16x8(b), acc);
 }
 
-template <bool FP8>
+template <bool FP8, int NRB>
 __global__ __launch_bounds__(256) void select16_kernel(const uint16_t* __restrict__ dq16, int stride,
                                                        const void* __restrict__ g, const float* __restrict__ sg,
                                                        const float* __restrict__ lz, int nt, int group, int ng,
                                                        int nb, int nb_pad, float* __restrict__ sel) {
+    constexpr int TR = 16 * NRB;                      // rows per tile
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int gi = blockIdx.x, h = blockIdx.z;
     const int64_t gs = (int64_t)h * ng + gi;
-    const int ts = TILE / stride;
+    const int ts = TR / stride;
     const int c0 = blockIdx.y * 256 + w * 64;
     float bsel[4][4];
 #pragma unroll
@@ -1081,13 +1089,13 @@ __global__ __launch_bounds__(256) void select16_kernel(const uint16_t* __restric
         const int t = gi * group + j;
         if (t >= nt) break;                           // padded tiles repeat the last one
         const int64_t th = (int64_t)h * nt + t;
-        u32x4 b[4][4];
-        bool val[4];
+        u32x4 b[NRB][4];
+        bool val[NRB];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int rb = 0; rb < NRB; ++rb) {
             const int r = 16 * rb + col;
             val[rb] = r < ts;
-            const int64_t p = th * TILE + (int64_t)(val[rb] ? r : 0) * stride;
+            const int64_t p = th * TR + (int64_t)(val[rb] ? r : 0) * stride;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) b[rb][ks] = *(const u32x4*)(dq16 + p * D + 32 * ks + 8 * grp);
         }
@@ -1096,20 +1104,20 @@ __global__ __launch_bounds__(256) void select16_kernel(const uint16_t* __restric
             const int c = c0 + 16 * lb;
             if (c < nb) {
                 const int64_t s0 = gs * nb_pad + c;
-                f32x4 acc[4];
+                f32x4 acc[NRB];
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int rb = 0; rb < NRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-                    for (int rb = 0; rb < 4; ++rb) acc[rb] = state_qk<FP8>(g, s0 + col, ks, grp, b[rb][ks], acc[rb]);
+                    for (int rb = 0; rb < NRB; ++rb) acc[rb] = state_qk<FP8>(g, s0 + col, ks, grp, b[rb][ks], acc[rb]);
                 const f32x4 sgv = FP8 ? *(const f32x4*)(sg + s0 + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     float best = -INFINITY;
                     const float sc = __fmul_rn(sgv[i], 256.0f);
 #pragma unroll
-                    for (int rb = 0; rb < 4; ++rb)
+                    for (int rb = 0; rb < NRB; ++rb)
                         if (val[rb]) best = fmaxf(best, FP8 ? __fmul_rn(acc[rb][i], sc) : acc[rb][i]);
                     bsel[lb][i] = fmaxf(bsel[lb][i], col_max(best));
                 }
@@ -1171,16 +1179,16 @@ __global__ __launch_bounds__(256) void tile16_kernel(
     const uint16_t* __restrict__ q16, const uint16_t* __restrict__ dq16, const void* __restrict__ g,
     const float* __restrict__ sg, const float* __restrict__ lz, const void* __restrict__ vb,
     const float* __restrict__ sv, const int8_t* __restrict__ excl, const int32_t* __restrict__ idx,
-    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t nq, int nt, int group, int ng,
-    const int32_t* __restrict__ perm, int64_t nk, int nb, int nb_pad, int kx, int lps, int eps, float scale,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t nq, int nt, int tile, int group,
+    int ng, const int32_t* __restrict__ perm, int64_t nk, int nb, int nb_pad, int kx, int lps, int eps, float scale,
     float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc, float* __restrict__ out,
     float* __restrict__ logz) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int t = blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
     const int64_t th = (int64_t)h * nt + t;
     const int64_t gs = (int64_t)h * ng + t / group;       // state / routing row: the tile's group
-    const int r = w * 16 + col;
-    const int64_t p = th * TILE + r;
+    const int r = w * 16 + col;                           // blockDim = 4 * tile: one wave per 16 rows
+    const int64_t p = th * tile + r;
     u32x4 qb[4], dqh[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -1264,12 +1272,12 @@ __global__ __launch_bounds__(256) void tile16_kernel(
     }
     const float ltot = grp_sum(st.l);
     if (pacc == nullptr) {   // single split: normalise in place
-        const int64_t qi = (int64_t)t * TILE + r;
+        const int64_t qi = (int64_t)t * tile + r;
         const int64_t oq = qi < nq ? perm_row(perm, h, nq, qi) : qi;
         write_final(st, ltot, (int64_t)h * nq + oq, qi < nq, out, logz);
         return;
     }
-    const int64_t base = (th * ns + sp) * TILE + r;
+    const int64_t base = (th * ns + sp) * tile + r;
     if (grp == 0) {
         pm[base] = st.m;
         pl[base] = ltot;
@@ -1278,25 +1286,26 @@ __global__ __launch_bounds__(256) void tile16_kernel(
     for (int db = 0; db < 8; ++db) *(f32x4*)(pacc + base * D + 16 * db + 4 * grp) = st.o[db];
 }
 
-// merge: (h3/htrc_flat_triton.py:257-273) + logZ = mm + log(den).  One workgroup per tile.
+// merge: (h3/htrc_flat_triton.py:257-273) + logZ = mm + log(den).  One workgroup (4 * tile
+// threads) per tile.
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
                                                     const float* __restrict__ pacc, int ns, int64_t nq, int nt,
-                                                    const int32_t* __restrict__ perm, float* __restrict__ out,
-                                                    float* __restrict__ logz) {
+                                                    int tile, const int32_t* __restrict__ perm,
+                                                    float* __restrict__ out, float* __restrict__ logz) {
     const int t = blockIdx.x, h = blockIdx.y;
     const int64_t th = (int64_t)h * nt + t;
     const int r = threadIdx.x >> 2, part = threadIdx.x & 3;   // 4 threads per row, 32 dims each
-    const int64_t qi = (int64_t)t * TILE + r;
+    const int64_t qi = (int64_t)t * tile + r;
     if (qi >= nq) return;
     float mm = -INFINITY;
-    for (int s = 0; s < ns; ++s) mm = fmaxf(mm, pm[(th * ns + s) * TILE + r]);
+    for (int s = 0; s < ns; ++s) mm = fmaxf(mm, pm[(th * ns + s) * tile + r]);
     if (mm == -INFINITY) mm = 0.0f;
     float den = 0.0f;
     float num[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) num[i] = 0.0f;
     for (int s = 0; s < ns; ++s) {
-        const int64_t b = (th * ns + s) * TILE + r;
+        const int64_t b = (th * ns + s) * tile + r;
         const float wv = __expf(__fsub_rn(pm[b], mm));
         den = __fadd_rn(den, __fmul_rn(pl[b], wv));
 #pragma unroll
@@ -1323,24 +1332,27 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm
 //     the select_kernel arithmetic), top-k -> idx, and each row's largest far-field score;
 //   route_kernel, one 8-wave workgroup per tile: far + near field in one online softmax whose
 //     reference max is that score.  Wave pair pr = wave % 4 takes a quarter of the keys (its
-//     far leaves, then its near tokens, in 32-key blocks) and wave wave / 4 of the pair takes 32
-//     of the 64 rows: two waves share each SIMD, and each block in LDS feeds both.  A pair's
+//     far leaves, then its near tokens, in 32-key blocks) and wave wave / 4 of the pair takes
+//     half of the tile's rows (32 of 64, or 16 of 32): two waves share each SIMD, and each
+//     block in LDS feeds both.  A pair's
 //     blocks stream through a 3-slot LDS ring, loaded two blocks ahead by direct global->LDS
 //     loads split between the two waves; the four partial states merge through LDS.
 // SEL and the partial states never reach HBM.
 // ---------------------------------------------------------------------------------------------
-struct Rows2 {         // softmax state of the 32 rows of one wave
-    float m[2];        // reference max (log2 units), fixed during a pass
-    float l[2];        // this lane's share of the row sums
-    f32x4 o[2][8];     // O^T per row block: dims 16db + 4grp + i of row 16rb + lane%16
+template <int RB>
+struct RowsN {         // softmax state of the 16 RB rows of one wave
+    float m[RB];       // reference max (log2 units), fixed during a pass
+    float l[RB];       // this lane's share of the row sums
+    f32x4 o[RB][8];    // O^T per row block: dims 16db + 4grp + i of row 16rb + lane%16
 };
 
-// p = 2^(u - m) for the log2-domain scores u[rb][0..7] of the two row blocks (keys
+// p = 2^(u - m) for the log2-domain scores u[rb][0..7] of the RB row blocks (keys
 // 16(e/4) + 4grp + e%4 of the block; masked keys -inf), l += p, O^T += V^T P^T.
-__device__ __forceinline__ void rows2_update(Rows2& st, const float (&sc)[2][8], const u32x2 (&v)[8][2]) {
-    bf16x8 P[2];
+template <int RB>
+__device__ __forceinline__ void rows_update(RowsN<RB>& st, const float (&sc)[RB][8], const u32x2 (&v)[8][2]) {
+    bf16x8 P[RB];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) {
         float p[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(__fsub_rn(sc[rb][e], st.m[rb]));
@@ -1352,7 +1364,7 @@ __device__ __forceinline__ void rows2_update(Rows2& st, const float (&sc)[2][8],
     for (int db = 0; db < 8; ++db) {
         const bf16x8 A = as_bf16x8(v[db][0], v[db][1]);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) st.o[rb][db] = mfma_bf16(A, P[rb], st.o[rb][db]);
+        for (int rb = 0; rb < RB; ++rb) st.o[rb][db] = mfma_bf16(A, P[rb], st.o[rb][db]);
     }
 }
 
@@ -1413,7 +1425,9 @@ __device__ __forceinline__ void dma_rows27(const uint16_t* x0, const uint16_t* x
 //   fixed softmax reference of route_kernel (the tile maximum when rows are sampled).
 // Small register and LDS footprint: several tiles share a CU, so their load latency and their
 // top-k overlap.  SEL never reaches HBM.
-template <bool MULTI>      // MULTI: tile groups of G > 1 tiles (keys merged by max over the tiles)
+// MULTI: tile groups of G > 1 tiles (keys merged by max over the tiles); NRB = tile / 16 row
+// blocks of 16 rows per tile.
+template <bool MULTI, int NRB>
 __global__ __launch_bounds__(256, 4) void route_select_kernel(
     const int8_t* __restrict__ dq8, const float* __restrict__ sdq, const int8_t* __restrict__ g8,
     const float* __restrict__ sg, const float* __restrict__ lz, int nt, int group, int ng, int nb, int nb_pad,
@@ -1426,7 +1440,8 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
     const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
     const int gi = (int)(blk % (uint32_t)ng), h = (int)(blk / (uint32_t)ng);
     const int64_t gs = (int64_t)h * ng + gi;
-    const int ts = TILE / stride;
+    constexpr int TR = 16 * NRB;              // rows per tile
+    const int ts = TR / stride;
     struct SelOps {
         i32x4 a[2];
         f32x4 sg, lz;
@@ -1438,15 +1453,15 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
         o.sg = *(const f32x4*)(sg + s0 + 4 * grp);
         o.lz = *(const f32x4*)(lz + s0 + 4 * grp);
     };
-    i32x4 b[4][2];
-    bool val[4];
-    float srow[4];
-    float rmax[4];                            // row max of the far scores
+    i32x4 b[NRB][2];
+    bool val[NRB];
+    float srow[NRB];
+    float rmax[NRB];                          // row max of the far scores
     bool first = true;                        // first tile of the group: set the keys, later: max
     auto sel_block = [&](const SelOps& o, int c) {
-        i32x4 acc[4];
+        i32x4 acc[NRB];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int rb = 0; rb < NRB; ++rb) {
             acc[rb] = mfma_i8(o.a[0], b[rb][0], i32x4{0, 0, 0, 0});
             acc[rb] = mfma_i8(o.a[1], b[rb][1], acc[rb]);
         }
@@ -1456,7 +1471,7 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
             const bool lv = c + 4 * grp + i < nb;
             best[i] = -INFINITY;
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < NRB; ++rb) {
                 const float x = __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], o.sg[i]));
                 best[i] = fmaxf(best[i], val[rb] ? x : -INFINITY);
                 rmax[rb] = fmaxf(rmax[rb], lv ? __fadd_rn(x, o.lz[i]) : -INFINITY);
@@ -1478,10 +1493,10 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
         const int t = gi * group + j;
         if (t >= nt) break;                   // padded tiles repeat the last one
         const int64_t th = (int64_t)h * nt + t;
-        load_rows_i8(dq8, th * TILE, stride, ts, col, grp, b, val);
+        load_rows_i8(dq8, th * TR, stride, ts, col, grp, b, val);
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            srow[rb] = sdq[th * TILE + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
+        for (int rb = 0; rb < NRB; ++rb) {
+            srow[rb] = sdq[th * TR + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
             rmax[rb] = -INFINITY;
         }
         // wave w: 16-leaf groups c = 16 w + 64 j, each loaded one group ahead
@@ -1496,7 +1511,7 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
             sel_block(sb, c1);
         }
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {      // row r = stride * (16 rb + col) of the sampled rows
+        for (int rb = 0; rb < NRB; ++rb) {    // row r = stride * (16 rb + col) of the sampled rows
             const float mx = grp_max(rmax[rb]);
             if (grp == 0) red_m[w][16 * rb + col] = mx;
         }
@@ -1505,7 +1520,7 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
             const int r = lane;
             float m = r < ts ? fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r])) : -INFINITY;
             if (stride != 1) m = wave_max(m); // sampled rows: one reference for the whole tile
-            rowmax[th * TILE + r] = m;
+            if (r < TR) rowmax[th * TR + r] = m;
         }
         if (MULTI) __syncthreads();           // red_m is free for the next tile
         first = false;
@@ -1514,7 +1529,7 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
     if (kxe > 0) topk_row(keys, nb, kxe, sm, idx + gs * kxe, nullptr, nullptr);
 }
 
-template <int LEAF>
+template <int LEAF, int RB>    // RB = tile / 32: 16-row blocks per wave (tiles of 64 or 32 rows)
 __global__ __launch_bounds__(512) void route_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ sq, const int8_t* __restrict__ dq8,
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
@@ -1527,6 +1542,7 @@ __global__ __launch_bounds__(512) void route_kernel(
     __shared__ uint32_t exbits[MAX_NB_LDS / 32 + 1];
     __shared__ float red_m[64], red_l[4][64];
     __shared__ int redo;
+    constexpr int TR = 32 * RB;                                // rows per tile
     float* mrg = (float*)&ring[0][0][0];                       // merge staging: 4 x 64 x MRG_STRIDE floats
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar bookkeeping
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
@@ -1538,7 +1554,7 @@ __global__ __launch_bounds__(512) void route_kernel(
     const int64_t th = (int64_t)h * nt + t;
     const int64_t gs = (int64_t)h * ng + t / group;            // state / routing row: the tile's group
     const int64_t kh = (int64_t)h * nk;
-    const int64_t row0 = th * TILE + 32 * hr + col;            // this lane's rows: row0, row0 + 16
+    const int64_t row0 = th * TR + 16 * RB * hr + col;         // this lane's rows: row0 (+ 16 when RB = 2)
     // ---- routing of this tile (route_select_kernel)
     // exclusion bits: the selected (near) leaves, and every leaf >= nb, so the far loop needs no
     // range test (far blocks are 32-leaf aligned and a pair's range ends on a 32-leaf boundary
@@ -1548,9 +1564,9 @@ __global__ __launch_bounds__(512) void route_kernel(
         exbits[i] = past >= 32 ? 0u : (past <= 0 ? ~0u : ~0u << past);
     }
     for (int j = threadIdx.x; j < kxe; j += 512) sidx[j] = idx[gs * kxe + j];
-    float mref[2];
+    float mref[RB];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) {
         const float m = rowmax[row0 + 16 * rb];
         mref[rb] = m == -INFINITY ? 0.0f : __fmul_rn(m, LOG2E);
     }
@@ -1593,21 +1609,21 @@ __global__ __launch_bounds__(512) void route_kernel(
             dma_rows27(XV + r0 * D, XV + r1 * D, bo, slot);
         }
     };
-    Rows2 st;
+    RowsN<RB> st;
 #pragma unroll 1
     for (int pass = 0; pass < MAX_PASSES; ++pass) {
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
+        for (int rb = 0; rb < RB; ++rb) {
             st.m[rb] = mref[rb];
             st.l[rb] = 0.0f;
 #pragma unroll
             for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
         {   // ---- far field: S^T = g8 dq8^T, score = dot * sdq * sg + lz, excluded leaves masked
-            i32x4 bq[2][2];
-            float srow[2];
+            i32x4 bq[RB][2];
+            float srow[RB];
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 const int64_t p = row0 + 16 * rb;
                 bq[rb][0] = *(const i32x4*)(dq8 + p * D + 16 * grp);
                 bq[rb][1] = *(const i32x4*)(dq8 + p * D + 64 + 16 * grp);
@@ -1632,14 +1648,14 @@ __global__ __launch_bounds__(512) void route_kernel(
                 const char* slot = pring + S * SLOT_BYTES;
                 const int c0 = lo + 32 * bi;
                 const uint32_t exw = exbits[c0 >> 5] >> (4 * grp);       // bit 16 hh + i: this lane's key
-                float sc[2][8];
+                float sc[RB][8];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
                     const i32x4 A0 = *(const i32x4*)(slot + ((hh * 2 + 0) * 64 + lane) * 16);
                     const i32x4 A1 = *(const i32x4*)(slot + ((hh * 2 + 1) * 64 + lane) * 16);
-                    i32x4 acc[2];
+                    i32x4 acc[RB];
 #pragma unroll
-                    for (int rb = 0; rb < 2; ++rb) {
+                    for (int rb = 0; rb < RB; ++rb) {
                         acc[rb] = mfma_i8(A0, bq[rb][0], i32x4{0, 0, 0, 0});
                         acc[rb] = mfma_i8(A1, bq[rb][1], acc[rb]);
                     }
@@ -1650,7 +1666,7 @@ __global__ __launch_bounds__(512) void route_kernel(
                         const bool ok = ((exw >> (16 * hh + i)) & 1u) == 0u;
                         const float bias = ok ? __fmul_rn(lzv[i], LOG2E) : -INFINITY;
 #pragma unroll
-                        for (int rb = 0; rb < 2; ++rb)
+                        for (int rb = 0; rb < RB; ++rb)
                             sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i]), bias);
                     }
                 }
@@ -1659,7 +1675,7 @@ __global__ __launch_bounds__(512) void route_kernel(
                 for (int db = 0; db < 8; ++db)
 #pragma unroll
                     for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
-                rows2_update(st, sc, pvop);
+                rows_update<RB>(st, sc, pvop);
             };
             issue(0, 0);
             issue(1, 1);
@@ -1671,10 +1687,10 @@ __global__ __launch_bounds__(512) void route_kernel(
             }
         }
         {   // ---- near field: S^T = k8 q8^T, score = dot * sq * ks * scale
-            i32x4 bq[2][2];
-            float srow[2];
+            i32x4 bq[RB][2];
+            float srow[RB];
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 const int64_t p = row0 + 16 * rb;
                 bq[rb][0] = *(const i32x4*)(q8 + p * D + 16 * grp);
                 bq[rb][1] = *(const i32x4*)(q8 + p * D + 64 + 16 * grp);
@@ -1700,14 +1716,14 @@ __global__ __launch_bounds__(512) void route_kernel(
                 if (bi >= nn) return;
                 const char* slot = pring + S * SLOT_BYTES;
                 const int e0 = e_lo + 32 * bi;
-                float sc[2][8];
+                float sc[RB][8];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
                     const i32x4 A0 = *(const i32x4*)(slot + ((hh * 2 + 0) * 64 + lane) * 16);
                     const i32x4 A1 = *(const i32x4*)(slot + ((hh * 2 + 1) * 64 + lane) * 16);
-                    i32x4 acc[2];
+                    i32x4 acc[RB];
 #pragma unroll
-                    for (int rb = 0; rb < 2; ++rb) {
+                    for (int rb = 0; rb < RB; ++rb) {
                         acc[rb] = mfma_i8(A0, bq[rb][0], i32x4{0, 0, 0, 0});
                         acc[rb] = mfma_i8(A1, bq[rb][1], acc[rb]);
                     }
@@ -1717,13 +1733,13 @@ __global__ __launch_bounds__(512) void route_kernel(
                     for (int i = 0; i < 4; ++i) {
                         if constexpr (LEAF % 32 == 0) {   // the near list is whole 32-token blocks
 #pragma unroll
-                            for (int rb = 0; rb < 2; ++rb)
+                            for (int rb = 0; rb < RB; ++rb)
                                 sc[rb][4 * hh + i] = __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]));
                         } else {                          // leaf 16: the last block may be half empty
                             const bool ok = (e0 + 16 * hh + 4 * grp + i) < e_hi;
                             const float bias = ok ? 0.0f : -INFINITY;
 #pragma unroll
-                            for (int rb = 0; rb < 2; ++rb)
+                            for (int rb = 0; rb < RB; ++rb)
                                 sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]), bias);
                         }
                     }
@@ -1733,7 +1749,7 @@ __global__ __launch_bounds__(512) void route_kernel(
                 for (int db = 0; db < 8; ++db)
 #pragma unroll
                     for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
-                rows2_update(st, sc, pvop);
+                rows_update<RB>(st, sc, pvop);
             };
             issue(0, 0);
             issue(1, 1);
@@ -1749,16 +1765,16 @@ __global__ __launch_bounds__(512) void route_kernel(
         // (never observed on real scores): every p <= total, so the pass is redone with the
         // reference moved to m + log2(total).
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
+        for (int rb = 0; rb < RB; ++rb) {
             const float lt = grp_sum(st.l[rb]);
-            if (grp == 0) red_l[pr][32 * hr + 16 * rb + col] = lt;
+            if (grp == 0) red_l[pr][16 * RB * hr + 16 * rb + col] = lt;
         }
         if (threadIdx.x == 0) redo = 0;
         __syncthreads();
         bool bad = false;
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            const int r = 32 * hr + 16 * rb + col;
+        for (int rb = 0; rb < RB; ++rb) {
+            const int r = 16 * RB * hr + 16 * rb + col;
             const float tot = __fadd_rn(__fadd_rn(red_l[0][r], red_l[1][r]), __fadd_rn(red_l[2][r], red_l[3][r]));
             if (!(tot >= 0x1p-60f && tot <= 0x1p64f)) {
                 bad = true;
@@ -1773,24 +1789,25 @@ __global__ __launch_bounds__(512) void route_kernel(
     // ---- merge: every pair used the same reference per row, so the partial sums simply add
     // (h3/htrc_flat_triton.py:263-273 with equal maxima)
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        const int r = 32 * hr + 16 * rb + col;
+    for (int rb = 0; rb < RB; ++rb) {
+        const int r = 16 * RB * hr + 16 * rb + col;
         if (pr == 0 && grp == 0) red_m[r] = st.m[rb];
         float* dst = mrg + (pr * 64 + r) * MRG_STRIDE + 4 * grp;
 #pragma unroll
         for (int db = 0; db < 8; ++db) *(f32x4*)(dst + 16 * db) = st.o[rb][db];
     }
     __syncthreads();
-    const int r_out = threadIdx.x >> 3, part = threadIdx.x & 7;    // row, 16-dim eighth
+    constexpr int TPR = 512 / TR, DPT = D / TPR;                   // threads per row, dims per thread
+    const int r_out = threadIdx.x / TPR, part = threadIdx.x % TPR;
     const float den =
         __fadd_rn(__fadd_rn(red_l[0][r_out], red_l[1][r_out]), __fadd_rn(red_l[2][r_out], red_l[3][r_out]));
     const float inv = 1.0f / (den < 1e-30f ? 1e-30f : den);
-    const int64_t qi = (int64_t)t * TILE + r_out;
+    const int64_t qi = (int64_t)t * TR + r_out;
     if (qi < nq) {
         const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int dl = 16 * part + 4 * u;
+        for (int u = 0; u < DPT / 4; ++u) {
+            const int dl = DPT * part + 4 * u;
             f32x4 acc = *(const f32x4*)(mrg + r_out * MRG_STRIDE + dl);
 #pragma unroll
             for (int s = 1; s < 4; ++s) {
@@ -2134,32 +2151,34 @@ const char* htrc_last_error(void) { return g_err; }
 
 int htrc_nb_pad(int64_t nb) { return (int)((nb + 31) / 32 * 32); }
 
-int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, const int32_t* perm,
-                float* mu, int8_t* q8, float* sq, int8_t* dq8, float* sdq, void* stream) {
+int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int tile, int group,
+                const int32_t* perm, float* mu, int8_t* q8, float* sq, int8_t* dq8, float* sdq, void* stream) {
     REQUIRE(q && mu && q8 && sq && dq8 && sdq, "htrc_pack_q: null pointer");
     REQUIRE(d == D, "htrc_pack_q: head dim must be 128");
+    REQUIRE(tile == 32 || tile == 64, "htrc_pack_q: tile must be 32 or 64 rows");
     REQUIRE(heads > 0 && heads <= 65535 && nq > 0, "htrc_pack_q: bad heads / rows");
     REQUIRE(group >= 1 && group <= 1024, "htrc_pack_q: group must be in [1, 1024]");
     REQUIRE(aligned(q, 16) && aligned(q8, 16) && aligned(dq8, 16), "htrc_pack_q: q and the int8 outputs must be 16-byte aligned");
-    const int64_t nt = (nq + TILE - 1) / TILE;
+    const int64_t nt = (nq + tile - 1) / tile;
     REQUIRE(nt <= 0x7fffffff, "htrc_pack_q: too many tiles");
     const int64_t ng = (nt + group - 1) / group;
     hipStream_t s = (hipStream_t)stream;
     if (group > 1) {
         const dim3 gg((unsigned)ng, (unsigned)heads);
         if (q_is_bf16)
-            hipLaunchKernelGGL(group_centres_kernel<true>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, perm, mu);
+            hipLaunchKernelGGL(group_centres_kernel<true>, gg, dim3(D), 0, s, q, nq, (int)nt, tile, group, (int)ng,
+                               perm, mu);
         else
-            hipLaunchKernelGGL(group_centres_kernel<false>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, perm,
-                               mu);
+            hipLaunchKernelGGL(group_centres_kernel<false>, gg, dim3(D), 0, s, q, nq, (int)nt, tile, group, (int)ng,
+                               perm, mu);
     }
     dim3 grid((unsigned)nt, (unsigned)heads);
     if (q_is_bf16)
-        hipLaunchKernelGGL(pack_q_kernel<true>, grid, dim3(256), 0, s, q, nq, (int)nt, group, (int)ng, perm, mu, q8,
-                           sq, dq8, sdq);
+        hipLaunchKernelGGL(pack_q_kernel<true>, grid, dim3(256), 0, s, q, nq, (int)nt, tile, group, (int)ng, perm, mu,
+                           q8, sq, dq8, sdq);
     else
-        hipLaunchKernelGGL(pack_q_kernel<false>, grid, dim3(256), 0, s, q, nq, (int)nt, group, (int)ng, perm, mu, q8,
-                           sq, dq8, sdq);
+        hipLaunchKernelGGL(pack_q_kernel<false>, grid, dim3(256), 0, s, q, nq, (int)nt, tile, group, (int)ng, perm, mu,
+                           q8, sq, dq8, sdq);
     return launched("htrc_pack_q");
 }
 
@@ -2269,17 +2288,23 @@ int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, 
 }
 
 int htrc_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
-                int64_t heads, int64_t nt, int64_t nb, int stride, int group, int d, float* sel, void* stream) {
+                int64_t heads, int64_t nt, int64_t nb, int stride, int tile, int group, int d, float* sel,
+                void* stream) {
     REQUIRE(dq8 && sdq && g8 && sg && lz && sel, "htrc_select: null pointer");
     REQUIRE(d == D, "htrc_select: head dim must be 128");
-    REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_select: stride must divide 64");
+    REQUIRE(tile == 32 || tile == 64, "htrc_select: tile must be 32 or 64 rows");
+    REQUIRE(stride >= 1 && stride <= tile && tile % stride == 0, "htrc_select: stride must divide the tile");
     REQUIRE(group >= 1 && group <= 1024, "htrc_select: group must be in [1, 1024]");
     REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff && nb > 0, "htrc_select: bad sizes");
     const int nbp = htrc_nb_pad(nb);
     const int64_t ng = (nt + group - 1) / group;
     dim3 grid((unsigned)ng, (unsigned)((nb + 255) / 256), (unsigned)heads);
-    hipLaunchKernelGGL(select_kernel, grid, dim3(256), 0, (hipStream_t)stream, dq8, sdq, stride, g8, sg, lz,
-                       (int)nt, group, (int)ng, (int)nb, nbp, sel);
+    if (tile == 64)
+        hipLaunchKernelGGL(select_kernel<4>, grid, dim3(256), 0, (hipStream_t)stream, dq8, sdq, stride, g8, sg, lz,
+                           (int)nt, group, (int)ng, (int)nb, nbp, sel);
+    else
+        hipLaunchKernelGGL(select_kernel<2>, grid, dim3(256), 0, (hipStream_t)stream, dq8, sdq, stride, g8, sg, lz,
+                           (int)nt, group, (int)ng, (int)nb, nbp, sel);
     return launched("htrc_select");
 }
 
@@ -2302,14 +2327,15 @@ static int64_t split_len(int64_t n, int64_t ns, int64_t bn) {   // _split, h3/ht
 int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
               const float* sg, const float* lz, const uint16_t* vb, const int8_t* excl, const int32_t* idx,
               const int8_t* k8, const float* ks, const uint16_t* v, int64_t heads, int64_t nq, int64_t nk,
-              int leaf, int d, int kx, int group, const int32_t* perm, int splits, int bn, float scale, float* pm,
-              float* pl, float* pacc, float* out, float* logz, void* stream) {
+              int leaf, int d, int kx, int tile, int group, const int32_t* perm, int splits, int bn, float scale,
+              float* pm, float* pl, float* pacc, float* out, float* logz, void* stream) {
     REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && excl && k8 && ks && v,
             "htrc_tile: null input pointer");
     REQUIRE(d == D, "htrc_tile: head dim must be 128");
+    REQUIRE(tile == 32 || tile == 64, "htrc_tile: tile must be 32 or 64 rows");
     REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_tile: leaf must be 16/32/64/128");
     REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_tile: bad sizes");
-    const int64_t nb = nk / leaf, nt = (nq + TILE - 1) / TILE;
+    const int64_t nb = nk / leaf, nt = (nq + tile - 1) / tile;
     REQUIRE(kx >= 0 && kx <= nb && (kx == 0 || idx), "htrc_tile: need 0 <= kx <= leaves and idx when kx > 0");
     REQUIRE(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0, "htrc_tile: need 1 <= splits <= 64 and a block that is a multiple of 32");
     REQUIRE(splits == 1 ? (out && logz) : (pm && pl && pacc), "htrc_tile: missing outputs");
@@ -2323,9 +2349,9 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
     float* ppa = splits == 1 ? nullptr : pacc;
 #define TILE_CASE(L)                                                                                            \
     case L:                                                                                                     \
-        hipLaunchKernelGGL(tile_kernel<L>, grid, dim3(256), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, excl, idx, k8, \
-                           ks, v, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps,   \
-                           scale, ppm, ppl, ppa, out, logz);                                                    \
+        hipLaunchKernelGGL(tile_kernel<L>, grid, dim3(4 * tile), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, excl, idx, \
+                           k8, ks, v, nq, (int)nt, tile, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, \
+                           eps, scale, ppm, ppl, ppa, out, logz);                                               \
         break;
     switch (leaf) {
         TILE_CASE(16)
@@ -2337,31 +2363,33 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
     return launched("htrc_tile");
 }
 
-int htrc_pack_q16(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, const int32_t* perm,
-                  int dq_fp16, float* mu, uint16_t* q16, uint16_t* dq16, void* stream) {
+int htrc_pack_q16(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int tile, int group,
+                  const int32_t* perm, int dq_fp16, float* mu, uint16_t* q16, uint16_t* dq16, void* stream) {
     REQUIRE(q && mu && q16 && dq16, "htrc_pack_q16: null pointer");
     REQUIRE(d == D, "htrc_pack_q16: head dim must be 128");
+    REQUIRE(tile == 32 || tile == 64, "htrc_pack_q16: tile must be 32 or 64 rows");
     REQUIRE(heads > 0 && heads <= 65535 && nq > 0, "htrc_pack_q16: bad heads / rows");
     REQUIRE(group >= 1 && group <= 1024, "htrc_pack_q16: group must be in [1, 1024]");
     REQUIRE(aligned(q, 16) && aligned(q16, 16) && aligned(dq16, 16), "htrc_pack_q16: misaligned buffer");
-    const int64_t nt = (nq + TILE - 1) / TILE;
+    const int64_t nt = (nq + tile - 1) / tile;
     REQUIRE(nt <= 0x7fffffff, "htrc_pack_q16: too many tiles");
     const int64_t ng = (nt + group - 1) / group;
     hipStream_t s = (hipStream_t)stream;
     if (group > 1) {
         const dim3 gg((unsigned)ng, (unsigned)heads);
         if (q_is_bf16)
-            hipLaunchKernelGGL(group_centres_kernel<true>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, perm, mu);
+            hipLaunchKernelGGL(group_centres_kernel<true>, gg, dim3(D), 0, s, q, nq, (int)nt, tile, group, (int)ng,
+                               perm, mu);
         else
-            hipLaunchKernelGGL(group_centres_kernel<false>, gg, dim3(D), 0, s, q, nq, (int)nt, group, (int)ng, perm,
-                               mu);
+            hipLaunchKernelGGL(group_centres_kernel<false>, gg, dim3(D), 0, s, q, nq, (int)nt, tile, group, (int)ng,
+                               perm, mu);
     }
     dim3 grid((unsigned)nt, (unsigned)heads);
     int8_t* a = (int8_t*)q16;
     int8_t* b = (int8_t*)dq16;
 #define PACK16(BF, QM)                                                                                          \
-    hipLaunchKernelGGL((pack_q_kernel<BF, QM>), grid, dim3(256), 0, s, q, nq, (int)nt, group, (int)ng, perm, mu, a, \
-                       nullptr, b, nullptr)
+    hipLaunchKernelGGL((pack_q_kernel<BF, QM>), grid, dim3(256), 0, s, q, nq, (int)nt, tile, group, (int)ng, perm, \
+                       mu, a, nullptr, b, nullptr)
     if (q_is_bf16) {
         if (dq_fp16) PACK16(true, 2); else PACK16(true, 1);
     } else {
@@ -2372,47 +2400,58 @@ int htrc_pack_q16(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d
 }
 
 int htrc_select_fp8(const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz, int64_t heads, int64_t nt,
-                    int64_t nb, int stride, int group, int d, float* sel, void* stream) {
+                    int64_t nb, int stride, int tile, int group, int d, float* sel, void* stream) {
     REQUIRE(dq16 && g && sg && lz && sel, "htrc_select_fp8: null pointer");
     REQUIRE(d == D, "htrc_select_fp8: head dim must be 128");
-    REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_select_fp8: stride must divide 64");
+    REQUIRE(tile == 32 || tile == 64, "htrc_select_fp8: tile must be 32 or 64 rows");
+    REQUIRE(stride >= 1 && stride <= tile && tile % stride == 0, "htrc_select_fp8: stride must divide the tile");
     REQUIRE(group >= 1 && group <= 1024, "htrc_select_fp8: group must be in [1, 1024]");
     REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff && nb > 0, "htrc_select_fp8: bad sizes");
     REQUIRE(aligned(dq16, 16) && aligned(g, 16) && aligned(sg, 16) && aligned(lz, 16), "htrc_select_fp8: misaligned buffer");
     const int nbp = htrc_nb_pad(nb);
     const int64_t ng = (nt + group - 1) / group;
     dim3 grid((unsigned)ng, (unsigned)((nb + 255) / 256), (unsigned)heads);
-    hipLaunchKernelGGL(select16_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, sg, lz, (int)nt,
-                       group, (int)ng, (int)nb, nbp, sel);
+    if (tile == 64)
+        hipLaunchKernelGGL((select16_kernel<true, 4>), grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, sg, lz,
+                           (int)nt, group, (int)ng, (int)nb, nbp, sel);
+    else
+        hipLaunchKernelGGL((select16_kernel<true, 2>), grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, sg, lz,
+                           (int)nt, group, (int)ng, (int)nb, nbp, sel);
     return launched("htrc_select_fp8");
 }
 
 int htrc_select_bf16(const uint16_t* dq16, const uint16_t* g, const float* lz, int64_t heads, int64_t nt, int64_t nb,
-                     int stride, int group, int d, float* sel, void* stream) {
+                     int stride, int tile, int group, int d, float* sel, void* stream) {
     REQUIRE(dq16 && g && lz && sel, "htrc_select_bf16: null pointer");
     REQUIRE(d == D, "htrc_select_bf16: head dim must be 128");
-    REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_select_bf16: stride must divide 64");
+    REQUIRE(tile == 32 || tile == 64, "htrc_select_bf16: tile must be 32 or 64 rows");
+    REQUIRE(stride >= 1 && stride <= tile && tile % stride == 0, "htrc_select_bf16: stride must divide the tile");
     REQUIRE(group >= 1 && group <= 1024, "htrc_select_bf16: group must be in [1, 1024]");
     REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff && nb > 0, "htrc_select_bf16: bad sizes");
     REQUIRE(aligned(dq16, 16) && aligned(g, 16) && aligned(lz, 16), "htrc_select_bf16: misaligned buffer");
     const int nbp = htrc_nb_pad(nb);
     const int64_t ng = (nt + group - 1) / group;
     dim3 grid((unsigned)ng, (unsigned)((nb + 255) / 256), (unsigned)heads);
-    hipLaunchKernelGGL(select16_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, nullptr, lz,
-                       (int)nt, group, (int)ng, (int)nb, nbp, sel);
+    if (tile == 64)
+        hipLaunchKernelGGL((select16_kernel<false, 4>), grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, nullptr,
+                           lz, (int)nt, group, (int)ng, (int)nb, nbp, sel);
+    else
+        hipLaunchKernelGGL((select16_kernel<false, 2>), grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, nullptr,
+                           lz, (int)nt, group, (int)ng, (int)nb, nbp, sel);
     return launched("htrc_select_bf16");
 }
 
 int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz,
                   const uint8_t* vb, const float* sv, const int8_t* excl, const int32_t* idx, const uint16_t* k,
-                  const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int group,
-                  const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out,
-                  float* logz, void* stream) {
+                  const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int tile,
+                  int group, const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
+                  float* out, float* logz, void* stream) {
     REQUIRE(q16 && dq16 && g && sg && lz && vb && sv && excl && k && v, "htrc_tile_fp8: null input pointer");
     REQUIRE(d == D, "htrc_tile_fp8: head dim must be 128");
+    REQUIRE(tile == 32 || tile == 64, "htrc_tile_fp8: tile must be 32 or 64 rows");
     REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_tile_fp8: leaf must be 16/32/64/128");
     REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_tile_fp8: bad sizes");
-    const int64_t nb = nk / leaf, nt = (nq + TILE - 1) / TILE;
+    const int64_t nb = nk / leaf, nt = (nq + tile - 1) / tile;
     REQUIRE(kx >= 0 && kx <= nb && (kx == 0 || idx), "htrc_tile_fp8: need 0 <= kx <= leaves and idx when kx > 0");
     REQUIRE(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0, "htrc_tile_fp8: need 1 <= splits <= 64 and a block that is a multiple of 32");
     REQUIRE(splits == 1 ? (out && logz) : (pm && pl && pacc), "htrc_tile_fp8: missing outputs");
@@ -2429,9 +2468,9 @@ int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, c
     float* ppa = splits == 1 ? nullptr : pacc;
 #define TILE8_CASE(L)                                                                                              \
     case L:                                                                                                        \
-        hipLaunchKernelGGL((tile16_kernel<L, true>), grid, dim3(256), 0, s, q16, dq16, g, sg, lz, vb, sv, excl, idx, k, v, nq, \
-                           (int)nt, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps, scale, ppm, ppl,   \
-                           ppa, out, logz);                                                                        \
+        hipLaunchKernelGGL((tile16_kernel<L, true>), grid, dim3(4 * tile), 0, s, q16, dq16, g, sg, lz, vb, sv, excl, idx, \
+                           k, v, nq, (int)nt, tile, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps,   \
+                           scale, ppm, ppl, ppa, out, logz);                                                       \
         break;
     switch (leaf) {
         TILE8_CASE(16)
@@ -2445,13 +2484,15 @@ int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, c
 
 int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g, const float* lz, const uint16_t* vb,
                    const int8_t* excl, const int32_t* idx, const uint16_t* k, const uint16_t* v, int64_t heads,
-                   int64_t nq, int64_t nk, int leaf, int d, int kx, int group, const int32_t* perm, int splits, int bn,
-                   float scale, float* pm, float* pl, float* pacc, float* out, float* logz, void* stream) {
+                   int64_t nq, int64_t nk, int leaf, int d, int kx, int tile, int group, const int32_t* perm,
+                   int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out, float* logz,
+                   void* stream) {
     REQUIRE(q16 && dq16 && g && lz && vb && excl && k && v, "htrc_tile_bf16: null input pointer");
     REQUIRE(d == D, "htrc_tile_bf16: head dim must be 128");
+    REQUIRE(tile == 32 || tile == 64, "htrc_tile_bf16: tile must be 32 or 64 rows");
     REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_tile_bf16: leaf must be 16/32/64/128");
     REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_tile_bf16: bad sizes");
-    const int64_t nb = nk / leaf, nt = (nq + TILE - 1) / TILE;
+    const int64_t nb = nk / leaf, nt = (nq + tile - 1) / tile;
     REQUIRE(kx >= 0 && kx <= nb && (kx == 0 || idx), "htrc_tile_bf16: need 0 <= kx <= leaves and idx when kx > 0");
     REQUIRE(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0, "htrc_tile_bf16: need 1 <= splits <= 64 and a block that is a multiple of 32");
     REQUIRE(splits == 1 ? (out && logz) : (pm && pl && pacc), "htrc_tile_bf16: missing outputs");
@@ -2467,9 +2508,9 @@ int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g,
     float* ppa = splits == 1 ? nullptr : pacc;
 #define TILEB_CASE(L)                                                                                              \
     case L:                                                                                                        \
-        hipLaunchKernelGGL((tile16_kernel<L, false>), grid, dim3(256), 0, s, q16, dq16, g, nullptr, lz, vb, nullptr, excl, \
-                           idx, k, v, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps,  \
-                           scale, ppm, ppl, ppa, out, logz);                                                       \
+        hipLaunchKernelGGL((tile16_kernel<L, false>), grid, dim3(4 * tile), 0, s, q16, dq16, g, nullptr, lz, vb, nullptr, \
+                           excl, idx, k, v, nq, (int)nt, tile, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx,  \
+                           lps, eps, scale, ppm, ppl, ppa, out, logz);                                             \
         break;
     switch (leaf) {
         TILEB_CASE(16)
@@ -2481,19 +2522,21 @@ int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g,
     return launched("htrc_tile_bf16");
 }
 
-int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int splits,
+int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int tile, int splits,
                int d, const int32_t* perm, float* out, float* logz, void* stream) {
     REQUIRE(pm && pl && pacc && out && logz, "htrc_merge: null pointer");
+    REQUIRE(tile == 32 || tile == 64, "htrc_merge: tile must be 32 or 64 rows");
     REQUIRE(d == D && splits >= 1 && heads > 0 && heads <= 65535 && nq > 0, "htrc_merge: bad sizes");
-    const int64_t nt = (nq + TILE - 1) / TILE;
-    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)nt, (unsigned)heads), dim3(256), 0, (hipStream_t)stream, pm,
-                       pl, pacc, splits, nq, (int)nt, perm, out, logz);
+    const int64_t nt = (nq + tile - 1) / tile;
+    REQUIRE(nt <= 0x7fffffff, "htrc_merge: too many tiles");
+    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)nt, (unsigned)heads), dim3(4 * tile), 0, (hipStream_t)stream, pm,
+                       pl, pacc, splits, nq, (int)nt, tile, perm, out, logz);
     return launched("htrc_merge");
 }
 
 // Shape checks shared by the route entry points; sets nb, nt, ng (tile groups), kxe.
-static int route_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int group,
-                        int64_t& nb, int64_t& nt, int64_t& ng, int& kxe) {
+static int route_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int tile,
+                        int group, int64_t& nb, int64_t& nt, int64_t& ng, int& kxe) {
     static thread_local char msg[160];
     auto bad = [&](const char* what) {
         snprintf(msg, sizeof msg, "%s: %s", who, what);
@@ -2501,9 +2544,10 @@ static int route_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, 
     };
     if (d != D) return bad("head dim must be 128");
     if (!(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128)) return bad("leaf must be 16/32/64/128");
+    if (!(tile == 32 || tile == 64)) return bad("tile must be 32 or 64 rows");
     if (!(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535)) return bad("bad sizes");
     nb = nk / leaf;
-    nt = (nq + TILE - 1) / TILE;
+    nt = (nq + tile - 1) / tile;
     if (nb > MAX_NB_LDS) return bad("at most 8192 leaves per head");
     if (kx < 0) return bad("need kx >= 0");
     if (group < 1 || group > 1024) return bad("group must be in [1, 1024]");
@@ -2516,33 +2560,35 @@ static int route_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, 
 
 int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
                       int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink, int stride,
-                      int group, int32_t* idx, float* rowmax, void* stream) {
+                      int tile, int group, int32_t* idx, float* rowmax, void* stream) {
     REQUIRE(dq8 && sdq && g8 && sg && lz && rowmax, "htrc_route_select: null pointer");
     REQUIRE(aligned(g8, 16) && aligned(sg, 16) && aligned(lz, 16), "htrc_route_select: misaligned buffer");
     int64_t nb, nt, ng;
     int kxe;
-    const int rc = route_shapes("htrc_route_select", heads, nq, nk, leaf, d, kx, group, nb, nt, ng, kxe);
+    const int rc = route_shapes("htrc_route_select", heads, nq, nk, leaf, d, kx, tile, group, nb, nt, ng, kxe);
     if (rc != HTRC_OK) return rc;
     REQUIRE(sink >= 0, "htrc_route_select: need sink >= 0");
     REQUIRE(kxe == 0 || idx, "htrc_route_select: idx is required when kx > 0");
-    REQUIRE(stride >= 1 && stride <= TILE && TILE % stride == 0, "htrc_route_select: stride must divide 64");
+    REQUIRE(stride >= 1 && stride <= tile && tile % stride == 0, "htrc_route_select: stride must divide the tile");
     const int nbp = htrc_nb_pad(nb);
-    if (group == 1)
-        hipLaunchKernelGGL(route_select_kernel<false>, dim3((unsigned)(ng * heads)), dim3(256), (size_t)4 * nbp,
-                           (hipStream_t)stream, dq8, sdq, g8, sg, lz, (int)nt, group, (int)ng, (int)nb, nbp, kxe, sink,
-                           stride, idx, rowmax);
-    else
-        hipLaunchKernelGGL(route_select_kernel<true>, dim3((unsigned)(ng * heads)), dim3(256), (size_t)4 * nbp,
-                           (hipStream_t)stream, dq8, sdq, g8, sg, lz, (int)nt, group, (int)ng, (int)nb, nbp, kxe, sink,
-                           stride, idx, rowmax);
+#define RSEL(M, N)                                                                                              \
+    hipLaunchKernelGGL((route_select_kernel<M, N>), dim3((unsigned)(ng * heads)), dim3(256), (size_t)4 * nbp,    \
+                       (hipStream_t)stream, dq8, sdq, g8, sg, lz, (int)nt, group, (int)ng, (int)nb, nbp, kxe, sink, \
+                       stride, idx, rowmax)
+    if (tile == 64) {
+        if (group == 1) RSEL(false, 4); else RSEL(true, 4);
+    } else {
+        if (group == 1) RSEL(false, 2); else RSEL(true, 2);
+    }
+#undef RSEL
     return launched("htrc_route_select");
 }
 
 int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                       const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                       const uint16_t* v, const int32_t* idx, const float* rowmax, int64_t heads, int64_t nq,
-                      int64_t nk, int leaf, int d, int kx, int group, const int32_t* perm, float scale, float* out,
-                      float* logz, void* stream) {
+                      int64_t nk, int leaf, int d, int kx, int tile, int group, const int32_t* perm, float scale,
+                      float* out, float* logz, void* stream) {
     REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && k8 && ks && v && rowmax && out && logz,
             "htrc_route_attend: null pointer");
     REQUIRE(aligned(vb, 16) && aligned(v, 16) && aligned(g8, 16) && aligned(k8, 16) && aligned(sg, 16) &&
@@ -2550,7 +2596,7 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
             "htrc_route_attend: misaligned buffer");
     int64_t nb, nt, ng;
     int kxe;
-    const int rc = route_shapes("htrc_route_attend", heads, nq, nk, leaf, d, kx, group, nb, nt, ng, kxe);
+    const int rc = route_shapes("htrc_route_attend", heads, nq, nk, leaf, d, kx, tile, group, nb, nt, ng, kxe);
     if (rc != HTRC_OK) return rc;
     REQUIRE(kxe == 0 || idx, "htrc_route_attend: idx is required when kx > 0");
     const int nbp = htrc_nb_pad(nb);
@@ -2558,8 +2604,12 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
     hipStream_t s = (hipStream_t)stream;
 #define ROUTE_CASE(L)                                                                                          \
     case L:                                                                                                    \
-        hipLaunchKernelGGL(route_kernel<L>, grid, dim3(512), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, \
-                           rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp, kxe, scale, out, logz); \
+        if (tile == 64)                                                                                        \
+            hipLaunchKernelGGL((route_kernel<L, 2>), grid, dim3(512), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, \
+                               idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp, kxe, scale, out, logz); \
+        else                                                                                                   \
+            hipLaunchKernelGGL((route_kernel<L, 1>), grid, dim3(512), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, \
+                               idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp, kxe, scale, out, logz); \
         break;
     switch (leaf) {
         ROUTE_CASE(16)
@@ -2574,14 +2624,14 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
-               int stride, int group, const int32_t* perm, float scale, float* out, float* logz, int32_t* idx,
-               float* rowmax, void* stream) {
+               int stride, int tile, int group, const int32_t* perm, float scale, float* out, float* logz,
+               int32_t* idx, float* rowmax, void* stream) {
     REQUIRE(q8 && sq && vb && k8 && ks && v && out && logz, "htrc_route: null pointer");
-    int rc = htrc_route_select(dq8, sdq, g8, sg, lz, heads, nq, nk, leaf, d, kx, sink, stride, group, idx, rowmax,
-                               stream);
+    int rc = htrc_route_select(dq8, sdq, g8, sg, lz, heads, nq, nk, leaf, d, kx, sink, stride, tile, group, idx,
+                               rowmax, stream);
     if (rc != HTRC_OK) return rc;
     return htrc_route_attend(q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, rowmax, heads, nq, nk, leaf, d, kx,
-                             group, perm, scale, out, logz, stream);
+                             tile, group, perm, scale, out, logz, stream);
 }
 
 int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,

@@ -1,7 +1,7 @@
 """Flat (tree-free) HTRC attention operator on MI355X -- the drop-in for h3/htrc_flat.py.
 
 Same call surface as the reference (``flat_attention``, ``PROD``, ``flat_attention_prod``):
-queries are cut into 64-row tiles with centre mu_t; every (tile, leaf) gets the exact
+queries are cut into tiles of 64 (or 32) rows with centre mu_t; every (tile, leaf) gets the exact
 leaf cumulants at the centre (log-partition lz, tilted key mean g, value mean vb); each
 query sees far leaves through lz + (q - mu).g with value vb, and the ``exact_leaves``
 leaves of largest row-max far logit exactly; both merge in one online softmax.
@@ -77,8 +77,8 @@ def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot
             raise ValueError("tail keys / values must be [n, D] (or [H, n, D] with q [H, N, D])")
     if int(kern.get("group", 1)) > 1024:
         raise ValueError("kern['group'] must be at most 1024 tiles")
-    if int(tile) != hip.TILE:
-        raise ValueError("the HIP backend uses tile=64")
+    if int(tile) not in hip.TILES:
+        raise ValueError("the HIP backend uses tile=64 or tile=32")
     if leaf not in (16, 32, 64, 128):
         raise ValueError("leaf must be 16, 32, 64 or 128")
     if q.dim() not in (2, 3) or k.dim() != q.dim() or v.shape != k.shape:
@@ -122,17 +122,18 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     kx = min(int(exact_leaves) + sink, nb)
     if kx < 0:
         raise ValueError("exact_leaves must be >= 0")
+    tile = int(tile)
     stride = int(sel_stride)
-    if stride < 1 or hip.TILE % stride:
-        raise ValueError("sel_stride must divide 64")
+    if stride < 1 or tile % stride:
+        raise ValueError(f"sel_stride must divide the tile ({tile})")
     group = max(1, int(kern.get("group", 1)))           # G consecutive tiles share one centre
     if qh.dtype not in (torch.float32, torch.bfloat16):
         qh = qh.float()
     perm = hip.kmeans_order(qh, ws=ws) if order == "kmeans" else None   # query rows regrouped by k-means
     if store in ("fp8", "bf16"):
         return _flat16(store, qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, stride, group, perm, splits,
-                       kern, tail, ws, return_logz, state)
-    mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), ws=ws, group=group, perm=perm)
+                       kern, tail, ws, return_logz, state, tile)
+    mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm)
     kb = kh.to(torch.bfloat16).contiguous()
     vb = vh.to(torch.bfloat16).contiguous()
     k8, ks = hip.pack_k(kb, ws=ws)
@@ -147,12 +148,13 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         if state is not None and kx > 0:
             idx = hip._buf(ws, "idx", (h, ng, kx), torch.int32, qh.device)
         out, logz = hip.route(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, sink=sink, stride=stride,
-                              ws=ws, idx=idx, group=group, perm=perm)
+                              ws=ws, idx=idx, group=group, perm=perm, tile=tile)
         tick("tile")
     else:
         excl = None
         if kx > 0:
-            sel = hip.rowmax_select(g=g8, lz=lz, sg=sg, stride=stride, nb=nb, dq8=dq8, sdq=sdq, ws=ws, group=group)
+            sel = hip.rowmax_select(g=g8, lz=lz, sg=sg, stride=stride, nb=nb, dq8=dq8, sdq=sdq, ws=ws, group=group,
+                                    tile=tile)
             idx, excl = hip.topk_excl(sel, nb, kx, sink, ws=ws)
             if state is not None:
                 state["sel"] = sel
@@ -161,7 +163,7 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
             excl.zero_()
         tick("select")
         out, logz = hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
-                                       bn=int(kern.get("tile_bn", 32)), ws=ws, group=group, perm=perm)
+                                       bn=int(kern.get("tile_bn", 32)), ws=ws, group=group, perm=perm, tile=tile)
         tick("tile")
         if state is not None:
             state["excl"] = excl
@@ -169,7 +171,7 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         state.update(packed)
         state.update(lstate)
         state["idx"] = idx
-        state["nb"], state["kx"], state["group"], state["perm"] = nb, kx, group, perm
+        state["nb"], state["kx"], state["group"], state["perm"], state["tile"] = nb, kx, group, perm, tile
     if tail is not None and int(tail[0].shape[-2]) > 0:
         # keys past the last full leaf, exact for every query (h3/htrc_flat_triton.py:187-207, 381-388)
         tk, tv = (x.unsqueeze(0) if squeeze else x for x in tail)
@@ -182,14 +184,14 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
 
 
 def _flat16(store, qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, stride, group, perm, splits, kern, tail,
-            ws, return_logz, state):
+            ws, return_logz, state, tile):
     """store="fp8": e4m3 leaf state with row scales, fp16 far dots; store="bf16": bf16 leaf
     state and far dots; both with bf16 near dots, run as the reference's stage structure
     (select, top-k, split tile kernel, merge; h3/htrc_flat_triton.py:65-72, 82-83, 104-108,
     132-153, 165-184, 214-254)."""
     h = int(qh.shape[0])
     fp8 = store == "fp8"
-    mu, q16, dq16 = hip.pack_q16(qh.contiguous(), ws=ws, group=group, perm=perm, dq_fp16=fp8)
+    mu, q16, dq16 = hip.pack_q16(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm, dq_fp16=fp8)
     kb = kh.to(torch.bfloat16).contiguous()
     vb = vh.to(torch.bfloat16).contiguous()
     tick("prep")
@@ -199,7 +201,7 @@ def _flat16(store, qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, str
     ng = int(mu.shape[1])
     idx = None
     if kx > 0:
-        sel = hip.rowmax_select(g=g, lz=lz, sg=sg, stride=stride, nb=nb, dq8=dq16, ws=ws, group=group)
+        sel = hip.rowmax_select(g=g, lz=lz, sg=sg, stride=stride, nb=nb, dq8=dq16, ws=ws, group=group, tile=tile)
         idx, excl = hip.topk_excl(sel, nb, kx, sink, ws=ws)
         if state is not None:
             state["sel"] = sel
@@ -210,13 +212,13 @@ def _flat16(store, qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, str
     packed = {"q16": q16, "dq16": dq16, "k": kb, "v": vb, "mu": mu}
     lstate = {"g8": g, "sg": sg, "lz": lz, "vb": vbs, "sv": sv}
     out, logz = hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
-                                   bn=int(kern.get("tile_bn", 32)), ws=ws, group=group, perm=perm)
+                                   bn=int(kern.get("tile_bn", 32)), ws=ws, group=group, perm=perm, tile=tile)
     tick("tile")
     if state is not None:
         state.update(packed)
         state.update(lstate)
         state["idx"], state["excl"] = idx, excl
-        state["nb"], state["kx"], state["group"], state["perm"] = nb, kx, group, perm
+        state["nb"], state["kx"], state["group"], state["perm"], state["tile"] = nb, kx, group, perm, tile
     if tail is not None and int(tail[0].shape[-2]) > 0:
         tk, tv = (x.unsqueeze(0) if squeeze else x for x in tail)
         hip.tail_merge(qh, tk.to(qh.device), tv.to(qh.device), scale=scale, out=out, logz=logz)

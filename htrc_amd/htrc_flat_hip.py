@@ -23,7 +23,15 @@ from . import _lib
 from ._lib import call, ptr, stream_handle, nb_pad
 
 TILE = 64
+TILES = (64, 32)          # query rows per tile the kernels take (32: the runner's mode "max")
 D = 128
+
+
+def _tile(tile) -> int:
+    tile = int(tile)
+    if tile not in TILES:
+        raise ValueError("the HIP kernels use query tiles of 64 or 32 rows")
+    return tile
 
 
 def _split(n: int, ns: int, bn: int) -> int:
@@ -64,8 +72,7 @@ def pack_q(q: torch.Tensor, tile: int = TILE, ws=None, group: int = 1, perm=None
     centre of each tile over its real rows (h3/htrc_flat.py:142-156); group G: the centre of
     each G tiles over their padded rows (:223-229).  perm (int32 [H, nq], optional): row p of
     the packed operands is query perm[p] (order="kmeans", :148-149)."""
-    if tile != TILE:
-        raise ValueError("the HIP kernels use 64-row query tiles")
+    tile = _tile(tile)
     group = int(group)
     if group < 1:
         raise ValueError("group must be >= 1")
@@ -75,45 +82,44 @@ def pack_q(q: torch.Tensor, tile: int = TILE, ws=None, group: int = 1, perm=None
     q = q.contiguous()
     _need(q, None, "q")
     h, nq, d = (int(x) for x in q.shape)
-    nt = -(-nq // TILE)
+    nt = -(-nq // tile)
     ng = -(-nt // group)
     dev = q.device
     mu = _buf(ws, "mu", (h, ng, d), torch.float32, dev)
-    q8 = _buf(ws, "q8", (h, nt * TILE, d), torch.int8, dev)
-    dq8 = _buf(ws, "dq8", (h, nt * TILE, d), torch.int8, dev)
-    sq = _buf(ws, "sq", (h, nt * TILE), torch.float32, dev)
-    sdq = _buf(ws, "sdq", (h, nt * TILE), torch.float32, dev)
+    q8 = _buf(ws, "q8", (h, nt * tile, d), torch.int8, dev)
+    dq8 = _buf(ws, "dq8", (h, nt * tile, d), torch.int8, dev)
+    sq = _buf(ws, "sq", (h, nt * tile), torch.float32, dev)
+    sdq = _buf(ws, "sdq", (h, nt * tile), torch.float32, dev)
     if perm is not None:
         _need(perm, torch.int32, "perm")
         if tuple(perm.shape) != (h, nq):
             raise ValueError("perm must be int32 [H, nq]")
-    call("htrc_pack_q", ptr(q), int(q.dtype == torch.bfloat16), h, nq, d, group, ptr(perm), ptr(mu), ptr(q8), ptr(sq),
-         ptr(dq8), ptr(sdq), stream_handle(dev))
+    call("htrc_pack_q", ptr(q), int(q.dtype == torch.bfloat16), h, nq, d, tile, group, ptr(perm), ptr(mu), ptr(q8),
+         ptr(sq), ptr(dq8), ptr(sdq), stream_handle(dev))
     return mu, q8, sq, dq8, sdq
 
 
 def pack_q16(q: torch.Tensor, tile: int = TILE, ws=None, group: int = 1, perm=None, dq_fp16: bool = True):
     """Centres and the 16-bit operands of the fp8 (and bf16) state stores -> (mu [H,ng,D],
-    q16 bf16 [H,nt*64,D] = bf16(q), dq16 [H,nt*64,D] = fp16(q - mu) (bf16 when dq_fp16 is
+    q16 bf16 [H,nt*tile,D] = bf16(q), dq16 [H,nt*tile,D] = fp16(q - mu) (bf16 when dq_fp16 is
     False)) over the padded tile rows (h3/htrc_flat_triton.py:104-108)."""
-    if tile != TILE:
-        raise ValueError("the HIP kernels use 64-row query tiles")
+    tile = _tile(tile)
     q = _heads(q)
     if q.dtype not in (torch.float32, torch.bfloat16):
         q = q.float()
     q = q.contiguous()
     _need(q, None, "q")
     h, nq, d = (int(x) for x in q.shape)
-    nt = -(-nq // TILE)
+    nt = -(-nq // tile)
     ng = -(-nt // int(group))
     dev = q.device
     if perm is not None:
         _need(perm, torch.int32, "perm")
     mu = _buf(ws, "mu", (h, ng, d), torch.float32, dev)
-    q16 = _buf(ws, "q16", (h, nt * TILE, d), torch.bfloat16, dev)
-    dq16 = _buf(ws, "dq16" if dq_fp16 else "dqb16", (h, nt * TILE, d), torch.float16 if dq_fp16 else torch.bfloat16, dev)
-    call("htrc_pack_q16", ptr(q), int(q.dtype == torch.bfloat16), h, nq, d, int(group), ptr(perm), int(bool(dq_fp16)),
-         ptr(mu), ptr(q16), ptr(dq16), stream_handle(dev))
+    q16 = _buf(ws, "q16", (h, nt * tile, d), torch.bfloat16, dev)
+    dq16 = _buf(ws, "dq16" if dq_fp16 else "dqb16", (h, nt * tile, d), torch.float16 if dq_fp16 else torch.bfloat16, dev)
+    call("htrc_pack_q16", ptr(q), int(q.dtype == torch.bfloat16), h, nq, d, tile, int(group), ptr(perm),
+         int(bool(dq_fp16)), ptr(mu), ptr(q16), ptr(dq16), stream_handle(dev))
     return mu, q16, dq16
 
 
@@ -175,43 +181,44 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
 
 
 def rowmax_select(q_c=None, mu_c=None, g=None, lz=None, prec="ieee", bn=32, warps=4, splits=8, stride=1, dot=1,
-                  ws=None, sg=None, *, nb=None, dq8=None, sdq=None, group=1):
+                  ws=None, sg=None, *, nb=None, dq8=None, sdq=None, group=1, tile=TILE):
     """SEL [H,ng,nbp] (h3/htrc_flat_triton.py:315-326), the max over the rows of each group of
     ``group`` tiles.  Takes the packed rows dq8/sdq (pack_q); when absent they are packed from
     q_c (fp32 [H,nq,D] rows)."""
+    tile = _tile(tile)
     if g.dtype in (torch.float8_e4m3fn, torch.bfloat16):
-        return _select16(g, lz, sg, stride, nb, dq8, group, ws, q_c)
+        return _select16(g, lz, sg, stride, nb, dq8, group, ws, q_c, tile)
     if dq8 is None or sdq is None:
-        _, _, _, dq8, sdq = pack_q(q_c, group=group)
+        _, _, _, dq8, sdq = pack_q(q_c, tile=tile, group=group)
     g = _heads(g) if g.dim() == 3 else g
     h, ng, nbp, d = (int(x) for x in g.shape)
-    nt = int(_heads(dq8).shape[1]) // TILE
+    nt = int(_heads(dq8).shape[1]) // tile
     if -(-nt // int(group)) != ng:
         raise ValueError("state rows do not match the tile groups of the packed rows")
     nb = nbp if nb is None else int(nb)
     dev = g.device
     sel = _buf(ws, "sel", (h, ng, nbp), torch.float32, dev)
-    call("htrc_select", ptr(dq8), ptr(sdq), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), int(group), d,
+    call("htrc_select", ptr(dq8), ptr(sdq), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), tile, int(group), d,
          ptr(sel), stream_handle(dev))
     return sel
 
 
-def _select16(g, lz, sg, stride, nb, dq16, group, ws, q_c):
+def _select16(g, lz, sg, stride, nb, dq16, group, ws, q_c, tile):
     """SEL over a 16-bit state: dq16 are the rows of pack_q16 (passed as ``dq8``): fp16 for the
     fp8 state, bf16 for the bf16 state."""
     fp8 = g.dtype == torch.float8_e4m3fn
     if dq16 is None:
-        _, _, dq16 = pack_q16(q_c, group=group, dq_fp16=fp8)
+        _, _, dq16 = pack_q16(q_c, tile=tile, group=group, dq_fp16=fp8)
     _need(dq16, torch.float16 if fp8 else torch.bfloat16, "dq16")
     h, ng, nbp, d = (int(x) for x in g.shape)
-    nt = int(_heads(dq16).shape[1]) // TILE
+    nt = int(_heads(dq16).shape[1]) // tile
     nb = nbp if nb is None else int(nb)
     sel = _buf(ws, "sel", (h, ng, nbp), torch.float32, g.device)
     if fp8:
-        call("htrc_select_fp8", ptr(dq16), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), int(group), d, ptr(sel),
-             stream_handle(g.device))
+        call("htrc_select_fp8", ptr(dq16), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), tile, int(group), d,
+             ptr(sel), stream_handle(g.device))
     else:
-        call("htrc_select_bf16", ptr(dq16), ptr(g), ptr(lz), h, nt, nb, int(stride), int(group), d, ptr(sel),
+        call("htrc_select_bf16", ptr(dq16), ptr(g), ptr(lz), h, nt, nb, int(stride), tile, int(group), d, ptr(sel),
              stream_handle(g.device))
     return sel
 
@@ -228,17 +235,18 @@ def topk_excl(sel, nb: int, kx: int, sink: int = 0, ws=None):
 
 
 def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, scale: float, splits: int = 4,
-                   bn: int = 64, ws=None, out=None, logz=None, group: int = 1, perm=None):
+                   bn: int = 64, ws=None, out=None, logz=None, group: int = 1, perm=None, tile: int = TILE):
     """Far + near online softmax per (tile, split) and the merge
     (h3/htrc_flat_triton.py:348-391) -> (out [H,nq,D] fp32, logz [H,nq] fp32)."""
+    tile = _tile(tile)
     if state["g8"].dtype in (torch.float8_e4m3fn, torch.bfloat16):
         return _tile16(packed, state, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits, bn=bn, ws=ws,
-                         out=out, logz=logz, group=group, perm=perm)
+                       out=out, logz=logz, group=group, perm=perm, tile=tile)
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
     g8, sg, lz, vb = state["g8"], state["sg"], state["lz"], state["vb"]
     h, nk, d = (int(x) for x in k8.shape)
-    nt = -(-nq // TILE)
+    nt = -(-nq // tile)
     kx = int(idx.shape[-1]) if idx is not None else 0
     dev = q8.device
     ns = max(1, int(splits))
@@ -248,25 +256,26 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     pm = pl = pacc = None
     if ns > 1:
-        pm = _buf(ws, "pm", (h, nt, ns, TILE), torch.float32, dev)
-        pl = _buf(ws, "pl", (h, nt, ns, TILE), torch.float32, dev)
-        pacc = _buf(ws, "pacc", (h, nt, ns, TILE, d), torch.float32, dev)
+        pm = _buf(ws, "pm", (h, nt, ns, tile), torch.float32, dev)
+        pl = _buf(ws, "pl", (h, nt, ns, tile), torch.float32, dev)
+        pacc = _buf(ws, "pacc", (h, nt, ns, tile, d), torch.float32, dev)
     call("htrc_tile", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(excl),
-         ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(v), h, nq, nk, int(leaf), d, kx, int(group), ptr(perm), ns, int(bn),
-         float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
+         ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(v), h, nq, nk, int(leaf), d, kx, tile, int(group), ptr(perm), ns,
+         int(bn), float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
     if ns > 1:
-        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, ns, d, ptr(perm), ptr(out), ptr(logz), stream_handle(dev))
+        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, tile, ns, d, ptr(perm), ptr(out), ptr(logz),
+             stream_handle(dev))
     return out, logz
 
 
-def _tile16(packed, state, excl, idx, *, nq, leaf, scale, splits, bn, ws, out, logz, group, perm):
+def _tile16(packed, state, excl, idx, *, nq, leaf, scale, splits, bn, ws, out, logz, group, perm, tile):
     """Far + near softmax per (tile, split) over a 16-bit state, and the merge: packed holds q16,
     dq16 (pack_q16) and the bf16 k, v; state g8 / vb (e4m3 with sg, sv; or bf16) and lz."""
     q16, dq16, k, v = packed["q16"], packed["dq16"], packed["k"], packed["v"]
     g, sg, lz, vb, sv = state["g8"], state.get("sg"), state["lz"], state["vb"], state.get("sv")
     fp8 = g.dtype == torch.float8_e4m3fn
     h, nk, d = (int(x) for x in k.shape)
-    nt = -(-nq // TILE)
+    nt = -(-nq // tile)
     kx = int(idx.shape[-1]) if idx is not None else 0
     dev = q16.device
     ns = max(1, int(splits))
@@ -276,24 +285,25 @@ def _tile16(packed, state, excl, idx, *, nq, leaf, scale, splits, bn, ws, out, l
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     pm = pl = pacc = None
     if ns > 1:
-        pm = _buf(ws, "pm", (h, nt, ns, TILE), torch.float32, dev)
-        pl = _buf(ws, "pl", (h, nt, ns, TILE), torch.float32, dev)
-        pacc = _buf(ws, "pacc", (h, nt, ns, TILE, d), torch.float32, dev)
+        pm = _buf(ws, "pm", (h, nt, ns, tile), torch.float32, dev)
+        pl = _buf(ws, "pl", (h, nt, ns, tile), torch.float32, dev)
+        pacc = _buf(ws, "pacc", (h, nt, ns, tile, d), torch.float32, dev)
     if fp8:
         call("htrc_tile_fp8", ptr(q16), ptr(dq16), ptr(g), ptr(sg), ptr(lz), ptr(vb), ptr(sv), ptr(excl),
-             ptr(idx) if kx else None, ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, int(group), ptr(perm), ns, int(bn),
-             float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
+             ptr(idx) if kx else None, ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, tile, int(group), ptr(perm), ns,
+             int(bn), float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
     else:
         call("htrc_tile_bf16", ptr(q16), ptr(dq16), ptr(g), ptr(lz), ptr(vb), ptr(excl), ptr(idx) if kx else None,
-             ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, int(group), ptr(perm), ns, int(bn), float(scale), ptr(pm),
-             ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
+             ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, tile, int(group), ptr(perm), ns, int(bn), float(scale),
+             ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
     if ns > 1:
-        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, ns, d, ptr(perm), ptr(out), ptr(logz), stream_handle(dev))
+        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, tile, ns, d, ptr(perm), ptr(out), ptr(logz),
+             stream_handle(dev))
     return out, logz
 
 
 def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: float, sink: int = 0, stride: int = 1,
-          ws=None, out=None, logz=None, idx=None, group: int = 1, perm=None):
+          ws=None, out=None, logz=None, idx=None, group: int = 1, perm=None, tile: int = TILE):
     """Fused select -> top-k, then far + near -> normalised output (two launches per layer call).
     -> (out [H,nq,D], logz [H,nq]); idx [H,ng,min(kx,nb)] int32 receives the routing (a
     workspace buffer when not given)."""
@@ -302,7 +312,8 @@ def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: floa
     g8, sg, lz, vb = state["g8"], state["sg"], state["lz"], state["vb"]
     h, nk, d = (int(x) for x in k8.shape)
     dev = q8.device
-    nt = -(-int(nq) // TILE)
+    tile = _tile(tile)
+    nt = -(-int(nq) // tile)
     ng = -(-nt // int(group))
     kxe = min(int(kx), nk // int(leaf))
     if out is None:
@@ -311,34 +322,35 @@ def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: floa
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     if idx is None and kxe > 0:
         idx = _buf(ws, "idx", (h, ng, kxe), torch.int32, dev)
-    rowmax = _buf(ws, "rowmax", (h, nt * TILE), torch.float32, dev)
+    rowmax = _buf(ws, "rowmax", (h, nt * tile), torch.float32, dev)
     call("htrc_route", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8), ptr(ks),
-         ptr(v), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), int(group), ptr(perm), float(scale),
+         ptr(v), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), tile, int(group), ptr(perm), float(scale),
          ptr(out), ptr(logz), ptr(idx), ptr(rowmax), stream_handle(dev))
     return out, logz
 
 
 def route_select(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, sink: int = 0, stride: int = 1,
-                 ws=None, idx=None, group: int = 1):
+                 ws=None, idx=None, group: int = 1, tile: int = TILE):
     """First launch of route: select -> top-k per tile group -> (idx [H,ng,min(kx,nb)] int32 or
-    None, rowmax [H,nt*64] fp32, each row's largest far-field score)."""
+    None, rowmax [H,nt*tile] fp32, each row's largest far-field score)."""
     dq8, sdq = packed["dq8"], packed["sdq"]
     g8, sg, lz = state["g8"], state["sg"], state["lz"]
     h, nk = int(packed["k8"].shape[0]), int(packed["k8"].shape[1])
     dev = dq8.device
-    nt = -(-int(nq) // TILE)
+    tile = _tile(tile)
+    nt = -(-int(nq) // tile)
     ng = -(-nt // int(group))
     kxe = min(int(kx), nk // int(leaf))
     if idx is None and kxe > 0:
         idx = _buf(ws, "idx", (h, ng, kxe), torch.int32, dev)
-    rowmax = _buf(ws, "rowmax", (h, nt * TILE), torch.float32, dev)
+    rowmax = _buf(ws, "rowmax", (h, nt * tile), torch.float32, dev)
     call("htrc_route_select", ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), h, nq, nk, int(leaf), D, int(kx),
-         int(sink), int(stride), int(group), ptr(idx), ptr(rowmax), stream_handle(dev))
+         int(sink), int(stride), tile, int(group), ptr(idx), ptr(rowmax), stream_handle(dev))
     return idx, rowmax
 
 
 def route_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, kx: int, scale: float, ws=None,
-                 out=None, logz=None, group: int = 1, perm=None):
+                 out=None, logz=None, group: int = 1, perm=None, tile: int = TILE):
     """Second launch of route: far + near field with the row reference rowmax -> (out, logz)."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
@@ -350,8 +362,8 @@ def route_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, 
     if logz is None:
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     call("htrc_route_attend", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8),
-         ptr(ks), ptr(v), ptr(idx), ptr(rowmax), h, nq, nk, int(leaf), d, int(kx), int(group), ptr(perm),
-         float(scale), ptr(out), ptr(logz), stream_handle(dev))
+         ptr(ks), ptr(v), ptr(idx), ptr(rowmax), h, nq, nk, int(leaf), d, int(kx), _tile(tile), int(group),
+         ptr(perm), float(scale), ptr(out), ptr(logz), stream_handle(dev))
     return out, logz
 
 

@@ -30,21 +30,22 @@ MODES = {
     "accurate": dict(exact_leaves=1024, order="kmeans", tile=64),
     "max": dict(exact_leaves=1024, order="kmeans", tile=32),
 }
-# The reference's quality modes (h3/htrc_flat_runner.py:48-53).  "max" needs 32-row tiles,
-# which the HIP kernels (64-row tiles) do not implement.
-SUPPORTED_MODES = ("fast", "balanced", "accurate")
+# The reference's quality modes (h3/htrc_flat_runner.py:48-53), all implemented ("max" runs
+# 32-row tiles).
+SUPPORTED_MODES = ("fast", "balanced", "accurate", "max")
 CHUNKS = (1024, 512, 256, 128, 64, 32, 16)
 TILE = 64
 
 
 def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, heads: int = 1,
-                    splits: int = 1, kx: int = 0, group: int = 1, order: str = "seq") -> int:
+                    splits: int = 1, kx: int = 0, group: int = 1, order: str = "seq", tile: int = TILE) -> int:
     """Device bytes the operator's workspace holds for one call (all tiles at once); the leaf
-    state and the routing hold one row per centre (ng = ceil(nt / group)); order="kmeans"
-    adds the permutation, the assignments and 32 centres."""
-    nt = -(-int(queries) // TILE)
+    state and the routing hold one row per centre (ng = ceil(nt / group), nt tiles of ``tile``
+    rows); order="kmeans" adds the permutation, the assignments and 32 centres."""
+    tile = int(tile)
+    nt = -(-int(queries) // tile)
     ng = -(-nt // max(1, int(group)))
-    rows = nt * TILE
+    rows = nt * tile
     nb = int(keys) // int(leaf)
     nbp = (nb + 31) // 32 * 32
     per_head = (
@@ -58,7 +59,7 @@ def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, hea
         + 4 * ng * kx                      # idx (when recorded)
     )
     if splits > 1:
-        per_head += nt * splits * TILE * (2 + dim) * 4 + ng * nbp * 5 + 4 * ng * kx   # partials, excl, sel
+        per_head += nt * splits * tile * (2 + dim) * 4 + ng * nbp * 5 + 4 * ng * kx   # partials, excl, sel
     if order == "kmeans":
         per_head += 8 * int(queries) + 4 * 32 * dim                                   # perm, assign, centres
     return int(heads) * per_head
@@ -72,7 +73,7 @@ def predicted_peak_mib(keys: int, tile: int, tile_chunk: int, splits: int = 8, l
     bound the workspace; ``queries`` (default: as many as keys) sizes it.  Graph mode adds
     the static fp32 q and bf16 k/v copies."""
     q = int(queries) if queries else int(keys)
-    b = workspace_bytes(q, keys, leaf, dim, heads, splits=1, group=group, order=order)
+    b = workspace_bytes(q, keys, leaf, dim, heads, splits=1, group=group, order=order, tile=tile)
     if graph:
         b += int(heads) * (4 * q * dim + 2 * 2 * int(keys) * dim)
     return b / 2 ** 20
@@ -96,8 +97,6 @@ class FlatRunner:
                  **overrides):
         if mode not in MODES:
             raise ValueError(f"mode must be one of {list(MODES)}")
-        if mode not in SUPPORTED_MODES:
-            raise ValueError(f"mode {mode!r} needs 32-row tiles, which the HIP kernels do not implement")
         from . import htrc_flat
         self.flat = htrc_flat
         self.mode = mode

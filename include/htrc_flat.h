@@ -8,16 +8,20 @@
  *
  * All tensors carry a leading head dimension H and are contiguous:
  *   q        fp32 or bf16 [H, nq, 128]          k, v  bf16 [H, nk, 128]
- *   mu       fp32 [H, ng, 128]                  nt = ceil(nq / 64)  (tiles of 64 query rows)
- *   q8, dq8  int8 [H, nt*64, 128]               sq, sdq fp32 [H, nt*64]   (padded rows)
+ *   mu       fp32 [H, ng, 128]                  nt = ceil(nq / T)  (tiles of T = 64 or 32 rows)
+ *   q8, dq8  int8 [H, nt*T, 128]                sq, sdq fp32 [H, nt*T]    (padded rows)
  *   k8       int8 [H, nk, 128], ks fp32 [H, nk]
  *   g8       int8 [H, ng, nbp, 128]             nb = nk / leaf, nbp = htrc_nb_pad(nb)
  *   sg, lz   fp32 [H, ng, nbp]                  padded leaves: sg = 0, lz = -inf
  *   vb       bf16 [H, ng, nbp, 128]             leaf value means
  *   sel      fp32 [H, ng, nbp]                  excl int8 [H, ng, nbp]; idx int32 [H, ng, kx]
- *   pm, pl   fp32 [H, nt, splits, 64]           pacc fp32 [H, nt, splits, 64, 128]
+ *   pm, pl   fp32 [H, nt, splits, T]            pacc fp32 [H, nt, splits, T, 128]
  *   out      fp32 [H, nq, 128]                  logz fp32 [H, nq]
- *   rowmax   fp32 [H, nt*64]                    per-row far-field maximum (route)
+ *   rowmax   fp32 [H, nt*T]                     per-row far-field maximum (route)
+ *
+ * tile = T, the query rows per tile (one expansion centre each): 64, or 32 (the reference's
+ * runner mode "max", h3/htrc_flat_runner.py:52).  Every entry point of one call chain takes
+ * the same T.
  *
  * group = G >= 1 consecutive tiles share one expansion centre, one leaf state and one near
  * set (the reference's kern["group"], h3/htrc_flat.py:223-231): ng = ceil(nt / G) centres,
@@ -38,7 +42,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 10
+#define HTRC_ABI_VERSION 11
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -51,13 +55,13 @@ const char* htrc_last_error(void);
 int htrc_nb_pad(int64_t nb);
 
 /* Centres and the row int8 of q and q - mu.  group 1: mu[t] is the mean of tile t's real rows;
- * group G > 1: mu[g] is the mean of the G * 64 padded rows of tiles gG.., and q - mu uses the
+ * group G > 1: mu[g] is the mean of the G * T padded rows of tiles gG.., and q - mu uses the
  * centre of the row's group.
  * Replaces _tiles (h3/htrc_flat.py:142-156), the group centres (:223-229) and the in-kernel
  * Q / dQ quantisation of _tile_kernel and _rowmax_kernel (h3/htrc_flat_triton.py:104-117,
  * 225-233). */
-int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, const int32_t* perm,
-                float* mu, int8_t* q8, float* sq, int8_t* dq8, float* sdq, void* stream);
+int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int tile, int group,
+                const int32_t* perm, float* mu, int8_t* q8, float* sq, int8_t* dq8, float* sdq, void* stream);
 
 /* K int8 pack (round half to even, per-row scale).
  * Replaces the host-side K pack of _flat_triton (h3/htrc_flat.py:213-219). */
@@ -72,7 +76,8 @@ int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64
 /* Row-max routing score SEL[g, l] over every `stride`-th row of the group's tiles; nt = tiles.
  * Replaces rowmax_select / _rowmax_kernel (h3/htrc_flat_triton.py:315-326, 214-254). */
 int htrc_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
-                int64_t heads, int64_t nt, int64_t nb, int stride, int group, int d, float* sel, void* stream);
+                int64_t heads, int64_t nt, int64_t nb, int stride, int tile, int group, int d, float* sel,
+                void* stream);
 
 /* kx largest SEL per row (leaves < sink forced in), idx ascending, exclusion mask.
  * Replaces torch.topk + excl.scatter_ (h3/htrc_flat.py:262-265). `rows` = H * ng. */
@@ -85,21 +90,21 @@ int htrc_topk(const float* sel, int64_t rows, int64_t nb, int kx, int sink, int3
 int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
               const float* sg, const float* lz, const uint16_t* vb, const int8_t* excl, const int32_t* idx,
               const int8_t* k8, const float* ks, const uint16_t* v, int64_t heads, int64_t nq, int64_t nk,
-              int leaf, int d, int kx, int group, const int32_t* perm, int splits, int bn, float scale, float* pm,
-              float* pl, float* pacc, float* out, float* logz, void* stream);
+              int leaf, int d, int kx, int tile, int group, const int32_t* perm, int splits, int bn, float scale,
+              float* pm, float* pl, float* pacc, float* out, float* logz, void* stream);
 
 /* Merge of split partials into normalised rows, plus logz = max + log(sum).
  * Replaces _merge_kernel (h3/htrc_flat_triton.py:257-273, launched at :389-390). */
-int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int splits,
+int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int tile, int splits,
                int d, const int32_t* perm, float* out, float* logz, void* stream);
 
 /* Production path, first launch: select -> top-k per tile group with SEL kept in LDS, writing
  * the routing idx [H, ng, min(kx, nb)] (ascending; required when kx > 0) and rowmax fp32
- * [H, nt*64], each row's largest far-field score (the tile's largest when stride > 1).
+ * [H, nt*T], each row's largest far-field score (the tile's largest when stride > 1).
  * Replaces rowmax_select + torch.topk of the chunk loop (h3/htrc_flat.py:258-265). */
 int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
                       int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink, int stride,
-                      int group, int32_t* idx, float* rowmax, void* stream);
+                      int tile, int group, int32_t* idx, float* rowmax, void* stream);
 
 /* Production path, second launch: far + near field of every tile in one softmax whose
  * reference is rowmax, merged into normalised out / logz (one split per tile).
@@ -107,16 +112,16 @@ int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, con
 int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                       const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                       const uint16_t* v, const int32_t* idx, const float* rowmax, int64_t heads, int64_t nq,
-                      int64_t nk, int leaf, int d, int kx, int group, const int32_t* perm, float scale, float* out,
-                      float* logz, void* stream);
+                      int64_t nk, int leaf, int d, int kx, int tile, int group, const int32_t* perm, float scale,
+                      float* out, float* logz, void* stream);
 
 /* Both launches of the production path: htrc_route_select then htrc_route_attend.
  * Replaces the chunk loop body of _flat_triton after leaf_stats (h3/htrc_flat.py:250-271). */
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
-               int stride, int group, const int32_t* perm, float scale, float* out, float* logz, int32_t* idx,
-               float* rowmax, void* stream);
+               int stride, int tile, int group, const int32_t* perm, float scale, float* out, float* logz,
+               int32_t* idx, float* rowmax, void* stream);
 
 /* Tail keys: tk, tv fp32 [H, ntail, 128] (keys past the last full leaf) attended exactly by
  * every query and merged in place into a finished out / logz (log-sum-exp merge).  Up to 16
@@ -127,24 +132,24 @@ int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, in
 
 /* fp8 state store (store="fp8"; h3/htrc_flat_triton.py:65-72, 104-108, 132-153, 165-184,
  * 214-254 with FP8 = 1), run in the reference's stage structure (select, top-k, tile, merge):
- *   q16 bf16 [H, nt*64, 128] = bf16(q), dq16 [H, nt*64, 128] = fp16(q - mu) (dq_fp16 = 1) or
+ *   q16 bf16 [H, nt*T, 128] = bf16(q), dq16 [H, nt*T, 128] = fp16(q - mu) (dq_fp16 = 1) or
  *   bf16(q - mu) (dq_fp16 = 0); g, vb uint8 e4m3fn [H, ng, nbp, 128] = code(x / s) with row
  *   scales sg, sv fp32 [H, ng, nbp] = max(max|x| * fp32(1/448), 1e-30); lz as the int8 path.
  *   select: SEL = max_r (fp16 dq . g) * sg + lz; tile far: (fp16 dq . g) * sg + lz with
  *   PV (p sv)(fp16) . vb; near: (bf16 q . bf16 k) * scale with PV bf16(p) . v.
  * Replace leaf_stats(store=float8_e4m3fn), rowmax_select and tile_attention on that state. */
-int htrc_pack_q16(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int group, const int32_t* perm,
-                  int dq_fp16, float* mu, uint16_t* q16, uint16_t* dq16, void* stream);
+int htrc_pack_q16(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int tile, int group,
+                  const int32_t* perm, int dq_fp16, float* mu, uint16_t* q16, uint16_t* dq16, void* stream);
 int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
                         int leaf, int d, float scale, uint8_t* g, float* sg, uint8_t* vb, float* sv, float* lz,
                         void* stream);
 int htrc_select_fp8(const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz, int64_t heads, int64_t nt,
-                    int64_t nb, int stride, int group, int d, float* sel, void* stream);
+                    int64_t nb, int stride, int tile, int group, int d, float* sel, void* stream);
 int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz,
                   const uint8_t* vb, const float* sv, const int8_t* excl, const int32_t* idx, const uint16_t* k,
-                  const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int group,
-                  const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out,
-                  float* logz, void* stream);
+                  const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int tile,
+                  int group, const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
+                  float* out, float* logz, void* stream);
 
 /* bf16 state store (store="bf16"; DOT = 1 without FP8 / I8 in h3/htrc_flat_triton.py:82-83,
  * 132-153, 165-184, 214-254): g, vb bf16 [H, ng, nbp, 128], no row scales; q16 / dq16 from
@@ -154,11 +159,12 @@ int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, c
 int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
                          int leaf, int d, float scale, uint16_t* g, uint16_t* vb, float* lz, void* stream);
 int htrc_select_bf16(const uint16_t* dq16, const uint16_t* g, const float* lz, int64_t heads, int64_t nt, int64_t nb,
-                     int stride, int group, int d, float* sel, void* stream);
+                     int stride, int tile, int group, int d, float* sel, void* stream);
 int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g, const float* lz, const uint16_t* vb,
                    const int8_t* excl, const int32_t* idx, const uint16_t* k, const uint16_t* v, int64_t heads,
-                   int64_t nq, int64_t nk, int leaf, int d, int kx, int group, const int32_t* perm, int splits, int bn,
-                   float scale, float* pm, float* pl, float* pacc, float* out, float* logz, void* stream);
+                   int64_t nq, int64_t nk, int leaf, int d, int kx, int tile, int group, const int32_t* perm,
+                   int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out, float* logz,
+                   void* stream);
 
 /* k-means query order: perm int32 [H, nq], the queries ordered by their nearest of `clusters`
  * centres (stable), the centres from `iters` Lloyd steps on `sample` evenly spaced queries.

@@ -45,12 +45,12 @@ def test_nb_pad():
 _FAKE = ctypes.c_void_p(256)   # never dereferenced: validation fails before any launch
 
 
-@pytest.mark.parametrize("case", ["null", "dim", "leaf", "block", "leaves", "group"])
+@pytest.mark.parametrize("case", ["null", "dim", "leaf", "block", "leaves", "group", "tile", "stride"])
 def test_launchers_reject_bad_arguments_on_host(case):
     lib = _lib.lib()
     f = _FAKE
     if case == "null":
-        rc = lib.htrc_pack_q(None, 1, 1, 64, 128, 1, None, f, f, f, f, f, None)
+        rc = lib.htrc_pack_q(None, 1, 1, 64, 128, 64, 1, None, f, f, f, f, f, None)
         msg = "null"
     elif case == "dim":
         rc = lib.htrc_pack_k(f, 1, 64, 64, f, f, None)
@@ -59,21 +59,27 @@ def test_launchers_reject_bad_arguments_on_host(case):
         rc = lib.htrc_leaf_stats(f, f, f, 1, 1, 96, 48, 128, 0.1, f, f, f, f, None)
         msg = "leaf"
     elif case == "block":
-        rc = lib.htrc_tile(*([f] * 13), 1, 64, 128, 64, 128, 1, 1, None, 4, 48, 0.1, f, f, f, f, f, None)
+        rc = lib.htrc_tile(*([f] * 13), 1, 64, 128, 64, 128, 1, 64, 1, None, 4, 48, 0.1, f, f, f, f, f, None)
         msg = "multiple of 32"
     elif case == "leaves":
-        rc = lib.htrc_route(*([f] * 11), 1, 64, 64 * 9000, 64, 128, 4, 0, 1, 1, None, 0.1, f, f, None, f, None)
+        rc = lib.htrc_route(*([f] * 11), 1, 64, 64 * 9000, 64, 128, 4, 0, 1, 64, 1, None, 0.1, f, f, None, f, None)
         msg = "8192"
-    else:
-        rc = lib.htrc_route_select(*([f] * 5), 1, 640, 640, 64, 128, 4, 0, 1, 0, f, f, None)
+    elif case == "group":
+        rc = lib.htrc_route_select(*([f] * 5), 1, 640, 640, 64, 128, 4, 0, 1, 64, 0, f, f, None)
         msg = "group"
+    elif case == "tile":
+        rc = lib.htrc_route_select(*([f] * 5), 1, 640, 640, 64, 128, 4, 0, 1, 48, 1, f, f, None)
+        msg = "32 or 64"
+    else:                                          # stride must divide a 32-row tile
+        rc = lib.htrc_select(*([f] * 5), 1, 10, 20, 64, 32, 1, 128, f, None)
+        msg = "divide"
     assert rc == 1
     assert msg in lib.htrc_last_error().decode()
 
 
 def test_call_maps_errors_to_value_error():
     with pytest.raises(ValueError, match="null"):
-        _lib.call("htrc_pack_q", None, 1, 1, 64, 128, 1, None, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, None)
+        _lib.call("htrc_pack_q", None, 1, 1, 64, 128, 64, 1, None, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, None)
 
 
 def test_split_and_buf_match_reference_semantics():
@@ -100,7 +106,8 @@ def _qkv(n=128, m=128, d=128):
     ({"curvature": "iso"}, "curvature"),
     ({"select": "bound"}, "select"),
     ({"order": "hilbert"}, "order"),
-    ({"tile": 32}, "tile=64"),
+    ({"tile": 16}, "tile=64 or tile=32"),
+    ({"tile": 32, "sel_stride": 64}, "divide the tile"),
     ({"leaf": 48}, "leaf"),
     ({"quant": {"q": "int8"}}, "quant"),
     ({"kern": {"group": 2000}}, "group"),
@@ -142,7 +149,9 @@ def test_runner_modes_and_memory_model():
         htrc_flat_runner.plan_chunk(1 << 30, 64512, 64, leaf=64, queries=64512, heads=24)
     with pytest.raises(ValueError, match="mode"):
         htrc_flat_runner.FlatRunner(64, 64, mode="nope")
-    with pytest.raises(ValueError, match="32-row"):
-        htrc_flat_runner.FlatRunner(64, 64, mode="max")
+    assert htrc_flat_runner.SUPPORTED_MODES == ("fast", "balanced", "accurate", "max")
+    # 32-row tiles double the centres: the per-(tile, leaf) state doubles
+    m32 = htrc_flat_runner.predicted_peak_mib(64512, 32, 128, leaf=64, queries=64512, heads=24)
+    assert m32 - mib == pytest.approx(24 * 1008 * 1024 * 392 / 2 ** 20, rel=0.02)
     km = htrc_flat_runner.predicted_peak_mib(64512, 64, 128, leaf=64, queries=64512, heads=24, order="kmeans")
     assert km - mib == pytest.approx(24 * (8 * 64512 + 4 * 32 * 128) / 2 ** 20)

@@ -223,3 +223,26 @@ def test_bf16_store_vs_oracle(device, n, leaf, ex, group):
     assert mism <= max(1, ref["idx"].shape[0] // 50)
     assert rel_l2(out.cpu().numpy(), ref["out"]) <= OUT_REL_L2
     assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
+
+
+@pytest.mark.parametrize("store,fused,order", [("int8", True, "seq"), ("int8", False, "seq"), ("int8", True, "kmeans"),
+                                               ("fp8", False, "seq")])
+def test_tile32_vs_oracle(device, store, fused, order):
+    """tile=32 (the runner's mode "max", h3/htrc_flat_runner.py:52) end to end: 32-row tiles,
+    each with its own centre, state and near set; routing and output as above."""
+    n, leaf, ex = 6000, 16, 48
+    nk = (n // leaf) * leaf
+    q, k, v = workloads.clustered_runs(n=n, runs=max(1, n // 64), heads=1, seed=n + 32)
+    k, v = k[:, :nk].contiguous(), v[:, :nk].contiguous()
+    st = {}
+    out, logz = htrc_flat.flat_attention(q[0].to(device), k[0].to(device), v[0].to(device), backend="hip", tile=32,
+                                         store=store, dot="bf16", leaf=leaf, exact_leaves=ex, splits=4, order=order,
+                                         kern={"tile_bn": 64, "fused": fused}, return_logz=True, state=st)
+    torch.cuda.synchronize()
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=32, leaf=leaf, exact_leaves=ex,
+                          splits=1 if fused else 4, bn=64, order=order, store=store)
+    assert st["tile"] == 32 and st["idx"].shape[1] == -(-n // 32)
+    mism = _routing_check(st["idx"][0].cpu().numpy(), ref)
+    assert mism <= max(1, ref["idx"].shape[0] // 50)
+    assert rel_l2(out.cpu().numpy(), ref["out"]) <= OUT_REL_L2
+    assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS

@@ -99,9 +99,9 @@ def test_pack_edge_rows(device):
     assert np.array_equal(_np(k8[0]), ok8) and np.array_equal(_np(ks[0]).view(np.uint32), oks.view(np.uint32))
 
 
-def _oracle_state(q, k, v, leaf, ex, splits=4, bn=64, stride=1, sink=0, group=1):
+def _oracle_state(q, k, v, leaf, ex, splits=4, bn=64, stride=1, sink=0, group=1, tile=64):
     return flat_i8.flat_i8(bits(q[0]) if q.dtype == torch.bfloat16 else q[0].numpy(), bits(k[0]), bits(v[0]),
-                           tile=64, leaf=leaf, exact_leaves=ex, splits=splits, bn=bn, sel_stride=stride,
+                           tile=tile, leaf=leaf, exact_leaves=ex, splits=splits, bn=bn, sel_stride=stride,
                            sink_leaves=sink, group=group)
 
 
@@ -493,6 +493,95 @@ def test_select_and_tile_bf16_on_oracle_state(device, group, stride):
                                 dq8=packed["dq16"], group=group)
         out, logz = hip.tile_attention(packed, state, excl, idx, nq=n, leaf=leaf, scale=scale, splits=splits, bn=64,
                                        group=group)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(_np(sel[0])[:, :nb], ref["sel"], rtol=2e-5, atol=2e-5)
+        assert rel_l2(_np(out[0]), ref["out"]) <= OUT_REL_L2
+        assert np.abs(_np(logz[0]) - ref["logz"]).max() <= LOGZ_ABS
+
+
+# ---- 32-row tiles (tile=32, the runner's mode "max", h3/htrc_flat_runner.py:52)
+
+@pytest.mark.parametrize("nq,group", [(4096, 1), (1000, 1), (33, 1), (1, 1), (1000, 2), (32 * 9 + 5, 4)])
+@pytest.mark.parametrize("qdtype", ["bf16", "fp32"])
+def test_pack_tile32_bitexact(device, nq, group, qdtype):
+    q, _, _ = _data(max(nq, 256), nk=256, seed=nq + 32 * group)
+    q = q[:, :nq]
+    if qdtype == "fp32":
+        q = q.float() + 1e-3 * torch.randn(q.shape, generator=torch.Generator().manual_seed(5))
+    mu, q8, sq, dq8, sdq = hip.pack_q(q.to(device).contiguous(), tile=32, group=group)
+    _, q16, dq16 = hip.pack_q16(q.to(device).contiguous(), tile=32, group=group)
+    torch.cuda.synchronize()
+    qf = q[0].float().numpy()
+    omu = flat_i8.tile_centres(qf, 32) if group == 1 else flat_i8.group_centres(qf, 32, group)
+    oq8, osq, odq8, osdq = flat_i8.pack_q(qf, 32, omu, group)
+    assert q8.shape[1] == -(-nq // 32) * 32
+    assert np.array_equal(_np(mu[0]).view(np.uint32), omu.view(np.uint32))
+    for a, b in ((q8, oq8), (sq, osq), (dq8, odq8), (sdq, osdq)):
+        assert np.array_equal(_np(a[0]), b)
+    oq16, odq16 = flat_i8.pack_q16(qf, 32, omu, group, dq_fp16=True)
+    assert np.array_equal(_np(q16[0].view(torch.int16)).view(np.uint16), oq16)
+    assert np.array_equal(_np(dq16[0].view(torch.int16)).view(np.uint16), odq16)
+
+
+@pytest.mark.parametrize("leaf,ex,stride,group", [(64, 8, 1, 1), (16, 40, 1, 1), (32, 16, 2, 1), (64, 0, 1, 1),
+                                                  (64, 6, 1, 3), (16, 64, 1, 1)])
+def test_route_tile32_on_oracle_state(device, leaf, ex, stride, group):
+    """Route kernels on 32-row tiles, on the oracle's state: idx bit-exact, rowmax bit-exact
+    (every row's largest far score, or the tile's when rows are sampled), output and logZ
+    within the bar; the split tile kernel + merge agrees."""
+    n = 32 * 61 + 7
+    q, k, v = _data(n, nk=64 * 32, seed=leaf + ex + group)
+    ref = _oracle_state(q, k, v, leaf, ex, splits=1, bn=64, stride=stride, group=group, tile=32)
+    packed, state, excl, _ = _device_state(ref, q, k, v, device)
+    kx = ref["idx"].shape[1]
+    ng, nb, d = ref["g8"].shape
+    idx = torch.full((1, ng, max(kx, 1)), -1, dtype=torch.int32, device=device)
+    scale = 1 / math.sqrt(128)
+    out, logz = hip.route(packed, state, nq=n, leaf=leaf, kx=kx, scale=scale, stride=stride, group=group, tile=32,
+                          idx=idx if kx else None)
+    idx2, rowmax = hip.route_select(packed, state, nq=n, leaf=leaf, kx=kx, stride=stride, group=group, tile=32)
+    torch.cuda.synchronize()
+    if kx:
+        assert np.array_equal(_np(idx[0]), ref["idx"])
+    assert rel_l2(_np(out[0]), ref["out"]) <= OUT_REL_L2
+    assert np.abs(_np(logz[0]) - ref["logz"]).max() <= LOGZ_ABS
+    if group == 1:
+        nt = ng
+        dq = ref["dq8"].astype(np.int64).reshape(nt, 32, d)
+        acc = np.einsum("trd,tld->trl", dq, ref["g8"].astype(np.int64)).astype(np.float32)
+        c = (ref["sdq"].reshape(nt, 32)[:, :, None] * ref["sg"][:, None, :]).astype(np.float32)
+        want = ((acc * c).astype(np.float32) + ref["lz"][:, None, :]).astype(np.float32).max(axis=2)
+        if stride > 1:
+            want = np.repeat(want[:, ::stride].max(1, keepdims=True), 32, axis=1)
+        assert np.array_equal(_np(rowmax[0]).reshape(nt, 32), want)
+    for splits in (1, 3):
+        refs = _oracle_state(q, k, v, leaf, ex, splits=splits, bn=64, stride=stride, group=group, tile=32)
+        packed, state, excl, idxs = _device_state(refs, q, k, v, device)
+        out2, logz2 = hip.tile_attention(packed, state, excl, idxs if kx else None, nq=n, leaf=leaf, scale=scale,
+                                         splits=splits, bn=64, group=group, tile=32)
+        sel = hip.rowmax_select(g=state["g8"], lz=state["lz"], sg=state["sg"], stride=stride, nb=nb,
+                                dq8=packed["dq8"], sdq=packed["sdq"], group=group, tile=32)
+        torch.cuda.synchronize()
+        if kx:
+            assert np.array_equal(_np(sel[0])[:, :nb].view(np.uint32), refs["sel"].view(np.uint32))
+        assert rel_l2(_np(out2[0]), refs["out"]) <= OUT_REL_L2
+        assert np.abs(_np(logz2[0]) - refs["logz"]).max() <= LOGZ_ABS
+
+
+@pytest.mark.parametrize("store", ["fp8", "bf16"])
+def test_select_and_tile16_tile32_on_oracle_state(device, store):
+    n, leaf, ex = 32 * 41 + 5, 64, 6
+    q, k, v = _data(n, nk=64 * 24, seed=77)
+    scale = 1 / math.sqrt(128)
+    for splits, stride in ((1, 1), (4, 2)):
+        ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=32, leaf=leaf, exact_leaves=ex, splits=splits,
+                              bn=64, sel_stride=stride, store=store)
+        packed, state, excl, idx = (_fp8_state if store == "fp8" else _bf16_state)(ref, k, v, device)
+        nb = (ref["g8"] if store == "fp8" else ref["g16"]).shape[1]
+        sel = hip.rowmax_select(g=state["g8"], lz=state["lz"], sg=state["sg"], stride=stride, nb=nb,
+                                dq8=packed["dq16"], tile=32)
+        out, logz = hip.tile_attention(packed, state, excl, idx, nq=n, leaf=leaf, scale=scale, splits=splits, bn=64,
+                                       tile=32)
         torch.cuda.synchronize()
         np.testing.assert_allclose(_np(sel[0])[:, :nb], ref["sel"], rtol=2e-5, atol=2e-5)
         assert rel_l2(_np(out[0]), ref["out"]) <= OUT_REL_L2

@@ -103,3 +103,22 @@ def test_accurate_mode_graph_replays_equal_eager(device):
         for o, e in zip(outs, eager):
             assert torch.equal(o, e), f"replay {rep} differs from eager"
         _ = torch.randn(1 << 20, device=device).sum().item()
+
+
+def test_max_mode_graph_replays_equal_eager(device):
+    """mode="max" (32-row tiles with k-means order, h3/htrc_flat_runner.py:52): every replay of
+    the captured graph equals the eager operator call, and the tiles are 32 rows."""
+    jobs = _jobs(device, heads=2, seed=6)
+    r = htrc_flat_runner.FlatRunner(2048, 2048, mode="max", **KW)
+    assert r.cfg["tile"] == 32 and r.cfg["order"] == "kmeans"
+    assert r.graph is not None, r.graph_error
+    st = {}
+    eager = [htrc_flat.flat_attention(j[1], j[2], j[3], **r.cfg) for j in jobs]
+    htrc_flat.flat_attention(jobs[0][1], jobs[0][2], jobs[0][3], state=st, **r.cfg)
+    assert st["idx"].shape[1] == 2048 // 32
+    for rep in range(3):
+        outs = r.run(jobs)
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {rep} differs from eager"
+        _ = torch.randn(1 << 20, device=device).sum().item()
