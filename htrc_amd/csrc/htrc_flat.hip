@@ -280,20 +280,28 @@ __device__ __forceinline__ void settle(const i32x4 (&b)[4][2], const float (&s)[
     for (int rb = 0; rb < 4; ++rb) asm volatile("" : : "v"(b[rb][0]), "v"(b[rb][1]), "v"(s[rb]));
 }
 
-// Stage leaf rows [key0, key0 + LEAF) of K and V: LDS chunk s = j*256 + tid holds the
-// 16-byte chunk (s % 16) ^ swz(row) of row (s / 16) % LEAF of K (first half) or V.  Row
-// 16 jj + tid / 16 of chunk j keeps the swizzle of row tid / 16, so every chunk of a thread
-// uses one per-lane offset from a wave-uniform base (rows 16 jj).  lds0 = LDS address of buf.
-template <int LEAF>
+// Stage leaf rows [key0, key0 + LEAF) of K and V with NT threads: LDS chunk s = j*NT + tid
+// holds the 16-byte chunk (s % 16) ^ swz(row) of row (s / 16) % LEAF of K (first LEAF * 16
+// chunks) or V.  A wave's 64 chunks are 4 rows r0 .. r0 + 3 of one matrix, r0 = 4 w (mod 16)
+// for every j (NT / 16 is a multiple of 16), so with swz's period 16 every chunk of a thread
+// uses one per-lane offset voff = stage_voff() from a wave-uniform base (row r0).
+__device__ __forceinline__ uint32_t stage_voff() {
+    const int lane = threadIdx.x & 63, row = (4 * (threadIdx.x >> 6) + (lane >> 4)) & 15;
+    return (uint32_t)((lane >> 4) * 2 * D + 16 * ((lane & 15) ^ swz(row)));
+}
+
+template <int LEAF, int NT>
 __device__ __forceinline__ void stage_leaf(const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
                                            int64_t key0, uint32_t lds0, uint32_t voff) {
-    constexpr int NJ = 32 * LEAF / 256;         // 16-byte chunks per thread (K and V)
+    constexpr int NJ = 32 * LEAF / NT;          // 16-byte chunks per thread (K and V)
+    static_assert(NJ >= 1 && (32 * LEAF) % NT == 0 && NT % 256 == 0, "stage_leaf shape");
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        const int jj = j % (NJ / 2);
-        const uint16_t* X = j < NJ / 2 ? K : V;
-        dma16s(X + (key0 + 16 * jj) * D, voff, lds0 + (uint32_t)(j * 256 + w * 64) * 16);
+        const int s0 = j * NT + w * 64;         // the wave's first chunk
+        const uint16_t* X = s0 < LEAF * 16 ? K : V;
+        const int r0 = (s0 >> 4) % LEAF;
+        dma16s(X + (key0 + r0) * D, voff, lds0 + (uint32_t)s0 * 16);
     }
 }
 
@@ -350,8 +358,11 @@ __device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
 // STORE 1: g and vb bf16, no scales (store="bf16", :82-83);
 // STORE 2: g and vb as e4m3 codes of x / s with row scales s = max(max|x| * fp32(1/448), 1e-30)
 // (sg, sv; store="fp8", :65-72); vb then holds bytes.
-template <int LEAF, int STORE = 0>
-__global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__ mu, int nt,
+// NW waves of 16 centres each share every staged leaf (workgroup = 16 NW centres).
+constexpr int STATS_NW = 4;
+constexpr int STATS_TPW = 16 * STATS_NW;
+template <int LEAF, int STORE, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restrict__ mu, int nt,
                                                        const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v, int64_t nk, int nb,
                                                        int nb_pad, int lpb, float scale,
@@ -363,21 +374,20 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
     constexpr int LEAF_BYTES = 32 * LEAF * 16;
     constexpr int LPB = 16;                       // leaves per workgroup (the launcher's lpb)
     constexpr bool FP8 = STORE == 2, BF16 = STORE == 1;
+    constexpr int TPW = 16 * NW;                  // centres per workgroup
     __shared__ __align__(16) char lds[2 * LEAF_BYTES];
-    __shared__ __align__(16) float s_sg[64][LPB], s_lz[64][LPB];   // per tile, the workgroup's leaves
-    __shared__ __align__(16) float s_sv[FP8 ? 64 : 1][LPB];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    // 1-D grid over (tile group, leaf group, head), tile group fastest: the tile groups that
-    // read the same leaves run together on one XCD and share its L2.
-    const int ntg = (nt + 63) / 64, nlg = (nb_pad + lpb - 1) / lpb;
+    // 1-D grid over (centre group, leaf group, head), centre group fastest: the centre groups
+    // that read the same leaves run together on one XCD and share its L2.
+    const int ntg = (nt + TPW - 1) / TPW, nlg = (nb_pad + lpb - 1) / lpb;
     const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
     const int tg = (int)(blk % (uint32_t)ntg), lg = (int)((blk / (uint32_t)ntg) % (uint32_t)nlg);
     const int h = (int)(blk / ((uint32_t)ntg * (uint32_t)nlg));
-    const int t = tg * 64 + w * 16 + col;           // tile centre of this lane's C column
+    const int t = tg * TPW + w * 16 + col;          // centre of this lane's C column
     const bool tval = t < nt;
     const int64_t th = (int64_t)h * nt + (tval ? t : 0);
     const uint32_t lds0 = lds_addr(lds);
-    const uint32_t voff = (uint32_t)((threadIdx.x >> 4) * 2 * D + 16 * ((threadIdx.x & 15) ^ swz(threadIdx.x >> 4)));
+    const uint32_t voff = stage_voff();
     const float sl2 = __fmul_rn(scale, LOG2E);
 
     // mu in two bf16 terms (~16 bits; the reference's production path computes these dots in TF32)
@@ -458,7 +468,73 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
             store_rows16(pv, vb, hf);
         }
     };
-    if (l0 < lr) stage_leaf<LEAF>(k, v, kh + (int64_t)l0 * LEAF, lds0, voff);
+    // sg, lz (and sv) of the workgroup's 16 leaves stay in registers: every lane of a column
+    // holds its centre's values, a 4-leaf shift register takes each leaf, and lane grp keeps
+    // leaves 4 grp .. 4 grp + 3, written at the end as 64 contiguous bytes per centre.
+    // Leaves past the real ones keep the padding values (sg = sv = 0, lz = -inf).
+    f32x4 sh_sg = {0.f, 0.f, 0.f, 0.f}, sh_lz = sh_sg, sh_sv = sh_sg;
+    f32x4 kp_sg = sh_sg, kp_sv = sh_sg, kp_lz = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    auto push = [&](int l, float vsg, float vlz, float vsv) {
+        sh_sg = f32x4{sh_sg[1], sh_sg[2], sh_sg[3], vsg};
+        sh_lz = f32x4{sh_lz[1], sh_lz[2], sh_lz[3], vlz};
+        if (FP8) sh_sv = f32x4{sh_sv[1], sh_sv[2], sh_sv[3], vsv};
+        if (((l - l0) & 3) == 3 && ((l - l0) >> 2) == grp) {
+            kp_sg = sh_sg;
+            kp_lz = sh_lz;
+            if (FP8) kp_sv = sh_sv;
+        }
+    };
+    // products of the current leaf and its log-partition
+    f32x4 gacc[8], vacc[8];
+    float lzq = 0.0f;
+    // g^T = scale gacc^T, vb^T of leaf lq: lane holds dims 16db + 4grp + i of centre t.  The int8
+    // code of g is round(127 g / max|g|) = round(gacc * 127 scale / max|g|).
+    auto quantise = [&](int lq) {
+        float am = 0.0f;
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) am = fmaxf(am, fabsf(gacc[db][i]));
+        am = __fmul_rn(grp_max(am), scale);             // max |g|
+        if constexpr (BF16) {
+            // g = gacc * scale and vb rounded to bf16, no scales
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                pgb[db] = u32x2{pack2bf(__fmul_rn(gacc[db][0], scale), __fmul_rn(gacc[db][1], scale)),
+                                pack2bf(__fmul_rn(gacc[db][2], scale), __fmul_rn(gacc[db][3], scale))};
+                pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
+            }
+            push(lq, 0.0f, lzq, 0.0f);
+        } else if constexpr (FP8) {
+            // sg = max(max|g| / 448, 1e-30), code = e4m3(g / sg) with g / sg taken as
+            // gacc * (scale / sg); vb the same with sv
+            const float sgv = fmaxf(__fmul_rn(am, R448), 1e-30f);
+            float av = 0.0f;
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) av = fmaxf(av, fabsf(vacc[db][i]));
+            const float svv = fmaxf(__fmul_rn(grp_max(av), R448), 1e-30f);
+            const float cg = __fdiv_rn(scale, sgv), cv = __fdiv_rn(1.0f, svv);
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                pg[db] = quant4_e4m3(gacc[db], cg);
+                pv[db] = u32x2{quant4_e4m3(vacc[db], cv), 0u};
+            }
+            push(lq, sgv, lzq, svv);
+        } else {
+            am = am < 1e-30f ? 1e-30f : am;
+            const float cq = __fdiv_rn(__fmul_rn(127.0f, scale), am);
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                pg[db] = quant4(gacc[db], cq);
+                pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
+            }
+            push(lq, __fmul_rn(am, R127), lzq, 0.0f);
+        }
+        pl = lq;
+    };
+    if (l0 < lr) stage_leaf<LEAF, 64 * NW>(k, v, kh + (int64_t)l0 * LEAF, lds0, voff);
     for (int l = l0; l < lr; ++l) {
         // Leaf l landed and the stores of leaf l - 2 are done (measured: issuing the next
         // loads ahead of the stores, or letting the stores stay in flight past this wait, is
@@ -466,7 +542,8 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
         wait_vmcnt<0>();
         __syncthreads();                       // ... for every wave; buffer of leaf l - 1 free
         if (l + 1 < lr)
-            stage_leaf<LEAF>(k, v, kh + (int64_t)(l + 1) * LEAF, lds0 + ((l + 1 - l0) & 1) * LEAF_BYTES, voff);
+            stage_leaf<LEAF, 64 * NW>(k, v, kh + (int64_t)(l + 1) * LEAF, lds0 + ((l + 1 - l0) & 1) * LEAF_BYTES,
+                                      voff);
         const char* Kr = lds + ((l - l0) & 1) * LEAF_BYTES;
         const char* Vr = Kr + 16 * LEAF * 16;
         f32x4 a[KB];
@@ -502,7 +579,6 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
         z = grp_sum(z);
         const float rz = __fdiv_rn(1.0f, z);
         // w = e / z in two bf16 terms, shared by both products: gacc = w K (g = scale gacc), vb = w V
-        f32x4 gacc[8], vacc[8];
 #pragma unroll
         for (int db = 0; db < 8; ++db) gacc[db] = vacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -532,62 +608,28 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
         }
         if (KK == 1) store_v(0);
         store_v(1);
-        // g^T = scale gacc^T, vb^T: lane holds dims 16db + 4grp + i of centre t.  The int8 code
-        // of g is round(127 g / max|g|) = round(gacc * 127 scale / max|g|).
-        float am = 0.0f;
-#pragma unroll
-        for (int db = 0; db < 8; ++db)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) am = fmaxf(am, fabsf(gacc[db][i]));
-        am = __fmul_rn(grp_max(am), scale);             // max |g|
-        if constexpr (BF16) {
-            // g = gacc * scale and vb rounded to bf16, no scales
-#pragma unroll
-            for (int db = 0; db < 8; ++db) {
-                pgb[db] = u32x2{pack2bf(__fmul_rn(gacc[db][0], scale), __fmul_rn(gacc[db][1], scale)),
-                                pack2bf(__fmul_rn(gacc[db][2], scale), __fmul_rn(gacc[db][3], scale))};
-                pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
-            }
-            if (grp == 0) s_lz[w * 16 + col][l - l0] = __fadd_rn(mx, __logf(z));
-        } else if constexpr (FP8) {
-            // sg = max(max|g| / 448, 1e-30), code = e4m3(g / sg) with g / sg taken as
-            // gacc * (scale / sg); vb the same with sv
-            const float sgv = fmaxf(__fmul_rn(am, R448), 1e-30f);
-            float av = 0.0f;
-#pragma unroll
-            for (int db = 0; db < 8; ++db)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) av = fmaxf(av, fabsf(vacc[db][i]));
-            const float svv = fmaxf(__fmul_rn(grp_max(av), R448), 1e-30f);
-            const float cg = __fdiv_rn(scale, sgv), cv = __fdiv_rn(1.0f, svv);
-#pragma unroll
-            for (int db = 0; db < 8; ++db) {
-                pg[db] = quant4_e4m3(gacc[db], cg);
-                pv[db] = u32x2{quant4_e4m3(vacc[db], cv), 0u};
-            }
-            if (grp == 0) {
-                s_sg[w * 16 + col][l - l0] = sgv;
-                s_sv[w * 16 + col][l - l0] = svv;
-                s_lz[w * 16 + col][l - l0] = __fadd_rn(mx, __logf(z));
-            }
-        } else {
-            am = am < 1e-30f ? 1e-30f : am;
-            const float cq = __fdiv_rn(__fmul_rn(127.0f, scale), am);
-#pragma unroll
-            for (int db = 0; db < 8; ++db) {
-                pg[db] = quant4(gacc[db], cq);
-                pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
-            }
-            if (grp == 0) {
-                s_sg[w * 16 + col][l - l0] = __fmul_rn(am, R127);
-                s_lz[w * 16 + col][l - l0] = __fadd_rn(mx, __logf(z));
-            }
-        }
-        pl = l;
+        // quantised after the last stores of leaf l - 1: this VALU work covers their latency
+        // before the next iteration's wait
+        lzq = __fadd_rn(mx, __logf(z));
+        quantise(l);
     }
     store_g();
     store_v(0);
     store_v(1);
+    {   // a last, partial quad of real leaves: its rem leaves are the newest rem of the shift
+        // register, the rest padding
+        const int rem = (lr - l0) & 3;
+        if (lr > l0 && rem != 0 && ((lr - l0) >> 2) == grp) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = 4 - rem + i;     // shift-register slot of quad slot i (i < rem)
+                const bool real = i < rem;
+                kp_sg[i] = real ? sh_sg[j & 3] : 0.0f;
+                kp_lz[i] = real ? sh_lz[j & 3] : -INFINITY;
+                if (FP8) kp_sv[i] = real ? sh_sv[j & 3] : 0.0f;
+            }
+        }
+    }
     // padded leaves [max(l0, nb), l1): empty state, excluded everywhere
     if (tval) {
         for (int l = max(l0, nb); l < l1; ++l) {
@@ -603,23 +645,15 @@ __global__ __launch_bounds__(256, 2) void stats_kernel(const float* __restrict__
                 else
                     *(u32x2*)(vb + s * D + 16 * db + 4 * grp) = u32x2{0u, 0u};
             }
-            if (grp == 0) {
-                s_sg[w * 16 + col][l - l0] = 0.0f;
-                if (FP8) s_sv[w * 16 + col][l - l0] = 0.0f;
-                s_lz[w * 16 + col][l - l0] = -INFINITY;
-            }
         }
     }
-    __syncthreads();
-    {   // sg, lz of the workgroup's leaves: 64 contiguous bytes per tile
-        const int tt = threadIdx.x >> 2, qq = threadIdx.x & 3;
-        const int tq = tg * 64 + tt;
-        if (tq < nt && 4 * qq < l1 - l0) {
-            const int64_t s = ((int64_t)h * nt + tq) * nb_pad + l0 + 4 * qq;
-            if (!BF16) *(f32x4*)(sg + s) = *(const f32x4*)&s_sg[tt][4 * qq];
-            *(f32x4*)(lz + s) = *(const f32x4*)&s_lz[tt][4 * qq];
-            if (FP8) *(f32x4*)(sv + s) = *(const f32x4*)&s_sv[tt][4 * qq];
-        }
+    // sg, lz (sv) of the workgroup's leaves: lane grp writes leaves l0 + 4 grp .. + 3 (l1 - l0 is
+    // 16: nb_pad is a multiple of 32), the column's four lanes 64 contiguous bytes
+    if (tval && 4 * grp < l1 - l0) {
+        const int64_t s = th * nb_pad + l0 + 4 * grp;
+        if (!BF16) *(f32x4*)(sg + s) = kp_sg;
+        *(f32x4*)(lz + s) = kp_lz;
+        if (FP8) *(f32x4*)(sv + s) = kp_sv;
     }
 }
 
@@ -1375,9 +1409,9 @@ constexpr int DMA_W0 = 7;                           // loads per block, first wa
 constexpr int DMA_W1 = 6;                           // ... second wave
 constexpr int MAX_KX_LDS = 1024;                    // near leaves per tile the route kernel holds
 constexpr int MAX_PASSES = 3;                       // reference-max retries of a tile
-// Merge: the four wave pairs' partial O, 64 rows x 128 dims each, rows padded to 132 floats.
+// Merge: the wave pairs' partial O, 64 rows x 128 dims each, rows padded to 132 floats.
 constexpr int MRG_STRIDE = 132;
-static_assert(4 * 64 * MRG_STRIDE * 4 <= 4 * RING_SLOTS * SLOT_BYTES, "merge staging");
+constexpr int ROUTE_NP = 2;                         // wave pairs (key parts) per route workgroup
 
 // Per-lane byte offsets of the 32-key block loads (loop invariant): the QK operand chunk of
 // lane (col, grp) and the swizzled PV row chunks (see dma_rows).
@@ -1529,24 +1563,35 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
     if (kxe > 0) topk_row(keys, nb, kxe, sm, idx + gs * kxe, nullptr, nullptr);
 }
 
-template <int LEAF, int RB>    // RB = tile / 32: 16-row blocks per wave (tiles of 64 or 32 rows)
-__global__ __launch_bounds__(512) void route_kernel(
+// RB = tile / 32: 16-row blocks per wave (tiles of 64 or 32 rows); NP wave pairs split the keys.
+template <int LEAF, int RB, int NP>
+__global__ __launch_bounds__(128 * NP) void route_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ sq, const int8_t* __restrict__ dq8,
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ k8,
     const float* __restrict__ ks, const uint16_t* __restrict__ v, const int32_t* __restrict__ idx,
     const float* __restrict__ rowmax, int64_t nq, int nt, int group, int ng, const int32_t* __restrict__ perm, int64_t nk,
     int nb, int nb_pad, int kxe, float scale, float* __restrict__ out, float* __restrict__ logz) {
-    __shared__ __align__(16) char ring[4][RING_SLOTS][SLOT_BYTES];   // one per wave pair; also merge staging
-    __shared__ int32_t sidx[MAX_KX_LDS];
+    constexpr int NT = 128 * NP;                               // threads
+    __shared__ __align__(16) char ring[NP][RING_SLOTS][SLOT_BYTES];  // one per wave pair; also merge staging
+    __shared__ uint16_t sidx[MAX_KX_LDS];
     __shared__ uint32_t exbits[MAX_NB_LDS / 32 + 1];
-    __shared__ float red_m[64], red_l[4][64];
+    __shared__ float red_m[64], red_l[NP][64];
     __shared__ int redo;
+    static_assert(NP * 64 * MRG_STRIDE * 4 <= NP * RING_SLOTS * SLOT_BYTES, "merge staging");
     constexpr int TR = 32 * RB;                                // rows per tile
-    float* mrg = (float*)&ring[0][0][0];                       // merge staging: 4 x 64 x MRG_STRIDE floats
+    float* mrg = (float*)&ring[0][0][0];                       // merge staging: NP x 64 x MRG_STRIDE floats
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar bookkeeping
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    const int pr = wv & 3, hr = wv >> 2;                       // key quarter (wave pair), row half
+    const int pr = wv % NP, hr = wv / NP;                      // key part (wave pair), row half
+    auto row_total = [&](int r) {                              // a row's sum over the NP parts
+        if constexpr (NP == 4)
+            return __fadd_rn(__fadd_rn(red_l[0][r], red_l[1][r]), __fadd_rn(red_l[2][r], red_l[3][r]));
+        else if constexpr (NP == 2)
+            return __fadd_rn(red_l[0][r], red_l[1][r]);
+        else
+            return red_l[0][r];
+    };
     // 1-D grid over (tile, head), tile fastest: each XCD runs a contiguous run of tiles of one
     // head at a time, so the near-field leaves adjacent tiles share are fetched into one L2.
     const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
@@ -1559,11 +1604,11 @@ __global__ __launch_bounds__(512) void route_kernel(
     // exclusion bits: the selected (near) leaves, and every leaf >= nb, so the far loop needs no
     // range test (far blocks are 32-leaf aligned and a pair's range ends on a 32-leaf boundary
     // or at nb)
-    for (int i = threadIdx.x; i <= nb / 32; i += 512) {
+    for (int i = threadIdx.x; i <= nb / 32; i += NT) {
         const int past = nb - 32 * i;          // leaves of word i below nb
         exbits[i] = past >= 32 ? 0u : (past <= 0 ? ~0u : ~0u << past);
     }
-    for (int j = threadIdx.x; j < kxe; j += 512) sidx[j] = idx[gs * kxe + j];
+    for (int j = threadIdx.x; j < kxe; j += NT) sidx[j] = (uint16_t)idx[gs * kxe + j];
     float mref[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -1571,12 +1616,12 @@ __global__ __launch_bounds__(512) void route_kernel(
         mref[rb] = m == -INFINITY ? 0.0f : __fmul_rn(m, LOG2E);
     }
     __syncthreads();
-    for (int j = threadIdx.x; j < kxe; j += 512) atomicOr(&exbits[sidx[j] >> 5], 1u << (sidx[j] & 31));
+    for (int j = threadIdx.x; j < kxe; j += NT) atomicOr(&exbits[sidx[j] >> 5], 1u << (sidx[j] & 31));
     // ---- key ranges: pair q owns far leaves [q lpw, q lpw + lpw) and near list positions
     // [q epw, q epw + epw), in 32-key blocks; every wave runs the longest pair's step count
-    const int lpw = ((nb + 3) / 4 + 31) / 32 * 32;
+    const int lpw = ((nb + NP - 1) / NP + 31) / 32 * 32;
     const int e_n = kxe * LEAF;
-    const int epw = ((e_n + 3) / 4 + 31) / 32 * 32;
+    const int epw = ((e_n + NP - 1) / NP + 31) / 32 * 32;
     const int lo = pr * lpw, hi = min(nb, lo + lpw);
     const int e_lo = pr * epw, e_hi = min(e_n, e_lo + epw);
     const int nf = hi > lo ? (hi - lo + 31) / 32 : 0;
@@ -1775,7 +1820,7 @@ __global__ __launch_bounds__(512) void route_kernel(
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const int r = 16 * RB * hr + 16 * rb + col;
-            const float tot = __fadd_rn(__fadd_rn(red_l[0][r], red_l[1][r]), __fadd_rn(red_l[2][r], red_l[3][r]));
+            const float tot = row_total(r);
             if (!(tot >= 0x1p-60f && tot <= 0x1p64f)) {
                 bad = true;
                 mref[rb] = tot > 0.0f && tot <= 3.0e38f ? __fadd_rn(mref[rb], __log2f(tot))
@@ -1797,10 +1842,10 @@ __global__ __launch_bounds__(512) void route_kernel(
         for (int db = 0; db < 8; ++db) *(f32x4*)(dst + 16 * db) = st.o[rb][db];
     }
     __syncthreads();
-    constexpr int TPR = 512 / TR, DPT = D / TPR;                   // threads per row, dims per thread
+    constexpr int TPR = NT / TR, DPT = D / TPR;                    // threads per row, dims per thread
     const int r_out = threadIdx.x / TPR, part = threadIdx.x % TPR;
     const float den =
-        __fadd_rn(__fadd_rn(red_l[0][r_out], red_l[1][r_out]), __fadd_rn(red_l[2][r_out], red_l[3][r_out]));
+        row_total(r_out);
     const float inv = 1.0f / (den < 1e-30f ? 1e-30f : den);
     const int64_t qi = (int64_t)t * TR + r_out;
     if (qi < nq) {
@@ -1810,7 +1855,7 @@ __global__ __launch_bounds__(512) void route_kernel(
             const int dl = DPT * part + 4 * u;
             f32x4 acc = *(const f32x4*)(mrg + r_out * MRG_STRIDE + dl);
 #pragma unroll
-            for (int s = 1; s < 4; ++s) {
+            for (int s = 1; s < NP; ++s) {
                 const f32x4 y = *(const f32x4*)(mrg + (s * 64 + r_out) * MRG_STRIDE + dl);
                 acc = f32x4{__fadd_rn(acc[0], y[0]), __fadd_rn(acc[1], y[1]), __fadd_rn(acc[2], y[2]),
                             __fadd_rn(acc[3], y[3])};
@@ -2204,14 +2249,14 @@ int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
     const int lpb = 16;                    // stats_kernel's LPB
-    const int64_t nblocks = (nt + 63) / 64 * ((nbp + lpb - 1) / lpb) * heads;
+    const int64_t nblocks = (nt + STATS_TPW - 1) / STATS_TPW * ((nbp + lpb - 1) / lpb) * heads;
     REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats: too many tiles x leaves x heads for one launch");
     dim3 grid((unsigned)nblocks);
     hipStream_t s = (hipStream_t)stream;
 #define STATS_CASE(L)                                                                                         \
     case L:                                                                                                   \
-        hipLaunchKernelGGL(stats_kernel<L>, grid, dim3(256), 0, s, mu, (int)nt, k, v, nk, (int)nb, nbp, lpb, scale, \
-                           g8, sg, vb, nullptr, lz);                                                          \
+        hipLaunchKernelGGL((stats_kernel<L, 0, STATS_NW>), grid, dim3(64 * STATS_NW), 0, s, mu, (int)nt, k, v, nk, \
+                           (int)nb, nbp, lpb, scale, g8, sg, vb, nullptr, lz);                                \
         break;
     switch (leaf) {
         STATS_CASE(16)
@@ -2237,13 +2282,14 @@ int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, i
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
     const int lpb = 16;
-    const int64_t nblocks = (nt + 63) / 64 * ((nbp + lpb - 1) / lpb) * heads;
+    const int64_t nblocks = (nt + STATS_TPW - 1) / STATS_TPW * ((nbp + lpb - 1) / lpb) * heads;
     REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats_fp8: too many tiles x leaves x heads for one launch");
     dim3 grid((unsigned)nblocks);
     hipStream_t s = (hipStream_t)stream;
 #define STATS8_CASE(L)                                                                                         \
     case L:                                                                                                    \
-        hipLaunchKernelGGL((stats_kernel<L, 2>), grid, dim3(256), 0, s, mu, (int)nt, k, v, nk, (int)nb, nbp, lpb,    \
+        hipLaunchKernelGGL((stats_kernel<L, 2, STATS_NW>), grid, dim3(64 * STATS_NW), 0, s, mu, (int)nt, k, v, nk,   \
+                           (int)nb, nbp, lpb,                                                                  \
                            scale, (int8_t*)g, sg, (uint16_t*)vb, sv, lz);                                      \
         break;
     switch (leaf) {
@@ -2268,13 +2314,14 @@ int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, 
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
     const int lpb = 16;
-    const int64_t nblocks = (nt + 63) / 64 * ((nbp + lpb - 1) / lpb) * heads;
+    const int64_t nblocks = (nt + STATS_TPW - 1) / STATS_TPW * ((nbp + lpb - 1) / lpb) * heads;
     REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats_bf16: too many tiles x leaves x heads for one launch");
     dim3 grid((unsigned)nblocks);
     hipStream_t s = (hipStream_t)stream;
 #define STATSB_CASE(L)                                                                                         \
     case L:                                                                                                    \
-        hipLaunchKernelGGL((stats_kernel<L, 1>), grid, dim3(256), 0, s, mu, (int)nt, k, v, nk, (int)nb, nbp, lpb,    \
+        hipLaunchKernelGGL((stats_kernel<L, 1, STATS_NW>), grid, dim3(64 * STATS_NW), 0, s, mu, (int)nt, k, v, nk,   \
+                           (int)nb, nbp, lpb,                                                                  \
                            scale, (int8_t*)g, nullptr, vb, nullptr, lz);                                       \
         break;
     switch (leaf) {
@@ -2605,11 +2652,13 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
 #define ROUTE_CASE(L)                                                                                          \
     case L:                                                                                                    \
         if (tile == 64)                                                                                        \
-            hipLaunchKernelGGL((route_kernel<L, 2>), grid, dim3(512), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, \
-                               idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp, kxe, scale, out, logz); \
+            hipLaunchKernelGGL((route_kernel<L, 2, ROUTE_NP>), grid, dim3(128 * ROUTE_NP), 0, s, q8, sq, dq8, sdq, g8, sg, \
+                               lz, vb, k8, ks, v, idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp,   \
+                               kxe, scale, out, logz);                                                         \
         else                                                                                                   \
-            hipLaunchKernelGGL((route_kernel<L, 1>), grid, dim3(512), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, \
-                               idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp, kxe, scale, out, logz); \
+            hipLaunchKernelGGL((route_kernel<L, 1, ROUTE_NP>), grid, dim3(128 * ROUTE_NP), 0, s, q8, sq, dq8, sdq, g8, sg, \
+                               lz, vb, k8, ks, v, idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp,   \
+                               kxe, scale, out, logz);                                                         \
         break;
     switch (leaf) {
         ROUTE_CASE(16)
