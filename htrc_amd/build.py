@@ -23,6 +23,7 @@ HIPCC_FLAGS = [
     "-shared",
     "-fPIC",
     "-ffp-contract=off",                 # no FMA contraction: pack/select are bit-exact restatements
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",   # MFMA results in VGPRs: no accumulator-register copies
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
 ]

@@ -1381,15 +1381,17 @@ struct RowsN {         // softmax state of the 16 RB rows of one wave
 };
 
 // p = 2^(u - m) for the log2-domain scores u[rb][0..7] of the RB row blocks (keys
-// 16(e/4) + 4grp + e%4 of the block; masked keys -inf), l += p, O^T += V^T P^T.
-template <int RB>
+// 16(e/4) + 4grp + e%4 of the block; masked keys -inf), l += p, O^T += V^T P^T.  SHIFTED:
+// the scores are u - m already.
+template <int RB, bool SHIFTED>
 __device__ __forceinline__ void rows_update(RowsN<RB>& st, const float (&sc)[RB][8], const u32x2 (&v)[8][2]) {
     bf16x8 P[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         float p[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(__fsub_rn(sc[rb][e], st.m[rb]));
+        for (int e = 0; e < 8; ++e)
+            p[e] = __builtin_amdgcn_exp2f(SHIFTED ? sc[rb][e] : __fsub_rn(sc[rb][e], st.m[rb]));
         st.l[rb] = __fadd_rn(st.l[rb], __fadd_rn(__fadd_rn(__fadd_rn(p[0], p[1]), __fadd_rn(p[2], p[3])),
                                                  __fadd_rn(__fadd_rn(p[4], p[5]), __fadd_rn(p[6], p[7]))));
         P[rb] = to_bf16x8(p);
@@ -1720,7 +1722,7 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
                 for (int db = 0; db < 8; ++db)
 #pragma unroll
                     for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
-                rows_update<RB>(st, sc, pvop);
+                rows_update<RB, false>(st, sc, pvop);
             };
             issue(0, 0);
             issue(1, 1);
@@ -1776,16 +1778,17 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
                     const f32x4 ksv = *(const f32x4*)(slot + 12288 + 128 * hh + 16 * grp);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
+                        // score - m in one rounding
                         if constexpr (LEAF % 32 == 0) {   // the near list is whole 32-token blocks
 #pragma unroll
                             for (int rb = 0; rb < RB; ++rb)
-                                sc[rb][4 * hh + i] = __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]));
+                                sc[rb][4 * hh + i] = __fmaf_rn((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]), -st.m[rb]);
                         } else {                          // leaf 16: the last block may be half empty
                             const bool ok = (e0 + 16 * hh + 4 * grp + i) < e_hi;
-                            const float bias = ok ? 0.0f : -INFINITY;
 #pragma unroll
                             for (int rb = 0; rb < RB; ++rb)
-                                sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]), bias);
+                                sc[rb][4 * hh + i] = __fmaf_rn((float)acc[rb][i], __fmul_rn(srow[rb], ksv[i]),
+                                                               ok ? -st.m[rb] : -INFINITY);
                         }
                     }
                 }
@@ -1794,7 +1797,7 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
                 for (int db = 0; db < 8; ++db)
 #pragma unroll
                     for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
-                rows_update<RB>(st, sc, pvop);
+                rows_update<RB, true>(st, sc, pvop);
             };
             issue(0, 0);
             issue(1, 1);
