@@ -294,14 +294,17 @@ template <int LEAF, int NT>
 __device__ __forceinline__ void stage_leaf(const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
                                            int64_t key0, uint32_t lds0, uint32_t voff) {
     constexpr int NJ = 32 * LEAF / NT;          // 16-byte chunks per thread (K and V)
-    static_assert(NJ >= 1 && (32 * LEAF) % NT == 0 && NT % 256 == 0, "stage_leaf shape");
+    constexpr int RPJ = NT / 16;                // rows per chunk step; the wave's are 4 w .. 4 w + 3
+    static_assert(NJ >= 1 && (32 * LEAF) % NT == 0 && NT % 256 == 0 && NT <= 16 * LEAF, "stage_leaf shape");
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint16_t* Kw = K + (key0 + 4 * w) * D;
+    const uint16_t* Vw = V + (key0 + 4 * w) * D;
+    const uint32_t ldsw = lds0 + (uint32_t)w * 1024;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int s0 = j * NT + w * 64;         // the wave's first chunk
-        const uint16_t* X = s0 < LEAF * 16 ? K : V;
-        const int r0 = (s0 >> 4) % LEAF;
-        dma16s(X + (key0 + r0) * D, voff, lds0 + (uint32_t)s0 * 16);
+    for (int j = 0; j < NJ; ++j) {              // step j: chunks j NT .., rows (j RPJ) % LEAF + 4 w ..
+        const bool isk = j * NT < 16 * LEAF;
+        const int rj = (j * RPJ) % LEAF;
+        dma16s((isk ? Kw : Vw) + rj * D, voff, ldsw + (uint32_t)(j * NT) * 16);
     }
 }
 
