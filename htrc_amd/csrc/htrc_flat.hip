@@ -1748,21 +1748,24 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
                 asm volatile("" : : "v"(bq[rb][0]), "v"(bq[rb][1]), "v"(srow[rb]));
             }
             __syncthreads();            // every wave is done with the far blocks in the ring
-            auto tok_of = [&](int j) {  // first token of the 16-token run at list position j
-                const int jj = j < e_hi ? j : e_lo;
-                return kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[jj / LEAF]) * LEAF + (jj % LEAF);
-            };
-            auto issue = [&](int bi, int slot) {
+            // the 16-token runs of block bi start at list positions e_lo + 32 bi and + 16 (past
+            // e_hi: the range start again, loaded and masked); token = leaf * LEAF + position % LEAF
+            auto run_pos = [&](int j) { return j < e_hi ? j : e_lo; };
+            auto issue = [&](int bi, int slot, uint32_t la, uint32_t lb) {
                 if (bi >= nn) return;
-                const int e0 = e_lo + 32 * bi;
-                const int64_t r0 = tok_of(e0), r1 = tok_of(e0 + 16);
+                const int e0 = e_lo + 32 * bi, ja = run_pos(e0), jb = run_pos(e0 + 16);
+                const int64_t r0 = kh + (int64_t)__builtin_amdgcn_readfirstlane(la) * LEAF + (ja % LEAF);
+                const int64_t r1 = kh + (int64_t)__builtin_amdgcn_readfirstlane(lb) * LEAF + (jb % LEAF);
                 load_block(pring_lds + slot * SLOT_BYTES, k8, v, r0, r1, ks + r0, ks + r1, 3);
             };
             auto step = [&](auto S_, int bi) {
                 constexpr int S = decltype(S_)::value;
+                // leaves of block bi + 2, read before the waits so their LDS latency is hidden
+                const int en = e_lo + 32 * (bi + 2);
+                const uint32_t la = sidx[run_pos(en) / LEAF], lb = sidx[run_pos(en + 16) / LEAF];
                 if (bi < nn) wait_block(bi, nn);
                 __syncthreads();
-                issue(bi + 2, (S + 2) % RING_SLOTS);
+                issue(bi + 2, (S + 2) % RING_SLOTS, la, lb);
                 if (bi >= nn) return;
                 const char* slot = pring + S * SLOT_BYTES;
                 const int e0 = e_lo + 32 * bi;
@@ -1802,8 +1805,8 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
                     for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
                 rows_update<RB, true>(st, sc, pvop);
             };
-            issue(0, 0);
-            issue(1, 1);
+            issue(0, 0, sidx[run_pos(e_lo) / LEAF], sidx[run_pos(e_lo + 16) / LEAF]);
+            issue(1, 1, sidx[run_pos(e_lo + 32) / LEAF], sidx[run_pos(e_lo + 48) / LEAF]);
 #pragma unroll 1
             for (int bi = 0; bi < sn_steps; bi += RING_SLOTS) {
                 step(std::integral_constant<int, 0>{}, bi);
