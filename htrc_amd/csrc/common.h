@@ -118,15 +118,21 @@ __device__ __forceinline__ void rows_transpose(uint32_t (&x)[8]) {
 
 // Max across the 16 lanes of one group (the columns of an MFMA C tile) with DPP: xor 1,
 // xor 2 (quad permutes), then half-row and row mirrors; every lane ends with the maximum.
-template <int CTRL>
-__device__ __forceinline__ float dpp_max(float v) {
-    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xf, 0xf, false)));
-}
+// Four v_max_f32 with the DPP operand folded in (fmaxf on a DPP move costs a move, the DPP
+// move, a NaN-quieting max and the max); inputs are never NaN.  Each DPP read of a VGPR
+// written by the previous VALU instruction needs two wait states (s_nop 1).
 __device__ __forceinline__ float col_max(float v) {
-    v = dpp_max<0xB1>(v);     // quad_perm [1,0,3,2]
-    v = dpp_max<0x4E>(v);     // quad_perm [2,3,0,1]
-    v = dpp_max<0x141>(v);    // row_half_mirror
-    return dpp_max<0x140>(v);   // row_mirror
+    float r;
+    asm("s_nop 1\n\t"
+        "v_max_f32_dpp %0, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf"
+        : "=&v"(r) : "v"(v));
+    return r;
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 u) { return __builtin_bit_cast(bf16x8, u); }
