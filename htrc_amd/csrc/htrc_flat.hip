@@ -731,7 +731,7 @@ __global__ __launch_bounds__(256) void select_kernel(const int8_t* __restrict__ 
                     float best = -INFINITY;
 #pragma unroll
                     for (int rb = 0; rb < NRB; ++rb)
-                        if (val[rb]) best = fmaxf(best, __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i])));
+                        best = fmaxf(best, __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i])));   // rows past ts repeat row 0
                     bsel[lb][i] = fmaxf(bsel[lb][i], col_max(best));
                 }
             }
@@ -1155,7 +1155,7 @@ __global__ __launch_bounds__(256) void select16_kernel(const uint16_t* __restric
                     const float sc = __fmul_rn(sgv[i], 256.0f);
 #pragma unroll
                     for (int rb = 0; rb < NRB; ++rb)
-                        if (val[rb]) best = fmaxf(best, FP8 ? __fmul_rn(acc[rb][i], sc) : acc[rb][i]);
+                        best = fmaxf(best, FP8 ? __fmul_rn(acc[rb][i], sc) : acc[rb][i]);   // rows past ts repeat row 0
                     bsel[lb][i] = fmaxf(bsel[lb][i], col_max(best));
                 }
             }
@@ -1504,16 +1504,17 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
             acc[rb] = mfma_i8(o.a[0], b[rb][0], i32x4{0, 0, 0, 0});
             acc[rb] = mfma_i8(o.a[1], b[rb][1], acc[rb]);
         }
+        // No masks: rows past the sampled ones repeat row 0 (the maximum is unchanged; their
+        // rmax is never written), and leaves past nb have lz = -inf (sg = 0) in the state.
         float best[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const bool lv = c + 4 * grp + i < nb;
             best[i] = -INFINITY;
 #pragma unroll
             for (int rb = 0; rb < NRB; ++rb) {
                 const float x = __fmul_rn((float)acc[rb][i], __fmul_rn(srow[rb], o.sg[i]));
-                best[i] = fmaxf(best[i], val[rb] ? x : -INFINITY);
-                rmax[rb] = fmaxf(rmax[rb], lv ? __fadd_rn(x, o.lz[i]) : -INFINITY);
+                best[i] = fmaxf(best[i], x);
+                rmax[rb] = fmaxf(rmax[rb], __fadd_rn(x, o.lz[i]));
             }
             best[i] = col_max(best[i]);
         }
