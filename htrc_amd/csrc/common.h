@@ -59,6 +59,16 @@ __device__ __forceinline__ int round_even_clamp(float x) {
     return (int)y;
 }
 
+// x / s rounded to nearest from y = x / s's correctly rounded reciprocal y = RN(1 / s):
+// q = x y, r = x - q s (exact, one FMA), q + r y (Markstein's correction).  For |x| <= 127 s
+// (row quantisation: s = max|x| / 127) it equals the IEEE quotient whenever |x / s| >= 0.25,
+// and below that both round to the integer 0 (checked for every bf16 x against every bf16
+// row maximum and on 3.5e8 random fp32 pairs); three VALU operations instead of ten.
+__device__ __forceinline__ float div_by(float x, float s, float y) {
+    const float q = __fmul_rn(x, y);
+    return __fmaf_rn(__fmaf_rn(-q, s, x), y, q);
+}
+
 __device__ __forceinline__ float row_scale(float amax, float floor_) {
     float s = __fmul_rn(amax, R127);
     return s < floor_ ? floor_ : s;

@@ -153,11 +153,12 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
             continue;
         }
         const float s1 = row_scale(col_max(aq), 1e-20f), s2 = row_scale(col_max(ad), 1e-20f);
+        const float y1 = __fdiv_rn(1.0f, s1), y2 = __fdiv_rn(1.0f, s2);
         int cq[8], cd[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            cq[e] = round_away(__fdiv_rn(x[e], s1));
-            cd[e] = round_away(__fdiv_rn(d[e], s2));
+            cq[e] = round_away(div_by(x[e], s1, y1));
+            cd[e] = round_away(div_by(d[e], s2, y2));
         }
         *(u32x2*)(q8 + p * D + 8 * i) = pack8_i8(cq);
         *(u32x2*)(dq8 + p * D + 8 * i) = pack8_i8(cd);
@@ -188,9 +189,10 @@ __global__ __launch_bounds__(256) void pack_k_kernel(const uint16_t* __restrict_
 #pragma unroll
         for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(x[e]));
         const float sc = row_scale(col_max(a), 1e-20f);
+        const float y = __fdiv_rn(1.0f, sc);
         int c[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) c[e] = round_even_clamp(__fdiv_rn(x[e], sc));
+        for (int e = 0; e < 8; ++e) c[e] = round_even_clamp(div_by(x[e], sc, y));
         *(u32x2*)(k8 + (base + r) * D + 8 * i) = pack8_i8(c);
         if (i == 0) ks[base + r] = sc;
     }
