@@ -8,6 +8,11 @@ per-kernel figures, and the reference's CPU path (NumPy restatement of the torch
 _flat, h3/htrc_flat.py:279-388) timed on a bounded sample of the same workload.
 
   python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--config cfg3] [--no-cpu-baseline]
+
+--config cfg5 is BASELINE configuration 5 instead: 50 sequential cfg2-shape calls (fresh
+seeded inputs, seeds 0..49) reported as the total ms, and the ablation grid leaf
+{32, 64, 128} x near leaves {16, 32, 64} x Q/K dtype {int8, bf16} with each point's log-Z
+error and output rel-L2 against exact softmax attention (fp32 on the GPU).
 """
 from __future__ import annotations
 
@@ -119,13 +124,83 @@ def cpu_baseline(name, budget_s=10.0):
             "cpu": cpu_model, "os_cpu_count": os.cpu_count()}
 
 
+def exact_attention(q, k, v, scale, chunk=4096):
+    """Exact softmax attention of one head in fp32 on the GPU -> (out [N, d], logZ [N])."""
+    import torch
+    kt = k.float().t().contiguous()
+    vf = v.float().contiguous()
+    outs, lzs = [], []
+    for r0 in range(0, q.shape[0], chunk):
+        s_ = torch.matmul(q[r0:r0 + chunk].float().contiguous(), kt) * scale
+        lz = torch.logsumexp(s_, dim=1)
+        outs.append(torch.matmul(torch.exp(s_ - lz[:, None]), vf))
+        lzs.append(lz)
+    return torch.cat(outs), torch.cat(lzs)
+
+
+def sweep_cfg5(calls=50, warmup=2, leaves=(32, 64, 128), nears=(16, 32, 64), stores=("int8", "bf16"), reps=5):
+    """`calls` sequential cfg2-shape layer calls on fresh seeded inputs
+    (total ms) and the ablation grid, each point's error against exact softmax attention."""
+    import torch
+    from htrc_amd import htrc_flat, workloads
+    dev = torch.device("cuda:0")
+    data = [workloads.make("cfg2", seed=s, device=dev) for s in range(calls)]
+    _, _, _, leaf0, ex0 = data[0]
+    kw = dict(backend="hip", store="int8", dot="bf16", leaf=leaf0, exact_leaves=ex0)
+    ws = {}
+    for j in range(warmup):
+        q, k, v = data[j % calls][:3]
+        htrc_flat.flat_attention(q[0], k[0], v[0], ws=ws, **kw)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for q, k, v, _, _ in data:
+        htrc_flat.flat_attention(q[0], k[0], v[0], ws=ws, **kw)
+    e1.record()
+    torch.cuda.synchronize()
+    total = e0.elapsed_time(e1)
+    q, k, v = (x[0] for x in data[0][:3])
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    ref_out, ref_lz = exact_attention(q, k, v, scale)
+    grid = []
+    for leaf in leaves:
+        for near in nears:
+            for store in stores:
+                kwp = dict(backend="hip", store=store, dot="bf16", leaf=leaf, exact_leaves=near)
+                wsp = {}
+                out, lz = htrc_flat.flat_attention(q, k, v, ws=wsp, return_logz=True, **kwp)
+                a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a0.record()
+                for _ in range(reps):
+                    htrc_flat.flat_attention(q, k, v, ws=wsp, **kwp)
+                a1.record()
+                torch.cuda.synchronize()
+                err = (lz - ref_lz).abs()
+                grid.append({"leaf": leaf, "near_leaves": near, "qk": store, "ms": round(a0.elapsed_time(a1) / reps, 4),
+                             "logz_err_max": round(float(err.max()), 6), "logz_err_mean": round(float(err.mean()), 6),
+                             "out_rel_l2": round(float((out - ref_out).norm() / ref_out.norm()), 6)})
+    return total, grid
+
+
+def main_cfg5(a):
+    total, grid = sweep_cfg5(calls=a.calls)
+    res = {"metric": f"cfg5: {a.calls} sequential cfg2-shape flat-HTRC calls (seeds 0..{a.calls - 1}), total ms",
+           "value": round(total, 3), "unit": "ms", "n_gpus": 1, "steps": a.calls, "warmup": 2,
+           "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "i8/bf16 (fp32 accumulate)",
+           "data": "synthetic: clustered 64-token runs (cfg2 generator), seeds 0..49, generated on device",
+           "config": {"workload": f"cfg5: B=1 H=1 N=16384 d=128 leaf=64 near=16 tile=64, {a.calls} calls"},
+           "ablation": grid}
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4"])
+    ap.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5"])
     ap.add_argument("--kernel-reps", type=int, default=10)
+    ap.add_argument("--calls", type=int, default=50, help="cfg5: sequential layer calls")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calib-copy", action="store_true",
@@ -140,6 +215,8 @@ def main():
     from htrc_amd import htrc_flat, htrc_flat_hip as hip, workloads
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    if a.config == "cfg5":
+        return main_cfg5(a)
     dev = torch.device("cuda:0")
     q, k, v, leaf, ex = workloads.make(a.config, seed=0, device=dev)
     h, nq, d = (int(x) for x in q.shape)

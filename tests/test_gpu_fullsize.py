@@ -85,3 +85,19 @@ def test_fullsize_repeat_and_single_head_are_bit_identical(layer):
     o1, l1 = htrc_flat.flat_attention(q[h], k[h], v[h], tile=tile, leaf=leaf, exact_leaves=ex, return_logz=True, **KW)
     torch.cuda.synchronize()
     assert torch.equal(o1, out[h]) and torch.equal(l1, logz[h])
+
+
+def test_cfg5_sweep_reports_every_grid_point(device):
+    """BASELINE configuration 5 (bench.py --config cfg5) on a reduced grid: every point runs,
+    errors against exact softmax are finite and small, more near leaves never hurt much, and
+    the bf16 Q/K point is at least as close as the int8 one."""
+    import bench
+    total, grid = bench.sweep_cfg5(calls=3, warmup=1, leaves=(64,), nears=(16, 64), reps=1)
+    assert total > 0 and len(grid) == 4
+    for g in grid:
+        assert 0.0 <= g["logz_err_max"] < 0.5 and 0.0 <= g["out_rel_l2"] < 0.5 and g["ms"] > 0
+    by = {(g["near_leaves"], g["qk"]): g for g in grid}
+    for qk in ("int8", "bf16"):
+        assert by[(64, qk)]["out_rel_l2"] <= by[(16, qk)]["out_rel_l2"] * 1.05
+    for near in (16, 64):
+        assert by[(near, "bf16")]["out_rel_l2"] <= by[(near, "int8")]["out_rel_l2"] * 1.05
