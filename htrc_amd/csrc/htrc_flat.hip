@@ -1369,13 +1369,12 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm
 // route: the production path, two launches per layer call.
 //   route_select_kernel, one 4-wave workgroup per tile: SEL of every leaf into LDS (bit-exact,
 //     the select_kernel arithmetic), top-k -> idx, and each row's largest far-field score;
-//   route_kernel, one 8-wave workgroup per tile: far + near field in one online softmax whose
-//     reference max is that score.  Wave pair pr = wave % 4 takes a quarter of the keys (its
-//     far leaves, then its near tokens, in 32-key blocks) and wave wave / 4 of the pair takes
-//     half of the tile's rows (32 of 64, or 16 of 32): two waves share each SIMD, and each
-//     block in LDS feeds both.  A pair's
-//     blocks stream through a 3-slot LDS ring, loaded two blocks ahead by direct global->LDS
-//     loads split between the two waves; the four partial states merge through LDS.
+//   route_kernel, one 4-wave workgroup per tile (two per CU): far + near field in one online
+//     softmax whose reference max is that score.  Wave pair pr = wave % 2 takes half of the keys
+//     (its far leaves, then its near tokens, in 32-key blocks) and wave wave / 2 of the pair
+//     takes half of the tile's rows (32 of 64, or 16 of 32); each block in LDS feeds both.  A
+//     pair's blocks stream through a 2-slot LDS ring, loaded one block ahead by direct
+//     global->LDS loads split between the two waves; the two partial states merge through LDS.
 // SEL and the partial states never reach HBM.
 // ---------------------------------------------------------------------------------------------
 template <int RB>
@@ -1410,7 +1409,6 @@ __device__ __forceinline__ void rows_update(RowsN<RB>& st, const float (&sc)[RB]
 }
 
 // Ring slot of one 32-key block: [QK A operands 4 KB | PV rows 8 KB | scales 256 B].
-constexpr int RING_SLOTS = 3;
 constexpr int SLOT_BYTES = 4096 + 8192 + 256;
 constexpr int DMA_W0 = 7;                           // loads per block, first wave of a pair
 constexpr int DMA_W1 = 6;                           // ... second wave
@@ -1419,6 +1417,11 @@ constexpr int MAX_PASSES = 3;                       // reference-max retries of 
 // Merge: the wave pairs' partial O, 64 rows x 128 dims each, rows padded to 132 floats.
 constexpr int MRG_STRIDE = 132;
 constexpr int ROUTE_NP = 2;                         // wave pairs (key parts) per route workgroup
+// Ring slots per pair: blocks are loaded RS - 1 ahead.  Two slots (one block in flight while the
+// other is computed on) measured 1.8% faster than three at cfg3, and their 54 KB leave room for
+// a third workgroup per CU, which is slower again (register spills and contention).
+constexpr int ROUTE_RS = 2;
+constexpr int ROUTE_MINWG = 2;                      // waves per SIMD (= workgroups per CU) to fit
 
 // Per-lane byte offsets of the 32-key block loads (loop invariant): the QK operand chunk of
 // lane (col, grp) and the swizzled PV row chunks (see dma_rows).
@@ -1571,9 +1574,10 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
     if (kxe > 0) topk_row(keys, nb, kxe, sm, idx + gs * kxe, nullptr, nullptr);
 }
 
-// RB = tile / 32: 16-row blocks per wave (tiles of 64 or 32 rows); NP wave pairs split the keys.
-template <int LEAF, int RB, int NP>
-__global__ __launch_bounds__(128 * NP) void route_kernel(
+// RB = tile / 32: 16-row blocks per wave (tiles of 64 or 32 rows); NP wave pairs split the keys;
+// RS ring slots per pair.
+template <int LEAF, int RB, int NP, int RS>
+__global__ __launch_bounds__(128 * NP, ROUTE_MINWG) void route_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ sq, const int8_t* __restrict__ dq8,
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ k8,
@@ -1581,13 +1585,16 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
     const float* __restrict__ rowmax, int64_t nq, int nt, int group, int ng, const int32_t* __restrict__ perm, int64_t nk,
     int nb, int nb_pad, int kxe, float scale, float* __restrict__ out, float* __restrict__ logz) {
     constexpr int NT = 128 * NP;                               // threads
-    __shared__ __align__(16) char ring[NP][RING_SLOTS][SLOT_BYTES];  // one per wave pair; also merge staging
+    __shared__ __align__(16) char ring[NP][RS][SLOT_BYTES];    // one per wave pair; also merge staging
     __shared__ uint16_t sidx[MAX_KX_LDS];
     __shared__ uint32_t exbits[MAX_NB_LDS / 32 + 1];
     __shared__ float red_m[64], red_l[NP][64];
     __shared__ int redo;
-    static_assert(NP * 64 * MRG_STRIDE * 4 <= NP * RING_SLOTS * SLOT_BYTES, "merge staging");
     constexpr int TR = 32 * RB;                                // rows per tile
+    // merge staging in the ring: all rows at once, or one row half (one wave of each pair) at a time
+    constexpr bool MRG2 = NP * TR * MRG_STRIDE * 4 > NP * RS * SLOT_BYTES;
+    constexpr int RR = MRG2 ? TR / 2 : TR;                     // rows per merge round
+    static_assert(NP * RR * MRG_STRIDE * 4 <= NP * RS * SLOT_BYTES, "merge staging");
     float* mrg = (float*)&ring[0][0][0];                       // merge staging: NP x 64 x MRG_STRIDE floats
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar bookkeeping
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
@@ -1640,7 +1647,7 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
     char* pring = &ring[pr][0][0];
     const uint32_t pring_lds = lds_addr(pring);
     auto wait_block = [&](int bi, int nblk) {    // this wave's loads of block bi have landed
-        if (bi + 1 < nblk) {
+        if (RS == 3 && bi + 1 < nblk) {             // block bi + 1 may still be in flight
             if (hr == 0) wait_vmcnt<DMA_W0>();
             else wait_vmcnt<DMA_W1>();
         } else {
@@ -1690,13 +1697,13 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
                 const int64_t r0 = srow0 + lo + 32 * bi;
                 load_block(pring_lds + slot * SLOT_BYTES, g8, vb, r0, r0 + 16, sg + r0, lz + r0, 7);
             };
-            // one step per 32-leaf block; the ring slot of block bi is bi % 3, a constant in each
-            // of the three unrolled steps, so every LDS read uses an immediate offset
+            // one step per 32-leaf block; the ring slot of block bi is bi % RS, a constant in each
+            // of the RS unrolled steps, so every LDS read uses an immediate offset
             auto step = [&](auto S_, int bi) {
                 constexpr int S = decltype(S_)::value;
                 if (bi < nf) wait_block(bi, nf);
-                __syncthreads();        // the partner's loads have landed too; slot (bi + 2) % 3 is free
-                issue(bi + 2, (S + 2) % RING_SLOTS);
+                __syncthreads();        // the partner's loads have landed too; slot (bi - 1) % RS is free
+                issue(bi + RS - 1, (S + RS - 1) % RS);
                 if (bi >= nf) return;
                 const char* slot = pring + S * SLOT_BYTES;
                 const int c0 = lo + 32 * bi;
@@ -1731,12 +1738,13 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
                 rows_update<RB, false>(st, sc, pvop);
             };
             issue(0, 0);
-            issue(1, 1);
+            if (RS == 3) issue(1, 1);
 #pragma unroll 1
-            for (int bi = 0; bi < sf_steps; bi += RING_SLOTS) {
+            for (int bi = 0; bi < sf_steps; bi += RS) {
                 step(std::integral_constant<int, 0>{}, bi);
                 if (bi + 1 < sf_steps) step(std::integral_constant<int, 1>{}, bi + 1);
-                if (bi + 2 < sf_steps) step(std::integral_constant<int, 2>{}, bi + 2);
+                if constexpr (RS == 3)
+                    if (bi + 2 < sf_steps) step(std::integral_constant<int, 2 % RS>{}, bi + 2);
             }
         }
         {   // ---- near field: S^T = k8 q8^T, score = dot * sq * ks * scale
@@ -1763,12 +1771,12 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
             };
             auto step = [&](auto S_, int bi) {
                 constexpr int S = decltype(S_)::value;
-                // leaves of block bi + 2, read before the waits so their LDS latency is hidden
-                const int en = e_lo + 32 * (bi + 2);
+                // leaves of block bi + RS - 1, read before the waits so their LDS latency is hidden
+                const int en = e_lo + 32 * (bi + RS - 1);
                 const uint32_t la = sidx[run_pos(en) / LEAF], lb = sidx[run_pos(en + 16) / LEAF];
                 if (bi < nn) wait_block(bi, nn);
                 __syncthreads();
-                issue(bi + 2, (S + 2) % RING_SLOTS, la, lb);
+                issue(bi + RS - 1, (S + RS - 1) % RS, la, lb);
                 if (bi >= nn) return;
                 const char* slot = pring + S * SLOT_BYTES;
                 const int e0 = e_lo + 32 * bi;
@@ -1809,15 +1817,16 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
                 rows_update<RB, true>(st, sc, pvop);
             };
             issue(0, 0, sidx[run_pos(e_lo) / LEAF], sidx[run_pos(e_lo + 16) / LEAF]);
-            issue(1, 1, sidx[run_pos(e_lo + 32) / LEAF], sidx[run_pos(e_lo + 48) / LEAF]);
+            if (RS == 3) issue(1, 1, sidx[run_pos(e_lo + 32) / LEAF], sidx[run_pos(e_lo + 48) / LEAF]);
 #pragma unroll 1
-            for (int bi = 0; bi < sn_steps; bi += RING_SLOTS) {
+            for (int bi = 0; bi < sn_steps; bi += RS) {
                 step(std::integral_constant<int, 0>{}, bi);
                 if (bi + 1 < sn_steps) step(std::integral_constant<int, 1>{}, bi + 1);
-                if (bi + 2 < sn_steps) step(std::integral_constant<int, 2>{}, bi + 2);
+                if constexpr (RS == 3)
+                    if (bi + 2 < sn_steps) step(std::integral_constant<int, 2 % RS>{}, bi + 2);
             }
         }
-        // Row totals over the four key quarters (all at the same reference).  A total outside
+        // Row totals over the NP key parts (all at the same reference).  A total outside
         // [2^-60, 2^64] means the reference missed the row's maximum by more than 60 octaves
         // (never observed on real scores): every p <= total, so the pass is redone with the
         // reference moved to m + log2(total).
@@ -1844,38 +1853,44 @@ __global__ __launch_bounds__(128 * NP) void route_kernel(
         if (redo == 0 || pass + 1 == MAX_PASSES) break;
     }
     // ---- merge: every pair used the same reference per row, so the partial sums simply add
-    // (h3/htrc_flat_triton.py:263-273 with equal maxima)
+    // (h3/htrc_flat_triton.py:263-273 with equal maxima).  MRG2: two rounds, the rows of row
+    // half 0, then of row half 1, so the staging fits a 2-slot ring.
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        const int r = 16 * RB * hr + 16 * rb + col;
-        if (pr == 0 && grp == 0) red_m[r] = st.m[rb];
-        float* dst = mrg + (pr * 64 + r) * MRG_STRIDE + 4 * grp;
+    for (int round = 0; round < (MRG2 ? 2 : 1); ++round) {
+        if (!MRG2 || hr == round) {
 #pragma unroll
-        for (int db = 0; db < 8; ++db) *(f32x4*)(dst + 16 * db) = st.o[rb][db];
-    }
-    __syncthreads();
-    constexpr int TPR = NT / TR, DPT = D / TPR;                    // threads per row, dims per thread
-    const int r_out = threadIdx.x / TPR, part = threadIdx.x % TPR;
-    const float den =
-        row_total(r_out);
-    const float inv = 1.0f / (den < 1e-30f ? 1e-30f : den);
-    const int64_t qi = (int64_t)t * TR + r_out;
-    if (qi < nq) {
-        const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
+            for (int rb = 0; rb < RB; ++rb) {
+                const int r = 16 * RB * hr + 16 * rb + col;
+                if (pr == 0 && grp == 0) red_m[r] = st.m[rb];
+                float* dst = mrg + (pr * RR + r - round * RR) * MRG_STRIDE + 4 * grp;
 #pragma unroll
-        for (int u = 0; u < DPT / 4; ++u) {
-            const int dl = DPT * part + 4 * u;
-            f32x4 acc = *(const f32x4*)(mrg + r_out * MRG_STRIDE + dl);
-#pragma unroll
-            for (int s = 1; s < NP; ++s) {
-                const f32x4 y = *(const f32x4*)(mrg + (s * 64 + r_out) * MRG_STRIDE + dl);
-                acc = f32x4{__fadd_rn(acc[0], y[0]), __fadd_rn(acc[1], y[1]), __fadd_rn(acc[2], y[2]),
-                            __fadd_rn(acc[3], y[3])};
+                for (int db = 0; db < 8; ++db) *(f32x4*)(dst + 16 * db) = st.o[rb][db];
             }
-            *(f32x4*)(out + orow * D + dl) = f32x4{__fmul_rn(acc[0], inv), __fmul_rn(acc[1], inv),
-                                                   __fmul_rn(acc[2], inv), __fmul_rn(acc[3], inv)};
         }
-        if (part == 0) logz[orow] = __fadd_rn(__fmul_rn(red_m[r_out], LN2), __logf(den));   // m in log2 units
+        __syncthreads();
+        constexpr int TPR = NT / RR, DPT = D / TPR;                // threads per row, dims per thread
+        const int r_loc = threadIdx.x / TPR, part = threadIdx.x % TPR, r_out = round * RR + r_loc;
+        const float den = row_total(r_out);
+        const float inv = 1.0f / (den < 1e-30f ? 1e-30f : den);
+        const int64_t qi = (int64_t)t * TR + r_out;
+        if (qi < nq) {
+            const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
+#pragma unroll
+            for (int u = 0; u < DPT / 4; ++u) {
+                const int dl = DPT * part + 4 * u;
+                f32x4 acc = *(const f32x4*)(mrg + r_loc * MRG_STRIDE + dl);
+#pragma unroll
+                for (int s = 1; s < NP; ++s) {
+                    const f32x4 y = *(const f32x4*)(mrg + (s * RR + r_loc) * MRG_STRIDE + dl);
+                    acc = f32x4{__fadd_rn(acc[0], y[0]), __fadd_rn(acc[1], y[1]), __fadd_rn(acc[2], y[2]),
+                                __fadd_rn(acc[3], y[3])};
+                }
+                *(f32x4*)(out + orow * D + dl) = f32x4{__fmul_rn(acc[0], inv), __fmul_rn(acc[1], inv),
+                                                       __fmul_rn(acc[2], inv), __fmul_rn(acc[3], inv)};
+            }
+            if (part == 0) logz[orow] = __fadd_rn(__fmul_rn(red_m[r_out], LN2), __logf(den));   // m in log2 units
+        }
+        if (MRG2 && round == 0) __syncthreads();                   // the staging is reused
     }
 }
 
@@ -2664,11 +2679,11 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
 #define ROUTE_CASE(L)                                                                                          \
     case L:                                                                                                    \
         if (tile == 64)                                                                                        \
-            hipLaunchKernelGGL((route_kernel<L, 2, ROUTE_NP>), grid, dim3(128 * ROUTE_NP), 0, s, q8, sq, dq8, sdq, g8, sg, \
+            hipLaunchKernelGGL((route_kernel<L, 2, ROUTE_NP, ROUTE_RS>), grid, dim3(128 * ROUTE_NP), 0, s, q8, sq, dq8, sdq, g8, sg, \
                                lz, vb, k8, ks, v, idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp,   \
                                kxe, scale, out, logz);                                                         \
         else                                                                                                   \
-            hipLaunchKernelGGL((route_kernel<L, 1, ROUTE_NP>), grid, dim3(128 * ROUTE_NP), 0, s, q8, sq, dq8, sdq, g8, sg, \
+            hipLaunchKernelGGL((route_kernel<L, 1, ROUTE_NP, ROUTE_RS>), grid, dim3(128 * ROUTE_NP), 0, s, q8, sq, dq8, sdq, g8, sg, \
                                lz, vb, k8, ks, v, idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp,   \
                                kxe, scale, out, logz);                                                         \
         break;
