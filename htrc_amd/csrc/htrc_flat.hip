@@ -86,8 +86,13 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
                                                      float* __restrict__ mu, int8_t* __restrict__ q8,
                                                      float* __restrict__ sq, int8_t* __restrict__ dq8,
                                                      float* __restrict__ sdq) {
-    __shared__ __align__(16) float tq[TILE][D + 4];
+    // the tile's rows as loaded (bf16 rows padded by 16 bytes, fp32 rows by 16 bytes): 17 KB for
+    // bf16 input, so eight workgroups share a CU and hide each other's load latency
+    using TQ = typename std::conditional<IN_BF16, uint16_t, float>::type;
+    constexpr int TQP = IN_BF16 ? 8 : 4;
+    __shared__ __align__(16) TQ tq[TILE][D + TQP];
     __shared__ __align__(16) float smu[D];
+    auto tq_at = [&](int r, int c) { return IN_BF16 ? bf2f(tq[r][c]) : (float)tq[r][c]; };
     const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const int64_t r0 = (int64_t)t * tile;
     const int nr = (int)(nq - r0 < tile ? nq - r0 : tile);
@@ -98,24 +103,19 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
         const int c = tid + 256 * j, r = c >> 4, c8 = (c & 15) * 8;
         const int64_t pr = r0 + r < nq ? r0 + r : nq - 1;                      // pad rows repeat the last row
         const int64_t src = qbase + perm_row(perm, h, nq, pr) * D + c8;
-        f32x4 lo, hi;
-        if (IN_BF16) {
-            const u32x4 u = *(const u32x4*)((const uint16_t*)qin + src);
-            lo = f32x4{bf2f(u.x & 0xffffu), bf2f(u.x >> 16), bf2f(u.y & 0xffffu), bf2f(u.y >> 16)};
-            hi = f32x4{bf2f(u.z & 0xffffu), bf2f(u.z >> 16), bf2f(u.w & 0xffffu), bf2f(u.w >> 16)};
+        if constexpr (IN_BF16) {
+            *(u32x4*)&tq[r][c8] = *(const u32x4*)((const uint16_t*)qin + src);
         } else {
-            lo = *(const f32x4*)((const float*)qin + src);
-            hi = *(const f32x4*)((const float*)qin + src + 4);
+            *(f32x4*)&tq[r][c8] = *(const f32x4*)((const float*)qin + src);
+            *(f32x4*)&tq[r][c8 + 4] = *(const f32x4*)((const float*)qin + src + 4);
         }
-        *(f32x4*)&tq[r][c8] = lo;
-        *(f32x4*)&tq[r][c8 + 4] = hi;
     }
     __syncthreads();
     const int64_t tg = (int64_t)h * nt + t;
     if (tid < D) {
         if (group == 1) {
             float s = 0.0f;
-            for (int r = 0; r < nr; ++r) s = __fadd_rn(s, tq[r][tid]);
+            for (int r = 0; r < nr; ++r) s = __fadd_rn(s, tq_at(r, tid));
             const float m = __fdiv_rn(s, (float)nr);
             smu[tid] = m;
             mu[tg * D + tid] = m;
@@ -133,9 +133,20 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
     for (int it = 0; it < 4; ++it) {
         const int r = 16 * w + 4 * it + g;         // row of this 16-lane group
         float x[8], d[8], aq = 0.0f, ad = 0.0f;
+        if constexpr (IN_BF16) {
+            const u32x4 u = *(const u32x4*)&tq[r][8 * i];
+            const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[2 * e] = __uint_as_float(w4[e] << 16);
+                x[2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = tq[r][8 * i + e];
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            x[e] = tq[r][8 * i + e];
             d[e] = __fsub_rn(x[e], m[e]);
             aq = fmaxf(aq, fabsf(x[e]));
             ad = fmaxf(ad, fabsf(d[e]));
@@ -201,10 +212,10 @@ __global__ __launch_bounds__(256) void pack_k_kernel(const uint16_t* __restrict_
 // ---------------------------------------------------------------------------------------------
 // stats: leaf statistics at the tile centres (h3/htrc_flat_triton.py:41-85, I8 store).
 // Workgroup = 64 tile centres (16 per wave) x a range of leaves of one head.  Per leaf:
-//   a^T = K_l mu^T                      bf16 MFMA, mu split into three bf16 terms (~fp32)
+//   a^T = K_l mu^T                      bf16 MFMA, mu split into two bf16 terms (~16 bits)
 //   e = exp(a - max) per centre (lane%16 = centre), z = sum e
-//   g^T = K_l^T w_g^T, vb^T = V_l^T w_v^T   w_g = e * scale / z in three bf16 terms,
-//                                            w_v = e / z in two
+//   g^T = K_l^T w^T, vb^T = V_l^T w^T   w = e / z in two bf16 terms shared by both products
+//                                        (g = scale * K_l^T w^T)
 // The leaf's K and V rows are staged in LDS (XOR-swizzled 16-byte chunks) by gfx950 direct
 // global->LDS loads one leaf ahead; the QK operand is a plain 16-byte read, the PV-type
 // operands come from the same rows through transposing reads.  Each leaf's outputs are
