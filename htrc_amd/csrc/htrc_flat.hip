@@ -1734,11 +1734,15 @@ __global__ __launch_bounds__(128 * NP, ROUTE_MINWG) void route_kernel(
                     const f32x4 lzv = *(const f32x4*)(slot + 12288 + 128 + (16 * hh + 4 * grp) * 4);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const bool ok = ((exw >> (16 * hh + i)) & 1u) == 0u;
-                        const float bias = ok ? __fmul_rn(lzv[i], LOG2E) : -INFINITY;
+                        // excluded key: lz -> -inf, one bit select (v_bfi_b32) on the sign-extended bit
+                        const uint32_t ex = (uint32_t)__builtin_amdgcn_sbfe((int)exw, 16 * hh + i, 1);
+                        uint32_t lzb;
+                        asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(lzb) : "v"(ex), "v"(0xff800000u), "v"(__float_as_uint(lzv[i])));
+                        const float lzm = __uint_as_float(lzb);
 #pragma unroll
-                        for (int rb = 0; rb < RB; ++rb)
-                            sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i]), bias);
+                        for (int rb = 0; rb < RB; ++rb)   // score - m: the bias lz log2e - m in one rounding
+                            sc[rb][4 * hh + i] = fmaf((float)acc[rb][i], __fmul_rn(srow[rb], sgv[i]),
+                                                      __fmaf_rn(lzm, LOG2E, -st.m[rb]));
                     }
                 }
                 u32x2 pvop[8][2];
@@ -1746,7 +1750,7 @@ __global__ __launch_bounds__(128 * NP, ROUTE_MINWG) void route_kernel(
                 for (int db = 0; db < 8; ++db)
 #pragma unroll
                     for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
-                rows_update<RB, false>(st, sc, pvop);
+                rows_update<RB, true>(st, sc, pvop);
             };
             issue(0, 0);
             if (RS == 3) issue(1, 1);
