@@ -85,6 +85,52 @@ def roofline_entry(name, ms, fig):
     return e
 
 
+def measured_peaks(dev, reps=5):
+    """Rates torch reaches on this GPU, beside the spec peaks, as tools/profile_flat_kernel.py:43-65
+    measures them for the reference: a device copy of 1 GiB (read + write bytes / time), a bf16
+    GEMM 8192^3 (torch.matmul, hipBLASLt), the skinny batched product of the tile kernel's shape
+    (640 x [64,128] @ [128,2560], bf16), and an int8 GEMM 8192^3 (torch._int_mm) for this path's
+    QK dtype; None for a rate this torch build cannot produce."""
+    import torch
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3
+
+    res = {}
+    src = torch.empty(1 << 28, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    res["copy_GBps"] = round(2 * src.numel() * 4 / timed(lambda: dst.copy_(src)) / 1e9, 1)
+    del src, dst
+    n = 8192
+    a = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+    res["bf16_gemm_TFLOPs"] = round(2 * n ** 3 / timed(lambda: torch.matmul(a, b)) / 1e12, 1)
+    del a, b
+    qs = torch.randn(640, 64, 128, device=dev, dtype=torch.bfloat16)
+    ks = torch.randn(640, 128, 2560, device=dev, dtype=torch.bfloat16)    # contiguous right operand
+    res["bmm_64x128x2560_TFLOPs"] = round(2 * 640 * 64 * 128 * 2560 / timed(lambda: torch.bmm(qs, ks)) / 1e12, 1)
+    del qs, ks
+    try:
+        a8 = torch.randint(-127, 128, (n, n), device=dev, dtype=torch.int8)
+        b8 = torch.randint(-127, 128, (n, n), device=dev, dtype=torch.int8)
+        res["int8_gemm_TOPs"] = round(2 * n ** 3 / timed(lambda: torch._int_mm(a8, b8)) / 1e12, 1)
+        del a8, b8
+    except (RuntimeError, AttributeError, NotImplementedError) as err:
+        res["int8_gemm_TOPs"] = None
+        res["int8_gemm_error"] = str(err).splitlines()[0][:200]
+    torch.cuda.empty_cache()
+    res["cu_count"] = torch.cuda.get_device_properties(dev).multi_processor_count
+    return res
+
+
 def cpu_baseline(name, budget_s=10.0):
     """Reference CPU path (NumPy restatement of _flat) on whole heads until budget_s has
     elapsed; extrapolated to the layer's head count."""
@@ -280,6 +326,13 @@ def main():
         del src, dst
     figs = algorithmic(h, nq, nk, leaf, kx, d)
     kernels = {n: roofline_entry(n, kms[n], figs[n]) for n in stages}
+    peaks = measured_peaks(dev)
+    for n, e in kernels.items():        # the same figures against the measured rates
+        e["hbm_frac_measured"] = round(e["hbm_GBps"] / peaks["copy_GBps"], 4)
+        if "mfma_frac" in e and peaks.get("int8_gemm_TOPs"):
+            t = figs[n]["i8_ops"] / (peaks["int8_gemm_TOPs"] * 1e12) + figs[n]["bf16_flops"] / (
+                peaks["bf16_gemm_TFLOPs"] * 1e12)
+            e["mfma_frac_measured"] = round(t / (e["ms"] * 1e-3), 4)
     traffic = measured_traffic(a.config)
     for n, e in kernels.items():
         e["traffic"] = traffic.get(n)
@@ -296,13 +349,18 @@ def main():
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic.get(dom["kernel"]),
                 "kernel": dom["kernel"], "note": "bf16-equivalent: int8 ops weighted by 2.5/5.0"}
+    if roof["bound"] == "hbm":
+        roof["measured_peak"] = peaks["copy_GBps"]
+        roof["frac_measured"] = dom["hbm_frac_measured"]
+    elif "mfma_frac_measured" in dom:
+        roof["frac_measured"] = dom["mfma_frac_measured"]
     res = {"metric": METRIC, "value": round(ms, 4), "unit": "ms/call", "n_gpus": 1, "steps": a.steps,
            "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
            "vs_baseline": None, "dtype": "i8/bf16 (fp32 accumulate)",
            "data": "synthetic: clustered spatiotemporal regions, seed 0, generated on device",
            "config": {"workload": f"{a.config}: B=1 H={h} N={nq} d={d} leaf={leaf} near={kx} tile=64",
                       "heads": h, "queries": nq, "keys": nk, "leaf": leaf, "near_leaves": kx},
-           "roofline": roof, "kernels": kernels}
+           "roofline": roof, "kernels": kernels, "measured_peaks": peaks}
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(a.config, a.cpu_budget)
     print(json.dumps(res), flush=True)
