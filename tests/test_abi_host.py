@@ -132,6 +132,16 @@ def test_flat_attention_shape_errors_and_no_cpu_fallback():
         htrc_flat.flat_attention_prod(q, k, v, leaf=16, exact_leaves=2)
 
 
+def test_missing_library_raises_instead_of_falling_back(monkeypatch, tmp_path):
+    """Without the built library every launcher raises: there is no CPU or torch path to take."""
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIBPATH", tmp_path / "libhtrc_flat.so")
+    with pytest.raises(RuntimeError, match="no fallback"):
+        _lib.lib()
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.call("htrc_abi_version")
+
+
 def test_prod_knobs_match_reference():
     assert htrc_flat.PROD == dict(tile=64, exact_leaves=256, tile_chunk=128, backend="triton", precision="tf32",
                                   store="int8", dot="bf16", splits=4,
