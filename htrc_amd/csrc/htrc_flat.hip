@@ -22,6 +22,7 @@
 
 #include <stdio.h>
 #include <string.h>
+#include <atomic>
 
 using namespace htrc;
 
@@ -381,14 +382,13 @@ template <int LEAF, int STORE, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restrict__ mu, int nt,
                                                        const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v, int64_t nk, int nb,
-                                                       int nb_pad, int lpb, float scale,
+                                                       int nb_pad, int lpb, float scale,   // lpb: 4, 8 or 16
                                                        int8_t* __restrict__ g8, float* __restrict__ sg,
                                                        uint16_t* __restrict__ vb, float* __restrict__ sv,
                                                        float* __restrict__ lz) {
     constexpr int KB = LEAF / 16;                 // 16-key blocks per leaf
     constexpr int KK = (LEAF + 31) / 32;          // 32-key MFMA k-steps per leaf
     constexpr int LEAF_BYTES = 32 * LEAF * 16;
-    constexpr int LPB = 16;                       // leaves per workgroup (the launcher's lpb)
     constexpr bool FP8 = STORE == 2, BF16 = STORE == 1;
     constexpr int TPW = 16 * NW;                  // centres per workgroup
     __shared__ __align__(16) char lds[2 * LEAF_BYTES];
@@ -2279,6 +2279,32 @@ int htrc_pack_k(const uint16_t* k, int64_t heads, int64_t nk, int d, int8_t* k8,
     return launched("htrc_pack_k");
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+    if (dev < 64) {
+        const int c = cache[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+// Leaves per stats workgroup: 16, or 8 / 4 when 16 would give the device fewer than two
+// workgroups per CU (small layers: more, shorter workgroups).  A multiple of 4 (the kernel's
+// sg/lz shift register keeps four leaves per lane group) that divides nb_pad (a multiple of 32).
+static int stats_lpb(int64_t nt, int nbp, int64_t heads) {
+    const int64_t ntg = (nt + STATS_TPW - 1) / STATS_TPW;
+    const int64_t want = 2 * (int64_t)device_cus();
+    for (int lpb = 16; lpb > 4; lpb /= 2)
+        if (ntg * ((nbp + lpb - 1) / lpb) * heads >= want) return lpb;
+    return 4;
+}
+
 int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
                     int leaf, int d, float scale, int8_t* g8, float* sg, uint16_t* vb, float* lz, void* stream) {
     REQUIRE(mu && k && v && g8 && sg && vb && lz, "htrc_leaf_stats: null pointer");
@@ -2290,7 +2316,7 @@ int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64
             "htrc_leaf_stats: misaligned buffer");
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
-    const int lpb = 16;                    // stats_kernel's LPB
+    const int lpb = stats_lpb(nt, nbp, heads);
     const int64_t nblocks = (nt + STATS_TPW - 1) / STATS_TPW * ((nbp + lpb - 1) / lpb) * heads;
     REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats: too many tiles x leaves x heads for one launch");
     dim3 grid((unsigned)nblocks);
@@ -2323,7 +2349,7 @@ int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, i
             "htrc_leaf_stats_fp8: misaligned buffer");
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
-    const int lpb = 16;
+    const int lpb = stats_lpb(nt, nbp, heads);
     const int64_t nblocks = (nt + STATS_TPW - 1) / STATS_TPW * ((nbp + lpb - 1) / lpb) * heads;
     REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats_fp8: too many tiles x leaves x heads for one launch");
     dim3 grid((unsigned)nblocks);
@@ -2355,7 +2381,7 @@ int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, 
             "htrc_leaf_stats_bf16: misaligned buffer");
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
-    const int lpb = 16;
+    const int lpb = stats_lpb(nt, nbp, heads);
     const int64_t nblocks = (nt + STATS_TPW - 1) / STATS_TPW * ((nbp + lpb - 1) / lpb) * heads;
     REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats_bf16: too many tiles x leaves x heads for one launch");
     dim3 grid((unsigned)nblocks);
