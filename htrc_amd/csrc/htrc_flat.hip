@@ -1380,12 +1380,14 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm
 // route: the production path, two launches per layer call.
 //   route_select_kernel, one 4-wave workgroup per tile: SEL of every leaf into LDS (bit-exact,
 //     the select_kernel arithmetic), top-k -> idx, and each row's largest far-field score;
-//   route_kernel, one 4-wave workgroup per tile (two per CU): far + near field in one online
-//     softmax whose reference max is that score.  Wave pair pr = wave % 2 takes half of the keys
-//     (its far leaves, then its near tokens, in 32-key blocks) and wave wave / 2 of the pair
+//   route_kernel, one workgroup per tile: far + near field in one online softmax whose
+//     reference max is that score.  NP wave pairs split the keys (large grids: one pair, all
+//     keys, four tiles per CU; small grids: two pairs, key halves): pair pr = wave % NP takes
+//     its far leaves, then its near tokens, in 32-key blocks, and wave wave / NP of the pair
 //     takes half of the tile's rows (32 of 64, or 16 of 32); each block in LDS feeds both.  A
 //     pair's blocks stream through a 2-slot LDS ring, loaded one block ahead by direct
-//     global->LDS loads split between the two waves; the two partial states merge through LDS.
+//     global->LDS loads split between the two waves; the pairs' partial states merge through
+//     LDS.
 // SEL and the partial states never reach HBM.
 // ---------------------------------------------------------------------------------------------
 template <int RB>
@@ -1427,7 +1429,6 @@ constexpr int MAX_KX_LDS = 1024;                    // near leaves per tile the 
 constexpr int MAX_PASSES = 3;                       // reference-max retries of a tile
 // Merge: the wave pairs' partial O, 64 rows x 128 dims each, rows padded to 132 floats.
 constexpr int MRG_STRIDE = 132;
-constexpr int ROUTE_NP = 2;                         // wave pairs (key parts) per route workgroup
 // Ring slots per pair: blocks are loaded RS - 1 ahead.  Two slots (one block in flight while the
 // other is computed on) measured 1.8% faster than three at cfg3, and their 54 KB leave room for
 // a third workgroup per CU, which is slower again (register spills and contention).
@@ -2717,16 +2718,23 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
     const int nbp = htrc_nb_pad(nb);
     const dim3 grid((unsigned)(nt * heads));
     hipStream_t s = (hipStream_t)stream;
+    // One wave pair per tile (all of its keys; four tiles per CU) when the grid gives every CU
+    // at least two tiles, two pairs (key halves merged in LDS) for smaller grids, which the
+    // tiles alone cannot fill.  The choice depends on the grid only, so repeated calls of one
+    // shape give identical bits.
+    const bool one_pair = nt * heads >= 2 * (int64_t)device_cus();
+#define ROUTE_LAUNCH(L, RB, NP)                                                                                \
+    hipLaunchKernelGGL((route_kernel<L, RB, NP, ROUTE_RS>), grid, dim3(128 * NP), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, \
+                       k8, ks, v, idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp, kxe, scale, out, logz)
 #define ROUTE_CASE(L)                                                                                          \
     case L:                                                                                                    \
-        if (tile == 64)                                                                                        \
-            hipLaunchKernelGGL((route_kernel<L, 2, ROUTE_NP, ROUTE_RS>), grid, dim3(128 * ROUTE_NP), 0, s, q8, sq, dq8, sdq, g8, sg, \
-                               lz, vb, k8, ks, v, idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp,   \
-                               kxe, scale, out, logz);                                                         \
-        else                                                                                                   \
-            hipLaunchKernelGGL((route_kernel<L, 1, ROUTE_NP, ROUTE_RS>), grid, dim3(128 * ROUTE_NP), 0, s, q8, sq, dq8, sdq, g8, sg, \
-                               lz, vb, k8, ks, v, idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp,   \
-                               kxe, scale, out, logz);                                                         \
+        if (tile == 64) {                                                                                      \
+            if (one_pair) ROUTE_LAUNCH(L, 2, 1);                                                               \
+            else ROUTE_LAUNCH(L, 2, 2);                                                                        \
+        } else {                                                                                               \
+            if (one_pair) ROUTE_LAUNCH(L, 1, 1);                                                               \
+            else ROUTE_LAUNCH(L, 1, 2);                                                                        \
+        }                                                                                                      \
         break;
     switch (leaf) {
         ROUTE_CASE(16)
@@ -2735,6 +2743,7 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
         ROUTE_CASE(128)
     }
 #undef ROUTE_CASE
+#undef ROUTE_LAUNCH
     return launched("htrc_route_attend");
 }
 
