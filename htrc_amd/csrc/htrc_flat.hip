@@ -1386,8 +1386,8 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm
 //     its far leaves, then its near tokens, in 32-key blocks, and wave wave / NP of the pair
 //     takes half of the tile's rows (32 of 64, or 16 of 32); each block in LDS feeds both.  A
 //     pair's blocks stream through a 2-slot LDS ring, loaded one block ahead by direct
-//     global->LDS loads split between the two waves; the pairs' partial states merge through
-//     LDS.
+//     global->LDS loads split between the two waves; two pairs' partial states merge through
+//     LDS, one pair's waves store their rows straight from registers.
 // SEL and the partial states never reach HBM.
 // ---------------------------------------------------------------------------------------------
 template <int RB>
@@ -1867,6 +1867,28 @@ __global__ __launch_bounds__(128 * NP, ROUTE_MINWG) void route_kernel(
         if (bad) redo = 1;
         __syncthreads();
         if (redo == 0 || pass + 1 == MAX_PASSES) break;
+    }
+    if constexpr (NP == 1) {
+        // one pair: each wave holds its rows' finished O^T; lanes (col, grp) write dims
+        // 16 db + 4 grp .. + 3 of row 16 RB hr + 16 rb + col, normalised by the row total
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int r = 16 * RB * hr + 16 * rb + col;
+            const float den = red_l[0][r];
+            const float inv = 1.0f / (den < 1e-30f ? 1e-30f : den);
+            const int64_t qi = (int64_t)t * TR + r;
+            if (qi < nq) {
+                const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
+#pragma unroll
+                for (int db = 0; db < 8; ++db) {
+                    const f32x4 o = st.o[rb][db];
+                    *(f32x4*)(out + orow * D + 16 * db + 4 * grp) =
+                        f32x4{__fmul_rn(o[0], inv), __fmul_rn(o[1], inv), __fmul_rn(o[2], inv), __fmul_rn(o[3], inv)};
+                }
+                if (grp == 0) logz[orow] = __fadd_rn(__fmul_rn(st.m[rb], LN2), __logf(den));   // m in log2 units
+            }
+        }
+        return;
     }
     // ---- merge: every pair used the same reference per row, so the partial sums simply add
     // (h3/htrc_flat_triton.py:263-273 with equal maxima).  MRG2: two rounds, the rows of row
