@@ -1433,7 +1433,11 @@ constexpr int MRG_STRIDE = 132;
 // other is computed on) measured 1.8% faster than three at cfg3, and their 54 KB leave room for
 // a third workgroup per CU, which is slower again (register spills and contention).
 constexpr int ROUTE_RS = 2;
-constexpr int ROUTE_MINWG = 2;                      // waves per SIMD (= workgroups per CU) to fit
+// Waves per SIMD the route kernel's register budget allows: three for one wave pair per tile
+// (168 VGPRs; the 3 spilled values sit outside the key loops; 3.012 -> 2.995 ms at cfg3), two
+// for two pairs (there a 168-VGPR cap spills inside the loops).
+template <int NP>
+constexpr int route_waves_per_simd() { return NP == 1 ? 3 : 2; }
 
 // Per-lane byte offsets of the 32-key block loads (loop invariant): the QK operand chunk of
 // lane (col, grp) and the swizzled PV row chunks (see dma_rows).
@@ -1589,7 +1593,7 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
 // RB = tile / 32: 16-row blocks per wave (tiles of 64 or 32 rows); NP wave pairs split the keys;
 // RS ring slots per pair.
 template <int LEAF, int RB, int NP, int RS>
-__global__ __launch_bounds__(128 * NP, ROUTE_MINWG) void route_kernel(
+__global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ sq, const int8_t* __restrict__ dq8,
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ k8,
