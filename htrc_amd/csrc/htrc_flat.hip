@@ -1487,6 +1487,7 @@ __device__ __forceinline__ void dma_rows27(const uint16_t* x0, const uint16_t* x
 // top-k overlap.  SEL never reaches HBM.
 // MULTI: tile groups of G > 1 tiles (keys merged by max over the tiles); NRB = tile / 16 row
 // blocks of 16 rows per tile.
+constexpr int SEL_RING = 3;                         // route_select ring slots per wave
 template <bool MULTI, int NRB>
 __global__ __launch_bounds__(256, 4) void route_select_kernel(
     const int8_t* __restrict__ dq8, const float* __restrict__ sdq, const int8_t* __restrict__ g8,
@@ -1495,6 +1496,10 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
     extern __shared__ uint32_t keys[];        // [nb]
     __shared__ TopkSmem sm;
     __shared__ float red_m[4][64];
+    // each wave's own ring of 16-leaf groups: g8 rows as the two 1 KB QK operand chunks
+    // (kss = 0, 1; lane-linear), then sg (64 B) and lz (64 B)
+    constexpr int SEL_SLOT = 2048 + 128;
+    __shared__ __align__(16) char sring[4][SEL_RING][SEL_SLOT];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     // one workgroup per tile group (G tiles sharing a centre, state and near leaves; G = 1: a tile)
     const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
@@ -1506,12 +1511,24 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
         i32x4 a[2];
         f32x4 sg, lz;
     };
-    auto sel_load = [&](SelOps& o, int c) {
-        const int64_t s0 = gs * nb_pad + c;
+    const uint32_t ring_lds = lds_addr(&sring[w][0][0]);
+    const uint32_t voff0 = (uint32_t)(col * D + 16 * grp), voff1 = voff0 + 64;
+    // group gj of this wave (leaves c = 16 w + 64 gj ..) into ring slot gj % SEL_RING: three
+    // direct loads; lane (col, grp) of operand chunk kss gets bytes 64 kss + 16 grp of row col
+    auto sel_issue = [&](int gj, int ngr) {
+        if (gj >= ngr) return;
+        const int64_t s0 = gs * nb_pad + 16 * w + 64 * gj;
+        const uint32_t slot = ring_lds + (uint32_t)(gj % SEL_RING) * SEL_SLOT;
+        dma16s(g8 + s0 * D, voff0, slot);
+        dma16s(g8 + s0 * D, voff1, slot + 1024);
+        if (lane < 8) dma16(lane < 4 ? sg + s0 + 4 * lane : lz + s0 + 4 * (lane - 4), slot + 2048);
+    };
+    auto sel_read = [&](SelOps& o, int gj) {
+        const char* slot = &sring[w][gj % SEL_RING][0];
 #pragma unroll
-        for (int kss = 0; kss < 2; ++kss) o.a[kss] = *(const i32x4*)(g8 + (s0 + col) * D + 64 * kss + 16 * grp);
-        o.sg = *(const f32x4*)(sg + s0 + 4 * grp);
-        o.lz = *(const f32x4*)(lz + s0 + 4 * grp);
+        for (int kss = 0; kss < 2; ++kss) o.a[kss] = *(const i32x4*)(slot + 1024 * kss + 16 * lane);
+        o.sg = *(const f32x4*)(slot + 2048 + 16 * grp);
+        o.lz = *(const f32x4*)(slot + 2048 + 64 + 16 * grp);
     };
     i32x4 b[NRB][2];
     bool val[NRB];
@@ -1559,17 +1576,21 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
         for (int rb = 0; rb < NRB; ++rb) {
             srow[rb] = sdq[th * TR + (int64_t)(val[rb] ? 16 * rb + col : 0) * stride];
             rmax[rb] = -INFINITY;
+            // consumed before the first direct load: the compiler's own wait for them would
+            // otherwise drain the ring
+            asm volatile("" : : "v"(b[rb][0]), "v"(b[rb][1]), "v"(srow[rb]));
         }
-        // wave w: 16-leaf groups c = 16 w + 64 j, each loaded one group ahead
-        SelOps sa, sb;
-        if (16 * w < nb) sel_load(sa, 16 * w);
-        for (int c = 16 * w; c < nb; c += 128) {
-            const int c1 = c + 64;
-            if (c1 < nb) sel_load(sb, c1);
-            sel_block(sa, c);
-            if (c1 >= nb) break;
-            if (c1 + 64 < nb) sel_load(sa, c1 + 64);
-            sel_block(sb, c1);
+        // wave w: 16-leaf groups c = 16 w + 64 gj through its ring, loaded SEL_RING - 1 ahead
+        const int ngr = 16 * w < nb ? (nb - 16 * w + 63) / 64 : 0;
+#pragma unroll
+        for (int gj = 0; gj < SEL_RING - 1; ++gj) sel_issue(gj, ngr);
+        for (int gj = 0; gj < ngr; ++gj) {
+            if (gj + SEL_RING - 2 < ngr) wait_vmcnt<3 * (SEL_RING - 2)>();   // the later groups stay in flight
+            else wait_vmcnt<0>();
+            SelOps o;
+            sel_read(o, gj);
+            sel_issue(gj + SEL_RING - 1, ngr);       // into the slot of group gj - 1, read last iteration
+            sel_block(o, 16 * w + 64 * gj);
         }
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {    // row r = stride * (16 rb + col) of the sampled rows
