@@ -2765,22 +2765,25 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
     const int nbp = htrc_nb_pad(nb);
     const dim3 grid((unsigned)(nt * heads));
     hipStream_t s = (hipStream_t)stream;
-    // One wave pair per tile (all of its keys; four tiles per CU) when the grid gives every CU
-    // at least two tiles, two pairs (key halves merged in LDS) for smaller grids, which the
-    // tiles alone cannot fill.  The choice depends on the grid only, so repeated calls of one
-    // shape give identical bits.
-    const bool one_pair = nt * heads >= 2 * (int64_t)device_cus();
+    // Wave pairs per tile by grid size: one (all of the tile's keys; five tiles per CU) when
+    // the grid gives every CU at least two tiles, two (key halves merged in LDS) below that,
+    // four (key quarters, one tile per CU) when the grid has no more tiles than CUs.  The
+    // choice depends on the grid only, so repeated calls of one shape give identical bits.
+    const int64_t cus = device_cus();
+    const int np = nt * heads >= 2 * cus ? 1 : (nt * heads > cus ? 2 : 4);
 #define ROUTE_LAUNCH(L, RB, NP)                                                                                \
     hipLaunchKernelGGL((route_kernel<L, RB, NP, ROUTE_RS>), grid, dim3(128 * NP), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, \
                        k8, ks, v, idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp, kxe, scale, out, logz)
 #define ROUTE_CASE(L)                                                                                          \
     case L:                                                                                                    \
         if (tile == 64) {                                                                                      \
-            if (one_pair) ROUTE_LAUNCH(L, 2, 1);                                                               \
-            else ROUTE_LAUNCH(L, 2, 2);                                                                        \
+            if (np == 1) ROUTE_LAUNCH(L, 2, 1);                                                                \
+            else if (np == 2) ROUTE_LAUNCH(L, 2, 2);                                                           \
+            else ROUTE_LAUNCH(L, 2, 4);                                                                        \
         } else {                                                                                               \
-            if (one_pair) ROUTE_LAUNCH(L, 1, 1);                                                               \
-            else ROUTE_LAUNCH(L, 1, 2);                                                                        \
+            if (np == 1) ROUTE_LAUNCH(L, 1, 1);                                                                \
+            else if (np == 2) ROUTE_LAUNCH(L, 1, 2);                                                           \
+            else ROUTE_LAUNCH(L, 1, 4);                                                                        \
         }                                                                                                      \
         break;
     switch (leaf) {

@@ -68,6 +68,30 @@ def test_multihead_equals_per_head(device):
         assert torch.equal(out[h], oh)
 
 
+def test_route_grid_shapes_agree(device):
+    """The attend launch splits a tile's keys over 4, 2 or 1 wave pairs by grid size (at most
+    one tile per CU, up to two, more).  One head's data in grids of 128, 384 and 1152 tiles
+    (1, 3 and 9 heads, N = 8192) takes each shape on a 256-CU MI355X: the outputs agree to
+    fp32 summation order, and sampled whole tiles match the oracle on the head's full key set."""
+    n, leaf, ex = 8192, 64, 16
+    q, k, v = workloads.clustered_runs(n=n, runs=n // 64, heads=9, seed=21)
+    q, k, v = q.to(device), k.to(device), v.to(device)
+    kw = dict(backend="hip", store="int8", dot="bf16", leaf=leaf, exact_leaves=ex)
+    res = [htrc_flat.flat_attention(q[:h], k[:h], v[:h], return_logz=True, **kw) for h in (1, 3, 9)]
+    torch.cuda.synchronize()
+    o0, l0 = res[0][0][0], res[0][1][0]
+    for out, logz in res[1:]:
+        assert rel_l2(out[0].cpu().numpy(), o0.cpu().numpy()) <= 1e-5
+        assert float((logz[0] - l0).abs().max()) <= 1e-5
+    tiles = (0, 1, 64, 127)
+    rows = torch.from_numpy(np.concatenate([np.arange(64 * t, 64 * t + 64) for t in tiles])).to(device)
+    ref = flat_i8.flat_i8(bits(q[0, rows].cpu()), bits(k[0].cpu()), bits(v[0].cpu()), tile=64, leaf=leaf,
+                          exact_leaves=ex, splits=1, bn=64)
+    for out, logz in res:
+        assert rel_l2(out[0, rows].cpu().numpy(), ref["out"]) <= OUT_REL_L2
+        assert np.abs(logz[0, rows].cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
+
+
 def test_deterministic(device):
     q, k, v = workloads.clustered_runs(n=4096, runs=64, heads=2, seed=1)
     kw = dict(backend="hip", store="int8", dot="bf16", leaf=64, exact_leaves=16)
