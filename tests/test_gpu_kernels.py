@@ -131,6 +131,33 @@ def test_stats_close_to_oracle(device, leaf):
         assert np.all(_np(lz[0])[:, nb:] == -np.inf) and np.all(_np(g8[0])[:, nb:] == 0)
 
 
+@pytest.mark.parametrize("n", [8192, 32768, 65536])
+def test_stats_leaf_split_sizes(device, n):
+    """The stats launchers give each workgroup 16, 8 or 4 leaves so that a grid has at least
+    two workgroups per CU; one head of N = 8192, 32768, 65536 takes 4, 8 and 16 on a 256-CU
+    MI355X.  Sampled centres against the oracle on every leaf, with the bars of
+    test_stats_close_to_oracle; padded leaves empty."""
+    leaf = 64
+    q, k, v = _data(n, seed=n // 1024)
+    nb, nbp = n // leaf, nb_pad(n // leaf)
+    mu = flat_i8.tile_centres(q[0].float().numpy(), 64)
+    g8, lz, vbs, sg, _ = hip.leaf_stats(torch.from_numpy(mu)[None].to(device), k.to(device), v.to(device), nb,
+                                        1 / math.sqrt(128), leaf=leaf)
+    torch.cuda.synchronize()
+    cs = np.array([0, 1, mu.shape[0] // 2, mu.shape[0] - 1])
+    og8, osg, ovb, olz = flat_i8.stats(mu[cs], bits(k[0]), bits(v[0]), leaf, 1 / math.sqrt(128))
+    c = torch.from_numpy(cs).to(device)
+    diff = np.abs(_np(g8[0, c])[:, :nb].astype(np.int32) - og8.astype(np.int32))
+    assert diff.max() <= 1 and (diff > 0).mean() < 2e-3
+    np.testing.assert_allclose(_np(lz[0, c])[:, :nb], olz, rtol=0, atol=2e-5 * (1 + np.abs(olz).max()))
+    np.testing.assert_allclose(_np(sg[0, c])[:, :nb], osg, rtol=1e-5, atol=0)
+    vb = bf16.to_f32(bits(vbs[0, c, :nb].contiguous()))
+    ovbf = bf16.to_f32(ovb)
+    assert np.abs(vb - ovbf).max() <= 2 ** -7 * np.abs(ovbf).max() and (vb != ovbf).mean() < 2e-2
+    if nbp > nb:
+        assert bool((lz[0, :, nb:] == -math.inf).all()) and bool((g8[0, :, nb:] == 0).all())
+
+
 def test_select_bitexact_on_oracle_state(device):
     n, leaf = 4096, 64
     q, k, v = _data(n, seed=11)
