@@ -275,21 +275,22 @@ def test_route_on_oracle_state(device, leaf, ex):
 
 
 @pytest.mark.parametrize("ex", [0, 8, 64])
-@pytest.mark.parametrize("heads", [1, 5, 9])
-def test_route_grid_shapes_on_oracle_state(device, ex, heads):
-    """One head's oracle state (n = 4096: 64 tiles, 64 leaves) replicated over 1, 5 and 9 heads
-    (64, 320 and 576 tiles: four, two and one wave pairs per tile on a 256-CU MI355X), with no
-    near leaves, 8, and every leaf near (an empty far field): every head matches the oracle and
-    all heads are bit-identical."""
+@pytest.mark.parametrize("tile,heads", [(64, 1), (64, 5), (64, 9), (32, 1), (32, 3), (32, 5)])
+def test_route_grid_shapes_on_oracle_state(device, ex, tile, heads):
+    """One head's oracle state (n = 4096, 64 leaves; 64 tiles of 64 rows or 128 of 32)
+    replicated over heads so that the grid takes four, two and one wave pairs per tile on a
+    256-CU MI355X (at most 256, up to 511, at least 512 tiles), with no near leaves, 8, and
+    every leaf near (an empty far field): every head matches the oracle and all heads are
+    bit-identical."""
     n, leaf = 4096, 64
     q, k, v = _data(n, seed=31 + ex)
-    ref = _oracle_state(q, k, v, leaf, ex, splits=1, bn=64)
+    ref = _oracle_state(q, k, v, leaf, ex, splits=1, bn=64, tile=tile)
     packed, state, _, _ = _device_state(ref, q, k, v, device)
     rep = lambda t: t.repeat(heads, *([1] * (t.dim() - 1))).contiguous()  # noqa: E731
     packed = {name: rep(t) for name, t in packed.items()}
     state = {name: rep(t) for name, t in state.items()}
     kx = ref["idx"].shape[1]
-    out, logz = hip.route(packed, state, nq=n, leaf=leaf, kx=kx, scale=1 / math.sqrt(128))
+    out, logz = hip.route(packed, state, nq=n, leaf=leaf, kx=kx, scale=1 / math.sqrt(128), tile=tile)
     torch.cuda.synchronize()
     for h in range(1, heads):
         assert torch.equal(out[h], out[0]) and torch.equal(logz[h], logz[0]), f"head {h}"
