@@ -1382,11 +1382,11 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm
 //     the select_kernel arithmetic), top-k -> idx, and each row's largest far-field score;
 //   route_kernel, one workgroup per tile: far + near field in one online softmax whose
 //     reference max is that score.  NP wave pairs split the keys (large grids: one pair, all
-//     keys, four tiles per CU; small grids: two pairs, key halves): pair pr = wave % NP takes
+//     keys, five tiles per CU; smaller grids: two or four pairs): pair pr = wave % NP takes
 //     its far leaves, then its near tokens, in 32-key blocks, and wave wave / NP of the pair
 //     takes half of the tile's rows (32 of 64, or 16 of 32); each block in LDS feeds both.  A
 //     pair's blocks stream through a 2-slot LDS ring, loaded one block ahead by direct
-//     global->LDS loads split between the two waves; two pairs' partial states merge through
+//     global->LDS loads split between the two waves; several pairs' partial states merge through
 //     LDS, one pair's waves store their rows straight from registers.
 // SEL and the partial states never reach HBM.
 // ---------------------------------------------------------------------------------------------
