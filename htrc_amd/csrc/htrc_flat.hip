@@ -1623,8 +1623,11 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
     int nb, int nb_pad, int kxe, float scale, float* __restrict__ out, float* __restrict__ logz) {
     constexpr int NT = 128 * NP;                               // threads
     __shared__ __align__(16) char ring[NP][RS][SLOT_BYTES];    // one per wave pair; also merge staging
-    __shared__ uint16_t sidx[MAX_KX_LDS];
-    __shared__ uint32_t exbits[MAX_NB_LDS / 32 + 1];
+    // sized by the launch (route_dyn_bytes): exclusion bits [nb / 32 + 1], then the tile's near
+    // leaves [kxe], so small shapes leave room for more tiles per CU
+    extern __shared__ __align__(16) uint32_t route_dyn[];
+    uint32_t* exbits = route_dyn;
+    uint16_t* sidx = (uint16_t*)(route_dyn + (nb / 32 + 1));
     __shared__ float red_m[64], red_l[NP][64];
     __shared__ int redo;
     constexpr int TR = 32 * RB;                                // rows per tile
@@ -2771,8 +2774,9 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
     // choice depends on the grid only, so repeated calls of one shape give identical bits.
     const int64_t cus = device_cus();
     const int np = nt * heads >= 2 * cus ? 1 : (nt * heads > cus ? 2 : 4);
+    const size_t dyn = ((size_t)(nb / 32 + 1) * 4 + (size_t)kxe * 2 + 15) / 16 * 16;
 #define ROUTE_LAUNCH(L, RB, NP)                                                                                \
-    hipLaunchKernelGGL((route_kernel<L, RB, NP, ROUTE_RS>), grid, dim3(128 * NP), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, \
+    hipLaunchKernelGGL((route_kernel<L, RB, NP, ROUTE_RS>), grid, dim3(128 * NP), dyn, s, q8, sq, dq8, sdq, g8, sg, lz, vb, \
                        k8, ks, v, idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp, kxe, scale, out, logz)
 #define ROUTE_CASE(L)                                                                                          \
     case L:                                                                                                    \
