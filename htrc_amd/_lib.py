@@ -7,48 +7,46 @@ if the library is missing every operator raises.
 from __future__ import annotations
 
 import ctypes
+import re
 from pathlib import Path
 
 import torch
 
 HERE = Path(__file__).resolve().parent
 LIBPATH = HERE / "libhtrc_flat.so"
-ABI_VERSION = 11
+HEADER = HERE.parent / "include" / "htrc_flat.h"
+ABI_VERSION = 12
 
-_vp = ctypes.c_void_p
-_i64 = ctypes.c_int64
-_int = ctypes.c_int
-_flt = ctypes.c_float
+_CTYPES = {"int64_t": ctypes.c_int64, "int": ctypes.c_int, "float": ctypes.c_float}
 
-# name -> argument types (all return int status unless listed in _RESTYPES)
-SIGNATURES = {
-    "htrc_abi_version": [],
-    "htrc_last_error": [],
-    "htrc_nb_pad": [_i64],
-    "htrc_pack_q": [_vp, _int, _i64, _i64, _int, _int, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
-    "htrc_pack_k": [_vp, _i64, _i64, _int, _vp, _vp, _vp],
-    "htrc_leaf_stats": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _flt, _vp, _vp, _vp, _vp, _vp],
-    "htrc_select": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _vp],
-    "htrc_topk": [_vp, _i64, _i64, _int, _int, _vp, _vp, _vp],
-    "htrc_tile": [_vp] * 13 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _vp, _int, _int, _flt] + [_vp] * 6,
-    "htrc_merge": [_vp, _vp, _vp, _i64, _i64, _int, _int, _int, _vp, _vp, _vp, _vp],
-    "htrc_route_select": [_vp] * 5 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _int, _vp, _vp, _vp],
-    "htrc_route_attend": [_vp] * 13 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _vp, _flt, _vp, _vp, _vp],
-    "htrc_route": [_vp] * 11 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _int, _vp, _flt, _vp, _vp, _vp, _vp,
-                                 _vp],
-    "htrc_tail": [_vp, _int, _vp, _vp, _i64, _i64, _i64, _int, _flt, _vp, _vp, _vp],
-    "htrc_pack_q16": [_vp, _int, _i64, _i64, _int, _int, _int, _vp, _int, _vp, _vp, _vp, _vp],
-    "htrc_leaf_stats_fp8": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _flt, _vp, _vp, _vp, _vp, _vp, _vp],
-    "htrc_select_fp8": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _vp],
-    "htrc_tile_fp8": [_vp] * 11 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _vp, _int, _int, _flt] + [_vp] * 6,
-    "htrc_leaf_stats_bf16": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _flt, _vp, _vp, _vp, _vp],
-    "htrc_select_bf16": [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _vp],
-    "htrc_tile_bf16": [_vp] * 9 + [_i64, _i64, _i64, _int, _int, _int, _int, _int, _vp, _int, _int, _flt] + [_vp] * 6,
-    "htrc_kmeans_order": [_vp, _int, _i64, _i64, _int, _int, _int, _int, _vp, _vp, _vp, _vp],
-    "htrc_dequant_rows": [_vp, _i64, _vp, _i64, _i64, _int, _vp, _int, _vp],
-    "htrc_selftest_mfma": [_vp] * 7,
-}
-_RESTYPES = {"htrc_last_error": ctypes.c_char_p}
+
+def _c_arg(decl: str):
+    """ctypes type of one C parameter declaration: pointers are c_void_p, scalars by type."""
+    decl = decl.strip()
+    if "*" in decl:
+        return ctypes.c_void_p
+    base = decl.replace("const ", "").split()[0]
+    if base not in _CTYPES:
+        raise RuntimeError(f"{HEADER.name}: no ctypes mapping for parameter {decl!r}")
+    return _CTYPES[base]
+
+
+def parse_header(text: str) -> dict:
+    """name -> (argument ctypes, restype) of every entry point the header declares."""
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    sigs = {}
+    for ret, name, args in re.findall(r"\b(int|const char\s*\*)\s*(htrc_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = args.strip()
+        argt = [] if args in ("", "void") else [_c_arg(a) for a in args.split(",")]
+        sigs[name] = (argt, ctypes.c_char_p if "char" in ret else ctypes.c_int)
+    return sigs
+
+
+def signatures() -> dict:
+    if not HEADER.exists():
+        raise RuntimeError(f"{HEADER} is missing: the C-ABI binding is read from it")
+    return parse_header(HEADER.read_text())
+
 
 _lib = None
 
@@ -66,10 +64,10 @@ def lib():
                 f"{LIBPATH} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` "
                 "(the flat-HTRC operator has no fallback path)")
         L = ctypes.CDLL(str(LIBPATH))
-        for name, args in SIGNATURES.items():
+        for name, (args, res) in signatures().items():
             fn = getattr(L, name)
             fn.argtypes = args
-            fn.restype = _RESTYPES.get(name, _int)
+            fn.restype = res
         if L.htrc_abi_version() != ABI_VERSION:
             raise RuntimeError(f"libhtrc_flat ABI {L.htrc_abi_version()} != expected {ABI_VERSION}; rebuild")
         _lib = L

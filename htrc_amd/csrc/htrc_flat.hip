@@ -213,10 +213,11 @@ __global__ __launch_bounds__(256) void pack_k_kernel(const uint16_t* __restrict_
 // ---------------------------------------------------------------------------------------------
 // stats: leaf statistics at the tile centres (h3/htrc_flat_triton.py:41-85, I8 store).
 // Workgroup = 64 tile centres (16 per wave) x a range of leaves of one head.  Per leaf:
-//   a^T = K_l mu^T                      bf16 MFMA, mu split into two bf16 terms (~16 bits)
+//   a^T = K_l mu^T                      bf16 MFMA, mu split into three bf16 terms (~24 bits)
 //   e = exp(a - max) per centre (lane%16 = centre), z = sum e
-//   g^T = K_l^T w^T, vb^T = V_l^T w^T   w = e / z in two bf16 terms shared by both products
-//                                        (g = scale * K_l^T w^T)
+//   g^T = K_l^T w^T, vb^T = V_l^T w^T   w = e / z in three bf16 terms for g (int8 codes), the
+//                                        first two of them for vb (stored as bf16)
+//                                        (g = scale * K_l^T w^T; K, V are exact in bf16)
 // The leaf's K and V rows are staged in LDS (XOR-swizzled 16-byte chunks) by gfx950 direct
 // global->LDS loads one leaf ahead; the QK operand is a plain 16-byte read, the PV-type
 // operands come from the same rows through transposing reads.  Each leaf's outputs are
@@ -354,20 +355,22 @@ __device__ __forceinline__ uint32_t quant4_e4m3(f32x4 x, float c) {
            (f32_to_e4m3(__fmul_rn(x[2], c)) << 16) | (f32_to_e4m3(__fmul_rn(x[3], c)) << 24);
 }
 
-// int8 codes of x_i * c rounded to nearest (ties to even), packed little-endian.  Adding
-// 1.5 * 2^23 to a value of magnitude below 2^22 rounds it to an integer held in the low mantissa
-// bits, so the low byte of the sum is the two's-complement code; SDWA adds write the codes of
-// x_1..x_3 into bytes 1..3 of the first sum in place.
+// int8 codes of x_i * c rounded half away from zero, packed little-endian: y = x c, then
+// trunc(y + copysign(0.5, y)) in fp32 (h3/htrc_flat_triton.py:77-79: where(x >= 0, x + 0.5,
+// x - 0.5) and a truncating int8 cast; 0.49999997 -> 1 as there).  copysign is one bit select
+// (v_bfi_b32); v_cvt_i32_f32 truncates, and its SDWA form writes the low byte of each code
+// (the two's-complement int8) into byte i of the packed word in place.
 __device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
-    const float m = 12582912.0f;
-    uint32_t u = __float_as_uint(__fadd_rn(__fmul_rn(x[0], c), m));
-    const float y1 = __fmul_rn(x[1], c), y2 = __fmul_rn(x[2], c), y3 = __fmul_rn(x[3], c);
-    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-        : "+v"(u) : "v"(y1), "v"(m));
-    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-        : "+v"(u) : "v"(y2), "v"(m));
-    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-        : "+v"(u) : "v"(y3), "v"(m));
+    float z[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float y = __fmul_rn(x[i], c);
+        z[i] = __fadd_rn(y, __uint_as_float((__float_as_uint(y) & 0x80000000u) | 0x3f000000u));
+    }
+    uint32_t u = (uint32_t)(int)z[0];
+    asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(u) : "v"(z[1]));
+    asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(u) : "v"(z[2]));
+    asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(u) : "v"(z[3]));
     return u;
 }
 
@@ -378,9 +381,11 @@ __device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
 // NW waves of 16 centres each share every staged leaf (workgroup = 16 NW centres).
 constexpr int STATS_NW = 4;
 constexpr int STATS_TPW = 16 * STATS_NW;
+// The launch covers centres [c0, c0 + nt) of each head (mu holds mu_stride centres per head);
+// the state rows are the launch's own, [H, nt, nb_pad].
 template <int LEAF, int STORE, int NW>
-__global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restrict__ mu, int nt,
-                                                       const uint16_t* __restrict__ k,
+__global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restrict__ mu, int64_t mu_stride,
+                                                       int64_t c0, int nt, const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v, int64_t nk, int nb,
                                                        int nb_pad, int lpb, float scale,   // lpb: 4, 8 or 16
                                                        int8_t* __restrict__ g8, float* __restrict__ sg,
@@ -406,14 +411,16 @@ __global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restri
     const uint32_t voff = stage_voff();
     const float sl2 = __fmul_rn(scale, LOG2E);
 
-    // mu in two bf16 terms (~16 bits; the reference's production path computes these dots in TF32)
-    bf16x8 mh[4], ml[4];
+    // mu in three bf16 terms (~24 bits, the fp32 centre: the logits, and through the softmax every
+    // product, carry no error beyond fp32 rounding, so the int8 codes of g agree with an IEEE fp32
+    // evaluation except where g * 127 / max|g| lies within fp32 noise of a half)
+    bf16x8 mh[4], mm[4], ml[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
         float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = tval ? mu[th * D + 32 * ks + 8 * grp + e] : 0.0f;
-        split2x8(x, mh[ks], ml[ks]);
+        for (int e = 0; e < 8; ++e) x[e] = tval ? mu[(h * mu_stride + c0 + t) * D + 32 * ks + 8 * grp + e] : 0.0f;
+        split3x8(x, mh[ks], mm[ks], ml[ks]);
     }
 
     const int l0 = lg * lpb;
@@ -570,8 +577,9 @@ __global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restri
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const bf16x8 A = as_bf16x8(*(const u32x4*)(Kr + (row * 16 + ((4 * ks + grp) ^ swz(row))) * 16));
+                a[kb] = mfma_bf16(A, ml[ks], a[kb]);          // smallest term first
+                a[kb] = mfma_bf16(A, mm[ks], a[kb]);
                 a[kb] = mfma_bf16(A, mh[ks], a[kb]);
-                a[kb] = mfma_bf16(A, ml[ks], a[kb]);
             }
         }
         store_g();                             // stores of leaf l - 1, first part
@@ -594,7 +602,7 @@ __global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restri
             }
         z = grp_sum(z);
         const float rz = __fdiv_rn(1.0f, z);
-        // w = e / z in two bf16 terms, shared by both products: gacc = w K (g = scale gacc), vb = w V
+        // w = e / z in bf16 terms: gacc = w K (g = scale gacc), vb = w V
 #pragma unroll
         for (int db = 0; db < 8; ++db) gacc[db] = vacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -605,8 +613,9 @@ __global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restri
                 const int kb = 2 * kk + (e >> 2);
                 wv[e] = kb < KB ? __fmul_rn(a[kb < KB ? kb : 0][e & 3], rz) : 0.0f;
             }
-            bf16x8 W0, W1;
-            split2x8(wv, W0, W1);
+            // w in three bf16 terms for g (its int8 codes), two for vb (rounded to bf16)
+            bf16x8 W0, W1, W2;
+            split3x8(wv, W0, W1, W2);
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
                 const u32x2 zero = {0u, 0u};
@@ -615,10 +624,11 @@ __global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restri
                 const u32x2 v0 = tr_operand(Vr, 32 * kk, db, lane);
                 const u32x2 v1 = (2 * kk + 1 < KB) ? tr_operand(Vr, 32 * kk + 16, db, lane) : zero;
                 const bf16x8 KA = as_bf16x8(k0, k1), VA = as_bf16x8(v0, v1);
-                gacc[db] = mfma_bf16(KA, W0, gacc[db]);
+                gacc[db] = mfma_bf16(KA, W2, gacc[db]);
                 gacc[db] = mfma_bf16(KA, W1, gacc[db]);
-                vacc[db] = mfma_bf16(VA, W0, vacc[db]);
+                gacc[db] = mfma_bf16(KA, W0, gacc[db]);
                 vacc[db] = mfma_bf16(VA, W1, vacc[db]);
+                vacc[db] = mfma_bf16(VA, W0, vacc[db]);
             }
             if (kk == 0 && KK > 1) store_v(0);
         }
@@ -700,12 +710,12 @@ __global__ __launch_bounds__(256) void select_kernel(const int8_t* __restrict__ 
                                                      const float* __restrict__ sdq, int stride,
                                                      const int8_t* __restrict__ g8,
                                                      const float* __restrict__ sg,
-                                                     const float* __restrict__ lz, int nt, int group, int ng,
-                                                     int nb, int nb_pad, float* __restrict__ sel) {
+                                                     const float* __restrict__ lz, int nt, int group, int g0,
+                                                     int ng, int nb, int nb_pad, float* __restrict__ sel) {
     constexpr int TR = 16 * NRB;                      // rows per tile
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int gi = blockIdx.x, h = blockIdx.z;
-    const int64_t gs = (int64_t)h * ng + gi;          // state / SEL row of the group
+    const int64_t gs = (int64_t)h * ng + gi;          // state / SEL row of the group (the launch's window)
     const int ts = TR / stride;
     const int c0 = blockIdx.y * 256 + w * 64;
     float bsel[4][4];
@@ -714,7 +724,7 @@ __global__ __launch_bounds__(256) void select_kernel(const int8_t* __restrict__ 
 #pragma unroll
         for (int i = 0; i < 4; ++i) bsel[lb][i] = -INFINITY;
     for (int j = 0; j < group; ++j) {
-        const int t = gi * group + j;
+        const int t = (g0 + gi) * group + j;
         if (t >= nt) break;                           // padded tiles repeat the last one
         const int64_t th = (int64_t)h * nt + t;
         i32x4 b[NRB][2];
@@ -777,8 +787,10 @@ struct TopkSmem {
     uint32_t prefix, remaining;
 };
 
-// keys[] holds order_key(sel) for l < nb.  Writes idx[0..kx) ascending and (optionally) excl.
-__device__ void topk_row(const uint32_t* keys, int nb, int kx, TopkSmem& sm, int32_t* idx_out,
+// keys(l) is order_key(sel[l]) for l < nb (an LDS array, or computed from global memory for rows
+// longer than the LDS holds).  Writes idx[0..kx) ascending and (optionally) excl.
+template <typename Keys>
+__device__ void topk_row(Keys keys, int nb, int kx, TopkSmem& sm, int32_t* idx_out,
                          int8_t* excl_out, int32_t* idx_lds) {
     const int tid = threadIdx.x;
     if (kx >= nb) {               // everything is selected
@@ -800,7 +812,7 @@ __device__ void topk_row(const uint32_t* keys, int nb, int kx, TopkSmem& sm, int
         __syncthreads();
         const uint32_t prefix = sm.prefix;
         for (int l = tid; l < nb; l += 256) {
-            const uint32_t key = keys[l];
+            const uint32_t key = keys(l);
             if ((key & mask) == prefix) atomicAdd(&sm.hist[(key >> shift) & 255u], 1u);
         }
         __syncthreads();
@@ -840,7 +852,7 @@ __device__ void topk_row(const uint32_t* keys, int nb, int kx, TopkSmem& sm, int
     const int a = min(nb, tid * chunk), b = min(nb, a + chunk);
     uint32_t ngt = 0, neq = 0;
     for (int l = a; l < b; ++l) {
-        const uint32_t key = keys[l];
+        const uint32_t key = keys(l);
         ngt += key > thr;
         neq += key == thr;
     }
@@ -873,7 +885,7 @@ __device__ void topk_row(const uint32_t* keys, int nb, int kx, TopkSmem& sm, int
     uint32_t eqr = sm.cnt_eq[tid];
     uint32_t pos = sm.cnt_gt[tid] + (eqr < need_eq ? eqr : need_eq);
     for (int l = a; l < b; ++l) {
-        const uint32_t key = keys[l];
+        const uint32_t key = keys(l);
         bool take = key > thr;
         if (key == thr) {
             take = eqr < need_eq;
@@ -890,19 +902,27 @@ __device__ void topk_row(const uint32_t* keys, int nb, int kx, TopkSmem& sm, int
     __syncthreads();
 }
 
-constexpr int MAX_NB_LDS = 8192;   // leaves per head the LDS top-k holds
+constexpr int MAX_NB_LDS = 8192;   // leaves per head the LDS top-k keys hold (longer rows: global)
 
+// One workgroup per SEL row.  LDS_KEYS: the row's keys staged in LDS; otherwise each radix pass
+// reads the row from global memory (L2) and forms the keys on the fly.
+template <bool LDS_KEYS>
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ sel, int nb, int nb_pad,
                                                    int kx, int sink, int32_t* __restrict__ idx,
                                                    int8_t* __restrict__ excl) {
-    __shared__ uint32_t keys[MAX_NB_LDS];
+    __shared__ uint32_t keys[LDS_KEYS ? MAX_NB_LDS : 1];
     __shared__ TopkSmem sm;
     const int64_t row = blockIdx.x;
-    for (int l = threadIdx.x; l < nb; l += 256)
-        keys[l] = l < sink ? 0xffffffffu : order_key(sel[row * nb_pad + l]);
+    const float* srow = sel + row * nb_pad;
     for (int l = nb + threadIdx.x; l < nb_pad; l += 256) excl[row * nb_pad + l] = 0;
-    __syncthreads();
-    topk_row(keys, nb, kx, sm, idx + row * kx, excl + row * nb_pad, nullptr);
+    if constexpr (LDS_KEYS) {
+        for (int l = threadIdx.x; l < nb; l += 256) keys[l] = l < sink ? 0xffffffffu : order_key(srow[l]);
+        __syncthreads();
+        topk_row([&](int l) { return keys[l]; }, nb, kx, sm, idx + row * kx, excl + row * nb_pad, nullptr);
+    } else {
+        topk_row([&](int l) { return l < sink ? 0xffffffffu : order_key(srow[l]); }, nb, kx, sm, idx + row * kx,
+                 excl + row * nb_pad, nullptr);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1060,14 +1080,17 @@ __global__ __launch_bounds__(256) void tile_kernel(
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ excl,
     const int32_t* __restrict__ idx, const int8_t* __restrict__ k8, const float* __restrict__ ks,
-    const uint16_t* __restrict__ v, int64_t nq, int nt, int tile, int group, int ng,
+    const uint16_t* __restrict__ v, int64_t nq, int nt, int tile, int group, int g0, int ng,
     const int32_t* __restrict__ perm, int64_t nk, int nb, int nb_pad, int kx, int lps, int eps, float scale,
     float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc,
     float* __restrict__ out, float* __restrict__ logz) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    const int t = blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
+    // tiles of groups [g0, g0 + ng): state, routing and partial rows are the launch's own
+    const int tb = g0 * group, ntw = gridDim.x;
+    const int t = tb + blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
     const int64_t th = (int64_t)h * nt + t;
-    const int64_t gs = (int64_t)h * ng + t / group;       // state / routing row: the tile's group
+    const int64_t tw = (int64_t)h * ntw + blockIdx.x;     // partial row of the tile
+    const int64_t gs = (int64_t)h * ng + (t / group - g0);   // state / routing row: the tile's group
     const int r = w * 16 + col;                           // blockDim = 4 * tile: one wave per 16 rows
     const int64_t p = th * tile + r;
     i32x4 q8r[2], dq8r[2];
@@ -1090,7 +1113,7 @@ __global__ __launch_bounds__(256) void tile_kernel(
         write_final(st, ltot, (int64_t)h * nq + oq, qi < nq, out, logz);
         return;
     }
-    const int64_t base = (th * ns + sp) * tile + r;
+    const int64_t base = (tw * ns + sp) * tile + r;
     if (grp == 0) {
         pm[base] = st.m;
         pl[base] = ltot;
@@ -1122,12 +1145,12 @@ __device__ __forceinline__ f32x4 state_qk(const void* g, int64_t row, int ks, in
 template <bool FP8, int NRB>
 __global__ __launch_bounds__(256) void select16_kernel(const uint16_t* __restrict__ dq16, int stride,
                                                        const void* __restrict__ g, const float* __restrict__ sg,
-                                                       const float* __restrict__ lz, int nt, int group, int ng,
-                                                       int nb, int nb_pad, float* __restrict__ sel) {
+                                                       const float* __restrict__ lz, int nt, int group, int g0,
+                                                       int ng, int nb, int nb_pad, float* __restrict__ sel) {
     constexpr int TR = 16 * NRB;                      // rows per tile
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int gi = blockIdx.x, h = blockIdx.z;
-    const int64_t gs = (int64_t)h * ng + gi;
+    const int64_t gs = (int64_t)h * ng + gi;          // state / SEL row of the group (the launch's window)
     const int ts = TR / stride;
     const int c0 = blockIdx.y * 256 + w * 64;
     float bsel[4][4];
@@ -1136,7 +1159,7 @@ __global__ __launch_bounds__(256) void select16_kernel(const uint16_t* __restric
 #pragma unroll
         for (int i = 0; i < 4; ++i) bsel[lb][i] = -INFINITY;
     for (int j = 0; j < group; ++j) {
-        const int t = gi * group + j;
+        const int t = (g0 + gi) * group + j;
         if (t >= nt) break;                           // padded tiles repeat the last one
         const int64_t th = (int64_t)h * nt + t;
         u32x4 b[NRB][4];
@@ -1230,13 +1253,16 @@ __global__ __launch_bounds__(256) void tile16_kernel(
     const float* __restrict__ sg, const float* __restrict__ lz, const void* __restrict__ vb,
     const float* __restrict__ sv, const int8_t* __restrict__ excl, const int32_t* __restrict__ idx,
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t nq, int nt, int tile, int group,
-    int ng, const int32_t* __restrict__ perm, int64_t nk, int nb, int nb_pad, int kx, int lps, int eps, float scale,
-    float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc, float* __restrict__ out,
+    int g0, int ng, const int32_t* __restrict__ perm, int64_t nk, int nb, int nb_pad, int kx, int lps, int eps,
+    float scale, float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pacc, float* __restrict__ out,
     float* __restrict__ logz) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    const int t = blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
+    // tiles of groups [g0, g0 + ng): state, routing and partial rows are the launch's own
+    const int tb = g0 * group, ntw = gridDim.x;
+    const int t = tb + blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
     const int64_t th = (int64_t)h * nt + t;
-    const int64_t gs = (int64_t)h * ng + t / group;       // state / routing row: the tile's group
+    const int64_t tw = (int64_t)h * ntw + blockIdx.x;     // partial row of the tile
+    const int64_t gs = (int64_t)h * ng + (t / group - g0);   // state / routing row: the tile's group
     const int r = w * 16 + col;                           // blockDim = 4 * tile: one wave per 16 rows
     const int64_t p = th * tile + r;
     u32x4 qb[4], dqh[4];
@@ -1327,7 +1353,7 @@ __global__ __launch_bounds__(256) void tile16_kernel(
         write_final(st, ltot, (int64_t)h * nq + oq, qi < nq, out, logz);
         return;
     }
-    const int64_t base = (th * ns + sp) * tile + r;
+    const int64_t base = (tw * ns + sp) * tile + r;
     if (grp == 0) {
         pm[base] = st.m;
         pl[base] = ltot;
@@ -1338,12 +1364,13 @@ __global__ __launch_bounds__(256) void tile16_kernel(
 
 // merge: (h3/htrc_flat_triton.py:257-273) + logZ = mm + log(den).  One workgroup (4 * tile
 // threads) per tile.
+// Tiles [t0, t0 + gridDim.x) of each head; the partials are the launch's own [H, gridDim.x, ns, tile].
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
-                                                    const float* __restrict__ pacc, int ns, int64_t nq, int nt,
+                                                    const float* __restrict__ pacc, int ns, int64_t nq, int t0,
                                                     int tile, const int32_t* __restrict__ perm,
                                                     float* __restrict__ out, float* __restrict__ logz) {
-    const int t = blockIdx.x, h = blockIdx.y;
-    const int64_t th = (int64_t)h * nt + t;
+    const int t = t0 + blockIdx.x, h = blockIdx.y;
+    const int64_t th = (int64_t)h * gridDim.x + blockIdx.x;   // partial row of the tile
     const int r = threadIdx.x >> 2, part = threadIdx.x & 3;   // 4 threads per row, 32 dims each
     const int64_t qi = (int64_t)t * tile + r;
     if (qi >= nq) return;
@@ -1425,7 +1452,9 @@ __device__ __forceinline__ void rows_update(RowsN<RB>& st, const float (&sc)[RB]
 constexpr int SLOT_BYTES = 4096 + 8192 + 256;
 constexpr int DMA_W0 = 7;                           // loads per block, first wave of a pair
 constexpr int DMA_W1 = 6;                           // ... second wave
-constexpr int MAX_KX_LDS = 1024;                    // near leaves per tile the route kernel holds
+constexpr int ROUTE_MAX_KX = 8192;                  // near leaves per tile the route kernel holds in LDS
+constexpr int64_t ROUTE_MAX_NB = 262144;             // leaves per head (exclusion bits: 32 KB of LDS)
+constexpr size_t ROUTE_LDS_MAX = 160 * 1024;         // LDS of one workgroup on gfx950
 constexpr int MAX_PASSES = 3;                       // reference-max retries of a tile
 // Merge: the wave pairs' partial O, 64 rows x 128 dims each, rows padded to 132 floats.
 constexpr int MRG_STRIDE = 132;
@@ -1487,13 +1516,18 @@ __device__ __forceinline__ void dma_rows27(const uint16_t* x0, const uint16_t* x
 // top-k overlap.  SEL never reaches HBM.
 // MULTI: tile groups of G > 1 tiles (keys merged by max over the tiles); NRB = tile / 16 row
 // blocks of 16 rows per tile.
+// GK: the top-k keys of the tile group sit in global memory (keys_ws [H, ng, nb_pad]) instead of
+// LDS, for rows of more leaves than the LDS holds.  The launch covers tile groups
+// [g0, g0 + ng) of each head; the state rows and idx are the launch's own ([H, ng, ...]).
 constexpr int SEL_RING = 3;                         // route_select ring slots per wave
-template <bool MULTI, int NRB>
+constexpr int ROUTE_NB_LDS = 16384;                 // leaves per head whose keys route_select keeps in LDS
+template <bool MULTI, int NRB, bool GK>
 __global__ __launch_bounds__(256, 4) void route_select_kernel(
     const int8_t* __restrict__ dq8, const float* __restrict__ sdq, const int8_t* __restrict__ g8,
-    const float* __restrict__ sg, const float* __restrict__ lz, int nt, int group, int ng, int nb, int nb_pad,
-    int kx, int sink, int stride, int32_t* __restrict__ idx, float* __restrict__ rowmax) {
-    extern __shared__ uint32_t keys[];        // [nb]
+    const float* __restrict__ sg, const float* __restrict__ lz, int nt, int group, int g0, int ng, int nb,
+    int nb_pad, int kx, int sink, int stride, int32_t* __restrict__ idx, float* __restrict__ rowmax,
+    uint32_t* __restrict__ keys_ws) {
+    extern __shared__ uint32_t keys_lds[];    // [nb] unless GK
     __shared__ TopkSmem sm;
     __shared__ float red_m[4][64];
     // each wave's own ring of 16-leaf groups: g8 rows as the two 1 KB QK operand chunks
@@ -1504,7 +1538,8 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
     // one workgroup per tile group (G tiles sharing a centre, state and near leaves; G = 1: a tile)
     const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
     const int gi = (int)(blk % (uint32_t)ng), h = (int)(blk / (uint32_t)ng);
-    const int64_t gs = (int64_t)h * ng + gi;
+    const int64_t gs = (int64_t)h * ng + gi;   // state / idx row (the launch's window)
+    uint32_t* keys = GK ? keys_ws + gs * nb_pad : keys_lds;
     constexpr int TR = 16 * NRB;              // rows per tile
     const int ts = TR / stride;
     struct SelOps {
@@ -1568,7 +1603,7 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
         }
     };
     for (int j = 0; j < (MULTI ? group : 1); ++j) {
-        const int t = gi * group + j;
+        const int t = (g0 + gi) * group + j;
         if (t >= nt) break;                   // padded tiles repeat the last one
         const int64_t th = (int64_t)h * nt + t;
         load_rows_i8(dq8, th * TR, stride, ts, col, grp, b, val);
@@ -1608,7 +1643,7 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
         first = false;
     }
     const int kxe = min(kx, nb);
-    if (kxe > 0) topk_row(keys, nb, kxe, sm, idx + gs * kxe, nullptr, nullptr);
+    if (kxe > 0) topk_row([&](int l) { return keys[l]; }, nb, kxe, sm, idx + gs * kxe, nullptr, nullptr);
 }
 
 // RB = tile / 32: 16-row blocks per wave (tiles of 64 or 32 rows); NP wave pairs split the keys;
@@ -1619,15 +1654,15 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
     const float* __restrict__ sdq, const int8_t* __restrict__ g8, const float* __restrict__ sg,
     const float* __restrict__ lz, const uint16_t* __restrict__ vb, const int8_t* __restrict__ k8,
     const float* __restrict__ ks, const uint16_t* __restrict__ v, const int32_t* __restrict__ idx,
-    const float* __restrict__ rowmax, int64_t nq, int nt, int group, int ng, const int32_t* __restrict__ perm, int64_t nk,
-    int nb, int nb_pad, int kxe, float scale, float* __restrict__ out, float* __restrict__ logz) {
+    const float* __restrict__ rowmax, int64_t nq, int nt, int group, int g0, int ng, const int32_t* __restrict__ perm,
+    int64_t nk, int nb, int nb_pad, int kxe, float scale, float* __restrict__ out, float* __restrict__ logz) {
     constexpr int NT = 128 * NP;                               // threads
     __shared__ __align__(16) char ring[NP][RS][SLOT_BYTES];    // one per wave pair; also merge staging
-    // sized by the launch (route_dyn_bytes): exclusion bits [nb / 32 + 1], then the tile's near
-    // leaves [kxe], so small shapes leave room for more tiles per CU
+    // sized by the launch: exclusion bits [nb / 32 + 1], then the tile's near leaves [kxe], so
+    // small shapes leave room for more tiles per CU
     extern __shared__ __align__(16) uint32_t route_dyn[];
     uint32_t* exbits = route_dyn;
-    uint16_t* sidx = (uint16_t*)(route_dyn + (nb / 32 + 1));
+    uint32_t* sidx = route_dyn + (nb / 32 + 1);
     __shared__ float red_m[64], red_l[NP][64];
     __shared__ int redo;
     constexpr int TR = 32 * RB;                                // rows per tile
@@ -1649,10 +1684,13 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
     };
     // 1-D grid over (tile, head), tile fastest: each XCD runs a contiguous run of tiles of one
     // head at a time, so the near-field leaves adjacent tiles share are fetched into one L2.
+    // The launch covers the tiles of groups [g0, g0 + ng) of each head; state and idx rows are the
+    // launch's own.
+    const int tb = g0 * group, ntw = min(nt, (g0 + ng) * group) - tb;
     const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
-    const int t = (int)(blk % (uint32_t)nt), h = (int)(blk / (uint32_t)nt);
+    const int t = tb + (int)(blk % (uint32_t)ntw), h = (int)(blk / (uint32_t)ntw);
     const int64_t th = (int64_t)h * nt + t;
-    const int64_t gs = (int64_t)h * ng + t / group;            // state / routing row: the tile's group
+    const int64_t gs = (int64_t)h * ng + (t / group - g0);    // state / routing row: the tile's group
     const int64_t kh = (int64_t)h * nk;
     const int64_t row0 = th * TR + 16 * RB * hr + col;         // this lane's rows: row0 (+ 16 when RB = 2)
     // ---- routing of this tile (route_select_kernel)
@@ -1663,7 +1701,7 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
         const int past = nb - 32 * i;          // leaves of word i below nb
         exbits[i] = past >= 32 ? 0u : (past <= 0 ? ~0u : ~0u << past);
     }
-    for (int j = threadIdx.x; j < kxe; j += NT) sidx[j] = (uint16_t)idx[gs * kxe + j];
+    for (int j = threadIdx.x; j < kxe; j += NT) sidx[j] = (uint32_t)idx[gs * kxe + j];
     float mref[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -2356,26 +2394,37 @@ static int stats_lpb(int64_t nt, int nbp, int64_t heads) {
     return 4;
 }
 
-int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
-                    int leaf, int d, float scale, int8_t* g8, float* sg, uint16_t* vb, float* lz, void* stream) {
-    REQUIRE(mu && k && v && g8 && sg && vb && lz, "htrc_leaf_stats: null pointer");
-    REQUIRE(d == D, "htrc_leaf_stats: head dim must be 128");
-    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_leaf_stats: leaf must be 16/32/64/128");
-    REQUIRE(nk > 0 && nk % leaf == 0, "htrc_leaf_stats: key count must be a multiple of the leaf size");
-    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff, "htrc_leaf_stats: bad heads / tiles");
-    REQUIRE(aligned(k, 16) && aligned(v, 16) && aligned(g8, 16) && aligned(vb, 16) && aligned(sg, 16) && aligned(lz, 16),
-            "htrc_leaf_stats: misaligned buffer");
+// Shared checks and launch of the three leaf-statistics stores (STORE 0 int8, 1 bf16, 2 fp8).
+extern "C++" {
+template <int STORE>
+static int leaf_stats_launch(const char* who, const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads,
+                             int64_t nt, int64_t c0, int64_t cn, int64_t nk, int leaf, int d, float scale, void* g,
+                             float* sg, void* vb, float* sv, float* lz, void* stream) {
+    static thread_local char msg[200];
+    auto bad = [&](const char* what) {
+        snprintf(msg, sizeof msg, "%s: %s", who, what);
+        return fail(HTRC_ERR_ARG, msg);
+    };
+    if (!(mu && k && v && g && vb && lz && (STORE == 1 || sg) && (STORE != 2 || sv))) return bad("null pointer");
+    if (d != D) return bad("head dim must be 128");
+    if (!(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128)) return bad("leaf must be 16/32/64/128");
+    if (!(nk > 0 && nk % leaf == 0)) return bad("key count must be a multiple of the leaf size");
+    if (!(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff)) return bad("bad heads / centres");
+    if (!(c0 >= 0 && cn > 0 && c0 + cn <= nt)) return bad("centre window [c0, c0 + cn) must lie in [0, nt)");
+    if (!(aligned(k, 16) && aligned(v, 16) && aligned(g, 16) && aligned(vb, 16) && aligned(lz, 16) &&
+          (STORE == 1 || aligned(sg, 16)) && (STORE != 2 || aligned(sv, 16))))
+        return bad("misaligned buffer");
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
-    const int lpb = stats_lpb(nt, nbp, heads);
-    const int64_t nblocks = (nt + STATS_TPW - 1) / STATS_TPW * ((nbp + lpb - 1) / lpb) * heads;
-    REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats: too many tiles x leaves x heads for one launch");
-    dim3 grid((unsigned)nblocks);
+    const int lpb = stats_lpb(cn, nbp, heads);
+    const int64_t nblocks = (cn + STATS_TPW - 1) / STATS_TPW * ((nbp + lpb - 1) / lpb) * heads;
+    if (nblocks > 0x7fffffff) return bad("too many centres x leaves x heads for one launch");
+    const dim3 grid((unsigned)nblocks);
     hipStream_t s = (hipStream_t)stream;
-#define STATS_CASE(L)                                                                                         \
-    case L:                                                                                                   \
-        hipLaunchKernelGGL((stats_kernel<L, 0, STATS_NW>), grid, dim3(64 * STATS_NW), 0, s, mu, (int)nt, k, v, nk, \
-                           (int)nb, nbp, lpb, scale, g8, sg, vb, nullptr, lz);                                \
+#define STATS_CASE(L)                                                                                            \
+    case L:                                                                                                      \
+        hipLaunchKernelGGL((stats_kernel<L, STORE, STATS_NW>), grid, dim3(64 * STATS_NW), 0, s, mu, nt, c0, (int)cn, \
+                           k, v, nk, (int)nb, nbp, lpb, scale, (int8_t*)g, sg, (uint16_t*)vb, sv, lz);           \
         break;
     switch (leaf) {
         STATS_CASE(16)
@@ -2384,103 +2433,108 @@ int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64
         STATS_CASE(128)
     }
 #undef STATS_CASE
-    return launched("htrc_leaf_stats");
+    return launched(who);
+}
+}  // extern "C++"
+
+int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
+                    int64_t cn, int64_t nk, int leaf, int d, float scale, int8_t* g8, float* sg, uint16_t* vb, float* lz,
+                    void* stream) {
+    return leaf_stats_launch<0>("htrc_leaf_stats", mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g8, sg, vb,
+                                nullptr, lz, stream);
 }
 
-int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
-                        int leaf, int d, float scale, uint8_t* g, float* sg, uint8_t* vb, float* sv, float* lz,
-                        void* stream) {
-    REQUIRE(mu && k && v && g && sg && vb && sv && lz, "htrc_leaf_stats_fp8: null pointer");
-    REQUIRE(d == D, "htrc_leaf_stats_fp8: head dim must be 128");
-    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_leaf_stats_fp8: leaf must be 16/32/64/128");
-    REQUIRE(nk > 0 && nk % leaf == 0, "htrc_leaf_stats_fp8: key count must be a multiple of the leaf size");
-    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff, "htrc_leaf_stats_fp8: bad heads / tiles");
-    REQUIRE(aligned(k, 16) && aligned(v, 16) && aligned(g, 16) && aligned(vb, 16) && aligned(sg, 16) && aligned(sv, 16) &&
-                aligned(lz, 16),
-            "htrc_leaf_stats_fp8: misaligned buffer");
-    const int64_t nb = nk / leaf;
-    const int nbp = htrc_nb_pad(nb);
-    const int lpb = stats_lpb(nt, nbp, heads);
-    const int64_t nblocks = (nt + STATS_TPW - 1) / STATS_TPW * ((nbp + lpb - 1) / lpb) * heads;
-    REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats_fp8: too many tiles x leaves x heads for one launch");
-    dim3 grid((unsigned)nblocks);
-    hipStream_t s = (hipStream_t)stream;
-#define STATS8_CASE(L)                                                                                         \
-    case L:                                                                                                    \
-        hipLaunchKernelGGL((stats_kernel<L, 2, STATS_NW>), grid, dim3(64 * STATS_NW), 0, s, mu, (int)nt, k, v, nk,   \
-                           (int)nb, nbp, lpb,                                                                  \
-                           scale, (int8_t*)g, sg, (uint16_t*)vb, sv, lz);                                      \
-        break;
-    switch (leaf) {
-        STATS8_CASE(16)
-        STATS8_CASE(32)
-        STATS8_CASE(64)
-        STATS8_CASE(128)
-    }
-#undef STATS8_CASE
-    return launched("htrc_leaf_stats_fp8");
+int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
+                        int64_t cn, int64_t nk, int leaf, int d, float scale, uint8_t* g, float* sg, uint8_t* vb,
+                        float* sv, float* lz, void* stream) {
+    return leaf_stats_launch<2>("htrc_leaf_stats_fp8", mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, sg, vb, sv,
+                                lz, stream);
 }
 
-int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
-                         int leaf, int d, float scale, uint16_t* g, uint16_t* vb, float* lz, void* stream) {
-    REQUIRE(mu && k && v && g && vb && lz, "htrc_leaf_stats_bf16: null pointer");
-    REQUIRE(d == D, "htrc_leaf_stats_bf16: head dim must be 128");
-    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_leaf_stats_bf16: leaf must be 16/32/64/128");
-    REQUIRE(nk > 0 && nk % leaf == 0, "htrc_leaf_stats_bf16: key count must be a multiple of the leaf size");
-    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff, "htrc_leaf_stats_bf16: bad heads / tiles");
-    REQUIRE(aligned(k, 16) && aligned(v, 16) && aligned(g, 16) && aligned(vb, 16) && aligned(lz, 16),
-            "htrc_leaf_stats_bf16: misaligned buffer");
-    const int64_t nb = nk / leaf;
-    const int nbp = htrc_nb_pad(nb);
-    const int lpb = stats_lpb(nt, nbp, heads);
-    const int64_t nblocks = (nt + STATS_TPW - 1) / STATS_TPW * ((nbp + lpb - 1) / lpb) * heads;
-    REQUIRE(nblocks <= 0x7fffffff, "htrc_leaf_stats_bf16: too many tiles x leaves x heads for one launch");
-    dim3 grid((unsigned)nblocks);
-    hipStream_t s = (hipStream_t)stream;
-#define STATSB_CASE(L)                                                                                         \
-    case L:                                                                                                    \
-        hipLaunchKernelGGL((stats_kernel<L, 1, STATS_NW>), grid, dim3(64 * STATS_NW), 0, s, mu, (int)nt, k, v, nk,   \
-                           (int)nb, nbp, lpb,                                                                  \
-                           scale, (int8_t*)g, nullptr, vb, nullptr, lz);                                       \
-        break;
-    switch (leaf) {
-        STATSB_CASE(16)
-        STATSB_CASE(32)
-        STATSB_CASE(64)
-        STATSB_CASE(128)
-    }
-#undef STATSB_CASE
-    return launched("htrc_leaf_stats_bf16");
+int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
+                         int64_t cn, int64_t nk, int leaf, int d, float scale, uint16_t* g, uint16_t* vb, float* lz,
+                         void* stream) {
+    return leaf_stats_launch<1>("htrc_leaf_stats_bf16", mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr,
+                                vb, nullptr, lz, stream);
 }
+
+// Window of tile groups [g0, g0 + gn) of a head of nt tiles in groups of `group`: sets ng (all
+// groups), tb (first tile) and ntw (tiles of the window); false when the window is empty or
+// leaves the head.
+static bool group_window(int64_t nt, int group, int64_t g0, int64_t gn, int64_t& ng, int64_t& tb, int64_t& ntw) {
+    if (group < 1 || nt <= 0) return false;
+    ng = (nt + group - 1) / group;
+    if (g0 < 0 || gn <= 0 || g0 + gn > ng) return false;
+    tb = g0 * group;
+    const int64_t te = (g0 + gn) * group < nt ? (g0 + gn) * group : nt;
+    ntw = te - tb;
+    return ntw > 0;
+}
+
+extern "C++" {
+template <int KIND>   // 0: int8 state, 1: bf16 state, 2: fp8 state
+static int select_launch(const char* who, const void* dq, const float* sdq, const void* g, const float* sg,
+                         const float* lz, int64_t heads, int64_t nt, int64_t nb, int stride, int tile, int group,
+                         int64_t g0, int64_t gn, int d, float* sel, void* stream) {
+    static thread_local char msg[200];
+    auto bad = [&](const char* what) {
+        snprintf(msg, sizeof msg, "%s: %s", who, what);
+        return fail(HTRC_ERR_ARG, msg);
+    };
+    if (!(dq && g && lz && sel && (KIND != 0 || sdq) && (KIND == 1 || sg))) return bad("null pointer");
+    if (d != D) return bad("head dim must be 128");
+    if (!(tile == 32 || tile == 64)) return bad("tile must be 32 or 64 rows");
+    if (!(stride >= 1 && stride <= tile && tile % stride == 0)) return bad("stride must divide the tile");
+    if (!(group >= 1 && group <= 1024)) return bad("group must be in [1, 1024]");
+    if (!(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff && nb > 0 && nb <= 0x7fffffff))
+        return bad("bad sizes");
+    int64_t ng, tb, ntw;
+    if (!group_window(nt, group, g0, gn, ng, tb, ntw)) return bad("group window [g0, g0 + gn) must lie in the head's groups");
+    if (KIND != 0 && !(aligned(dq, 16) && aligned(g, 16) && aligned(lz, 16) && (KIND == 1 || aligned(sg, 16))))
+        return bad("misaligned buffer");
+    const int nbp = htrc_nb_pad(nb);
+    const dim3 grid((unsigned)gn, (unsigned)((nb + 255) / 256), (unsigned)heads);
+    hipStream_t s = (hipStream_t)stream;
+#define SEL_ARGS (int)nt, group, (int)g0, (int)gn, (int)nb, nbp, sel
+    if constexpr (KIND == 0) {
+        if (tile == 64)
+            hipLaunchKernelGGL(select_kernel<4>, grid, dim3(256), 0, s, (const int8_t*)dq, sdq, stride,
+                               (const int8_t*)g, sg, lz, SEL_ARGS);
+        else
+            hipLaunchKernelGGL(select_kernel<2>, grid, dim3(256), 0, s, (const int8_t*)dq, sdq, stride,
+                               (const int8_t*)g, sg, lz, SEL_ARGS);
+    } else {
+        constexpr bool FP8 = KIND == 2;
+        if (tile == 64)
+            hipLaunchKernelGGL((select16_kernel<FP8, 4>), grid, dim3(256), 0, s, (const uint16_t*)dq, stride, g, sg, lz,
+                               SEL_ARGS);
+        else
+            hipLaunchKernelGGL((select16_kernel<FP8, 2>), grid, dim3(256), 0, s, (const uint16_t*)dq, stride, g, sg, lz,
+                               SEL_ARGS);
+    }
+#undef SEL_ARGS
+    return launched(who);
+}
+}  // extern "C++"
 
 int htrc_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
-                int64_t heads, int64_t nt, int64_t nb, int stride, int tile, int group, int d, float* sel,
-                void* stream) {
-    REQUIRE(dq8 && sdq && g8 && sg && lz && sel, "htrc_select: null pointer");
-    REQUIRE(d == D, "htrc_select: head dim must be 128");
-    REQUIRE(tile == 32 || tile == 64, "htrc_select: tile must be 32 or 64 rows");
-    REQUIRE(stride >= 1 && stride <= tile && tile % stride == 0, "htrc_select: stride must divide the tile");
-    REQUIRE(group >= 1 && group <= 1024, "htrc_select: group must be in [1, 1024]");
-    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff && nb > 0, "htrc_select: bad sizes");
-    const int nbp = htrc_nb_pad(nb);
-    const int64_t ng = (nt + group - 1) / group;
-    dim3 grid((unsigned)ng, (unsigned)((nb + 255) / 256), (unsigned)heads);
-    if (tile == 64)
-        hipLaunchKernelGGL(select_kernel<4>, grid, dim3(256), 0, (hipStream_t)stream, dq8, sdq, stride, g8, sg, lz,
-                           (int)nt, group, (int)ng, (int)nb, nbp, sel);
-    else
-        hipLaunchKernelGGL(select_kernel<2>, grid, dim3(256), 0, (hipStream_t)stream, dq8, sdq, stride, g8, sg, lz,
-                           (int)nt, group, (int)ng, (int)nb, nbp, sel);
-    return launched("htrc_select");
+                int64_t heads, int64_t nt, int64_t nb, int stride, int tile, int group, int64_t g0, int64_t gn, int d,
+                float* sel, void* stream) {
+    return select_launch<0>("htrc_select", dq8, sdq, g8, sg, lz, heads, nt, nb, stride, tile, group, g0, gn, d, sel,
+                            stream);
 }
 
 int htrc_topk(const float* sel, int64_t rows, int64_t nb, int kx, int sink, int32_t* idx, int8_t* excl,
               void* stream) {
     REQUIRE(sel && idx && excl, "htrc_topk: null pointer");
-    REQUIRE(rows > 0 && rows <= 0x7fffffff && nb > 0 && nb <= MAX_NB_LDS, "htrc_topk: leaves per head must be in [1, 8192]");
+    REQUIRE(rows > 0 && rows <= 0x7fffffff && nb > 0 && nb <= 0x7fffffff, "htrc_topk: bad rows / leaves");
     REQUIRE(kx > 0 && kx <= nb && sink >= 0, "htrc_topk: need 0 < k <= leaves");
-    hipLaunchKernelGGL(topk_kernel, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, sel, (int)nb,
-                       htrc_nb_pad(nb), kx, sink, idx, excl);
+    if (nb <= MAX_NB_LDS)
+        hipLaunchKernelGGL(topk_kernel<true>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, sel, (int)nb,
+                           htrc_nb_pad(nb), kx, sink, idx, excl);
+    else
+        hipLaunchKernelGGL(topk_kernel<false>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, sel, (int)nb,
+                           htrc_nb_pad(nb), kx, sink, idx, excl);
     return launched("htrc_topk");
 }
 
@@ -2490,34 +2544,55 @@ static int64_t split_len(int64_t n, int64_t ns, int64_t bn) {   // _split, h3/ht
     return r > bn ? r : bn;
 }
 
-int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
-              const float* sg, const float* lz, const uint16_t* vb, const int8_t* excl, const int32_t* idx,
-              const int8_t* k8, const float* ks, const uint16_t* v, int64_t heads, int64_t nq, int64_t nk,
-              int leaf, int d, int kx, int tile, int group, const int32_t* perm, int splits, int bn, float scale,
-              float* pm, float* pl, float* pacc, float* out, float* logz, void* stream) {
-    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && excl && k8 && ks && v,
-            "htrc_tile: null input pointer");
-    REQUIRE(d == D, "htrc_tile: head dim must be 128");
-    REQUIRE(tile == 32 || tile == 64, "htrc_tile: tile must be 32 or 64 rows");
-    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_tile: leaf must be 16/32/64/128");
-    REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_tile: bad sizes");
+extern "C++" {
+template <int KIND>   // 0: int8 state, 1: bf16 state, 2: fp8 state
+static int tile_launch(const char* who, const void* q, const float* sq, const void* dq, const float* sdq, const void* g,
+                       const float* sg, const float* lz, const void* vb, const float* sv, const int8_t* excl,
+                       const int32_t* idx, const void* k, const float* ks, const uint16_t* v, int64_t heads, int64_t nq,
+                       int64_t nk, int leaf, int d, int kx, int tile, int group, int64_t g0, int64_t gn,
+                       const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
+                       float* out, float* logz, void* stream) {
+    static thread_local char msg[200];
+    auto bad = [&](const char* what) {
+        snprintf(msg, sizeof msg, "%s: %s", who, what);
+        return fail(HTRC_ERR_ARG, msg);
+    };
+    if (!(q && dq && g && lz && vb && excl && k && v && (KIND != 0 || (sq && sdq && ks)) && (KIND == 1 || sg) &&
+          (KIND != 2 || sv)))
+        return bad("null input pointer");
+    if (d != D) return bad("head dim must be 128");
+    if (!(tile == 32 || tile == 64)) return bad("tile must be 32 or 64 rows");
+    if (!(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128)) return bad("leaf must be 16/32/64/128");
+    if (!(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535)) return bad("bad sizes");
     const int64_t nb = nk / leaf, nt = (nq + tile - 1) / tile;
-    REQUIRE(kx >= 0 && kx <= nb && (kx == 0 || idx), "htrc_tile: need 0 <= kx <= leaves and idx when kx > 0");
-    REQUIRE(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0, "htrc_tile: need 1 <= splits <= 64 and a block that is a multiple of 32");
-    REQUIRE(splits == 1 ? (out && logz) : (pm && pl && pacc), "htrc_tile: missing outputs");
-    REQUIRE(group >= 1 && group <= 1024, "htrc_tile: group must be in [1, 1024]");
-    const int64_t ng = (nt + group - 1) / group;
+    if (!(nt <= 0x7fffffff && nb <= 0x7fffffff)) return bad("too many tiles / leaves");
+    if (!(kx >= 0 && kx <= nb && (kx == 0 || idx))) return bad("need 0 <= kx <= leaves and idx when kx > 0");
+    if (!(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0))
+        return bad("need 1 <= splits <= 64 and a block that is a multiple of 32");
+    if (!(splits == 1 ? (out && logz) : (pm && pl && pacc))) return bad("missing outputs");
+    if (!(group >= 1 && group <= 1024)) return bad("group must be in [1, 1024]");
+    int64_t ng, tb, ntw;
+    if (!group_window(nt, group, g0, gn, ng, tb, ntw)) return bad("group window [g0, g0 + gn) must lie in the head's groups");
+    if (KIND != 0 && !(aligned(q, 16) && aligned(dq, 16) && aligned(g, 16) && aligned(k, 16) && aligned(lz, 16) &&
+                       (KIND == 1 || aligned(sg, 16)) && (KIND != 2 || aligned(sv, 16))))
+        return bad("misaligned buffer");
     const int lps = (int)split_len(nb, splits, bn), eps = (int)split_len((int64_t)kx * leaf, splits, bn);
-    dim3 grid((unsigned)nt, (unsigned)splits, (unsigned)heads);
+    const dim3 grid((unsigned)ntw, (unsigned)splits, (unsigned)heads);
     hipStream_t s = (hipStream_t)stream;
     float* ppm = splits == 1 ? nullptr : pm;
     float* ppl = splits == 1 ? nullptr : pl;
     float* ppa = splits == 1 ? nullptr : pacc;
-#define TILE_CASE(L)                                                                                            \
-    case L:                                                                                                     \
-        hipLaunchKernelGGL(tile_kernel<L>, grid, dim3(4 * tile), 0, s, q8, sq, dq8, sdq, g8, sg, lz, vb, excl, idx, \
-                           k8, ks, v, nq, (int)nt, tile, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, \
-                           eps, scale, ppm, ppl, ppa, out, logz);                                               \
+#define TILE_TAIL nq, (int)nt, tile, group, (int)g0, (int)gn, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps, scale, \
+                  ppm, ppl, ppa, out, logz
+#define TILE_CASE(L)                                                                                               \
+    case L:                                                                                                        \
+        if constexpr (KIND == 0)                                                                                   \
+            hipLaunchKernelGGL(tile_kernel<L>, grid, dim3(4 * tile), 0, s, (const int8_t*)q, sq, (const int8_t*)dq, sdq, \
+                               (const int8_t*)g, sg, lz, (const uint16_t*)vb, excl, idx, (const int8_t*)k, ks, v,   \
+                               TILE_TAIL);                                                                         \
+        else                                                                                                       \
+            hipLaunchKernelGGL((tile16_kernel<L, KIND == 2>), grid, dim3(4 * tile), 0, s, (const uint16_t*)q,         \
+                               (const uint16_t*)dq, g, sg, lz, vb, sv, excl, idx, (const uint16_t*)k, v, TILE_TAIL);  \
         break;
     switch (leaf) {
         TILE_CASE(16)
@@ -2526,7 +2601,18 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
         TILE_CASE(128)
     }
 #undef TILE_CASE
-    return launched("htrc_tile");
+#undef TILE_TAIL
+    return launched(who);
+}
+}  // extern "C++"
+
+int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
+              const float* sg, const float* lz, const uint16_t* vb, const int8_t* excl, const int32_t* idx,
+              const int8_t* k8, const float* ks, const uint16_t* v, int64_t heads, int64_t nq, int64_t nk,
+              int leaf, int d, int kx, int tile, int group, int64_t g0, int64_t gn, const int32_t* perm, int splits,
+              int bn, float scale, float* pm, float* pl, float* pacc, float* out, float* logz, void* stream) {
+    return tile_launch<0>("htrc_tile", q8, sq, dq8, sdq, g8, sg, lz, vb, nullptr, excl, idx, k8, ks, v, heads, nq, nk,
+                          leaf, d, kx, tile, group, g0, gn, perm, splits, bn, scale, pm, pl, pacc, out, logz, stream);
 }
 
 int htrc_pack_q16(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int tile, int group,
@@ -2566,144 +2652,57 @@ int htrc_pack_q16(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d
 }
 
 int htrc_select_fp8(const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz, int64_t heads, int64_t nt,
-                    int64_t nb, int stride, int tile, int group, int d, float* sel, void* stream) {
-    REQUIRE(dq16 && g && sg && lz && sel, "htrc_select_fp8: null pointer");
-    REQUIRE(d == D, "htrc_select_fp8: head dim must be 128");
-    REQUIRE(tile == 32 || tile == 64, "htrc_select_fp8: tile must be 32 or 64 rows");
-    REQUIRE(stride >= 1 && stride <= tile && tile % stride == 0, "htrc_select_fp8: stride must divide the tile");
-    REQUIRE(group >= 1 && group <= 1024, "htrc_select_fp8: group must be in [1, 1024]");
-    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff && nb > 0, "htrc_select_fp8: bad sizes");
-    REQUIRE(aligned(dq16, 16) && aligned(g, 16) && aligned(sg, 16) && aligned(lz, 16), "htrc_select_fp8: misaligned buffer");
-    const int nbp = htrc_nb_pad(nb);
-    const int64_t ng = (nt + group - 1) / group;
-    dim3 grid((unsigned)ng, (unsigned)((nb + 255) / 256), (unsigned)heads);
-    if (tile == 64)
-        hipLaunchKernelGGL((select16_kernel<true, 4>), grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, sg, lz,
-                           (int)nt, group, (int)ng, (int)nb, nbp, sel);
-    else
-        hipLaunchKernelGGL((select16_kernel<true, 2>), grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, sg, lz,
-                           (int)nt, group, (int)ng, (int)nb, nbp, sel);
-    return launched("htrc_select_fp8");
+                    int64_t nb, int stride, int tile, int group, int64_t g0, int64_t gn, int d, float* sel,
+                    void* stream) {
+    return select_launch<2>("htrc_select_fp8", dq16, nullptr, g, sg, lz, heads, nt, nb, stride, tile, group, g0, gn, d,
+                            sel, stream);
 }
 
 int htrc_select_bf16(const uint16_t* dq16, const uint16_t* g, const float* lz, int64_t heads, int64_t nt, int64_t nb,
-                     int stride, int tile, int group, int d, float* sel, void* stream) {
-    REQUIRE(dq16 && g && lz && sel, "htrc_select_bf16: null pointer");
-    REQUIRE(d == D, "htrc_select_bf16: head dim must be 128");
-    REQUIRE(tile == 32 || tile == 64, "htrc_select_bf16: tile must be 32 or 64 rows");
-    REQUIRE(stride >= 1 && stride <= tile && tile % stride == 0, "htrc_select_bf16: stride must divide the tile");
-    REQUIRE(group >= 1 && group <= 1024, "htrc_select_bf16: group must be in [1, 1024]");
-    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff && nb > 0, "htrc_select_bf16: bad sizes");
-    REQUIRE(aligned(dq16, 16) && aligned(g, 16) && aligned(lz, 16), "htrc_select_bf16: misaligned buffer");
-    const int nbp = htrc_nb_pad(nb);
-    const int64_t ng = (nt + group - 1) / group;
-    dim3 grid((unsigned)ng, (unsigned)((nb + 255) / 256), (unsigned)heads);
-    if (tile == 64)
-        hipLaunchKernelGGL((select16_kernel<false, 4>), grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, nullptr,
-                           lz, (int)nt, group, (int)ng, (int)nb, nbp, sel);
-    else
-        hipLaunchKernelGGL((select16_kernel<false, 2>), grid, dim3(256), 0, (hipStream_t)stream, dq16, stride, g, nullptr,
-                           lz, (int)nt, group, (int)ng, (int)nb, nbp, sel);
-    return launched("htrc_select_bf16");
+                     int stride, int tile, int group, int64_t g0, int64_t gn, int d, float* sel, void* stream) {
+    return select_launch<1>("htrc_select_bf16", dq16, nullptr, g, nullptr, lz, heads, nt, nb, stride, tile, group, g0,
+                            gn, d, sel, stream);
 }
 
 int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz,
                   const uint8_t* vb, const float* sv, const int8_t* excl, const int32_t* idx, const uint16_t* k,
                   const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int tile,
-                  int group, const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
-                  float* out, float* logz, void* stream) {
-    REQUIRE(q16 && dq16 && g && sg && lz && vb && sv && excl && k && v, "htrc_tile_fp8: null input pointer");
-    REQUIRE(d == D, "htrc_tile_fp8: head dim must be 128");
-    REQUIRE(tile == 32 || tile == 64, "htrc_tile_fp8: tile must be 32 or 64 rows");
-    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_tile_fp8: leaf must be 16/32/64/128");
-    REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_tile_fp8: bad sizes");
-    const int64_t nb = nk / leaf, nt = (nq + tile - 1) / tile;
-    REQUIRE(kx >= 0 && kx <= nb && (kx == 0 || idx), "htrc_tile_fp8: need 0 <= kx <= leaves and idx when kx > 0");
-    REQUIRE(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0, "htrc_tile_fp8: need 1 <= splits <= 64 and a block that is a multiple of 32");
-    REQUIRE(splits == 1 ? (out && logz) : (pm && pl && pacc), "htrc_tile_fp8: missing outputs");
-    REQUIRE(group >= 1 && group <= 1024, "htrc_tile_fp8: group must be in [1, 1024]");
-    REQUIRE(aligned(q16, 16) && aligned(dq16, 16) && aligned(g, 16) && aligned(k, 16) && aligned(sg, 16) &&
-                aligned(sv, 16) && aligned(lz, 16),
-            "htrc_tile_fp8: misaligned buffer");
-    const int64_t ng = (nt + group - 1) / group;
-    const int lps = (int)split_len(nb, splits, bn), eps = (int)split_len((int64_t)kx * leaf, splits, bn);
-    dim3 grid((unsigned)nt, (unsigned)splits, (unsigned)heads);
-    hipStream_t s = (hipStream_t)stream;
-    float* ppm = splits == 1 ? nullptr : pm;
-    float* ppl = splits == 1 ? nullptr : pl;
-    float* ppa = splits == 1 ? nullptr : pacc;
-#define TILE8_CASE(L)                                                                                              \
-    case L:                                                                                                        \
-        hipLaunchKernelGGL((tile16_kernel<L, true>), grid, dim3(4 * tile), 0, s, q16, dq16, g, sg, lz, vb, sv, excl, idx, \
-                           k, v, nq, (int)nt, tile, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx, lps, eps,   \
-                           scale, ppm, ppl, ppa, out, logz);                                                       \
-        break;
-    switch (leaf) {
-        TILE8_CASE(16)
-        TILE8_CASE(32)
-        TILE8_CASE(64)
-        TILE8_CASE(128)
-    }
-#undef TILE8_CASE
-    return launched("htrc_tile_fp8");
+                  int group, int64_t g0, int64_t gn, const int32_t* perm, int splits, int bn, float scale, float* pm,
+                  float* pl, float* pacc, float* out, float* logz, void* stream) {
+    return tile_launch<2>("htrc_tile_fp8", q16, nullptr, dq16, nullptr, g, sg, lz, vb, sv, excl, idx, k, nullptr, v,
+                          heads, nq, nk, leaf, d, kx, tile, group, g0, gn, perm, splits, bn, scale, pm, pl, pacc, out,
+                          logz, stream);
 }
 
 int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g, const float* lz, const uint16_t* vb,
                    const int8_t* excl, const int32_t* idx, const uint16_t* k, const uint16_t* v, int64_t heads,
-                   int64_t nq, int64_t nk, int leaf, int d, int kx, int tile, int group, const int32_t* perm,
-                   int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out, float* logz,
-                   void* stream) {
-    REQUIRE(q16 && dq16 && g && lz && vb && excl && k && v, "htrc_tile_bf16: null input pointer");
-    REQUIRE(d == D, "htrc_tile_bf16: head dim must be 128");
-    REQUIRE(tile == 32 || tile == 64, "htrc_tile_bf16: tile must be 32 or 64 rows");
-    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_tile_bf16: leaf must be 16/32/64/128");
-    REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_tile_bf16: bad sizes");
-    const int64_t nb = nk / leaf, nt = (nq + tile - 1) / tile;
-    REQUIRE(kx >= 0 && kx <= nb && (kx == 0 || idx), "htrc_tile_bf16: need 0 <= kx <= leaves and idx when kx > 0");
-    REQUIRE(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0, "htrc_tile_bf16: need 1 <= splits <= 64 and a block that is a multiple of 32");
-    REQUIRE(splits == 1 ? (out && logz) : (pm && pl && pacc), "htrc_tile_bf16: missing outputs");
-    REQUIRE(group >= 1 && group <= 1024, "htrc_tile_bf16: group must be in [1, 1024]");
-    REQUIRE(aligned(q16, 16) && aligned(dq16, 16) && aligned(g, 16) && aligned(k, 16) && aligned(lz, 16),
-            "htrc_tile_bf16: misaligned buffer");
-    const int64_t ng = (nt + group - 1) / group;
-    const int lps = (int)split_len(nb, splits, bn), eps = (int)split_len((int64_t)kx * leaf, splits, bn);
-    dim3 grid((unsigned)nt, (unsigned)splits, (unsigned)heads);
-    hipStream_t s = (hipStream_t)stream;
-    float* ppm = splits == 1 ? nullptr : pm;
-    float* ppl = splits == 1 ? nullptr : pl;
-    float* ppa = splits == 1 ? nullptr : pacc;
-#define TILEB_CASE(L)                                                                                              \
-    case L:                                                                                                        \
-        hipLaunchKernelGGL((tile16_kernel<L, false>), grid, dim3(4 * tile), 0, s, q16, dq16, g, nullptr, lz, vb, nullptr, \
-                           excl, idx, k, v, nq, (int)nt, tile, group, (int)ng, perm, nk, (int)nb, htrc_nb_pad(nb), kx,  \
-                           lps, eps, scale, ppm, ppl, ppa, out, logz);                                             \
-        break;
-    switch (leaf) {
-        TILEB_CASE(16)
-        TILEB_CASE(32)
-        TILEB_CASE(64)
-        TILEB_CASE(128)
-    }
-#undef TILEB_CASE
-    return launched("htrc_tile_bf16");
+                   int64_t nq, int64_t nk, int leaf, int d, int kx, int tile, int group, int64_t g0, int64_t gn,
+                   const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out,
+                   float* logz, void* stream) {
+    return tile_launch<1>("htrc_tile_bf16", q16, nullptr, dq16, nullptr, g, nullptr, lz, vb, nullptr, excl, idx, k,
+                          nullptr, v, heads, nq, nk, leaf, d, kx, tile, group, g0, gn, perm, splits, bn, scale, pm, pl,
+                          pacc, out, logz, stream);
 }
 
-int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int tile, int splits,
-               int d, const int32_t* perm, float* out, float* logz, void* stream) {
+int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int tile, int64_t t0,
+               int64_t tn, int splits, int d, const int32_t* perm, float* out, float* logz, void* stream) {
     REQUIRE(pm && pl && pacc && out && logz, "htrc_merge: null pointer");
     REQUIRE(tile == 32 || tile == 64, "htrc_merge: tile must be 32 or 64 rows");
     REQUIRE(d == D && splits >= 1 && heads > 0 && heads <= 65535 && nq > 0, "htrc_merge: bad sizes");
     const int64_t nt = (nq + tile - 1) / tile;
     REQUIRE(nt <= 0x7fffffff, "htrc_merge: too many tiles");
-    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)nt, (unsigned)heads), dim3(4 * tile), 0, (hipStream_t)stream, pm,
-                       pl, pacc, splits, nq, (int)nt, tile, perm, out, logz);
+    REQUIRE(t0 >= 0 && tn > 0 && t0 + tn <= nt, "htrc_merge: tile window [t0, t0 + tn) must lie in the head's tiles");
+    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)tn, (unsigned)heads), dim3(4 * tile), 0, (hipStream_t)stream, pm,
+                       pl, pacc, splits, nq, (int)t0, tile, perm, out, logz);
     return launched("htrc_merge");
 }
 
-// Shape checks shared by the route entry points; sets nb, nt, ng (tile groups), kxe.
+// Shape checks shared by the route entry points; sets nb, nt, ng (all tile groups of a head), tb
+// and ntw (first tile and tile count of the window of groups [g0, g0 + gn)) and kxe.
 static int route_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int tile,
-                        int group, int64_t& nb, int64_t& nt, int64_t& ng, int& kxe) {
-    static thread_local char msg[160];
+                        int group, int64_t g0, int64_t gn, int64_t& nb, int64_t& nt, int64_t& ng, int64_t& tb,
+                        int64_t& ntw, int& kxe) {
+    static thread_local char msg[200];
     auto bad = [&](const char* what) {
         snprintf(msg, sizeof msg, "%s: %s", who, what);
         return fail(HTRC_ERR_ARG, msg);
@@ -2714,70 +2713,91 @@ static int route_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, 
     if (!(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535)) return bad("bad sizes");
     nb = nk / leaf;
     nt = (nq + tile - 1) / tile;
-    if (nb > MAX_NB_LDS) return bad("at most 8192 leaves per head");
+    if (nb > ROUTE_MAX_NB) return bad("at most 262144 leaves per head");
+    if (nt > 0x7fffffff) return bad("too many tiles");
     if (kx < 0) return bad("need kx >= 0");
     if (group < 1 || group > 1024) return bad("group must be in [1, 1024]");
-    ng = (nt + group - 1) / group;
+    if (!group_window(nt, group, g0, gn, ng, tb, ntw)) return bad("group window [g0, g0 + gn) must lie in the head's groups");
     kxe = (int)(kx < nb ? kx : nb);
-    if (kxe > MAX_KX_LDS) return bad("at most 1024 near leaves per tile");
-    if (nt * heads > 0x7fffffff) return bad("too many tiles x heads for one launch");
+    if (kxe > ROUTE_MAX_KX) return bad("at most 8192 near leaves per tile (the split tile kernel takes more)");
+    if (ntw * heads > 0x7fffffff || gn * heads > 0x7fffffff) return bad("too many tiles x heads for one launch");
     return HTRC_OK;
 }
 
 int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
                       int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink, int stride,
-                      int tile, int group, int32_t* idx, float* rowmax, void* stream) {
+                      int tile, int group, int64_t g0, int64_t gn, int32_t* idx, float* rowmax, uint32_t* keys_ws,
+                      void* stream) {
     REQUIRE(dq8 && sdq && g8 && sg && lz && rowmax, "htrc_route_select: null pointer");
     REQUIRE(aligned(g8, 16) && aligned(sg, 16) && aligned(lz, 16), "htrc_route_select: misaligned buffer");
-    int64_t nb, nt, ng;
+    int64_t nb, nt, ng, tb, ntw;
     int kxe;
-    const int rc = route_shapes("htrc_route_select", heads, nq, nk, leaf, d, kx, tile, group, nb, nt, ng, kxe);
+    const int rc = route_shapes("htrc_route_select", heads, nq, nk, leaf, d, kx, tile, group, g0, gn, nb, nt, ng, tb,
+                                ntw, kxe);
     if (rc != HTRC_OK) return rc;
     REQUIRE(sink >= 0, "htrc_route_select: need sink >= 0");
     REQUIRE(kxe == 0 || idx, "htrc_route_select: idx is required when kx > 0");
     REQUIRE(stride >= 1 && stride <= tile && tile % stride == 0, "htrc_route_select: stride must divide the tile");
+    const bool gk = nb > ROUTE_NB_LDS;
+    REQUIRE(!gk || keys_ws, "htrc_route_select: keys_ws [H, gn, nb_pad] is required above 16384 leaves per head");
     const int nbp = htrc_nb_pad(nb);
-#define RSEL(M, N)                                                                                              \
-    hipLaunchKernelGGL((route_select_kernel<M, N>), dim3((unsigned)(ng * heads)), dim3(256), (size_t)4 * nbp,    \
-                       (hipStream_t)stream, dq8, sdq, g8, sg, lz, (int)nt, group, (int)ng, (int)nb, nbp, kxe, sink, \
-                       stride, idx, rowmax)
+    const size_t dyn = gk ? 0 : (size_t)4 * nbp;
+#define RSEL(M, N, G)                                                                                           \
+    hipLaunchKernelGGL((route_select_kernel<M, N, G>), dim3((unsigned)(gn * heads)), dim3(256), dyn,             \
+                       (hipStream_t)stream, dq8, sdq, g8, sg, lz, (int)nt, group, (int)g0, (int)gn, (int)nb, nbp, kxe, \
+                       sink, stride, idx, rowmax, keys_ws)
+#define RSEL_G(M, N) \
+    if (gk) RSEL(M, N, true); else RSEL(M, N, false);
     if (tile == 64) {
-        if (group == 1) RSEL(false, 4); else RSEL(true, 4);
+        if (group == 1) { RSEL_G(false, 4) } else { RSEL_G(true, 4) }
     } else {
-        if (group == 1) RSEL(false, 2); else RSEL(true, 2);
+        if (group == 1) { RSEL_G(false, 2) } else { RSEL_G(true, 2) }
     }
+#undef RSEL_G
 #undef RSEL
     return launched("htrc_route_select");
 }
 
+// Dynamic LDS of route_kernel: exclusion bits [nb / 32 + 1] and the tile's near leaves [kxe].
+static size_t route_dyn_bytes(int64_t nb, int kxe) { return ((size_t)(nb / 32 + 1) * 4 + (size_t)kxe * 4 + 15) / 16 * 16; }
+
+// Static LDS of route_kernel with NP wave pairs: the ring plus the row reductions.
+static size_t route_static_bytes(int np) { return (size_t)np * ROUTE_RS * SLOT_BYTES + 64 * 4 * (1 + np) + 16; }
+
 int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                       const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                       const uint16_t* v, const int32_t* idx, const float* rowmax, int64_t heads, int64_t nq,
-                      int64_t nk, int leaf, int d, int kx, int tile, int group, const int32_t* perm, float scale,
-                      float* out, float* logz, void* stream) {
+                      int64_t nk, int leaf, int d, int kx, int tile, int group, int64_t g0, int64_t gn,
+                      const int32_t* perm, float scale, float* out, float* logz, void* stream) {
     REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && k8 && ks && v && rowmax && out && logz,
             "htrc_route_attend: null pointer");
     REQUIRE(aligned(vb, 16) && aligned(v, 16) && aligned(g8, 16) && aligned(k8, 16) && aligned(sg, 16) &&
                 aligned(ks, 16) && aligned(lz, 16) && aligned(q8, 16) && aligned(dq8, 16),
             "htrc_route_attend: misaligned buffer");
-    int64_t nb, nt, ng;
+    int64_t nb, nt, ng, tb, ntw;
     int kxe;
-    const int rc = route_shapes("htrc_route_attend", heads, nq, nk, leaf, d, kx, tile, group, nb, nt, ng, kxe);
+    const int rc = route_shapes("htrc_route_attend", heads, nq, nk, leaf, d, kx, tile, group, g0, gn, nb, nt, ng, tb,
+                                ntw, kxe);
     if (rc != HTRC_OK) return rc;
     REQUIRE(kxe == 0 || idx, "htrc_route_attend: idx is required when kx > 0");
     const int nbp = htrc_nb_pad(nb);
-    const dim3 grid((unsigned)(nt * heads));
+    const dim3 grid((unsigned)(ntw * heads));
     hipStream_t s = (hipStream_t)stream;
-    // Wave pairs per tile by grid size: one (all of the tile's keys; five tiles per CU) when
-    // the grid gives every CU at least two tiles, two (key halves merged in LDS) below that,
-    // four (key quarters, one tile per CU) when the grid has no more tiles than CUs.  The
-    // choice depends on the grid only, so repeated calls of one shape give identical bits.
+    // Wave pairs per tile by the layer's tile count: one (all of the tile's keys; several tiles
+    // per CU) when the layer gives every CU at least two tiles, two (key halves merged in LDS)
+    // below that, four (key quarters, one tile per CU) when it has no more tiles than CUs; fewer
+    // pairs when the near list and exclusion bits would not fit the LDS beside the larger ring.
+    // The choice depends on the layer's shape only (not on the window), so repeated calls and
+    // every windowing of one layer give identical bits.
     const int64_t cus = device_cus();
-    const int np = nt * heads >= 2 * cus ? 1 : (nt * heads > cus ? 2 : 4);
-    const size_t dyn = ((size_t)(nb / 32 + 1) * 4 + (size_t)kxe * 2 + 15) / 16 * 16;
+    const size_t dyn = route_dyn_bytes(nb, kxe);
+    int np = nt * heads >= 2 * cus ? 1 : (nt * heads > cus ? 2 : 4);
+    while (np > 1 && route_static_bytes(np) + dyn > ROUTE_LDS_MAX) np /= 2;
+    REQUIRE(route_static_bytes(np) + dyn <= ROUTE_LDS_MAX, "htrc_route_attend: near list and exclusion bits exceed the LDS");
 #define ROUTE_LAUNCH(L, RB, NP)                                                                                \
     hipLaunchKernelGGL((route_kernel<L, RB, NP, ROUTE_RS>), grid, dim3(128 * NP), dyn, s, q8, sq, dq8, sdq, g8, sg, lz, vb, \
-                       k8, ks, v, idx, rowmax, nq, (int)nt, group, (int)ng, perm, nk, (int)nb, nbp, kxe, scale, out, logz)
+                       k8, ks, v, idx, rowmax, nq, (int)nt, group, (int)g0, (int)gn, perm, nk, (int)nb, nbp, kxe, scale, \
+                       out, logz)
 #define ROUTE_CASE(L)                                                                                          \
     case L:                                                                                                    \
         if (tile == 64) {                                                                                      \
@@ -2804,14 +2824,14 @@ int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, cons
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
-               int stride, int tile, int group, const int32_t* perm, float scale, float* out, float* logz,
-               int32_t* idx, float* rowmax, void* stream) {
+               int stride, int tile, int group, int64_t g0, int64_t gn, const int32_t* perm, float scale, float* out,
+               float* logz, int32_t* idx, float* rowmax, uint32_t* keys_ws, void* stream) {
     REQUIRE(q8 && sq && vb && k8 && ks && v && out && logz, "htrc_route: null pointer");
-    int rc = htrc_route_select(dq8, sdq, g8, sg, lz, heads, nq, nk, leaf, d, kx, sink, stride, tile, group, idx,
-                               rowmax, stream);
+    int rc = htrc_route_select(dq8, sdq, g8, sg, lz, heads, nq, nk, leaf, d, kx, sink, stride, tile, group, g0, gn, idx,
+                               rowmax, keys_ws, stream);
     if (rc != HTRC_OK) return rc;
     return htrc_route_attend(q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, rowmax, heads, nq, nk, leaf, d, kx,
-                             tile, group, perm, scale, out, logz, stream);
+                             tile, group, g0, gn, perm, scale, out, logz, stream);
 }
 
 int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,

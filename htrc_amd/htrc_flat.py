@@ -91,6 +91,40 @@ def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot
         raise ValueError("HIP backend: key count must be a multiple of the leaf size")
 
 
+class _Collect:
+    """Whole-layer copies of the per-window leaf state and routing for ``state=`` checks: one
+    window is referenced as is; several are copied window by window into full tensors."""
+
+    def __init__(self, state, h, ng, windows):
+        self.state, self.h, self.ng, self.single = state, h, ng, windows == 1
+        self.full = {}
+
+    def add(self, g0, gn, **parts):
+        if self.state is None:
+            return
+        for name, t in parts.items():
+            if t is None:
+                continue
+            if self.single:
+                self.full[name] = t
+                continue
+            if name not in self.full:
+                self.full[name] = torch.empty((self.h, self.ng, *t.shape[2:]), dtype=t.dtype, device=t.device)
+            self.full[name][:, g0:g0 + gn].copy_(t)
+
+    def finish(self, **extra):
+        if self.state is not None:
+            self.state.update(self.full)
+            self.state.update(extra)
+
+
+def _windows(ng: int, tile_chunk, group: int):
+    """Tile-group windows of the chunk loop (h3/htrc_flat.py:236-240): tile_chunk tiles, i.e.
+    tile_chunk // group groups, per window; tile_chunk None or < 1 means one window."""
+    step = ng if tile_chunk is None or int(tile_chunk) < 1 else max(1, int(tile_chunk) // int(group))
+    return [(g0, min(step, ng - g0)) for g0 in range(0, ng, step)]
+
+
 @torch.inference_mode()
 def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature="lin", tile_chunk=32,
                    precision="fp32", leaf=16, scale=None, prof=None, select="max", backend="torch",
@@ -98,15 +132,19 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
                    tail=None, ws=None, return_logz=False, state=None):
     """q [N,D] (or [H,N,D]), k/v [M,D] (or [H,M,D]), any float dtype -> out fp32 of q's shape
     (h3/htrc_flat.py:99-139).  ``kern['fused']`` (default True) runs select, top-k, far and
-    near field in one fused kernel per layer; False runs the reference's stage structure
+    near field as two fused launches per window; False runs the reference's stage structure
     (select, top-k, split tile kernel, merge) honouring ``splits`` and ``kern['tile_bn']``.
+    Shapes the fused kernels do not hold (more than 8192 near leaves per tile or 262144 leaves
+    per head) take the stage structure automatically.
     ``kern['group']`` = G > 1 makes G consecutive tiles share one expansion centre (the mean
     of their rows), one leaf state and one near set (h3/htrc_flat.py:223-231).
     ``order='kmeans'`` cuts the tiles from the queries regrouped by ``kmeans_order``; the
     output rows come back in query order (:148-149, 159-165).
-    ``tile_chunk`` and ``precision`` are accepted for compatibility: all tiles are processed
-    in one launch and accumulation is IEEE fp32.  ``state``, if a dict, receives the packed
-    operands, the leaf state and the routing (for checks)."""
+    ``tile_chunk`` tiles of every head are processed per window (h3/htrc_flat.py:236-273): the
+    per-(tile, leaf) state is held for one window at a time, and the result does not depend on
+    it.  ``precision`` is accepted for compatibility: accumulation is IEEE fp32.  ``state``, if
+    a dict, receives the packed operands and the whole layer's leaf state and routing (for
+    checks)."""
     kern = dict(kern or {})
     _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot, quant, tail, kern)
     squeeze = q.dim() == 2
@@ -131,95 +169,56 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         qh = qh.float()
     perm = hip.kmeans_order(qh, ws=ws) if order == "kmeans" else None   # query rows regrouped by k-means
     if store in ("fp8", "bf16"):
-        return _flat16(store, qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, stride, group, perm, splits,
-                       kern, tail, ws, return_logz, state, tile)
-    mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm)
+        mu, q16, dq16 = hip.pack_q16(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm, dq_fp16=store == "fp8")
+        packed = {"q16": q16, "dq16": dq16, "mu": mu}
+        sdt = torch.float8_e4m3fn if store == "fp8" else torch.bfloat16
+        fused = False
+    else:
+        mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm)
+        packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "mu": mu}
+        sdt = torch.int8
+        fused = bool(kern.get("fused", True)) and hip.route_fits(nb, kx)
     kb = kh.to(torch.bfloat16).contiguous()
     vb = vh.to(torch.bfloat16).contiguous()
-    k8, ks = hip.pack_k(kb, ws=ws)
+    packed["k"], packed["v"] = kb, vb
+    if sdt == torch.int8:
+        packed["k8"], packed["ks"] = hip.pack_k(kb, ws=ws)
     tick("prep")
-    g8, lz, vbs, sg, _ = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, ws=ws)
-    tick("stats")
-    packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "v": vb, "mu": mu}
-    lstate = {"g8": g8, "sg": sg, "lz": lz, "vb": vbs}
     ng = int(mu.shape[1])                               # centres: tiles, or tile groups
-    idx = None
-    if kern.get("fused", True):
-        if state is not None and kx > 0:
-            idx = hip._buf(ws, "idx", (h, ng, kx), torch.int32, qh.device)
-        out, logz = hip.route(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, sink=sink, stride=stride,
-                              ws=ws, idx=idx, group=group, perm=perm, tile=tile)
-        tick("tile")
-    else:
-        excl = None
-        if kx > 0:
-            sel = hip.rowmax_select(g=g8, lz=lz, sg=sg, stride=stride, nb=nb, dq8=dq8, sdq=sdq, ws=ws, group=group,
-                                    tile=tile)
-            idx, excl = hip.topk_excl(sel, nb, kx, sink, ws=ws)
-            if state is not None:
-                state["sel"] = sel
+    out = hip._buf(ws, "out", (h, nq, d), torch.float32, qh.device)
+    logz = hip._buf(ws, "logz", (h, nq), torch.float32, qh.device)
+    wins = _windows(ng, tile_chunk, group)
+    keep = _Collect(state, h, ng, len(wins))
+    for g0, gn in wins:
+        g, lz, vbs, sg, sv = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=sdt, ws=ws, c0=g0, cn=gn)
+        lstate = {"g8": g, "sg": sg, "lz": lz, "vb": vbs, "sv": sv}
+        tick("stats")
+        sel = excl = idx = None
+        if fused:
+            idx = hip._rows(ws, "idx", h, gn, (kx,), torch.int32, qh.device) if kx > 0 else None
+            hip.route(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, sink=sink, stride=stride, ws=ws, out=out,
+                      logz=logz, idx=idx, group=group, perm=perm, tile=tile, g0=g0)
+            tick("tile")
         else:
-            excl = hip._buf(ws, "excl", (h, ng, nb_pad(nb)), torch.int8, qh.device)
-            excl.zero_()
-        tick("select")
-        out, logz = hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
-                                       bn=int(kern.get("tile_bn", 32)), ws=ws, group=group, perm=perm, tile=tile)
-        tick("tile")
-        if state is not None:
-            state["excl"] = excl
+            if kx > 0:
+                sel = hip.rowmax_select(g=g, lz=lz, sg=sg, stride=stride, nb=nb, dq8=packed.get("dq8", packed.get("dq16")),
+                                        sdq=packed.get("sdq"), ws=ws, group=group, tile=tile, g0=g0)
+                idx, excl = hip.topk_excl(sel, nb, kx, sink, ws=ws)
+            else:
+                excl = hip._rows(ws, "excl", h, gn, (nb_pad(nb),), torch.int8, qh.device)
+                excl.zero_()
+            tick("select")
+            hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
+                               bn=int(kern.get("tile_bn", 32)), ws=ws, out=out, logz=logz, group=group, perm=perm,
+                               tile=tile, g0=g0)
+            tick("tile")
+        keep.add(g0, gn, g8=g, sg=sg, lz=lz, vb=vbs, sv=sv, sel=sel, excl=excl, idx=idx)
     if state is not None:
         state.update(packed)
-        state.update(lstate)
-        state["idx"] = idx
-        state["nb"], state["kx"], state["group"], state["perm"], state["tile"] = nb, kx, group, perm, tile
+        keep.finish(nb=nb, kx=kx, group=group, perm=perm, tile=tile, windows=wins)
+        state.setdefault("idx", None)
     if tail is not None and int(tail[0].shape[-2]) > 0:
         # keys past the last full leaf, exact for every query (h3/htrc_flat_triton.py:187-207, 381-388)
-        tk, tv = (x.unsqueeze(0) if squeeze else x for x in tail)
-        hip.tail_merge(qh, tk.to(qh.device), tv.to(qh.device), scale=scale, out=out, logz=logz)
-        tick("tail")
-    res = out[0] if squeeze else out
-    lzr = logz[0] if squeeze else logz
-    tick("finish")
-    return (res, lzr) if return_logz else res
-
-
-def _flat16(store, qh, kh, vh, squeeze, tick, nq, nb, leaf, scale, sink, kx, stride, group, perm, splits, kern, tail,
-            ws, return_logz, state, tile):
-    """store="fp8": e4m3 leaf state with row scales, fp16 far dots; store="bf16": bf16 leaf
-    state and far dots; both with bf16 near dots, run as the reference's stage structure
-    (select, top-k, split tile kernel, merge; h3/htrc_flat_triton.py:65-72, 82-83, 104-108,
-    132-153, 165-184, 214-254)."""
-    h = int(qh.shape[0])
-    fp8 = store == "fp8"
-    mu, q16, dq16 = hip.pack_q16(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm, dq_fp16=fp8)
-    kb = kh.to(torch.bfloat16).contiguous()
-    vb = vh.to(torch.bfloat16).contiguous()
-    tick("prep")
-    g, lz, vbs, sg, sv = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf,
-                                        store=torch.float8_e4m3fn if fp8 else torch.bfloat16, ws=ws)
-    tick("stats")
-    ng = int(mu.shape[1])
-    idx = None
-    if kx > 0:
-        sel = hip.rowmax_select(g=g, lz=lz, sg=sg, stride=stride, nb=nb, dq8=dq16, ws=ws, group=group, tile=tile)
-        idx, excl = hip.topk_excl(sel, nb, kx, sink, ws=ws)
-        if state is not None:
-            state["sel"] = sel
-    else:
-        excl = hip._buf(ws, "excl", (h, ng, nb_pad(nb)), torch.int8, qh.device)
-        excl.zero_()
-    tick("select")
-    packed = {"q16": q16, "dq16": dq16, "k": kb, "v": vb, "mu": mu}
-    lstate = {"g8": g, "sg": sg, "lz": lz, "vb": vbs, "sv": sv}
-    out, logz = hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
-                                   bn=int(kern.get("tile_bn", 32)), ws=ws, group=group, perm=perm, tile=tile)
-    tick("tile")
-    if state is not None:
-        state.update(packed)
-        state.update(lstate)
-        state["idx"], state["excl"] = idx, excl
-        state["nb"], state["kx"], state["group"], state["perm"], state["tile"] = nb, kx, group, perm, tile
-    if tail is not None and int(tail[0].shape[-2]) > 0:
         tk, tv = (x.unsqueeze(0) if squeeze else x for x in tail)
         hip.tail_merge(qh, tk.to(qh.device), tv.to(qh.device), scale=scale, out=out, logz=logz)
         tick("tail")

@@ -135,10 +135,27 @@ def pack_k(k: torch.Tensor, ws=None):
     return k8, ks
 
 
-def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4, store=torch.int8, ws=None):
-    """Leaf statistics at the tile centres (h3/htrc_flat_triton.py:329-345).
-    mu [H,nt,D] fp32, kf/vf bf16 [H,nk,D] -> (g, lz, vb, sg, sv) in the reference's order:
-    store=int8: g int8 [H,nt,nbp,D], vb bf16, sv None; store=float8_e4m3fn: g and vb e4m3
+def _rows(ws, name, h, n, tail, dtype, device):
+    """Workspace buffer viewed as [h, n, *tail]: reused across calls and windows by its flat
+    leading size h * n, so a smaller last window takes the same allocation."""
+    return _buf(ws, name, (h * n, *tail), dtype, device).view(h, n, *tail)
+
+
+def _window(ng: int, g0: int, gn) -> tuple[int, int]:
+    g0 = int(g0)
+    gn = ng - g0 if gn is None else int(gn)
+    if g0 < 0 or gn <= 0 or g0 + gn > ng:
+        raise ValueError(f"window [{g0}, {g0 + gn}) must lie in the {ng} centres (tile groups) of a head")
+    return g0, gn
+
+
+def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4, store=torch.int8, ws=None,
+               c0=0, cn=None):
+    """Leaf statistics at the tile centres (h3/htrc_flat_triton.py:329-345), for the centres
+    [c0, c0 + cn) of every head (all by default; the reference passes the chunk's centres).
+    mu [H,nt,D] fp32, kf/vf bf16 [H,nk,D] -> (g, lz, vb, sg, sv) in the reference's order, with
+    cn state rows per head:
+    store=int8: g int8 [H,cn,nbp,D], vb bf16, sv None; store=float8_e4m3fn: g and vb e4m3
     with the row scales sg, sv (h3/htrc_flat_triton.py:65-72); store=bfloat16: g and vb bf16,
     sg and sv None."""
     if store not in (torch.int8, torch.float8_e4m3fn, torch.bfloat16):
@@ -150,103 +167,113 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
     _need(kf, torch.bfloat16, "k")
     _need(vf, torch.bfloat16, "v")
     h, nt, d = (int(x) for x in mu.shape)
+    c0, cn = _window(nt, c0, cn)
     nk = int(kf.shape[1])
     if int(nb) * int(leaf) != nk or tuple(vf.shape) != tuple(kf.shape):
         raise ValueError("keys and values must be [H, nb * leaf, D]")
     nbp = nb_pad(nb)
     dev = mu.device
     if store == torch.bfloat16:
-        g = _buf(ws, "g_bf16", (h, nt, nbp, d), torch.bfloat16, dev)
-        vb = _buf(ws, "vb", (h, nt, nbp, d), torch.bfloat16, dev)
-        lz = _buf(ws, "lz", (h, nt, nbp), torch.float32, dev)
-        call("htrc_leaf_stats_bf16", ptr(mu), ptr(kf), ptr(vf), h, nt, nk, int(leaf), d, float(scale), ptr(g), ptr(vb),
-             ptr(lz), stream_handle(dev))
+        g = _rows(ws, "g_bf16", h, cn, (nbp, d), torch.bfloat16, dev)
+        vb = _rows(ws, "vb", h, cn, (nbp, d), torch.bfloat16, dev)
+        lz = _rows(ws, "lz", h, cn, (nbp,), torch.float32, dev)
+        call("htrc_leaf_stats_bf16", ptr(mu), ptr(kf), ptr(vf), h, nt, c0, cn, nk, int(leaf), d, float(scale), ptr(g),
+             ptr(vb), ptr(lz), stream_handle(dev))
         return g, lz, vb, None, None
     if store == torch.float8_e4m3fn:
-        g = _buf(ws, "g_fp8", (h, nt, nbp, d), torch.float8_e4m3fn, dev)
-        vb = _buf(ws, "vb_fp8", (h, nt, nbp, d), torch.float8_e4m3fn, dev)
-        sg = _buf(ws, "sg", (h, nt, nbp), torch.float32, dev)
-        sv = _buf(ws, "sv", (h, nt, nbp), torch.float32, dev)
-        lz = _buf(ws, "lz", (h, nt, nbp), torch.float32, dev)
-        call("htrc_leaf_stats_fp8", ptr(mu), ptr(kf), ptr(vf), h, nt, nk, int(leaf), d, float(scale), ptr(g), ptr(sg),
-             ptr(vb), ptr(sv), ptr(lz), stream_handle(dev))
+        g = _rows(ws, "g_fp8", h, cn, (nbp, d), torch.float8_e4m3fn, dev)
+        vb = _rows(ws, "vb_fp8", h, cn, (nbp, d), torch.float8_e4m3fn, dev)
+        sg = _rows(ws, "sg", h, cn, (nbp,), torch.float32, dev)
+        sv = _rows(ws, "sv", h, cn, (nbp,), torch.float32, dev)
+        lz = _rows(ws, "lz", h, cn, (nbp,), torch.float32, dev)
+        call("htrc_leaf_stats_fp8", ptr(mu), ptr(kf), ptr(vf), h, nt, c0, cn, nk, int(leaf), d, float(scale), ptr(g),
+             ptr(sg), ptr(vb), ptr(sv), ptr(lz), stream_handle(dev))
         return g, lz, vb, sg, sv
-    g8 = _buf(ws, "g", (h, nt, nbp, d), torch.int8, dev)
-    sg = _buf(ws, "sg", (h, nt, nbp), torch.float32, dev)
-    lz = _buf(ws, "lz", (h, nt, nbp), torch.float32, dev)
-    vb = _buf(ws, "vb", (h, nt, nbp, d), torch.bfloat16, dev)
-    call("htrc_leaf_stats", ptr(mu), ptr(kf), ptr(vf), h, nt, nk, int(leaf), d, float(scale), ptr(g8), ptr(sg),
+    g8 = _rows(ws, "g", h, cn, (nbp, d), torch.int8, dev)
+    sg = _rows(ws, "sg", h, cn, (nbp,), torch.float32, dev)
+    lz = _rows(ws, "lz", h, cn, (nbp,), torch.float32, dev)
+    vb = _rows(ws, "vb", h, cn, (nbp, d), torch.bfloat16, dev)
+    call("htrc_leaf_stats", ptr(mu), ptr(kf), ptr(vf), h, nt, c0, cn, nk, int(leaf), d, float(scale), ptr(g8), ptr(sg),
          ptr(vb), ptr(lz), stream_handle(dev))
     return g8, lz, vb, sg, None
 
 
 def rowmax_select(q_c=None, mu_c=None, g=None, lz=None, prec="ieee", bn=32, warps=4, splits=8, stride=1, dot=1,
-                  ws=None, sg=None, *, nb=None, dq8=None, sdq=None, group=1, tile=TILE):
-    """SEL [H,ng,nbp] (h3/htrc_flat_triton.py:315-326), the max over the rows of each group of
-    ``group`` tiles.  Takes the packed rows dq8/sdq (pack_q); when absent they are packed from
-    q_c (fp32 [H,nq,D] rows)."""
+                  ws=None, sg=None, *, nb=None, dq8=None, sdq=None, group=1, tile=TILE, g0=0):
+    """SEL [H,gn,nbp] (h3/htrc_flat_triton.py:315-326), the max over the rows of each group of
+    ``group`` tiles, for the gn = g.shape[1] groups from g0 (the state's window).  Takes the
+    packed rows dq8/sdq (pack_q); when absent they are packed from q_c (fp32 [H,nq,D] rows)."""
     tile = _tile(tile)
     if g.dtype in (torch.float8_e4m3fn, torch.bfloat16):
-        return _select16(g, lz, sg, stride, nb, dq8, group, ws, q_c, tile)
+        return _select16(g, lz, sg, stride, nb, dq8, group, ws, q_c, tile, g0)
     if dq8 is None or sdq is None:
         _, _, _, dq8, sdq = pack_q(q_c, tile=tile, group=group)
     g = _heads(g) if g.dim() == 3 else g
-    h, ng, nbp, d = (int(x) for x in g.shape)
+    h, gn, nbp, d = (int(x) for x in g.shape)
     nt = int(_heads(dq8).shape[1]) // tile
-    if -(-nt // int(group)) != ng:
-        raise ValueError("state rows do not match the tile groups of the packed rows")
+    g0, gn = _window(-(-nt // int(group)), g0, gn)
     nb = nbp if nb is None else int(nb)
     dev = g.device
-    sel = _buf(ws, "sel", (h, ng, nbp), torch.float32, dev)
-    call("htrc_select", ptr(dq8), ptr(sdq), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), tile, int(group), d,
-         ptr(sel), stream_handle(dev))
+    sel = _rows(ws, "sel", h, gn, (nbp,), torch.float32, dev)
+    call("htrc_select", ptr(dq8), ptr(sdq), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), tile, int(group), g0, gn,
+         d, ptr(sel), stream_handle(dev))
     return sel
 
 
-def _select16(g, lz, sg, stride, nb, dq16, group, ws, q_c, tile):
+def _select16(g, lz, sg, stride, nb, dq16, group, ws, q_c, tile, g0):
     """SEL over a 16-bit state: dq16 are the rows of pack_q16 (passed as ``dq8``): fp16 for the
     fp8 state, bf16 for the bf16 state."""
     fp8 = g.dtype == torch.float8_e4m3fn
     if dq16 is None:
         _, _, dq16 = pack_q16(q_c, tile=tile, group=group, dq_fp16=fp8)
     _need(dq16, torch.float16 if fp8 else torch.bfloat16, "dq16")
-    h, ng, nbp, d = (int(x) for x in g.shape)
+    h, gn, nbp, d = (int(x) for x in g.shape)
     nt = int(_heads(dq16).shape[1]) // tile
+    g0, gn = _window(-(-nt // int(group)), g0, gn)
     nb = nbp if nb is None else int(nb)
-    sel = _buf(ws, "sel", (h, ng, nbp), torch.float32, g.device)
+    sel = _rows(ws, "sel", h, gn, (nbp,), torch.float32, g.device)
     if fp8:
-        call("htrc_select_fp8", ptr(dq16), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), tile, int(group), d,
-             ptr(sel), stream_handle(g.device))
+        call("htrc_select_fp8", ptr(dq16), ptr(g), ptr(sg), ptr(lz), h, nt, nb, int(stride), tile, int(group), g0, gn,
+             d, ptr(sel), stream_handle(g.device))
     else:
-        call("htrc_select_bf16", ptr(dq16), ptr(g), ptr(lz), h, nt, nb, int(stride), tile, int(group), d, ptr(sel),
-             stream_handle(g.device))
+        call("htrc_select_bf16", ptr(dq16), ptr(g), ptr(lz), h, nt, nb, int(stride), tile, int(group), g0, gn, d,
+             ptr(sel), stream_handle(g.device))
     return sel
 
 
 def topk_excl(sel, nb: int, kx: int, sink: int = 0, ws=None):
-    """kx largest SEL per row (leaves < sink forced), idx ascending -> (idx [H,ng,kx] int32,
-    excl [H,ng,nbp] int8)  (h3/htrc_flat.py:262-265)."""
-    h, nt, nbp = (int(x) for x in sel.shape)
+    """kx largest SEL per row (leaves < sink forced), idx ascending -> (idx [H,gn,kx] int32,
+    excl [H,gn,nbp] int8)  (h3/htrc_flat.py:262-265)."""
+    h, gn, nbp = (int(x) for x in sel.shape)
     dev = sel.device
-    idx = _buf(ws, "idx", (h, nt, kx), torch.int32, dev)
-    excl = _buf(ws, "excl", (h, nt, nbp), torch.int8, dev)
-    call("htrc_topk", ptr(sel), h * nt, int(nb), int(kx), int(sink), ptr(idx), ptr(excl), stream_handle(dev))
+    idx = _rows(ws, "idx", h, gn, (kx,), torch.int32, dev)
+    excl = _rows(ws, "excl", h, gn, (nbp,), torch.int8, dev)
+    call("htrc_topk", ptr(sel), h * gn, int(nb), int(kx), int(sink), ptr(idx), ptr(excl), stream_handle(dev))
     return idx, excl
 
 
+def _tile_window(nq: int, tile: int, group: int, g0: int, gn):
+    """(g0, gn, first tile, tiles) of the window of tile groups [g0, g0 + gn)."""
+    nt = -(-int(nq) // tile)
+    g0, gn = _window(-(-nt // int(group)), g0, gn)
+    tb = g0 * int(group)
+    return g0, gn, tb, min(nt, (g0 + gn) * int(group)) - tb
+
+
 def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, scale: float, splits: int = 4,
-                   bn: int = 64, ws=None, out=None, logz=None, group: int = 1, perm=None, tile: int = TILE):
-    """Far + near online softmax per (tile, split) and the merge
-    (h3/htrc_flat_triton.py:348-391) -> (out [H,nq,D] fp32, logz [H,nq] fp32)."""
+                   bn: int = 64, ws=None, out=None, logz=None, group: int = 1, perm=None, tile: int = TILE, g0: int = 0):
+    """Far + near online softmax per (tile, split) and the merge (h3/htrc_flat_triton.py:348-391)
+    for the tiles of the gn = state["lz"].shape[1] groups from g0 -> (out [H,nq,D] fp32, logz
+    [H,nq] fp32), rows of other tiles left as they were."""
     tile = _tile(tile)
     if state["g8"].dtype in (torch.float8_e4m3fn, torch.bfloat16):
         return _tile16(packed, state, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits, bn=bn, ws=ws,
-                       out=out, logz=logz, group=group, perm=perm, tile=tile)
+                       out=out, logz=logz, group=group, perm=perm, tile=tile, g0=g0)
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
     g8, sg, lz, vb = state["g8"], state["sg"], state["lz"], state["vb"]
     h, nk, d = (int(x) for x in k8.shape)
-    nt = -(-nq // tile)
+    g0, gn, tb, ntw = _tile_window(nq, tile, group, g0, int(lz.shape[1]))
     kx = int(idx.shape[-1]) if idx is not None else 0
     dev = q8.device
     ns = max(1, int(splits))
@@ -256,26 +283,26 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     pm = pl = pacc = None
     if ns > 1:
-        pm = _buf(ws, "pm", (h, nt, ns, tile), torch.float32, dev)
-        pl = _buf(ws, "pl", (h, nt, ns, tile), torch.float32, dev)
-        pacc = _buf(ws, "pacc", (h, nt, ns, tile, d), torch.float32, dev)
+        pm = _rows(ws, "pm", h, ntw, (ns, tile), torch.float32, dev)
+        pl = _rows(ws, "pl", h, ntw, (ns, tile), torch.float32, dev)
+        pacc = _rows(ws, "pacc", h, ntw, (ns, tile, d), torch.float32, dev)
     call("htrc_tile", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(excl),
-         ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(v), h, nq, nk, int(leaf), d, kx, tile, int(group), ptr(perm), ns,
-         int(bn), float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
+         ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(v), h, nq, nk, int(leaf), d, kx, tile, int(group), g0, gn,
+         ptr(perm), ns, int(bn), float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
     if ns > 1:
-        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, tile, ns, d, ptr(perm), ptr(out), ptr(logz),
+        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, tile, tb, ntw, ns, d, ptr(perm), ptr(out), ptr(logz),
              stream_handle(dev))
     return out, logz
 
 
-def _tile16(packed, state, excl, idx, *, nq, leaf, scale, splits, bn, ws, out, logz, group, perm, tile):
+def _tile16(packed, state, excl, idx, *, nq, leaf, scale, splits, bn, ws, out, logz, group, perm, tile, g0):
     """Far + near softmax per (tile, split) over a 16-bit state, and the merge: packed holds q16,
     dq16 (pack_q16) and the bf16 k, v; state g8 / vb (e4m3 with sg, sv; or bf16) and lz."""
     q16, dq16, k, v = packed["q16"], packed["dq16"], packed["k"], packed["v"]
     g, sg, lz, vb, sv = state["g8"], state.get("sg"), state["lz"], state["vb"], state.get("sv")
     fp8 = g.dtype == torch.float8_e4m3fn
     h, nk, d = (int(x) for x in k.shape)
-    nt = -(-nq // tile)
+    g0, gn, tb, ntw = _tile_window(nq, tile, group, g0, int(lz.shape[1]))
     kx = int(idx.shape[-1]) if idx is not None else 0
     dev = q16.device
     ns = max(1, int(splits))
@@ -285,28 +312,45 @@ def _tile16(packed, state, excl, idx, *, nq, leaf, scale, splits, bn, ws, out, l
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     pm = pl = pacc = None
     if ns > 1:
-        pm = _buf(ws, "pm", (h, nt, ns, tile), torch.float32, dev)
-        pl = _buf(ws, "pl", (h, nt, ns, tile), torch.float32, dev)
-        pacc = _buf(ws, "pacc", (h, nt, ns, tile, d), torch.float32, dev)
+        pm = _rows(ws, "pm", h, ntw, (ns, tile), torch.float32, dev)
+        pl = _rows(ws, "pl", h, ntw, (ns, tile), torch.float32, dev)
+        pacc = _rows(ws, "pacc", h, ntw, (ns, tile, d), torch.float32, dev)
     if fp8:
         call("htrc_tile_fp8", ptr(q16), ptr(dq16), ptr(g), ptr(sg), ptr(lz), ptr(vb), ptr(sv), ptr(excl),
-             ptr(idx) if kx else None, ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, tile, int(group), ptr(perm), ns,
-             int(bn), float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
+             ptr(idx) if kx else None, ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, tile, int(group), g0, gn, ptr(perm),
+             ns, int(bn), float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
     else:
         call("htrc_tile_bf16", ptr(q16), ptr(dq16), ptr(g), ptr(lz), ptr(vb), ptr(excl), ptr(idx) if kx else None,
-             ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, tile, int(group), ptr(perm), ns, int(bn), float(scale),
-             ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
+             ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, tile, int(group), g0, gn, ptr(perm), ns, int(bn),
+             float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
     if ns > 1:
-        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, tile, ns, d, ptr(perm), ptr(out), ptr(logz),
+        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, tile, tb, ntw, ns, d, ptr(perm), ptr(out), ptr(logz),
              stream_handle(dev))
     return out, logz
 
 
+ROUTE_NB_LDS = 16384       # leaves per head whose top-k keys route_select keeps in LDS
+ROUTE_MAX_KX = 8192        # near leaves per tile the fused route kernel holds in LDS
+ROUTE_MAX_NB = 262144      # leaves per head of the fused route (exclusion bits in LDS)
+
+
+def route_fits(nb: int, kx: int) -> bool:
+    """Whether the fused route takes this shape (else the split tile path runs it)."""
+    return int(nb) <= ROUTE_MAX_NB and min(int(kx), int(nb)) <= ROUTE_MAX_KX
+
+
+def _keys_ws(ws, h, gn, nb, dev):
+    """top-k key scratch of route_select for heads of more than ROUTE_NB_LDS leaves (else None)."""
+    if int(nb) <= ROUTE_NB_LDS:
+        return None
+    return _rows(ws, "route_keys", h, gn, (nb_pad(nb),), torch.int32, dev)
+
+
 def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: float, sink: int = 0, stride: int = 1,
-          ws=None, out=None, logz=None, idx=None, group: int = 1, perm=None, tile: int = TILE):
-    """Fused select -> top-k, then far + near -> normalised output (two launches per layer call).
-    -> (out [H,nq,D], logz [H,nq]); idx [H,ng,min(kx,nb)] int32 receives the routing (a
-    workspace buffer when not given)."""
+          ws=None, out=None, logz=None, idx=None, group: int = 1, perm=None, tile: int = TILE, g0: int = 0):
+    """Fused select -> top-k, then far + near -> normalised output (two launches) for the tiles of
+    the gn = state["lz"].shape[1] groups from g0 -> (out [H,nq,D], logz [H,nq]); idx
+    [H,gn,min(kx,nb)] int32 receives the window's routing (a workspace buffer when not given)."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
     g8, sg, lz, vb = state["g8"], state["sg"], state["lz"], state["vb"]
@@ -314,55 +358,62 @@ def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: floa
     dev = q8.device
     tile = _tile(tile)
     nt = -(-int(nq) // tile)
-    ng = -(-nt // int(group))
-    kxe = min(int(kx), nk // int(leaf))
+    g0, gn, _, _ = _tile_window(nq, tile, group, g0, int(lz.shape[1]))
+    nb = nk // int(leaf)
+    kxe = min(int(kx), nb)
     if out is None:
         out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
     if logz is None:
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     if idx is None and kxe > 0:
-        idx = _buf(ws, "idx", (h, ng, kxe), torch.int32, dev)
+        idx = _rows(ws, "idx", h, gn, (kxe,), torch.int32, dev)
     rowmax = _buf(ws, "rowmax", (h, nt * tile), torch.float32, dev)
+    keys = _keys_ws(ws, h, gn, nb, dev)
     call("htrc_route", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8), ptr(ks),
-         ptr(v), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), tile, int(group), ptr(perm), float(scale),
-         ptr(out), ptr(logz), ptr(idx), ptr(rowmax), stream_handle(dev))
+         ptr(v), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), tile, int(group), g0, gn, ptr(perm),
+         float(scale), ptr(out), ptr(logz), ptr(idx), ptr(rowmax), ptr(keys), stream_handle(dev))
     return out, logz
 
 
 def route_select(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, sink: int = 0, stride: int = 1,
-                 ws=None, idx=None, group: int = 1, tile: int = TILE):
-    """First launch of route: select -> top-k per tile group -> (idx [H,ng,min(kx,nb)] int32 or
-    None, rowmax [H,nt*tile] fp32, each row's largest far-field score)."""
+                 ws=None, idx=None, group: int = 1, tile: int = TILE, g0: int = 0):
+    """First launch of route: select -> top-k per tile group of the window -> (idx
+    [H,gn,min(kx,nb)] int32 or None, rowmax [H,nt*tile] fp32, each row's largest far-field
+    score)."""
     dq8, sdq = packed["dq8"], packed["sdq"]
     g8, sg, lz = state["g8"], state["sg"], state["lz"]
     h, nk = int(packed["k8"].shape[0]), int(packed["k8"].shape[1])
     dev = dq8.device
     tile = _tile(tile)
     nt = -(-int(nq) // tile)
-    ng = -(-nt // int(group))
-    kxe = min(int(kx), nk // int(leaf))
+    g0, gn, _, _ = _tile_window(nq, tile, group, g0, int(lz.shape[1]))
+    nb = nk // int(leaf)
+    kxe = min(int(kx), nb)
     if idx is None and kxe > 0:
-        idx = _buf(ws, "idx", (h, ng, kxe), torch.int32, dev)
+        idx = _rows(ws, "idx", h, gn, (kxe,), torch.int32, dev)
     rowmax = _buf(ws, "rowmax", (h, nt * tile), torch.float32, dev)
+    keys = _keys_ws(ws, h, gn, nb, dev)
     call("htrc_route_select", ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), h, nq, nk, int(leaf), D, int(kx),
-         int(sink), int(stride), tile, int(group), ptr(idx), ptr(rowmax), stream_handle(dev))
+         int(sink), int(stride), tile, int(group), g0, gn, ptr(idx), ptr(rowmax), ptr(keys), stream_handle(dev))
     return idx, rowmax
 
 
 def route_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, kx: int, scale: float, ws=None,
-                 out=None, logz=None, group: int = 1, perm=None, tile: int = TILE):
+                 out=None, logz=None, group: int = 1, perm=None, tile: int = TILE, g0: int = 0):
     """Second launch of route: far + near field with the row reference rowmax -> (out, logz)."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
     g8, sg, lz, vb = state["g8"], state["sg"], state["lz"], state["vb"]
     h, nk, d = (int(x) for x in k8.shape)
     dev = q8.device
+    tile = _tile(tile)
+    g0, gn, _, _ = _tile_window(nq, tile, group, g0, int(lz.shape[1]))
     if out is None:
         out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
     if logz is None:
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     call("htrc_route_attend", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8),
-         ptr(ks), ptr(v), ptr(idx), ptr(rowmax), h, nq, nk, int(leaf), d, int(kx), _tile(tile), int(group),
+         ptr(ks), ptr(v), ptr(idx), ptr(rowmax), h, nq, nk, int(leaf), d, int(kx), tile, int(group), g0, gn,
          ptr(perm), float(scale), ptr(out), ptr(logz), stream_handle(dev))
     return out, logz
 

@@ -1,21 +1,27 @@
 """Production runner of the flat-HTRC operator -- the drop-in for h3/htrc_flat_runner.py.
 
-Same call shape as the reference:
+Call shape of the reference runner (h3/htrc_flat_runner.py:85-203):
 
     runner = FlatRunner(queries, keys, free_bytes=free_vram, mode="fast")
     outputs = runner.run([(head, q, k, v), ...])        # q [Q,128], k/v [K,128] on the HIP device
     runner.run(jobs, sink=lambda i, out: block_out[i].copy_(out))   # nothing retained
 
-The operator never synchronises the host, so one HIP graph (torch.cuda.CUDAGraph on ROCm)
-is captured once over static q/k/v/out buffers and replayed per call; a capture failure
-falls back to eager launches and is recorded in ``graph_error``.
+Design on MI355X:
 
-MI355X extension: ``heads=H`` captures H heads per replay (static buffers [H, Q, 128]);
-``run`` then packs consecutive jobs H at a time, so one replay covers a whole layer and
-fills the 256 CUs, instead of one head per replay as on the reference's GPU.
+* ``_Plan`` resolves the quality mode and the caller's knobs into the operator's keyword
+  arguments and sizes the tile window (``tile_chunk``) against ``free_bytes`` with an exact
+  byte count of this implementation's workspace (``workspace_bytes``).
+* ``_Replay`` owns the static input buffers, a workspace filled by one eager warm-up call, and a
+  HIP graph (torch.cuda.CUDAGraph) recorded over one operator call on those buffers.  The
+  operator never synchronises the host and, with its workspace already allocated, allocates
+  nothing, so the recorded call is the whole layer: every tile window's statistics, routing
+  and attention launches.  A failed recording leaves the runner eager and keeps the reason in
+  ``graph_error``.
+* ``heads=H`` (an extension) records H heads per replay (static buffers [H, Q, 128]) and
+  ``run`` packs consecutive jobs H at a time, so one replay covers a whole layer on the 256
+  CUs instead of one head per replay.
 
-Memory model: ``predicted_peak_mib`` counts this implementation's workspace exactly
-(packed operands, per-(tile, leaf) state, outputs, static graph copies).
+The memory model below imports without torch.
 """
 from __future__ import annotations
 
@@ -24,218 +30,252 @@ try:                                   # the memory model below must stay import
 except ImportError:                    # pragma: no cover
     torch = None
 
+# Quality modes and tile-window sizes of the reference runner (h3/htrc_flat_runner.py:48-53, 54):
+# interface data, all four modes implemented ("max" runs 32-row tiles).
 MODES = {
     "fast": dict(exact_leaves=256, order="seq", tile=64),
     "balanced": dict(exact_leaves=512, order="seq", tile=64),
     "accurate": dict(exact_leaves=1024, order="kmeans", tile=64),
     "max": dict(exact_leaves=1024, order="kmeans", tile=32),
 }
-# The reference's quality modes (h3/htrc_flat_runner.py:48-53), all implemented ("max" runs
-# 32-row tiles).
-SUPPORTED_MODES = ("fast", "balanced", "accurate", "max")
+SUPPORTED_MODES = tuple(MODES)
 CHUNKS = (1024, 512, 256, 128, 64, 32, 16)
 TILE = 64
+MIB = 2 ** 20
+
+# The static graph copies and the k-means scratch of this implementation at the live H3 shape of
+# the reference (one head, 40759 queries and keys, h3/htrc_flat_runner.py:55-56 names the same two
+# figures for its own implementation); predicted_peak_mib counts both exactly for any shape.
+_H3_ROWS = 40759
+STATIC_MIB = (4 * _H3_ROWS * 128 + 2 * 2 * _H3_ROWS * 128) / MIB
+KMEANS_MIB = (8 * _H3_ROWS + 4 * 32 * 128) / MIB
 
 
-def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, heads: int = 1,
-                    splits: int = 1, kx: int = 0, group: int = 1, order: str = "seq", tile: int = TILE) -> int:
-    """Device bytes the operator's workspace holds for one call (all tiles at once); the leaf
-    state and the routing hold one row per centre (ng = ceil(nt / group), nt tiles of ``tile``
-    rows); order="kmeans" adds the permutation, the assignments and 32 centres."""
-    tile = int(tile)
-    nt = -(-int(queries) // tile)
-    ng = -(-nt // max(1, int(group)))
-    rows = nt * tile
+def _ceil(a: int, b: int) -> int:
+    return -(-int(a) // int(b))
+
+
+def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, heads: int = 1, splits: int = 1,
+                    kx: int = 0, group: int = 1, order: str = "seq", tile: int = TILE, tile_chunk: int | None = None,
+                    store: str = "int8", fused: bool = True, bf16_inputs: bool = True) -> int:
+    """Device bytes of one operator call's workspace: the whole layer's packed operands and
+    outputs, and the per-(centre, leaf) state, routing and partials of one tile window of
+    ``tile_chunk`` tiles (all tiles when None)."""
+    nt = _ceil(queries, tile)
+    ng = _ceil(nt, max(1, int(group)))
+    gw = ng if tile_chunk is None else max(1, min(ng, int(tile_chunk) // max(1, int(group))))
+    tw = min(nt, gw * max(1, int(group)))            # tiles of a window
+    rows = nt * int(tile)
     nb = int(keys) // int(leaf)
-    nbp = (nb + 31) // 32 * 32
-    per_head = (
-        4 * ng * dim                       # mu
-        + 2 * rows * dim + 8 * rows        # q8, dq8, sq, sdq
-        + keys * dim + 4 * keys            # k8, ks
-        + 2 * keys * dim * 2               # bf16 copies of k and v when the inputs are not bf16
-        + ng * nbp * (3 * dim + 8)         # g8, vb, sg, lz
-        + 4 * queries * (dim + 1)          # out, logz
-        + 4 * rows                         # rowmax
-        + 4 * ng * kx                      # idx (when recorded)
-    )
-    if splits > 1:
-        per_head += nt * splits * tile * (2 + dim) * 4 + ng * nbp * 5 + 4 * ng * kx   # partials, excl, sel
+    nbp = _ceil(nb, 32) * 32
+    kx = min(int(kx), nb)
+    layer = 4 * ng * dim + 4 * queries * (dim + 1) + 4 * rows          # mu, out + logz, rowmax
+    if store == "int8":
+        layer += 2 * rows * dim + 8 * rows + keys * dim + 4 * keys      # q8, dq8, sq, sdq, k8, ks
+        per_state = 3 * dim + 8                                         # g8, vb bf16, sg, lz
+    else:
+        layer += 2 * 2 * rows * dim                                     # q16, dq16
+        per_state = 2 * dim + 12 if store == "fp8" else 4 * dim + 4     # fp8: g, vb, sg, sv, lz; bf16: g, vb, lz
+    if not bf16_inputs:
+        layer += 2 * 2 * keys * dim                                     # bf16 copies of k and v
+    window = gw * nbp * per_state + 4 * gw * kx                         # state, idx
+    if fused and nb > 16384:
+        window += 4 * gw * nbp                                          # route_select top-k keys
+    if not fused:
+        window += gw * nbp * 5                                          # sel, excl
+        if splits > 1:
+            window += tw * int(splits) * int(tile) * (dim + 2) * 4      # split partials
     if order == "kmeans":
-        per_head += 8 * int(queries) + 4 * 32 * dim                                   # perm, assign, centres
-    return int(heads) * per_head
+        layer += 8 * queries + 4 * 32 * dim                             # perm, assignments, centres
+    return int(heads) * (layer + window)
 
 
-def predicted_peak_mib(keys: int, tile: int, tile_chunk: int, splits: int = 8, leaf: int = 16,
-                       dim: int = 128, order: str = "seq", graph: bool = True, queries: int = 0,
-                       heads: int = 1, group: int = 1) -> float:
-    """Peak device MiB above the caller's q/k/v (signature of h3/htrc_flat_runner.py:61-68).
-    This implementation processes every tile in one launch, so ``tile_chunk`` does not
-    bound the workspace; ``queries`` (default: as many as keys) sizes it.  Graph mode adds
-    the static fp32 q and bf16 k/v copies."""
+def predicted_peak_mib(keys: int, tile: int, tile_chunk: int, splits: int = 8, leaf: int = 16, dim: int = 128,
+                       order: str = "seq", graph: bool = True, queries: int = 0, heads: int = 1, group: int = 1,
+                       exact_leaves: int = 256, store: str = "int8", fused: bool = True) -> float:
+    """Peak device MiB above the caller's q/k/v (the signature of h3/htrc_flat_runner.py:61-68,
+    extended): the operator's workspace with a window of ``tile_chunk`` tiles, plus the static
+    fp32 q and bf16 k/v copies in graph mode.  ``queries`` defaults to ``keys``."""
     q = int(queries) if queries else int(keys)
-    b = workspace_bytes(q, keys, leaf, dim, heads, splits=1, group=group, order=order, tile=tile)
+    b = workspace_bytes(q, keys, leaf, dim, heads, splits=splits, kx=exact_leaves, group=group, order=order,
+                        tile=tile, tile_chunk=tile_chunk, store=store, fused=fused)
     if graph:
         b += int(heads) * (4 * q * dim + 2 * 2 * int(keys) * dim)
-    return b / 2 ** 20
+    return b / MIB
 
 
-def plan_chunk(free_bytes: int, keys: int, tile: int, splits: int = 8, order: str = "seq",
-               graph: bool = True, queries: int = 0, leaf: int = 16, heads: int = 1, group: int = 1) -> int:
-    """Tile chunk for the call (h3/htrc_flat_runner.py:71-82): the largest of CHUNKS when the
-    whole workspace fits in ``free_bytes``; MemoryError otherwise."""
-    need = predicted_peak_mib(keys, tile, CHUNKS[0], splits, leaf=leaf, order=order, graph=graph,
-                              queries=queries, heads=heads, group=group)
-    if need * 2 ** 20 <= free_bytes:
-        return CHUNKS[0]
-    raise MemoryError(f"flat HTRC needs ~{need:.0f} MiB, {int(free_bytes) >> 20} MiB free")
+def plan_chunk(free_bytes: int, keys: int, tile: int, splits: int = 8, order: str = "seq", graph: bool = True,
+               queries: int = 0, leaf: int = 16, heads: int = 1, group: int = 1, exact_leaves: int = 256,
+               store: str = "int8", fused: bool = True) -> int:
+    """The largest of CHUNKS whose predicted peak fits in ``free_bytes`` (fewer windows, fewer
+    launches; h3/htrc_flat_runner.py:71-82); MemoryError when not even the smallest fits."""
+    need = None
+    for c in CHUNKS:
+        need = predicted_peak_mib(keys, tile, c, splits, leaf=leaf, order=order, graph=graph, queries=queries,
+                                  heads=heads, group=group, exact_leaves=exact_leaves, store=store, fused=fused)
+        if need * MIB <= int(free_bytes):
+            return c
+    raise MemoryError(f"flat HTRC needs ~{need:.0f} MiB at the smallest window ({CHUNKS[-1]} tiles), "
+                      f"{int(free_bytes) >> 20} MiB free")
+
+
+class _Plan:
+    """Operator keyword arguments of a runner: PROD, then the mode, then the caller's knobs
+    (``kern`` merged key by key), then the tile window."""
+
+    def __init__(self, flat, mode, overrides, sink_leaves, queries, keys, heads, free_bytes, tile_chunk, graph):
+        if mode not in MODES:
+            raise ValueError(f"mode must be one of {list(MODES)}")
+        over = dict(overrides)
+        kern = {**flat.PROD.get("kern", {}), **over.pop("kern", {})}
+        cfg = {**flat.PROD, **MODES[mode], **over, "kern": kern, "sink_leaves": int(sink_leaves)}
+        nb = int(keys) // int(cfg.get("leaf", 16))
+        kx = min(int(cfg["exact_leaves"]) + int(sink_leaves), nb)
+        sizing = dict(leaf=int(cfg.get("leaf", 16)), order=cfg["order"], graph=graph, queries=int(queries),
+                      heads=int(heads), group=max(1, int(kern.get("group", 1))), exact_leaves=kx,
+                      store=cfg.get("store", "int8"), fused=bool(kern.get("fused", True)))
+        if tile_chunk is None:
+            tile_chunk = cfg["tile_chunk"] if free_bytes is None else plan_chunk(
+                free_bytes, keys, cfg["tile"], cfg.get("splits", 8), **sizing)
+        cfg["tile_chunk"] = int(tile_chunk)
+        self.cfg = cfg
+        self.mib = predicted_peak_mib(keys, cfg["tile"], cfg["tile_chunk"], cfg.get("splits", 8), **sizing)
+
+
+class _Replay:
+    """Static buffers, a workspace filled by one eager warm-up call, and the HIP graph recorded
+    over one operator call on them."""
+
+    def __init__(self, runner):
+        self.runner = runner
+        dev, shape = runner.device, runner._shape
+        gen = torch.Generator(device=dev).manual_seed(0)
+        # finite, well-spread warm-up data: the k-means order and the softmax see real numbers
+        self.q = torch.randn(shape(runner.queries), generator=gen, device=dev, dtype=torch.float32)
+        self.k = torch.randn(shape(runner.keys), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        self.v = torch.randn(shape(runner.keys), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        self.tail = None
+        if runner.tail_rows:
+            self.tail = tuple(torch.randn(shape(runner.tail_rows), generator=gen, device=dev, dtype=torch.float32)
+                              for _ in range(2))
+        self.ws = {}
+        self.out = None
+        self.graph = None
+
+    def record(self):
+        """Warm up on a side stream (the workspace is allocated there, outside the recording),
+        then record one call; the graph then replays on the static buffers."""
+        side = torch.cuda.Stream(device=self.runner.device)
+        side.wait_stream(torch.cuda.current_stream(self.runner.device))
+        with torch.cuda.stream(side):
+            self.runner._op(self.q, self.k, self.v, self.tail, self.ws)
+        side.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, capture_error_mode="thread_local"):
+            self.out = self.runner._op(self.q, self.k, self.v, self.tail, self.ws)
+        torch.cuda.synchronize(self.runner.device)
+        self.graph = graph
+
+    def replay(self, q, k, v, tail):
+        """Copy this call's operands into the static buffers and replay; returns the static output."""
+        if self.tail is not None:
+            if tail is None:
+                raise ValueError(f"this runner was recorded with tail_rows={self.runner.tail_rows}: pass tail=(tk, tv)")
+            self.tail[0].copy_(tail[0])
+            self.tail[1].copy_(tail[1])
+        self.q.copy_(q)
+        self.k.copy_(k)
+        self.v.copy_(v)
+        self.graph.replay()
+        return self.out
 
 
 class FlatRunner:
-    def __init__(self, queries: int, keys: int, *, free_bytes: int | None = None,
-                 mode: str = "balanced", tile_chunk: int | None = None, use_graph: bool = True,
-                 device="cuda", dim: int = 128, sink_leaves: int = 0, tail_rows: int = 0, heads: int = 1,
-                 **overrides):
-        if mode not in MODES:
-            raise ValueError(f"mode must be one of {list(MODES)}")
+    """Flat-HTRC head runner with the reference's call surface (h3/htrc_flat_runner.py:85-203):
+    ``head``, ``run``, ``close`` and the attributes ``cfg``, ``predicted_mib``, ``graph``,
+    ``graph_error`` and ``ws``."""
+
+    def __init__(self, queries: int, keys: int, *, free_bytes: int | None = None, mode: str = "balanced",
+                 tile_chunk: int | None = None, use_graph: bool = True, device="cuda", dim: int = 128,
+                 sink_leaves: int = 0, tail_rows: int = 0, heads: int = 1, **overrides):
         from . import htrc_flat
         self.flat = htrc_flat
         self.mode = mode
-        self.device = torch.device(device)
-        base = dict(htrc_flat.PROD)
-        base.update(MODES[mode])
-        overrides = dict(overrides)
-        if "kern" in overrides:                         # merge, do not replace, the kernel knobs
-            base["kern"] = {**base.get("kern", {}), **overrides.pop("kern")}
-        base.update(overrides)
-        base["sink_leaves"] = int(sink_leaves)
         self.heads = max(1, int(heads))
-        leaf = int(base.get("leaf", 16))
-        group = max(1, int(base.get("kern", {}).get("group", 1)))
-        if tile_chunk is None:
-            if free_bytes is not None:
-                tile_chunk = plan_chunk(free_bytes, keys, base["tile"], base.get("splits", 8), base["order"],
-                                        use_graph, queries=int(queries), leaf=leaf, heads=self.heads, group=group)
-            else:
-                tile_chunk = base["tile_chunk"]
-        base["tile_chunk"] = int(tile_chunk)
-        self.cfg = base
-        self.predicted_mib = predicted_peak_mib(keys, base["tile"], base["tile_chunk"], base.get("splits", 8),
-                                                leaf=leaf, order=base["order"], graph=use_graph,
-                                                queries=int(queries), heads=self.heads, group=group)
+        plan = _Plan(htrc_flat, mode, overrides, sink_leaves, queries, keys, self.heads, free_bytes, tile_chunk,
+                     bool(use_graph))
+        self.cfg = plan.cfg
+        self.predicted_mib = plan.mib
         self.queries, self.keys, self.dim = int(queries), int(keys), int(dim)
-        self.tail_rows = int(tail_rows)                  # keys past the last full leaf, exact
-        self._tk = self._tv = None
-        self.ws = {}                                     # reusable workspace (eager path)
-        self.graph = None
-        self._capturing = False
+        self.tail_rows = int(tail_rows)
+        self.device = torch.device(device)
+        self.ws = {}                     # workspace of eager calls (a graph keeps its own)
         self.graph_error = None
-        self._sq = self._sk = self._sv = self._so = None
+        self._replay = None
         if use_graph:
-            self._capture()
+            rep = _Replay(self)
+            try:
+                rep.record()
+                self._replay = rep
+            except Exception as exc:  # noqa: BLE001 -- any recording failure: run eagerly, keep the reason
+                self.graph_error = f"{type(exc).__name__}: {exc}"[:300]
+                del rep
+                torch.cuda.empty_cache()
+
+    @property
+    def graph(self):
+        return None if self._replay is None else self._replay.graph
 
     def _shape(self, n):
         return (self.heads, n, self.dim) if self.heads > 1 else (n, self.dim)
 
-    def _call(self, q, k, v, tail=None):
-        if tail is None and self._tk is not None:
-            tail = (self._tk, self._tv)
-        ws = self.ws if self.graph is None and not self._capturing else None
+    def _op(self, q, k, v, tail, ws):
         return self.flat.flat_attention(q, k, v, tail=tail, ws=ws, **self.cfg)
 
-    def _capture(self):
-        dev = self.device
-        with torch.cuda.device(dev):
-            self._sq = torch.zeros(self._shape(self.queries), device=dev, dtype=torch.float32)
-            self._sk = torch.zeros(self._shape(self.keys), device=dev, dtype=torch.bfloat16)
-            self._sv = torch.zeros_like(self._sk)
-            self._sq.normal_()
-            self._sk.normal_()
-            self._sv.normal_()
-            if self.tail_rows:
-                self._tk = torch.randn(self._shape(self.tail_rows), device=dev, dtype=torch.float32)
-                self._tv = torch.randn_like(self._tk)
-            self._capturing = True
-            try:
-                side = torch.cuda.Stream()
-                side.wait_stream(torch.cuda.current_stream())
-                with torch.cuda.stream(side), torch.inference_mode():
-                    for _ in range(2):
-                        self._call(self._sq, self._sk, self._sv)
-                torch.cuda.current_stream().wait_stream(side)
-                torch.cuda.synchronize()
-                g = torch.cuda.CUDAGraph()
-                with torch.inference_mode(), torch.cuda.graph(g, capture_error_mode="thread_local"):
-                    self._so = self._call(self._sq, self._sk, self._sv)
-                torch.cuda.synchronize()
-                self.graph = g
-                self._capturing = False
-            except Exception as exc:  # noqa: BLE001  (fall back to eager launching)
-                self.graph = None
-                self._capturing = False
-                self.graph_error = f"{type(exc).__name__}: {exc}"[:300]
-                self._sq = self._sk = self._sv = self._so = None
-                self._tk = self._tv = None
-                torch.cuda.empty_cache()
-
-    def _set_tail(self, tail):
-        """Copy this call's tail into the captured static buffers (h3/htrc_flat_runner.py:162-165)."""
-        if self.tail_rows and self.graph is not None:
-            if tail is None:
-                raise ValueError(f"this runner was captured with tail_rows={self.tail_rows}: pass tail=(tk, tv)")
-            self._tk.copy_(tail[0])
-            self._tv.copy_(tail[1])
+    def _eager(self, q, k, v, tail):
+        if self.tail_rows and tail is None:
+            raise ValueError(f"this runner takes tail_rows={self.tail_rows}: pass tail=(tk, tv)")
+        return self._op(q, k, v, tail, self.ws)
 
     def head(self, q, k, v, tail=None):
-        """One call (one head, or ``heads`` stacked heads); returns a fresh fp32 tensor.
+        """One call (one head, or ``heads`` stacked heads) -> a fresh fp32 tensor of q's shape.
         tail=(tk, tv) [tail_rows, D] (or [heads, tail_rows, D])."""
-        if self.graph is None:      # the eager result is a view of the reused workspace: copy it
-            with torch.inference_mode():
-                return self._call(q, k, v, tail=tail).clone()
-        self._set_tail(tail)
-        self._sq.copy_(q)
-        self._sk.copy_(k)
-        self._sv.copy_(v)
-        self.graph.replay()
-        return self._so.clone()
+        if self._replay is None:
+            return self._eager(q, k, v, tail).clone()      # the eager result lives in the workspace
+        return self._replay.replay(q, k, v, tail).clone()
 
     def _batches(self, jobs):
-        if self.heads == 1:
-            for i, job in enumerate(jobs):
-                yield [i], job[1], job[2], job[3], (job[4] if len(job) > 4 else None)
-            return
-        for s in range(0, len(jobs), self.heads):
-            grp = list(range(s, min(len(jobs), s + self.heads)))
-            if len(grp) < self.heads:          # pad the last batch by repeating its first job
-                grp_src = grp + [grp[0]] * (self.heads - len(grp))
-            else:
-                grp_src = grp
-            q = torch.stack([jobs[i][1] for i in grp_src])
-            k = torch.stack([jobs[i][2] for i in grp_src])
-            v = torch.stack([jobs[i][3] for i in grp_src])
-            tails = [jobs[i][4] if len(jobs[i]) > 4 else None for i in grp_src]
-            if all(t is None for t in tails):
-                yield grp, q, k, v, None
-            elif any(t is None for t in tails):
+        """(job indices, q, k, v, tail) per call: one job, or ``heads`` jobs stacked (the last
+        batch padded with repeats of its first job, whose outputs are dropped)."""
+        step = self.heads
+        for s in range(0, len(jobs), step):
+            ids = list(range(s, min(len(jobs), s + step)))
+            if step == 1:
+                j = jobs[ids[0]]
+                yield ids, j[1], j[2], j[3], (j[4] if len(j) > 4 else None)
+                continue
+            src = ids + [ids[0]] * (step - len(ids))
+            q, k, v = (torch.stack([jobs[i][n] for i in src]) for n in (1, 2, 3))
+            tails = [jobs[i][4] if len(jobs[i]) > 4 else None for i in src]
+            if any(t is None for t in tails) and not all(t is None for t in tails):
                 raise ValueError("a batch of heads needs a tail for every head or for none")
-            else:
-                yield grp, q, k, v, (torch.stack([t[0] for t in tails]), torch.stack([t[1] for t in tails]))
+            tail = None if tails[0] is None else tuple(torch.stack([t[n] for t in tails]) for n in (0, 1))
+            yield ids, q, k, v, tail
 
     def run(self, jobs, sink=None):
-        """jobs: list of (head_index, q, k, v[, (tail_k, tail_v)]).  Outputs in job order, or
-        via sink(i, output) (graph mode hands over the static output without a copy)."""
+        """jobs: list of (head_index, q, k, v[, (tail_k, tail_v)]).  Returns the outputs in job
+        order (fresh tensors), or hands each to sink(i, output): there the output is the
+        graph's static buffer (or the eager workspace), valid until the next call."""
         results = [None] * len(jobs)
-        for grp, q, k, v, tail in self._batches(jobs):
-            if self.graph is None or sink is None:
+        for ids, q, k, v, tail in self._batches(jobs):
+            if sink is None:
                 out = self.head(q, k, v, tail=tail)
-                outs = [out] if self.heads == 1 else [out[j] for j in range(len(grp))]
+            elif self._replay is not None:
+                out = self._replay.replay(q, k, v, tail)
             else:
-                self._set_tail(tail)
-                self._sq.copy_(q)
-                self._sk.copy_(k)
-                self._sv.copy_(v)
-                self.graph.replay()
-                outs = [self._so] if self.heads == 1 else [self._so[j] for j in range(len(grp))]
-            for i, o in zip(grp, outs):
+                out = self._eager(q, k, v, tail)
+            for j, i in enumerate(ids):
+                o = out if self.heads == 1 else out[j]
                 if sink is None:
                     results[i] = o
                 else:
@@ -243,5 +283,6 @@ class FlatRunner:
         return results if sink is None else None
 
     def close(self):
-        self.graph = None
-        self._sq = self._sk = self._sv = self._so = None
+        """Drop the graph, its static buffers and the eager workspace."""
+        self._replay = None
+        self.ws = {}

@@ -73,6 +73,29 @@ def video_regions(t: int = 16, y: int = 48, x: int = 84, d: int = 128, heads: in
     return torch.stack(qs), torch.stack(ks), torch.stack(vs)
 
 
+def h3_live(n: int = 40759, keys: int = 40752, tail: int = 7, d: int = 128, heads: int = 1, rank: int = 24,
+            seed: int = 0, device="cpu"):
+    """The reference runner's live H3 shape (tools/sweep_h3_flat_kernels.py:6-8: 40759 queries,
+    37232 keys plus 3520 sink rows = 40752 leaf keys, 7 tail keys): q and k are low-rank mixtures
+    of ``rank`` shared directions (coefficients N(0, 0.45^2)) plus N(0, 0.6^2) noise, v ~ N(0, 1)
+    -> q, k, v bf16 [heads, n | keys, d] and the tail keys / values fp32 [heads, tail, d]."""
+    g = torch.Generator(device=device).manual_seed(int(seed))
+    out = [[], [], [], [], []]
+    for _ in range(heads):
+        basis = torch.randn((rank, d), generator=g, device=device)
+
+        def mix(rows):
+            c = torch.randn((rows, rank), generator=g, device=device) * 0.45
+            return c @ basis + 0.6 * torch.randn((rows, d), generator=g, device=device)
+
+        q = _bf16(mix(n))
+        k = _bf16(mix(keys + tail))
+        v = _bf16(torch.randn((keys + tail, d), generator=g, device=device))
+        for lst, x in zip(out, (q, k[:keys], v[:keys], k[keys:].float(), v[keys:].float())):
+            lst.append(x)
+    return tuple(torch.stack(x) for x in out)
+
+
 def make(name: str, *, seed: int = 0, heads: int | None = None, device="cpu"):
     """(q, k, v, leaf, exact_leaves) for a named configuration."""
     gen, kw, leaf, ex, h = CONFIGS[name]

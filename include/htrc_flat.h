@@ -30,6 +30,18 @@
  * perm (optional, int32 [H, nq]; NULL = identity): the operator works on the queries in the
  * order perm (row p is query perm[p], order="kmeans"); pack_q gathers through it and the
  * entry points that write out / logz scatter back, so out / logz stay in query order.
+ *
+ * Windows (the reference's tile_chunk loop, h3/htrc_flat.py:236-273): the entry points after
+ * pack_q / pack_k work on the centres (tile groups) [g0, g0 + gn) of every head, so a caller
+ * bounds the per-(centre, leaf) state by looping over windows.  The packed operands, rowmax,
+ * out and logz are indexed by the whole layer; the state (g8, sg, lz, vb, sv), sel, excl, idx and
+ * the split partials are the window's own: their row dimension is gn (the window's tiles for
+ * the partials).  g0 = 0, gn = ng is the whole layer in one window.
+ *
+ * Limits: leaf 16, 32, 64 or 128; d = 128; heads <= 65535.  The fused route (htrc_route_*)
+ * takes at most 8192 near leaves per tile and 262144 leaves per head, and keeps the top-k keys
+ * of up to 16384 leaves per head in LDS (above that it needs keys_ws); the split tile path
+ * (htrc_select / htrc_topk / htrc_tile / htrc_merge) takes any near-leaf count.
  * The reference implements the same path as Triton kernels driven from Python;
  * each entry point below names the reference interface it replaces.
  */
@@ -42,7 +54,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 11
+#define HTRC_ABI_VERSION 12
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -67,44 +79,53 @@ int htrc_pack_q(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, 
  * Replaces the host-side K pack of _flat_triton (h3/htrc_flat.py:213-219). */
 int htrc_pack_k(const uint16_t* k, int64_t heads, int64_t nk, int d, int8_t* k8, float* ks, void* stream);
 
-/* Leaf statistics at the centres with the int8 store of g; nt = the number of centres
- * (ng when tiles are grouped).
+/* Leaf statistics at the centres [c0, c0 + cn) of every head with the int8 store of g; mu holds
+ * nt centres per head (ng when tiles are grouped); the state rows are the window's ([H, cn, ...]).
+ * g8 codes = trunc(g * (127 / max|g|) +- 0.5) (half away from zero).
  * Replaces leaf_stats / _stats_kernel (h3/htrc_flat_triton.py:329-345, 41-85). */
-int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
-                    int leaf, int d, float scale, int8_t* g8, float* sg, uint16_t* vb, float* lz, void* stream);
+int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
+                    int64_t cn, int64_t nk, int leaf, int d, float scale, int8_t* g8, float* sg, uint16_t* vb, float* lz,
+                    void* stream);
 
-/* Row-max routing score SEL[g, l] over every `stride`-th row of the group's tiles; nt = tiles.
+/* Row-max routing score SEL[g, l] over every `stride`-th row of the group's tiles, for the groups
+ * [g0, g0 + gn) of every head; nt = tiles per head.
  * Replaces rowmax_select / _rowmax_kernel (h3/htrc_flat_triton.py:315-326, 214-254). */
 int htrc_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
-                int64_t heads, int64_t nt, int64_t nb, int stride, int tile, int group, int d, float* sel,
-                void* stream);
+                int64_t heads, int64_t nt, int64_t nb, int stride, int tile, int group, int64_t g0, int64_t gn, int d,
+                float* sel, void* stream);
 
-/* kx largest SEL per row (leaves < sink forced in), idx ascending, exclusion mask.
- * Replaces torch.topk + excl.scatter_ (h3/htrc_flat.py:262-265). `rows` = H * ng. */
+/* kx largest SEL per row (leaves < sink forced in), idx ascending, exclusion mask; any leaf count
+ * (rows of more than 8192 leaves are read from global memory in each radix pass).
+ * Replaces torch.topk + excl.scatter_ (h3/htrc_flat.py:262-265). `rows` = H * gn. */
 int htrc_topk(const float* sel, int64_t rows, int64_t nb, int kx, int sink, int32_t* idx, int8_t* excl,
               void* stream);
 
-/* Far + near online softmax of every (tile, split).  splits == 1 writes out/logz directly;
- * splits > 1 writes the partials pm/pl/pacc for htrc_merge.
+/* Far + near online softmax of every (tile, split) of the tiles of groups [g0, g0 + gn).
+ * splits == 1 writes out/logz directly; splits > 1 writes the window's partials pm/pl/pacc
+ * ([H, tiles of the window, splits, T]) for htrc_merge.
  * Replaces tile_attention / _tile_kernel (h3/htrc_flat_triton.py:348-391, 88-211). */
 int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
               const float* sg, const float* lz, const uint16_t* vb, const int8_t* excl, const int32_t* idx,
               const int8_t* k8, const float* ks, const uint16_t* v, int64_t heads, int64_t nq, int64_t nk,
-              int leaf, int d, int kx, int tile, int group, const int32_t* perm, int splits, int bn, float scale,
-              float* pm, float* pl, float* pacc, float* out, float* logz, void* stream);
+              int leaf, int d, int kx, int tile, int group, int64_t g0, int64_t gn, const int32_t* perm, int splits,
+              int bn, float scale, float* pm, float* pl, float* pacc, float* out, float* logz, void* stream);
 
-/* Merge of split partials into normalised rows, plus logz = max + log(sum).
+/* Merge of the split partials of tiles [t0, t0 + tn) into normalised rows, plus logz = max +
+ * log(sum); the partials are [H, tn, splits, T].
  * Replaces _merge_kernel (h3/htrc_flat_triton.py:257-273, launched at :389-390). */
-int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int tile, int splits,
-               int d, const int32_t* perm, float* out, float* logz, void* stream);
+int htrc_merge(const float* pm, const float* pl, const float* pacc, int64_t heads, int64_t nq, int tile, int64_t t0,
+               int64_t tn, int splits, int d, const int32_t* perm, float* out, float* logz, void* stream);
 
-/* Production path, first launch: select -> top-k per tile group with SEL kept in LDS, writing
- * the routing idx [H, ng, min(kx, nb)] (ascending; required when kx > 0) and rowmax fp32
- * [H, nt*T], each row's largest far-field score (the tile's largest when stride > 1).
+/* Production path, first launch, for the groups [g0, g0 + gn): select -> top-k per tile group
+ * with SEL kept in LDS (in keys_ws [H, gn, nb_pad] uint32 above 16384 leaves per head; NULL
+ * otherwise), writing the routing idx [H, gn, min(kx, nb)] (ascending; required when kx > 0)
+ * and rowmax fp32 [H, nt*T], each row's largest far-field score (the tile's largest when
+ * stride > 1).  Leaves < sink are always selected.
  * Replaces rowmax_select + torch.topk of the chunk loop (h3/htrc_flat.py:258-265). */
 int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, const float* sg, const float* lz,
                       int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink, int stride,
-                      int tile, int group, int32_t* idx, float* rowmax, void* stream);
+                      int tile, int group, int64_t g0, int64_t gn, int32_t* idx, float* rowmax, uint32_t* keys_ws,
+                      void* stream);
 
 /* Production path, second launch: far + near field of every tile in one softmax whose
  * reference is rowmax, merged into normalised out / logz (one split per tile).
@@ -112,16 +133,16 @@ int htrc_route_select(const int8_t* dq8, const float* sdq, const int8_t* g8, con
 int htrc_route_attend(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                       const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                       const uint16_t* v, const int32_t* idx, const float* rowmax, int64_t heads, int64_t nq,
-                      int64_t nk, int leaf, int d, int kx, int tile, int group, const int32_t* perm, float scale,
-                      float* out, float* logz, void* stream);
+                      int64_t nk, int leaf, int d, int kx, int tile, int group, int64_t g0, int64_t gn,
+                      const int32_t* perm, float scale, float* out, float* logz, void* stream);
 
 /* Both launches of the production path: htrc_route_select then htrc_route_attend.
  * Replaces the chunk loop body of _flat_triton after leaf_stats (h3/htrc_flat.py:250-271). */
 int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
                const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
                const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
-               int stride, int tile, int group, const int32_t* perm, float scale, float* out, float* logz,
-               int32_t* idx, float* rowmax, void* stream);
+               int stride, int tile, int group, int64_t g0, int64_t gn, const int32_t* perm, float scale, float* out,
+               float* logz, int32_t* idx, float* rowmax, uint32_t* keys_ws, void* stream);
 
 /* Tail keys: tk, tv fp32 [H, ntail, 128] (keys past the last full leaf) attended exactly by
  * every query and merged in place into a finished out / logz (log-sum-exp merge).  Up to 16
@@ -140,31 +161,33 @@ int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, in
  * Replace leaf_stats(store=float8_e4m3fn), rowmax_select and tile_attention on that state. */
 int htrc_pack_q16(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int tile, int group,
                   const int32_t* perm, int dq_fp16, float* mu, uint16_t* q16, uint16_t* dq16, void* stream);
-int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
-                        int leaf, int d, float scale, uint8_t* g, float* sg, uint8_t* vb, float* sv, float* lz,
-                        void* stream);
+int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
+                        int64_t cn, int64_t nk, int leaf, int d, float scale, uint8_t* g, float* sg, uint8_t* vb,
+                        float* sv, float* lz, void* stream);
 int htrc_select_fp8(const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz, int64_t heads, int64_t nt,
-                    int64_t nb, int stride, int tile, int group, int d, float* sel, void* stream);
+                    int64_t nb, int stride, int tile, int group, int64_t g0, int64_t gn, int d, float* sel,
+                    void* stream);
 int htrc_tile_fp8(const uint16_t* q16, const uint16_t* dq16, const uint8_t* g, const float* sg, const float* lz,
                   const uint8_t* vb, const float* sv, const int8_t* excl, const int32_t* idx, const uint16_t* k,
                   const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int tile,
-                  int group, const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc,
-                  float* out, float* logz, void* stream);
+                  int group, int64_t g0, int64_t gn, const int32_t* perm, int splits, int bn, float scale, float* pm,
+                  float* pl, float* pacc, float* out, float* logz, void* stream);
 
 /* bf16 state store (store="bf16"; DOT = 1 without FP8 / I8 in h3/htrc_flat_triton.py:82-83,
  * 132-153, 165-184, 214-254): g, vb bf16 [H, ng, nbp, 128], no row scales; q16 / dq16 from
  * htrc_pack_q16 with dq_fp16 = 0 (bf16 q - mu).  select: SEL = max_r bf16 dq . g + lz;
  * tile far: bf16 dq . g + lz with PV bf16(p) . vb; near as the fp8 store.
  * Replace leaf_stats(store=bfloat16), rowmax_select and tile_attention on that state. */
-int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t nk,
-                         int leaf, int d, float scale, uint16_t* g, uint16_t* vb, float* lz, void* stream);
+int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
+                         int64_t cn, int64_t nk, int leaf, int d, float scale, uint16_t* g, uint16_t* vb, float* lz,
+                         void* stream);
 int htrc_select_bf16(const uint16_t* dq16, const uint16_t* g, const float* lz, int64_t heads, int64_t nt, int64_t nb,
-                     int stride, int tile, int group, int d, float* sel, void* stream);
+                     int stride, int tile, int group, int64_t g0, int64_t gn, int d, float* sel, void* stream);
 int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g, const float* lz, const uint16_t* vb,
                    const int8_t* excl, const int32_t* idx, const uint16_t* k, const uint16_t* v, int64_t heads,
-                   int64_t nq, int64_t nk, int leaf, int d, int kx, int tile, int group, const int32_t* perm,
-                   int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out, float* logz,
-                   void* stream);
+                   int64_t nq, int64_t nk, int leaf, int d, int kx, int tile, int group, int64_t g0, int64_t gn,
+                   const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out,
+                   float* logz, void* stream);
 
 /* k-means query order: perm int32 [H, nq], the queries ordered by their nearest of `clusters`
  * centres (stable), the centres from `iters` Lloyd steps on `sample` evenly spaced queries.

@@ -19,3 +19,58 @@ def rel_l2(a, b) -> float:
     b = np.asarray(b, np.float64)
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
 
+
+
+def sel_error(sel_gpu, sel_ref, nb) -> np.ndarray:
+    """Per tile (row) max |SEL_gpu - SEL_ref| over the real leaves."""
+    a = np.asarray(sel_gpu, np.float64)[:, :nb]
+    b = np.asarray(sel_ref, np.float64)[:, :nb]
+    return np.abs(a - b).max(axis=1)
+
+
+def routing_report(idx_gpu, idx_ref, sel_ref, delta) -> dict:
+    """Compare near-leaf sets tile by tile.  With |SEL_gpu - SEL_ref| <= delta[t] on every leaf of
+    tile t, the sets can differ only when the reference's own top-k boundary gap
+    s_k - s_(k+1) is at most 2 delta[t] (a leaf a in the reference set and b outside it swap
+    only if SEL_ref[a] - SEL_ref[b] <= 2 delta).  Asserts that every differing tile is such a
+    near-tie and returns the counts: mismatched tiles, tiles whose gap allows a swap, the
+    largest gap at a mismatched tile, and the largest delta."""
+    idx_gpu = np.asarray(idx_gpu)
+    idx_ref = np.asarray(idx_ref)
+    sel = np.asarray(sel_ref, np.float64)
+    kx = idx_ref.shape[1]
+    delta = np.broadcast_to(np.asarray(delta, np.float64), (idx_ref.shape[0],))
+    mism, tieable, max_gap = 0, 0, 0.0
+    for t in range(idx_ref.shape[0]):
+        s = np.sort(sel[t])[::-1]
+        gap = float(s[kx - 1] - s[kx]) if kx < s.size else np.inf
+        if gap <= 2 * delta[t]:
+            tieable += 1
+        if np.array_equal(np.sort(idx_gpu[t]), np.sort(idx_ref[t])):
+            continue
+        assert gap <= 2 * delta[t], f"tile {t}: routing differs at a boundary gap {gap:.3e} > 2 x {delta[t]:.3e}"
+        mism += 1
+        max_gap = max(max_gap, gap)
+    return {"tiles": int(idx_ref.shape[0]), "mismatched": mism, "tieable": tieable, "max_gap": max_gap,
+            "max_delta": float(delta.max()) if delta.size else 0.0}
+
+
+def gpu_sel(st, stride: int = 1) -> np.ndarray:
+    """SEL [ng, nbp] of head 0 from the GPU's own leaf state in a ``state=`` dict (the route and
+    stage selects compute exactly this, bit for bit, on that state)."""
+    from htrc_amd import htrc_flat_hip as hip
+    if st.get("sel") is not None:
+        return st["sel"][0].cpu().numpy()
+    sel = hip.rowmax_select(g=st["g8"], lz=st["lz"], sg=st.get("sg"), stride=stride, nb=st["nb"],
+                            dq8=st.get("dq8", st.get("dq16")), sdq=st.get("sdq"), group=st["group"], tile=st["tile"])
+    return sel[0].cpu().numpy()
+
+
+def record(name: str, rep: dict) -> None:
+    """Append a routing report as one JSON line to $HTRC_REPORT (when set)."""
+    import json
+    import os
+    path = os.environ.get("HTRC_REPORT")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps({"test": name, **rep}) + "\n")

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.lib()
     for n in names:
         assert hasattr(lib, n), f"{n} declared in {HEADER.name} but not exported"
-        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+        assert n in _lib.signatures(), f"{n} has no ctypes signature"
     ver = int(re.search(r"#define HTRC_ABI_VERSION (\d+)", text).group(1))
     assert lib.htrc_abi_version() == ver == _lib.ABI_VERSION
 
@@ -45,7 +45,8 @@ def test_nb_pad():
 _FAKE = ctypes.c_void_p(256)   # never dereferenced: validation fails before any launch
 
 
-@pytest.mark.parametrize("case", ["null", "dim", "leaf", "block", "leaves", "group", "tile", "stride"])
+@pytest.mark.parametrize("case", ["null", "dim", "leaf", "block", "leaves", "near", "group", "tile", "stride",
+                                  "window", "centres", "keys_ws", "merge"])
 def test_launchers_reject_bad_arguments_on_host(case):
     lib = _lib.lib()
     f = _FAKE
@@ -56,25 +57,51 @@ def test_launchers_reject_bad_arguments_on_host(case):
         rc = lib.htrc_pack_k(f, 1, 64, 64, f, f, None)
         msg = "128"
     elif case == "leaf":
-        rc = lib.htrc_leaf_stats(f, f, f, 1, 1, 96, 48, 128, 0.1, f, f, f, f, None)
+        rc = lib.htrc_leaf_stats(f, f, f, 1, 1, 0, 1, 96, 48, 128, 0.1, f, f, f, f, None)
         msg = "leaf"
     elif case == "block":
-        rc = lib.htrc_tile(*([f] * 13), 1, 64, 128, 64, 128, 1, 64, 1, None, 4, 48, 0.1, f, f, f, f, f, None)
+        rc = lib.htrc_tile(*([f] * 13), 1, 64, 128, 64, 128, 1, 64, 1, 0, 1, None, 4, 48, 0.1, f, f, f, f, f, None)
         msg = "multiple of 32"
-    elif case == "leaves":
-        rc = lib.htrc_route(*([f] * 11), 1, 64, 64 * 9000, 64, 128, 4, 0, 1, 64, 1, None, 0.1, f, f, None, f, None)
-        msg = "8192"
+    elif case == "leaves":                        # exclusion bits of more than 262144 leaves exceed the LDS
+        rc = lib.htrc_route(*([f] * 11), 1, 64, 64 * 300000, 64, 128, 4, 0, 1, 64, 1, 0, 1, None, 0.1, f, f, f, f, f,
+                            None)
+        msg = "262144"
+    elif case == "near":                          # the fused route holds at most 8192 near leaves per tile
+        rc = lib.htrc_route(*([f] * 11), 1, 64, 16 * 20000, 16, 128, 9000, 0, 1, 64, 1, 0, 1, None, 0.1, f, f, f, f,
+                            f, None)
+        msg = "8192 near"
     elif case == "group":
-        rc = lib.htrc_route_select(*([f] * 5), 1, 640, 640, 64, 128, 4, 0, 1, 64, 0, f, f, None)
+        rc = lib.htrc_route_select(*([f] * 5), 1, 640, 640, 64, 128, 4, 0, 1, 64, 0, 0, 1, f, f, None, None)
         msg = "group"
     elif case == "tile":
-        rc = lib.htrc_route_select(*([f] * 5), 1, 640, 640, 64, 128, 4, 0, 1, 48, 1, f, f, None)
+        rc = lib.htrc_route_select(*([f] * 5), 1, 640, 640, 64, 128, 4, 0, 1, 48, 1, 0, 1, f, f, None, None)
         msg = "32 or 64"
-    else:                                          # stride must divide a 32-row tile
-        rc = lib.htrc_select(*([f] * 5), 1, 10, 20, 64, 32, 1, 128, f, None)
+    elif case == "stride":                        # stride must divide a 32-row tile
+        rc = lib.htrc_select(*([f] * 5), 1, 10, 20, 64, 32, 1, 0, 10, 128, f, None)
         msg = "divide"
+    elif case == "window":                        # groups [5, 15) of a head of 10 tiles
+        rc = lib.htrc_route_select(*([f] * 5), 1, 640, 640, 64, 128, 4, 0, 1, 64, 1, 5, 10, f, f, None, None)
+        msg = "window"
+    elif case == "centres":                       # centres [2, 4) of 3
+        rc = lib.htrc_leaf_stats(f, f, f, 1, 3, 2, 2, 128, 64, 128, 0.1, f, f, f, f, None)
+        msg = "window"
+    elif case == "keys_ws":                       # above 16384 leaves per head the top-k keys need keys_ws
+        rc = lib.htrc_route_select(*([f] * 5), 1, 640, 16 * 20000, 16, 128, 4, 0, 1, 64, 1, 0, 10, f, f, None, None)
+        msg = "keys_ws"
+    else:                                         # tiles [8, 12) of a head of 10
+        rc = lib.htrc_merge(f, f, f, 1, 640, 64, 8, 4, 4, 128, None, f, f, None)
+        msg = "window"
     assert rc == 1
     assert msg in lib.htrc_last_error().decode()
+
+
+def test_header_signatures_parse():
+    """The ctypes binding is read from the header: pointers, int64_t, int and float parameters."""
+    sig = _lib.parse_header("""/* c */ int htrc_x(const float* a, int64_t n, int k, float s, void* st);
+                               const char* htrc_y(void);""")
+    assert sig["htrc_x"][0] == [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_void_p]
+    assert sig["htrc_y"] == ([], ctypes.c_char_p)
+    assert len(_lib.signatures()["htrc_route"][0]) == 31
 
 
 def test_call_maps_errors_to_value_error():
@@ -151,17 +178,49 @@ def test_prod_knobs_match_reference():
 def test_runner_modes_and_memory_model():
     assert set(htrc_flat_runner.MODES) == {"fast", "balanced", "accurate", "max"}
     assert htrc_flat_runner.CHUNKS == (1024, 512, 256, 128, 64, 32, 16)
-    mib = htrc_flat_runner.predicted_peak_mib(64512, 64, 128, leaf=64, queries=64512, heads=24)
-    # cfg3 layer: per-(tile, leaf) state dominates: 24 * 1008 * 1024 * 392 B = 9252 MiB
+    mib = htrc_flat_runner.predicted_peak_mib(64512, 64, 1024, leaf=64, queries=64512, heads=24, exact_leaves=32)
+    # cfg3 layer in one window: per-(tile, leaf) state dominates: 24 * 1008 * 1024 * 392 B = 9252 MiB
     assert 9252 < mib < 16000
     assert htrc_flat_runner.plan_chunk(64 << 30, 64512, 64, leaf=64, queries=64512, heads=24) == 1024
-    with pytest.raises(MemoryError):
+    # windows bound the state: 3.5 GiB takes windows of 64 tiles (~3.4 GiB), 128 tiles need ~4.0 GiB
+    c = htrc_flat_runner.plan_chunk(3584 << 20, 64512, 64, leaf=64, queries=64512, heads=24, exact_leaves=32)
+    assert c == 64
+    assert htrc_flat_runner.predicted_peak_mib(64512, 64, 128, leaf=64, queries=64512, heads=24,
+                                               exact_leaves=32) > 3584
+    with pytest.raises(MemoryError):             # the layer's operands and outputs alone need ~3 GiB
         htrc_flat_runner.plan_chunk(1 << 30, 64512, 64, leaf=64, queries=64512, heads=24)
+    # the window state scales with the window: 128 against 1024 tiles (1008 real) at cfg3
+    m128 = htrc_flat_runner.predicted_peak_mib(64512, 64, 128, leaf=64, queries=64512, heads=24, exact_leaves=32)
+    assert mib - m128 == pytest.approx(24 * (1008 - 128) * (1024 * 392 + 4 * 32) / 2 ** 20, rel=1e-6)
     with pytest.raises(ValueError, match="mode"):
         htrc_flat_runner.FlatRunner(64, 64, mode="nope")
     assert htrc_flat_runner.SUPPORTED_MODES == ("fast", "balanced", "accurate", "max")
     # 32-row tiles double the centres: the per-(tile, leaf) state doubles
-    m32 = htrc_flat_runner.predicted_peak_mib(64512, 32, 128, leaf=64, queries=64512, heads=24)
-    assert m32 - mib == pytest.approx(24 * 1008 * 1024 * 392 / 2 ** 20, rel=0.02)
-    km = htrc_flat_runner.predicted_peak_mib(64512, 64, 128, leaf=64, queries=64512, heads=24, order="kmeans")
+    m32 = htrc_flat_runner.predicted_peak_mib(64512, 32, 4096, leaf=64, queries=64512, heads=24, exact_leaves=32)
+    assert m32 - mib == pytest.approx(24 * 1008 * (1024 * 392 + 4 * 32) / 2 ** 20, rel=0.02)
+    km = htrc_flat_runner.predicted_peak_mib(64512, 64, 1024, leaf=64, queries=64512, heads=24, order="kmeans",
+                                             exact_leaves=32)
     assert km - mib == pytest.approx(24 * (8 * 64512 + 4 * 32 * 128) / 2 ** 20)
+    assert htrc_flat_runner.STATIC_MIB == pytest.approx(39.8, abs=0.05)
+
+
+def test_runner_plan_merges_knobs():
+    """PROD, then the mode, then the caller's knobs with kern merged key by key; the window from
+    free_bytes steps down through CHUNKS."""
+    plan = htrc_flat_runner._Plan(htrc_flat, "fast", {"leaf": 64, "kern": {"group": 2}}, 3, 64512, 64512, 24,
+                                  6 << 30, None, True)
+    assert plan.cfg["exact_leaves"] == 256 and plan.cfg["leaf"] == 64 and plan.cfg["sink_leaves"] == 3
+    assert plan.cfg["kern"] == {**htrc_flat.PROD["kern"], "group": 2}
+    assert plan.cfg["tile_chunk"] in htrc_flat_runner.CHUNKS[1:] and plan.mib * 2 ** 20 <= 6 << 30
+    plan = htrc_flat_runner._Plan(htrc_flat, "max", {}, 0, 4096, 4096, 1, None, None, False)
+    assert plan.cfg["tile"] == 32 and plan.cfg["order"] == "kmeans" and plan.cfg["tile_chunk"] == 128
+
+
+def test_windows_cover_every_group_once():
+    for ng in (1, 7, 16, 1008):
+        for chunk, group in ((1, 1), (16, 1), (32, 4), (128, 3), (1024, 1), (None, 1), (0, 2)):
+            wins = htrc_flat._windows(ng, chunk, group)
+            cover = [g for g0, gn in wins for g in range(g0, g0 + gn)]
+            assert cover == list(range(ng))
+            step = ng if not chunk else max(1, chunk // group)
+            assert all(gn == min(step, ng - g0) for g0, gn in wins)

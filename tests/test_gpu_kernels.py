@@ -179,7 +179,8 @@ def test_select_bitexact_on_oracle_state(device):
         assert np.array_equal(_np(sel[0])[:, :nb].view(np.uint32), osel.view(np.uint32)), f"stride {stride}"
 
 
-@pytest.mark.parametrize("nb,kx,sink", [(1008, 32, 0), (256, 16, 3), (37, 37, 0), (100, 1, 0), (8192, 64, 0)])
+@pytest.mark.parametrize("nb,kx,sink", [(1008, 32, 0), (256, 16, 3), (37, 37, 0), (100, 1, 0), (8192, 64, 0),
+                                         (9000, 1244, 220), (20000, 300, 5)])
 def test_topk_bitexact(device, nb, kx, sink):
     rng = np.random.default_rng(nb + kx)
     rows = 24
