@@ -4,8 +4,9 @@ One step = one flat-HTRC layer call: B=1, H=24, N=64512, d=128, leaf 64, 32 near
 int8 Q/K + bf16 PV, on synthetic clustered video-region inputs already resident in HBM.
 Prints ONE JSON line (the driver's contract) with the layer ms/call, the roofline of the
 dominant kernel (HIP events on the launch stream, algorithmic bytes or ops per launch),
-per-kernel figures, and the reference's CPU path (NumPy restatement of the torch backend
-_flat, h3/htrc_flat.py:279-388) timed on a bounded sample of the same workload.
+per-kernel figures, and the reference's CPU path timed on this host in the same run: the NumPy
+restatement of the torch backend _flat (h3/htrc_flat.py:279-388) over the whole layer, and
+BASELINE configuration 1's NumPy htrc_reference (src/htrc_reference/model.py:98-137, restated).
 
   python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--config cfg3] [--no-cpu-baseline]
 
@@ -53,6 +54,12 @@ def algorithmic(h, nq, nk, leaf, kx, d=128, tile=64):
                                        + 4 * nq * (d + 1)),
                          "i8_ops": h * (2 * rows * nb * d + 2 * rows * kx * leaf * d),
                          "bf16_flops": h * (2 * rows * nb * d + 2 * rows * kx * leaf * d)}
+    # the attend launch split into its two fields: far (every leaf's state, kx = 0) and near (the
+    # exact tokens of the kx near leaves, timed as the difference)
+    f["far_field"] = {"bytes": h * (state + rows * (d + 4) + rows * 4 + 4 * nq * (d + 1)),
+                      "i8_ops": h * 2 * rows * nb * d, "bf16_flops": h * 2 * rows * nb * d}
+    f["near_field"] = {"bytes": h * (rows * (d + 4) + nk * (3 * d + 4) + nt * kx * 4),
+                       "i8_ops": h * 2 * rows * kx * leaf * d, "bf16_flops": h * 2 * rows * kx * leaf * d}
     return f
 
 
@@ -131,43 +138,75 @@ def measured_peaks(dev, reps=5):
     return res
 
 
-def cpu_baseline(name, budget_s=10.0):
-    """Reference CPU path (NumPy restatement of _flat) on whole heads until budget_s has
-    elapsed; extrapolated to the layer's head count."""
-    import numpy as np
-    from htrc_amd import workloads
-    from oracle import flat_fp32
-    gen, kw, leaf, ex, heads = workloads.CONFIGS[name]
+def _cpu_info():
+    """(BLAS threads, CPU model) of this host."""
     try:
         from threadpoolctl import threadpool_info
         threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    except Exception:  # noqa: BLE001
+    except Exception:  # noqa: BLE001 -- threadpoolctl absent or failing: report the visible CPUs
         threads = os.cpu_count() or 1
-    done, elapsed = 0, 0.0
-    seed = 0
-    while done < heads and (elapsed < budget_s or done == 0):
-        q, k, v, _, _ = workloads.make(name, seed=1000 + seed, heads=1)
-        seed += 1
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return int(threads), model
+
+
+def cpu_flat_layer(name, heads=None):
+    """The reference's CPU operator (the torch backend _flat, h3/htrc_flat.py:279-388, restated
+    in NumPy fp32) over the configuration's heads, one pass -> (ms for the heads, heads)."""
+    from htrc_amd import workloads
+    from oracle import flat_fp32
+    gen, kw, leaf, ex, h0 = workloads.CONFIGS[name]
+    heads = h0 if heads is None else heads
+    elapsed = 0.0
+    for h in range(heads):
+        q, k, v, _, _ = workloads.make(name, seed=1000 + h, heads=1)
         qf, kf, vf = (x[0].float().numpy() for x in (q, k, v))
-        if done == 0:       # one warm chunk (BLAS threads, page faults) outside the timing
+        if h == 0:          # one warm chunk (BLAS threads, page faults) outside the timing
             flat_fp32.flat_fp32(qf, kf, vf, tile=64, leaf=leaf, exact_leaves=ex, tile_chunk=32, tiles=slice(0, 32))
         t0 = time.perf_counter()
         flat_fp32.flat_fp32(qf, kf, vf, tile=64, leaf=leaf, exact_leaves=ex, tile_chunk=32)
         elapsed += time.perf_counter() - t0
-        done += 1
-    per_layer_ms = elapsed / done * heads * 1e3
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(per_layer_ms, 1), "unit": "ms/call", "cores": int(threads), "kind": "port",
-            "sample": f"{done} of {heads} heads ({elapsed:.1f} s), extrapolated x{heads / done:.1f}; NumPy fp32 "
-                      f"restatement of the torch backend _flat (h3/htrc_flat.py:279-388), tile_chunk 32",
-            "cpu": cpu_model, "os_cpu_count": os.cpu_count()}
+    return elapsed * 1e3, heads
+
+
+def cpu_reference_cfg1():
+    """the NumPy float64 htrc_reference (src/htrc_reference/model.py:98-137,
+    restated) over all 1024 queries, 4096 keys, d = 64, leaves of 64, fanout 4 -> (ms, errors)."""
+    from oracle import htrc_ref
+    t0 = time.perf_counter()
+    res = htrc_ref.config1(seed=0)
+    return (time.perf_counter() - t0) * 1e3, res
+
+
+def cpu_baseline(name, heads=None):
+    """The reference's CPU path timed on this host in the same run: the flat operator (_flat) over
+    the whole layer of configuration ``name`` (all heads unless ``heads`` is given, then scaled
+    to the layer), and configuration 1's NumPy htrc_reference."""
+    from htrc_amd import workloads
+    h_layer = workloads.CONFIGS[name][4]
+    threads, model = _cpu_info()
+    ms, done = cpu_flat_layer(name, heads)
+    layer_ms = ms * h_layer / done
+    ref_ms, ref = cpu_reference_cfg1()
+    sample = (f"one full pass over all {h_layer} heads" if done == h_layer else
+              f"{done} of {h_layer} heads ({ms / 1e3:.1f} s), scaled x{h_layer / done:.2f}")
+    return {"value": round(layer_ms, 1), "unit": "ms/call", "cores": threads, "kind": "port",
+            "sample": f"{sample}; NumPy fp32 restatement of the torch backend _flat (h3/htrc_flat.py:279-388), "
+                      f"tile_chunk 32",
+            "cpu": model, "os_cpu_count": os.cpu_count(),
+            "htrc_reference_cfg1": {"value": round(ref_ms, 1), "unit": "ms (1024 queries)", "cores": threads,
+                                    "kind": "port",
+                                    "sample": "BASELINE configuration 1 whole: NumPy float64 htrc_reference "
+                                              "(src/htrc_reference/model.py:98-137, restated), 1024 queries x "
+                                              "4096 keys, d=64, leaves of 64, fanout 4",
+                                    "rel_l2_median": round(ref["rel_l2_median"], 4),
+                                    "logz_abs_max": round(ref["logz_abs_max"], 4)}}
 
 
 def exact_attention(q, k, v, scale, chunk=4096):
@@ -248,7 +287,8 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--calls", type=int, default=50, help="cfg5: sequential layer calls")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--cpu-heads", type=int, default=None,
+                    help="heads of the CPU baseline pass (default: the whole layer)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also launch one copy-shaped 1 GiB kernel (the scale of the FETCH_SIZE/WRITE_SIZE counters)")
     a = ap.parse_args()
@@ -258,7 +298,7 @@ def main():
         sys.exit(2)
 
     import torch
-    from htrc_amd import htrc_flat, htrc_flat_hip as hip, workloads
+    from htrc_amd import htrc_flat, htrc_flat_hip as hip, htrc_flat_runner, workloads
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     if a.config == "cfg5":
@@ -270,22 +310,30 @@ def main():
     nb = nk // leaf
     kx = min(ex, nb)
     ws = {}
-    kw = dict(backend="hip", store="int8", dot="bf16", leaf=leaf, exact_leaves=ex, kern={"fused": True})
+    # the tile window the production runner plans for this layer and the free device memory
+    # (h3/htrc_flat_runner.py:71-82): the whole layer in one window when it fits
+    chunk = htrc_flat_runner.plan_chunk(torch.cuda.mem_get_info(dev)[0], nk, 64, leaf=leaf, queries=nq, heads=h,
+                                        exact_leaves=kx, graph=False)
+    kw = dict(backend="hip", store="int8", dot="bf16", leaf=leaf, exact_leaves=ex, tile_chunk=chunk,
+              kern={"fused": True})
 
-    def step():
-        return htrc_flat.flat_attention(q, k, v, ws=ws, **kw)
+    def layer_ms(kwargs, steps, warmup):
+        for _ in range(warmup):
+            htrc_flat.flat_attention(q, k, v, ws=ws, **kwargs)
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(steps):
+            res = htrc_flat.flat_attention(q, k, v, ws=ws, **kwargs)
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / steps, res
 
-    for _ in range(a.warmup):
-        step()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(a.steps):
-        out = step()
-    ev1.record()
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / a.steps
+    ms, out = layer_ms(kw, a.steps, a.warmup)
     assert torch.isfinite(out).all().item(), "non-finite output"
+    # the same layer in the reference PROD's tile windows (tile_chunk 128): the memory-bounded mode
+    ms_prod_windows, _ = layer_ms({**kw, "tile_chunk": htrc_flat.PROD["tile_chunk"]}, max(3, a.steps // 2), 1)
+    ws.clear()
 
     # per-kernel launch durations, HIP events on the stream the kernels are launched on
     scale = 1.0 / math.sqrt(d)
@@ -302,6 +350,9 @@ def main():
         "route_select": lambda: hip.route_select(packed, lstate, nq=nq, leaf=leaf, kx=kx, ws=ws),
         "route_attend": lambda: hip.route_attend(packed, lstate, idx, rowmax, nq=nq, leaf=leaf, kx=kx, scale=scale,
                                                  ws=ws),
+        # the attend launch with no near leaves: the far field alone (the near field is the difference)
+        "far_field": lambda: hip.route_attend(packed, lstate, None, rowmax, nq=nq, leaf=leaf, kx=0, scale=scale,
+                                              ws=ws),
     }
     kms = {}
     stream = torch.cuda.current_stream(dev)
@@ -325,7 +376,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     figs = algorithmic(h, nq, nk, leaf, kx, d)
-    kernels = {n: roofline_entry(n, kms[n], figs[n]) for n in stages}
+    kms["near_field"] = max(kms["route_attend"] - kms["far_field"], 1e-6)
+    kernels = {n: roofline_entry(n, kms[n], figs[n]) for n in list(stages) + ["near_field"]}
     peaks = measured_peaks(dev)
     for n, e in kernels.items():        # the same figures against the measured rates
         e["hbm_frac_measured"] = round(e["hbm_GBps"] / peaks["copy_GBps"], 4)
@@ -336,7 +388,7 @@ def main():
     traffic = measured_traffic(a.config)
     for n, e in kernels.items():
         e["traffic"] = traffic.get(n)
-    dom = max(kernels.values(), key=lambda e: e["ms"])
+    dom = max((e for n, e in kernels.items() if n not in ("far_field", "near_field")), key=lambda e: e["ms"])
     fig = figs[dom["kernel"]]
     if dom["bound"] == "hbm":
         ach = fig["bytes"] / (dom["ms"] * 1e-3) / 1e9
@@ -361,10 +413,11 @@ def main():
            "vs_baseline": None, "dtype": "i8/bf16 (fp32 accumulate)",
            "data": "synthetic: clustered spatiotemporal regions, seed 0, generated on device",
            "config": {"workload": f"{a.config}: B=1 H={h} N={nq} d={d} leaf={leaf} near={kx} tile=64",
-                      "heads": h, "queries": nq, "keys": nk, "leaf": leaf, "near_leaves": kx},
+                      "heads": h, "queries": nq, "keys": nk, "leaf": leaf, "near_leaves": kx, "tile_chunk": chunk},
+           "ms_tile_chunk_128": round(ms_prod_windows, 4),
            "roofline": roof, "kernels": kernels, "measured_peaks": peaks}
     if not a.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(a.config, a.cpu_budget)
+        res["cpu_baseline"] = cpu_baseline(a.config, a.cpu_heads)
     print(json.dumps(res), flush=True)
 
 

@@ -98,9 +98,13 @@ def test_fullsize_whole_head_routing(layer):
                             dq8=st["dq8"][hr:hr + 1], sdq=st["sdq"][hr:hr + 1], tile=tile)[0].cpu().numpy()
     delta = sel_error(sel, osel, nb)
     rep = routing_report(st["idx"][hr].cpu().numpy(), oidx, osel, delta)
+    # a tile whose g8 codes all agree differs in SEL by the fp32 rounding of lz and sg only
+    clean = ~(g8 != og8).any(axis=(1, 2))
     rep["g8_flip_frac"] = flips
+    rep["tiles_with_flips"] = int((~clean).sum())
+    rep["max_delta_clean"] = float(delta[clean].max()) if clean.any() else 0.0
     record(f"{name} whole head {hr}", rep)
-    assert rep["max_delta"] <= 1e-4 * max(1.0, float(np.abs(osel).max()))
+    assert rep["max_delta_clean"] <= 2e-6 * max(1.0, float(np.abs(osel[:, :nb]).max()))
 
 
 def test_fullsize_windows_and_single_head_are_bit_identical(layer):
