@@ -23,6 +23,7 @@
 #include <stdio.h>
 #include <string.h>
 #include <atomic>
+#include <mutex>
 
 using namespace htrc;
 
@@ -2295,6 +2296,13 @@ __global__ __launch_bounds__(64) void selftest_mfma_kernel(const int8_t* __restr
 // =============================================================================================
 #include "htrc_flat.h"
 
+// Scratch of htrc_route_noalloc, the route entry point that allocates nothing: rowmax, the near
+// leaves and (above ROUTE_NB_LDS leaves per head) the top-k keys live here instead of in caller
+// workspace.  Each device that runs the library holds its own copy until the process ends; host
+// code reaches it only through the address hipGetSymbolAddress returns on that device.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
 static thread_local char g_err[512] = "";
 
 static int fail(int code, const char* msg) {
@@ -2832,6 +2840,64 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
     if (rc != HTRC_OK) return rc;
     return htrc_route_attend(q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, rowmax, heads, nq, nk, leaf, d, kx,
                              tile, group, g0, gn, perm, scale, out, logz, stream);
+}
+
+// Device address of `scratch` on the current device, resolved once per device (with that device
+// current) and kept; nullptr with the error set when the runtime cannot resolve it.
+static void* scratch_ptr() {
+    static std::mutex mu;
+    static void* addr[64] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        fail(HTRC_ERR_HIP, "htrc_route_noalloc: no current HIP device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            snprintf(g_err, sizeof(g_err), "htrc_route_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                     hipGetErrorString(e));
+            return nullptr;
+        }
+        addr[dev] = p;
+    }
+    return addr[dev];
+}
+
+int htrc_route_noalloc(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
+                       const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
+                       const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
+                       int stride, int tile, int group, int64_t g0, int64_t gn, const int32_t* perm, float scale,
+                       float* out, float* logz, void* stream) {
+    REQUIRE(q8 && sq && dq8 && sdq && g8 && sg && lz && vb && k8 && ks && v && out && logz,
+            "htrc_route_noalloc: null pointer");
+    int64_t nb, nt, ng, tb, ntw;
+    int kxe;
+    const int rc = route_shapes("htrc_route_noalloc", heads, nq, nk, leaf, d, kx, tile, group, g0, gn, nb, nt, ng, tb,
+                                ntw, kxe);
+    if (rc != HTRC_OK) return rc;
+    // rowmax [H, nt * tile] fp32 | idx [H, gn, kxe] int32 | keys [H, gn, nb_pad] uint32, 256-byte aligned parts;
+    // every part is written before it is read, so nothing needs clearing between calls
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t b_rowmax = up((size_t)heads * (size_t)nt * (size_t)tile * 4);
+    const size_t b_idx = up((size_t)heads * (size_t)gn * (size_t)kxe * 4);
+    const size_t b_keys = nb > ROUTE_NB_LDS ? up((size_t)heads * (size_t)gn * (size_t)htrc_nb_pad(nb) * 4) : 0;
+    if (b_rowmax + b_idx + b_keys > NOALLOC_SCRATCH_BYTES) {
+        snprintf(g_err, sizeof(g_err),
+                 "htrc_route_noalloc: this call needs %zu bytes of scratch; the allocation-free route holds %zu "
+                 "(use htrc_route with caller workspace, or fewer heads / a smaller window)",
+                 b_rowmax + b_idx + b_keys, NOALLOC_SCRATCH_BYTES);
+        return HTRC_ERR_ARG;
+    }
+    unsigned char* base = (unsigned char*)scratch_ptr();
+    if (!base) return HTRC_ERR_HIP;
+    float* rowmax = (float*)base;
+    int32_t* idx = kxe > 0 ? (int32_t*)(base + b_rowmax) : nullptr;
+    uint32_t* keys = b_keys ? (uint32_t*)(base + b_rowmax + b_idx) : nullptr;
+    return htrc_route(q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, heads, nq, nk, leaf, d, kx, sink, stride, tile, group,
+                      g0, gn, perm, scale, out, logz, idx, rowmax, keys, stream);
 }
 
 int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,

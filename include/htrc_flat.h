@@ -144,6 +144,20 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
                int stride, int tile, int group, int64_t g0, int64_t gn, const int32_t* perm, float scale, float* out,
                float* logz, int32_t* idx, float* rowmax, uint32_t* keys_ws, void* stream);
 
+/* htrc_route without caller workspace: rowmax, the near leaves and the top-k keys live in a
+ * scratch array of 32 MiB that the library keeps on each device (resolved at the first call on
+ * a device); the call allocates nothing, so callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc) can run the fused route.  It
+ * needs 4 * H * nt * T + 4 * H * gn * min(kx, nb) bytes (+ 4 * H * gn * nb_pad above 16384
+ * leaves per head) within 32 MiB and rejects larger calls with HTRC_ERR_ARG.  Every call on one
+ * device shares that device's scratch: calls that overlap on one device (several streams or
+ * threads) race and must be serialised by the caller.  No counterpart in the reference. */
+int htrc_route_noalloc(const int8_t* q8, const float* sq, const int8_t* dq8, const float* sdq, const int8_t* g8,
+                       const float* sg, const float* lz, const uint16_t* vb, const int8_t* k8, const float* ks,
+                       const uint16_t* v, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int sink,
+                       int stride, int tile, int group, int64_t g0, int64_t gn, const int32_t* perm, float scale,
+                       float* out, float* logz, void* stream);
+
 /* Tail keys: tk, tv fp32 [H, ntail, 128] (keys past the last full leaf) attended exactly by
  * every query and merged in place into a finished out / logz (log-sum-exp merge).  Up to 16
  * tail keys are taken with q, k, v and p rounded to bf16, more in fp32, as the reference does.
