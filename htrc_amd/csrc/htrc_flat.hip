@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
     float m[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) m[e] = smu[8 * i + e];
-#pragma unroll 1
+#pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int r = 16 * w + 4 * it + g;         // row of this 16-lane group
         float x[8], d[8], aq = 0.0f, ad = 0.0f;
@@ -191,11 +191,18 @@ __global__ __launch_bounds__(256) void pack_k_kernel(const uint16_t* __restrict_
                                                      int8_t* __restrict__ k8, float* __restrict__ ks) {
     const int h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
     const int64_t base = (int64_t)h * nk;
-#pragma unroll 1
+    // the four rows' loads are issued together, then each row is quantised and stored
+    u32x4 ld[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int64_t r = (int64_t)blockIdx.x * 64 + 16 * w + 4 * it + g;
+        ld[it] = r < nk ? *(const u32x4*)(k + (base + r) * D + 8 * i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int64_t r = (int64_t)blockIdx.x * 64 + 16 * w + 4 * it + g;
         if (r >= nk) break;                       // nk % 16 == 0: whole 16-lane groups leave together
-        const u32x4 u = *(const u32x4*)(k + (base + r) * D + 8 * i);
+        const u32x4 u = ld[it];
         const float x[8] = {bf2f(u.x & 0xffffu), bf2f(u.x >> 16), bf2f(u.y & 0xffffu), bf2f(u.y >> 16),
                             bf2f(u.z & 0xffffu), bf2f(u.z >> 16), bf2f(u.w & 0xffffu), bf2f(u.w >> 16)};
         float a = 0.0f;
@@ -2000,6 +2007,337 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
 }
 
 // ---------------------------------------------------------------------------------------------
+// route16: the fused production path for the 16-bit state stores (store="fp8": e4m3 g / vb with
+// row scales; store="bf16"), two launches per tile window like route:
+//   route_select16_kernel, one 4-wave workgroup per tile group: SEL of every leaf with the
+//     arithmetic of select16_kernel (bit-exact), kept in LDS, its kx largest (leaves < sink
+//     forced in) and every row's largest far-field score, the fixed softmax reference;
+//   route16_kernel, one workgroup per tile, one wave per 16 rows: one continuous stream of
+//     32-key blocks, the far leaves first, then the near tokens, each block staged once in LDS
+//     for every wave of the tile (a 2-slot ring filled through registers: the next block's
+//     loads are issued before the current block is computed); fp8 codes are widened to fp16
+//     (value * 2^-8, exactly) as they are staged.  Far: score = (dq . g) (* 256 sg) + lz, PV with
+//     fp16(p * 256 sv) . vb (fp8) or bf16(p) . vb (bf16); near: score = (q . k) * scale (bf16),
+//     PV bf16(p) . v -- the products of tile16_kernel, in one softmax whose reference is the
+//     row's far-field maximum (redone with a moved reference if a row total leaves
+//     [2^-60, 2^64], as route_kernel).
+// ---------------------------------------------------------------------------------------------
+template <bool FP8, int NRB>
+__global__ __launch_bounds__(256, 3) void route_select16_kernel(
+    const uint16_t* __restrict__ dq16, const void* __restrict__ g, const float* __restrict__ sg,
+    const float* __restrict__ lz, int nt, int group, int g0, int ng, int nb, int nb_pad, int kx, int sink,
+    int stride, int32_t* __restrict__ idx, float* __restrict__ rowmax) {
+    extern __shared__ uint32_t keys16[];      // [nb]
+    __shared__ TopkSmem sm;
+    __shared__ float red_m[4][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
+    const int gi = (int)(blk % (uint32_t)ng), h = (int)(blk / (uint32_t)ng);
+    const int64_t gs = (int64_t)h * ng + gi;  // state / idx row (the launch's window)
+    constexpr int TR = 16 * NRB;              // rows per tile
+    const int ts = TR / stride;
+    bool first = true;
+    for (int j = 0; j < group; ++j) {
+        const int t = (g0 + gi) * group + j;
+        if (t >= nt) break;                   // padded tiles repeat the last one
+        const int64_t th = (int64_t)h * nt + t;
+        u32x4 b[NRB][4];
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+            const int r = 16 * rb + col;
+            const int64_t p = th * TR + (int64_t)(r < ts ? r : 0) * stride;   // rows past ts repeat row 0
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) b[rb][ks] = *(const u32x4*)(dq16 + p * D + 32 * ks + 8 * grp);
+        }
+        float rmax[NRB];
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) rmax[rb] = -INFINITY;
+        for (int c = 16 * w; c < nb; c += 64) {          // the wave's 16-leaf groups
+            const int64_t s0 = gs * nb_pad + c;
+            f32x4 acc[NRB];
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int rb = 0; rb < NRB; ++rb) acc[rb] = state_qk<FP8>(g, s0 + col, ks, grp, b[rb][ks], acc[rb]);
+            const f32x4 sgv = FP8 ? *(const f32x4*)(sg + s0 + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
+            const f32x4 lzv = *(const f32x4*)(lz + s0 + 4 * grp);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float sc = __fmul_rn(sgv[i], 256.0f);
+                float best = -INFINITY;
+#pragma unroll
+                for (int rb = 0; rb < NRB; ++rb) {
+                    const float x = FP8 ? __fmul_rn(acc[rb][i], sc) : acc[rb][i];
+                    best = fmaxf(best, x);
+                    rmax[rb] = fmaxf(rmax[rb], __fadd_rn(x, lzv[i]));
+                }
+                best = col_max(best);
+                const int l = c + 4 * grp + i;
+                if (col == 0 && l < nb) {     // leaf l is always this lane's: no race across tiles
+                    const uint32_t key = l < sink ? 0xffffffffu : order_key(__fadd_rn(best, lzv[i]));
+                    keys16[l] = first ? key : max(keys16[l], key);
+                }
+            }
+        }
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+            const float mx = grp_max(rmax[rb]);
+            if (grp == 0) red_m[w][16 * rb + col] = mx;
+        }
+        __syncthreads();
+        if (w == 0) {
+            const int r = lane;
+            float m = r < ts ? fmaxf(fmaxf(red_m[0][r], red_m[1][r]), fmaxf(red_m[2][r], red_m[3][r])) : -INFINITY;
+            if (stride != 1) m = wave_max(m); // sampled rows: one reference for the whole tile
+            if (r < TR) rowmax[th * TR + r] = m;
+        }
+        __syncthreads();                      // red_m is free for the next tile of the group
+        first = false;
+    }
+    const int kxe = min(kx, nb);
+    if (kxe > 0) topk_row([&](int l) { return keys16[l]; }, nb, kxe, sm, idx + gs * kxe, nullptr, nullptr);
+}
+
+// One ring slot of route16_kernel: QK rows and PV rows, 32 rows of 128 16-bit values each (row r's
+// 16-byte chunk c at chunk c ^ swz(r)), then up to three 32-float scale vectors.
+constexpr int R16_ROWS = 32 * 256;
+constexpr int R16_SLOT = 2 * R16_ROWS + 3 * 32 * 4;
+
+// p = 2^u for the log2-domain shifted scores u[0..7] of one row block (keys 16(e/4) + 4grp + e%4),
+// l += p, O^T += V^T P^T with P = fp16(p * pscale) per key (the fp8 far field).
+__device__ __forceinline__ void rows_update_f16(RowsN<1>& st, const float (&u)[8], const float (&pscale)[8],
+                                                const u32x2 (&v)[8][2]) {
+    float p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(u[e]);
+    st.l[0] = __fadd_rn(st.l[0], __fadd_rn(__fadd_rn(__fadd_rn(p[0], p[1]), __fadd_rn(p[2], p[3])),
+                                           __fadd_rn(__fadd_rn(p[4], p[5]), __fadd_rn(p[6], p[7]))));
+    uint32_t ph[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        ph[j] = pack2h(__fmul_rn(p[2 * j], pscale[2 * j]), __fmul_rn(p[2 * j + 1], pscale[2 * j + 1]));
+    const u32x4 P = u32x4{ph[0], ph[1], ph[2], ph[3]};
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+        const u32x4 A = u32x4{v[db][0].x, v[db][0].y, v[db][1].x, v[db][1].y};
+        st.o[0][db] = mfma_f16(A, P, st.o[0][db]);
+    }
+}
+
+template <int LEAF, bool FP8, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
+    const uint16_t* __restrict__ q16, const uint16_t* __restrict__ dq16, const void* __restrict__ g,
+    const float* __restrict__ sg, const float* __restrict__ lz, const void* __restrict__ vb,
+    const float* __restrict__ sv, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const int32_t* __restrict__ idx, const float* __restrict__ rowmax, int64_t nq, int nt, int group, int g0, int ng,
+    const int32_t* __restrict__ perm, int64_t nk, int nb, int nb_pad, int kxe, float scale,
+    float* __restrict__ out, float* __restrict__ logz) {
+    constexpr int NT = 64 * NW, TR = 16 * NW;  // threads, rows per tile (one wave per 16 rows)
+    constexpr int NC = 512 / NT;               // 16-byte chunks of a 32 x 256-byte region per thread
+    __shared__ __align__(16) char ring[2][R16_SLOT];
+    // sized by the launch: exclusion bits [nb / 32 + 1], then the tile's near leaves [kxe]
+    extern __shared__ __align__(16) uint32_t r16_dyn[];
+    uint32_t* exbits = r16_dyn;
+    uint32_t* sidx = r16_dyn + (nb / 32 + 1);
+    __shared__ float red_l[TR];
+    __shared__ int redo;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    // 1-D grid over (tile, head), tile fastest (route_kernel's XCD-contiguous order); the tiles of
+    // groups [g0, g0 + ng), state and idx rows the launch's own
+    const int tb = g0 * group, ntw = min(nt, (g0 + ng) * group) - tb;
+    const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
+    const int t = tb + (int)(blk % (uint32_t)ntw), h = (int)(blk / (uint32_t)ntw);
+    const int64_t th = (int64_t)h * nt + t;
+    const int64_t gs = (int64_t)h * ng + (t / group - g0);
+    const int64_t kh = (int64_t)h * nk;
+    const int64_t prow = th * TR + 16 * wv + col;           // this lane's packed query row
+    for (int i = threadIdx.x; i <= nb / 32; i += NT) {     // leaves >= nb excluded
+        const int past = nb - 32 * i;
+        exbits[i] = past >= 32 ? 0u : (past <= 0 ? ~0u : ~0u << past);
+    }
+    for (int j = threadIdx.x; j < kxe; j += NT) sidx[j] = (uint32_t)idx[gs * kxe + j];
+    float mref;
+    {
+        const float m = rowmax[prow];
+        mref = m == -INFINITY ? 0.0f : __fmul_rn(m, LOG2E);
+    }
+    u32x4 bdq[4], bq[4];                                    // B operands: row's q - mu, q (16-bit)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        bdq[ks] = *(const u32x4*)(dq16 + prow * D + 32 * ks + 8 * grp);
+        bq[ks] = *(const u32x4*)(q16 + prow * D + 32 * ks + 8 * grp);
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < kxe; j += NT) atomicOr(&exbits[sidx[j] >> 5], 1u << (sidx[j] & 31));
+    __syncthreads();
+    const int nf = (nb + 31) / 32;                          // far blocks of 32 leaves (rows < nb_pad)
+    const int e_n = kxe * LEAF;
+    const int nn = (e_n + 31) / 32;                         // near blocks: two 16-token runs each
+    const int nblk = nf + nn;
+    const float qs = __fmul_rn(scale, LOG2E);
+    // staging registers of one block: this thread's chunks of the QK and PV regions and a scale
+    u32x4 rq[NC], rp[NC];
+    float rsc = 0.0f;
+    auto run_pos = [&](int j) { return j < e_n ? j : 0; };  // past the list: its start again (masked)
+    auto load = [&](int bi) {
+        if (bi < nf) {                                      // 32 consecutive state rows of the group
+            const int64_t r0 = gs * nb_pad + 32 * bi;
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const int c = threadIdx.x + NT * j, r = c >> 4, cc = c & 15;
+                const int64_t sr = r0 + r;
+                if constexpr (FP8) {
+                    const u32x2 a = *(const u32x2*)((const uint8_t*)g + sr * D + 8 * cc);
+                    const u32x2 b = *(const u32x2*)((const uint8_t*)vb + sr * D + 8 * cc);
+                    rq[j] = u32x4{a.x, a.y, 0u, 0u};
+                    rp[j] = u32x4{b.x, b.y, 0u, 0u};
+                } else {
+                    rq[j] = *(const u32x4*)((const uint16_t*)g + sr * D + 8 * cc);
+                    rp[j] = *(const u32x4*)((const uint16_t*)vb + sr * D + 8 * cc);
+                }
+            }
+            const int s = threadIdx.x;
+            if (s < 32) rsc = lz[r0 + s];
+            else if (FP8 && s < 64) rsc = sg[r0 + s - 32];
+            else if (FP8 && s < 96) rsc = sv[r0 + s - 64];
+        } else {                                            // near tokens: runs at 32 b and 32 b + 16
+            const int e0 = 32 * (bi - nf), ja = run_pos(e0), jb = run_pos(e0 + 16);
+            const int64_t ra = kh + (int64_t)sidx[ja / LEAF] * LEAF + (ja % LEAF);
+            const int64_t rb = kh + (int64_t)sidx[jb / LEAF] * LEAF + (jb % LEAF);
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const int c = threadIdx.x + NT * j, r = c >> 4, cc = c & 15;
+                const int64_t sr = r < 16 ? ra + r : rb + (r - 16);
+                rq[j] = *(const u32x4*)(k + sr * D + 8 * cc);
+                rp[j] = *(const u32x4*)(v + sr * D + 8 * cc);
+            }
+        }
+    };
+    auto store = [&](int bi, char* slot) {
+        const bool far8 = FP8 && bi < nf;                   // fp8 codes widened to fp16 here
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = threadIdx.x + NT * j, r = c >> 4, cc = c & 15;
+            const int off = r * 256 + 16 * (cc ^ swz(r));
+            *(u32x4*)(slot + off) = far8 ? e4m3x8_to_h8(u32x2{rq[j].x, rq[j].y}) : rq[j];
+            *(u32x4*)(slot + R16_ROWS + off) = far8 ? e4m3x8_to_h8(u32x2{rp[j].x, rp[j].y}) : rp[j];
+        }
+        if (bi < nf && threadIdx.x < (FP8 ? 96 : 32)) *(float*)(slot + 2 * R16_ROWS + 4 * threadIdx.x) = rsc;
+    };
+    RowsN<1> st;
+    for (int pass = 0; pass < MAX_PASSES; ++pass) {
+        st.m[0] = mref;
+        st.l[0] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) st.o[0][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        load(0);
+        store(0, &ring[0][0]);
+        __syncthreads();
+        for (int bi = 0; bi < nblk; ++bi) {
+            if (bi + 1 < nblk) load(bi + 1);                // in flight while block bi is computed
+            const char* slot = &ring[bi & 1][0];
+            float u[8];
+            if (bi < nf) {                                  // ---- far: 32 leaves c0 ..
+                const int c0 = 32 * bi;
+                const uint32_t exw = exbits[c0 >> 5] >> (4 * grp);
+                float pscale[8];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int r = 16 * hh + col;
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) {
+                        const u32x4 A = *(const u32x4*)(slot + r * 256 + 16 * ((4 * ks + grp) ^ swz(r)));
+                        if constexpr (FP8) acc = mfma_f16(A, bdq[ks], acc);
+                        else acc = mfma_bf16(as_bf16x8(A), as_bf16x8(bdq[ks]), acc);
+                    }
+                    const float* scl = (const float*)(slot + 2 * R16_ROWS);
+                    const f32x4 lzv = *(const f32x4*)(scl + 16 * hh + 4 * grp);
+                    const f32x4 sgv = FP8 ? *(const f32x4*)(scl + 32 + 16 * hh + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
+                    const f32x4 svv = FP8 ? *(const f32x4*)(scl + 64 + 16 * hh + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const bool ex = (exw >> (16 * hh + i)) & 1u;
+                        const float dot = FP8 ? __fmul_rn(acc[i], __fmul_rn(sgv[i], 256.0f)) : acc[i];
+                        u[4 * hh + i] = ex ? -INFINITY : __fmaf_rn(__fadd_rn(dot, lzv[i]), LOG2E, -st.m[0]);
+                        pscale[4 * hh + i] = __fmul_rn(svv[i], 256.0f);
+                    }
+                }
+                u32x2 pvop[8][2];
+#pragma unroll
+                for (int db = 0; db < 8; ++db)
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + R16_ROWS, 16 * hf, db, lane);
+                if constexpr (FP8) rows_update_f16(st, u, pscale, pvop);
+                else {
+                    const float (&uu)[1][8] = *reinterpret_cast<const float (*)[1][8]>(&u);
+                    rows_update<1, true>(st, uu, pvop);
+                }
+            } else {                                        // ---- near: 32 tokens
+                const int e0 = 32 * (bi - nf);
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int r = 16 * hh + col;
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) {
+                        const u32x4 A = *(const u32x4*)(slot + r * 256 + 16 * ((4 * ks + grp) ^ swz(r)));
+                        acc = mfma_bf16(as_bf16x8(A), as_bf16x8(bq[ks]), acc);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const bool ok = (e0 + 16 * hh + 4 * grp + i) < e_n;
+                        u[4 * hh + i] = ok ? __fmaf_rn(acc[i], qs, -st.m[0]) : -INFINITY;
+                    }
+                }
+                u32x2 pvop[8][2];
+#pragma unroll
+                for (int db = 0; db < 8; ++db)
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + R16_ROWS, 16 * hf, db, lane);
+                const float (&uu)[1][8] = *reinterpret_cast<const float (*)[1][8]>(&u);
+                rows_update<1, true>(st, uu, pvop);
+            }
+            if (bi + 1 < nblk) store(bi + 1, &ring[(bi + 1) & 1][0]);
+            __syncthreads();                                // block bi + 1 staged; slot bi free
+        }
+        // row totals: outside [2^-60, 2^64] the reference missed the row's maximum by more than 60
+        // octaves: the pass is redone with the reference moved to m + log2(total)
+        const float lt = grp_sum(st.l[0]);
+        if (grp == 0) red_l[16 * wv + col] = lt;
+        if (threadIdx.x == 0) redo = 0;
+        __syncthreads();
+        // (2^-8 with the fp8 store: its far-field P is fp16, whose subnormals would hold the far
+        // leaves of a row whose total is that small with too few bits)
+        const float tot = red_l[16 * wv + col];
+        if (!(tot >= (FP8 ? 0x1p-8f : 0x1p-60f) && tot <= 0x1p64f)) {
+            mref = tot > 0.0f && tot <= 3.0e38f ? __fadd_rn(mref, __log2f(tot))
+                                                : __fadd_rn(mref, tot == 0.0f ? -120.0f : 120.0f);
+            redo = 1;
+        }
+        __syncthreads();
+        if (redo == 0 || pass + 1 == MAX_PASSES) break;
+    }
+    const int r = 16 * wv + col;
+    const float den = red_l[r];
+    const float inv = 1.0f / (den < 1e-30f ? 1e-30f : den);
+    const int64_t qi = (int64_t)t * TR + r;
+    if (qi < nq) {
+        const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            const f32x4 o = st.o[0][db];
+            *(f32x4*)(out + orow * D + 16 * db + 4 * grp) =
+                f32x4{__fmul_rn(o[0], inv), __fmul_rn(o[1], inv), __fmul_rn(o[2], inv), __fmul_rn(o[3], inv)};
+        }
+        if (grp == 0) logz[orow] = __fadd_rn(__fmul_rn(st.m[0], LN2), __logf(den));   // m in log2 units
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // tail: keys past the last full leaf, attended exactly by every query, merged into a finished
 // (out, logz).  The reference folds up to 16 such keys into the last split of its tile kernel
 // with q, k, v and p rounded to bf16 (h3/htrc_flat_triton.py:187-207) and takes a host-side fp32
@@ -2840,6 +3178,104 @@ int htrc_route(const int8_t* q8, const float* sq, const int8_t* dq8, const float
     if (rc != HTRC_OK) return rc;
     return htrc_route_attend(q8, sq, dq8, sdq, g8, sg, lz, vb, k8, ks, v, idx, rowmax, heads, nq, nk, leaf, d, kx,
                              tile, group, g0, gn, perm, scale, out, logz, stream);
+}
+
+// Shared checks of the 16-bit fused route: route_shapes plus the LDS-held top-k keys.
+static int route16_shapes(const char* who, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int tile,
+                          int group, int64_t g0, int64_t gn, int64_t& nb, int64_t& nt, int64_t& ng, int64_t& tb,
+                          int64_t& ntw, int& kxe) {
+    const int rc = route_shapes(who, heads, nq, nk, leaf, d, kx, tile, group, g0, gn, nb, nt, ng, tb, ntw, kxe);
+    if (rc != HTRC_OK) return rc;
+    if (nb > ROUTE_NB_LDS) {
+        static thread_local char msg[160];
+        snprintf(msg, sizeof msg, "%s: at most 16384 leaves per head (the split tile path takes more)", who);
+        return fail(HTRC_ERR_ARG, msg);
+    }
+    return HTRC_OK;
+}
+
+int htrc_route16_select(const uint16_t* dq16, const void* g, const float* sg, const float* lz, int64_t heads,
+                        int64_t nq, int64_t nk, int leaf, int d, int kx, int sink, int stride, int tile, int group,
+                        int64_t g0, int64_t gn, int fp8, int32_t* idx, float* rowmax, void* stream) {
+    REQUIRE(dq16 && g && lz && rowmax && (!fp8 || sg), "htrc_route16_select: null pointer");
+    REQUIRE(aligned(dq16, 16) && aligned(g, 16) && aligned(lz, 16) && (!fp8 || aligned(sg, 16)),
+            "htrc_route16_select: misaligned buffer");
+    int64_t nb, nt, ng, tb, ntw;
+    int kxe;
+    const int rc = route16_shapes("htrc_route16_select", heads, nq, nk, leaf, d, kx, tile, group, g0, gn, nb, nt, ng,
+                                  tb, ntw, kxe);
+    if (rc != HTRC_OK) return rc;
+    REQUIRE(sink >= 0, "htrc_route16_select: need sink >= 0");
+    REQUIRE(kxe == 0 || idx, "htrc_route16_select: idx is required when kx > 0");
+    REQUIRE(stride >= 1 && stride <= tile && tile % stride == 0, "htrc_route16_select: stride must divide the tile");
+    const int nbp = htrc_nb_pad(nb);
+#define RSEL16(F, N)                                                                                             \
+    hipLaunchKernelGGL((route_select16_kernel<F, N>), dim3((unsigned)(gn * heads)), dim3(256), (size_t)4 * nbp,   \
+                       (hipStream_t)stream, dq16, g, sg, lz, (int)nt, group, (int)g0, (int)gn, (int)nb, nbp, kxe, sink, \
+                       stride, idx, rowmax)
+    if (tile == 64) {
+        if (fp8) RSEL16(true, 4); else RSEL16(false, 4);
+    } else {
+        if (fp8) RSEL16(true, 2); else RSEL16(false, 2);
+    }
+#undef RSEL16
+    return launched("htrc_route16_select");
+}
+
+int htrc_route16_attend(const uint16_t* q16, const uint16_t* dq16, const void* g, const float* sg, const float* lz,
+                        const void* vb, const float* sv, const uint16_t* k, const uint16_t* v, const int32_t* idx,
+                        const float* rowmax, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int tile,
+                        int group, int64_t g0, int64_t gn, const int32_t* perm, int fp8, float scale, float* out,
+                        float* logz, void* stream) {
+    REQUIRE(q16 && dq16 && g && lz && vb && k && v && rowmax && out && logz && (!fp8 || (sg && sv)),
+            "htrc_route16_attend: null pointer");
+    REQUIRE(aligned(q16, 16) && aligned(dq16, 16) && aligned(g, 16) && aligned(vb, 16) && aligned(k, 16) &&
+                aligned(v, 16) && aligned(lz, 16) && aligned(out, 16) && (!fp8 || (aligned(sg, 16) && aligned(sv, 16))),
+            "htrc_route16_attend: misaligned buffer");
+    int64_t nb, nt, ng, tb, ntw;
+    int kxe;
+    const int rc = route16_shapes("htrc_route16_attend", heads, nq, nk, leaf, d, kx, tile, group, g0, gn, nb, nt, ng,
+                                  tb, ntw, kxe);
+    if (rc != HTRC_OK) return rc;
+    REQUIRE(kxe == 0 || idx, "htrc_route16_attend: idx is required when kx > 0");
+    const int nbp = htrc_nb_pad(nb);
+    const size_t dyn = route_dyn_bytes(nb, kxe);
+    const size_t stat = (size_t)2 * R16_SLOT + 64 * 4 + 16;
+    REQUIRE(stat + dyn <= ROUTE_LDS_MAX, "htrc_route16_attend: near list and exclusion bits exceed the LDS");
+    const dim3 grid((unsigned)(ntw * heads));
+    hipStream_t s = (hipStream_t)stream;
+#define R16_LAUNCH(L, F, NW)                                                                                      \
+    hipLaunchKernelGGL((route16_kernel<L, F, NW>), grid, dim3(64 * NW), dyn, s, q16, dq16, g, sg, lz, vb, sv, k, v, idx, \
+                       rowmax, nq, (int)nt, group, (int)g0, (int)gn, perm, nk, (int)nb, nbp, kxe, scale, out, logz)
+#define R16_CASE(L)                                                                                               \
+    case L:                                                                                                       \
+        if (tile == 64) {                                                                                         \
+            if (fp8) R16_LAUNCH(L, true, 4); else R16_LAUNCH(L, false, 4);                                        \
+        } else {                                                                                                  \
+            if (fp8) R16_LAUNCH(L, true, 2); else R16_LAUNCH(L, false, 2);                                        \
+        }                                                                                                         \
+        break;
+    switch (leaf) {
+        R16_CASE(16)
+        R16_CASE(32)
+        R16_CASE(64)
+        R16_CASE(128)
+    }
+#undef R16_CASE
+#undef R16_LAUNCH
+    return launched("htrc_route16_attend");
+}
+
+int htrc_route16(const uint16_t* q16, const uint16_t* dq16, const void* g, const float* sg, const float* lz,
+                 const void* vb, const float* sv, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nq,
+                 int64_t nk, int leaf, int d, int kx, int sink, int stride, int tile, int group, int64_t g0, int64_t gn,
+                 const int32_t* perm, int fp8, float scale, float* out, float* logz, int32_t* idx, float* rowmax,
+                 void* stream) {
+    int rc = htrc_route16_select(dq16, g, sg, lz, heads, nq, nk, leaf, d, kx, sink, stride, tile, group, g0, gn, fp8,
+                                 idx, rowmax, stream);
+    if (rc != HTRC_OK) return rc;
+    return htrc_route16_attend(q16, dq16, g, sg, lz, vb, sv, k, v, idx, rowmax, heads, nq, nk, leaf, d, kx, tile, group,
+                               g0, gn, perm, fp8, scale, out, logz, stream);
 }
 
 // Device address of `scratch` on the current device, resolved once per device (with that device

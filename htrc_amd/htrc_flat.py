@@ -132,10 +132,11 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
                    tail=None, ws=None, return_logz=False, state=None):
     """q [N,D] (or [H,N,D]), k/v [M,D] (or [H,M,D]), any float dtype -> out fp32 of q's shape
     (h3/htrc_flat.py:99-139).  ``kern['fused']`` (default True) runs select, top-k, far and
-    near field as two fused launches per window; False runs the reference's stage structure
-    (select, top-k, split tile kernel, merge) honouring ``splits`` and ``kern['tile_bn']``.
-    Shapes the fused kernels do not hold (more than 8192 near leaves per tile or 262144 leaves
-    per head) take the stage structure automatically.
+    near field as two fused launches per window, for every state store; False runs the
+    reference's stage structure (select, top-k, split tile kernel, merge) honouring ``splits``
+    and ``kern['tile_bn']``.  Shapes the fused kernels do not hold (more than 8192 near leaves
+    per tile, or more than 262144 leaves per head for store="int8" and 16384 for the 16-bit
+    stores) take the stage structure automatically.
     ``kern['group']`` = G > 1 makes G consecutive tiles share one expansion centre (the mean
     of their rows), one leaf state and one near set (h3/htrc_flat.py:223-231).
     ``order='kmeans'`` cuts the tiles from the queries regrouped by ``kmeans_order``; the
@@ -172,7 +173,7 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         mu, q16, dq16 = hip.pack_q16(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm, dq_fp16=store == "fp8")
         packed = {"q16": q16, "dq16": dq16, "mu": mu}
         sdt = torch.float8_e4m3fn if store == "fp8" else torch.bfloat16
-        fused = False
+        fused = bool(kern.get("fused", True)) and hip.route16_fits(nb, kx)
     else:
         mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm)
         packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "mu": mu}
@@ -196,8 +197,9 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         sel = excl = idx = None
         if fused:
             idx = hip._rows(ws, "idx", h, gn, (kx,), torch.int32, qh.device) if kx > 0 else None
-            hip.route(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, sink=sink, stride=stride, ws=ws, out=out,
-                      logz=logz, idx=idx, group=group, perm=perm, tile=tile, g0=g0)
+            fn = hip.route if sdt == torch.int8 else hip.route16
+            fn(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, sink=sink, stride=stride, ws=ws, out=out,
+               logz=logz, idx=idx, group=group, perm=perm, tile=tile, g0=g0)
             tick("tile")
         else:
             if kx > 0:

@@ -418,6 +418,39 @@ def route_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, 
     return out, logz
 
 
+def route16(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: float, sink: int = 0, stride: int = 1,
+            ws=None, out=None, logz=None, idx=None, group: int = 1, perm=None, tile: int = TILE, g0: int = 0):
+    """Fused route of the 16-bit state stores (select -> top-k, then far + near in one softmax; two
+    launches) for the tiles of the gn = state["lz"].shape[1] groups from g0: packed holds q16,
+    dq16 (pack_q16) and the bf16 k, v; state g8 / vb (e4m3 with sg, sv; or bf16) and lz
+    -> (out [H,nq,D], logz [H,nq]); idx [H,gn,min(kx,nb)] receives the window's routing."""
+    q16, dq16, k, v = packed["q16"], packed["dq16"], packed["k"], packed["v"]
+    g, sg, lz, vb, sv = state["g8"], state.get("sg"), state["lz"], state["vb"], state.get("sv")
+    fp8 = g.dtype == torch.float8_e4m3fn
+    h, nk, d = (int(x) for x in k.shape)
+    dev = q16.device
+    tile = _tile(tile)
+    nt = -(-int(nq) // tile)
+    g0, gn, _, _ = _tile_window(nq, tile, group, g0, int(lz.shape[1]))
+    kxe = min(int(kx), nk // int(leaf))
+    if out is None:
+        out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
+    if logz is None:
+        logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
+    if idx is None and kxe > 0:
+        idx = _rows(ws, "idx", h, gn, (kxe,), torch.int32, dev)
+    rowmax = _buf(ws, "rowmax", (h, nt * tile), torch.float32, dev)
+    call("htrc_route16", ptr(q16), ptr(dq16), ptr(g), ptr(sg), ptr(lz), ptr(vb), ptr(sv), ptr(k), ptr(v), h, nq, nk,
+         int(leaf), d, int(kx), int(sink), int(stride), tile, int(group), g0, gn, ptr(perm), int(fp8), float(scale),
+         ptr(out), ptr(logz), ptr(idx), ptr(rowmax), stream_handle(dev))
+    return out, logz
+
+
+def route16_fits(nb: int, kx: int) -> bool:
+    """Whether the fused 16-bit route takes this shape (else the split tile path runs it)."""
+    return int(nb) <= ROUTE_NB_LDS and min(int(kx), int(nb)) <= ROUTE_MAX_KX
+
+
 def tail_merge(q, tk, tv, *, scale: float, out, logz):
     """Tail keys tk, tv [H, n, D] (past the last full leaf) attended exactly by every query and
     merged in place into out [H, nq, D] / logz [H, nq] (h3/htrc_flat_triton.py:187-207, 381-388)."""

@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 12
+#define HTRC_ABI_VERSION 13
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -202,6 +202,32 @@ int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g,
                    int64_t nq, int64_t nk, int leaf, int d, int kx, int tile, int group, int64_t g0, int64_t gn,
                    const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out,
                    float* logz, void* stream);
+
+/* Fused production path of the 16-bit state stores (fp8 = 1: store="fp8", g / vb e4m3 codes with
+ * row scales sg / sv; fp8 = 0: store="bf16", g / vb bf16, sg / sv unused), for the groups
+ * [g0, g0 + gn): q16 / dq16 from htrc_pack_q16 (dq fp16 for fp8, bf16 for bf16), k / v bf16.
+ * First launch (htrc_route16_select): SEL with the arithmetic of htrc_select_fp8 /
+ * htrc_select_bf16 (bit-exact) kept in LDS, its kx largest (leaves < sink forced in) into idx
+ * [H, gn, min(kx, nb)] ascending, and rowmax fp32 [H, nt*T], each row's largest far-field score.
+ * Second launch (htrc_route16_attend): far + near field of every tile in one softmax whose
+ * reference is rowmax, normalised into out / logz -- the products of htrc_tile_fp8 /
+ * htrc_tile_bf16.  At most 16384 leaves and 8192 near leaves per head (the split tile path takes
+ * more).  Replace rowmax_select + torch.topk + tile_attention of the chunk loop for
+ * store=float8_e4m3fn / bfloat16 (h3/htrc_flat.py:250-271; h3/htrc_flat_triton.py:65-72,
+ * 132-184, 214-254). */
+int htrc_route16_select(const uint16_t* dq16, const void* g, const float* sg, const float* lz, int64_t heads,
+                        int64_t nq, int64_t nk, int leaf, int d, int kx, int sink, int stride, int tile, int group,
+                        int64_t g0, int64_t gn, int fp8, int32_t* idx, float* rowmax, void* stream);
+int htrc_route16_attend(const uint16_t* q16, const uint16_t* dq16, const void* g, const float* sg, const float* lz,
+                        const void* vb, const float* sv, const uint16_t* k, const uint16_t* v, const int32_t* idx,
+                        const float* rowmax, int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int tile,
+                        int group, int64_t g0, int64_t gn, const int32_t* perm, int fp8, float scale, float* out,
+                        float* logz, void* stream);
+int htrc_route16(const uint16_t* q16, const uint16_t* dq16, const void* g, const float* sg, const float* lz,
+                 const void* vb, const float* sv, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nq,
+                 int64_t nk, int leaf, int d, int kx, int sink, int stride, int tile, int group, int64_t g0, int64_t gn,
+                 const int32_t* perm, int fp8, float scale, float* out, float* logz, int32_t* idx, float* rowmax,
+                 void* stream);
 
 /* k-means query order: perm int32 [H, nq], the queries ordered by their nearest of `clusters`
  * centres (stable), the centres from `iters` Lloyd steps on `sample` evenly spaced queries.

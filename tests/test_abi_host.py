@@ -46,7 +46,7 @@ _FAKE = ctypes.c_void_p(256)   # never dereferenced: validation fails before any
 
 
 @pytest.mark.parametrize("case", ["null", "dim", "leaf", "block", "leaves", "near", "group", "tile", "stride",
-                                  "window", "centres", "keys_ws", "merge"])
+                                  "window", "centres", "keys_ws", "merge", "route16_leaves", "route16_null"])
 def test_launchers_reject_bad_arguments_on_host(case):
     lib = _lib.lib()
     f = _FAKE
@@ -88,6 +88,14 @@ def test_launchers_reject_bad_arguments_on_host(case):
     elif case == "keys_ws":                       # above 16384 leaves per head the top-k keys need keys_ws
         rc = lib.htrc_route_select(*([f] * 5), 1, 640, 16 * 20000, 16, 128, 4, 0, 1, 64, 1, 0, 10, f, f, None, None)
         msg = "keys_ws"
+    elif case == "route16_leaves":                # the 16-bit route keeps its top-k keys in LDS
+        rc = lib.htrc_route16(*([f] * 9), 1, 640, 16 * 20000, 16, 128, 4, 0, 1, 64, 1, 0, 10, None, 1, 0.1, f, f, f,
+                              f, None)
+        msg = "16384"
+    elif case == "route16_null":                  # the fp8 store needs its row scales
+        rc = lib.htrc_route16(f, f, f, None, f, f, None, f, f, 1, 640, 640, 64, 128, 4, 0, 1, 64, 1, 0, 10, None, 1,
+                              0.1, f, f, f, f, None)
+        msg = "null"
     else:                                         # tiles [8, 12) of a head of 10
         rc = lib.htrc_merge(f, f, f, 1, 640, 64, 8, 4, 4, 128, None, f, f, None)
         msg = "window"
@@ -102,6 +110,7 @@ def test_header_signatures_parse():
     assert sig["htrc_x"][0] == [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_void_p]
     assert sig["htrc_y"] == ([], ctypes.c_char_p)
     assert len(_lib.signatures()["htrc_route"][0]) == 31
+    assert len(_lib.signatures()["htrc_route16"][0]) == 29
 
 
 def test_call_maps_errors_to_value_error():

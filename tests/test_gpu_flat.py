@@ -199,48 +199,56 @@ def test_kmeans_order_vs_oracle(device, fused, n, group):
     check_logz(logz.cpu().numpy(), ref, st, LOGZ_ABS)
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("n,leaf,ex,group", [(8192, 64, 16, 1), (3000, 32, 8, 2)])
-def test_fp8_store_vs_oracle(device, n, leaf, ex, group):
+def test_fp8_store_vs_oracle(device, fused, n, leaf, ex, group):
     """store="fp8" (h3/htrc_flat_triton.py:65-72 with FP8 = 1): e4m3 leaf state, fp16 far dots,
-    bf16 near dots, in the reference's stage structure; routing and output as above."""
+    bf16 near dots, on the fused route and in the reference's stage structure; routing and
+    output as above."""
     nk = (n // leaf) * leaf
     q, k, v = workloads.clustered_runs(n=n, runs=max(1, n // 64), heads=1, seed=n + leaf + 5)
     k, v = k[:, :nk].contiguous(), v[:, :nk].contiguous()
     st = {}
     out, logz = htrc_flat.flat_attention(q[0].to(device), k[0].to(device), v[0].to(device), backend="hip",
                                          store="fp8", dot="bf16", leaf=leaf, exact_leaves=ex, splits=4,
-                                         kern={"tile_bn": 64, "group": group}, return_logz=True, state=st)
+                                         kern={"tile_bn": 64, "group": group, "fused": fused}, return_logz=True,
+                                         state=st)
     torch.cuda.synchronize()
     ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=ex, splits=4, bn=64,
                           group=group, store="fp8")
     assert np.array_equal(st["dq16"][0].view(torch.int16).cpu().numpy().view(np.uint16), ref["dq16"])
-    _routing_check(st, ref, f"16-bit store n={n} leaf={leaf} G={group}")
+    assert (st.get("sel") is None) == fused
+    _routing_check(st, ref, f"fp8 store fused={fused} n={n} leaf={leaf} G={group}")
     assert rel_l2(out.cpu().numpy(), ref["out"]) <= OUT_REL_L2
     assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("n,leaf,ex,group", [(8192, 64, 16, 1), (3000, 32, 8, 2)])
-def test_bf16_store_vs_oracle(device, n, leaf, ex, group):
+def test_bf16_store_vs_oracle(device, fused, n, leaf, ex, group):
     """store="bf16" (the 16-bit state of h3/htrc_flat_triton.py:132-153, 214-254 with FP8 = 0):
-    bf16 leaf state, bf16 far and near dots, in the reference's stage structure."""
+    bf16 leaf state, bf16 far and near dots, on the fused route and in the reference's stage
+    structure."""
     nk = (n // leaf) * leaf
     q, k, v = workloads.clustered_runs(n=n, runs=max(1, n // 64), heads=1, seed=n + leaf + 7)
     k, v = k[:, :nk].contiguous(), v[:, :nk].contiguous()
     st = {}
     out, logz = htrc_flat.flat_attention(q[0].to(device), k[0].to(device), v[0].to(device), backend="hip",
                                          store="bf16", dot="bf16", leaf=leaf, exact_leaves=ex, splits=4,
-                                         kern={"tile_bn": 64, "group": group}, return_logz=True, state=st)
+                                         kern={"tile_bn": 64, "group": group, "fused": fused}, return_logz=True,
+                                         state=st)
     torch.cuda.synchronize()
     ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=ex, splits=4, bn=64,
                           group=group, store="bf16")
     assert np.array_equal(st["dq16"][0].view(torch.int16).cpu().numpy().view(np.uint16), ref["dq16"])
-    _routing_check(st, ref, f"16-bit store n={n} leaf={leaf} G={group}")
+    assert (st.get("sel") is None) == fused
+    _routing_check(st, ref, f"bf16 store fused={fused} n={n} leaf={leaf} G={group}")
     assert rel_l2(out.cpu().numpy(), ref["out"]) <= OUT_REL_L2
     assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
 
 
 @pytest.mark.parametrize("store,fused,order", [("int8", True, "seq"), ("int8", False, "seq"), ("int8", True, "kmeans"),
-                                               ("fp8", False, "seq")])
+                                               ("fp8", False, "seq"), ("fp8", True, "seq"), ("bf16", True, "kmeans")])
 def test_tile32_vs_oracle(device, store, fused, order):
     """tile=32 (the runner's mode "max", h3/htrc_flat_runner.py:52) end to end: 32-row tiles,
     each with its own centre, state and near set; routing and output as above."""

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bits, from_bits, rel_l2
+from helpers import bits, from_bits, rel_l2, routing_report, sel_error
 from htrc_amd import htrc_flat_hip as hip
 from htrc_amd import workloads
 from htrc_amd._lib import nb_pad
@@ -638,3 +638,50 @@ def test_select_and_tile16_tile32_on_oracle_state(device, store):
         np.testing.assert_allclose(_np(sel[0])[:, :nb], ref["sel"], rtol=2e-5, atol=2e-5)
         assert rel_l2(_np(out[0]), ref["out"]) <= OUT_REL_L2
         assert np.abs(_np(logz[0]) - ref["logz"]).max() <= LOGZ_ABS
+
+
+# ---- fused route of the 16-bit state stores (store="fp8" / "bf16"): route_select16 + route16
+
+@pytest.mark.parametrize("store", ["fp8", "bf16"])
+@pytest.mark.parametrize("tile,leaf,ex,group,stride,heads", [
+    (64, 64, 6, 1, 1, 1), (64, 64, 6, 2, 4, 1), (64, 32, 16, 1, 1, 2), (64, 128, 3, 1, 1, 1),
+    (64, 64, 0, 1, 1, 1), (64, 64, 24, 1, 1, 1), (32, 64, 6, 1, 1, 3), (32, 16, 40, 1, 2, 1),
+    (32, 64, 6, 3, 1, 1)])
+def test_route16_on_oracle_state(device, store, tile, leaf, ex, group, stride, heads):
+    """The oracle's 16-bit leaf state through the fused route: the near sets are exactly those of
+    the stage select + top-k on the same state (route_select16 uses select16's arithmetic), and
+    against the oracle's they differ only at SEL near-ties; outputs within the operator bar on
+    every tile whose near set is the oracle's; replicated heads give identical results.  ex = 24
+    near leaves of 24 leave an empty far field, ex = 0 an empty near field."""
+    n = tile * 41 + 5
+    q, k, v = _data(n, nk=64 * 24, seed=tile + leaf + ex + group)
+    scale = 1 / math.sqrt(128)
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=tile, leaf=leaf, exact_leaves=ex, splits=1,
+                          bn=64, sel_stride=stride, group=group, store=store)
+    packed, state, _, _ = (_fp8_state if store == "fp8" else _bf16_state)(ref, k, v, device)
+    rep = lambda t: t.repeat(heads, *([1] * (t.dim() - 1))).contiguous()  # noqa: E731
+    packed = {name: rep(t) for name, t in packed.items()}
+    state = {name: (None if t is None else rep(t)) for name, t in state.items()}
+    ng, nb = (ref["g8"] if store == "fp8" else ref["g16"]).shape[:2]
+    kx = min(ex, nb)
+    idx = torch.full((heads, ng, max(kx, 1)), -1, dtype=torch.int32, device=device)
+    out, logz = hip.route16(packed, state, nq=n, leaf=leaf, kx=kx, scale=scale, stride=stride, group=group,
+                            tile=tile, idx=idx if kx else None)
+    sel = hip.rowmax_select(g=state["g8"], lz=state["lz"], sg=state["sg"], stride=stride, nb=nb,
+                            dq8=packed["dq16"], group=group, tile=tile)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(logz).all())
+    for h in range(1, heads):
+        assert torch.equal(out[h], out[0]) and torch.equal(logz[h], logz[0]), f"head {h}"
+    rows_ok = np.ones(n, bool)
+    if kx:
+        sidx, _ = hip.topk_excl(sel, nb, kx)
+        torch.cuda.synchronize()
+        assert torch.equal(idx, sidx)
+        rp = routing_report(_np(idx[0]), ref["idx"], ref["sel"], sel_error(_np(sel[0]), ref["sel"], nb))
+        for gi in range(ng):
+            if not np.array_equal(_np(idx[0, gi]), ref["idx"][gi]):
+                rows_ok[gi * tile * group:(gi + 1) * tile * group] = False
+        assert rp["mismatched"] <= rp["tieable"] and rows_ok.mean() > 0.8
+    assert rel_l2(_np(out[0])[rows_ok], ref["out"][rows_ok]) <= OUT_REL_L2
+    assert np.abs(_np(logz[0])[rows_ok] - ref["logz"][rows_ok]).max() <= LOGZ_ABS

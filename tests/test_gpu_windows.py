@@ -44,8 +44,8 @@ def _kw(**over):
 
 def _gpu_sel(st, nb, group, tile, stride=1):
     """SEL from the GPU's own state (the route select computes exactly this, bit for bit)."""
-    sel = hip.rowmax_select(g=st["g8"], lz=st["lz"], sg=st["sg"], stride=stride, nb=nb, dq8=st["dq8"],
-                            sdq=st["sdq"], group=group, tile=tile)
+    sel = hip.rowmax_select(g=st["g8"], lz=st["lz"], sg=st.get("sg"), stride=stride, nb=nb,
+                            dq8=st.get("dq8", st.get("dq16")), sdq=st.get("sdq"), group=group, tile=tile)
     return sel.cpu().numpy()
 
 
@@ -58,14 +58,15 @@ def _check_routing(idx_gpu, ref, sel_gpu, nb, sink):
     return routing_report(idx_gpu[:, sink:] - sink, ref["idx"][:, sink:] - sink, osel, delta)
 
 
-@pytest.mark.parametrize("fused,group,tile,order", [(True, 1, 64, "seq"), (False, 1, 64, "seq"),
-                                                    (True, 3, 64, "seq"), (False, 2, 32, "seq"),
-                                                    (True, 1, 32, "kmeans"), (True, 2, 64, "kmeans")])
-def test_windows_bit_identical(device, fused, group, tile, order):
+@pytest.mark.parametrize("fused,group,tile,order,store", [
+    (True, 1, 64, "seq", "int8"), (False, 1, 64, "seq", "int8"), (True, 3, 64, "seq", "int8"),
+    (False, 2, 32, "seq", "int8"), (True, 1, 32, "kmeans", "int8"), (True, 2, 64, "kmeans", "int8"),
+    (True, 2, 64, "seq", "fp8"), (False, 1, 64, "seq", "fp8"), (True, 1, 32, "kmeans", "bf16")])
+def test_windows_bit_identical(device, fused, group, tile, order, store):
     n, leaf, ex = 4096, 64, 8
     q, k, v = workloads.clustered_runs(n=n, runs=n // 64, heads=2, seed=5 + group + tile)
     q, k, v = q.to(device), k.to(device), v.to(device)
-    kw = _kw(leaf=leaf, exact_leaves=ex, tile=tile, order=order, sink_leaves=2,
+    kw = _kw(leaf=leaf, exact_leaves=ex, tile=tile, order=order, sink_leaves=2, store=store,
              kern={"fused": fused, "group": group})
     st1 = {}
     one, lz1 = htrc_flat.flat_attention(q, k, v, tile_chunk=4096, return_logz=True, state=st1, **kw)
@@ -80,17 +81,18 @@ def test_windows_bit_identical(device, fused, group, tile, order):
         assert torch.equal(st["lz"], st1["lz"]) and torch.equal(st["g8"], st1["g8"])
 
 
-@pytest.mark.parametrize("fused,group", [(True, 1), (False, 1), (True, 2), (False, 3)])
-def test_sink_leaves_vs_oracle(device, fused, group):
+@pytest.mark.parametrize("fused,group,store", [(True, 1, "int8"), (False, 1, "int8"), (True, 2, "int8"),
+                                              (False, 3, "int8"), (True, 2, "fp8"), (True, 1, "bf16")])
+def test_sink_leaves_vs_oracle(device, fused, group, store):
     n, leaf, ex, sink = 4096, 32, 8, 5
     q, k, v = workloads.clustered_runs(n=n, runs=n // 64, heads=1, seed=77 + group)
     st = {}
     out, logz = htrc_flat.flat_attention(q[0].to(device), k[0].to(device), v[0].to(device), leaf=leaf,
                                          exact_leaves=ex, sink_leaves=sink, return_logz=True, state=st,
-                                         **_kw(kern={"fused": fused, "group": group}))
+                                         **_kw(store=store, kern={"fused": fused, "group": group}))
     torch.cuda.synchronize()
     ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=ex, sink_leaves=sink,
-                          splits=1 if fused else 4, bn=64, group=group)
+                          splits=1 if fused else 4, bn=64, group=group, store=store)
     nb = n // leaf
     assert st["kx"] == ex + sink
     rep = _check_routing(st["idx"][0].cpu().numpy(), ref, _gpu_sel(st, nb, group, 64)[0], nb, sink)
@@ -169,12 +171,13 @@ def test_many_leaves_vs_oracle(device, fused):
     assert np.abs(logz[r_t].cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
 
 
-@pytest.mark.parametrize("heads", [1, 6, 8])
-def test_reference_max_retry(device, heads):
+@pytest.mark.parametrize("heads,store", [(1, "int8"), (6, "int8"), (8, "int8"), (1, "fp8"), (2, "bf16")])
+def test_reference_max_retry(device, heads, store):
     """Row 5 of tile 0 is 30 e_0 and key 3 of leaf 0 (a sink, so always near) is 30 e_0: its exact
     score 900 / sqrt(128) ~ 80 nats sits ~75 nats above the row's far-field maximum, the row total
     at the fixed reference leaves [2^-60, 2^64] and the tile is redone with the reference moved.
-    1, 6 and 8 heads of 64 tiles take the attend kernel's four-, two- and one-pair shapes."""
+    1, 6 and 8 heads of 64 tiles take the attend kernel's four-, two- and one-pair shapes; the
+    16-bit stores take their own fused route."""
     n, leaf, ex = 4096, 64, 4
     q, k, v = workloads.clustered_runs(n=n, runs=n // 64, heads=heads, seed=31)
     q = (q.float() * 0.3).to(torch.bfloat16)
@@ -184,12 +187,12 @@ def test_reference_max_retry(device, heads):
     k[:, 3] = 0
     k[:, 3, 0] = 30
     out, logz = htrc_flat.flat_attention(q.to(device), k.to(device), v.to(device), leaf=leaf, exact_leaves=ex,
-                                         sink_leaves=1, return_logz=True, **KW)
+                                         sink_leaves=1, return_logz=True, **_kw(store=store))
     torch.cuda.synchronize()
     assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(logz).all())
     h = heads - 1
     ref = flat_i8.flat_i8(bits(q[h, :256]), bits(k[h]), bits(v[h]), tile=64, leaf=leaf, exact_leaves=ex,
-                          sink_leaves=1, splits=1, bn=64)
+                          sink_leaves=1, splits=1, bn=64, store=store)
     assert ref["logz"][5] > 70.0                          # the outlier dominates row 5
     assert rel_l2(out[h, :256].cpu().numpy(), ref["out"]) <= OUT_REL_L2
     assert np.abs(logz[h, :256].cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
