@@ -222,6 +222,19 @@ __device__ __forceinline__ uint32_t e4m3x2_to_h2(uint32_t b2) {
 __device__ __forceinline__ u32x4 e4m3x8_to_h8(u32x2 b) {
     return u32x4{e4m3x2_to_h2(b.x & 0xffffu), e4m3x2_to_h2(b.x >> 16), e4m3x2_to_h2(b.y & 0xffffu), e4m3x2_to_h2(b.y >> 16)};
 }
+// The same eight values with gfx950's conversion instruction (v_cvt_scalef32_pk_f16_fp8, OCP
+// e4m3, scale 2^-8): one instruction per pair.  Every finite code converts exactly (the fp16
+// grid holds all e4m3 values times 2^-8, subnormals included); htrc_selftest_e4m3 checks all
+// 256 codes against e4m3x8_to_h8 on the device.  The state never holds the NaN codes 0x7f / 0xff.
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t e4m3x2_to_h2_cvt(uint32_t w, bool hi) {
+    return __builtin_bit_cast(uint32_t, hi ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 0x1p-8f, true)
+                                           : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 0x1p-8f, false));
+}
+__device__ __forceinline__ u32x4 e4m3x8_to_h8_cvt(u32x2 b) {
+    return u32x4{e4m3x2_to_h2_cvt(b.x, false), e4m3x2_to_h2_cvt(b.x, true), e4m3x2_to_h2_cvt(b.y, false),
+                 e4m3x2_to_h2_cvt(b.y, true)};
+}
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

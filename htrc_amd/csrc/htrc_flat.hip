@@ -2100,10 +2100,14 @@ __global__ __launch_bounds__(256, 3) void route_select16_kernel(
     if (kxe > 0) topk_row([&](int l) { return keys16[l]; }, nb, kxe, sm, idx + gs * kxe, nullptr, nullptr);
 }
 
-// One ring slot of route16_kernel: QK rows and PV rows, 32 rows of 128 16-bit values each (row r's
-// 16-byte chunk c at chunk c ^ swz(r)), then up to three 32-float scale vectors.
+// One ring slot of route16_kernel: QK rows and PV rows, 32 rows of 128 16-bit values each, then
+// three 32-float scale vectors (lz, or -inf for a leaf of the near set or past nb; sg * 256;
+// sv * 256).  PV row r keeps its 16-byte chunk c at c ^ swz(r) (the transposing reads); QK row r
+// at c ^ swq(r), so that the QK operand reads (16 rows at one chunk) hit 16 different chunks and
+// every 8 consecutive rows 8 different chunks modulo 8: no bank conflicts in 8- or 16-lane phases.
 constexpr int R16_ROWS = 32 * 256;
 constexpr int R16_SLOT = 2 * R16_ROWS + 3 * 32 * 4;
+__device__ __forceinline__ int swq(int r) { return r & 15; }
 
 // p = 2^u for the log2-domain shifted scores u[0..7] of one row block (keys 16(e/4) + 4grp + e%4),
 // l += p, O^T += V^T P^T with P = fp16(p * pscale) per key (the fp8 far field).
@@ -2178,6 +2182,16 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
     const int nn = (e_n + 31) / 32;                         // near blocks: two 16-token runs each
     const int nblk = nf + nn;
     const float qs = __fmul_rn(scale, LOG2E);
+    // this thread's chunks of a 32-row region: row rr[j], 16-byte chunk cr[j]; LDS byte offsets
+    int rr[NC], cr[NC], oq[NC], op[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int c = threadIdx.x + NT * j;
+        rr[j] = c >> 4;
+        cr[j] = c & 15;
+        oq[j] = rr[j] * 256 + 16 * (cr[j] ^ swq(rr[j]));
+        op[j] = R16_ROWS + rr[j] * 256 + 16 * (cr[j] ^ swz(rr[j]));
+    }
     // staging registers of one block: this thread's chunks of the QK and PV regions and a scale
     u32x4 rq[NC], rp[NC];
     float rsc = 0.0f;
@@ -2187,16 +2201,15 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
             const int64_t r0 = gs * nb_pad + 32 * bi;
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
-                const int c = threadIdx.x + NT * j, r = c >> 4, cc = c & 15;
-                const int64_t sr = r0 + r;
+                const int64_t sr = r0 + rr[j];
                 if constexpr (FP8) {
-                    const u32x2 a = *(const u32x2*)((const uint8_t*)g + sr * D + 8 * cc);
-                    const u32x2 b = *(const u32x2*)((const uint8_t*)vb + sr * D + 8 * cc);
+                    const u32x2 a = *(const u32x2*)((const uint8_t*)g + sr * D + 8 * cr[j]);
+                    const u32x2 b = *(const u32x2*)((const uint8_t*)vb + sr * D + 8 * cr[j]);
                     rq[j] = u32x4{a.x, a.y, 0u, 0u};
                     rp[j] = u32x4{b.x, b.y, 0u, 0u};
                 } else {
-                    rq[j] = *(const u32x4*)((const uint16_t*)g + sr * D + 8 * cc);
-                    rp[j] = *(const u32x4*)((const uint16_t*)vb + sr * D + 8 * cc);
+                    rq[j] = *(const u32x4*)((const uint16_t*)g + sr * D + 8 * cr[j]);
+                    rp[j] = *(const u32x4*)((const uint16_t*)vb + sr * D + 8 * cr[j]);
                 }
             }
             const int s = threadIdx.x;
@@ -2205,29 +2218,118 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
             else if (FP8 && s < 96) rsc = sv[r0 + s - 64];
         } else {                                            // near tokens: runs at 32 b and 32 b + 16
             const int e0 = 32 * (bi - nf), ja = run_pos(e0), jb = run_pos(e0 + 16);
-            const int64_t ra = kh + (int64_t)sidx[ja / LEAF] * LEAF + (ja % LEAF);
-            const int64_t rb = kh + (int64_t)sidx[jb / LEAF] * LEAF + (jb % LEAF);
+            const int64_t ra = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[ja / LEAF]) * LEAF + (ja % LEAF);
+            const int64_t rb = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[jb / LEAF]) * LEAF + (jb % LEAF);
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
-                const int c = threadIdx.x + NT * j, r = c >> 4, cc = c & 15;
-                const int64_t sr = r < 16 ? ra + r : rb + (r - 16);
-                rq[j] = *(const u32x4*)(k + sr * D + 8 * cc);
-                rp[j] = *(const u32x4*)(v + sr * D + 8 * cc);
+                const int64_t sr = rr[j] < 16 ? ra + rr[j] : rb + (rr[j] - 16);
+                rq[j] = *(const u32x4*)(k + sr * D + 8 * cr[j]);
+                rp[j] = *(const u32x4*)(v + sr * D + 8 * cr[j]);
             }
         }
     };
     auto store = [&](int bi, char* slot) {
-        const bool far8 = FP8 && bi < nf;                   // fp8 codes widened to fp16 here
+        if (bi < nf) {
 #pragma unroll
-        for (int j = 0; j < NC; ++j) {
-            const int c = threadIdx.x + NT * j, r = c >> 4, cc = c & 15;
-            const int off = r * 256 + 16 * (cc ^ swz(r));
-            *(u32x4*)(slot + off) = far8 ? e4m3x8_to_h8(u32x2{rq[j].x, rq[j].y}) : rq[j];
-            *(u32x4*)(slot + R16_ROWS + off) = far8 ? e4m3x8_to_h8(u32x2{rp[j].x, rp[j].y}) : rp[j];
+            for (int j = 0; j < NC; ++j) {                  // fp8 codes widened to fp16 here
+                *(u32x4*)(slot + oq[j]) = FP8 ? e4m3x8_to_h8_cvt(u32x2{rq[j].x, rq[j].y}) : rq[j];
+                *(u32x4*)(slot + op[j]) = FP8 ? e4m3x8_to_h8_cvt(u32x2{rp[j].x, rp[j].y}) : rp[j];
+            }
+            const int s = threadIdx.x;
+            if (s < (FP8 ? 96 : 32)) {
+                // lz of a leaf in the near set (or past nb) -> -inf: its far score is -inf, p = 0
+                const float x = s < 32 ? (((exbits[bi] >> s) & 1u) ? -INFINITY : rsc) : __fmul_rn(rsc, 256.0f);
+                *(float*)(slot + 2 * R16_ROWS + 4 * s) = x;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                *(u32x4*)(slot + oq[j]) = rq[j];
+                *(u32x4*)(slot + op[j]) = rp[j];
+            }
         }
-        if (bi < nf && threadIdx.x < (FP8 ? 96 : 32)) *(float*)(slot + 2 * R16_ROWS + 4 * threadIdx.x) = rsc;
     };
     RowsN<1> st;
+    // one 32-key block of the far field from slot S: score = (dq . g) (* 256 sg) + lz
+    auto far_block = [&](const char* slot) {
+        float u[8], pscale[8];
+        const float* scl = (const float*)(slot + 2 * R16_ROWS);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int r = 16 * hh + col;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const u32x4 A = *(const u32x4*)(slot + r * 256 + 16 * ((4 * ks + grp) ^ swq(r)));
+                if constexpr (FP8) acc = mfma_f16(A, bdq[ks], acc);
+                else acc = mfma_bf16(as_bf16x8(A), as_bf16x8(bdq[ks]), acc);
+            }
+            const f32x4 lzv = *(const f32x4*)(scl + 16 * hh + 4 * grp);
+            const f32x4 sgv = FP8 ? *(const f32x4*)(scl + 32 + 16 * hh + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
+            const f32x4 svv = FP8 ? *(const f32x4*)(scl + 64 + 16 * hh + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float dot = FP8 ? __fmul_rn(acc[i], sgv[i]) : acc[i];
+                u[4 * hh + i] = __fmaf_rn(__fadd_rn(dot, lzv[i]), LOG2E, -st.m[0]);
+                pscale[4 * hh + i] = svv[i];
+            }
+        }
+        u32x2 pvop[8][2];
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + R16_ROWS, 16 * hf, db, lane);
+        if constexpr (FP8) rows_update_f16(st, u, pscale, pvop);
+        else {
+            const float (&uu)[1][8] = *reinterpret_cast<const float (*)[1][8]>(&u);
+            rows_update<1, true>(st, uu, pvop);
+        }
+    };
+    // one 32-token block of the near field: score = (q . k) * scale; the second run of 16 is past
+    // the list (masked) only in the last block when the list holds an odd number of 16-token runs
+    auto near_block = [&](const char* slot, int bi) {
+        const bool run2 = 32 * (bi - nf) + 16 < e_n;
+        float u[8];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int r = 16 * hh + col;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const u32x4 A = *(const u32x4*)(slot + r * 256 + 16 * ((4 * ks + grp) ^ swq(r)));
+                acc = mfma_bf16(as_bf16x8(A), as_bf16x8(bq[ks]), acc);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) u[4 * hh + i] = (hh == 0 || run2) ? __fmaf_rn(acc[i], qs, -st.m[0]) : -INFINITY;
+        }
+        u32x2 pvop[8][2];
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + R16_ROWS, 16 * hf, db, lane);
+        const float (&uu)[1][8] = *reinterpret_cast<const float (*)[1][8]>(&u);
+        rows_update<1, true>(st, uu, pvop);
+    };
+    // block bi from slot S (block bi + 1 loaded meanwhile and staged into the other slot); slot
+    // parity a template constant, so every LDS address is a fixed offset
+    auto far_step = [&](auto par, int bi) {
+        constexpr int S = decltype(par)::value;
+        const bool more = bi + 1 < nblk;
+        if (more) load(bi + 1);
+        far_block(&ring[S][0]);
+        if (more) store(bi + 1, &ring[S ^ 1][0]);
+        __syncthreads();
+    };
+    auto near_step = [&](auto par, int bi) {
+        constexpr int S = decltype(par)::value;
+        const bool more = bi + 1 < nblk;
+        if (more) load(bi + 1);
+        near_block(&ring[S][0], bi);
+        if (more) store(bi + 1, &ring[S ^ 1][0]);
+        __syncthreads();
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
     for (int pass = 0; pass < MAX_PASSES; ++pass) {
         st.m[0] = mref;
         st.l[0] = 0.0f;
@@ -2236,82 +2338,30 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
         load(0);
         store(0, &ring[0][0]);
         __syncthreads();
-        for (int bi = 0; bi < nblk; ++bi) {
-            if (bi + 1 < nblk) load(bi + 1);                // in flight while block bi is computed
-            const char* slot = &ring[bi & 1][0];
-            float u[8];
-            if (bi < nf) {                                  // ---- far: 32 leaves c0 ..
-                const int c0 = 32 * bi;
-                const uint32_t exw = exbits[c0 >> 5] >> (4 * grp);
-                float pscale[8];
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int r = 16 * hh + col;
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int ks = 0; ks < 4; ++ks) {
-                        const u32x4 A = *(const u32x4*)(slot + r * 256 + 16 * ((4 * ks + grp) ^ swz(r)));
-                        if constexpr (FP8) acc = mfma_f16(A, bdq[ks], acc);
-                        else acc = mfma_bf16(as_bf16x8(A), as_bf16x8(bdq[ks]), acc);
-                    }
-                    const float* scl = (const float*)(slot + 2 * R16_ROWS);
-                    const f32x4 lzv = *(const f32x4*)(scl + 16 * hh + 4 * grp);
-                    const f32x4 sgv = FP8 ? *(const f32x4*)(scl + 32 + 16 * hh + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
-                    const f32x4 svv = FP8 ? *(const f32x4*)(scl + 64 + 16 * hh + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const bool ex = (exw >> (16 * hh + i)) & 1u;
-                        const float dot = FP8 ? __fmul_rn(acc[i], __fmul_rn(sgv[i], 256.0f)) : acc[i];
-                        u[4 * hh + i] = ex ? -INFINITY : __fmaf_rn(__fadd_rn(dot, lzv[i]), LOG2E, -st.m[0]);
-                        pscale[4 * hh + i] = __fmul_rn(svv[i], 256.0f);
-                    }
-                }
-                u32x2 pvop[8][2];
-#pragma unroll
-                for (int db = 0; db < 8; ++db)
-#pragma unroll
-                    for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + R16_ROWS, 16 * hf, db, lane);
-                if constexpr (FP8) rows_update_f16(st, u, pscale, pvop);
-                else {
-                    const float (&uu)[1][8] = *reinterpret_cast<const float (*)[1][8]>(&u);
-                    rows_update<1, true>(st, uu, pvop);
-                }
-            } else {                                        // ---- near: 32 tokens
-                const int e0 = 32 * (bi - nf);
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int r = 16 * hh + col;
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int ks = 0; ks < 4; ++ks) {
-                        const u32x4 A = *(const u32x4*)(slot + r * 256 + 16 * ((4 * ks + grp) ^ swz(r)));
-                        acc = mfma_bf16(as_bf16x8(A), as_bf16x8(bq[ks]), acc);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const bool ok = (e0 + 16 * hh + 4 * grp + i) < e_n;
-                        u[4 * hh + i] = ok ? __fmaf_rn(acc[i], qs, -st.m[0]) : -INFINITY;
-                    }
-                }
-                u32x2 pvop[8][2];
-#pragma unroll
-                for (int db = 0; db < 8; ++db)
-#pragma unroll
-                    for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + R16_ROWS, 16 * hf, db, lane);
-                const float (&uu)[1][8] = *reinterpret_cast<const float (*)[1][8]>(&u);
-                rows_update<1, true>(st, uu, pvop);
+        // far blocks 0 .. nf - 1 in slots 0, 1, 0, ..; the near blocks continue the alternation
+        for (int bi = 0; bi < nf; bi += 2) {
+            far_step(P0(), bi);
+            if (bi + 1 < nf) far_step(P1(), bi + 1);
+        }
+        if (nf & 1) {
+            for (int bi = nf; bi < nblk; bi += 2) {
+                near_step(P1(), bi);
+                if (bi + 1 < nblk) near_step(P0(), bi + 1);
             }
-            if (bi + 1 < nblk) store(bi + 1, &ring[(bi + 1) & 1][0]);
-            __syncthreads();                                // block bi + 1 staged; slot bi free
+        } else {
+            for (int bi = nf; bi < nblk; bi += 2) {
+                near_step(P0(), bi);
+                if (bi + 1 < nblk) near_step(P1(), bi + 1);
+            }
         }
         // row totals: outside [2^-60, 2^64] the reference missed the row's maximum by more than 60
         // octaves: the pass is redone with the reference moved to m + log2(total)
+        // (2^-8 with the fp8 store: its far-field P is fp16, whose subnormals would hold the far
+        // leaves of a row whose total is that small with too few bits)
         const float lt = grp_sum(st.l[0]);
         if (grp == 0) red_l[16 * wv + col] = lt;
         if (threadIdx.x == 0) redo = 0;
         __syncthreads();
-        // (2^-8 with the fp8 store: its far-field P is fp16, whose subnormals would hold the far
-        // leaves of a row whose total is that small with too few bits)
         const float tot = red_l[16 * wv + col];
         if (!(tot >= (FP8 ? 0x1p-8f : 0x1p-60f) && tot <= 0x1p64f)) {
             mref = tot > 0.0f && tot <= 3.0e38f ? __fadd_rn(mref, __log2f(tot))
@@ -2627,6 +2677,17 @@ __global__ __launch_bounds__(64) void selftest_mfma_kernel(const int8_t* __restr
     f32x4 cc = mfma_bf16(fa, fbv, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
     for (int i = 0; i < 4; ++i) cf[(4 * grp + i) * 16 + col] = cc[i];
+}
+
+// selftest_e4m3: the route kernels' e4m3 -> fp16 widening (e4m3x8_to_h8_cvt), eight codes per
+// thread, next to the bit-exact field shift (e4m3x8_to_h8).
+__global__ __launch_bounds__(64) void selftest_e4m3_kernel(const uint8_t* __restrict__ codes, int n,
+                                                           uint16_t* __restrict__ cvt, uint16_t* __restrict__ bits) {
+    const int i = blockIdx.x * 64 + threadIdx.x;
+    if (8 * i >= n) return;
+    const u32x2 c = *(const u32x2*)(codes + 8 * i);
+    *(u32x4*)(cvt + 8 * i) = e4m3x8_to_h8_cvt(c);
+    *(u32x4*)(bits + 8 * i) = e4m3x8_to_h8(c);
 }
 
 // =============================================================================================
@@ -3399,6 +3460,15 @@ int htrc_dequant_rows(const uint8_t* x8, int64_t stride_x, const float* scale, i
         hipLaunchKernelGGL(dequant_kernel<false>, dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, x8,
                            stride_x, scale, stride_s, rows, d, out);
     return launched("htrc_dequant_rows");
+}
+
+int htrc_selftest_e4m3(const uint8_t* codes, int64_t n, uint16_t* cvt, uint16_t* bits, void* stream) {
+    REQUIRE(codes && cvt && bits, "htrc_selftest_e4m3: null pointer");
+    REQUIRE(n > 0 && n % 8 == 0 && n <= (1 << 24), "htrc_selftest_e4m3: n must be a positive multiple of 8");
+    REQUIRE(aligned(codes, 8) && aligned(cvt, 16) && aligned(bits, 16), "htrc_selftest_e4m3: misaligned buffer");
+    hipLaunchKernelGGL(selftest_e4m3_kernel, dim3((unsigned)((n / 8 + 63) / 64)), dim3(64), 0, (hipStream_t)stream,
+                       codes, (int)n, cvt, bits);
+    return launched("htrc_selftest_e4m3");
 }
 
 int htrc_selftest_mfma(const int8_t* ai, const int8_t* bi, int32_t* ci, const uint16_t* af, const uint16_t* bf,

@@ -525,6 +525,17 @@ def selftest_mfma(ai, bi, af, bf):
     return ci, cf
 
 
+def selftest_e4m3(codes):
+    """Widen uint8 e4m3 codes (a multiple of 8) to fp16 * 2^-8 bit patterns with the kernels'
+    conversion instruction and with the exact field shift -> (cvt int16 [n], bits int16 [n])."""
+    dev = codes.device
+    n = int(codes.numel())
+    cvt = torch.empty((n,), dtype=torch.int16, device=dev)
+    bits = torch.empty((n,), dtype=torch.int16, device=dev)
+    call("htrc_selftest_e4m3", ptr(codes), n, ptr(cvt), ptr(bits), stream_handle(dev))
+    return cvt, bits
+
+
 def library():
     """The loaded C-ABI library (raises when it is not built)."""
     return _lib.lib()

@@ -251,6 +251,12 @@ int htrc_dequant_rows(const uint8_t* x8, int64_t stride_x, const float* scale, i
 int htrc_selftest_mfma(const int8_t* ai, const int8_t* bi, int32_t* ci, const uint16_t* af, const uint16_t* bf,
                        float* cf, void* stream);
 
+/* Self-test of the e4m3 -> fp16 widening of the 16-bit route kernels (no reference counterpart):
+ * the n codes (n a multiple of 8) widened to fp16 holding value * 2^-8 by the conversion
+ * instruction the kernels use (cvt) and by the exact exponent / mantissa field shift (bits);
+ * device pointers. */
+int htrc_selftest_e4m3(const uint8_t* codes, int64_t n, uint16_t* cvt, uint16_t* bits, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

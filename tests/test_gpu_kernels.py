@@ -364,6 +364,20 @@ def test_dequant_rows_all_patterns(device, out_dtype):
     torch.testing.assert_close(out.cpu(), want, rtol=0, atol=0, equal_nan=True)
 
 
+def test_e4m3_widening_all_codes(device):
+    """The route kernels' e4m3 -> fp16 widening (gfx950 conversion instruction, scale 2^-8) against
+    the exact field shift and torch's float8_e4m3fn decode times 2^-8, on every finite code in
+    every byte position of the eight-code groups (the NaN codes 0x7f / 0xff never reach it)."""
+    codes = torch.arange(256, dtype=torch.uint8)
+    rolled = torch.cat([torch.roll(codes, j) for j in range(8)])          # each code at each position
+    cvt, bits = hip.selftest_e4m3(rolled.to(device))
+    torch.cuda.synchronize()
+    fin = (rolled & 0x7F) != 0x7F
+    want = (rolled.view(torch.float8_e4m3fn).float() * 2.0 ** -8).to(torch.float16).view(torch.int16)
+    assert torch.equal(bits.cpu()[fin], want[fin])
+    assert torch.equal(cvt.cpu()[fin], want[fin])
+
+
 @pytest.mark.parametrize("n,m", [(64512, 4096), (124992, 4096), (5000, 4096), (4096, 4096), (1000, 33),
                                  (64512, 32), (4096, 32), (77, 1)])
 def test_linspace_positions_equal_device_torch(device, n, m):
