@@ -363,6 +363,16 @@ __device__ __forceinline__ uint32_t quant4_e4m3(f32x4 x, float c) {
            (f32_to_e4m3(__fmul_rn(x[2], c)) << 16) | (f32_to_e4m3(__fmul_rn(x[3], c)) << 24);
 }
 
+// The same codes from gfx950's conversion instruction (v_cvt_pk_fp8_f32: OCP e4m3, round to
+// nearest even), two values per instruction.  It matches f32_to_e4m3 on every input with
+// |x| < 464 (htrc_selftest_f32_e4m3 checks code values, ties, their neighbours, subnormals and
+// random values on the device); the state scales keep |x c| <= 448 (1 + 2^-22).
+__device__ __forceinline__ uint32_t quant4_e4m3_cvt(f32x4 x, float c) {
+    int r = __builtin_amdgcn_cvt_pk_fp8_f32(__fmul_rn(x[0], c), __fmul_rn(x[1], c), 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(__fmul_rn(x[2], c), __fmul_rn(x[3], c), r, true);
+    return (uint32_t)r;
+}
+
 // int8 codes of x_i * c rounded half away from zero, packed little-endian: y = x c, then
 // trunc(y + copysign(0.5, y)) in fp32 (h3/htrc_flat_triton.py:77-79: where(x >= 0, x + 0.5,
 // x - 0.5) and a truncating int8 cast; 0.49999997 -> 1 as there).  copysign is one bit select
@@ -549,8 +559,8 @@ __global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restri
             const float cg = __fdiv_rn(scale, sgv), cv = __fdiv_rn(1.0f, svv);
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
-                pg[db] = quant4_e4m3(gacc[db], cg);
-                pv[db] = u32x2{quant4_e4m3(vacc[db], cv), 0u};
+                pg[db] = quant4_e4m3_cvt(gacc[db], cg);
+                pv[db] = u32x2{quant4_e4m3_cvt(vacc[db], cv), 0u};
             }
             push(lq, sgv, lzq, svv);
         } else {
@@ -1138,14 +1148,14 @@ __global__ __launch_bounds__(256) void tile_kernel(
 //   bf16 (store="bf16", DOT = 1 without FP8 / I8):
 //     select: SEL = max_r dq_r(bf16) . g_l(bf16) + lz_l; far: score = dq . g + lz, O += p(bf16) . vb;
 //   both, near: score = (q(bf16) . k(bf16)) * scale, O += p(bf16) . v(bf16).
-// The e4m3 codes are widened to fp16 holding value * 2^-8 (e4m3x8_to_h8), exactly; sg and sv
+// The e4m3 codes are widened to fp16 holding value * 2^-8 (e4m3x8_to_h8_cvt), exactly; sg and sv
 // are taken times 256 (exact), so every product is the reference's.
 // ---------------------------------------------------------------------------------------------
 // QK A operand of state rows: 16 leaves x dims 32 ks + 8 grp .. + 7 of row `row`.
 template <bool FP8>
 __device__ __forceinline__ f32x4 state_qk(const void* g, int64_t row, int ks, int grp, const u32x4& b, f32x4 acc) {
     if constexpr (FP8)
-        return mfma_f16(e4m3x8_to_h8(*(const u32x2*)((const uint8_t*)g + row * D + 32 * ks + 8 * grp)), b, acc);
+        return mfma_f16(e4m3x8_to_h8_cvt(*(const u32x2*)((const uint8_t*)g + row * D + 32 * ks + 8 * grp)), b, acc);
     else
         return mfma_bf16(as_bf16x8(*(const u32x4*)((const uint16_t*)g + row * D + 32 * ks + 8 * grp)), as_bf16x8(b), acc);
 }
@@ -1322,7 +1332,7 @@ __global__ __launch_bounds__(256) void tile16_kernel(
                     u[jh] = (uint32_t)b[0] | ((uint32_t)b[D] << 8) | ((uint32_t)b[2 * D] << 16) |
                             ((uint32_t)b[3 * D] << 24);
                 }
-                return e4m3x8_to_h8(u32x2{u[0], u[1]});
+                return e4m3x8_to_h8_cvt(u32x2{u[0], u[1]});
             });
         } else {
             const uint16_t* vb0 = (const uint16_t*)vb + (gs * nb_pad + c0) * D;
@@ -2052,17 +2062,43 @@ __global__ __launch_bounds__(256, 3) void route_select16_kernel(
         float rmax[NRB];
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) rmax[rb] = -INFINITY;
-        for (int c = 16 * w; c < nb; c += 64) {          // the wave's 16-leaf groups
+        // the wave's 16-leaf groups c = 16 w, 16 w + 64, ..: each group's state rows are fetched
+        // while the previous group's products run (two register sets; a third, two groups
+        // ahead, spills at three waves per SIMD and measured slower: 1.20 / 1.16 ms at cfg3 for
+        // fp8 / bf16 against 1.26 / 1.56)
+        using AT = std::conditional_t<FP8, u32x2, u32x4>;   // 8 e4m3 codes / 8 bf16 of a row chunk
+        struct Grp {
+            AT a[4];
+            f32x4 sgv, lzv;
+        };
+        auto fetch = [&](Grp& gr, int c) {
             const int64_t s0 = gs * nb_pad + c;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                if constexpr (FP8) gr.a[ks] = *(const u32x2*)((const uint8_t*)g + (s0 + col) * D + 32 * ks + 8 * grp);
+                else gr.a[ks] = *(const u32x4*)((const uint16_t*)g + (s0 + col) * D + 32 * ks + 8 * grp);
+            }
+            gr.sgv = FP8 ? *(const f32x4*)(sg + s0 + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
+            gr.lzv = *(const f32x4*)(lz + s0 + 4 * grp);
+        };
+        auto consume = [&](const Grp& gr, int c) {
+            // the products of state_qk, in its order
             f32x4 acc[NRB];
 #pragma unroll
             for (int rb = 0; rb < NRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
+            for (int ks = 0; ks < 4; ++ks) {
+                if constexpr (FP8) {
+                    const u32x4 A = e4m3x8_to_h8_cvt(gr.a[ks]);
 #pragma unroll
-                for (int rb = 0; rb < NRB; ++rb) acc[rb] = state_qk<FP8>(g, s0 + col, ks, grp, b[rb][ks], acc[rb]);
-            const f32x4 sgv = FP8 ? *(const f32x4*)(sg + s0 + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
-            const f32x4 lzv = *(const f32x4*)(lz + s0 + 4 * grp);
+                    for (int rb = 0; rb < NRB; ++rb) acc[rb] = mfma_f16(A, b[rb][ks], acc[rb]);
+                } else {
+#pragma unroll
+                    for (int rb = 0; rb < NRB; ++rb)
+                        acc[rb] = mfma_bf16(as_bf16x8(gr.a[ks]), as_bf16x8(b[rb][ks]), acc[rb]);
+                }
+            }
+            const f32x4 sgv = gr.sgv, lzv = gr.lzv;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float sc = __fmul_rn(sgv[i], 256.0f);
@@ -2080,6 +2116,16 @@ __global__ __launch_bounds__(256, 3) void route_select16_kernel(
                     keys16[l] = first ? key : max(keys16[l], key);
                 }
             }
+        };
+        Grp x0, x1;
+        const int cw = 16 * w;
+        if (cw < nb) fetch(x0, cw);
+        for (int c = cw; c < nb; c += 128) {
+            if (c + 64 < nb) fetch(x1, c + 64);
+            consume(x0, c);
+            if (c + 64 >= nb) break;
+            if (c + 128 < nb) fetch(x0, c + 128);
+            consume(x1, c + 64);
         }
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
@@ -2182,16 +2228,11 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
     const int nn = (e_n + 31) / 32;                         // near blocks: two 16-token runs each
     const int nblk = nf + nn;
     const float qs = __fmul_rn(scale, LOG2E);
-    // this thread's chunks of a 32-row region: row rr[j], 16-byte chunk cr[j]; LDS byte offsets
-    int rr[NC], cr[NC], oq[NC], op[NC];
-#pragma unroll
-    for (int j = 0; j < NC; ++j) {
-        const int c = threadIdx.x + NT * j;
-        rr[j] = c >> 4;
-        cr[j] = c & 15;
-        oq[j] = rr[j] * 256 + 16 * (cr[j] ^ swq(rr[j]));
-        op[j] = R16_ROWS + rr[j] * 256 + 16 * (cr[j] ^ swz(rr[j]));
-    }
+    // this thread's chunks j of a 32-row region: row rr(j), 16-byte chunk cr; LDS byte offsets
+    const int cr = threadIdx.x & 15;
+    auto rr = [&](int j) { return (int)(threadIdx.x >> 4) + (NT / 16) * j; };
+    auto oq = [&](int j) { return rr(j) * 256 + 16 * (cr ^ swq(rr(j))); };
+    auto op = [&](int j) { return R16_ROWS + rr(j) * 256 + 16 * (cr ^ swz(rr(j))); };
     // staging registers of one block: this thread's chunks of the QK and PV regions and a scale
     u32x4 rq[NC], rp[NC];
     float rsc = 0.0f;
@@ -2201,15 +2242,15 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
             const int64_t r0 = gs * nb_pad + 32 * bi;
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
-                const int64_t sr = r0 + rr[j];
+                const int64_t sr = r0 + rr(j);
                 if constexpr (FP8) {
-                    const u32x2 a = *(const u32x2*)((const uint8_t*)g + sr * D + 8 * cr[j]);
-                    const u32x2 b = *(const u32x2*)((const uint8_t*)vb + sr * D + 8 * cr[j]);
+                    const u32x2 a = *(const u32x2*)((const uint8_t*)g + sr * D + 8 * cr);
+                    const u32x2 b = *(const u32x2*)((const uint8_t*)vb + sr * D + 8 * cr);
                     rq[j] = u32x4{a.x, a.y, 0u, 0u};
                     rp[j] = u32x4{b.x, b.y, 0u, 0u};
                 } else {
-                    rq[j] = *(const u32x4*)((const uint16_t*)g + sr * D + 8 * cr[j]);
-                    rp[j] = *(const u32x4*)((const uint16_t*)vb + sr * D + 8 * cr[j]);
+                    rq[j] = *(const u32x4*)((const uint16_t*)g + sr * D + 8 * cr);
+                    rp[j] = *(const u32x4*)((const uint16_t*)vb + sr * D + 8 * cr);
                 }
             }
             const int s = threadIdx.x;
@@ -2222,9 +2263,9 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
             const int64_t rb = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[jb / LEAF]) * LEAF + (jb % LEAF);
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
-                const int64_t sr = rr[j] < 16 ? ra + rr[j] : rb + (rr[j] - 16);
-                rq[j] = *(const u32x4*)(k + sr * D + 8 * cr[j]);
-                rp[j] = *(const u32x4*)(v + sr * D + 8 * cr[j]);
+                const int64_t sr = rr(j) < 16 ? ra + rr(j) : rb + (rr(j) - 16);
+                rq[j] = *(const u32x4*)(k + sr * D + 8 * cr);
+                rp[j] = *(const u32x4*)(v + sr * D + 8 * cr);
             }
         }
     };
@@ -2232,8 +2273,8 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
         if (bi < nf) {
 #pragma unroll
             for (int j = 0; j < NC; ++j) {                  // fp8 codes widened to fp16 here
-                *(u32x4*)(slot + oq[j]) = FP8 ? e4m3x8_to_h8_cvt(u32x2{rq[j].x, rq[j].y}) : rq[j];
-                *(u32x4*)(slot + op[j]) = FP8 ? e4m3x8_to_h8_cvt(u32x2{rp[j].x, rp[j].y}) : rp[j];
+                *(u32x4*)(slot + oq(j)) = FP8 ? e4m3x8_to_h8_cvt(u32x2{rq[j].x, rq[j].y}) : rq[j];
+                *(u32x4*)(slot + op(j)) = FP8 ? e4m3x8_to_h8_cvt(u32x2{rp[j].x, rp[j].y}) : rp[j];
             }
             const int s = threadIdx.x;
             if (s < (FP8 ? 96 : 32)) {
@@ -2244,8 +2285,8 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
         } else {
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
-                *(u32x4*)(slot + oq[j]) = rq[j];
-                *(u32x4*)(slot + op[j]) = rp[j];
+                *(u32x4*)(slot + oq(j)) = rq[j];
+                *(u32x4*)(slot + op(j)) = rp[j];
             }
         }
     };
@@ -2677,6 +2718,17 @@ __global__ __launch_bounds__(64) void selftest_mfma_kernel(const int8_t* __restr
     f32x4 cc = mfma_bf16(fa, fbv, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
     for (int i = 0; i < 4; ++i) cf[(4 * grp + i) * 16 + col] = cc[i];
+}
+
+// selftest_f32_e4m3: the stats kernel's fp32 -> e4m3 codes (quant4_e4m3_cvt, c = 1) next to
+// f32_to_e4m3, four values per thread.
+__global__ __launch_bounds__(64) void selftest_f32_e4m3_kernel(const float* __restrict__ x, int n,
+                                                               uint32_t* __restrict__ cvt, uint32_t* __restrict__ soft) {
+    const int i = blockIdx.x * 64 + threadIdx.x;
+    if (4 * i >= n) return;
+    const f32x4 v = *(const f32x4*)(x + 4 * i);
+    cvt[i] = quant4_e4m3_cvt(v, 1.0f);
+    soft[i] = quant4_e4m3(v, 1.0f);
 }
 
 // selftest_e4m3: the route kernels' e4m3 -> fp16 widening (e4m3x8_to_h8_cvt), eight codes per
@@ -3460,6 +3512,15 @@ int htrc_dequant_rows(const uint8_t* x8, int64_t stride_x, const float* scale, i
         hipLaunchKernelGGL(dequant_kernel<false>, dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, x8,
                            stride_x, scale, stride_s, rows, d, out);
     return launched("htrc_dequant_rows");
+}
+
+int htrc_selftest_f32_e4m3(const float* x, int64_t n, uint8_t* cvt, uint8_t* soft, void* stream) {
+    REQUIRE(x && cvt && soft, "htrc_selftest_f32_e4m3: null pointer");
+    REQUIRE(n > 0 && n % 4 == 0 && n <= (1 << 26), "htrc_selftest_f32_e4m3: n must be a positive multiple of 4");
+    REQUIRE(aligned(x, 16) && aligned(cvt, 4) && aligned(soft, 4), "htrc_selftest_f32_e4m3: misaligned buffer");
+    hipLaunchKernelGGL(selftest_f32_e4m3_kernel, dim3((unsigned)((n / 4 + 63) / 64)), dim3(64), 0,
+                       (hipStream_t)stream, x, (int)n, (uint32_t*)cvt, (uint32_t*)soft);
+    return launched("htrc_selftest_f32_e4m3");
 }
 
 int htrc_selftest_e4m3(const uint8_t* codes, int64_t n, uint16_t* cvt, uint16_t* bits, void* stream) {

@@ -536,6 +536,17 @@ def selftest_e4m3(codes):
     return cvt, bits
 
 
+def selftest_f32_e4m3(x):
+    """e4m3 codes of fp32 values (a multiple of 4) from the stats kernel's conversion instruction
+    and from the exact software rounding -> (cvt uint8 [n], soft uint8 [n])."""
+    dev = x.device
+    n = int(x.numel())
+    cvt = torch.empty((n,), dtype=torch.uint8, device=dev)
+    soft = torch.empty((n,), dtype=torch.uint8, device=dev)
+    call("htrc_selftest_f32_e4m3", ptr(x), n, ptr(cvt), ptr(soft), stream_handle(dev))
+    return cvt, soft
+
+
 def library():
     """The loaded C-ABI library (raises when it is not built)."""
     return _lib.lib()

@@ -257,6 +257,11 @@ int htrc_selftest_mfma(const int8_t* ai, const int8_t* bi, int32_t* ci, const ui
  * device pointers. */
 int htrc_selftest_e4m3(const uint8_t* codes, int64_t n, uint16_t* cvt, uint16_t* bits, void* stream);
 
+/* Self-test of the fp32 -> e4m3 codes of the fp8 state store (no reference counterpart): the n
+ * values (n a multiple of 4) converted by the conversion instruction the stats kernel uses (cvt)
+ * and by the exact software rounding (soft, nearest even, |x| saturated at 448); device pointers. */
+int htrc_selftest_f32_e4m3(const float* x, int64_t n, uint8_t* cvt, uint8_t* soft, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -378,6 +378,37 @@ def test_e4m3_widening_all_codes(device):
     assert torch.equal(cvt.cpu()[fin], want[fin])
 
 
+def _e4m3_probe_values() -> np.ndarray:
+    """Every finite e4m3 value, the midpoints between neighbours (ties) and the floats one ulp
+    either side of them and of the values, both signs; values just past 448; subnormal-range and
+    fp32-denormal inputs; zeros; and log-uniform random values in [2^-12, 448]."""
+    mags = np.array(sorted({float(v) for v in torch.arange(0, 127, dtype=torch.uint8).view(torch.float8_e4m3fn).float()}),
+                    np.float32)
+    mids = ((mags[:-1].astype(np.float64) + mags[1:]) / 2).astype(np.float32)
+    base = np.concatenate([mags, mids, [448.5, 455.0, 463.0, 2.0 ** -10, 3 * 2.0 ** -11, 1e-40, 1e-30]]).astype(np.float32)
+    near = np.concatenate([base, np.nextafter(base, np.float32(np.inf)), np.nextafter(base, np.float32(0))])
+    rng = np.random.default_rng(8)
+    rnd = np.exp2(rng.uniform(-12, np.log2(448.0), 1 << 20)).astype(np.float32)
+    vals = np.concatenate([near, rnd]).astype(np.float32)
+    vals = vals[np.abs(vals) <= 463.0]
+    allv = np.concatenate([vals, -vals])
+    return np.concatenate([allv, np.zeros((-allv.size) % 4, np.float32)])
+
+
+def test_f32_to_e4m3_conversion_matches_software_rounding(device):
+    """The stats kernel's fp32 -> e4m3 conversion instruction gives the software rounding's codes
+    (nearest even, the subnormal grid, 448 for |x| < 464) on every probe value; the software
+    rounding is torch's float8_e4m3fn cast on those values."""
+    x = _e4m3_probe_values()
+    cvt, soft = hip.selftest_f32_e4m3(torch.from_numpy(x).to(device))
+    torch.cuda.synchronize()
+    cvt, soft = cvt.cpu().numpy(), soft.cpu().numpy()
+    want = torch.from_numpy(np.clip(x, -448.0, 448.0)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(soft, want)
+    bad = np.nonzero(cvt != soft)[0]
+    assert bad.size == 0, f"{bad.size} differ, e.g. x={x[bad[:4]]} cvt={cvt[bad[:4]]} soft={soft[bad[:4]]}"
+
+
 @pytest.mark.parametrize("n,m", [(64512, 4096), (124992, 4096), (5000, 4096), (4096, 4096), (1000, 33),
                                  (64512, 32), (4096, 32), (77, 1)])
 def test_linspace_positions_equal_device_torch(device, n, m):
