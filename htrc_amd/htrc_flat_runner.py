@@ -25,6 +25,8 @@ The memory model below imports without torch.
 """
 from __future__ import annotations
 
+import gc
+
 try:                                   # the memory model below must stay importable without torch
     import torch
 except ImportError:                    # pragma: no cover
@@ -144,19 +146,20 @@ class _Plan:
 
 class _Replay:
     """Static buffers, a workspace filled by one eager warm-up call, and the HIP graph recorded
-    over one operator call on them."""
+    over one operator call on them.  It holds the operator call, not the runner: a runner and
+    its replay form no reference cycle, so a dropped runner (its graph and memory pool with
+    it) is freed at once rather than by a later garbage-collector pass."""
 
-    def __init__(self, runner):
-        self.runner = runner
-        dev, shape = runner.device, runner._shape
-        gen = torch.Generator(device=dev).manual_seed(0)
+    def __init__(self, op, device, shape, queries: int, keys: int, tail_rows: int):
+        self.op, self.device, self.tail_rows = op, device, int(tail_rows)
+        gen = torch.Generator(device=device).manual_seed(0)
         # finite, well-spread warm-up data: the k-means order and the softmax see real numbers
-        self.q = torch.randn(shape(runner.queries), generator=gen, device=dev, dtype=torch.float32)
-        self.k = torch.randn(shape(runner.keys), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
-        self.v = torch.randn(shape(runner.keys), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        self.q = torch.randn(shape(queries), generator=gen, device=device, dtype=torch.float32)
+        self.k = torch.randn(shape(keys), generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+        self.v = torch.randn(shape(keys), generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
         self.tail = None
-        if runner.tail_rows:
-            self.tail = tuple(torch.randn(shape(runner.tail_rows), generator=gen, device=dev, dtype=torch.float32)
+        if tail_rows:
+            self.tail = tuple(torch.randn(shape(tail_rows), generator=gen, device=device, dtype=torch.float32)
                               for _ in range(2))
         self.ws = {}
         self.out = None
@@ -164,23 +167,34 @@ class _Replay:
 
     def record(self):
         """Warm up on a side stream (the workspace is allocated there, outside the recording),
-        then record one call; the graph then replays on the static buffers."""
-        side = torch.cuda.Stream(device=self.runner.device)
-        side.wait_stream(torch.cuda.current_stream(self.runner.device))
+        then record one call; the graph then replays on the static buffers.  The garbage
+        collector runs before the recording and is off during it: a collection there could
+        destroy some other dead object's graph or free its memory, which is illegal while a
+        stream is being captured (torch.cuda.graph collects first only when
+        torch.compiler.config.force_cudagraph_gc is set)."""
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(side):
-            self.runner._op(self.q, self.k, self.v, self.tail, self.ws)
+            self.op(self.q, self.k, self.v, self.tail, self.ws)
         side.synchronize()
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, capture_error_mode="thread_local"):
-            self.out = self.runner._op(self.q, self.k, self.v, self.tail, self.ws)
-        torch.cuda.synchronize(self.runner.device)
+        gc.collect()
+        was = gc.isenabled()
+        gc.disable()
+        try:
+            with torch.cuda.graph(graph, capture_error_mode="thread_local"):
+                self.out = self.op(self.q, self.k, self.v, self.tail, self.ws)
+        finally:
+            if was:
+                gc.enable()
+        torch.cuda.synchronize(self.device)
         self.graph = graph
 
     def replay(self, q, k, v, tail):
         """Copy this call's operands into the static buffers and replay; returns the static output."""
         if self.tail is not None:
             if tail is None:
-                raise ValueError(f"this runner was recorded with tail_rows={self.runner.tail_rows}: pass tail=(tk, tv)")
+                raise ValueError(f"this runner was recorded with tail_rows={self.tail_rows}: pass tail=(tk, tv)")
             self.tail[0].copy_(tail[0])
             self.tail[1].copy_(tail[1])
         self.q.copy_(q)
@@ -213,7 +227,9 @@ class FlatRunner:
         self.graph_error = None
         self._replay = None
         if use_graph:
-            rep = _Replay(self)
+            flat, cfg = self.flat, self.cfg
+            rep = _Replay(lambda q, k, v, tail, ws: flat.flat_attention(q, k, v, tail=tail, ws=ws, **cfg),
+                          self.device, self._shape, self.queries, self.keys, self.tail_rows)
             try:
                 rep.record()
                 self._replay = rep

@@ -213,6 +213,27 @@ def test_runner_modes_and_memory_model():
     assert htrc_flat_runner.STATIC_MIB == pytest.approx(39.8, abs=0.05)
 
 
+def test_runner_and_its_replay_form_no_reference_cycle(monkeypatch):
+    """A dropped runner, graph replay included, is freed by reference counting at once, not by a
+    later collector pass (which could fall inside another runner's capture, where destroying a
+    graph or freeing its pool is illegal).  The recording itself is stubbed: no GPU here."""
+    import gc
+    import weakref
+    monkeypatch.setattr(htrc_flat_runner._Replay, "record", lambda self: None)
+    r = htrc_flat_runner.FlatRunner(256, 256, mode="fast", device="cpu", free_bytes=8 << 30, tail_rows=3, leaf=64,
+                                    exact_leaves=2)
+    assert r._replay is not None and r._replay.tail[0].shape == (3, 128)
+    with pytest.raises(ValueError, match="tail_rows=3"):
+        r._replay.replay(torch.zeros(256, 128), torch.zeros(256, 128), torch.zeros(256, 128), None)
+    gc.disable()
+    try:
+        ref, rref = weakref.ref(r), weakref.ref(r._replay)
+        del r
+        assert ref() is None and rref() is None
+    finally:
+        gc.enable()
+
+
 def test_runner_plan_merges_knobs():
     """PROD, then the mode, then the caller's knobs with kern merged key by key; the window from
     free_bytes steps down through CHUNKS."""

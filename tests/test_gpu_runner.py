@@ -5,6 +5,9 @@ failure degrades to eager with ``graph_error`` recorded.
 """
 from __future__ import annotations
 
+import gc
+import weakref
+
 import pytest
 import torch
 
@@ -47,6 +50,33 @@ def test_head_batched_runner_matches_per_head(device):
     batched.run(jobs, sink=lambda i, o: got.__setitem__(i, o.clone()))
     for i, x in enumerate(a):
         assert torch.equal(got[i], x)
+
+
+def test_capture_runs_with_the_collector_off_and_runners_free_by_refcount(device, monkeypatch):
+    """The recording runs with Python's garbage collector off (a collection inside it could
+    destroy another dead runner's graph and pool, which is illegal during a capture), the
+    collector is back on afterwards, and a runner with its graph is freed as soon as its last
+    reference goes (no runner <-> replay cycle left for the collector)."""
+    seen = []
+    orig = torch.cuda.graph
+
+    class Spy(orig):
+        def __enter__(self):
+            seen.append(gc.isenabled())
+            return super().__enter__()
+
+    monkeypatch.setattr(torch.cuda, "graph", Spy)
+    r = htrc_flat_runner.FlatRunner(2048, 2048, mode="fast", **KW)
+    monkeypatch.setattr(torch.cuda, "graph", orig)
+    assert r.graph is not None, r.graph_error
+    assert seen == [False] and gc.isenabled()
+    gc.disable()
+    try:
+        ref = weakref.ref(r)
+        del r
+        assert ref() is None
+    finally:
+        gc.enable()
 
 
 def test_capture_failure_falls_back_to_eager(device, monkeypatch):
