@@ -1739,6 +1739,9 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
     const int nn = e_hi > e_lo ? (e_hi - e_lo + 31) / 32 : 0;
     const int sf_steps = min(nb, lpw) > 0 ? (min(nb, lpw) + 31) / 32 : 0;        // pair 0 is the longest
     const int sn_steps = min(e_n, epw) > 0 ? (min(e_n, epw) + 31) / 32 : 0;
+    // far steps rounded up to even (an odd count takes one empty step), so the near blocks
+    // start in ring slot 0 and the last far step issues the first of them
+    const int sf_even = (sf_steps + 1) & ~1;
     const int64_t srow0 = gs * nb_pad;
     char* pring = &ring[pr][0][0];
     const uint32_t pring_lds = lds_addr(pring);
@@ -1765,6 +1768,17 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
             dma_rows27(XV + r0 * D, XV + r1 * D, bo, slot);
         }
     };
+    // near block bi (list positions e_lo + 32 bi, + 16): the 16-token runs start there (past
+    // e_hi: the range start again, loaded and masked); token = leaf * LEAF + position % LEAF
+    auto run_pos = [&](int j) { return j < e_hi ? j : e_lo; };
+    auto issue_near = [&](int bi, int slot) {
+        if (bi >= nn) return;
+        const int e0 = e_lo + 32 * bi, ja = run_pos(e0), jb = run_pos(e0 + 16);
+        const int64_t r0 = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[ja / LEAF]) * LEAF + (ja % LEAF);
+        const int64_t r1 = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[jb / LEAF]) * LEAF + (jb % LEAF);
+        load_block(pring_lds + slot * SLOT_BYTES, k8, v, r0, r1, ks + r0, ks + r1, 3);
+    };
+    static_assert(RS == 2, "the far / near block stream alternates two ring slots");
     RowsN<RB> st;
 #pragma unroll 1
     for (int pass = 0; pass < MAX_PASSES; ++pass) {
@@ -1789,6 +1803,10 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
             }
             __syncthreads();            // exbits complete; the ring is free (merge / earlier pass)
             auto issue = [&](int bi, int slot) {
+                if (bi >= sf_even) {    // past the far steps: the near field's first block
+                    issue_near(bi - sf_even, slot);
+                    return;
+                }
                 if (bi >= nf) return;
                 const int64_t r0 = srow0 + lo + 32 * bi;
                 load_block(pring_lds + slot * SLOT_BYTES, g8, vb, r0, r0 + 16, sg + r0, lz + r0, 7);
@@ -1838,13 +1856,10 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
                 rows_update<RB, true>(st, sc, pvop);
             };
             issue(0, 0);
-            if (RS == 3) issue(1, 1);
 #pragma unroll 1
-            for (int bi = 0; bi < sf_steps; bi += RS) {
+            for (int bi = 0; bi < sf_even; bi += 2) {
                 step(std::integral_constant<int, 0>{}, bi);
-                if (bi + 1 < sf_steps) step(std::integral_constant<int, 1>{}, bi + 1);
-                if constexpr (RS == 3)
-                    if (bi + 2 < sf_steps) step(std::integral_constant<int, 2 % RS>{}, bi + 2);
+                step(std::integral_constant<int, 1>{}, bi + 1);
             }
         }
         {   // ---- near field: S^T = k8 q8^T, score = dot * sq * ks * scale
@@ -1858,10 +1873,9 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
                 srow[rb] = __fmul_rn(__fmul_rn(sq[p], scale), LOG2E);
                 asm volatile("" : : "v"(bq[rb][0]), "v"(bq[rb][1]), "v"(srow[rb]));
             }
-            __syncthreads();            // every wave is done with the far blocks in the ring
-            // the 16-token runs of block bi start at list positions e_lo + 32 bi and + 16 (past
-            // e_hi: the range start again, loaded and masked); token = leaf * LEAF + position % LEAF
-            auto run_pos = [&](int j) { return j < e_hi ? j : e_lo; };
+            // the near blocks continue the far stream: block 0 was issued by the last far step,
+            // into slot 0; every wave is done with the far blocks once it passes the first near
+            // step's barrier
             auto issue = [&](int bi, int slot, uint32_t la, uint32_t lb) {
                 if (bi >= nn) return;
                 const int e0 = e_lo + 32 * bi, ja = run_pos(e0), jb = run_pos(e0 + 16);
@@ -1916,14 +1930,10 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
                     for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
                 rows_update<RB, true>(st, sc, pvop);
             };
-            issue(0, 0, sidx[run_pos(e_lo) / LEAF], sidx[run_pos(e_lo + 16) / LEAF]);
-            if (RS == 3) issue(1, 1, sidx[run_pos(e_lo + 32) / LEAF], sidx[run_pos(e_lo + 48) / LEAF]);
 #pragma unroll 1
-            for (int bi = 0; bi < sn_steps; bi += RS) {
+            for (int bi = 0; bi < sn_steps; bi += 2) {
                 step(std::integral_constant<int, 0>{}, bi);
                 if (bi + 1 < sn_steps) step(std::integral_constant<int, 1>{}, bi + 1);
-                if constexpr (RS == 3)
-                    if (bi + 2 < sn_steps) step(std::integral_constant<int, 2 % RS>{}, bi + 2);
             }
         }
         // Row totals over the NP key parts (all at the same reference).  A total outside
