@@ -106,10 +106,10 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
         const int64_t pr = r0 + r < nq ? r0 + r : nq - 1;                      // pad rows repeat the last row
         const int64_t src = qbase + perm_row(perm, h, nq, pr) * D + c8;
         if constexpr (IN_BF16) {
-            *(u32x4*)&tq[r][c8] = *(const u32x4*)((const uint16_t*)qin + src);
+            *(u32x4*)&tq[r][c8] = __builtin_nontemporal_load((const u32x4*)((const uint16_t*)qin + src));
         } else {
-            *(f32x4*)&tq[r][c8] = *(const f32x4*)((const float*)qin + src);
-            *(f32x4*)&tq[r][c8 + 4] = *(const f32x4*)((const float*)qin + src + 4);
+            *(f32x4*)&tq[r][c8] = __builtin_nontemporal_load((const f32x4*)((const float*)qin + src));
+            *(f32x4*)&tq[r][c8 + 4] = __builtin_nontemporal_load((const f32x4*)((const float*)qin + src + 4));
         }
     }
     __syncthreads();
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void pack_k_kernel(const uint16_t* __restrict_
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int64_t r = (int64_t)blockIdx.x * 64 + 16 * w + 4 * it + g;
-        ld[it] = r < nk ? *(const u32x4*)(k + (base + r) * D + 8 * i) : u32x4{0u, 0u, 0u, 0u};
+        ld[it] = r < nk ? __builtin_nontemporal_load((const u32x4*)(k + (base + r) * D + 8 * i)) : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -242,21 +242,32 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(
 // pass treats every LDS DMA in flight as aliasing every later LDS read and puts a vmcnt(0)
 // before it, which would serialise each ring slot with the loads issued for the slots after
 // it.  The kernels order their LDS reads after the DMA themselves, with wait_vmcnt<N>.
+// NT: non-temporal (the data is read once: it should not displace cached lines others reuse).
+template <bool NT = false>
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-                 : : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+    if constexpr (NT)
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                     : : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                     : : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 
 // The same load from a wave-uniform base (kept in SGPRs) plus a 32-bit per-lane byte offset
 // voff.  (No instruction offset: on these loads it moves the LDS destination as well.)
+template <bool NT = false>
 __device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
     // readfirstlane returns int: widen each half through uint32_t so the low half is not
     // sign-extended into the high one
     const uint64_t b = (uint64_t)(uintptr_t)base;
     const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
                         (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-                 : : "v"(voff), "s"(bs), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+    if constexpr (NT)
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+                     : : "v"(voff), "s"(bs), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                     : : "v"(voff), "s"(bs), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 
 // Wave-uniform 64-bit address p - shift in an SGPR pair.
@@ -269,21 +280,38 @@ __device__ __forceinline__ uint64_t sbase(const void* p, uint32_t shift = 0) {
 // Direct global->LDS loads sharing one M0 (= LDS address lds): load i writes LDS lds + 1024 i
 // (+ lane * 16) from b_i + v_i + 1024 i.  The instruction offset moves the global and the LDS
 // address alike (checked on gfx950), so callers pass base i already lowered by 1024 i.
+template <bool NT = false>
 __device__ __forceinline__ void dma_x2(uint64_t b0, uint32_t v0, uint64_t b1, uint32_t v1, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %4\n\ts_nop 0\n\t"
-                 "global_load_lds_dwordx4 %0, %2\n\t"
-                 "global_load_lds_dwordx4 %1, %3 offset:1024"
-                 : : "v"(v0), "v"(v1), "s"(b0), "s"(b1), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+    if constexpr (NT)
+        asm volatile("s_mov_b32 m0, %4\n\ts_nop 0\n\t"
+                     "global_load_lds_dwordx4 %0, %2 nt\n\t"
+                     "global_load_lds_dwordx4 %1, %3 offset:1024 nt"
+                     : : "v"(v0), "v"(v1), "s"(b0), "s"(b1), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %4\n\ts_nop 0\n\t"
+                     "global_load_lds_dwordx4 %0, %2\n\t"
+                     "global_load_lds_dwordx4 %1, %3 offset:1024"
+                     : : "v"(v0), "v"(v1), "s"(b0), "s"(b1), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
+template <bool NT = false>
 __device__ __forceinline__ void dma_x4(uint64_t b0, uint32_t v0, uint64_t b1, uint32_t v1, uint64_t b2, uint32_t v2,
                                        uint64_t b3, uint32_t v3, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %8\n\ts_nop 0\n\t"
-                 "global_load_lds_dwordx4 %0, %4\n\t"
-                 "global_load_lds_dwordx4 %1, %5 offset:1024\n\t"
-                 "global_load_lds_dwordx4 %2, %6 offset:2048\n\t"
-                 "global_load_lds_dwordx4 %3, %7 offset:3072"
-                 : : "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(b0), "s"(b1), "s"(b2), "s"(b3),
-                   "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+    if constexpr (NT)
+        asm volatile("s_mov_b32 m0, %8\n\ts_nop 0\n\t"
+                     "global_load_lds_dwordx4 %0, %4 nt\n\t"
+                     "global_load_lds_dwordx4 %1, %5 offset:1024 nt\n\t"
+                     "global_load_lds_dwordx4 %2, %6 offset:2048 nt\n\t"
+                     "global_load_lds_dwordx4 %3, %7 offset:3072 nt"
+                     : : "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(b0), "s"(b1), "s"(b2), "s"(b3),
+                       "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %8\n\ts_nop 0\n\t"
+                     "global_load_lds_dwordx4 %0, %4\n\t"
+                     "global_load_lds_dwordx4 %1, %5 offset:1024\n\t"
+                     "global_load_lds_dwordx4 %2, %6 offset:2048\n\t"
+                     "global_load_lds_dwordx4 %3, %7 offset:3072"
+                     : : "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(b0), "s"(b1), "s"(b2), "s"(b3),
+                       "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 
 // s_waitcnt vmcnt(N): at most N vector-memory operations of this wave still in flight (they
@@ -1486,6 +1514,12 @@ constexpr int ROUTE_RS = 2;
 template <int NP>
 constexpr int route_waves_per_simd() { return NP == 1 ? 3 : 2; }
 
+// The per-(tile, leaf) state is read once per launch by route_select and once by the attend
+// kernel's far field.  Non-temporal loads keep such a stream from displacing cached lines
+// that others reuse (the K / V rows neighbouring tiles' near fields share).
+constexpr bool SEL_NT = false;
+constexpr bool FAR_NT = true;
+
 // Per-lane byte offsets of the 32-key block loads (loop invariant): the QK operand chunk of
 // lane (col, grp) and the swizzled PV row chunks (see dma_rows).
 struct BlockOffsets {
@@ -1508,21 +1542,24 @@ __device__ __forceinline__ BlockOffsets block_offsets(int lane) {
 
 // QK operand chunks j (0..3) of lane: [hh = j>>1][ks = j&1][grp][col] <- row (row0[hh] + col),
 // bytes (4ks + grp)*16 of an int8 [*, 128] matrix; x0/x1 point at rows row0a/row0b.  One M0.
+template <bool NT>
 __device__ __forceinline__ void dma_qk(const int8_t* x0, const int8_t* x1, const BlockOffsets& bo, uint32_t slot) {
-    dma_x4(sbase(x0), bo.qk[0], sbase(x0, 1024), bo.qk[1], sbase(x1, 2048), bo.qk[0], sbase(x1, 3072), bo.qk[1], slot);
+    dma_x4<NT>(sbase(x0), bo.qk[0], sbase(x0, 1024), bo.qk[1], sbase(x1, 2048), bo.qk[0], sbase(x1, 3072), bo.qk[1], slot);
 }
 
 // PV rows of a 32-key block: ring chunk s = 64j + lane (j = 0..7) holds the 16-byte chunk
 // (s % 16) ^ swz(row) of row s / 16 (rows 0..15 from x0, 16..31 from x1) of a bf16 [*, 128]
 // matrix; swz(row) = swz(row - 16), so both halves share the lane offsets.  Chunks 0, 1:
+template <bool NT>
 __device__ __forceinline__ void dma_rows01(const uint16_t* x0, const BlockOffsets& bo, uint32_t slot) {
-    dma_x2(sbase(x0), bo.rows[0], sbase(x0, 1024), bo.rows[1], slot + 4096);
+    dma_x2<NT>(sbase(x0), bo.rows[0], sbase(x0, 1024), bo.rows[1], slot + 4096);
 }
 // chunks 2..7:
+template <bool NT>
 __device__ __forceinline__ void dma_rows27(const uint16_t* x0, const uint16_t* x1, const BlockOffsets& bo,
                                            uint32_t slot) {
-    dma_x2(sbase(x0), bo.rows[2], sbase(x0, 1024), bo.rows[3], slot + 4096 + 2048);
-    dma_x4(sbase(x1), bo.rows[0], sbase(x1, 1024), bo.rows[1], sbase(x1, 2048), bo.rows[2], sbase(x1, 3072),
+    dma_x2<NT>(sbase(x0), bo.rows[2], sbase(x0, 1024), bo.rows[3], slot + 4096 + 2048);
+    dma_x4<NT>(sbase(x1), bo.rows[0], sbase(x1, 1024), bo.rows[1], sbase(x1, 2048), bo.rows[2], sbase(x1, 3072),
            bo.rows[3], slot + 8192);
 }
 
@@ -1572,9 +1609,9 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
         if (gj >= ngr) return;
         const int64_t s0 = gs * nb_pad + 16 * w + 64 * gj;
         const uint32_t slot = ring_lds + (uint32_t)(gj % SEL_RING) * SEL_SLOT;
-        dma16s(g8 + s0 * D, voff0, slot);
-        dma16s(g8 + s0 * D, voff1, slot + 1024);
-        if (lane < 8) dma16(lane < 4 ? sg + s0 + 4 * lane : lz + s0 + 4 * (lane - 4), slot + 2048);
+        dma16s<SEL_NT>(g8 + s0 * D, voff0, slot);
+        dma16s<SEL_NT>(g8 + s0 * D, voff1, slot + 1024);
+        if (lane < 8) dma16<SEL_NT>(lane < 4 ? sg + s0 + 4 * lane : lz + s0 + 4 * (lane - 4), slot + 2048);
     };
     auto sel_read = [&](SelOps& o, int gj) {
         const char* slot = &sring[w][gj % SEL_RING][0];
@@ -1758,14 +1795,15 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
     // scale area gets 32 floats from s_lo (lanes 0..7) and 32 from s_hi (lanes 8..15); a near
     // block's runs hold only 16 tokens each, so there (nlim = 3) lanes 4..7 and 12..15 repeat
     // the run's first 16 scales instead of reading past it.
-    auto load_block = [&](uint32_t slot, const int8_t* X8, const uint16_t* XV, int64_t r0, int64_t r1,
+    auto load_block = [&](auto nt_, uint32_t slot, const int8_t* X8, const uint16_t* XV, int64_t r0, int64_t r1,
                           const float* s_lo, const float* s_hi, int nlim) {
+        constexpr bool NTL = decltype(nt_)::value;
         if (hr == 0) {
-            dma_qk(X8 + r0 * D, X8 + r1 * D, bo, slot);
-            dma_rows01(XV + r0 * D, bo, slot);
-            if (lane < 16) dma16((lane < 8 ? s_lo : s_hi) + 4 * (lane & nlim), slot + 12288);
+            dma_qk<NTL>(X8 + r0 * D, X8 + r1 * D, bo, slot);
+            dma_rows01<NTL>(XV + r0 * D, bo, slot);
+            if (lane < 16) dma16<NTL>((lane < 8 ? s_lo : s_hi) + 4 * (lane & nlim), slot + 12288);
         } else {
-            dma_rows27(XV + r0 * D, XV + r1 * D, bo, slot);
+            dma_rows27<NTL>(XV + r0 * D, XV + r1 * D, bo, slot);
         }
     };
     // near block bi (list positions e_lo + 32 bi, + 16): the 16-token runs start there (past
@@ -1776,7 +1814,7 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
         const int e0 = e_lo + 32 * bi, ja = run_pos(e0), jb = run_pos(e0 + 16);
         const int64_t r0 = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[ja / LEAF]) * LEAF + (ja % LEAF);
         const int64_t r1 = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[jb / LEAF]) * LEAF + (jb % LEAF);
-        load_block(pring_lds + slot * SLOT_BYTES, k8, v, r0, r1, ks + r0, ks + r1, 3);
+        load_block(std::false_type{}, pring_lds + slot * SLOT_BYTES, k8, v, r0, r1, ks + r0, ks + r1, 3);
     };
     static_assert(RS == 2, "the far / near block stream alternates two ring slots");
     RowsN<RB> st;
@@ -1809,7 +1847,8 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
                 }
                 if (bi >= nf) return;
                 const int64_t r0 = srow0 + lo + 32 * bi;
-                load_block(pring_lds + slot * SLOT_BYTES, g8, vb, r0, r0 + 16, sg + r0, lz + r0, 7);
+                load_block(std::integral_constant<bool, FAR_NT>{}, pring_lds + slot * SLOT_BYTES, g8, vb, r0, r0 + 16,
+                           sg + r0, lz + r0, 7);
             };
             // one step per 32-leaf block; the ring slot of block bi is bi % RS, a constant in each
             // of the RS unrolled steps, so every LDS read uses an immediate offset
@@ -1881,7 +1920,7 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
                 const int e0 = e_lo + 32 * bi, ja = run_pos(e0), jb = run_pos(e0 + 16);
                 const int64_t r0 = kh + (int64_t)__builtin_amdgcn_readfirstlane(la) * LEAF + (ja % LEAF);
                 const int64_t r1 = kh + (int64_t)__builtin_amdgcn_readfirstlane(lb) * LEAF + (jb % LEAF);
-                load_block(pring_lds + slot * SLOT_BYTES, k8, v, r0, r1, ks + r0, ks + r1, 3);
+                load_block(std::false_type{}, pring_lds + slot * SLOT_BYTES, k8, v, r0, r1, ks + r0, ks + r1, 3);
             };
             auto step = [&](auto S_, int bi) {
                 constexpr int S = decltype(S_)::value;
