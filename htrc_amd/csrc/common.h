@@ -252,10 +252,17 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 
-// XOR swizzle of the 16-byte chunks of a 256-byte LDS row: row r keeps chunk c at c ^ swz(r).
-// 16 consecutive rows read at one chunk hit 16 different chunks (QK operand reads), and
-// 8 consecutive rows read at a chunk pair hit 16 different chunks (transposing reads).
-__device__ __forceinline__ int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+// XOR swizzle of the 16-byte chunks of a 256-byte LDS row: row r keeps chunk c at c ^ swz(r),
+// a linear map of r's low four bits (period 16).  Both read patterns on such rows are free of
+// bank conflicts whether the LDS serves 128 or 256 bytes per cycle: the 16-byte QK operand
+// reads (rows r0 .. r0 + 15 at one chunk: every 8 consecutive rows hit 8 different chunks
+// modulo 8, all 16 rows 16 different chunks) and the transposing reads (4 or 8 consecutive
+// rows at a chunk pair: 8 or 16 different chunks).  The previous swizzle, 2 (r & 7) + (r >> 3),
+// left rows r and r + 4 on one bank group for the QK reads, which the LDS serves 8 lanes
+// (128 bytes) at a time: measured, 9.9e7 conflict cycles per stats launch at cfg3.
+__device__ __forceinline__ int swz(int r) {
+    return ((r & 3) << 1) | ((r >> 2) & 1) | ((((r >> 2) ^ (r >> 3)) & 1) << 3);
+}
 
 // Order-preserving uint32 key of a float (larger float -> larger key); -0 maps to +0.
 __device__ __forceinline__ uint32_t order_key(float f) {
