@@ -35,39 +35,54 @@ PEAK_I8_TOPS = 5000.0          # dense int8 MFMA, TOP/s
 PEAK_BF16_TFLOPS = 2500.0      # dense bf16 MFMA, TFLOP/s
 
 
-def algorithmic(h, nq, nk, leaf, kx, d=128, tile=64):
+def algorithmic(h, nq, nk, leaf, kx, d=128, tile=64, store="int8"):
     """Per-launch algorithmic HBM bytes and MFMA ops of every kernel of one layer call.
     Each operand is counted once per launch (near-field K/V once per head: adjacent tiles
-    share leaves in L2); the per-(tile, leaf) state is g8 d + vb 2d + sg 4 + lz 4 bytes."""
+    share leaves in L2).  Per (tile, leaf) the state is, for store="int8", g8 d + vb 2d + sg 4
+    + lz 4 bytes (select reads g8, sg, lz); "fp8": g d + vb d + sg, sv, lz 12; "bf16": g 2d +
+    vb 2d + lz 4 (select reads g and lz).  The int8 path's query rows are int8 + a scale (d + 4
+    bytes) and its near field reads k8, ks, v (3d + 4 per token); the 16-bit paths read bf16 /
+    fp16 rows (2d) and bf16 k, v (4d), and all their products are 16-bit MFMA flops."""
     nt = -(-nq // tile)
     nb = nk // leaf
     rows = nt * tile
     kx = min(kx, nb)
-    state = nt * nb * (3 * d + 8)
+    i8 = store == "int8"
+    per_state = {"int8": 3 * d + 8, "fp8": 2 * d + 12, "bf16": 4 * d + 4}[store]
+    per_sel = {"int8": d + 8, "fp8": d + 8, "bf16": 2 * d + 4}[store]
+    row = d + 4 if i8 else 2 * d
+    tok = 3 * d + 4 if i8 else 4 * d
+    state = nt * nb * per_state
+    far_ops, near_ops = 2 * rows * nb * d, 2 * rows * kx * leaf * d
+
+    def ops(qk):
+        # the PV products match the QK products in count: int8 QK and bf16 PV on the int8
+        # path, both 16-bit on the others
+        return {"i8_ops": h * qk, "bf16_flops": h * qk} if i8 else {"i8_ops": 0, "bf16_flops": 2 * h * qk}
+
     f = {}
-    f["pack_q"] = {"bytes": h * (2 * nq * d + 2 * rows * d + 8 * rows + 4 * nt * d)}
-    f["pack_k"] = {"bytes": h * (2 * nk * d + nk * d + 4 * nk)}
+    f["pack_q"] = {"bytes": h * (2 * nq * d + 2 * rows * row + 4 * nt * d)}
+    if i8:
+        f["pack_k"] = {"bytes": h * (2 * nk * d + nk * d + 4 * nk)}
     f["stats"] = {"bytes": h * (4 * nk * d + state + 4 * nt * d)}
-    f["route_select"] = {"bytes": h * (nt * nb * (d + 8) + rows * (d + 4) + nt * kx * 4 + rows * 4),
-                         "i8_ops": h * 2 * rows * nb * d, "bf16_flops": 0}
-    f["route_attend"] = {"bytes": h * (state + 2 * rows * (d + 4) + nk * (3 * d + 4) + nt * kx * 4 + rows * 4
-                                       + 4 * nq * (d + 1)),
-                         "i8_ops": h * (2 * rows * nb * d + 2 * rows * kx * leaf * d),
-                         "bf16_flops": h * (2 * rows * nb * d + 2 * rows * kx * leaf * d)}
+    f["route_select"] = {"bytes": h * (nt * nb * per_sel + rows * row + nt * kx * 4 + rows * 4),
+                         **({"i8_ops": h * far_ops, "bf16_flops": 0} if i8 else {"i8_ops": 0, "bf16_flops": h * far_ops})}
+    f["route_attend"] = {"bytes": h * (state + 2 * rows * row + nk * tok + nt * kx * 4 + rows * 4 + 4 * nq * (d + 1)),
+                         **ops(far_ops + near_ops)}
     # the attend launch split into its two fields: far (every leaf's state, kx = 0) and near (the
     # exact tokens of the kx near leaves, timed as the difference)
-    f["far_field"] = {"bytes": h * (state + rows * (d + 4) + rows * 4 + 4 * nq * (d + 1)),
-                      "i8_ops": h * 2 * rows * nb * d, "bf16_flops": h * 2 * rows * nb * d}
-    f["near_field"] = {"bytes": h * (rows * (d + 4) + nk * (3 * d + 4) + nt * kx * 4),
-                       "i8_ops": h * 2 * rows * kx * leaf * d, "bf16_flops": h * 2 * rows * kx * leaf * d}
+    f["far_field"] = {"bytes": h * (state + rows * row + rows * 4 + 4 * nq * (d + 1)), **ops(far_ops)}
+    f["near_field"] = {"bytes": h * (rows * row + nk * tok + nt * kx * 4), **ops(near_ops)}
     return f
 
 
-def measured_traffic(config):
+def measured_traffic(config, store="int8"):
     """HBM bytes per launch of each kernel, measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes
     (scaled by a copy kernel of known size) and committed in profiles/flat_kernels_<config>.md
-    as a JSON block; {} when there is no such summary."""
-    path = ROOT / "profiles" / f"flat_kernels_{config}.md"
+    (profiles/flat_kernels_<config>_<store>.md for the 16-bit stores) as a JSON block; {} when
+    there is no such summary."""
+    name = config if store == "int8" else f"{config}_{store}"
+    path = ROOT / "profiles" / f"flat_kernels_{name}.md"
     try:
         text = path.read_text()
         block = text.split("```json", 1)[1].split("```", 1)[0]
@@ -284,6 +299,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--store", default="int8", choices=["int8", "fp8", "bf16"],
+                    help="leaf-state store of the layer (BASELINE's metric is quoted on int8)")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--calls", type=int, default=50, help="cfg5: sequential layer calls")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -313,8 +330,9 @@ def main():
     # the tile window the production runner plans for this layer and the free device memory
     # (h3/htrc_flat_runner.py:71-82): the whole layer in one window when it fits
     chunk = htrc_flat_runner.plan_chunk(torch.cuda.mem_get_info(dev)[0], nk, 64, leaf=leaf, queries=nq, heads=h,
-                                        exact_leaves=kx, graph=False)
-    kw = dict(backend="hip", store="int8", dot="bf16", leaf=leaf, exact_leaves=ex, tile_chunk=chunk,
+                                        exact_leaves=kx, graph=False, store=a.store)
+    store = a.store
+    kw = dict(backend="hip", store=store, dot="bf16", leaf=leaf, exact_leaves=ex, tile_chunk=chunk,
               kern={"fused": True})
 
     def layer_ms(kwargs, steps, warmup):
@@ -337,23 +355,31 @@ def main():
 
     # per-kernel launch durations, HIP events on the stream the kernels are launched on
     scale = 1.0 / math.sqrt(d)
-    mu, q8, sq, dq8, sdq = hip.pack_q(q, ws=ws)
-    k8, ks = hip.pack_k(k, ws=ws)
-    g8, lz, vbs, sg, _ = hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws)
-    packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "v": v}
-    lstate = {"g8": g8, "sg": sg, "lz": lz, "vb": vbs}
-    idx, rowmax = hip.route_select(packed, lstate, nq=nq, leaf=leaf, kx=kx, ws=ws)
-    stages = {
-        "pack_q": lambda: hip.pack_q(q, ws=ws),
-        "pack_k": lambda: hip.pack_k(k, ws=ws),
-        "stats": lambda: hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws),
-        "route_select": lambda: hip.route_select(packed, lstate, nq=nq, leaf=leaf, kx=kx, ws=ws),
-        "route_attend": lambda: hip.route_attend(packed, lstate, idx, rowmax, nq=nq, leaf=leaf, kx=kx, scale=scale,
-                                                 ws=ws),
+    if store == "int8":
+        mu, q8, sq, dq8, sdq = hip.pack_q(q, ws=ws)
+        k8, ks = hip.pack_k(k, ws=ws)
+        g8, lz, vbs, sg, _ = hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws)
+        packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "v": v}
+        lstate = {"g8": g8, "sg": sg, "lz": lz, "vb": vbs}
+        sel, att = hip.route_select, hip.route_attend
+        stages = {"pack_q": lambda: hip.pack_q(q, ws=ws), "pack_k": lambda: hip.pack_k(k, ws=ws),
+                  "stats": lambda: hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, ws=ws)}
+    else:
+        sdt = torch.float8_e4m3fn if store == "fp8" else torch.bfloat16
+        mu, q16, dq16 = hip.pack_q16(q, ws=ws, dq_fp16=store == "fp8")
+        g, lz, vbs, sg, sv = hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, store=sdt, ws=ws)
+        packed = {"q16": q16, "dq16": dq16, "k": k, "v": v}
+        lstate = {"g8": g, "sg": sg, "lz": lz, "vb": vbs, "sv": sv}
+        sel, att = hip.route16_select, hip.route16_attend
+        stages = {"pack_q": lambda: hip.pack_q16(q, ws=ws, dq_fp16=store == "fp8"),
+                  "stats": lambda: hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, store=sdt, ws=ws)}
+    idx, rowmax = sel(packed, lstate, nq=nq, leaf=leaf, kx=kx, ws=ws)
+    stages.update({
+        "route_select": lambda: sel(packed, lstate, nq=nq, leaf=leaf, kx=kx, ws=ws),
+        "route_attend": lambda: att(packed, lstate, idx, rowmax, nq=nq, leaf=leaf, kx=kx, scale=scale, ws=ws),
         # the attend launch with no near leaves: the far field alone (the near field is the difference)
-        "far_field": lambda: hip.route_attend(packed, lstate, None, rowmax, nq=nq, leaf=leaf, kx=0, scale=scale,
-                                              ws=ws),
-    }
+        "far_field": lambda: att(packed, lstate, None, rowmax, nq=nq, leaf=leaf, kx=0, scale=scale, ws=ws),
+    })
     kms = {}
     stream = torch.cuda.current_stream(dev)
     for name, fn in stages.items():
@@ -375,7 +401,7 @@ def main():
         torch.bitwise_not(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
-    figs = algorithmic(h, nq, nk, leaf, kx, d)
+    figs = algorithmic(h, nq, nk, leaf, kx, d, store=store)
     kms["near_field"] = max(kms["route_attend"] - kms["far_field"], 1e-6)
     kernels = {n: roofline_entry(n, kms[n], figs[n]) for n in list(stages) + ["near_field"]}
     peaks = measured_peaks(dev)
@@ -385,7 +411,7 @@ def main():
             t = figs[n]["i8_ops"] / (peaks["int8_gemm_TOPs"] * 1e12) + figs[n]["bf16_flops"] / (
                 peaks["bf16_gemm_TFLOPs"] * 1e12)
             e["mfma_frac_measured"] = round(t / (e["ms"] * 1e-3), 4)
-    traffic = measured_traffic(a.config)
+    traffic = measured_traffic(a.config, store)
     for n, e in kernels.items():
         e["traffic"] = traffic.get(n)
     dom = max((e for n, e in kernels.items() if n not in ("far_field", "near_field")), key=lambda e: e["ms"])
@@ -407,13 +433,18 @@ def main():
     elif "mfma_frac_measured" in dom:
         roof["frac_measured"] = dom["mfma_frac_measured"]
     # BASELINE's metric is quoted on cfg3; the other layer configurations carry their own shape
-    metric = METRIC if a.config == "cfg3" else f"flat-HTRC layer ms/call @B1 H{h} N{nq} d{d} ({a.config}); % MFMA peak, HBM GB/s"
+    tag = a.config if store == "int8" else f"{a.config}, store={store}"
+    metric = (METRIC if tag == "cfg3" else
+              f"flat-HTRC layer ms/call @B1 H{h} N{nq} d{d} ({tag}); % MFMA peak, HBM GB/s")
+    dtype = {"int8": "i8/bf16 (fp32 accumulate)", "fp8": "e4m3 state, fp16/bf16 MFMA (fp32 accumulate)",
+             "bf16": "bf16 (fp32 accumulate)"}[store]
     res = {"metric": metric, "value": round(ms, 4), "unit": "ms/call", "n_gpus": 1, "steps": a.steps,
            "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
-           "vs_baseline": None, "dtype": "i8/bf16 (fp32 accumulate)",
+           "vs_baseline": None, "dtype": dtype,
            "data": "synthetic: clustered spatiotemporal regions, seed 0, generated on device",
-           "config": {"workload": f"{a.config}: B=1 H={h} N={nq} d={d} leaf={leaf} near={kx} tile=64",
-                      "heads": h, "queries": nq, "keys": nk, "leaf": leaf, "near_leaves": kx, "tile_chunk": chunk},
+           "config": {"workload": f"{a.config}: B=1 H={h} N={nq} d={d} leaf={leaf} near={kx} tile=64 store={store}",
+                      "heads": h, "queries": nq, "keys": nk, "leaf": leaf, "near_leaves": kx, "tile_chunk": chunk,
+                      "store": store},
            "ms_tile_chunk_128": round(ms_prod_windows, 4),
            "roofline": roof, "kernels": kernels, "measured_peaks": peaks}
     if not a.no_cpu_baseline:

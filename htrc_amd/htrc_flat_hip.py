@@ -418,32 +418,61 @@ def route_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, 
     return out, logz
 
 
+def _r16(packed: dict, state: dict, nq: int, tile: int, group: int, g0: int, leaf: int, kx: int):
+    """Shared shapes of the 16-bit route launches."""
+    q16, dq16, k, v = packed["q16"], packed["dq16"], packed["k"], packed["v"]
+    g, sg, lz, vb, sv = state["g8"], state.get("sg"), state["lz"], state["vb"], state.get("sv")
+    fp8 = g.dtype == torch.float8_e4m3fn
+    h, nk, d = (int(x) for x in k.shape)
+    tile = _tile(tile)
+    nt = -(-int(nq) // tile)
+    g0, gn, _, _ = _tile_window(nq, tile, group, g0, int(lz.shape[1]))
+    kxe = min(int(kx), nk // int(leaf))
+    return q16, dq16, k, v, g, sg, lz, vb, sv, fp8, h, nk, d, tile, nt, g0, gn, kxe
+
+
+def route16_select(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, sink: int = 0, stride: int = 1,
+                   ws=None, idx=None, group: int = 1, tile: int = TILE, g0: int = 0):
+    """First launch of route16 (16-bit state stores): select -> top-k per tile group of the
+    window -> (idx [H,gn,min(kx,nb)] int32 or None, rowmax [H,nt*tile] fp32, each row's largest
+    far-field score, the attend launch's fixed softmax reference)."""
+    q16, dq16, k, v, g, sg, lz, vb, sv, fp8, h, nk, d, tile, nt, g0, gn, kxe = _r16(packed, state, nq, tile, group,
+                                                                                    g0, leaf, kx)
+    dev = dq16.device
+    if idx is None and kxe > 0:
+        idx = _rows(ws, "idx", h, gn, (kxe,), torch.int32, dev)
+    rowmax = _buf(ws, "rowmax", (h, nt * tile), torch.float32, dev)
+    call("htrc_route16_select", ptr(dq16), ptr(g), ptr(sg), ptr(lz), h, nq, nk, int(leaf), d, int(kx), int(sink),
+         int(stride), tile, int(group), g0, gn, int(fp8), ptr(idx), ptr(rowmax), stream_handle(dev))
+    return (idx if kxe > 0 else None), rowmax
+
+
+def route16_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int, kx: int, scale: float, ws=None,
+                   out=None, logz=None, group: int = 1, perm=None, tile: int = TILE, g0: int = 0):
+    """Second launch of route16: far + near field with the row reference rowmax -> (out, logz)."""
+    q16, dq16, k, v, g, sg, lz, vb, sv, fp8, h, nk, d, tile, nt, g0, gn, kxe = _r16(packed, state, nq, tile, group,
+                                                                                    g0, leaf, kx)
+    dev = q16.device
+    if out is None:
+        out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
+    if logz is None:
+        logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
+    call("htrc_route16_attend", ptr(q16), ptr(dq16), ptr(g), ptr(sg), ptr(lz), ptr(vb), ptr(sv), ptr(k), ptr(v),
+         ptr(idx), ptr(rowmax), h, nq, nk, int(leaf), d, int(kx), tile, int(group), g0, gn, ptr(perm), int(fp8),
+         float(scale), ptr(out), ptr(logz), stream_handle(dev))
+    return out, logz
+
+
 def route16(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: float, sink: int = 0, stride: int = 1,
             ws=None, out=None, logz=None, idx=None, group: int = 1, perm=None, tile: int = TILE, g0: int = 0):
     """Fused route of the 16-bit state stores (select -> top-k, then far + near in one softmax; two
     launches) for the tiles of the gn = state["lz"].shape[1] groups from g0: packed holds q16,
     dq16 (pack_q16) and the bf16 k, v; state g8 / vb (e4m3 with sg, sv; or bf16) and lz
     -> (out [H,nq,D], logz [H,nq]); idx [H,gn,min(kx,nb)] receives the window's routing."""
-    q16, dq16, k, v = packed["q16"], packed["dq16"], packed["k"], packed["v"]
-    g, sg, lz, vb, sv = state["g8"], state.get("sg"), state["lz"], state["vb"], state.get("sv")
-    fp8 = g.dtype == torch.float8_e4m3fn
-    h, nk, d = (int(x) for x in k.shape)
-    dev = q16.device
-    tile = _tile(tile)
-    nt = -(-int(nq) // tile)
-    g0, gn, _, _ = _tile_window(nq, tile, group, g0, int(lz.shape[1]))
-    kxe = min(int(kx), nk // int(leaf))
-    if out is None:
-        out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
-    if logz is None:
-        logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
-    if idx is None and kxe > 0:
-        idx = _rows(ws, "idx", h, gn, (kxe,), torch.int32, dev)
-    rowmax = _buf(ws, "rowmax", (h, nt * tile), torch.float32, dev)
-    call("htrc_route16", ptr(q16), ptr(dq16), ptr(g), ptr(sg), ptr(lz), ptr(vb), ptr(sv), ptr(k), ptr(v), h, nq, nk,
-         int(leaf), d, int(kx), int(sink), int(stride), tile, int(group), g0, gn, ptr(perm), int(fp8), float(scale),
-         ptr(out), ptr(logz), ptr(idx), ptr(rowmax), stream_handle(dev))
-    return out, logz
+    idx, rowmax = route16_select(packed, state, nq=nq, leaf=leaf, kx=kx, sink=sink, stride=stride, ws=ws, idx=idx,
+                                 group=group, tile=tile, g0=g0)
+    return route16_attend(packed, state, idx, rowmax, nq=nq, leaf=leaf, kx=kx, scale=scale, ws=ws, out=out,
+                          logz=logz, group=group, perm=perm, tile=tile, g0=g0)
 
 
 def route16_fits(nb: int, kx: int) -> bool:

@@ -81,6 +81,9 @@ def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, hea
     if not bf16_inputs:
         layer += 2 * 2 * keys * dim                                     # bf16 copies of k and v
     window = gw * nbp * per_state + 4 * gw * kx                         # state, idx
+    # the fused route takes up to 8192 near leaves, and 262144 leaves per head (int8; its top-k
+    # keys past 16384 in workspace) or 16384 (the 16-bit stores); larger layers run the stage path
+    fused = fused and kx <= 8192 and nb <= (262144 if store == "int8" else 16384)
     if fused and nb > 16384:
         window += 4 * gw * nbp                                          # route_select top-k keys
     if not fused:

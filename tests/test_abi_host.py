@@ -234,6 +234,22 @@ def test_runner_and_its_replay_form_no_reference_cycle(monkeypatch):
         gc.enable()
 
 
+def test_memory_model_follows_the_route_limits():
+    """Layers the fused route does not take run the stage path; the model counts its SEL / excl
+    buffers then (and the int8 route's top-k key workspace past 16384 leaves)."""
+    wb = htrc_flat_runner.workspace_bytes
+    for store in ("fp8", "bf16"):
+        # 20000 leaves of 16 keys: over the 16-bit route's 16384, so fused=True sizes the stage path
+        assert wb(2048, 320000, leaf=16, kx=64, store=store, fused=True) == \
+            wb(2048, 320000, leaf=16, kx=64, store=store, fused=False, splits=1)
+        assert wb(2048, 4096, leaf=16, kx=64, store=store, fused=True) < \
+            wb(2048, 4096, leaf=16, kx=64, store=store, fused=False, splits=1)
+    # int8 at 20000 leaves stays fused: 32 centres x 20000 leaves of 4-byte top-k keys, against the
+    # stage path's 5 bytes of SEL and excl
+    assert wb(2048, 320000, leaf=16, kx=64, store="int8", fused=False, splits=1) - \
+        wb(2048, 320000, leaf=16, kx=64, store="int8", fused=True) == 32 * 20000 * (5 - 4)
+
+
 def test_runner_plan_merges_knobs():
     """PROD, then the mode, then the caller's knobs with kern merged key by key; the window from
     free_bytes steps down through CHUNKS."""

@@ -364,6 +364,34 @@ def test_dequant_rows_all_patterns(device, out_dtype):
     torch.testing.assert_close(out.cpu(), want, rtol=0, atol=0, equal_nan=True)
 
 
+@pytest.mark.parametrize("store", ["fp8", "bf16"])
+def test_route16_one_entry_equals_two_launches(device, store):
+    """htrc_route16 (one C call) gives exactly htrc_route16_select + htrc_route16_attend (the
+    wrappers route16_select / route16_attend), sinks and sampled rows included."""
+    from htrc_amd import _lib
+    n, leaf, ex, sink, stride = 64 * 21 + 5, 64, 6, 2, 4
+    q, k, v = _data(n, nk=64 * 24, seed=91)
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=ex, splits=1, bn=64,
+                          sel_stride=stride, sink_leaves=sink, store=store)
+    packed, state, _, _ = (_fp8_state if store == "fp8" else _bf16_state)(ref, k, v, device)
+    kx = ref["idx"].shape[1]
+    scale = 1 / math.sqrt(128)
+    idx, rowmax = hip.route16_select(packed, state, nq=n, leaf=leaf, kx=kx, sink=sink, stride=stride)
+    out1, lz1 = hip.route16_attend(packed, state, idx, rowmax, nq=n, leaf=leaf, kx=kx, scale=scale)
+    out1, lz1, idx1 = out1.clone(), lz1.clone(), idx.clone()
+    out2, lz2 = torch.empty_like(out1), torch.empty_like(lz1)
+    idx2, rm2 = torch.empty_like(idx1), torch.empty_like(rowmax)
+    _lib.call("htrc_route16", _lib.ptr(packed["q16"]), _lib.ptr(packed["dq16"]), _lib.ptr(state["g8"]),
+              _lib.ptr(state["sg"]), _lib.ptr(state["lz"]), _lib.ptr(state["vb"]), _lib.ptr(state["sv"]),
+              _lib.ptr(packed["k"]), _lib.ptr(packed["v"]), 1, n, 64 * 24, leaf, 128, kx, sink, stride, 64, 1, 0,
+              int(state["lz"].shape[1]), None, int(store == "fp8"), scale, _lib.ptr(out2), _lib.ptr(lz2),
+              _lib.ptr(idx2), _lib.ptr(rm2), _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    assert torch.equal(idx1, idx2) and torch.equal(rowmax, rm2)
+    assert torch.equal(out1, out2) and torch.equal(lz1, lz2)
+    assert np.array_equal(_np(idx1[0])[:, :sink], np.broadcast_to(np.arange(sink), (idx1.shape[1], sink)))
+
+
 def test_e4m3_widening_all_codes(device):
     """The route kernels' e4m3 -> fp16 widening (gfx950 conversion instruction, scale 2^-8) against
     the exact field shift and torch's float8_e4m3fn decode times 2^-8, on every finite code in
