@@ -240,13 +240,15 @@ def exact_attention(q, k, v, scale, chunk=4096):
 
 def sweep_cfg5(calls=50, warmup=2, leaves=(32, 64, 128), nears=(16, 32, 64), stores=("int8", "bf16"), reps=5):
     """`calls` sequential cfg2-shape layer calls on fresh seeded inputs
-    (total ms) and the ablation grid, each point's error against exact softmax attention."""
+    (total ms) and the ablation grid, each point's error against exact softmax attention.  Every
+    call runs the layer in one tile window (tile_chunk 1024), as the reference's own sweep sets
+    it (tools/sweep_h3_flat_kernels.py:244)."""
     import torch
     from htrc_amd import htrc_flat, workloads
     dev = torch.device("cuda:0")
     data = [workloads.make("cfg2", seed=s, device=dev) for s in range(calls)]
     _, _, _, leaf0, ex0 = data[0]
-    kw = dict(backend="hip", store="int8", dot="bf16", leaf=leaf0, exact_leaves=ex0)
+    kw = dict(backend="hip", store="int8", dot="bf16", leaf=leaf0, exact_leaves=ex0, tile_chunk=1024)
     ws = {}
     for j in range(warmup):
         q, k, v = data[j % calls][:3]
@@ -266,7 +268,7 @@ def sweep_cfg5(calls=50, warmup=2, leaves=(32, 64, 128), nears=(16, 32, 64), sto
     for leaf in leaves:
         for near in nears:
             for store in stores:
-                kwp = dict(backend="hip", store=store, dot="bf16", leaf=leaf, exact_leaves=near)
+                kwp = dict(backend="hip", store=store, dot="bf16", leaf=leaf, exact_leaves=near, tile_chunk=1024)
                 wsp = {}
                 out, lz = htrc_flat.flat_attention(q, k, v, ws=wsp, return_logz=True, **kwp)
                 a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

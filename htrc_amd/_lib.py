@@ -70,13 +70,20 @@ def lib():
             fn.restype = res
         if L.htrc_abi_version() != ABI_VERSION:
             raise RuntimeError(f"libhtrc_flat ABI {L.htrc_abi_version()} != expected {ABI_VERSION}; rebuild")
+        _fns.clear()
         _lib = L
     return _lib
 
 
+_fns: dict = {}
+
+
 def call(name: str, *args) -> None:
     """Call a launcher; map HTRC_ERR_ARG to ValueError and HTRC_ERR_HIP to HTRCLaunchError."""
-    rc = getattr(lib(), name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(lib(), name)
+    rc = fn(*args)
     if rc != 0:
         msg = lib().htrc_last_error().decode()
         if rc == 1:
@@ -84,12 +91,22 @@ def call(name: str, *args) -> None:
         raise HTRCLaunchError(msg)
 
 
-def ptr(t) -> ctypes.c_void_p | None:
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+def ptr(t) -> int | None:
+    """Device address of a tensor (ctypes takes the int for a void* parameter), None for None."""
+    return None if t is None else t.data_ptr()
 
 
-def stream_handle(device=None) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+def stream_handle(device=None) -> int:
+    """The current HIP stream of the device (torch's), as a void* for the launchers.  Small
+    layers are bound by host time per call, so this takes torch's raw-stream query directly
+    when the build has it."""
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        if isinstance(device, torch.device) and device.index is not None:
+            return raw(device.index)
+        if isinstance(device, int):
+            return raw(device)
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 def nb_pad(nb: int) -> int:
