@@ -2747,6 +2747,54 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
         ((float*)out)[i] = y;
 }
 
+// ---------------------------------------------------------------------------------------------
+// fake_quant: the reference's accuracy simulation (h3/htrc_flat.py:68-96): each group of gsz
+// consecutive values round-trips through a low-bit format with one symmetric scale s =
+// max(max|x|, 1e-20) / qmax of the group: int8 / int4 (qmax 127 / 7): rint(x / s) clamped to
+// +-qmax, times s; fp8 (448): the e4m3fn code of x / s clamped to +-448 (nearest even), decoded,
+// times s; fp4 (6): the e2m1 magnitude {0, .5, 1, 1.5, 2, 3, 4, 6} chosen by the thresholds
+// {.25, .75, 1.25, 1.75, 2.5, 3.5, 5} (a value on a threshold takes the lower magnitude), with
+// x's sign, times s.  Divisions and products are single IEEE fp32 operations, as the torch ops
+// are.  One thread per group (groups of 16 .. 128 values: two passes over data in cache).
+// ---------------------------------------------------------------------------------------------
+enum FakeQuantFmt { FQ_INT8 = 0, FQ_INT4 = 1, FQ_FP8 = 2, FQ_FP4 = 3 };
+
+template <bool IN_BF16, bool OUT_BF16>
+__global__ __launch_bounds__(256) void fake_quant_kernel(const void* __restrict__ x, int64_t groups, int gsz, int fmt,
+                                                         void* __restrict__ out) {
+    const int64_t gi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gi >= groups) return;
+    const int64_t base = gi * gsz;
+    auto ld = [&](int j) {
+        return IN_BF16 ? bf2f(((const uint16_t*)x)[base + j]) : ((const float*)x)[base + j];
+    };
+    float amax = 0.0f;
+    for (int j = 0; j < gsz; ++j) amax = fmaxf(amax, fabsf(ld(j)));
+    amax = fmaxf(amax, 1e-20f);
+    const float qmax = fmt == FQ_INT8 ? 127.0f : fmt == FQ_INT4 ? 7.0f : fmt == FQ_FP8 ? 448.0f : 6.0f;
+    const float sc = __fdiv_rn(amax, qmax);
+    for (int j = 0; j < gsz; ++j) {
+        const float y = ld(j);
+        const float t = __fdiv_rn(y, sc);
+        float r;
+        if (fmt == FQ_INT8 || fmt == FQ_INT4) {
+            r = fminf(fmaxf(rintf(t), -qmax), qmax);
+        } else if (fmt == FQ_FP8) {
+            r = e4m3_to_f32(f32_to_e4m3(fminf(fmaxf(t, -448.0f), 448.0f)));
+        } else {
+            const float a = fabsf(t);
+            const float m = a <= 0.25f ? 0.0f : a <= 0.75f ? 0.5f : a <= 1.25f ? 1.0f : a <= 1.75f ? 1.5f
+                          : a <= 2.5f ? 2.0f : a <= 3.5f ? 3.0f : a <= 5.0f ? 4.0f : 6.0f;
+            r = y > 0.0f ? m : (y < 0.0f ? -m : 0.0f);
+        }
+        const float o = __fmul_rn(r, sc);
+        if (OUT_BF16)
+            ((uint16_t*)out)[base + j] = (uint16_t)f2bf(o);
+        else
+            ((float*)out)[base + j] = o;
+    }
+}
+
 __global__ __launch_bounds__(64) void selftest_mfma_kernel(const int8_t* __restrict__ ai, const int8_t* __restrict__ bi,
                                                            int32_t* __restrict__ ci, const uint16_t* __restrict__ af,
                                                            const uint16_t* __restrict__ bf, float* __restrict__ cf) {
@@ -3561,6 +3609,29 @@ int htrc_dequant_rows(const uint8_t* x8, int64_t stride_x, const float* scale, i
         hipLaunchKernelGGL(dequant_kernel<false>, dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, x8,
                            stride_x, scale, stride_s, rows, d, out);
     return launched("htrc_dequant_rows");
+}
+
+int htrc_fake_quant(const void* x, int x_is_bf16, int64_t rows, int d, int group, int fmt, void* out, int out_is_bf16,
+                    void* stream) {
+    REQUIRE(x && out, "htrc_fake_quant: null pointer");
+    REQUIRE(fmt >= FQ_INT8 && fmt <= FQ_FP4, "htrc_fake_quant: unknown quant format");
+    REQUIRE(rows >= 0 && d > 0 && group > 0 && group <= 4096 && d % group == 0,
+            "htrc_fake_quant: quant group must divide the feature size");
+    REQUIRE(rows * (int64_t)d <= ((int64_t)1 << 40), "htrc_fake_quant: too many elements");
+    if (rows == 0) return HTRC_OK;
+    const int64_t groups = rows * (d / group);
+    const int64_t nblk = (groups + 255) / 256;
+    REQUIRE(nblk <= 0x7fffffff, "htrc_fake_quant: too many groups for one launch");
+#define FQ_LAUNCH(I, O)                                                                                         \
+    hipLaunchKernelGGL((fake_quant_kernel<I, O>), dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, x, groups, \
+                       group, fmt, out)
+    if (x_is_bf16) {
+        if (out_is_bf16) FQ_LAUNCH(true, true); else FQ_LAUNCH(true, false);
+    } else {
+        if (out_is_bf16) FQ_LAUNCH(false, true); else FQ_LAUNCH(false, false);
+    }
+#undef FQ_LAUNCH
+    return launched("htrc_fake_quant");
 }
 
 int htrc_selftest_f32_e4m3(const float* x, int64_t n, uint8_t* cvt, uint8_t* soft, void* stream) {

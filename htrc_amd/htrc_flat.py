@@ -28,6 +28,26 @@ from . import htrc_flat_hip as hip
 from ._lib import nb_pad
 
 
+def fake_quant(x, fmt, group=0):
+    """Round-trip x [..., D] through a low-bit format with symmetric per-group scales
+    (h3/htrc_flat.py:68-96): group=0 is one scale per row; fmt int8, int4, fp8 (e4m3) or fp4
+    (e2m1, default group 16).  A simulation of low-bit operands (their accuracy cost), run by
+    the HIP kernel ``htrc_fake_quant`` on the device -> fp32 of x's shape."""
+    shape = x.shape
+    d = int(shape[-1])
+    if fmt == "fp4" and not group:
+        group = 16
+    gsz = d if not group else int(group)
+    if gsz < 1 or d % gsz:
+        raise ValueError("quant group must divide the feature size")
+    if fmt not in hip.FAKE_QUANT_FMTS:
+        raise ValueError(f"unknown quant format {fmt}")
+    if not x.is_cuda:
+        raise ValueError("fake_quant runs on the HIP device (this build has no CPU path)")
+    xin = x if x.dtype in (torch.float32, torch.bfloat16) else x.float()
+    return hip.fake_quant(xin.contiguous(), gsz, fmt)
+
+
 def kmeans_order(q, clusters=32, sample=4096, iters=8):
     """Permutation grouping queries by a small k-means (h3/htrc_flat.py:47-61): Lloyd's k-means
     on an even sample, every query to its nearest centre, stable order by centre.  q [N, D]
@@ -67,7 +87,14 @@ def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot
     if order not in ("seq", "kmeans"):
         raise ValueError("order must be seq or kmeans")
     if quant:
-        raise ValueError("quant (fake-quant simulation) is not implemented on the HIP backend")
+        if not isinstance(quant, dict) or set(quant) - {"q", "kv", "state", "group"}:
+            raise ValueError("quant is a dict of 'q', 'kv', 'state' (formats) and 'group'")
+        for key in ("q", "kv", "state"):
+            if quant.get(key) and quant[key] not in hip.FAKE_QUANT_FMTS:
+                raise ValueError(f"unknown quant format {quant[key]}")
+        if quant.get("state") and store != "bf16":
+            # h3/htrc_flat.py:209-210: the int8 / fp8 stores take no state fake-quant
+            raise ValueError(f"store={store!r} needs dot='bf16', select='max' and no state fake-quant")
     if tail is not None:
         if not isinstance(tail, (tuple, list)) or len(tail) != 2:
             raise ValueError("tail must be (tail_keys, tail_values)")
@@ -166,6 +193,13 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     if stride < 1 or tile % stride:
         raise ValueError(f"sel_stride must divide the tile ({tile})")
     group = max(1, int(kern.get("group", 1)))           # G consecutive tiles share one centre
+    quant = dict(quant or {})
+    qg = int(quant.get("group", 0))
+    if quant.get("kv"):                                  # h3/htrc_flat.py:190-195
+        kh = fake_quant(kh, quant["kv"], qg)
+        vh = fake_quant(vh, quant["kv"], qg)
+    if quant.get("q"):
+        qh = fake_quant(qh, quant["q"], qg)
     if qh.dtype not in (torch.float32, torch.bfloat16):
         qh = qh.float()
     perm = hip.kmeans_order(qh, ws=ws) if order == "kmeans" else None   # query rows regrouped by k-means
@@ -192,6 +226,11 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     keep = _Collect(state, h, ng, len(wins))
     for g0, gn in wins:
         g, lz, vbs, sg, sv = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=sdt, ws=ws, c0=g0, cn=gn)
+        if quant.get("state"):                           # h3/htrc_flat.py:246-248, in place
+            sfmt = quant["state"]
+            sgsz = hip.D if not qg and sfmt != "fp4" else (qg or 16)
+            hip.fake_quant(g, sgsz, sfmt, out=g)
+            hip.fake_quant(vbs, sgsz, sfmt, out=vbs)
         lstate = {"g8": g, "sg": sg, "lz": lz, "vb": vbs, "sv": sv}
         tick("stats")
         sel = excl = idx = None

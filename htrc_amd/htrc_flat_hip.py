@@ -554,6 +554,21 @@ def selftest_mfma(ai, bi, af, bf):
     return ci, cf
 
 
+FAKE_QUANT_FMTS = {"int8": 0, "int4": 1, "fp8": 2, "fp4": 3}
+
+
+def fake_quant(x: torch.Tensor, group: int, fmt: str, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [..., D] (fp32 or bf16, contiguous) round-tripped through ``fmt`` with one symmetric scale
+    per group of ``group`` values -> out (fp32 unless given: a bf16 out, or out = x, is allowed)."""
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    d = int(x.shape[-1])
+    rows = x.numel() // d if d else 0
+    call("htrc_fake_quant", ptr(x), int(x.dtype == torch.bfloat16), rows, d, int(group), FAKE_QUANT_FMTS[fmt],
+         ptr(out), int(out.dtype == torch.bfloat16), stream_handle(x.device))
+    return out
+
+
 def selftest_e4m3(codes):
     """Widen uint8 e4m3 codes (a multiple of 8) to fp16 * 2^-8 bit patterns with the kernels'
     conversion instruction and with the exact field shift -> (cvt int16 [n], bits int16 [n])."""

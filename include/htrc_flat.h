@@ -244,6 +244,14 @@ int htrc_kmeans_order(const void* q, int q_is_bf16, int64_t heads, int64_t nq, i
 int htrc_dequant_rows(const uint8_t* x8, int64_t stride_x, const float* scale, int64_t stride_s, int64_t rows,
                       int d, void* out, int out_is_bf16, void* stream);
 
+/* Fake quantisation (accuracy simulation): out = x round-tripped through a low-bit format with one
+ * symmetric scale per group of `group` consecutive values of each row (d % group == 0): fmt 0 int8,
+ * 1 int4 (round to nearest even, clamp), 2 fp8 e4m3fn (nearest even), 3 fp4 e2m1 (threshold
+ * table, ties to the lower magnitude); x and out are contiguous [rows, d] fp32 or bf16 (x_is_bf16,
+ * out_is_bf16; out may alias x).  Replaces fake_quant (h3/htrc_flat.py:68-96). */
+int htrc_fake_quant(const void* x, int x_is_bf16, int64_t rows, int d, int group, int fmt, void* out, int out_is_bf16,
+                    void* stream);
+
 /* Self-test of the MFMA operand conventions the kernels rely on (no reference counterpart):
  * one 64-lane wave computes C = A B for A int8 [16, 64] / B int8 [64, 16] (i8 path) and
  * A bf16 [16, 32] / B bf16 [32, 16] (bf16 path), loading operands the way the kernels do.

@@ -375,12 +375,14 @@ def tail_merge(out, logz, q, tk, tv, scale: float):
 def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: int = 64,
             splits: int = 4, bn: int = 64, sel_stride: int = 1, sink_leaves: int = 0,
             scale: float | None = None, keep: bool = True, group: int = 1, order: str = "seq",
-            store: str = "int8") -> dict:
+            store: str = "int8", state_quant: str | None = None, quant_group: int = 0) -> dict:
     """The INT8 flat operator for one head: q float32 (or bf16 bits) [n,d], k/v bf16 bits
     [nk,d] with nk % leaf == 0.  Returns every intermediate plus out [n,d] and logz [n].
     order="kmeans": the tiles are cut from q[perm] (perm = kmeans_order(q)) and out / logz
     are returned in query order (h3/htrc_flat.py:146-149, 159-165).  store="fp8": the fp8
-    state store (e4m3 g / vb with row scales, fp16 far dots, bf16 near dots)."""
+    state store (e4m3 g / vb with row scales, fp16 far dots, bf16 near dots).  state_quant (store
+    "bf16" only): g and vb fake-quantised in place after the statistics, as quant["state"] does
+    (h3/htrc_flat.py:246-248), with quant_group."""
     q = np.asarray(q)
     qf = bf16.to_f32(q) if q.dtype == np.uint16 else _c(q, np.float32)
     n, d = qf.shape
@@ -407,11 +409,17 @@ def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: 
         st["k"] = _c(k_bits, np.uint16)
         st["q16"], st["dq16"] = pack_q16(qf, tile, st["mu"], group, dq_fp16=False)
         st["g16"], st["vb16"], st["lz"] = stats_bf16(st["mu"], k_bits, v_bits, leaf, scale)
+        if state_quant:
+            from .fake_quant import fake_quant
+            for nm in ("g16", "vb16"):
+                st[nm] = bf16.from_f32(fake_quant(bf16.to_f32(st[nm]), state_quant, quant_group))
     elif store == "int8":
         st["q8"], st["sq"], st["dq8"], st["sdq"] = pack_q(qf, tile, st["mu"], group)
         st["g8"], st["sg"], st["vb"], st["lz"] = stats(st["mu"], k_bits, v_bits, leaf, scale)
     else:
         raise ValueError("store must be int8, fp8 or bf16")
+    if state_quant and store != "bf16":
+        raise ValueError("state fake-quant needs store='bf16'")
     if kx > 0:
         if store == "fp8":
             st["sel"] = select_fp8(st["dq16"], tile, st["g8"], st["sg"], st["lz"], sel_stride, group)

@@ -250,6 +250,53 @@ def test_bf16_store_vs_oracle(device, fused, n, leaf, ex, group):
     assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
 
 
+@pytest.mark.parametrize("store,quant", [("int8", {"q": "int8", "kv": "int8", "group": 32}),
+                                         ("int8", {"q": "fp8", "kv": "fp8"}),
+                                         ("fp8", {"kv": "int4", "group": 16}),
+                                         ("bf16", {"state": "int8"}),
+                                         ("bf16", {"q": "int8", "kv": "int8", "state": "fp4"})])
+def test_quant_simulation_vs_oracle(device, store, quant):
+    """quant= (h3/htrc_flat.py:190-195, 246-248): q and K/V fake-quantised before the operator,
+    the bf16 store's g and vb after the statistics; against the oracle run on the oracle's
+    fake-quantised inputs (K/V then rounded to bf16, as the operator feeds its kernels)."""
+    from oracle.fake_quant import fake_quant as ofq
+    n, leaf, ex = 4096, 64, 8
+    q, k, v = workloads.clustered_runs(n=n, runs=n // 64, heads=1, seed=41)
+    st = {}
+    out, logz = htrc_flat.flat_attention(q[0].to(device), k[0].to(device), v[0].to(device), backend="hip",
+                                         store=store, dot="bf16", leaf=leaf, exact_leaves=ex, splits=4,
+                                         kern={"tile_bn": 64}, quant=quant, return_logz=True, state=st)
+    torch.cuda.synchronize()
+    qg = quant.get("group", 0)
+    qf, kf, vf = (x[0].float().numpy() for x in (q, k, v))
+    if quant.get("q"):
+        qf = ofq(qf, quant["q"], qg)
+    if quant.get("kv"):
+        kf, vf = ofq(kf, quant["kv"], qg), ofq(vf, quant["kv"], qg)
+    ref = flat_i8.flat_i8(qf, bf16.from_f32(kf), bf16.from_f32(vf), tile=64, leaf=leaf, exact_leaves=ex, splits=4,
+                          bn=64, store=store, state_quant=quant.get("state"), quant_group=qg)
+    _routing_check(st, ref, f"quant {store} {quant}")
+    assert rel_l2(out.cpu().numpy(), ref["out"]) <= OUT_REL_L2
+    if store == "int8":
+        check_logz(logz.cpu().numpy(), ref, st, LOGZ_ABS)
+    else:
+        assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
+
+
+def test_quant_rejections(device):
+    q, k, v = workloads.clustered_runs(n=256, runs=4, heads=1, seed=1)
+    args = (q[0].to(device), k[0].to(device), v[0].to(device))
+    kw = dict(backend="hip", dot="bf16", leaf=64, exact_leaves=2)
+    with pytest.raises(ValueError, match="no state fake-quant"):
+        htrc_flat.flat_attention(*args, store="int8", quant={"state": "int8"}, **kw)
+    with pytest.raises(ValueError, match="unknown quant format"):
+        htrc_flat.flat_attention(*args, store="int8", quant={"q": "int3"}, **kw)
+    with pytest.raises(ValueError, match="divide"):
+        htrc_flat.fake_quant(args[0], "int8", 48)
+    with pytest.raises(ValueError, match="HIP device"):
+        htrc_flat.fake_quant(q[0], "int8")
+
+
 @pytest.mark.parametrize("store,fused,order", [("int8", True, "seq"), ("int8", False, "seq"), ("int8", True, "kmeans"),
                                                ("fp8", False, "seq"), ("fp8", True, "seq"), ("bf16", True, "kmeans")])
 def test_tile32_vs_oracle(device, store, fused, order):

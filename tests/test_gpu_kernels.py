@@ -392,6 +392,39 @@ def test_route16_one_entry_equals_two_launches(device, store):
     assert np.array_equal(_np(idx1[0])[:, :sink], np.broadcast_to(np.arange(sink), (idx1.shape[1], sink)))
 
 
+@pytest.mark.parametrize("fmt,group", [("int8", 0), ("int8", 32), ("int4", 0), ("int4", 16), ("fp8", 0),
+                                       ("fp8", 64), ("fp4", 0), ("fp4", 32)])
+@pytest.mark.parametrize("xdtype", ["fp32", "bf16"])
+def test_fake_quant_kernel_matches_oracle(device, fmt, group, xdtype):
+    """htrc_fake_quant against the restated fake_quant (h3/htrc_flat.py:68-96) bit for bit, with
+    exact ties (rows whose group maximum makes the scale 1) and an all-zero group; a bf16 output
+    written in place is the fp32 result rounded to bf16."""
+    from htrc_amd import htrc_flat
+    from oracle.fake_quant import fake_quant as ofq
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((300, 128)) * np.exp2(rng.integers(-10, 11, (300, 1)))).astype(np.float32)
+    qmax = {"int8": 127.0, "int4": 7.0, "fp8": 448.0, "fp4": 6.0}[fmt]
+    x[0] = 0.0
+    x[0, 0] = qmax                                               # scale 1 in every group of row 0 ...
+    x[0, 1:5] = [0.5, 1.5, -2.5, 0.25]                           # ... and values on ties / thresholds
+    x[1, :16] = 0.0
+    xt = torch.from_numpy(x)
+    if xdtype == "bf16":
+        xt = xt.to(torch.bfloat16)
+    xin = xt.float().numpy()
+    got = htrc_flat.fake_quant(xt.to(device), fmt, group)
+    torch.cuda.synchronize()
+    want = ofq(xin, fmt, group)
+    assert np.array_equal(_np(got).view(np.uint32), want.view(np.uint32))
+    # in place, bf16 in and out (the state fake-quant of the bf16 store)
+    xb = xt.to(torch.bfloat16).to(device)
+    gsz = 128 if not group and fmt != "fp4" else (group or 16)
+    hip.fake_quant(xb, gsz, fmt, out=xb)
+    torch.cuda.synchronize()
+    wantb = bf16.from_f32(ofq(xt.to(torch.bfloat16).float().numpy(), fmt, group))
+    assert np.array_equal(_np(xb.view(torch.int16)).view(np.uint16), wantb)
+
+
 def test_e4m3_widening_all_codes(device):
     """The route kernels' e4m3 -> fp16 widening (gfx950 conversion instruction, scale 2^-8) against
     the exact field shift and torch's float8_e4m3fn decode times 2^-8, on every finite code in
