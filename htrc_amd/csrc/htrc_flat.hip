@@ -2748,6 +2748,65 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------
+// bound_select: the reference's alternative routing score (select="bound", h3/htrc_flat.py:255-257;
+// the bf16 state store): SEL[t, l] = lz[t, l] + r_t * ||g_tl|| with r_t the largest ||q_row - mu_t||
+// over the tile group's rows, padded as the reference pads its tiles (rows past the last query
+// repeat it, tiles past the last tile repeat it).  Each norm is a sequential fp32 sum of squares
+// over the dims and one IEEE square root.  One workgroup per tile group of the window; padded
+// leaves get -inf.  (sqrtf, which HIP keeps correctly rounded by default: the header's __fsqrt_rn
+// is the native approximation unless the OCML rounded operations are enabled.)
+// ---------------------------------------------------------------------------------------------
+template <bool IN_BF16>
+__global__ __launch_bounds__(256) void bound_select_kernel(const void* __restrict__ qin, const float* __restrict__ mu,
+                                                           const uint16_t* __restrict__ g, const float* __restrict__ lz,
+                                                           int64_t nq, int nt, int tile, int group, int ng_all, int g0,
+                                                           int gn, int nb, int nb_pad, const int32_t* __restrict__ perm,
+                                                           float* __restrict__ sel) {
+    __shared__ float smu[D];
+    __shared__ float red[256];
+    const int gi = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int64_t gs = (int64_t)h * gn + gi;                 // state / SEL row of the window
+    const int64_t mrow = (int64_t)h * ng_all + g0 + gi;      // centre of the group
+    if (tid < D) smu[tid] = mu[mrow * D + tid];
+    __syncthreads();
+    const int rows = group * tile;
+    const int64_t qbase = (int64_t)h * nq * D;
+    float best = 0.0f;                                       // norms are >= 0
+    for (int rr = tid; rr < rows; rr += 256) {
+        const int t = min((g0 + gi) * group + rr / tile, nt - 1);
+        const int64_t pp = min((int64_t)t * tile + rr % tile, nq - 1);
+        const int64_t p = perm_row(perm, h, nq, pp);
+        float s = 0.0f;
+        for (int c = 0; c < D; ++c) {
+            const float x = IN_BF16 ? bf2f(((const uint16_t*)qin)[qbase + p * D + c]) : ((const float*)qin)[qbase + p * D + c];
+            const float dl = __fsub_rn(x, smu[c]);
+            s = __fadd_rn(s, __fmul_rn(dl, dl));
+        }
+        best = fmaxf(best, sqrtf(s));
+    }
+    red[tid] = best;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+        __syncthreads();
+    }
+    const float r = red[0];
+    for (int l = tid; l < nb_pad; l += 256) {
+        float val = -INFINITY;
+        if (l < nb) {
+            const uint16_t* gr = g + (gs * nb_pad + l) * D;
+            float s = 0.0f;
+            for (int c = 0; c < D; ++c) {
+                const float x = bf2f(gr[c]);
+                s = __fadd_rn(s, __fmul_rn(x, x));
+            }
+            val = __fadd_rn(lz[gs * nb_pad + l], __fmul_rn(r, sqrtf(s)));
+        }
+        sel[gs * nb_pad + l] = val;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // fake_quant: the reference's accuracy simulation (h3/htrc_flat.py:68-96): each group of gsz
 // consecutive values round-trips through a low-bit format with one symmetric scale s =
 // max(max|x|, 1e-20) / qmax of the group: int8 / int4 (qmax 127 / 7): rint(x / s) clamped to
@@ -3609,6 +3668,30 @@ int htrc_dequant_rows(const uint8_t* x8, int64_t stride_x, const float* scale, i
         hipLaunchKernelGGL(dequant_kernel<false>, dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, x8,
                            stride_x, scale, stride_s, rows, d, out);
     return launched("htrc_dequant_rows");
+}
+
+int htrc_bound_select(const void* q, int q_is_bf16, const float* mu, const uint16_t* g, const float* lz, int64_t heads,
+                      int64_t nq, int64_t nk, int leaf, int d, int tile, int group, int64_t g0, int64_t gn,
+                      const int32_t* perm, float* sel, void* stream) {
+    REQUIRE(q && mu && g && lz && sel, "htrc_bound_select: null pointer");
+    REQUIRE(d == D, "htrc_bound_select: head dim must be 128");
+    REQUIRE(tile == 32 || tile == 64, "htrc_bound_select: tile must be 32 or 64 rows");
+    REQUIRE(leaf > 0 && nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535,
+            "htrc_bound_select: bad sizes");
+    REQUIRE(group >= 1 && group <= 1024, "htrc_bound_select: group must be in [1, 1024]");
+    const int64_t nt = (nq + tile - 1) / tile, nb = nk / leaf;
+    REQUIRE(nt <= 0x7fffffff && nb <= 0x7fffffff, "htrc_bound_select: too many tiles or leaves");
+    int64_t ng, tb, ntw;
+    REQUIRE(group_window(nt, group, g0, gn, ng, tb, ntw), "htrc_bound_select: group window [g0, g0 + gn) must lie in the head's groups");
+    REQUIRE(gn <= 0x7fffffff, "htrc_bound_select: too many groups");
+    const dim3 grid((unsigned)gn, (unsigned)heads);
+    if (q_is_bf16)
+        hipLaunchKernelGGL(bound_select_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, q, mu, g, lz, nq, (int)nt,
+                           tile, group, (int)ng, (int)g0, (int)gn, (int)nb, htrc_nb_pad(nb), perm, sel);
+    else
+        hipLaunchKernelGGL(bound_select_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, q, mu, g, lz, nq, (int)nt,
+                           tile, group, (int)ng, (int)g0, (int)gn, (int)nb, htrc_nb_pad(nb), perm, sel);
+    return launched("htrc_bound_select");
 }
 
 int htrc_fake_quant(const void* x, int x_is_bf16, int64_t rows, int d, int group, int fmt, void* out, int out_is_bf16,

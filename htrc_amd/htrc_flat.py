@@ -82,8 +82,11 @@ def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot
     if store not in ("int8", "fp8", "bf16") or dot != "bf16":
         raise ValueError("the HIP backend implements dot='bf16' with store='int8' (int8 Q/K dots, bf16 PV), "
                          "store='fp8' (e4m3 leaf state) or store='bf16'")
-    if select != "max":
-        raise ValueError("the HIP backend implements select='max'")
+    if select not in ("max", "bound"):
+        raise ValueError("select must be 'max' or 'bound'")
+    if select == "bound" and store != "bf16":
+        # h3/htrc_flat.py:209-210: the int8 / fp8 stores route by the row-max score only
+        raise ValueError(f"store={store!r} needs dot='bf16', select='max' and no state fake-quant")
     if order not in ("seq", "kmeans"):
         raise ValueError("order must be seq or kmeans")
     if quant:
@@ -203,11 +206,12 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     if qh.dtype not in (torch.float32, torch.bfloat16):
         qh = qh.float()
     perm = hip.kmeans_order(qh, ws=ws) if order == "kmeans" else None   # query rows regrouped by k-means
+    qsrc = qh.contiguous()                               # the query rows select="bound" measures
     if store in ("fp8", "bf16"):
         mu, q16, dq16 = hip.pack_q16(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm, dq_fp16=store == "fp8")
         packed = {"q16": q16, "dq16": dq16, "mu": mu}
         sdt = torch.float8_e4m3fn if store == "fp8" else torch.bfloat16
-        fused = bool(kern.get("fused", True)) and hip.route16_fits(nb, kx)
+        fused = bool(kern.get("fused", True)) and hip.route16_fits(nb, kx) and select == "max"
     else:
         mu, q8, sq, dq8, sdq = hip.pack_q(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm)
         packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "mu": mu}
@@ -241,9 +245,12 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
                logz=logz, idx=idx, group=group, perm=perm, tile=tile, g0=g0)
             tick("tile")
         else:
-            if kx > 0:
+            if kx > 0 and select == "bound":            # h3/htrc_flat.py:255-257
+                sel = hip.bound_select(qsrc, mu, g, lz, nb, leaf=leaf, ws=ws, group=group, tile=tile, g0=g0, perm=perm)
+            if kx > 0 and select == "max":
                 sel = hip.rowmax_select(g=g, lz=lz, sg=sg, stride=stride, nb=nb, dq8=packed.get("dq8", packed.get("dq16")),
                                         sdq=packed.get("sdq"), ws=ws, group=group, tile=tile, g0=g0)
+            if kx > 0:
                 idx, excl = hip.topk_excl(sel, nb, kx, sink, ws=ws)
             else:
                 excl = hip._rows(ws, "excl", h, gn, (nb_pad(nb),), torch.int8, qh.device)

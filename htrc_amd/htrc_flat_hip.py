@@ -554,6 +554,21 @@ def selftest_mfma(ai, bi, af, bf):
     return ci, cf
 
 
+def bound_select(q: torch.Tensor, mu: torch.Tensor, g: torch.Tensor, lz: torch.Tensor, nb: int, *, leaf: int,
+                 ws=None, group: int = 1, tile: int = TILE, g0: int = 0, perm=None) -> torch.Tensor:
+    """select="bound" of the bf16 store (h3/htrc_flat.py:255-257): q [H,N,D] (fp32 or bf16, query
+    order), mu [H,ng,D], the window's g bf16 [H,gn,nbp,D] and lz -> SEL [H,gn,nbp] fp32 =
+    lz + r * ||g||, r the tile group's largest ||q - mu||."""
+    q = _heads(q)
+    h, nq, d = (int(x) for x in q.shape)
+    tile = _tile(tile)
+    gn = int(lz.shape[1])
+    sel = _rows(ws, "sel", h, gn, (int(lz.shape[2]),), torch.float32, q.device)
+    call("htrc_bound_select", ptr(q), int(q.dtype == torch.bfloat16), ptr(mu), ptr(g), ptr(lz), h, nq,
+         int(nb) * int(leaf), int(leaf), d, tile, int(group), int(g0), gn, ptr(perm), ptr(sel), stream_handle(q.device))
+    return sel
+
+
 FAKE_QUANT_FMTS = {"int8": 0, "int4": 1, "fp8": 2, "fp4": 3}
 
 

@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 13
+#define HTRC_ABI_VERSION 14
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -243,6 +243,18 @@ int htrc_kmeans_order(const void* q, int q_is_bf16, int64_t heads, int64_t nq, i
  * Replaces dequant_rows / _dequant_kernel (h3/htrc_flat_triton.py:276-294). */
 int htrc_dequant_rows(const uint8_t* x8, int64_t stride_x, const float* scale, int64_t stride_s, int64_t rows,
                       int d, void* out, int out_is_bf16, void* stream);
+
+/* Bound routing score of the bf16 state store (select="bound"): sel[h, gi, l] = lz + r * ||g_l||
+ * with r the largest ||q_row - mu|| over the rows of tile group g0 + gi (rows past the last query
+ * and tiles past the last tile repeat the last, as the reference pads its tiles); q [H, nq, d] fp32
+ * or bf16 (q_is_bf16), in query order, perm (optional) maps operator rows to queries; mu the
+ * layer's centres [H, ceil(nt / group), d]; g bf16 [H, gn, nb_pad, d] and lz [H, gn, nb_pad] the
+ * window's state; sel [H, gn, nb_pad] (padded leaves -inf).  Norms: sequential fp32 sums of squares,
+ * one IEEE square root.  Replaces the select == "bound" branch of the chunk loop
+ * (h3/htrc_flat.py:255-257). */
+int htrc_bound_select(const void* q, int q_is_bf16, const float* mu, const uint16_t* g, const float* lz, int64_t heads,
+                      int64_t nq, int64_t nk, int leaf, int d, int tile, int group, int64_t g0, int64_t gn,
+                      const int32_t* perm, float* sel, void* stream);
 
 /* Fake quantisation (accuracy simulation): out = x round-tripped through a low-bit format with one
  * symmetric scale per group of `group` consecutive values of each row (d % group == 0): fmt 0 int8,

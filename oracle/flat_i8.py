@@ -347,6 +347,35 @@ def tile_partials_fp8(st: dict, *, tile: int, leaf: int, scale: float, splits: i
     return pm, pl, pacc
 
 
+def bound_select(qf: np.ndarray, tile: int, mu: np.ndarray, g16: np.ndarray, lz: np.ndarray,
+                 group: int = 1) -> np.ndarray:
+    """select="bound" (h3/htrc_flat.py:255-257) of the bf16 store: SEL[t, l] = lz + r_t * ||g_tl||,
+    r_t the largest ||q_row - mu_t|| over the tile group's rows, padded as the reference pads its
+    tiles (rows past the last query and tiles past the last tile repeat the last).  Norms are
+    sequential fp32 sums of squares over the dims and one IEEE square root."""
+    n, d = qf.shape
+    nt = -(-n // tile)
+    ng = mu.shape[0]
+    sel = np.empty(lz.shape, np.float32)
+    gf = bf16.to_f32(g16)                                           # [ng, nb, d]
+    gs = np.zeros(gf.shape[:2], np.float32)
+    for c in range(d):
+        gs = (gs + gf[:, :, c] * gf[:, :, c]).astype(np.float32)
+    gnorm = np.sqrt(gs).astype(np.float32)
+    for gi in range(ng):
+        rows = []
+        for j in range(group):
+            t = min(gi * group + j, nt - 1)
+            rows.extend(min(t * tile + r, n - 1) for r in range(tile))
+        x = (qf[rows] - mu[gi][None, :]).astype(np.float32)
+        s = np.zeros(len(rows), np.float32)
+        for c in range(d):
+            s = (s + x[:, c] * x[:, c]).astype(np.float32)
+        r = np.float32(np.sqrt(s).astype(np.float32).max())
+        sel[gi] = (lz[gi] + (r * gnorm[gi]).astype(np.float32)).astype(np.float32)
+    return sel
+
+
 def tail_merge(out, logz, q, tk, tv, scale: float):
     """Keys past the last full leaf, attended exactly by every query, merged into a finished
     (out [n,d], logz [n]).  Up to 16 tail keys: q, k, v and p rounded to bf16, fp32
@@ -375,14 +404,16 @@ def tail_merge(out, logz, q, tk, tv, scale: float):
 def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: int = 64,
             splits: int = 4, bn: int = 64, sel_stride: int = 1, sink_leaves: int = 0,
             scale: float | None = None, keep: bool = True, group: int = 1, order: str = "seq",
-            store: str = "int8", state_quant: str | None = None, quant_group: int = 0) -> dict:
+            store: str = "int8", state_quant: str | None = None, quant_group: int = 0,
+            select_mode: str = "max") -> dict:
     """The INT8 flat operator for one head: q float32 (or bf16 bits) [n,d], k/v bf16 bits
     [nk,d] with nk % leaf == 0.  Returns every intermediate plus out [n,d] and logz [n].
     order="kmeans": the tiles are cut from q[perm] (perm = kmeans_order(q)) and out / logz
     are returned in query order (h3/htrc_flat.py:146-149, 159-165).  store="fp8": the fp8
     state store (e4m3 g / vb with row scales, fp16 far dots, bf16 near dots).  state_quant (store
     "bf16" only): g and vb fake-quantised in place after the statistics, as quant["state"] does
-    (h3/htrc_flat.py:246-248), with quant_group."""
+    (h3/htrc_flat.py:246-248), with quant_group.  select_mode "bound" (store "bf16" only): the
+    bound routing score (bound_select) in place of the row-max SEL."""
     q = np.asarray(q)
     qf = bf16.to_f32(q) if q.dtype == np.uint16 else _c(q, np.float32)
     n, d = qf.shape
@@ -418,11 +449,13 @@ def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: 
         st["g8"], st["sg"], st["vb"], st["lz"] = stats(st["mu"], k_bits, v_bits, leaf, scale)
     else:
         raise ValueError("store must be int8, fp8 or bf16")
-    if state_quant and store != "bf16":
-        raise ValueError("state fake-quant needs store='bf16'")
+    if (state_quant or select_mode != "max") and store != "bf16":
+        raise ValueError("state fake-quant and select='bound' need store='bf16'")
     if kx > 0:
         if store == "fp8":
             st["sel"] = select_fp8(st["dq16"], tile, st["g8"], st["sg"], st["lz"], sel_stride, group)
+        elif store == "bf16" and select_mode == "bound":
+            st["sel"] = bound_select(qf, tile, st["mu"], st["g16"], st["lz"], group)
         elif store == "bf16":
             st["sel"] = select_bf16(st["dq16"], tile, st["g16"], st["lz"], sel_stride, group)
         else:

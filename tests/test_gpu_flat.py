@@ -283,6 +283,30 @@ def test_quant_simulation_vs_oracle(device, store, quant):
         assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
 
 
+@pytest.mark.parametrize("order,group,sink,tile", [("seq", 1, 0, 64), ("kmeans", 2, 3, 64), ("seq", 1, 2, 32)])
+def test_bound_select_vs_oracle(device, order, group, sink, tile):
+    """select="bound" (h3/htrc_flat.py:255-257), store="bf16": near sets chosen by lz + r ||g||, on
+    the stage path; routing, output and logZ against the oracle."""
+    n, leaf, ex = 4096, 64, 8
+    q, k, v = workloads.clustered_runs(n=n, runs=n // 64, heads=1, seed=53 + group)
+    st = {}
+    out, logz = htrc_flat.flat_attention(q[0].to(device), k[0].to(device), v[0].to(device), backend="hip",
+                                         store="bf16", dot="bf16", leaf=leaf, exact_leaves=ex, splits=4, tile=tile,
+                                         select="bound", order=order, sink_leaves=sink,
+                                         kern={"tile_bn": 64, "group": group}, return_logz=True, state=st)
+    torch.cuda.synchronize()
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=tile, leaf=leaf, exact_leaves=ex, splits=4, bn=64,
+                          group=group, order=order, sink_leaves=sink, store="bf16", select_mode="bound")
+    assert st.get("sel") is not None                     # the stage path ran
+    nb = st["nb"]
+    sel = st["sel"][0].cpu().numpy()
+    rep = routing_report(st["idx"][0].cpu().numpy(), ref["idx"], ref["sel"][:, :nb], sel_error(sel, ref["sel"], nb))
+    record(f"bound order={order} G={group} sink={sink} tile={tile}", rep)
+    assert rep["mismatched"] <= rep["tieable"]
+    assert rel_l2(out.cpu().numpy(), ref["out"]) <= OUT_REL_L2
+    assert np.abs(logz.cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
+
+
 def test_quant_rejections(device):
     q, k, v = workloads.clustered_runs(n=256, runs=4, heads=1, seed=1)
     args = (q[0].to(device), k[0].to(device), v[0].to(device))
@@ -295,6 +319,10 @@ def test_quant_rejections(device):
         htrc_flat.fake_quant(args[0], "int8", 48)
     with pytest.raises(ValueError, match="HIP device"):
         htrc_flat.fake_quant(q[0], "int8")
+    with pytest.raises(ValueError, match="select='max'"):
+        htrc_flat.flat_attention(*args, store="int8", select="bound", **kw)
+    with pytest.raises(ValueError, match="select must be"):
+        htrc_flat.flat_attention(*args, store="bf16", select="mean", **kw)
 
 
 @pytest.mark.parametrize("store,fused,order", [("int8", True, "seq"), ("int8", False, "seq"), ("int8", True, "kmeans"),

@@ -425,6 +425,27 @@ def test_fake_quant_kernel_matches_oracle(device, fmt, group, xdtype):
     assert np.array_equal(_np(xb.view(torch.int16)).view(np.uint16), wantb)
 
 
+@pytest.mark.parametrize("n,tile,group,qdtype", [(64 * 21 + 5, 64, 1, "fp32"), (32 * 41 + 5, 32, 3, "bf16"),
+                                                  (64 * 16, 64, 2, "fp32")])
+def test_bound_select_matches_oracle(device, n, tile, group, qdtype):
+    """htrc_bound_select (select="bound", h3/htrc_flat.py:255-257) on the oracle's bf16 state: SEL
+    bit for bit against the oracle's sequential-norm restatement, padded rows and tiles included."""
+    q, k, v = _data(n, nk=64 * 24, seed=n + group)
+    if qdtype == "fp32":
+        q = q.float() + 1e-3 * torch.randn(q.shape, generator=torch.Generator().manual_seed(5))
+    ref = flat_i8.flat_i8(q[0].float().numpy() if qdtype == "fp32" else bits(q[0]), bits(k[0]), bits(v[0]),
+                          tile=tile, leaf=64, exact_leaves=4, splits=1, bn=64, group=group, store="bf16",
+                          select_mode="bound")
+    _, state, _, _ = _bf16_state(ref, k, v, device)
+    mu = torch.from_numpy(ref["mu"])[None].to(device)
+    nb = ref["g16"].shape[1]
+    sel = hip.bound_select(q.to(device).contiguous(), mu, state["g8"], state["lz"], nb, leaf=64, group=group,
+                           tile=tile)
+    torch.cuda.synchronize()
+    assert np.array_equal(_np(sel[0])[:, :nb].view(np.uint32), ref["sel"].view(np.uint32))
+    assert bool(torch.isinf(sel[0][:, nb:]).all())
+
+
 def test_e4m3_widening_all_codes(device):
     """The route kernels' e4m3 -> fp16 widening (gfx950 conversion instruction, scale 2^-8) against
     the exact field shift and torch's float8_e4m3fn decode times 2^-8, on every finite code in

@@ -109,3 +109,42 @@ def test_errors():
         fake_quant(np.zeros((2, 128), np.float32), "int8", 48)
     with pytest.raises(ValueError, match="unknown quant format"):
         fake_quant(np.zeros((2, 128), np.float32), "int2", 0)
+
+
+# ---- select="bound" (oracle flat_i8.bound_select; h3/htrc_flat.py:255-257)
+
+def _bound_case(seed, n, tile, group, nb=12):
+    from oracle import bf16, flat_i8
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((n, 128)).astype(np.float32)
+    mu = flat_i8.tile_centres(q, tile) if group == 1 else flat_i8.group_centres(q, tile, group)
+    g16 = bf16.from_f32(rng.standard_normal((mu.shape[0], nb, 128)).astype(np.float32))
+    lz = rng.standard_normal((mu.shape[0], nb)).astype(np.float32)
+    return q, mu, g16, lz, flat_i8.bound_select(q, tile, mu, g16, lz, group)
+
+
+@pytest.mark.parametrize("n,tile,group", [(640, 64, 1), (600, 64, 1), (330, 32, 3), (1000, 64, 4)])
+def test_bound_select_against_float64_norms(n, tile, group):
+    """SEL = lz + r ||g||: r the largest distance of the group's (padded) rows from the centre and
+    ||g|| the leaf slope norm, both against float64 norms; padding repeats real rows, so r is the
+    maximum over the group's real rows."""
+    from oracle import bf16
+    q, mu, g16, lz, sel = _bound_case(n + tile + group, n, tile, group)
+    nt = -(-n // tile)
+    gnorm = np.linalg.norm(bf16.to_f32(g16).astype(np.float64), axis=-1)
+    for gi in range(mu.shape[0]):
+        t0, t1 = gi * group, min(nt, (gi + 1) * group)
+        rows = np.arange(t0 * tile, min(n, t1 * tile))
+        r = np.linalg.norm(q[rows].astype(np.float64) - mu[gi].astype(np.float64), axis=-1).max()
+        want = lz[gi].astype(np.float64) + r * gnorm[gi]
+        assert np.allclose(sel[gi], want, rtol=2e-6, atol=2e-6 * (1 + np.abs(want).max()))
+
+
+def test_bound_select_rows_at_the_centre_give_lz():
+    from oracle import bf16, flat_i8
+    # integer rows: the 64-row sums and the centre are exact, so every row sits on its centre
+    q = np.repeat(np.random.default_rng(3).integers(-8, 9, (1, 128)).astype(np.float32), 128, 0)
+    mu = flat_i8.tile_centres(q, 64)
+    g16 = bf16.from_f32(np.ones((2, 5, 128), np.float32))
+    lz = np.arange(10, dtype=np.float32).reshape(2, 5)
+    assert np.array_equal(flat_i8.bound_select(q, 64, mu, g16, lz), lz)
