@@ -2071,11 +2071,13 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
 //   route_select16_kernel, one 4-wave workgroup per tile group: SEL of every leaf with the
 //     arithmetic of select16_kernel (bit-exact), kept in LDS, its kx largest (leaves < sink
 //     forced in) and every row's largest far-field score, the fixed softmax reference;
-//   route16_kernel, one workgroup per tile, one wave per 16 rows: one continuous stream of
-//     32-key blocks, the far leaves first, then the near tokens, each block staged once in LDS
-//     for every wave of the tile (a 2-slot ring filled through registers: the next block's
-//     loads are issued before the current block is computed); fp8 codes are widened to fp16
-//     (value * 2^-8, exactly) as they are staged.  Far: score = (dq . g) (* 256 sg) + lz, PV with
+//   route16_kernel, one workgroup of two waves per tile (each wave 16 RB rows: 32 at tile 64,
+//     so every LDS operand read feeds two row blocks): one continuous stream of 32-key blocks,
+//     the far leaves first, then the near tokens, each block staged once in LDS for both waves
+//     through a 2-slot ring, the next block's loads issued before the current block is
+//     computed.  Near blocks and bf16 far blocks arrive by direct global->LDS loads (each wave
+//     its 16 rows); fp8 far blocks come through registers, their codes widened to fp16 (value *
+//     2^-8, exactly) as they are staged.  Far: score = (dq . g) (* 256 sg) + lz, PV with
 //     fp16(p * 256 sv) . vb (fp8) or bf16(p) . vb (bf16); near: score = (q . k) * scale (bf16),
 //     PV bf16(p) . v -- the products of tile16_kernel, in one softmax whose reference is the
 //     row's far-field maximum (redone with a moved reference if a row total leaves
@@ -2204,28 +2206,57 @@ constexpr int R16_ROWS = 32 * 256;
 constexpr int R16_SLOT = 2 * R16_ROWS + 3 * 32 * 4;
 __device__ __forceinline__ int swq(int r) { return r & 15; }
 
-// p = 2^u for the log2-domain shifted scores u[0..7] of one row block (keys 16(e/4) + 4grp + e%4),
-// l += p, O^T += V^T P^T with P = fp16(p * pscale) per key (the fp8 far field).
-__device__ __forceinline__ void rows_update_f16(RowsN<1>& st, const float (&u)[8], const float (&pscale)[8],
-                                                const u32x2 (&v)[8][2]) {
-    float p[8];
+// p = 2^u for the log2-domain shifted scores u[rb][0..7] of the RB row blocks (keys 16(e/4) + 4grp
+// + e%4), l += p, O^T += V^T P^T with P = fp16(p * pscale) per key (the fp8 far field).
+template <int RB, typename VOp>
+__device__ __forceinline__ void rows_update_f16(RowsN<RB>& st, const float (&u)[RB][8], const float (&pscale)[8],
+                                                VOp vop) {
+    u32x4 P[RB];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(u[e]);
-    st.l[0] = __fadd_rn(st.l[0], __fadd_rn(__fadd_rn(__fadd_rn(p[0], p[1]), __fadd_rn(p[2], p[3])),
-                                           __fadd_rn(__fadd_rn(p[4], p[5]), __fadd_rn(p[6], p[7]))));
-    uint32_t ph[4];
+    for (int rb = 0; rb < RB; ++rb) {
+        float p[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        ph[j] = pack2h(__fmul_rn(p[2 * j], pscale[2 * j]), __fmul_rn(p[2 * j + 1], pscale[2 * j + 1]));
-    const u32x4 P = u32x4{ph[0], ph[1], ph[2], ph[3]};
+        for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(u[rb][e]);
+        st.l[rb] = __fadd_rn(st.l[rb], __fadd_rn(__fadd_rn(__fadd_rn(p[0], p[1]), __fadd_rn(p[2], p[3])),
+                                                 __fadd_rn(__fadd_rn(p[4], p[5]), __fadd_rn(p[6], p[7]))));
+        uint32_t ph[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            ph[j] = pack2h(__fmul_rn(p[2 * j], pscale[2 * j]), __fmul_rn(p[2 * j + 1], pscale[2 * j + 1]));
+        P[rb] = u32x4{ph[0], ph[1], ph[2], ph[3]};
+    }
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
-        const u32x4 A = u32x4{v[db][0].x, v[db][0].y, v[db][1].x, v[db][1].y};
-        st.o[0][db] = mfma_f16(A, P, st.o[0][db]);
+        if (db == 4) __builtin_amdgcn_sched_barrier(0);   // at most half the V^T operands in registers
+        const u32x4 A = vop(db);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) st.o[rb][db] = mfma_f16(A, P[rb], st.o[rb][db]);
     }
 }
 
-template <int LEAF, bool FP8, int NW>
+// rows_update with the V^T operand of dims block db read by vop(db) as it is consumed.
+template <int RB, typename VOp>
+__device__ __forceinline__ void rows_update_bf16(RowsN<RB>& st, const float (&sc)[RB][8], VOp vop) {
+    bf16x8 P[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        float p[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(sc[rb][e]);
+        st.l[rb] = __fadd_rn(st.l[rb], __fadd_rn(__fadd_rn(__fadd_rn(p[0], p[1]), __fadd_rn(p[2], p[3])),
+                                                 __fadd_rn(__fadd_rn(p[4], p[5]), __fadd_rn(p[6], p[7]))));
+        P[rb] = to_bf16x8(p);
+    }
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+        if (db == 4) __builtin_amdgcn_sched_barrier(0);   // at most half the V^T operands in registers
+        const bf16x8 A = as_bf16x8(vop(db));
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) st.o[rb][db] = mfma_bf16(A, P[rb], st.o[rb][db]);
+    }
+}
+
+template <int LEAF, bool FP8, int NW, int RB>
 __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
     const uint16_t* __restrict__ q16, const uint16_t* __restrict__ dq16, const void* __restrict__ g,
     const float* __restrict__ sg, const float* __restrict__ lz, const void* __restrict__ vb,
@@ -2233,8 +2264,9 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
     const int32_t* __restrict__ idx, const float* __restrict__ rowmax, int64_t nq, int nt, int group, int g0, int ng,
     const int32_t* __restrict__ perm, int64_t nk, int nb, int nb_pad, int kxe, float scale,
     float* __restrict__ out, float* __restrict__ logz) {
-    constexpr int NT = 64 * NW, TR = 16 * NW;  // threads, rows per tile (one wave per 16 rows)
-    constexpr int NC = 512 / NT;               // 16-byte chunks of a 32 x 256-byte region per thread
+    static_assert(NW == 2, "two waves per tile: wave w stages rows 16 w .. 16 w + 15 of every block");
+    constexpr int NT = 64 * NW, TR = 16 * RB * NW;   // threads, rows per tile (16 RB rows per wave)
+    constexpr int NC = 512 / NT;                     // 16-byte chunks of a 32 x 256-byte region per thread
     __shared__ __align__(16) char ring[2][R16_SLOT];
     // sized by the launch: exclusion bits [nb / 32 + 1], then the tile's near leaves [kxe]
     extern __shared__ __align__(16) uint32_t r16_dyn[];
@@ -2252,23 +2284,27 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
     const int64_t th = (int64_t)h * nt + t;
     const int64_t gs = (int64_t)h * ng + (t / group - g0);
     const int64_t kh = (int64_t)h * nk;
-    const int64_t prow = th * TR + 16 * wv + col;           // this lane's packed query row
+    const int64_t prow0 = th * TR + 16 * RB * wv + col;     // this lane's packed query row of block 0
     for (int i = threadIdx.x; i <= nb / 32; i += NT) {     // leaves >= nb excluded
         const int past = nb - 32 * i;
         exbits[i] = past >= 32 ? 0u : (past <= 0 ? ~0u : ~0u << past);
     }
     for (int j = threadIdx.x; j < kxe; j += NT) sidx[j] = (uint32_t)idx[gs * kxe + j];
-    float mref;
-    {
-        const float m = rowmax[prow];
-        mref = m == -INFINITY ? 0.0f : __fmul_rn(m, LOG2E);
-    }
-    u32x4 bdq[4], bq[4];                                    // B operands: row's q - mu, q (16-bit)
+    float mref[RB];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        bdq[ks] = *(const u32x4*)(dq16 + prow * D + 32 * ks + 8 * grp);
-        bq[ks] = *(const u32x4*)(q16 + prow * D + 32 * ks + 8 * grp);
+    for (int rb = 0; rb < RB; ++rb) {
+        const float m = rowmax[prow0 + 16 * rb];
+        mref[rb] = m == -INFINITY ? 0.0f : __fmul_rn(m, LOG2E);
     }
+    // B operands of the rows: q - mu through the far blocks, then q through the near blocks (one
+    // register set, reloaded at the switch)
+    u32x4 bx[RB][4];
+    auto load_rows = [&](const uint16_t* x) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) bx[rb][ks] = *(const u32x4*)(x + (prow0 + 16 * rb) * D + 32 * ks + 8 * grp);
+    };
     __syncthreads();
     for (int j = threadIdx.x; j < kxe; j += NT) atomicOr(&exbits[sidx[j] >> 5], 1u << (sidx[j] & 31));
     __syncthreads();
@@ -2277,162 +2313,216 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
     const int nn = (e_n + 31) / 32;                         // near blocks: two 16-token runs each
     const int nblk = nf + nn;
     const float qs = __fmul_rn(scale, LOG2E);
+    // Direct global -> LDS loads of 256-byte rows: wave w stages rows 16 w .. 16 w + 15 of a block's
+    // QK and PV regions, four rows per load; lane L of load i gets row 4 i + L / 16 at position
+    // L % 16, i.e. the row's 16-byte chunk (L % 16) ^ swq (QK) or ^ swz (PV) of that row.
+    // With g = L / 16 and r = 4 i + g (bits of i above those of g): swq(r) = 4 i ^ g and
+    // swz(r) = (g << 1) ^ f(i), f = 0, 9, 8, 1, so load i's offsets are load 0's XOR a constant.
+    // The per-block lambdas derive their lane offsets from ln, which every pass redefines through
+    // an empty asm: otherwise those offsets are hoisted out of the pass loop and all of them stay
+    // live (and spill) through both key loops.
+    int ln = lane;
+    auto dma_rows16 = [&](const uint16_t* xq, const uint16_t* xp, uint32_t slot_lds) {
+        const uint32_t voq0 = (uint32_t)((ln >> 4) * 256 + 16 * ((ln & 15) ^ swq(ln >> 4)));
+        const uint32_t vop0 = (uint32_t)((ln >> 4) * 256 + 16 * ((ln & 15) ^ swz(ln >> 4)));
+        const uint64_t bq_ = sbase(xq), bp_ = sbase(xp);
+        const uint32_t lq = slot_lds + (uint32_t)wv * 4096, lp = slot_lds + R16_ROWS + (uint32_t)wv * 4096;
+        dma_x4<false>(bq_, voq0, bq_, voq0 ^ 64u, bq_, voq0 ^ 128u, bq_, voq0 ^ 192u, lq);
+        dma_x4<false>(bp_, vop0, bp_, vop0 ^ 144u, bp_, vop0 ^ 128u, bp_, vop0 ^ 16u, lp);
+    };
+    // fp8 far blocks go through registers (their codes are widened to fp16 on the way to LDS):
     // this thread's chunks j of a 32-row region: row rr(j), 16-byte chunk cr; LDS byte offsets
-    const int cr = threadIdx.x & 15;
-    auto rr = [&](int j) { return (int)(threadIdx.x >> 4) + (NT / 16) * j; };
-    auto oq = [&](int j) { return rr(j) * 256 + 16 * (cr ^ swq(rr(j))); };
-    auto op = [&](int j) { return R16_ROWS + rr(j) * 256 + 16 * (cr ^ swz(rr(j))); };
-    // staging registers of one block: this thread's chunks of the QK and PV regions and a scale
-    u32x4 rq[NC], rp[NC];
+    int tn = (int)threadIdx.x;                              // redefined every pass, as ln
+    auto rr = [&](int j) { return (tn >> 4) + (NT / 16) * j; };
+    auto oq = [&](int j) { return rr(j) * 256 + 16 * ((tn & 15) ^ swq(rr(j))); };
+    auto op = [&](int j) { return R16_ROWS + rr(j) * 256 + 16 * ((tn & 15) ^ swz(rr(j))); };
+    u32x2 rq[FP8 ? NC : 1], rp[FP8 ? NC : 1];
     float rsc = 0.0f;
     auto run_pos = [&](int j) { return j < e_n ? j : 0; };  // past the list: its start again (masked)
-    auto load = [&](int bi) {
+    // near block bi (tokens of the near list from 32 (bi - nf)): wave w loads the 16-token run
+    // 32 (bi - nf) + 16 w (past the list: the list's start again, masked)
+    auto fetch_near = [&](int bi, uint32_t sl_lds) {
+        const int e0 = 32 * (bi - nf) + 16 * wv, j = run_pos(e0);
+        const int64_t ra = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[j / LEAF]) * LEAF + (j % LEAF);
+        dma_rows16(k + ra * D, v + ra * D, sl_lds);
+    };
+    // Block bi into ring slot `slot`: a bf16 far block or a near block by direct loads (landed
+    // once this wave's vmcnt drains), an fp8 far block into registers (fetch) and LDS (put).
+    auto fetch = [&](int bi, int slot) {
+        char* sl = &ring[slot][0];
+        const uint32_t sl_lds = lds_addr(sl);
         if (bi < nf) {                                      // 32 consecutive state rows of the group
             const int64_t r0 = gs * nb_pad + 32 * bi;
+            if constexpr (FP8) {
 #pragma unroll
-            for (int j = 0; j < NC; ++j) {
-                const int64_t sr = r0 + rr(j);
-                if constexpr (FP8) {
-                    const u32x2 a = *(const u32x2*)((const uint8_t*)g + sr * D + 8 * cr);
-                    const u32x2 b = *(const u32x2*)((const uint8_t*)vb + sr * D + 8 * cr);
-                    rq[j] = u32x4{a.x, a.y, 0u, 0u};
-                    rp[j] = u32x4{b.x, b.y, 0u, 0u};
-                } else {
-                    rq[j] = *(const u32x4*)((const uint16_t*)g + sr * D + 8 * cr);
-                    rp[j] = *(const u32x4*)((const uint16_t*)vb + sr * D + 8 * cr);
+                for (int j = 0; j < NC; ++j) {
+                    const int64_t sr = r0 + rr(j);
+                    rq[j] = *(const u32x2*)((const uint8_t*)g + sr * D + 8 * (tn & 15));
+                    rp[j] = *(const u32x2*)((const uint8_t*)vb + sr * D + 8 * (tn & 15));
                 }
-            }
-            const int s = threadIdx.x;
-            if (s < 32) rsc = lz[r0 + s];
-            else if (FP8 && s < 64) rsc = sg[r0 + s - 32];
-            else if (FP8 && s < 96) rsc = sv[r0 + s - 64];
-        } else {                                            // near tokens: runs at 32 b and 32 b + 16
-            const int e0 = 32 * (bi - nf), ja = run_pos(e0), jb = run_pos(e0 + 16);
-            const int64_t ra = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[ja / LEAF]) * LEAF + (ja % LEAF);
-            const int64_t rb = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[jb / LEAF]) * LEAF + (jb % LEAF);
-#pragma unroll
-            for (int j = 0; j < NC; ++j) {
-                const int64_t sr = rr(j) < 16 ? ra + rr(j) : rb + (rr(j) - 16);
-                rq[j] = *(const u32x4*)(k + sr * D + 8 * cr);
-                rp[j] = *(const u32x4*)(v + sr * D + 8 * cr);
-            }
-        }
-    };
-    auto store = [&](int bi, char* slot) {
-        if (bi < nf) {
-#pragma unroll
-            for (int j = 0; j < NC; ++j) {                  // fp8 codes widened to fp16 here
-                *(u32x4*)(slot + oq(j)) = FP8 ? e4m3x8_to_h8_cvt(u32x2{rq[j].x, rq[j].y}) : rq[j];
-                *(u32x4*)(slot + op(j)) = FP8 ? e4m3x8_to_h8_cvt(u32x2{rp[j].x, rp[j].y}) : rp[j];
-            }
-            const int s = threadIdx.x;
-            if (s < (FP8 ? 96 : 32)) {
-                // lz of a leaf in the near set (or past nb) -> -inf: its far score is -inf, p = 0
-                const float x = s < 32 ? (((exbits[bi] >> s) & 1u) ? -INFINITY : rsc) : __fmul_rn(rsc, 256.0f);
-                *(float*)(slot + 2 * R16_ROWS + 4 * s) = x;
+                const int s = threadIdx.x;
+                if (s < 32) rsc = lz[r0 + s];
+                else if (s < 64) rsc = sg[r0 + s - 32];
+                else if (s < 96) rsc = sv[r0 + s - 64];
+            } else {
+                const int64_t rw = r0 + 16 * wv;
+                dma_rows16((const uint16_t*)g + rw * D, (const uint16_t*)vb + rw * D, sl_lds);
+                if (wv == 0 && lane < 8) dma16<false>(lz + r0 + 4 * lane, sl_lds + 2 * R16_ROWS);
             }
         } else {
+            fetch_near(bi, sl_lds);
+        }
+    };
+    auto put = [&](int bi, int slot) {                     // the register half of an fp8 far block
+        if constexpr (FP8) {
+            if (bi < nf) {
+                char* sl = &ring[slot][0];
 #pragma unroll
-            for (int j = 0; j < NC; ++j) {
-                *(u32x4*)(slot + oq(j)) = rq[j];
-                *(u32x4*)(slot + op(j)) = rp[j];
+                for (int j = 0; j < NC; ++j) {
+                    *(u32x4*)(sl + oq(j)) = e4m3x8_to_h8_cvt(rq[j]);
+                    *(u32x4*)(sl + op(j)) = e4m3x8_to_h8_cvt(rp[j]);
+                }
+                const int s = threadIdx.x;
+                if (s < 96) {
+                    // lz of a leaf in the near set (or past nb) -> -inf: its far score is -inf, p = 0
+                    const float x = s < 32 ? (((exbits[bi] >> s) & 1u) ? -INFINITY : rsc) : __fmul_rn(rsc, 256.0f);
+                    *(float*)(sl + 2 * R16_ROWS + 4 * s) = x;
+                }
             }
         }
     };
-    RowsN<1> st;
-    // one 32-key block of the far field from slot S: score = (dq . g) (* 256 sg) + lz
-    auto far_block = [&](const char* slot) {
-        float u[8], pscale[8];
+    RowsN<RB> st;
+    // one 32-key block of the far field: score = (dq . g) (* 256 sg) + lz; each LDS operand read
+    // feeds the RB row blocks
+    auto far_block = [&](const char* slot, int bi) {
+        const int col = ln & 15, grp = ln >> 4, lane = ln;
+        float u[RB][8], pscale[8];
         const float* scl = (const float*)(slot + 2 * R16_ROWS);
+        const uint32_t exw = FP8 ? 0u : exbits[bi] >> (4 * grp);   // bf16: excluded leaves masked here
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
+            if (hh == 1) __builtin_amdgcn_sched_barrier(0);   // one key half's QK operands at a time
             const int r = 16 * hh + col;
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            f32x4 acc[RB];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const u32x4 A = *(const u32x4*)(slot + r * 256 + 16 * ((4 * ks + grp) ^ swq(r)));
-                if constexpr (FP8) acc = mfma_f16(A, bdq[ks], acc);
-                else acc = mfma_bf16(as_bf16x8(A), as_bf16x8(bdq[ks]), acc);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) {
+                    if constexpr (FP8) acc[rb] = mfma_f16(A, bx[rb][ks], acc[rb]);
+                    else acc[rb] = mfma_bf16(as_bf16x8(A), as_bf16x8(bx[rb][ks]), acc[rb]);
+                }
             }
             const f32x4 lzv = *(const f32x4*)(scl + 16 * hh + 4 * grp);
             const f32x4 sgv = FP8 ? *(const f32x4*)(scl + 32 + 16 * hh + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
             const f32x4 svv = FP8 ? *(const f32x4*)(scl + 64 + 16 * hh + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float dot = FP8 ? __fmul_rn(acc[i], sgv[i]) : acc[i];
-                u[4 * hh + i] = __fmaf_rn(__fadd_rn(dot, lzv[i]), LOG2E, -st.m[0]);
+                float lzi = lzv[i];
+                if constexpr (!FP8) {   // excluded key: lz -> -inf, one bit select on the sign-extended bit
+                    const uint32_t ex = (uint32_t)__builtin_amdgcn_sbfe((int)exw, 16 * hh + i, 1);
+                    uint32_t lzb;
+                    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(lzb) : "v"(ex), "v"(0xff800000u), "v"(__float_as_uint(lzi)));
+                    lzi = __uint_as_float(lzb);
+                }
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) {
+                    const float dot = FP8 ? __fmul_rn(acc[rb][i], sgv[i]) : acc[rb][i];
+                    u[rb][4 * hh + i] = __fmaf_rn(__fadd_rn(dot, lzi), LOG2E, -st.m[rb]);
+                }
                 pscale[4 * hh + i] = svv[i];
             }
         }
-        u32x2 pvop[8][2];
-#pragma unroll
-        for (int db = 0; db < 8; ++db)
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + R16_ROWS, 16 * hf, db, lane);
-        if constexpr (FP8) rows_update_f16(st, u, pscale, pvop);
-        else {
-            const float (&uu)[1][8] = *reinterpret_cast<const float (*)[1][8]>(&u);
-            rows_update<1, true>(st, uu, pvop);
-        }
+        auto vop_ = [&](int db) {
+            const u32x2 lo = tr_operand(slot + R16_ROWS, 0, db, lane), hi = tr_operand(slot + R16_ROWS, 16, db, lane);
+            return u32x4{lo.x, lo.y, hi.x, hi.y};
+        };
+        if constexpr (FP8) rows_update_f16<RB>(st, u, pscale, vop_);
+        else rows_update_bf16<RB>(st, u, vop_);
     };
     // one 32-token block of the near field: score = (q . k) * scale; the second run of 16 is past
     // the list (masked) only in the last block when the list holds an odd number of 16-token runs
     auto near_block = [&](const char* slot, int bi) {
+        const int col = ln & 15, grp = ln >> 4, lane = ln;
         const bool run2 = 32 * (bi - nf) + 16 < e_n;
-        float u[8];
+        float u[RB][8];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
+            if (hh == 1) __builtin_amdgcn_sched_barrier(0);   // one key half's QK operands at a time
             const int r = 16 * hh + col;
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            f32x4 acc[RB];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const u32x4 A = *(const u32x4*)(slot + r * 256 + 16 * ((4 * ks + grp) ^ swq(r)));
-                acc = mfma_bf16(as_bf16x8(A), as_bf16x8(bq[ks]), acc);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma_bf16(as_bf16x8(A), as_bf16x8(bx[rb][ks]), acc[rb]);
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) u[4 * hh + i] = (hh == 0 || run2) ? __fmaf_rn(acc[i], qs, -st.m[0]) : -INFINITY;
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+                    u[rb][4 * hh + i] = (hh == 0 || run2) ? __fmaf_rn(acc[rb][i], qs, -st.m[rb]) : -INFINITY;
         }
-        u32x2 pvop[8][2];
-#pragma unroll
-        for (int db = 0; db < 8; ++db)
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + R16_ROWS, 16 * hf, db, lane);
-        const float (&uu)[1][8] = *reinterpret_cast<const float (*)[1][8]>(&u);
-        rows_update<1, true>(st, uu, pvop);
+        auto vop_ = [&](int db) {
+            const u32x2 lo = tr_operand(slot + R16_ROWS, 0, db, lane), hi = tr_operand(slot + R16_ROWS, 16, db, lane);
+            return u32x4{lo.x, lo.y, hi.x, hi.y};
+        };
+        rows_update_bf16<RB>(st, u, vop_);
     };
-    // block bi from slot S (block bi + 1 loaded meanwhile and staged into the other slot); slot
-    // parity a template constant, so every LDS address is a fixed offset
+    // block bi from slot S while block bi + 1 is fetched into the other slot (put after the
+    // compute when it comes through registers); the step ends with both waves' loads landed
     auto far_step = [&](auto par, int bi) {
         constexpr int S = decltype(par)::value;
         const bool more = bi + 1 < nblk;
-        if (more) load(bi + 1);
-        far_block(&ring[S][0]);
-        if (more) store(bi + 1, &ring[S ^ 1][0]);
+        if (more) fetch(bi + 1, S ^ 1);
+        far_block(&ring[S][0], bi);
+        if (more) put(bi + 1, S ^ 1);
+        wait_vmcnt<0>();
         __syncthreads();
     };
     auto near_step = [&](auto par, int bi) {
         constexpr int S = decltype(par)::value;
-        const bool more = bi + 1 < nblk;
-        if (more) load(bi + 1);
+        if (bi + 1 < nblk) fetch_near(bi + 1, lds_addr(&ring[S ^ 1][0]));
         near_block(&ring[S][0], bi);
-        if (more) store(bi + 1, &ring[S ^ 1][0]);
+        wait_vmcnt<0>();
         __syncthreads();
     };
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
     for (int pass = 0; pass < MAX_PASSES; ++pass) {
-        st.m[0] = mref;
-        st.l[0] = 0.0f;
+        asm volatile("" : "+v"(ln), "+v"(tn));
 #pragma unroll
-        for (int db = 0; db < 8; ++db) st.o[0][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-        load(0);
-        store(0, &ring[0][0]);
+        for (int rb = 0; rb < RB; ++rb) {
+            st.m[rb] = mref[rb];
+            st.l[rb] = 0.0f;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) st.o[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        load_rows(dq16);
+        // the row operands are in registers before the first direct load (the compiler's own wait
+        // for them would otherwise also drain it)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) asm volatile("" : : "v"(bx[rb][ks]));
+        fetch(0, 0);
+        put(0, 0);
+        wait_vmcnt<0>();
         __syncthreads();
         // far blocks 0 .. nf - 1 in slots 0, 1, 0, ..; the near blocks continue the alternation
         for (int bi = 0; bi < nf; bi += 2) {
             far_step(P0(), bi);
             if (bi + 1 < nf) far_step(P1(), bi + 1);
         }
+        load_rows(q16);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) asm volatile("" : : "v"(bx[rb][ks]));
         if (nf & 1) {
             for (int bi = nf; bi < nblk; bi += 2) {
                 near_step(P1(), bi);
@@ -2448,32 +2538,43 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
         // octaves: the pass is redone with the reference moved to m + log2(total)
         // (2^-8 with the fp8 store: its far-field P is fp16, whose subnormals would hold the far
         // leaves of a row whose total is that small with too few bits)
-        const float lt = grp_sum(st.l[0]);
-        if (grp == 0) red_l[16 * wv + col] = lt;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const float lt = grp_sum(st.l[rb]);
+            if (grp == 0) red_l[16 * RB * wv + 16 * rb + col] = lt;
+        }
         if (threadIdx.x == 0) redo = 0;
         __syncthreads();
-        const float tot = red_l[16 * wv + col];
-        if (!(tot >= (FP8 ? 0x1p-8f : 0x1p-60f) && tot <= 0x1p64f)) {
-            mref = tot > 0.0f && tot <= 3.0e38f ? __fadd_rn(mref, __log2f(tot))
-                                                : __fadd_rn(mref, tot == 0.0f ? -120.0f : 120.0f);
-            redo = 1;
+        bool bad = false;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const float tot = red_l[16 * RB * wv + 16 * rb + col];
+            if (!(tot >= (FP8 ? 0x1p-8f : 0x1p-60f) && tot <= 0x1p64f)) {
+                mref[rb] = tot > 0.0f && tot <= 3.0e38f ? __fadd_rn(mref[rb], __log2f(tot))
+                                                        : __fadd_rn(mref[rb], tot == 0.0f ? -120.0f : 120.0f);
+                bad = true;
+            }
         }
+        if (bad) redo = 1;
         __syncthreads();
         if (redo == 0 || pass + 1 == MAX_PASSES) break;
     }
-    const int r = 16 * wv + col;
-    const float den = red_l[r];
-    const float inv = 1.0f / (den < 1e-30f ? 1e-30f : den);
-    const int64_t qi = (int64_t)t * TR + r;
-    if (qi < nq) {
-        const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-            const f32x4 o = st.o[0][db];
-            *(f32x4*)(out + orow * D + 16 * db + 4 * grp) =
-                f32x4{__fmul_rn(o[0], inv), __fmul_rn(o[1], inv), __fmul_rn(o[2], inv), __fmul_rn(o[3], inv)};
+    for (int rb = 0; rb < RB; ++rb) {
+        const int r = 16 * RB * wv + 16 * rb + col;
+        const float den = red_l[r];
+        const float inv = 1.0f / (den < 1e-30f ? 1e-30f : den);
+        const int64_t qi = (int64_t)t * TR + r;
+        if (qi < nq) {
+            const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                const f32x4 o = st.o[rb][db];
+                *(f32x4*)(out + orow * D + 16 * db + 4 * grp) =
+                    f32x4{__fmul_rn(o[0], inv), __fmul_rn(o[1], inv), __fmul_rn(o[2], inv), __fmul_rn(o[3], inv)};
+            }
+            if (grp == 0) logz[orow] = __fadd_rn(__fmul_rn(st.m[rb], LN2), __logf(den));   // m in log2 units
         }
-        if (grp == 0) logz[orow] = __fadd_rn(__fmul_rn(st.m[0], LN2), __logf(den));   // m in log2 units
     }
 }
 
@@ -3513,15 +3614,15 @@ int htrc_route16_attend(const uint16_t* q16, const uint16_t* dq16, const void* g
     REQUIRE(stat + dyn <= ROUTE_LDS_MAX, "htrc_route16_attend: near list and exclusion bits exceed the LDS");
     const dim3 grid((unsigned)(ntw * heads));
     hipStream_t s = (hipStream_t)stream;
-#define R16_LAUNCH(L, F, NW)                                                                                      \
-    hipLaunchKernelGGL((route16_kernel<L, F, NW>), grid, dim3(64 * NW), dyn, s, q16, dq16, g, sg, lz, vb, sv, k, v, idx, \
+#define R16_LAUNCH(L, F, NW, RB)                                                                                  \
+    hipLaunchKernelGGL((route16_kernel<L, F, NW, RB>), grid, dim3(64 * NW), dyn, s, q16, dq16, g, sg, lz, vb, sv, k, v, idx, \
                        rowmax, nq, (int)nt, group, (int)g0, (int)gn, perm, nk, (int)nb, nbp, kxe, scale, out, logz)
 #define R16_CASE(L)                                                                                               \
     case L:                                                                                                       \
         if (tile == 64) {                                                                                         \
-            if (fp8) R16_LAUNCH(L, true, 4); else R16_LAUNCH(L, false, 4);                                        \
+            if (fp8) R16_LAUNCH(L, true, 2, 2); else R16_LAUNCH(L, false, 2, 2);                                  \
         } else {                                                                                                  \
-            if (fp8) R16_LAUNCH(L, true, 2); else R16_LAUNCH(L, false, 2);                                        \
+            if (fp8) R16_LAUNCH(L, true, 2, 1); else R16_LAUNCH(L, false, 2, 1);                                  \
         }                                                                                                         \
         break;
     switch (leaf) {
