@@ -2091,6 +2091,8 @@ __global__ __launch_bounds__(256, 3) void route_select16_kernel(
     extern __shared__ uint32_t keys16[];      // [nb]
     __shared__ TopkSmem sm;
     __shared__ float red_m[4][64];
+    constexpr int S16_RING = 3, S16_SLOT = 2048 + 128;
+    __shared__ __align__(16) char s16ring[4][FP8 ? S16_RING : 1][FP8 ? S16_SLOT : 16];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
     const int gi = (int)(blk % (uint32_t)ng), h = (int)(blk / (uint32_t)ng);
@@ -2113,10 +2115,10 @@ __global__ __launch_bounds__(256, 3) void route_select16_kernel(
         float rmax[NRB];
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) rmax[rb] = -INFINITY;
-        // the wave's 16-leaf groups c = 16 w, 16 w + 64, ..: each group's state rows are fetched
-        // while the previous group's products run (two register sets; a third, two groups
-        // ahead, spills at three waves per SIMD and measured slower: 1.20 / 1.16 ms at cfg3 for
-        // fp8 / bf16 against 1.26 / 1.56)
+        // the wave's 16-leaf groups c = 16 w, 16 w + 64, ..: bf16 state rows are fetched into
+        // registers while the previous group's products run (two register sets; a third, two
+        // groups ahead, spills at three waves per SIMD and measured slower: 1.16 against 1.56
+        // ms at cfg3); fp8 rows stream through a ring in LDS (below)
         using AT = std::conditional_t<FP8, u32x2, u32x4>;   // 8 e4m3 codes / 8 bf16 of a row chunk
         struct Grp {
             AT a[4];
@@ -2168,15 +2170,54 @@ __global__ __launch_bounds__(256, 3) void route_select16_kernel(
                 }
             }
         };
-        Grp x0, x1;
         const int cw = 16 * w;
-        if (cw < nb) fetch(x0, cw);
-        for (int c = cw; c < nb; c += 128) {
-            if (c + 64 < nb) fetch(x1, c + 64);
-            consume(x0, c);
-            if (c + 64 >= nb) break;
-            if (c + 128 < nb) fetch(x0, c + 128);
-            consume(x1, c + 64);
+        if constexpr (FP8) {
+            // fp8: each wave streams its groups through its own 3-slot LDS ring by direct loads,
+            // two groups ahead (the wave reads only what it loaded: no barriers).  Slot: 16 rows
+            // of 128 code bytes, chunk k of row r at 16-byte position k ^ (r & 7) (one 8-lane
+            // phase of a read touches 8 positions), then sg (64 B) and lz (64 B).
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)   // the row operands land before the first direct load
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) asm volatile("" : : "v"(b[rb][ks]));
+            const uint32_t ring_w = lds_addr(&s16ring[w][0][0]);
+            const uint32_t voff = (uint32_t)((lane >> 3) * D + 16 * ((lane & 7) ^ ((lane >> 3) & 7)));
+            const int ngr = cw < nb ? (nb - cw + 63) / 64 : 0;
+            auto issue = [&](int gj) {
+                if (gj >= ngr) return;
+                const int64_t s0 = gs * nb_pad + cw + 64 * gj;
+                const uint32_t slot = ring_w + (uint32_t)(gj % S16_RING) * S16_SLOT;
+                dma16s((const uint8_t*)g + s0 * D, voff, slot);
+                dma16s((const uint8_t*)g + (s0 + 8) * D, voff, slot + 1024);
+                if (lane < 8) dma16(lane < 4 ? sg + s0 + 4 * lane : lz + s0 + 4 * (lane - 4), slot + 2048);
+            };
+#pragma unroll
+            for (int gj = 0; gj < S16_RING - 1; ++gj) issue(gj);
+            for (int gj = 0; gj < ngr; ++gj) {
+                if (gj + 1 < ngr) wait_vmcnt<3>();          // the next group's loads stay in flight
+                else wait_vmcnt<0>();
+                const char* slot = &s16ring[w][gj % S16_RING][0];
+                Grp x;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const int kc = 2 * ks + (grp >> 1);
+                    x.a[ks] = *(const u32x2*)(slot + col * D + 16 * (kc ^ (col & 7)) + 8 * (grp & 1));
+                }
+                x.sgv = *(const f32x4*)(slot + 2048 + 16 * grp);
+                x.lzv = *(const f32x4*)(slot + 2048 + 64 + 16 * grp);
+                issue(gj + S16_RING - 1);                    // into the slot read last iteration
+                consume(x, cw + 64 * gj);
+            }
+        } else {
+            Grp x0, x1;
+            if (cw < nb) fetch(x0, cw);
+            for (int c = cw; c < nb; c += 128) {
+                if (c + 64 < nb) fetch(x1, c + 64);
+                consume(x0, c);
+                if (c + 64 >= nb) break;
+                if (c + 128 < nb) fetch(x0, c + 128);
+                consume(x1, c + 64);
+            }
         }
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
