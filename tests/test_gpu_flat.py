@@ -97,6 +97,27 @@ def test_deterministic(device):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("fused,chunk", [(True, 1024), (False, 1024), (True, 16)])
+def test_prof_stage_times(device, fused, chunk):
+    """prof={} (h3/htrc_flat.py:32-44): wall times in ms per stage, a device sync at each, summed
+    over the tile windows under the reference's stage names; the result is the one without prof."""
+    q, k, v = workloads.clustered_runs(n=4096, runs=64, heads=1, seed=5)
+    args = (q[0].to(device), k[0].to(device), v[0].to(device))
+    kw = dict(backend="hip", store="int8", dot="bf16", leaf=64, exact_leaves=16, tile_chunk=chunk,
+              kern={"fused": fused})
+    ref = htrc_flat.flat_attention(*args, **kw).clone()
+    prof = {}
+    out = htrc_flat.flat_attention(*args, prof=prof, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    names = {"prep", "stats", "tile", "finish"} | ({"select"} if not fused else set())
+    assert set(prof) == names
+    assert all(isinstance(t, float) and t >= 0.0 for t in prof.values())
+    prof2 = dict(prof)
+    htrc_flat.flat_attention(*args, prof=prof2, **kw)
+    assert all(prof2[n] >= prof[n] for n in names)    # accumulates into the caller's dict
+
+
 @pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("ntail", [7, 16, 33])
 def test_tail_keys_vs_oracle(device, fused, ntail):
