@@ -36,6 +36,23 @@ def test_graph_replays_equal_eager(device):
         _ = torch.randn(1 << 20, device=device).sum().item()      # eager work between replays
 
 
+@pytest.mark.parametrize("store", ["fp8", "bf16"])
+def test_16bit_store_graph_replays_equal_eager(device, store):
+    """The runner with a 16-bit state store (its stats and route16 launches inside the graph):
+    every replay equals the eager call bit for bit."""
+    jobs = _jobs(device, heads=2, seed=3)
+    r = htrc_flat_runner.FlatRunner(2048, 2048, mode="fast", store=store, **KW)
+    assert r.graph is not None, r.graph_error
+    assert r.cfg["store"] == store
+    eager = [htrc_flat.flat_attention(j[1], j[2], j[3], **r.cfg) for j in jobs]
+    for rep in range(3):
+        outs = r.run(jobs)
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {rep} differs from eager"
+        _ = torch.randn(1 << 20, device=device).sum().item()      # eager work between replays
+
+
 def test_head_batched_runner_matches_per_head(device):
     jobs = _jobs(device, heads=5, seed=1)
     single = htrc_flat_runner.FlatRunner(2048, 2048, mode="fast", use_graph=False, **KW)
