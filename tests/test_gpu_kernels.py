@@ -773,13 +773,14 @@ def test_select_and_tile16_tile32_on_oracle_state(device, store):
 @pytest.mark.parametrize("tile,leaf,ex,group,stride,heads", [
     (64, 64, 6, 1, 1, 1), (64, 64, 6, 2, 4, 1), (64, 32, 16, 1, 1, 2), (64, 128, 3, 1, 1, 1),
     (64, 64, 0, 1, 1, 1), (64, 64, 24, 1, 1, 1), (32, 64, 6, 1, 1, 3), (32, 16, 40, 1, 2, 1),
-    (32, 64, 6, 3, 1, 1)])
+    (32, 64, 6, 3, 1, 1), (64, 16, 7, 1, 1, 1), (32, 16, 7, 2, 1, 2)])
 def test_route16_on_oracle_state(device, store, tile, leaf, ex, group, stride, heads):
     """The oracle's 16-bit leaf state through the fused route: the near sets are exactly those of
     the stage select + top-k on the same state (route_select16 uses select16's arithmetic), and
     against the oracle's they differ only at SEL near-ties; outputs within the operator bar on
     every tile whose near set is the oracle's; replicated heads give identical results.  ex = 24
-    near leaves of 24 leave an empty far field, ex = 0 an empty near field."""
+    near leaves of 24 leave an empty far field, ex = 0 an empty near field; leaf 16 with 7 near
+    leaves ends the near list with a half block (its second 16-token run masked)."""
     n = tile * 41 + 5
     q, k, v = _data(n, nk=64 * 24, seed=tile + leaf + ex + group)
     scale = 1 / math.sqrt(128)
