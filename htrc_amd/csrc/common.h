@@ -252,6 +252,16 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 
+// gfx950 transposing 8-bit read: within each group of 16 lanes, lanes 2j and 2j + 1 address the
+// two 8-byte halves of a 16-byte piece of "row" j (j = 0..7), and lane L receives byte L % 16 of
+// rows 0..7 in order (checked on the device: a byte column of eight rows per lane).
+typedef int v2i_lds __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i_lds lds_v2i;
+__device__ __forceinline__ u32x2 lds_read_tr8(const void* p) {
+    const v2i_lds v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(p));
+    return __builtin_bit_cast(u32x2, v);
+}
+
 // XOR swizzle of the 16-byte chunks of a 256-byte LDS row: row r keeps chunk c at c ^ swz(r),
 // a linear map of r's low four bits (period 16).  Both read patterns on such rows are free of
 // bank conflicts whether the LDS serves 128 or 256 bytes per cycle: the 16-byte QK operand

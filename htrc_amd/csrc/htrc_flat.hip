@@ -2075,14 +2075,21 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
 //     so every LDS operand read feeds two row blocks): one continuous stream of 32-key blocks,
 //     the far leaves first, then the near tokens, each block staged once in LDS for both waves
 //     through a 2-slot ring, the next block's loads issued before the current block is
-//     computed.  Near blocks and bf16 far blocks arrive by direct global->LDS loads (each wave
-//     its 16 rows); fp8 far blocks come through registers, their codes widened to fp16 (value *
-//     2^-8, exactly) as they are staged.  Far: score = (dq . g) (* 256 sg) + lz, PV with
+//     computed.  Every block arrives by direct global->LDS loads (each wave its 16 rows); fp8
+//     far blocks stay e4m3 codes in LDS, widened to fp16 (value * 2^-8, exactly) as the operands
+//     are read.  Far: score = (dq . g) (* 256 sg) + lz, PV with
 //     fp16(p * 256 sv) . vb (fp8) or bf16(p) . vb (bf16); near: score = (q . k) * scale (bf16),
 //     PV bf16(p) . v -- the products of tile16_kernel, in one softmax whose reference is the
 //     row's far-field maximum (redone with a moved reference if a row total leaves
 //     [2^-60, 2^64], as route_kernel).
 // ---------------------------------------------------------------------------------------------
+// 16-byte position of chunk c of row r of 128-byte rows (e4m3 codes) staged in LDS: c ^ sw8(r).
+// A read of 8 bytes per lane whose 32 lanes touch 16 rows, rows 16 h + 0..15 or 4 g + 0..3,
+// 16 + 4 g + 0..3 (g = 2 p, 2 p + 1), covers all 64 banks once: sw8 maps each such set of rows
+// one-to-one onto (r % 2, position), while r & 7 would put rows r, r + 8 (resp. r + 16) on the
+// same banks.
+__device__ __forceinline__ int sw8(int r) { return ((r >> 1) & 7) ^ ((r >> 2) & 4); }
+
 template <bool FP8, int NRB>
 __global__ __launch_bounds__(256, 3) void route_select16_kernel(
     const uint16_t* __restrict__ dq16, const void* __restrict__ g, const float* __restrict__ sg,
@@ -2174,21 +2181,22 @@ __global__ __launch_bounds__(256, 3) void route_select16_kernel(
         if constexpr (FP8) {
             // fp8: each wave streams its groups through its own 3-slot LDS ring by direct loads,
             // two groups ahead (the wave reads only what it loaded: no barriers).  Slot: 16 rows
-            // of 128 code bytes, chunk k of row r at 16-byte position k ^ (r & 7) (one 8-lane
-            // phase of a read touches 8 positions), then sg (64 B) and lz (64 B).
+            // of 128 code bytes, chunk k of row r at 16-byte position k ^ sw8(r), then sg (64 B)
+            // and lz (64 B); lane L of load i (rows 8 i + L / 8) gets position L % 8 of its row,
+            // chunk (L % 8) ^ ((L / 16) % 4) ^ 4 i.
 #pragma unroll
             for (int rb = 0; rb < NRB; ++rb)   // the row operands land before the first direct load
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) asm volatile("" : : "v"(b[rb][ks]));
             const uint32_t ring_w = lds_addr(&s16ring[w][0][0]);
-            const uint32_t voff = (uint32_t)((lane >> 3) * D + 16 * ((lane & 7) ^ ((lane >> 3) & 7)));
+            const uint32_t voff = (uint32_t)((lane >> 3) * D + 16 * ((lane & 7) ^ ((lane >> 4) & 3)));
             const int ngr = cw < nb ? (nb - cw + 63) / 64 : 0;
             auto issue = [&](int gj) {
                 if (gj >= ngr) return;
                 const int64_t s0 = gs * nb_pad + cw + 64 * gj;
                 const uint32_t slot = ring_w + (uint32_t)(gj % S16_RING) * S16_SLOT;
                 dma16s((const uint8_t*)g + s0 * D, voff, slot);
-                dma16s((const uint8_t*)g + (s0 + 8) * D, voff, slot + 1024);
+                dma16s((const uint8_t*)g + (s0 + 8) * D, voff ^ 64u, slot + 1024);
                 if (lane < 8) dma16(lane < 4 ? sg + s0 + 4 * lane : lz + s0 + 4 * (lane - 4), slot + 2048);
             };
 #pragma unroll
@@ -2201,7 +2209,7 @@ __global__ __launch_bounds__(256, 3) void route_select16_kernel(
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
                     const int kc = 2 * ks + (grp >> 1);
-                    x.a[ks] = *(const u32x2*)(slot + col * D + 16 * (kc ^ (col & 7)) + 8 * (grp & 1));
+                    x.a[ks] = *(const u32x2*)(slot + col * D + 16 * (kc ^ sw8(col)) + 8 * (grp & 1));
                 }
                 x.sgv = *(const f32x4*)(slot + 2048 + 16 * grp);
                 x.lzv = *(const f32x4*)(slot + 2048 + 64 + 16 * grp);
@@ -2239,10 +2247,12 @@ __global__ __launch_bounds__(256, 3) void route_select16_kernel(
 }
 
 // One ring slot of route16_kernel: QK rows and PV rows, 32 rows of 128 16-bit values each, then
-// three 32-float scale vectors (lz, or -inf for a leaf of the near set or past nb; sg * 256;
-// sv * 256).  PV row r keeps its 16-byte chunk c at c ^ swz(r) (the transposing reads); QK row r
-// at c ^ swq(r), so that the QK operand reads (16 rows at one chunk) hit 16 different chunks and
-// every 8 consecutive rows 8 different chunks modulo 8: no bank conflicts in 8- or 16-lane phases.
+// the far block's 32-float scale vectors (lz; for fp8 also sg and sv, as stored).  PV row r keeps
+// its 16-byte chunk c at c ^ swz(r) (the transposing reads); QK row r at c ^ swq(r), so that the
+// QK operand reads (16 rows at one chunk) hit 16 different chunks and every 8 consecutive rows 8
+// different chunks modulo 8: no bank conflicts in 8- or 16-lane phases.  An fp8 far block fills
+// the first 4 KiB of each region: 32 rows of 128 codes, chunk c of row r at c ^ sw8(r) (its QK
+// reads touch rows 16 h + 0..15 per 32 lanes, its PV reads rows 4 g + 0..3, 16 + 4 g + 0..3).
 constexpr int R16_ROWS = 32 * 256;
 constexpr int R16_SLOT = 2 * R16_ROWS + 3 * 32 * 4;
 __device__ __forceinline__ int swq(int r) { return r & 15; }
@@ -2307,7 +2317,6 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
     float* __restrict__ out, float* __restrict__ logz) {
     static_assert(NW == 2, "two waves per tile: wave w stages rows 16 w .. 16 w + 15 of every block");
     constexpr int NT = 64 * NW, TR = 16 * RB * NW;   // threads, rows per tile (16 RB rows per wave)
-    constexpr int NC = 512 / NT;                     // 16-byte chunks of a 32 x 256-byte region per thread
     __shared__ __align__(16) char ring[2][R16_SLOT];
     // sized by the launch: exclusion bits [nb / 32 + 1], then the tile's near leaves [kxe]
     extern __shared__ __align__(16) uint32_t r16_dyn[];
@@ -2371,14 +2380,18 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
         dma_x4<false>(bq_, voq0, bq_, voq0 ^ 64u, bq_, voq0 ^ 128u, bq_, voq0 ^ 192u, lq);
         dma_x4<false>(bp_, vop0, bp_, vop0 ^ 144u, bp_, vop0 ^ 128u, bp_, vop0 ^ 16u, lp);
     };
-    // fp8 far blocks go through registers (their codes are widened to fp16 on the way to LDS):
-    // this thread's chunks j of a 32-row region: row rr(j), 16-byte chunk cr; LDS byte offsets
-    int tn = (int)threadIdx.x;                              // redefined every pass, as ln
-    auto rr = [&](int j) { return (tn >> 4) + (NT / 16) * j; };
-    auto oq = [&](int j) { return rr(j) * 256 + 16 * ((tn & 15) ^ swq(rr(j))); };
-    auto op = [&](int j) { return R16_ROWS + rr(j) * 256 + 16 * ((tn & 15) ^ swz(rr(j))); };
-    u32x2 rq[FP8 ? NC : 1], rp[FP8 ? NC : 1];
-    float rsc = 0.0f;
+    // fp8 far blocks: the code rows (128 bytes) as they are, chunk c of row r at 16-byte
+    // position c ^ sw8(r) of the QK and PV regions (rows 128 bytes apart), widened to fp16 as
+    // they are read.  Lane L of load i (rows 16 w + 8 i + L / 8) gets position L % 8 of its row,
+    // chunk (L % 8) ^ sw8(row) = (L % 8) ^ ((L / 16) % 4) ^ 4 (i ^ w).
+    auto dma_rows8 = [&](const uint8_t* xq, const uint8_t* xp, uint32_t slot_lds) {
+        const uint32_t vo = (uint32_t)((ln >> 3) * D + 16 * ((ln & 7) ^ ((ln >> 4) & 3) ^ (4 * wv)));
+        const uint32_t lq = slot_lds + (uint32_t)wv * 2048, lp = slot_lds + R16_ROWS + (uint32_t)wv * 2048;
+        dma16s(xq, vo, lq);
+        dma16s(xq + 8 * D, vo ^ 64u, lq + 1024);
+        dma16s(xp, vo, lp);
+        dma16s(xp + 8 * D, vo ^ 64u, lp + 1024);
+    };
     auto run_pos = [&](int j) { return j < e_n ? j : 0; };  // past the list: its start again (masked)
     // near block bi (tokens of the near list from 32 (bi - nf)): wave w loads the 16-token run
     // 32 (bi - nf) + 16 w (past the list: the list's start again, masked)
@@ -2387,49 +2400,28 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
         const int64_t ra = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[j / LEAF]) * LEAF + (j % LEAF);
         dma_rows16(k + ra * D, v + ra * D, sl_lds);
     };
-    // Block bi into ring slot `slot`: a bf16 far block or a near block by direct loads (landed
-    // once this wave's vmcnt drains), an fp8 far block into registers (fetch) and LDS (put).
+    // Block bi into ring slot `slot` by direct loads (landed once this wave's vmcnt drains): a
+    // far block (its rows 16 w .. of g and vb from wave w; lz, and for fp8 sg and sv, from wave 0)
+    // or a near block.
     auto fetch = [&](int bi, int slot) {
         char* sl = &ring[slot][0];
         const uint32_t sl_lds = lds_addr(sl);
         if (bi < nf) {                                      // 32 consecutive state rows of the group
             const int64_t r0 = gs * nb_pad + 32 * bi;
+            const int64_t rw = r0 + 16 * wv;
             if constexpr (FP8) {
-#pragma unroll
-                for (int j = 0; j < NC; ++j) {
-                    const int64_t sr = r0 + rr(j);
-                    rq[j] = *(const u32x2*)((const uint8_t*)g + sr * D + 8 * (tn & 15));
-                    rp[j] = *(const u32x2*)((const uint8_t*)vb + sr * D + 8 * (tn & 15));
+                dma_rows8((const uint8_t*)g + rw * D, (const uint8_t*)vb + rw * D, sl_lds);
+                if (wv == 0 && lane < 8) {
+                    dma16<false>(lz + r0 + 4 * lane, sl_lds + 2 * R16_ROWS);
+                    dma16<false>(sg + r0 + 4 * lane, sl_lds + 2 * R16_ROWS + 128);
+                    dma16<false>(sv + r0 + 4 * lane, sl_lds + 2 * R16_ROWS + 256);
                 }
-                const int s = threadIdx.x;
-                if (s < 32) rsc = lz[r0 + s];
-                else if (s < 64) rsc = sg[r0 + s - 32];
-                else if (s < 96) rsc = sv[r0 + s - 64];
             } else {
-                const int64_t rw = r0 + 16 * wv;
                 dma_rows16((const uint16_t*)g + rw * D, (const uint16_t*)vb + rw * D, sl_lds);
                 if (wv == 0 && lane < 8) dma16<false>(lz + r0 + 4 * lane, sl_lds + 2 * R16_ROWS);
             }
         } else {
             fetch_near(bi, sl_lds);
-        }
-    };
-    auto put = [&](int bi, int slot) {                     // the register half of an fp8 far block
-        if constexpr (FP8) {
-            if (bi < nf) {
-                char* sl = &ring[slot][0];
-#pragma unroll
-                for (int j = 0; j < NC; ++j) {
-                    *(u32x4*)(sl + oq(j)) = e4m3x8_to_h8_cvt(rq[j]);
-                    *(u32x4*)(sl + op(j)) = e4m3x8_to_h8_cvt(rp[j]);
-                }
-                const int s = threadIdx.x;
-                if (s < 96) {
-                    // lz of a leaf in the near set (or past nb) -> -inf: its far score is -inf, p = 0
-                    const float x = s < 32 ? (((exbits[bi] >> s) & 1u) ? -INFINITY : rsc) : __fmul_rn(rsc, 256.0f);
-                    *(float*)(sl + 2 * R16_ROWS + 4 * s) = x;
-                }
-            }
         }
     };
     RowsN<RB> st;
@@ -2439,7 +2431,7 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
         const int col = ln & 15, grp = ln >> 4, lane = ln;
         float u[RB][8], pscale[8];
         const float* scl = (const float*)(slot + 2 * R16_ROWS);
-        const uint32_t exw = FP8 ? 0u : exbits[bi] >> (4 * grp);   // bf16: excluded leaves masked here
+        const uint32_t exw = exbits[bi] >> (4 * grp);      // excluded leaves: lz -> -inf below
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             if (hh == 1) __builtin_amdgcn_sched_barrier(0);   // one key half's QK operands at a time
@@ -2449,7 +2441,13 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
             for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const u32x4 A = *(const u32x4*)(slot + r * 256 + 16 * ((4 * ks + grp) ^ swq(r)));
+                u32x4 A;
+                if constexpr (FP8) {   // eight codes of row r, dims 32 ks + 8 grp ..: chunk 2 ks + grp / 2
+                    const int kc = 2 * ks + (grp >> 1);
+                    A = e4m3x8_to_h8_cvt(*(const u32x2*)(slot + r * D + 16 * (kc ^ sw8(r)) + 8 * (grp & 1)));
+                } else {
+                    A = *(const u32x4*)(slot + r * 256 + 16 * ((4 * ks + grp) ^ swq(r)));
+                }
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb) {
                     if constexpr (FP8) acc[rb] = mfma_f16(A, bx[rb][ks], acc[rb]);
@@ -2461,27 +2459,38 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
             const f32x4 svv = FP8 ? *(const f32x4*)(scl + 64 + 16 * hh + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float lzi = lzv[i];
-                if constexpr (!FP8) {   // excluded key: lz -> -inf, one bit select on the sign-extended bit
-                    const uint32_t ex = (uint32_t)__builtin_amdgcn_sbfe((int)exw, 16 * hh + i, 1);
-                    uint32_t lzb;
-                    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(lzb) : "v"(ex), "v"(0xff800000u), "v"(__float_as_uint(lzi)));
-                    lzi = __uint_as_float(lzb);
-                }
+                // excluded key: lz -> -inf, one bit select on the sign-extended bit
+                const uint32_t ex = (uint32_t)__builtin_amdgcn_sbfe((int)exw, 16 * hh + i, 1);
+                uint32_t lzb;
+                asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(lzb) : "v"(ex), "v"(0xff800000u), "v"(__float_as_uint(lzv[i])));
+                const float lzi = __uint_as_float(lzb);
+                // fp8: the widened codes are value * 2^-8, so the row scales enter * 256 (exactly)
+                const float sgi = FP8 ? __fmul_rn(sgv[i], 256.0f) : 1.0f;
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb) {
-                    const float dot = FP8 ? __fmul_rn(acc[rb][i], sgv[i]) : acc[rb][i];
+                    const float dot = FP8 ? __fmul_rn(acc[rb][i], sgi) : acc[rb][i];
                     u[rb][4 * hh + i] = __fmaf_rn(__fadd_rn(dot, lzi), LOG2E, -st.m[rb]);
                 }
-                pscale[4 * hh + i] = svv[i];
+                pscale[4 * hh + i] = FP8 ? __fmul_rn(svv[i], 256.0f) : 1.0f;
             }
         }
-        auto vop_ = [&](int db) {
-            const u32x2 lo = tr_operand(slot + R16_ROWS, 0, db, lane), hi = tr_operand(slot + R16_ROWS, 16, db, lane);
-            return u32x4{lo.x, lo.y, hi.x, hi.y};
-        };
-        if constexpr (FP8) rows_update_f16<RB>(st, u, pscale, vop_);
-        else rows_update_bf16<RB>(st, u, vop_);
+        if constexpr (FP8) {
+            // V^T of dims 16 db + L % 16 at the keys of P's k-items in lane group grp (4 grp + 0..3,
+            // then 16 + 4 grp + 0..3: the QK accumulator layout): lanes 2 j, 2 j + 1 of the group
+            // address the two halves of chunk db of the j-th of those key rows; the transposing byte
+            // read hands lane L that dim of the eight rows, widened to fp16
+            auto vop8 = [&](int db) {
+                const int j = col >> 1, rw8 = 4 * grp + (j & 3) + 16 * (j >> 2);
+                return e4m3x8_to_h8_cvt(lds_read_tr8(slot + R16_ROWS + rw8 * D + 16 * (db ^ sw8(rw8)) + 8 * (col & 1)));
+            };
+            rows_update_f16<RB>(st, u, pscale, vop8);
+        } else {
+            auto vop_ = [&](int db) {
+                const u32x2 lo = tr_operand(slot + R16_ROWS, 0, db, lane), hi = tr_operand(slot + R16_ROWS, 16, db, lane);
+                return u32x4{lo.x, lo.y, hi.x, hi.y};
+            };
+            rows_update_bf16<RB>(st, u, vop_);
+        }
     };
     // one 32-token block of the near field: score = (q . k) * scale; the second run of 16 is past
     // the list (masked) only in the last block when the list holds an odd number of 16-token runs
@@ -2514,14 +2523,12 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
         };
         rows_update_bf16<RB>(st, u, vop_);
     };
-    // block bi from slot S while block bi + 1 is fetched into the other slot (put after the
-    // compute when it comes through registers); the step ends with both waves' loads landed
+    // block bi from slot S while block bi + 1 is fetched into the other slot; the step ends with
+    // both waves' loads landed
     auto far_step = [&](auto par, int bi) {
         constexpr int S = decltype(par)::value;
-        const bool more = bi + 1 < nblk;
-        if (more) fetch(bi + 1, S ^ 1);
+        if (bi + 1 < nblk) fetch(bi + 1, S ^ 1);
         far_block(&ring[S][0], bi);
-        if (more) put(bi + 1, S ^ 1);
         wait_vmcnt<0>();
         __syncthreads();
     };
@@ -2535,7 +2542,7 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
     for (int pass = 0; pass < MAX_PASSES; ++pass) {
-        asm volatile("" : "+v"(ln), "+v"(tn));
+        asm volatile("" : "+v"(ln));
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             st.m[rb] = mref[rb];
@@ -2551,7 +2558,6 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) asm volatile("" : : "v"(bx[rb][ks]));
         fetch(0, 0);
-        put(0, 0);
         wait_vmcnt<0>();
         __syncthreads();
         // far blocks 0 .. nf - 1 in slots 0, 1, 0, ..; the near blocks continue the alternation
