@@ -401,18 +401,18 @@ __device__ __forceinline__ uint32_t quant4_e4m3_cvt(f32x4 x, float c) {
     return (uint32_t)r;
 }
 
-// int8 codes of x_i * c rounded half away from zero, packed little-endian: y = x c, then
-// trunc(y + copysign(0.5, y)) in fp32 (h3/htrc_flat_triton.py:77-79: where(x >= 0, x + 0.5,
-// x - 0.5) and a truncating int8 cast; 0.49999997 -> 1 as there).  copysign is one bit select
-// (v_bfi_b32); v_cvt_i32_f32 truncates, and its SDWA form writes the low byte of each code
-// (the two's-complement int8) into byte i of the packed word in place.
+// int8 codes of x_i * c rounded half away from zero, packed little-endian: trunc(x c +
+// copysign(0.5, x)) (h3/htrc_flat_triton.py:77-79: where(x >= 0, x + 0.5, x - 0.5) and a
+// truncating int8 cast; 0.49999997 -> 1 as there), with x c +- 1/2 taken in one FMA (c > 0, so
+// the sign is x's): against rounding x c first this differs only where x c lies within an ulp
+// of a half-integer, and saves an instruction per code.  copysign is one bit select; v_cvt_i32_f32
+// truncates, and its SDWA form writes the low byte of each code (the two's-complement int8) into
+// byte i of the packed word in place.
 __device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
     float z[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float y = __fmul_rn(x[i], c);
-        z[i] = __fadd_rn(y, __uint_as_float((__float_as_uint(y) & 0x80000000u) | 0x3f000000u));
-    }
+    for (int i = 0; i < 4; ++i)
+        z[i] = __fmaf_rn(x[i], c, __uint_as_float((__float_as_uint(x[i]) & 0x80000000u) | 0x3f000000u));
     uint32_t u = (uint32_t)(int)z[0];
     asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(u) : "v"(z[1]));
     asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(u) : "v"(z[2]));
