@@ -160,6 +160,14 @@ __device__ __forceinline__ uint32_t pack2bf(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// The same pair, opaque to the optimiser: reading bf16(a) back as a float (h << 16) otherwise
+// becomes a second conversion of a alone instead of a shift of the packed word.
+__device__ __forceinline__ uint32_t pack2bf_opaque(float a, float b) {
+    uint32_t h = pack2bf(a, b);
+    asm("" : "+v"(h));
+    return h;
+}
+
 // Two fp32 -> packed fp16 pair, round to nearest even (v_cvt_f16_f32 in the default mode).
 __device__ __forceinline__ uint32_t pack2h(float a, float b) {
     const _Float16 ha = (_Float16)a, hb = (_Float16)b;
@@ -180,10 +188,10 @@ __device__ __forceinline__ void split3x8(const float* x, bf16x8& hi, bf16x8& mid
     uint32_t h[4], m[4], l[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        h[j] = pack2bf(x[2 * j], x[2 * j + 1]);
+        h[j] = pack2bf_opaque(x[2 * j], x[2 * j + 1]);
         const float r0 = __fsub_rn(x[2 * j], __uint_as_float(h[j] << 16));
         const float r1 = __fsub_rn(x[2 * j + 1], __uint_as_float(h[j] & 0xffff0000u));
-        m[j] = pack2bf(r0, r1);
+        m[j] = pack2bf_opaque(r0, r1);
         l[j] = pack2bf(__fsub_rn(r0, __uint_as_float(m[j] << 16)), __fsub_rn(r1, __uint_as_float(m[j] & 0xffff0000u)));
     }
     hi = as_bf16x8(u32x4{h[0], h[1], h[2], h[3]});
@@ -196,7 +204,7 @@ __device__ __forceinline__ void split2x8(const float* x, bf16x8& hi, bf16x8& lo)
     uint32_t h[4], l[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        h[j] = pack2bf(x[2 * j], x[2 * j + 1]);
+        h[j] = pack2bf_opaque(x[2 * j], x[2 * j + 1]);
         l[j] = pack2bf(__fsub_rn(x[2 * j], __uint_as_float(h[j] << 16)),
                        __fsub_rn(x[2 * j + 1], __uint_as_float(h[j] & 0xffff0000u)));
     }

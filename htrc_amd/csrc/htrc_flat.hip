@@ -547,10 +547,13 @@ __global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restri
         sh_sg = f32x4{sh_sg[1], sh_sg[2], sh_sg[3], vsg};
         sh_lz = f32x4{sh_lz[1], sh_lz[2], sh_lz[3], vlz};
         if (FP8) sh_sv = f32x4{sh_sv[1], sh_sv[2], sh_sv[3], vsv};
-        if (((l - l0) & 3) == 3 && ((l - l0) >> 2) == grp) {
-            kp_sg = sh_sg;
-            kp_lz = sh_lz;
-            if (FP8) kp_sv = sh_sv;
+        if (((l - l0) & 3) == 3) {           // wave-uniform: a real branch, every fourth leaf
+            asm volatile("");
+            if (((l - l0) >> 2) == grp) {
+                kp_sg = sh_sg;
+                kp_lz = sh_lz;
+                if (FP8) kp_sv = sh_sv;
+            }
         }
     };
     // products of the current leaf and its log-partition
