@@ -836,6 +836,85 @@ struct TopkSmem {
     uint32_t prefix, remaining;
 };
 
+// Small kx (<= 64), idx only: the same set as the radix select below, from a lower bound of the
+// threshold.  Wave 0 takes the maxima of the 64 strided subsets l = j (mod 64) and sorts them
+// (bitonic, across the lanes); the kx-th largest, L, has kx subsets holding a key >= L, so at
+// least kx keys are >= L and the kx-th largest key is too.  The keys >= L (a few more than kx
+// for score rows) are compacted in leaf order and each is ranked exactly: keys above it, and
+// equal keys at lower leaves.  More than 256 candidates (many equal keys): returns false before
+// anything is written, and the radix select runs.  Five barriers, every thread through each.
+template <typename Keys>
+__device__ bool topk_small(Keys keys, int nb, int kx, TopkSmem& sm, int32_t* idx_out) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    uint32_t* ck = sm.hist;        // candidate keys
+    uint32_t* cl = sm.cnt_gt;      // candidate leaves
+    if (wv == 0) {
+        uint32_t m = 0;            // below every order key of a real score
+#pragma unroll 4
+        for (int l = lane; l < nb; l += 64) m = max(m, keys(l));
+#pragma unroll
+        for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+            for (int j = k >> 1; j > 0; j >>= 1) {   // blocks of k descending where lane & k == 0
+                const uint32_t o = (uint32_t)__shfl_xor((int)m, j, 64);
+                m = (((lane & j) == 0) == ((lane & k) == 0)) ? max(m, o) : min(m, o);
+            }
+        if (lane == kx - 1) sm.prefix = m;
+    }
+    __syncthreads();
+    const uint32_t lb = sm.prefix;
+    const int chunk = (nb + 255) / 256;
+    const int a = min(nb, tid * chunk), b = min(nb, a + chunk);
+    uint32_t n = 0;
+    for (int l = a; l < b; ++l) n += keys(l) >= lb;
+    uint32_t incl = n;             // inclusive prefix over the wave, then the waves before
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = (uint32_t)__shfl_up((int)incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) sm.cnt_eq[wv] = incl;
+    __syncthreads();
+    uint32_t off = incl - n, nc = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t c = sm.cnt_eq[j];
+        if (j < wv) off += c;
+        nc += c;
+    }
+    if (nc > 256) return false;    // the same nc in every thread
+    for (int l = a; l < b; ++l) {
+        const uint32_t key = keys(l);
+        if (key >= lb) {
+            ck[off] = key;
+            cl[off] = (uint32_t)l;
+            ++off;
+        }
+    }
+    __syncthreads();
+    bool sel = false;
+    uint32_t leaf = 0;
+    if ((uint32_t)tid < nc) {
+        const uint32_t key = ck[tid];
+        uint32_t r = 0;
+#pragma unroll 8
+        for (uint32_t j = 0; j < nc; ++j) {
+            const uint32_t kj = ck[j];
+            r += (kj > key || (kj == key && j < (uint32_t)tid)) ? 1u : 0u;
+        }
+        sel = r < (uint32_t)kx;
+        leaf = cl[tid];
+    }
+    const uint64_t bal = __ballot(sel);   // output position: selected candidates before this one
+    if (lane == 0) sm.cnt_eq[4 + wv] = (uint32_t)__popcll(bal);
+    __syncthreads();
+    uint32_t pos = (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
+    for (int j = 0; j < wv; ++j) pos += sm.cnt_eq[4 + j];
+    if (sel) idx_out[pos] = (int32_t)leaf;
+    __syncthreads();
+    return true;
+}
+
 // keys(l) is order_key(sel[l]) for l < nb (an LDS array, or computed from global memory for rows
 // longer than the LDS holds).  Writes idx[0..kx) ascending and (optionally) excl.
 template <typename Keys>
@@ -851,6 +930,7 @@ __device__ void topk_row(Keys keys, int nb, int kx, TopkSmem& sm, int32_t* idx_o
         __syncthreads();
         return;
     }
+    if (kx <= 64 && idx_out && !excl_out && !idx_lds && topk_small(keys, nb, kx, sm, idx_out)) return;
     if (tid == 0) {
         sm.prefix = 0;
         sm.remaining = (uint32_t)kx;

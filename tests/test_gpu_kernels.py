@@ -179,6 +179,58 @@ def test_select_bitexact_on_oracle_state(device):
         assert np.array_equal(_np(sel[0])[:, :nb].view(np.uint32), osel.view(np.uint32)), f"stride {stride}"
 
 
+def _tie_rows(rng, rows, nb):
+    """SEL rows for top-k checks: normal scores with every seventh leaf tied at 0.25, a row of
+    all ties, a row with -0.0 among them, and a row of eight levels."""
+    sel = rng.standard_normal((rows, nb)).astype(np.float32)
+    sel[:, ::7] = np.float32(0.25)
+    sel[0, :] = 1.0
+    sel[1, :5] = -0.0
+    sel[2, :] = rng.integers(0, 8, nb).astype(np.float32)
+    return sel
+
+
+@pytest.mark.parametrize("store", ["int8", "fp8", "bf16"])
+@pytest.mark.parametrize("nb,kx,sink", [(1008, 32, 0), (256, 16, 3), (100, 1, 0), (64, 7, 0), (8192, 64, 0),
+                                         (1008, 100, 0), (9000, 64, 4)])
+def test_fused_select_topk_ties(device, store, nb, kx, sink):
+    """The fused selects' top-k (for kx <= 64 a candidate ranking under a lower bound of the
+    threshold, falling back to the radix select when more than 256 keys reach the bound) on
+    rows full of ties: with a zero g state SEL equals lz exactly, so the index sets must equal
+    the oracle's top-k of the lz rows (ties to the lower leaf, leaves < sink forced)."""
+    leaf, rows = 16, 6
+    if store != "int8" and not hip.route16_fits(nb, kx):
+        pytest.skip("beyond the 16-bit fused route's leaf limit")
+    rng = np.random.default_rng(nb + kx + sink)
+    sel = _tie_rows(rng, rows, nb)
+    nbp, nk, nq = nb_pad(nb), nb * leaf, rows * 64
+    lz = torch.full((1, rows, nbp), -math.inf, dtype=torch.float32)
+    lz[0, :, :nb] = torch.from_numpy(sel)
+    lz = lz.to(device)
+    kxe = min(kx, nb)
+    if store == "int8":
+        packed = {"dq8": torch.zeros(1, nq, 128, dtype=torch.int8, device=device),
+                  "sdq": torch.ones(1, nq, device=device),
+                  "k8": torch.zeros(1, nk, 128, dtype=torch.int8, device=device)}
+        state = {"g8": torch.zeros(1, rows, nbp, 128, dtype=torch.int8, device=device),
+                 "sg": torch.ones(1, rows, nbp, device=device), "lz": lz}
+        idx, _ = hip.route_select(packed, state, nq=nq, leaf=leaf, kx=kx, sink=sink, ws={})
+    else:
+        gdt = torch.float8_e4m3fn if store == "fp8" else torch.bfloat16
+        zero16 = torch.zeros(1, nq, 128, dtype=torch.bfloat16, device=device)
+        packed = {"q16": zero16, "dq16": zero16, "k": torch.zeros(1, nk, 128, dtype=torch.bfloat16, device=device)}
+        packed["v"] = packed["k"]
+        state = {"g8": torch.zeros(1, rows, nbp, 128, dtype=gdt, device=device), "lz": lz,
+                 "vb": torch.zeros(1, rows, nbp, 128, dtype=gdt, device=device)}
+        if store == "fp8":
+            state["sg"] = torch.ones(1, rows, nbp, device=device)
+            state["sv"] = torch.ones(1, rows, nbp, device=device)
+        idx, _ = hip.route16_select(packed, state, nq=nq, leaf=leaf, kx=kx, sink=sink, ws={})
+    torch.cuda.synchronize()
+    oidx, _ = flat_i8.topk(sel, kxe, sink)
+    assert np.array_equal(_np(idx[0]), oidx)
+
+
 @pytest.mark.parametrize("nb,kx,sink", [(1008, 32, 0), (256, 16, 3), (37, 37, 0), (100, 1, 0), (8192, 64, 0),
                                          (9000, 1244, 220), (20000, 300, 5)])
 def test_topk_bitexact(device, nb, kx, sink):
