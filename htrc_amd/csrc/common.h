@@ -83,15 +83,33 @@ __device__ __forceinline__ float wave_max(float v) {
 // Reductions across the four 16-lane groups that share a column of an MFMA C tile, with the
 // gfx950 lane swaps: with both operands equal, the two results of v_permlane{16,32}_swap hold
 // {v[i], v[i ^ 16]} (resp. {v[i], v[i ^ 32]}) in each lane, so one max / add reduces a pair.
+// Maximum of two values that are never NaN: one v_max_f32 (fmaxf on the swapped words would
+// first quiet each operand with a v_max_f32 of its own).
+__device__ __forceinline__ float max_nonan(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 __device__ __forceinline__ float xor16_max(float v) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return max_nonan(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor32_max(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return max_nonan(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float grp_max(float v) { return xor32_max(xor16_max(v)); }
+
+// ln z for z >= 1 (a partition sum whose largest term is exp(0) = 1): log2 z by v_log_f32 (no
+// subnormal input to rescale, no infinity to pass through), times ln 2 as hi + lo with hi = ln 2
+// truncated to 24 bits (0x3f317217) and lo = fp32(ln 2 - hi) (0x3377d1cf), the product y hi
+// carried exactly by an FMA: log2 z ln 2 to within about an ulp.
+__device__ __forceinline__ float ln_ge1(float z) {
+    const float y = __builtin_amdgcn_logf(z);
+    const float hi = __uint_as_float(0x3f317217u), lo = __uint_as_float(0x3377d1cfu);
+    const float p = __fmul_rn(y, hi);
+    return __fadd_rn(p, __fmaf_rn(y, lo, __fmaf_rn(y, hi, -p)));
+}
 __device__ __forceinline__ float grp_sum(float v) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     v = __fadd_rn(__uint_as_float(a[0]), __uint_as_float(a[1]));

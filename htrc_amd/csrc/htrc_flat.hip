@@ -685,7 +685,7 @@ __global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restri
         store_v(1);
         // quantised after the last stores of leaf l - 1: this VALU work covers their latency
         // before the next iteration's wait
-        lzq = __fadd_rn(mx, __logf(z));
+        lzq = __fadd_rn(mx, ln_ge1(z));        // z >= 1: its largest term is exp(0)
         quantise(l);
     }
     store_g();
