@@ -173,8 +173,10 @@ __global__ __launch_bounds__(256) void pack_q_kernel(const void* __restrict__ qi
             cq[e] = round_away(div_by(x[e], s1, y1));
             cd[e] = round_away(div_by(d[e], s2, y2));
         }
-        *(u32x2*)(q8 + p * D + 8 * i) = pack8_i8(cq);
-        *(u32x2*)(dq8 + p * D + 8 * i) = pack8_i8(cd);
+        // non-temporal: the rows are next read only after the statistics have streamed the whole
+        // state through the caches (pack_q 3% faster alone)
+        __builtin_nontemporal_store(pack8_i8(cq), (u32x2*)(q8 + p * D + 8 * i));
+        __builtin_nontemporal_store(pack8_i8(cd), (u32x2*)(dq8 + p * D + 8 * i));
         if (i == 0) {
             sq[p] = s1;
             sdq[p] = s2;
