@@ -22,9 +22,10 @@ def rel_l2(a, b) -> float:
 
 
 def sel_error(sel_gpu, sel_ref, nb) -> np.ndarray:
-    """Per tile (row) max |SEL_gpu - SEL_ref| over the real leaves."""
-    a = np.asarray(sel_gpu, np.float64)[:, :nb]
-    b = np.asarray(sel_ref, np.float64)[:, :nb]
+    """Per tile (row) max |SEL_gpu - SEL_ref| over the real leaves (the padding columns past nb
+    are never written or read by the kernels: sliced off before any conversion)."""
+    a = np.asarray(sel_gpu)[:, :nb].astype(np.float64)
+    b = np.asarray(sel_ref)[:, :nb].astype(np.float64)
     return np.abs(a - b).max(axis=1)
 
 

@@ -1,0 +1,74 @@
+"""Seeded random knob combinations of flat_attention against the CPU oracle.
+
+Each case draws the state store, the fused route or the reference's stage structure, the tile
+(64 or 32 rows), the leaf size, ragged query and key counts, the near-leaf count, shared
+centres (kern["group"]), the select row stride, forced sink leaves and the query order from
+its own seed, so a failure names a reproducible combination.  The bars are those of the
+single-knob tests: every tile's near set equals the oracle's except where the oracle's own
+top-k boundary gap is within twice the measured SEL error, output rel-L2 <= 1e-2, and
+|dlogZ| <= 1e-3 (for the int8 state plus each row's far-score drift from the state's
+rounding, as in test_gpu_flat).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits, check_logz, gpu_sel, record, rel_l2, routing_report, sel_error
+from htrc_amd import htrc_flat, workloads
+from oracle import flat_i8
+
+pytestmark = pytest.mark.gpu
+
+OUT_REL_L2 = 1e-2
+LOGZ_ABS = 1e-3
+CASES = 48
+
+
+def _case(seed: int) -> dict:
+    rng = np.random.default_rng(1000 + seed)
+    leaf = int(rng.choice([16, 32, 64, 128]))
+    nb = int(rng.integers(max(4, 640 // leaf), 5000 // leaf + 1))
+    return dict(store=("int8", "fp8", "bf16")[seed % 3], tile=int(rng.choice([64, 32])), leaf=leaf,
+                n=int(rng.integers(700, 4001)), nk=nb * leaf, ex=int(rng.integers(0, min(40, nb) + 1)),
+                group=int(rng.choice([1, 1, 2, 3])), stride=int(rng.choice([1, 1, 2, 4])),
+                sink=int(rng.choice([0, 0, 2, 5])), order=str(rng.choice(["seq", "seq", "kmeans"])),
+                fused=bool(rng.integers(0, 2)))
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_random_knobs_vs_oracle(device, seed):
+    c = _case(seed)
+    name = "random " + " ".join(f"{k}={v}" for k, v in c.items())
+    print(name, flush=True)
+    q, k, v = workloads.clustered_runs(n=max(c["n"], c["nk"]), runs=max(1, max(c["n"], c["nk"]) // 64), heads=1,
+                                       seed=2000 + seed)
+    q = q[:, :c["n"]].contiguous()
+    k, v = k[:, :c["nk"]].contiguous(), v[:, :c["nk"]].contiguous()
+    st = {}
+    out, logz = htrc_flat.flat_attention(q[0].to(device), k[0].to(device), v[0].to(device), backend="hip",
+                                         tile=c["tile"], store=c["store"], dot="bf16", leaf=c["leaf"],
+                                         exact_leaves=c["ex"], sink_leaves=c["sink"], sel_stride=c["stride"],
+                                         order=c["order"], splits=4,
+                                         kern={"tile_bn": 64, "fused": c["fused"], "group": c["group"]},
+                                         return_logz=True, state=st)
+    torch.cuda.synchronize()
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=c["tile"], leaf=c["leaf"],
+                          exact_leaves=c["ex"], splits=1 if c["fused"] else 4, bn=64, sel_stride=c["stride"],
+                          sink_leaves=c["sink"], group=c["group"], order=c["order"], store=c["store"])
+    assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(logz).all()), name
+    nb = st["nb"]
+    if min(c["ex"] + c["sink"], nb) > 0:              # else no near set: the far field alone
+        sel = gpu_sel(st, c["stride"])
+        rep = routing_report(st["idx"][0].cpu().numpy(), ref["idx"], ref["sel"][:, :nb],
+                             sel_error(sel, ref["sel"], nb))
+        record(name, rep)
+        assert rep["mismatched"] <= rep["tieable"], f"{name}: {rep}"
+    err = rel_l2(out.cpu().numpy(), ref["out"])
+    assert err <= OUT_REL_L2, f"{name}: rel-L2 {err:.3e}"
+    if c["store"] == "int8":
+        check_logz(logz.cpu().numpy(), ref, st, LOGZ_ABS)
+    else:
+        dl = float(np.abs(logz.cpu().numpy() - ref["logz"]).max())
+        assert dl <= LOGZ_ABS, f"{name}: |dlogZ| {dl:.3e}"
