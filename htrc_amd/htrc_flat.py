@@ -19,6 +19,7 @@ backend does).
 """
 from __future__ import annotations
 
+import contextlib
 import math
 import time
 
@@ -148,6 +149,19 @@ class _Collect:
             self.state.update(extra)
 
 
+_WINDOW_STREAMS: dict = {}
+
+
+def _window_streams(device) -> tuple:
+    """Two side streams of the device (default priority), created once, that alternate the
+    tile windows of a call."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    pair = _WINDOW_STREAMS.get(idx)
+    if pair is None:
+        pair = _WINDOW_STREAMS[idx] = (torch.cuda.Stream(device=idx), torch.cuda.Stream(device=idx))
+    return pair
+
+
 def _windows(ng: int, tile_chunk, group: int):
     """Tile-group windows of the chunk loop (h3/htrc_flat.py:236-240): tile_chunk tiles, i.e.
     tile_chunk // group groups, per window; tile_chunk None or < 1 means one window."""
@@ -172,8 +186,9 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     ``order='kmeans'`` cuts the tiles from the queries regrouped by ``kmeans_order``; the
     output rows come back in query order (:148-149, 159-165).
     ``tile_chunk`` tiles of every head are processed per window (h3/htrc_flat.py:236-273): the
-    per-(tile, leaf) state is held for one window at a time, and the result does not depend on
-    it.  ``precision`` is accepted for compatibility: accumulation is IEEE fp32.  ``state``, if
+    per-(tile, leaf) state is held for at most two windows at a time (several windows alternate
+    over two streams; ``kern['window_streams'] = 1`` keeps one), and the result does not
+    depend on it.  ``precision`` is accepted for compatibility: accumulation is IEEE fp32.  ``state``, if
     a dict, receives the packed operands and the whole layer's leaf state and routing (for
     checks)."""
     kern = dict(kern or {})
@@ -226,10 +241,11 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     ng = int(mu.shape[1])                               # centres: tiles, or tile groups
     out = hip._buf(ws, "out", (h, nq, d), torch.float32, qh.device)
     logz = hip._buf(ws, "logz", (h, nq), torch.float32, qh.device)
-    wins = _windows(ng, tile_chunk, group)
-    keep = _Collect(state, h, ng, len(wins))
-    for g0, gn in wins:
-        g, lz, vbs, sg, sv = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=sdt, ws=ws, c0=g0, cn=gn)
+
+    def _window(w, g0, gn):
+        """Statistics, select / top-k and attention of the tile groups [g0, g0 + gn), the window's
+        buffers in workspace w."""
+        g, lz, vbs, sg, sv = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=sdt, ws=w, c0=g0, cn=gn)
         if quant.get("state"):                           # h3/htrc_flat.py:246-248, in place
             sfmt = quant["state"]
             sgsz = hip.D if not qg and sfmt != "fp4" else (qg or 16)
@@ -239,28 +255,48 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         tick("stats")
         sel = excl = idx = None
         if fused:
-            idx = hip._rows(ws, "idx", h, gn, (kx,), torch.int32, qh.device) if kx > 0 else None
+            idx = hip._rows(w, "idx", h, gn, (kx,), torch.int32, qh.device) if kx > 0 else None
             fn = hip.route if sdt == torch.int8 else hip.route16
-            fn(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, sink=sink, stride=stride, ws=ws, out=out,
+            fn(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, sink=sink, stride=stride, ws=w, out=out,
                logz=logz, idx=idx, group=group, perm=perm, tile=tile, g0=g0)
             tick("tile")
         else:
             if kx > 0 and select == "bound":            # h3/htrc_flat.py:255-257
-                sel = hip.bound_select(qsrc, mu, g, lz, nb, leaf=leaf, ws=ws, group=group, tile=tile, g0=g0, perm=perm)
+                sel = hip.bound_select(qsrc, mu, g, lz, nb, leaf=leaf, ws=w, group=group, tile=tile, g0=g0, perm=perm)
             if kx > 0 and select == "max":
                 sel = hip.rowmax_select(g=g, lz=lz, sg=sg, stride=stride, nb=nb, dq8=packed.get("dq8", packed.get("dq16")),
-                                        sdq=packed.get("sdq"), ws=ws, group=group, tile=tile, g0=g0)
+                                        sdq=packed.get("sdq"), ws=w, group=group, tile=tile, g0=g0)
             if kx > 0:
-                idx, excl = hip.topk_excl(sel, nb, kx, sink, ws=ws)
+                idx, excl = hip.topk_excl(sel, nb, kx, sink, ws=w)
             else:
-                excl = hip._rows(ws, "excl", h, gn, (nb_pad(nb),), torch.int8, qh.device)
+                excl = hip._rows(w, "excl", h, gn, (nb_pad(nb),), torch.int8, qh.device)
                 excl.zero_()
             tick("select")
             hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
-                               bn=int(kern.get("tile_bn", 32)), ws=ws, out=out, logz=logz, group=group, perm=perm,
+                               bn=int(kern.get("tile_bn", 32)), ws=w, out=out, logz=logz, group=group, perm=perm,
                                tile=tile, g0=g0)
             tick("tile")
         keep.add(g0, gn, g8=g, sg=sg, lz=lz, vb=vbs, sv=sv, sel=sel, excl=excl, idx=idx)
+
+    wins = _windows(ng, tile_chunk, group)
+    keep = _Collect(state, h, ng, len(wins))
+    # Several windows: the even and odd ones on two side streams, each with its own window
+    # buffers, so that a window's statistics run beside the previous window's select and attend
+    # (filling the tails of their launches; two windows' state in flight).  One window, stage
+    # timing (prof), state checks or kern["window_streams"] = 1: the caller's stream, in order.
+    pipe = len(wins) > 1 and prof is None and state is None and int(kern.get("window_streams", 2)) > 1
+    if pipe:
+        cur = torch.cuda.current_stream(qh.device)
+        side = _window_streams(qh.device)
+        for s in side:
+            s.wait_stream(cur)
+        wsw = (None, None) if ws is None else (ws.setdefault("window_a", {}), ws.setdefault("window_b", {}))
+    for wi, (g0, gn) in enumerate(wins):
+        with torch.cuda.stream(side[wi & 1]) if pipe else contextlib.nullcontext():
+            _window(wsw[wi & 1] if pipe else ws, g0, gn)
+    if pipe:
+        for s in side:
+            cur.wait_stream(s)
     if state is not None:
         state.update(packed)
         keep.finish(nb=nb, kx=kx, group=group, perm=perm, tile=tile, windows=wins)

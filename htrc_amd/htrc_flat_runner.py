@@ -59,10 +59,12 @@ def _ceil(a: int, b: int) -> int:
 
 def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, heads: int = 1, splits: int = 1,
                     kx: int = 0, group: int = 1, order: str = "seq", tile: int = TILE, tile_chunk: int | None = None,
-                    store: str = "int8", fused: bool = True, bf16_inputs: bool = True) -> int:
+                    store: str = "int8", fused: bool = True, bf16_inputs: bool = True, window_streams: int = 2) -> int:
     """Device bytes of one operator call's workspace: the whole layer's packed operands and
-    outputs, and the per-(centre, leaf) state, routing and partials of one tile window of
-    ``tile_chunk`` tiles (all tiles when None)."""
+    outputs, and the per-(centre, leaf) state, routing and partials of the tile windows of
+    ``tile_chunk`` tiles (all tiles when None) in flight: one, or two when there are several
+    windows and the operator alternates them over two streams (kern["window_streams"] = 2, its
+    default)."""
     nt = _ceil(queries, tile)
     ng = _ceil(nt, max(1, int(group)))
     gw = ng if tile_chunk is None else max(1, min(ng, int(tile_chunk) // max(1, int(group))))
@@ -92,18 +94,21 @@ def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, hea
             window += tw * int(splits) * int(tile) * (dim + 2) * 4      # split partials
     if order == "kmeans":
         layer += 8 * queries + 4 * 32 * dim                             # perm, assignments, centres
+    if gw < ng and int(window_streams) > 1:
+        window *= 2                                                     # two windows in flight
     return int(heads) * (layer + window)
 
 
 def predicted_peak_mib(keys: int, tile: int, tile_chunk: int, splits: int = 8, leaf: int = 16, dim: int = 128,
                        order: str = "seq", graph: bool = True, queries: int = 0, heads: int = 1, group: int = 1,
-                       exact_leaves: int = 256, store: str = "int8", fused: bool = True) -> float:
+                       exact_leaves: int = 256, store: str = "int8", fused: bool = True,
+                       window_streams: int = 2) -> float:
     """Peak device MiB above the caller's q/k/v (the signature of h3/htrc_flat_runner.py:61-68,
     extended): the operator's workspace with a window of ``tile_chunk`` tiles, plus the static
     fp32 q and bf16 k/v copies in graph mode.  ``queries`` defaults to ``keys``."""
     q = int(queries) if queries else int(keys)
     b = workspace_bytes(q, keys, leaf, dim, heads, splits=splits, kx=exact_leaves, group=group, order=order,
-                        tile=tile, tile_chunk=tile_chunk, store=store, fused=fused)
+                        tile=tile, tile_chunk=tile_chunk, store=store, fused=fused, window_streams=window_streams)
     if graph:
         b += int(heads) * (4 * q * dim + 2 * 2 * int(keys) * dim)
     return b / MIB
@@ -111,13 +116,14 @@ def predicted_peak_mib(keys: int, tile: int, tile_chunk: int, splits: int = 8, l
 
 def plan_chunk(free_bytes: int, keys: int, tile: int, splits: int = 8, order: str = "seq", graph: bool = True,
                queries: int = 0, leaf: int = 16, heads: int = 1, group: int = 1, exact_leaves: int = 256,
-               store: str = "int8", fused: bool = True) -> int:
+               store: str = "int8", fused: bool = True, window_streams: int = 2) -> int:
     """The largest of CHUNKS whose predicted peak fits in ``free_bytes`` (fewer windows, fewer
     launches; h3/htrc_flat_runner.py:71-82); MemoryError when not even the smallest fits."""
     need = None
     for c in CHUNKS:
         need = predicted_peak_mib(keys, tile, c, splits, leaf=leaf, order=order, graph=graph, queries=queries,
-                                  heads=heads, group=group, exact_leaves=exact_leaves, store=store, fused=fused)
+                                  heads=heads, group=group, exact_leaves=exact_leaves, store=store, fused=fused,
+                                  window_streams=window_streams)
         if need * MIB <= int(free_bytes):
             return c
     raise MemoryError(f"flat HTRC needs ~{need:.0f} MiB at the smallest window ({CHUNKS[-1]} tiles), "
@@ -138,7 +144,8 @@ class _Plan:
         kx = min(int(cfg["exact_leaves"]) + int(sink_leaves), nb)
         sizing = dict(leaf=int(cfg.get("leaf", 16)), order=cfg["order"], graph=graph, queries=int(queries),
                       heads=int(heads), group=max(1, int(kern.get("group", 1))), exact_leaves=kx,
-                      store=cfg.get("store", "int8"), fused=bool(kern.get("fused", True)))
+                      store=cfg.get("store", "int8"), fused=bool(kern.get("fused", True)),
+                      window_streams=int(kern.get("window_streams", 2)))
         if tile_chunk is None:
             tile_chunk = cfg["tile_chunk"] if free_bytes is None else plan_chunk(
                 free_bytes, keys, cfg["tile"], cfg.get("splits", 8), **sizing)

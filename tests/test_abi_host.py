@@ -191,16 +191,21 @@ def test_runner_modes_and_memory_model():
     # cfg3 layer in one window: per-(tile, leaf) state dominates: 24 * 1008 * 1024 * 392 B = 9252 MiB
     assert 9252 < mib < 16000
     assert htrc_flat_runner.plan_chunk(64 << 30, 64512, 64, leaf=64, queries=64512, heads=24) == 1024
-    # windows bound the state: 3.5 GiB takes windows of 64 tiles (~3.4 GiB), 128 tiles need ~4.0 GiB
+    # windows bound the state, two windows of it in flight (the operator alternates them over two
+    # streams): 3.5 GiB takes windows of 32 tiles (~3.4 GiB), 64 tiles need ~4.0 GiB; with one in
+    # flight (kern["window_streams"] = 1) 64 tiles fit
     c = htrc_flat_runner.plan_chunk(3584 << 20, 64512, 64, leaf=64, queries=64512, heads=24, exact_leaves=32)
-    assert c == 64
-    assert htrc_flat_runner.predicted_peak_mib(64512, 64, 128, leaf=64, queries=64512, heads=24,
+    assert c == 32
+    assert htrc_flat_runner.predicted_peak_mib(64512, 64, 64, leaf=64, queries=64512, heads=24,
                                                exact_leaves=32) > 3584
+    assert htrc_flat_runner.plan_chunk(3584 << 20, 64512, 64, leaf=64, queries=64512, heads=24, exact_leaves=32,
+                                       window_streams=1) == 64
     with pytest.raises(MemoryError):             # the layer's operands and outputs alone need ~3 GiB
         htrc_flat_runner.plan_chunk(1 << 30, 64512, 64, leaf=64, queries=64512, heads=24)
-    # the window state scales with the window: 128 against 1024 tiles (1008 real) at cfg3
+    # the window state scales with the window: 1024 tiles (1008 real, one window) against two
+    # windows of 128 in flight at cfg3
     m128 = htrc_flat_runner.predicted_peak_mib(64512, 64, 128, leaf=64, queries=64512, heads=24, exact_leaves=32)
-    assert mib - m128 == pytest.approx(24 * (1008 - 128) * (1024 * 392 + 4 * 32) / 2 ** 20, rel=1e-6)
+    assert mib - m128 == pytest.approx(24 * (1008 - 2 * 128) * (1024 * 392 + 4 * 32) / 2 ** 20, rel=1e-6)
     with pytest.raises(ValueError, match="mode"):
         htrc_flat_runner.FlatRunner(64, 64, mode="nope")
     assert htrc_flat_runner.SUPPORTED_MODES == ("fast", "balanced", "accurate", "max")
