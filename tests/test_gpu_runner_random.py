@@ -25,7 +25,7 @@ def _case(seed: int) -> dict:
     return dict(mode=str(rng.choice(["fast", "balanced", "accurate", "max"])),
                 store=("int8", "fp8", "bf16")[seed % 3], batch=int(rng.choice([1, 2, 3])),
                 sink=int(rng.choice([0, 0, 3])), tail=int(rng.choice([0, 0, 5])),
-                chunk=int(rng.choice([0, 0, 64])), leaf=leaf, ex=int(rng.integers(1, 24)),
+                chunk=int(rng.choice([0, 8, 16])), leaf=leaf, ex=int(rng.integers(1, 24)),
                 n=int(rng.integers(600, 2600)), m=int(rng.integers(1024 // leaf, 2600 // leaf)) * leaf,
                 heads=int(rng.integers(2, 5)))
 
