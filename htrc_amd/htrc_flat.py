@@ -6,10 +6,11 @@ leaf cumulants at the centre (log-partition lz, tilted key mean g, value mean vb
 query sees far leaves through lz + (q - mu).g with value vb, and the ``exact_leaves``
 leaves of largest row-max far logit exactly; both merge in one online softmax.
 
-One backend: hand-written gfx950 HIP kernels (``htrc_flat_hip``), INT8 Q/K dots and bf16
-PV dots with fp32 accumulation (the reference's ``store="int8", dot="bf16"`` path).
-``backend="triton"`` (the reference's GPU backend name) and ``backend="hip"`` select it;
-any other backend, or knobs the HIP path does not implement, raise ``ValueError``.
+One backend: hand-written gfx950 HIP kernels (``htrc_flat_hip``) for the reference's
+``dot="bf16"`` state stores: ``store="int8"`` (INT8 Q/K dots, bf16 PV, fp32 accumulation:
+the production path), ``"fp8"`` (e4m3 leaf state) and ``"bf16"``.  ``backend="triton"`` (the
+reference's GPU backend name) and ``backend="hip"`` select it; any other backend, or knobs
+the HIP path does not implement, raise ``ValueError``.
 
 Extensions over the reference: q/k/v may carry a leading head dimension ([H, N, D]) so a
 whole layer runs in one set of launches, and ``return_logz=True`` also returns the
