@@ -79,34 +79,50 @@ def record(name: str, rep: dict) -> None:
 
 def far_score_drift(st, ref) -> np.ndarray:
     """Per operator row (the packed row order): the largest |far score from the GPU's leaf state -
-    far score from the oracle's| over the leaves of the row's tile group (int8 state).  logZ is
-    1-Lipschitz in the scores, so the GPU and oracle logZ of a row may differ by this much more
-    than the operator bar when a g8 code of the GPU state rounds the other way at an fp32-noise
-    tie (and near-field scores, taken from exact tokens, do not move)."""
+    far score from the oracle's| over the leaves of the row's tile group (int8, fp8 or bf16
+    state).  logZ is 1-Lipschitz in the scores, so the GPU and oracle logZ of a row may differ by
+    this much more than the operator bar when a code of the GPU state rounds the other way at an
+    fp32-noise tie (and near-field scores, taken from exact tokens, do not move)."""
+    import torch
+    from oracle import bf16
     nb, tile, group = st["nb"], st["tile"], st["group"]
-    dq8 = ref["dq8"].astype(np.int64)
-    sdq = ref["sdq"].astype(np.float64)
-    gg = st["g8"][0, :, :nb].cpu().numpy().astype(np.int64)
-    sgg = st["sg"][0, :, :nb].cpu().numpy().astype(np.float64)
+    gdt = st["g8"].dtype
+    gg = st["g8"][0, :, :nb].float().cpu().numpy().astype(np.float64)      # exact decode of every store
     lzg = st["lz"][0, :, :nb].cpu().numpy().astype(np.float64)
-    gr, sgr, lzr = ref["g8"].astype(np.int64), ref["sg"].astype(np.float64), ref["lz"].astype(np.float64)
-    drift = np.zeros(dq8.shape[0])
+    lzr = ref["lz"].astype(np.float64)
+    if gdt == torch.int8:           # int8 codes, dq8 with row scales sdq, g row scales sg
+        dq = ref["dq8"].astype(np.float64) * ref["sdq"].astype(np.float64)[:, None]
+        gr = ref["g8"].astype(np.float64)
+    elif gdt == torch.float8_e4m3fn:   # e4m3 codes with row scales sg, dq in fp16
+        dq = ref["dq16"].view(np.float16).astype(np.float64)
+        gr = torch.from_numpy(np.ascontiguousarray(ref["g8"])).view(torch.float8_e4m3fn).float().numpy()
+    else:                           # bf16 g and dq, no scales
+        dq = bf16.to_f32(ref["dq16"]).astype(np.float64)
+        gr = bf16.to_f32(ref["g16"]).astype(np.float64)
+    if gdt == torch.bfloat16:
+        sgg = np.ones_like(lzg)
+        sgr = np.ones_like(lzr)
+    else:
+        sgg = st["sg"][0, :, :nb].cpu().numpy().astype(np.float64)
+        sgr = ref["sg"].astype(np.float64)
+    drift = np.zeros(dq.shape[0])
     span = tile * group
     for gi in range(gg.shape[0]):
-        rs = slice(gi * span, min(dq8.shape[0], (gi + 1) * span))
+        rs = slice(gi * span, min(dq.shape[0], (gi + 1) * span))
         if rs.start >= rs.stop:
             break
-        fg = (dq8[rs] @ gg[gi].T) * sdq[rs, None] * sgg[gi][None] + lzg[gi][None]
-        fr = (dq8[rs] @ gr[gi].T) * sdq[rs, None] * sgr[gi][None] + lzr[gi][None]
+        fg = (dq[rs] @ gg[gi].T) * sgg[gi][None] + lzg[gi][None]
+        fr = (dq[rs] @ gr[gi].T) * sgr[gi][None] + lzr[gi][None]
         far = ref["excl"][gi] == 0                     # near leaves are attended exactly
         drift[rs] = np.abs(fg - fr)[:, far].max(axis=1) if far.any() else 0.0
     return drift
 
 
-def check_logz(logz_gpu, ref, st, bar: float) -> float:
+def check_logz(logz_gpu, ref, st, bar: float, rows=None) -> float:
     """|logZ_gpu - logZ_oracle| <= bar + the row's far-score drift (far_score_drift), rows in query
-    order (through the k-means permutation when there is one); returns the largest excess over
-    ``bar`` that the drift allowed."""
+    order (through the k-means permutation when there is one), on the rows of ``rows`` (a bool
+    mask in query order; all rows by default); returns the largest excess over ``bar`` that the
+    drift allowed."""
     drift = far_score_drift(st, ref)
     n = ref["logz"].shape[0]
     allow = np.empty(n)
@@ -115,6 +131,7 @@ def check_logz(logz_gpu, ref, st, bar: float) -> float:
     else:
         allow[:] = drift[:n]
     err = np.abs(np.asarray(logz_gpu, np.float64) - ref["logz"])
-    bad = np.where(err > bar + allow)[0]
+    sel = np.ones(n, bool) if rows is None else np.asarray(rows, bool)
+    bad = np.where((err > bar + allow) & sel)[0]
     assert bad.size == 0, f"row {bad[0]}: |dlogZ| {err[bad[0]]:.3e} > {bar} + drift {allow[bad[0]]:.3e}"
-    return float(max(0.0, (err - bar).max()))
+    return float(max(0.0, (err[sel] - bar).max())) if sel.any() else 0.0
