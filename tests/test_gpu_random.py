@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 
 OUT_REL_L2 = 1e-2
 LOGZ_ABS = 1e-3
-CASES = 48
+CASES = 96
 
 
 def _case(seed: int) -> dict:
