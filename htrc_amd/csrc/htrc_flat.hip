@@ -2814,99 +2814,134 @@ __global__ __launch_bounds__(128) void km_init_kernel(const void* __restrict__ q
     cen[((int64_t)h * C + j) * D + i] = qval<IN_BF16>(q, ((int64_t)h * nq + row) * D + i);
 }
 
-// Nearest centre of 64 rows (of the sample when sm > 0, else of the queries): four lanes per
-// row, lane `part` taking centres part, part + 4, ..; rows and centres staged in LDS.
+// Nearest centre of 256 rows (of the sample when sm > 0, else of the queries): one row per
+// lane, its 128 values in registers.  The centres are wave-uniform: read straight from memory
+// (scalar loads into operands, no per-lane copies), two centres per step as independent sums,
+// compared in increasing order so that ties keep the lower centre.
 template <bool IN_BF16>
 __global__ __launch_bounds__(256) void km_assign_kernel(const void* __restrict__ q, int64_t nq, int64_t nrows, int sm,
                                                         int C, const float* __restrict__ cen,
                                                         int32_t* __restrict__ assign) {
-    __shared__ __align__(16) float xs[64][D + 4];
-    __shared__ __align__(16) float cs[KM_MAX_C][D + 4];
     const int h = blockIdx.y, tid = threadIdx.x;
-    const int64_t r0 = (int64_t)blockIdx.x * 64;
-    for (int e = tid; e < C * D; e += 256) cs[e / D][e % D] = cen[(int64_t)h * C * D + e];
-    for (int e = tid; e < 64 * (D / 4); e += 256) {
-        const int r = e / (D / 4), c4 = (e % (D / 4)) * 4;
-        const int64_t ri = r0 + r < nrows ? r0 + r : nrows - 1;
-        const int64_t row = sm > 0 ? linspace_round(nq - 1, sm, ri) : ri;
-        const int64_t base = ((int64_t)h * nq + row) * D + c4;
-        f32x4 x;
-        if (IN_BF16) {
-            const u32x2 u = *(const u32x2*)((const uint16_t*)q + base);
-            x = f32x4{bf2f(u.x & 0xffffu), bf2f(u.x >> 16), bf2f(u.y & 0xffffu), bf2f(u.y >> 16)};
-        } else {
-            x = *(const f32x4*)((const float*)q + base);
-        }
-        *(f32x4*)&xs[r][c4] = x;
-    }
-    __syncthreads();
-    const int r = tid >> 2, part = tid & 3;
-    float best = INFINITY;
-    int bj = C;
-    for (int j = part; j < C; j += 4) {
-        float acc = 0.0f;
-        for (int d0 = 0; d0 < D; d0 += 4) {
-            const f32x4 x = *(const f32x4*)&xs[r][d0], c = *(const f32x4*)&cs[j][d0];
+    const float* __restrict__ ch = cen + (int64_t)h * C * D;
+    const int64_t ri = (int64_t)blockIdx.x * 256 + tid;
+    const int64_t rc = ri < nrows ? ri : nrows - 1;
+    const int64_t row = sm > 0 ? linspace_round(nq - 1, sm, rc) : rc;
+    const int64_t base = ((int64_t)h * nq + row) * D;
+    float x[D];
+    if constexpr (IN_BF16) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float df = __fsub_rn(x[u], c[u]);
-                acc = __fadd_rn(acc, __fmul_rn(df, df));
+        for (int c8 = 0; c8 < D / 8; ++c8) {
+            const u32x4 u = *(const u32x4*)((const uint16_t*)q + base + 8 * c8);
+            const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[8 * c8 + 2 * e] = __uint_as_float(w4[e] << 16);
+                x[8 * c8 + 2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u);
             }
         }
-        if (acc < best) {            // centres visited in increasing order: ties keep the lower
+    } else {
+#pragma unroll
+        for (int c4 = 0; c4 < D / 4; ++c4) {
+            const f32x4 v = *(const f32x4*)((const float*)q + base + 4 * c4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[4 * c4 + e] = v[e];
+        }
+    }
+    float best = INFINITY;
+    int bj = C;
+    auto consider = [&](float acc, int j) {
+        if (acc < best) {
             best = acc;
             bj = j;
         }
-    }
+    };
+    int j = 0;
+    for (; j + 1 < C; j += 2) {
+        const float* c0 = ch + (int64_t)j * D;
+        const float* c1 = c0 + D;
+        float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-    for (int o = 1; o < 4; o <<= 1) {   // the row's four lanes: lowest distance, then lowest centre
-        const float ob = __shfl_xor(best, o);
-        const int oj = __shfl_xor(bj, o);
-        if (ob < best || (ob == best && oj < bj)) {
-            best = ob;
-            bj = oj;
+        for (int d = 0; d < D; ++d) {
+            const float e0 = __fsub_rn(x[d], c0[d]), e1 = __fsub_rn(x[d], c1[d]);
+            a0 = __fadd_rn(a0, __fmul_rn(e0, e0));
+            a1 = __fadd_rn(a1, __fmul_rn(e1, e1));
         }
+        consider(a0, j);
+        consider(a1, j + 1);
     }
-    if (bj < 0 || bj >= C) bj = 0;      // no finite distance (non-finite rows): centre 0
-    if (part == 0 && r0 + r < nrows) assign[(int64_t)h * nq + r0 + r] = bj;
+    if (j < C) {                        // an odd last centre
+        const float* c0 = ch + (int64_t)j * D;
+        float a0 = 0.0f;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const float e0 = __fsub_rn(x[d], c0[d]);
+            a0 = __fadd_rn(a0, __fmul_rn(e0, e0));
+        }
+        consider(a0, j);
+    }
+    if (bj >= C) bj = 0;                // no finite distance (non-finite rows): centre 0
+    if (ri < nrows) assign[(int64_t)h * nq + ri] = bj;
 }
 
-// New centre j: the samples assigned to j (listed in sample order by a ballot compaction) summed
-// in that order and divided by their count.
+// New centre j: the samples assigned to j (listed in sample order by a ballot compaction, as
+// their rows of q) summed in that order and divided by their count.  The assignments are read
+// four 128-sample chunks ahead and compacted four chunks per barrier pair, and the rows are
+// gathered sixteen at a time, so that neither walk waits on one load per step.
 template <bool IN_BF16>
 __global__ __launch_bounds__(128) void km_update_kernel(const void* __restrict__ q, int64_t nq, int m, int C,
                                                         const int32_t* __restrict__ assign,
                                                         float* __restrict__ cen) {
+    constexpr int PF = 4;
     __shared__ int32_t list[KM_MAX_SAMPLE];
-    __shared__ int wcnt[2];
+    __shared__ int wcnt[2 * PF];                  // [wave][chunk] hit counts
     const int j = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int32_t* a = assign + (int64_t)h * nq;
+    int pre[PF];
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+        const int i = 128 * p + tid;
+        pre[p] = i < m ? a[i] : -1;
+    }
     int cnt = 0;
-    for (int i0 = 0; i0 < m; i0 += 128) {
-        const int i = i0 + tid;
-        const bool hit = i < m && assign[(int64_t)h * nq + i] == j;
-        const uint64_t bal = __ballot(hit);
-        if (lane == 0) wcnt[w] = __popcll(bal);
+    for (int i0 = 0; i0 < m; i0 += 128 * PF) {
+        int cur[PF];
+        uint64_t bal[PF];
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            cur[p] = pre[p];
+            const int i = i0 + 128 * (PF + p) + tid;
+            pre[p] = i < m ? a[i] : -1;
+            bal[p] = __ballot(cur[p] == j);       // -1 past the sample
+            if (lane == 0) wcnt[PF * w + p] = __popcll(bal[p]);
+        }
         __syncthreads();
-        if (hit) list[cnt + (w ? wcnt[0] : 0) + __popcll(bal & ((1ull << lane) - 1ull))] = i;
-        cnt += wcnt[0] + wcnt[1];
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {            // chunk p: wave 0's hits, then wave 1's
+            if (cur[p] == j)
+                list[cnt + (w ? wcnt[p] : 0) + __popcll(bal[p] & ((1ull << lane) - 1ull))] =
+                    (int32_t)linspace_round(nq - 1, m, i0 + 128 * p + tid);
+            cnt += wcnt[p] + wcnt[PF + p];
+        }
         __syncthreads();
     }
     float acc = 0.0f;
-    for (int k0 = 0; k0 < cnt; k0 += 8) {
-        float x[8];
+    constexpr int B = 16;
+    for (int k0 = 0; k0 < cnt; k0 += B) {
+        float x[B];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            x[u] = k0 + u < cnt ? qval<IN_BF16>(q, ((int64_t)h * nq + linspace_round(nq - 1, m, list[k0 + u])) * D + tid)
-                                : 0.0f;
+        for (int u = 0; u < B; ++u)
+            x[u] = k0 + u < cnt ? qval<IN_BF16>(q, ((int64_t)h * nq + list[k0 + u]) * D + tid) : 0.0f;
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < B; ++u)
             if (k0 + u < cnt) acc = __fadd_rn(acc, x[u]);
     }
     if (cnt > 0) cen[((int64_t)h * C + j) * D + tid] = __fdiv_rn(acc, (float)cnt);
 }
 
 // perm = the rows ordered by centre, the rows of one centre in row order (stable counting sort
-// of one head per workgroup: histogram, prefix, then 1024-row chunks placed with ballot ranks).
+// of one head per workgroup: histogram, prefix, then 1024-row chunks placed with ballot ranks,
+// one ballot per distinct centre of a wave, the next chunk's centres read ahead).
 __global__ __launch_bounds__(1024) void km_sort_kernel(const int32_t* __restrict__ assign, int64_t nq, int C,
                                                        int32_t* __restrict__ perm) {
     __shared__ uint32_t cnt[KM_MAX_C], base[KM_MAX_C];
@@ -2927,14 +2962,22 @@ __global__ __launch_bounds__(1024) void km_sort_kernel(const int32_t* __restrict
         }
     }
     __syncthreads();
+    int cn = tid < nq ? centre(tid) : -1;               // the next chunk's centres, read a chunk ahead
     for (int64_t p0 = 0; p0 < nq; p0 += 1024) {
         const int64_t p = p0 + tid;
-        const int c = p < nq ? centre(p) : -1;
+        const int c = cn;
+        cn = p + 1024 < nq ? centre(p + 1024) : -1;
+        // this wave's count of every centre, and each lane's rank among the lanes of its centre:
+        // one ballot per distinct centre present (rows that cluster bring few)
+        if (lane < C) wc[w][lane] = 0u;
         uint32_t rank = 0u;
-        for (int cc = 0; cc < C; ++cc) {
+        uint64_t todo = __ballot(c >= 0);
+        while (todo) {
+            const int cc = __builtin_amdgcn_readlane(c, __builtin_ctzll(todo));
             const uint64_t bal = __ballot(c == cc);
             if (lane == 0) wc[w][cc] = (uint32_t)__popcll(bal);
             if (c == cc) rank = (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
+            todo &= ~bal;
         }
         __syncthreads();
         if (c >= 0) {
@@ -3868,7 +3911,7 @@ int htrc_kmeans_order(const void* q, int q_is_bf16, int64_t heads, int64_t nq, i
     REQUIRE(m <= KM_MAX_SAMPLE, "htrc_kmeans_order: at most 16384 sample rows");
     hipStream_t s = (hipStream_t)stream;
     const dim3 gc((unsigned)clusters, (unsigned)heads);
-    const dim3 gs((unsigned)((m + 63) / 64), (unsigned)heads), ga((unsigned)((nq + 63) / 64), (unsigned)heads);
+    const dim3 gs((unsigned)((m + 255) / 256), (unsigned)heads), ga((unsigned)((nq + 255) / 256), (unsigned)heads);
 #define KM_LAUNCH(BF)                                                                                              \
     hipLaunchKernelGGL(km_init_kernel<BF>, gc, dim3(D), 0, s, q, nq, (int)m, clusters, centres);                 \
     for (int it = 0; it < iters; ++it) {                                                                           \
