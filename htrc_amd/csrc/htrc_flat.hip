@@ -2887,7 +2887,7 @@ __global__ __launch_bounds__(256) void km_assign_kernel(const void* __restrict__
 // New centre j: the samples assigned to j (listed in sample order by a ballot compaction, as
 // their rows of q) summed in that order and divided by their count.  The assignments are read
 // four 128-sample chunks ahead and compacted four chunks per barrier pair, and the rows are
-// gathered sixteen at a time, so that neither walk waits on one load per step.
+// gathered 32 at a time, so that neither walk waits on one load per step.
 template <bool IN_BF16>
 __global__ __launch_bounds__(128) void km_update_kernel(const void* __restrict__ q, int64_t nq, int m, int C,
                                                         const int32_t* __restrict__ assign,
@@ -2930,7 +2930,7 @@ __global__ __launch_bounds__(128) void km_update_kernel(const void* __restrict__
     // aligned dword holding the value (shared with the neighbouring lane), its half taken.
     const int64_t hb = (int64_t)h * nq * D + tid;
     float acc = 0.0f;
-    constexpr int B = 16;
+    constexpr int B = 32;
     for (int k0 = 0; k0 < cnt; k0 += B) {
         uint32_t raw[B];
 #pragma unroll
