@@ -2948,34 +2948,70 @@ __global__ __launch_bounds__(128) void km_update_kernel(const void* __restrict__
     if (cnt > 0) cen[((int64_t)h * C + j) * D + tid] = __fdiv_rn(acc, (float)cnt);
 }
 
-// perm = the rows ordered by centre, the rows of one centre in row order (stable counting sort
-// of one head per workgroup: histogram, prefix, then 1024-row chunks placed with ballot ranks,
-// one ballot per distinct centre of a wave, the next chunk's centres read ahead).
-__global__ __launch_bounds__(1024) void km_sort_kernel(const int32_t* __restrict__ assign, int64_t nq, int C,
-                                                       int32_t* __restrict__ perm) {
-    __shared__ uint32_t cnt[KM_MAX_C], base[KM_MAX_C];
-    __shared__ uint32_t wc[16][KM_MAX_C];
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+// perm = the rows ordered by centre, the rows of one centre in row order: a stable counting sort
+// over at most KM_SORT_RANGES row ranges of whole 1024-row chunks per head, one workgroup per
+// range.  km_count_kernel writes every range's count of each centre; km_place_kernel starts
+// each centre at the rows of the centres before it plus that centre's rows in earlier ranges,
+// then places its range chunk by chunk with ballot ranks (one ballot per distinct centre of a
+// wave, the next chunk's centres read ahead).
+constexpr int KM_SORT_RANGES = 128;
+
+// rows per range: whole 1024-row chunks, at most KM_SORT_RANGES ranges
+inline int64_t km_sort_span(int64_t nq) {
+    const int64_t chunks = (nq + 1023) / 1024;
+    return 1024 * ((chunks + KM_SORT_RANGES - 1) / KM_SORT_RANGES);
+}
+
+__device__ __forceinline__ int km_centre(const int32_t* a, int64_t p, int C) {
+    const int c = a[p];
+    return c >= 0 && c < C ? c : 0;
+}
+
+// counts[h][range][c]: the rows of range `range` of head h assigned to centre c
+__global__ __launch_bounds__(1024) void km_count_kernel(const int32_t* __restrict__ assign, int64_t nq, int C,
+                                                        int64_t span, uint32_t* __restrict__ counts) {
+    __shared__ uint32_t cnt[KM_MAX_C];
+    const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const int32_t* a = assign + (int64_t)h * nq;
-    int32_t* out = perm + (int64_t)h * nq;
-    auto centre = [&](int64_t p) { const int c = a[p]; return c >= 0 && c < C ? c : 0; };
     if (tid < C) cnt[tid] = 0u;
     __syncthreads();
-    for (int64_t p = tid; p < nq; p += 1024) atomicAdd(&cnt[centre(p)], 1u);
+    const int64_t p1 = min(nq, (int64_t)(r + 1) * span);
+    for (int64_t p = (int64_t)r * span + tid; p < p1; p += 1024) atomicAdd(&cnt[km_centre(a, p, C)], 1u);
+    __syncthreads();
+    if (tid < C) counts[((int64_t)h * gridDim.x + r) * C + tid] = cnt[tid];
+}
+
+__global__ __launch_bounds__(1024) void km_place_kernel(const int32_t* __restrict__ assign, int64_t nq, int C,
+                                                        int64_t span, const uint32_t* __restrict__ counts,
+                                                        int32_t* __restrict__ perm) {
+    __shared__ uint32_t tot[KM_MAX_C], base[KM_MAX_C];
+    __shared__ uint32_t wc[16][KM_MAX_C];
+    const int r = blockIdx.x, nr = gridDim.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int32_t* a = assign + (int64_t)h * nq;
+    int32_t* out = perm + (int64_t)h * nq;
+    const uint32_t* ch = counts + (int64_t)h * nr * C;
+    if (tid < C) tot[tid] = base[tid] = 0u;
+    __syncthreads();
+    for (int i = tid; i < nr * C; i += 1024) {       // every centre's total, and its rows in earlier ranges
+        const uint32_t v = ch[i];
+        atomicAdd(&tot[i % C], v);
+        if (i / C < r) atomicAdd(&base[i % C], v);
+    }
     __syncthreads();
     if (tid == 0) {
         uint32_t acc = 0u;
         for (int c = 0; c < C; ++c) {
-            base[c] = acc;
-            acc += cnt[c];
+            base[c] += acc;
+            acc += tot[c];
         }
     }
     __syncthreads();
-    int cn = tid < nq ? centre(tid) : -1;               // the next chunk's centres, read a chunk ahead
-    for (int64_t p0 = 0; p0 < nq; p0 += 1024) {
+    const int64_t p0s = (int64_t)r * span, p1 = min(nq, p0s + span);
+    int cn = p0s + tid < p1 ? km_centre(a, p0s + tid, C) : -1;
+    for (int64_t p0 = p0s; p0 < p1; p0 += 1024) {
         const int64_t p = p0 + tid;
         const int c = cn;
-        cn = p + 1024 < nq ? centre(p + 1024) : -1;
+        cn = p + 1024 < p1 ? km_centre(a, p + 1024, C) : -1;
         // this wave's count of every centre, and each lane's rank among the lanes of its centre:
         // one ballot per distinct centre present (rows that cluster bring few)
         if (lane < C) wc[w][lane] = 0u;
@@ -3934,7 +3970,15 @@ int htrc_kmeans_order(const void* q, int q_is_bf16, int64_t heads, int64_t nq, i
         KM_LAUNCH(false)
     }
 #undef KM_LAUNCH
-    hipLaunchKernelGGL(km_sort_kernel, dim3((unsigned)heads), dim3(1024), 0, s, assign, nq, clusters, perm);
+    // the sort's per-range counts go to the centres workspace, spent once the last assignment
+    // has run: at most KM_SORT_RANGES * clusters <= clusters * D words per head
+    const int64_t span = km_sort_span(nq), ranges = (nq + span - 1) / span;
+    static_assert(KM_SORT_RANGES <= D, "per-range counts must fit the centres workspace");
+    uint32_t* counts = (uint32_t*)centres;
+    hipLaunchKernelGGL(km_count_kernel, dim3((unsigned)ranges, (unsigned)heads), dim3(1024), 0, s, assign, nq,
+                       clusters, span, counts);
+    hipLaunchKernelGGL(km_place_kernel, dim3((unsigned)ranges, (unsigned)heads), dim3(1024), 0, s, assign, nq,
+                       clusters, span, counts, perm);
     return launched("htrc_kmeans_order");
 }
 

@@ -231,8 +231,8 @@ int htrc_route16(const uint16_t* q16, const uint16_t* dq16, const void* g, const
 
 /* k-means query order: perm int32 [H, nq], the queries ordered by their nearest of `clusters`
  * centres (stable), the centres from `iters` Lloyd steps on `sample` evenly spaced queries.
- * Workspace: centres fp32 [H, clusters, 128], assign int32 [H, nq].  1 <= clusters <= 64,
- * min(sample, nq) <= 16384.
+ * Workspace: centres fp32 [H, clusters, 128], assign int32 [H, nq]; on return centres holds
+ * the sort's per-range counts, not the centres.  1 <= clusters <= 64, min(sample, nq) <= 16384.
  * Replaces kmeans_order (h3/htrc_flat.py:47-61). */
 int htrc_kmeans_order(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int clusters, int sample,
                       int iters, float* centres, int32_t* assign, int32_t* perm, void* stream);

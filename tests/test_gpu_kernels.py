@@ -554,11 +554,13 @@ def test_linspace_positions_equal_device_torch(device, n, m):
 
 
 @pytest.mark.parametrize("n,clusters,sample,iters", [(64512, 32, 4096, 8), (5000, 32, 4096, 8), (3001, 17, 700, 4),
-                                                     (64, 32, 4096, 8), (9000, 64, 9000, 2), (10, 3, 5, 0)])
+                                                     (64, 32, 4096, 8), (9000, 64, 9000, 2), (10, 3, 5, 0),
+                                                     (300001, 32, 4096, 3)])
 @pytest.mark.parametrize("qdtype", ["bf16", "fp32"])
 def test_kmeans_order_bitexact(device, n, clusters, sample, iters, qdtype):
     """k-means order (h3/htrc_flat.py:47-61): the GPU permutation is the oracle's, bit for bit
-    (same sample, distances, update order and stable sort), for every head."""
+    (same sample, distances, update order and stable sort), for every head.  300001 rows place
+    three 1024-row chunks per sort range (98 ranges, the last one ragged)."""
     q, _, _ = _data(n, nk=64, seed=n + clusters, heads=2)
     if qdtype == "fp32":
         q = q.float() + 1e-3 * torch.randn(q.shape, generator=torch.Generator().manual_seed(5))
