@@ -2816,8 +2816,8 @@ __global__ __launch_bounds__(128) void km_init_kernel(const void* __restrict__ q
 
 // Nearest centre of 256 rows (of the sample when sm > 0, else of the queries): one row per
 // lane, its 128 values in registers.  The centres are wave-uniform: read straight from memory
-// (scalar loads into operands, no per-lane copies), two centres per step as independent sums,
-// compared in increasing order so that ties keep the lower centre.
+// (scalar loads into operands, no per-lane copies), four centres per step as independent sums
+// (then pairs, then one), compared in increasing order so that ties keep the lower centre.
 template <bool IN_BF16>
 __global__ __launch_bounds__(256) void km_assign_kernel(const void* __restrict__ q, int64_t nq, int64_t nrows, int sm,
                                                         int C, const float* __restrict__ cen,
@@ -2857,6 +2857,22 @@ __global__ __launch_bounds__(256) void km_assign_kernel(const void* __restrict__
         }
     };
     int j = 0;
+    for (; j + 3 < C; j += 4) {
+        const float* c0 = ch + (int64_t)j * D;
+        float a[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a[u] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float e = __fsub_rn(x[d], c0[u * D + d]);
+                a[u] = __fadd_rn(a[u], __fmul_rn(e, e));
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) consider(a[u], j + u);
+    }
     for (; j + 1 < C; j += 2) {
         const float* c0 = ch + (int64_t)j * D;
         const float* c1 = c0 + D;
