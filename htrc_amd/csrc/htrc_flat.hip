@@ -2942,8 +2942,7 @@ __global__ __launch_bounds__(128) void km_update_kernel(const void* __restrict__
         __syncthreads();
     }
     // dim tid of B rows per step: the raw words first (every load unconditional, indices past
-    // the list repeating its first row), then the values summed in list order.  bf16: the
-    // aligned dword holding the value (shared with the neighbouring lane), its half taken.
+    // the list repeating its first row), then the values summed in list order.
     const int64_t hb = (int64_t)h * nq * D + tid;
     float acc = 0.0f;
     constexpr int B = 32;
@@ -2952,12 +2951,11 @@ __global__ __launch_bounds__(128) void km_update_kernel(const void* __restrict__
 #pragma unroll
         for (int u = 0; u < B; ++u) {
             const int64_t e = hb + (int64_t)list[k0 + u < cnt ? k0 + u : k0] * D;
-            raw[u] = IN_BF16 ? ((const uint32_t*)q)[e >> 1] : ((const uint32_t*)q)[e];
+            raw[u] = IN_BF16 ? (uint32_t)((const uint16_t*)q)[e] : ((const uint32_t*)q)[e];
         }
 #pragma unroll
         for (int u = 0; u < B; ++u) {
-            const float x = IN_BF16 ? __uint_as_float((tid & 1) ? (raw[u] & 0xffff0000u) : (raw[u] << 16))
-                                    : __uint_as_float(raw[u]);
+            const float x = IN_BF16 ? __uint_as_float(raw[u] << 16) : __uint_as_float(raw[u]);
             if (k0 + u < cnt) acc = __fadd_rn(acc, x);
         }
     }
