@@ -153,14 +153,14 @@ class _Collect:
 _WINDOW_STREAMS: dict = {}
 
 
-def _window_streams(device) -> tuple:
-    """Two side streams of the device (default priority), created once, that alternate the
-    tile windows of a call."""
+def _window_streams(device, n: int) -> tuple:
+    """``n`` side streams of the device (default priority), created once, over which the tile
+    windows of a call are dealt in turn."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    pair = _WINDOW_STREAMS.get(idx)
-    if pair is None:
-        pair = _WINDOW_STREAMS[idx] = (torch.cuda.Stream(device=idx), torch.cuda.Stream(device=idx))
-    return pair
+    have = _WINDOW_STREAMS.setdefault(idx, [])
+    while len(have) < n:
+        have.append(torch.cuda.Stream(device=idx))
+    return tuple(have[:n])
 
 
 def _windows(ng: int, tile_chunk, group: int):
@@ -187,8 +187,8 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     ``order='kmeans'`` cuts the tiles from the queries regrouped by ``kmeans_order``; the
     output rows come back in query order (:148-149, 159-165).
     ``tile_chunk`` tiles of every head are processed per window (h3/htrc_flat.py:236-273): the
-    per-(tile, leaf) state is held for at most two windows at a time (several windows alternate
-    over two streams; ``kern['window_streams'] = 1`` keeps one), and the result does not
+    per-(tile, leaf) state is held for at most S windows at a time (several windows are dealt
+    over S = ``kern['window_streams']`` streams, default 2; S = 1 keeps one), and the result does not
     depend on it.  ``precision`` is accepted for compatibility: accumulation is IEEE fp32.  ``state``, if
     a dict, receives the packed operands and the whole layer's leaf state and routing (for
     checks)."""
@@ -281,20 +281,22 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
 
     wins = _windows(ng, tile_chunk, group)
     keep = _Collect(state, h, ng, len(wins))
-    # Several windows: the even and odd ones on two side streams, each with its own window
-    # buffers, so that a window's statistics run beside the previous window's select and attend
-    # (filling the tails of their launches; two windows' state in flight).  One window, stage
-    # timing (prof), state checks or kern["window_streams"] = 1: the caller's stream, in order.
-    pipe = len(wins) > 1 and prof is None and state is None and int(kern.get("window_streams", 2)) > 1
+    # Several windows: dealt in turn over S = kern["window_streams"] side streams (default 2),
+    # each with its own window buffers, so that a window's statistics run beside the previous
+    # window's select and attend (filling the tails of their launches; S windows' state in
+    # flight).  One window, stage timing (prof), state checks or S = 1: the caller's stream, in
+    # order.
+    nst = min(int(kern.get("window_streams", 2)), len(wins))
+    pipe = nst > 1 and prof is None and state is None
     if pipe:
         cur = torch.cuda.current_stream(qh.device)
-        side = _window_streams(qh.device)
+        side = _window_streams(qh.device, nst)
         for s in side:
             s.wait_stream(cur)
-        wsw = (None, None) if ws is None else (ws.setdefault("window_a", {}), ws.setdefault("window_b", {}))
+        wsw = (None,) * nst if ws is None else tuple(ws.setdefault(f"window_{i}", {}) for i in range(nst))
     for wi, (g0, gn) in enumerate(wins):
-        with torch.cuda.stream(side[wi & 1]) if pipe else contextlib.nullcontext():
-            _window(wsw[wi & 1] if pipe else ws, g0, gn)
+        with torch.cuda.stream(side[wi % nst]) if pipe else contextlib.nullcontext():
+            _window(wsw[wi % nst] if pipe else ws, g0, gn)
     if pipe:
         for s in side:
             cur.wait_stream(s)

@@ -62,8 +62,8 @@ def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, hea
                     store: str = "int8", fused: bool = True, bf16_inputs: bool = True, window_streams: int = 2) -> int:
     """Device bytes of one operator call's workspace: the whole layer's packed operands and
     outputs, and the per-(centre, leaf) state, routing and partials of the tile windows of
-    ``tile_chunk`` tiles (all tiles when None) in flight: one, or two when there are several
-    windows and the operator alternates them over two streams (kern["window_streams"] = 2, its
+    ``tile_chunk`` tiles (all tiles when None) in flight: one, or min(S, windows) when there are
+    several windows and the operator deals them over S = kern["window_streams"] streams (2 by
     default)."""
     nt = _ceil(queries, tile)
     ng = _ceil(nt, max(1, int(group)))
@@ -95,7 +95,7 @@ def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, hea
     if order == "kmeans":
         layer += 8 * queries + 4 * 32 * dim                             # perm, assignments, centres
     if gw < ng and int(window_streams) > 1:
-        window *= 2                                                     # two windows in flight
+        window *= min(int(window_streams), _ceil(ng, gw))               # windows in flight
     return int(heads) * (layer + window)
 
 

@@ -206,6 +206,15 @@ def test_runner_modes_and_memory_model():
     # windows of 128 in flight at cfg3
     m128 = htrc_flat_runner.predicted_peak_mib(64512, 64, 128, leaf=64, queries=64512, heads=24, exact_leaves=32)
     assert mib - m128 == pytest.approx(24 * (1008 - 2 * 128) * (1024 * 392 + 4 * 32) / 2 ** 20, rel=1e-6)
+    # S window streams keep min(S, windows) windows in flight: three of 128 tiles, and no more
+    # than the two windows of 512 tiles there are
+    per = 24 * 128 * (1024 * 392 + 4 * 32) / 2 ** 20
+    m3 = htrc_flat_runner.predicted_peak_mib(64512, 64, 128, leaf=64, queries=64512, heads=24, exact_leaves=32,
+                                             window_streams=3)
+    assert m3 - m128 == pytest.approx(per, rel=1e-6)
+    kw512 = dict(leaf=64, queries=64512, heads=24, exact_leaves=32)
+    assert htrc_flat_runner.predicted_peak_mib(64512, 64, 512, window_streams=3, **kw512) == \
+        htrc_flat_runner.predicted_peak_mib(64512, 64, 512, window_streams=2, **kw512)
     with pytest.raises(ValueError, match="mode"):
         htrc_flat_runner.FlatRunner(64, 64, mode="nope")
     assert htrc_flat_runner.SUPPORTED_MODES == ("fast", "balanced", "accurate", "max")

@@ -79,6 +79,11 @@ def test_windows_bit_identical(device, fused, group, tile, order, store):
         assert torch.equal(out, one) and torch.equal(lz, lz1), f"tile_chunk {chunk}"
         assert torch.equal(st["idx"], st1["idx"])
         assert torch.equal(st["lz"], st1["lz"]) and torch.equal(st["g8"], st1["g8"])
+    for nst in (1, 2, 3):            # no state: the windows dealt over nst streams
+        out, lz = htrc_flat.flat_attention(q, k, v, tile_chunk=16, return_logz=True,
+                                           **{**kw, "kern": {**kw["kern"], "window_streams": nst}})
+        torch.cuda.synchronize()
+        assert torch.equal(out, one) and torch.equal(lz, lz1), f"{nst} window streams"
 
 
 @pytest.mark.parametrize("fused,group,store", [(True, 1, "int8"), (False, 1, "int8"), (True, 2, "int8"),
