@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import contextlib
 import math
+import threading
 import time
 
 import torch
@@ -115,8 +116,8 @@ def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot
         raise ValueError("leaf must be 16, 32, 64 or 128")
     if q.dim() not in (2, 3) or k.dim() != q.dim() or v.shape != k.shape:
         raise ValueError("q [N,D] with k/v [M,D], or q [H,N,D] with k/v [H,M,D]")
-    if q.shape[-1] != hip.D or k.shape[-1] != hip.D:
-        raise ValueError("head dim must be 128")
+    if not 1 <= q.shape[-1] <= hip.D or k.shape[-1] != q.shape[-1]:
+        raise ValueError("head dim must be at most 128 and the same for q and k/v")
     if q.dim() == 3 and q.shape[0] != k.shape[0]:
         raise ValueError("q and k/v must have the same number of heads")
     if int(k.shape[-2]) % int(leaf):
@@ -150,17 +151,33 @@ class _Collect:
             self.state.update(extra)
 
 
-_WINDOW_STREAMS: dict = {}
+_WINDOW_STREAMS = threading.local()
 
 
 def _window_streams(device, n: int) -> tuple:
-    """``n`` side streams of the device (default priority), created once, over which the tile
-    windows of a call are dealt in turn."""
+    """``n`` side streams of the device (default priority), created once per (device, thread),
+    over which the tile windows of a call are dealt in turn.  Each thread owns its streams: a
+    graph capture in one thread (``FlatRunner`` records with capture_error_mode="thread_local")
+    records its windows on streams no other thread's eager call launches on or waits for."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    have = _WINDOW_STREAMS.setdefault(idx, [])
+    per = getattr(_WINDOW_STREAMS, "by_device", None)
+    if per is None:
+        per = _WINDOW_STREAMS.by_device = {}
+    have = per.setdefault(idx, [])
     while len(have) < n:
         have.append(torch.cuda.Stream(device=idx))
     return tuple(have[:n])
+
+
+def _pad_dims(x, ws, name: str, dtype):
+    """x [H, n, d] (d < 128) -> a workspace copy [H, n, 128] of ``dtype`` whose dims past d are
+    zero (the pad dims are cleared by a fill kernel on every call, so a reused buffer and a
+    graph replay see zeros there)."""
+    buf = hip._buf(ws, name, (*x.shape[:-1], hip.D), dtype, x.device)
+    d = int(x.shape[-1])
+    buf[..., d:].zero_()
+    buf[..., :d].copy_(x)
+    return buf
 
 
 def _windows(ng: int, tile_chunk, group: int):
@@ -221,6 +238,15 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         qh = fake_quant(qh, quant["q"], qg)
     if qh.dtype not in (torch.float32, torch.bfloat16):
         qh = qh.float()
+    d_in = d
+    if d < hip.D:
+        # head dims below 128 (the reference takes any power-of-two D, h3/htrc_flat_triton.py:43, 90):
+        # zero dims leave every row maximum, int32 dot, state code and softmax as they are, so the
+        # kernels run at 128 on copies padded with zeros and the output keeps the first d dims
+        qh = _pad_dims(qh, ws, "q_pad", qh.dtype)
+        kh = _pad_dims(kh, ws, "k_pad", torch.bfloat16)
+        vh = _pad_dims(vh, ws, "v_pad", torch.bfloat16)
+        d = hip.D
     perm = hip.kmeans_order(qh, ws=ws) if order == "kmeans" else None   # query rows regrouped by k-means
     qsrc = qh.contiguous()                               # the query rows select="bound" measures
     if store in ("fp8", "bf16"):
@@ -242,6 +268,9 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     ng = int(mu.shape[1])                               # centres: tiles, or tile groups
     out = hip._buf(ws, "out", (h, nq, d), torch.float32, qh.device)
     logz = hip._buf(ws, "logz", (h, nq), torch.float32, qh.device)
+    # each row's largest far-field score (the fused route's softmax reference): one layer-wide
+    # buffer, every window writing and reading only its own tiles' rows
+    rowmax = hip._buf(ws, "rowmax", (h, -(-nq // tile) * tile), torch.float32, qh.device) if fused else None
 
     def _window(w, g0, gn):
         """Statistics, select / top-k and attention of the tile groups [g0, g0 + gn), the window's
@@ -259,7 +288,7 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
             idx = hip._rows(w, "idx", h, gn, (kx,), torch.int32, qh.device) if kx > 0 else None
             fn = hip.route if sdt == torch.int8 else hip.route16
             fn(packed, lstate, nq=nq, leaf=leaf, kx=kx, scale=scale, sink=sink, stride=stride, ws=w, out=out,
-               logz=logz, idx=idx, group=group, perm=perm, tile=tile, g0=g0)
+               logz=logz, idx=idx, group=group, perm=perm, tile=tile, g0=g0, rowmax=rowmax)
             tick("tile")
         else:
             if kx > 0 and select == "bound":            # h3/htrc_flat.py:255-257
@@ -307,8 +336,12 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     if tail is not None and int(tail[0].shape[-2]) > 0:
         # keys past the last full leaf, exact for every query (h3/htrc_flat_triton.py:187-207, 381-388)
         tk, tv = (x.unsqueeze(0) if squeeze else x for x in tail)
+        if d_in < d:
+            tk, tv = (_pad_dims(x.to(qh.device), ws, n, torch.float32) for x, n in ((tk, "tk_pad"), (tv, "tv_pad")))
         hip.tail_merge(qh, tk.to(qh.device), tv.to(qh.device), scale=scale, out=out, logz=logz)
         tick("tail")
+    if d_in < d:
+        out = out[..., :d_in]
     res = out[0] if squeeze else out
     lzr = logz[0] if squeeze else logz
     tick("finish")

@@ -346,11 +346,24 @@ def _keys_ws(ws, h, gn, nb, dev):
     return _rows(ws, "route_keys", h, gn, (nb_pad(nb),), torch.int32, dev)
 
 
+def _rowmax(ws, rowmax, h: int, rows: int, dev):
+    """Each row's largest far-field score [H, rows] fp32: the caller's buffer, else a workspace one."""
+    if rowmax is None:
+        return _buf(ws, "rowmax", (h, rows), torch.float32, dev)
+    _need(rowmax, torch.float32, "rowmax")
+    if tuple(rowmax.shape) != (h, rows):
+        raise ValueError(f"rowmax must be fp32 [{h}, {rows}]")
+    return rowmax
+
+
 def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: float, sink: int = 0, stride: int = 1,
-          ws=None, out=None, logz=None, idx=None, group: int = 1, perm=None, tile: int = TILE, g0: int = 0):
+          ws=None, out=None, logz=None, idx=None, group: int = 1, perm=None, tile: int = TILE, g0: int = 0,
+          rowmax=None):
     """Fused select -> top-k, then far + near -> normalised output (two launches) for the tiles of
     the gn = state["lz"].shape[1] groups from g0 -> (out [H,nq,D], logz [H,nq]); idx
-    [H,gn,min(kx,nb)] int32 receives the window's routing (a workspace buffer when not given)."""
+    [H,gn,min(kx,nb)] int32 receives the window's routing (a workspace buffer when not given).
+    rowmax [H, nt * tile] fp32 (a workspace buffer when not given): the window writes and reads
+    only its own tiles' rows, so the windows of a layer may share one."""
     q8, sq, dq8, sdq = packed["q8"], packed["sq"], packed["dq8"], packed["sdq"]
     k8, ks, v = packed["k8"], packed["ks"], packed["v"]
     g8, sg, lz, vb = state["g8"], state["sg"], state["lz"], state["vb"]
@@ -367,7 +380,7 @@ def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: floa
         logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
     if idx is None and kxe > 0:
         idx = _rows(ws, "idx", h, gn, (kxe,), torch.int32, dev)
-    rowmax = _buf(ws, "rowmax", (h, nt * tile), torch.float32, dev)
+    rowmax = _rowmax(ws, rowmax, h, nt * tile, dev)
     keys = _keys_ws(ws, h, gn, nb, dev)
     call("htrc_route", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(k8), ptr(ks),
          ptr(v), h, nq, nk, int(leaf), d, int(kx), int(sink), int(stride), tile, int(group), g0, gn, ptr(perm),
@@ -376,7 +389,7 @@ def route(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: floa
 
 
 def route_select(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, sink: int = 0, stride: int = 1,
-                 ws=None, idx=None, group: int = 1, tile: int = TILE, g0: int = 0):
+                 ws=None, idx=None, group: int = 1, tile: int = TILE, g0: int = 0, rowmax=None):
     """First launch of route: select -> top-k per tile group of the window -> (idx
     [H,gn,min(kx,nb)] int32 or None, rowmax [H,nt*tile] fp32, each row's largest far-field
     score)."""
@@ -391,7 +404,7 @@ def route_select(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, sink
     kxe = min(int(kx), nb)
     if idx is None and kxe > 0:
         idx = _rows(ws, "idx", h, gn, (kxe,), torch.int32, dev)
-    rowmax = _buf(ws, "rowmax", (h, nt * tile), torch.float32, dev)
+    rowmax = _rowmax(ws, rowmax, h, nt * tile, dev)
     keys = _keys_ws(ws, h, gn, nb, dev)
     call("htrc_route_select", ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), h, nq, nk, int(leaf), D, int(kx),
          int(sink), int(stride), tile, int(group), g0, gn, ptr(idx), ptr(rowmax), ptr(keys), stream_handle(dev))
@@ -432,7 +445,7 @@ def _r16(packed: dict, state: dict, nq: int, tile: int, group: int, g0: int, lea
 
 
 def route16_select(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, sink: int = 0, stride: int = 1,
-                   ws=None, idx=None, group: int = 1, tile: int = TILE, g0: int = 0):
+                   ws=None, idx=None, group: int = 1, tile: int = TILE, g0: int = 0, rowmax=None):
     """First launch of route16 (16-bit state stores): select -> top-k per tile group of the
     window -> (idx [H,gn,min(kx,nb)] int32 or None, rowmax [H,nt*tile] fp32, each row's largest
     far-field score, the attend launch's fixed softmax reference)."""
@@ -441,7 +454,7 @@ def route16_select(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, si
     dev = dq16.device
     if idx is None and kxe > 0:
         idx = _rows(ws, "idx", h, gn, (kxe,), torch.int32, dev)
-    rowmax = _buf(ws, "rowmax", (h, nt * tile), torch.float32, dev)
+    rowmax = _rowmax(ws, rowmax, h, nt * tile, dev)
     call("htrc_route16_select", ptr(dq16), ptr(g), ptr(sg), ptr(lz), h, nq, nk, int(leaf), d, int(kx), int(sink),
          int(stride), tile, int(group), g0, gn, int(fp8), ptr(idx), ptr(rowmax), stream_handle(dev))
     return (idx if kxe > 0 else None), rowmax
@@ -464,13 +477,14 @@ def route16_attend(packed: dict, state: dict, idx, rowmax, *, nq: int, leaf: int
 
 
 def route16(packed: dict, state: dict, *, nq: int, leaf: int, kx: int, scale: float, sink: int = 0, stride: int = 1,
-            ws=None, out=None, logz=None, idx=None, group: int = 1, perm=None, tile: int = TILE, g0: int = 0):
+            ws=None, out=None, logz=None, idx=None, group: int = 1, perm=None, tile: int = TILE, g0: int = 0,
+            rowmax=None):
     """Fused route of the 16-bit state stores (select -> top-k, then far + near in one softmax; two
     launches) for the tiles of the gn = state["lz"].shape[1] groups from g0: packed holds q16,
     dq16 (pack_q16) and the bf16 k, v; state g8 / vb (e4m3 with sg, sv; or bf16) and lz
     -> (out [H,nq,D], logz [H,nq]); idx [H,gn,min(kx,nb)] receives the window's routing."""
     idx, rowmax = route16_select(packed, state, nq=nq, leaf=leaf, kx=kx, sink=sink, stride=stride, ws=ws, idx=idx,
-                                 group=group, tile=tile, g0=g0)
+                                 group=group, tile=tile, g0=g0, rowmax=rowmax)
     return route16_attend(packed, state, idx, rowmax, nq=nq, leaf=leaf, kx=kx, scale=scale, ws=ws, out=out,
                           logz=logz, group=group, perm=perm, tile=tile, g0=g0)
 

@@ -65,6 +65,8 @@ def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, hea
     ``tile_chunk`` tiles (all tiles when None) in flight: one, or min(S, windows) when there are
     several windows and the operator deals them over S = kern["window_streams"] streams (2 by
     default)."""
+    pad = int(dim) < 128                 # head dims below 128 run at 128 on zero-padded copies
+    dim = 128 if pad else int(dim)
     nt = _ceil(queries, tile)
     ng = _ceil(nt, max(1, int(group)))
     gw = ng if tile_chunk is None else max(1, min(ng, int(tile_chunk) // max(1, int(group))))
@@ -73,19 +75,23 @@ def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, hea
     nb = int(keys) // int(leaf)
     nbp = _ceil(nb, 32) * 32
     kx = min(int(kx), nb)
-    layer = 4 * ng * dim + 4 * queries * (dim + 1) + 4 * rows          # mu, out + logz, rowmax
+    layer = 4 * ng * dim + 4 * queries * (dim + 1)                     # mu, out + logz
     if store == "int8":
         layer += 2 * rows * dim + 8 * rows + keys * dim + 4 * keys      # q8, dq8, sq, sdq, k8, ks
         per_state = 3 * dim + 8                                         # g8, vb bf16, sg, lz
     else:
         layer += 2 * 2 * rows * dim                                     # q16, dq16
         per_state = 2 * dim + 12 if store == "fp8" else 4 * dim + 4     # fp8: g, vb, sg, sv, lz; bf16: g, vb, lz
-    if not bf16_inputs:
+    if pad:
+        layer += 4 * queries * dim + 2 * 2 * keys * dim                 # padded copies: q (fp32), k, v (bf16)
+    elif not bf16_inputs:
         layer += 2 * 2 * keys * dim                                     # bf16 copies of k and v
     window = gw * nbp * per_state + 4 * gw * kx                         # state, idx
     # the fused route takes up to 8192 near leaves, and 262144 leaves per head (int8; its top-k
     # keys past 16384 in workspace) or 16384 (the 16-bit stores); larger layers run the stage path
     fused = fused and kx <= 8192 and nb <= (262144 if store == "int8" else 16384)
+    if fused:
+        layer += 4 * rows                                               # rowmax, shared by the windows
     if fused and nb > 16384:
         window += 4 * gw * nbp                                          # route_select top-k keys
     if not fused:
@@ -116,14 +122,14 @@ def predicted_peak_mib(keys: int, tile: int, tile_chunk: int, splits: int = 8, l
 
 def plan_chunk(free_bytes: int, keys: int, tile: int, splits: int = 8, order: str = "seq", graph: bool = True,
                queries: int = 0, leaf: int = 16, heads: int = 1, group: int = 1, exact_leaves: int = 256,
-               store: str = "int8", fused: bool = True, window_streams: int = 2) -> int:
+               store: str = "int8", fused: bool = True, window_streams: int = 2, dim: int = 128) -> int:
     """The largest of CHUNKS whose predicted peak fits in ``free_bytes`` (fewer windows, fewer
     launches; h3/htrc_flat_runner.py:71-82); MemoryError when not even the smallest fits."""
     need = None
     for c in CHUNKS:
-        need = predicted_peak_mib(keys, tile, c, splits, leaf=leaf, order=order, graph=graph, queries=queries,
-                                  heads=heads, group=group, exact_leaves=exact_leaves, store=store, fused=fused,
-                                  window_streams=window_streams)
+        need = predicted_peak_mib(keys, tile, c, splits, leaf=leaf, dim=dim, order=order, graph=graph,
+                                  queries=queries, heads=heads, group=group, exact_leaves=exact_leaves, store=store,
+                                  fused=fused, window_streams=window_streams)
         if need * MIB <= int(free_bytes):
             return c
     raise MemoryError(f"flat HTRC needs ~{need:.0f} MiB at the smallest window ({CHUNKS[-1]} tiles), "
@@ -134,7 +140,8 @@ class _Plan:
     """Operator keyword arguments of a runner: PROD, then the mode, then the caller's knobs
     (``kern`` merged key by key), then the tile window."""
 
-    def __init__(self, flat, mode, overrides, sink_leaves, queries, keys, heads, free_bytes, tile_chunk, graph):
+    def __init__(self, flat, mode, overrides, sink_leaves, queries, keys, heads, free_bytes, tile_chunk, graph,
+                 dim=128):
         if mode not in MODES:
             raise ValueError(f"mode must be one of {list(MODES)}")
         over = dict(overrides)
@@ -145,7 +152,7 @@ class _Plan:
         sizing = dict(leaf=int(cfg.get("leaf", 16)), order=cfg["order"], graph=graph, queries=int(queries),
                       heads=int(heads), group=max(1, int(kern.get("group", 1))), exact_leaves=kx,
                       store=cfg.get("store", "int8"), fused=bool(kern.get("fused", True)),
-                      window_streams=int(kern.get("window_streams", 2)))
+                      window_streams=int(kern.get("window_streams", 2)), dim=int(dim))
         if tile_chunk is None:
             tile_chunk = cfg["tile_chunk"] if free_bytes is None else plan_chunk(
                 free_bytes, keys, cfg["tile"], cfg.get("splits", 8), **sizing)
@@ -227,7 +234,7 @@ class FlatRunner:
         self.mode = mode
         self.heads = max(1, int(heads))
         plan = _Plan(htrc_flat, mode, overrides, sink_leaves, queries, keys, self.heads, free_bytes, tile_chunk,
-                     bool(use_graph))
+                     bool(use_graph), dim=dim)
         self.cfg = plan.cfg
         self.predicted_mib = plan.mib
         self.queries, self.keys, self.dim = int(queries), int(keys), int(dim)

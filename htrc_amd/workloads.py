@@ -96,6 +96,19 @@ def h3_live(n: int = 40759, keys: int = 40752, tail: int = 7, d: int = 128, head
     return tuple(torch.stack(x) for x in out)
 
 
+def config1(seed: int = 0, queries: int = 1024, keys: int = 4096, d: int = 64):
+    """BASELINE configuration 1's inputs (src/htrc_reference/model.py evaluated on q, k, v ~ N(0, 1)
+    from numpy's default_rng(seed), drawn q, then k, then v; the reference scales q by 1 / sqrt(d))
+    rounded once to bf16 -> q, k, v bf16 [1, n, d] with q unscaled: the flat operator's default
+    scale 1 / sqrt(d) (0.125 at d = 64, a power of two) gives the reference's logits exactly."""
+    import numpy as np
+    rng = np.random.default_rng(int(seed))
+    q = rng.standard_normal((queries, d))
+    k = rng.standard_normal((keys, d))
+    v = rng.standard_normal((keys, d))
+    return tuple(_bf16(torch.from_numpy(x).float()).unsqueeze(0) for x in (q, k, v))
+
+
 def make(name: str, *, seed: int = 0, heads: int | None = None, device="cpu"):
     """(q, k, v, leaf, exact_leaves) for a named configuration."""
     gen, kw, leaf, ex, h = CONFIGS[name]

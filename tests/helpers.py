@@ -118,11 +118,15 @@ def far_score_drift(st, ref) -> np.ndarray:
     return drift
 
 
-def check_logz(logz_gpu, ref, st, bar: float, rows=None) -> float:
+INT8_DRIFT_EXCESS = 1e-4
+
+
+def check_logz(logz_gpu, ref, st, bar: float, rows=None, name: str = "check_logz") -> float:
     """|logZ_gpu - logZ_oracle| <= bar + the row's far-score drift (far_score_drift), rows in query
     order (through the k-means permutation when there is one), on the rows of ``rows`` (a bool
     mask in query order; all rows by default); returns the largest excess over ``bar`` that the
-    drift allowed."""
+    drift allowed, records it under ``name``, and fails when it passes INT8_DRIFT_EXCESS on the
+    int8 store (whose g codes flip at fp32-noise ties only, a few per million)."""
     drift = far_score_drift(st, ref)
     n = ref["logz"].shape[0]
     allow = np.empty(n)
@@ -134,4 +138,35 @@ def check_logz(logz_gpu, ref, st, bar: float, rows=None) -> float:
     sel = np.ones(n, bool) if rows is None else np.asarray(rows, bool)
     bad = np.where((err > bar + allow) & sel)[0]
     assert bad.size == 0, f"row {bad[0]}: |dlogZ| {err[bad[0]]:.3e} > {bar} + drift {allow[bad[0]]:.3e}"
-    return float(max(0.0, (err[sel] - bar).max())) if sel.any() else 0.0
+    excess = float(max(0.0, (err[sel] - bar).max())) if sel.any() else 0.0
+    import torch
+    int8 = st["g8"].dtype == torch.int8
+    record(name, {"logz_abs_max": float(err[sel].max()) if sel.any() else 0.0, "drift_excess": excess,
+                  "store": "int8" if int8 else str(st["g8"].dtype)})
+    assert not int8 or excess <= INT8_DRIFT_EXCESS, f"int8 store: logZ drift excess {excess:.3e}"
+    return excess
+
+
+def oracle_with_routing(ref: dict, idx, *, store: str, tile: int, leaf: int, scale: float, group: int = 1,
+                        n: int) -> dict:
+    """The oracle's out / logZ (query order) recomputed on its own state and operands with the near
+    sets ``idx`` [ng, kx] (the GPU's routing) in place of its own: where a near-tie made the GPU
+    pick other near leaves, this is the output those leaves give, so every row can be held to the
+    operator bars.  -> {"out", "logz", "idx", "excl"} to update ``ref`` with."""
+    from oracle import flat_i8
+    st = dict(ref)
+    idx = np.asarray(idx, np.int32)
+    st["idx"] = idx
+    excl = np.zeros_like(ref["excl"])
+    for t in range(idx.shape[0]):
+        excl[t, idx[t]] = 1
+    st["excl"] = excl
+    tp = {"fp8": flat_i8.tile_partials_fp8, "bf16": flat_i8.tile_partials_bf16}.get(store, flat_i8.tile_partials)
+    pm, pl, pacc = tp(st, tile=tile, leaf=leaf, scale=scale, splits=1, bn=64, group=group)
+    out, logz = flat_i8.merge(pm, pl, pacc)
+    out, logz = out[:n], logz[:n]
+    if ref.get("perm") is not None:
+        o, z = np.empty_like(out), np.empty_like(logz)
+        o[ref["perm"]], z[ref["perm"]] = out, logz
+        out, logz = o, z
+    return {"out": out, "logz": logz, "idx": idx, "excl": excl}

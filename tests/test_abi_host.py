@@ -160,9 +160,12 @@ def test_flat_attention_shape_errors_and_no_cpu_fallback():
     q, k, v = _qkv(m=100)
     with pytest.raises(ValueError, match="multiple of the leaf"):
         htrc_flat.flat_attention_prod(q, k, v, leaf=16)
-    q, k, v = _qkv(d=64)
-    with pytest.raises(ValueError, match="128"):
+    q, k, v = _qkv(d=256)
+    with pytest.raises(ValueError, match="at most 128"):
         htrc_flat.flat_attention_prod(q, k, v)
+    q, k, v = _qkv(d=64)
+    with pytest.raises(ValueError, match="same for q and k"):
+        htrc_flat.flat_attention_prod(q[:, :32], k, v)
     q, k, v = _qkv()
     with pytest.raises(ValueError, match="HIP device"):      # CPU tensors never fall back to a CPU path
         htrc_flat.flat_attention_prod(q, k, v, leaf=16, exact_leaves=2)
@@ -258,10 +261,10 @@ def test_memory_model_follows_the_route_limits():
             wb(2048, 320000, leaf=16, kx=64, store=store, fused=False, splits=1)
         assert wb(2048, 4096, leaf=16, kx=64, store=store, fused=True) < \
             wb(2048, 4096, leaf=16, kx=64, store=store, fused=False, splits=1)
-    # int8 at 20000 leaves stays fused: 32 centres x 20000 leaves of 4-byte top-k keys, against the
-    # stage path's 5 bytes of SEL and excl
+    # int8 at 20000 leaves stays fused: 32 centres x 20000 leaves of 4-byte top-k keys and the
+    # layer's rowmax (2048 rows x 4 bytes), against the stage path's 5 bytes of SEL and excl
     assert wb(2048, 320000, leaf=16, kx=64, store="int8", fused=False, splits=1) - \
-        wb(2048, 320000, leaf=16, kx=64, store="int8", fused=True) == 32 * 20000 * (5 - 4)
+        wb(2048, 320000, leaf=16, kx=64, store="int8", fused=True) == 32 * 20000 * (5 - 4) - 4 * 2048
 
 
 def test_runner_plan_merges_knobs():
@@ -284,3 +287,39 @@ def test_windows_cover_every_group_once():
             assert cover == list(range(ng))
             step = ng if not chunk else max(1, chunk // group)
             assert all(gn == min(step, ng - g0) for g0, gn in wins)
+
+
+def test_noalloc_rejects_calls_beyond_the_scratch():
+    """24 heads of 200000 queries need 24 * 200000 * 4 bytes of rowmax alone (19.2 MB) plus the
+    near leaves of 3125 tiles x 200 near leaves x 24 heads (60 MB): more than the 32 MiB scratch of
+    htrc_route_noalloc, refused on the host before the scratch is resolved or any launch (the
+    pointers are never dereferenced, so this needs no device)."""
+    f = _FAKE
+    rc = _lib.lib().htrc_route_noalloc(*([f] * 11), 24, 200000, 200000 * 64, 64, 128, 200, 0, 1, 64, 1, 0, 3125,
+                                       None, 0.088, f, f, None)
+    assert rc == 1
+    assert "bytes of scratch" in _lib.lib().htrc_last_error().decode()
+
+
+def test_window_streams_are_owned_per_thread(monkeypatch):
+    """Each host thread deals its tile windows over side streams of its own (a capture in one
+    thread must not see another thread's eager launches on them); one thread reuses its streams.
+    Streams are stubbed: no GPU here."""
+    import threading
+    made = []
+
+    def stream(device=None):
+        made.append(object())
+        return made[-1]
+
+    monkeypatch.setattr(htrc_flat.torch.cuda, "Stream", stream)
+    monkeypatch.setattr(htrc_flat, "_WINDOW_STREAMS", threading.local())     # the stubs stay in this test
+    dev = torch.device("cuda:0")
+    mine = htrc_flat._window_streams(dev, 2)
+    assert htrc_flat._window_streams(dev, 2) == mine and len(mine) == 2
+    got = {}
+    t = threading.Thread(target=lambda: got.setdefault("other", htrc_flat._window_streams(dev, 2)))
+    t.start()
+    t.join()
+    assert len(got["other"]) == 2 and not set(map(id, got["other"])) & set(map(id, mine))
+    assert htrc_flat._window_streams(dev, 3)[:2] == mine and len(made) == 5

@@ -1,0 +1,85 @@
+"""BASELINE configuration 1 on the HIP path: 1024 queries x 4096 keys, d = 64, leaves of 64
+contiguous keys, q / k / v ~ N(0, 1) from numpy's default_rng(0) (bf16-rounded), the inputs the
+NumPy htrc_reference is evaluated on (src/htrc_reference/model.py:98-137).
+
+Head dims below 128 run on copies padded with zero dims (the reference's kernels take any
+power-of-two D, h3/htrc_flat_triton.py:43, 90).  Against the CPU oracle run at d = 64 on the same
+bits: the packed operands bit-exact on the real dims and zero on the padding, the routing equal up
+to the oracle's own near-ties, out rel-L2 <= 1e-2 and |dlogZ| <= 1e-3.  The flat operator's error
+against exact softmax attention is recorded beside the forest's (median rel-L2 0.25).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits, gpu_sel, record, rel_l2, routing_report, sel_error
+from htrc_amd import htrc_flat, htrc_flat_runner, workloads
+from oracle import flat_i8
+
+pytestmark = pytest.mark.gpu
+
+D1 = 64
+
+
+def _exact(q, k, v, scale):
+    """Exact softmax attention in float64 on the CPU -> (out [n, d], logZ [n])."""
+    s = q.double() @ k.double().T * scale
+    lz = torch.logsumexp(s, dim=1)
+    return (torch.exp(s - lz[:, None]) @ v.double()).numpy(), lz.numpy()
+
+
+@pytest.mark.parametrize("store,near", [("int8", 16), ("int8", 4), ("fp8", 16), ("bf16", 16)])
+def test_config1_inputs_vs_oracle(device, store, near):
+    q, k, v = workloads.config1(seed=0)
+    st = {}
+    out, logz = htrc_flat.flat_attention(q.to(device), k.to(device), v.to(device), backend="hip", store=store,
+                                         dot="bf16", leaf=64, exact_leaves=near, return_logz=True, state=st)
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (1, 1024, D1)
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=64, exact_leaves=near, splits=1,
+                          bn=32, store=store)
+    if store == "int8":
+        for name in ("q8", "dq8", "k8"):
+            got = st[name][0].cpu().numpy()
+            assert np.array_equal(got[:, :D1], ref[name]), name
+            assert not got[:, D1:].any(), f"{name}: padded dims must stay zero"
+        for name in ("sq", "sdq", "ks"):
+            assert np.array_equal(st[name][0].cpu().numpy(), ref[name]), name
+    mu = st["mu"][0].cpu().numpy()
+    assert np.array_equal(mu[:, :D1], ref["mu"]) and not mu[:, D1:].any()
+    nb = 4096 // 64
+    idx = st["idx"][0].cpu().numpy()
+    rep = routing_report(idx, ref["idx"], ref["sel"][:, :nb], sel_error(gpu_sel(st), ref["sel"], nb))
+    o = out[0].cpu().numpy()
+    rel = rel_l2(o, ref["out"])
+    dlz = float(np.abs(logz[0].cpu().numpy().astype(np.float64) - ref["logz"]).max())
+    ex_out, ex_lz = _exact(q[0].float(), k[0].float(), v[0].float(), 1 / math.sqrt(D1))
+    per_row = np.linalg.norm(o - ex_out, axis=1) / np.linalg.norm(ex_out, axis=1)
+    rep.update(store=store, near=near, rel_l2=rel, dlogz=dlz, exact_rel_l2_median=float(np.median(per_row)),
+               exact_rel_l2_max=float(per_row.max()),
+               exact_logz_abs_max=float(np.abs(logz[0].cpu().numpy() - ex_lz).max()))
+    record(f"config1[{store}-{near}]", rep)
+    assert rel <= 1e-2 and dlz <= 1e-3, rep
+    assert np.isfinite(o).all() and per_row.max() < 1.0, rep
+
+
+def test_config1_runner_graph_equals_eager(device):
+    """FlatRunner(dim=64): the graph replay of a 64-dim head equals the eager operator bit for bit,
+    tail keys included."""
+    q, k, v = (x[0].to(device) for x in workloads.config1(seed=0))
+    g = torch.Generator().manual_seed(1)
+    tail = tuple(torch.randn((5, D1), generator=g).to(device) for _ in range(2))
+    kw = dict(leaf=64, exact_leaves=16, tile_chunk=8)
+    r = htrc_flat_runner.FlatRunner(1024, 4096, mode="fast", dim=D1, tail_rows=5, **kw)
+    assert r.graph is not None, r.graph_error
+    got = r.head(q, k, v, tail=tail)
+    want = htrc_flat.flat_attention(q, k, v, tail=tail, **r.cfg)
+    torch.cuda.synchronize()
+    assert tuple(got.shape) == (1024, D1) and torch.equal(got, want)
+    got2 = r.head(q.flip(0).contiguous(), k, v, tail=tail)
+    want2 = htrc_flat.flat_attention(q.flip(0).contiguous(), k, v, tail=tail, **r.cfg)
+    assert torch.equal(got2, want2)

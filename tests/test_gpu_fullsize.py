@@ -5,8 +5,9 @@
 * tiles are independent given the keys, so whole tiles of the full-size run (first, second,
   middle, last) of two or three heads are compared with the oracle run on just those tiles and
   the head's full key set: pack bit-exact, output rel-L2 <= 1e-2 and |dlogZ| <= 1e-3;
-* routing of one whole head: the oracle's leaf state and SEL of every tile of the head against
-  the GPU's, the near sets compared through the measured SEL error (helpers.routing_report);
+* routing of one whole head of each shape (32-row tiles included): the oracle's leaf state and SEL
+  of every tile of the head against the GPU's, the near sets compared through the measured SEL
+  error (helpers.routing_report);
 * a run in tile windows of 128 tiles (PROD's tile_chunk) gives the one-window result bit for bit,
   and one head run alone gives exactly the head-batched result.
 
@@ -33,7 +34,7 @@ KW = dict(backend="hip", store="int8", dot="bf16", splits=4, kern={"tile_bn": 64
 # (workload, tile, leaf, near leaves, heads, checked tiles, checked heads, whole-head routing head)
 SHAPES = {
     "cfg3": ("cfg3", 64, None, None, 24, (0, 1, 503, 1007), (0, 11, 23), 11),
-    "tile32": ("cfg3", 32, 16, 256, 4, (0, 1, 1007, 2015), (0, 3), None),
+    "tile32": ("cfg3", 32, 16, 256, 4, (0, 1, 1007, 2015), (0, 3), 1),
     "cfg4": ("cfg4", 64, None, None, 24, (0, 1, 976, 1952), (0, 12, 23), 12),
 }
 
@@ -85,8 +86,6 @@ def test_fullsize_whole_head_routing(layer):
     g8 codes agree except at fp32-noise ties, and the near sets differ only where the oracle's
     top-k boundary gap is within twice the measured SEL error of the tile."""
     name, q, k, v, tile, leaf, ex, tiles, hs, hr, st, out, logz = layer
-    if hr is None:
-        pytest.skip("whole-head routing is checked at cfg3 and cfg4")
     nb = st["nb"]
     mu = st["mu"][hr].cpu().numpy()
     og8, osg, _, olz = flat_i8.stats(mu, bits(k[hr].cpu()), bits(v[hr].cpu()), leaf, 1 / math.sqrt(128))

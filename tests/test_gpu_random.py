@@ -6,9 +6,10 @@ centres (kern["group"]), the select row stride, forced sink leaves, the query or
 tile window from its own seed, so a failure names a reproducible combination.  The bars are
 those of the single-knob tests: every tile's near set equals the oracle's except where the
 oracle's own top-k boundary gap is within twice the measured SEL error, and on the rows of
-every tile whose near set is the oracle's, output rel-L2 <= 1e-2 and |dlogZ| <= 1e-3 plus each
-row's far-score drift from the state's rounding (as test_gpu_flat allows for the int8 state);
-the same call in tile windows reproduces the result bit for bit.
+every row output rel-L2 <= 1e-2 and |dlogZ| <= 1e-3 plus each row's far-score drift from the
+state's rounding (as test_gpu_flat allows for the int8 state) against the oracle, re-run with
+the GPU's near sets where a near-tie swapped one; the same call in tile windows reproduces the
+result bit for bit.
 """
 from __future__ import annotations
 
@@ -16,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bits, check_logz, gpu_sel, record, rel_l2, routing_report, sel_error
+from helpers import bits, check_logz, gpu_sel, oracle_with_routing, record, rel_l2, routing_report, sel_error
 from htrc_amd import htrc_flat, workloads
 from oracle import flat_i8
 
@@ -62,20 +63,17 @@ def test_random_knobs_vs_oracle(device, seed):
                           sink_leaves=c["sink"], group=c["group"], order=c["order"], store=c["store"])
     assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(logz).all()), name
     nb = st["nb"]
-    ok = np.ones(c["n"], bool)                        # query rows whose tile group's near set is the oracle's
     if min(c["ex"] + c["sink"], nb) > 0:              # else no near set: the far field alone
         sel = gpu_sel(st, c["stride"])
         gi = st["idx"][0].cpu().numpy()
         rep = routing_report(gi, ref["idx"], ref["sel"][:, :nb], sel_error(sel, ref["sel"], nb))
         record(name, rep)
         assert rep["mismatched"] <= rep["tieable"], f"{name}: {rep}"
-        # a near-tie swap changes which leaves a tile attends exactly (with one near leaf, all of
-        # them): those tiles' rows are held to the routing check above, the rest to the bars below
-        span = c["tile"] * c["group"]
-        for gidx in range(ref["idx"].shape[0]):
-            if not np.array_equal(np.sort(gi[gidx]), np.sort(ref["idx"][gidx])):
-                prow = np.arange(gidx * span, min((gidx + 1) * span, c["n"]))
-                ok[ref["perm"][prow] if c["order"] == "kmeans" else prow] = False
-    err = rel_l2(out.cpu().numpy()[ok], ref["out"][ok])
+        if rep["mismatched"]:
+            # a near-tie swap changes which leaves a tile attends exactly: the oracle re-run with
+            # the GPU's near sets gives the output those leaves give, so every row meets the bars
+            ref = {**ref, **oracle_with_routing(ref, gi, store=c["store"], tile=c["tile"], leaf=c["leaf"],
+                                                scale=1 / np.sqrt(128), group=c["group"], n=c["n"])}
+    err = rel_l2(out.cpu().numpy(), ref["out"])
     assert err <= OUT_REL_L2, f"{name}: rel-L2 {err:.3e}"
-    check_logz(logz.cpu().numpy(), ref, st, LOGZ_ABS, rows=ok)
+    check_logz(logz.cpu().numpy(), ref, st, LOGZ_ABS, name=name)

@@ -201,3 +201,27 @@ def test_reference_max_retry(device, heads, store):
     assert ref["logz"][5] > 70.0                          # the outlier dominates row 5
     assert rel_l2(out[h, :256].cpu().numpy(), ref["out"]) <= OUT_REL_L2
     assert np.abs(logz[h, :256].cpu().numpy() - ref["logz"]).max() <= LOGZ_ABS
+
+
+def _ws_bytes(ws) -> int:
+    """Device bytes held by a workspace dict (window workspaces nested inside it)."""
+    n = 0
+    for t in ws.values():
+        n += _ws_bytes(t) if isinstance(t, dict) else t.numel() * t.element_size()
+    return n
+
+
+@pytest.mark.parametrize("store,chunk,streams", [("int8", None, 2), ("int8", 4, 2), ("int8", 4, 1), ("int8", 3, 3),
+                                                 ("fp8", 4, 2), ("bf16", 5, 2)])
+def test_memory_model_equals_the_buffers_a_call_allocates(device, store, chunk, streams):
+    """htrc_flat_runner.workspace_bytes (what plan_chunk sizes tile windows against) is the byte
+    count of the buffers one operator call leaves in its workspace: the layer's operands, outputs
+    and one shared rowmax, plus the state and routing of each window stream's buffers."""
+    q, k, v = (x.to(device) for x in workloads.clustered_runs(n=1024, runs=16, heads=2, seed=7))
+    ws = {}
+    htrc_flat.flat_attention(q, k, v, ws=ws, **_kw(store=store, leaf=64, exact_leaves=3, tile_chunk=chunk,
+                                                 kern={"window_streams": streams}))
+    torch.cuda.synchronize()
+    want = htrc_flat_runner.workspace_bytes(1024, 1024, leaf=64, heads=2, kx=3, tile_chunk=chunk, store=store,
+                                            window_streams=streams)
+    assert _ws_bytes(ws) == want
