@@ -636,7 +636,9 @@ def test_stats_fp8_close_to_oracle(device, leaf):
         assert np.all(np.abs(a - b) <= step * 1.001)
         rates[name] = float((gv != want).mean())
     record(f"stats_fp8_flips[{leaf}]", rates)
-    assert rates["g"] < 2e-2 and rates["vb"] < 2e-2, rates
+    # measured (leaf 64 / 32): g 1.5e-5 / 0, vb 1.7e-4 / 1.9e-4 of the codes a step away; bars at
+    # twice the largest
+    assert rates["g"] <= 3.1e-5 and rates["vb"] <= 3.8e-4, rates
 
 
 @pytest.mark.parametrize("group,stride", [(1, 1), (2, 4)])
@@ -710,15 +712,20 @@ def test_stats_bf16_close_to_oracle(device, leaf):
     for name, got, want in (("g", g, ref["g16"]), ("vb", vbs, ref["vb16"])):
         a = _np(got[0].float())[:, :nb].astype(np.float64)
         b = bf16.to_f32(want).astype(np.float64)
-        # one bf16 step, over a floor at 2^-8 of the row's largest entry (fp32 moment sums)
-        floor = np.abs(b).max(-1, keepdims=True) * 2 ** -8
-        assert np.all(np.abs(a - b) <= np.maximum(np.abs(b) * 2 ** -7, floor) * 1.001)
+        # one bf16 step at the oracle's value (2^(e - 8) for |b| = m 2^e, m in [1/2, 1)) plus fp32
+        # noise of the moment sums (2^-20 of the row's largest entry)
+        _, e = np.frexp(np.abs(b))
+        step = np.where(b != 0, np.ldexp(1.0, e - 8), 0.0)
+        noise = np.abs(b).max(-1, keepdims=True) * 2.0 ** -20
+        assert np.all(np.abs(a - b) <= step + noise), name
         rates[name] = float((_np(got[0].view(torch.int16))[:, :nb].view(np.uint16) != want).mean())
         # measured error against the row's largest entry, beside the floor above
         rates[name + "_err_vs_rowmax"] = float((np.abs(a - b) / np.maximum(np.abs(b).max(-1, keepdims=True),
                                                                            1e-300)).max())
     record(f"stats_bf16_flips[{leaf}]", rates)
-    assert rates["g"] < 5e-2 and rates["vb"] < 5e-2, rates
+    # measured (leaf 64 / 32): g 7.6e-5 / 7.6e-5, vb 2.3e-3 / 2.4e-3 of the values a step away
+    # (vb's weights carry two bf16 terms); bars at twice the largest
+    assert rates["g"] <= 1.6e-4 and rates["vb"] <= 4.9e-3, rates
 
 
 @pytest.mark.parametrize("group,stride", [(1, 1), (2, 4)])
