@@ -4,8 +4,8 @@ One step = one flat-HTRC layer call: B=1, H=24, N=64512, d=128, leaf 64, 32 near
 int8 Q/K + bf16 PV, on synthetic clustered video-region inputs already resident in HBM.
 Prints ONE JSON line (the driver's contract) with the layer ms/call, the roofline of the
 dominant kernel (HIP events on the launch stream, algorithmic bytes or ops per launch),
-per-kernel figures, and the reference's CPU path timed on this host in the same run: the NumPy
-restatement of the torch backend _flat (h3/htrc_flat.py:279-388) over the whole layer, and
+per-kernel figures, and the reference's CPU path timed on this host in the same run: the torch
+backend _flat (h3/htrc_flat.py:279-388) restated with torch CPU ops over the whole layer, and
 BASELINE configuration 1's NumPy htrc_reference (src/htrc_reference/model.py:98-137, restated).
 
   python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--config cfg3] [--no-cpu-baseline]
@@ -181,22 +181,26 @@ def _cpu_info():
 
 
 def cpu_flat_layer(name, heads=None):
-    """The reference's CPU operator (the torch backend _flat, h3/htrc_flat.py:279-388, restated
-    in NumPy fp32) over the configuration's heads, one pass -> (ms for the heads, heads)."""
+    """The reference's CPU operator, its torch backend _flat (h3/htrc_flat.py:279-388), restated
+    with torch ops on CPU tensors (oracle/flat_torch.py) and run with torch's threads on every
+    CPU of this host, over the configuration's heads, one pass -> (ms for the heads, heads,
+    torch threads)."""
+    import torch
     from htrc_amd import workloads
-    from oracle import flat_fp32
+    from oracle import flat_torch
     gen, kw, leaf, ex, h0 = workloads.CONFIGS[name]
     heads = h0 if heads is None else heads
+    torch.set_num_threads(os.cpu_count() or 1)
     elapsed = 0.0
     for h in range(heads):
         q, k, v, _, _ = workloads.make(name, seed=1000 + h, heads=1)
-        qf, kf, vf = (x[0].float().numpy() for x in (q, k, v))
-        if h == 0:          # one warm chunk (BLAS threads, page faults) outside the timing
-            flat_fp32.flat_fp32(qf, kf, vf, tile=64, leaf=leaf, exact_leaves=ex, tile_chunk=32, tiles=slice(0, 32))
+        qf, kf, vf = (x[0].float() for x in (q, k, v))
+        if h == 0:          # one warm window (thread pool, page faults) outside the timing
+            flat_torch.flat_torch(qf, kf, vf, tile=64, leaf=leaf, exact_leaves=ex, tile_chunk=32, tiles=slice(0, 32))
         t0 = time.perf_counter()
-        flat_fp32.flat_fp32(qf, kf, vf, tile=64, leaf=leaf, exact_leaves=ex, tile_chunk=32)
+        flat_torch.flat_torch(qf, kf, vf, tile=64, leaf=leaf, exact_leaves=ex, tile_chunk=32)
         elapsed += time.perf_counter() - t0
-    return elapsed * 1e3, heads
+    return elapsed * 1e3, heads, torch.get_num_threads()
 
 
 def cpu_reference_cfg1():
@@ -215,15 +219,15 @@ def cpu_baseline(name, heads=None):
     from htrc_amd import workloads
     h_layer = workloads.CONFIGS[name][4]
     threads, model = _cpu_info()
-    ms, done = cpu_flat_layer(name, heads)
+    ms, done, torch_threads = cpu_flat_layer(name, heads)
     layer_ms = ms * h_layer / done
     ref_ms, ref = cpu_reference_cfg1()
     sample = (f"one full pass over all {h_layer} heads" if done == h_layer else
               f"{done} of {h_layer} heads ({ms / 1e3:.1f} s), scaled x{h_layer / done:.2f}")
-    return {"value": round(layer_ms, 1), "unit": "ms/call", "cores": threads, "kind": "port",
-            "sample": f"{sample}; NumPy fp32 restatement of the torch backend _flat (h3/htrc_flat.py:279-388), "
-                      f"tile_chunk 32",
-            "cpu": model, "os_cpu_count": os.cpu_count(),
+    return {"value": round(layer_ms, 1), "unit": "ms/call", "cores": torch_threads, "kind": "port",
+            "sample": f"{sample}; the torch backend _flat (h3/htrc_flat.py:279-388) restated with torch CPU ops "
+                      f"(oracle/flat_torch.py), fp32, tile_chunk 32, torch.get_num_threads() = {torch_threads}",
+            "cpu": model, "os_cpu_count": os.cpu_count(), "torch_threads": torch_threads,
             "htrc_reference_cfg1": {"value": round(ref_ms, 1), "unit": "ms (1024 queries)", "cores": threads,
                                     "kind": "port",
                                     "sample": "BASELINE configuration 1 whole: NumPy float64 htrc_reference "

@@ -1586,7 +1586,9 @@ constexpr int DMA_W1 = 6;                           // ... second wave
 constexpr int ROUTE_MAX_KX = 8192;                  // near leaves per tile the route kernel holds in LDS
 constexpr int64_t ROUTE_MAX_NB = 262144;             // leaves per head (exclusion bits: 32 KB of LDS)
 constexpr size_t ROUTE_LDS_MAX = 160 * 1024;         // LDS of one workgroup on gfx950
-constexpr int MAX_PASSES = 3;                       // reference-max retries of a tile
+// Passes of a tile in the route kernels: one at the select launch's reference, and when a row
+// total leaves range one more at every row's exact largest score (in range by construction).
+constexpr int MAX_PASSES = 2;
 // Merge: the wave pairs' partial O, 64 rows x 128 dims each, rows padded to 132 floats.
 constexpr int MRG_STRIDE = 132;
 // Ring slots per pair: blocks are loaded RS - 1 ahead.  Two slots (one block in flight while the
@@ -1784,6 +1786,81 @@ __global__ __launch_bounds__(256, 4) void route_select_kernel(
     }
     const int kxe = min(kx, nb);
     if (kxe > 0) topk_row([&](int l) { return keys[l]; }, nb, kxe, sm, idx + gs * kxe, nullptr, nullptr);
+}
+
+// Largest scores of a wave's rows: the repair of a missed softmax reference in the route kernels.
+template <int RB>
+struct RowMax {
+    float m[RB];
+};
+
+// The largest score (log2 units) of each of this wave's rows (rowb + 16 rb + col, rowb wave-uniform,
+// lane (col, grp)) over
+// a key part of route_kernel: the far leaves [lo, hi) not excluded, then the near tokens
+// [e_lo, e_hi) of the list sidx, 16 keys per MFMA pair with both operands loaded straight from
+// global memory; every lane of a row's column ends with it.  It runs only when a tile's
+// reference missed.  Every lane-dependent address is derived from a lane index redefined through
+// an empty asm here, so the compiler cannot hoist them out of the caller's pass loop (they would
+// stay live, and spill, through its key loops).
+template <int LEAF, int RB>
+__device__ __forceinline__ RowMax<RB> route_exact_max(const int8_t* dq8, const float* sdq, const int8_t* q8,
+                                                   const float* sq, float scale, const int8_t* g8, const float* sg,
+                                                   const float* lz, const uint32_t* exbits, int64_t srow0, int lo,
+                                                   int hi, const int8_t* k8, const float* ks, const uint32_t* sidx,
+                                                   int64_t kh, int e_lo, int e_hi, int64_t rowb) {
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
+    const int col = lane & 15, grp = lane >> 4;
+    const int64_t row0 = rowb + col;
+    RowMax<RB> mx;
+    i32x4 bq[RB][2];
+    float srow[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int64_t p = row0 + 16 * rb;
+        bq[rb][0] = *(const i32x4*)(dq8 + p * D + 16 * grp);
+        bq[rb][1] = *(const i32x4*)(dq8 + p * D + 64 + 16 * grp);
+        srow[rb] = __fmul_rn(sdq[p], LOG2E);
+        mx.m[rb] = -INFINITY;
+    }
+    for (int c = lo; c < hi; c += 16) {           // rows < nb_pad; leaves >= nb are excluded
+        const int64_t r = srow0 + c;
+        const i32x4 A0 = *(const i32x4*)(g8 + (r + col) * D + 16 * grp);
+        const i32x4 A1 = *(const i32x4*)(g8 + (r + col) * D + 64 + 16 * grp);
+        const f32x4 sgv = *(const f32x4*)(sg + r + 4 * grp), lzv = *(const f32x4*)(lz + r + 4 * grp);
+        const uint32_t exw = exbits[c >> 5] >> ((c & 31) + 4 * grp);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const i32x4 acc = mfma_i8(A1, bq[rb][1], mfma_i8(A0, bq[rb][0], i32x4{0, 0, 0, 0}));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float lzm = (exw >> i) & 1u ? -INFINITY : lzv[i];
+                mx.m[rb] = fmaxf(mx.m[rb], __fmaf_rn((float)acc[i], __fmul_rn(srow[rb], sgv[i]), __fmul_rn(lzm, LOG2E)));
+            }
+        }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int64_t p = row0 + 16 * rb;
+        bq[rb][0] = *(const i32x4*)(q8 + p * D + 16 * grp);
+        bq[rb][1] = *(const i32x4*)(q8 + p * D + 64 + 16 * grp);
+        srow[rb] = __fmul_rn(__fmul_rn(sq[p], scale), LOG2E);
+    }
+    for (int j = e_lo; j < e_hi; j += 16) {       // 16-token runs of the near leaves
+        const int64_t tok = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[j / LEAF]) * LEAF + (j % LEAF);
+        const i32x4 A0 = *(const i32x4*)(k8 + (tok + col) * D + 16 * grp);
+        const i32x4 A1 = *(const i32x4*)(k8 + (tok + col) * D + 64 + 16 * grp);
+        const f32x4 ksv = *(const f32x4*)(ks + tok + 4 * grp);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const i32x4 acc = mfma_i8(A1, bq[rb][1], mfma_i8(A0, bq[rb][0], i32x4{0, 0, 0, 0}));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx.m[rb] = fmaxf(mx.m[rb], __fmul_rn((float)acc[i], __fmul_rn(srow[rb], ksv[i])));
+        }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) mx.m[rb] = grp_max(mx.m[rb]);
+    return mx;
 }
 
 // RB = tile / 32: 16-row blocks per wave (tiles of 64 or 32 rows); NP wave pairs split the keys;
@@ -2062,8 +2139,9 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
         }
         // Row totals over the NP key parts (all at the same reference).  A total outside
         // [2^-60, 2^64] means the reference missed the row's maximum by more than 60 octaves
-        // (never observed on real scores): every p <= total, so the pass is redone with the
-        // reference moved to m + log2(total).
+        // (an outlier key far above the far-field maximum, or rows under a sampled tile
+        // reference far below it; never observed on real scores): the tile is redone once at
+        // every row's exact largest score, where each row total lies in [1, keys].
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const float lt = grp_sum(st.l[rb]);
@@ -2074,17 +2152,26 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
         bool bad = false;
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
-            const int r = 16 * RB * hr + 16 * rb + col;
-            const float tot = row_total(r);
-            if (!(tot >= 0x1p-60f && tot <= 0x1p64f)) {
-                bad = true;
-                mref[rb] = tot > 0.0f && tot <= 3.0e38f ? __fadd_rn(mref[rb], __log2f(tot))
-                                                        : __fadd_rn(mref[rb], tot == 0.0f ? -120.0f : 120.0f);
-            }
+            const float tot = row_total(16 * RB * hr + 16 * rb + col);
+            if (!(tot >= 0x1p-60f && tot <= 0x1p64f)) bad = true;
         }
         if (bad) redo = 1;
         __syncthreads();
-        if (redo == 0 || pass + 1 == MAX_PASSES) break;
+        if (__builtin_expect(redo == 0 || pass + 1 == MAX_PASSES, 1)) break;
+        const RowMax<RB> mx = route_exact_max<LEAF, RB>(dq8, sdq, q8, sq, scale, g8, sg, lz, exbits, srow0, lo, hi, k8,
+                                                        ks, sidx, kh, e_lo, e_hi, th * TR + 16 * RB * hr);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+            if (grp == 0) red_l[pr][16 * RB * hr + 16 * rb + col] = mx.m[rb];
+        __syncthreads();
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int r = 16 * RB * hr + 16 * rb + col;
+            float m = red_l[0][r];
+#pragma unroll
+            for (int s = 1; s < NP; ++s) m = fmaxf(m, red_l[s][r]);
+            if (m > -INFINITY) mref[rb] = m;
+        }
     }
     if constexpr (NP == 1) {
         // one pair: each wave holds its rows' finished O^T; lanes (col, grp) write dims
@@ -2392,6 +2479,84 @@ __device__ __forceinline__ void rows_update_bf16(RowsN<RB>& st, const float (&sc
     }
 }
 
+// The largest score (log2 units) of each of this wave's rows (prowb + 16 rb + col, prowb
+// wave-uniform) over every key it
+// attends in route16_kernel: the far leaves not excluded, then the near tokens, 16 keys at a time
+// with both MFMA operands loaded straight from global memory; every lane of a row's column ends
+// with it.  It runs only when a tile's reference missed; lane-dependent addresses come from a
+// lane index redefined through an empty asm (route_exact_max).
+template <int LEAF, bool FP8, int RB>
+__device__ __forceinline__ RowMax<RB> route16_exact_max(const uint16_t* dq16, const uint16_t* q16, const void* g,
+                                                     const float* sg, const float* lz, const uint32_t* exbits,
+                                                     int64_t srow0, int nb, const uint16_t* k, const uint32_t* sidx,
+                                                     int64_t kh, int e_n, int64_t prowb, float qs) {
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
+    const int col = lane & 15, grp = lane >> 4;
+    const int64_t prow0 = prowb + col;
+    RowMax<RB> mx;
+    u32x4 bx[RB][4];
+    auto load_rows = [&](const uint16_t* x) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) bx[rb][ks] = *(const u32x4*)(x + (prow0 + 16 * rb) * D + 32 * ks + 8 * grp);
+    };
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) mx.m[rb] = -INFINITY;
+    load_rows(dq16);
+    for (int c = 0; c < nb; c += 16) {            // rows < nb_pad; leaves >= nb are excluded
+        const int64_t r = srow0 + c;
+        f32x4 acc[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int64_t off = (r + col) * D + 32 * ks + 8 * grp;
+            const u32x4 A = FP8 ? e4m3x8_to_h8_cvt(*(const u32x2*)((const uint8_t*)g + off))
+                                : *(const u32x4*)((const uint16_t*)g + off);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                if constexpr (FP8) acc[rb] = mfma_f16(A, bx[rb][ks], acc[rb]);
+                else acc[rb] = mfma_bf16(as_bf16x8(A), as_bf16x8(bx[rb][ks]), acc[rb]);
+            }
+        }
+        const f32x4 lzv = *(const f32x4*)(lz + r + 4 * grp);
+        const f32x4 sgv = FP8 ? *(const f32x4*)(sg + r + 4 * grp) : f32x4{1.f, 1.f, 1.f, 1.f};
+        const uint32_t exw = exbits[c >> 5] >> ((c & 31) + 4 * grp);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float lzi = (exw >> i) & 1u ? -INFINITY : lzv[i];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                // fp8: the widened codes are value * 2^-8, the row scale enters * 256 (exactly)
+                const float dot = FP8 ? __fmul_rn(acc[rb][i], __fmul_rn(sgv[i], 256.0f)) : acc[rb][i];
+                mx.m[rb] = fmaxf(mx.m[rb], __fmul_rn(__fadd_rn(dot, lzi), LOG2E));
+            }
+        }
+    }
+    load_rows(q16);
+    for (int j = 0; j < e_n; j += 16) {           // 16-token runs of the near leaves
+        const int64_t tok = kh + (int64_t)__builtin_amdgcn_readfirstlane(sidx[j / LEAF]) * LEAF + (j % LEAF);
+        f32x4 acc[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const u32x4 A = *(const u32x4*)(k + (tok + col) * D + 32 * ks + 8 * grp);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma_bf16(as_bf16x8(A), as_bf16x8(bx[rb][ks]), acc[rb]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) mx.m[rb] = fmaxf(mx.m[rb], __fmul_rn(acc[rb][i], qs));
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) mx.m[rb] = grp_max(mx.m[rb]);
+    return mx;
+}
+
 template <int LEAF, bool FP8, int NW, int RB>
 __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
     const uint16_t* __restrict__ q16, const uint16_t* __restrict__ dq16, const void* __restrict__ g,
@@ -2667,9 +2832,9 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
             }
         }
         // row totals: outside [2^-60, 2^64] the reference missed the row's maximum by more than 60
-        // octaves: the pass is redone with the reference moved to m + log2(total)
-        // (2^-8 with the fp8 store: its far-field P is fp16, whose subnormals would hold the far
-        // leaves of a row whose total is that small with too few bits)
+        // octaves (2^-8 with the fp8 store: its far-field P is fp16, whose subnormals would hold
+        // the far leaves of a row whose total is that small with too few bits): the tile is redone
+        // once at every row's exact largest score, where each row total lies in [1, keys]
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const float lt = grp_sum(st.l[rb]);
@@ -2681,15 +2846,16 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const float tot = red_l[16 * RB * wv + 16 * rb + col];
-            if (!(tot >= (FP8 ? 0x1p-8f : 0x1p-60f) && tot <= 0x1p64f)) {
-                mref[rb] = tot > 0.0f && tot <= 3.0e38f ? __fadd_rn(mref[rb], __log2f(tot))
-                                                        : __fadd_rn(mref[rb], tot == 0.0f ? -120.0f : 120.0f);
-                bad = true;
-            }
+            if (!(tot >= (FP8 ? 0x1p-8f : 0x1p-60f) && tot <= 0x1p64f)) bad = true;
         }
         if (bad) redo = 1;
         __syncthreads();
-        if (redo == 0 || pass + 1 == MAX_PASSES) break;
+        if (__builtin_expect(redo == 0 || pass + 1 == MAX_PASSES, 1)) break;
+        const RowMax<RB> mx = route16_exact_max<LEAF, FP8, RB>(dq16, q16, g, sg, lz, exbits, gs * nb_pad, nb, k, sidx,
+                                                              kh, e_n, th * TR + 16 * RB * wv, qs);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+            if (mx.m[rb] > -INFINITY) mref[rb] = mx.m[rb];
     }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
