@@ -69,10 +69,12 @@ def algorithmic(h, nq, nk, leaf, kx, d=128, tile=64, store="int8"):
                          **({"i8_ops": h * far_ops, "bf16_flops": 0} if i8 else {"i8_ops": 0, "bf16_flops": h * far_ops})}
     f["route_attend"] = {"bytes": h * (state + 2 * rows * row + nk * tok + nt * kx * 4 + rows * 4 + 4 * nq * (d + 1)),
                          **ops(far_ops + near_ops)}
-    # the attend launch split into its two fields: far (every leaf's state, kx = 0) and near (the
-    # exact tokens of the kx near leaves, timed as the difference)
+    # the attend launch's two fields, each timed as a launch of its own: far (kx = 0: every leaf
+    # through its state) and near (heads of kx * leaf keys, all kx leaves near: each tile attends
+    # the same kx * leaf exact tokens as in the layer, its far field one excluded 32-leaf block)
     f["far_field"] = {"bytes": h * (state + rows * row + rows * 4 + 4 * nq * (d + 1)), **ops(far_ops)}
-    f["near_field"] = {"bytes": h * (rows * row + nk * tok + nt * kx * 4), **ops(near_ops)}
+    f["near_field"] = {"bytes": h * (nt * kx * per_state + 2 * rows * row + kx * leaf * tok + nt * kx * 4 + rows * 4
+                                     + 4 * nq * (d + 1)), **ops(near_ops)}
     return f
 
 
@@ -237,6 +239,34 @@ def cpu_baseline(name, heads=None):
                                     "logz_abs_max": round(ref["logz_abs_max"], 4)}}
 
 
+def near_field_launch(q, k, v, leaf, kx, scale, store):
+    """The attend launch whose work is the layer's near field: the same heads and queries against
+    heads of the first kx * leaf keys, every one of the kx leaves near, so each tile attends kx *
+    leaf exact tokens (int8 QK and bf16 PV on the int8 store) as it does in the layer, with a far
+    field of one excluded 32-leaf block -> the launch, its operands prepared."""
+    import torch
+    from htrc_amd import htrc_flat_hip as hip
+    nq = int(q.shape[1])
+    kn, vn = (x[:, :kx * leaf].contiguous() for x in (k, v))
+    ws = {}
+    if store == "int8":
+        mu, q8, sq, dq8, sdq = hip.pack_q(q, ws=ws)
+        k8, ks = hip.pack_k(kn, ws=ws)
+        g8, lz, vbs, sg, _ = hip.leaf_stats(mu, kn, vn, kx, scale, leaf=leaf, ws=ws)
+        packed = {"q8": q8, "sq": sq, "dq8": dq8, "sdq": sdq, "k8": k8, "ks": ks, "v": vn}
+        lstate = {"g8": g8, "sg": sg, "lz": lz, "vb": vbs}
+        sel, att = hip.route_select, hip.route_attend
+    else:
+        sdt = torch.float8_e4m3fn if store == "fp8" else torch.bfloat16
+        mu, q16, dq16 = hip.pack_q16(q, ws=ws, dq_fp16=store == "fp8")
+        g, lz, vbs, sg, sv = hip.leaf_stats(mu, kn, vn, kx, scale, leaf=leaf, store=sdt, ws=ws)
+        packed = {"q16": q16, "dq16": dq16, "k": kn, "v": vn}
+        lstate = {"g8": g, "sg": sg, "lz": lz, "vb": vbs, "sv": sv}
+        sel, att = hip.route16_select, hip.route16_attend
+    idx, rowmax = sel(packed, lstate, nq=nq, leaf=leaf, kx=kx, ws=ws)
+    return lambda: att(packed, lstate, idx, rowmax, nq=nq, leaf=leaf, kx=kx, scale=scale, ws=ws)
+
+
 def exact_attention(q, k, v, scale, chunk=4096):
     """Exact softmax attention of one head in fp32 on the GPU -> (out [N, d], logZ [N])."""
     import torch
@@ -321,6 +351,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=None,
                     help="heads of the CPU baseline pass (default: the whole layer)")
+    ap.add_argument("--kernel", default=None,
+                    choices=["pack_q", "pack_k", "stats", "route_select", "route_attend", "far_field", "near_field"],
+                    help="run only this stage's launches (--kernel-reps of them), for rocprofv3 counter passes")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also launch one copy-shaped 1 GiB kernel (the scale of the FETCH_SIZE/WRITE_SIZE counters)")
     a = ap.parse_args()
@@ -362,12 +395,16 @@ def main():
         torch.cuda.synchronize()
         return ev0.elapsed_time(ev1) / steps, res
 
-    ms, out = layer_ms(kw, a.steps, a.warmup)
-    assert torch.isfinite(out).all().item(), "non-finite output"
+    ms = ms_prod_windows = None
+    if not a.kernel:
+        ms, out = layer_ms(kw, a.steps, a.warmup)
+        assert torch.isfinite(out).all().item(), "non-finite output"
+        del out
     # the same layer in the reference PROD's tile windows (tile_chunk 128): the memory-bounded mode
     # (two warm-up calls: the first calls after the window buffers are allocated run slower,
     # measured 8.27 against 8.04 ms at cfg3)
-    ms_prod_windows, _ = layer_ms({**kw, "tile_chunk": htrc_flat.PROD["tile_chunk"]}, max(5, a.steps // 2), 2)
+    if not a.kernel:
+        ms_prod_windows, _ = layer_ms({**kw, "tile_chunk": htrc_flat.PROD["tile_chunk"]}, max(5, a.steps // 2), 2)
     ws.clear()
 
     # per-kernel launch durations, HIP events on the stream the kernels are launched on
@@ -391,12 +428,23 @@ def main():
         stages = {"pack_q": lambda: hip.pack_q16(q, ws=ws, dq_fp16=store == "fp8"),
                   "stats": lambda: hip.leaf_stats(mu, k, v, nb, scale, leaf=leaf, store=sdt, ws=ws)}
     idx, rowmax = sel(packed, lstate, nq=nq, leaf=leaf, kx=kx, ws=ws)
+    near = near_field_launch(q, k, v, leaf, kx, scale, store)
     stages.update({
         "route_select": lambda: sel(packed, lstate, nq=nq, leaf=leaf, kx=kx, ws=ws),
         "route_attend": lambda: att(packed, lstate, idx, rowmax, nq=nq, leaf=leaf, kx=kx, scale=scale, ws=ws),
-        # the attend launch with no near leaves: the far field alone (the near field is the difference)
+        # the attend launch with no near leaves: the far field alone
         "far_field": lambda: att(packed, lstate, None, rowmax, nq=nq, leaf=leaf, kx=0, scale=scale, ws=ws),
+        # the attend launch on heads of kx * leaf keys, every leaf near: the near field alone
+        "near_field": near,
     })
+    if a.kernel:
+        # profiling passes (rocprofv3 --pmc): one stage's launches only, nothing else timed
+        fn = stages[a.kernel]
+        for _ in range(a.kernel_reps):
+            fn()
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel": a.kernel, "launches": a.kernel_reps}), flush=True)
+        return
     kms = {}
     stream = torch.cuda.current_stream(dev)
     for name, fn in stages.items():
@@ -419,8 +467,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     figs = algorithmic(h, nq, nk, leaf, kx, d, store=store)
-    kms["near_field"] = max(kms["route_attend"] - kms["far_field"], 1e-6)
-    kernels = {n: roofline_entry(n, kms[n], figs[n]) for n in list(stages) + ["near_field"]}
+    kernels = {n: roofline_entry(n, kms[n], figs[n]) for n in stages}
     peaks = measured_peaks(dev)
     for n, e in kernels.items():        # the same figures against the measured rates
         e["hbm_frac_measured"] = round(e["hbm_GBps"] / peaks["stream_GBps"], 4)

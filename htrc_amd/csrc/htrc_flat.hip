@@ -422,315 +422,282 @@ __device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
     return u;
 }
 
+// Leaf statistics at the tile centres (h3/htrc_flat_triton.py:41-85), per (centre, leaf): the
+// logits a = (mu . k) scale by bf16 MFMA with mu in three bf16 terms (fp32-accurate), lz = max +
+// log sum exp, w = softmax, g = (w K) scale with w in three terms, vb = w V with two.
 // STORE 0: g int8 with row scale sg, vb bf16 (the production I8 store, :73-80);
 // STORE 1: g and vb bf16, no scales (store="bf16", :82-83);
 // STORE 2: g and vb as e4m3 codes of x / s with row scales s = max(max|x| * fp32(1/448), 1e-30)
 // (sg, sv; store="fp8", :65-72); vb then holds bytes.
-// NW waves of 16 centres each share every staged leaf (workgroup = 16 NW centres).
-constexpr int STATS_NW = 4;
-constexpr int STATS_TPW = 16 * STATS_NW;
-// The launch covers centres [c0, c0 + nt) of each head (mu holds mu_stride centres per head);
-// the state rows are the launch's own, [H, nt, nb_pad].
-template <int LEAF, int STORE, int NW>
-__global__ __launch_bounds__(64 * NW, 2) void stats_kernel(const float* __restrict__ mu, int64_t mu_stride,
-                                                       int64_t c0, int nt, const uint16_t* __restrict__ k,
-                                                       const uint16_t* __restrict__ v, int64_t nk, int nb,
-                                                       int nb_pad, int lpb, float scale,   // lpb: 4, 8 or 16
-                                                       int8_t* __restrict__ g8, float* __restrict__ sg,
-                                                       uint16_t* __restrict__ vb, float* __restrict__ sv,
-                                                       float* __restrict__ lz) {
-    constexpr int KB = LEAF / 16;                 // 16-key blocks per leaf
-    constexpr int KK = (LEAF + 31) / 32;          // 32-key MFMA k-steps per leaf
+// Leaf-stationary schedule: a workgroup of four waves stages the K / V of NL leaves
+// in LDS once (NL * LEAF = 128 keys, 64 KB), then each wave sweeps its share of the launch's
+// centres, 16 at a time, through those leaves: every leaf's K / V leaves HBM once, and the loop
+// has no barrier and no load wait for K / V.  The centres of the next group of 16 are loaded
+// into registers while the current group is computed.  Its state rows are stored as soon as
+// they are quantised; sg / lz (sv) of the NL leaves are NL contiguous floats per centre.
+// ncs: the centre groups of a head are dealt over ncs workgroups (small layers).
+template <int LEAF, int STORE, int NL>
+__global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restrict__ mu, int64_t mu_stride,
+                                                          int64_t c0, int nt, const uint16_t* __restrict__ k,
+                                                          const uint16_t* __restrict__ v, int64_t nk, int nb,
+                                                          int nb_pad, int ncs, float scale, int8_t* __restrict__ g8,
+                                                          float* __restrict__ sg, uint16_t* __restrict__ vb,
+                                                          float* __restrict__ sv, float* __restrict__ lz) {
+    constexpr int KB = LEAF / 16;
+    constexpr int KK = (LEAF + 31) / 32;
     constexpr int LEAF_BYTES = 32 * LEAF * 16;
     constexpr bool FP8 = STORE == 2, BF16 = STORE == 1;
-    constexpr int TPW = 16 * NW;                  // centres per workgroup
-    __shared__ __align__(16) char lds[2 * LEAF_BYTES];
+    static_assert(NL * LEAF_BYTES <= 65536 && (NL == 1 || NL == 2 || NL == 4 || NL == 8), "stats_ls shape");
+    __shared__ __align__(16) char lds[NL * LEAF_BYTES];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    // 1-D grid over (centre group, leaf group, head), centre group fastest: the centre groups
-    // that read the same leaves run together on one XCD and share its L2.
-    const int ntg = (nt + TPW - 1) / TPW, nlg = (nb_pad + lpb - 1) / lpb;
+    // 1-D grid over (centre part, leaf group, head), centre part fastest: the workgroups of one
+    // head run together on one XCD, whose L2 then serves the head's centres to all of them
+    const int nlg = nb_pad / NL;
     const uint32_t blk = xcd_block(blockIdx.x, gridDim.x);
-    const int tg = (int)(blk % (uint32_t)ntg), lg = (int)((blk / (uint32_t)ntg) % (uint32_t)nlg);
-    const int h = (int)(blk / ((uint32_t)ntg * (uint32_t)nlg));
-    const int t = tg * TPW + w * 16 + col;          // centre of this lane's C column
-    const bool tval = t < nt;
-    const int64_t th = (int64_t)h * nt + (tval ? t : 0);
-    const uint32_t lds0 = lds_addr(lds);
-    const uint32_t voff = stage_voff();
-    const float sl2 = __fmul_rn(scale, LOG2E);
-
-    // mu in three bf16 terms (~24 bits, the fp32 centre: the logits, and through the softmax every
-    // product, carry no error beyond fp32 rounding, so the int8 codes of g agree with an IEEE fp32
-    // evaluation except where g * 127 / max|g| lies within fp32 noise of a half)
-    bf16x8 mh[4], mm[4], ml[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = tval ? mu[(h * mu_stride + c0 + t) * D + 32 * ks + 8 * grp + e] : 0.0f;
-        split3x8(x, mh[ks], mm[ks], ml[ks]);
-    }
-
-    const int l0 = lg * lpb;
-    const int l1 = min(nb_pad, l0 + lpb);
-    const int lr = min(nb, l1);                   // real leaves of this workgroup: [l0, lr)
+    const int cs = (int)(blk % (uint32_t)ncs), lg = (int)((blk / (uint32_t)ncs) % (uint32_t)nlg);
+    const int h = (int)(blk / ((uint32_t)ncs * (uint32_t)nlg));
+    const int l0 = lg * NL;
+    const int lr = min(nb, l0 + NL);              // real leaves [l0, lr)
     const int64_t kh = (int64_t)h * nk;
-    // g8 / vb of the previous leaf, stored during the next one
-    uint32_t pg[8];              // g codes (int8 / e4m3)
-    u32x2 pgb[BF16 ? 8 : 1];     // g bf16 pairs (STORE 1)
-    u32x2 pv[8];                 // vb bf16 pairs (FP8: pv[db].x holds the four e4m3 codes)
-    int pl = -1;
-    // The MFMA C layout leaves lane (col, grp) with dims 16db + 4grp.. of centre col.  Lanes
-    // exchange dwords within the column so that every store instruction writes 64 contiguous
-    // bytes of each row (the four lanes of a column side by side): measured on the state rows,
-    // 64-byte segments store at 5.2 TB/s where 16-byte pieces 32 bytes apart reach 4.2 TB/s.
-    // The six stores of leaf l - 1 are spread through leaf l's products, so the write queue
-    // sees a steady stream rather than one burst per leaf.
-    // one-byte rows (g8, FP8 vb): 4 x 4 block transpose of (c[g], c[4 + g]); row g then holds
-    // dims 16g + 4c in x[2c] and 64 + 16g + 4c in x[2c + 1]
-    auto store_bytes = [&](const uint32_t (&c)[8], uint8_t* dst) {
-        uint32_t x[8] = {c[0], c[4], c[1], c[5], c[2], c[6], c[3], c[7]};
-        rows_transpose(x);
-        if (tval) {
-            const int64_t s = th * nb_pad + pl;
-            *(u32x4*)(dst + s * D + 16 * grp) = u32x4{x[0], x[2], x[4], x[6]};
-            *(u32x4*)(dst + s * D + 64 + 16 * grp) = u32x4{x[1], x[3], x[5], x[7]};
+    const int ncg = (nt + 15) / 16, gpp = (ncg + ncs - 1) / ncs;
+    const int jb = cs * gpp, je = min(ncg, jb + gpp);
+    const float sl2 = __fmul_rn(scale, LOG2E);
+    {
+        const uint32_t voff = stage_voff();
+        for (int li = 0; l0 + li < lr; ++li)
+            stage_leaf<LEAF, 256>(k, v, kh + (int64_t)(l0 + li) * LEAF, lds_addr(lds) + li * LEAF_BYTES, voff);
+        wait_vmcnt<0>();
+        __syncthreads();
+    }
+    // this lane's 32 centre values (dims 32 ks + 8 grp + e of centre 16 j + col), fp32
+    auto load_mu = [&](int j, f32x4 (&m)[8]) {
+        const int t = min(16 * j + col, nt - 1);
+        const float* src = mu + ((int64_t)h * mu_stride + c0 + t) * D + 8 * grp;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            m[2 * ks] = *(const f32x4*)(src + 32 * ks);
+            m[2 * ks + 1] = *(const f32x4*)(src + 32 * ks + 4);
         }
     };
-    // bf16 rows, half hf (dims 64hf..): rows 2j and 2j + 1 swap halves; row g then holds, for
-    // db = 2m + (g & 1), the dims 16db + 8(g >> 1) .. + 3 in va and .. + 4 .. + 7 in vc
-    auto store_rows16 = [&](const u32x2 (&c)[8], uint16_t* dst, int hf) {
-        u32x2 va[2], vc[2];
+    // mu of a group in three bf16 terms (~24 bits: the logits, and through the softmax g, carry no
+    // error beyond fp32 rounding)
+    bf16x8 mh[4], mm[4], ml[4];
+    auto split_mu = [&](const f32x4 (&m)[8]) {
 #pragma unroll
-        for (int mm = 0; mm < 2; ++mm) {
-            const int m = 2 * hf + mm;
-            uint32_t a0 = c[2 * m].x, a1 = c[2 * m].y, c0 = c[2 * m + 1].x, c1 = c[2 * m + 1].y;
-            swap16(a0, c0);
-            swap16(a1, c1);
-            va[mm] = u32x2{a0, a1};
-            vc[mm] = u32x2{c0, c1};
-        }
-        if (tval) {
-            const int64_t s = th * nb_pad + pl;
-            uint16_t* vr = dst + s * D + 16 * (grp & 1) + 8 * (grp >> 1);
+        for (int ks = 0; ks < 4; ++ks) {
+            float x[8];
 #pragma unroll
-            for (int mm = 0; mm < 2; ++mm)
-                *(u32x4*)(vr + 32 * (2 * hf + mm)) = u32x4{va[mm].x, va[mm].y, vc[mm].x, vc[mm].y};
-        }
-    };
-    auto store_g = [&]() {
-        if (pl < 0) return;
-        if constexpr (BF16) {
-            store_rows16(pgb, (uint16_t*)g8, 0);
-            store_rows16(pgb, (uint16_t*)g8, 1);
-        } else {
-            store_bytes(pg, (uint8_t*)g8);
-        }
-    };
-    auto store_v = [&](int hf) {
-        if constexpr (FP8) {
-            if (pl >= 0 && hf == 0) {
-                uint32_t c[8];
-#pragma unroll
-                for (int db = 0; db < 8; ++db) c[db] = pv[db].x;
-                store_bytes(c, (uint8_t*)vb);
+            for (int e = 0; e < 4; ++e) {
+                x[e] = m[2 * ks][e];
+                x[4 + e] = m[2 * ks + 1][e];
             }
-        } else if (pl >= 0) {
-            store_rows16(pv, vb, hf);
+            split3x8(x, mh[ks], mm[ks], ml[ks]);
         }
     };
-    // sg, lz (and sv) of the workgroup's 16 leaves stay in registers: every lane of a column
-    // holds its centre's values, a 4-leaf shift register takes each leaf, and lane grp keeps
-    // leaves 4 grp .. 4 grp + 3, written at the end as 64 contiguous bytes per centre.
-    // Leaves past the real ones keep the padding values (sg = sv = 0, lz = -inf).
-    f32x4 sh_sg = {0.f, 0.f, 0.f, 0.f}, sh_lz = sh_sg, sh_sv = sh_sg;
-    f32x4 kp_sg = sh_sg, kp_sv = sh_sg, kp_lz = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    auto push = [&](int l, float vsg, float vlz, float vsv) {
-        sh_sg = f32x4{sh_sg[1], sh_sg[2], sh_sg[3], vsg};
-        sh_lz = f32x4{sh_lz[1], sh_lz[2], sh_lz[3], vlz};
-        if (FP8) sh_sv = f32x4{sh_sv[1], sh_sv[2], sh_sv[3], vsv};
-        if (((l - l0) & 3) == 3) {           // wave-uniform: a real branch, every fourth leaf
-            asm volatile("");
-            if (((l - l0) >> 2) == grp) {
-                kp_sg = sh_sg;
-                kp_lz = sh_lz;
-                if (FP8) kp_sv = sh_sv;
-            }
+    f32x4 mnext[8];
+    if (jb + w < je) {
+        load_mu(jb + w, mnext);
+        split_mu(mnext);
+    }
+    for (int j = jb + w; j < je; j += 4) {
+        // Centres past the last (t >= nt) compute and store the last centre's state: the same bits
+        // to the same rows.  Every store is unconditional and the next group's centres are loaded
+        // at the top of the iteration (a valid group even past the wave's last) and split at its
+        // end, so the compiler's wait for them counts the iteration's stores issued after them
+        // instead of draining them all.
+        const int64_t th = (int64_t)h * nt + min(16 * j + col, nt - 1);
+        load_mu(min(j + 4, je - 1), mnext);
+        float sgs[NL], lzs[NL], svs[NL];
+#pragma unroll
+        for (int li = 0; li < NL; ++li) {
+            sgs[li] = 0.0f;
+            lzs[li] = -INFINITY;
+            svs[li] = 0.0f;
         }
-    };
-    // products of the current leaf and its log-partition
-    f32x4 gacc[8], vacc[8];
-    float lzq = 0.0f;
-    // g^T = scale gacc^T, vb^T of leaf lq: lane holds dims 16db + 4grp + i of centre t.  The int8
-    // code of g is round(127 g / max|g|) = round(gacc * 127 scale / max|g|).
-    auto quantise = [&](int lq) {
-        float am = 0.0f;
 #pragma unroll
-        for (int db = 0; db < 8; ++db)
+        for (int li = 0; li < NL; ++li) {
+            const int l = l0 + li;
+            const int64_t s = th * nb_pad + l;
+            if (l >= lr) {                         // padded leaf: empty state, excluded everywhere
+                // (zero rows by the store instructions of a real leaf: the same count on both paths)
+                if (BF16) {
+                    *(u32x4*)((uint16_t*)g8 + s * D + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
+                    *(u32x4*)((uint16_t*)g8 + s * D + 32 + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
+                    *(u32x4*)((uint16_t*)g8 + s * D + 64 + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
+                    *(u32x4*)((uint16_t*)g8 + s * D + 96 + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
+                } else {
+                    *(u32x4*)(g8 + s * D + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
+                    *(u32x4*)(g8 + s * D + 64 + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
+                }
+                if (FP8) {
+                    *(u32x4*)((uint8_t*)vb + s * D + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
+                    *(u32x4*)((uint8_t*)vb + s * D + 64 + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
+                } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) am = fmaxf(am, fabsf(gacc[db][i]));
-        am = __fmul_rn(grp_max(am), scale);             // max |g|
-        if constexpr (BF16) {
-            // g = gacc * scale and vb rounded to bf16, no scales
-#pragma unroll
-            for (int db = 0; db < 8; ++db) {
-                pgb[db] = u32x2{pack2bf(__fmul_rn(gacc[db][0], scale), __fmul_rn(gacc[db][1], scale)),
-                                pack2bf(__fmul_rn(gacc[db][2], scale), __fmul_rn(gacc[db][3], scale))};
-                pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
+                    for (int q = 0; q < 4; ++q) *(u32x4*)(vb + s * D + 32 * q + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
+                }
+                continue;
             }
-            push(lq, 0.0f, lzq, 0.0f);
-        } else if constexpr (FP8) {
-            // sg = max(max|g| / 448, 1e-30), code = e4m3(g / sg) with g / sg taken as
-            // gacc * (scale / sg); vb the same with sv
-            const float sgv = fmaxf(__fmul_rn(am, R448), 1e-30f);
-            float av = 0.0f;
+            const char* Kr = lds + li * LEAF_BYTES;
+            const char* Vr = Kr + 16 * LEAF * 16;
+            f32x4 a[KB];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                a[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const int row = 16 * kb + col;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const bf16x8 A = as_bf16x8(*(const u32x4*)(Kr + (row * 16 + ((4 * ks + grp) ^ swz(row))) * 16));
+                    a[kb] = mfma_bf16(A, ml[ks], a[kb]);          // smallest term first
+                    a[kb] = mfma_bf16(A, mm[ks], a[kb]);
+                    a[kb] = mfma_bf16(A, mh[ks], a[kb]);
+                }
+            }
+            float amx = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) amx = fmaxf(amx, a[kb][i]);
+            amx = grp_max(amx);
+            const float mx = __fmul_rn(amx, scale), mlog = __fmul_rn(amx, sl2);
+            float z = 0.0f;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    a[kb][i] = __builtin_amdgcn_exp2f(__fmaf_rn(a[kb][i], sl2, -mlog));
+                    z = __fadd_rn(z, a[kb][i]);
+                }
+            z = grp_sum(z);
+            const float rz = __fdiv_rn(1.0f, z);
+            f32x4 gacc[8], vacc[8];
+#pragma unroll
+            for (int db = 0; db < 8; ++db) gacc[db] = vacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                float wv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int kb = 2 * kk + (e >> 2);
+                    wv[e] = kb < KB ? __fmul_rn(a[kb < KB ? kb : 0][e & 3], rz) : 0.0f;
+                }
+                bf16x8 W0, W1, W2;
+                split3x8(wv, W0, W1, W2);
+#pragma unroll
+                for (int db = 0; db < 8; ++db) {
+                    const u32x2 zero = {0u, 0u};
+                    const u32x2 k0 = tr_operand(Kr, 32 * kk, db, lane);
+                    const u32x2 k1 = (2 * kk + 1 < KB) ? tr_operand(Kr, 32 * kk + 16, db, lane) : zero;
+                    const u32x2 v0 = tr_operand(Vr, 32 * kk, db, lane);
+                    const u32x2 v1 = (2 * kk + 1 < KB) ? tr_operand(Vr, 32 * kk + 16, db, lane) : zero;
+                    const bf16x8 KA = as_bf16x8(k0, k1), VA = as_bf16x8(v0, v1);
+                    gacc[db] = mfma_bf16(KA, W2, gacc[db]);
+                    gacc[db] = mfma_bf16(KA, W1, gacc[db]);
+                    gacc[db] = mfma_bf16(KA, W0, gacc[db]);
+                    vacc[db] = mfma_bf16(VA, W1, vacc[db]);
+                    vacc[db] = mfma_bf16(VA, W0, vacc[db]);
+                }
+            }
+            lzs[li] = __fadd_rn(mx, ln_ge1(z));   // z >= 1: its largest term is exp(0)
+            float am = 0.0f;
 #pragma unroll
             for (int db = 0; db < 8; ++db)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) av = fmaxf(av, fabsf(vacc[db][i]));
-            const float svv = fmaxf(__fmul_rn(grp_max(av), R448), 1e-30f);
-            const float cg = __fdiv_rn(scale, sgv), cv = __fdiv_rn(1.0f, svv);
+                for (int i = 0; i < 4; ++i) am = fmaxf(am, fabsf(gacc[db][i]));
+            am = __fmul_rn(grp_max(am), scale);   // max |g|
+            // one-byte rows (g8, FP8 g / vb): 4 x 4 block transpose of (c[g], c[4 + g]); row g then
+            // holds dims 16g + 4c in x[2c] and 64 + 16g + 4c in x[2c + 1]: each store instruction
+            // writes 64 contiguous bytes of a row per lane group
+            auto store_bytes = [&](const uint32_t (&c)[8], uint8_t* dst) {
+                uint32_t x[8] = {c[0], c[4], c[1], c[5], c[2], c[6], c[3], c[7]};
+                rows_transpose(x);
+                *(u32x4*)(dst + s * D + 16 * grp) = u32x4{x[0], x[2], x[4], x[6]};
+                *(u32x4*)(dst + s * D + 64 + 16 * grp) = u32x4{x[1], x[3], x[5], x[7]};
+            };
+            // bf16 rows, both halves hf (dims 64 hf ..): rows 2j and 2j + 1 swap halves; row g then
+            // holds, for db = 2m + (g & 1), dims 16db + 8(g >> 1) .. + 3 in va and .. + 4 .. + 7 in vc
+            auto store_rows16 = [&](const u32x2 (&c)[8], uint16_t* dst) {
 #pragma unroll
-            for (int db = 0; db < 8; ++db) {
-                pg[db] = quant4_e4m3_cvt(gacc[db], cg);
-                pv[db] = u32x2{quant4_e4m3_cvt(vacc[db], cv), 0u};
-            }
-            push(lq, sgv, lzq, svv);
-        } else {
-            am = am < 1e-30f ? 1e-30f : am;
-            const float cq = __fdiv_rn(__fmul_rn(127.0f, scale), am);
+                for (int hf = 0; hf < 2; ++hf) {
+                    u32x2 va[2], vc[2];
 #pragma unroll
-            for (int db = 0; db < 8; ++db) {
-                pg[db] = quant4(gacc[db], cq);
-                pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
-            }
-            push(lq, __fmul_rn(am, R127), lzq, 0.0f);
-        }
-        pl = lq;
-    };
-    if (l0 < lr) stage_leaf<LEAF, 64 * NW>(k, v, kh + (int64_t)l0 * LEAF, lds0, voff);
-    for (int l = l0; l < lr; ++l) {
-        // Leaf l landed and the stores of leaf l - 2 are done (measured: issuing the next
-        // loads ahead of the stores, or letting the stores stay in flight past this wait, is
-        // slower).
-        wait_vmcnt<0>();
-        __syncthreads();                       // ... for every wave; buffer of leaf l - 1 free
-        if (l + 1 < lr)
-            stage_leaf<LEAF, 64 * NW>(k, v, kh + (int64_t)(l + 1) * LEAF, lds0 + ((l + 1 - l0) & 1) * LEAF_BYTES,
-                                      voff);
-        const char* Kr = lds + ((l - l0) & 1) * LEAF_BYTES;
-        const char* Vr = Kr + 16 * LEAF * 16;
-        f32x4 a[KB];
+                    for (int m2 = 0; m2 < 2; ++m2) {
+                        const int m = 2 * hf + m2;
+                        uint32_t a0 = c[2 * m].x, a1 = c[2 * m].y, cc0 = c[2 * m + 1].x, cc1 = c[2 * m + 1].y;
+                        swap16(a0, cc0);
+                        swap16(a1, cc1);
+                        va[m2] = u32x2{a0, a1};
+                        vc[m2] = u32x2{cc0, cc1};
+                    }
+                    uint16_t* vr = dst + s * D + 16 * (grp & 1) + 8 * (grp >> 1);
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-            a[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            const int row = 16 * kb + col;
+                    for (int m2 = 0; m2 < 2; ++m2)
+                        *(u32x4*)(vr + 32 * (2 * hf + m2)) = u32x4{va[m2].x, va[m2].y, vc[m2].x, vc[m2].y};
+                }
+            };
+            if constexpr (BF16) {
+                u32x2 pgb[8], pv[8];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const bf16x8 A = as_bf16x8(*(const u32x4*)(Kr + (row * 16 + ((4 * ks + grp) ^ swz(row))) * 16));
-                a[kb] = mfma_bf16(A, ml[ks], a[kb]);          // smallest term first
-                a[kb] = mfma_bf16(A, mm[ks], a[kb]);
-                a[kb] = mfma_bf16(A, mh[ks], a[kb]);
-            }
-        }
-        store_g();                             // stores of leaf l - 1, first part
-        // a[kb][i] = mu_t . k_{16kb + 4grp + i}; the logits are a * scale, their maximum
-        // mx = amx * scale (rounding is monotone), e = 2^(a * scale * log2e - amx * scale * log2e)
-        float amx = -INFINITY;
+                for (int db = 0; db < 8; ++db) {
+                    pgb[db] = u32x2{pack2bf(__fmul_rn(gacc[db][0], scale), __fmul_rn(gacc[db][1], scale)),
+                                    pack2bf(__fmul_rn(gacc[db][2], scale), __fmul_rn(gacc[db][3], scale))};
+                    pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
+                }
+                store_rows16(pgb, (uint16_t*)g8);
+                store_rows16(pv, vb);
+            } else if constexpr (FP8) {
+                const float sgv = fmaxf(__fmul_rn(am, R448), 1e-30f);
+                float av = 0.0f;
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
+                for (int db = 0; db < 8; ++db)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) amx = fmaxf(amx, a[kb][i]);
-        amx = grp_max(amx);
-        const float mx = __fmul_rn(amx, scale), ml = __fmul_rn(amx, sl2);
-        float z = 0.0f;
+                    for (int i = 0; i < 4; ++i) av = fmaxf(av, fabsf(vacc[db][i]));
+                const float svv = fmaxf(__fmul_rn(grp_max(av), R448), 1e-30f);
+                const float cg = __fdiv_rn(scale, sgv), cv = __fdiv_rn(1.0f, svv);
+                uint32_t pg[8], pvc[8];
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
+                for (int db = 0; db < 8; ++db) {
+                    pg[db] = quant4_e4m3_cvt(gacc[db], cg);
+                    pvc[db] = quant4_e4m3_cvt(vacc[db], cv);
+                }
+                store_bytes(pg, (uint8_t*)g8);
+                store_bytes(pvc, (uint8_t*)vb);
+                sgs[li] = sgv;
+                svs[li] = svv;
+            } else {
+                am = am < 1e-30f ? 1e-30f : am;
+                const float cq = __fdiv_rn(__fmul_rn(127.0f, scale), am);
+                uint32_t pg[8];
+                u32x2 pv[8];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                a[kb][i] = __builtin_amdgcn_exp2f(__fmaf_rn(a[kb][i], sl2, -ml));
-                z = __fadd_rn(z, a[kb][i]);
-            }
-        z = grp_sum(z);
-        const float rz = __fdiv_rn(1.0f, z);
-        // w = e / z in bf16 terms: gacc = w K (g = scale gacc), vb = w V
-#pragma unroll
-        for (int db = 0; db < 8; ++db) gacc[db] = vacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            float wv[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int kb = 2 * kk + (e >> 2);
-                wv[e] = kb < KB ? __fmul_rn(a[kb < KB ? kb : 0][e & 3], rz) : 0.0f;
-            }
-            // w in three bf16 terms for g (its int8 codes), two for vb (rounded to bf16)
-            bf16x8 W0, W1, W2;
-            split3x8(wv, W0, W1, W2);
-#pragma unroll
-            for (int db = 0; db < 8; ++db) {
-                const u32x2 zero = {0u, 0u};
-                const u32x2 k0 = tr_operand(Kr, 32 * kk, db, lane);
-                const u32x2 k1 = (2 * kk + 1 < KB) ? tr_operand(Kr, 32 * kk + 16, db, lane) : zero;
-                const u32x2 v0 = tr_operand(Vr, 32 * kk, db, lane);
-                const u32x2 v1 = (2 * kk + 1 < KB) ? tr_operand(Vr, 32 * kk + 16, db, lane) : zero;
-                const bf16x8 KA = as_bf16x8(k0, k1), VA = as_bf16x8(v0, v1);
-                gacc[db] = mfma_bf16(KA, W2, gacc[db]);
-                gacc[db] = mfma_bf16(KA, W1, gacc[db]);
-                gacc[db] = mfma_bf16(KA, W0, gacc[db]);
-                vacc[db] = mfma_bf16(VA, W1, vacc[db]);
-                vacc[db] = mfma_bf16(VA, W0, vacc[db]);
-            }
-            if (kk == 0 && KK > 1) store_v(0);
-        }
-        if (KK == 1) store_v(0);
-        store_v(1);
-        // quantised after the last stores of leaf l - 1: this VALU work covers their latency
-        // before the next iteration's wait
-        lzq = __fadd_rn(mx, ln_ge1(z));        // z >= 1: its largest term is exp(0)
-        quantise(l);
-    }
-    store_g();
-    store_v(0);
-    store_v(1);
-    {   // a last, partial quad of real leaves: its rem leaves are the newest rem of the shift
-        // register, the rest padding
-        const int rem = (lr - l0) & 3;
-        if (lr > l0 && rem != 0 && ((lr - l0) >> 2) == grp) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int j = 4 - rem + i;     // shift-register slot of quad slot i (i < rem)
-                const bool real = i < rem;
-                kp_sg[i] = real ? sh_sg[j & 3] : 0.0f;
-                kp_lz[i] = real ? sh_lz[j & 3] : -INFINITY;
-                if (FP8) kp_sv[i] = real ? sh_sv[j & 3] : 0.0f;
+                for (int db = 0; db < 8; ++db) {
+                    pg[db] = quant4(gacc[db], cq);
+                    pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
+                }
+                store_bytes(pg, (uint8_t*)g8);
+                store_rows16(pv, vb);
+                sgs[li] = __fmul_rn(am, R127);
             }
         }
-    }
-    // padded leaves [max(l0, nb), l1): empty state, excluded everywhere
-    if (tval) {
-        for (int l = max(l0, nb); l < l1; ++l) {
-            const int64_t s = th * nb_pad + l;
+        // sg, lz (sv) of the NL leaves: NL contiguous floats per centre (the four lanes of a column
+        // hold the same values and write them alike)
+        {
+            const int64_t s = th * nb_pad + l0;
+            auto put = [&](float* dst, const float (&x)[NL]) {
+                if constexpr (NL == 1) {
+                    dst[s] = x[0];
+                } else if constexpr (NL == 2) {
+                    *(u32x2*)(dst + s) = u32x2{__float_as_uint(x[0]), __float_as_uint(x[1])};
+                } else {
 #pragma unroll
-            for (int db = 0; db < 8; ++db) {
-                if (BF16)
-                    *(u32x2*)((uint16_t*)g8 + s * D + 16 * db + 4 * grp) = u32x2{0u, 0u};
-                else
-                    *(uint32_t*)(g8 + s * D + 16 * db + 4 * grp) = 0u;
-                if (FP8)
-                    *(uint32_t*)((uint8_t*)vb + s * D + 16 * db + 4 * grp) = 0u;
-                else
-                    *(u32x2*)(vb + s * D + 16 * db + 4 * grp) = u32x2{0u, 0u};
-            }
+                    for (int q = 0; q < NL; q += 4) *(f32x4*)(dst + s + q) = f32x4{x[q], x[q + 1], x[q + 2], x[q + 3]};
+                }
+            };
+            if (!BF16) put(sg, sgs);
+            put(lz, lzs);
+            if (FP8) put(sv, svs);
         }
-    }
-    // sg, lz (sv) of the workgroup's leaves: lane grp writes leaves l0 + 4 grp .. + 3 (l1 - l0 is
-    // 16: nb_pad is a multiple of 32), the column's four lanes 64 contiguous bytes
-    if (tval && 4 * grp < l1 - l0) {
-        const int64_t s = th * nb_pad + l0 + 4 * grp;
-        if (!BF16) *(f32x4*)(sg + s) = kp_sg;
-        *(f32x4*)(lz + s) = kp_lz;
-        if (FP8) *(f32x4*)(sv + s) = kp_sv;
+        split_mu(mnext);
     }
 }
 
@@ -3499,17 +3466,6 @@ static int device_cus() {
     return n;
 }
 
-// Leaves per stats workgroup: 16, or 8 / 4 when 16 would give the device fewer than two
-// workgroups per CU (small layers: more, shorter workgroups).  A multiple of 4 (the kernel's
-// sg/lz shift register keeps four leaves per lane group) that divides nb_pad (a multiple of 32).
-static int stats_lpb(int64_t nt, int nbp, int64_t heads) {
-    const int64_t ntg = (nt + STATS_TPW - 1) / STATS_TPW;
-    const int64_t want = 2 * (int64_t)device_cus();
-    for (int lpb = 16; lpb > 4; lpb /= 2)
-        if (ntg * ((nbp + lpb - 1) / lpb) * heads >= want) return lpb;
-    return 4;
-}
-
 // Shared checks and launch of the three leaf-statistics stores (STORE 0 int8, 1 bf16, 2 fp8).
 extern "C++" {
 template <int STORE>
@@ -3532,15 +3488,22 @@ static int leaf_stats_launch(const char* who, const float* mu, const uint16_t* k
         return bad("misaligned buffer");
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
-    const int lpb = stats_lpb(cn, nbp, heads);
-    const int64_t nblocks = (cn + STATS_TPW - 1) / STATS_TPW * ((nbp + lpb - 1) / lpb) * heads;
+    // leaf-stationary: NL leaves (64 KB of K / V) per workgroup; the centre groups of a head dealt
+    // over ncs workgroups when the leaf groups alone give fewer than two workgroups per CU (each
+    // wave keeps at least one group of 16 centres)
+    const int nl = 65536 / (512 * leaf);
+    const int64_t nlg = nbp / nl, ncg = (cn + 15) / 16;
+    const int64_t want = 2 * (int64_t)device_cus();
+    int64_t ncs = (want + nlg * heads - 1) / (nlg * heads);
+    ncs = ncs < 1 ? 1 : (ncs > (ncg + 3) / 4 ? (ncg + 3) / 4 : ncs);
+    const int64_t nblocks = ncs * nlg * heads;
     if (nblocks > 0x7fffffff) return bad("too many centres x leaves x heads for one launch");
     const dim3 grid((unsigned)nblocks);
     hipStream_t s = (hipStream_t)stream;
 #define STATS_CASE(L)                                                                                            \
     case L:                                                                                                      \
-        hipLaunchKernelGGL((stats_kernel<L, STORE, STATS_NW>), grid, dim3(64 * STATS_NW), 0, s, mu, nt, c0, (int)cn, \
-                           k, v, nk, (int)nb, nbp, lpb, scale, (int8_t*)g, sg, (uint16_t*)vb, sv, lz);           \
+        hipLaunchKernelGGL((stats_ls_kernel<L, STORE, 65536 / (512 * L)>), grid, dim3(256), 0, s, mu, nt, c0,      \
+                           (int)cn, k, v, nk, (int)nb, nbp, (int)ncs, scale, (int8_t*)g, sg, (uint16_t*)vb, sv, lz); \
         break;
     switch (leaf) {
         STATS_CASE(16)
