@@ -14,6 +14,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
 
 // fp32(1/127) = 0x3C010204, the per-row int8 scale factor.
 __device__ constexpr float R127 = 1.0f / 127.0f;
@@ -178,18 +179,11 @@ __device__ __forceinline__ uint32_t pack2bf(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// The same pair, opaque to the optimiser: reading bf16(a) back as a float (h << 16) otherwise
-// becomes a second conversion of a alone instead of a shift of the packed word.
-__device__ __forceinline__ uint32_t pack2bf_opaque(float a, float b) {
-    uint32_t h = pack2bf(a, b);
-    asm("" : "+v"(h));
-    return h;
-}
-
-// Two fp32 -> packed fp16 pair, round to nearest even (v_cvt_f16_f32 in the default mode).
+// Two fp32 -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32): a in the low half,
+// b in the high half.
 __device__ __forceinline__ uint32_t pack2h(float a, float b) {
-    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
-    return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+    const h16x2 v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 // fp32 rounded to the nearest bf16 value (returned as fp32).
@@ -201,33 +195,32 @@ __device__ __forceinline__ bf16x8 to_bf16x8(const float* x) {
     return as_bf16x8(u);
 }
 
-// Three-term bf16 split of eight fp32 values: x = hi + mid + lo to ~24 bits.
-__device__ __forceinline__ void split3x8(const float* x, bf16x8& hi, bf16x8& mid, bf16x8& lo) {
-    uint32_t h[4], m[4], l[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        h[j] = pack2bf_opaque(x[2 * j], x[2 * j + 1]);
-        const float r0 = __fsub_rn(x[2 * j], __uint_as_float(h[j] << 16));
-        const float r1 = __fsub_rn(x[2 * j + 1], __uint_as_float(h[j] & 0xffff0000u));
-        m[j] = pack2bf_opaque(r0, r1);
-        l[j] = pack2bf(__fsub_rn(r0, __uint_as_float(m[j] << 16)), __fsub_rn(r1, __uint_as_float(m[j] & 0xffff0000u)));
-    }
-    hi = as_bf16x8(u32x4{h[0], h[1], h[2], h[3]});
-    mid = as_bf16x8(u32x4{m[0], m[1], m[2], m[3]});
-    lo = as_bf16x8(u32x4{l[0], l[1], l[2], l[3]});
+// x minus the fp16 value in the low (sub_h_lo) or high (sub_h_hi) half of h, in one
+// v_fma_mix_f32 (x + (-h) * 1 with h widened to fp32, one rounding): exact when h is x rounded
+// to fp16, the residual of the split below.
+__device__ __forceinline__ float sub_h_lo(float x, uint32_t h) {
+    float r;
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+    return r;
+}
+__device__ __forceinline__ float sub_h_hi(float x, uint32_t h) {
+    float r;
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+    return r;
 }
 
-// Two-term bf16 split of eight fp32 values: x = hi + lo to ~16 bits (|x - hi - lo| <= 2^-17 |x|).
-__device__ __forceinline__ void split2x8(const float* x, bf16x8& hi, bf16x8& lo) {
+// Two-term fp16 split of eight fp32 values, x = hi + lo (both rounded to nearest even): 22
+// significant bits while lo stays normal (|x| >= 2^-3), an absolute 2^-25 below that; callers
+// scale x into [2^-3, 2^15].  Packed pairs in element order, the layout of an MFMA operand.
+__device__ __forceinline__ void split2h8(const float* x, u32x4& hi, u32x4& lo) {
     uint32_t h[4], l[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        h[j] = pack2bf_opaque(x[2 * j], x[2 * j + 1]);
-        l[j] = pack2bf(__fsub_rn(x[2 * j], __uint_as_float(h[j] << 16)),
-                       __fsub_rn(x[2 * j + 1], __uint_as_float(h[j] & 0xffff0000u)));
+        h[j] = pack2h(x[2 * j], x[2 * j + 1]);
+        l[j] = pack2h(sub_h_lo(x[2 * j], h[j]), sub_h_hi(x[2 * j + 1], h[j]));
     }
-    hi = as_bf16x8(u32x4{h[0], h[1], h[2], h[3]});
-    lo = as_bf16x8(u32x4{l[0], l[1], l[2], l[3]});
+    hi = u32x4{h[0], h[1], h[2], h[3]};
+    lo = u32x4{l[0], l[1], l[2], l[3]};
 }
 
 __device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
@@ -252,7 +245,6 @@ __device__ __forceinline__ u32x4 e4m3x8_to_h8(u32x2 b) {
 // e4m3, scale 2^-8): one instruction per pair.  Every finite code converts exactly (the fp16
 // grid holds all e4m3 values times 2^-8, subnormals included); htrc_selftest_e4m3 checks all
 // 256 codes against e4m3x8_to_h8 on the device.  The state never holds the NaN codes 0x7f / 0xff.
-typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t e4m3x2_to_h2_cvt(uint32_t w, bool hi) {
     return __builtin_bit_cast(uint32_t, hi ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 0x1p-8f, true)
                                            : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 0x1p-8f, false));

@@ -221,18 +221,15 @@ __global__ __launch_bounds__(256) void pack_k_kernel(const uint16_t* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------
-// stats: leaf statistics at the tile centres (h3/htrc_flat_triton.py:41-85, I8 store).
-// Workgroup = 64 tile centres (16 per wave) x a range of leaves of one head.  Per leaf:
-//   a^T = K_l mu^T                      bf16 MFMA, mu split into three bf16 terms (~24 bits)
+// stats: leaf statistics at the tile centres (h3/htrc_flat_triton.py:41-85).  A workgroup
+// holds a few leaves of one head and sweeps the head's centres, 16 per wave.  Per leaf:
+//   a^T = K_l mu^T                      fp16 MFMA, mu in two fp16 terms (22 bits)
 //   e = exp(a - max) per centre (lane%16 = centre), z = sum e
-//   g^T = K_l^T w^T, vb^T = V_l^T w^T   w = e / z in three bf16 terms for g (int8 codes), the
-//                                        first two of them for vb (stored as bf16)
-//                                        (g = scale * K_l^T w^T; K, V are exact in bf16)
-// The leaf's K and V rows are staged in LDS (XOR-swizzled 16-byte chunks) by gfx950 direct
-// global->LDS loads one leaf ahead; the QK operand is a plain 16-byte read, the PV-type
-// operands come from the same rows through transposing reads.  Each leaf's outputs are
-// stored during the next leaf, so the one vmcnt wait per leaf only covers loads and stores
-// issued a full leaf earlier.
+//   g^T = K_l^T w^T, vb^T = V_l^T w^T   w = e / z in two fp16 terms (g = scale * K_l^T w^T;
+//                                        K, V exact in fp16 after a power-of-two scale)
+// The leaves' K and V rows are staged in LDS as fp16 (XOR-swizzled 16-byte chunks); the QK
+// operand is a plain 16-byte read, the PV-type operands come from the same rows through
+// transposing reads.
 // ---------------------------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -333,32 +330,71 @@ __device__ __forceinline__ void settle(const i32x4 (&b)[4][2], const float (&s)[
     for (int rb = 0; rb < 4; ++rb) asm volatile("" : : "v"(b[rb][0]), "v"(b[rb][1]), "v"(s[rb]));
 }
 
-// Stage leaf rows [key0, key0 + LEAF) of K and V with NT threads: LDS chunk s = j*NT + tid
-// holds the 16-byte chunk (s % 16) ^ swz(row) of row (s / 16) % LEAF of K (first LEAF * 16
-// chunks) or V.  A wave's 64 chunks are 4 rows r0 .. r0 + 3 of one matrix, r0 = 4 w (mod 16)
-// for every j (NT / 16 is a multiple of 16), so with swz's period 16 every chunk of a thread
-// uses one per-lane offset voff = stage_voff() from a wave-uniform base (row r0).
-__device__ __forceinline__ uint32_t stage_voff() {
-    const int lane = threadIdx.x & 63, row = (4 * (threadIdx.x >> 6) + (lane >> 4)) & 15;
-    return (uint32_t)((lane >> 4) * 2 * D + 16 * ((lane & 15) ^ swz(row)));
+// Exponent t of the power of two that brings a leaf's largest magnitude m into [2^14, 2^15)
+// (m 2^-t; floored at -24, so rows of tiny values are raised by at most 2^24): every bf16 value
+// of the leaf then converts to fp16 exactly unless it is below m 2^-28, and none overflows.
+__device__ __forceinline__ int f16_exp(float m) {
+    const int e = (int)((__float_as_uint(m) >> 23) & 0xffu) - 127;
+    return e - 14 < -24 ? -24 : e - 14;
 }
 
-template <int LEAF, int NT>
-__device__ __forceinline__ void stage_leaf(const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-                                           int64_t key0, uint32_t lds0, uint32_t voff) {
-    constexpr int NJ = 32 * LEAF / NT;          // 16-byte chunks per thread (K and V)
-    constexpr int RPJ = NT / 16;                // rows per chunk step; the wave's are 4 w .. 4 w + 3
-    static_assert(NJ >= 1 && (32 * LEAF) % NT == 0 && NT % 256 == 0 && NT <= 16 * LEAF, "stage_leaf shape");
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint16_t* Kw = K + (key0 + 4 * w) * D;
-    const uint16_t* Vw = V + (key0 + 4 * w) * D;
-    const uint32_t ldsw = lds0 + (uint32_t)w * 1024;
+// The NL leaves [l0, l0 + NL) of K and V (rows of LEAF keys; leaves from lr on are padding and
+// not loaded) as fp16 in LDS, each leaf's K and V scaled by its own power of two 2^-t (f16_exp of
+// the matrix's largest |value| in the leaf); the exponents come back in tk, tv (wave-uniform).
+// Layout per leaf (LEAF_BYTES = 32 LEAF 16): LDS chunk s = 256 j + tid holds the 16-byte chunk
+// (s % 16) ^ swz(row) of row (s / 16) % LEAF of K (the first 16 LEAF chunks) or V.  Thread tid
+// loads those chunks itself (16-byte global loads), so its rows are r_j + 4 w + lane / 16 with
+// r_j = 16 j mod LEAF.  Two barriers: after the per-wave maxima, after the fp16 rows.
+template <int LEAF, int NL>
+__device__ __forceinline__ void stage_leaves_f16(const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+                                                 int64_t key0, int nreal, char* lds, float (*lmax)[2][4],
+                                                 int (&tk)[NL], int (&tv)[NL]) {
+    constexpr int NJ = 32 * LEAF / 256;         // 16-byte chunks per thread and leaf (K: j < NJ / 2)
+    constexpr int LEAF_BYTES = 32 * LEAF * 16;
+    typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int rw = 4 * w + (lane >> 4);
+    const int cg = (lane & 15) ^ swz(rw & 15);
+    u32x4 ch[NL][NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {              // step j: chunks j NT .., rows (j RPJ) % LEAF + 4 w ..
-        const bool isk = j * NT < 16 * LEAF;
-        const int rj = (j * RPJ) % LEAF;
-        dma16s((isk ? Kw : Vw) + rj * D, voff, ldsw + (uint32_t)(j * NT) * 16);
+    for (int li = 0; li < NL; ++li) {
+        us2 mk = {0, 0}, mv = {0, 0};
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const uint16_t* src = (j < NJ / 2 ? K : V) + (key0 + (int64_t)li * LEAF + (16 * j) % LEAF + rw) * D + 8 * cg;
+            ch[li][j] = li < nreal ? *(const u32x4*)src : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const us2 x = __builtin_bit_cast(us2, ch[li][j][e] & 0x7fff7fffu);    // |bf16| bits order as integers
+                if (j < NJ / 2) mk = __builtin_elementwise_max(mk, x); else mv = __builtin_elementwise_max(mv, x);
+            }
+        }
+        const float fk = wave_max(bf2f(mk.x > mk.y ? mk.x : mk.y)), fv = wave_max(bf2f(mv.x > mv.y ? mv.x : mv.y));
+        if (lane == 0) {
+            lmax[li][0][w] = fk;
+            lmax[li][1][w] = fv;
+        }
     }
+    __syncthreads();
+#pragma unroll
+    for (int li = 0; li < NL; ++li) {
+        tk[li] = __builtin_amdgcn_readfirstlane(
+            f16_exp(fmaxf(fmaxf(lmax[li][0][0], lmax[li][0][1]), fmaxf(lmax[li][0][2], lmax[li][0][3]))));
+        tv[li] = __builtin_amdgcn_readfirstlane(
+            f16_exp(fmaxf(fmaxf(lmax[li][1][0], lmax[li][1][1]), fmaxf(lmax[li][1][2], lmax[li][1][3]))));
+        if (li >= nreal) continue;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int t = j < NJ / 2 ? -tk[li] : -tv[li];
+            const u32x4 u = ch[li][j];
+            const u32x4 hv = {pack2h(ldexpf(bf2f(u.x & 0xffffu), t), ldexpf(bf2f(u.x >> 16), t)),
+                              pack2h(ldexpf(bf2f(u.y & 0xffffu), t), ldexpf(bf2f(u.y >> 16), t)),
+                              pack2h(ldexpf(bf2f(u.z & 0xffffu), t), ldexpf(bf2f(u.z >> 16), t)),
+                              pack2h(ldexpf(bf2f(u.w & 0xffffu), t), ldexpf(bf2f(u.w >> 16), t))};
+            *(u32x4*)(lds + li * LEAF_BYTES + (256 * j + tid) * 16) = hv;
+        }
+    }
+    __syncthreads();
 }
 
 // PV-type operand half from swizzled LDS rows: keys rbase + 4grp + j (j = 0..3) at column
@@ -423,14 +459,18 @@ __device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
 }
 
 // Leaf statistics at the tile centres (h3/htrc_flat_triton.py:41-85), per (centre, leaf): the
-// logits a = (mu . k) scale by bf16 MFMA with mu in three bf16 terms (fp32-accurate), lz = max +
-// log sum exp, w = softmax, g = (w K) scale with w in three terms, vb = w V with two.
+// logits a = (mu . k) scale, lz = max + log sum exp, w = softmax, g = (w K) scale, vb = w V, by
+// fp16 MFMA on fp32-accurate operands: K and V exact in fp16 (each leaf scaled by a power of
+// two, stage_leaves_f16), mu and w as two fp16 terms hi + lo (22 bits; mu of each centre scaled
+// by a power of two into [2^14, 2^15), w by 2^14, so lo keeps its bits: products exact, fp32
+// sums).  Every power of two is taken out again exactly where the reference's scale enters
+// (one rounding per value, as there).
 // STORE 0: g int8 with row scale sg, vb bf16 (the production I8 store, :73-80);
 // STORE 1: g and vb bf16, no scales (store="bf16", :82-83);
 // STORE 2: g and vb as e4m3 codes of x / s with row scales s = max(max|x| * fp32(1/448), 1e-30)
 // (sg, sv; store="fp8", :65-72); vb then holds bytes.
 // Leaf-stationary schedule: a workgroup of four waves stages the K / V of NL leaves
-// in LDS once (NL * LEAF = 128 keys, 64 KB), then each wave sweeps its share of the launch's
+// in LDS once (NL * LEAF = 128 keys, 64 KB of fp16), then each wave sweeps its share of the launch's
 // centres, 16 at a time, through those leaves: every leaf's K / V leaves HBM once, and the loop
 // has no barrier and no load wait for K / V.  The centres of the next group of 16 are loaded
 // into registers while the current group is computed.  Its state rows are stored as soon as
@@ -449,6 +489,7 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
     constexpr bool FP8 = STORE == 2, BF16 = STORE == 1;
     static_assert(NL * LEAF_BYTES <= 65536 && (NL == 1 || NL == 2 || NL == 4 || NL == 8), "stats_ls shape");
     __shared__ __align__(16) char lds[NL * LEAF_BYTES];
+    __shared__ float lmax[NL][2][4];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     // 1-D grid over (centre part, leaf group, head), centre part fastest: the workgroups of one
     // head run together on one XCD, whose L2 then serves the head's centres to all of them
@@ -462,13 +503,8 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
     const int ncg = (nt + 15) / 16, gpp = (ncg + ncs - 1) / ncs;
     const int jb = cs * gpp, je = min(ncg, jb + gpp);
     const float sl2 = __fmul_rn(scale, LOG2E);
-    {
-        const uint32_t voff = stage_voff();
-        for (int li = 0; l0 + li < lr; ++li)
-            stage_leaf<LEAF, 256>(k, v, kh + (int64_t)(l0 + li) * LEAF, lds_addr(lds) + li * LEAF_BYTES, voff);
-        wait_vmcnt<0>();
-        __syncthreads();
-    }
+    int tk[NL], tv[NL];
+    stage_leaves_f16<LEAF, NL>(k, v, kh + (int64_t)l0 * LEAF, lr - l0, lds, lmax, tk, tv);
     // this lane's 32 centre values (dims 32 ks + 8 grp + e of centre 16 j + col), fp32
     auto load_mu = [&](int j, f32x4 (&m)[8]) {
         const int t = min(16 * j + col, nt - 1);
@@ -479,19 +515,29 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
             m[2 * ks + 1] = *(const f32x4*)(src + 32 * ks + 4);
         }
     };
-    // mu of a group in three bf16 terms (~24 bits: the logits, and through the softmax g, carry no
+    // mu of a group scaled by 2^smu (per centre: its largest |value| into [2^14, 2^15), smu in
+    // [-64, 64]) and split into two fp16 terms (the logits, and through the softmax g, carry no
     // error beyond fp32 rounding)
-    bf16x8 mh[4], mm[4], ml[4];
+    u32x4 mh[4], ml[4];
+    int smu = 0;
     auto split_mu = [&](const f32x4 (&m)[8]) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fabsf(m[q][e]));
+        mx = grp_max(mx);
+        const int e = (int)((__float_as_uint(mx) >> 23) & 0xffu) - 127;
+        smu = 14 - e < -64 ? -64 : (14 - e > 64 ? 64 : 14 - e);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             float x[8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[e] = m[2 * ks][e];
-                x[4 + e] = m[2 * ks + 1][e];
+            for (int e2 = 0; e2 < 4; ++e2) {
+                x[e2] = ldexpf(m[2 * ks][e2], smu);
+                x[4 + e2] = ldexpf(m[2 * ks + 1][e2], smu);
             }
-            split3x8(x, mh[ks], mm[ks], ml[ks]);
+            split2h8(x, mh[ks], ml[ks]);
         }
     };
     f32x4 mnext[8];
@@ -540,6 +586,9 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
             }
             const char* Kr = lds + li * LEAF_BYTES;
             const char* Vr = Kr + 16 * LEAF * 16;
+            // a' = a 2^(smu - tk): the logits' power of two ca = tk - smu goes into their scale
+            const int ca = tk[li] - smu;
+            const float sca = ldexpf(scale, ca), sl2a = ldexpf(sl2, ca);
             f32x4 a[KB];
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
@@ -547,10 +596,9 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                 const int row = 16 * kb + col;
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
-                    const bf16x8 A = as_bf16x8(*(const u32x4*)(Kr + (row * 16 + ((4 * ks + grp) ^ swz(row))) * 16));
-                    a[kb] = mfma_bf16(A, ml[ks], a[kb]);          // smallest term first
-                    a[kb] = mfma_bf16(A, mm[ks], a[kb]);
-                    a[kb] = mfma_bf16(A, mh[ks], a[kb]);
+                    const u32x4 A = *(const u32x4*)(Kr + (row * 16 + ((4 * ks + grp) ^ swz(row))) * 16);
+                    a[kb] = mfma_f16(A, ml[ks], a[kb]);          // smaller term first
+                    a[kb] = mfma_f16(A, mh[ks], a[kb]);
                 }
             }
             float amx = -INFINITY;
@@ -559,17 +607,18 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
 #pragma unroll
                 for (int i = 0; i < 4; ++i) amx = fmaxf(amx, a[kb][i]);
             amx = grp_max(amx);
-            const float mx = __fmul_rn(amx, scale), mlog = __fmul_rn(amx, sl2);
+            const float mx = __fmul_rn(amx, sca), mlog = __fmul_rn(amx, sl2a);
             float z = 0.0f;
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    a[kb][i] = __builtin_amdgcn_exp2f(__fmaf_rn(a[kb][i], sl2, -mlog));
+                    a[kb][i] = __builtin_amdgcn_exp2f(__fmaf_rn(a[kb][i], sl2a, -mlog));
                     z = __fadd_rn(z, a[kb][i]);
                 }
             z = grp_sum(z);
-            const float rz = __fdiv_rn(1.0f, z);
+            // w 2^14 (in [0, 2^14]): the weights' low fp16 terms stay normal down to w = 2^-14
+            const float rz = __fmul_rn(__fdiv_rn(1.0f, z), 16384.0f);
             f32x4 gacc[8], vacc[8];
 #pragma unroll
             for (int db = 0; db < 8; ++db) gacc[db] = vacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -581,8 +630,8 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                     const int kb = 2 * kk + (e >> 2);
                     wv[e] = kb < KB ? __fmul_rn(a[kb < KB ? kb : 0][e & 3], rz) : 0.0f;
                 }
-                bf16x8 W0, W1, W2;
-                split3x8(wv, W0, W1, W2);
+                u32x4 W1, W0;
+                split2h8(wv, W1, W0);
 #pragma unroll
                 for (int db = 0; db < 8; ++db) {
                     const u32x2 zero = {0u, 0u};
@@ -590,21 +639,23 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                     const u32x2 k1 = (2 * kk + 1 < KB) ? tr_operand(Kr, 32 * kk + 16, db, lane) : zero;
                     const u32x2 v0 = tr_operand(Vr, 32 * kk, db, lane);
                     const u32x2 v1 = (2 * kk + 1 < KB) ? tr_operand(Vr, 32 * kk + 16, db, lane) : zero;
-                    const bf16x8 KA = as_bf16x8(k0, k1), VA = as_bf16x8(v0, v1);
-                    gacc[db] = mfma_bf16(KA, W2, gacc[db]);
-                    gacc[db] = mfma_bf16(KA, W1, gacc[db]);
-                    gacc[db] = mfma_bf16(KA, W0, gacc[db]);
-                    vacc[db] = mfma_bf16(VA, W1, vacc[db]);
-                    vacc[db] = mfma_bf16(VA, W0, vacc[db]);
+                    const u32x4 KA = {k0.x, k0.y, k1.x, k1.y}, VA = {v0.x, v0.y, v1.x, v1.y};
+                    gacc[db] = mfma_f16(KA, W0, gacc[db]);
+                    gacc[db] = mfma_f16(KA, W1, gacc[db]);
+                    vacc[db] = mfma_f16(VA, W0, vacc[db]);
+                    vacc[db] = mfma_f16(VA, W1, vacc[db]);
                 }
             }
             lzs[li] = __fadd_rn(mx, ln_ge1(z));   // z >= 1: its largest term is exp(0)
+            // gacc = g 2^(14 - tk) / scale, vacc = vb 2^(14 - tv)
+            const float scg = ldexpf(scale, tk[li] - 14);
+            const int ev = tv[li] - 14;
             float am = 0.0f;
 #pragma unroll
             for (int db = 0; db < 8; ++db)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) am = fmaxf(am, fabsf(gacc[db][i]));
-            am = __fmul_rn(grp_max(am), scale);   // max |g|
+            am = __fmul_rn(grp_max(am), scg);     // max |g|
             // one-byte rows (g8, FP8 g / vb): 4 x 4 block transpose of (c[g], c[4 + g]); row g then
             // holds dims 16g + 4c in x[2c] and 64 + 16g + 4c in x[2c + 1]: each store instruction
             // writes 64 contiguous bytes of a row per lane group
@@ -639,9 +690,10 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                 u32x2 pgb[8], pv[8];
 #pragma unroll
                 for (int db = 0; db < 8; ++db) {
-                    pgb[db] = u32x2{pack2bf(__fmul_rn(gacc[db][0], scale), __fmul_rn(gacc[db][1], scale)),
-                                    pack2bf(__fmul_rn(gacc[db][2], scale), __fmul_rn(gacc[db][3], scale))};
-                    pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
+                    pgb[db] = u32x2{pack2bf(__fmul_rn(gacc[db][0], scg), __fmul_rn(gacc[db][1], scg)),
+                                    pack2bf(__fmul_rn(gacc[db][2], scg), __fmul_rn(gacc[db][3], scg))};
+                    pv[db] = u32x2{pack2bf(ldexpf(vacc[db][0], ev), ldexpf(vacc[db][1], ev)),
+                                   pack2bf(ldexpf(vacc[db][2], ev), ldexpf(vacc[db][3], ev))};
                 }
                 store_rows16(pgb, (uint16_t*)g8);
                 store_rows16(pv, vb);
@@ -652,8 +704,8 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                 for (int db = 0; db < 8; ++db)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) av = fmaxf(av, fabsf(vacc[db][i]));
-                const float svv = fmaxf(__fmul_rn(grp_max(av), R448), 1e-30f);
-                const float cg = __fdiv_rn(scale, sgv), cv = __fdiv_rn(1.0f, svv);
+                const float svv = fmaxf(__fmul_rn(ldexpf(grp_max(av), ev), R448), 1e-30f);
+                const float cg = __fdiv_rn(scg, sgv), cv = ldexpf(__fdiv_rn(1.0f, svv), ev);
                 uint32_t pg[8], pvc[8];
 #pragma unroll
                 for (int db = 0; db < 8; ++db) {
@@ -666,13 +718,14 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                 svs[li] = svv;
             } else {
                 am = am < 1e-30f ? 1e-30f : am;
-                const float cq = __fdiv_rn(__fmul_rn(127.0f, scale), am);
+                const float cq = __fdiv_rn(__fmul_rn(127.0f, scg), am);
                 uint32_t pg[8];
                 u32x2 pv[8];
 #pragma unroll
                 for (int db = 0; db < 8; ++db) {
                     pg[db] = quant4(gacc[db], cq);
-                    pv[db] = u32x2{pack2bf(vacc[db][0], vacc[db][1]), pack2bf(vacc[db][2], vacc[db][3])};
+                    pv[db] = u32x2{pack2bf(ldexpf(vacc[db][0], ev), ldexpf(vacc[db][1], ev)),
+                                   pack2bf(ldexpf(vacc[db][2], ev), ldexpf(vacc[db][3], ev))};
                 }
                 store_bytes(pg, (uint8_t*)g8);
                 store_rows16(pv, vb);

@@ -125,7 +125,9 @@ def test_stats_close_to_oracle(device, leaf):
     vb = bf16.to_f32(bits(vbs[0, :, :nb].contiguous()))
     ovb = bf16.to_f32(ref["vb"])
     assert np.abs(vb - ovb).max() <= 2 ** -7 * np.abs(ovb).max()
-    assert (vb != ovb).mean() < 2e-2
+    record(f"stats_int8_flips[{leaf}]", {"g8": float((diff > 0).mean()), "vb": float((vb != ovb).mean())})
+    # the bf16 store's vb rounding (measured there 6.9e-4 of the values a step away), bar at twice
+    assert (vb != ovb).mean() < 1.4e-3
     # padded leaves: empty state
     if nbp > nb:
         assert np.all(_np(lz[0])[:, nb:] == -np.inf) and np.all(_np(g8[0])[:, nb:] == 0)
@@ -156,7 +158,7 @@ def test_stats_leaf_split_sizes(device, n):
     np.testing.assert_allclose(_np(sg[0, c])[:, :nb], osg, rtol=1e-5, atol=0)
     vb = bf16.to_f32(bits(vbs[0, c, :nb].contiguous()))
     ovbf = bf16.to_f32(ovb)
-    assert np.abs(vb - ovbf).max() <= 2 ** -7 * np.abs(ovbf).max() and (vb != ovbf).mean() < 2e-2
+    assert np.abs(vb - ovbf).max() <= 2 ** -7 * np.abs(ovbf).max() and (vb != ovbf).mean() < 1.4e-3
     if nbp > nb:
         assert bool((lz[0, :, nb:] == -math.inf).all()) and bool((g8[0, :, nb:] == 0).all())
 
@@ -639,9 +641,9 @@ def test_stats_fp8_close_to_oracle(device, leaf):
         assert np.all(np.abs(a - b) <= step * 1.001)
         rates[name] = float((gv != want).mean())
     record(f"stats_fp8_flips[{leaf}]", rates)
-    # measured (leaf 64 / 32): g 1.5e-5 / 0, vb 1.7e-4 / 1.9e-4 of the codes a step away; bars at
+    # measured (leaf 64 / 32): g 1.5e-5 / 0, vb 3.1e-5 / 3.4e-5 of the codes a step away; bars at
     # twice the largest
-    assert rates["g"] <= 3.1e-5 and rates["vb"] <= 3.8e-4, rates
+    assert rates["g"] <= 3.1e-5 and rates["vb"] <= 7e-5, rates
 
 
 @pytest.mark.parametrize("group,stride", [(1, 1), (2, 4)])
@@ -713,8 +715,8 @@ def test_stats_bf16_close_to_oracle(device, leaf):
     np.testing.assert_allclose(_np(lz[0])[:, :nb], ref["lz"], rtol=0, atol=2e-5 * (1 + np.abs(ref["lz"]).max()))
     rates = {}
     # largest |k| and |v| of each leaf: the moment sums' error bounds scale with them (the weights
-    # sum to one): g's weights carry three bf16 terms (2^-24 relative) and fp32 sums, |dg| <=
-    # 2^-18 scale max|k|; vb's two (2^-17), |dvb| <= 2^-17 max|v| (bars at twice these)
+    # sum to one): the weights carry two fp16 terms (2^-22 relative) and the sums are fp32 over
+    # the leaf's keys, |dg| <= 2^-18 scale max|k|, |dvb| <= 2^-17 max|v| (bars at twice these)
     kmax = np.abs(bf16.to_f32(bits(k[0])).reshape(nb, leaf, -1)).max(axis=(1, 2))
     vmax = np.abs(bf16.to_f32(bits(v[0])).reshape(nb, leaf, -1)).max(axis=(1, 2))
     for name, got, want, noise in (("g", g, ref["g16"], 2.0 ** -17 * kmax / math.sqrt(128)),
@@ -731,9 +733,9 @@ def test_stats_bf16_close_to_oracle(device, leaf):
         rates[name + "_err_vs_rowmax"] = float((np.abs(a - b) / np.maximum(np.abs(b).max(-1, keepdims=True),
                                                                            1e-300)).max())
     record(f"stats_bf16_flips[{leaf}]", rates)
-    # measured (leaf 64 / 32): g 7.6e-5 / 7.6e-5, vb 2.3e-3 / 2.4e-3 of the values a step away
-    # (vb's weights carry two bf16 terms); bars at twice the largest
-    assert rates["g"] <= 1.6e-4 and rates["vb"] <= 4.9e-3, rates
+    # measured (leaf 64 / 32): g 5.3e-5 / 7.6e-5, vb 6.9e-4 / 6.7e-4 of the values a step away;
+    # bars at twice the largest
+    assert rates["g"] <= 1.6e-4 and rates["vb"] <= 1.4e-3, rates
 
 
 @pytest.mark.parametrize("group,stride", [(1, 1), (2, 4)])
