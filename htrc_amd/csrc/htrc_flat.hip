@@ -560,46 +560,58 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
             lzs[li] = -INFINITY;
             svs[li] = 0.0f;
         }
-#pragma unroll
-        for (int li = 0; li < NL; ++li) {
-            const int l = l0 + li;
-            const int64_t s = th * nb_pad + l;
-            if (l >= lr) {                         // padded leaf: empty state, excluded everywhere
-                // (zero rows by the store instructions of a real leaf: the same count on both paths)
-                if (BF16) {
-                    *(u32x4*)((uint16_t*)g8 + s * D + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
-                    *(u32x4*)((uint16_t*)g8 + s * D + 32 + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
-                    *(u32x4*)((uint16_t*)g8 + s * D + 64 + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
-                    *(u32x4*)((uint16_t*)g8 + s * D + 96 + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
-                } else {
-                    *(u32x4*)(g8 + s * D + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
-                    *(u32x4*)(g8 + s * D + 64 + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
-                }
-                if (FP8) {
-                    *(u32x4*)((uint8_t*)vb + s * D + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
-                    *(u32x4*)((uint8_t*)vb + s * D + 64 + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
-                } else {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) *(u32x4*)(vb + s * D + 32 * q + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
-                }
-                continue;
+        // padded leaf: empty state, excluded everywhere (zero rows by the store instructions of a
+        // real leaf: the same count on both paths)
+        auto pad_leaf = [&](int li) {
+            const int64_t s = th * nb_pad + l0 + li;
+            if (BF16) {
+                *(u32x4*)((uint16_t*)g8 + s * D + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
+                *(u32x4*)((uint16_t*)g8 + s * D + 32 + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
+                *(u32x4*)((uint16_t*)g8 + s * D + 64 + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
+                *(u32x4*)((uint16_t*)g8 + s * D + 96 + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
+            } else {
+                *(u32x4*)(g8 + s * D + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
+                *(u32x4*)(g8 + s * D + 64 + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
             }
+            if (FP8) {
+                *(u32x4*)((uint8_t*)vb + s * D + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
+                *(u32x4*)((uint8_t*)vb + s * D + 64 + 16 * grp) = u32x4{0u, 0u, 0u, 0u};
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) *(u32x4*)(vb + s * D + 32 * q + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
+            }
+        };
+        auto real_leaf = [&](int li) {
+            const int64_t s = th * nb_pad + l0 + li;
             const char* Kr = lds + li * LEAF_BYTES;
             const char* Vr = Kr + 16 * LEAF * 16;
             // a' = a 2^(smu - tk): the logits' power of two ca = tk - smu goes into their scale
             const int ca = tk[li] - smu;
             const float sca = ldexpf(scale, ca), sl2a = ldexpf(sl2, ca);
+            // QK by k-steps ks: the K operands of the KB key blocks for step ks + 1 are read from
+            // LDS while step ks's products run, and each step's products alternate over the KB
+            // accumulators (lo terms, then hi terms) so no product waits on the one before it
+            auto qk_op = [&](int kb, int ks) {
+                const int row = 16 * kb + col;
+                return *(const u32x4*)(Kr + (row * 16 + ((4 * ks + grp) ^ swz(row))) * 16);
+            };
             f32x4 a[KB];
+            u32x4 aop[2][KB];
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
                 a[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-                const int row = 16 * kb + col;
+                aop[0][kb] = qk_op(kb, 0);
+            }
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const u32x4 A = *(const u32x4*)(Kr + (row * 16 + ((4 * ks + grp) ^ swz(row))) * 16);
-                    a[kb] = mfma_f16(A, ml[ks], a[kb]);          // smaller term first
-                    a[kb] = mfma_f16(A, mh[ks], a[kb]);
+            for (int ks = 0; ks < 4; ++ks) {
+                if (ks + 1 < 4) {
+#pragma unroll
+                    for (int kb = 0; kb < KB; ++kb) aop[(ks + 1) & 1][kb] = qk_op(kb, ks + 1);
                 }
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) a[kb] = mfma_f16(aop[ks & 1][kb], ml[ks], a[kb]);   // smaller term first
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) a[kb] = mfma_f16(aop[ks & 1][kb], mh[ks], a[kb]);
             }
             float amx = -INFINITY;
 #pragma unroll
@@ -622,6 +634,7 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
             f32x4 gacc[8], vacc[8];
 #pragma unroll
             for (int db = 0; db < 8; ++db) gacc[db] = vacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+            u32x4 W1[KK], W0[KK];
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) {
                 float wv[8];
@@ -630,21 +643,32 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                     const int kb = 2 * kk + (e >> 2);
                     wv[e] = kb < KB ? __fmul_rn(a[kb < KB ? kb : 0][e & 3], rz) : 0.0f;
                 }
-                u32x4 W1, W0;
-                split2h8(wv, W1, W0);
+                split2h8(wv, W1[kk], W0[kk]);
+            }
+            // PV over steps p = (kk, db): each step's K^T / V^T operands are read from LDS one
+            // step ahead of its four products
+            constexpr int NP = 8 * KK;
+            auto pv_op = [&](int p, u32x4& ka, u32x4& va) {
+                const int kk = p / 8, db = p % 8;
+                const u32x2 zero = {0u, 0u};
+                const u32x2 k0 = tr_operand(Kr, 32 * kk, db, lane);
+                const u32x2 k1 = (2 * kk + 1 < KB) ? tr_operand(Kr, 32 * kk + 16, db, lane) : zero;
+                const u32x2 v0 = tr_operand(Vr, 32 * kk, db, lane);
+                const u32x2 v1 = (2 * kk + 1 < KB) ? tr_operand(Vr, 32 * kk + 16, db, lane) : zero;
+                ka = u32x4{k0.x, k0.y, k1.x, k1.y};
+                va = u32x4{v0.x, v0.y, v1.x, v1.y};
+            };
+            u32x4 kop[2], vop[2];
+            pv_op(0, kop[0], vop[0]);
 #pragma unroll
-                for (int db = 0; db < 8; ++db) {
-                    const u32x2 zero = {0u, 0u};
-                    const u32x2 k0 = tr_operand(Kr, 32 * kk, db, lane);
-                    const u32x2 k1 = (2 * kk + 1 < KB) ? tr_operand(Kr, 32 * kk + 16, db, lane) : zero;
-                    const u32x2 v0 = tr_operand(Vr, 32 * kk, db, lane);
-                    const u32x2 v1 = (2 * kk + 1 < KB) ? tr_operand(Vr, 32 * kk + 16, db, lane) : zero;
-                    const u32x4 KA = {k0.x, k0.y, k1.x, k1.y}, VA = {v0.x, v0.y, v1.x, v1.y};
-                    gacc[db] = mfma_f16(KA, W0, gacc[db]);
-                    gacc[db] = mfma_f16(KA, W1, gacc[db]);
-                    vacc[db] = mfma_f16(VA, W0, vacc[db]);
-                    vacc[db] = mfma_f16(VA, W1, vacc[db]);
-                }
+            for (int p = 0; p < NP; ++p) {
+                const int kk = p / 8, db = p % 8;
+                const u32x4 KA = kop[p & 1], VA = vop[p & 1];
+                if (p + 1 < NP) pv_op(p + 1, kop[(p + 1) & 1], vop[(p + 1) & 1]);
+                gacc[db] = mfma_f16(KA, W0[kk], gacc[db]);
+                gacc[db] = mfma_f16(KA, W1[kk], gacc[db]);
+                vacc[db] = mfma_f16(VA, W0[kk], vacc[db]);
+                vacc[db] = mfma_f16(VA, W1[kk], vacc[db]);
             }
             lzs[li] = __fadd_rn(mx, ln_ge1(z));   // z >= 1: its largest term is exp(0)
             // gacc = g 2^(14 - tk) / scale, vacc = vb 2^(14 - tv)
@@ -730,6 +754,16 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                 store_bytes(pg, (uint8_t*)g8);
                 store_rows16(pv, vb);
                 sgs[li] = __fmul_rn(am, R127);
+            }
+        };
+        if (lr - l0 == NL) {                        // every leaf real: one straight-line body
+#pragma unroll
+            for (int li = 0; li < NL; ++li) real_leaf(li);
+        } else {
+#pragma unroll
+            for (int li = 0; li < NL; ++li) {
+                if (l0 + li >= lr) pad_leaf(li);
+                else real_leaf(li);
             }
         }
         // sg, lz (sv) of the NL leaves: NL contiguous floats per centre (the four lanes of a column
