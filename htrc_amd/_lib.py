@@ -15,7 +15,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIBPATH = HERE / "libhtrc_flat.so"
 HEADER = HERE.parent / "include" / "htrc_flat.h"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 _CTYPES = {"int64_t": ctypes.c_int64, "int": ctypes.c_int, "float": ctypes.c_float}
 

@@ -186,6 +186,13 @@ __device__ __forceinline__ uint32_t pack2h(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// fp32 rounded to TF32 (10 explicit mantissa bits), to nearest with ties away from zero, the
+// conversion of a TF32 tensor-core operand (cvt.rna.tf32.f32); infinities and NaN pass unchanged.
+__device__ __forceinline__ float tf32_rna(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u & 0x7f800000u) == 0x7f800000u ? x : __uint_as_float((u + 0x1000u) & 0xffffe000u);
+}
+
 // fp32 rounded to the nearest bf16 value (returned as fp32).
 __device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
 

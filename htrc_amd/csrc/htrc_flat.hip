@@ -476,7 +476,7 @@ __device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
 // into registers while the current group is computed.  Its state rows are stored as soon as
 // they are quantised; sg / lz (sv) of the NL leaves are NL contiguous floats per centre.
 // ncs: the centre groups of a head are dealt over ncs workgroups (small layers).
-template <int LEAF, int STORE, int NL>
+template <int LEAF, int STORE, int NL, bool TF32 = false>
 __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restrict__ mu, int64_t mu_stride,
                                                           int64_t c0, int nt, const uint16_t* __restrict__ k,
                                                           const uint16_t* __restrict__ v, int64_t nk, int nb,
@@ -486,7 +486,7 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
     constexpr int KB = LEAF / 16;
     constexpr int KK = (LEAF + 31) / 32;
     constexpr int LEAF_BYTES = 32 * LEAF * 16;
-    constexpr bool FP8 = STORE == 2, BF16 = STORE == 1;
+    constexpr bool FP8 = STORE == 2, BF16 = STORE == 1, F32 = STORE == 3, HAS_SG = STORE == 0 || STORE == 2;
     static_assert(NL * LEAF_BYTES <= 65536 && (NL == 1 || NL == 2 || NL == 4 || NL == 8), "stats_ls shape");
     __shared__ __align__(16) char lds[NL * LEAF_BYTES];
     __shared__ float lmax[NL][2][4];
@@ -533,9 +533,9 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
         for (int ks = 0; ks < 4; ++ks) {
             float x[8];
 #pragma unroll
-            for (int e2 = 0; e2 < 4; ++e2) {
-                x[e2] = ldexpf(m[2 * ks][e2], smu);
-                x[4 + e2] = ldexpf(m[2 * ks + 1][e2], smu);
+            for (int e2 = 0; e2 < 4; ++e2) {    // (TF32: the operand rounded first; lo is then 0)
+                x[e2] = ldexpf(TF32 ? tf32_rna(m[2 * ks][e2]) : m[2 * ks][e2], smu);
+                x[4 + e2] = ldexpf(TF32 ? tf32_rna(m[2 * ks + 1][e2]) : m[2 * ks + 1][e2], smu);
             }
             split2h8(x, mh[ks], ml[ks]);
         }
@@ -564,6 +564,14 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
         // real leaf: the same count on both paths)
         auto pad_leaf = [&](int li) {
             const int64_t s = th * nb_pad + l0 + li;
+            if (F32) {
+#pragma unroll
+                for (int db = 0; db < 8; ++db) {
+                    *(u32x4*)((float*)g8 + s * D + 16 * db + 4 * grp) = u32x4{0u, 0u, 0u, 0u};
+                    *(u32x4*)((float*)vb + s * D + 16 * db + 4 * grp) = u32x4{0u, 0u, 0u, 0u};
+                }
+                return;
+            }
             if (BF16) {
                 *(u32x4*)((uint16_t*)g8 + s * D + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
                 *(u32x4*)((uint16_t*)g8 + s * D + 32 + 8 * grp) = u32x4{0u, 0u, 0u, 0u};
@@ -609,7 +617,8 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                     for (int kb = 0; kb < KB; ++kb) aop[(ks + 1) & 1][kb] = qk_op(kb, ks + 1);
                 }
 #pragma unroll
-                for (int kb = 0; kb < KB; ++kb) a[kb] = mfma_f16(aop[ks & 1][kb], ml[ks], a[kb]);   // smaller term first
+                for (int kb = 0; kb < KB; ++kb)                  // smaller term first
+                    if constexpr (!TF32) a[kb] = mfma_f16(aop[ks & 1][kb], ml[ks], a[kb]);
 #pragma unroll
                 for (int kb = 0; kb < KB; ++kb) a[kb] = mfma_f16(aop[ks & 1][kb], mh[ks], a[kb]);
             }
@@ -642,6 +651,7 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                 for (int e = 0; e < 8; ++e) {
                     const int kb = 2 * kk + (e >> 2);
                     wv[e] = kb < KB ? __fmul_rn(a[kb < KB ? kb : 0][e & 3], rz) : 0.0f;
+                    if constexpr (TF32) wv[e] = tf32_rna(wv[e]);
                 }
                 split2h8(wv, W1[kk], W0[kk]);
             }
@@ -665,9 +675,9 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                 const int kk = p / 8, db = p % 8;
                 const u32x4 KA = kop[p & 1], VA = vop[p & 1];
                 if (p + 1 < NP) pv_op(p + 1, kop[(p + 1) & 1], vop[(p + 1) & 1]);
-                gacc[db] = mfma_f16(KA, W0[kk], gacc[db]);
+                if constexpr (!TF32) gacc[db] = mfma_f16(KA, W0[kk], gacc[db]);
                 gacc[db] = mfma_f16(KA, W1[kk], gacc[db]);
-                vacc[db] = mfma_f16(VA, W0[kk], vacc[db]);
+                if constexpr (!TF32) vacc[db] = mfma_f16(VA, W0[kk], vacc[db]);
                 vacc[db] = mfma_f16(VA, W1[kk], vacc[db]);
             }
             lzs[li] = __fadd_rn(mx, ln_ge1(z));   // z >= 1: its largest term is exp(0)
@@ -710,7 +720,17 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                         *(u32x4*)(vr + 32 * (2 * hf + m2)) = u32x4{va[m2].x, va[m2].y, vc[m2].x, vc[m2].y};
                 }
             };
-            if constexpr (BF16) {
+            if constexpr (F32) {               // fp32 rows: dims 16 db + 4 grp .. of centre col
+#pragma unroll
+                for (int db = 0; db < 8; ++db) {
+                    *(f32x4*)((float*)g8 + s * D + 16 * db + 4 * grp) =
+                        f32x4{__fmul_rn(gacc[db][0], scg), __fmul_rn(gacc[db][1], scg), __fmul_rn(gacc[db][2], scg),
+                              __fmul_rn(gacc[db][3], scg)};
+                    *(f32x4*)((float*)vb + s * D + 16 * db + 4 * grp) =
+                        f32x4{ldexpf(vacc[db][0], ev), ldexpf(vacc[db][1], ev), ldexpf(vacc[db][2], ev),
+                              ldexpf(vacc[db][3], ev)};
+                }
+            } else if constexpr (BF16) {
                 u32x2 pgb[8], pv[8];
 #pragma unroll
                 for (int db = 0; db < 8; ++db) {
@@ -780,7 +800,7 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                     for (int q = 0; q < NL; q += 4) *(f32x4*)(dst + s + q) = f32x4{x[q], x[q + 1], x[q + 2], x[q + 3]};
                 }
             };
-            if (!BF16) put(sg, sgs);
+            if (HAS_SG) put(sg, sgs);
             put(lz, lzs);
             if (FP8) put(sv, svs);
         }
@@ -1545,6 +1565,258 @@ __global__ __launch_bounds__(256) void tile16_kernel(
     }
 #pragma unroll
     for (int db = 0; db < 8; ++db) *(f32x4*)(pacc + base * D + 16 * db + 4 * grp) = st.o[db];
+}
+
+// ---------------------------------------------------------------------------------------------
+// fp32 dots (dot other than "bf16": h3/htrc_flat_triton.py:138-141, 159-161, 171-174, 184-185,
+// 245-247 with DOT = 0): the state g, vb in fp32 (store="fp32") or bf16 (store="bf16", widened
+// exactly), q and q - mu in fp32, k and v the bf16 keys / values widened exactly; every product
+// by the fp32 MFMA (v_mfma_f32_16x16x4_f32) with fp32 sums.  TF32 (precision="tf32", the
+// reference's PREC "tf32"): every operand is first rounded to TF32 (tf32_rna), whose products
+// fp32 holds exactly.
+// 16x16x4 operands: lane l supplies A[m = l%16][k = l/16] and B[k = l/16][n = l%16].  In a QK
+// product, step s (0..31) lets k-index l/16 stand for dim 32 (l/16) + s, so each lane holds 32
+// consecutive dims of its key row (A) and of its query row (B).  In a PV product over 16 keys,
+// step s lets it stand for key 4 (l/16) + s, which is item s of the lane's score tile C[4 (l/16)
+// + i][l%16] (no shuffle), and row m of the O^T block db stands for dim 8 m + db, so the A
+// operand is 8 consecutive dims of a value row and the lane's O^T items are dims 32 (l/16) ..
+// + 31 of its query row.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// N consecutive values (bf16 when BF, else fp32) from p, as fp32; TF32-rounded when TF32 (a
+// no-op on bf16 values, which TF32 holds).
+template <int N, bool BF, bool TF32>
+__device__ __forceinline__ void load_f32(const void* p, float (&x)[N]) {
+    static_assert(N % 8 == 0, "load_f32: whole 16-byte pieces");
+    if constexpr (BF) {
+#pragma unroll
+        for (int q = 0; q < N / 8; ++q) {
+            const u32x4 u = ((const u32x4*)p)[q];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[8 * q + 2 * e] = bf2f(u[e] & 0xffffu);
+                x[8 * q + 2 * e + 1] = bf2f(u[e] >> 16);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < N / 4; ++q) {
+            const f32x4 f = ((const f32x4*)p)[q];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[4 * q + e] = TF32 ? tf32_rna(f[e]) : f[e];
+        }
+    }
+}
+
+// S^T tile of 16 keys x 16 rows: item i of lane l = sum over dims of key (4 (l/16) + i)'s A row
+// and row l%16's B row, from the 32 dims each lane holds of both.
+__device__ __forceinline__ f32x4 dot_tile_f32(const float (&a)[32], const float (&b)[32]) {
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 32; ++s) c = mfma_f32(a[s], b[s], c);
+    return c;
+}
+
+struct RowF32 {        // running softmax state of one row (h3/htrc_flat_triton.py:142-157)
+    float m;           // running max (natural log units; the same in the four lanes of a row)
+    float l;           // this lane's share of the running sum
+    f32x4 o[8];        // O^T: item i of block db is dim 8 (4 grp + i) + db
+};
+
+// One block of 16 keys: scores sc[i] of keys 4 grp + i (masked: -inf), value rows va[s] = dims
+// 8 col .. + 7 of key 4 grp + s.  The reference's update: m_new = max(m, rowmax), m_s = m_new, or
+// 0 when -inf, p = exp(sc - m_s), alpha = exp(m - m_s), l = l alpha + sum p, O = O alpha + P V.
+template <bool TF32>
+__device__ __forceinline__ void f32_update(RowF32& st, const float (&sc)[4], const float (&va)[4][8]) {
+    const float bm = grp_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+    const float mn = fmaxf(st.m, bm);
+    const float ms = mn == -INFINITY ? 0.0f : mn;
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = __expf(__fsub_rn(sc[i], ms));
+    const float alpha = __expf(__fsub_rn(st.m, ms));
+    st.l = __fadd_rn(__fmul_rn(st.l, alpha), __fadd_rn(__fadd_rn(p[0], p[1]), __fadd_rn(p[2], p[3])));
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st.o[db][i] = __fmul_rn(st.o[db][i], alpha);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const float ps = TF32 ? tf32_rna(p[s]) : p[s];
+#pragma unroll
+        for (int db = 0; db < 8; ++db) st.o[db] = mfma_f32(va[s][db], ps, st.o[db]);
+    }
+    st.m = mn;
+}
+
+// Far + near field of one (tile, split) with fp32 dots (h3/htrc_flat_triton.py:88-211, DOT = 0):
+// far leaves [sp lps, + lps) not excluded, score = (q - mu) . g + lz; near tokens [sp eps, + eps)
+// of the tile group's idx leaves, score = (q . k) scale.  One wave per 16 rows; every wave reads
+// its key rows itself (the tile's waves share them in L2).  ns == 1 (pacc null): normalised rows
+// and logz = m + log l; else the partial (m, l, O) for merge_kernel.
+template <bool QBF, bool SB, bool TF32>
+__global__ __launch_bounds__(256) void tile_f32_kernel(
+    const void* __restrict__ q, const float* __restrict__ mu, int mu_stride, const void* __restrict__ g,
+    const float* __restrict__ lz, const void* __restrict__ vb, const int8_t* __restrict__ excl,
+    const int32_t* __restrict__ idx, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t nq,
+    int nt, int tile, int group, int g0, int ng, const int32_t* __restrict__ perm, int64_t nk, int leaf, int nb,
+    int nb_pad, int kx, int lps, int eps, float scale, float* __restrict__ pm, float* __restrict__ pl,
+    float* __restrict__ pacc, float* __restrict__ out, float* __restrict__ logz) {
+    constexpr int QB = QBF ? 2 : 4, SBB = SB ? 2 : 4;          // bytes per value
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int tb = g0 * group, ntw = gridDim.x;
+    const int t = tb + blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
+    const int64_t tw = (int64_t)h * ntw + blockIdx.x;         // partial row of the tile
+    const int64_t gs = (int64_t)h * ng + (t / group - g0);    // state / routing row: the tile's group
+    const int r = 16 * w + col;                                // blockDim = 4 * tile: one wave per 16 rows
+    const int64_t qi = (int64_t)t * tile + r;                  // pad rows repeat the last query
+    const int64_t src = perm_row(perm, h, nq, qi < nq ? qi : nq - 1);
+    float qx[32], dq[32];
+    load_f32<32, QBF, false>((const char*)q + (((int64_t)h * nq + src) * D + 32 * grp) * QB, qx);
+    {
+        float mx[32];
+        load_f32<32, false, false>(mu + ((int64_t)h * mu_stride + t / group) * D + 32 * grp, mx);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            dq[e] = __fsub_rn(qx[e], mx[e]);
+            if constexpr (TF32) {
+                dq[e] = tf32_rna(dq[e]);
+                qx[e] = tf32_rna(qx[e]);
+            }
+        }
+    }
+    RowF32 st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) st.o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // ---- far field: 16 leaves per block
+    const int lo = sp * lps, hi = min(nb, lo + lps);
+    const int64_t srow = gs * nb_pad;
+    const char* gb = (const char*)g;
+    const char* vbb = (const char*)vb;
+    for (int c0 = lo; c0 < hi; c0 += 16) {
+        float ga[32];
+        load_f32<32, SB, TF32>(gb + ((srow + min(c0 + col, hi - 1)) * D + 32 * grp) * SBB, ga);
+        const f32x4 s4 = dot_tile_f32(ga, dq);
+        float sc[4], va[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = c0 + 4 * grp + i, cc = min(c, hi - 1);
+            sc[i] = (c < hi && excl[srow + cc] == 0) ? __fadd_rn(s4[i], lz[srow + cc]) : -INFINITY;
+            load_f32<8, SB, TF32>(vbb + ((srow + cc) * D + 8 * col) * SBB, va[i]);
+        }
+        f32_update<TF32>(st, sc, va);
+    }
+    // ---- near field: 16 tokens per block
+    const int e_n = kx * leaf;
+    const int e_lo = sp * eps, e_hi = min(e_n, e_lo + eps);
+    const int64_t kh = (int64_t)h * nk;
+    const int32_t* ix = idx + gs * (int64_t)(kx > 0 ? kx : 1);
+    for (int e0 = e_lo; e0 < e_hi; e0 += 16) {
+        const int ja = min(e0 + col, e_hi - 1);
+        float ka[32];
+        load_f32<32, true, false>(k + (kh + (int64_t)ix[ja / leaf] * leaf + ja % leaf) * D + 32 * grp, ka);
+        const f32x4 s4 = dot_tile_f32(ka, qx);
+        float sc[4], va[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = e0 + 4 * grp + i, jj = min(j, e_hi - 1);
+            sc[i] = j < e_hi ? __fmul_rn(s4[i], scale) : -INFINITY;
+            load_f32<8, true, false>(v + (kh + (int64_t)ix[jj / leaf] * leaf + jj % leaf) * D + 8 * col, va[i]);
+        }
+        f32_update<TF32>(st, sc, va);
+    }
+    const float ltot = grp_sum(st.l);
+    // the lane's O^T items in dim order: dims 32 grp + 8 i + db are st.o[db][i]
+    auto dims4 = [&](int i, int hf, float den) {
+        return f32x4{__fdiv_rn(st.o[4 * hf][i], den), __fdiv_rn(st.o[4 * hf + 1][i], den),
+                     __fdiv_rn(st.o[4 * hf + 2][i], den), __fdiv_rn(st.o[4 * hf + 3][i], den)};
+    };
+    if (pacc == nullptr) {                                     // single split: normalise in place
+        if (qi >= nq) return;
+        const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
+        const float ms = st.m == -INFINITY ? 0.0f : st.m;
+        const float den = ltot < 1e-30f ? 1e-30f : ltot;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) *(f32x4*)(out + orow * D + 32 * grp + 8 * i + 4 * hf) = dims4(i, hf, den);
+        if (grp == 0) logz[orow] = __fadd_rn(ms, __logf(ltot));
+        return;
+    }
+    const int64_t base = (tw * ns + sp) * tile + r;
+    if (grp == 0) {
+        pm[base] = st.m;
+        pl[base] = ltot;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) *(f32x4*)(pacc + base * D + 32 * grp + 8 * i + 4 * hf) = dims4(i, hf, 1.0f);
+}
+
+// SEL[g, l] = max over every stride-th row of the group's tiles of (q - mu_g) . g_l, + lz_l, with
+// fp32 dots (h3/htrc_flat_triton.py:214-254, DOT = 0).  Workgroup = one group x 256 leaves; each
+// wave holds the A operands of its 64 leaves (four blocks of 16) and sweeps the group's rows 16
+// at a time (rows past the last query repeat it, tiles past the last repeat it: as the
+// reference pads them, which leaves every maximum unchanged).
+template <bool QBF, bool SB, bool TF32>
+__global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict__ q, const float* __restrict__ mu,
+                                                         int mu_stride, const void* __restrict__ g,
+                                                         const float* __restrict__ lz, int64_t nq, int nt, int tile,
+                                                         int stride, int group, int g0, int ng,
+                                                         const int32_t* __restrict__ perm, int nb, int nb_pad,
+                                                         float* __restrict__ sel) {
+    constexpr int QB = QBF ? 2 : 4, SBB = SB ? 2 : 4;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int gi = blockIdx.y, h = blockIdx.z, gg = g0 + gi;
+    const int l0 = blockIdx.x * 256 + 64 * w;                 // this wave's 64 leaves
+    if (l0 >= nb) return;                                      // (no barriers in this kernel)
+    const int64_t srow = ((int64_t)h * ng + gi) * nb_pad;
+    float ga[4][32];
+#pragma unroll
+    for (int lb = 0; lb < 4; ++lb)
+        load_f32<32, SB, TF32>((const char*)g + ((srow + min(l0 + 16 * lb + col, nb - 1)) * D + 32 * grp) * SBB,
+                               ga[lb]);
+    float mx[32];
+    load_f32<32, false, false>(mu + ((int64_t)h * mu_stride + gg) * D + 32 * grp, mx);
+    float best[4][4];
+#pragma unroll
+    for (int lb = 0; lb < 4; ++lb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) best[lb][i] = -INFINITY;
+    const int rpt = tile / stride, nsel = group * rpt;
+    for (int j0 = 0; j0 < nsel; j0 += 16) {
+        const int j = min(j0 + col, nsel - 1);
+        const int tt = min(gg * group + j / rpt, nt - 1);
+        const int64_t qi = min((int64_t)tt * tile + (j % rpt) * stride, nq - 1);
+        float dq[32];
+        load_f32<32, QBF, false>((const char*)q + (((int64_t)h * nq + perm_row(perm, h, nq, qi)) * D + 32 * grp) * QB,
+                                 dq);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            dq[e] = __fsub_rn(dq[e], mx[e]);
+            if constexpr (TF32) dq[e] = tf32_rna(dq[e]);
+        }
+#pragma unroll
+        for (int lb = 0; lb < 4; ++lb) {
+            const f32x4 s4 = dot_tile_f32(ga[lb], dq);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) best[lb][i] = fmaxf(best[lb][i], s4[i]);
+        }
+    }
+#pragma unroll
+    for (int lb = 0; lb < 4; ++lb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float m = col_max(best[lb][i]);          // over the 16 rows of the lane group
+            const int c = l0 + 16 * lb + 4 * grp + i;
+            if (col == 0 && c < nb) sel[srow + c] = __fadd_rn(m, lz[srow + c]);
+        }
 }
 
 // merge: (h3/htrc_flat_triton.py:257-273) + logZ = mm + log(den).  One workgroup (4 * tile
@@ -2937,26 +3209,29 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
 // partial for more (:381-388); both end as one softmax over far, near and tail, which is what
 // the log-sum-exp merge here computes.  Four lanes per query row (32 dims each).
 // ---------------------------------------------------------------------------------------------
-template <bool IN_BF16>
+// MODE 0: the dot="bf16" paths (up to 16 keys in bf16, more in fp32); 1: fp32 operands; 2: TF32
+// operands (the fp32-dot path, h3/htrc_flat_triton.py:198-207 with DOT = 0).
+template <bool IN_BF16, int MODE = 0>
 __global__ __launch_bounds__(256) void tail_kernel(const void* __restrict__ q, const float* __restrict__ tk,
                                                    const float* __restrict__ tv, int64_t nq, int ntail,
                                                    float scale, float* __restrict__ out, float* __restrict__ logz) {
     const int t = blockIdx.x, h = blockIdx.y, r = threadIdx.x >> 2, qd = threadIdx.x & 3;
     const int64_t qi = (int64_t)t * TILE + r;
     if (qi >= nq) return;                         // whole 4-lane groups leave together
-    const bool bfr = ntail <= 16;                 // the in-kernel path of the reference works in bf16
+    const bool bfr = MODE == 0 && ntail <= 16;    // the in-kernel path of the reference works in bf16
+    auto op = [&](float x) { return bfr ? bf16_round(x) : (MODE == 2 ? tf32_rna(x) : x); };
     const int64_t row = (int64_t)h * nq + qi;
     float qv[32];
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
         const float x = IN_BF16 ? bf2f(((const uint16_t*)q)[row * D + 32 * qd + e]) : ((const float*)q)[row * D + 32 * qd + e];
-        qv[e] = bfr ? bf16_round(x) : x;
+        qv[e] = op(x);
     }
     auto score = [&](int j) {                     // (q . k_j) * scale, the row's four lanes together
         const float* kj = tk + ((int64_t)h * ntail + j) * D + 32 * qd;
         float sdot = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) sdot = fmaf(qv[e], bfr ? bf16_round(kj[e]) : kj[e], sdot);
+        for (int e = 0; e < 32; ++e) sdot = fmaf(qv[e], op(kj[e]), sdot);
         sdot = __fadd_rn(sdot, __shfl_xor(sdot, 1, 4));
         sdot = __fadd_rn(sdot, __shfl_xor(sdot, 2, 4));
         return __fmul_rn(sdot, scale);
@@ -2971,9 +3246,9 @@ __global__ __launch_bounds__(256) void tail_kernel(const void* __restrict__ q, c
         const float* vj = tv + ((int64_t)h * ntail + j) * D + 32 * qd;
         const float p = expf(__fsub_rn(score(j), m));
         l = __fadd_rn(l, p);
-        const float pv = bfr ? bf16_round(p) : p;
+        const float pv = op(p);
 #pragma unroll
-        for (int e = 0; e < 32; ++e) acc[e] = fmaf(pv, bfr ? bf16_round(vj[e]) : vj[e], acc[e]);
+        for (int e = 0; e < 32; ++e) acc[e] = fmaf(pv, op(vj[e]), acc[e]);
     }
     const float lse = __fadd_rn(m, logf(l));
     const float lz0 = logz[row];
@@ -3311,9 +3586,9 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 // leaves get -inf.  (sqrtf, which HIP keeps correctly rounded by default: the header's __fsqrt_rn
 // is the native approximation unless the OCML rounded operations are enabled.)
 // ---------------------------------------------------------------------------------------------
-template <bool IN_BF16>
+template <bool IN_BF16, bool G_F32 = false>
 __global__ __launch_bounds__(256) void bound_select_kernel(const void* __restrict__ qin, const float* __restrict__ mu,
-                                                           const uint16_t* __restrict__ g, const float* __restrict__ lz,
+                                                           const void* __restrict__ g, const float* __restrict__ lz,
                                                            int64_t nq, int nt, int tile, int group, int ng_all, int g0,
                                                            int gn, int nb, int nb_pad, const int32_t* __restrict__ perm,
                                                            float* __restrict__ sel) {
@@ -3349,10 +3624,10 @@ __global__ __launch_bounds__(256) void bound_select_kernel(const void* __restric
     for (int l = tid; l < nb_pad; l += 256) {
         float val = -INFINITY;
         if (l < nb) {
-            const uint16_t* gr = g + (gs * nb_pad + l) * D;
+            const int64_t gr = (gs * nb_pad + l) * D;
             float s = 0.0f;
             for (int c = 0; c < D; ++c) {
-                const float x = bf2f(gr[c]);
+                const float x = G_F32 ? ((const float*)g)[gr + c] : bf2f(((const uint16_t*)g)[gr + c]);
                 s = __fadd_rn(s, __fmul_rn(x, x));
             }
             val = __fadd_rn(lz[gs * nb_pad + l], __fmul_rn(r, sqrtf(s)));
@@ -3555,7 +3830,7 @@ static int device_cus() {
 
 // Shared checks and launch of the three leaf-statistics stores (STORE 0 int8, 1 bf16, 2 fp8).
 extern "C++" {
-template <int STORE>
+template <int STORE, bool TF32 = false>
 static int leaf_stats_launch(const char* who, const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads,
                              int64_t nt, int64_t c0, int64_t cn, int64_t nk, int leaf, int d, float scale, void* g,
                              float* sg, void* vb, float* sv, float* lz, void* stream) {
@@ -3564,14 +3839,15 @@ static int leaf_stats_launch(const char* who, const float* mu, const uint16_t* k
         snprintf(msg, sizeof msg, "%s: %s", who, what);
         return fail(HTRC_ERR_ARG, msg);
     };
-    if (!(mu && k && v && g && vb && lz && (STORE == 1 || sg) && (STORE != 2 || sv))) return bad("null pointer");
+    constexpr bool HAS_SG = STORE == 0 || STORE == 2;
+    if (!(mu && k && v && g && vb && lz && (!HAS_SG || sg) && (STORE != 2 || sv))) return bad("null pointer");
     if (d != D) return bad("head dim must be 128");
     if (!(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128)) return bad("leaf must be 16/32/64/128");
     if (!(nk > 0 && nk % leaf == 0)) return bad("key count must be a multiple of the leaf size");
     if (!(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff)) return bad("bad heads / centres");
     if (!(c0 >= 0 && cn > 0 && c0 + cn <= nt)) return bad("centre window [c0, c0 + cn) must lie in [0, nt)");
     if (!(aligned(k, 16) && aligned(v, 16) && aligned(g, 16) && aligned(vb, 16) && aligned(lz, 16) &&
-          (STORE == 1 || aligned(sg, 16)) && (STORE != 2 || aligned(sv, 16))))
+          (!HAS_SG || aligned(sg, 16)) && (STORE != 2 || aligned(sv, 16))))
         return bad("misaligned buffer");
     const int64_t nb = nk / leaf;
     const int nbp = htrc_nb_pad(nb);
@@ -3589,7 +3865,7 @@ static int leaf_stats_launch(const char* who, const float* mu, const uint16_t* k
     hipStream_t s = (hipStream_t)stream;
 #define STATS_CASE(L)                                                                                            \
     case L:                                                                                                      \
-        hipLaunchKernelGGL((stats_ls_kernel<L, STORE, 65536 / (512 * L)>), grid, dim3(256), 0, s, mu, nt, c0,      \
+        hipLaunchKernelGGL((stats_ls_kernel<L, STORE, 65536 / (512 * L), TF32>), grid, dim3(256), 0, s, mu, nt, c0, \
                            (int)cn, k, v, nk, (int)nb, nbp, (int)ncs, scale, (int8_t*)g, sg, (uint16_t*)vb, sv, lz); \
         break;
     switch (leaf) {
@@ -3622,6 +3898,21 @@ int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, 
                          void* stream) {
     return leaf_stats_launch<1>("htrc_leaf_stats_bf16", mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr,
                                 vb, nullptr, lz, stream);
+}
+
+int htrc_leaf_stats_f32(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
+                        int64_t cn, int64_t nk, int leaf, int d, float scale, int state_bf16, int tf32, void* g,
+                        void* vb, float* lz, void* stream) {
+    const char* who = "htrc_leaf_stats_f32";
+    if (state_bf16)
+        return tf32 ? leaf_stats_launch<1, true>(who, mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb,
+                                                 nullptr, lz, stream)
+                    : leaf_stats_launch<1>(who, mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb, nullptr,
+                                           lz, stream);
+    return tf32 ? leaf_stats_launch<3, true>(who, mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb,
+                                             nullptr, lz, stream)
+                : leaf_stats_launch<3>(who, mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb, nullptr,
+                                       lz, stream);
 }
 
 // Window of tile groups [g0, g0 + gn) of a head of nt tiles in groups of `group`: sets ng (all
@@ -3780,6 +4071,75 @@ int htrc_tile(const int8_t* q8, const float* sq, const int8_t* dq8, const float*
     return tile_launch<0>("htrc_tile", q8, sq, dq8, sdq, g8, sg, lz, vb, nullptr, excl, idx, k8, ks, v, heads, nq, nk,
                           leaf, d, kx, tile, group, g0, gn, perm, splits, bn, scale, pm, pl, pacc, out, logz, stream);
 }
+
+// The three template flags of the fp32-dot kernels: q in bf16, state in bf16, TF32 operands.
+#define F32_DISPATCH(KERNEL, GRID, BLOCK, ...)                                                                      \
+    do {                                                                                                           \
+        const int code_ = (q_is_bf16 ? 4 : 0) | (state_bf16 ? 2 : 0) | (tf32 ? 1 : 0);                             \
+        switch (code_) {                                                                                           \
+            case 0: hipLaunchKernelGGL((KERNEL<false, false, false>), GRID, BLOCK, 0, s, __VA_ARGS__); break;      \
+            case 1: hipLaunchKernelGGL((KERNEL<false, false, true>), GRID, BLOCK, 0, s, __VA_ARGS__); break;       \
+            case 2: hipLaunchKernelGGL((KERNEL<false, true, false>), GRID, BLOCK, 0, s, __VA_ARGS__); break;       \
+            case 3: hipLaunchKernelGGL((KERNEL<false, true, true>), GRID, BLOCK, 0, s, __VA_ARGS__); break;        \
+            case 4: hipLaunchKernelGGL((KERNEL<true, false, false>), GRID, BLOCK, 0, s, __VA_ARGS__); break;       \
+            case 5: hipLaunchKernelGGL((KERNEL<true, false, true>), GRID, BLOCK, 0, s, __VA_ARGS__); break;        \
+            case 6: hipLaunchKernelGGL((KERNEL<true, true, false>), GRID, BLOCK, 0, s, __VA_ARGS__); break;        \
+            default: hipLaunchKernelGGL((KERNEL<true, true, true>), GRID, BLOCK, 0, s, __VA_ARGS__); break;        \
+        }                                                                                                          \
+    } while (0)
+
+int htrc_select_f32(const void* q, int q_is_bf16, const float* mu, const void* g, int state_bf16, const float* lz,
+                    int64_t heads, int64_t nq, int64_t nb, int stride, int tile, int group, int64_t g0, int64_t gn,
+                    const int32_t* perm, int tf32, int d, float* sel, void* stream) {
+    REQUIRE(q && mu && g && lz && sel, "htrc_select_f32: null pointer");
+    REQUIRE(d == D, "htrc_select_f32: head dim must be 128");
+    REQUIRE(tile == 32 || tile == 64, "htrc_select_f32: tile must be 32 or 64 rows");
+    REQUIRE(stride >= 1 && tile % stride == 0, "htrc_select_f32: stride must divide the tile");
+    REQUIRE(heads > 0 && heads <= 65535 && nq > 0 && nb > 0 && nb <= 0x7fffffff, "htrc_select_f32: bad sizes");
+    REQUIRE(group >= 1 && group <= 1024, "htrc_select_f32: group must be in [1, 1024]");
+    REQUIRE(aligned(q, 16) && aligned(mu, 16) && aligned(g, 16), "htrc_select_f32: misaligned buffer");
+    const int64_t nt = (nq + tile - 1) / tile;
+    REQUIRE(nt <= 0x7fffffff, "htrc_select_f32: too many tiles");
+    int64_t ng, tb, ntw;
+    REQUIRE(group_window(nt, group, g0, gn, ng, tb, ntw), "htrc_select_f32: group window [g0, g0 + gn) must lie in the head's groups");
+    REQUIRE(gn <= 65535, "htrc_select_f32: at most 65535 groups per launch");
+    const dim3 grid((unsigned)((nb + 255) / 256), (unsigned)gn, (unsigned)heads);
+    hipStream_t s = (hipStream_t)stream;
+    F32_DISPATCH(select_f32_kernel, grid, dim3(256), q, mu, (int)ng, g, lz, nq, (int)nt, tile, stride, group, (int)g0,
+                 (int)gn, perm, (int)nb, htrc_nb_pad(nb), sel);
+    return launched("htrc_select_f32");
+}
+
+int htrc_tile_f32(const void* q, int q_is_bf16, const float* mu, const void* g, int state_bf16, const float* lz,
+                  const void* vb, const int8_t* excl, const int32_t* idx, const uint16_t* k, const uint16_t* v,
+                  int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int tile, int group, int64_t g0,
+                  int64_t gn, const int32_t* perm, int splits, int bn, int tf32, float scale, float* pm, float* pl,
+                  float* pacc, float* out, float* logz, void* stream) {
+    REQUIRE(q && mu && g && lz && vb && excl && k && v, "htrc_tile_f32: null input pointer");
+    REQUIRE(d == D, "htrc_tile_f32: head dim must be 128");
+    REQUIRE(tile == 32 || tile == 64, "htrc_tile_f32: tile must be 32 or 64 rows");
+    REQUIRE(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128, "htrc_tile_f32: leaf must be 16/32/64/128");
+    REQUIRE(nk > 0 && nk % leaf == 0 && nq > 0 && heads > 0 && heads <= 65535, "htrc_tile_f32: bad sizes");
+    const int64_t nb = nk / leaf, nt = (nq + tile - 1) / tile;
+    REQUIRE(nt <= 0x7fffffff && nb <= 0x7fffffff, "htrc_tile_f32: too many tiles / leaves");
+    REQUIRE(kx >= 0 && kx <= nb && (kx == 0 || idx), "htrc_tile_f32: need 0 <= kx <= leaves and idx when kx > 0");
+    REQUIRE(splits >= 1 && splits <= 64 && bn >= 32 && bn % 32 == 0,
+            "htrc_tile_f32: need 1 <= splits <= 64 and a block that is a multiple of 32");
+    REQUIRE(splits == 1 ? (out && logz) : (pm && pl && pacc), "htrc_tile_f32: missing outputs");
+    REQUIRE(group >= 1 && group <= 1024, "htrc_tile_f32: group must be in [1, 1024]");
+    REQUIRE(aligned(q, 16) && aligned(mu, 16) && aligned(g, 16) && aligned(vb, 16) && aligned(k, 16) && aligned(v, 16),
+            "htrc_tile_f32: misaligned buffer");
+    int64_t ng, tb, ntw;
+    REQUIRE(group_window(nt, group, g0, gn, ng, tb, ntw), "htrc_tile_f32: group window [g0, g0 + gn) must lie in the head's groups");
+    const int lps = (int)split_len(nb, splits, bn), eps = (int)split_len((int64_t)kx * leaf, splits, bn);
+    const dim3 grid((unsigned)ntw, (unsigned)splits, (unsigned)heads);
+    hipStream_t s = (hipStream_t)stream;
+    F32_DISPATCH(tile_f32_kernel, grid, dim3(4 * tile), q, mu, (int)ng, g, lz, vb, excl, idx, k, v, nq, (int)nt, tile,
+                 group, (int)g0, (int)gn, perm, nk, leaf, (int)nb, htrc_nb_pad(nb), kx, lps, eps, scale,
+                 splits == 1 ? nullptr : pm, splits == 1 ? nullptr : pl, splits == 1 ? nullptr : pacc, out, logz);
+    return launched("htrc_tile_f32");
+}
+#undef F32_DISPATCH
 
 int htrc_pack_q16(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int tile, int group,
                   const int32_t* perm, int dq_fp16, float* mu, uint16_t* q16, uint16_t* dq16, void* stream) {
@@ -4156,8 +4516,8 @@ int htrc_route_noalloc(const int8_t* q8, const float* sq, const int8_t* dq8, con
                       g0, gn, perm, scale, out, logz, idx, rowmax, keys, stream);
 }
 
-int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
-              int64_t ntail, int d, float scale, float* out, float* logz, void* stream) {
+static int tail_launch(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
+                       int64_t ntail, int d, int mode, float scale, float* out, float* logz, void* stream) {
     REQUIRE(q && tk && tv && out && logz, "htrc_tail: null pointer");
     REQUIRE(d == D, "htrc_tail: head dim must be 128");
     REQUIRE(heads > 0 && heads <= 65535 && nq > 0 && ntail > 0 && ntail <= (1 << 24), "htrc_tail: bad sizes");
@@ -4165,13 +4525,26 @@ int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, in
     const int64_t nt = (nq + TILE - 1) / TILE;
     REQUIRE(nt <= 0x7fffffff, "htrc_tail: too many tiles");
     const dim3 grid((unsigned)nt, (unsigned)heads);
-    if (q_is_bf16)
-        hipLaunchKernelGGL(tail_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, q, tk, tv, nq, (int)ntail, scale,
-                           out, logz);
-    else
-        hipLaunchKernelGGL(tail_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, q, tk, tv, nq, (int)ntail,
-                           scale, out, logz);
+#define TAIL(QB, M)                                                                                         \
+    hipLaunchKernelGGL((tail_kernel<QB, M>), grid, dim3(256), 0, (hipStream_t)stream, q, tk, tv, nq, (int)ntail, \
+                       scale, out, logz)
+    if (q_is_bf16) {
+        if (mode == 0) TAIL(true, 0); else if (mode == 1) TAIL(true, 1); else TAIL(true, 2);
+    } else {
+        if (mode == 0) TAIL(false, 0); else if (mode == 1) TAIL(false, 1); else TAIL(false, 2);
+    }
+#undef TAIL
     return launched("htrc_tail");
+}
+
+int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
+              int64_t ntail, int d, float scale, float* out, float* logz, void* stream) {
+    return tail_launch(q, q_is_bf16, tk, tv, heads, nq, ntail, d, 0, scale, out, logz, stream);
+}
+
+int htrc_tail_f32(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
+                  int64_t ntail, int d, int tf32, float scale, float* out, float* logz, void* stream) {
+    return tail_launch(q, q_is_bf16, tk, tv, heads, nq, ntail, d, tf32 ? 2 : 1, scale, out, logz, stream);
 }
 
 int htrc_kmeans_order(const void* q, int q_is_bf16, int64_t heads, int64_t nq, int d, int clusters, int sample,
@@ -4229,9 +4602,9 @@ int htrc_dequant_rows(const uint8_t* x8, int64_t stride_x, const float* scale, i
     return launched("htrc_dequant_rows");
 }
 
-int htrc_bound_select(const void* q, int q_is_bf16, const float* mu, const uint16_t* g, const float* lz, int64_t heads,
-                      int64_t nq, int64_t nk, int leaf, int d, int tile, int group, int64_t g0, int64_t gn,
-                      const int32_t* perm, float* sel, void* stream) {
+static int bound_select_launch(const void* q, int q_is_bf16, const float* mu, const void* g, int g_f32, const float* lz,
+                               int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int tile, int group, int64_t g0,
+                               int64_t gn, const int32_t* perm, float* sel, void* stream) {
     REQUIRE(q && mu && g && lz && sel, "htrc_bound_select: null pointer");
     REQUIRE(d == D, "htrc_bound_select: head dim must be 128");
     REQUIRE(tile == 32 || tile == 64, "htrc_bound_select: tile must be 32 or 64 rows");
@@ -4244,13 +4617,30 @@ int htrc_bound_select(const void* q, int q_is_bf16, const float* mu, const uint1
     REQUIRE(group_window(nt, group, g0, gn, ng, tb, ntw), "htrc_bound_select: group window [g0, g0 + gn) must lie in the head's groups");
     REQUIRE(gn <= 0x7fffffff, "htrc_bound_select: too many groups");
     const dim3 grid((unsigned)gn, (unsigned)heads);
-    if (q_is_bf16)
-        hipLaunchKernelGGL(bound_select_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, q, mu, g, lz, nq, (int)nt,
-                           tile, group, (int)ng, (int)g0, (int)gn, (int)nb, htrc_nb_pad(nb), perm, sel);
-    else
-        hipLaunchKernelGGL(bound_select_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, q, mu, g, lz, nq, (int)nt,
-                           tile, group, (int)ng, (int)g0, (int)gn, (int)nb, htrc_nb_pad(nb), perm, sel);
+#define BOUND(QB, GF)                                                                                            \
+    hipLaunchKernelGGL((bound_select_kernel<QB, GF>), grid, dim3(256), 0, (hipStream_t)stream, q, mu, g, lz, nq, \
+                       (int)nt, tile, group, (int)ng, (int)g0, (int)gn, (int)nb, htrc_nb_pad(nb), perm, sel)
+    if (q_is_bf16) {
+        if (g_f32) BOUND(true, true); else BOUND(true, false);
+    } else {
+        if (g_f32) BOUND(false, true); else BOUND(false, false);
+    }
+#undef BOUND
     return launched("htrc_bound_select");
+}
+
+int htrc_bound_select(const void* q, int q_is_bf16, const float* mu, const uint16_t* g, const float* lz, int64_t heads,
+                      int64_t nq, int64_t nk, int leaf, int d, int tile, int group, int64_t g0, int64_t gn,
+                      const int32_t* perm, float* sel, void* stream) {
+    return bound_select_launch(q, q_is_bf16, mu, g, 0, lz, heads, nq, nk, leaf, d, tile, group, g0, gn, perm, sel,
+                               stream);
+}
+
+int htrc_bound_select_f32(const void* q, int q_is_bf16, const float* mu, const float* g, const float* lz, int64_t heads,
+                          int64_t nq, int64_t nk, int leaf, int d, int tile, int group, int64_t g0, int64_t gn,
+                          const int32_t* perm, float* sel, void* stream) {
+    return bound_select_launch(q, q_is_bf16, mu, g, 1, lz, heads, nq, nk, leaf, d, tile, group, g0, gn, perm, sel,
+                               stream);
 }
 
 int htrc_fake_quant(const void* x, int x_is_bf16, int64_t rows, int d, int group, int fmt, void* out, int out_is_bf16,

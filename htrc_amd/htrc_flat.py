@@ -76,18 +76,26 @@ class _Tick:
             self.t = t
 
 
+def _store_dtype(store):
+    """The state element type of a store name (h3/htrc_flat.py:123: any other name is fp32)."""
+    return {"bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn, "int8": torch.int8}.get(store, torch.float32)
+
+
 def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot, quant, tail, kern):
     if backend not in ("hip", "triton"):
         raise ValueError(f"backend {backend!r} is not part of this build: the flat operator runs only as "
                          "HIP kernels (backend='hip', alias 'triton')")
     if curvature != "lin":
         raise ValueError("the HIP backend needs curvature='lin'")
-    if store not in ("int8", "fp8", "bf16") or dot != "bf16":
-        raise ValueError("the HIP backend implements dot='bf16' with store='int8' (int8 Q/K dots, bf16 PV), "
-                         "store='fp8' (e4m3 leaf state) or store='bf16'")
+    # h3/htrc_flat.py:123, 196-210: any store other than int8 / fp8 / bf16 is the fp32 state, and
+    # any dot other than "bf16" runs fp32 dots (the precision knob picks IEEE or TF32 operands)
+    if dot == "bf16" and _store_dtype(store) == torch.float32:
+        raise ValueError("dot='bf16' needs store='bf16', 'fp8' or 'int8'")
+    if store in ("fp8", "int8") and dot != "bf16":
+        raise ValueError(f"store={store!r} needs dot='bf16', select='max' and no state fake-quant")
     if select not in ("max", "bound"):
         raise ValueError("select must be 'max' or 'bound'")
-    if select == "bound" and store != "bf16":
+    if select == "bound" and store in ("int8", "fp8"):
         # h3/htrc_flat.py:209-210: the int8 / fp8 stores route by the row-max score only
         raise ValueError(f"store={store!r} needs dot='bf16', select='max' and no state fake-quant")
     if order not in ("seq", "kmeans"):
@@ -98,7 +106,7 @@ def _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot
         for key in ("q", "kv", "state"):
             if quant.get(key) and quant[key] not in hip.FAKE_QUANT_FMTS:
                 raise ValueError(f"unknown quant format {quant[key]}")
-        if quant.get("state") and store != "bf16":
+        if quant.get("state") and store in ("int8", "fp8"):
             # h3/htrc_flat.py:209-210: the int8 / fp8 stores take no state fake-quant
             raise ValueError(f"store={store!r} needs dot='bf16', select='max' and no state fake-quant")
     if tail is not None:
@@ -206,9 +214,11 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     ``tile_chunk`` tiles of every head are processed per window (h3/htrc_flat.py:236-273): the
     per-(tile, leaf) state is held for at most S windows at a time (several windows are dealt
     over S = ``kern['window_streams']`` streams, default 2; S = 1 keeps one), and the result does not
-    depend on it.  ``precision`` is accepted for compatibility: accumulation is IEEE fp32.  ``state``, if
-    a dict, receives the packed operands and the whole layer's leaf state and routing (for
-    checks)."""
+    depend on it.  ``dot`` other than "bf16" runs fp32 dots over an fp32 (``store="fp32"``, the
+    reference's default) or bf16 state in the reference's stage structure, with IEEE operands or,
+    for ``precision="tf32"``, TF32 ones (h3/htrc_flat.py:122-123, 196-212); the dot="bf16" paths
+    always compute their leaf statistics at IEEE fp32.  ``state``, if a dict, receives the packed
+    operands and the whole layer's leaf state and routing (for checks)."""
     kern = dict(kern or {})
     _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot, quant, tail, kern)
     squeeze = q.dim() == 2
@@ -249,7 +259,16 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         d = hip.D
     perm = hip.kmeans_order(qh, ws=ws) if order == "kmeans" else None   # query rows regrouped by k-means
     qsrc = qh.contiguous()                               # the query rows select="bound" measures
-    if store in ("fp8", "bf16"):
+    f32dots = dot != "bf16"
+    prec = "tf32" if precision == "tf32" else "ieee"    # h3/htrc_flat.py:122
+    if f32dots:
+        # fp32 dots (h3/htrc_flat.py:196-212 with dot != "bf16"): centres from pack_q16, q itself
+        # read by the select and tile kernels; the reference's stage structure
+        mu, _, _ = hip.pack_q16(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm, dq_fp16=False)
+        packed = {"mu": mu}
+        sdt = _store_dtype(store)
+        fused = False
+    elif store in ("fp8", "bf16"):
         mu, q16, dq16 = hip.pack_q16(qh.contiguous(), tile=tile, ws=ws, group=group, perm=perm, dq_fp16=store == "fp8")
         packed = {"q16": q16, "dq16": dq16, "mu": mu}
         sdt = torch.float8_e4m3fn if store == "fp8" else torch.bfloat16
@@ -264,6 +283,8 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     packed["k"], packed["v"] = kb, vb
     if sdt == torch.int8:
         packed["k8"], packed["ks"] = hip.pack_k(kb, ws=ws)
+    if f32dots:
+        packed["q"] = qsrc
     tick("prep")
     ng = int(mu.shape[1])                               # centres: tiles, or tile groups
     out = hip._buf(ws, "out", (h, nq, d), torch.float32, qh.device)
@@ -275,7 +296,8 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     def _window(w, g0, gn):
         """Statistics, select / top-k and attention of the tile groups [g0, g0 + gn), the window's
         buffers in workspace w."""
-        g, lz, vbs, sg, sv = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=sdt, ws=w, c0=g0, cn=gn)
+        g, lz, vbs, sg, sv = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=sdt, ws=w, c0=g0, cn=gn,
+                                            prec=prec if f32dots else "ieee")
         if quant.get("state"):                           # h3/htrc_flat.py:246-248, in place
             sfmt = quant["state"]
             sgsz = hip.D if not qg and sfmt != "fp4" else (qg or 16)
@@ -293,7 +315,10 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         else:
             if kx > 0 and select == "bound":            # h3/htrc_flat.py:255-257
                 sel = hip.bound_select(qsrc, mu, g, lz, nb, leaf=leaf, ws=w, group=group, tile=tile, g0=g0, perm=perm)
-            if kx > 0 and select == "max":
+            if kx > 0 and select == "max" and f32dots:
+                sel = hip.select_f32(qsrc, mu, g, lz, nb, stride=stride, group=group, tile=tile, g0=g0, perm=perm,
+                                     prec=prec, ws=w)
+            elif kx > 0 and select == "max":
                 sel = hip.rowmax_select(g=g, lz=lz, sg=sg, stride=stride, nb=nb, dq8=packed.get("dq8", packed.get("dq16")),
                                         sdq=packed.get("sdq"), ws=w, group=group, tile=tile, g0=g0)
             if kx > 0:
@@ -302,9 +327,14 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
                 excl = hip._rows(w, "excl", h, gn, (nb_pad(nb),), torch.int8, qh.device)
                 excl.zero_()
             tick("select")
-            hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
-                               bn=int(kern.get("tile_bn", 32)), ws=w, out=out, logz=logz, group=group, perm=perm,
-                               tile=tile, g0=g0)
+            if f32dots:
+                hip.tile_f32(qsrc, mu, lstate, excl, idx, kb, vb, nq=nq, leaf=leaf, scale=scale, splits=splits,
+                             bn=int(kern.get("tile_bn", 32)), ws=w, out=out, logz=logz, group=group, perm=perm,
+                             tile=tile, g0=g0, prec=prec)
+            else:
+                hip.tile_attention(packed, lstate, excl, idx, nq=nq, leaf=leaf, scale=scale, splits=splits,
+                                   bn=int(kern.get("tile_bn", 32)), ws=w, out=out, logz=logz, group=group, perm=perm,
+                                   tile=tile, g0=g0)
             tick("tile")
         keep.add(g0, gn, g8=g, sg=sg, lz=lz, vb=vbs, sv=sv, sel=sel, excl=excl, idx=idx)
 
@@ -338,7 +368,8 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         tk, tv = (x.unsqueeze(0) if squeeze else x for x in tail)
         if d_in < d:
             tk, tv = (_pad_dims(x.to(qh.device), ws, n, torch.float32) for x, n in ((tk, "tk_pad"), (tv, "tv_pad")))
-        hip.tail_merge(qh, tk.to(qh.device), tv.to(qh.device), scale=scale, out=out, logz=logz)
+        hip.tail_merge(qh, tk.to(qh.device), tv.to(qh.device), scale=scale, out=out, logz=logz, f32dots=f32dots,
+                       prec=prec)
         tick("tail")
     if d_in < d:
         out = out[..., :d_in]

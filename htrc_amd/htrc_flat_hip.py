@@ -157,9 +157,13 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
     cn state rows per head:
     store=int8: g int8 [H,cn,nbp,D], vb bf16, sv None; store=float8_e4m3fn: g and vb e4m3
     with the row scales sg, sv (h3/htrc_flat_triton.py:65-72); store=bfloat16: g and vb bf16,
-    sg and sv None."""
-    if store not in (torch.int8, torch.float8_e4m3fn, torch.bfloat16):
-        raise ValueError("the HIP leaf statistics store g as int8, float8_e4m3fn or bfloat16")
+    sg and sv None; store=float32: g and vb fp32, sg and sv None.  prec="tf32" (the reference's
+    PREC) rounds the centres and weights to TF32 for the fp32 and bf16 stores; the int8 and fp8
+    stores always take IEEE fp32 statistics."""
+    if store not in (torch.int8, torch.float8_e4m3fn, torch.bfloat16, torch.float32):
+        raise ValueError("the HIP leaf statistics store g as int8, float8_e4m3fn, bfloat16 or float32")
+    if prec not in ("ieee", "tf32"):
+        raise ValueError("prec must be 'ieee' or 'tf32'")
     mu = _heads(mu).contiguous()
     kf = _heads(kf).contiguous()
     vf = _heads(vf).contiguous()
@@ -173,12 +177,17 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
         raise ValueError("keys and values must be [H, nb * leaf, D]")
     nbp = nb_pad(nb)
     dev = mu.device
-    if store == torch.bfloat16:
-        g = _rows(ws, "g_bf16", h, cn, (nbp, d), torch.bfloat16, dev)
-        vb = _rows(ws, "vb", h, cn, (nbp, d), torch.bfloat16, dev)
+    if store in (torch.bfloat16, torch.float32):
+        sb = store == torch.bfloat16
+        g = _rows(ws, "g_bf16" if sb else "g_f32", h, cn, (nbp, d), store, dev)
+        vb = _rows(ws, "vb" if sb else "vb_f32", h, cn, (nbp, d), store, dev)
         lz = _rows(ws, "lz", h, cn, (nbp,), torch.float32, dev)
-        call("htrc_leaf_stats_bf16", ptr(mu), ptr(kf), ptr(vf), h, nt, c0, cn, nk, int(leaf), d, float(scale), ptr(g),
-             ptr(vb), ptr(lz), stream_handle(dev))
+        if sb and prec == "ieee":
+            call("htrc_leaf_stats_bf16", ptr(mu), ptr(kf), ptr(vf), h, nt, c0, cn, nk, int(leaf), d, float(scale),
+                 ptr(g), ptr(vb), ptr(lz), stream_handle(dev))
+        else:
+            call("htrc_leaf_stats_f32", ptr(mu), ptr(kf), ptr(vf), h, nt, c0, cn, nk, int(leaf), d, float(scale),
+                 int(sb), int(prec == "tf32"), ptr(g), ptr(vb), ptr(lz), stream_handle(dev))
         return g, lz, vb, None, None
     if store == torch.float8_e4m3fn:
         g = _rows(ws, "g_fp8", h, cn, (nbp, d), torch.float8_e4m3fn, dev)
@@ -289,6 +298,57 @@ def tile_attention(packed: dict, state: dict, excl, idx, *, nq: int, leaf: int, 
     call("htrc_tile", ptr(q8), ptr(sq), ptr(dq8), ptr(sdq), ptr(g8), ptr(sg), ptr(lz), ptr(vb), ptr(excl),
          ptr(idx) if kx else None, ptr(k8), ptr(ks), ptr(v), h, nq, nk, int(leaf), d, kx, tile, int(group), g0, gn,
          ptr(perm), ns, int(bn), float(scale), ptr(pm), ptr(pl), ptr(pacc), ptr(out), ptr(logz), stream_handle(dev))
+    if ns > 1:
+        call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, tile, tb, ntw, ns, d, ptr(perm), ptr(out), ptr(logz),
+             stream_handle(dev))
+    return out, logz
+
+
+def select_f32(q, mu, g, lz, nb: int, *, stride: int = 1, group: int = 1, tile: int = TILE, g0: int = 0, perm=None,
+               prec: str = "ieee", ws=None):
+    """SEL [H,gn,nbp] with fp32 dots (rowmax_select with dot=0, h3/htrc_flat_triton.py:214-254):
+    the max over every stride-th row of each group of (q - mu) . g, plus lz.  q [H,nq,D] fp32 or
+    bf16 in query order (perm maps operator rows to queries), mu [H,ng,D] the layer's centres,
+    g fp32 or bf16 [H,gn,nbp,D] and lz the window's state; prec "tf32" rounds the operands."""
+    q = _heads(q).contiguous()
+    tile = _tile(tile)
+    h, nq, d = (int(x) for x in q.shape)
+    gn, nbp = int(g.shape[1]), int(g.shape[2])
+    sel = _rows(ws, "sel", h, gn, (nbp,), torch.float32, g.device)
+    call("htrc_select_f32", ptr(q), int(q.dtype == torch.bfloat16), ptr(mu), ptr(g), int(g.dtype == torch.bfloat16),
+         ptr(lz), h, nq, int(nb), int(stride), tile, int(group), int(g0), gn, ptr(perm), int(prec == "tf32"), d,
+         ptr(sel), stream_handle(g.device))
+    return sel
+
+
+def tile_f32(q, mu, state: dict, excl, idx, k, v, *, nq: int, leaf: int, scale: float, splits: int = 4,
+             bn: int = 64, ws=None, out=None, logz=None, group: int = 1, perm=None, tile: int = TILE, g0: int = 0,
+             prec: str = "ieee"):
+    """Far + near softmax per (tile, split) with fp32 dots (tile_attention with dot=0,
+    h3/htrc_flat_triton.py:88-211, 348-391) and the merge, for the tiles of the gn =
+    state["lz"].shape[1] groups from g0: q [H,nq,D] fp32 or bf16 in query order, mu [H,ng,D],
+    state g / vb fp32 or bf16 and lz, k / v bf16 [H,nk,D] -> (out, logz)."""
+    q = _heads(q).contiguous()
+    tile = _tile(tile)
+    g, lz, vb = state["g8"], state["lz"], state["vb"]
+    h, nk, d = (int(x) for x in k.shape)
+    g0, gn, tb, ntw = _tile_window(nq, tile, group, g0, int(lz.shape[1]))
+    kx = int(idx.shape[-1]) if idx is not None else 0
+    dev = q.device
+    ns = max(1, int(splits))
+    if out is None:
+        out = _buf(ws, "out", (h, nq, d), torch.float32, dev)
+    if logz is None:
+        logz = _buf(ws, "logz", (h, nq), torch.float32, dev)
+    pm = pl = pacc = None
+    if ns > 1:
+        pm = _rows(ws, "pm", h, ntw, (ns, tile), torch.float32, dev)
+        pl = _rows(ws, "pl", h, ntw, (ns, tile), torch.float32, dev)
+        pacc = _rows(ws, "pacc", h, ntw, (ns, tile, d), torch.float32, dev)
+    call("htrc_tile_f32", ptr(q), int(q.dtype == torch.bfloat16), ptr(mu), ptr(g), int(g.dtype == torch.bfloat16),
+         ptr(lz), ptr(vb), ptr(excl), ptr(idx) if kx else None, ptr(k), ptr(v), h, nq, nk, int(leaf), d, kx, tile,
+         int(group), g0, gn, ptr(perm), ns, int(bn), int(prec == "tf32"), float(scale), ptr(pm), ptr(pl), ptr(pacc),
+         ptr(out), ptr(logz), stream_handle(dev))
     if ns > 1:
         call("htrc_merge", ptr(pm), ptr(pl), ptr(pacc), h, nq, tile, tb, ntw, ns, d, ptr(perm), ptr(out), ptr(logz),
              stream_handle(dev))
@@ -494,9 +554,10 @@ def route16_fits(nb: int, kx: int) -> bool:
     return int(nb) <= ROUTE_NB_LDS and min(int(kx), int(nb)) <= ROUTE_MAX_KX
 
 
-def tail_merge(q, tk, tv, *, scale: float, out, logz):
+def tail_merge(q, tk, tv, *, scale: float, out, logz, f32dots: bool = False, prec: str = "ieee"):
     """Tail keys tk, tv [H, n, D] (past the last full leaf) attended exactly by every query and
-    merged in place into out [H, nq, D] / logz [H, nq] (h3/htrc_flat_triton.py:187-207, 381-388)."""
+    merged in place into out [H, nq, D] / logz [H, nq] (h3/htrc_flat_triton.py:187-207, 381-388).
+    f32dots: the fp32-dot path's operands (IEEE, or TF32 for prec="tf32")."""
     q = _heads(q)
     if q.dtype not in (torch.float32, torch.bfloat16):
         q = q.float()
@@ -511,8 +572,12 @@ def tail_merge(q, tk, tv, *, scale: float, out, logz):
         raise ValueError("tail keys / values must be [H, n, D] matching q")
     _need(out, torch.float32, "out")
     _need(logz, torch.float32, "logz")
-    call("htrc_tail", ptr(q), int(q.dtype == torch.bfloat16), ptr(tk), ptr(tv), h, nq, int(tk.shape[1]), d,
-         float(scale), ptr(out), ptr(logz), stream_handle(q.device))
+    if f32dots:
+        call("htrc_tail_f32", ptr(q), int(q.dtype == torch.bfloat16), ptr(tk), ptr(tv), h, nq, int(tk.shape[1]), d,
+             int(prec == "tf32"), float(scale), ptr(out), ptr(logz), stream_handle(q.device))
+    else:
+        call("htrc_tail", ptr(q), int(q.dtype == torch.bfloat16), ptr(tk), ptr(tv), h, nq, int(tk.shape[1]), d,
+             float(scale), ptr(out), ptr(logz), stream_handle(q.device))
     return out, logz
 
 
@@ -570,15 +635,16 @@ def selftest_mfma(ai, bi, af, bf):
 
 def bound_select(q: torch.Tensor, mu: torch.Tensor, g: torch.Tensor, lz: torch.Tensor, nb: int, *, leaf: int,
                  ws=None, group: int = 1, tile: int = TILE, g0: int = 0, perm=None) -> torch.Tensor:
-    """select="bound" of the bf16 store (h3/htrc_flat.py:255-257): q [H,N,D] (fp32 or bf16, query
-    order), mu [H,ng,D], the window's g bf16 [H,gn,nbp,D] and lz -> SEL [H,gn,nbp] fp32 =
-    lz + r * ||g||, r the tile group's largest ||q - mu||."""
+    """select="bound" of the bf16 and fp32 stores (h3/htrc_flat.py:255-257): q [H,N,D] (fp32 or
+    bf16, query order), mu [H,ng,D], the window's g bf16 or fp32 [H,gn,nbp,D] and lz -> SEL
+    [H,gn,nbp] fp32 = lz + r * ||g||, r the tile group's largest ||q - mu||."""
     q = _heads(q)
     h, nq, d = (int(x) for x in q.shape)
     tile = _tile(tile)
     gn = int(lz.shape[1])
     sel = _rows(ws, "sel", h, gn, (int(lz.shape[2]),), torch.float32, q.device)
-    call("htrc_bound_select", ptr(q), int(q.dtype == torch.bfloat16), ptr(mu), ptr(g), ptr(lz), h, nq,
+    fn = "htrc_bound_select_f32" if g.dtype == torch.float32 else "htrc_bound_select"
+    call(fn, ptr(q), int(q.dtype == torch.bfloat16), ptr(mu), ptr(g), ptr(lz), h, nq,
          int(nb) * int(leaf), int(leaf), d, tile, int(group), int(g0), gn, ptr(perm), ptr(sel), stream_handle(q.device))
     return sel
 

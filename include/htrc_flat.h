@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define HTRC_ABI_VERSION 14
+#define HTRC_ABI_VERSION 15
 
 #define HTRC_OK 0
 #define HTRC_ERR_ARG 1 /* invalid argument: shape, alignment, null pointer, knob */
@@ -164,6 +164,10 @@ int htrc_route_noalloc(const int8_t* q8, const float* sq, const int8_t* dq8, con
  * Replaces the tail handling of tile_attention (h3/htrc_flat_triton.py:187-207, 366-388). */
 int htrc_tail(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
               int64_t ntail, int d, float scale, float* out, float* logz, void* stream);
+/* The same merge for the fp32-dot path (dot other than "bf16"): every tail key in fp32
+ * operands, TF32-rounded when tf32 = 1 (h3/htrc_flat_triton.py:198-207 with DOT = 0). */
+int htrc_tail_f32(const void* q, int q_is_bf16, const float* tk, const float* tv, int64_t heads, int64_t nq,
+                  int64_t ntail, int d, int tf32, float scale, float* out, float* logz, void* stream);
 
 /* fp8 state store (store="fp8"; h3/htrc_flat_triton.py:65-72, 104-108, 132-153, 165-184,
  * 214-254 with FP8 = 1), run in the reference's stage structure (select, top-k, tile, merge):
@@ -202,6 +206,35 @@ int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g,
                    int64_t nq, int64_t nk, int leaf, int d, int kx, int tile, int group, int64_t g0, int64_t gn,
                    const int32_t* perm, int splits, int bn, float scale, float* pm, float* pl, float* pacc, float* out,
                    float* logz, void* stream);
+
+/* fp32 dots (dot other than "bf16", DOT = 0 in h3/htrc_flat_triton.py:81-83, 138-141, 159-161,
+ * 171-174, 184-185, 245-247; the default flat_attention(..., backend="triton") call): the state g,
+ * vb fp32 (store="fp32") or bf16 (store="bf16"; state_bf16 = 1) [H, ng, nbp, 128], lz fp32; q fp32
+ * or bf16 (q_is_bf16) [H, nq, 128] in query order with the optional row permutation perm, mu the
+ * layer's centres [H, ceil(nt / group), 128] (htrc_pack_q16's), k / v bf16.  Every product is an
+ * fp32 MFMA with fp32 sums; tf32 = 1 (precision="tf32", PREC "tf32") rounds every operand to TF32
+ * (to nearest, ties away) first.  Statistics: g = (w K) scale and vb = w V stored as fp32 or as
+ * bf16 (the htrc_leaf_stats_bf16 values when tf32 = 0).  select: SEL = max over every stride-th row
+ * of (q - mu) . g + lz.  tile far: (q - mu) . g + lz, PV p . vb; near: (q . k) scale, PV p . v;
+ * the reference's running-max softmax per block of 16 keys; splits > 1 writes the partials for
+ * htrc_merge.  htrc_bound_select_f32: select="bound" on an fp32 g (htrc_bound_select's rule).
+ * Replace leaf_stats(store=float32 / bfloat16, prec), rowmax_select(dot=0) and
+ * tile_attention(dot=0) (h3/htrc_flat_triton.py:315-391) and the store="fp32" / dot="tf32"
+ * dispatch of h3/htrc_flat.py:196-212. */
+int htrc_leaf_stats_f32(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
+                        int64_t cn, int64_t nk, int leaf, int d, float scale, int state_bf16, int tf32, void* g,
+                        void* vb, float* lz, void* stream);
+int htrc_select_f32(const void* q, int q_is_bf16, const float* mu, const void* g, int state_bf16, const float* lz,
+                    int64_t heads, int64_t nq, int64_t nb, int stride, int tile, int group, int64_t g0, int64_t gn,
+                    const int32_t* perm, int tf32, int d, float* sel, void* stream);
+int htrc_tile_f32(const void* q, int q_is_bf16, const float* mu, const void* g, int state_bf16, const float* lz,
+                  const void* vb, const int8_t* excl, const int32_t* idx, const uint16_t* k, const uint16_t* v,
+                  int64_t heads, int64_t nq, int64_t nk, int leaf, int d, int kx, int tile, int group, int64_t g0,
+                  int64_t gn, const int32_t* perm, int splits, int bn, int tf32, float scale, float* pm, float* pl,
+                  float* pacc, float* out, float* logz, void* stream);
+int htrc_bound_select_f32(const void* q, int q_is_bf16, const float* mu, const float* g, const float* lz, int64_t heads,
+                          int64_t nq, int64_t nk, int leaf, int d, int tile, int group, int64_t g0, int64_t gn,
+                          const int32_t* perm, float* sel, void* stream);
 
 /* Fused production path of the 16-bit state stores (fp8 = 1: store="fp8", g / vb e4m3 codes with
  * row scales sg / sv; fp8 = 0: store="bf16", g / vb bf16, sg / sv unused), for the groups
