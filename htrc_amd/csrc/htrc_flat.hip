@@ -458,6 +458,29 @@ __device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
     return u;
 }
 
+// Precomputed centre operands of the statistics kernel: per centre row of the window, its
+// exponent smu (its largest |value| times 2^smu in [2^14, 2^15), smu in [-64, 64]) and the two fp16
+// terms hi + lo of every dim times 2^smu (TF32: of the dim rounded to TF32 first, lo then 0), the
+// same words stats_ls_kernel's in-kernel split makes.  Row: hi[128] | lo[128] | smu (int32) | pad.
+constexpr int MUT_ROW = 2 * D + 8;
+template <bool TF32>
+__global__ __launch_bounds__(64) void centre_terms_kernel(const float* __restrict__ mu, int64_t mu_stride, int64_t c0,
+                                                          int cn, uint16_t* __restrict__ mut) {
+    const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const float* src = mu + ((int64_t)h * mu_stride + c0 + t) * D;
+    const float x0 = src[2 * lane], x1 = src[2 * lane + 1];
+    const float mx = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+    const int e = (int)((__float_as_uint(mx) >> 23) & 0xffu) - 127;
+    const int sm = 14 - e < -64 ? -64 : (14 - e > 64 ? 64 : 14 - e);
+    const float y0 = ldexpf(TF32 ? tf32_rna(x0) : x0, sm), y1 = ldexpf(TF32 ? tf32_rna(x1) : x1, sm);
+    const uint32_t hi = pack2h(y0, y1);
+    const uint32_t lo = pack2h(sub_h_lo(y0, hi), sub_h_hi(y1, hi));
+    uint16_t* row = mut + ((int64_t)h * cn + t) * MUT_ROW;
+    *(uint32_t*)(row + 2 * lane) = hi;
+    *(uint32_t*)(row + D + 2 * lane) = lo;
+    if (lane == 0) *(int*)(row + 2 * D) = sm;
+}
+
 // Leaf statistics at the tile centres (h3/htrc_flat_triton.py:41-85), per (centre, leaf): the
 // logits a = (mu . k) scale, lz = max + log sum exp, w = softmax, g = (w K) scale, vb = w V, by
 // fp16 MFMA on fp32-accurate operands: K and V exact in fp16 (each leaf scaled by a power of
@@ -476,8 +499,9 @@ __device__ __forceinline__ uint32_t quant4(f32x4 x, float c) {
 // into registers while the current group is computed.  Its state rows are stored as soon as
 // they are quantised; sg / lz (sv) of the NL leaves are NL contiguous floats per centre.
 // ncs: the centre groups of a head are dealt over ncs workgroups (small layers).
-template <int LEAF, int STORE, int NL, bool TF32 = false>
-__global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restrict__ mu, int64_t mu_stride,
+template <int LEAF, int STORE, int NL, bool TF32 = false, bool MUT = false>
+__global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restrict__ mu, const uint16_t* __restrict__ mut,
+                                                          int64_t mu_stride,
                                                           int64_t c0, int nt, const uint16_t* __restrict__ k,
                                                           const uint16_t* __restrict__ v, int64_t nk, int nb,
                                                           int nb_pad, int ncs, float scale, int8_t* __restrict__ g8,
@@ -505,9 +529,21 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
     const float sl2 = __fmul_rn(scale, LOG2E);
     int tk[NL], tv[NL];
     stage_leaves_f16<LEAF, NL>(k, v, kh + (int64_t)l0 * LEAF, lr - l0, lds, lmax, tk, tv);
-    // this lane's 32 centre values (dims 32 ks + 8 grp + e of centre 16 j + col), fp32
-    auto load_mu = [&](int j, f32x4 (&m)[8]) {
+    // this lane's 32 centre values (dims 32 ks + 8 grp + e of centre 16 j + col), fp32; with
+    // precomputed terms (mut, centre_terms_kernel) their hi / lo fp16 words in the same registers
+    // (m[2 ks] hi, m[2 ks + 1] lo) and the centre's exponent in sm
+    auto load_mu = [&](int j, f32x4 (&m)[8], int& sm) {
         const int t = min(16 * j + col, nt - 1);
+        if constexpr (MUT) {
+            const uint16_t* src = mut + ((int64_t)h * nt + t) * MUT_ROW + 8 * grp;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                m[2 * ks] = *(const f32x4*)(src + 32 * ks);
+                m[2 * ks + 1] = *(const f32x4*)(src + D + 32 * ks);
+            }
+            sm = *(const int*)(mut + ((int64_t)h * nt + t) * MUT_ROW + 2 * D);
+            return;
+        }
         const float* src = mu + ((int64_t)h * mu_stride + c0 + t) * D + 8 * grp;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
@@ -520,7 +556,16 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
     // error beyond fp32 rounding)
     u32x4 mh[4], ml[4];
     int smu = 0;
-    auto split_mu = [&](const f32x4 (&m)[8]) {
+    auto split_mu = [&](const f32x4 (&m)[8], int sm) {
+        if constexpr (MUT) {
+            smu = sm;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                mh[ks] = __builtin_bit_cast(u32x4, m[2 * ks]);
+                ml[ks] = __builtin_bit_cast(u32x4, m[2 * ks + 1]);
+            }
+            return;
+        }
         float mx = 0.0f;
 #pragma unroll
         for (int q = 0; q < 8; ++q)
@@ -541,9 +586,10 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
         }
     };
     f32x4 mnext[8];
+    int snext = 0;
     if (jb + w < je) {
-        load_mu(jb + w, mnext);
-        split_mu(mnext);
+        load_mu(jb + w, mnext, snext);
+        split_mu(mnext, snext);
     }
     for (int j = jb + w; j < je; j += 4) {
         // Centres past the last (t >= nt) compute and store the last centre's state: the same bits
@@ -552,7 +598,7 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
         // end, so the compiler's wait for them counts the iteration's stores issued after them
         // instead of draining them all.
         const int64_t th = (int64_t)h * nt + min(16 * j + col, nt - 1);
-        load_mu(min(j + 4, je - 1), mnext);
+        load_mu(min(j + 4, je - 1), mnext, snext);
         float sgs[NL], lzs[NL], svs[NL];
 #pragma unroll
         for (int li = 0; li < NL; ++li) {
@@ -804,7 +850,7 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
             put(lz, lzs);
             if (FP8) put(sv, svs);
         }
-        split_mu(mnext);
+        split_mu(mnext, snext);
     }
 }
 
@@ -3831,7 +3877,8 @@ static int device_cus() {
 // Shared checks and launch of the three leaf-statistics stores (STORE 0 int8, 1 bf16, 2 fp8).
 extern "C++" {
 template <int STORE, bool TF32 = false>
-static int leaf_stats_launch(const char* who, const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads,
+static int leaf_stats_launch(const char* who, const float* mu, const uint16_t* mut, const uint16_t* k, const uint16_t* v,
+                             int64_t heads,
                              int64_t nt, int64_t c0, int64_t cn, int64_t nk, int leaf, int d, float scale, void* g,
                              float* sg, void* vb, float* sv, float* lz, void* stream) {
     static thread_local char msg[200];
@@ -3840,13 +3887,13 @@ static int leaf_stats_launch(const char* who, const float* mu, const uint16_t* k
         return fail(HTRC_ERR_ARG, msg);
     };
     constexpr bool HAS_SG = STORE == 0 || STORE == 2;
-    if (!(mu && k && v && g && vb && lz && (!HAS_SG || sg) && (STORE != 2 || sv))) return bad("null pointer");
+    if (!((mu || mut) && k && v && g && vb && lz && (!HAS_SG || sg) && (STORE != 2 || sv))) return bad("null pointer");
     if (d != D) return bad("head dim must be 128");
     if (!(leaf == 16 || leaf == 32 || leaf == 64 || leaf == 128)) return bad("leaf must be 16/32/64/128");
     if (!(nk > 0 && nk % leaf == 0)) return bad("key count must be a multiple of the leaf size");
     if (!(heads > 0 && heads <= 65535 && nt > 0 && nt <= 0x7fffffff)) return bad("bad heads / centres");
     if (!(c0 >= 0 && cn > 0 && c0 + cn <= nt)) return bad("centre window [c0, c0 + cn) must lie in [0, nt)");
-    if (!(aligned(k, 16) && aligned(v, 16) && aligned(g, 16) && aligned(vb, 16) && aligned(lz, 16) &&
+    if (!(aligned(k, 16) && aligned(v, 16) && aligned(g, 16) && aligned(vb, 16) && aligned(lz, 16) && aligned(mut, 16) &&
           (!HAS_SG || aligned(sg, 16)) && (STORE != 2 || aligned(sv, 16))))
         return bad("misaligned buffer");
     const int64_t nb = nk / leaf;
@@ -3865,8 +3912,14 @@ static int leaf_stats_launch(const char* who, const float* mu, const uint16_t* k
     hipStream_t s = (hipStream_t)stream;
 #define STATS_CASE(L)                                                                                            \
     case L:                                                                                                      \
-        hipLaunchKernelGGL((stats_ls_kernel<L, STORE, 65536 / (512 * L), TF32>), grid, dim3(256), 0, s, mu, nt, c0, \
-                           (int)cn, k, v, nk, (int)nb, nbp, (int)ncs, scale, (int8_t*)g, sg, (uint16_t*)vb, sv, lz); \
+        if (mut)                                                                                                 \
+            hipLaunchKernelGGL((stats_ls_kernel<L, STORE, 65536 / (512 * L), TF32, true>), grid, dim3(256), 0, s, mu,  \
+                               mut, nt, c0, (int)cn, k, v, nk, (int)nb, nbp, (int)ncs, scale, (int8_t*)g, sg,        \
+                               (uint16_t*)vb, sv, lz);                                                             \
+        else                                                                                                     \
+            hipLaunchKernelGGL((stats_ls_kernel<L, STORE, 65536 / (512 * L), TF32>), grid, dim3(256), 0, s, mu, mut,   \
+                               nt, c0, (int)cn, k, v, nk, (int)nb, nbp, (int)ncs, scale, (int8_t*)g, sg,            \
+                               (uint16_t*)vb, sv, lz);                                                             \
         break;
     switch (leaf) {
         STATS_CASE(16)
@@ -3882,22 +3935,64 @@ static int leaf_stats_launch(const char* who, const float* mu, const uint16_t* k
 int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
                     int64_t cn, int64_t nk, int leaf, int d, float scale, int8_t* g8, float* sg, uint16_t* vb, float* lz,
                     void* stream) {
-    return leaf_stats_launch<0>("htrc_leaf_stats", mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g8, sg, vb,
+    return leaf_stats_launch<0>("htrc_leaf_stats", mu, nullptr, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g8, sg, vb,
                                 nullptr, lz, stream);
 }
 
 int htrc_leaf_stats_fp8(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
                         int64_t cn, int64_t nk, int leaf, int d, float scale, uint8_t* g, float* sg, uint8_t* vb,
                         float* sv, float* lz, void* stream) {
-    return leaf_stats_launch<2>("htrc_leaf_stats_fp8", mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, sg, vb, sv,
+    return leaf_stats_launch<2>("htrc_leaf_stats_fp8", mu, nullptr, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, sg, vb, sv,
                                 lz, stream);
 }
 
 int htrc_leaf_stats_bf16(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
                          int64_t cn, int64_t nk, int leaf, int d, float scale, uint16_t* g, uint16_t* vb, float* lz,
                          void* stream) {
-    return leaf_stats_launch<1>("htrc_leaf_stats_bf16", mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr,
+    return leaf_stats_launch<1>("htrc_leaf_stats_bf16", mu, nullptr, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr,
                                 vb, nullptr, lz, stream);
+}
+
+int htrc_centre_terms(const float* mu, int64_t heads, int64_t nt, int64_t c0, int64_t cn, int d, int tf32,
+                      uint16_t* terms, void* stream) {
+    REQUIRE(mu && terms, "htrc_centre_terms: null pointer");
+    REQUIRE(d == D, "htrc_centre_terms: head dim must be 128");
+    REQUIRE(heads > 0 && heads <= 65535 && nt > 0 && c0 >= 0 && cn > 0 && c0 + cn <= nt && cn <= 0x7fffffff,
+            "htrc_centre_terms: centre window [c0, c0 + cn) must lie in [0, nt)");
+    REQUIRE(aligned(terms, 16), "htrc_centre_terms: terms must be 16-byte aligned");
+    const dim3 grid((unsigned)cn, (unsigned)heads);
+    if (tf32)
+        hipLaunchKernelGGL(centre_terms_kernel<true>, grid, dim3(64), 0, (hipStream_t)stream, mu, nt, c0, (int)cn, terms);
+    else
+        hipLaunchKernelGGL(centre_terms_kernel<false>, grid, dim3(64), 0, (hipStream_t)stream, mu, nt, c0, (int)cn, terms);
+    return launched("htrc_centre_terms");
+}
+
+int htrc_leaf_stats_terms(const uint16_t* terms, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t cn,
+                          int64_t nk, int leaf, int d, float scale, int store, int tf32, void* g, float* sg, void* vb,
+                          float* sv, float* lz, void* stream) {
+    const char* who = "htrc_leaf_stats_terms";
+    REQUIRE(terms, "htrc_leaf_stats_terms: null terms");
+    REQUIRE(store >= 0 && store <= 3, "htrc_leaf_stats_terms: store must be 0 (int8), 1 (bf16), 2 (fp8) or 3 (fp32)");
+    REQUIRE(!tf32 || store == 1 || store == 3, "htrc_leaf_stats_terms: TF32 operands go with the bf16 and fp32 stores");
+    switch (store) {
+        case 0:
+            return leaf_stats_launch<0>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g, sg, vb, nullptr,
+                                        lz, stream);
+        case 2:
+            return leaf_stats_launch<2>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g, sg, vb, sv, lz,
+                                        stream);
+        case 1:
+            return tf32 ? leaf_stats_launch<1, true>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g,
+                                                     nullptr, vb, nullptr, lz, stream)
+                        : leaf_stats_launch<1>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g, nullptr,
+                                               vb, nullptr, lz, stream);
+        default:
+            return tf32 ? leaf_stats_launch<3, true>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g,
+                                                     nullptr, vb, nullptr, lz, stream)
+                        : leaf_stats_launch<3>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g, nullptr,
+                                               vb, nullptr, lz, stream);
+    }
 }
 
 int htrc_leaf_stats_f32(const float* mu, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t nt, int64_t c0,
@@ -3905,13 +4000,13 @@ int htrc_leaf_stats_f32(const float* mu, const uint16_t* k, const uint16_t* v, i
                         void* vb, float* lz, void* stream) {
     const char* who = "htrc_leaf_stats_f32";
     if (state_bf16)
-        return tf32 ? leaf_stats_launch<1, true>(who, mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb,
+        return tf32 ? leaf_stats_launch<1, true>(who, mu, nullptr, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb,
                                                  nullptr, lz, stream)
-                    : leaf_stats_launch<1>(who, mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb, nullptr,
+                    : leaf_stats_launch<1>(who, mu, nullptr, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb, nullptr,
                                            lz, stream);
-    return tf32 ? leaf_stats_launch<3, true>(who, mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb,
+    return tf32 ? leaf_stats_launch<3, true>(who, mu, nullptr, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb,
                                              nullptr, lz, stream)
-                : leaf_stats_launch<3>(who, mu, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb, nullptr,
+                : leaf_stats_launch<3>(who, mu, nullptr, k, v, heads, nt, c0, cn, nk, leaf, d, scale, g, nullptr, vb, nullptr,
                                        lz, stream);
 }
 

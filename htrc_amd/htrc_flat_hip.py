@@ -149,8 +149,11 @@ def _window(ng: int, g0: int, gn) -> tuple[int, int]:
     return g0, gn
 
 
+MUT_ROW = 2 * D + 8          # one centre's row of htrc_centre_terms (uint16 words)
+
+
 def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4, store=torch.int8, ws=None,
-               c0=0, cn=None):
+               c0=0, cn=None, terms=True):
     """Leaf statistics at the tile centres (h3/htrc_flat_triton.py:329-345), for the centres
     [c0, c0 + cn) of every head (all by default; the reference passes the chunk's centres).
     mu [H,nt,D] fp32, kf/vf bf16 [H,nk,D] -> (g, lz, vb, sg, sv) in the reference's order, with
@@ -159,7 +162,9 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
     with the row scales sg, sv (h3/htrc_flat_triton.py:65-72); store=bfloat16: g and vb bf16,
     sg and sv None; store=float32: g and vb fp32, sg and sv None.  prec="tf32" (the reference's
     PREC) rounds the centres and weights to TF32 for the fp32 and bf16 stores; the int8 and fp8
-    stores always take IEEE fp32 statistics."""
+    stores always take IEEE fp32 statistics.  terms (default): the centres' fp16 operands are made
+    once (htrc_centre_terms) and the statistics read them (htrc_leaf_stats_terms); terms=False
+    runs the per-store entries, which split the centres themselves (the same state, bit for bit)."""
     if store not in (torch.int8, torch.float8_e4m3fn, torch.bfloat16, torch.float32):
         raise ValueError("the HIP leaf statistics store g as int8, float8_e4m3fn, bfloat16 or float32")
     if prec not in ("ieee", "tf32"):
@@ -177,6 +182,22 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
         raise ValueError("keys and values must be [H, nb * leaf, D]")
     nbp = nb_pad(nb)
     dev = mu.device
+    tf32 = prec == "tf32" and store in (torch.bfloat16, torch.float32)
+    if terms:
+        # the centres' fp16 operands once per window (htrc_centre_terms), then the statistics
+        mut = _rows(ws, "mu_terms", h, cn, (MUT_ROW,), torch.int16, dev)
+        call("htrc_centre_terms", ptr(mu), h, nt, c0, cn, d, int(tf32), ptr(mut), stream_handle(dev))
+        code = {torch.int8: 0, torch.bfloat16: 1, torch.float8_e4m3fn: 2, torch.float32: 3}[store]
+        names = {0: ("g", "vb", torch.bfloat16), 1: ("g_bf16", "vb", torch.bfloat16),
+                 2: ("g_fp8", "vb_fp8", torch.float8_e4m3fn), 3: ("g_f32", "vb_f32", torch.float32)}[code]
+        g = _rows(ws, names[0], h, cn, (nbp, d), store, dev)
+        vb = _rows(ws, names[1], h, cn, (nbp, d), names[2], dev)
+        lz = _rows(ws, "lz", h, cn, (nbp,), torch.float32, dev)
+        sg = _rows(ws, "sg", h, cn, (nbp,), torch.float32, dev) if code in (0, 2) else None
+        sv = _rows(ws, "sv", h, cn, (nbp,), torch.float32, dev) if code == 2 else None
+        call("htrc_leaf_stats_terms", ptr(mut), ptr(kf), ptr(vf), h, cn, nk, int(leaf), d, float(scale), code,
+             int(tf32), ptr(g), ptr(sg), ptr(vb), ptr(sv), ptr(lz), stream_handle(dev))
+        return g, lz, vb, sg, sv
     if store in (torch.bfloat16, torch.float32):
         sb = store == torch.bfloat16
         g = _rows(ws, "g_bf16" if sb else "g_f32", h, cn, (nbp, d), store, dev)

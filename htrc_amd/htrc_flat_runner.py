@@ -81,12 +81,14 @@ def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, hea
         per_state = 3 * dim + 8                                         # g8, vb bf16, sg, lz
     else:
         layer += 2 * 2 * rows * dim                                     # q16, dq16
-        per_state = 2 * dim + 12 if store == "fp8" else 4 * dim + 4     # fp8: g, vb, sg, sv, lz; bf16: g, vb, lz
+        # fp8: g, vb, sg, sv, lz; bf16: g, vb, lz; fp32 (the fp32-dot path): g, vb, lz
+        per_state = {"fp8": 2 * dim + 12, "bf16": 4 * dim + 4}.get(store, 8 * dim + 4)
     if pad:
         layer += 4 * queries * dim + 2 * 2 * keys * dim                 # padded copies: q (fp32), k, v (bf16)
     elif not bf16_inputs:
         layer += 2 * 2 * keys * dim                                     # bf16 copies of k and v
     window = gw * nbp * per_state + 4 * gw * kx                         # state, idx
+    window += gw * (2 * 2 * dim + 16)                                   # the centres' fp16 terms
     # the fused route takes up to 8192 near leaves, and 262144 leaves per head (int8; its top-k
     # keys past 16384 in workspace) or 16384 (the 16-bit stores); larger layers run the stage path
     fused = fused and kx <= 8192 and nb <= (262144 if store == "int8" else 16384)

@@ -87,6 +87,19 @@ int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64
                     int64_t cn, int64_t nk, int leaf, int d, float scale, int8_t* g8, float* sg, uint16_t* vb, float* lz,
                     void* stream);
 
+/* The statistics' centre operands computed once per layer window (no reference counterpart: the
+ * reference's stats kernel takes mu as a tl.dot operand directly, h3/htrc_flat_triton.py:52-58):
+ * terms [H, cn, 264] uint16, per centre row c0 + c the fp16 words hi[128] | lo[128] of mu 2^s
+ * (mu rounded to TF32 first when tf32 = 1) and s (int32) with max|mu| 2^s in [2^14, 2^15).
+ * htrc_leaf_stats_terms: the leaf statistics of those cn centres, with the results of the
+ * htrc_leaf_stats* entries (bit for bit) and without their per-group split of mu; store 0 int8
+ * (sg), 1 bf16, 2 fp8 (sg, sv), 3 fp32; tf32 with stores 1 and 3 only, as htrc_leaf_stats_f32. */
+int htrc_centre_terms(const float* mu, int64_t heads, int64_t nt, int64_t c0, int64_t cn, int d, int tf32,
+                      uint16_t* terms, void* stream);
+int htrc_leaf_stats_terms(const uint16_t* terms, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t cn,
+                          int64_t nk, int leaf, int d, float scale, int store, int tf32, void* g, float* sg, void* vb,
+                          float* sv, float* lz, void* stream);
+
 /* Row-max routing score SEL[g, l] over every `stride`-th row of the group's tiles, for the groups
  * [g0, g0 + gn) of every head; nt = tiles per head.
  * Replaces rowmax_select / _rowmax_kernel (h3/htrc_flat_triton.py:315-326, 214-254). */

@@ -208,10 +208,10 @@ def test_runner_modes_and_memory_model():
     # the window state scales with the window: 1024 tiles (1008 real, one window) against two
     # windows of 128 in flight at cfg3
     m128 = htrc_flat_runner.predicted_peak_mib(64512, 64, 128, leaf=64, queries=64512, heads=24, exact_leaves=32)
-    assert mib - m128 == pytest.approx(24 * (1008 - 2 * 128) * (1024 * 392 + 4 * 32) / 2 ** 20, rel=1e-6)
+    assert mib - m128 == pytest.approx(24 * (1008 - 2 * 128) * (1024 * 392 + 4 * 32 + 528) / 2 ** 20, rel=1e-6)
     # S window streams keep min(S, windows) windows in flight: three of 128 tiles, and no more
     # than the two windows of 512 tiles there are
-    per = 24 * 128 * (1024 * 392 + 4 * 32) / 2 ** 20
+    per = 24 * 128 * (1024 * 392 + 4 * 32 + 528) / 2 ** 20
     m3 = htrc_flat_runner.predicted_peak_mib(64512, 64, 128, leaf=64, queries=64512, heads=24, exact_leaves=32,
                                              window_streams=3)
     assert m3 - m128 == pytest.approx(per, rel=1e-6)
@@ -223,7 +223,7 @@ def test_runner_modes_and_memory_model():
     assert htrc_flat_runner.SUPPORTED_MODES == ("fast", "balanced", "accurate", "max")
     # 32-row tiles double the centres: the per-(tile, leaf) state doubles
     m32 = htrc_flat_runner.predicted_peak_mib(64512, 32, 4096, leaf=64, queries=64512, heads=24, exact_leaves=32)
-    assert m32 - mib == pytest.approx(24 * 1008 * (1024 * 392 + 4 * 32) / 2 ** 20, rel=0.02)
+    assert m32 - mib == pytest.approx(24 * 1008 * (1024 * 392 + 4 * 32 + 528) / 2 ** 20, rel=0.02)
     km = htrc_flat_runner.predicted_peak_mib(64512, 64, 1024, leaf=64, queries=64512, heads=24, order="kmeans",
                                              exact_leaves=32)
     assert km - mib == pytest.approx(24 * (8 * 64512 + 4 * 32 * 128) / 2 ** 20)

@@ -893,3 +893,28 @@ def test_route16_on_oracle_state(device, store, tile, leaf, ex, group, stride, h
         assert rp["mismatched"] <= rp["tieable"] and rows_ok.mean() > 0.8
     assert rel_l2(_np(out[0])[rows_ok], ref["out"][rows_ok]) <= OUT_REL_L2
     assert np.abs(_np(logz[0])[rows_ok] - ref["logz"][rows_ok]).max() <= LOGZ_ABS
+
+
+@pytest.mark.parametrize("store,prec", [(torch.int8, "ieee"), (torch.float8_e4m3fn, "ieee"), (torch.bfloat16, "ieee"),
+                                        (torch.bfloat16, "tf32"), (torch.float32, "ieee"), (torch.float32, "tf32")])
+@pytest.mark.parametrize("leaf", [64, 16])
+def test_stats_centre_terms_bit_identical(device, store, prec, leaf):
+    """The statistics from the centres' precomputed fp16 terms (htrc_centre_terms +
+    htrc_leaf_stats_terms) equal those of the per-store entries, which split the centres in the
+    kernel, bit for bit: a window of 40 of 64 centres, the centres scaled by powers of two from
+    2^-40 to 2^30 (and one zero centre), so every exponent path of the split runs."""
+    n = 4096
+    q, k, v = _data(n, seed=leaf + 5)
+    nb = n // leaf
+    mu = torch.from_numpy(flat_i8.tile_centres(q[0].float().numpy(), 64))
+    mu = mu * torch.pow(2.0, torch.arange(-40, 30, 70 / mu.shape[0])[: mu.shape[0], None].floor())
+    mu[7] = 0.0
+    mu = mu[None].to(device).contiguous()
+    kd, vd = k.to(device), v.to(device)
+    a = hip.leaf_stats(mu, kd, vd, nb, 1 / math.sqrt(128), leaf=leaf, store=store, prec=prec, c0=3, cn=40, terms=True)
+    b = hip.leaf_stats(mu, kd, vd, nb, 1 / math.sqrt(128), leaf=leaf, store=store, prec=prec, c0=3, cn=40, terms=False)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert (x is None) == (y is None)
+        if x is not None:
+            assert torch.equal(x.view(torch.uint8), y.view(torch.uint8))
