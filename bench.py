@@ -32,6 +32,7 @@ METRIC = "flat-HTRC layer ms/call @B1 H24 N64512 d128; % MFMA peak, HBM GB/s"
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, GB/s
 PEAK_I8_TOPS = 5000.0          # dense int8 MFMA, TOP/s
 PEAK_BF16_TFLOPS = 2500.0      # dense bf16 MFMA, TFLOP/s
+PEAK_F32_TFLOPS = 157.3        # dense fp32 MFMA, TFLOP/s
 
 
 def algorithmic(h, nq, nk, leaf, kx, d=128, tile=64, store="int8"):
@@ -75,6 +76,141 @@ def algorithmic(h, nq, nk, leaf, kx, d=128, tile=64, store="int8"):
     f["near_field"] = {"bytes": h * (nt * kx * per_state + 2 * rows * row + kx * leaf * tok + nt * kx * 4 + rows * 4
                                      + 4 * nq * (d + 1)), **ops(near_ops)}
     return f
+
+
+def algorithmic_f32(h, nq, nk, leaf, kx, d=128, tile=64, splits=4):
+    """Per-launch algorithmic HBM bytes and fp32 MFMA flops of the fp32-dot path's stages (the
+    reference's default store="fp32" with fp32 dots): the state per (tile, leaf) is g and vb fp32
+    (8d bytes) + lz 4; q rows fp32 (4d), k / v bf16 (4d per token, once per head); the tile
+    launch's far field 2 x 2d flops per row and leaf (score, PV), its near field 2 x 2d per row
+    and near token; the select 2d per row and leaf."""
+    nt = -(-nq // tile)
+    nb = nk // leaf
+    rows = nt * tile
+    kx = min(kx, nb)
+    state = nt * nb * (8 * d + 4)
+    f = {"stats": {"bytes": h * (4 * nk * d + state + nt * (4 * d + 16))},
+         "select": {"bytes": h * (nt * nb * (4 * d + 4) + 4 * nq * d + 4 * nt * d), "f32_flops": h * 2 * rows * nb * d},
+         "topk": {"bytes": h * (nt * nb * 5 + nt * kx * 4)},
+         "tile": {"bytes": h * (state + 4 * nq * d + 4 * nk * d + nt * nb + nt * kx * 4 + 4 * nq * (d + 1)
+                                + 2 * splits * rows * (d + 2) * 4),
+                  "f32_flops": h * (4 * rows * nb * d + 4 * rows * kx * leaf * d)}}
+    return f
+
+
+def calib_copy(dev):
+    """One copy-shaped elementwise kernel (bitwise_not over 1 GiB int32: reads 1 GiB once, writes
+    1 GiB once), the scale of the FETCH_SIZE / WRITE_SIZE counters in the profiles."""
+    import torch
+    src = torch.empty(1 << 28, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.bitwise_not(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def main_f32(a):
+    """The fp32-dot path (store="fp32": the reference's default triton store, fp32 state and fp32
+    dots, IEEE or TF32 operands by --precision): the layer in the reference's stage structure
+    (statistics, select, top-k, split tile + merge) timed like the int8 layer, and each stage's
+    launches back to back."""
+    import torch
+    from htrc_amd import htrc_flat, htrc_flat_hip as hip, htrc_flat_runner, workloads
+    dev = torch.device("cuda:0")
+    q, k, v, leaf, ex = workloads.make(a.config, seed=0, device=dev)
+    h, nq, d = (int(x) for x in q.shape)
+    nk = int(k.shape[1])
+    nb = nk // leaf
+    kx = min(ex, nb)
+    prec = "tf32" if a.precision == "tf32" else "ieee"
+    splits = 4
+    chunk = htrc_flat_runner.plan_chunk(torch.cuda.mem_get_info(dev)[0], nk, 64, splits=splits, leaf=leaf, queries=nq,
+                                        heads=h, exact_leaves=kx, graph=False, store="fp32", fused=False)
+    kw = dict(backend="triton", store="fp32", dot="tf32", precision=a.precision, leaf=leaf, exact_leaves=ex,
+              tile_chunk=chunk, splits=splits)
+    ws = {}
+    scale = 1.0 / math.sqrt(d)
+    ms = None
+    if not a.kernel:
+        for _ in range(a.warmup):
+            htrc_flat.flat_attention(q, k, v, ws=ws, **kw)
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(a.steps):
+            out = htrc_flat.flat_attention(q, k, v, ws=ws, **kw)
+        ev1.record()
+        torch.cuda.synchronize()
+        ms = ev0.elapsed_time(ev1) / a.steps
+        assert torch.isfinite(out).all().item(), "non-finite output"
+        del out
+    ws.clear()
+    # stages of one window holding the whole layer (when it fits; else the first window's tiles)
+    mu, _, _ = hip.pack_q16(q, ws=ws, dq_fp16=False)
+    kb, vb = k.contiguous(), v.contiguous()
+    ng = int(mu.shape[1])
+    gn = min(ng, chunk)
+    g, lz, vbs, _, _ = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=torch.float32, ws=ws, cn=gn, prec=prec)
+    st = {"g8": g, "lz": lz, "vb": vbs, "sg": None, "sv": None}
+    sel = hip.select_f32(q, mu, g, lz, nb, prec=prec, ws=ws)
+    idx, excl = hip.topk_excl(sel, nb, kx, 0, ws=ws)
+    sws = {}
+    stages = {
+        "stats": lambda: hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=torch.float32, ws=sws, cn=gn, prec=prec),
+        "select": lambda: hip.select_f32(q, mu, g, lz, nb, prec=prec, ws=sws),
+        "topk": lambda: hip.topk_excl(sel, nb, kx, 0, ws=sws),
+        "tile": lambda: hip.tile_f32(q, mu, st, excl, idx, kb, vb, nq=nq, leaf=leaf, scale=scale, splits=splits, ws=sws,
+                                     prec=prec),
+    }
+    if a.kernel:
+        fn = stages[a.kernel]
+        for _ in range(a.kernel_reps):
+            fn()
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel": a.kernel, "launches": a.kernel_reps}), flush=True)
+        return
+    stream = torch.cuda.current_stream(dev)
+    kms = {}
+    for name, fn in stages.items():
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(a.kernel_reps):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        kms[name] = e0.elapsed_time(e1) / a.kernel_reps
+    if a.calib_copy:
+        calib_copy(dev)
+    frac = gn / ng                                    # the stages ran over gn of the ng tiles
+    figs = algorithmic_f32(h, nq, nk, leaf, kx, d, splits=splits)
+    kernels = {}
+    for n, t in kms.items():
+        e = {"kernel": n, "ms": round(t, 4)}
+        gbs = figs[n]["bytes"] * frac / (t * 1e-3) / 1e9
+        e["hbm_GBps"] = round(gbs, 1)
+        e["hbm_frac"] = round(gbs / PEAK_HBM_GBS, 4)
+        if "f32_flops" in figs[n]:
+            tf = figs[n]["f32_flops"] * frac / (t * 1e-3) / 1e12
+            e["f32_TFLOPs"] = round(tf, 2)
+            e["mfma_frac"] = round(tf / PEAK_F32_TFLOPS, 4)
+        kernels[n] = e
+    dom = kernels["tile"]
+    roof = {"bound": "mfma", "achieved": dom["f32_TFLOPs"], "peak": PEAK_F32_TFLOPS, "unit": "TFLOP/s",
+            "frac": dom["mfma_frac"], "traffic": None, "kernel": "tile",
+            "note": "fp32 MFMA (v_mfma_f32_16x16x4_f32) flops of the far and near fields"}
+    res = {"metric": f"flat-HTRC layer ms/call @B1 H{h} N{nq} d{d} ({a.config}, store=fp32, {prec} dots)",
+           "value": round(ms, 4), "unit": "ms/call", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+           "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f32" if prec == "ieee" else "tf32 operands, f32 accumulate",
+           "data": "synthetic: clustered spatiotemporal regions, seed 0, generated on device",
+           "config": {"workload": f"{a.config}: B=1 H={h} N={nq} d={d} leaf={leaf} near={kx} tile=64 store=fp32 "
+                                  f"precision={a.precision} splits={splits}", "tile_chunk": chunk,
+                      "stage_tiles": gn},
+           "roofline": roof, "kernels": kernels}
+    print(json.dumps(res), flush=True)
 
 
 def measured_traffic(config, store="int8"):
@@ -343,15 +479,19 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5"])
-    ap.add_argument("--store", default="int8", choices=["int8", "fp8", "bf16"],
-                    help="leaf-state store of the layer (BASELINE's metric is quoted on int8)")
+    ap.add_argument("--store", default="int8", choices=["int8", "fp8", "bf16", "fp32"],
+                    help="leaf-state store of the layer (BASELINE's metric is quoted on int8); fp32: the "
+                         "reference's default fp32-dot path, timed in its stage structure")
+    ap.add_argument("--precision", default="fp32", choices=["fp32", "tf32"],
+                    help="--store fp32: IEEE fp32 (the reference's default) or TF32 dot operands")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--calls", type=int, default=50, help="cfg5: sequential layer calls")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=None,
                     help="heads of the CPU baseline pass (default: the whole layer)")
     ap.add_argument("--kernel", default=None,
-                    choices=["pack_q", "pack_k", "stats", "route_select", "route_attend", "far_field", "near_field"],
+                    choices=["pack_q", "pack_k", "stats", "route_select", "route_attend", "far_field", "near_field",
+                             "select", "topk", "tile"],
                     help="run only this stage's launches (--kernel-reps of them), for rocprofv3 counter passes")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also launch one copy-shaped 1 GiB kernel (the scale of the FETCH_SIZE/WRITE_SIZE counters)")
@@ -367,6 +507,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     if a.config == "cfg5":
         return main_cfg5(a)
+    if a.store == "fp32":
+        return main_f32(a)
     dev = torch.device("cuda:0")
     q, k, v, leaf, ex = workloads.make(a.config, seed=0, device=dev)
     h, nq, d = (int(x) for x in q.shape)
@@ -461,13 +603,7 @@ def main():
         e1.synchronize()
         kms[name] = e0.elapsed_time(e1) / a.kernel_reps
     if a.calib_copy:
-        # copy-shaped elementwise kernel: reads 1 GiB once, writes 1 GiB once
-        src = torch.empty(1 << 28, dtype=torch.int32, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        torch.bitwise_not(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
+        calib_copy(dev)
     figs = algorithmic(h, nq, nk, leaf, kx, d, store=store)
     kernels = {n: roofline_entry(n, kms[n], figs[n]) for n in stages}
     peaks = measured_peaks(dev)

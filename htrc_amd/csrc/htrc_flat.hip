@@ -1658,12 +1658,26 @@ __device__ __forceinline__ void load_f32(const void* p, float (&x)[N]) {
 }
 
 // S^T tile of 16 keys x 16 rows: item i of lane l = sum over dims of key (4 (l/16) + i)'s A row
-// and row l%16's B row, from the 32 dims each lane holds of both.
+// and row l%16's B row, from the 32 dims each lane holds of both.  NC independent accumulation
+// chains (steps s = NC j + c into chain c, added at the end): with four the select kernel's
+// products no longer wait on each other (5.92 -> 5.55 ms at cfg3; the tile kernel, whose value
+// products sit between its score products, is no faster with them).
+template <int NC = 1>
 __device__ __forceinline__ f32x4 dot_tile_f32(const float (&a)[32], const float (&b)[32]) {
-    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+    f32x4 c[NC];
 #pragma unroll
-    for (int s = 0; s < 32; ++s) c = mfma_f32(a[s], b[s], c);
-    return c;
+    for (int j = 0; j < NC; ++j) c[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 32; ++s) c[s % NC] = mfma_f32(a[s], b[s], c[s % NC]);
+    if constexpr (NC == 4) {
+        f32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = __fadd_rn(__fadd_rn(c[0][i], c[1][i]), __fadd_rn(c[2][i], c[3][i]));
+        return r;
+    } else {
+        static_assert(NC == 1, "dot_tile_f32: one or four chains");
+        return c[0];
+    }
 }
 
 struct RowF32 {        // running softmax state of one row (h3/htrc_flat_triton.py:142-157)
@@ -1685,10 +1699,13 @@ __device__ __forceinline__ void f32_update(RowF32& st, const float (&sc)[4], con
     for (int i = 0; i < 4; ++i) p[i] = __expf(__fsub_rn(sc[i], ms));
     const float alpha = __expf(__fsub_rn(st.m, ms));
     st.l = __fadd_rn(__fmul_rn(st.l, alpha), __fadd_rn(__fadd_rn(p[0], p[1]), __fadd_rn(p[2], p[3])));
+    // O alpha: skipped when every row's alpha is 1 (no running maximum moved: the same bits)
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-    for (int db = 0; db < 8; ++db)
+        for (int db = 0; db < 8; ++db)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st.o[db][i] = __fmul_rn(st.o[db][i], alpha);
+            for (int i = 0; i < 4; ++i) st.o[db][i] = __fmul_rn(st.o[db][i], alpha);
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         const float ps = TF32 ? tf32_rna(p[s]) : p[s];
@@ -1704,7 +1721,7 @@ __device__ __forceinline__ void f32_update(RowF32& st, const float (&sc)[4], con
 // its key rows itself (the tile's waves share them in L2).  ns == 1 (pacc null): normalised rows
 // and logz = m + log l; else the partial (m, l, O) for merge_kernel.
 template <bool QBF, bool SB, bool TF32>
-__global__ __launch_bounds__(256) void tile_f32_kernel(
+__global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     const void* __restrict__ q, const float* __restrict__ mu, int mu_stride, const void* __restrict__ g,
     const float* __restrict__ lz, const void* __restrict__ vb, const int8_t* __restrict__ excl,
     const int32_t* __restrict__ idx, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int64_t nq,
@@ -1748,11 +1765,15 @@ __global__ __launch_bounds__(256) void tile_f32_kernel(
         float ga[32];
         load_f32<32, SB, TF32>(gb + ((srow + min(c0 + col, hi - 1)) * D + 32 * grp) * SBB, ga);
         const f32x4 s4 = dot_tile_f32(ga, dq);
+        // leaves c0 + 4 grp .. + 3: exclusion bytes and lz of the padded row (nb_pad is a
+        // multiple of 32 and c0 of 16, so they lie inside it; leaves >= hi are masked)
+        const uint32_t ex4 = *(const uint32_t*)(excl + srow + c0 + 4 * grp);
+        const f32x4 lz4 = *(const f32x4*)(lz + srow + c0 + 4 * grp);
         float sc[4], va[4][8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = c0 + 4 * grp + i, cc = min(c, hi - 1);
-            sc[i] = (c < hi && excl[srow + cc] == 0) ? __fadd_rn(s4[i], lz[srow + cc]) : -INFINITY;
+            sc[i] = (c < hi && ((ex4 >> (8 * i)) & 0xffu) == 0) ? __fadd_rn(s4[i], lz4[i]) : -INFINITY;
             load_f32<8, SB, TF32>(vbb + ((srow + cc) * D + 8 * col) * SBB, va[i]);
         }
         f32_update<TF32>(st, sc, va);
@@ -1763,16 +1784,19 @@ __global__ __launch_bounds__(256) void tile_f32_kernel(
     const int64_t kh = (int64_t)h * nk;
     const int32_t* ix = idx + gs * (int64_t)(kx > 0 ? kx : 1);
     for (int e0 = e_lo; e0 < e_hi; e0 += 16) {
-        const int ja = min(e0 + col, e_hi - 1);
+        // the block's 16 tokens lie in one leaf (leaf, e_lo and the split length are multiples
+        // of 16): one wave-uniform base; positions past e_hi repeat its last token
+        const int64_t tok0 = kh + (int64_t)ix[e0 / leaf] * leaf + e0 % leaf;
+        const int last = e_hi - 1 - e0;
         float ka[32];
-        load_f32<32, true, false>(k + (kh + (int64_t)ix[ja / leaf] * leaf + ja % leaf) * D + 32 * grp, ka);
+        load_f32<32, true, false>(k + (tok0 + min(col, last)) * D + 32 * grp, ka);
         const f32x4 s4 = dot_tile_f32(ka, qx);
         float sc[4], va[4][8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int j = e0 + 4 * grp + i, jj = min(j, e_hi - 1);
-            sc[i] = j < e_hi ? __fmul_rn(s4[i], scale) : -INFINITY;
-            load_f32<8, true, false>(v + (kh + (int64_t)ix[jj / leaf] * leaf + jj % leaf) * D + 8 * col, va[i]);
+            const int j = 4 * grp + i;
+            sc[i] = j <= last ? __fmul_rn(s4[i], scale) : -INFINITY;
+            load_f32<8, true, false>(v + (tok0 + min(j, last)) * D + 8 * col, va[i]);
         }
         f32_update<TF32>(st, sc, va);
     }
@@ -1850,7 +1874,7 @@ __global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict_
         }
 #pragma unroll
         for (int lb = 0; lb < 4; ++lb) {
-            const f32x4 s4 = dot_tile_f32(ga[lb], dq);
+            const f32x4 s4 = dot_tile_f32<4>(ga[lb], dq);
 #pragma unroll
             for (int i = 0; i < 4; ++i) best[lb][i] = fmaxf(best[lb][i], s4[i]);
         }
