@@ -95,6 +95,8 @@ def algorithmic_f32(h, nq, nk, leaf, kx, d=128, tile=64, splits=4):
          "tile": {"bytes": h * (state + 4 * nq * d + 4 * nk * d + nt * nb + nt * kx * 4 + 4 * nq * (d + 1)
                                 + 2 * splits * rows * (d + 2) * 4),
                   "f32_flops": h * (4 * rows * nb * d + 4 * rows * kx * leaf * d)}}
+    if splits == 1:                                   # no split partials
+        f["tile"]["bytes"] -= h * 2 * rows * (d + 2) * 4
     return f
 
 
@@ -146,11 +148,14 @@ def main_f32(a):
         assert torch.isfinite(out).all().item(), "non-finite output"
         del out
     ws.clear()
-    # stages of one window holding the whole layer (when it fits; else the first window's tiles)
+    # stages of one window holding the whole layer (when it fits; else the first window's tiles);
+    # the tile launch split as the operator splits it (unsplit for windows of many tiles)
     mu, _, _ = hip.pack_q16(q, ws=ws, dq_fp16=False)
     kb, vb = k.contiguous(), v.contiguous()
     ng = int(mu.shape[1])
     gn = min(ng, chunk)
+    if h * gn >= htrc_flat_runner.F32_UNSPLIT_TILES:
+        splits = 1
     g, lz, vbs, _, _ = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=torch.float32, ws=ws, cn=gn, prec=prec)
     st = {"g8": g, "lz": lz, "vb": vbs, "sg": None, "sv": None}
     sel = hip.select_f32(q, mu, g, lz, nb, prec=prec, ws=ws)

@@ -29,6 +29,7 @@ import torch
 
 from . import htrc_flat_hip as hip
 from ._lib import nb_pad
+from .htrc_flat_runner import F32_UNSPLIT_TILES
 
 
 def fake_quant(x, fmt, group=0):
@@ -216,7 +217,8 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     over S = ``kern['window_streams']`` streams, default 2; S = 1 keeps one), and the result does not
     depend on it.  ``dot`` other than "bf16" runs fp32 dots over an fp32 (``store="fp32"``, the
     reference's default) or bf16 state in the reference's stage structure, with IEEE operands or,
-    for ``precision="tf32"``, TF32 ones (h3/htrc_flat.py:122-123, 196-212); the dot="bf16" paths
+    for ``precision="tf32"``, TF32 ones (h3/htrc_flat.py:122-123, 196-212), its tile kernel
+    unsplit when a window holds F32_UNSPLIT_TILES (head, tile) pairs or more; the dot="bf16" paths
     always compute their leaf statistics at IEEE fp32.  ``state``, if a dict, receives the packed
     operands and the whole layer's leaf state and routing (for checks)."""
     kern = dict(kern or {})
@@ -328,7 +330,11 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
                 excl.zero_()
             tick("select")
             if f32dots:
-                hip.tile_f32(qsrc, mu, lstate, excl, idx, kb, vb, nq=nq, leaf=leaf, scale=scale, splits=splits,
+                # splits is a launch parameter: a window whose tiles alone fill the device runs
+                # unsplit, with no merge launch (the result differs by the merge's rounding only)
+                ntw = min(-(-nq // tile), (g0 + gn) * group) - g0 * group
+                fs = 1 if h * ntw >= F32_UNSPLIT_TILES else splits
+                hip.tile_f32(qsrc, mu, lstate, excl, idx, kb, vb, nq=nq, leaf=leaf, scale=scale, splits=fs,
                              bn=int(kern.get("tile_bn", 32)), ws=w, out=out, logz=logz, group=group, perm=perm,
                              tile=tile, g0=g0, prec=prec)
             else:

@@ -57,14 +57,21 @@ def _ceil(a: int, b: int) -> int:
     return -(-int(a) // int(b))
 
 
+# fp32-dot path: windows of at least this many (head, tile) pairs run the tile kernel unsplit
+# (one 4-wave workgroup each; 2048 fill the 256 CUs eight times over), with no split partials or
+# merge: cfg3's tile stage 24.4 ms with four splits and their merge, 23.1 ms unsplit.
+F32_UNSPLIT_TILES = 2048
+
+
 def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, heads: int = 1, splits: int = 1,
                     kx: int = 0, group: int = 1, order: str = "seq", tile: int = TILE, tile_chunk: int | None = None,
-                    store: str = "int8", fused: bool = True, bf16_inputs: bool = True, window_streams: int = 2) -> int:
+                    store: str = "int8", fused: bool = True, bf16_inputs: bool = True, window_streams: int = 2,
+                    f32dots: bool = False) -> int:
     """Device bytes of one operator call's workspace: the whole layer's packed operands and
     outputs, and the per-(centre, leaf) state, routing and partials of the tile windows of
     ``tile_chunk`` tiles (all tiles when None) in flight: one, or min(S, windows) when there are
     several windows and the operator deals them over S = kern["window_streams"] streams (2 by
-    default)."""
+    default).  ``f32dots``: the fp32-dot path (always so for store="fp32")."""
     pad = int(dim) < 128                 # head dims below 128 run at 128 on zero-padded copies
     dim = 128 if pad else int(dim)
     nt = _ceil(queries, tile)
@@ -98,7 +105,8 @@ def workspace_bytes(queries: int, keys: int, leaf: int = 16, dim: int = 128, hea
         window += 4 * gw * nbp                                          # route_select top-k keys
     if not fused:
         window += gw * nbp * 5                                          # sel, excl
-        if splits > 1:
+        unsplit = (f32dots or store == "fp32") and int(heads) * tw >= F32_UNSPLIT_TILES
+        if splits > 1 and not unsplit:
             window += tw * int(splits) * int(tile) * (dim + 2) * 4      # split partials
     if order == "kmeans":
         layer += 8 * queries + 4 * 32 * dim                             # perm, assignments, centres

@@ -176,6 +176,31 @@ def test_flat_attention_fp32_dots_vs_oracle(device, store, precision, kw):
                     f"flat_f32[{store},{precision},{sorted(kw)}]")
 
 
+@pytest.mark.parametrize("store,tile_chunk", [("fp32", None), ("bf16", 5)])
+def test_fp32_dots_unsplit_tile_windows(device, monkeypatch, store, tile_chunk):
+    """Windows of F32_UNSPLIT_TILES (head, tile) pairs or more run the fp32 tile kernel unsplit,
+    writing the rows directly: the threshold lowered so that this layer's windows (one, or
+    windows of 5 tiles over two streams) run unsplit, against the oracle head by head and
+    against the same call split in four with its merge (the merge's rounding apart)."""
+    h, n, nk, leaf, ex = 2, 1200, 2048, 64, 3
+    q, k, v = _data(n, nk, seed=31, heads=h)
+    kw = dict(backend="triton", store=store, dot="tf32", leaf=leaf, exact_leaves=ex, splits=4, tile_chunk=tile_chunk,
+              return_logz=True)
+    split_out, split_lz = htrc_flat.flat_attention(q.to(device), k.to(device), v.to(device), **kw)
+    monkeypatch.setattr(htrc_flat, "F32_UNSPLIT_TILES", 1)
+    gst: dict = {}
+    out, logz = htrc_flat.flat_attention(q.to(device), k.to(device), v.to(device), state=gst, **kw)
+    torch.cuda.synchronize()
+    assert rel_l2(_np(out), _np(split_out)) <= 1e-6
+    assert float((logz - split_lz).abs().max()) <= 1e-5
+    for hh in range(h):
+        ref = flat_f32.flat_f32(q[hh].float().numpy(), k[hh].float().numpy(), v[hh].float().numpy(), tile=64,
+                                leaf=leaf, exact_leaves=ex, store=store)
+        one = {"idx": gst["idx"][hh:hh + 1], "excl": gst["excl"][hh:hh + 1]}
+        _check_operator(_np(out[hh]), _np(logz[hh]), one, ref, "ieee", q[hh:hh + 1], k[hh:hh + 1], v[hh:hh + 1], 64,
+                        leaf, 1, f"flat_f32[unsplit,{store},{tile_chunk}]")
+
+
 def test_reference_default_call(device):
     """flat_attention(q, k, v, backend="triton") with every other knob at the reference's default
     (tile 64, 64 exact leaves, leaf 16, store fp32, dot tf32, precision fp32, splits 8)."""
