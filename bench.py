@@ -551,6 +551,11 @@ def main():
     # measured 8.27 against 8.04 ms at cfg3)
     if not a.kernel:
         ms_prod_windows, _ = layer_ms({**kw, "tile_chunk": htrc_flat.PROD["tile_chunk"]}, max(5, a.steps // 2), 2)
+    # the same layer at PROD's precision="tf32": the leaf statistics on TF32 operands, as the
+    # reference's PROD computes them (the value above keeps the default IEEE fp32 statistics)
+    ms_tf32 = None
+    if not a.kernel:
+        ms_tf32, _ = layer_ms({**kw, "precision": "tf32"}, max(5, a.steps // 2), 2)
     ws.clear()
 
     # per-kernel launch durations, HIP events on the stream the kernels are launched on
@@ -653,6 +658,7 @@ def main():
                       "heads": h, "queries": nq, "keys": nk, "leaf": leaf, "near_leaves": kx, "tile_chunk": chunk,
                       "store": store},
            "ms_tile_chunk_128": round(ms_prod_windows, 4),
+           "ms_precision_tf32": round(ms_tf32, 4),
            "roofline": roof, "kernels": kernels, "measured_peaks": peaks}
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(a.config, a.cpu_heads)

@@ -3998,14 +3998,17 @@ int htrc_leaf_stats_terms(const uint16_t* terms, const uint16_t* k, const uint16
     const char* who = "htrc_leaf_stats_terms";
     REQUIRE(terms, "htrc_leaf_stats_terms: null terms");
     REQUIRE(store >= 0 && store <= 3, "htrc_leaf_stats_terms: store must be 0 (int8), 1 (bf16), 2 (fp8) or 3 (fp32)");
-    REQUIRE(!tf32 || store == 1 || store == 3, "htrc_leaf_stats_terms: TF32 operands go with the bf16 and fp32 stores");
     switch (store) {
         case 0:
-            return leaf_stats_launch<0>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g, sg, vb, nullptr,
-                                        lz, stream);
+            return tf32 ? leaf_stats_launch<0, true>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g, sg,
+                                                     vb, nullptr, lz, stream)
+                        : leaf_stats_launch<0>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g, sg, vb,
+                                               nullptr, lz, stream);
         case 2:
-            return leaf_stats_launch<2>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g, sg, vb, sv, lz,
-                                        stream);
+            return tf32 ? leaf_stats_launch<2, true>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g, sg,
+                                                     vb, sv, lz, stream)
+                        : leaf_stats_launch<2>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g, sg, vb, sv,
+                                               lz, stream);
         case 1:
             return tf32 ? leaf_stats_launch<1, true>(who, nullptr, terms, k, v, heads, cn, 0, cn, nk, leaf, d, scale, g,
                                                      nullptr, vb, nullptr, lz, stream)

@@ -218,9 +218,11 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
     depend on it.  ``dot`` other than "bf16" runs fp32 dots over an fp32 (``store="fp32"``, the
     reference's default) or bf16 state in the reference's stage structure, with IEEE operands or,
     for ``precision="tf32"``, TF32 ones (h3/htrc_flat.py:122-123, 196-212), its tile kernel
-    unsplit when a window holds F32_UNSPLIT_TILES (head, tile) pairs or more; the dot="bf16" paths
-    always compute their leaf statistics at IEEE fp32.  ``state``, if a dict, receives the packed
-    operands and the whole layer's leaf state and routing (for checks)."""
+    unsplit when a window holds F32_UNSPLIT_TILES (head, tile) pairs or more.  Every store's leaf
+    statistics take TF32 operands for ``precision="tf32"`` (PROD's setting), as the reference's
+    leaf_stats takes PREC for every store (h3/htrc_flat.py:243-245), and IEEE fp32 ones otherwise.
+    ``state``, if a dict, receives the packed operands and the whole layer's leaf state and routing
+    (for checks)."""
     kern = dict(kern or {})
     _validate(q, k, v, tile, order, curvature, leaf, select, backend, store, dot, quant, tail, kern)
     squeeze = q.dim() == 2
@@ -299,7 +301,7 @@ def flat_attention(q, k, v, *, tile=64, exact_leaves=64, order="seq", curvature=
         """Statistics, select / top-k and attention of the tile groups [g0, g0 + gn), the window's
         buffers in workspace w."""
         g, lz, vbs, sg, sv = hip.leaf_stats(mu, kb, vb, nb, scale, leaf=leaf, store=sdt, ws=w, c0=g0, cn=gn,
-                                            prec=prec if f32dots else "ieee")
+                                            prec=prec)
         if quant.get("state"):                           # h3/htrc_flat.py:246-248, in place
             sfmt = quant["state"]
             sgsz = hip.D if not qg and sfmt != "fp4" else (qg or 16)

@@ -161,10 +161,11 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
     store=int8: g int8 [H,cn,nbp,D], vb bf16, sv None; store=float8_e4m3fn: g and vb e4m3
     with the row scales sg, sv (h3/htrc_flat_triton.py:65-72); store=bfloat16: g and vb bf16,
     sg and sv None; store=float32: g and vb fp32, sg and sv None.  prec="tf32" (the reference's
-    PREC) rounds the centres and weights to TF32 for the fp32 and bf16 stores; the int8 and fp8
-    stores always take IEEE fp32 statistics.  terms (default): the centres' fp16 operands are made
-    once (htrc_centre_terms) and the statistics read them (htrc_leaf_stats_terms); terms=False
-    runs the per-store entries, which split the centres themselves (the same state, bit for bit)."""
+    PREC, which its leaf_stats takes for every store) rounds the centres and weights to TF32.
+    terms (default): the centres' fp16 operands are made once (htrc_centre_terms) and the
+    statistics read them (htrc_leaf_stats_terms); terms=False runs the per-store entries, which
+    split the centres themselves (the same state, bit for bit; TF32 there for the bf16 and fp32
+    stores only)."""
     if store not in (torch.int8, torch.float8_e4m3fn, torch.bfloat16, torch.float32):
         raise ValueError("the HIP leaf statistics store g as int8, float8_e4m3fn, bfloat16 or float32")
     if prec not in ("ieee", "tf32"):
@@ -182,7 +183,9 @@ def leaf_stats(mu, kf, vf, nb, scale, leaf=16, prec="ieee", bt=16, bl=4, warps=4
         raise ValueError("keys and values must be [H, nb * leaf, D]")
     nbp = nb_pad(nb)
     dev = mu.device
-    tf32 = prec == "tf32" and store in (torch.bfloat16, torch.float32)
+    tf32 = prec == "tf32"
+    if tf32 and not terms and store in (torch.int8, torch.float8_e4m3fn):
+        raise ValueError("TF32 statistics of the int8 and fp8 stores run through the centre terms (terms=True)")
     if terms:
         # the centres' fp16 operands once per window (htrc_centre_terms), then the statistics
         mut = _rows(ws, "mu_terms", h, cn, (MUT_ROW,), torch.int16, dev)

@@ -93,7 +93,9 @@ int htrc_leaf_stats(const float* mu, const uint16_t* k, const uint16_t* v, int64
  * (mu rounded to TF32 first when tf32 = 1) and s (int32) with max|mu| 2^s in [2^14, 2^15).
  * htrc_leaf_stats_terms: the leaf statistics of those cn centres, with the results of the
  * htrc_leaf_stats* entries (bit for bit) and without their per-group split of mu; store 0 int8
- * (sg), 1 bf16, 2 fp8 (sg, sv), 3 fp32; tf32 with stores 1 and 3 only, as htrc_leaf_stats_f32. */
+ * (sg), 1 bf16, 2 fp8 (sg, sv), 3 fp32.  tf32 = 1 (the reference's PREC "tf32", which its
+ * leaf_stats applies for every store, h3/htrc_flat.py:243-245): the terms made with tf32 = 1, and
+ * the softmax weights rounded to TF32 before their products. */
 int htrc_centre_terms(const float* mu, int64_t heads, int64_t nt, int64_t c0, int64_t cn, int d, int tf32,
                       uint16_t* terms, void* stream);
 int htrc_leaf_stats_terms(const uint16_t* terms, const uint16_t* k, const uint16_t* v, int64_t heads, int64_t cn,

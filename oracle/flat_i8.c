@@ -35,7 +35,7 @@
  * (h3/htrc_flat.py:217, h3/htrc_flat_triton.py:76,112,115,231). */
 static const float R127 = 1.0f / 127.0f;
 
-int oracle_abi_version(void) { return 5; }
+int oracle_abi_version(void) { return 6; }
 
 float oracle_r127(void) { return R127; }
 
@@ -175,14 +175,28 @@ void oracle_pack_q(const float *q, int64_t n, int d, int tile, int group, const 
  *   am = max(max|g|, 1e-30); sg = am * fp32(1/127); g8 = round_away(g * (127 / am))
  *   vb stored as bf16 (RNE).
  * Dots are sequential fp32 sums (dims for a, leaf tokens for g / vb). */
+/* TF32 operand (h3/htrc_flat_triton.py's dots with input_precision="tf32"): 10 explicit mantissa
+ * bits, to nearest with ties away from zero; infinities and NaN unchanged. */
+static inline float tf32_rna(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) != 0x7f800000u) u = (u + 0x1000u) & 0xffffe000u;
+    memcpy(&x, &u, 4);
+    return x;
+}
+
 /* The fp32 leaf state of centre m_ and leaf rows K, V (bf16): g (scaled) in gs, vb in vs,
- * returning max a and z through mx, z.  a, kf are work arrays of leaf and leaf * d floats. */
+ * returning max a and z through mx, z.  a, kf are work arrays of leaf and leaf * d floats.
+ * tf32: the dots take TF32 operands (PREC "tf32"): the centre and the normalised weights are
+ * rounded first (k and v, bf16, are TF32 values already). */
 static void leaf_state(const float *m_, const uint16_t *K, const uint16_t *V, int leaf, int d, float scale,
-                       float *a, float *kf, float *gs, float *vs, float *mx_out, float *z_out) {
+                       int tf32, float *a, float *kf, float *gs, float *vs, float *mx_out, float *z_out) {
     for (int s = 0; s < leaf * d; ++s) kf[s] = bf2f(K[s]);
     for (int s = 0; s < leaf; ++s) a[s] = 0.0f;
-    for (int i = 0; i < d; ++i)          /* a[s] summed over i in order, vectorised over s */
-        for (int s = 0; s < leaf; ++s) a[s] += m_[i] * kf[s * d + i];
+    for (int i = 0; i < d; ++i) {        /* a[s] summed over i in order, vectorised over s */
+        const float mi = tf32 ? tf32_rna(m_[i]) : m_[i];
+        for (int s = 0; s < leaf; ++s) a[s] += mi * kf[s * d + i];
+    }
     float mx = -INFINITY;
     for (int s = 0; s < leaf; ++s) {
         a[s] = a[s] * scale;
@@ -193,7 +207,7 @@ static void leaf_state(const float *m_, const uint16_t *K, const uint16_t *V, in
         a[s] = expf(a[s] - mx);
         z += a[s];
     }
-    for (int s = 0; s < leaf; ++s) a[s] = a[s] / z;
+    for (int s = 0; s < leaf; ++s) a[s] = tf32 ? tf32_rna(a[s] / z) : a[s] / z;
     for (int i = 0; i < d; ++i) gs[i] = vs[i] = 0.0f;
     for (int s = 0; s < leaf; ++s)       /* summed over tokens in order, vectorised over dims */
         for (int i = 0; i < d; ++i) {
@@ -206,7 +220,7 @@ static void leaf_state(const float *m_, const uint16_t *K, const uint16_t *V, in
 }
 
 void oracle_stats(const float *mu, int64_t nt, const uint16_t *k, const uint16_t *v,
-                  int64_t nb, int leaf, int d, float scale,
+                  int64_t nb, int leaf, int d, float scale, int tf32,
                   int8_t *g8, float *sg, uint16_t *vb, float *lz) {
 #pragma omp parallel
     {
@@ -218,7 +232,7 @@ void oracle_stats(const float *mu, int64_t nt, const uint16_t *k, const uint16_t
         for (int64_t tl_ = 0; tl_ < nt * nb; ++tl_) {
             int64_t t = tl_ / nb, l = tl_ % nb;
             float mx, z;
-            leaf_state(mu + t * d, k + l * leaf * d, v + l * leaf * d, leaf, d, scale, a, kf, gs, vs, &mx, &z);
+            leaf_state(mu + t * d, k + l * leaf * d, v + l * leaf * d, leaf, d, scale, tf32, a, kf, gs, vs, &mx, &z);
             float am = 0.0f;
             for (int i = 0; i < d; ++i) {
                 float x = fabsf(gs[i]);
@@ -271,7 +285,7 @@ float oracle_e4m3_to_f32(uint8_t b) {
 /* Leaf statistics with the fp8 state store, h3/htrc_flat_triton.py:65-72:
  *   sg = max(max|g| * fp32(1/448), 1e-30), g code = e4m3(g / sg); sv, vb code likewise. */
 void oracle_stats_fp8(const float *mu, int64_t nt, const uint16_t *k, const uint16_t *v,
-                      int64_t nb, int leaf, int d, float scale,
+                      int64_t nb, int leaf, int d, float scale, int tf32,
                       uint8_t *g8, float *sg, uint8_t *vb8, float *sv, float *lz) {
     const float r448 = 1.0f / 448.0f;
 #pragma omp parallel
@@ -284,7 +298,7 @@ void oracle_stats_fp8(const float *mu, int64_t nt, const uint16_t *k, const uint
         for (int64_t tl_ = 0; tl_ < nt * nb; ++tl_) {
             int64_t t = tl_ / nb, l = tl_ % nb;
             float mx, z;
-            leaf_state(mu + t * d, k + l * leaf * d, v + l * leaf * d, leaf, d, scale, a, kf, gs, vs, &mx, &z);
+            leaf_state(mu + t * d, k + l * leaf * d, v + l * leaf * d, leaf, d, scale, tf32, a, kf, gs, vs, &mx, &z);
             float ag = 0.0f, av = 0.0f;
             for (int i = 0; i < d; ++i) {
                 if (fabsf(gs[i]) > ag) ag = fabsf(gs[i]);
@@ -649,7 +663,7 @@ void oracle_tile_fp8(int64_t nt, int tile, int d, int64_t nb, int leaf, int kx, 
 
 /* Leaf statistics with the bf16 state store (store="bf16"): g (scaled) and vb rounded to bf16. */
 void oracle_stats_bf16(const float *mu, int64_t nt, const uint16_t *k, const uint16_t *v,
-                       int64_t nb, int leaf, int d, float scale, uint16_t *g16, uint16_t *vb16, float *lz) {
+                       int64_t nb, int leaf, int d, float scale, int tf32, uint16_t *g16, uint16_t *vb16, float *lz) {
 #pragma omp parallel
     {
         float *a = (float *)malloc(sizeof(float) * (size_t)leaf);
@@ -660,7 +674,7 @@ void oracle_stats_bf16(const float *mu, int64_t nt, const uint16_t *k, const uin
         for (int64_t tl_ = 0; tl_ < nt * nb; ++tl_) {
             int64_t t = tl_ / nb, l = tl_ % nb;
             float mx, z;
-            leaf_state(mu + t * d, k + l * leaf * d, v + l * leaf * d, leaf, d, scale, a, kf, gs, vs, &mx, &z);
+            leaf_state(mu + t * d, k + l * leaf * d, v + l * leaf * d, leaf, d, scale, tf32, a, kf, gs, vs, &mx, &z);
             for (int i = 0; i < d; ++i) {
                 g16[tl_ * d + i] = f2bf(gs[i]);
                 vb16[tl_ * d + i] = f2bf(vs[i]);

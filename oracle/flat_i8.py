@@ -55,7 +55,7 @@ def lib():
         L.oracle_tile_centres.argtypes = [_F32, _i64, _int, _int, _F32]
         L.oracle_group_centres.argtypes = [_F32, _i64, _int, _int, _int, _F32]
         L.oracle_pack_q.argtypes = [_F32, _i64, _int, _int, _int, _F32, _I8, _F32, _I8, _F32]
-        L.oracle_stats.argtypes = [_F32, _i64, _U16, _U16, _i64, _int, _int, _flt,
+        L.oracle_stats.argtypes = [_F32, _i64, _U16, _U16, _i64, _int, _int, _flt, _int,
                                    _I8, _F32, _U16, _F32]
         L.oracle_select.argtypes = [_I8, _F32, _int, _int, _int, _i64, _I8, _F32, _F32, _i64, _i64, _int, _F32]
         L.oracle_topk.argtypes = [_F32, _i64, _i64, _int, _int, _I32, _I8]
@@ -73,15 +73,16 @@ def lib():
         L.oracle_f32_to_f16.restype = ctypes.c_uint16
         L.oracle_f32_to_f16.argtypes = [_flt]
         _U8 = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
-        L.oracle_stats_fp8.argtypes = [_F32, _i64, _U16, _U16, _i64, _int, _int, _flt, _U8, _F32, _U8, _F32, _F32]
+        L.oracle_stats_fp8.argtypes = [_F32, _i64, _U16, _U16, _i64, _int, _int, _flt, _int, _U8, _F32, _U8, _F32,
+                                       _F32]
         L.oracle_select_fp8.argtypes = [_U16, _int, _int, _int, _i64, _U8, _F32, _F32, _i64, _i64, _int, _F32]
         L.oracle_tile_fp8.argtypes = [_i64, _int, _int, _i64, _int, _int, _int, _I32, _I8, _U16, _U16,
                                       _U8, _F32, _F32, _U8, _F32, _U16, _U16, _flt, _int, _int, _F32, _F32, _F32]
-        L.oracle_stats_bf16.argtypes = [_F32, _i64, _U16, _U16, _i64, _int, _int, _flt, _U16, _U16, _F32]
+        L.oracle_stats_bf16.argtypes = [_F32, _i64, _U16, _U16, _i64, _int, _int, _flt, _int, _U16, _U16, _F32]
         L.oracle_select_bf16.argtypes = [_U16, _int, _int, _int, _i64, _U16, _F32, _i64, _i64, _int, _F32]
         L.oracle_tile_bf16.argtypes = [_i64, _int, _int, _i64, _int, _int, _int, _I32, _I8, _U16, _U16,
                                        _U16, _F32, _U16, _U16, _U16, _flt, _int, _int, _F32, _F32, _F32]
-        if L.oracle_abi_version() != 5:
+        if L.oracle_abi_version() != 6:
             raise RuntimeError(f"{path} is stale (oracle ABI {L.oracle_abi_version()}): rebuild it")
         _lib = L
     return _lib
@@ -161,9 +162,17 @@ def pack_q(q: np.ndarray, tile: int, mu: np.ndarray, group: int = 1):
     return q8, sq, dq8, sdq
 
 
-def stats(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int, scale: float):
+def _tf32(prec: str) -> int:
+    if prec not in ("ieee", "tf32"):
+        raise ValueError("prec must be 'ieee' or 'tf32'")
+    return int(prec == "tf32")
+
+
+def stats(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int, scale: float, prec: str = "ieee"):
     """Leaf statistics (h3/htrc_flat_triton.py:41-85, I8 store)
-    -> g8 int8 [nt,nb,d], sg f32 [nt,nb], vb bf16 bits [nt,nb,d], lz f32 [nt,nb]."""
+    -> g8 int8 [nt,nb,d], sg f32 [nt,nb], vb bf16 bits [nt,nb,d], lz f32 [nt,nb].
+    prec="tf32": the dots' fp32 operands (the centre, the normalised weights) rounded to TF32
+    first, as PREC "tf32" makes them (the reference's leaf_stats takes prec for every store)."""
     mu = _c(mu, np.float32)
     k_bits, v_bits = _c(k_bits, np.uint16), _c(v_bits, np.uint16)
     nt, d = mu.shape
@@ -172,7 +181,7 @@ def stats(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int, sca
     vb = np.empty((nt, nb, d), np.uint16)
     sg = np.empty((nt, nb), np.float32)
     lz = np.empty((nt, nb), np.float32)
-    lib().oracle_stats(mu, nt, k_bits, v_bits, nb, leaf, d, float(scale), g8, sg, vb, lz)
+    lib().oracle_stats(mu, nt, k_bits, v_bits, nb, leaf, d, float(scale), _tf32(prec), g8, sg, vb, lz)
     return g8, sg, vb, lz
 
 
@@ -260,7 +269,7 @@ def pack_q16(q: np.ndarray, tile: int, mu: np.ndarray, group: int = 1, dq_fp16: 
     return q16, dq16
 
 
-def stats_fp8(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int, scale: float):
+def stats_fp8(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int, scale: float, prec: str = "ieee"):
     """Leaf statistics with the fp8 state store (h3/htrc_flat_triton.py:65-72)
     -> g8 e4m3 [nt,nb,d], sg [nt,nb], vb8 e4m3 [nt,nb,d], sv [nt,nb], lz [nt,nb]."""
     mu = _c(mu, np.float32)
@@ -272,11 +281,11 @@ def stats_fp8(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int,
     sg = np.empty((nt, nb), np.float32)
     sv = np.empty((nt, nb), np.float32)
     lz = np.empty((nt, nb), np.float32)
-    lib().oracle_stats_fp8(mu, nt, k_bits, v_bits, nb, leaf, d, float(scale), g8, sg, vb8, sv, lz)
+    lib().oracle_stats_fp8(mu, nt, k_bits, v_bits, nb, leaf, d, float(scale), _tf32(prec), g8, sg, vb8, sv, lz)
     return g8, sg, vb8, sv, lz
 
 
-def stats_bf16(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int, scale: float):
+def stats_bf16(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int, scale: float, prec: str = "ieee"):
     """Leaf statistics with the bf16 state store -> g bf16 bits [nt,nb,d], vb bf16 bits, lz [nt,nb]."""
     mu = _c(mu, np.float32)
     k_bits, v_bits = _c(k_bits, np.uint16), _c(v_bits, np.uint16)
@@ -285,7 +294,7 @@ def stats_bf16(mu: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, leaf: int
     g16 = np.empty((nt, nb, d), np.uint16)
     vb16 = np.empty((nt, nb, d), np.uint16)
     lz = np.empty((nt, nb), np.float32)
-    lib().oracle_stats_bf16(mu, nt, k_bits, v_bits, nb, leaf, d, float(scale), g16, vb16, lz)
+    lib().oracle_stats_bf16(mu, nt, k_bits, v_bits, nb, leaf, d, float(scale), _tf32(prec), g16, vb16, lz)
     return g16, vb16, lz
 
 
@@ -405,7 +414,7 @@ def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: 
             splits: int = 4, bn: int = 64, sel_stride: int = 1, sink_leaves: int = 0,
             scale: float | None = None, keep: bool = True, group: int = 1, order: str = "seq",
             store: str = "int8", state_quant: str | None = None, quant_group: int = 0,
-            select_mode: str = "max") -> dict:
+            select_mode: str = "max", prec: str = "ieee") -> dict:
     """The INT8 flat operator for one head: q float32 (or bf16 bits) [n,d], k/v bf16 bits
     [nk,d] with nk % leaf == 0.  Returns every intermediate plus out [n,d] and logz [n].
     order="kmeans": the tiles are cut from q[perm] (perm = kmeans_order(q)) and out / logz
@@ -413,7 +422,8 @@ def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: 
     state store (e4m3 g / vb with row scales, fp16 far dots, bf16 near dots).  state_quant (store
     "bf16" only): g and vb fake-quantised in place after the statistics, as quant["state"] does
     (h3/htrc_flat.py:246-248), with quant_group.  select_mode "bound" (store "bf16" only): the
-    bound routing score (bound_select) in place of the row-max SEL."""
+    bound routing score (bound_select) in place of the row-max SEL.  prec="tf32": the leaf
+    statistics on TF32 operands (the operator's precision="tf32", h3/htrc_flat.py:122, 243)."""
     q = np.asarray(q)
     qf = bf16.to_f32(q) if q.dtype == np.uint16 else _c(q, np.float32)
     n, d = qf.shape
@@ -435,18 +445,18 @@ def flat_i8(q, k_bits, v_bits, *, tile: int = 64, leaf: int = 64, exact_leaves: 
     if store == "fp8":
         st["k"] = _c(k_bits, np.uint16)
         st["q16"], st["dq16"] = pack_q16(qf, tile, st["mu"], group, dq_fp16=True)
-        st["g8"], st["sg"], st["vb8"], st["sv"], st["lz"] = stats_fp8(st["mu"], k_bits, v_bits, leaf, scale)
+        st["g8"], st["sg"], st["vb8"], st["sv"], st["lz"] = stats_fp8(st["mu"], k_bits, v_bits, leaf, scale, prec)
     elif store == "bf16":
         st["k"] = _c(k_bits, np.uint16)
         st["q16"], st["dq16"] = pack_q16(qf, tile, st["mu"], group, dq_fp16=False)
-        st["g16"], st["vb16"], st["lz"] = stats_bf16(st["mu"], k_bits, v_bits, leaf, scale)
+        st["g16"], st["vb16"], st["lz"] = stats_bf16(st["mu"], k_bits, v_bits, leaf, scale, prec)
         if state_quant:
             from .fake_quant import fake_quant
             for nm in ("g16", "vb16"):
                 st[nm] = bf16.from_f32(fake_quant(bf16.to_f32(st[nm]), state_quant, quant_group))
     elif store == "int8":
         st["q8"], st["sq"], st["dq8"], st["sdq"] = pack_q(qf, tile, st["mu"], group)
-        st["g8"], st["sg"], st["vb"], st["lz"] = stats(st["mu"], k_bits, v_bits, leaf, scale)
+        st["g8"], st["sg"], st["vb"], st["lz"] = stats(st["mu"], k_bits, v_bits, leaf, scale, prec)
     else:
         raise ValueError("store must be int8, fp8 or bf16")
     if (state_quant or select_mode != "max") and store != "bf16":

@@ -56,6 +56,30 @@ def test_flat_attention_vs_oracle(device, fused, n, leaf, ex):
     check_logz(logz.cpu().numpy(), ref, st, LOGZ_ABS)
 
 
+@pytest.mark.parametrize("store", ["int8", "fp8", "bf16"])
+def test_flat_attention_tf32_statistics_vs_oracle(device, store):
+    """precision="tf32" (the reference PROD's setting) on the dot="bf16" stores: the leaf
+    statistics on TF32 operands, as the reference's leaf_stats takes PREC for every store, against
+    the oracle run at TF32; routing up to the oracle's near-ties, outputs within the bar."""
+    n, leaf, ex = 4096, 64, 8
+    q, k, v = workloads.clustered_runs(n=n, runs=n // 64, heads=1, seed=77)
+    st = {}
+    out, logz = htrc_flat.flat_attention(q[0].to(device), k[0].to(device), v[0].to(device), backend="hip",
+                                         store=store, dot="bf16", precision="tf32", leaf=leaf, exact_leaves=ex,
+                                         return_logz=True, state=st)
+    torch.cuda.synchronize()
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=ex, splits=1, bn=64,
+                          store=store, prec="tf32")
+    if store == "int8":
+        _routing_check(st, ref, f"flat tf32 statistics {store}")
+    else:
+        assert (st["idx"][0].cpu().numpy() != ref["idx"]).any(1).mean() <= 0.05
+    err = rel_l2(out.cpu().numpy(), ref["out"])
+    dl = float(np.abs(logz.cpu().numpy() - ref["logz"]).max())
+    record(f"flat tf32 statistics {store} errors", {"rel_l2": err, "dlogz_max": dl})
+    assert err <= OUT_REL_L2 and dl <= LOGZ_ABS, (err, dl)
+
+
 def test_multihead_equals_per_head(device):
     q, k, v = workloads.clustered_runs(n=2048, runs=32, heads=3, seed=9)
     kw = dict(backend="hip", store="int8", dot="bf16", leaf=64, exact_leaves=8)

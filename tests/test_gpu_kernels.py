@@ -133,6 +133,55 @@ def test_stats_close_to_oracle(device, leaf):
         assert np.all(_np(lz[0])[:, nb:] == -np.inf) and np.all(_np(g8[0])[:, nb:] == 0)
 
 
+@pytest.mark.parametrize("store", ["int8", "fp8"])
+@pytest.mark.parametrize("leaf", [64, 16])
+def test_stats_tf32_close_to_oracle(device, store, leaf):
+    """precision="tf32" (PROD's setting; the reference's leaf_stats takes PREC for every store):
+    the int8 and fp8 stores' statistics on TF32 centres and weights against the oracle's TF32
+    statistics: codes within one step, lz within fp32 noise, rates recorded and held near the
+    measured ones (a weight at a TF32 rounding point can round either way in the two sums)."""
+    n = 2048
+    q, k, v = _data(n, seed=leaf + 60)
+    nb = n // leaf
+    sc = 1 / math.sqrt(128)
+    ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=4, store=store,
+                          prec="tf32")
+    ieee = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=64, leaf=leaf, exact_leaves=4, store=store)
+    mu = torch.from_numpy(ref["mu"])[None].to(device)
+    sdt = torch.int8 if store == "int8" else torch.float8_e4m3fn
+    g, lz, vbs, sg, sv = hip.leaf_stats(mu, k.to(device), v.to(device), nb, sc, leaf=leaf, store=sdt, prec="tf32")
+    torch.cuda.synchronize()
+    lzg = _np(lz[0])[:, :nb]
+    atol = 2e-5 * (1 + np.abs(ref["lz"]).max())
+    np.testing.assert_allclose(lzg, ref["lz"], rtol=0, atol=atol)
+    # TF32 operands, not IEEE ones: far nearer the TF32 oracle than the IEEE one (measured
+    # against the IEEE oracle 2.2e-3 to 2.3e-3)
+    err_t, err_i = float(np.abs(lzg - ref["lz"]).max()), float(np.abs(lzg - ieee["lz"]).max())
+    assert err_t * 8 < err_i, (err_t, err_i)
+    if store == "int8":
+        diff = np.abs(_np(g[0])[:, :nb].astype(np.int32) - ref["g8"].astype(np.int32))
+        vb = bf16.to_f32(bits(vbs[0, :, :nb].contiguous()))
+        ovb = bf16.to_f32(ref["vb"])
+        assert diff.max() <= 1 and np.abs(vb - ovb).max() <= 2 ** -7 * np.abs(ovb).max()
+        rates = {"g8": float((diff > 0).mean()), "vb": float((vb != ovb).mean())}
+    else:
+        rates = {}
+        for name, got, want in (("g", g, ref["g8"]), ("vb", vbs, ref["vb8"])):
+            gv = _np(got[0].view(torch.uint8))[:, :nb]
+            a_ = flat_i8.e4m3_to_f32(gv).astype(np.float64)
+            b_ = flat_i8.e4m3_to_f32(want).astype(np.float64)
+            # one e4m3 step, or (a weight whose fp32 value sits at a TF32 rounding point rounds
+            # either way in the two sums) 2^-11 of the row's largest value (448), doubled
+            allow = np.maximum(np.maximum(np.abs(b_) * 2 ** -3, 2.0 ** -9) * 1.001, 2.0 ** -10 * 448)
+            assert np.all(np.abs(a_ - b_) <= allow)
+            rates[name] = float((gv != want).mean())
+    record(f"stats_tf32_flips[{store},{leaf}]", rates)
+    # measured (leaf 64 / 16): int8 g8 7.6e-6 / 1.9e-6, vb 1.6e-3 / 4.2e-4 of the values a step
+    # away; fp8 g 0 / 0, vb 1.4e-4 / 3.2e-5; bars at twice the largest
+    bars = {"g8": 2e-5, "vb": 3.2e-3} if store == "int8" else {"g": 2e-5, "vb": 3e-4}
+    assert all(rates[n_] <= bars[n_] for n_ in rates), rates
+
+
 @pytest.mark.parametrize("n", [8192, 32768, 65536, 2368])
 def test_stats_leaf_split_sizes(device, n):
     """The statistics launcher stages two leaves of 64 keys per workgroup and deals a head's

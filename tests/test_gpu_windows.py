@@ -138,8 +138,9 @@ def test_live_h3_shape_accurate_mode(device):
     tiles = (0, 1, 318, 636)
     rows = np.concatenate([perm[64 * t: min(n, 64 * t + 64)] for t in tiles])
     qr = q[h].float().numpy()[rows]
+    # the runner runs PROD's precision="tf32": the oracle's statistics on TF32 operands too
     ref = flat_i8.flat_i8(qr, bits(k[h]), bits(v[h]), tile=64, leaf=16, exact_leaves=1024, sink_leaves=sink, splits=1,
-                          bn=64)
+                          bn=64, prec="tf32")
     ref_out, ref_lz = flat_i8.tail_merge(ref["out"], ref["logz"], qr, tk[h].numpy(), tv[h].numpy(),
                                          1 / math.sqrt(128))
     tix = torch.tensor(tiles, device=device)

@@ -111,3 +111,43 @@ def test_tf32_operands_change_results_at_tf32_level():
     b = flat_f32.flat_f32(q, k, v, leaf=64, exact_leaves=3, prec="tf32")
     r = _rel(b["out"], a["out"])
     assert 1e-7 < r < 2e-3
+
+
+def _stats_inputs(seed=0, nt=8, nk=1024, d=128):
+    rng = np.random.default_rng(seed)
+    cent = rng.normal(0, 1.5, (16, d))
+    mu = (cent[rng.integers(0, 16, nt)] + rng.normal(0, 0.5, (nt, d))).astype(np.float32)
+    k = cent[np.repeat(rng.integers(0, 16, nk // 64), 64)] + rng.normal(0, 0.5, (nk, d))
+    v = rng.normal(0, 1, (nk, d))
+    return mu, bf16.from_f32(k.astype(np.float32)), bf16.from_f32(v.astype(np.float32))
+
+
+def test_tf32_statistics_of_the_c_oracle_equal_the_numpy_restatement():
+    """The C oracle's leaf statistics with prec="tf32" (every store: the reference's leaf_stats
+    takes PREC for all of them) against flat_f32.stats at TF32: lz within fp32 noise where IEEE
+    and TF32 differ by ~1e-3 (the centre's rounding), g8 within half a code, and the bf16 store's
+    g bits equal to the restatement's bf16 rounding except at fp32-noise ties, where the IEEE
+    restatement's differ in 1.4% of entries (the weights' rounding)."""
+    from oracle import flat_i8
+    mu, kb, vb = _stats_inputs()
+    leaf, sc = 64, 1 / math.sqrt(128)
+    kf, vf = bf16.to_f32(kb), bf16.to_f32(vb)
+    g_t, vb_t, lz_t = flat_f32.stats(mu, kf, vf, leaf, sc, "tf32")
+    g_i, _, lz_i = flat_f32.stats(mu, kf, vf, leaf, sc, "ieee")
+    assert np.abs(lz_t - lz_i).max() > 3e-4                       # the two precisions do differ
+    g8, sg, vb16, lz = flat_i8.stats(mu, kb, vb, leaf, sc, "tf32")
+    assert np.abs(lz - lz_t).max() <= 2e-5
+    assert np.all(np.abs(g8 * sg[..., None].astype(np.float64) - g_t) <= 0.501 * sg[..., None])
+    # vb: half a bf16 step (plus fp32 noise where a row's sum cancels), but for the few weights
+    # whose fp32 values straddle a TF32 rounding point in the two restatements (2^-11 of a weight)
+    far = np.abs(bf16.to_f32(vb16) - vb_t) > 2.0 ** -8 * np.abs(vb_t) + 1e-5
+    assert far.mean() <= 0.01, far.mean()
+    g16, _, lz16 = flat_i8.stats_bf16(mu, kb, vb, leaf, sc, "tf32")
+    assert np.array_equal(lz16, lz)
+    flips_t = (g16 != bf16.from_f32(g_t.astype(np.float32))).mean()
+    flips_i = (g16 != bf16.from_f32(g_i.astype(np.float32))).mean()
+    assert flips_t <= 0.002 and flips_i >= 0.005, (flips_t, flips_i)    # measured 1.2e-4 and 1.4e-2
+    g8f, sgf, vb8, svf, lzf = flat_i8.stats_fp8(mu, kb, vb, leaf, sc, "tf32")
+    assert np.array_equal(lzf, lz)
+    # ieee stays the default
+    assert np.array_equal(flat_i8.stats(mu, kb, vb, leaf, sc)[3], flat_i8.stats(mu, kb, vb, leaf, sc, "ieee")[3])
