@@ -1745,9 +1745,39 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
 #pragma unroll
         for (int e = 0; e < 32; ++e) {
             dq[e] = __fsub_rn(qx[e], mx[e]);
-            if constexpr (TF32) {
-                dq[e] = tf32_rna(dq[e]);
-                qx[e] = tf32_rna(qx[e]);
+            if constexpr (TF32) dq[e] = tf32_rna(dq[e]);
+        }
+    }
+    // Near-field score operands on the bf16 MFMA (16x16x32): k-step s takes lane group grp's dims
+    // 32 s + 8 grp .. + 7 of the row as NQT bf16 terms whose sum is the row exactly (a bf16 row:
+    // itself; TF32: 11 bits in two; fp32: 24 bits in three, each residual exact), so every product
+    // with a bf16 key is the exact product the fp32 MFMA forms and only the grouping of the fp32
+    // sums differs, at a quarter (fp32 rows) to an eighth (bf16 rows) of its matrix cycles.
+    constexpr int NQT = QBF ? 1 : (TF32 ? 2 : 3);
+    bf16x8 qt[NQT][4];
+    {
+        const char* qrow = (const char*)q + ((int64_t)h * nq + src) * D * QB;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            float x[8];
+            load_f32<8, QBF, false>(qrow + (32 * ks + 8 * grp) * QB, x);
+#pragma unroll
+            for (int tt = 0; tt < NQT; ++tt) {
+                if constexpr (TF32) {
+                    if (tt == 0) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) x[e] = tf32_rna(x[e]);
+                    }
+                }
+                const u32x4 u = {pack2bf(x[0], x[1]), pack2bf(x[2], x[3]), pack2bf(x[4], x[5]), pack2bf(x[6], x[7])};
+                qt[tt][ks] = as_bf16x8(u);
+                if (tt + 1 < NQT) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {       // the residual, exact
+                        x[2 * e] = __fsub_rn(x[2 * e], __uint_as_float(u[e] << 16));
+                        x[2 * e + 1] = __fsub_rn(x[2 * e + 1], __uint_as_float(u[e] & 0xffff0000u));
+                    }
+                }
             }
         }
     }
@@ -1788,9 +1818,15 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         // of 16): one wave-uniform base; positions past e_hi repeat its last token
         const int64_t tok0 = kh + (int64_t)ix[e0 / leaf] * leaf + e0 % leaf;
         const int last = e_hi - 1 - e0;
-        float ka[32];
-        load_f32<32, true, false>(k + (tok0 + min(col, last)) * D + 32 * grp, ka);
-        const f32x4 s4 = dot_tile_f32(ka, qx);
+        u32x4 kq[4];
+        const uint16_t* krow = k + (tok0 + min(col, last)) * D + 8 * grp;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) kq[ks] = *(const u32x4*)(krow + 32 * ks);
+        f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int tt = NQT - 1; tt >= 0; --tt)            // smaller terms first
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) s4 = mfma_bf16(as_bf16x8(kq[ks]), qt[tt][ks], s4);
         float sc[4], va[4][8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -1830,10 +1866,14 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
 }
 
 // SEL[g, l] = max over every stride-th row of the group's tiles of (q - mu_g) . g_l, + lz_l, with
-// fp32 dots (h3/htrc_flat_triton.py:214-254, DOT = 0).  Workgroup = one group x 256 leaves; each
-// wave holds the A operands of its 64 leaves (four blocks of 16) and sweeps the group's rows 16
-// at a time (rows past the last query repeat it, tiles past the last repeat it: as the
+// fp32 dots (h3/htrc_flat_triton.py:214-254, DOT = 0).  Workgroup = one group x 4 SEL_F32_LB x 16
+// leaves; each wave holds the A operands of its SEL_F32_LB blocks of 16 leaves and sweeps the
+// group's rows 16 at a time (rows past the last query repeat it, tiles past the last repeat it: as the
 // reference pads them, which leaves every maximum unchanged).
+// 16-leaf blocks per wave of select_f32_kernel: two (152 VGPRs, three waves per SIMD) 5.17 ms at
+// cfg3, four (229 VGPRs, two waves) 5.55, one (four waves, each row block's q reloaded per 16
+// leaves) 5.80
+constexpr int SEL_F32_LB = 2;
 template <bool QBF, bool SB, bool TF32>
 __global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict__ q, const float* __restrict__ mu,
                                                          int mu_stride, const void* __restrict__ g,
@@ -1844,19 +1884,20 @@ __global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict_
     constexpr int QB = QBF ? 2 : 4, SBB = SB ? 2 : 4;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int gi = blockIdx.y, h = blockIdx.z, gg = g0 + gi;
-    const int l0 = blockIdx.x * 256 + 64 * w;                 // this wave's 64 leaves
+    constexpr int LB = SEL_F32_LB;
+    const int l0 = (blockIdx.x * 4 + w) * 16 * LB;            // this wave's 16 LB leaves
     if (l0 >= nb) return;                                      // (no barriers in this kernel)
     const int64_t srow = ((int64_t)h * ng + gi) * nb_pad;
-    float ga[4][32];
+    float ga[LB][32];
 #pragma unroll
-    for (int lb = 0; lb < 4; ++lb)
+    for (int lb = 0; lb < LB; ++lb)
         load_f32<32, SB, TF32>((const char*)g + ((srow + min(l0 + 16 * lb + col, nb - 1)) * D + 32 * grp) * SBB,
                                ga[lb]);
     float mx[32];
     load_f32<32, false, false>(mu + ((int64_t)h * mu_stride + gg) * D + 32 * grp, mx);
-    float best[4][4];
+    float best[LB][4];
 #pragma unroll
-    for (int lb = 0; lb < 4; ++lb)
+    for (int lb = 0; lb < LB; ++lb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) best[lb][i] = -INFINITY;
     const int rpt = tile / stride, nsel = group * rpt;
@@ -1873,14 +1914,14 @@ __global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict_
             if constexpr (TF32) dq[e] = tf32_rna(dq[e]);
         }
 #pragma unroll
-        for (int lb = 0; lb < 4; ++lb) {
+        for (int lb = 0; lb < LB; ++lb) {
             const f32x4 s4 = dot_tile_f32<4>(ga[lb], dq);
 #pragma unroll
             for (int i = 0; i < 4; ++i) best[lb][i] = fmaxf(best[lb][i], s4[i]);
         }
     }
 #pragma unroll
-    for (int lb = 0; lb < 4; ++lb)
+    for (int lb = 0; lb < LB; ++lb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float m = col_max(best[lb][i]);          // over the 16 rows of the lane group
@@ -4225,7 +4266,8 @@ int htrc_select_f32(const void* q, int q_is_bf16, const float* mu, const void* g
     int64_t ng, tb, ntw;
     REQUIRE(group_window(nt, group, g0, gn, ng, tb, ntw), "htrc_select_f32: group window [g0, g0 + gn) must lie in the head's groups");
     REQUIRE(gn <= 65535, "htrc_select_f32: at most 65535 groups per launch");
-    const dim3 grid((unsigned)((nb + 255) / 256), (unsigned)gn, (unsigned)heads);
+    const int64_t per = 4 * 16 * SEL_F32_LB;               // leaves per workgroup
+    const dim3 grid((unsigned)((nb + per - 1) / per), (unsigned)gn, (unsigned)heads);
     hipStream_t s = (hipStream_t)stream;
     F32_DISPATCH(select_f32_kernel, grid, dim3(256), q, mu, (int)ng, g, lz, nq, (int)nt, tile, stride, group, (int)g0,
                  (int)gn, perm, (int)nb, htrc_nb_pad(nb), sel);
