@@ -122,9 +122,12 @@ def test_tile_f32_on_oracle_state(device, store, prec, splits, leaf, tile, group
     assert np.abs(_np(logz[0]) - st["logz"]).max() <= LOGZ[prec]
 
 
-def _check_operator(out, logz, gst, ref, prec, q, k, v, tile, leaf, group, name):
+def _check_operator(out, logz, gst, ref, prec, q, k, v, tile, leaf, group, name, store="fp32"):
     """The GPU output against the oracle; where the GPU's near sets differ from the oracle's
-    (near-ties of fp32 SEL), against the oracle's attention under the GPU's routing."""
+    (near-ties of fp32 SEL), against the oracle's attention under the GPU's routing.  The bf16
+    store's outputs may differ by its state's bf16 rounding: a g or vb value the GPU's fp32 sums
+    put on the other side of a rounding point moves by one bf16 step (2^-8), ~1e-3 of them, so
+    rel-L2 up to 2e-4 where the far field carries a row."""
     idx = gst["idx"][0].cpu().numpy()
     same = np.array_equal(idx, ref["idx"])
     want, wlz = ref["out"], ref["logz"]
@@ -146,7 +149,8 @@ def _check_operator(out, logz, gst, ref, prec, q, k, v, tile, leaf, group, name)
     r = rel_l2(out, want)
     dl = float(np.abs(logz - wlz).max())
     record(name, {"rel_l2": r, "max_dlogz": dl, "same_routing": bool(same)})
-    assert r <= OUT[prec] and dl <= LOGZ[prec], (r, dl)
+    bar = max(OUT[prec], 2e-4) if store == "bf16" else OUT[prec]
+    assert r <= bar and dl <= LOGZ[prec], (r, dl)
 
 
 @pytest.mark.parametrize("store,precision,kw", [
@@ -173,7 +177,7 @@ def test_flat_attention_fp32_dots_vs_oracle(device, store, precision, kw):
                             exact_leaves=ex, store=store, prec=prec, group=group,
                             sel_stride=int(kw.get("sel_stride", 1)), sink_leaves=int(kw.get("sink_leaves", 0)))
     _check_operator(_np(out), _np(logz), gst, ref, prec, q, k, v, tile, leaf, group,
-                    f"flat_f32[{store},{precision},{sorted(kw)}]")
+                    f"flat_f32[{store},{precision},{sorted(kw)}]", store=store)
 
 
 @pytest.mark.parametrize("store,tile_chunk", [("fp32", None), ("bf16", 5)])
@@ -198,7 +202,7 @@ def test_fp32_dots_unsplit_tile_windows(device, monkeypatch, store, tile_chunk):
                                 leaf=leaf, exact_leaves=ex, store=store)
         one = {"idx": gst["idx"][hh:hh + 1], "excl": gst["excl"][hh:hh + 1]}
         _check_operator(_np(out[hh]), _np(logz[hh]), one, ref, "ieee", q[hh:hh + 1], k[hh:hh + 1], v[hh:hh + 1], 64,
-                        leaf, 1, f"flat_f32[unsplit,{store},{tile_chunk}]")
+                        leaf, 1, f"flat_f32[unsplit,{store},{tile_chunk}]", store=store)
 
 
 def test_reference_default_call(device):

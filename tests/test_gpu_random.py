@@ -2,8 +2,8 @@
 
 Each case draws the state store, the fused route or the reference's stage structure, the tile
 (64 or 32 rows), the leaf size, ragged query and key counts, the near-leaf count, shared
-centres (kern["group"]), the select row stride, forced sink leaves, the query order and a
-tile window from its own seed, so a failure names a reproducible combination.  The bars are
+centres (kern["group"]), the select row stride, forced sink leaves, the query order, a
+tile window and the statistics' precision (IEEE or PROD's TF32) from its own seed, so a failure names a reproducible combination.  The bars are
 those of the single-knob tests: every tile's near set equals the oracle's except where the
 oracle's own top-k boundary gap is within twice the measured SEL error, and on the rows of
 every row output rel-L2 <= 1e-2 and |dlogZ| <= 1e-3 plus each row's far-score drift from the
@@ -36,7 +36,8 @@ def _case(seed: int) -> dict:
                 n=int(rng.integers(700, 4001)), nk=nb * leaf, ex=int(rng.integers(0, min(40, nb) + 1)),
                 group=int(rng.choice([1, 1, 2, 3])), stride=int(rng.choice([1, 1, 2, 4])),
                 sink=int(rng.choice([0, 0, 2, 5])), order=str(rng.choice(["seq", "seq", "kmeans"])),
-                fused=bool(rng.integers(0, 2)), chunk=int(rng.choice([24, 64, 96, 160])))
+                fused=bool(rng.integers(0, 2)), chunk=int(rng.choice([24, 64, 96, 160])),
+                precision=str(rng.choice(["fp32", "fp32", "tf32"])))
 
 
 @pytest.mark.parametrize("seed", range(CASES))
@@ -49,7 +50,8 @@ def test_random_knobs_vs_oracle(device, seed):
     q = q[:, :c["n"]].contiguous()
     k, v = k[:, :c["nk"]].contiguous(), v[:, :c["nk"]].contiguous()
     st = {}
-    kw = dict(backend="hip", tile=c["tile"], store=c["store"], dot="bf16", leaf=c["leaf"], exact_leaves=c["ex"],
+    kw = dict(backend="hip", tile=c["tile"], store=c["store"], dot="bf16", precision=c["precision"],
+              leaf=c["leaf"], exact_leaves=c["ex"],
               sink_leaves=c["sink"], sel_stride=c["stride"], order=c["order"], splits=4,
               kern={"tile_bn": 64, "fused": c["fused"], "group": c["group"]}, return_logz=True)
     qd, kd, vd = q[0].to(device), k[0].to(device), v[0].to(device)
@@ -60,7 +62,8 @@ def test_random_knobs_vs_oracle(device, seed):
     assert torch.equal(out_w, out) and torch.equal(logz_w, logz), f"{name}: windows differ"
     ref = flat_i8.flat_i8(bits(q[0]), bits(k[0]), bits(v[0]), tile=c["tile"], leaf=c["leaf"],
                           exact_leaves=c["ex"], splits=1 if c["fused"] else 4, bn=64, sel_stride=c["stride"],
-                          sink_leaves=c["sink"], group=c["group"], order=c["order"], store=c["store"])
+                          sink_leaves=c["sink"], group=c["group"], order=c["order"], store=c["store"],
+                          prec="tf32" if c["precision"] == "tf32" else "ieee")
     assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(logz).all()), name
     nb = st["nb"]
     if min(c["ex"] + c["sink"], nb) > 0:              # else no near set: the far field alone
