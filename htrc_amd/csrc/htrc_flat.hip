@@ -399,6 +399,19 @@ __device__ __forceinline__ void stage_leaves_f16(const uint16_t* __restrict__ K,
 
 // PV-type operand half from swizzled LDS rows: keys rbase + 4grp + j (j = 0..3) at column
 // 16db + lane%16.
+__device__ __forceinline__ uint32_t tr_offset(int rbase, int db, int lane) {
+    const int L = lane & 15, grp = lane >> 4;
+    const int row = rbase + 4 * grp + (L >> 2);
+    const int c = 2 * db + ((L & 3) >> 1);
+    return (uint32_t)((row * 16 + (c ^ swz(row))) * 16 + 8 * (L & 1));
+}
+// The same read at LDS byte address a (an offset from tr_offset plus the rows' base): keys 16 on
+// (rbase + 16) share the lane's swizzle (swz looks at the row's low four bits), so a caller
+// adds 4096 for them, and a ring slot's byte offset, as constants the read takes as immediates.
+__device__ __forceinline__ u32x2 tr_read(uint32_t a) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)a);
+    return __builtin_bit_cast(u32x2, v);
+}
 __device__ __forceinline__ u32x2 tr_operand(const char* rows, int rbase, int db, int lane) {
     const int L = lane & 15, grp = lane >> 4;
     const int row = rbase + 4 * grp + (L >> 2);
@@ -2416,6 +2429,14 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
         load_block(std::false_type{}, pring_lds + slot * SLOT_BYTES, k8, v, r0, r1, ks + r0, ks + r1, 3);
     };
     static_assert(RS == 2, "the far / near block stream alternates two ring slots");
+    // LDS addresses of this lane's PV operand reads (slot 0, keys 0..15 of a block): the slot's
+    // and the second key half's offsets are immediates of the reads
+    uint32_t tra[8];
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+        tra[db] = pring_lds + 4096 + tr_offset(0, db, lane);
+        asm volatile("" : "+v"(tra[db]));   // one register each: no add at every read
+    }
     RowsN<RB> st;
 #pragma unroll 1
     for (int pass = 0; pass < MAX_PASSES; ++pass) {
@@ -2490,7 +2511,7 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
 #pragma unroll
                 for (int db = 0; db < 8; ++db)
 #pragma unroll
-                    for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
+                    for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_read(tra[db] + S * SLOT_BYTES + 4096 * hf);
                 rows_update<RB, true>(st, sc, pvop);
             };
             issue(0, 0);
@@ -2565,7 +2586,7 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
 #pragma unroll
                 for (int db = 0; db < 8; ++db)
 #pragma unroll
-                    for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_operand(slot + 4096, 16 * hf, db, lane);
+                    for (int hf = 0; hf < 2; ++hf) pvop[db][hf] = tr_read(tra[db] + S * SLOT_BYTES + 4096 * hf);
                 rows_update<RB, true>(st, sc, pvop);
             };
 #pragma unroll 1
