@@ -1821,33 +1821,148 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         }
         f32_update<TF32>(st, sc, va);
     }
-    // ---- near field: 16 tokens per block
+    // ---- near field: 32 tokens per block, on the bf16 MFMA.  Scores in two 16-key halves (the
+    // lane's keys 4 grp + i and 16 + 4 grp + i of the block); the PV products take the block's
+    // values from LDS, each row staged with its dims permuted (column 16 e + m holds dim 8 m + e),
+    // so the transposing read of column block db gives dims 8 m + db, the O^T layout the far
+    // field's fp32 products keep, and the weights as NPT bf16 terms that sum to them exactly
+    // (each product with a bf16 value exact, as in the fp32 MFMA).  The block's running maximum
+    // is taken over its 32 keys (the reference's block size is a launch parameter).
+    constexpr int NPT = TF32 ? 2 : 3;
+    __shared__ __align__(16) char vstage[32 * 256];
     const int e_n = kx * leaf;
     const int e_lo = sp * eps, e_hi = min(e_n, e_lo + eps);
     const int64_t kh = (int64_t)h * nk;
     const int32_t* ix = idx + gs * (int64_t)(kx > 0 ? kx : 1);
-    for (int e0 = e_lo; e0 < e_hi; e0 += 16) {
-        // the block's 16 tokens lie in one leaf (leaf, e_lo and the split length are multiples
-        // of 16): one wave-uniform base; positions past e_hi repeat its last token
-        const int64_t tok0 = kh + (int64_t)ix[e0 / leaf] * leaf + e0 % leaf;
-        const int last = e_hi - 1 - e0;
-        u32x4 kq[4];
-        const uint16_t* krow = k + (tok0 + min(col, last)) * D + 8 * grp;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) kq[ks] = *(const u32x4*)(krow + 32 * ks);
-        f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int tt = NQT - 1; tt >= 0; --tt)            // smaller terms first
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) s4 = mfma_bf16(as_bf16x8(kq[ks]), qt[tt][ks], s4);
-        float sc[4], va[4][8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int j = 4 * grp + i;
-            sc[i] = j <= last ? __fmul_rn(s4[i], scale) : -INFINITY;
-            load_f32<8, true, false>(v + (tok0 + min(j, last)) * D + 8 * col, va[i]);
+    const int tid = threadIdx.x, nth = blockDim.x;   // 4 tile threads: 256 or 128
+    // a block's two 16-token runs (each in one leaf: leaf, e_lo and the split length are
+    // multiples of 16): wave-uniform bases, and the last valid position of each (a run past e_hi
+    // repeats the first run, masked)
+    struct Runs {
+        int64_t b[2];
+        int last[2];
+    };
+    auto runs = [&](int e0) {
+        Runs r;
+        r.b[0] = kh + (int64_t)ix[e0 / leaf] * leaf + e0 % leaf;
+        r.last[0] = min(15, e_hi - 1 - e0);
+        if (e0 + 16 < e_hi) {
+            r.b[1] = kh + (int64_t)ix[(e0 + 16) / leaf] * leaf + (e0 + 16) % leaf;
+            r.last[1] = min(15, e_hi - 17 - e0);
+        } else {
+            r.b[1] = r.b[0];
+            r.last[1] = -1;
         }
-        f32_update<TF32>(st, sc, va);
+        return r;
+    };
+    // two 16-byte pieces of a block's values per thread and round: piece c = base + tid + nth u is
+    // token c / 16, dims 8 (c % 16) .. + 7 (one round of 2 nth pieces for 64-row tiles, two for
+    // 32-row tiles, the second loaded as it is staged)
+    auto vload = [&](const Runs& r, u32x4 (&vr)[2], int base) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int c = base + tid + nth * u, row = c >> 4, j = c & 15, hh = row >> 4;
+            const int pos = min(row & 15, r.last[hh] >= 0 ? r.last[hh] : r.last[0]);
+            vr[u] = *(const u32x4*)(v + (r.b[hh] + pos) * D + 8 * j);
+        }
+    };
+    auto vstore = [&](const u32x4 (&vr)[2], int base) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int c = base + tid + nth * u, row = c >> 4, j = c & 15, sw = swz(row);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {          // dim 8 j + e -> column 16 e + j
+                const uint32_t w = vr[u][e >> 1];
+                *(uint16_t*)(vstage + row * 256 + (((2 * e + (j >> 3)) ^ sw) << 4) + ((j & 7) << 1)) =
+                    (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
+            }
+        }
+    };
+    u32x4 vr[2];
+    Runs rn{};
+    if (e_lo < e_hi) {
+        rn = runs(e_lo);
+        vload(rn, vr, 0);
+    }
+    for (int e0 = e_lo; e0 < e_hi; e0 += 32) {
+        const Runs cur = rn;
+        __syncthreads();                        // every wave done with the previous block's values
+        vstore(vr, 0);
+        for (int base = 2 * nth; base < 512; base += 2 * nth) {
+            u32x4 vx[2];
+            vload(cur, vx, base);
+            vstore(vx, base);
+        }
+        if (e0 + 32 < e_hi) {                   // the next block's values load under this one
+            rn = runs(e0 + 32);
+            vload(rn, vr, 0);
+        }
+        __syncthreads();                        // the block's values staged
+        float sc[8];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            u32x4 kq[4];
+            const uint16_t* krow = k + (cur.b[hh] + max(0, min(col, cur.last[hh]))) * D + 8 * grp;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) kq[ks] = *(const u32x4*)(krow + 32 * ks);
+            f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int tt = NQT - 1; tt >= 0; --tt)        // smaller terms first
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) s4 = mfma_bf16(as_bf16x8(kq[ks]), qt[tt][ks], s4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                sc[4 * hh + i] = 4 * grp + i <= cur.last[hh] ? __fmul_rn(s4[i], scale) : -INFINITY;
+        }
+        // the reference's update over the block: m_new = max(m, rowmax), m_s = m_new or 0 when
+        // -inf, p = exp(sc - m_s), alpha = exp(m - m_s), l = l alpha + sum p, O = O alpha + P V
+        float bm = sc[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) bm = fmaxf(bm, sc[i]);
+        bm = grp_max(bm);
+        const float mn = fmaxf(st.m, bm);
+        const float ms = mn == -INFINITY ? 0.0f : mn;
+        float pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pr[i] = __expf(__fsub_rn(sc[i], ms));
+        const float alpha = __expf(__fsub_rn(st.m, ms));
+        st.l = __fadd_rn(__fmul_rn(st.l, alpha),
+                         __fadd_rn(__fadd_rn(__fadd_rn(pr[0], pr[1]), __fadd_rn(pr[2], pr[3])),
+                                   __fadd_rn(__fadd_rn(pr[4], pr[5]), __fadd_rn(pr[6], pr[7]))));
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) st.o[db][i] = __fmul_rn(st.o[db][i], alpha);
+        }
+        st.m = mn;
+        // the weights (TF32-rounded for TF32 operands) as NPT bf16 terms, k slot j of lane group
+        // grp = key 4 grp + j (j < 4) or 16 + 4 grp + j - 4
+        bf16x8 pt[NPT];
+        {
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = TF32 ? tf32_rna(pr[i]) : pr[i];
+#pragma unroll
+            for (int tt = 0; tt < NPT; ++tt) {
+                const u32x4 u = {pack2bf(x[0], x[1]), pack2bf(x[2], x[3]), pack2bf(x[4], x[5]), pack2bf(x[6], x[7])};
+                pt[tt] = as_bf16x8(u);
+                if (tt + 1 < NPT) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        x[2 * e] = __fsub_rn(x[2 * e], __uint_as_float(u[e] << 16));
+                        x[2 * e + 1] = __fsub_rn(x[2 * e + 1], __uint_as_float(u[e] & 0xffff0000u));
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            const u32x2 a0 = tr_operand(vstage, 0, db, lane), a1 = tr_operand(vstage, 16, db, lane);
+            const bf16x8 A = as_bf16x8(a0, a1);
+#pragma unroll
+            for (int tt = NPT - 1; tt >= 0; --tt) st.o[db] = mfma_bf16(A, pt[tt], st.o[db]);
+        }
     }
     const float ltot = grp_sum(st.l);
     // the lane's O^T items in dim order: dims 32 grp + 8 i + db are st.o[db][i]
