@@ -1761,6 +1761,36 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
             if constexpr (TF32) dq[e] = tf32_rna(dq[e]);
         }
     }
+    RowF32 st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) st.o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // ---- far field: 16 leaves per block
+    const int lo = sp * lps, hi = min(nb, lo + lps);
+    const int64_t srow = gs * nb_pad;
+    const char* gb = (const char*)g;
+    const char* vbb = (const char*)vb;
+    for (int c0 = lo; c0 < hi; c0 += 16) {
+        // the block's loads all issued before its score products, so the value rows arrive under
+        // them; leaves c0 + 4 grp .. + 3: exclusion bytes and lz of the padded row (nb_pad is a
+        // multiple of 32 and c0 of 16, so they lie inside it; leaves >= hi are masked)
+        float ga[32], va[4][8];
+        load_f32<32, SB, TF32>(gb + ((srow + min(c0 + col, hi - 1)) * D + 32 * grp) * SBB, ga);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            load_f32<8, SB, TF32>(vbb + ((srow + min(c0 + 4 * grp + i, hi - 1)) * D + 8 * col) * SBB, va[i]);
+        const uint32_t ex4 = *(const uint32_t*)(excl + srow + c0 + 4 * grp);
+        const f32x4 lz4 = *(const f32x4*)(lz + srow + c0 + 4 * grp);
+        const f32x4 s4 = dot_tile_f32(ga, dq);
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = c0 + 4 * grp + i;
+            sc[i] = (c < hi && ((ex4 >> (8 * i)) & 0xffu) == 0) ? __fadd_rn(s4[i], lz4[i]) : -INFINITY;
+        }
+        f32_update<TF32>(st, sc, va);
+    }
     // Near-field score operands on the bf16 MFMA (16x16x32): k-step s takes lane group grp's dims
     // 32 s + 8 grp .. + 7 of the row as NQT bf16 terms whose sum is the row exactly (a bf16 row:
     // itself; TF32: 11 bits in two; fp32: 24 bits in three, each residual exact), so every product
@@ -1793,33 +1823,6 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
                 }
             }
         }
-    }
-    RowF32 st;
-    st.m = -INFINITY;
-    st.l = 0.0f;
-#pragma unroll
-    for (int db = 0; db < 8; ++db) st.o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // ---- far field: 16 leaves per block
-    const int lo = sp * lps, hi = min(nb, lo + lps);
-    const int64_t srow = gs * nb_pad;
-    const char* gb = (const char*)g;
-    const char* vbb = (const char*)vb;
-    for (int c0 = lo; c0 < hi; c0 += 16) {
-        float ga[32];
-        load_f32<32, SB, TF32>(gb + ((srow + min(c0 + col, hi - 1)) * D + 32 * grp) * SBB, ga);
-        const f32x4 s4 = dot_tile_f32(ga, dq);
-        // leaves c0 + 4 grp .. + 3: exclusion bytes and lz of the padded row (nb_pad is a
-        // multiple of 32 and c0 of 16, so they lie inside it; leaves >= hi are masked)
-        const uint32_t ex4 = *(const uint32_t*)(excl + srow + c0 + 4 * grp);
-        const f32x4 lz4 = *(const f32x4*)(lz + srow + c0 + 4 * grp);
-        float sc[4], va[4][8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = c0 + 4 * grp + i, cc = min(c, hi - 1);
-            sc[i] = (c < hi && ((ex4 >> (8 * i)) & 0xffu) == 0) ? __fadd_rn(s4[i], lz4[i]) : -INFINITY;
-            load_f32<8, SB, TF32>(vbb + ((srow + cc) * D + 8 * col) * SBB, va[i]);
-        }
-        f32_update<TF32>(st, sc, va);
     }
     // ---- near field: 32 tokens per block, on the bf16 MFMA.  Scores in two 16-key halves (the
     // lane's keys 4 grp + i and 16 + 4 grp + i of the block); the PV products take the block's
