@@ -1766,22 +1766,81 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     st.l = 0.0f;
 #pragma unroll
     for (int db = 0; db < 8; ++db) st.o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // ---- far field: 16 leaves per block
+    // ---- far field: 16 leaves per block, the block's state rows staged in LDS by direct loads
+    // one block ahead (two slots) and read by all the workgroup's waves.  Slot: g rows, vb rows
+    // (16 each), lz (16 floats), the exclusion bytes.  Row r keeps its 16-byte chunk c at position
+    // c ^ r, so the 16 lanes that read one chunk of 16 rows address 16 positions.
+    constexpr int RBY = D * SBB;                   // state row bytes: 512 (fp32) or 256 (bf16)
+    constexpr int CR = RBY / 16;                   // chunks per row: 32 or 16
+    constexpr int GV = 16 * RBY;                   // g rows of a block; the vb rows follow
+    constexpr int FSLOT = 2 * 16 * D * 4 + 128;
+    __shared__ __align__(16) char fring[2][FSLOT];
     const int lo = sp * lps, hi = min(nb, lo + lps);
     const int64_t srow = gs * nb_pad;
-    const char* gb = (const char*)g;
-    const char* vbb = (const char*)vb;
-    for (int c0 = lo; c0 < hi; c0 += 16) {
-        // the block's loads all issued before its score products, so the value rows arrive under
-        // them; leaves c0 + 4 grp .. + 3: exclusion bytes and lz of the padded row (nb_pad is a
-        // multiple of 32 and c0 of 16, so they lie inside it; leaves >= hi are masked)
+    const int nblk = hi > lo ? (hi - lo + 15) / 16 : 0;
+    const int nw = blockDim.x >> 6;                // waves: 4 (64-row tiles) or 2
+    const uint32_t fring_lds = lds_addr(&fring[0][0]);
+    // block bi into slot: instruction i loads chunks p = 64 i + lane (g rows, then vb rows); rows
+    // up to c0 + 15 < nb_pad exist in the state (nb_pad is a multiple of 32, c0 of 16), those past
+    // hi are masked
+    auto far_issue = [&](int bi, int slot) {
+        const int c0 = lo + 16 * bi;
+        const uint32_t sl = fring_lds + (uint32_t)(slot * FSLOT);
+        for (int i = w; i < (2 * GV) / 1024; i += nw) {
+            const int pc = 64 * i + lane;
+            const int isv = pc >= 16 * CR ? 1 : 0;
+            const int pr = pc - isv * 16 * CR;
+            const int r = pr / CR, c = (pr % CR) ^ r;
+            const char* base = isv ? (const char*)vb : (const char*)g;
+            dma16(base + (srow + c0 + r) * RBY + c * 16, sl + 1024 * i);
+        }
+        if (w == 0 && lane < 5)        // lz of the 16 leaves (lanes 0..3), their exclusion bytes (4)
+            dma16(lane < 4 ? (const void*)(lz + srow + c0 + 4 * lane) : (const void*)(excl + srow + c0), sl + 2 * GV);
+    };
+    auto far_block = [&](int bi, int slot) {
+        const int c0 = lo + 16 * bi;
+        const char* sl = &fring[slot][0];
         float ga[32], va[4][8];
-        load_f32<32, SB, TF32>(gb + ((srow + min(c0 + col, hi - 1)) * D + 32 * grp) * SBB, ga);
+        if constexpr (SB) {                        // bf16 rows: dims 32 grp .. in chunks 4 grp + k
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            load_f32<8, SB, TF32>(vbb + ((srow + min(c0 + 4 * grp + i, hi - 1)) * D + 8 * col) * SBB, va[i]);
-        const uint32_t ex4 = *(const uint32_t*)(excl + srow + c0 + 4 * grp);
-        const f32x4 lz4 = *(const f32x4*)(lz + srow + c0 + 4 * grp);
+            for (int kk = 0; kk < 4; ++kk) {
+                const u32x4 u = *(const u32x4*)(sl + col * RBY + (((4 * grp + kk) ^ col) << 4));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ga[8 * kk + 2 * e] = bf2f(u[e] & 0xffffu);
+                    ga[8 * kk + 2 * e + 1] = bf2f(u[e] >> 16);
+                }
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const int r = 4 * grp + s2;
+                const u32x4 u = *(const u32x4*)(sl + GV + r * RBY + ((col ^ r) << 4));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    va[s2][2 * e] = bf2f(u[e] & 0xffffu);
+                    va[s2][2 * e + 1] = bf2f(u[e] >> 16);
+                }
+            }
+        } else {                                   // fp32 rows: dims 32 grp .. in chunks 8 grp + k
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const f32x4 f = *(const f32x4*)(sl + col * RBY + (((8 * grp + kk) ^ col) << 4));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ga[4 * kk + e] = TF32 ? tf32_rna(f[e]) : f[e];
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const int r = 4 * grp + s2;
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const f32x4 f = *(const f32x4*)(sl + GV + r * RBY + (((2 * col + hf) ^ r) << 4));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) va[s2][4 * hf + e] = TF32 ? tf32_rna(f[e]) : f[e];
+                }
+            }
+        }
+        const f32x4 lz4 = *(const f32x4*)(sl + 2 * GV + 16 * grp);
+        const uint32_t ex4 = *(const uint32_t*)(sl + 2 * GV + 64 + 4 * grp);
         const f32x4 s4 = dot_tile_f32(ga, dq);
         float sc[4];
 #pragma unroll
@@ -1790,6 +1849,13 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
             sc[i] = (c < hi && ((ex4 >> (8 * i)) & 0xffu) == 0) ? __fadd_rn(s4[i], lz4[i]) : -INFINITY;
         }
         f32_update<TF32>(st, sc, va);
+    };
+    if (nblk > 0) far_issue(0, 0);
+    for (int bi = 0; bi < nblk; ++bi) {
+        wait_vmcnt<0>();                           // this wave's loads of block bi have landed
+        __syncthreads();                           // every wave's; slot (bi + 1) & 1 is free
+        if (bi + 1 < nblk) far_issue(bi + 1, (bi + 1) & 1);
+        far_block(bi, bi & 1);
     }
     // Near-field score operands on the bf16 MFMA (16x16x32): k-step s takes lane group grp's dims
     // 32 s + 8 grp .. + 7 of the row as NQT bf16 terms whose sum is the row exactly (a bf16 row:
