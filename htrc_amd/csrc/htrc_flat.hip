@@ -1947,13 +1947,27 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
             }
         }
     };
+    // the block's 32 key rows into a slot of the far field's ring by direct loads (chunk c of row
+    // r at c ^ (r % 16), so the 16 lanes reading one chunk of 16 rows address 16 positions); a row
+    // past its run's last valid position repeats that position's token
+    auto kload = [&](const Runs& rr, int slot) {
+        const uint32_t sl = fring_lds + (uint32_t)(slot * FSLOT);
+        for (int i = w; i < 8; i += nw) {
+            const int pc = 64 * i + lane, row = pc >> 4, hh = row >> 4, c = (pc & 15) ^ (row & 15);
+            const int pos = min(row & 15, rr.last[hh] >= 0 ? rr.last[hh] : rr.last[0]);
+            dma16(k + (rr.b[hh] + pos) * D + 8 * c, sl + 1024 * i);
+        }
+    };
     u32x4 vr[2];
     Runs rn{};
+    __syncthreads();                            // every wave done with the far field's slots
     if (e_lo < e_hi) {
         rn = runs(e_lo);
-        vload(rn, vr, 0);
+        kload(rn, 0);                           // issued before the values: waiting for those
+        vload(rn, vr, 0);                       // (in issue order) waits for the keys too
     }
-    for (int e0 = e_lo; e0 < e_hi; e0 += 32) {
+    int kslot = 0;
+    for (int e0 = e_lo; e0 < e_hi; e0 += 32, kslot ^= 1) {
         const Runs cur = rn;
         __syncthreads();                        // every wave done with the previous block's values
         vstore(vr, 0);
@@ -1962,18 +1976,21 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
             vload(cur, vx, base);
             vstore(vx, base);
         }
-        if (e0 + 32 < e_hi) {                   // the next block's values load under this one
+        wait_vmcnt<0>();                        // this block's keys have landed (and its values)
+        if (e0 + 32 < e_hi) {                   // the next block's keys and values load under this one
             rn = runs(e0 + 32);
+            kload(rn, kslot ^ 1);
             vload(rn, vr, 0);
         }
-        __syncthreads();                        // the block's values staged
+        __syncthreads();                        // the block's values and keys staged
+        const char* ks_ = &fring[kslot][0];
         float sc[8];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             u32x4 kq[4];
-            const uint16_t* krow = k + (cur.b[hh] + max(0, min(col, cur.last[hh]))) * D + 8 * grp;
+            const int krw = 16 * hh + col;
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) kq[ks] = *(const u32x4*)(krow + 32 * ks);
+            for (int ks = 0; ks < 4; ++ks) kq[ks] = *(const u32x4*)(ks_ + krw * 256 + (((4 * ks + grp) ^ col) << 4));
             f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int tt = NQT - 1; tt >= 0; --tt)        // smaller terms first
