@@ -94,7 +94,8 @@ def algorithmic_f32(h, nq, nk, leaf, kx, d=128, tile=64, splits=4):
          "topk": {"bytes": h * (nt * nb * 5 + nt * kx * 4)},
          "tile": {"bytes": h * (state + 4 * nq * d + 4 * nk * d + nt * nb + nt * kx * 4 + 4 * nq * (d + 1)
                                 + 2 * splits * rows * (d + 2) * 4),
-                  "f32_flops": h * (4 * rows * nb * d + 4 * rows * kx * leaf * d)}}
+                  "f32_flops": h * (4 * rows * nb * d + 4 * rows * kx * leaf * d),
+                  "far_flops": h * 4 * rows * nb * d, "near_flops": h * 4 * rows * kx * leaf * d}}
     if splits == 1:                                   # no split partials
         f["tile"]["bytes"] -= h * 2 * rows * (d + 2) * 4
     return f
@@ -202,10 +203,22 @@ def main_f32(a):
             e["f32_TFLOPs"] = round(tf, 2)
             e["mfma_frac"] = round(tf / PEAK_F32_TFLOPS, 4)
         kernels[n] = e
+    # the tile kernel's matrix work: the far field on the fp32 MFMA; the near field on the bf16
+    # MFMA, its scores with the query row in nqt bf16 terms and its PV products with the weights in
+    # npt terms (each term one product of the fp32-equivalent count)
+    nqt = 1 if q.dtype == torch.bfloat16 else (2 if prec == "tf32" else 3)
+    npt = 2 if prec == "tf32" else 3
+    ft = figs["tile"]
+    ideal_s = frac * (ft["far_flops"] / (PEAK_F32_TFLOPS * 1e12)
+                      + ft["near_flops"] / 2 * (nqt + npt) / (PEAK_BF16_TFLOPS * 1e12))
     dom = kernels["tile"]
-    roof = {"bound": "mfma", "achieved": dom["f32_TFLOPs"], "peak": PEAK_F32_TFLOPS, "unit": "TFLOP/s",
+    peak_eff = ft["f32_flops"] * frac / ideal_s / 1e12
+    dom["mfma_frac"] = round(ideal_s / (dom["ms"] * 1e-3), 4)
+    roof = {"bound": "mfma", "achieved": dom["f32_TFLOPs"], "peak": round(peak_eff, 1), "unit": "TFLOP/s",
             "frac": dom["mfma_frac"], "traffic": None, "kernel": "tile",
-            "note": "fp32 MFMA (v_mfma_f32_16x16x4_f32) flops of the far and near fields"}
+            "note": f"fp32-equivalent flops; peak = the kernel's mix: far field at the fp32 MFMA peak "
+                    f"{PEAK_F32_TFLOPS}, near field on the bf16 MFMA ({PEAK_BF16_TFLOPS}) with the query in "
+                    f"{nqt} and the weights in {npt} bf16 terms"}
     res = {"metric": f"flat-HTRC layer ms/call @B1 H{h} N{nq} d{d} ({a.config}, store=fp32, {prec} dots)",
            "value": round(ms, 4), "unit": "ms/call", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
            "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
