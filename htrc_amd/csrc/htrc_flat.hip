@@ -1730,9 +1730,10 @@ __device__ __forceinline__ void f32_update(RowF32& st, const float (&sc)[4], con
 
 // Far + near field of one (tile, split) with fp32 dots (h3/htrc_flat_triton.py:88-211, DOT = 0):
 // far leaves [sp lps, + lps) not excluded, score = (q - mu) . g + lz; near tokens [sp eps, + eps)
-// of the tile group's idx leaves, score = (q . k) scale.  One wave per 16 rows; every wave reads
-// its key rows itself (the tile's waves share them in L2).  ns == 1 (pacc null): normalised rows
-// and logz = m + log l; else the partial (m, l, O) for merge_kernel.
+// of the tile group's idx leaves, score = (q . k) scale.  One wave per 16 rows; the workgroup
+// stages each block's state rows, and the near field's key and value rows, in LDS once for all
+// its waves.  ns == 1 (pacc null): normalised rows and logz = m + log l; else the partial
+// (m, l, O) for merge_kernel.
 template <bool QBF, bool SB, bool TF32>
 __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     const void* __restrict__ q, const float* __restrict__ mu, int mu_stride, const void* __restrict__ g,
