@@ -227,12 +227,14 @@ int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g,
  * vb fp32 (store="fp32") or bf16 (store="bf16"; state_bf16 = 1) [H, ng, nbp, 128], lz fp32; q fp32
  * or bf16 (q_is_bf16) [H, nq, 128] in query order with the optional row permutation perm, mu the
  * layer's centres [H, ceil(nt / group), 128] (htrc_pack_q16's), k / v bf16.  Every product is an
- * fp32 MFMA with fp32 sums; tf32 = 1 (precision="tf32", PREC "tf32") rounds every operand to TF32
+ * exact product of the fp32 operands with fp32 sums: fp32 MFMA for the select and the far field,
+ * bf16 MFMA for the near field with the query row and the softmax weights split into bf16 terms
+ * that sum to them exactly; tf32 = 1 (precision="tf32", PREC "tf32") rounds every operand to TF32
  * (to nearest, ties away) first.  Statistics: g = (w K) scale and vb = w V stored as fp32 or as
  * bf16 (the htrc_leaf_stats_bf16 values when tf32 = 0).  select: SEL = max over every stride-th row
  * of (q - mu) . g + lz.  tile far: (q - mu) . g + lz, PV p . vb; near: (q . k) scale, PV p . v;
- * the reference's running-max softmax per block of 16 keys; splits > 1 writes the partials for
- * htrc_merge.  htrc_bound_select_f32: select="bound" on an fp32 g (htrc_bound_select's rule).
+ * the reference's running-max softmax per block of 16 far leaves and 32 near tokens; splits > 1
+ * writes the partials for htrc_merge.  htrc_bound_select_f32: select="bound" on an fp32 g (htrc_bound_select's rule).
  * Replace leaf_stats(store=float32 / bfloat16, prec), rowmax_select(dot=0) and
  * tile_attention(dot=0) (h3/htrc_flat_triton.py:315-391) and the store="fp32" / dot="tf32"
  * dispatch of h3/htrc_flat.py:196-212. */
