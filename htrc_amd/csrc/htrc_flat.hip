@@ -1671,26 +1671,12 @@ __device__ __forceinline__ void load_f32(const void* p, float (&x)[N]) {
 }
 
 // S^T tile of 16 keys x 16 rows: item i of lane l = sum over dims of key (4 (l/16) + i)'s A row
-// and row l%16's B row, from the 32 dims each lane holds of both.  NC independent accumulation
-// chains (steps s = NC j + c into chain c, added at the end): with four the select kernel's
-// products no longer wait on each other (5.92 -> 5.55 ms at cfg3; the tile kernel, whose value
-// products sit between its score products, is no faster with them).
-template <int NC = 1>
+// and row l%16's B row, from the 32 dims each lane holds of both.
 __device__ __forceinline__ f32x4 dot_tile_f32(const float (&a)[32], const float (&b)[32]) {
-    f32x4 c[NC];
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < NC; ++j) c[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 32; ++s) c[s % NC] = mfma_f32(a[s], b[s], c[s % NC]);
-    if constexpr (NC == 4) {
-        f32x4 r;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = __fadd_rn(__fadd_rn(c[0][i], c[1][i]), __fadd_rn(c[2][i], c[3][i]));
-        return r;
-    } else {
-        static_assert(NC == 1, "dot_tile_f32: one or four chains");
-        return c[0];
-    }
+    for (int s = 0; s < 32; ++s) c = mfma_f32(a[s], b[s], c);
+    return c;
 }
 
 struct RowF32 {        // running softmax state of one row (h3/htrc_flat_triton.py:142-157)
@@ -2085,9 +2071,11 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
 // leaves; each wave holds the A operands of its SEL_F32_LB blocks of 16 leaves and sweeps the
 // group's rows 16 at a time (rows past the last query repeat it, tiles past the last repeat it: as the
 // reference pads them, which leaves every maximum unchanged).
-// 16-leaf blocks per wave of select_f32_kernel: two (152 VGPRs, three waves per SIMD) 5.17 ms at
-// cfg3, four (229 VGPRs, two waves) 5.55, one (four waves, each row block's q reloaded per 16
-// leaves) 5.80
+// The products run on the bf16 MFMA over exact term splits (below): at cfg3 5.06 ms with fp32
+// operands and 4.11 with TF32 ones, against 5.19 and 5.38 for the same sweep on the fp32 MFMA
+// (16x16x4, four accumulation chains).  16-leaf blocks per wave: two (198 VGPRs for fp32 operands,
+// two waves per SIMD); one (150 VGPRs, three waves, each row block's q split once per 16 leaves)
+// 5.81 ms.
 constexpr int SEL_F32_LB = 2;
 template <bool QBF, bool SB, bool TF32>
 __global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict__ q, const float* __restrict__ mu,
@@ -2103,13 +2091,41 @@ __global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict_
     const int l0 = (blockIdx.x * 4 + w) * 16 * LB;            // this wave's 16 LB leaves
     if (l0 >= nb) return;                                      // (no barriers in this kernel)
     const int64_t srow = ((int64_t)h * ng + gi) * nb_pad;
-    float ga[LB][32];
+    // Products on the bf16 MFMA (16x16x32: k-step ks takes lane group grp's dims 32 ks + 8 grp ..
+    // + 7): g and q - mu each split into bf16 terms that sum to them exactly (a bf16 g: one term;
+    // TF32 operands: two; fp32: three), every term product formed, so each dim's product is
+    // exactly the one the fp32 MFMA forms and only the grouping of the fp32 sums differs.
+    constexpr int NG = SB ? 1 : (TF32 ? 2 : 3), ND = TF32 ? 2 : 3;
+    auto split = [&](float (&x)[8], bf16x8 (&t)[3], int n) {
 #pragma unroll
-    for (int lb = 0; lb < LB; ++lb)
-        load_f32<32, SB, TF32>((const char*)g + ((srow + min(l0 + 16 * lb + col, nb - 1)) * D + 32 * grp) * SBB,
-                               ga[lb]);
-    float mx[32];
-    load_f32<32, false, false>(mu + ((int64_t)h * mu_stride + gg) * D + 32 * grp, mx);
+        for (int tt = 0; tt < 3; ++tt) {
+            if (tt >= n) break;
+            const u32x4 u = {pack2bf(x[0], x[1]), pack2bf(x[2], x[3]), pack2bf(x[4], x[5]), pack2bf(x[6], x[7])};
+            t[tt] = as_bf16x8(u);
+            if (tt + 1 < n) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x[2 * e] = __fsub_rn(x[2 * e], __uint_as_float(u[e] << 16));
+                    x[2 * e + 1] = __fsub_rn(x[2 * e + 1], __uint_as_float(u[e] & 0xffff0000u));
+                }
+            }
+        }
+    };
+    bf16x8 gt[LB][4][3];
+#pragma unroll
+    for (int lb = 0; lb < LB; ++lb) {
+        const char* grow = (const char*)g + (srow + min(l0 + 16 * lb + col, nb - 1)) * D * SBB;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            float x[8];
+            load_f32<8, SB, TF32>(grow + (32 * ks + 8 * grp) * SBB, x);
+            split(x, gt[lb][ks], NG);
+        }
+    }
+    float mx[4][8];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        load_f32<8, false, false>(mu + ((int64_t)h * mu_stride + gg) * D + 32 * ks + 8 * grp, mx[ks]);
     float best[LB][4];
 #pragma unroll
     for (int lb = 0; lb < LB; ++lb)
@@ -2120,17 +2136,31 @@ __global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict_
         const int j = min(j0 + col, nsel - 1);
         const int tt = min(gg * group + j / rpt, nt - 1);
         const int64_t qi = min((int64_t)tt * tile + (j % rpt) * stride, nq - 1);
-        float dq[32];
-        load_f32<32, QBF, false>((const char*)q + (((int64_t)h * nq + perm_row(perm, h, nq, qi)) * D + 32 * grp) * QB,
-                                 dq);
+        const char* qrow = (const char*)q + ((int64_t)h * nq + perm_row(perm, h, nq, qi)) * D * QB;
+        bf16x8 dt[4][3];
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            dq[e] = __fsub_rn(dq[e], mx[e]);
-            if constexpr (TF32) dq[e] = tf32_rna(dq[e]);
+        for (int ks = 0; ks < 4; ++ks) {
+            float x[8];
+            load_f32<8, QBF, false>(qrow + (32 * ks + 8 * grp) * QB, x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                x[e] = __fsub_rn(x[e], mx[ks][e]);
+                if constexpr (TF32) x[e] = tf32_rna(x[e]);
+            }
+            split(x, dt[ks], ND);
         }
 #pragma unroll
         for (int lb = 0; lb < LB; ++lb) {
-            const f32x4 s4 = dot_tile_f32<4>(ga[lb], dq);
+            f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int sum = NG + ND - 2; sum >= 0; --sum)        // smaller products first
+#pragma unroll
+                for (int a = 0; a < NG; ++a) {
+                    const int b = sum - a;
+                    if (b < 0 || b >= ND) continue;
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) s4 = mfma_bf16(gt[lb][ks][a], dt[ks][b], s4);
+                }
 #pragma unroll
             for (int i = 0; i < 4; ++i) best[lb][i] = fmaxf(best[lb][i], s4[i]);
         }
