@@ -1808,12 +1808,12 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
                     va[s2][2 * e + 1] = bf2f(u[e] >> 16);
                 }
             }
-        } else {                                   // fp32 rows: dims 32 grp .. in chunks 8 grp + k
+        } else {                                   // fp32 rows (TF32: rounded in the slot): dims 32 grp ..
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
+            for (int kk = 0; kk < 8; ++kk) {           // .. in chunks 8 grp + k
                 const f32x4 f = *(const f32x4*)(sl + col * RBY + (((8 * grp + kk) ^ col) << 4));
 #pragma unroll
-                for (int e = 0; e < 4; ++e) ga[4 * kk + e] = TF32 ? tf32_rna(f[e]) : f[e];
+                for (int e = 0; e < 4; ++e) ga[4 * kk + e] = f[e];
             }
 #pragma unroll
             for (int s2 = 0; s2 < 4; ++s2) {
@@ -1822,7 +1822,7 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
                 for (int hf = 0; hf < 2; ++hf) {
                     const f32x4 f = *(const f32x4*)(sl + GV + r * RBY + (((2 * col + hf) ^ r) << 4));
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) va[s2][4 * hf + e] = TF32 ? tf32_rna(f[e]) : f[e];
+                    for (int e = 0; e < 4; ++e) va[s2][4 * hf + e] = f[e];
                 }
             }
         }
@@ -1837,11 +1837,26 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         }
         f32_update<TF32>(st, sc, va);
     };
+    // TF32 on fp32 rows: the workgroup rounds the block's g and vb rows in their slot once (each
+    // thread its chunks), instead of every wave rounding each operand it reads
+    auto far_round = [&](int slot) {
+        char* sl = &fring[slot][0];
+        for (int c = threadIdx.x; c < (2 * GV) / 16; c += blockDim.x) {
+            f32x4 f = *(const f32x4*)(sl + 16 * c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) f[e] = tf32_rna(f[e]);
+            *(f32x4*)(sl + 16 * c) = f;
+        }
+    };
     if (nblk > 0) far_issue(0, 0);
     for (int bi = 0; bi < nblk; ++bi) {
         wait_vmcnt<0>();                           // this wave's loads of block bi have landed
         __syncthreads();                           // every wave's; slot (bi + 1) & 1 is free
         if (bi + 1 < nblk) far_issue(bi + 1, (bi + 1) & 1);
+        if constexpr (TF32 && !SB) {
+            far_round(bi & 1);
+            __syncthreads();
+        }
         far_block(bi, bi & 1);
     }
     // Near-field score operands on the bf16 MFMA (16x16x32): k-step s takes lane group grp's dims
