@@ -1682,7 +1682,8 @@ __device__ __forceinline__ f32x4 dot_tile_f32(const float (&a)[32], const float 
 struct RowF32 {        // running softmax state of one row (h3/htrc_flat_triton.py:142-157)
     float m;           // running max (natural log units; the same in the four lanes of a row)
     float l;           // this lane's share of the running sum
-    f32x4 o[8];        // O^T: item i of block db is dim 8 (4 grp + i) + db
+    f32x4 o[8];        // O^T: item i of block db is dim 8 (4 grp + i) + db (far field), then
+                       // dim 16 db + 4 grp + i (near field)
 };
 
 // One block of 16 keys: scores sc[i] of keys 4 grp + i (masked: -inf), value rows va[s] = dims
@@ -1729,7 +1730,8 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     int nb_pad, int kx, int lps, int eps, float scale, float* __restrict__ pm, float* __restrict__ pl,
     float* __restrict__ pacc, float* __restrict__ out, float* __restrict__ logz) {
     constexpr int QB = QBF ? 2 : 4, SBB = SB ? 2 : 4;          // bytes per value
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, col = lane & 15,
+              grp = lane >> 4;
     const int tb = g0 * group, ntw = gridDim.x;
     const int t = tb + blockIdx.x, sp = blockIdx.y, ns = gridDim.y, h = blockIdx.z;
     const int64_t tw = (int64_t)h * ntw + blockIdx.x;         // partial row of the tile
@@ -1765,21 +1767,26 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     const int lo = sp * lps, hi = min(nb, lo + lps);
     const int64_t srow = gs * nb_pad;
     const int nblk = hi > lo ? (hi - lo + 15) / 16 : 0;
-    const int nw = blockDim.x >> 6;                // waves: 4 (64-row tiles) or 2
+    const int nw = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);   // waves: 4 (64-row tiles) or 2
     const uint32_t fring_lds = lds_addr(&fring[0][0]);
-    // block bi into slot: instruction i loads chunks p = 64 i + lane (g rows, then vb rows); rows
-    // up to c0 + 15 < nb_pad exist in the state (nb_pad is a multiple of 32, c0 of 16), those past
-    // hi are masked
+    // block bi into slot: instruction i (NI per matrix: g rows, then vb rows) loads chunks
+    // p = 64 i' + lane of its matrix (i' = i mod NI): row p / CR, chunk (p % CR) ^ row, from the
+    // block's first row (wave-uniform, in SGPRs) plus a 32-bit lane offset.  Wave w issues
+    // instructions w, w + nw, ..; rows up to c0 + 15 < nb_pad exist in the state (nb_pad is a
+    // multiple of 32, c0 of 16), those past hi are masked.
+    constexpr int NI = GV / 1024;
+    const int lr = lane / CR, lc = lane % CR;
     auto far_issue = [&](int bi, int slot) {
         const int c0 = lo + 16 * bi;
         const uint32_t sl = fring_lds + (uint32_t)(slot * FSLOT);
-        for (int i = w; i < (2 * GV) / 1024; i += nw) {
-            const int pc = 64 * i + lane;
-            const int isv = pc >= 16 * CR ? 1 : 0;
-            const int pr = pc - isv * 16 * CR;
-            const int r = pr / CR, c = (pr % CR) ^ r;
-            const char* base = isv ? (const char*)vb : (const char*)g;
-            dma16(base + (srow + c0 + r) * RBY + c * 16, sl + 1024 * i);
+        const char* gb = (const char*)g + (srow + c0) * RBY;
+        const char* vbb = (const char*)vb + (srow + c0) * RBY;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {         // nw >= 2: at most NI instructions per wave
+            const int i = w + nw * j;
+            if (i >= 2 * NI) break;
+            const int r = (64 / CR) * (i >= NI ? i - NI : i) + lr;
+            dma16s(i >= NI ? vbb : gb, (uint32_t)(r * RBY + ((lc ^ r) << 4)), sl + 1024 * i);
         }
         if (w == 0 && lane < 5)        // lz of the 16 leaves (lanes 0..3), their exclusion bytes (4)
             dma16(lane < 4 ? (const void*)(lz + srow + c0 + 4 * lane) : (const void*)(excl + srow + c0), sl + 2 * GV);
@@ -1894,18 +1901,15 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     }
     // ---- near field: 32 tokens per block, on the bf16 MFMA.  Scores in two 16-key halves (the
     // lane's keys 4 grp + i and 16 + 4 grp + i of the block); the PV products take the block's
-    // values from LDS, each row staged with its dims permuted (column 16 e + m holds dim 8 m + e),
-    // so the transposing read of column block db gives dims 8 m + db, the O^T layout the far
-    // field's fp32 products keep, and the weights as NPT bf16 terms that sum to them exactly
-    // (each product with a bf16 value exact, as in the fp32 MFMA).  The block's running maximum
-    // is taken over its 32 keys (the reference's block size is a launch parameter).
+    // values from LDS by transposing reads (O^T item i of block db: dim 16 db + 4 grp + i) and
+    // the weights as NPT bf16 terms that sum to them exactly (each product with a bf16 value
+    // exact, as in the fp32 MFMA).  The block's running maximum is taken over its 32 keys (the
+    // reference's block size is a launch parameter).
     constexpr int NPT = TF32 ? 2 : 3;
-    __shared__ __align__(16) char vstage[32 * 256];
     const int e_n = kx * leaf;
     const int e_lo = sp * eps, e_hi = min(e_n, e_lo + eps);
     const int64_t kh = (int64_t)h * nk;
     const int32_t* ix = idx + gs * (int64_t)(kx > 0 ? kx : 1);
-    const int tid = threadIdx.x, nth = blockDim.x;   // 4 tile threads: 256 or 128
     // a block's two 16-token runs (each in one leaf: leaf, e_lo and the split length are
     // multiples of 16): wave-uniform bases, and the last valid position of each (a run past e_hi
     // repeats the first run, masked)
@@ -1926,66 +1930,60 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         }
         return r;
     };
-    // two 16-byte pieces of a block's values per thread and round: piece c = base + tid + nth u is
-    // token c / 16, dims 8 (c % 16) .. + 7 (one round of 2 nth pieces for 64-row tiles, two for
-    // 32-row tiles, the second loaded as it is staged)
-    auto vload = [&](const Runs& r, u32x4 (&vr)[2], int base) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int c = base + tid + nth * u, row = c >> 4, j = c & 15, hh = row >> 4;
-            const int pos = min(row & 15, r.last[hh] >= 0 ? r.last[hh] : r.last[0]);
-            vr[u] = *(const u32x4*)(v + (r.b[hh] + pos) * D + 8 * j);
-        }
-    };
-    auto vstore = [&](const u32x4 (&vr)[2], int base) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int c = base + tid + nth * u, row = c >> 4, j = c & 15, sw = swz(row);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {          // dim 8 j + e -> column 16 e + j
-                const uint32_t w = vr[u][e >> 1];
-                *(uint16_t*)(vstage + row * 256 + (((2 * e + (j >> 3)) ^ sw) << 4) + ((j & 7) << 1)) =
-                    (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
-            }
-        }
-    };
-    // the block's 32 key rows into a slot of the far field's ring by direct loads (chunk c of row
-    // r at c ^ (r % 16), so the 16 lanes reading one chunk of 16 rows address 16 positions); a row
-    // past its run's last valid position repeats that position's token
-    auto kload = [&](const Runs& rr, int slot) {
-        const uint32_t sl = fring_lds + (uint32_t)(slot * FSLOT);
-        for (int i = w; i < 8; i += nw) {
-            const int pc = 64 * i + lane, row = pc >> 4, hh = row >> 4, c = (pc & 15) ^ (row & 15);
-            const int pos = min(row & 15, rr.last[hh] >= 0 ? rr.last[hh] : rr.last[0]);
-            dma16(k + (rr.b[hh] + pos) * D + 8 * c, sl + 1024 * i);
-        }
-    };
-    u32x4 vr[2];
-    Runs rn{};
+    // The accumulators move to the near field's order through this wave's 8 KB of the far ring
+    // (row col, 16-byte chunk c at c ^ col): far order dims 32 grp + 8 i + 4 hf .. + 3 (chunk
+    // 8 grp + 2 i + hf) = st.o[4 hf .. 4 hf + 3][i]; near order dims 16 db + 4 grp .. + 3 (chunk
+    // 4 db + grp) = st.o[db].
     __syncthreads();                            // every wave done with the far field's slots
+    {
+        char* tw_ = &fring[0][0] + w * 8192;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+                *(f32x4*)(tw_ + col * 512 + (((8 * grp + 2 * i + hf) ^ col) << 4)) =
+                    f32x4{st.o[4 * hf][i], st.o[4 * hf + 1][i], st.o[4 * hf + 2][i], st.o[4 * hf + 3][i]};
+        __syncthreads();
+#pragma unroll
+        for (int db = 0; db < 8; ++db) st.o[db] = *(const f32x4*)(tw_ + col * 512 + (((4 * db + grp) ^ col) << 4));
+    }
+    __syncthreads();                            // every wave's accumulators read: the slots are free
+    // a block's 32 key rows (bytes 0.., chunk c of row r at c ^ (r % 16), so the 16 lanes that
+    // read one chunk of 16 rows address 16 positions) and its 32 value rows (bytes 8192.., chunk
+    // c of row r at c ^ swz(r), the transposing reads' layout) into a slot of the far field's
+    // ring by direct loads; a row past its run's last valid position repeats that position's token
+    // (instruction i: keys for i < 8, values after; its rows 4 (i % 8) + lane / 16, in run
+    // hh = (i % 8) / 4, wave-uniform; the run's first token in SGPRs, a 32-bit lane offset)
+    auto kvload = [&](const Runs& rr, int slot) {
+        const uint32_t sl = fring_lds + (uint32_t)(slot * FSLOT);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {           // nw >= 2: at most 8 instructions per wave
+            const int i = w + nw * j;
+            if (i >= 16) break;
+            const int isv = i >> 3, ii = i & 7, hh = ii >> 2;
+            const int rw = 4 * (ii & 3) + (lane >> 4);       // row % 16
+            const int lst = hh ? (rr.last[1] >= 0 ? rr.last[1] : rr.last[0]) : rr.last[0];
+            const int c = (lane & 15) ^ (isv ? swz(rw) : rw);
+            dma16s((isv ? v : k) + (hh ? rr.b[1] : rr.b[0]) * D, (uint32_t)(min(rw, lst) * 256 + (c << 4)),
+                   sl + 1024 * i);
+        }
+    };
+    Runs rn{};
     if (e_lo < e_hi) {
         rn = runs(e_lo);
-        kload(rn, 0);                           // issued before the values: waiting for those
-        vload(rn, vr, 0);                       // (in issue order) waits for the keys too
+        kvload(rn, 0);
     }
     int kslot = 0;
     for (int e0 = e_lo; e0 < e_hi; e0 += 32, kslot ^= 1) {
         const Runs cur = rn;
-        __syncthreads();                        // every wave done with the previous block's values
-        vstore(vr, 0);
-        for (int base = 2 * nth; base < 512; base += 2 * nth) {
-            u32x4 vx[2];
-            vload(cur, vx, base);
-            vstore(vx, base);
-        }
-        wait_vmcnt<0>();                        // this block's keys have landed (and its values)
-        if (e0 + 32 < e_hi) {                   // the next block's keys and values load under this one
+        wait_vmcnt<0>();                        // this wave's loads of the block have landed
+        __syncthreads();                        // every wave's; the other slot is free
+        if (e0 + 32 < e_hi) {                   // the next block loads under this one
             rn = runs(e0 + 32);
-            kload(rn, kslot ^ 1);
-            vload(rn, vr, 0);
+            kvload(rn, kslot ^ 1);
         }
-        __syncthreads();                        // the block's values and keys staged
         const char* ks_ = &fring[kslot][0];
+        const char* vs_ = ks_ + 8192;
         float sc[8];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
@@ -2046,27 +2044,24 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         }
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
-            const u32x2 a0 = tr_operand(vstage, 0, db, lane), a1 = tr_operand(vstage, 16, db, lane);
+            const u32x2 a0 = tr_operand(vs_, 0, db, lane), a1 = tr_operand(vs_, 16, db, lane);
             const bf16x8 A = as_bf16x8(a0, a1);
 #pragma unroll
             for (int tt = NPT - 1; tt >= 0; --tt) st.o[db] = mfma_bf16(A, pt[tt], st.o[db]);
         }
     }
     const float ltot = grp_sum(st.l);
-    // the lane's O^T items in dim order: dims 32 grp + 8 i + db are st.o[db][i]
-    auto dims4 = [&](int i, int hf, float den) {
-        return f32x4{__fdiv_rn(st.o[4 * hf][i], den), __fdiv_rn(st.o[4 * hf + 1][i], den),
-                     __fdiv_rn(st.o[4 * hf + 2][i], den), __fdiv_rn(st.o[4 * hf + 3][i], den)};
-    };
+    // the lane's O^T items: dims 16 db + 4 grp .. + 3 are st.o[db]
     if (pacc == nullptr) {                                     // single split: normalise in place
         if (qi >= nq) return;
         const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
         const float ms = st.m == -INFINITY ? 0.0f : st.m;
         const float den = ltot < 1e-30f ? 1e-30f : ltot;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) *(f32x4*)(out + orow * D + 32 * grp + 8 * i + 4 * hf) = dims4(i, hf, den);
+        for (int db = 0; db < 8; ++db)
+            *(f32x4*)(out + orow * D + 16 * db + 4 * grp) =
+                f32x4{__fdiv_rn(st.o[db][0], den), __fdiv_rn(st.o[db][1], den), __fdiv_rn(st.o[db][2], den),
+                      __fdiv_rn(st.o[db][3], den)};
         if (grp == 0) logz[orow] = __fadd_rn(ms, __logf(ltot));
         return;
     }
@@ -2076,9 +2071,7 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         pl[base] = ltot;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) *(f32x4*)(pacc + base * D + 32 * grp + 8 * i + 4 * hf) = dims4(i, hf, 1.0f);
+    for (int db = 0; db < 8; ++db) *(f32x4*)(pacc + base * D + 16 * db + 4 * grp) = st.o[db];
 }
 
 // SEL[g, l] = max over every stride-th row of the group's tiles of (q - mu_g) . g_l, + lz_l, with
