@@ -2075,16 +2075,18 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
 }
 
 // SEL[g, l] = max over every stride-th row of the group's tiles of (q - mu_g) . g_l, + lz_l, with
-// fp32 dots (h3/htrc_flat_triton.py:214-254, DOT = 0).  Workgroup = one group x 4 SEL_F32_LB x 16
-// leaves; each wave holds the A operands of its SEL_F32_LB blocks of 16 leaves and sweeps the
-// group's rows 16 at a time (rows past the last query repeat it, tiles past the last repeat it: as the
-// reference pads them, which leaves every maximum unchanged).
-// The products run on the bf16 MFMA over exact term splits (below): at cfg3 5.06 ms with fp32
-// operands and 4.11 with TF32 ones, against 5.19 and 5.38 for the same sweep on the fp32 MFMA
-// (16x16x4, four accumulation chains).  16-leaf blocks per wave: two (198 VGPRs for fp32 operands,
-// two waves per SIMD); one (150 VGPRs, three waves, each row block's q split once per 16 leaves)
-// 5.81 ms.
-constexpr int SEL_F32_LB = 2;
+// fp32 dots (h3/htrc_flat_triton.py:214-254, DOT = 0).  Workgroup = one group x SEL_F32_LPW
+// leaves, 4 waves; wave w holds the split q - mu of 16 of the group's sampled rows (rows 64 c +
+// 16 w .. of row chunk c; rows past the last repeat it, tiles past the last repeat it, as the
+// reference pads them, which leaves every maximum unchanged) and the workgroup streams its
+// leaves' g rows 16 at a time: each thread fetches its 8 dims of one leaf two blocks ahead into
+// registers and splits them once into the block's bf16 terms in LDS (two buffers, one barrier
+// per block), which every wave reads as its MFMA operands.
+// Products on the bf16 MFMA (16x16x32, rows as A, leaves as B: k-step ks takes lane group grp's
+// dims 32 ks + 8 grp .. + 7): g and q - mu each split into bf16 terms that sum to them exactly (a
+// bf16 g: one term; TF32 operands: two; fp32: three), every term product formed, so each dim's
+// product is exactly the one the fp32 MFMA forms and only the grouping of the fp32 sums differs.
+constexpr int SEL_F32_LPW = 256;   // leaves per workgroup
 template <bool QBF, bool SB, bool TF32>
 __global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict__ q, const float* __restrict__ mu,
                                                          int mu_stride, const void* __restrict__ g,
@@ -2093,17 +2095,16 @@ __global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict_
                                                          const int32_t* __restrict__ perm, int nb, int nb_pad,
                                                          float* __restrict__ sel) {
     constexpr int QB = QBF ? 2 : 4, SBB = SB ? 2 : 4;
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    const int gi = blockIdx.y, h = blockIdx.z, gg = g0 + gi;
-    constexpr int LB = SEL_F32_LB;
-    const int l0 = (blockIdx.x * 4 + w) * 16 * LB;            // this wave's 16 LB leaves
-    if (l0 >= nb) return;                                      // (no barriers in this kernel)
-    const int64_t srow = ((int64_t)h * ng + gi) * nb_pad;
-    // Products on the bf16 MFMA (16x16x32: k-step ks takes lane group grp's dims 32 ks + 8 grp ..
-    // + 7): g and q - mu each split into bf16 terms that sum to them exactly (a bf16 g: one term;
-    // TF32 operands: two; fp32: three), every term product formed, so each dim's product is
-    // exactly the one the fp32 MFMA forms and only the grouping of the fp32 sums differs.
     constexpr int NG = SB ? 1 : (TF32 ? 2 : 3), ND = TF32 ? 2 : 3;
+    constexpr int RW = SB ? 1 : 2;                             // 16-byte pieces per 8 dims of g
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, col = lane & 15,
+              grp = lane >> 4, tid = threadIdx.x;
+    const int gi = blockIdx.y, h = blockIdx.z, gg = g0 + gi;
+    const int lw0 = blockIdx.x * SEL_F32_LPW, nlw = min(nb - lw0, SEL_F32_LPW);   // leaves [lw0, lw0 + nlw)
+    const int nblk = (nlw + 15) / 16;
+    const int64_t srow = ((int64_t)h * ng + gi) * nb_pad;
+    __shared__ __align__(16) char terms[2][NG][16 * 256];     // block terms: leaf row of 256 B, chunk c at c ^ leaf
+    __shared__ float wmax[4][SEL_F32_LPW];                     // per wave: each leaf's max over its rows
     auto split = [&](float (&x)[8], bf16x8 (&t)[3], int n) {
 #pragma unroll
         for (int tt = 0; tt < 3; ++tt) {
@@ -2119,68 +2120,92 @@ __global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict_
             }
         }
     };
-    bf16x8 gt[LB][4][3];
+    // thread tid's part of block b: leaf 16 b + tid / 16 (the last leaf past the range), dims
+    // 8 (tid % 16) .. + 7
+    auto gfetch = [&](int b, u32x4 (&raw)[RW]) {
+        const int leaf = lw0 + min(16 * b + (tid >> 4), nlw - 1);
+        const char* p = (const char*)g + ((srow + leaf) * D + 8 * (tid & 15)) * SBB;
 #pragma unroll
-    for (int lb = 0; lb < LB; ++lb) {
-        const char* grow = (const char*)g + (srow + min(l0 + 16 * lb + col, nb - 1)) * D * SBB;
+        for (int u = 0; u < RW; ++u) raw[u] = *(const u32x4*)(p + 16 * u);
+    };
+    auto gstage = [&](const u32x4 (&raw)[RW], int buf) {
+        float x[8];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            float x[8];
-            load_f32<8, SB, TF32>(grow + (32 * ks + 8 * grp) * SBB, x);
-            split(x, gt[lb][ks], NG);
+        for (int e = 0; e < 8; ++e) {
+            if constexpr (SB) x[e] = bf2f((e & 1) ? (raw[0][e >> 1] >> 16) : (raw[0][e >> 1] & 0xffffu));
+            else x[e] = TF32 ? tf32_rna(__uint_as_float(raw[e >> 2][e & 3])) : __uint_as_float(raw[e >> 2][e & 3]);
         }
-    }
-    float mx[4][8];
+        bf16x8 t[3];
+        split(x, t, NG);
+        const int lf = tid >> 4, c = tid & 15;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-        load_f32<8, false, false>(mu + ((int64_t)h * mu_stride + gg) * D + 32 * ks + 8 * grp, mx[ks]);
-    float best[LB][4];
-#pragma unroll
-    for (int lb = 0; lb < LB; ++lb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) best[lb][i] = -INFINITY;
+        for (int a = 0; a < NG; ++a) *(bf16x8*)(&terms[buf][a][lf * 256 + ((c ^ lf) << 4)]) = t[a];
+    };
+    for (int i = lane; i < SEL_F32_LPW; i += 64) wmax[w][i] = -INFINITY;
+    const float* murow = mu + ((int64_t)h * mu_stride + gg) * D + 8 * grp;
     const int rpt = tile / stride, nsel = group * rpt;
-    for (int j0 = 0; j0 < nsel; j0 += 16) {
-        const int j = min(j0 + col, nsel - 1);
-        const int tt = min(gg * group + j / rpt, nt - 1);
-        const int64_t qi = min((int64_t)tt * tile + (j % rpt) * stride, nq - 1);
-        const char* qrow = (const char*)q + ((int64_t)h * nq + perm_row(perm, h, nq, qi)) * D * QB;
+    for (int rc = 0; rc < nsel; rc += 64) {
+        const bool active = rc + 16 * w < nsel;                // wave-uniform: the wave has rows here
         bf16x8 dt[4][3];
+        if (active) {
+            const int j = min(rc + 16 * w + col, nsel - 1);
+            const int tt = min(gg * group + j / rpt, nt - 1);
+            const int64_t qi = min((int64_t)tt * tile + (j % rpt) * stride, nq - 1);
+            const char* qrow = (const char*)q + ((int64_t)h * nq + perm_row(perm, h, nq, qi)) * D * QB;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            float x[8];
-            load_f32<8, QBF, false>(qrow + (32 * ks + 8 * grp) * QB, x);
+            for (int ks = 0; ks < 4; ++ks) {
+                float x[8], mx[8];
+                load_f32<8, QBF, false>(qrow + (32 * ks + 8 * grp) * QB, x);
+                load_f32<8, false, false>(murow + 32 * ks, mx);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                x[e] = __fsub_rn(x[e], mx[ks][e]);
-                if constexpr (TF32) x[e] = tf32_rna(x[e]);
-            }
-            split(x, dt[ks], ND);
-        }
-#pragma unroll
-        for (int lb = 0; lb < LB; ++lb) {
-            f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int sum = NG + ND - 2; sum >= 0; --sum)        // smaller products first
-#pragma unroll
-                for (int a = 0; a < NG; ++a) {
-                    const int b = sum - a;
-                    if (b < 0 || b >= ND) continue;
-#pragma unroll
-                    for (int ks = 0; ks < 4; ++ks) s4 = mfma_bf16(gt[lb][ks][a], dt[ks][b], s4);
+                for (int e = 0; e < 8; ++e) {
+                    x[e] = __fsub_rn(x[e], mx[e]);
+                    if constexpr (TF32) x[e] = tf32_rna(x[e]);
                 }
+                split(x, dt[ks], ND);
+            }
+        }
+        // block b: its terms in buffer b % 2; rs holds block b + 1's raw g, refilled with b + 3
+        auto step = [&](int b, u32x4 (&rs)[RW]) {
+            if (active) {
+                const char* tb_ = &terms[b & 1][0][0];
+                f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) best[lb][i] = fmaxf(best[lb][i], s4[i]);
+                for (int sum = NG + ND - 2; sum >= 0; --sum)    // smaller products first
+#pragma unroll
+                    for (int a = 0; a < NG; ++a) {
+                        const int bt = sum - a;
+                        if (bt < 0 || bt >= ND) continue;
+#pragma unroll
+                        for (int ks = 0; ks < 4; ++ks) {
+                            const bf16x8 gb = *(const bf16x8*)(tb_ + a * (16 * 256) + col * 256 + (((4 * ks + grp) ^ col) << 4));
+                            s4 = mfma_bf16(dt[ks][bt], gb, s4);
+                        }
+                    }
+                // rows 4 grp + i of leaf 16 b + col: the max over the wave's 16 rows
+                float m = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3]));
+                m = grp_max(m);
+                if (grp == 0) wmax[w][16 * b + col] = fmaxf(wmax[w][16 * b + col], m);
+            }
+            if (b + 1 < nblk) gstage(rs, (b + 1) & 1);
+            if (b + 3 < nblk) gfetch(b + 3, rs);
+            __syncthreads();
+        };
+        u32x4 ra[RW], rb[RW];
+        gfetch(0, ra);
+        gstage(ra, 0);
+        if (nblk > 1) gfetch(1, ra);
+        if (nblk > 2) gfetch(2, rb);
+        __syncthreads();
+        for (int b = 0; b < nblk; b += 2) {
+            step(b, ra);
+            if (b + 1 < nblk) step(b + 1, rb);
         }
     }
-#pragma unroll
-    for (int lb = 0; lb < LB; ++lb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float m = col_max(best[lb][i]);          // over the 16 rows of the lane group
-            const int c = l0 + 16 * lb + 4 * grp + i;
-            if (col == 0 && c < nb) sel[srow + c] = __fadd_rn(m, lz[srow + c]);
-        }
+    for (int i = tid; i < nlw; i += 256) {
+        const float m = fmaxf(fmaxf(wmax[0][i], wmax[1][i]), fmaxf(wmax[2][i], wmax[3][i]));
+        sel[srow + lw0 + i] = __fadd_rn(m, lz[srow + lw0 + i]);
+    }
 }
 
 // merge: (h3/htrc_flat_triton.py:257-273) + logZ = mm + log(den).  One workgroup (4 * tile
@@ -4527,7 +4552,7 @@ int htrc_select_f32(const void* q, int q_is_bf16, const float* mu, const void* g
     int64_t ng, tb, ntw;
     REQUIRE(group_window(nt, group, g0, gn, ng, tb, ntw), "htrc_select_f32: group window [g0, g0 + gn) must lie in the head's groups");
     REQUIRE(gn <= 65535, "htrc_select_f32: at most 65535 groups per launch");
-    const int64_t per = 4 * 16 * SEL_F32_LB;               // leaves per workgroup
+    const int64_t per = SEL_F32_LPW;                       // leaves per workgroup
     const dim3 grid((unsigned)((nb + per - 1) / per), (unsigned)gn, (unsigned)heads);
     hipStream_t s = (hipStream_t)stream;
     F32_DISPATCH(select_f32_kernel, grid, dim3(256), q, mu, (int)ng, g, lz, nq, (int)nt, tile, stride, group, (int)g0,
