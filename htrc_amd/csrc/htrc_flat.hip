@@ -1670,6 +1670,37 @@ __device__ __forceinline__ void load_f32(const void* p, float (&x)[N]) {
     }
 }
 
+// x (8 floats) as n bf16 terms whose sum is x exactly: each term the bf16 rounding of what the
+// terms before it leave (that residual is exact in fp32); n = 3 holds any fp32 value, n = 2 a
+// TF32 one, n = 1 a bf16 one.  x is consumed.
+__device__ __forceinline__ void split_terms(float (&x)[8], bf16x8 (&t)[3], int n) {
+#pragma unroll
+    for (int tt = 0; tt < 3; ++tt) {
+        if (tt >= n) break;
+        const u32x4 u = {pack2bf(x[0], x[1]), pack2bf(x[2], x[3]), pack2bf(x[4], x[5]), pack2bf(x[6], x[7])};
+        t[tt] = as_bf16x8(u);
+        if (tt + 1 < n) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[2 * e] = __fsub_rn(x[2 * e], __uint_as_float(u[e] << 16));
+                x[2 * e + 1] = __fsub_rn(x[2 * e + 1], __uint_as_float(u[e] & 0xffff0000u));
+            }
+        }
+    }
+}
+// 16x16x16 bf16 MFMA: a and b hold 4 bf16 each (A[l % 16][4 (l / 16) + j], B[4 (l / 16) + j][l % 16])
+__device__ __forceinline__ f32x4 mfma_bf16_k16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c, 0,
+                                                      0, 0);
+}
+
+struct RowF32 {        // running softmax state of one row (h3/htrc_flat_triton.py:142-157)
+    float m;           // running max (natural log units; the same in the four lanes of a row)
+    float l;           // this lane's share of the running sum
+    f32x4 o[8];        // O^T: item i of block db is dim 16 db + 4 grp + i (the fp32-MFMA far
+                       // field keeps dim 8 (4 grp + i) + db and reorders once, before the near field)
+};
+
 // S^T tile of 16 keys x 16 rows: item i of lane l = sum over dims of key (4 (l/16) + i)'s A row
 // and row l%16's B row, from the 32 dims each lane holds of both.
 __device__ __forceinline__ f32x4 dot_tile_f32(const float (&a)[32], const float (&b)[32]) {
@@ -1678,13 +1709,6 @@ __device__ __forceinline__ f32x4 dot_tile_f32(const float (&a)[32], const float 
     for (int s = 0; s < 32; ++s) c = mfma_f32(a[s], b[s], c);
     return c;
 }
-
-struct RowF32 {        // running softmax state of one row (h3/htrc_flat_triton.py:142-157)
-    float m;           // running max (natural log units; the same in the four lanes of a row)
-    float l;           // this lane's share of the running sum
-    f32x4 o[8];        // O^T: item i of block db is dim 8 (4 grp + i) + db (far field), then
-                       // dim 16 db + 4 grp + i (near field)
-};
 
 // One block of 16 keys: scores sc[i] of keys 4 grp + i (masked: -inf), value rows va[s] = dims
 // 8 col .. + 7 of key 4 grp + s.  The reference's update: m_new = max(m, rowmax), m_s = m_new, or
@@ -1715,6 +1739,7 @@ __device__ __forceinline__ void f32_update(RowF32& st, const float (&sc)[4], con
     st.m = mn;
 }
 
+
 // Far + near field of one (tile, split) with fp32 dots (h3/htrc_flat_triton.py:88-211, DOT = 0):
 // far leaves [sp lps, + lps) not excluded, score = (q - mu) . g + lz; near tokens [sp eps, + eps)
 // of the tile group's idx leaves, score = (q . k) scale.  One wave per 16 rows; the workgroup
@@ -1739,15 +1764,38 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     const int r = 16 * w + col;                                // blockDim = 4 * tile: one wave per 16 rows
     const int64_t qi = (int64_t)t * tile + r;                  // pad rows repeat the last query
     const int64_t src = perm_row(perm, h, nq, qi < nq ? qi : nq - 1);
-    float qx[32], dq[32];
-    load_f32<32, QBF, false>((const char*)q + (((int64_t)h * nq + src) * D + 32 * grp) * QB, qx);
-    {
+    // Products on the bf16 MFMA over exact bf16 terms (split_terms): a state value (g, vb) in NGT
+    // terms, q - mu in ND, a far weight in NPF, so every product is the exact product the fp32
+    // MFMA forms and only the grouping of the fp32 sums differs.
+    constexpr int NGT = SB ? 1 : (TF32 ? 2 : 3), ND = TF32 ? 2 : 3, NPF = TF32 ? 2 : 3;
+    // The far field takes these products for TF32 operands and bf16 rows; for IEEE operands on
+    // fp32 rows it runs on the fp32 MFMA (v_mfma_f32_16x16x4_f32), which measured faster there:
+    // three terms of every state value cost more splitting than their products save.
+    constexpr bool FTERMS = TF32 || SB;
+    // q - mu of row r: k-step ks holds lane group grp's dims 32 ks + 8 grp .. + 7 (FTERMS), or
+    // the fp32 values of dims 32 grp .. + 31
+    bf16x8 dqt[4][3];
+    float dq[32];
+    if constexpr (!FTERMS) {
         float mx[32];
+        load_f32<32, QBF, false>((const char*)q + (((int64_t)h * nq + src) * D + 32 * grp) * QB, dq);
         load_f32<32, false, false>(mu + ((int64_t)h * mu_stride + t / group) * D + 32 * grp, mx);
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            dq[e] = __fsub_rn(qx[e], mx[e]);
-            if constexpr (TF32) dq[e] = tf32_rna(dq[e]);
+        for (int e = 0; e < 32; ++e) dq[e] = __fsub_rn(dq[e], mx[e]);
+    } else {
+        const char* qrow = (const char*)q + ((int64_t)h * nq + src) * D * QB;
+        const float* murow = mu + ((int64_t)h * mu_stride + t / group) * D + 8 * grp;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            float x[8], mx[8];
+            load_f32<8, QBF, false>(qrow + (32 * ks + 8 * grp) * QB, x);
+            load_f32<8, false, false>(murow + 32 * ks, mx);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                x[e] = __fsub_rn(x[e], mx[e]);
+                if constexpr (TF32) x[e] = tf32_rna(x[e]);
+            }
+            split_terms(x, dqt[ks], ND);
         }
     }
     RowF32 st;
@@ -1755,82 +1803,185 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     st.l = 0.0f;
 #pragma unroll
     for (int db = 0; db < 8; ++db) st.o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // ---- far field: 16 leaves per block, the block's state rows staged in LDS by direct loads
-    // one block ahead (two slots) and read by all the workgroup's waves.  Slot: g rows, vb rows
-    // (16 each), lz (16 floats), the exclusion bytes.  Row r keeps its 16-byte chunk c at position
-    // c ^ r, so the 16 lanes that read one chunk of 16 rows address 16 positions.
+    // ---- far field: 16 leaves per block.  The block's state rows reach a raw slot in LDS by
+    // direct loads (g rows, vb rows, lz, the exclusion bytes; row r keeps its 16-byte chunk c at
+    // c ^ r); the workgroup then splits them once into bf16 terms (g term rows with chunk c at
+    // c ^ leaf, for the score operands; vb term rows with chunk c at c ^ swz(leaf), for the
+    // transposing PV reads) and loads the next block into the raw slot while its waves take
+    // their products from the terms.  The near field reuses the buffer as two key + value slots.
     constexpr int RBY = D * SBB;                   // state row bytes: 512 (fp32) or 256 (bf16)
     constexpr int CR = RBY / 16;                   // chunks per row: 32 or 16
     constexpr int GV = 16 * RBY;                   // g rows of a block; the vb rows follow
-    constexpr int FSLOT = 2 * 16 * D * 4 + 128;
-    __shared__ __align__(16) char fring[2][FSLOT];
+    constexpr int RAW = 2 * GV + 128;              // raw slot: g, vb rows, lz (64 B), exclusion bytes
+    constexpr int TB = 16 * 256;                   // one term of 16 leaf rows (bf16)
+    constexpr int NSLOT = 16384;                   // near field slot: 32 key rows, 32 value rows
+    constexpr int FSLOT = RAW;                     // fp32-MFMA far field: two raw slots, no terms
+    constexpr int LDSZ_T = RAW + 2 * NGT * TB + 128 > 2 * NSLOT ? RAW + 2 * NGT * TB + 128 : 2 * NSLOT;
+    constexpr int LDSZ = FTERMS ? LDSZ_T : (2 * FSLOT > 2 * NSLOT ? 2 * FSLOT : 2 * NSLOT);
+    __shared__ __align__(16) char lbuf[LDSZ];
+    char* const tgs = lbuf + RAW;                  // g terms
+    char* const tvs = tgs + NGT * TB;              // vb terms
+    char* const taux = tvs + NGT * TB;             // the block's lz (16 floats) and exclusion bytes
     const int lo = sp * lps, hi = min(nb, lo + lps);
     const int64_t srow = gs * nb_pad;
     const int nblk = hi > lo ? (hi - lo + 15) / 16 : 0;
     const int nw = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);   // waves: 4 (64-row tiles) or 2
-    const uint32_t fring_lds = lds_addr(&fring[0][0]);
-    // block bi into slot: instruction i (NI per matrix: g rows, then vb rows) loads chunks
+    const int tid = threadIdx.x, nth = blockDim.x;
+    const uint32_t lbuf_lds = lds_addr(lbuf);
+    // block bi into the raw slot: instruction i (NI per matrix: g rows, then vb rows) loads chunks
     // p = 64 i' + lane of its matrix (i' = i mod NI): row p / CR, chunk (p % CR) ^ row, from the
     // block's first row (wave-uniform, in SGPRs) plus a 32-bit lane offset.  Wave w issues
     // instructions w, w + nw, ..; rows up to c0 + 15 < nb_pad exist in the state (nb_pad is a
-    // multiple of 32, c0 of 16), those past hi are masked.
+    // multiple of 32, c0 of 16; rows past nb hold the zero state of padded leaves), those past
+    // hi are masked.
     constexpr int NI = GV / 1024;
     const int lr = lane / CR, lc = lane % CR;
-    auto far_issue = [&](int bi, int slot) {
+    auto far_issue = [&](int bi, uint32_t dst) {
         const int c0 = lo + 16 * bi;
-        const uint32_t sl = fring_lds + (uint32_t)(slot * FSLOT);
         const char* gb = (const char*)g + (srow + c0) * RBY;
         const char* vbb = (const char*)vb + (srow + c0) * RBY;
+        int lrx = lr;
+        asm volatile("" : "+v"(lrx));          // the lane offsets computed here, not held across the loop
 #pragma unroll
         for (int j = 0; j < NI; ++j) {         // nw >= 2: at most NI instructions per wave
             const int i = w + nw * j;
             if (i >= 2 * NI) break;
-            const int r = (64 / CR) * (i >= NI ? i - NI : i) + lr;
-            dma16s(i >= NI ? vbb : gb, (uint32_t)(r * RBY + ((lc ^ r) << 4)), sl + 1024 * i);
+            const int r = (64 / CR) * (i >= NI ? i - NI : i) + lrx;
+            dma16s(i >= NI ? vbb : gb, (uint32_t)(r * RBY + ((lc ^ r) << 4)), dst + 1024 * i);
         }
         if (w == 0 && lane < 5)        // lz of the 16 leaves (lanes 0..3), their exclusion bytes (4)
-            dma16(lane < 4 ? (const void*)(lz + srow + c0 + 4 * lane) : (const void*)(excl + srow + c0), sl + 2 * GV);
+            dma16(lane < 4 ? (const void*)(lz + srow + c0 + 4 * lane) : (const void*)(excl + srow + c0),
+                  dst + 2 * GV);
     };
-    auto far_block = [&](int bi, int slot) {
+    // raw slot -> terms: unit u = leaf u / 16, dims 8 (u % 16) .. + 7 of g and of vb (TF32: each
+    // value rounded first); the lz and exclusion bytes copied beside the terms
+    auto far_split = [&]() {
+        for (int u = tid; u < 256; u += nth) {
+            const int lf = u >> 4, c = u & 15;
+#pragma unroll
+            for (int mtx = 0; mtx < 2; ++mtx) {
+                const char* row = lbuf + mtx * GV + lf * RBY;
+                float x[8];
+                if constexpr (SB) {
+                    const u32x4 raw = *(const u32x4*)(row + ((c ^ lf) << 4));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        x[2 * e] = bf2f(raw[e] & 0xffffu);
+                        x[2 * e + 1] = bf2f(raw[e] >> 16);
+                    }
+                } else {
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) {
+                        const f32x4 f = *(const f32x4*)(row + (((2 * c + hf) ^ lf) << 4));
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) x[4 * hf + e] = TF32 ? tf32_rna(f[e]) : f[e];
+                    }
+                }
+                bf16x8 tt[3];
+                split_terms(x, tt, NGT);
+                char* dst = mtx == 0 ? tgs + lf * 256 + ((c ^ lf) << 4) : tvs + lf * 256 + ((c ^ swz(lf)) << 4);
+#pragma unroll
+                for (int a = 0; a < NGT; ++a) *(bf16x8*)(dst + a * TB) = tt[a];
+            }
+        }
+        if (tid < 5) *(u32x4*)(taux + 16 * tid) = *(const u32x4*)(lbuf + 2 * GV + 16 * tid);
+    };
+    // the reference's update over the block (h3/htrc_flat_triton.py:142-157): m_new = max(m,
+    // rowmax), m_s = m_new or 0 when -inf, p = exp(sc - m_s), alpha = exp(m - m_s), l = l alpha +
+    // sum p, O = O alpha + P V
+    auto far_block = [&](int bi) {
         const int c0 = lo + 16 * bi;
-        const char* sl = &fring[slot][0];
+        // S^T: leaf 4 grp + i, row col (g terms as A, q - mu terms as B), smaller products first
+        f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int sum = NGT + ND - 2; sum >= 0; --sum)
+#pragma unroll
+            for (int a = 0; a < NGT; ++a) {
+                const int b = sum - a;
+                if (b < 0 || b >= ND) continue;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const bf16x8 ga = *(const bf16x8*)(tgs + a * TB + col * 256 + (((4 * ks + grp) ^ col) << 4));
+                    s4 = mfma_bf16(ga, dqt[ks][b], s4);
+                }
+            }
+        const f32x4 lz4 = *(const f32x4*)(taux + 16 * grp);
+        const uint32_t ex4 = *(const uint32_t*)(taux + 64 + 4 * grp);
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = c0 + 4 * grp + i;
+            sc[i] = (c < hi && ((ex4 >> (8 * i)) & 0xffu) == 0) ? __fadd_rn(s4[i], lz4[i]) : -INFINITY;
+        }
+        const float bm = grp_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+        const float mn = fmaxf(st.m, bm);
+        const float ms = mn == -INFINITY ? 0.0f : mn;
+        float pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[i] = __expf(__fsub_rn(sc[i], ms));
+        const float alpha = __expf(__fsub_rn(st.m, ms));
+        st.l = __fadd_rn(__fmul_rn(st.l, alpha), __fadd_rn(__fadd_rn(pr[0], pr[1]), __fadd_rn(pr[2], pr[3])));
+        // O alpha: skipped when every row's alpha is 1 (no running maximum moved: the same bits)
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) st.o[db][i] = __fmul_rn(st.o[db][i], alpha);
+        }
+        st.m = mn;
+        // the weights (TF32-rounded for TF32 operands) as NPF bf16 terms: B of the 16x16x16
+        // products, k = leaf 4 grp + j
+        u32x2 pt[3];
+        {
+            float x[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = TF32 ? tf32_rna(pr[i]) : pr[i];
+#pragma unroll
+            for (int tt = 0; tt < NPF; ++tt) {
+                const u32x2 u = {pack2bf(x[0], x[1]), pack2bf(x[2], x[3])};
+                pt[tt] = u;
+                if (tt + 1 < NPF) {
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        x[2 * e] = __fsub_rn(x[2 * e], __uint_as_float(u[e] << 16));
+                        x[2 * e + 1] = __fsub_rn(x[2 * e + 1], __uint_as_float(u[e] & 0xffff0000u));
+                    }
+                }
+            }
+        }
+        // O^T += vb^T P^T: A = vb terms by transposing reads (leaves 4 grp + j, dim 16 db + col)
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+#pragma unroll
+            for (int sum = NGT + NPF - 2; sum >= 0; --sum)
+#pragma unroll
+                for (int a = 0; a < NGT; ++a) {
+                    const int b = sum - a;
+                    if (b < 0 || b >= NPF) continue;
+                    st.o[db] = mfma_bf16_k16(tr_operand(tvs + a * TB, 0, db, lane), pt[b], st.o[db]);
+                }
+    };
+    // fp32 MFMA (IEEE operands on fp32 rows): two raw slots, the next block's loads issued before
+    // this block's products; each wave reads its operands from the raw rows (dims 32 grp .. of g,
+    // dims 8 col .. of vb rows 4 grp + s)
+    auto far_block_f32 = [&](int bi, int slot) {
+        const int c0 = lo + 16 * bi;
+        const char* sl = lbuf + slot * FSLOT;
         float ga[32], va[4][8];
-        if constexpr (SB) {                        // bf16 rows: dims 32 grp .. in chunks 4 grp + k
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const u32x4 u = *(const u32x4*)(sl + col * RBY + (((4 * grp + kk) ^ col) << 4));
+        for (int kk = 0; kk < 8; ++kk) {
+            const f32x4 f = *(const f32x4*)(sl + col * RBY + (((8 * grp + kk) ^ col) << 4));
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    ga[8 * kk + 2 * e] = bf2f(u[e] & 0xffffu);
-                    ga[8 * kk + 2 * e + 1] = bf2f(u[e] >> 16);
-                }
-            }
+            for (int e = 0; e < 4; ++e) ga[4 * kk + e] = f[e];
+        }
 #pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-                const int r = 4 * grp + s2;
-                const u32x4 u = *(const u32x4*)(sl + GV + r * RBY + ((col ^ r) << 4));
+        for (int s2 = 0; s2 < 4; ++s2) {
+            const int rr = 4 * grp + s2;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    va[s2][2 * e] = bf2f(u[e] & 0xffffu);
-                    va[s2][2 * e + 1] = bf2f(u[e] >> 16);
-                }
-            }
-        } else {                                   // fp32 rows (TF32: rounded in the slot): dims 32 grp ..
+            for (int hf = 0; hf < 2; ++hf) {
+                const f32x4 f = *(const f32x4*)(sl + GV + rr * RBY + (((2 * col + hf) ^ rr) << 4));
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {           // .. in chunks 8 grp + k
-                const f32x4 f = *(const f32x4*)(sl + col * RBY + (((8 * grp + kk) ^ col) << 4));
-#pragma unroll
-                for (int e = 0; e < 4; ++e) ga[4 * kk + e] = f[e];
-            }
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-                const int r = 4 * grp + s2;
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    const f32x4 f = *(const f32x4*)(sl + GV + r * RBY + (((2 * col + hf) ^ r) << 4));
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) va[s2][4 * hf + e] = f[e];
-                }
+                for (int e = 0; e < 4; ++e) va[s2][4 * hf + e] = f[e];
             }
         }
         const f32x4 lz4 = *(const f32x4*)(sl + 2 * GV + 16 * grp);
@@ -1842,29 +1993,26 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
             const int c = c0 + 4 * grp + i;
             sc[i] = (c < hi && ((ex4 >> (8 * i)) & 0xffu) == 0) ? __fadd_rn(s4[i], lz4[i]) : -INFINITY;
         }
-        f32_update<TF32>(st, sc, va);
+        f32_update<false>(st, sc, va);
     };
-    // TF32 on fp32 rows: the workgroup rounds the block's g and vb rows in their slot once (each
-    // thread its chunks), instead of every wave rounding each operand it reads
-    auto far_round = [&](int slot) {
-        char* sl = &fring[slot][0];
-        for (int c = threadIdx.x; c < (2 * GV) / 16; c += blockDim.x) {
-            f32x4 f = *(const f32x4*)(sl + 16 * c);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) f[e] = tf32_rna(f[e]);
-            *(f32x4*)(sl + 16 * c) = f;
+    if constexpr (FTERMS) {
+        if (nblk > 0) far_issue(0, lbuf_lds);
+        for (int bi = 0; bi < nblk; ++bi) {
+            wait_vmcnt<0>();                       // this wave's loads of block bi have landed
+            __syncthreads();                       // every wave's; every wave done with the terms
+            far_split();
+            __syncthreads();                       // the terms complete; the raw slot is free
+            if (bi + 1 < nblk) far_issue(bi + 1, lbuf_lds);
+            far_block(bi);
         }
-    };
-    if (nblk > 0) far_issue(0, 0);
-    for (int bi = 0; bi < nblk; ++bi) {
-        wait_vmcnt<0>();                           // this wave's loads of block bi have landed
-        __syncthreads();                           // every wave's; slot (bi + 1) & 1 is free
-        if (bi + 1 < nblk) far_issue(bi + 1, (bi + 1) & 1);
-        if constexpr (TF32 && !SB) {
-            far_round(bi & 1);
-            __syncthreads();
+    } else {
+        if (nblk > 0) far_issue(0, lbuf_lds);
+        for (int bi = 0; bi < nblk; ++bi) {
+            wait_vmcnt<0>();                       // this wave's loads of block bi have landed
+            __syncthreads();                       // every wave's; slot (bi + 1) & 1 is free
+            if (bi + 1 < nblk) far_issue(bi + 1, lbuf_lds + (uint32_t)(((bi + 1) & 1) * FSLOT));
+            far_block_f32(bi, bi & 1);
         }
-        far_block(bi, bi & 1);
     }
     // Near-field score operands on the bf16 MFMA (16x16x32): k-step s takes lane group grp's dims
     // 32 s + 8 grp .. + 7 of the row as NQT bf16 terms whose sum is the row exactly (a bf16 row:
@@ -1930,13 +2078,13 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         }
         return r;
     };
-    // The accumulators move to the near field's order through this wave's 8 KB of the far ring
-    // (row col, 16-byte chunk c at c ^ col): far order dims 32 grp + 8 i + 4 hf .. + 3 (chunk
-    // 8 grp + 2 i + hf) = st.o[4 hf .. 4 hf + 3][i]; near order dims 16 db + 4 grp .. + 3 (chunk
-    // 4 db + grp) = st.o[db].
-    __syncthreads();                            // every wave done with the far field's slots
-    {
-        char* tw_ = &fring[0][0] + w * 8192;
+    __syncthreads();                            // every wave done with the far field's buffer
+    if constexpr (!FTERMS) {
+        // the fp32-MFMA far field's accumulators to the near field's order, through this wave's
+        // 8 KB of the buffer (row col, 16-byte chunk c at c ^ col): far order dims 32 grp + 8 i +
+        // 4 hf .. + 3 (chunk 8 grp + 2 i + hf) = st.o[4 hf .. 4 hf + 3][i]; near order dims 16 db +
+        // 4 grp .. + 3 (chunk 4 db + grp) = st.o[db]
+        char* tw_ = lbuf + w * 8192;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1946,16 +2094,16 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         __syncthreads();
 #pragma unroll
         for (int db = 0; db < 8; ++db) st.o[db] = *(const f32x4*)(tw_ + col * 512 + (((4 * db + grp) ^ col) << 4));
+        __syncthreads();                        // every wave's accumulators read: the buffer is free
     }
-    __syncthreads();                            // every wave's accumulators read: the slots are free
     // a block's 32 key rows (bytes 0.., chunk c of row r at c ^ (r % 16), so the 16 lanes that
     // read one chunk of 16 rows address 16 positions) and its 32 value rows (bytes 8192.., chunk
-    // c of row r at c ^ swz(r), the transposing reads' layout) into a slot of the far field's
-    // ring by direct loads; a row past its run's last valid position repeats that position's token
+    // c of row r at c ^ swz(r), the transposing reads' layout) into a slot of the shared buffer
+    // by direct loads; a row past its run's last valid position repeats that position's token
     // (instruction i: keys for i < 8, values after; its rows 4 (i % 8) + lane / 16, in run
     // hh = (i % 8) / 4, wave-uniform; the run's first token in SGPRs, a 32-bit lane offset)
     auto kvload = [&](const Runs& rr, int slot) {
-        const uint32_t sl = fring_lds + (uint32_t)(slot * FSLOT);
+        const uint32_t sl = lbuf_lds + (uint32_t)(slot * NSLOT);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {           // nw >= 2: at most 8 instructions per wave
             const int i = w + nw * j;
@@ -1982,7 +2130,7 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
             rn = runs(e0 + 32);
             kvload(rn, kslot ^ 1);
         }
-        const char* ks_ = &fring[kslot][0];
+        const char* ks_ = lbuf + kslot * NSLOT;
         const char* vs_ = ks_ + 8192;
         float sc[8];
 #pragma unroll
@@ -2053,8 +2201,11 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     const float ltot = grp_sum(st.l);
     // the lane's O^T items: dims 16 db + 4 grp .. + 3 are st.o[db]
     if (pacc == nullptr) {                                     // single split: normalise in place
-        if (qi >= nq) return;
-        const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qi);
+        int rx = r;
+        asm volatile("" : "+v"(rx));           // the row index recomputed here, not held across the loops
+        const int64_t qo = (int64_t)t * tile + rx;
+        if (qo >= nq) return;
+        const int64_t orow = (int64_t)h * nq + perm_row(perm, h, nq, qo);
         const float ms = st.m == -INFINITY ? 0.0f : st.m;
         const float den = ltot < 1e-30f ? 1e-30f : ltot;
 #pragma unroll
