@@ -2829,7 +2829,9 @@ __global__ __launch_bounds__(128 * NP, route_waves_per_simd<NP>()) void route_ke
         if (hr == 0) {
             dma_qk<NTL>(X8 + r0 * D, X8 + r1 * D, bo, slot);
             dma_rows01<NTL>(XV + r0 * D, bo, slot);
-            if (lane < 16) dma16<NTL>((lane < 8 ? s_lo : s_hi) + 4 * (lane & nlim), slot + 12288);
+            // (the saddr form, one base per lane half: no 64-bit lane address held across the loop)
+            if (lane < 8) dma16s<NTL>(s_lo, (uint32_t)(16 * (lane & nlim)), slot + 12288);
+            else if (lane < 16) dma16s<NTL>(s_hi, (uint32_t)(16 * (lane & nlim)), slot + 12288);
         } else {
             dma_rows27<NTL>(XV + r0 * D, XV + r1 * D, bo, slot);
         }
@@ -3536,13 +3538,13 @@ __global__ __launch_bounds__(64 * NW, 2) void route16_kernel(
             if constexpr (FP8) {
                 dma_rows8((const uint8_t*)g + rw * D, (const uint8_t*)vb + rw * D, sl_lds);
                 if (wv == 0 && lane < 8) {
-                    dma16<false>(lz + r0 + 4 * lane, sl_lds + 2 * R16_ROWS);
-                    dma16<false>(sg + r0 + 4 * lane, sl_lds + 2 * R16_ROWS + 128);
-                    dma16<false>(sv + r0 + 4 * lane, sl_lds + 2 * R16_ROWS + 256);
+                    dma16s<false>(lz + r0, (uint32_t)(16 * lane), sl_lds + 2 * R16_ROWS);
+                    dma16s<false>(sg + r0, (uint32_t)(16 * lane), sl_lds + 2 * R16_ROWS + 128);
+                    dma16s<false>(sv + r0, (uint32_t)(16 * lane), sl_lds + 2 * R16_ROWS + 256);
                 }
             } else {
                 dma_rows16((const uint16_t*)g + rw * D, (const uint16_t*)vb + rw * D, sl_lds);
-                if (wv == 0 && lane < 8) dma16<false>(lz + r0 + 4 * lane, sl_lds + 2 * R16_ROWS);
+                if (wv == 0 && lane < 8) dma16s<false>(lz + r0, (uint32_t)(16 * lane), sl_lds + 2 * R16_ROWS);
             }
         } else {
             fetch_near(bi, sl_lds);
