@@ -1701,15 +1701,6 @@ struct RowF32 {        // running softmax state of one row (h3/htrc_flat_triton.
                        // field keeps dim 8 (4 grp + i) + db and reorders once, before the near field)
 };
 
-// S^T tile of 16 keys x 16 rows: item i of lane l = sum over dims of key (4 (l/16) + i)'s A row
-// and row l%16's B row, from the 32 dims each lane holds of both.
-__device__ __forceinline__ f32x4 dot_tile_f32(const float (&a)[32], const float (&b)[32]) {
-    f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 32; ++s) c = mfma_f32(a[s], b[s], c);
-    return c;
-}
-
 // One block of 16 keys: scores sc[i] of keys 4 grp + i (masked: -inf), value rows va[s] = dims
 // 8 col .. + 7 of key 4 grp + s.  The reference's update: m_new = max(m, rowmax), m_s = m_new, or
 // 0 when -inf, p = exp(sc - m_s), alpha = exp(m - m_s), l = l alpha + sum p, O = O alpha + P V.
@@ -1769,20 +1760,14 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     // MFMA forms and only the grouping of the fp32 sums differs.
     constexpr int NGT = SB ? 1 : (TF32 ? 2 : 3), ND = TF32 ? 2 : 3, NPF = TF32 ? 2 : 3;
     // The far field takes these products for TF32 operands and bf16 rows; for IEEE operands on
-    // fp32 rows it runs on the fp32 MFMA (v_mfma_f32_16x16x4_f32), which measured faster there:
-    // three terms of every state value cost more splitting than their products save.
+    // fp32 rows only its scores do (g in three terms), and its PV products run on the fp32 MFMA
+    // (v_mfma_f32_16x16x4_f32), which measured faster there: three terms of every vb value cost
+    // more splitting than their products save.
     constexpr bool FTERMS = TF32 || SB;
     // q - mu of row r: k-step ks holds lane group grp's dims 32 ks + 8 grp .. + 7 (FTERMS), or
     // the fp32 values of dims 32 grp .. + 31
     bf16x8 dqt[4][3];
-    float dq[32];
-    if constexpr (!FTERMS) {
-        float mx[32];
-        load_f32<32, QBF, false>((const char*)q + (((int64_t)h * nq + src) * D + 32 * grp) * QB, dq);
-        load_f32<32, false, false>(mu + ((int64_t)h * mu_stride + t / group) * D + 32 * grp, mx);
-#pragma unroll
-        for (int e = 0; e < 32; ++e) dq[e] = __fsub_rn(dq[e], mx[e]);
-    } else {
+    {
         const char* qrow = (const char*)q + ((int64_t)h * nq + src) * D * QB;
         const float* murow = mu + ((int64_t)h * mu_stride + t / group) * D + 8 * grp;
 #pragma unroll
@@ -1817,7 +1802,7 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     constexpr int NSLOT = 16384;                   // near field slot: 32 key rows, 32 value rows
     constexpr int FSLOT = RAW;                     // fp32-MFMA far field: two raw slots, no terms
     constexpr int LDSZ_T = RAW + 2 * NGT * TB + 128 > 2 * NSLOT ? RAW + 2 * NGT * TB + 128 : 2 * NSLOT;
-    constexpr int LDSZ = FTERMS ? LDSZ_T : (2 * FSLOT > 2 * NSLOT ? 2 * FSLOT : 2 * NSLOT);
+    constexpr int LDSZ = FTERMS ? LDSZ_T : 2 * FSLOT + NGT * TB;   // (2 FSLOT > 2 NSLOT)
     __shared__ __align__(16) char lbuf[LDSZ];
     char* const tgs = lbuf + RAW;                  // g terms
     char* const tvs = tgs + NGT * TB;              // vb terms
@@ -1961,19 +1946,32 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
                     st.o[db] = mfma_bf16_k16(tr_operand(tvs + a * TB, 0, db, lane), pt[b], st.o[db]);
                 }
     };
-    // fp32 MFMA (IEEE operands on fp32 rows): two raw slots, the next block's loads issued before
-    // this block's products; each wave reads its operands from the raw rows (dims 32 grp .. of g,
-    // dims 8 col .. of vb rows 4 grp + s)
+    // IEEE operands on fp32 rows: two raw slots, the next block's loads issued before this
+    // block's work; the workgroup splits the block's g rows once into three bf16 terms (after
+    // the raw slots) for the score products, and the PV products run on the fp32 MFMA with each
+    // wave reading its vb operands from the raw rows (dims 8 col .. of rows 4 grp + s)
+    char* const tg3 = lbuf + 2 * FSLOT;
+    auto far_split_g = [&](int slot) {
+        for (int u = tid; u < 256; u += nth) {
+            const int lf = u >> 4, c = u & 15;
+            const char* row = lbuf + slot * FSLOT + lf * RBY;
+            float x[8];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const f32x4 f = *(const f32x4*)(row + (((2 * c + hf) ^ lf) << 4));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[4 * hf + e] = f[e];
+            }
+            bf16x8 tt[3];
+            split_terms(x, tt, NGT);
+#pragma unroll
+            for (int a = 0; a < NGT; ++a) *(bf16x8*)(tg3 + a * TB + lf * 256 + ((c ^ lf) << 4)) = tt[a];
+        }
+    };
     auto far_block_f32 = [&](int bi, int slot) {
         const int c0 = lo + 16 * bi;
         const char* sl = lbuf + slot * FSLOT;
-        float ga[32], va[4][8];
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            const f32x4 f = *(const f32x4*)(sl + col * RBY + (((8 * grp + kk) ^ col) << 4));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ga[4 * kk + e] = f[e];
-        }
+        float va[4][8];
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2) {
             const int rr = 4 * grp + s2;
@@ -1986,7 +1984,22 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         }
         const f32x4 lz4 = *(const f32x4*)(sl + 2 * GV + 16 * grp);
         const uint32_t ex4 = *(const uint32_t*)(sl + 2 * GV + 64 + 4 * grp);
-        const f32x4 s4 = dot_tile_f32(ga, dq);
+        // (k-step by k-step: the step's three g terms held, its nine products smallest first)
+        f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            bf16x8 ga[3];
+#pragma unroll
+            for (int a = 0; a < NGT; ++a)
+                ga[a] = *(const bf16x8*)(tg3 + a * TB + col * 256 + (((4 * ks + grp) ^ col) << 4));
+#pragma unroll
+            for (int sum = NGT + ND - 2; sum >= 0; --sum)
+#pragma unroll
+                for (int a = 0; a < NGT; ++a) {
+                    const int b = sum - a;
+                    if (b >= 0 && b < ND) s4 = mfma_bf16(ga[a], dqt[ks][b], s4);
+                }
+        }
         float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -2009,8 +2022,10 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         if (nblk > 0) far_issue(0, lbuf_lds);
         for (int bi = 0; bi < nblk; ++bi) {
             wait_vmcnt<0>();                       // this wave's loads of block bi have landed
-            __syncthreads();                       // every wave's; slot (bi + 1) & 1 is free
+            __syncthreads();                       // every wave's; slot (bi + 1) & 1 and the terms free
             if (bi + 1 < nblk) far_issue(bi + 1, lbuf_lds + (uint32_t)(((bi + 1) & 1) * FSLOT));
+            far_split_g(bi & 1);
+            __syncthreads();                       // the g terms complete
             far_block_f32(bi, bi & 1);
         }
     }
