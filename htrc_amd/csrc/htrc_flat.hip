@@ -2252,7 +2252,7 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
 // dims 32 ks + 8 grp .. + 7): g and q - mu each split into bf16 terms that sum to them exactly (a
 // bf16 g: one term; TF32 operands: two; fp32: three), every term product formed, so each dim's
 // product is exactly the one the fp32 MFMA forms and only the grouping of the fp32 sums differs.
-constexpr int SEL_F32_LPW = 256;   // leaves per workgroup
+constexpr int SEL_F32_LPW = 1024;  // leaves per workgroup
 template <bool QBF, bool SB, bool TF32>
 __global__ __launch_bounds__(256) void select_f32_kernel(const void* __restrict__ q, const float* __restrict__ mu,
                                                          int mu_stride, const void* __restrict__ g,
