@@ -227,9 +227,10 @@ int htrc_tile_bf16(const uint16_t* q16, const uint16_t* dq16, const uint16_t* g,
  * vb fp32 (store="fp32") or bf16 (store="bf16"; state_bf16 = 1) [H, ng, nbp, 128], lz fp32; q fp32
  * or bf16 (q_is_bf16) [H, nq, 128] in query order with the optional row permutation perm, mu the
  * layer's centres [H, ceil(nt / group), 128] (htrc_pack_q16's), k / v bf16.  Every product is an
- * exact product of the fp32 operands with fp32 sums: fp32 MFMA for the far field; bf16 MFMA for
- * the select, with g and q - mu each split into bf16 terms that sum to them exactly, and for the
- * near field, with the query row and the softmax weights so split; tf32 = 1 (precision="tf32", PREC "tf32") rounds every operand to TF32
+ * exact product of the fp32 operands with fp32 sums: bf16 MFMA over operands split into bf16 terms
+ * that sum to them exactly (g and q - mu in the select and the far scores, the query row and the
+ * softmax weights in the near field, vb and the weights in the far PV), except the far PV of IEEE
+ * operands on fp32 rows, on the fp32 MFMA (v_mfma_f32_16x16x4_f32); tf32 = 1 (precision="tf32", PREC "tf32") rounds every operand to TF32
  * (to nearest, ties away) first.  Statistics: g = (w K) scale and vb = w V stored as fp32 or as
  * bf16 (the htrc_leaf_stats_bf16 values when tf32 = 0).  select: SEL = max over every stride-th row
  * of (q - mu) . g + lz.  tile far: (q - mu) . g + lz, PV p . vb; near: (q . k) scale, PV p . v;
