@@ -1767,8 +1767,7 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
     // (v_mfma_f32_16x16x4_f32), which measured faster there: three terms of every vb value cost
     // more splitting than their products save.
     constexpr bool FTERMS = TF32 || SB;
-    // q - mu of row r: k-step ks holds lane group grp's dims 32 ks + 8 grp .. + 7 (FTERMS), or
-    // the fp32 values of dims 32 grp .. + 31
+    // q - mu of row r in ND terms: k-step ks holds lane group grp's dims 32 ks + 8 grp .. + 7
     bf16x8 dqt[4][3];
     {
         const char* qrow = (const char*)q + ((int64_t)h * nq + src) * D * QB;
