@@ -101,6 +101,15 @@ __device__ __forceinline__ float xor32_max(float v) {
 }
 __device__ __forceinline__ float grp_max(float v) { return xor32_max(xor16_max(v)); }
 
+// Orders one wave's LDS writes before its lanes' later reads of them (and reads before later
+// writes): a lane reading what another lane of its wave wrote is a cross-thread access, which
+// the compiler may otherwise move across the writes.  Wave scope, no workgroup barrier.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ln z for z >= 1 (a partition sum whose largest term is exp(0) = 1): log2 z by v_log_f32 (no
 // subnormal input to rescale, no infinity to pass through), times ln 2 as hi + lo with hi = ln 2
 // truncated to 24 bits (0x3f317217) and lo = fp32(ln 2 - hi) (0x3377d1cf), the product y hi

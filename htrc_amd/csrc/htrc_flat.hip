@@ -527,6 +527,8 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
     static_assert(NL * LEAF_BYTES <= 65536 && (NL == 1 || NL == 2 || NL == 4 || NL == 8), "stats_ls shape");
     __shared__ __align__(16) char lds[NL * LEAF_BYTES];
     __shared__ float lmax[NL][2][4];
+    // fp32 rows: per wave 2 KB to turn 4 centres' rows into whole-row stores (below)
+    __shared__ __align__(16) char rowbuf[STORE == 3 ? 4 : 1][STORE == 3 ? 2048 : 16];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     // 1-D grid over (centre part, leaf group, head), centre part fastest: the workgroups of one
     // head run together on one XCD, whose L2 then serves the head's centres to all of them
@@ -782,16 +784,39 @@ __global__ __launch_bounds__(256, 2) void stats_ls_kernel(const float* __restric
                         *(u32x4*)(vr + 32 * (2 * hf + m2)) = u32x4{va[m2].x, va[m2].y, vc[m2].x, vc[m2].y};
                 }
             };
-            if constexpr (F32) {               // fp32 rows: dims 16 db + 4 grp .. of centre col
+            if constexpr (F32) {
+                // fp32 rows (the lane holds dims 16 db + 4 grp .. of centre col) through this wave's
+                // 2 KB of LDS, 4 centres at a time, so each store instruction writes two whole
+                // 512-byte rows instead of 16 rows' 64-byte pieces (cfg3: 7.13 -> 5.3 ms when every
+                // store instruction is one contiguous KB).  Buffered row rr keeps its 16-byte chunk c
+                // (dims 4 c ..) at c ^ 4 rr: the 16 writing lanes and the 32 lanes reading a row
+                // address distinct banks.
+                char* tb = &rowbuf[w][0];
+                const int hl = lane >> 5, cl = lane & 31;
+                auto put = [&](const f32x4 (&acc)[8], float sc, float* dst) {
 #pragma unroll
-                for (int db = 0; db < 8; ++db) {
-                    *(f32x4*)((float*)g8 + s * D + 16 * db + 4 * grp) =
-                        f32x4{__fmul_rn(gacc[db][0], scg), __fmul_rn(gacc[db][1], scg), __fmul_rn(gacc[db][2], scg),
-                              __fmul_rn(gacc[db][3], scg)};
-                    *(f32x4*)((float*)vb + s * D + 16 * db + 4 * grp) =
-                        f32x4{__fmul_rn(vacc[db][0], pev), __fmul_rn(vacc[db][1], pev), __fmul_rn(vacc[db][2], pev),
-                              __fmul_rn(vacc[db][3], pev)};
-                }
+                    for (int r = 0; r < 4; ++r) {
+                        if ((col >> 2) == r) {
+                            const int rr = col & 3;
+#pragma unroll
+                            for (int db = 0; db < 8; ++db)
+                                *(f32x4*)(tb + rr * 512 + (((4 * db + grp) ^ (4 * rr)) << 4)) =
+                                    f32x4{__fmul_rn(acc[db][0], sc), __fmul_rn(acc[db][1], sc),
+                                          __fmul_rn(acc[db][2], sc), __fmul_rn(acc[db][3], sc)};
+                        }
+                        wave_lds_sync();               // the 4 rows written before any lane reads them
+#pragma unroll
+                        for (int ii = 0; ii < 2; ++ii) {
+                            const int rr = 2 * ii + hl, cc = 4 * r + rr;
+                            const f32x4 v4 = *(const f32x4*)(tb + rr * 512 + ((cl ^ (4 * rr)) << 4));
+                            const int64_t sr = ((int64_t)h * nt + min(16 * j + cc, nt - 1)) * nb_pad + l0 + li;
+                            *(f32x4*)(dst + sr * D + 4 * cl) = v4;
+                        }
+                        wave_lds_sync();               // read before the next 4 rows overwrite them
+                    }
+                };
+                put(gacc, scg, (float*)g8);
+                put(vacc, pev, (float*)vb);
             } else if constexpr (BF16) {
                 u32x2 pgb[8], pv[8];
 #pragma unroll
