@@ -2107,12 +2107,13 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         int64_t b[2];
         int last[2];
     };
+    const int lsh = __builtin_ctz(leaf);        // leaf is a power of two
     auto runs = [&](int e0) {
         Runs r;
-        r.b[0] = kh + (int64_t)ix[e0 / leaf] * leaf + e0 % leaf;
+        r.b[0] = kh + (int64_t)ix[e0 >> lsh] * leaf + (e0 & (leaf - 1));
         r.last[0] = min(15, e_hi - 1 - e0);
         if (e0 + 16 < e_hi) {
-            r.b[1] = kh + (int64_t)ix[(e0 + 16) / leaf] * leaf + (e0 + 16) % leaf;
+            r.b[1] = kh + (int64_t)ix[(e0 + 16) >> lsh] * leaf + ((e0 + 16) & (leaf - 1));
             r.last[1] = min(15, e_hi - 17 - e0);
         } else {
             r.b[1] = r.b[0];
@@ -2158,10 +2159,13 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
                    sl + 1024 * i);
         }
     };
-    Runs rn{};
+    // run bases one block ahead of the loads that use them (their index reads then land under
+    // a block's products instead of delaying the next block's loads)
+    Runs rn{}, rn1{};
     if (e_lo < e_hi) {
         rn = runs(e_lo);
         kvload(rn, 0);
+        if (e_lo + 32 < e_hi) rn1 = runs(e_lo + 32);
     }
     int kslot = 0;
     for (int e0 = e_lo; e0 < e_hi; e0 += 32, kslot ^= 1) {
@@ -2169,8 +2173,9 @@ __global__ __launch_bounds__(256, 3) void tile_f32_kernel(
         wait_vmcnt<0>();                        // this wave's loads of the block have landed
         __syncthreads();                        // every wave's; the other slot is free
         if (e0 + 32 < e_hi) {                   // the next block loads under this one
-            rn = runs(e0 + 32);
+            rn = rn1;
             kvload(rn, kslot ^ 1);
+            if (e0 + 64 < e_hi) rn1 = runs(e0 + 64);
         }
         const char* ks_ = lbuf + kslot * NSLOT;
         const char* vs_ = ks_ + 8192;
