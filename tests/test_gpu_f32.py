@@ -100,6 +100,24 @@ def test_select_f32_on_oracle_state(device, store, prec, group, stride, tile):
     assert np.abs(got - want).max() <= 4e-6 * (1 + np.abs(want).max())
 
 
+@pytest.mark.parametrize("prec", ["ieee", "tf32"])
+def test_select_f32_leaves_past_one_workgroup(device, prec):
+    """A group's 1100 leaves span two select workgroups (1024 leaves each): both halves of SEL
+    against the oracle."""
+    n, leaf, nb = 300, 16, 1100
+    q, k, v = _data(n, nb * leaf, seed=11)
+    st = flat_f32.flat_f32(q[0].float().numpy(), k[0].float().numpy(), v[0].float().numpy(), tile=64, leaf=leaf,
+                           exact_leaves=4, store="fp32", prec=prec)
+    sg = _state_gpu(st, "fp32", device)
+    mu = torch.from_numpy(st["mu"])[None].to(device)
+    sel = hip.select_f32(q.to(device), mu, sg["g8"], sg["lz"], nb, tile=64, prec=prec)
+    torch.cuda.synchronize()
+    got = _np(sel[0])[:, :nb]
+    want = st["sel"]
+    assert got.shape == want.shape
+    assert np.abs(got - want).max() <= 4e-6 * (1 + np.abs(want).max())
+
+
 @pytest.mark.parametrize("store,prec,splits,leaf,tile,group", [
     ("fp32", "ieee", 1, 64, 64, 1), ("fp32", "ieee", 4, 32, 64, 2), ("fp32", "tf32", 3, 64, 32, 1),
     ("bf16", "ieee", 2, 16, 64, 1), ("bf16", "tf32", 1, 128, 32, 3)])
